@@ -1,0 +1,261 @@
+/*
+ * talos_hip.h -- C ABI of the MI355X (gfx950) autograd hot path for Talos-XII's
+ * transformer and linear policy layers.
+ *
+ * Every entry point takes plain pointers and sizes. Device pointers are fp32 (or
+ * bf16 stored as uint16_t) buffers allocated with talos_malloc or any HIP allocator.
+ * Streams are hipStream_t passed as void*; NULL means the calling thread's default
+ * stream (hipStreamPerThread). Unless a name ends in _async, a call returns after its
+ * work on that stream has finished, matching the synchronous semantics of the
+ * reference's Tensor ops. Status codes: 0 on success, a talos_status otherwise;
+ * talos_last_error() returns a thread-local message for the last failure.
+ * Arguments are validated on the host before any launch, so every error path below
+ * can be exercised on a machine without a GPU.
+ *
+ * Reference citations are file:line in zayokami/Talos-XII (Rust crate, src/).
+ */
+#ifndef TALOS_HIP_H
+#define TALOS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* talos_stream_t;
+
+enum talos_status {
+  TALOS_OK = 0,
+  TALOS_ERR_SHAPE = 1,       /* shape / stride / size mismatch (reference: assert! panics, autograd.rs:96-100, 209) */
+  TALOS_ERR_NULL = 2,        /* null pointer argument */
+  TALOS_ERR_DTYPE = 3,       /* unsupported dtype, op code or layout enum */
+  TALOS_ERR_NO_DEVICE = 4,   /* no usable GPU */
+  TALOS_ERR_HIP = 5,         /* HIP runtime error (message carries hipGetErrorString) */
+  TALOS_ERR_ALLOC = 6,       /* device allocation failed */
+  TALOS_ERR_HANDLE = 7,      /* invalid or freed handle */
+  TALOS_ERR_UNSUPPORTED = 8  /* configuration outside what the kernels cover (message says which limit) */
+};
+
+/* ------------------------------------------------------------------------- */
+/* Runtime                                                                    */
+/* ------------------------------------------------------------------------- */
+
+/* Thread-local message describing the last non-zero status on this thread. */
+const char* talos_last_error(void);
+/* Library version string. */
+const char* talos_version(void);
+/* Initialises the HIP device context once per process (std::call_once). */
+int talos_init(void);
+/* Number of visible GPUs (0 on a machine without one; returns TALOS_OK). */
+int talos_device_count(int* count);
+int talos_malloc(void** ptr, size_t bytes);
+int talos_free(void* ptr);
+/* Host<->device copies. The _f64 variants convert between the reference's f64
+ * host vectors (Tensor.data / Tensor.grad, autograd.rs:14-20) and fp32 device buffers. */
+int talos_memcpy_h2d(void* dst, const void* src, size_t bytes, talos_stream_t stream);
+int talos_memcpy_d2h(void* dst, const void* src, size_t bytes, talos_stream_t stream);
+int talos_memcpy_h2d_f64(float* dst, const double* src, size_t n, talos_stream_t stream);
+int talos_memcpy_d2h_f64(double* dst, const float* src, size_t n, talos_stream_t stream);
+/* Zero-fills with a kernel (no hipMemsetAsync, so it is safe inside a captured graph). */
+int talos_fill_zero(void* dst, size_t bytes, talos_stream_t stream);
+int talos_stream_sync(talos_stream_t stream);
+
+/* ------------------------------------------------------------------------- */
+/* Kernel-level entry points (device pointers, fp32 unless stated)            */
+/* ------------------------------------------------------------------------- */
+
+/* C[M,N] = alpha * op(A) * op(B) + beta * C, row-major.
+ * op(A) is A[M,K] (lda >= K) when transA == 0, or the transpose of A stored [K,M] (lda >= M).
+ * op(B) is B[K,N] (ldb >= N) when transB == 0, or the transpose of B stored [N,K] (ldb >= K).
+ * Replaces Tensor::matmul (autograd.rs:200-354): forward C = A.B is (0,0); the backward
+ * dA += dC.B^T is (0,1) with beta 1 and dB += A^T.dC is (1,0) with beta 1 (grads accumulate,
+ * autograd.rs:290, 330). beta must be 0 or 1. MFMA v_mfma_f32_32x32x2f32 tiles. */
+int talos_gemm_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
+                   const float* B, int ldb, float beta, float* C, int ldc, talos_stream_t stream);
+
+/* Same contract with bf16 inputs (uint16_t bit patterns) and fp32 accumulation/output.
+ * MFMA v_mfma_f32_32x32x16_bf16 tiles. No reference counterpart: the reference is f64 only
+ * (autograd.rs:16-17); this is the bf16-in/fp32-acc variant of talos_gemm_f32. */
+int talos_gemm_bf16(int transA, int transB, int M, int N, int K, float alpha, const uint16_t* A, int lda,
+                    const uint16_t* B, int ldb, float beta, float* C, int ldc, talos_stream_t stream);
+
+/* Round-to-nearest-even fp32 -> bf16 conversion of n elements. */
+int talos_cast_f32_to_bf16(const float* x, uint16_t* y, size_t n, talos_stream_t stream);
+
+/* Batched C_b = alpha * A_b . op(B_b) + beta * C_b for b in [0,batch) with element strides
+ * sA, sB, sC between consecutive matrices (same trans conventions as talos_gemm_f32).
+ * Replaces batched_matmul_qt_k (transformer.rs:877-958: S = Q.K^T is transB = 1) and
+ * batched_matmul_probs_v (transformer.rs:961-1050: O = P.V is transB = 0) and their backward. */
+int talos_gemm_batched_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
+                           long long sA, const float* B, int ldb, long long sB, float beta, float* C, int ldc,
+                           long long sC, int batch, talos_stream_t stream);
+
+/* db[cols] = beta * db + sum_rows dy[rows, cols]. Backward of broadcast_to_batch
+ * (autograd.rs:530-544), i.e. the Linear bias gradient (nn.rs:96-101). Partials are
+ * combined in f64. */
+int talos_bias_grad_f32(int rows, int cols, const float* dy, float beta, float* db, talos_stream_t stream);
+
+/* RMSNorm forward (nn.rs:182-230): rms = sqrt(mean(x^2) + eps), y = x / rms * w.
+ * Saves rstd[rows] = 1/rms (the reference caches rms and x_hat, nn.rs:196-197; x_hat is
+ * recomputed from x and rstd instead of being stored). */
+int talos_rmsnorm_fwd_f32(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
+                          talos_stream_t stream);
+/* RMSNorm backward (nn.rs:234-296): dx += rstd * (g*w - x_hat * mean(g*w*x_hat)),
+ * dw += sum_rows g * x_hat. beta_dx / beta_dw in {0,1} select overwrite or accumulate. */
+int talos_rmsnorm_bwd_f32(int rows, int dim, const float* x, const float* w, const float* rstd, const float* dy,
+                          float beta_dx, float* dx, float beta_dw, float* dw, talos_stream_t stream);
+
+/* Row softmax (transformer.rs:1074-1096) with max subtraction. causal != 0 adds the
+ * causal mask: row r is query q = r mod cols, keys j > q get probability exactly 0
+ * (extension; the reference has no mask). */
+int talos_softmax_fwd_f32(int rows, int cols, int causal, const float* x, float* y, talos_stream_t stream);
+/* dx = beta*dx + y * (g - sum(g*y)) (transformer.rs:1098-1117). Masked entries get 0. */
+int talos_softmax_bwd_f32(int rows, int cols, int causal, const float* y, const float* dy, float beta, float* dx,
+                          talos_stream_t stream);
+
+/* Rotary embedding on x[n_seq, seq_len, heads, dim] (row-major, interleaved pairs
+ * (2i, 2i+1)), position of token t is start_pos + t, theta_i = base^(-2i/dim) with the
+ * cos/sin table computed in f64 and rounded to fp32 (transformer.rs:239-251, 255-292).
+ * The reference's training path rotates by the index along shape[-2] (transformer.rs:262);
+ * here the position is always the sequence index. */
+int talos_rope_fwd_f32(int n_seq, int seq_len, int heads, int dim, int start_pos, float base, const float* x,
+                       float* y, talos_stream_t stream);
+/* Backward = rotation by -theta (transformer.rs:305-333): dx = beta*dx + R^T dy. */
+int talos_rope_bwd_f32(int n_seq, int seq_len, int heads, int dim, int start_pos, float base, const float* dy,
+                       float beta, float* dx, talos_stream_t stream);
+/* Writes the fp32 cos/sin table [max_len, dim/2] the kernels use (bit-exact check). */
+int talos_rope_table_f32(int max_len, int dim, float base, float* cos_out, float* sin_out, talos_stream_t stream);
+
+/* Fused scaled-dot-product attention over q/k/v laid out [batch, seq, heads, dim]
+ * with row strides ld_q/ld_k/ld_v/ld_o (elements between consecutive tokens), replacing
+ * the chain transpose -> batched_matmul_qt_k -> scale_tensor -> softmax -> batched_matmul_probs_v
+ * -> transpose (transformer.rs:519-557, 877-1121). Saves lse[batch, heads, seq] (natural
+ * log-sum-exp of the scaled scores) for the backward. qk_dim <= 128, v_dim <= 128, seq <= 256. */
+int talos_attn_fwd_f32(int batch, int seq, int heads, int qk_dim, int v_dim, float scale, int causal,
+                       const float* q, int ld_q, const float* k, int ld_k, const float* v, int ld_v,
+                       float* o, int ld_o, float* lse, talos_stream_t stream);
+/* Backward of talos_attn_fwd_f32: writes dq, dk, dv (overwrite) with the same layouts. */
+int talos_attn_bwd_f32(int batch, int seq, int heads, int qk_dim, int v_dim, float scale, int causal,
+                       const float* q, int ld_q, const float* k, int ld_k, const float* v, int ld_v,
+                       const float* o, int ld_o, const float* lse, const float* dout, int ld_do,
+                       float* dq, int ld_dq, float* dk, int ld_dk, float* dv, int ld_dv, talos_stream_t stream);
+
+/* Element-wise ops of the tape (autograd.rs:356-792, 1606-1862). */
+enum talos_unary_op {
+  TALOS_RELU = 0, TALOS_LOG = 1, TALOS_EXP = 2, TALOS_SIN = 3, TALOS_COS = 4, TALOS_SQRT = 5,
+  TALOS_NEG = 6, TALOS_SCALE = 7, TALOS_CLIP = 8, TALOS_GELU = 9, TALOS_COPY = 10
+};
+enum talos_binary_op { TALOS_ADD = 0, TALOS_SUB = 1, TALOS_MUL = 2, TALOS_DIV = 3 };
+/* y = op(x); p0/p1 are the scale factor (SCALE) or [min,max] (CLIP). */
+int talos_unary_fwd_f32(int op, size_t n, float p0, float p1, const float* x, float* y, talos_stream_t stream);
+/* dx += dop(x) * dy, exactly the reference closures (e.g. relu passes where x > 0,
+ * clip where min <= x <= max, sqrt only where x > 0). */
+int talos_unary_bwd_f32(int op, size_t n, float p0, float p1, const float* x, const float* dy, float* dx,
+                        talos_stream_t stream);
+int talos_binary_fwd_f32(int op, size_t n, const float* a, const float* b, float* y, talos_stream_t stream);
+/* da += d/da, db += d/db. When da == db (the same tensor on both sides, autograd.rs:1729, 1792)
+ * the combined derivative is accumulated once. */
+int talos_binary_bwd_f32(int op, size_t n, const float* a, const float* b, const float* dy, float* da, float* db,
+                         talos_stream_t stream);
+/* out[0] = scale * sum(x) (sum / mean, autograd.rs:433-482), partials combined in f64. */
+int talos_reduce_sum_f32(size_t n, float scale, const float* x, float* out, talos_stream_t stream);
+/* dx[i] += scale * g[0] (backward of sum / mean / broadcast-from-scalar). */
+int talos_fill_add_f32(size_t n, float scale, const float* g, float* dx, talos_stream_t stream);
+/* y[..] = x with dims dim0, dim1 swapped (autograd.rs:632-739). accumulate != 0 adds into y
+ * (the backward scatter-add). rank <= 6. */
+int talos_transpose_f32(int rank, const long long* shape, int dim0, int dim1, const float* x, float* y,
+                        int accumulate, talos_stream_t stream);
+/* out[rows, ca+cb] = [a | b] (concat_last_dim, transformer.rs:1123-1160); backward splits. */
+int talos_concat_last_f32(size_t rows, int ca, int cb, const float* a, const float* b, float* out,
+                          talos_stream_t stream);
+int talos_concat_last_bwd_f32(size_t rows, int ca, int cb, const float* dout, float* da, float* db,
+                              talos_stream_t stream);
+/* out[rows, cols] = broadcast_to_batch of v[cols] (autograd.rs:511-528). */
+int talos_broadcast_rows_f32(size_t rows, int cols, const float* v, float* out, talos_stream_t stream);
+
+/* ------------------------------------------------------------------------- */
+/* Fused model-level entry points                                             */
+/* ------------------------------------------------------------------------- */
+
+enum talos_activation { TALOS_ACT_GELU = 0, TALOS_ACT_RELU = 1 };
+
+/* Pre-norm transformer block with standard multi-head attention and RoPE:
+ *   h2  = x + Wo . attn(rope(q), rope(k), v),  [q|k|v] = rmsnorm(x; g1) . Wqkv
+ *   out = h2 + W2 . act(rmsnorm(h2; g2) . W1 + b1) + b2
+ * The reference block (transformer.rs:71-90) is the same pre-norm residual layout with MLA
+ * attention and a 2x ReLU MLP; this is its standard-MHA / 4x GELU restatement.
+ * Parameter layout (fp32, contiguous, in this order), d = d_model, F = ffn_dim:
+ *   g1[d] | Wqkv[d,3d] (columns q | k | v, heads contiguous) | Wo[d,d] | g2[d] |
+ *   W1[d,F] | b1[F] | W2[F,d] | b2[d]
+ * Linear weights are stored [in, out] as in the reference (nn.rs:22). */
+typedef struct talos_block_cfg {
+  int batch;
+  int seq;
+  int d_model;
+  int n_heads;
+  int head_dim;   /* n_heads * head_dim == d_model */
+  int ffn_dim;
+  int causal;     /* 1: causal attention mask */
+  int activation; /* talos_activation */
+  float eps;      /* RMSNorm eps */
+  float rope_base;
+} talos_block_cfg;
+
+size_t talos_block_param_count(const talos_block_cfg* cfg);
+
+/* Policy network of the PPO actor-critic (ppo.rs:246-307): embed Linear(in,d)+b ->
+ * n_layers blocks -> RMSNorm -> out_proj Linear(d,d)+b -> last token -> actor Linear(d,A)+b
+ * and critic Linear(d,1)+b. Parameter layout:
+ *   We[in,d] | be[d] | block_0 ... block_{L-1} (talos_block_cfg layout) | gf[d] |
+ *   Wout[d,d] | bout[d] | Wa[d,A] | ba[A] | Wc[d,1] | bc[1] */
+typedef struct talos_ppo_cfg {
+  int batch;      /* samples per minibatch */
+  int seq;        /* tokens per sample (all samples padded to seq) */
+  int in_dim;     /* state features per token (8, sim.rs:347-356) */
+  int d_model;
+  int n_layers;
+  int n_heads;
+  int head_dim;
+  int ffn_dim;
+  int n_actions;
+  int causal;
+  int activation;
+  float eps;
+  float rope_base;
+  float clip_eps;     /* 0.2, ppo.rs:17 */
+  float value_coef;   /* 0.5, ppo.rs:20 */
+  float entropy_coef; /* 0.01, ppo.rs:21 */
+} talos_ppo_cfg;
+
+size_t talos_ppo_param_count(const talos_ppo_cfg* cfg);
+
+/* Opaque plans own device workspace sized for one configuration. */
+typedef struct talos_plan_s* talos_plan;
+
+/* One pre-norm block forward + backward for loss = sum(out * gout):
+ * writes out[batch*seq, d], dparams (same layout as params), dx. */
+int talos_block_plan_create(const talos_block_cfg* cfg, talos_plan* plan);
+int talos_block_fwd_bwd_f32(talos_plan plan, const float* params, const float* x, const float* gout, float* out,
+                            float* dparams, float* dx, talos_stream_t stream);
+
+/* PPO minibatch forward + backward (ppo.rs:686-757 for one minibatch, with the
+ * backbone evaluated once and the last-token gather differentiable): states[batch, seq, in_dim],
+ * actions[batch] (int32), adv/ret/old_logp[batch]. Writes the mean loss (device scalar,
+ * loss_out[0]) and dparams (overwritten, same layout as params). */
+int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan);
+int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* states, const int32_t* actions,
+                          const float* adv, const float* ret, const float* old_logp, float* loss_out,
+                          float* dparams, talos_stream_t stream);
+/* Forward only: logits[batch, A] and values[batch] of the policy (for old log-probs). */
+int talos_ppo_forward_f32(talos_plan plan, const float* params, const float* states, float* logits,
+                          float* values, talos_stream_t stream);
+
+int talos_plan_destroy(talos_plan plan);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TALOS_HIP_H */
