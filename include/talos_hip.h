@@ -2,15 +2,15 @@
  * talos_hip.h -- C ABI of the MI355X (gfx950) autograd hot path for Talos-XII's
  * transformer and linear policy layers.
  *
- * Every entry point takes plain pointers and sizes. Device pointers are fp32 (or
- * bf16 stored as uint16_t) buffers allocated with talos_malloc or any HIP allocator.
- * Streams are hipStream_t passed as void*; NULL means the calling thread's default
- * stream (hipStreamPerThread). Unless a name ends in _async, a call returns after its
- * work on that stream has finished, matching the synchronous semantics of the
- * reference's Tensor ops. Status codes: 0 on success, a talos_status otherwise;
- * talos_last_error() returns a thread-local message for the last failure.
- * Arguments are validated on the host before any launch, so every error path below
- * can be exercised on a machine without a GPU.
+ * Every entry point takes plain pointers and sizes. Device pointers are fp32 buffers
+ * allocated with talos_malloc or any HIP allocator. Streams are hipStream_t passed as void*;
+ * NULL is the null (default) stream. Kernel entry points enqueue their work on the stream and
+ * return without waiting (talos_stream_sync waits), as GPU libraries do; the host <-> device
+ * copies are synchronous. The reference's Tensor ops are synchronous (src/autograd.rs:200-354
+ * return finished host vectors); a caller that mirrors them syncs before reading results.
+ * Status codes: 0 on success, a talos_status otherwise; talos_last_error() returns a
+ * thread-local message for the last failure. Arguments are validated on the host before any
+ * launch, so every error path below can be exercised on a machine without a GPU.
  *
  * Reference citations are file:line in zayokami/Talos-XII (Rust crate, src/).
  */
@@ -56,11 +56,23 @@ int talos_free(void* ptr);
  * host vectors (Tensor.data / Tensor.grad, autograd.rs:14-20) and fp32 device buffers. */
 int talos_memcpy_h2d(void* dst, const void* src, size_t bytes, talos_stream_t stream);
 int talos_memcpy_d2h(void* dst, const void* src, size_t bytes, talos_stream_t stream);
+/* Device-to-device copy, enqueued on the stream. */
+int talos_memcpy_d2d(void* dst, const void* src, size_t bytes, talos_stream_t stream);
 int talos_memcpy_h2d_f64(float* dst, const double* src, size_t n, talos_stream_t stream);
 int talos_memcpy_d2h_f64(double* dst, const float* src, size_t n, talos_stream_t stream);
 /* Zero-fills with a kernel (no hipMemsetAsync, so it is safe inside a captured graph). */
 int talos_fill_zero(void* dst, size_t bytes, talos_stream_t stream);
 int talos_stream_sync(talos_stream_t stream);
+/* Non-blocking stream at the default priority. */
+int talos_stream_create(talos_stream_t* stream);
+int talos_stream_destroy(talos_stream_t stream);
+/* Events for timing the work of a stream: elapsed_ms waits for stop. */
+int talos_event_create(void** ev);
+int talos_event_destroy(void* ev);
+int talos_event_record(void* ev, talos_stream_t stream);
+int talos_event_elapsed_ms(void* start, void* stop, float* ms);
+/* Name (with gfx arch), compute-unit count, peak clock (kHz) and memory of device 0. */
+int talos_device_info(char* name, size_t name_len, int* cu_count, int* clock_khz, size_t* total_mem);
 
 /* ------------------------------------------------------------------------- */
 /* Kernel-level entry points (device pointers, fp32 unless stated)            */
@@ -71,18 +83,10 @@ int talos_stream_sync(talos_stream_t stream);
  * op(B) is B[K,N] (ldb >= N) when transB == 0, or the transpose of B stored [N,K] (ldb >= K).
  * Replaces Tensor::matmul (autograd.rs:200-354): forward C = A.B is (0,0); the backward
  * dA += dC.B^T is (0,1) with beta 1 and dB += A^T.dC is (1,0) with beta 1 (grads accumulate,
- * autograd.rs:290, 330). beta must be 0 or 1. MFMA v_mfma_f32_32x32x2f32 tiles. */
+ * autograd.rs:290, 330). beta must be 0 or 1. MFMA v_mfma_f32_32x32x2_f32 tiles; long-K
+ * products with a small C are split over K with the partial tiles summed in f64. */
 int talos_gemm_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
                    const float* B, int ldb, float beta, float* C, int ldc, talos_stream_t stream);
-
-/* Same contract with bf16 inputs (uint16_t bit patterns) and fp32 accumulation/output.
- * MFMA v_mfma_f32_32x32x16_bf16 tiles. No reference counterpart: the reference is f64 only
- * (autograd.rs:16-17); this is the bf16-in/fp32-acc variant of talos_gemm_f32. */
-int talos_gemm_bf16(int transA, int transB, int M, int N, int K, float alpha, const uint16_t* A, int lda,
-                    const uint16_t* B, int ldb, float beta, float* C, int ldc, talos_stream_t stream);
-
-/* Round-to-nearest-even fp32 -> bf16 conversion of n elements. */
-int talos_cast_f32_to_bf16(const float* x, uint16_t* y, size_t n, talos_stream_t stream);
 
 /* Batched C_b = alpha * A_b . op(B_b) + beta * C_b for b in [0,batch) with element strides
  * sA, sB, sC between consecutive matrices (same trans conventions as talos_gemm_f32).

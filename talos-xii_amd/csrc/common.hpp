@@ -1,0 +1,109 @@
+// common.hpp -- internal helpers shared by the HIP translation units of libtalos_hip.so:
+// status reporting, host-side argument validation and the small device utilities
+// (wave64 reductions, f64 partial combination) every kernel family uses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/talos_hip.h"
+
+namespace talos {
+
+// Thread-local message of the last failure (talos_last_error).
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+const char* last_error();
+
+// Lazily initialises the device context; returns TALOS_OK or TALOS_ERR_NO_DEVICE.
+int ensure_device();
+
+inline hipStream_t as_stream(talos_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Returns TALOS_ERR_HIP with the runtime's message when e != hipSuccess.
+int hip_status(hipError_t e, const char* what);
+
+// Checks the launch that was just enqueued.
+int launch_status(const char* kernel);
+
+}  // namespace talos
+
+// Host-side validation: every entry point checks its arguments before touching the device,
+// so the error paths run on machines without a GPU.
+#define TALOS_REQUIRE(cond, code, ...)   \
+  do {                                   \
+    if (!(cond)) {                       \
+      ::talos::set_error(__VA_ARGS__);   \
+      return (code);                     \
+    }                                    \
+  } while (0)
+
+#define TALOS_NONNULL(p) TALOS_REQUIRE((p) != nullptr, TALOS_ERR_NULL, "%s: null pointer argument '%s'", __func__, #p)
+
+#define TALOS_DEVICE()                          \
+  do {                                          \
+    int _rc = ::talos::ensure_device();         \
+    if (_rc != TALOS_OK) return _rc;            \
+  } while (0)
+
+#define TALOS_HIP(call)                                         \
+  do {                                                          \
+    int _rc = ::talos::hip_status((call), #call);               \
+    if (_rc != TALOS_OK) return _rc;                            \
+  } while (0)
+
+#define TALOS_LAUNCHED(name)                          \
+  do {                                                \
+    int _rc = ::talos::launch_status(name);           \
+    if (_rc != TALOS_OK) return _rc;                  \
+  } while (0)
+
+namespace talos {
+
+// ---------------------------------------------------------------------------
+// Device utilities
+// ---------------------------------------------------------------------------
+constexpr int kWave = 64;
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Block-wide sum for blockDim.x <= 1024 (multiple of 64); every thread gets the result.
+// red must hold blockDim.x / 64 elements.
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave, nw = blockDim.x / kWave;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  T t = 0;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
+__device__ __forceinline__ float gelu_f(float x) {
+  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+}
+// d/dx of x * Phi(x) = Phi(x) + x * phi(x)
+__device__ __forceinline__ float gelu_d(float x) {
+  const float cdf = 0.5f * (1.0f + erff(x * 0.70710678118654752f));
+  const float pdf = 0.39894228040143268f * expf(-0.5f * x * x);
+  return cdf + x * pdf;
+}
+
+inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace talos

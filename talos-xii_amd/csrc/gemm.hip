@@ -1,0 +1,474 @@
+// gemm.hip -- fp32 GEMM on CDNA4 matrix cores (v_mfma_f32_32x32x2_f32) for gfx950.
+//
+// Replaces the row-accumulation matmul of the reference and its backward
+// (src/autograd.rs:200-354): forward C = A.B, dA += dC.B^T, dB += A^T.dC, plus the batched
+// Q.K^T / P.V products of attention (src/transformer.rs:877-1050).
+//
+// Tiling: a 256-thread workgroup owns a 128x128 tile of C; each of its four waves owns a
+// 64x64 quarter as 2x2 MFMA 32x32 accumulators (64 accumulator registers per lane). K advances
+// in chunks of 32 staged through LDS as k-major panels As[k][m], Bs[k][n]; the next chunk is
+// fetched into registers while the matrix cores work on the current one. Both transposed and
+// plain operand layouts are read with 16-byte loads along their contiguous dimension.
+// Long-K products with a small C (the weight gradients, K = tokens) are split over K; the fp32
+// partial tiles are combined in f64 by a second kernel, which keeps the gradient sums over
+// 10^5 tokens within the accuracy of an fp32 dot product of length K/ksplit.
+#include "gemm.hpp"
+
+namespace talos {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int LDS_S = 160;  // panel row stride (floats): the two half-waves read rows k, k+1
+                            // whose offset 160 = 32 mod 64 keeps them on disjoint LDS banks
+constexpr int NT = 256;
+
+struct GemmArgs {
+  int M, N, K;
+  const float* A;
+  long long lda, sA;
+  const float* B;
+  long long ldb, sB;
+  float* C;
+  long long ldc, sC;
+  float alpha, beta;
+  const float* bias;
+  const float* resid;
+  long long ldr;
+  int act, dact;
+  float* aux;
+  long long ldaux;
+  const float* rcos;
+  const float* rsin;
+  int rope_cols, rope_dim, rope_seq;
+  int ksplit, kper;
+  float* part;
+  int vecA, vecB;
+};
+
+// Loads the op(A) panel [BM x BK] of chunk k0 into registers.
+template <bool TA>
+__device__ __forceinline__ void load_a(const GemmArgs& p, const float* __restrict__ A, int m0, int k0, int kend,
+                                       float4 (&r)[4]) {
+  const int t = threadIdx.x;
+  if (!TA) {
+    const int m = m0 + (t & 127);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = k0 + 4 * ((t >> 7) + 2 * i);
+      const float* src = A + (long long)m * p.lda + k;
+      if (p.vecA && m < p.M && k + 3 < kend) {
+        r[i] = *reinterpret_cast<const float4*>(src);
+      } else {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (m < p.M && k + j < kend) ? src[j] : 0.f;
+        r[i] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  } else {
+    const int m = m0 + 4 * (t & 31);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = k0 + (t >> 5) + 8 * i;
+      const float* src = A + (long long)k * p.lda + m;
+      if (p.vecA && k < kend && m + 3 < p.M) {
+        r[i] = *reinterpret_cast<const float4*>(src);
+      } else {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (k < kend && m + j < p.M) ? src[j] : 0.f;
+        r[i] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  }
+}
+
+template <bool TA>
+__device__ __forceinline__ void store_a(float* As, const float4 (&r)[4]) {
+  const int t = threadIdx.x;
+  if (!TA) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kk = 4 * ((t >> 7) + 2 * i);
+      float* d = As + kk * LDS_S + (t & 127);
+      d[0] = r[i].x;
+      d[LDS_S] = r[i].y;
+      d[2 * LDS_S] = r[i].z;
+      d[3 * LDS_S] = r[i].w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kk = (t >> 5) + 8 * i;
+      *reinterpret_cast<float4*>(As + kk * LDS_S + 4 * (t & 31)) = r[i];
+    }
+  }
+}
+
+// op(B) panel [BK x BN]: transB = 0 is the same access pattern as transA = 1 and vice versa.
+template <bool TB>
+__device__ __forceinline__ void load_b(const GemmArgs& p, const float* __restrict__ B, int n0, int k0, int kend,
+                                       float4 (&r)[4]) {
+  const int t = threadIdx.x;
+  if (TB) {
+    const int n = n0 + (t & 127);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = k0 + 4 * ((t >> 7) + 2 * i);
+      const float* src = B + (long long)n * p.ldb + k;
+      if (p.vecB && n < p.N && k + 3 < kend) {
+        r[i] = *reinterpret_cast<const float4*>(src);
+      } else {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (n < p.N && k + j < kend) ? src[j] : 0.f;
+        r[i] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  } else {
+    const int n = n0 + 4 * (t & 31);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = k0 + (t >> 5) + 8 * i;
+      const float* src = B + (long long)k * p.ldb + n;
+      if (p.vecB && k < kend && n + 3 < p.N) {
+        r[i] = *reinterpret_cast<const float4*>(src);
+      } else {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (k < kend && n + j < p.N) ? src[j] : 0.f;
+        r[i] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  }
+}
+
+template <bool TB>
+__device__ __forceinline__ void store_b(float* Bs, const float4 (&r)[4]) {
+  store_a<!TB>(Bs, r);
+}
+
+// Epilogue of one element (everything but RoPE, which needs the neighbouring lane).
+__device__ __forceinline__ float epi_value(const GemmArgs& p, float acc, int row, int col, float* __restrict__ C,
+                                           const float* __restrict__ resid, float* __restrict__ aux) {
+  float v = p.alpha * acc;
+  if (p.beta != 0.f) v += p.beta * C[(long long)row * p.ldc + col];
+  if (p.bias) v += p.bias[col];
+  if (resid) v += resid[(long long)row * p.ldr + col];
+  if (p.dact == GEMM_DACT_GELU) {
+    v *= gelu_d(aux[(long long)row * p.ldaux + col]);
+  } else if (p.dact == GEMM_DACT_RELU) {
+    v = aux[(long long)row * p.ldaux + col] > 0.f ? v : 0.f;
+  }
+  if (p.act != GEMM_ACT_NONE) {
+    if (aux) aux[(long long)row * p.ldaux + col] = v;
+    v = p.act == GEMM_ACT_GELU ? gelu_f(v) : fmaxf(v, 0.f);
+  }
+  return v;
+}
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
+  __shared__ float As[BK * LDS_S];
+  __shared__ float Bs[BK * LDS_S];
+
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int m0 = (blockIdx.x / tiles_n) * BM;
+  const int n0 = (blockIdx.x % tiles_n) * BN;
+  const int bz = blockIdx.y;
+  const int b = bz / p.ksplit, split = bz % p.ksplit;
+  const float* A = p.A + (long long)b * p.sA;
+  const float* B = p.B + (long long)b * p.sB;
+  const int kbeg = split * p.kper;
+  const int kend = min(p.K, kbeg + p.kper);
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  const int l32 = lane & 31, h = lane >> 5;
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  float4 ra[4], rb[4];
+  if (kbeg < kend) {
+    load_a<TA>(p, A, m0, kbeg, kend, ra);
+    load_b<TB>(p, B, n0, kbeg, kend, rb);
+    store_a<TA>(As, ra);
+    store_b<TB>(Bs, rb);
+  }
+  __syncthreads();
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+    const bool more = k0 + BK < kend;
+    if (more) {
+      load_a<TA>(p, A, m0, k0 + BK, kend, ra);
+      load_b<TB>(p, B, n0, k0 + BK, kend, rb);
+    }
+    const float* ap = As + h * LDS_S + wm * 64 + l32;
+    const float* bp = Bs + h * LDS_S + wn * 64 + l32;
+#pragma unroll
+    for (int s = 0; s < BK / 2; ++s) {
+      const float a0 = ap[2 * s * LDS_S], a1 = ap[2 * s * LDS_S + 32];
+      const float b0 = bp[2 * s * LDS_S], b1 = bp[2 * s * LDS_S + 32];
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+    }
+    __syncthreads();
+    if (more) {
+      store_a<TA>(As, ra);
+      store_b<TB>(Bs, rb);
+      __syncthreads();
+    }
+  }
+
+  // Accumulator layout of v_mfma_f32_32x32x2_f32: lane l, register r holds
+  // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 block.
+  if (p.ksplit > 1) {
+    float* P = p.part + ((long long)b * p.ksplit + split) * (long long)p.M * p.N;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const int col = n0 + wn * 64 + nt * 32 + l32;
+          if (row < p.M && col < p.N) P[(long long)row * p.N + col] = acc[mt][nt][r];
+        }
+    return;
+  }
+  float* C = p.C + (long long)b * p.sC;
+  const float* resid = p.resid ? p.resid + (long long)b * p.sC : nullptr;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int col = n0 + wn * 64 + nt * 32 + l32;
+        float v = acc[mt][nt][r];
+        if (p.rope_cols > 0) {
+          // interleaved pair (2i, 2i+1) of a head: the partner column is the neighbouring lane
+          const float partner = __shfl_xor(v, 1, 64);
+          if (col < p.rope_cols) {
+            const int half = p.rope_dim >> 1;
+            const int pi = (col % p.rope_dim) >> 1;
+            const int pos = row % p.rope_seq;
+            const float c = p.rcos[pos * half + pi], s = p.rsin[pos * half + pi];
+            v = (col & 1) ? fmaf(partner, s, v * c) : fmaf(v, c, -partner * s);
+          }
+        }
+        if (row < p.M && col < p.N) C[(long long)row * p.ldc + col] = epi_value(p, v, row, col, C, resid, p.aux);
+      }
+}
+
+// Sums the split-K partials in f64 and applies the epilogue.
+__global__ void gemm_splitk_reduce(GemmArgs p) {
+  const long long MN = (long long)p.M * p.N;
+  const long long total = MN * (p.ksplit > 0 ? 1 : 1);
+  const int b = blockIdx.y;
+  const float* P = p.part + (long long)b * p.ksplit * MN;
+  float* C = p.C + (long long)b * p.sC;
+  const float* resid = p.resid ? p.resid + (long long)b * p.sC : nullptr;
+  for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (long long)gridDim.x * blockDim.x) {
+    double s = 0.0;
+    for (int k = 0; k < p.ksplit; ++k) s += (double)P[k * MN + e];
+    const int row = (int)(e / p.N), col = (int)(e % p.N);
+    C[(long long)row * p.ldc + col] = epi_value(p, (float)s, row, col, C, resid, p.aux);
+  }
+}
+
+static GemmArgs to_args(const GemmDesc& d) {
+  GemmArgs a;
+  a.M = d.M;
+  a.N = d.N;
+  a.K = d.K;
+  a.A = d.A;
+  a.lda = d.lda;
+  a.sA = d.sA;
+  a.B = d.B;
+  a.ldb = d.ldb;
+  a.sB = d.sB;
+  a.C = d.C;
+  a.ldc = d.ldc;
+  a.sC = d.sC;
+  a.alpha = d.alpha;
+  a.beta = d.beta;
+  a.bias = d.bias;
+  a.resid = d.resid;
+  a.ldr = d.ldr;
+  a.act = d.act;
+  a.dact = d.dact;
+  a.aux = d.aux;
+  a.ldaux = d.ldaux;
+  a.rcos = d.rope_cos;
+  a.rsin = d.rope_sin;
+  a.rope_cols = d.rope_cols;
+  a.rope_dim = d.rope_dim > 0 ? d.rope_dim : 2;
+  a.rope_seq = d.rope_seq > 0 ? d.rope_seq : 1;
+  a.ksplit = d.ksplit < 1 ? 1 : d.ksplit;
+  a.kper = d.K;
+  a.part = d.workspace;
+  auto aligned = [](const void* ptr, long long ld) {
+    return ((reinterpret_cast<uintptr_t>(ptr) & 15) == 0) && (ld % 4 == 0);
+  };
+  a.vecA = aligned(d.A, d.lda) && (d.batch == 1 || d.sA % 4 == 0);
+  a.vecB = aligned(d.B, d.ldb) && (d.batch == 1 || d.sB % 4 == 0);
+  if (a.ksplit > 1) {
+    int kper = (d.K + a.ksplit - 1) / a.ksplit;
+    kper = (kper + BK - 1) / BK * BK;
+    a.kper = kper;
+    a.ksplit = (d.K + kper - 1) / kper;
+  }
+  return a;
+}
+
+size_t gemm_plan_split(GemmDesc& d, int num_cu) {
+  if (d.ksplit == 0) {
+    const long long tiles = (long long)((d.M + BM - 1) / BM) * ((d.N + BN - 1) / BN) * d.batch;
+    int ks = 1;
+    // Split until the grid fills the CUs once, keeping >= 512 of K per split: fewer, longer
+    // splits keep the partial traffic (ksplit * M * N floats) small next to A and B.
+    while (tiles * ks * 2 <= (long long)num_cu && (long long)d.K / (ks * 2) >= 512) ks *= 2;
+    d.ksplit = ks;
+  }
+  if (d.rope_cols > 0 || d.act != GEMM_ACT_NONE) d.ksplit = 1;
+  if (d.ksplit <= 1) return 0;
+  GemmArgs a = to_args(d);
+  return (size_t)a.ksplit * d.M * d.N * d.batch * sizeof(float);
+}
+
+int gemm_launch(const GemmDesc& d, hipStream_t stream) {
+  GemmArgs a = to_args(d);
+  if (d.M == 0 || d.N == 0 || d.batch == 0) return TALOS_OK;
+  const unsigned tiles = ceil_div(d.M, BM) * ceil_div(d.N, BN);
+  dim3 grid(tiles, d.batch * a.ksplit);
+  if (d.K == 0) {
+    // C = beta*C (+ epilogue): run the kernel with an empty K loop.
+    a.ksplit = 1;
+    a.kper = 0;
+    grid.y = d.batch;
+  }
+  const int key = (d.transA ? 2 : 0) | (d.transB ? 1 : 0);
+  switch (key) {
+    case 0: hipLaunchKernelGGL((gemm_f32_kernel<false, false>), grid, dim3(NT), 0, stream, a); break;
+    case 1: hipLaunchKernelGGL((gemm_f32_kernel<false, true>), grid, dim3(NT), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((gemm_f32_kernel<true, false>), grid, dim3(NT), 0, stream, a); break;
+    default: hipLaunchKernelGGL((gemm_f32_kernel<true, true>), grid, dim3(NT), 0, stream, a); break;
+  }
+  TALOS_LAUNCHED("gemm_f32_kernel");
+  if (a.ksplit > 1) {
+    const long long MN = (long long)d.M * d.N;
+    dim3 rg((unsigned)std::min<long long>((MN + 255) / 256, 4096), d.batch);
+    hipLaunchKernelGGL(gemm_splitk_reduce, rg, dim3(256), 0, stream, a);
+    TALOS_LAUNCHED("gemm_splitk_reduce");
+  }
+  return TALOS_OK;
+}
+
+static int num_cus() {
+  static int n = -1;
+  if (n < 0) {
+    hipDeviceProp_t prop;
+    n = (hipGetDeviceProperties(&prop, 0) == hipSuccess) ? prop.multiProcessorCount : 256;
+  }
+  return n;
+}
+
+// Host validation shared by the kernel-level GEMM entry points.
+static int check_gemm(const char* fn, int transA, int transB, int M, int N, int K, const void* A, long long lda,
+                      const void* B, long long ldb, float beta, const void* C, long long ldc, int batch) {
+  TALOS_REQUIRE(A && B && C, TALOS_ERR_NULL, "%s: null matrix pointer", fn);
+  TALOS_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, TALOS_ERR_SHAPE, "%s: negative size (M=%d N=%d K=%d batch=%d)",
+                fn, M, N, K, batch);
+  TALOS_REQUIRE((transA == 0 || transA == 1) && (transB == 0 || transB == 1), TALOS_ERR_DTYPE,
+                "%s: trans flags must be 0 or 1", fn);
+  TALOS_REQUIRE(lda >= (transA ? M : K) && lda >= 1, TALOS_ERR_SHAPE, "%s: lda=%lld too small for %s A", fn, lda,
+                transA ? "transposed" : "plain");
+  TALOS_REQUIRE(ldb >= (transB ? K : N) && ldb >= 1, TALOS_ERR_SHAPE, "%s: ldb=%lld too small for %s B", fn, ldb,
+                transB ? "transposed" : "plain");
+  TALOS_REQUIRE(ldc >= N && ldc >= 1, TALOS_ERR_SHAPE, "%s: ldc=%lld < N=%d", fn, ldc, N);
+  TALOS_REQUIRE(beta == 0.f || beta == 1.f, TALOS_ERR_UNSUPPORTED, "%s: beta must be 0 or 1 (got %g)", fn, beta);
+  return TALOS_OK;
+}
+
+static int run_gemm(GemmDesc& d, hipStream_t stream) {
+  const size_t ws = gemm_plan_split(d, num_cus());
+  if (ws) {
+    TALOS_HIP(hipMallocAsync(reinterpret_cast<void**>(&d.workspace), ws, stream));
+  }
+  int rc = gemm_launch(d, stream);
+  if (ws) {
+    hipError_t e = hipFreeAsync(d.workspace, stream);
+    if (rc == TALOS_OK) rc = hip_status(e, "hipFreeAsync");
+  }
+  return rc;
+}
+
+}  // namespace talos
+
+using namespace talos;
+
+extern "C" {
+
+int talos_gemm_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda, const float* B,
+                   int ldb, float beta, float* C, int ldc, talos_stream_t stream) {
+  int rc = check_gemm(__func__, transA, transB, M, N, K, A, lda, B, ldb, beta, C, ldc, 1);
+  if (rc) return rc;
+  TALOS_DEVICE();
+  GemmDesc d;
+  d.transA = transA;
+  d.transB = transB;
+  d.M = M;
+  d.N = N;
+  d.K = K;
+  d.A = A;
+  d.lda = lda;
+  d.B = B;
+  d.ldb = ldb;
+  d.C = C;
+  d.ldc = ldc;
+  d.alpha = alpha;
+  d.beta = beta;
+  d.ksplit = 0;
+  return run_gemm(d, as_stream(stream));
+}
+
+int talos_gemm_batched_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
+                           long long sA, const float* B, int ldb, long long sB, float beta, float* C, int ldc,
+                           long long sC, int batch, talos_stream_t stream) {
+  int rc = check_gemm(__func__, transA, transB, M, N, K, A, lda, B, ldb, beta, C, ldc, batch);
+  if (rc) return rc;
+  TALOS_REQUIRE(sA >= 0 && sB >= 0 && sC >= 0, TALOS_ERR_SHAPE, "%s: negative batch stride", __func__);
+  TALOS_DEVICE();
+  GemmDesc d;
+  d.transA = transA;
+  d.transB = transB;
+  d.M = M;
+  d.N = N;
+  d.K = K;
+  d.batch = batch;
+  d.A = A;
+  d.lda = lda;
+  d.sA = sA;
+  d.B = B;
+  d.ldb = ldb;
+  d.sB = sB;
+  d.C = C;
+  d.ldc = ldc;
+  d.sC = sC;
+  d.alpha = alpha;
+  d.beta = beta;
+  d.ksplit = 0;
+  return run_gemm(d, as_stream(stream));
+}
+
+}  // extern "C"

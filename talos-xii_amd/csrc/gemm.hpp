@@ -1,0 +1,51 @@
+// gemm.hpp -- internal interface of the fp32 MFMA GEMM (gemm.hip) used by the kernel-level
+// entry points and by the fused block / policy plans.
+#pragma once
+
+#include "common.hpp"
+
+namespace talos {
+
+enum GemmAct { GEMM_ACT_NONE = 0, GEMM_ACT_GELU = 1, GEMM_ACT_RELU = 2 };
+// Epilogue multiplier of the backward of an activation: C = acc * act'(aux).
+enum GemmDAct { GEMM_DACT_NONE = 0, GEMM_DACT_GELU = 1, GEMM_DACT_RELU = 2 };
+
+// C[b][M,N] = alpha * op(A[b]) . op(B[b]) + beta * C[b]  (+ bias[N]) (+ resid[M,N]),
+// then optionally act(.) with the pre-activation stored to aux, or the activation derivative
+// act'(aux) multiplied in; RoPE on columns [0, rope_cols) with position row % rope_seq.
+// Row-major storage; op(A) is [M,K]: A[m*lda + k] (transA = 0) or A[k*lda + m] (transA = 1);
+// op(B) is [K,N]: B[k*ldb + n] (transB = 0) or B[n*ldb + k] (transB = 1).
+struct GemmDesc {
+  int transA = 0, transB = 0;
+  int M = 0, N = 0, K = 0;
+  int batch = 1;
+  const float* A = nullptr;
+  long long lda = 0, sA = 0;
+  const float* B = nullptr;
+  long long ldb = 0, sB = 0;
+  float* C = nullptr;
+  long long ldc = 0, sC = 0;
+  float alpha = 1.f, beta = 0.f;
+  const float* bias = nullptr;
+  const float* resid = nullptr;
+  long long ldr = 0;
+  int act = GEMM_ACT_NONE;
+  int dact = GEMM_DACT_NONE;
+  float* aux = nullptr;  // act: pre-activation output; dact: pre-activation input
+  long long ldaux = 0;
+  // RoPE epilogue (interleaved pairs (2i, 2i+1) inside each rot_dim-wide head)
+  const float* rope_cos = nullptr;
+  const float* rope_sin = nullptr;
+  int rope_cols = 0, rope_dim = 0, rope_seq = 1;
+  // Split-K: the K range is cut into ksplit parts of kper (multiple of 32) whose fp32 partial
+  // tiles are summed in f64 by a second kernel. ksplit = 0 lets the library choose.
+  int ksplit = 1;
+  float* workspace = nullptr;  // >= gemm_workspace_bytes(desc) when ksplit > 1
+};
+
+// Fills in ksplit (when 0) and returns the workspace bytes the descriptor needs.
+size_t gemm_plan_split(GemmDesc& d, int num_cu);
+// Enqueues the GEMM. Validation of shapes and pointers is the caller's job.
+int gemm_launch(const GemmDesc& d, hipStream_t stream);
+
+}  // namespace talos

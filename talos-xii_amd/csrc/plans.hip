@@ -1,0 +1,741 @@
+// plans.hip -- fused pre-norm transformer block and PPO policy forward + backward.
+//
+// A plan owns every device buffer one configuration needs (saved activations, gradient
+// scratch, split-K partials, the RoPE table), so a training step allocates nothing.
+//
+// Block (talos_block_cfg; the wiring of LuckTransformer::forward, src/transformer.rs:71-90, with
+// standard multi-head attention in place of MLA):
+//   xn1 = rmsnorm(x; g1)                       rowops  (rstd saved)
+//   qkv = xn1 . Wqkv, RoPE on the q|k columns   GEMM, RoPE in the epilogue
+//   o   = attention(q, k, v)                    fused attention (lse saved)
+//   h2  = x + o . Wo                            GEMM, residual in the epilogue
+//   xn2 = rmsnorm(h2; g2)
+//   a   = act(xn2 . W1 + b1)                    GEMM, bias + activation epilogue (u saved)
+//   out = h2 + a . W2 + b2                      GEMM, bias + residual epilogue
+// and the backward in reverse, with weight gradients as split-K GEMMs (f64 partial sums) and
+// the activation derivative / RoPE^T folded into the producing kernels.
+//
+// Policy (talos_ppo_cfg; ActorCritic, src/ppo.rs:246-307): embed Linear -> blocks -> last token
+// -> RMSNorm -> out_proj -> actor / critic Linear heads -> clipped PPO loss (src/ppo.rs:691-756).
+// The final RMSNorm and out_proj act on each token independently and only the last token of a
+// sequence reaches the heads, so they run on the B last-token rows (same result as running them
+// on all B*S tokens and gathering afterwards, as the reference does).
+#include <cmath>
+#include <vector>
+
+#include "attention.hpp"
+#include "gemm.hpp"
+#include "rowops.hpp"
+
+struct talos_plan_s {
+  int kind = 0;  // 1 block, 2 ppo
+  talos_block_cfg blk{};
+  talos_ppo_cfg ppo{};
+  std::vector<void*> allocs;
+  // rope table [seq, head_dim/2]
+  float* rcos = nullptr;
+  float* rsin = nullptr;
+  // per layer saved activations
+  struct Layer {
+    float *x, *xn1, *rstd1, *qkv, *o, *lse, *h2, *xn2, *rstd2, *u, *a, *out;
+  };
+  std::vector<Layer> layers;
+  // backward scratch
+  float *g_out = nullptr, *g_h2 = nullptr, *g_u = nullptr, *g_xn = nullptr, *g_o = nullptr, *g_qkv = nullptr,
+        *g_x = nullptr;
+  float* attn_ws = nullptr;
+  float* gemm_ws = nullptr;
+  size_t gemm_ws_bytes = 0;
+  double* red_ws = nullptr;
+  size_t red_ws_bytes = 0;
+  // ppo
+  float *h0 = nullptr, *last = nullptr, *lastn = nullptr, *rstdf = nullptr, *pout = nullptr, *logits = nullptr,
+        *values = nullptr, *g_logits = nullptr, *g_values = nullptr, *g_pout = nullptr, *g_lastn = nullptr,
+        *g_last = nullptr;
+  double* loss_ws = nullptr;
+  int num_cu = 256;
+};
+
+namespace talos {
+
+static size_t block_params(const talos_block_cfg& c) {
+  const size_t d = c.d_model, F = c.ffn_dim;
+  return d + 3 * d * d + d * d + d + d * F + F + F * d + d;
+}
+
+static size_t ppo_params(const talos_ppo_cfg& c) {
+  const size_t d = c.d_model, F = c.ffn_dim;
+  const size_t blk = d + 3 * d * d + d * d + d + d * F + F + F * d + d;
+  return (size_t)c.in_dim * d + d + (size_t)c.n_layers * blk + d + d * d + d + d * (size_t)c.n_actions +
+         (size_t)c.n_actions + d + 1;
+}
+
+// Offsets of one block's parameters inside a flat buffer.
+struct BlockOff {
+  size_t g1, wqkv, wo, g2, w1, b1, w2, b2, end;
+};
+static BlockOff block_offsets(const talos_block_cfg& c, size_t base) {
+  const size_t d = c.d_model, F = c.ffn_dim;
+  BlockOff o;
+  o.g1 = base;
+  o.wqkv = o.g1 + d;
+  o.wo = o.wqkv + 3 * d * d;
+  o.g2 = o.wo + d * d;
+  o.w1 = o.g2 + d;
+  o.b1 = o.w1 + d * F;
+  o.w2 = o.b1 + F;
+  o.b2 = o.w2 + F * d;
+  o.end = o.b2 + d;
+  return o;
+}
+
+struct PpoOff {
+  size_t we, be, blocks, gf, wout, bout, wa, ba, wc, bc, end;
+};
+static PpoOff ppo_offsets(const talos_ppo_cfg& c) {
+  const size_t d = c.d_model;
+  PpoOff o;
+  o.we = 0;
+  o.be = (size_t)c.in_dim * d;
+  o.blocks = o.be + d;
+  talos_block_cfg bc{};
+  bc.d_model = c.d_model;
+  bc.ffn_dim = c.ffn_dim;
+  o.gf = o.blocks + (size_t)c.n_layers * block_params(bc);
+  o.wout = o.gf + d;
+  o.bout = o.wout + d * d;
+  o.wa = o.bout + d;
+  o.ba = o.wa + d * (size_t)c.n_actions;
+  o.wc = o.ba + c.n_actions;
+  o.bc = o.wc + d;
+  o.end = o.bc + 1;
+  return o;
+}
+
+static int check_block_cfg(const talos_block_cfg& c) {
+  TALOS_REQUIRE(c.batch > 0 && c.seq > 0 && c.d_model > 0 && c.n_heads > 0 && c.head_dim > 0 && c.ffn_dim > 0,
+                TALOS_ERR_SHAPE, "block cfg: sizes must be positive");
+  TALOS_REQUIRE(c.n_heads * c.head_dim == c.d_model, TALOS_ERR_SHAPE, "block cfg: n_heads * head_dim (%d * %d) != d_model %d",
+                c.n_heads, c.head_dim, c.d_model);
+  TALOS_REQUIRE(c.head_dim % 2 == 0, TALOS_ERR_SHAPE, "block cfg: head_dim must be even for RoPE pairs");
+  TALOS_REQUIRE(c.head_dim <= 128, TALOS_ERR_UNSUPPORTED, "block cfg: head_dim %d > 128", c.head_dim);
+  TALOS_REQUIRE(c.causal == 0 || c.causal == 1, TALOS_ERR_DTYPE, "block cfg: causal must be 0 or 1");
+  TALOS_REQUIRE(c.activation == TALOS_ACT_GELU || c.activation == TALOS_ACT_RELU, TALOS_ERR_DTYPE,
+                "block cfg: unknown activation %d", c.activation);
+  TALOS_REQUIRE(c.d_model % 4 == 0 && c.ffn_dim % 4 == 0, TALOS_ERR_UNSUPPORTED,
+                "block cfg: d_model and ffn_dim must be multiples of 4");
+  TALOS_REQUIRE(c.eps >= 0.f && c.rope_base > 0.f, TALOS_ERR_SHAPE, "block cfg: eps >= 0 and rope_base > 0 required");
+  TALOS_REQUIRE((long long)c.batch * c.seq * (3LL * c.d_model) < (1LL << 31), TALOS_ERR_UNSUPPORTED,
+                "block cfg: batch*seq*3*d_model must stay below 2^31 elements");
+  return TALOS_OK;
+}
+
+static talos_block_cfg block_cfg_of(const talos_ppo_cfg& p) {
+  talos_block_cfg c{};
+  c.batch = p.batch;
+  c.seq = p.seq;
+  c.d_model = p.d_model;
+  c.n_heads = p.n_heads;
+  c.head_dim = p.head_dim;
+  c.ffn_dim = p.ffn_dim;
+  c.causal = p.causal;
+  c.activation = p.activation;
+  c.eps = p.eps;
+  c.rope_base = p.rope_base;
+  return c;
+}
+
+static int plan_alloc(talos_plan_s* p, float** out, size_t n) {
+  void* ptr = nullptr;
+  if (n == 0) n = 1;
+  hipError_t e = hipMalloc(&ptr, n * sizeof(float));
+  if (e != hipSuccess) {
+    set_error("plan allocation of %zu floats failed: %s", n, hipGetErrorString(e));
+    return TALOS_ERR_ALLOC;
+  }
+  p->allocs.push_back(ptr);
+  *out = static_cast<float*>(ptr);
+  return TALOS_OK;
+}
+
+static void plan_free(talos_plan_s* p) {
+  for (void* a : p->allocs) (void)hipFree(a);
+  p->allocs.clear();
+}
+
+// Largest split-K workspace among the weight-gradient GEMMs of a configuration.
+static size_t wgrad_ws(talos_plan_s* p, int M_tok, int rows, int cols) {
+  GemmDesc g;
+  g.transA = 1;
+  g.M = rows;
+  g.N = cols;
+  g.K = M_tok;
+  g.ksplit = 0;
+  return gemm_plan_split(g, p->num_cu);
+}
+
+static int alloc_block_buffers(talos_plan_s* p, const talos_block_cfg& c, int n_layers, bool own_input) {
+  const size_t M = (size_t)c.batch * c.seq, d = c.d_model, F = c.ffn_dim;
+  p->layers.resize(n_layers);
+  for (int l = 0; l < n_layers; ++l) {
+    auto& L = p->layers[l];
+    int rc = 0;
+    L.x = nullptr;
+    if (own_input || l > 0) {
+      // x of layer l is the out of layer l-1 (set below) except for the first layer
+    }
+    rc |= plan_alloc(p, &L.xn1, M * d);
+    rc |= plan_alloc(p, &L.rstd1, M);
+    rc |= plan_alloc(p, &L.qkv, M * 3 * d);
+    rc |= plan_alloc(p, &L.o, M * d);
+    rc |= plan_alloc(p, &L.lse, M * c.n_heads);
+    rc |= plan_alloc(p, &L.h2, M * d);
+    rc |= plan_alloc(p, &L.xn2, M * d);
+    rc |= plan_alloc(p, &L.rstd2, M);
+    rc |= plan_alloc(p, &L.u, M * F);
+    rc |= plan_alloc(p, &L.a, M * F);
+    rc |= plan_alloc(p, &L.out, M * d);
+    if (rc) return TALOS_ERR_ALLOC;
+  }
+  int rc = 0;
+  rc |= plan_alloc(p, &p->g_out, M * d);
+  rc |= plan_alloc(p, &p->g_h2, M * d);
+  rc |= plan_alloc(p, &p->g_u, M * F);
+  rc |= plan_alloc(p, &p->g_xn, M * d);
+  rc |= plan_alloc(p, &p->g_o, M * d);
+  rc |= plan_alloc(p, &p->g_qkv, M * 3 * d);
+  rc |= plan_alloc(p, &p->g_x, M * d);
+  rc |= plan_alloc(p, &p->attn_ws, M * c.n_heads);
+  if (rc) return TALOS_ERR_ALLOC;
+  size_t ws = 0;
+  ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, 3 * (int)d));
+  ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, (int)d));
+  ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, (int)F));
+  ws = std::max(ws, wgrad_ws(p, (int)M, (int)F, (int)d));
+  p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, ws);
+  size_t red = std::max(colsum_workspace_bytes((int)M, (int)F), rmsnorm_bwd_workspace_bytes((int)M, (int)d));
+  p->red_ws_bytes = std::max(p->red_ws_bytes, red);
+  // rope table
+  std::vector<float> cs, sn;
+  rope_table_host(c.seq, c.head_dim, (double)c.rope_base, cs, sn);
+  rc |= plan_alloc(p, &p->rcos, cs.size());
+  rc |= plan_alloc(p, &p->rsin, sn.size());
+  if (rc) return TALOS_ERR_ALLOC;
+  TALOS_HIP(hipMemcpy(p->rcos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  TALOS_HIP(hipMemcpy(p->rsin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  return TALOS_OK;
+}
+
+static int alloc_workspaces(talos_plan_s* p) {
+  int rc = 0;
+  rc |= plan_alloc(p, &p->gemm_ws, (p->gemm_ws_bytes + 3) / 4);
+  float* red = nullptr;
+  rc |= plan_alloc(p, &red, (p->red_ws_bytes + 3) / 4 + 2);
+  p->red_ws = reinterpret_cast<double*>(red);
+  return rc ? TALOS_ERR_ALLOC : TALOS_OK;
+}
+
+// GEMM helpers ---------------------------------------------------------------
+static int mm(talos_plan_s* p, hipStream_t s, int tA, int tB, int M, int N, int K, const float* A, long long lda,
+              const float* B, long long ldb, float* C, long long ldc, float beta = 0.f, const float* bias = nullptr,
+              const float* resid = nullptr, long long ldr = 0) {
+  GemmDesc g;
+  g.transA = tA;
+  g.transB = tB;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.A = A;
+  g.lda = lda;
+  g.B = B;
+  g.ldb = ldb;
+  g.C = C;
+  g.ldc = ldc;
+  g.beta = beta;
+  g.bias = bias;
+  g.resid = resid;
+  g.ldr = ldr;
+  g.ksplit = 0;
+  const size_t ws = gemm_plan_split(g, p->num_cu);
+  if (ws > p->gemm_ws_bytes) {
+    set_error("internal: split-K workspace %zu > planned %zu", ws, p->gemm_ws_bytes);
+    return TALOS_ERR_UNSUPPORTED;
+  }
+  g.workspace = p->gemm_ws;
+  return gemm_launch(g, s);
+}
+
+// Forward of one block; L.x must be set. Writes L.out.
+static int block_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
+                         talos_plan_s::Layer& L, hipStream_t s) {
+  const int M = c.batch * c.seq, d = c.d_model, F = c.ffn_dim;
+  int rc = rmsnorm_fwd_launch(M, d, c.eps, L.x, P + o.g1, L.xn1, L.rstd1, s);
+  if (rc) return rc;
+  {
+    GemmDesc g;
+    g.M = M;
+    g.N = 3 * d;
+    g.K = d;
+    g.A = L.xn1;
+    g.lda = d;
+    g.B = P + o.wqkv;
+    g.ldb = 3 * d;
+    g.C = L.qkv;
+    g.ldc = 3 * d;
+    g.rope_cos = p->rcos;
+    g.rope_sin = p->rsin;
+    g.rope_cols = 2 * d;
+    g.rope_dim = c.head_dim;
+    g.rope_seq = c.seq;
+    g.ksplit = 1;
+    rc = gemm_launch(g, s);
+    if (rc) return rc;
+  }
+  {
+    AttnDesc a;
+    a.batch = c.batch;
+    a.seq = c.seq;
+    a.heads = c.n_heads;
+    a.dk = a.dv = c.head_dim;
+    a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+    a.causal = c.causal;
+    a.q = L.qkv;
+    a.k = L.qkv + d;
+    a.v = L.qkv + 2 * d;
+    a.ldq = a.ldk = a.ldv = 3 * d;
+    a.o = L.o;
+    a.ldo = d;
+    a.lse = L.lse;
+    rc = attn_fwd_launch(a, s);
+    if (rc) return rc;
+  }
+  rc = mm(p, s, 0, 0, M, d, d, L.o, d, P + o.wo, d, L.h2, d, 0.f, nullptr, L.x, d);
+  if (rc) return rc;
+  rc = rmsnorm_fwd_launch(M, d, c.eps, L.h2, P + o.g2, L.xn2, L.rstd2, s);
+  if (rc) return rc;
+  {
+    GemmDesc g;
+    g.M = M;
+    g.N = F;
+    g.K = d;
+    g.A = L.xn2;
+    g.lda = d;
+    g.B = P + o.w1;
+    g.ldb = F;
+    g.C = L.a;
+    g.ldc = F;
+    g.bias = P + o.b1;
+    g.act = c.activation == TALOS_ACT_GELU ? GEMM_ACT_GELU : GEMM_ACT_RELU;
+    g.aux = L.u;
+    g.ldaux = F;
+    g.ksplit = 1;
+    rc = gemm_launch(g, s);
+    if (rc) return rc;
+  }
+  return mm(p, s, 0, 0, M, d, F, L.a, F, P + o.w2, d, L.out, d, 0.f, P + o.b2, L.h2, d);
+}
+
+// Backward of one block: gout = dL/dout (read), writes dparams slots and dx.
+static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
+                          talos_plan_s::Layer& L, const float* gout, float* dx, hipStream_t s) {
+  const int M = c.batch * c.seq, d = c.d_model, F = c.ffn_dim;
+  int rc;
+  // out = h2 + a.W2 + b2
+  rc = mm(p, s, 1, 0, F, d, M, L.a, F, gout, d, G + o.w2, d);
+  if (rc) return rc;
+  rc = colsum_launch(M, d, gout, d, 0.f, G + o.b2, p->red_ws, s);
+  if (rc) return rc;
+  {
+    GemmDesc g;
+    g.transB = 1;
+    g.M = M;
+    g.N = F;
+    g.K = d;
+    g.A = gout;
+    g.lda = d;
+    g.B = P + o.w2;
+    g.ldb = d;
+    g.C = p->g_u;
+    g.ldc = F;
+    g.dact = c.activation == TALOS_ACT_GELU ? GEMM_DACT_GELU : GEMM_DACT_RELU;
+    g.aux = L.u;
+    g.ldaux = F;
+    g.ksplit = 1;
+    rc = gemm_launch(g, s);
+    if (rc) return rc;
+  }
+  // u = xn2.W1 + b1
+  rc = mm(p, s, 1, 0, d, F, M, L.xn2, d, p->g_u, F, G + o.w1, F);
+  if (rc) return rc;
+  rc = colsum_launch(M, F, p->g_u, F, 0.f, G + o.b1, p->red_ws, s);
+  if (rc) return rc;
+  rc = mm(p, s, 0, 1, M, d, F, p->g_u, F, P + o.w1, F, p->g_xn, d);
+  if (rc) return rc;
+  // h2 -> (residual) + rmsnorm2
+  TALOS_HIP(hipMemcpyAsync(p->g_h2, gout, (size_t)M * d * 4, hipMemcpyDeviceToDevice, s));
+  rc = rmsnorm_bwd_launch(M, d, L.h2, P + o.g2, L.rstd2, p->g_xn, 1.f, p->g_h2, 0.f, G + o.g2, p->red_ws, s);
+  if (rc) return rc;
+  // h2 = x + o.Wo
+  rc = mm(p, s, 1, 0, d, d, M, L.o, d, p->g_h2, d, G + o.wo, d);
+  if (rc) return rc;
+  rc = mm(p, s, 0, 1, M, d, d, p->g_h2, d, P + o.wo, d, p->g_o, d);
+  if (rc) return rc;
+  {
+    AttnDesc a;
+    a.batch = c.batch;
+    a.seq = c.seq;
+    a.heads = c.n_heads;
+    a.dk = a.dv = c.head_dim;
+    a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+    a.causal = c.causal;
+    a.q = L.qkv;
+    a.k = L.qkv + d;
+    a.v = L.qkv + 2 * d;
+    a.ldq = a.ldk = a.ldv = 3 * d;
+    a.o = L.o;
+    a.ldo = d;
+    a.lse = L.lse;
+    a.dout = p->g_o;
+    a.lddo = d;
+    a.dq = p->g_qkv;
+    a.dk_out = p->g_qkv + d;
+    a.dv_out = p->g_qkv + 2 * d;
+    a.lddq = a.lddk = a.lddv = 3 * d;
+    a.rope_cos = p->rcos;
+    a.rope_sin = p->rsin;
+    a.rope_off = 0;
+    a.rope_dim = c.head_dim;
+    rc = attn_bwd_launch(a, p->attn_ws, s);
+    if (rc) return rc;
+  }
+  // qkv = xn1.Wqkv
+  rc = mm(p, s, 1, 0, d, 3 * d, M, L.xn1, d, p->g_qkv, 3 * d, G + o.wqkv, 3 * d);
+  if (rc) return rc;
+  rc = mm(p, s, 0, 1, M, d, 3 * d, p->g_qkv, 3 * d, P + o.wqkv, 3 * d, p->g_xn, d);
+  if (rc) return rc;
+  if (dx != p->g_h2) TALOS_HIP(hipMemcpyAsync(dx, p->g_h2, (size_t)M * d * 4, hipMemcpyDeviceToDevice, s));
+  return rmsnorm_bwd_launch(M, d, L.x, P + o.g1, L.rstd1, p->g_xn, 1.f, dx, 0.f, G + o.g1, p->red_ws, s);
+}
+
+// Last-token gather / scatter -----------------------------------------------
+__global__ void gather_last_kernel(int B, int S, int d, const float* __restrict__ h, float* __restrict__ out) {
+  const long long n = (long long)B * d;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+    const long long b = i / d;
+    const int e = (int)(i % d);
+    out[i] = h[(b * S + (S - 1)) * d + e];
+  }
+}
+// g[M, d] = 0 except rows b*S + S-1 which receive gl[b]
+__global__ void scatter_last_kernel(int B, int S, int d, const float* __restrict__ gl, float* __restrict__ g) {
+  const long long n = (long long)B * S * d;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+    const long long row = i / d;
+    const int e = (int)(i % d);
+    const int t = (int)(row % S);
+    g[i] = t == S - 1 ? gl[(row / S) * d + e] : 0.f;
+  }
+}
+
+// Clipped PPO loss over the minibatch (closed form of the per-sample graph of
+// src/ppo.rs:702-749, mean over the batch as src/ppo.rs:754-755). One workgroup; f64 math.
+// Per sample: lp = z - lse(z); ratio = exp(lp[a] - old); surr1 = ratio*adv;
+// surr2 = clip(ratio, 1-eps, 1+eps)*adv; the smaller by value is kept (ties take surr2, whose
+// gradient passes only inside the clip range); v = (value - ret)^2; ent = -sum p*lp;
+// loss = -pol + cv*v - ce*ent.
+__global__ __launch_bounds__(256) void ppo_loss_kernel(int B, int A, float clip_eps, float cv, float ce,
+                                                       const float* __restrict__ logits,
+                                                       const float* __restrict__ values,
+                                                       const int32_t* __restrict__ actions,
+                                                       const float* __restrict__ adv, const float* __restrict__ ret,
+                                                       const float* __restrict__ old_logp, float* __restrict__ loss,
+                                                       float* __restrict__ dlogits, float* __restrict__ dvalues,
+                                                       int with_grad) {
+  __shared__ double red[4];
+  double total = 0.0;
+  const double invB = 1.0 / (double)B;
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    const float* z = logits + (long long)b * A;
+    double mx = -INFINITY;
+    for (int j = 0; j < A; ++j) mx = fmax(mx, (double)z[j]);
+    double se = 0.0;
+    for (int j = 0; j < A; ++j) se += exp((double)z[j] - mx);
+    const double lse = log(se) + mx;
+    double ent = 0.0;
+    for (int j = 0; j < A; ++j) {
+      const double lp = (double)z[j] - lse;
+      ent -= exp(lp) * lp;
+    }
+    const int a = actions[b];
+    if (a < 0 || a >= A) {
+      // the reference panics on an out-of-range action (mask[action], src/ppo.rs:714-720); here
+      // the loss becomes NaN and the sample contributes no gradient
+      total = NAN;
+      if (with_grad) {
+        for (int k = 0; k < A; ++k) dlogits[(long long)b * A + k] = 0.f;
+        dvalues[b] = 0.f;
+      }
+      continue;
+    }
+    const double ratio = exp(((double)z[a] - lse) - (double)old_logp[b]);
+    const double ad = adv[b];
+    const double lo = 1.0 - (double)clip_eps, hi = 1.0 + (double)clip_eps;
+    const double s1 = ratio * ad;
+    const double rc = fmin(fmax(ratio, lo), hi);
+    const double s2 = rc * ad;
+    double pol, gr;
+    if (s1 < s2) {
+      pol = s1;
+      gr = ad;
+    } else {
+      pol = s2;
+      gr = (ratio >= lo && ratio <= hi) ? ad : 0.0;
+    }
+    const double vd = (double)values[b] - (double)ret[b];
+    total += -pol + (double)cv * vd * vd - (double)ce * ent;
+    if (with_grad) {
+      for (int k = 0; k < A; ++k) {
+        const double lp = (double)z[k] - lse;
+        const double pk = exp(lp);
+        const double dk = (k == a ? 1.0 : 0.0) - pk;
+        dlogits[(long long)b * A + k] = (float)((-gr * ratio * dk + (double)ce * pk * (lp + ent)) * invB);
+      }
+      dvalues[b] = (float)(2.0 * (double)cv * vd * invB);
+    }
+  }
+  total = block_sum(total, red);
+  if (threadIdx.x == 0 && loss) loss[0] = (float)(total * invB);
+}
+
+static int check_ppo_cfg(const talos_ppo_cfg& c) {
+  TALOS_REQUIRE(c.in_dim > 0 && c.n_layers >= 0 && c.n_actions > 0, TALOS_ERR_SHAPE,
+                "ppo cfg: in_dim, n_actions must be positive and n_layers >= 0");
+  TALOS_REQUIRE(c.n_actions <= 64, TALOS_ERR_UNSUPPORTED, "ppo cfg: n_actions %d > 64", c.n_actions);
+  TALOS_REQUIRE(c.clip_eps >= 0.f, TALOS_ERR_SHAPE, "ppo cfg: clip_eps must be >= 0");
+  return check_block_cfg(block_cfg_of(c));
+}
+
+// Policy forward up to logits / values.
+static int ppo_forward(talos_plan_s* p, const float* P, const float* states, hipStream_t s) {
+  const talos_ppo_cfg& c = p->ppo;
+  const talos_block_cfg bc = block_cfg_of(c);
+  const PpoOff po = ppo_offsets(c);
+  const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions;
+  int rc = mm(p, s, 0, 0, M, d, c.in_dim, states, c.in_dim, P + po.we, d, p->h0, d, 0.f, P + po.be);
+  if (rc) return rc;
+  const float* h = p->h0;
+  size_t base = po.blocks;
+  for (int l = 0; l < c.n_layers; ++l) {
+    BlockOff bo = block_offsets(bc, base);
+    p->layers[l].x = const_cast<float*>(h);
+    rc = block_forward(p, bc, P, bo, p->layers[l], s);
+    if (rc) return rc;
+    h = p->layers[l].out;
+    base = bo.end;
+  }
+  hipLaunchKernelGGL(gather_last_kernel, dim3(ceil_div((size_t)c.batch * d, 256)), dim3(256), 0, s, c.batch, c.seq, d,
+                     h, p->last);
+  TALOS_LAUNCHED("gather_last_kernel");
+  rc = rmsnorm_fwd_launch(c.batch, d, c.eps, p->last, P + po.gf, p->lastn, p->rstdf, s);
+  if (rc) return rc;
+  rc = mm(p, s, 0, 0, c.batch, d, d, p->lastn, d, P + po.wout, d, p->pout, d, 0.f, P + po.bout);
+  if (rc) return rc;
+  rc = mm(p, s, 0, 0, c.batch, A, d, p->pout, d, P + po.wa, A, p->logits, A, 0.f, P + po.ba);
+  if (rc) return rc;
+  return mm(p, s, 0, 0, c.batch, 1, d, p->pout, d, P + po.wc, 1, p->values, 1, 0.f, P + po.bc);
+}
+
+}  // namespace talos
+
+using namespace talos;
+
+extern "C" {
+
+size_t talos_block_param_count(const talos_block_cfg* cfg) { return cfg ? block_params(*cfg) : 0; }
+
+size_t talos_ppo_param_count(const talos_ppo_cfg* cfg) { return cfg ? ppo_params(*cfg) : 0; }
+
+int talos_block_plan_create(const talos_block_cfg* cfg, talos_plan* plan) {
+  TALOS_NONNULL(cfg);
+  TALOS_NONNULL(plan);
+  *plan = nullptr;
+  int rc = check_block_cfg(*cfg);
+  if (rc) return rc;
+  TALOS_DEVICE();
+  auto* p = new talos_plan_s();
+  p->kind = 1;
+  p->blk = *cfg;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, 0) == hipSuccess) p->num_cu = prop.multiProcessorCount;
+  rc = alloc_block_buffers(p, *cfg, 1, true);
+  if (rc == TALOS_OK) rc = alloc_workspaces(p);
+  if (rc) {
+    plan_free(p);
+    delete p;
+    return rc;
+  }
+  *plan = p;
+  return TALOS_OK;
+}
+
+int talos_block_fwd_bwd_f32(talos_plan plan, const float* params, const float* x, const float* gout, float* out,
+                            float* dparams, float* dx, talos_stream_t stream) {
+  TALOS_REQUIRE(plan != nullptr && plan->kind == 1, TALOS_ERR_HANDLE, "%s: not a block plan", __func__);
+  TALOS_NONNULL(params);
+  TALOS_NONNULL(x);
+  TALOS_NONNULL(gout);
+  TALOS_NONNULL(dparams);
+  TALOS_NONNULL(dx);
+  TALOS_DEVICE();
+  hipStream_t s = as_stream(stream);
+  const talos_block_cfg& c = plan->blk;
+  const size_t M = (size_t)c.batch * c.seq, d = c.d_model;
+  BlockOff bo = block_offsets(c, 0);
+  auto& L = plan->layers[0];
+  L.x = const_cast<float*>(x);
+  int rc = block_forward(plan, c, params, bo, L, s);
+  if (rc) return rc;
+  if (out) TALOS_HIP(hipMemcpyAsync(out, L.out, M * d * 4, hipMemcpyDeviceToDevice, s));
+  return block_backward(plan, c, params, dparams, bo, L, gout, dx, s);
+}
+
+int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
+  TALOS_NONNULL(cfg);
+  TALOS_NONNULL(plan);
+  *plan = nullptr;
+  int rc = check_ppo_cfg(*cfg);
+  if (rc) return rc;
+  TALOS_DEVICE();
+  auto* p = new talos_plan_s();
+  p->kind = 2;
+  p->ppo = *cfg;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, 0) == hipSuccess) p->num_cu = prop.multiProcessorCount;
+  const talos_block_cfg bc = block_cfg_of(*cfg);
+  const size_t M = (size_t)cfg->batch * cfg->seq, d = cfg->d_model, B = cfg->batch, A = cfg->n_actions;
+  rc = alloc_block_buffers(p, bc, cfg->n_layers, false);
+  rc |= plan_alloc(p, &p->h0, M * d);
+  rc |= plan_alloc(p, &p->last, B * d);
+  rc |= plan_alloc(p, &p->lastn, B * d);
+  rc |= plan_alloc(p, &p->rstdf, B);
+  rc |= plan_alloc(p, &p->pout, B * d);
+  rc |= plan_alloc(p, &p->logits, B * A);
+  rc |= plan_alloc(p, &p->values, B);
+  rc |= plan_alloc(p, &p->g_logits, B * A);
+  rc |= plan_alloc(p, &p->g_values, B);
+  rc |= plan_alloc(p, &p->g_pout, B * d);
+  rc |= plan_alloc(p, &p->g_lastn, B * d);
+  rc |= plan_alloc(p, &p->g_last, B * d);
+  if (rc == TALOS_OK) {
+    p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, wgrad_ws(p, (int)M, cfg->in_dim, (int)d));
+    p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, wgrad_ws(p, (int)B, (int)d, (int)d));
+    p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, wgrad_ws(p, (int)B, (int)d, (int)A));
+    p->red_ws_bytes = std::max(p->red_ws_bytes, colsum_workspace_bytes((int)M, (int)d));
+    rc = alloc_workspaces(p);
+  }
+  if (rc) {
+    plan_free(p);
+    delete p;
+    return rc ? rc : TALOS_ERR_ALLOC;
+  }
+  *plan = p;
+  return TALOS_OK;
+}
+
+int talos_ppo_forward_f32(talos_plan plan, const float* params, const float* states, float* logits, float* values,
+                          talos_stream_t stream) {
+  TALOS_REQUIRE(plan != nullptr && plan->kind == 2, TALOS_ERR_HANDLE, "%s: not a ppo plan", __func__);
+  TALOS_NONNULL(params);
+  TALOS_NONNULL(states);
+  TALOS_DEVICE();
+  hipStream_t s = as_stream(stream);
+  int rc = ppo_forward(plan, params, states, s);
+  if (rc) return rc;
+  const talos_ppo_cfg& c = plan->ppo;
+  if (logits)
+    TALOS_HIP(hipMemcpyAsync(logits, plan->logits, (size_t)c.batch * c.n_actions * 4, hipMemcpyDeviceToDevice, s));
+  if (values) TALOS_HIP(hipMemcpyAsync(values, plan->values, (size_t)c.batch * 4, hipMemcpyDeviceToDevice, s));
+  return TALOS_OK;
+}
+
+int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* states, const int32_t* actions,
+                          const float* adv, const float* ret, const float* old_logp, float* loss_out, float* dparams,
+                          talos_stream_t stream) {
+  TALOS_REQUIRE(plan != nullptr && plan->kind == 2, TALOS_ERR_HANDLE, "%s: not a ppo plan", __func__);
+  TALOS_NONNULL(params);
+  TALOS_NONNULL(states);
+  TALOS_NONNULL(actions);
+  TALOS_NONNULL(adv);
+  TALOS_NONNULL(ret);
+  TALOS_NONNULL(old_logp);
+  TALOS_NONNULL(dparams);
+  TALOS_DEVICE();
+  hipStream_t s = as_stream(stream);
+  talos_plan_s* p = plan;
+  const talos_ppo_cfg& c = p->ppo;
+  const talos_block_cfg bc = block_cfg_of(c);
+  const PpoOff po = ppo_offsets(c);
+  const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions, B = c.batch;
+  int rc = ppo_forward(p, params, states, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(ppo_loss_kernel, dim3(1), dim3(256), 0, s, B, A, c.clip_eps, c.value_coef, c.entropy_coef,
+                     p->logits, p->values, actions, adv, ret, old_logp, loss_out, p->g_logits, p->g_values, 1);
+  TALOS_LAUNCHED("ppo_loss_kernel");
+  float* G = dparams;
+  // heads
+  rc = mm(p, s, 1, 0, d, A, B, p->pout, d, p->g_logits, A, G + po.wa, A);
+  if (rc) return rc;
+  rc = colsum_launch(B, A, p->g_logits, A, 0.f, G + po.ba, p->red_ws, s);
+  if (rc) return rc;
+  rc = mm(p, s, 1, 0, d, 1, B, p->pout, d, p->g_values, 1, G + po.wc, 1);
+  if (rc) return rc;
+  rc = colsum_launch(B, 1, p->g_values, 1, 0.f, G + po.bc, p->red_ws, s);
+  if (rc) return rc;
+  rc = mm(p, s, 0, 1, B, d, A, p->g_logits, A, params + po.wa, A, p->g_pout, d);
+  if (rc) return rc;
+  rc = mm(p, s, 0, 1, B, d, 1, p->g_values, 1, params + po.wc, 1, p->g_pout, d, 1.f);
+  if (rc) return rc;
+  // out_proj
+  rc = mm(p, s, 1, 0, d, d, B, p->lastn, d, p->g_pout, d, G + po.wout, d);
+  if (rc) return rc;
+  rc = colsum_launch(B, d, p->g_pout, d, 0.f, G + po.bout, p->red_ws, s);
+  if (rc) return rc;
+  rc = mm(p, s, 0, 1, B, d, d, p->g_pout, d, params + po.wout, d, p->g_lastn, d);
+  if (rc) return rc;
+  // final rmsnorm on the last-token rows
+  rc = rmsnorm_bwd_launch(B, d, p->last, params + po.gf, p->rstdf, p->g_lastn, 0.f, p->g_last, 0.f, G + po.gf,
+                          p->red_ws, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(scatter_last_kernel, dim3(ceil_div((size_t)M * d, 256) > 65536 ? 65536 : ceil_div((size_t)M * d, 256)),
+                     dim3(256), 0, s, B, c.seq, d, p->g_last, p->g_out);
+  TALOS_LAUNCHED("scatter_last_kernel");
+  // blocks, last to first; the gradient ping-pongs between g_out and g_x
+  float* gcur = p->g_out;
+  float* gnext = p->g_x;
+  std::vector<BlockOff> offs;
+  size_t base = po.blocks;
+  for (int l = 0; l < c.n_layers; ++l) {
+    offs.push_back(block_offsets(bc, base));
+    base = offs.back().end;
+  }
+  for (int l = c.n_layers - 1; l >= 0; --l) {
+    rc = block_backward(p, bc, params, G, offs[l], p->layers[l], gcur, gnext, s);
+    if (rc) return rc;
+    std::swap(gcur, gnext);
+  }
+  // embed
+  rc = mm(p, s, 1, 0, c.in_dim, d, M, states, c.in_dim, gcur, d, G + po.we, d);
+  if (rc) return rc;
+  return colsum_launch(M, d, gcur, d, 0.f, G + po.be, p->red_ws, s);
+}
+
+int talos_plan_destroy(talos_plan plan) {
+  if (plan == nullptr) return TALOS_OK;
+  TALOS_DEVICE();
+  (void)hipDeviceSynchronize();
+  plan_free(plan);
+  delete plan;
+  return TALOS_OK;
+}
+
+}  // extern "C"

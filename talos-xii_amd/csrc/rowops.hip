@@ -1,0 +1,890 @@
+// rowops.hip -- HBM-bound row and element-wise kernels of the autograd tape:
+// RMSNorm (src/nn.rs:182-296), softmax (src/transformer.rs:1074-1121), RoPE
+// (src/transformer.rs:219-337), the Linear bias gradient (src/autograd.rs:530-544) and the
+// element-wise / layout ops (src/autograd.rs:356-792, 1606-1862; src/transformer.rs:1123-1183).
+//
+// Row kernels give each row to one wave64: a lane holds dim/64 consecutive elements read with
+// 16-byte loads, row statistics are wave shuffles (no LDS, no block barriers), and per-feature
+// reductions over rows (RMSNorm dgain, bias grads) write one f64 partial per workgroup that a
+// second pass sums in f64.
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
+#include "rowops.hpp"
+
+namespace talos {
+
+// ---------------------------------------------------------------------------
+// Fill / copy
+// ---------------------------------------------------------------------------
+__global__ void fill_zero_kernel(uint32_t* __restrict__ p, size_t n_words) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+__global__ void fill_zero_bytes_kernel(uint8_t* __restrict__ p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
+}
+
+static unsigned grid_for(size_t n, unsigned block = 256, unsigned cap = 65536) {
+  size_t g = (n + block - 1) / block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (unsigned)g;
+}
+
+int fill_zero(void* dst, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return TALOS_OK;
+  if ((reinterpret_cast<uintptr_t>(dst) & 3) == 0 && bytes % 4 == 0) {
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_for(bytes / 4)), dim3(256), 0, s, (uint32_t*)dst, bytes / 4);
+  } else {
+    hipLaunchKernelGGL(fill_zero_bytes_kernel, dim3(grid_for(bytes)), dim3(256), 0, s, (uint8_t*)dst, bytes);
+  }
+  TALOS_LAUNCHED("fill_zero");
+  return TALOS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Column sums (bias gradient): db[c] = beta*db[c] + sum_r dy[r, c]
+// ---------------------------------------------------------------------------
+constexpr int kColRows = 256;  // rows per partial
+
+__global__ void colsum_partial_kernel(int rows, int cols, const float* __restrict__ dy, long long ld,
+                                      double* __restrict__ part) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  const int r0 = blockIdx.y * kColRows;
+  if (c >= cols) return;
+  const int r1 = min(rows, r0 + kColRows);
+  double s = 0.0;
+  for (int r = r0; r < r1; ++r) s += (double)dy[(long long)r * ld + c];
+  part[(long long)blockIdx.y * cols + c] = s;
+}
+
+__global__ void colsum_final_kernel(int cols, int nparts, const double* __restrict__ part, float beta,
+                                    float* __restrict__ out) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= cols) return;
+  double s = 0.0;
+  for (int p = 0; p < nparts; ++p) s += part[(long long)p * cols + c];
+  out[c] = (float)(s + (beta != 0.f ? (double)out[c] : 0.0));
+}
+
+size_t colsum_workspace_bytes(int rows, int cols) {
+  return (size_t)((rows + kColRows - 1) / kColRows) * cols * sizeof(double);
+}
+
+int colsum_launch(int rows, int cols, const float* dy, long long ld, float beta, float* out, double* ws,
+                  hipStream_t s) {
+  if (cols == 0) return TALOS_OK;
+  const int nparts = (rows + kColRows - 1) / kColRows;
+  if (nparts > 0) {
+    dim3 g(ceil_div(cols, 256), nparts);
+    hipLaunchKernelGGL(colsum_partial_kernel, g, dim3(256), 0, s, rows, cols, dy, ld, ws);
+    TALOS_LAUNCHED("colsum_partial_kernel");
+  }
+  hipLaunchKernelGGL(colsum_final_kernel, dim3(ceil_div(cols, 256)), dim3(256), 0, s, cols, nparts, ws, beta, out);
+  TALOS_LAUNCHED("colsum_final_kernel");
+  return TALOS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm
+// ---------------------------------------------------------------------------
+// Each wave handles rows; lane l holds elements [4*l + 256*j, +4) for j < dim/256 (dim % 4 == 0,
+// dim <= 1024 on the vector path). Generic dims fall back to a strided scalar loop.
+template <int V>  // float4 vectors per lane
+__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(int rows, int dim, float eps, const float* __restrict__ x,
+                                                          const float* __restrict__ w, float* __restrict__ y,
+                                                          float* __restrict__ rstd) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + (long long)row * dim;
+  float4 v[V];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int c = 4 * lane + 256 * j;
+    v[j] = c < dim ? *reinterpret_cast<const float4*>(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)dim + eps);
+  if (lane == 0 && rstd) rstd[row] = r;
+  float* yr = y + (long long)row * dim;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int c = 4 * lane + 256 * j;
+    if (c < dim) {
+      const float4 g = *reinterpret_cast<const float4*>(w + c);
+      *reinterpret_cast<float4*>(yr + c) =
+          make_float4(v[j].x * r * g.x, v[j].y * r * g.y, v[j].z * r * g.z, v[j].w * r * g.w);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_fwd_generic(int rows, int dim, float eps, const float* __restrict__ x,
+                                                           const float* __restrict__ w, float* __restrict__ y,
+                                                           float* __restrict__ rstd) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + (long long)row * dim;
+  float ss = 0.f;
+  for (int c = lane; c < dim; c += 64) ss += xr[c] * xr[c];
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)dim + eps);
+  if (lane == 0 && rstd) rstd[row] = r;
+  for (int c = lane; c < dim; c += 64) y[(long long)row * dim + c] = xr[c] * r * w[c];
+}
+
+// Backward: each wave processes kRowsPerWave rows; dgain partials per workgroup in f64.
+constexpr int kRmsRowsPerWave = 4;
+constexpr int kRmsRowsPerBlock = 4 * kRmsRowsPerWave;
+
+template <int V>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(int rows, int dim, const float* __restrict__ x,
+                                                          const float* __restrict__ w,
+                                                          const float* __restrict__ rstd,
+                                                          const float* __restrict__ dy, float beta_dx,
+                                                          float* __restrict__ dx, double* __restrict__ dw_part) {
+  __shared__ float red[4][V * 256];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  float4 gw[V], dwacc[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int c = 4 * lane + 256 * j;
+    gw[j] = c < dim ? *reinterpret_cast<const float4*>(w + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    dwacc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const float inv_dim = 1.0f / (float)dim;
+  for (int i = 0; i < kRmsRowsPerWave; ++i) {
+    const int row = blockIdx.x * kRmsRowsPerBlock + wv * kRmsRowsPerWave + i;
+    if (row >= rows) break;
+    const float r = rstd[row];
+    const float* xr = x + (long long)row * dim;
+    const float* gr = dy + (long long)row * dim;
+    float4 xh[V], gg[V];
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const int c = 4 * lane + 256 * j;
+      if (c < dim) {
+        const float4 xv = *reinterpret_cast<const float4*>(xr + c);
+        gg[j] = *reinterpret_cast<const float4*>(gr + c);
+        xh[j] = make_float4(xv.x * r, xv.y * r, xv.z * r, xv.w * r);
+      } else {
+        gg[j] = xh[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      dot += gg[j].x * gw[j].x * xh[j].x + gg[j].y * gw[j].y * xh[j].y + gg[j].z * gw[j].z * xh[j].z +
+             gg[j].w * gw[j].w * xh[j].w;
+      dwacc[j].x += gg[j].x * xh[j].x;
+      dwacc[j].y += gg[j].y * xh[j].y;
+      dwacc[j].z += gg[j].z * xh[j].z;
+      dwacc[j].w += gg[j].w * xh[j].w;
+    }
+    const float md = wave_sum(dot) * inv_dim;
+    float* dxr = dx + (long long)row * dim;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const int c = 4 * lane + 256 * j;
+      if (c < dim) {
+        float4 o = make_float4(r * (gg[j].x * gw[j].x - xh[j].x * md), r * (gg[j].y * gw[j].y - xh[j].y * md),
+                               r * (gg[j].z * gw[j].z - xh[j].z * md), r * (gg[j].w * gw[j].w - xh[j].w * md));
+        if (beta_dx != 0.f) {
+          const float4 old = *reinterpret_cast<const float4*>(dxr + c);
+          o.x += old.x;
+          o.y += old.y;
+          o.z += old.z;
+          o.w += old.w;
+        }
+        *reinterpret_cast<float4*>(dxr + c) = o;
+      }
+    }
+  }
+  if (dw_part == nullptr) return;
+#pragma unroll
+  for (int j = 0; j < V; ++j) *reinterpret_cast<float4*>(&red[wv][4 * lane + 256 * j]) = dwacc[j];
+  __syncthreads();
+  for (int c = threadIdx.x; c < dim; c += 256) {
+    const double s = (double)red[0][c] + (double)red[1][c] + (double)red[2][c] + (double)red[3][c];
+    dw_part[(long long)blockIdx.x * dim + c] = s;
+  }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_bwd_generic(int rows, int dim, const float* __restrict__ x,
+                                                           const float* __restrict__ w,
+                                                           const float* __restrict__ rstd,
+                                                           const float* __restrict__ dy, float beta_dx,
+                                                           float* __restrict__ dx, double* __restrict__ dw_part) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int i = 0; i < kRmsRowsPerWave; ++i) {
+    const int row = blockIdx.x * kRmsRowsPerBlock + wv * kRmsRowsPerWave + i;
+    if (row >= rows) break;
+    const float r = rstd[row];
+    const float* xr = x + (long long)row * dim;
+    const float* gr = dy + (long long)row * dim;
+    float dot = 0.f;
+    for (int c = lane; c < dim; c += 64) dot += gr[c] * w[c] * xr[c] * r;
+    const float md = wave_sum(dot) / (float)dim;
+    for (int c = lane; c < dim; c += 64) {
+      float o = r * (gr[c] * w[c] - xr[c] * r * md);
+      if (beta_dx != 0.f) o += dx[(long long)row * dim + c];
+      dx[(long long)row * dim + c] = o;
+    }
+  }
+  if (dw_part == nullptr) return;
+  // per-feature partial over this workgroup's rows
+  for (int c = threadIdx.x; c < dim; c += 256) {
+    double s = 0.0;
+    for (int i = 0; i < kRmsRowsPerBlock; ++i) {
+      const int row = blockIdx.x * kRmsRowsPerBlock + i;
+      if (row >= rows) break;
+      s += (double)dy[(long long)row * dim + c] * (double)(x[(long long)row * dim + c] * rstd[row]);
+    }
+    dw_part[(long long)blockIdx.x * dim + c] = s;
+  }
+}
+
+__global__ void sum_partials_kernel(int cols, int nparts, const double* __restrict__ part, float beta,
+                                    float* __restrict__ out) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= cols) return;
+  double s = 0.0;
+  for (int p = 0; p < nparts; ++p) s += part[(long long)p * cols + c];
+  out[c] = (float)(s + (beta != 0.f ? (double)out[c] : 0.0));
+}
+
+size_t rmsnorm_bwd_workspace_bytes(int rows, int dim) {
+  return (size_t)((rows + kRmsRowsPerBlock - 1) / kRmsRowsPerBlock) * dim * sizeof(double);
+}
+
+int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
+                       hipStream_t s) {
+  if (rows == 0) return TALOS_OK;
+  dim3 g(ceil_div(rows, 4)), b(256);
+  const bool vec = dim % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
+                                     reinterpret_cast<uintptr_t>(w)) & 15) == 0;
+  if (vec && dim <= 256) hipLaunchKernelGGL(rmsnorm_fwd_kernel<1>, g, b, 0, s, rows, dim, eps, x, w, y, rstd);
+  else if (vec && dim <= 512) hipLaunchKernelGGL(rmsnorm_fwd_kernel<2>, g, b, 0, s, rows, dim, eps, x, w, y, rstd);
+  else if (vec && dim <= 1024) hipLaunchKernelGGL(rmsnorm_fwd_kernel<4>, g, b, 0, s, rows, dim, eps, x, w, y, rstd);
+  else hipLaunchKernelGGL(rmsnorm_fwd_generic, g, b, 0, s, rows, dim, eps, x, w, y, rstd);
+  TALOS_LAUNCHED("rmsnorm_fwd");
+  return TALOS_OK;
+}
+
+int rmsnorm_bwd_launch(int rows, int dim, const float* x, const float* w, const float* rstd, const float* dy,
+                       float beta_dx, float* dx, float beta_dw, float* dw, double* ws, hipStream_t s) {
+  const int nblk = (rows + kRmsRowsPerBlock - 1) / kRmsRowsPerBlock;
+  if (nblk > 0) {
+    dim3 g(nblk), b(256);
+    double* part = dw ? ws : nullptr;
+    const bool vec = dim % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy) |
+                                       reinterpret_cast<uintptr_t>(dx) | reinterpret_cast<uintptr_t>(w)) & 15) == 0;
+    if (vec && dim <= 256)
+      hipLaunchKernelGGL(rmsnorm_bwd_kernel<1>, g, b, 0, s, rows, dim, x, w, rstd, dy, beta_dx, dx, part);
+    else if (vec && dim <= 512)
+      hipLaunchKernelGGL(rmsnorm_bwd_kernel<2>, g, b, 0, s, rows, dim, x, w, rstd, dy, beta_dx, dx, part);
+    else
+      hipLaunchKernelGGL(rmsnorm_bwd_generic, g, b, 0, s, rows, dim, x, w, rstd, dy, beta_dx, dx, part);
+    TALOS_LAUNCHED("rmsnorm_bwd");
+  }
+  if (dw) {
+    hipLaunchKernelGGL(sum_partials_kernel, dim3(ceil_div(dim, 256)), dim3(256), 0, s, dim, nblk, ws, beta_dw, dw);
+    TALOS_LAUNCHED("rmsnorm_dw_sum");
+  }
+  return TALOS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Softmax over rows of length cols (optionally causal: row r is query q = r mod cols and keys
+// j > q are masked to probability 0).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void softmax_fwd_kernel(int rows, int cols, int causal, const float* __restrict__ x,
+                                                          float* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lim = causal ? (row % cols) + 1 : cols;
+  const float* xr = x + (long long)row * cols;
+  float* yr = y + (long long)row * cols;
+  float mx = -INFINITY;
+  for (int c = lane; c < lim; c += 64) mx = fmaxf(mx, xr[c]);
+  mx = wave_max(mx);
+  float s = 0.f;
+  for (int c = lane; c < lim; c += 64) s += expf(xr[c] - mx);
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+  for (int c = lane; c < cols; c += 64) yr[c] = c < lim ? expf(xr[c] - mx) * inv : 0.f;
+}
+
+// dx = beta*dx + y * (g - sum(g*y)); masked entries (y = 0) get exactly 0 and are not read.
+// Vector path: each lane owns float4 groups; a group entirely past the causal limit is skipped.
+__global__ __launch_bounds__(256) void softmax_bwd_kernel(int rows, int cols, int causal, const float* __restrict__ y,
+                                                          const float* __restrict__ dy, float beta,
+                                                          float* __restrict__ dx, int vec) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lim = causal ? (row % cols) + 1 : cols;
+  const long long base = (long long)row * cols;
+  if (vec) {
+    // pass 1: sum(g*y) over the unmasked prefix
+    float dot = 0.f;
+    for (int c = 4 * lane; c < lim; c += 256) {
+      const float4 yv = *reinterpret_cast<const float4*>(y + base + c);
+      const float4 gv = *reinterpret_cast<const float4*>(dy + base + c);
+      dot += yv.x * gv.x;
+      if (c + 1 < lim) dot += yv.y * gv.y;
+      if (c + 2 < lim) dot += yv.z * gv.z;
+      if (c + 3 < lim) dot += yv.w * gv.w;
+    }
+    dot = wave_sum(dot);
+    for (int c = 4 * lane; c < cols; c += 256) {
+      float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (c < lim) {
+        const float4 yv = *reinterpret_cast<const float4*>(y + base + c);
+        const float4 gv = *reinterpret_cast<const float4*>(dy + base + c);
+        o.x = yv.x * (gv.x - dot);
+        o.y = c + 1 < lim ? yv.y * (gv.y - dot) : 0.f;
+        o.z = c + 2 < lim ? yv.z * (gv.z - dot) : 0.f;
+        o.w = c + 3 < lim ? yv.w * (gv.w - dot) : 0.f;
+      }
+      if (beta != 0.f) {
+        const float4 old = *reinterpret_cast<const float4*>(dx + base + c);
+        o.x += old.x;
+        o.y += old.y;
+        o.z += old.z;
+        o.w += old.w;
+      }
+      *reinterpret_cast<float4*>(dx + base + c) = o;
+    }
+    return;
+  }
+  float dot = 0.f;
+  for (int c = lane; c < lim; c += 64) dot += y[base + c] * dy[base + c];
+  dot = wave_sum(dot);
+  for (int c = lane; c < cols; c += 64) {
+    float o = c < lim ? y[base + c] * (dy[base + c] - dot) : 0.f;
+    if (beta != 0.f) o += dx[base + c];
+    dx[base + c] = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RoPE on [n_seq, seq, heads, dim], interleaved pairs, position start_pos + t.
+// ---------------------------------------------------------------------------
+__global__ void rope_kernel(long long npairs, int seq, int heads, int dim, int start_pos, float sign,
+                            const float* __restrict__ cosv, const float* __restrict__ sinv,
+                            const float* __restrict__ x, float beta, float* __restrict__ y) {
+  const int half = dim >> 1;
+  for (long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x; p < npairs;
+       p += (long long)gridDim.x * blockDim.x) {
+    const int i = (int)(p % half);
+    const long long tok = p / half / heads;
+    const int t = (int)(tok % seq);
+    const int ci = (start_pos + t) * half + i;
+    const float c = cosv[ci], s = sign * sinv[ci];
+    const float2 v = reinterpret_cast<const float2*>(x)[p];
+    float2 o = make_float2(v.x * c - v.y * s, v.x * s + v.y * c);
+    if (beta != 0.f) {
+      const float2 old = reinterpret_cast<const float2*>(y)[p];
+      o.x += old.x;
+      o.y += old.y;
+    }
+    reinterpret_cast<float2*>(y)[p] = o;
+  }
+}
+
+// Host-side table cache: cos/sin(pos * theta_i), theta_i = 1 / base^(2i/dim), evaluated in f64
+// as the reference does (src/transformer.rs:239-251) and rounded to fp32.
+void rope_table_host(int max_len, int dim, double base, std::vector<float>& c, std::vector<float>& s) {
+  const int half = dim / 2;
+  c.resize((size_t)max_len * half);
+  s.resize((size_t)max_len * half);
+  for (int pos = 0; pos < max_len; ++pos)
+    for (int i = 0; i < half; ++i) {
+      const double theta = 1.0 / std::pow(base, (double)(2 * i) / (double)dim);
+      const double ang = (double)pos * theta;
+      c[(size_t)pos * half + i] = (float)std::cos(ang);
+      s[(size_t)pos * half + i] = (float)std::sin(ang);
+    }
+}
+
+struct RopeTable {
+  float* cos = nullptr;
+  float* sin = nullptr;
+  int max_len = 0;
+};
+static std::mutex g_rope_mu;
+static std::map<std::tuple<int, uint32_t>, RopeTable> g_rope_tables;  // (dim, base bits) -> table
+
+// Returns device cos/sin tables covering positions [0, need_len). Tables are kept for the life
+// of the process and only grow.
+int rope_table_device(int need_len, int dim, float base, const float** cosv, const float** sinv) {
+  uint32_t bb;
+  std::memcpy(&bb, &base, 4);
+  std::lock_guard<std::mutex> lk(g_rope_mu);
+  RopeTable& t = g_rope_tables[std::make_tuple(dim, bb)];
+  if (t.max_len < need_len) {
+    int len = std::max(need_len, 256);
+    std::vector<float> c, s;
+    rope_table_host(len, dim, (double)base, c, s);
+    float *dc = nullptr, *ds = nullptr;
+    TALOS_HIP(hipMalloc(&dc, c.size() * 4));
+    TALOS_HIP(hipMalloc(&ds, s.size() * 4));
+    TALOS_HIP(hipMemcpy(dc, c.data(), c.size() * 4, hipMemcpyHostToDevice));
+    TALOS_HIP(hipMemcpy(ds, s.data(), s.size() * 4, hipMemcpyHostToDevice));
+    // Older tables stay allocated: work already enqueued on other streams may still read them.
+    t.cos = dc;
+    t.sin = ds;
+    t.max_len = len;
+  }
+  *cosv = t.cos;
+  *sinv = t.sin;
+  return TALOS_OK;
+}
+
+int rope_launch(int n_seq, int seq, int heads, int dim, int start_pos, const float* cosv, const float* sinv,
+                const float* x, float beta, float* y, bool backward, hipStream_t s) {
+  const long long npairs = (long long)n_seq * seq * heads * (dim / 2);
+  if (npairs == 0) return TALOS_OK;
+  hipLaunchKernelGGL(rope_kernel, dim3(grid_for((size_t)npairs)), dim3(256), 0, s, npairs, seq, heads, dim,
+                     start_pos, backward ? -1.f : 1.f, cosv, sinv, x, beta, y);
+  TALOS_LAUNCHED("rope_kernel");
+  return TALOS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Element-wise ops
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float unary_f(int op, float v, float p0, float p1) {
+  switch (op) {
+    case TALOS_RELU: return v > 0.f ? v : 0.f;
+    case TALOS_LOG: return logf(v);
+    case TALOS_EXP: return expf(v);
+    case TALOS_SIN: return sinf(v);
+    case TALOS_COS: return cosf(v);
+    case TALOS_SQRT: return sqrtf(v);
+    case TALOS_NEG: return -v;
+    case TALOS_SCALE: return v * p0;
+    case TALOS_CLIP: return fminf(fmaxf(v, p0), p1);
+    case TALOS_GELU: return gelu_f(v);
+    default: return v;
+  }
+}
+// d op / dx at x (the reference closures, src/autograd.rs:356-792).
+__device__ __forceinline__ float unary_d(int op, float v, float p0, float p1) {
+  switch (op) {
+    case TALOS_RELU: return v > 0.f ? 1.f : 0.f;
+    case TALOS_LOG: return 1.f / v;
+    case TALOS_EXP: return expf(v);
+    case TALOS_SIN: return cosf(v);
+    case TALOS_COS: return -sinf(v);
+    case TALOS_SQRT: return v > 0.f ? 0.5f / sqrtf(v) : 0.f;
+    case TALOS_NEG: return -1.f;
+    case TALOS_SCALE: return p0;
+    case TALOS_CLIP: return (v >= p0 && v <= p1) ? 1.f : 0.f;
+    case TALOS_GELU: return gelu_d(v);
+    default: return 1.f;
+  }
+}
+
+__global__ void unary_fwd_kernel(int op, size_t n, float p0, float p1, const float* __restrict__ x,
+                                 float* __restrict__ y) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    y[i] = unary_f(op, x[i], p0, p1);
+}
+__global__ void unary_bwd_kernel(int op, size_t n, float p0, float p1, const float* __restrict__ x,
+                                 const float* __restrict__ dy, float* __restrict__ dx) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dx[i] += unary_d(op, x[i], p0, p1) * dy[i];
+}
+__global__ void binary_fwd_kernel(int op, size_t n, const float* __restrict__ a, const float* __restrict__ b,
+                                  float* __restrict__ y) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const float u = a[i], v = b[i];
+    y[i] = op == TALOS_ADD ? u + v : op == TALOS_SUB ? u - v : op == TALOS_MUL ? u * v : u / v;
+  }
+}
+// da / db may alias (x op x): then the two partial derivatives are summed into one write.
+__global__ void binary_bwd_kernel(int op, size_t n, const float* a, const float* b, const float* __restrict__ dy,
+                                  float* da, float* db) {
+  const bool alias = da == db;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const float g = dy[i], u = a[i], v = b[i];
+    float ga, gb;
+    switch (op) {
+      case TALOS_ADD: ga = g; gb = g; break;
+      case TALOS_SUB: ga = g; gb = -g; break;
+      case TALOS_MUL: ga = g * v; gb = g * u; break;
+      default: ga = g / v; gb = -g * u / (v * v); break;
+    }
+    if (alias) {
+      if (da) da[i] += ga + gb;
+    } else {
+      if (da) da[i] += ga;
+      if (db) db[i] += gb;
+    }
+  }
+}
+
+__global__ void reduce_partial_kernel(size_t n, const float* __restrict__ x, double* __restrict__ part) {
+  __shared__ double red[4];
+  double s = 0.0;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    s += (double)x[i];
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = s;
+}
+__global__ void reduce_final_kernel(int nparts, float scale, const double* __restrict__ part, float* __restrict__ out) {
+  __shared__ double red[4];
+  double s = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += blockDim.x) s += part[i];
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) out[0] = (float)(s * (double)scale);
+}
+__global__ void fill_add_kernel(size_t n, float scale, const float* __restrict__ g, float* __restrict__ dx) {
+  const float v = scale * g[0];
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) dx[i] += v;
+}
+
+struct TShape {
+  long long d[6];
+  long long stride_in[6];
+  int rank;
+};
+__global__ void transpose_kernel(size_t n, TShape s, const float* __restrict__ x, float* __restrict__ y, int acc) {
+  for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < n; o += (size_t)gridDim.x * blockDim.x) {
+    size_t rem = o;
+    long long src = 0;
+    for (int k = s.rank - 1; k >= 0; --k) {
+      const long long idx = (long long)(rem % (size_t)s.d[k]);
+      rem /= (size_t)s.d[k];
+      src += idx * s.stride_in[k];
+    }
+    if (acc) y[o] += x[src];
+    else y[o] = x[src];
+  }
+}
+__global__ void concat_kernel(size_t rows, int ca, int cb, const float* __restrict__ a, const float* __restrict__ b,
+                              float* __restrict__ out) {
+  const int w = ca + cb;
+  const size_t n = rows * w;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t r = i / w;
+    const int c = (int)(i % w);
+    out[i] = c < ca ? a[r * ca + c] : b[r * cb + (c - ca)];
+  }
+}
+__global__ void concat_bwd_kernel(size_t rows, int ca, int cb, const float* __restrict__ g, float* __restrict__ da,
+                                  float* __restrict__ db) {
+  const int w = ca + cb;
+  const size_t n = rows * w;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t r = i / w;
+    const int c = (int)(i % w);
+    if (c < ca) da[r * ca + c] += g[i];
+    else db[r * cb + (c - ca)] += g[i];
+  }
+}
+__global__ void broadcast_rows_kernel(size_t rows, int cols, const float* __restrict__ v, float* __restrict__ out) {
+  const size_t n = rows * cols;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    out[i] = v[i % cols];
+}
+
+}  // namespace talos
+
+using namespace talos;
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+int talos_fill_zero(void* dst, size_t bytes, talos_stream_t stream) {
+  TALOS_NONNULL(dst);
+  TALOS_DEVICE();
+  return fill_zero(dst, bytes, as_stream(stream));
+}
+
+int talos_bias_grad_f32(int rows, int cols, const float* dy, float beta, float* db, talos_stream_t stream) {
+  TALOS_NONNULL(dy);
+  TALOS_NONNULL(db);
+  TALOS_REQUIRE(rows >= 0 && cols >= 0, TALOS_ERR_SHAPE, "%s: negative size", __func__);
+  TALOS_REQUIRE(beta == 0.f || beta == 1.f, TALOS_ERR_UNSUPPORTED, "%s: beta must be 0 or 1", __func__);
+  TALOS_DEVICE();
+  hipStream_t s = as_stream(stream);
+  double* ws = nullptr;
+  const size_t bytes = colsum_workspace_bytes(rows, cols);
+  if (bytes) TALOS_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, s));
+  int rc = colsum_launch(rows, cols, dy, cols, beta, db, ws, s);
+  if (ws) TALOS_HIP(hipFreeAsync(ws, s));
+  return rc;
+}
+
+int talos_rmsnorm_fwd_f32(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
+                          talos_stream_t stream) {
+  TALOS_NONNULL(x);
+  TALOS_NONNULL(w);
+  TALOS_NONNULL(y);
+  TALOS_REQUIRE(rows >= 0 && dim > 0, TALOS_ERR_SHAPE, "%s: bad shape rows=%d dim=%d", __func__, rows, dim);
+  TALOS_REQUIRE(eps >= 0.f, TALOS_ERR_SHAPE, "%s: eps must be >= 0", __func__);
+  TALOS_DEVICE();
+  return rmsnorm_fwd_launch(rows, dim, eps, x, w, y, rstd, as_stream(stream));
+}
+
+int talos_rmsnorm_bwd_f32(int rows, int dim, const float* x, const float* w, const float* rstd, const float* dy,
+                          float beta_dx, float* dx, float beta_dw, float* dw, talos_stream_t stream) {
+  TALOS_NONNULL(x);
+  TALOS_NONNULL(w);
+  TALOS_NONNULL(rstd);
+  TALOS_NONNULL(dy);
+  TALOS_NONNULL(dx);
+  TALOS_REQUIRE(rows >= 0 && dim > 0, TALOS_ERR_SHAPE, "%s: bad shape rows=%d dim=%d", __func__, rows, dim);
+  TALOS_REQUIRE((beta_dx == 0.f || beta_dx == 1.f) && (beta_dw == 0.f || beta_dw == 1.f), TALOS_ERR_UNSUPPORTED,
+                "%s: beta_dx / beta_dw must be 0 or 1", __func__);
+  TALOS_DEVICE();
+  hipStream_t s = as_stream(stream);
+  double* ws = nullptr;
+  const size_t bytes = dw ? rmsnorm_bwd_workspace_bytes(rows, dim) : 0;
+  if (bytes) TALOS_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, s));
+  int rc = rmsnorm_bwd_launch(rows, dim, x, w, rstd, dy, beta_dx, dx, beta_dw, dw, ws, s);
+  if (ws) TALOS_HIP(hipFreeAsync(ws, s));
+  return rc;
+}
+
+int talos_softmax_fwd_f32(int rows, int cols, int causal, const float* x, float* y, talos_stream_t stream) {
+  TALOS_NONNULL(x);
+  TALOS_NONNULL(y);
+  TALOS_REQUIRE(rows >= 0 && cols > 0, TALOS_ERR_SHAPE, "%s: bad shape rows=%d cols=%d", __func__, rows, cols);
+  TALOS_REQUIRE(causal == 0 || causal == 1, TALOS_ERR_DTYPE, "%s: causal must be 0 or 1", __func__);
+  TALOS_DEVICE();
+  if (rows == 0) return TALOS_OK;
+  hipLaunchKernelGGL(softmax_fwd_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, as_stream(stream), rows, cols, causal,
+                     x, y);
+  TALOS_LAUNCHED("softmax_fwd_kernel");
+  return TALOS_OK;
+}
+
+int talos_softmax_bwd_f32(int rows, int cols, int causal, const float* y, const float* dy, float beta, float* dx,
+                          talos_stream_t stream) {
+  TALOS_NONNULL(y);
+  TALOS_NONNULL(dy);
+  TALOS_NONNULL(dx);
+  TALOS_REQUIRE(rows >= 0 && cols > 0, TALOS_ERR_SHAPE, "%s: bad shape rows=%d cols=%d", __func__, rows, cols);
+  TALOS_REQUIRE(causal == 0 || causal == 1, TALOS_ERR_DTYPE, "%s: causal must be 0 or 1", __func__);
+  TALOS_REQUIRE(beta == 0.f || beta == 1.f, TALOS_ERR_UNSUPPORTED, "%s: beta must be 0 or 1", __func__);
+  TALOS_DEVICE();
+  if (rows == 0) return TALOS_OK;
+  const int vec = cols % 4 == 0 && ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(dy) |
+                                     reinterpret_cast<uintptr_t>(dx)) & 15) == 0;
+  hipLaunchKernelGGL(softmax_bwd_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, as_stream(stream), rows, cols, causal,
+                     y, dy, beta, dx, vec);
+  TALOS_LAUNCHED("softmax_bwd_kernel");
+  return TALOS_OK;
+}
+
+static int check_rope(const char* fn, int n_seq, int seq_len, int heads, int dim, int start_pos, float base) {
+  TALOS_REQUIRE(n_seq >= 0 && seq_len >= 0 && heads >= 0 && dim > 0, TALOS_ERR_SHAPE, "%s: bad shape", fn);
+  TALOS_REQUIRE(dim % 2 == 0, TALOS_ERR_SHAPE, "%s: dim=%d must be even (interleaved pairs)", fn, dim);
+  TALOS_REQUIRE(start_pos >= 0, TALOS_ERR_SHAPE, "%s: start_pos must be >= 0", fn);
+  TALOS_REQUIRE(base > 0.f, TALOS_ERR_SHAPE, "%s: base must be > 0", fn);
+  return TALOS_OK;
+}
+
+int talos_rope_fwd_f32(int n_seq, int seq_len, int heads, int dim, int start_pos, float base, const float* x, float* y,
+                       talos_stream_t stream) {
+  TALOS_NONNULL(x);
+  TALOS_NONNULL(y);
+  int rc = check_rope(__func__, n_seq, seq_len, heads, dim, start_pos, base);
+  if (rc) return rc;
+  TALOS_DEVICE();
+  const float *c, *s;
+  rc = rope_table_device(start_pos + seq_len, dim, base, &c, &s);
+  if (rc) return rc;
+  return rope_launch(n_seq, seq_len, heads, dim, start_pos, c, s, x, 0.f, y, false, as_stream(stream));
+}
+
+int talos_rope_bwd_f32(int n_seq, int seq_len, int heads, int dim, int start_pos, float base, const float* dy,
+                       float beta, float* dx, talos_stream_t stream) {
+  TALOS_NONNULL(dy);
+  TALOS_NONNULL(dx);
+  int rc = check_rope(__func__, n_seq, seq_len, heads, dim, start_pos, base);
+  if (rc) return rc;
+  TALOS_REQUIRE(beta == 0.f || beta == 1.f, TALOS_ERR_UNSUPPORTED, "%s: beta must be 0 or 1", __func__);
+  TALOS_DEVICE();
+  const float *c, *s;
+  rc = rope_table_device(start_pos + seq_len, dim, base, &c, &s);
+  if (rc) return rc;
+  return rope_launch(n_seq, seq_len, heads, dim, start_pos, c, s, dy, beta, dx, true, as_stream(stream));
+}
+
+int talos_rope_table_f32(int max_len, int dim, float base, float* cos_out, float* sin_out, talos_stream_t stream) {
+  TALOS_NONNULL(cos_out);
+  TALOS_NONNULL(sin_out);
+  TALOS_REQUIRE(max_len >= 0 && dim > 0 && dim % 2 == 0, TALOS_ERR_SHAPE, "%s: bad shape", __func__);
+  TALOS_DEVICE();
+  std::vector<float> c, s;
+  rope_table_host(max_len, dim, (double)base, c, s);
+  if (c.empty()) return TALOS_OK;
+  TALOS_HIP(hipMemcpyAsync(cos_out, c.data(), c.size() * 4, hipMemcpyHostToDevice, as_stream(stream)));
+  TALOS_HIP(hipMemcpyAsync(sin_out, s.data(), s.size() * 4, hipMemcpyHostToDevice, as_stream(stream)));
+  TALOS_HIP(hipStreamSynchronize(as_stream(stream)));
+  return TALOS_OK;
+}
+
+int talos_unary_fwd_f32(int op, size_t n, float p0, float p1, const float* x, float* y, talos_stream_t stream) {
+  TALOS_NONNULL(x);
+  TALOS_NONNULL(y);
+  TALOS_REQUIRE(op >= TALOS_RELU && op <= TALOS_COPY, TALOS_ERR_DTYPE, "%s: unknown op %d", __func__, op);
+  TALOS_DEVICE();
+  if (n == 0) return TALOS_OK;
+  hipLaunchKernelGGL(unary_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), op, n, p0, p1, x, y);
+  TALOS_LAUNCHED("unary_fwd_kernel");
+  return TALOS_OK;
+}
+
+int talos_unary_bwd_f32(int op, size_t n, float p0, float p1, const float* x, const float* dy, float* dx,
+                        talos_stream_t stream) {
+  TALOS_NONNULL(x);
+  TALOS_NONNULL(dy);
+  TALOS_NONNULL(dx);
+  TALOS_REQUIRE(op >= TALOS_RELU && op <= TALOS_COPY, TALOS_ERR_DTYPE, "%s: unknown op %d", __func__, op);
+  TALOS_DEVICE();
+  if (n == 0) return TALOS_OK;
+  hipLaunchKernelGGL(unary_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), op, n, p0, p1, x, dy, dx);
+  TALOS_LAUNCHED("unary_bwd_kernel");
+  return TALOS_OK;
+}
+
+int talos_binary_fwd_f32(int op, size_t n, const float* a, const float* b, float* y, talos_stream_t stream) {
+  TALOS_NONNULL(a);
+  TALOS_NONNULL(b);
+  TALOS_NONNULL(y);
+  TALOS_REQUIRE(op >= TALOS_ADD && op <= TALOS_DIV, TALOS_ERR_DTYPE, "%s: unknown op %d", __func__, op);
+  TALOS_DEVICE();
+  if (n == 0) return TALOS_OK;
+  hipLaunchKernelGGL(binary_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), op, n, a, b, y);
+  TALOS_LAUNCHED("binary_fwd_kernel");
+  return TALOS_OK;
+}
+
+int talos_binary_bwd_f32(int op, size_t n, const float* a, const float* b, const float* dy, float* da, float* db,
+                         talos_stream_t stream) {
+  TALOS_NONNULL(a);
+  TALOS_NONNULL(b);
+  TALOS_NONNULL(dy);
+  TALOS_REQUIRE(da || db, TALOS_ERR_NULL, "%s: da and db are both null", __func__);
+  TALOS_REQUIRE(op >= TALOS_ADD && op <= TALOS_DIV, TALOS_ERR_DTYPE, "%s: unknown op %d", __func__, op);
+  TALOS_DEVICE();
+  if (n == 0) return TALOS_OK;
+  hipLaunchKernelGGL(binary_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), op, n, a, b, dy, da, db);
+  TALOS_LAUNCHED("binary_bwd_kernel");
+  return TALOS_OK;
+}
+
+int talos_reduce_sum_f32(size_t n, float scale, const float* x, float* out, talos_stream_t stream) {
+  TALOS_NONNULL(x);
+  TALOS_NONNULL(out);
+  TALOS_DEVICE();
+  hipStream_t s = as_stream(stream);
+  const int nparts = (int)std::min<size_t>(1024, std::max<size_t>(1, (n + 1023) / 1024));
+  double* ws = nullptr;
+  TALOS_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), nparts * sizeof(double), s));
+  hipLaunchKernelGGL(reduce_partial_kernel, dim3(nparts), dim3(256), 0, s, n, x, ws);
+  int rc = launch_status("reduce_partial_kernel");
+  if (rc == TALOS_OK) {
+    hipLaunchKernelGGL(reduce_final_kernel, dim3(1), dim3(256), 0, s, nparts, scale, ws, out);
+    rc = launch_status("reduce_final_kernel");
+  }
+  TALOS_HIP(hipFreeAsync(ws, s));
+  return rc;
+}
+
+int talos_fill_add_f32(size_t n, float scale, const float* g, float* dx, talos_stream_t stream) {
+  TALOS_NONNULL(g);
+  TALOS_NONNULL(dx);
+  TALOS_DEVICE();
+  if (n == 0) return TALOS_OK;
+  hipLaunchKernelGGL(fill_add_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), n, scale, g, dx);
+  TALOS_LAUNCHED("fill_add_kernel");
+  return TALOS_OK;
+}
+
+int talos_transpose_f32(int rank, const long long* shape, int dim0, int dim1, const float* x, float* y, int accumulate,
+                        talos_stream_t stream) {
+  TALOS_NONNULL(shape);
+  TALOS_NONNULL(x);
+  TALOS_NONNULL(y);
+  TALOS_REQUIRE(rank >= 1 && rank <= 6, TALOS_ERR_SHAPE, "%s: rank %d outside [1, 6]", __func__, rank);
+  TALOS_REQUIRE(dim0 >= 0 && dim0 < rank && dim1 >= 0 && dim1 < rank, TALOS_ERR_SHAPE,
+                "%s: dims (%d, %d) out of range for rank %d", __func__, dim0, dim1, rank);
+  size_t n = 1;
+  long long in_stride[6];
+  for (int k = rank - 1; k >= 0; --k) {
+    TALOS_REQUIRE(shape[k] >= 0, TALOS_ERR_SHAPE, "%s: negative extent", __func__);
+    in_stride[k] = (long long)n;
+    n *= (size_t)shape[k];
+  }
+  TALOS_DEVICE();
+  if (n == 0) return TALOS_OK;
+  TShape ts;
+  ts.rank = rank;
+  for (int k = 0; k < rank; ++k) {
+    ts.d[k] = shape[k];
+    ts.stride_in[k] = in_stride[k];
+  }
+  // output shape = input shape with dim0, dim1 swapped; output index k reads input stride of the swapped dim
+  std::swap(ts.d[dim0], ts.d[dim1]);
+  std::swap(ts.stride_in[dim0], ts.stride_in[dim1]);
+  hipLaunchKernelGGL(transpose_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), n, ts, x, y, accumulate);
+  TALOS_LAUNCHED("transpose_kernel");
+  return TALOS_OK;
+}
+
+int talos_concat_last_f32(size_t rows, int ca, int cb, const float* a, const float* b, float* out,
+                          talos_stream_t stream) {
+  TALOS_NONNULL(a);
+  TALOS_NONNULL(b);
+  TALOS_NONNULL(out);
+  TALOS_REQUIRE(ca >= 0 && cb >= 0, TALOS_ERR_SHAPE, "%s: negative width", __func__);
+  TALOS_DEVICE();
+  if (rows == 0 || ca + cb == 0) return TALOS_OK;
+  hipLaunchKernelGGL(concat_kernel, dim3(grid_for(rows * (ca + cb))), dim3(256), 0, as_stream(stream), rows, ca, cb, a,
+                     b, out);
+  TALOS_LAUNCHED("concat_kernel");
+  return TALOS_OK;
+}
+
+int talos_concat_last_bwd_f32(size_t rows, int ca, int cb, const float* dout, float* da, float* db,
+                              talos_stream_t stream) {
+  TALOS_NONNULL(dout);
+  TALOS_NONNULL(da);
+  TALOS_NONNULL(db);
+  TALOS_REQUIRE(ca >= 0 && cb >= 0, TALOS_ERR_SHAPE, "%s: negative width", __func__);
+  TALOS_DEVICE();
+  if (rows == 0 || ca + cb == 0) return TALOS_OK;
+  hipLaunchKernelGGL(concat_bwd_kernel, dim3(grid_for(rows * (ca + cb))), dim3(256), 0, as_stream(stream), rows, ca, cb,
+                     dout, da, db);
+  TALOS_LAUNCHED("concat_bwd_kernel");
+  return TALOS_OK;
+}
+
+int talos_broadcast_rows_f32(size_t rows, int cols, const float* v, float* out, talos_stream_t stream) {
+  TALOS_NONNULL(v);
+  TALOS_NONNULL(out);
+  TALOS_REQUIRE(cols >= 0, TALOS_ERR_SHAPE, "%s: negative width", __func__);
+  TALOS_DEVICE();
+  if (rows == 0 || cols == 0) return TALOS_OK;
+  hipLaunchKernelGGL(broadcast_rows_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, as_stream(stream), rows, cols, v,
+                     out);
+  TALOS_LAUNCHED("broadcast_rows_kernel");
+  return TALOS_OK;
+}
+
+}  // extern "C"

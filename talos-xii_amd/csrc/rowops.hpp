@@ -1,0 +1,28 @@
+// rowops.hpp -- internal launchers of the row / element-wise kernels (rowops.hip) shared with
+// the fused plans.
+#pragma once
+
+#include <vector>
+
+#include "common.hpp"
+
+namespace talos {
+
+int fill_zero(void* dst, size_t bytes, hipStream_t s);
+
+size_t colsum_workspace_bytes(int rows, int cols);
+int colsum_launch(int rows, int cols, const float* dy, long long ld, float beta, float* out, double* ws,
+                  hipStream_t s);
+
+size_t rmsnorm_bwd_workspace_bytes(int rows, int dim);
+int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
+                       hipStream_t s);
+int rmsnorm_bwd_launch(int rows, int dim, const float* x, const float* w, const float* rstd, const float* dy,
+                       float beta_dx, float* dx, float beta_dw, float* dw, double* ws, hipStream_t s);
+
+void rope_table_host(int max_len, int dim, double base, std::vector<float>& c, std::vector<float>& s);
+int rope_table_device(int need_len, int dim, float base, const float** cosv, const float** sinv);
+int rope_launch(int n_seq, int seq, int heads, int dim, int start_pos, const float* cosv, const float* sinv,
+                const float* x, float beta, float* y, bool backward, hipStream_t s);
+
+}  // namespace talos

@@ -1,0 +1,225 @@
+// runtime.hip -- device context, allocation, copies and status reporting of libtalos_hip.so.
+//
+// The reference keeps tensors in host f64 vectors (Tensor.data / Tensor.grad,
+// src/autograd.rs:14-20) and runs ops synchronously on the calling thread. Here tensors live in
+// device memory as fp32; the _f64 copies convert at the host/device boundary, and kernel entry
+// points enqueue on the caller's stream (talos_stream_sync waits for them).
+#include <mutex>
+#include <cstdarg>
+#include <vector>
+
+#include "common.hpp"
+
+namespace talos {
+
+static thread_local std::string g_last_error;
+
+void set_error(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+}
+
+const char* last_error() { return g_last_error.c_str(); }
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return TALOS_OK;
+  set_error("%s failed: %s", what, hipGetErrorString(e));
+  return TALOS_ERR_HIP;
+}
+
+int launch_status(const char* kernel) {
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return TALOS_OK;
+  set_error("launch of %s failed: %s", kernel, hipGetErrorString(e));
+  return TALOS_ERR_HIP;
+}
+
+static std::once_flag g_init_once;
+static int g_init_status = TALOS_OK;
+static std::string g_init_error;
+
+int ensure_device() {
+  std::call_once(g_init_once, [] {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) {
+      g_init_status = TALOS_ERR_NO_DEVICE;
+      g_init_error = std::string("no usable GPU (hipGetDeviceCount: ") +
+                     (e == hipSuccess ? "0 devices" : hipGetErrorString(e)) + ")";
+      return;
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, 0) == hipSuccess) {
+      std::string arch = prop.gcnArchName;
+      if (arch.rfind("gfx950", 0) != 0) {
+        g_init_status = TALOS_ERR_NO_DEVICE;
+        g_init_error = "device 0 is " + arch + "; this library is built for gfx950 (MI355X) only";
+      }
+    }
+  });
+  if (g_init_status != TALOS_OK) set_error("%s", g_init_error.c_str());
+  return g_init_status;
+}
+
+}  // namespace talos
+
+using namespace talos;
+
+extern "C" {
+
+const char* talos_last_error(void) { return last_error(); }
+
+const char* talos_version(void) { return "talos_hip 0.1 (gfx950)"; }
+
+int talos_init(void) { return ensure_device(); }
+
+int talos_device_count(int* count) {
+  TALOS_NONNULL(count);
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+  *count = n;
+  return TALOS_OK;
+}
+
+int talos_malloc(void** ptr, size_t bytes) {
+  TALOS_NONNULL(ptr);
+  TALOS_DEVICE();
+  *ptr = nullptr;
+  if (bytes == 0) return TALOS_OK;
+  hipError_t e = hipMalloc(ptr, bytes);
+  if (e != hipSuccess) {
+    set_error("hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    *ptr = nullptr;
+    return TALOS_ERR_ALLOC;
+  }
+  return TALOS_OK;
+}
+
+int talos_free(void* ptr) {
+  if (ptr == nullptr) return TALOS_OK;
+  TALOS_DEVICE();
+  TALOS_HIP(hipFree(ptr));
+  return TALOS_OK;
+}
+
+int talos_memcpy_h2d(void* dst, const void* src, size_t bytes, talos_stream_t stream) {
+  TALOS_NONNULL(dst);
+  TALOS_NONNULL(src);
+  TALOS_DEVICE();
+  TALOS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)));
+  TALOS_HIP(hipStreamSynchronize(as_stream(stream)));
+  return TALOS_OK;
+}
+
+int talos_memcpy_d2h(void* dst, const void* src, size_t bytes, talos_stream_t stream) {
+  TALOS_NONNULL(dst);
+  TALOS_NONNULL(src);
+  TALOS_DEVICE();
+  TALOS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)));
+  TALOS_HIP(hipStreamSynchronize(as_stream(stream)));
+  return TALOS_OK;
+}
+
+int talos_memcpy_d2d(void* dst, const void* src, size_t bytes, talos_stream_t stream) {
+  TALOS_NONNULL(dst);
+  TALOS_NONNULL(src);
+  TALOS_DEVICE();
+  TALOS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)));
+  return TALOS_OK;
+}
+
+int talos_memcpy_h2d_f64(float* dst, const double* src, size_t n, talos_stream_t stream) {
+  TALOS_NONNULL(dst);
+  TALOS_NONNULL(src);
+  TALOS_DEVICE();
+  std::vector<float> tmp(n);
+  for (size_t i = 0; i < n; ++i) tmp[i] = (float)src[i];
+  TALOS_HIP(hipMemcpyAsync(dst, tmp.data(), n * sizeof(float), hipMemcpyHostToDevice, as_stream(stream)));
+  TALOS_HIP(hipStreamSynchronize(as_stream(stream)));
+  return TALOS_OK;
+}
+
+int talos_memcpy_d2h_f64(double* dst, const float* src, size_t n, talos_stream_t stream) {
+  TALOS_NONNULL(dst);
+  TALOS_NONNULL(src);
+  TALOS_DEVICE();
+  std::vector<float> tmp(n);
+  TALOS_HIP(hipMemcpyAsync(tmp.data(), src, n * sizeof(float), hipMemcpyDeviceToHost, as_stream(stream)));
+  TALOS_HIP(hipStreamSynchronize(as_stream(stream)));
+  for (size_t i = 0; i < n; ++i) dst[i] = (double)tmp[i];
+  return TALOS_OK;
+}
+
+int talos_stream_sync(talos_stream_t stream) {
+  TALOS_DEVICE();
+  TALOS_HIP(hipStreamSynchronize(as_stream(stream)));
+  return TALOS_OK;
+}
+
+int talos_stream_create(talos_stream_t* stream) {
+  TALOS_NONNULL(stream);
+  TALOS_DEVICE();
+  hipStream_t s = nullptr;
+  TALOS_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *stream = reinterpret_cast<talos_stream_t>(s);
+  return TALOS_OK;
+}
+
+int talos_stream_destroy(talos_stream_t stream) {
+  if (stream == nullptr) return TALOS_OK;
+  TALOS_DEVICE();
+  TALOS_HIP(hipStreamDestroy(as_stream(stream)));
+  return TALOS_OK;
+}
+
+// Events for timing the work enqueued on a stream (bench.py measures kernels with these on
+// the stream they run on).
+int talos_event_create(void** ev) {
+  TALOS_NONNULL(ev);
+  TALOS_DEVICE();
+  hipEvent_t e = nullptr;
+  TALOS_HIP(hipEventCreate(&e));
+  *ev = reinterpret_cast<void*>(e);
+  return TALOS_OK;
+}
+
+int talos_event_destroy(void* ev) {
+  if (ev == nullptr) return TALOS_OK;
+  TALOS_DEVICE();
+  TALOS_HIP(hipEventDestroy(reinterpret_cast<hipEvent_t>(ev)));
+  return TALOS_OK;
+}
+
+int talos_event_record(void* ev, talos_stream_t stream) {
+  TALOS_NONNULL(ev);
+  TALOS_DEVICE();
+  TALOS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(ev), as_stream(stream)));
+  return TALOS_OK;
+}
+
+int talos_event_elapsed_ms(void* start, void* stop, float* ms) {
+  TALOS_NONNULL(start);
+  TALOS_NONNULL(stop);
+  TALOS_NONNULL(ms);
+  TALOS_DEVICE();
+  TALOS_HIP(hipEventSynchronize(reinterpret_cast<hipEvent_t>(stop)));
+  TALOS_HIP(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(stop)));
+  return TALOS_OK;
+}
+
+int talos_device_info(char* name, size_t name_len, int* cu_count, int* clock_khz, size_t* total_mem) {
+  TALOS_DEVICE();
+  hipDeviceProp_t prop;
+  TALOS_HIP(hipGetDeviceProperties(&prop, 0));
+  if (name && name_len) snprintf(name, name_len, "%s (%s)", prop.name, prop.gcnArchName);
+  if (cu_count) *cu_count = prop.multiProcessorCount;
+  if (clock_khz) *clock_khz = prop.clockRate;
+  if (total_mem) *total_mem = prop.totalGlobalMem;
+  return TALOS_OK;
+}
+
+}  // extern "C"

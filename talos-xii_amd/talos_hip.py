@@ -1,0 +1,258 @@
+"""ctypes binding of libtalos_hip.so (include/talos_hip.h) with a small device-buffer helper.
+
+This is the Python side of the C ABI used by the tests and bench.py. It loads the in-tree
+library built by build_lib.py and fails loudly when it is missing: there is no CPU fallback.
+Device memory comes from the library's own allocator (talos_malloc), so a process using this
+module needs no other GPU runtime.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtalos_hip.so")
+
+# status codes (enum talos_status)
+OK, ERR_SHAPE, ERR_NULL, ERR_DTYPE, ERR_NO_DEVICE, ERR_HIP, ERR_ALLOC, ERR_HANDLE, ERR_UNSUPPORTED = range(9)
+# enum talos_unary_op / talos_binary_op / talos_activation
+RELU, LOG, EXP, SIN, COS, SQRT, NEG, SCALE, CLIP, GELU, COPY = range(11)
+ADD, SUB, MUL, DIV = range(4)
+ACT_GELU, ACT_RELU = 0, 1
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+_ll = ctypes.c_longlong
+
+
+class TalosError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"talos status {code}: {msg}")
+        self.code = code
+
+
+class BlockCfg(ctypes.Structure):
+    _fields_ = [("batch", _i), ("seq", _i), ("d_model", _i), ("n_heads", _i), ("head_dim", _i), ("ffn_dim", _i),
+                ("causal", _i), ("activation", _i), ("eps", _f), ("rope_base", _f)]
+
+
+class PpoCfg(ctypes.Structure):
+    _fields_ = [("batch", _i), ("seq", _i), ("in_dim", _i), ("d_model", _i), ("n_layers", _i), ("n_heads", _i),
+                ("head_dim", _i), ("ffn_dim", _i), ("n_actions", _i), ("causal", _i), ("activation", _i),
+                ("eps", _f), ("rope_base", _f), ("clip_eps", _f), ("value_coef", _f), ("entropy_coef", _f)]
+
+
+# name -> argtypes (restype int unless listed in _RESTYPE)
+_SIGS = {
+    "talos_last_error": [],
+    "talos_version": [],
+    "talos_init": [],
+    "talos_device_count": [ctypes.POINTER(_i)],
+    "talos_malloc": [ctypes.POINTER(_vp), _sz],
+    "talos_free": [_vp],
+    "talos_memcpy_h2d": [_vp, _vp, _sz, _vp],
+    "talos_memcpy_d2h": [_vp, _vp, _sz, _vp],
+    "talos_memcpy_d2d": [_vp, _vp, _sz, _vp],
+    "talos_memcpy_h2d_f64": [_vp, _vp, _sz, _vp],
+    "talos_memcpy_d2h_f64": [_vp, _vp, _sz, _vp],
+    "talos_fill_zero": [_vp, _sz, _vp],
+    "talos_stream_sync": [_vp],
+    "talos_stream_create": [ctypes.POINTER(_vp)],
+    "talos_stream_destroy": [_vp],
+    "talos_event_create": [ctypes.POINTER(_vp)],
+    "talos_event_destroy": [_vp],
+    "talos_event_record": [_vp, _vp],
+    "talos_event_elapsed_ms": [_vp, _vp, ctypes.POINTER(_f)],
+    "talos_device_info": [ctypes.c_char_p, _sz, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_sz)],
+    "talos_gemm_f32": [_i, _i, _i, _i, _i, _f, _vp, _i, _vp, _i, _f, _vp, _i, _vp],
+    "talos_gemm_batched_f32": [_i, _i, _i, _i, _i, _f, _vp, _i, _ll, _vp, _i, _ll, _f, _vp, _i, _ll, _i, _vp],
+    "talos_bias_grad_f32": [_i, _i, _vp, _f, _vp, _vp],
+    "talos_rmsnorm_fwd_f32": [_i, _i, _f, _vp, _vp, _vp, _vp, _vp],
+    "talos_rmsnorm_bwd_f32": [_i, _i, _vp, _vp, _vp, _vp, _f, _vp, _f, _vp, _vp],
+    "talos_softmax_fwd_f32": [_i, _i, _i, _vp, _vp, _vp],
+    "talos_softmax_bwd_f32": [_i, _i, _i, _vp, _vp, _f, _vp, _vp],
+    "talos_rope_fwd_f32": [_i, _i, _i, _i, _i, _f, _vp, _vp, _vp],
+    "talos_rope_bwd_f32": [_i, _i, _i, _i, _i, _f, _vp, _f, _vp, _vp],
+    "talos_rope_table_f32": [_i, _i, _f, _vp, _vp, _vp],
+    "talos_attn_fwd_f32": [_i, _i, _i, _i, _i, _f, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _vp],
+    "talos_attn_bwd_f32": [_i, _i, _i, _i, _i, _f, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _vp, _i, _vp, _i,
+                           _vp, _i, _vp, _i, _vp],
+    "talos_unary_fwd_f32": [_i, _sz, _f, _f, _vp, _vp, _vp],
+    "talos_unary_bwd_f32": [_i, _sz, _f, _f, _vp, _vp, _vp, _vp],
+    "talos_binary_fwd_f32": [_i, _sz, _vp, _vp, _vp, _vp],
+    "talos_binary_bwd_f32": [_i, _sz, _vp, _vp, _vp, _vp, _vp, _vp],
+    "talos_reduce_sum_f32": [_sz, _f, _vp, _vp, _vp],
+    "talos_fill_add_f32": [_sz, _f, _vp, _vp, _vp],
+    "talos_transpose_f32": [_i, ctypes.POINTER(_ll), _i, _i, _vp, _vp, _i, _vp],
+    "talos_concat_last_f32": [_sz, _i, _i, _vp, _vp, _vp, _vp],
+    "talos_concat_last_bwd_f32": [_sz, _i, _i, _vp, _vp, _vp, _vp],
+    "talos_broadcast_rows_f32": [_sz, _i, _vp, _vp, _vp],
+    "talos_block_param_count": [ctypes.POINTER(BlockCfg)],
+    "talos_ppo_param_count": [ctypes.POINTER(PpoCfg)],
+    "talos_block_plan_create": [ctypes.POINTER(BlockCfg), ctypes.POINTER(_vp)],
+    "talos_block_fwd_bwd_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    "talos_ppo_plan_create": [ctypes.POINTER(PpoCfg), ctypes.POINTER(_vp)],
+    "talos_ppo_fwd_bwd_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    "talos_ppo_forward_f32": [_vp, _vp, _vp, _vp, _vp, _vp],
+    "talos_plan_destroy": [_vp],
+}
+_RESTYPE = {"talos_last_error": ctypes.c_char_p, "talos_version": ctypes.c_char_p,
+            "talos_block_param_count": _sz, "talos_ppo_param_count": _sz}
+
+_lib = None
+
+
+def lib():
+    """Loads libtalos_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with talos-xii_amd/build_lib.py "
+                               "(or __graft_entry__.build()); there is no fallback path")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, args in _SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPE.get(name, _i)
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != OK:
+        raise TalosError(rc, lib().talos_last_error().decode())
+    return rc
+
+
+def call(name, *args):
+    return check(getattr(lib(), name)(*args))
+
+
+def device_count():
+    n = _i(0)
+    call("talos_device_count", ctypes.byref(n))
+    return n.value
+
+
+def device_info():
+    name = ctypes.create_string_buffer(256)
+    cu, clk, mem = _i(), _i(), _sz()
+    call("talos_device_info", name, 256, ctypes.byref(cu), ctypes.byref(clk), ctypes.byref(mem))
+    return {"name": name.value.decode(), "cu_count": cu.value, "clock_khz": clk.value, "total_mem": mem.value}
+
+
+class DeviceArray:
+    """A device buffer of a numpy dtype (float32 or int32) owned by talos_malloc."""
+
+    def __init__(self, shape, dtype=np.float32):
+        self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.size = int(np.prod(self.shape)) if self.shape else 1
+        self.nbytes = self.size * self.dtype.itemsize
+        p = _vp()
+        call("talos_malloc", ctypes.byref(p), max(self.nbytes, 4))
+        self.ptr = p.value
+
+    @classmethod
+    def from_numpy(cls, a, dtype=np.float32):
+        a = np.ascontiguousarray(np.asarray(a, dtype=dtype))
+        d = cls(a.shape, dtype)
+        if a.nbytes:
+            call("talos_memcpy_h2d", d.ptr, a.ctypes.data, a.nbytes, None)
+        return d
+
+    @classmethod
+    def zeros(cls, shape, dtype=np.float32):
+        d = cls(shape, dtype)
+        call("talos_fill_zero", d.ptr, max(d.nbytes, 4), None)
+        return d
+
+    def numpy(self):
+        call("talos_stream_sync", None)
+        out = np.empty(self.shape, self.dtype)
+        if self.nbytes:
+            call("talos_memcpy_d2h", out.ctypes.data, self.ptr, self.nbytes, None)
+        return out
+
+    def upload(self, a):
+        a = np.ascontiguousarray(np.asarray(a, dtype=self.dtype))
+        assert a.nbytes == self.nbytes, (a.shape, self.shape)
+        call("talos_memcpy_h2d", self.ptr, a.ctypes.data, a.nbytes, None)
+
+    def offset(self, n_elems):
+        """Raw device pointer n_elems elements into the buffer."""
+        return self.ptr + int(n_elems) * self.dtype.itemsize
+
+    def free(self):
+        if self.ptr:
+            lib().talos_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if getattr(self, "ptr", None) and _lib is not None:
+                _lib.talos_free(self.ptr)
+        except Exception:
+            pass
+
+
+def sync():
+    call("talos_stream_sync", None)
+
+
+class Plan:
+    """Owns a talos_plan (block or ppo)."""
+
+    def __init__(self, kind, cfg):
+        self.cfg = cfg
+        self.kind = kind
+        h = _vp()
+        if kind == "block":
+            call("talos_block_plan_create", ctypes.byref(cfg), ctypes.byref(h))
+            self.n_params = lib().talos_block_param_count(ctypes.byref(cfg))
+        else:
+            call("talos_ppo_plan_create", ctypes.byref(cfg), ctypes.byref(h))
+            self.n_params = lib().talos_ppo_param_count(ctypes.byref(cfg))
+        self.h = h.value
+
+    def destroy(self):
+        if self.h:
+            lib().talos_plan_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None) and _lib is not None:
+                _lib.talos_plan_destroy(self.h)
+        except Exception:
+            pass
+
+
+class Timer:
+    """HIP events on a stream (the stream the measured kernels are launched on)."""
+
+    def __init__(self, stream=None):
+        self.stream = stream
+        a, b = _vp(), _vp()
+        call("talos_event_create", ctypes.byref(a))
+        call("talos_event_create", ctypes.byref(b))
+        self.a, self.b = a.value, b.value
+
+    def start(self):
+        call("talos_event_record", self.a, self.stream)
+
+    def stop_ms(self):
+        call("talos_event_record", self.b, self.stream)
+        ms = _f()
+        call("talos_event_elapsed_ms", self.a, self.b, ctypes.byref(ms))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if _lib is not None:
+                _lib.talos_event_destroy(self.a)
+                _lib.talos_event_destroy(self.b)
+        except Exception:
+            pass

@@ -14,13 +14,25 @@ def f32(a):
     return np.asarray(a, dtype=np.float32).astype(np.float64)
 
 
-def check_close(got, ref, rtol=FP32_RTOL, atol=FP32_ATOL, name=""):
-    """Element-wise |got - ref| <= rtol * |ref| + atol; reports the worst element."""
+# Parameter gradients that are sums over many token rows (dW = X^T dY, dgain, db) with an
+# unscaled loss hold elements that cancel to a tiny fraction of the tensor's scale; there the
+# fp32 rounding of the inputs alone exceeds 1e-5 absolute (torch's own fp32 CPU autograd fails
+# the plain rule on the C3 block: 118 of 197504 parameter-gradient elements at batch 64). For
+# those tensors the absolute floor is raised to 1e-6 of the tensor's largest |ref| (16 fp32 ulps
+# of its largest element); everything else uses the plain floor.
+GRAD_SCALE_FLOOR = 1e-6
+
+
+def check_close(got, ref, rtol=FP32_RTOL, atol=FP32_ATOL, name="", scale_floor=0.0):
+    """Element-wise |got - ref| <= rtol * |ref| + max(atol, scale_floor * max|ref|); reports the
+    worst element."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     assert got.shape == ref.shape, f"{name}: shape {got.shape} vs {ref.shape}"
     assert np.all(np.isfinite(got)), f"{name}: non-finite values"
     err = np.abs(got - ref)
+    if scale_floor and ref.size:
+        atol = max(atol, scale_floor * float(np.abs(ref).max()))
     bound = rtol * np.abs(ref) + atol
     bad = err > bound
     if bad.any():

@@ -1,0 +1,110 @@
+"""CPU-side tests of the C ABI: the library loads, exports every function include/talos_hip.h
+declares, and rejects bad arguments on the host before any device work (the reference panics via
+assert! on the same conditions, src/autograd.rs:96-100, 209; src/nn.rs:187)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import talos_hip as th
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "talos_hip.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int|size_t|void)\s+(talos_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    return th.lib()
+
+
+def test_header_symbols_exported(L):
+    names = header_functions()
+    assert len(names) >= 40
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, f"declared in talos_hip.h but not exported: {missing}"
+    # and the binding's signature table covers exactly the header
+    assert sorted(th._SIGS) == names
+
+
+def test_version_and_device_count(L):
+    assert b"gfx950" in L.talos_version()
+    assert th.device_count() >= 0
+
+
+def _null():
+    return ctypes.c_void_p(0)
+
+
+def test_gemm_argument_errors(L):
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    assert L.talos_gemm_f32(0, 0, 4, 4, 4, 1.0, None, 4, p, 4, 0.0, p, 4, None) == th.ERR_NULL
+    assert L.talos_gemm_f32(0, 0, -1, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4, None) == th.ERR_SHAPE
+    assert L.talos_gemm_f32(0, 0, 4, 4, 8, 1.0, p, 4, p, 4, 0.0, p, 4, None) == th.ERR_SHAPE  # lda < K
+    assert L.talos_gemm_f32(1, 0, 8, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4, None) == th.ERR_SHAPE  # lda < M (transA)
+    assert L.talos_gemm_f32(0, 1, 4, 4, 8, 1.0, p, 8, p, 4, 0.0, p, 4, None) == th.ERR_SHAPE  # ldb < K (transB)
+    assert L.talos_gemm_f32(0, 0, 4, 8, 4, 1.0, p, 4, p, 8, 0.0, p, 4, None) == th.ERR_SHAPE  # ldc < N
+    assert L.talos_gemm_f32(2, 0, 4, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4, None) == th.ERR_DTYPE
+    assert L.talos_gemm_f32(0, 0, 4, 4, 4, 1.0, p, 4, p, 4, 0.5, p, 4, None) == th.ERR_UNSUPPORTED
+    assert b"beta" in L.talos_last_error()
+
+
+def test_row_op_argument_errors(L):
+    p = ctypes.c_void_p(16)
+    assert L.talos_rmsnorm_fwd_f32(4, 0, 1e-6, p, p, p, p, None) == th.ERR_SHAPE
+    assert L.talos_rmsnorm_fwd_f32(4, 8, 1e-6, None, p, p, p, None) == th.ERR_NULL
+    assert L.talos_rmsnorm_bwd_f32(4, 8, p, p, p, p, 2.0, p, 0.0, p, None) == th.ERR_UNSUPPORTED
+    assert L.talos_softmax_fwd_f32(4, 8, 3, p, p, None) == th.ERR_DTYPE
+    assert L.talos_rope_fwd_f32(1, 4, 2, 7, 0, 1e4, p, p, None) == th.ERR_SHAPE  # odd dim
+    assert L.talos_rope_fwd_f32(1, 4, 2, 8, -1, 1e4, p, p, None) == th.ERR_SHAPE
+    assert L.talos_unary_fwd_f32(99, 4, 0.0, 0.0, p, p, None) == th.ERR_DTYPE
+    assert L.talos_binary_fwd_f32(7, 4, p, p, p, None) == th.ERR_DTYPE
+    shape = (ctypes.c_longlong * 2)(2, 3)
+    assert L.talos_transpose_f32(2, shape, 0, 2, p, p, 0, None) == th.ERR_SHAPE
+    assert L.talos_transpose_f32(7, shape, 0, 1, p, p, 0, None) == th.ERR_SHAPE
+
+
+def test_attention_argument_errors(L):
+    p = ctypes.c_void_p(16)
+    args = [p, 96, p, 96, p, 96, p, 32, p, None]
+    assert L.talos_attn_fwd_f32(2, 8, 4, 200, 32, 0.1, 1, *args) == th.ERR_UNSUPPORTED  # head dim > 128
+    assert L.talos_attn_fwd_f32(2, 8, 4, 32, 32, 0.1, 2, *args) == th.ERR_DTYPE
+    assert L.talos_attn_fwd_f32(2, 8, 4, 32, 32, 0.1, 1, p, 64, p, 96, p, 96, p, 32, p, None) == th.ERR_SHAPE
+
+
+def test_plan_config_errors(L):
+    cfg = th.BlockCfg(2, 8, 30, 4, 8, 64, 1, 0, 1e-6, 1e4)  # 4 * 8 != 30
+    h = ctypes.c_void_p()
+    assert L.talos_block_plan_create(ctypes.byref(cfg), ctypes.byref(h)) == th.ERR_SHAPE
+    cfg = th.BlockCfg(2, 8, 32, 4, 8, 64, 1, 7, 1e-6, 1e4)  # bad activation
+    assert L.talos_block_plan_create(ctypes.byref(cfg), ctypes.byref(h)) == th.ERR_DTYPE
+    assert L.talos_block_fwd_bwd_f32(None, *([ctypes.c_void_p(16)] * 6), None) == th.ERR_HANDLE
+    pc = th.PpoCfg(4, 8, 8, 32, 2, 4, 8, 64, 0, 1, 0, 1e-5, 1e4, 0.2, 0.5, 0.01)  # 0 actions
+    assert L.talos_ppo_plan_create(ctypes.byref(pc), ctypes.byref(h)) == th.ERR_SHAPE
+
+
+def test_param_counts_match_oracle(oracle):
+    import common
+    bc = th.BlockCfg(4, 64, 128, 4, 32, 512, 1, 0, 1e-6, 1e4)
+    assert th.lib().talos_block_param_count(ctypes.byref(bc)) == 128 + 3 * 128 * 128 + 128 * 128 + 128 + 2 * 128 * 512 + 512 + 128
+    pc = th.PpoCfg(8, 32, 8, 128, 2, 4, 32, 512, 3, 1, 0, 1e-5, 1e4, 0.2, 0.5, 0.01)
+    opc = oracle.PpoCfg(8, 32, 8, 128, 2, 4, 32, 512, 3, 1, 0, 1e-5, 1e4, 0.2, 0.5, 0.01)
+    n = th.lib().talos_ppo_param_count(ctypes.byref(pc))
+    assert n == oracle.ppo_param_count(opc)
+    assert n == common.ppo_params(np.random.default_rng(0), opc).size
+
+
+def test_no_device_is_a_clean_error(L):
+    if th.device_count() > 0:
+        pytest.skip("a GPU is present")
+    p = ctypes.c_void_p()
+    assert L.talos_malloc(ctypes.byref(p), 64) == th.ERR_NO_DEVICE
+    assert L.talos_init() == th.ERR_NO_DEVICE
+    assert b"GPU" in L.talos_last_error()

@@ -1,0 +1,122 @@
+"""GPU parity of the fused block (C3) and PPO policy minibatch (C4) plans against the f64 oracle.
+
+Reduced batch sizes keep the oracle within seconds; the kernels and launch geometry are the
+ones of the full configurations (d_model 128, 4 heads x 32, seq 64 / 32, 4x GELU MLP).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import talos_hip as th
+from common import GRAD_SCALE_FLOOR, block_params, check_close, f32, gacha_states, ppo_params
+
+pytestmark = pytest.mark.gpu
+DA = th.DeviceArray
+
+BLOCK_NAMES = ["g1", "wqkv", "wo", "g2", "w1", "b1", "w2", "b2"]
+
+
+def block_slices(d, F):
+    sizes = [d, 3 * d * d, d * d, d, d * F, F, F * d, d]
+    out, o = {}, 0
+    for n, s in zip(BLOCK_NAMES, sizes):
+        out[n] = slice(o, o + s)
+        o += s
+    return out
+
+
+def run_block(cfg, p, x, G):
+    plan = th.Plan("block", cfg)
+    P, X, Gd = DA.from_numpy(p), DA.from_numpy(x), DA.from_numpy(G)
+    out, dp, dx = DA.zeros(x.shape), DA.zeros(p.size), DA.zeros(x.shape)
+    th.call("talos_block_fwd_bwd_f32", plan.h, P.ptr, X.ptr, Gd.ptr, out.ptr, dp.ptr, dx.ptr, None)
+    res = out.numpy(), dp.numpy(), dx.numpy()
+    plan.destroy()
+    return res
+
+
+@pytest.mark.parametrize("B,S,d,H,F,causal,act", [(2, 6, 16, 4, 64, 1, 0), (3, 64, 128, 4, 512, 1, 0),
+                                                  (2, 33, 64, 2, 128, 0, 1)])
+def test_block_fwd_bwd_vs_oracle(oracle, B, S, d, H, F, causal, act):
+    rng = np.random.default_rng(1000 + S + d)
+    cfg = th.BlockCfg(B, S, d, H, d // H, F, causal, act, 1e-6, 10000.0)
+    ocfg = oracle.BlockCfg(B, S, d, H, d // H, F, causal, act, 1e-6, 10000.0)
+    p = f32(block_params(rng, d, F, gain_jitter=True))
+    x, G = f32(rng.normal(size=(B, S, d))), f32(rng.normal(size=(B, S, d)))
+    out_r, dp_r, dx_r = oracle.block_fwd_bwd(ocfg, p, x, G)
+    out, dp, dx = run_block(cfg, p, x, G)
+    check_close(out, out_r, name="out")
+    check_close(dx, dx_r, name="dx")
+    for n, sl in block_slices(d, F).items():
+        check_close(dp[sl], dp_r[sl], name=f"d{n}", scale_floor=GRAD_SCALE_FLOOR)
+
+
+def ppo_cfgs(oracle, B, S=32, d=128, L=2, H=4, F=512, A=3):
+    args = (B, S, 8, d, L, H, d // H, F, A, 1, 0, 1e-5, 10000.0, 0.2, 0.5, 0.01)
+    return th.PpoCfg(*args), oracle.PpoCfg(*args)
+
+
+def ppo_inputs(rng, ocfg, p, oracle, spread=0.3):
+    B, A = ocfg.batch, ocfg.n_actions
+    states = f32(gacha_states(rng, B, ocfg.seq))
+    actions = rng.integers(0, A, B).astype(np.int32)
+    adv, ret = f32(rng.normal(size=B)), f32(rng.normal(size=B))
+    _, logits, _, _ = oracle.ppo_fwd_bwd(ocfg, p, states, actions, adv, ret, np.zeros(B))
+    mx = logits.max(1, keepdims=True)
+    lp = logits - mx - np.log(np.exp(logits - mx).sum(1, keepdims=True))
+    old = f32(lp[np.arange(B), actions] + rng.uniform(-spread, spread, B))
+    return states, actions, adv, ret, old
+
+
+def run_ppo(cfg, p, states, actions, adv, ret, old):
+    plan = th.Plan("ppo", cfg)
+    P, St = DA.from_numpy(p), DA.from_numpy(states)
+    Ac = DA.from_numpy(actions, np.int32)
+    Ad, Re, Ol = DA.from_numpy(adv), DA.from_numpy(ret), DA.from_numpy(old)
+    loss, dp = DA.zeros(1), DA.zeros(p.size)
+    th.call("talos_ppo_fwd_bwd_f32", plan.h, P.ptr, St.ptr, Ac.ptr, Ad.ptr, Re.ptr, Ol.ptr, loss.ptr, dp.ptr, None)
+    lg, vl = DA.zeros((cfg.batch, cfg.n_actions)), DA.zeros(cfg.batch)
+    th.call("talos_ppo_forward_f32", plan.h, P.ptr, St.ptr, lg.ptr, vl.ptr, None)
+    res = float(loss.numpy()[0]), dp.numpy(), lg.numpy(), vl.numpy()
+    plan.destroy()
+    return res
+
+
+def ppo_slices(cfg):
+    d, F, I, A = cfg.d_model, cfg.ffn_dim, cfg.in_dim, cfg.n_actions
+    names = [("We", I * d), ("be", d)]
+    for l in range(cfg.n_layers):
+        names += [(f"L{l}.{n}", s) for n, s in zip(BLOCK_NAMES, [d, 3 * d * d, d * d, d, d * F, F, F * d, d])]
+    names += [("gf", d), ("Wout", d * d), ("bout", d), ("Wa", d * A), ("ba", A), ("Wc", d), ("bc", 1)]
+    out, o = {}, 0
+    for n, s in names:
+        out[n] = slice(o, o + s)
+        o += s
+    return out
+
+
+@pytest.mark.parametrize("B,S,L", [(6, 5, 2), (64, 32, 2), (16, 32, 1)])
+def test_ppo_minibatch_vs_oracle(oracle, B, S, L):
+    rng = np.random.default_rng(2000 + B + S)
+    cfg, ocfg = ppo_cfgs(oracle, B, S=S, L=L)
+    p = f32(ppo_params(rng, ocfg))
+    states, actions, adv, ret, old = ppo_inputs(rng, ocfg, p, oracle)
+    loss_r, logits_r, values_r, dp_r = oracle.ppo_fwd_bwd(ocfg, p, states, actions, adv, ret, old)
+    loss, dp, logits, values = run_ppo(cfg, p, states, actions, adv, ret, old)
+    check_close(logits, logits_r, name="logits")
+    check_close(values, values_r, name="values")
+    check_close(loss, loss_r, name="loss")
+    for n, sl in ppo_slices(ocfg).items():
+        check_close(dp[sl], dp_r[sl], name=f"d{n}", scale_floor=GRAD_SCALE_FLOOR)
+
+
+def test_ppo_bad_action_is_nan_not_a_fault(oracle):
+    rng = np.random.default_rng(7)
+    cfg, ocfg = ppo_cfgs(oracle, 4, S=4, L=1)
+    p = f32(ppo_params(rng, ocfg))
+    states = f32(gacha_states(rng, 4, 4))
+    actions = np.array([0, 1, 5, 2], np.int32)  # 5 is out of range for 3 actions
+    z = np.zeros(4, np.float32)
+    loss, dp, _, _ = run_ppo(cfg, p, states, actions, z, z, z)
+    assert np.isnan(loss)
