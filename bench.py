@@ -1,0 +1,232 @@
+#!/usr/bin/env python3
+"""PPO policy minibatch forward + backward throughput on one MI355X (BASELINE.json metric).
+
+One step = one talos_ppo_fwd_bwd_f32 call on the C4 configuration: a minibatch of 4096 gacha
+state sequences of 32 tokens through the 2-layer d128 policy (4 heads x 32, RoPE, causal
+attention, 4x GELU MLP, last-token actor/critic heads), the clipped PPO loss, and the gradients
+of every parameter, all fp32 and resident in HBM before the timed region starts.
+
+Printed (one JSON line): samples/s over the timed steps; the roofline of the dominant kernel
+(algorithmic flops or bytes per launch over its average launch time, measured with HIP events
+on the stream the kernels run on); and the CPU baseline: the f64 oracle (a C++ restatement of
+the reference's Rust autograd) timed on this host's cores on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "talos-xii_amd"), os.path.join(ROOT, "oracle")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+import talos_hip as th  # noqa: E402
+import workload as wl  # noqa: E402
+
+METRIC = "PPO policy fwd+bwd samples/sec (d128 block, 1 GPU); % MFMA/HBM roofline"
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def ppo_cfg(B, S):
+    # batch, seq, in_dim, d_model, n_layers, n_heads, head_dim, ffn_dim, n_actions, causal,
+    # activation (GELU), eps, rope_base, clip_eps, value_coef, entropy_coef
+    return (B, S, 8, 128, 2, 4, 32, 512, 3, 1, th.ACT_GELU, 1e-5, 10000.0, 0.2, 0.5, 0.01)
+
+
+def make_inputs(cfg_t, seed=0):
+    B, S = cfg_t[0], cfg_t[1]
+    cfg = th.PpoCfg(*cfg_t)
+    rng = np.random.default_rng(seed)
+    p = wl.ppo_params(rng, cfg).astype(np.float32)
+    states = wl.gacha_states(rng, B, S).astype(np.float32)
+    actions = rng.integers(0, cfg.n_actions, B).astype(np.int32)
+    adv = rng.normal(size=B).astype(np.float32)
+    ret = rng.normal(size=B).astype(np.float32)
+    return cfg, p, states, actions, adv, ret
+
+
+def aggregate(records):
+    agg = {}
+    for k, fl, by, ms in records:
+        a = agg.setdefault(k, [0, 0.0, 0.0, 0.0])
+        a[0] += 1
+        a[1] += fl
+        a[2] += by
+        a[3] += ms
+    return agg
+
+
+def roofline_of(name, n, flops, bytes_, ms):
+    avg_ms = ms / n
+    if name.startswith("gemm_f32_kernel"):
+        achieved = flops / n / (avg_ms * 1e-3) / 1e12
+        return {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4)}
+    achieved = bytes_ / n / (avg_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4)}
+
+
+def traffic_of(kernel):
+    """HBM bytes per launch of the kernel from the committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        return json.load(open(path)).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(cfg_t, seconds_budget=20.0):
+    """The f64 oracle on this host: reference-faithful per-sample batch-1 graphs (the backbone run
+    for the actor and again for the critic, src/ppo.rs:691-757) on a bounded sample, plus the
+    batched restatement. Threads: this host's cores, at most 16 (a GPU box's CPU share)."""
+    import pyoracle
+    if not os.path.exists(pyoracle.LIB_PATH):
+        pyoracle.build()
+    threads = max(1, min(16, os.cpu_count() or 1))
+    pyoracle.set_threads(threads)
+
+    def run(n, per_sample):
+        t = ppo_cfg(n, cfg_t[1])
+        ocfg = pyoracle.PpoCfg(*t)
+        _, p, states, actions, adv, ret = make_inputs(t, seed=1)
+        old = np.full(n, -1.1)
+        t0 = time.perf_counter()
+        if per_sample:
+            pyoracle.ppo_fwd_bwd_per_sample(ocfg, p, states, actions, adv, ret, old, True)
+        else:
+            pyoracle.ppo_fwd_bwd(ocfg, p, states, actions, adv, ret, old)
+        return time.perf_counter() - t0
+
+    # calibrate on 4 samples, then size the sample to about half the budget per mode
+    t4 = run(4, True)
+    n_ps = int(max(8, min(512, 0.5 * seconds_budget / max(t4 / 4, 1e-4))))
+    t_ps = run(n_ps, True)
+    t16 = run(16, False)
+    n_b = int(max(16, min(1024, 0.5 * seconds_budget / max(t16 / 16, 1e-4))))
+    t_b = run(n_b, False)
+    return {"value": round(n_ps / t_ps, 2), "unit": "samples/s", "cores": threads, "kind": "port",
+            "sample": f"{n_ps} samples of the C4 minibatch (seq 32, 2-layer d128), one batch-1 f64 graph per "
+                      f"sample with the backbone run for actor and critic as src/ppo.rs:691-757 does; C++ "
+                      f"restatement of the Rust autograd on {threads} threads",
+            "batched_value": round(n_b / t_b, 2),
+            "batched_sample": f"{n_b} samples as one batched f64 graph"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=4096)
+    ap.add_argument("--seq", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--profile-table", action="store_true", help="print the per-kernel table to stderr")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+              "The minibatch would shard over samples with one gradient all-reduce; see DESIGN.md.",
+              file=sys.stderr)
+        sys.exit(2)
+    rank = int(os.environ.get("RANK", "0"))
+
+    cfg_t = ppo_cfg(args.batch, args.seq)
+    cfg, p, states, actions, adv, ret = make_inputs(cfg_t)
+    B = cfg.batch
+    plan = th.Plan("ppo", cfg)
+    P, St = th.DeviceArray.from_numpy(p), th.DeviceArray.from_numpy(states)
+    Ac = th.DeviceArray.from_numpy(actions, np.int32)
+    Ad, Re = th.DeviceArray.from_numpy(adv), th.DeviceArray.from_numpy(ret)
+    # old log-probs: the initial policy's (ratio = 1 on the first epoch, as in a PPO update)
+    lg, vl = th.DeviceArray.zeros((B, cfg.n_actions)), th.DeviceArray.zeros(B)
+    th.call("talos_ppo_forward_f32", plan.h, P.ptr, St.ptr, lg.ptr, vl.ptr, None)
+    old = wl.log_softmax(lg.numpy().astype(np.float64))[np.arange(B), actions].astype(np.float32)
+    Ol = th.DeviceArray.from_numpy(old)
+    loss, dP = th.DeviceArray.zeros(1), th.DeviceArray.zeros(p.size)
+
+    def step():
+        th.call("talos_ppo_fwd_bwd_f32", plan.h, P.ptr, St.ptr, Ac.ptr, Ad.ptr, Re.ptr, Ol.ptr, loss.ptr, dP.ptr, None)
+
+    for _ in range(args.warmup):
+        step()
+    th.sync()
+    assert np.isfinite(loss.numpy()[0]), "non-finite loss"
+
+    # 1) per-kernel breakdown of one step (all launches event-bracketed)
+    plan.profile(True)
+    step()
+    th.sync()
+    agg = aggregate(plan.profile_records())
+    plan.profile(False)
+    dominant = max(agg, key=lambda k: agg[k][3])
+
+    # 2) the timed region: K steps, synchronised on both sides
+    timer = th.Timer(None)
+    th.sync()
+    timer.start()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    ms_total = timer.stop_ms()
+    wall = time.perf_counter() - t0
+    ms_step = ms_total / args.steps
+    value = B * args.steps / (ms_total * 1e-3)
+
+    # 3) the same K steps again with the dominant kernel's launches event-bracketed
+    plan.profile(True, dominant)
+    for _ in range(args.steps):
+        step()
+    th.sync()
+    dom = aggregate(plan.profile_records()).get(dominant)
+    plan.profile(False)
+    n, fl, by, ms = dom
+    roof = roofline_of(dominant, n, fl, by, ms)
+    roof["kernel"] = dominant
+    roof["launches_per_step"] = n // args.steps
+    roof["avg_launch_us"] = round(ms / n * 1e3, 2)
+    roof["traffic"] = traffic_of(dominant)
+    roof["algorithmic_per_launch"] = {"flops": fl / n, "bytes": by / n}
+
+    step_flops = wl.ppo_step_flops(B, cfg.seq, cfg.in_dim, cfg.d_model, cfg.n_layers, cfg.n_heads, cfg.ffn_dim,
+                                   cfg.n_actions)
+    info = th.device_info()
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": "C4: PPO policy minibatch fwd+bwd, 4096 samples x seq 32 gacha states (8 features), "
+                               "2-layer pre-norm d128, 4 heads x 32, RoPE, causal attention, 4x GELU MLP, 3 actions",
+                   "batch": B, "seq": cfg.seq, "d_model": cfg.d_model, "n_layers": cfg.n_layers,
+                   "n_heads": cfg.n_heads, "ffn_dim": cfg.ffn_dim, "n_actions": cfg.n_actions},
+        "roofline": roof,
+        "step": {"algorithmic_gflop": round(step_flops / 1e9, 2),
+                 "tflops": round(step_flops / (ms_step * 1e-3) / 1e12, 2),
+                 "frac_fp32_mfma_peak": round(step_flops / (ms_step * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+                 "wall_ms_per_step": round(wall * 1e3 / args.steps, 4)},
+        "kernels": {k: {"launches": v[0], "ms": round(v[3], 4), "pct": round(100 * v[3] / sum(a[3] for a in agg.values()), 1)}
+                    for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3])},
+        "device": info["name"],
+    }
+    if args.profile_table:
+        for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3]):
+            print(f"{k:40s} n={v[0]:3d} {v[3]:8.3f} ms  {v[1] / max(v[3], 1e-9) / 1e9:8.2f} TFLOP/s "
+                  f"{v[2] / max(v[3], 1e-9) / 1e6:8.1f} GB/s", file=sys.stderr)
+    if rank == 0 and not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(cfg_t, args.cpu_seconds)
+    elif rank == 0:
+        out["cpu_baseline"] = None
+    plan.destroy()
+    if rank == 0:
+        print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -258,6 +258,23 @@ int talos_ppo_forward_f32(talos_plan plan, const float* params, const float* sta
 
 int talos_plan_destroy(talos_plan plan);
 
+/* Per-launch profiling of a plan's entry points (the reference has only ad-hoc Instant timers
+ * that print, src/dqn.rs:483-583 and src/autograd.rs:1877-1890). While enabled, every kernel the
+ * plan launches is bracketed by two HIP events on its stream and recorded with the kernel's name
+ * and its algorithmic flops and HBM bytes. kernel_filter (NULL = all) keeps only launches whose
+ * kernel name contains it. Enabling clears earlier records (after a device synchronise). */
+typedef struct talos_profiler_s* talos_profiler;
+typedef struct talos_prof_record {
+  char kernel[64];
+  double flops;
+  double bytes;
+  float ms;
+} talos_prof_record;
+int talos_plan_profiler(talos_plan plan, talos_profiler* prof);
+int talos_profiler_enable(talos_profiler prof, int enable, const char* kernel_filter);
+/* Copies up to max_records records (waiting for their events); *count = records held. */
+int talos_profiler_read(talos_profiler prof, talos_prof_record* out, int max_records, int* count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -62,6 +62,20 @@ __device__ __forceinline__ void rope_transpose_row(float (&g)[DKM], const AttnAr
   }
 }
 
+// Dot product of a register row with an LDS row, as four independent FMA chains.
+template <int D>
+__device__ __forceinline__ float dot_row(const float (&r)[D], const float* __restrict__ t) {
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+  for (int e = 0; e < D; e += 4) {
+    s0 = fmaf(r[e], t[e], s0);
+    s1 = fmaf(r[e + 1], t[e + 1], s1);
+    s2 = fmaf(r[e + 2], t[e + 2], s2);
+    s3 = fmaf(r[e + 3], t[e + 3], s3);
+  }
+  return (s0 + s1) + (s2 + s3);
+}
+
 // Cooperative copy of rows [r0, r0 + nr) of each of the workgroup's P pairs into an LDS tile
 // [P][nr][DM] (dims >= dim are zero-filled).
 template <int DM>
@@ -120,9 +134,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     const float* kt = Ks + pl * a.KT * DKM;
     const float* vt = Vs + pl * a.KT * DVM;
     for (int j = 0; j < jn; ++j) {
-      float s = 0.f;
-#pragma unroll
-      for (int e = 0; e < DKM; ++e) s = fmaf(q[e], kt[j * DKM + e], s);
+      const float s = dot_row<DKM>(q, kt + j * DKM);
       if (s > m) {
         const float corr = expf(m - s);
         l *= corr;
@@ -193,11 +205,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     const float* kt = Ks + pl * a.KT * DKM;
     const float* vt = Vs + pl * a.KT * DVM;
     for (int j = 0; j < jn; ++j) {
-      float s = 0.f, dp = 0.f;
-#pragma unroll
-      for (int e = 0; e < DKM; ++e) s = fmaf(q[e], kt[j * DKM + e], s);
-#pragma unroll
-      for (int e = 0; e < DVM; ++e) dp = fmaf(g[e], vt[j * DVM + e], dp);
+      const float s = dot_row<DKM>(q, kt + j * DKM);
+      const float dp = dot_row<DVM>(g, vt + j * DVM);
       const float p = expf(s - lse);
       const float ds = p * (dp - D);
 #pragma unroll
@@ -268,18 +277,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a) {
     const float* lt = Ls + pl * a.KT;
     const float* dt = Ds + pl * a.KT;
     for (int i = ibeg; i < ni; ++i) {
-      float s = 0.f;
-#pragma unroll
-      for (int e = 0; e < DKM; ++e) s = fmaf(k[e], qt[i * DKM + e], s);
+      const float s = dot_row<DKM>(k, qt + i * DKM);
       const float p = expf(s - lt[i]);
       if (DO_DV) {
 #pragma unroll
         for (int e = 0; e < DVM; ++e) dv[e] = fmaf(p, gt[i * DVM + e], dv[e]);
       }
       if (DO_DK) {
-        float dp = 0.f;
-#pragma unroll
-        for (int e = 0; e < DVM; ++e) dp = fmaf(v[e], gt[i * DVM + e], dp);
+        const float dp = dot_row<DVM>(v, gt + i * DVM);
         const float ds = p * (dp - dt[i]);
 #pragma unroll
         for (int e = 0; e < DKM; ++e) dk[e] = fmaf(ds, qt[i * DKM + e], dk[e]);
@@ -324,10 +329,18 @@ static bool pick_dims(int dk, int dv, int* dkm, int* dvm) {
   return false;
 }
 
-#define ATTN_DISPATCH(DK, DV, KERNEL, ...)                                            \
-  if (dkm == DK && dvm == DV) {                                                       \
-    hipLaunchKernelGGL((KERNEL<DK, DV, ##__VA_ARGS__>), grid, dim3(256), lds, s, a); \
-    return launch_status(#KERNEL);                                                    \
+// Algorithmic work of one pass over all (batch, head) pairs: `per_pair_flops` flops per
+// (query, key) pair that the mask keeps, `bytes` of HBM traffic.
+static double kept_pairs(const AttnArgs& a) {
+  const double S = a.S;
+  return (double)a.B * a.H * (a.causal ? S * (S + 1) / 2 : S * S);
+}
+
+#define ATTN_DISPATCH(DK, DV, KERNEL, ...)                                                          \
+  if (dkm == DK && dvm == DV) {                                                                     \
+    ProfScope ps(s, #KERNEL "<" #DK ", " #DV ">", flops, bytes);                                    \
+    hipLaunchKernelGGL((KERNEL<DK, DV, ##__VA_ARGS__>), grid, dim3(256), lds, s, a);               \
+    return launch_status(#KERNEL);                                                                  \
   }
 
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
@@ -344,6 +357,10 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
   geometry(a, dkm, dvm, 0);
   const size_t lds = (size_t)a.P * a.KT * (dkm + dvm) * sizeof(float);
   dim3 grid(ceil_div((size_t)a.B * a.H, a.P), ceil_div(a.S, a.QB));
+  const double rows = (double)a.B * a.S * a.H;  // (token, head) rows
+  // QK^T and PV over the kept pairs; q, k, v read, o and lse written
+  const double flops = kept_pairs(a) * (2.0 * a.dk + 2.0 * a.dv);
+  const double bytes = 4.0 * rows * (2.0 * a.dk + a.dv) + 4.0 * rows * (a.dv + 1.0);
   ATTN_DISPATCH(32, 32, attn_fwd_kernel)
   ATTN_DISPATCH(64, 64, attn_fwd_kernel)
   ATTN_DISPATCH(96, 64, attn_fwd_kernel)
@@ -370,11 +387,15 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
   a.D = ws;
   a.rcos = d.rope_cos; a.rsin = d.rope_sin; a.rope_off = d.rope_off; a.rope_dim = d.rope_dim;
   if ((long long)a.B * a.H * a.S == 0) return TALOS_OK;
+  const double rows = (double)a.B * a.S * a.H;
   int rc;
   {
     geometry(a, dkm, dvm, 0);
     const size_t lds = (size_t)a.P * a.KT * (dkm + dvm) * sizeof(float);
     dim3 grid(ceil_div((size_t)a.B * a.H, a.P), ceil_div(a.S, a.QB));
+    // s = q.k, dp = dO.v, dq += ds k; reads q k v o dO lse, writes dq and D
+    const double flops = kept_pairs(a) * (4.0 * a.dk + 2.0 * a.dv);
+    const double bytes = 4.0 * rows * (3.0 * a.dk + 3.0 * a.dv + 2.0);
     rc = [&]() -> int {
       ATTN_DISPATCH(32, 32, attn_bwd_dq_kernel)
       ATTN_DISPATCH(64, 64, attn_bwd_dq_kernel)
@@ -388,16 +409,22 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
   const size_t lds = (size_t)a.P * a.KT * (dkm + dvm + 2) * sizeof(float);
   dim3 grid(ceil_div((size_t)a.B * a.H, a.P), ceil_div(a.S, a.QB));
   if (dkm + dvm <= 64) {
-    // small heads: one pass computes both dK and dV
+    // small heads: one pass computes both dK and dV; reads q dO lse D k v, writes dk dv
+    const double flops = kept_pairs(a) * (4.0 * a.dk + 4.0 * a.dv);
+    const double bytes = 4.0 * rows * (3.0 * a.dk + 3.0 * a.dv + 2.0);
     ATTN_DISPATCH(32, 32, attn_bwd_dkv_kernel, true, true)
   }
   rc = [&]() -> int {
+    const double flops = kept_pairs(a) * (4.0 * a.dk + 2.0 * a.dv);
+    const double bytes = 4.0 * rows * (3.0 * a.dk + 2.0 * a.dv + 2.0);
     ATTN_DISPATCH(64, 64, attn_bwd_dkv_kernel, true, false)
     ATTN_DISPATCH(96, 64, attn_bwd_dkv_kernel, true, false)
     ATTN_DISPATCH(128, 128, attn_bwd_dkv_kernel, true, false)
     return TALOS_ERR_UNSUPPORTED;
   }();
   if (rc) return rc;
+  const double flops = kept_pairs(a) * (2.0 * a.dk + 2.0 * a.dv);
+  const double bytes = 4.0 * rows * (2.0 * a.dk + 2.0 * a.dv + 1.0);
   ATTN_DISPATCH(64, 64, attn_bwd_dkv_kernel, false, true)
   ATTN_DISPATCH(96, 64, attn_bwd_dkv_kernel, false, true)
   ATTN_DISPATCH(128, 128, attn_bwd_dkv_kernel, false, true)

@@ -28,6 +28,24 @@ int hip_status(hipError_t e, const char* what);
 // Checks the launch that was just enqueued.
 int launch_status(const char* kernel);
 
+// Per-launch event profiling (talos_plan_profile): when a profiler is active on the calling
+// thread, every kernel launch is bracketed by two HIP events on its stream and tagged with the
+// kernel's name and its algorithmic flops / bytes.
+struct Profiler;
+Profiler* profiler_new();
+void profiler_delete(Profiler* p);
+void profiler_set_current(Profiler* p);  // thread-local; nullptr switches profiling off
+int prof_begin(hipStream_t s, const char* kernel, double flops, double bytes);
+void prof_end(hipStream_t s, int idx);
+
+struct ProfScope {
+  hipStream_t s;
+  int idx;
+  ProfScope(hipStream_t s_, const char* kernel, double flops, double bytes)
+      : s(s_), idx(prof_begin(s_, kernel, flops, bytes)) {}
+  ~ProfScope() { prof_end(s, idx); }
+};
+
 }  // namespace talos
 
 // Host-side validation: every entry point checks its arguments before touching the device,

@@ -8,7 +8,10 @@
 // 64x64 quarter as 2x2 MFMA 32x32 accumulators (64 accumulator registers per lane). K advances
 // in chunks of 32 staged through LDS as k-major panels As[k][m], Bs[k][n]; the next chunk is
 // fetched into registers while the matrix cores work on the current one. Both transposed and
-// plain operand layouts are read with 16-byte loads along their contiguous dimension.
+// plain operand layouts are read with 16-byte loads along their contiguous dimension; interior
+// tiles take an unchecked load / store path and only edge tiles test bounds per element.
+// The epilogue (bias, residual, activation or its derivative, RoPE) is a compile-time set of
+// flags, so each instantiation carries only the code it uses.
 // Long-K products with a small C (the weight gradients, K = tokens) are split over K; the fp32
 // partial tiles are combined in f64 by a second kernel, which keeps the gradient sums over
 // 10^5 tokens within the accuracy of an fp32 dot product of length K/ksplit.
@@ -23,6 +26,19 @@ constexpr int LDS_S = 160;  // panel row stride (floats): the two half-waves rea
                             // whose offset 160 = 32 mod 64 keeps them on disjoint LDS banks
 constexpr int NT = 256;
 
+// Epilogue flags (template parameter E).
+enum : int {
+  E_BETA = 1,    // + beta * C
+  E_BIAS = 2,    // + bias[col]
+  E_RESID = 4,   // + resid[row, col]
+  E_GELU = 8,    // aux = v; v = gelu(v)
+  E_RELU = 16,   // aux = v; v = relu(v)
+  E_DGELU = 32,  // v *= gelu'(aux)
+  E_DRELU = 64,  // v = aux > 0 ? v : 0
+  E_ROPE = 128,  // rotate interleaved pairs of columns [0, rope_cols)
+  E_SPLIT = 256  // write the fp32 partial tile of this K split (no epilogue)
+};
+
 struct GemmArgs {
   int M, N, K;
   const float* A;
@@ -35,7 +51,6 @@ struct GemmArgs {
   const float* bias;
   const float* resid;
   long long ldr;
-  int act, dact;
   float* aux;
   long long ldaux;
   const float* rcos;
@@ -46,8 +61,9 @@ struct GemmArgs {
   int vecA, vecB;
 };
 
-// Loads the op(A) panel [BM x BK] of chunk k0 into registers.
-template <bool TA>
+// Loads the op(A) panel [BM x BK] of chunk k0 into registers. CHECK = false: the whole panel
+// is in bounds and 16-byte aligned.
+template <bool TA, bool CHECK>
 __device__ __forceinline__ void load_a(const GemmArgs& p, const float* __restrict__ A, int m0, int k0, int kend,
                                        float4 (&r)[4]) {
   const int t = threadIdx.x;
@@ -57,7 +73,7 @@ __device__ __forceinline__ void load_a(const GemmArgs& p, const float* __restric
     for (int i = 0; i < 4; ++i) {
       const int k = k0 + 4 * ((t >> 7) + 2 * i);
       const float* src = A + (long long)m * p.lda + k;
-      if (p.vecA && m < p.M && k + 3 < kend) {
+      if (!CHECK || (p.vecA && m < p.M && k + 3 < kend)) {
         r[i] = *reinterpret_cast<const float4*>(src);
       } else {
         float v[4];
@@ -72,7 +88,7 @@ __device__ __forceinline__ void load_a(const GemmArgs& p, const float* __restric
     for (int i = 0; i < 4; ++i) {
       const int k = k0 + (t >> 5) + 8 * i;
       const float* src = A + (long long)k * p.lda + m;
-      if (p.vecA && k < kend && m + 3 < p.M) {
+      if (!CHECK || (p.vecA && k < kend && m + 3 < p.M)) {
         r[i] = *reinterpret_cast<const float4*>(src);
       } else {
         float v[4];
@@ -107,7 +123,7 @@ __device__ __forceinline__ void store_a(float* As, const float4 (&r)[4]) {
 }
 
 // op(B) panel [BK x BN]: transB = 0 is the same access pattern as transA = 1 and vice versa.
-template <bool TB>
+template <bool TB, bool CHECK>
 __device__ __forceinline__ void load_b(const GemmArgs& p, const float* __restrict__ B, int n0, int k0, int kend,
                                        float4 (&r)[4]) {
   const int t = threadIdx.x;
@@ -117,7 +133,7 @@ __device__ __forceinline__ void load_b(const GemmArgs& p, const float* __restric
     for (int i = 0; i < 4; ++i) {
       const int k = k0 + 4 * ((t >> 7) + 2 * i);
       const float* src = B + (long long)n * p.ldb + k;
-      if (p.vecB && n < p.N && k + 3 < kend) {
+      if (!CHECK || (p.vecB && n < p.N && k + 3 < kend)) {
         r[i] = *reinterpret_cast<const float4*>(src);
       } else {
         float v[4];
@@ -132,7 +148,7 @@ __device__ __forceinline__ void load_b(const GemmArgs& p, const float* __restric
     for (int i = 0; i < 4; ++i) {
       const int k = k0 + (t >> 5) + 8 * i;
       const float* src = B + (long long)k * p.ldb + n;
-      if (p.vecB && k < kend && n + 3 < p.N) {
+      if (!CHECK || (p.vecB && k < kend && n + 3 < p.N)) {
         r[i] = *reinterpret_cast<const float4*>(src);
       } else {
         float v[4];
@@ -149,26 +165,37 @@ __device__ __forceinline__ void store_b(float* Bs, const float4 (&r)[4]) {
   store_a<!TB>(Bs, r);
 }
 
-// Epilogue of one element (everything but RoPE, which needs the neighbouring lane).
-__device__ __forceinline__ float epi_value(const GemmArgs& p, float acc, int row, int col, float* __restrict__ C,
-                                           const float* __restrict__ resid, float* __restrict__ aux) {
-  float v = p.alpha * acc;
-  if (p.beta != 0.f) v += p.beta * C[(long long)row * p.ldc + col];
-  if (p.bias) v += p.bias[col];
-  if (resid) v += resid[(long long)row * p.ldr + col];
-  if (p.dact == GEMM_DACT_GELU) {
-    v *= gelu_d(aux[(long long)row * p.ldaux + col]);
-  } else if (p.dact == GEMM_DACT_RELU) {
-    v = aux[(long long)row * p.ldaux + col] > 0.f ? v : 0.f;
+template <bool TA, bool TB>
+__device__ __forceinline__ void load_chunk(const GemmArgs& p, const float* A, const float* B, int m0, int n0, int k0,
+                                           int kend, bool interior, float4 (&ra)[4], float4 (&rb)[4]) {
+  if (interior && k0 + BK <= kend) {
+    load_a<TA, false>(p, A, m0, k0, kend, ra);
+    load_b<TB, false>(p, B, n0, k0, kend, rb);
+  } else {
+    load_a<TA, true>(p, A, m0, k0, kend, ra);
+    load_b<TB, true>(p, B, n0, k0, kend, rb);
   }
-  if (p.act != GEMM_ACT_NONE) {
-    if (aux) aux[(long long)row * p.ldaux + col] = v;
-    v = p.act == GEMM_ACT_GELU ? gelu_f(v) : fmaxf(v, 0.f);
+}
+
+// Epilogue of one element (everything but RoPE, which needs the neighbouring lane).
+template <int E>
+__device__ __forceinline__ float epi_value(const GemmArgs& p, float acc, int row, int col, const float* C,
+                                           const float* __restrict__ resid) {
+  float v = p.alpha * acc;
+  if constexpr ((E & E_BETA) != 0) v += p.beta * C[(long long)row * p.ldc + col];
+  if constexpr ((E & E_BIAS) != 0) v += p.bias[col];
+  if constexpr ((E & E_RESID) != 0) v += resid[(long long)row * p.ldr + col];
+  if constexpr ((E & E_DGELU) != 0) v *= gelu_d(p.aux[(long long)row * p.ldaux + col]);
+  if constexpr ((E & E_DRELU) != 0) v = p.aux[(long long)row * p.ldaux + col] > 0.f ? v : 0.f;
+  if constexpr ((E & (E_GELU | E_RELU)) != 0) {
+    if (p.aux) p.aux[(long long)row * p.ldaux + col] = v;
+    if constexpr ((E & E_GELU) != 0) v = gelu_f(v);
+    else v = fmaxf(v, 0.f);
   }
   return v;
 }
 
-template <bool TA, bool TB>
+template <bool TA, bool TB, int E>
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
   __shared__ float As[BK * LDS_S];
   __shared__ float Bs[BK * LDS_S];
@@ -182,6 +209,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
   const float* B = p.B + (long long)b * p.sB;
   const int kbeg = split * p.kper;
   const int kend = min(p.K, kbeg + p.kper);
+  const bool interior = p.vecA && p.vecB && m0 + BM <= p.M && n0 + BN <= p.N;
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
@@ -197,18 +225,14 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
 
   float4 ra[4], rb[4];
   if (kbeg < kend) {
-    load_a<TA>(p, A, m0, kbeg, kend, ra);
-    load_b<TB>(p, B, n0, kbeg, kend, rb);
+    load_chunk<TA, TB>(p, A, B, m0, n0, kbeg, kend, interior, ra, rb);
     store_a<TA>(As, ra);
     store_b<TB>(Bs, rb);
   }
   __syncthreads();
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
     const bool more = k0 + BK < kend;
-    if (more) {
-      load_a<TA>(p, A, m0, k0 + BK, kend, ra);
-      load_b<TB>(p, B, n0, k0 + BK, kend, rb);
-    }
+    if (more) load_chunk<TA, TB>(p, A, B, m0, n0, k0 + BK, kend, interior, ra, rb);
     const float* ap = As + h * LDS_S + wm * 64 + l32;
     const float* bp = Bs + h * LDS_S + wn * 64 + l32;
 #pragma unroll
@@ -230,7 +254,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
 
   // Accumulator layout of v_mfma_f32_32x32x2_f32: lane l, register r holds
   // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 block.
-  if (p.ksplit > 1) {
+  if constexpr ((E & E_SPLIT) != 0) {
     float* P = p.part + ((long long)b * p.ksplit + split) * (long long)p.M * p.N;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -240,49 +264,53 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
         for (int r = 0; r < 16; ++r) {
           const int row = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
           const int col = n0 + wn * 64 + nt * 32 + l32;
-          if (row < p.M && col < p.N) P[(long long)row * p.N + col] = acc[mt][nt][r];
+          if (interior || (row < p.M && col < p.N)) P[(long long)row * p.N + col] = acc[mt][nt][r];
         }
-    return;
-  }
-  float* C = p.C + (long long)b * p.sC;
-  const float* resid = p.resid ? p.resid + (long long)b * p.sC : nullptr;
+  } else {
+    float* C = p.C + (long long)b * p.sC;
+    const float* resid = ((E & E_RESID) != 0) ? p.resid + (long long)b * p.sC : nullptr;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+      for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        const int col = n0 + wn * 64 + nt * 32 + l32;
-        float v = acc[mt][nt][r];
-        if (p.rope_cols > 0) {
-          // interleaved pair (2i, 2i+1) of a head: the partner column is the neighbouring lane
-          const float partner = __shfl_xor(v, 1, 64);
-          if (col < p.rope_cols) {
-            const int half = p.rope_dim >> 1;
-            const int pi = (col % p.rope_dim) >> 1;
-            const int pos = row % p.rope_seq;
-            const float c = p.rcos[pos * half + pi], s = p.rsin[pos * half + pi];
-            v = (col & 1) ? fmaf(partner, s, v * c) : fmaf(v, c, -partner * s);
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const int col = n0 + wn * 64 + nt * 32 + l32;
+          float v = acc[mt][nt][r];
+          if constexpr ((E & E_ROPE) != 0) {
+            // interleaved pair (2i, 2i+1) of a head: the partner column is the neighbouring lane
+            const float partner = __shfl_xor(v, 1, 64);
+            if (col < p.rope_cols) {
+              const int half = p.rope_dim >> 1;
+              const int pi = (col % p.rope_dim) >> 1;
+              const int pos = row % p.rope_seq;
+              const float c = p.rcos[pos * half + pi], s = p.rsin[pos * half + pi];
+              v = (col & 1) ? fmaf(partner, s, v * c) : fmaf(v, c, -partner * s);
+            }
           }
+          if (interior || (row < p.M && col < p.N)) C[(long long)row * p.ldc + col] = epi_value<E>(p, v, row, col, C, resid);
         }
-        if (row < p.M && col < p.N) C[(long long)row * p.ldc + col] = epi_value(p, v, row, col, C, resid, p.aux);
-      }
+  }
 }
 
-// Sums the split-K partials in f64 and applies the epilogue.
+// Sums the split-K partials in f64 and applies the epilogue (beta and bias only).
+template <int E>
 __global__ void gemm_splitk_reduce(GemmArgs p) {
   const long long MN = (long long)p.M * p.N;
-  const long long total = MN * (p.ksplit > 0 ? 1 : 1);
   const int b = blockIdx.y;
   const float* P = p.part + (long long)b * p.ksplit * MN;
   float* C = p.C + (long long)b * p.sC;
-  const float* resid = p.resid ? p.resid + (long long)b * p.sC : nullptr;
-  for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (long long)gridDim.x * blockDim.x) {
-    double s = 0.0;
-    for (int k = 0; k < p.ksplit; ++k) s += (double)P[k * MN + e];
+  for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < MN; e += (long long)gridDim.x * blockDim.x) {
+    double s0 = 0.0, s1 = 0.0;
+    int k = 0;
+    for (; k + 1 < p.ksplit; k += 2) {
+      s0 += (double)P[k * MN + e];
+      s1 += (double)P[(k + 1) * MN + e];
+    }
+    if (k < p.ksplit) s0 += (double)P[k * MN + e];
     const int row = (int)(e / p.N), col = (int)(e % p.N);
-    C[(long long)row * p.ldc + col] = epi_value(p, (float)s, row, col, C, resid, p.aux);
+    C[(long long)row * p.ldc + col] = epi_value<E>(p, (float)(s0 + s1), row, col, C, nullptr);
   }
 }
 
@@ -305,8 +333,6 @@ static GemmArgs to_args(const GemmDesc& d) {
   a.bias = d.bias;
   a.resid = d.resid;
   a.ldr = d.ldr;
-  a.act = d.act;
-  a.dact = d.dact;
   a.aux = d.aux;
   a.ldaux = d.ldaux;
   a.rcos = d.rope_cos;
@@ -331,7 +357,21 @@ static GemmArgs to_args(const GemmDesc& d) {
   return a;
 }
 
+static int epi_flags(const GemmDesc& d) {
+  int e = 0;
+  if (d.beta != 0.f) e |= E_BETA;
+  if (d.bias) e |= E_BIAS;
+  if (d.resid) e |= E_RESID;
+  if (d.act == GEMM_ACT_GELU) e |= E_GELU;
+  if (d.act == GEMM_ACT_RELU) e |= E_RELU;
+  if (d.dact == GEMM_DACT_GELU) e |= E_DGELU;
+  if (d.dact == GEMM_DACT_RELU) e |= E_DRELU;
+  if (d.rope_cols > 0) e |= E_ROPE;
+  return e;
+}
+
 size_t gemm_plan_split(GemmDesc& d, int num_cu) {
+  const int e = epi_flags(d);
   if (d.ksplit == 0) {
     const long long tiles = (long long)((d.M + BM - 1) / BM) * ((d.N + BN - 1) / BN) * d.batch;
     int ks = 1;
@@ -340,11 +380,41 @@ size_t gemm_plan_split(GemmDesc& d, int num_cu) {
     while (tiles * ks * 2 <= (long long)num_cu && (long long)d.K / (ks * 2) >= 512) ks *= 2;
     d.ksplit = ks;
   }
-  if (d.rope_cols > 0 || d.act != GEMM_ACT_NONE) d.ksplit = 1;
+  if ((e & ~(E_BETA | E_BIAS)) != 0) d.ksplit = 1;  // only beta / bias survive a split
   if (d.ksplit <= 1) return 0;
   GemmArgs a = to_args(d);
   return (size_t)a.ksplit * d.M * d.N * d.batch * sizeof(float);
 }
+
+typedef void (*GemmKernel)(GemmArgs);
+
+// Instantiated (transA, transB, epilogue) combinations.
+#define GEMM_CASE(TA, TB, E)                                           \
+  if (tA == TA && tB == TB && e == (E)) return &gemm_f32_kernel<TA, TB, (E)>;
+static GemmKernel pick_kernel(bool tA, bool tB, int e) {
+  GEMM_CASE(false, false, 0)
+  GEMM_CASE(false, false, E_BETA)
+  GEMM_CASE(false, false, E_BIAS)
+  GEMM_CASE(false, false, E_ROPE)
+  GEMM_CASE(false, false, E_RESID)
+  GEMM_CASE(false, false, E_BIAS | E_RESID)
+  GEMM_CASE(false, false, E_BIAS | E_GELU)
+  GEMM_CASE(false, false, E_BIAS | E_RELU)
+  GEMM_CASE(false, false, E_SPLIT)
+  GEMM_CASE(false, true, 0)
+  GEMM_CASE(false, true, E_BETA)
+  GEMM_CASE(false, true, E_DGELU)
+  GEMM_CASE(false, true, E_DRELU)
+  GEMM_CASE(false, true, E_SPLIT)
+  GEMM_CASE(true, false, 0)
+  GEMM_CASE(true, false, E_BETA)
+  GEMM_CASE(true, false, E_SPLIT)
+  GEMM_CASE(true, true, 0)
+  GEMM_CASE(true, true, E_BETA)
+  GEMM_CASE(true, true, E_SPLIT)
+  return nullptr;
+}
+#undef GEMM_CASE
 
 int gemm_launch(const GemmDesc& d, hipStream_t stream) {
   GemmArgs a = to_args(d);
@@ -357,18 +427,38 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
     a.kper = 0;
     grid.y = d.batch;
   }
-  const int key = (d.transA ? 2 : 0) | (d.transB ? 1 : 0);
-  switch (key) {
-    case 0: hipLaunchKernelGGL((gemm_f32_kernel<false, false>), grid, dim3(NT), 0, stream, a); break;
-    case 1: hipLaunchKernelGGL((gemm_f32_kernel<false, true>), grid, dim3(NT), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((gemm_f32_kernel<true, false>), grid, dim3(NT), 0, stream, a); break;
-    default: hipLaunchKernelGGL((gemm_f32_kernel<true, true>), grid, dim3(NT), 0, stream, a); break;
+  const int e = epi_flags(d);
+  const bool split = a.ksplit > 1;
+  GemmKernel kern = pick_kernel(d.transA != 0, d.transB != 0, split ? E_SPLIT : e);
+  if (kern == nullptr) {
+    set_error("gemm: epilogue combination 0x%x is not instantiated for transA=%d transB=%d", e, d.transA, d.transB);
+    return TALOS_ERR_UNSUPPORTED;
   }
-  TALOS_LAUNCHED("gemm_f32_kernel");
-  if (a.ksplit > 1) {
+  static const char* names[4] = {"gemm_f32_kernel<false, false", "gemm_f32_kernel<false, true",
+                                 "gemm_f32_kernel<true, false", "gemm_f32_kernel<true, true"};
+  const int key = (d.transA ? 2 : 0) | (d.transB ? 1 : 0);
+  {
+    // algorithmic work: 2MNK flops; A, B read once, C written once (+ C / residual / aux reads)
+    const double MN = (double)d.M * d.N;
+    double bytes = 4.0 * ((double)d.M * d.K + (double)d.K * d.N + MN);
+    if (!split) {
+      if (d.beta != 0.f) bytes += 4.0 * MN;
+      if (d.resid) bytes += 4.0 * MN;
+      if (d.aux) bytes += 4.0 * MN;
+      if (d.bias) bytes += 4.0 * d.N;
+    }
+    ProfScope ps(stream, names[key], 2.0 * MN * d.K * d.batch, bytes * d.batch);
+    hipLaunchKernelGGL(kern, grid, dim3(NT), 0, stream, a);
+    TALOS_LAUNCHED("gemm_f32_kernel");
+  }
+  if (split) {
     const long long MN = (long long)d.M * d.N;
     dim3 rg((unsigned)std::min<long long>((MN + 255) / 256, 4096), d.batch);
-    hipLaunchKernelGGL(gemm_splitk_reduce, rg, dim3(256), 0, stream, a);
+    ProfScope ps(stream, "gemm_splitk_reduce", 0.0, 4.0 * (double)MN * d.batch * (a.ksplit + 1 + (d.beta != 0.f)));
+    if (e == 0) hipLaunchKernelGGL(gemm_splitk_reduce<0>, rg, dim3(256), 0, stream, a);
+    else if (e == E_BETA) hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA>, rg, dim3(256), 0, stream, a);
+    else if (e == E_BIAS) hipLaunchKernelGGL(gemm_splitk_reduce<E_BIAS>, rg, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA | E_BIAS>, rg, dim3(256), 0, stream, a);
     TALOS_LAUNCHED("gemm_splitk_reduce");
   }
   return TALOS_OK;

@@ -54,6 +54,7 @@ struct talos_plan_s {
         *g_last = nullptr;
   double* loss_ws = nullptr;
   int num_cu = 256;
+  talos::Profiler* prof = nullptr;
 };
 
 namespace talos {
@@ -161,7 +162,15 @@ static int plan_alloc(talos_plan_s* p, float** out, size_t n) {
 static void plan_free(talos_plan_s* p) {
   for (void* a : p->allocs) (void)hipFree(a);
   p->allocs.clear();
+  profiler_delete(p->prof);
+  p->prof = nullptr;
 }
+
+// Makes the plan's profiler current on this thread for the duration of an entry point.
+struct PlanCall {
+  explicit PlanCall(talos_plan_s* p) { profiler_set_current(p->prof); }
+  ~PlanCall() { profiler_set_current(nullptr); }
+};
 
 // Largest split-K workspace among the weight-gradient GEMMs of a configuration.
 static size_t wgrad_ws(talos_plan_s* p, int M_tok, int rows, int cols) {
@@ -533,9 +542,12 @@ static int ppo_forward(talos_plan_s* p, const float* P, const float* states, hip
     h = p->layers[l].out;
     base = bo.end;
   }
-  hipLaunchKernelGGL(gather_last_kernel, dim3(ceil_div((size_t)c.batch * d, 256)), dim3(256), 0, s, c.batch, c.seq, d,
-                     h, p->last);
-  TALOS_LAUNCHED("gather_last_kernel");
+  {
+    ProfScope ps_g(s, "gather_last_kernel", 0.0, 8.0 * c.batch * d);
+    hipLaunchKernelGGL(gather_last_kernel, dim3(ceil_div((size_t)c.batch * d, 256)), dim3(256), 0, s, c.batch, c.seq,
+                       d, h, p->last);
+    TALOS_LAUNCHED("gather_last_kernel");
+  }
   rc = rmsnorm_fwd_launch(c.batch, d, c.eps, p->last, P + po.gf, p->lastn, p->rstdf, s);
   if (rc) return rc;
   rc = mm(p, s, 0, 0, c.batch, d, d, p->lastn, d, P + po.wout, d, p->pout, d, 0.f, P + po.bout);
@@ -564,6 +576,7 @@ int talos_block_plan_create(const talos_block_cfg* cfg, talos_plan* plan) {
   TALOS_DEVICE();
   auto* p = new talos_plan_s();
   p->kind = 1;
+  p->prof = profiler_new();
   p->blk = *cfg;
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, 0) == hipSuccess) p->num_cu = prop.multiProcessorCount;
@@ -588,6 +601,7 @@ int talos_block_fwd_bwd_f32(talos_plan plan, const float* params, const float* x
   TALOS_NONNULL(dx);
   TALOS_DEVICE();
   hipStream_t s = as_stream(stream);
+  PlanCall pc(plan);
   const talos_block_cfg& c = plan->blk;
   const size_t M = (size_t)c.batch * c.seq, d = c.d_model;
   BlockOff bo = block_offsets(c, 0);
@@ -608,6 +622,7 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
   TALOS_DEVICE();
   auto* p = new talos_plan_s();
   p->kind = 2;
+  p->prof = profiler_new();
   p->ppo = *cfg;
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, 0) == hipSuccess) p->num_cu = prop.multiProcessorCount;
@@ -649,6 +664,7 @@ int talos_ppo_forward_f32(talos_plan plan, const float* params, const float* sta
   TALOS_NONNULL(states);
   TALOS_DEVICE();
   hipStream_t s = as_stream(stream);
+  PlanCall pc(plan);
   int rc = ppo_forward(plan, params, states, s);
   if (rc) return rc;
   const talos_ppo_cfg& c = plan->ppo;
@@ -672,15 +688,19 @@ int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* sta
   TALOS_DEVICE();
   hipStream_t s = as_stream(stream);
   talos_plan_s* p = plan;
+  PlanCall pc(p);
   const talos_ppo_cfg& c = p->ppo;
   const talos_block_cfg bc = block_cfg_of(c);
   const PpoOff po = ppo_offsets(c);
   const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions, B = c.batch;
   int rc = ppo_forward(p, params, states, s);
   if (rc) return rc;
+  {
+  ProfScope ps_l(s, "ppo_loss_kernel", 0.0, 4.0 * B * (2.0 * A + 5.0));
   hipLaunchKernelGGL(ppo_loss_kernel, dim3(1), dim3(256), 0, s, B, A, c.clip_eps, c.value_coef, c.entropy_coef,
                      p->logits, p->values, actions, adv, ret, old_logp, loss_out, p->g_logits, p->g_values, 1);
   TALOS_LAUNCHED("ppo_loss_kernel");
+  }
   float* G = dparams;
   // heads
   rc = mm(p, s, 1, 0, d, A, B, p->pout, d, p->g_logits, A, G + po.wa, A);
@@ -706,9 +726,12 @@ int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* sta
   rc = rmsnorm_bwd_launch(B, d, p->last, params + po.gf, p->rstdf, p->g_lastn, 0.f, p->g_last, 0.f, G + po.gf,
                           p->red_ws, s);
   if (rc) return rc;
+  {
+  ProfScope ps_s(s, "scatter_last_kernel", 0.0, 4.0 * ((double)M * d + (double)B * d));
   hipLaunchKernelGGL(scatter_last_kernel, dim3(ceil_div((size_t)M * d, 256) > 65536 ? 65536 : ceil_div((size_t)M * d, 256)),
                      dim3(256), 0, s, B, c.seq, d, p->g_last, p->g_out);
   TALOS_LAUNCHED("scatter_last_kernel");
+  }
   // blocks, last to first; the gradient ping-pongs between g_out and g_x
   float* gcur = p->g_out;
   float* gnext = p->g_x;
@@ -727,6 +750,13 @@ int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* sta
   rc = mm(p, s, 1, 0, c.in_dim, d, M, states, c.in_dim, gcur, d, G + po.we, d);
   if (rc) return rc;
   return colsum_launch(M, d, gcur, d, 0.f, G + po.be, p->red_ws, s);
+}
+
+int talos_plan_profiler(talos_plan plan, talos_profiler* prof) {
+  TALOS_REQUIRE(plan != nullptr && plan->prof != nullptr, TALOS_ERR_HANDLE, "%s: invalid plan", __func__);
+  TALOS_NONNULL(prof);
+  *prof = reinterpret_cast<talos_profiler>(plan->prof);
+  return TALOS_OK;
 }
 
 int talos_plan_destroy(talos_plan plan) {

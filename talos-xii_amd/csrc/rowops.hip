@@ -50,44 +50,81 @@ int fill_zero(void* dst, size_t bytes, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // Column sums (bias gradient): db[c] = beta*db[c] + sum_r dy[r, c]
 // ---------------------------------------------------------------------------
-constexpr int kColRows = 256;  // rows per partial
+// Row chunks: at most kMaxParts partials per column, each over >= 64 rows.
+constexpr int kMaxParts = 256;
 
-__global__ void colsum_partial_kernel(int rows, int cols, const float* __restrict__ dy, long long ld,
-                                      double* __restrict__ part) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  const int r0 = blockIdx.y * kColRows;
-  if (c >= cols) return;
-  const int r1 = min(rows, r0 + kColRows);
-  double s = 0.0;
-  for (int r = r0; r < r1; ++r) s += (double)dy[(long long)r * ld + c];
-  part[(long long)blockIdx.y * cols + c] = s;
+static int colsum_parts(int rows) {
+  int p = (rows + 63) / 64;
+  return p < 1 ? 1 : (p > kMaxParts ? kMaxParts : p);
 }
 
-__global__ void colsum_final_kernel(int cols, int nparts, const double* __restrict__ part, float beta,
-                                    float* __restrict__ out) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
-  double s = 0.0;
-  for (int p = 0; p < nparts; ++p) s += part[(long long)p * cols + c];
-  out[c] = (float)(s + (beta != 0.f ? (double)out[c] : 0.0));
+// Workgroup (x = 64-column group, y = row chunk): lane = column, the 4 waves stride over the
+// chunk's rows (each row read is one 256-byte segment), f64 accumulation, LDS combine.
+__global__ __launch_bounds__(256) void colsum_partial_kernel(int rows, int cols, const float* __restrict__ dy,
+                                                             long long ld, int nparts, double* __restrict__ part) {
+  __shared__ double red[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  const int per = (rows + nparts - 1) / nparts;
+  const int r0 = blockIdx.y * per, r1 = min(rows, r0 + per);
+  double s0 = 0.0, s1 = 0.0;
+  if (c < cols) {
+    int r = r0 + w;
+    for (; r + 4 < r1; r += 8) {
+      s0 += (double)dy[(long long)r * ld + c];
+      s1 += (double)dy[(long long)(r + 4) * ld + c];
+    }
+    if (r < r1) s0 += (double)dy[(long long)r * ld + c];
+  }
+  red[w][lane] = s0 + s1;
+  __syncthreads();
+  if (w == 0 && c < cols) part[(long long)blockIdx.y * cols + c] = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
 }
 
-size_t colsum_workspace_bytes(int rows, int cols) {
-  return (size_t)((rows + kColRows - 1) / kColRows) * cols * sizeof(double);
+// out[c] = beta*out[c] + sum_p part[p][c]: 16 waves per 64 columns, LDS combine in f64.
+__global__ __launch_bounds__(1024) void reduce_parts_kernel(int cols, int nparts, const double* __restrict__ part,
+                                                            float beta, float* __restrict__ out) {
+  __shared__ double red[16][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  double s0 = 0.0, s1 = 0.0;
+  if (c < cols) {
+    int p = w;
+    for (; p + 16 < nparts; p += 32) {
+      s0 += part[(long long)p * cols + c];
+      s1 += part[(long long)(p + 16) * cols + c];
+    }
+    if (p < nparts) s0 += part[(long long)p * cols + c];
+  }
+  red[w][lane] = s0 + s1;
+  __syncthreads();
+  if (w == 0 && c < cols) {
+    double s = 0.0;
+    for (int i = 0; i < 16; ++i) s += red[i][lane];
+    out[c] = (float)(s + (beta != 0.f ? (double)out[c] : 0.0));
+  }
 }
+
+int reduce_parts_launch(int cols, int nparts, const double* part, float beta, float* out, hipStream_t s) {
+  ProfScope ps(s, "reduce_parts_kernel", (double)nparts * cols, 8.0 * nparts * cols + 4.0 * cols);
+  hipLaunchKernelGGL(reduce_parts_kernel, dim3(ceil_div(cols, 64)), dim3(1024), 0, s, cols, nparts, part, beta, out);
+  TALOS_LAUNCHED("reduce_parts_kernel");
+  return TALOS_OK;
+}
+
+size_t colsum_workspace_bytes(int rows, int cols) { return (size_t)colsum_parts(rows) * cols * sizeof(double); }
 
 int colsum_launch(int rows, int cols, const float* dy, long long ld, float beta, float* out, double* ws,
                   hipStream_t s) {
   if (cols == 0) return TALOS_OK;
-  const int nparts = (rows + kColRows - 1) / kColRows;
+  const int nparts = rows > 0 ? colsum_parts(rows) : 0;
   if (nparts > 0) {
-    dim3 g(ceil_div(cols, 256), nparts);
-    hipLaunchKernelGGL(colsum_partial_kernel, g, dim3(256), 0, s, rows, cols, dy, ld, ws);
+    dim3 g(ceil_div(cols, 64), nparts);
+    ProfScope ps(s, "colsum_partial_kernel", (double)rows * cols, 4.0 * rows * cols + 8.0 * nparts * cols);
+    hipLaunchKernelGGL(colsum_partial_kernel, g, dim3(256), 0, s, rows, cols, dy, ld, nparts, ws);
     TALOS_LAUNCHED("colsum_partial_kernel");
   }
-  hipLaunchKernelGGL(colsum_final_kernel, dim3(ceil_div(cols, 256)), dim3(256), 0, s, cols, nparts, ws, beta, out);
-  TALOS_LAUNCHED("colsum_final_kernel");
-  return TALOS_OK;
+  return reduce_parts_launch(cols, nparts, ws, beta, out, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -141,9 +178,13 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_generic(int rows, int dim, fl
   for (int c = lane; c < dim; c += 64) y[(long long)row * dim + c] = xr[c] * r * w[c];
 }
 
-// Backward: each wave processes kRowsPerWave rows; dgain partials per workgroup in f64.
-constexpr int kRmsRowsPerWave = 4;
-constexpr int kRmsRowsPerBlock = 4 * kRmsRowsPerWave;
+// Backward: a bounded grid (at most kMaxParts workgroups) strides over the rows, one row per wave
+// at a time; each lane keeps its columns' dgain sums in registers, so a workgroup writes a single
+// f64 partial row that reduce_parts_kernel combines.
+static int rms_bwd_blocks(int rows) {
+  int b = (rows + 3) / 4;
+  return b < 1 ? 1 : (b > kMaxParts ? kMaxParts : b);
+}
 
 template <int V>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(int rows, int dim, const float* __restrict__ x,
@@ -161,9 +202,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(int rows, int dim, con
     dwacc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   const float inv_dim = 1.0f / (float)dim;
-  for (int i = 0; i < kRmsRowsPerWave; ++i) {
-    const int row = blockIdx.x * kRmsRowsPerBlock + wv * kRmsRowsPerWave + i;
-    if (row >= rows) break;
+  for (int row = blockIdx.x * 4 + wv; row < rows; row += gridDim.x * 4) {
     const float r = rstd[row];
     const float* xr = x + (long long)row * dim;
     const float* gr = dy + (long long)row * dim;
@@ -221,9 +260,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_generic(int rows, int dim, co
                                                            const float* __restrict__ dy, float beta_dx,
                                                            float* __restrict__ dx, double* __restrict__ dw_part) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  for (int i = 0; i < kRmsRowsPerWave; ++i) {
-    const int row = blockIdx.x * kRmsRowsPerBlock + wv * kRmsRowsPerWave + i;
-    if (row >= rows) break;
+  for (int row = blockIdx.x * 4 + wv; row < rows; row += gridDim.x * 4) {
     const float r = rstd[row];
     const float* xr = x + (long long)row * dim;
     const float* gr = dy + (long long)row * dim;
@@ -237,29 +274,18 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_generic(int rows, int dim, co
     }
   }
   if (dw_part == nullptr) return;
-  // per-feature partial over this workgroup's rows
+  // per-feature partial over the rows this workgroup visited
   for (int c = threadIdx.x; c < dim; c += 256) {
     double s = 0.0;
-    for (int i = 0; i < kRmsRowsPerBlock; ++i) {
-      const int row = blockIdx.x * kRmsRowsPerBlock + i;
-      if (row >= rows) break;
-      s += (double)dy[(long long)row * dim + c] * (double)(x[(long long)row * dim + c] * rstd[row]);
-    }
+    for (int r0 = blockIdx.x * 4; r0 < rows; r0 += gridDim.x * 4)
+      for (int row = r0; row < r0 + 4 && row < rows; ++row)
+        s += (double)dy[(long long)row * dim + c] * (double)(x[(long long)row * dim + c] * rstd[row]);
     dw_part[(long long)blockIdx.x * dim + c] = s;
   }
 }
 
-__global__ void sum_partials_kernel(int cols, int nparts, const double* __restrict__ part, float beta,
-                                    float* __restrict__ out) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
-  double s = 0.0;
-  for (int p = 0; p < nparts; ++p) s += part[(long long)p * cols + c];
-  out[c] = (float)(s + (beta != 0.f ? (double)out[c] : 0.0));
-}
-
 size_t rmsnorm_bwd_workspace_bytes(int rows, int dim) {
-  return (size_t)((rows + kRmsRowsPerBlock - 1) / kRmsRowsPerBlock) * dim * sizeof(double);
+  return (size_t)rms_bwd_blocks(rows) * dim * sizeof(double);
 }
 
 int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
@@ -268,6 +294,10 @@ int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float
   dim3 g(ceil_div(rows, 4)), b(256);
   const bool vec = dim % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
                                      reinterpret_cast<uintptr_t>(w)) & 15) == 0;
+  // x read, y written, gain read, rstd written
+  ProfScope ps(s, vec && dim <= 256 ? "rmsnorm_fwd_kernel<1>" : vec && dim <= 512 ? "rmsnorm_fwd_kernel<2>"
+                  : vec && dim <= 1024 ? "rmsnorm_fwd_kernel<4>" : "rmsnorm_fwd_generic",
+               4.0 * rows * dim, 4.0 * (2.0 * rows * dim + dim + (rstd ? rows : 0)));
   if (vec && dim <= 256) hipLaunchKernelGGL(rmsnorm_fwd_kernel<1>, g, b, 0, s, rows, dim, eps, x, w, y, rstd);
   else if (vec && dim <= 512) hipLaunchKernelGGL(rmsnorm_fwd_kernel<2>, g, b, 0, s, rows, dim, eps, x, w, y, rstd);
   else if (vec && dim <= 1024) hipLaunchKernelGGL(rmsnorm_fwd_kernel<4>, g, b, 0, s, rows, dim, eps, x, w, y, rstd);
@@ -278,12 +308,17 @@ int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float
 
 int rmsnorm_bwd_launch(int rows, int dim, const float* x, const float* w, const float* rstd, const float* dy,
                        float beta_dx, float* dx, float beta_dw, float* dw, double* ws, hipStream_t s) {
-  const int nblk = (rows + kRmsRowsPerBlock - 1) / kRmsRowsPerBlock;
+  const int nblk = rows > 0 ? rms_bwd_blocks(rows) : 0;
   if (nblk > 0) {
     dim3 g(nblk), b(256);
     double* part = dw ? ws : nullptr;
     const bool vec = dim % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy) |
                                        reinterpret_cast<uintptr_t>(dx) | reinterpret_cast<uintptr_t>(w)) & 15) == 0;
+    // x, dy read, dx written (read too when accumulating), gain + rstd read, dgain partials written
+    ProfScope ps(s, vec && dim <= 256 ? "rmsnorm_bwd_kernel<1>" : vec && dim <= 512 ? "rmsnorm_bwd_kernel<2>"
+                    : "rmsnorm_bwd_generic",
+                 8.0 * rows * dim, 4.0 * ((3.0 + (beta_dx != 0.f)) * rows * dim + dim + rows) +
+                                       (part ? 8.0 * nblk * dim : 0.0));
     if (vec && dim <= 256)
       hipLaunchKernelGGL(rmsnorm_bwd_kernel<1>, g, b, 0, s, rows, dim, x, w, rstd, dy, beta_dx, dx, part);
     else if (vec && dim <= 512)
@@ -292,10 +327,7 @@ int rmsnorm_bwd_launch(int rows, int dim, const float* x, const float* w, const 
       hipLaunchKernelGGL(rmsnorm_bwd_generic, g, b, 0, s, rows, dim, x, w, rstd, dy, beta_dx, dx, part);
     TALOS_LAUNCHED("rmsnorm_bwd");
   }
-  if (dw) {
-    hipLaunchKernelGGL(sum_partials_kernel, dim3(ceil_div(dim, 256)), dim3(256), 0, s, dim, nblk, ws, beta_dw, dw);
-    TALOS_LAUNCHED("rmsnorm_dw_sum");
-  }
+  if (dw) return reduce_parts_launch(dim, nblk, ws, beta_dw, dw, s);
   return TALOS_OK;
 }
 

@@ -65,11 +65,99 @@ int ensure_device() {
   return g_init_status;
 }
 
+// ---------------------------------------------------------------------------
+// Per-launch profiler
+// ---------------------------------------------------------------------------
+struct ProfRec {
+  std::string kernel;
+  double flops, bytes;
+  hipEvent_t a, b;
+};
+struct Profiler {
+  bool enabled = false;
+  std::string filter;
+  std::vector<ProfRec> recs;
+  std::vector<hipEvent_t> pool;
+  size_t used = 0;
+};
+
+static thread_local Profiler* g_prof = nullptr;
+
+Profiler* profiler_new() { return new Profiler(); }
+
+void profiler_delete(Profiler* p) {
+  if (!p) return;
+  for (hipEvent_t e : p->pool) (void)hipEventDestroy(e);
+  delete p;
+}
+
+void profiler_set_current(Profiler* p) { g_prof = p; }
+
+static hipEvent_t next_event(Profiler* p) {
+  if (p->used == p->pool.size()) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    p->pool.push_back(e);
+  }
+  return p->pool[p->used++];
+}
+
+int prof_begin(hipStream_t s, const char* kernel, double flops, double bytes) {
+  Profiler* p = g_prof;
+  if (!p || !p->enabled) return -1;
+  if (!p->filter.empty() && std::string(kernel).find(p->filter) == std::string::npos) return -1;
+  hipEvent_t a = next_event(p), b = next_event(p);
+  if (!a || !b) return -1;
+  (void)hipEventRecord(a, s);
+  p->recs.push_back(ProfRec{kernel, flops, bytes, a, b});
+  return (int)p->recs.size() - 1;
+}
+
+void prof_end(hipStream_t s, int idx) {
+  Profiler* p = g_prof;
+  if (idx < 0 || !p || idx >= (int)p->recs.size()) return;
+  (void)hipEventRecord(p->recs[idx].b, s);
+}
+
 }  // namespace talos
 
 using namespace talos;
 
 extern "C" {
+
+int talos_profiler_enable(talos_profiler prof, int enable, const char* kernel_filter) {
+  TALOS_NONNULL(prof);
+  Profiler* p = reinterpret_cast<Profiler*>(prof);
+  if (enable) {
+    TALOS_DEVICE();
+    TALOS_HIP(hipDeviceSynchronize());
+    p->recs.clear();
+    p->used = 0;
+    p->filter = kernel_filter ? kernel_filter : "";
+  }
+  p->enabled = enable != 0;
+  return TALOS_OK;
+}
+
+int talos_profiler_read(talos_profiler prof, talos_prof_record* out, int max_records, int* count) {
+  TALOS_NONNULL(prof);
+  TALOS_NONNULL(count);
+  TALOS_DEVICE();
+  Profiler* p = reinterpret_cast<Profiler*>(prof);
+  *count = (int)p->recs.size();
+  for (int i = 0; i < (int)p->recs.size() && i < max_records; ++i) {
+    TALOS_NONNULL(out);
+    const ProfRec& r = p->recs[i];
+    TALOS_HIP(hipEventSynchronize(r.b));
+    float ms = 0.f;
+    TALOS_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+    snprintf(out[i].kernel, sizeof(out[i].kernel), "%s", r.kernel.c_str());
+    out[i].flops = r.flops;
+    out[i].bytes = r.bytes;
+    out[i].ms = ms;
+  }
+  return TALOS_OK;
+}
 
 const char* talos_last_error(void) { return last_error(); }
 

@@ -97,7 +97,15 @@ _SIGS = {
     "talos_ppo_fwd_bwd_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "talos_ppo_forward_f32": [_vp, _vp, _vp, _vp, _vp, _vp],
     "talos_plan_destroy": [_vp],
+    "talos_plan_profiler": [_vp, ctypes.POINTER(_vp)],
+    "talos_profiler_enable": [_vp, _i, ctypes.c_char_p],
+    "talos_profiler_read": [_vp, _vp, _i, ctypes.POINTER(_i)],
 }
+
+
+class ProfRecord(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_char * 64), ("flops", ctypes.c_double), ("bytes", ctypes.c_double),
+                ("ms", ctypes.c_float)]
 _RESTYPE = {"talos_last_error": ctypes.c_char_p, "talos_version": ctypes.c_char_p,
             "talos_block_param_count": _sz, "talos_ppo_param_count": _sz}
 
@@ -216,6 +224,22 @@ class Plan:
             call("talos_ppo_plan_create", ctypes.byref(cfg), ctypes.byref(h))
             self.n_params = lib().talos_ppo_param_count(ctypes.byref(cfg))
         self.h = h.value
+
+    def profile(self, enable=True, kernel_filter=None):
+        """Switches per-launch event profiling of this plan on (clearing old records) or off."""
+        prof = _vp()
+        call("talos_plan_profiler", self.h, ctypes.byref(prof))
+        call("talos_profiler_enable", prof, int(enable), kernel_filter.encode() if kernel_filter else None)
+
+    def profile_records(self):
+        """[(kernel, flops, bytes, ms)] of the profiled launches so far."""
+        prof = _vp()
+        call("talos_plan_profiler", self.h, ctypes.byref(prof))
+        n = _i()
+        call("talos_profiler_read", prof, None, 0, ctypes.byref(n))
+        recs = (ProfRecord * max(1, n.value))()
+        call("talos_profiler_read", prof, ctypes.cast(recs, _vp), n.value, ctypes.byref(n))
+        return [(r.kernel.decode(), r.flops, r.bytes, r.ms) for r in recs[:n.value]]
 
     def destroy(self):
         if self.h:
