@@ -1,21 +1,31 @@
-// attention.hip -- fused scaled-dot-product attention forward and backward for gfx950.
+// attention.hip -- fused scaled-dot-product attention forward and backward on CDNA4 matrix cores.
 //
 // Replaces the reference chain transpose -> batched_matmul_qt_k -> scale_tensor -> softmax ->
 // batched_matmul_probs_v -> transpose (src/transformer.rs:519-557, 877-1121) and its backward
 // closures (src/transformer.rs:920-955, 1010-1047, 1098-1117). q/k/v/o stay in the token-major
 // projection layout [batch, seq, heads, dim] (row stride ld), so no transpose or reshape copy is
-// ever made; the S x S score matrix never leaves registers.
+// ever made, and no S x S matrix is ever stored.
 //
-// The sequences of the policy configurations are short (32..256 tokens, head dims 32..96), so
-// one lane owns one query (forward, dQ) or one key (dK, dV) and keeps its rows in registers;
-// key/value (or query/dO) tiles of all the (batch, head) pairs of a workgroup are staged in LDS
-// and read as wave-wide broadcasts. The forward keeps an online (running max) softmax and saves
-// lse = max + log(sum) per query; the backward recomputes P = exp(s - lse) and uses
-// D_i = dO_i . O_i, so neither pass stores an S x S matrix. Causal masking (key j <= query i)
-// is applied by loop bounds, so masked probabilities are exactly 0 and cost nothing.
+// Work unit: one wave64 per 32-row block of one (batch, head) pair -- a query block for the
+// forward and dQ, a key block for dK / dV. Every product is a chain of v_mfma_f32_32x32x2_f32
+// over the head dimension or over a 32-key / 32-query block:
+//   forward   S^T[key, q] = K . Q^T        O[q, e]  += P . V
+//   dQ pass   S^T, dP^T[key, q] = V . dO^T, dS^T = P^T (dP^T - D)     dQ[q, e] += dS . K
+//   dK/dV     S[q, key] = Q . K^T, dP = dO . V^T, dS = P (dP - D)     dV += P^T . dO, dK += dS^T . Q
+// The 32x32 accumulator layout of the score MFMA (lane <-> column, register r <-> row
+// 8*(r/4) + 4*(lane/32) + r%4) is exactly the A-operand layout of the next MFMA when the
+// contraction over the block's 32 rows visits them in that order, so probabilities feed the
+// second product straight from registers. Operand rows are read from global memory by the lane
+// that owns them (each lane holds half of a row: elements [D/2 * (lane/32), D/2 * (lane/32 + 1))).
+// The forward makes two passes over the key blocks when there are several (row max / sum, then
+// normalised P . V) and saves lse = max + log(sum); the backward recomputes P = exp(s - lse)
+// and uses D_q = dO_q . O_q. Causal masking (key <= query) and the sequence end are applied to
+// the scores, so masked probabilities are exactly 0; key blocks past the diagonal are skipped.
 #include "attention.hpp"
 
 namespace talos {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 struct AttnArgs {
   int B, S, H, dk, dv;
@@ -42,285 +52,315 @@ struct AttnArgs {
   const float* rcos;
   const float* rsin;
   int rope_off, rope_dim;
-  int P, QB, KT;
+  int vec;  // every row half is 16-byte aligned and the head dims equal the template dims
 };
 
-// Applies R^T (rotation by -theta at position pos) to dims [off, off + rdim) of a register row.
-template <int DKM>
-__device__ __forceinline__ void rope_transpose_row(float (&g)[DKM], const AttnArgs& a, int pos) {
-  if (a.rcos == nullptr) return;
+constexpr float kNegInf = -INFINITY;
+
+// Loads half of row `row` (elements [HALF*h, HALF*h + HALF) of the head's `dim` values starting
+// at column col0) times `scale`; rows >= S and elements >= dim read as 0.
+template <int HALF>
+__device__ __forceinline__ void load_half(float (&r)[HALF], const float* __restrict__ base, long long ld,
+                                          long long tok0, int row, int S, int col0, int dim, int h, float scale,
+                                          bool vec) {
+  if (row >= S) {
+#pragma unroll
+    for (int i = 0; i < HALF; ++i) r[i] = 0.f;
+    return;
+  }
+  const float* src = base + (tok0 + row) * ld + col0 + HALF * h;
+  if (vec) {
+#pragma unroll
+    for (int i = 0; i < HALF; i += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(src + i);
+      r[i] = v.x * scale;
+      r[i + 1] = v.y * scale;
+      r[i + 2] = v.z * scale;
+      r[i + 3] = v.w * scale;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < HALF; ++i) r[i] = (HALF * h + i < dim) ? src[i] * scale : 0.f;
+  }
+}
+
+// Row index within a 32-row block held by accumulator register r of this lane.
+__device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+// acc += X_block . Y_block^T over the head dimension: lane rows x (A operand, rows of the result)
+// and y (B operand, columns of the result), both given as this lane's row halves.
+template <int HALF>
+__device__ __forceinline__ floatx16 mfma_rows(const float (&x)[HALF], const float (&y)[HALF], floatx16 acc) {
+#pragma unroll
+  for (int s = 0; s < HALF; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x[s], y[s], acc, 0, 0, 0);
+  return acc;
+}
+
+// acc[eb] += P_block . M[rows of the block, eb*32 + lane%32] for each 32-column block eb of the
+// head: P is given in accumulator layout (register s <-> block row acc_row(s, h)), M is read
+// from global memory row by row (rows >= S and columns >= dim read as 0).
+template <int NB>
+__device__ __forceinline__ void mfma_p_rows(const float (&P)[16], const float* __restrict__ base, long long ld,
+                                            long long tok0, int row0, int S, int col0, int dim, int l32, int h,
+                                            floatx16 (&acc)[NB]) {
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const int row = row0 + acc_row(s, h);
+    const float* src = base + (tok0 + row) * ld + col0 + l32;
+#pragma unroll
+    for (int eb = 0; eb < NB; ++eb) {
+      const float m = (row < S && eb * 32 + l32 < dim) ? src[eb * 32] : 0.f;
+      acc[eb] = __builtin_amdgcn_mfma_f32_32x32x2f32(P[s], m, acc[eb], 0, 0, 0);
+    }
+  }
+}
+
+// Applies R^T (rotation by -theta at position pos) to an output element of column e whose
+// pair partner (column e ^ 1) sits in the neighbouring lane. All lanes must call it.
+__device__ __forceinline__ float rope_t(float g, int e, int pos, const AttnArgs& a, bool active) {
+  const float partner = __shfl_xor(g, 1, 64);
+  if (a.rcos == nullptr || !active || e < a.rope_off || e >= a.rope_off + a.rope_dim) return g;
   const int half = a.rope_dim >> 1;
-#pragma unroll
-  for (int e = 0; e < DKM; e += 2) {
-    if (e >= a.rope_off && e < a.rope_off + a.rope_dim) {
-      const int pi = (e - a.rope_off) >> 1;
-      const float c = a.rcos[pos * half + pi], s = a.rsin[pos * half + pi];
-      const float g0 = g[e], g1 = g[e + 1];
-      g[e] = g0 * c + g1 * s;
-      g[e + 1] = -g0 * s + g1 * c;
-    }
-  }
+  const int pi = (e - a.rope_off) >> 1;
+  const float c = a.rcos[pos * half + pi], s = a.rsin[pos * half + pi];
+  // (g0, g1) -> (g0 c + g1 s, -g0 s + g1 c)
+  return (e & 1) ? fmaf(-partner, s, g * c) : fmaf(g, c, partner * s);
 }
 
-// Dot product of a register row with an LDS row, as four independent FMA chains.
-template <int D>
-__device__ __forceinline__ float dot_row(const float (&r)[D], const float* __restrict__ t) {
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-#pragma unroll
-  for (int e = 0; e < D; e += 4) {
-    s0 = fmaf(r[e], t[e], s0);
-    s1 = fmaf(r[e + 1], t[e + 1], s1);
-    s2 = fmaf(r[e + 2], t[e + 2], s2);
-    s3 = fmaf(r[e + 3], t[e + 3], s3);
-  }
-  return (s0 + s1) + (s2 + s3);
-}
-
-// Cooperative copy of rows [r0, r0 + nr) of each of the workgroup's P pairs into an LDS tile
-// [P][nr][DM] (dims >= dim are zero-filled).
-template <int DM>
-__device__ __forceinline__ void stage_rows(float* tile, const float* __restrict__ src, long long ld, int dim,
-                                           const AttnArgs& a, int pair0, int r0, int nr) {
-  const int n = a.P * nr * DM;
-  for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
-    const int e = idx % DM;
-    const int r = (idx / DM) % nr;
-    const int pp = idx / (DM * nr);
-    const int pair = pair0 + pp;
-    const int row = r0 + r;
-    float val = 0.f;
-    if (e < dim && row < a.S && pair < a.B * a.H) {
-      const int b = pair / a.H, h = pair % a.H;
-      val = src[((long long)b * a.S + row) * ld + (long long)h * dim + e];
-    }
-    tile[idx] = val;
-  }
-}
-
+// ---------------------------------------------------------------------------
+// Forward: wave per (pair, query block)
+// ---------------------------------------------------------------------------
 template <int DKM, int DVM>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
-  extern __shared__ float smem[];
-  float* Ks = smem;
-  float* Vs = smem + a.P * a.KT * DKM;
-  const int t = threadIdx.x;
-  const int pl = t / a.QB;
-  const int qi = blockIdx.y * a.QB + t % a.QB;
-  const int pair0 = blockIdx.x * a.P;
-  const int pair = pair0 + pl;
-  const bool active = pl < a.P && pair < a.B * a.H && qi < a.S;
-  const int b = pair / a.H, h = pair % a.H;
+  constexpr int KH = DKM / 2, OB = DVM / 32;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int nqb = (a.S + 31) >> 5;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= a.B * a.H * nqb) return;  // uniform per wave
+  const int pair = item / nqb, qb = item % nqb;
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int q = qb * 32 + l32;  // this lane's query (score columns)
 
-  float q[DKM], o[DVM];
+  float qv[KH];
+  load_half<KH>(qv, a.q, a.ldq, tok0, q, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
+  const int kb_last = a.causal ? qb : (a.S - 1) >> 5;
+
+  // scores of key block kb in S^T layout, masked
+  auto scores = [&](int kb, float (&sv)[16]) {
+    float kv[KH];
+    load_half<KH>(kv, a.k, a.ldk, tok0, kb * 32 + l32, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
+    floatx16 acc;
 #pragma unroll
-  for (int e = 0; e < DKM; ++e) q[e] = 0.f;
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    acc = mfma_rows<KH>(kv, qv, acc);
 #pragma unroll
-  for (int e = 0; e < DVM; ++e) o[e] = 0.f;
-  if (active) {
-    const float* qr = a.q + ((long long)b * a.S + qi) * a.ldq + (long long)h * a.dk;
-#pragma unroll
-    for (int e = 0; e < DKM; ++e) q[e] = e < a.dk ? qr[e] * a.scale : 0.f;
-  }
-  float m = -INFINITY, l = 0.f;
-  const int qmax = min(a.S, (int)(blockIdx.y + 1) * a.QB);  // exclusive bound of this block's queries
-  const int kend = a.causal ? qmax : a.S;
-  for (int k0 = 0; k0 < kend; k0 += a.KT) {
-    const int nk = min(a.KT, kend - k0);
-    __syncthreads();
-    stage_rows<DKM>(Ks, a.k, a.ldk, a.dk, a, pair0, k0, a.KT);
-    stage_rows<DVM>(Vs, a.v, a.ldv, a.dv, a, pair0, k0, a.KT);
-    __syncthreads();
-    if (!active) continue;
-    const int jn = a.causal ? min(nk, qi - k0 + 1) : nk;
-    const float* kt = Ks + pl * a.KT * DKM;
-    const float* vt = Vs + pl * a.KT * DVM;
-    for (int j = 0; j < jn; ++j) {
-      const float s = dot_row<DKM>(q, kt + j * DKM);
-      if (s > m) {
-        const float corr = expf(m - s);
-        l *= corr;
-#pragma unroll
-        for (int e = 0; e < DVM; ++e) o[e] *= corr;
-        m = s;
-      }
-      const float p = expf(s - m);
-      l += p;
-#pragma unroll
-      for (int e = 0; e < DVM; ++e) o[e] = fmaf(p, vt[j * DVM + e], o[e]);
+    for (int r = 0; r < 16; ++r) {
+      const int key = kb * 32 + acc_row(r, h);
+      const bool ok = key < a.S && (!a.causal || key <= q);
+      sv[r] = ok ? acc[r] : kNegInf;
     }
-  }
-  if (!active) return;
-  const float inv = 1.0f / l;
-  float* orow = a.o + ((long long)b * a.S + qi) * a.ldo + (long long)h * a.dv;
+  };
+
+  float m = kNegInf, l = 0.f;
+  float sv[16];
+  for (int kb = 0; kb <= kb_last; ++kb) {
+    scores(kb, sv);
+    float bm = kNegInf;
 #pragma unroll
-  for (int e = 0; e < DVM; ++e)
-    if (e < a.dv) orow[e] = o[e] * inv;
-  a.lse[(long long)pair * a.S + qi] = m + logf(l);
+    for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sv[r]);
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mn = fmaxf(m, bm);
+    float bs = 0.f;
+    if (mn != kNegInf) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) bs += expf(sv[r] - mn);
+    }
+    bs += __shfl_xor(bs, 32, 64);
+    l = (m == kNegInf ? 0.f : l * expf(m - mn)) + bs;
+    m = mn;
+  }
+  const float inv_l = l > 0.f ? 1.f / l : 0.f;
+
+  floatx16 oacc[OB];
+#pragma unroll
+  for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[ob][r] = 0.f;
+  for (int kb = 0; kb <= kb_last; ++kb) {
+    if (kb_last > 0) scores(kb, sv);  // one key block: the scores of pass 1 are still in sv
+    float P[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) P[r] = (m == kNegInf) ? 0.f : expf(sv[r] - m) * inv_l;
+    mfma_p_rows<OB>(P, a.v, a.ldv, tok0, kb * 32, a.S, hd * a.dv, a.dv, l32, h, oacc);
+  }
+  // O in accumulator layout: register r <-> query qb*32 + acc_row(r, h), lane <-> column
+#pragma unroll
+  for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qr = qb * 32 + acc_row(r, h);
+      const int e = ob * 32 + l32;
+      if (qr < a.S && e < a.dv) a.o[(tok0 + qr) * a.ldo + hd * a.dv + e] = oacc[ob][r];
+    }
+  if (h == 0 && q < a.S) a.lse[(long long)pair * a.S + q] = (l > 0.f) ? m + logf(l) : kNegInf;
 }
 
-// dQ (and D = dO . O) with one lane per query.
+// ---------------------------------------------------------------------------
+// dQ (and D = dO . O): wave per (pair, query block), S^T layout
+// ---------------------------------------------------------------------------
 template <int DKM, int DVM>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
-  extern __shared__ float smem[];
-  float* Ks = smem;
-  float* Vs = smem + a.P * a.KT * DKM;
-  const int t = threadIdx.x;
-  const int pl = t / a.QB;
-  const int qi = blockIdx.y * a.QB + t % a.QB;
-  const int pair0 = blockIdx.x * a.P;
-  const int pair = pair0 + pl;
-  const bool active = pl < a.P && pair < a.B * a.H && qi < a.S;
-  const int b = pair / a.H, h = pair % a.H;
+  constexpr int KH = DKM / 2, VH = DVM / 2, QB = DKM / 32;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int nqb = (a.S + 31) >> 5;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= a.B * a.H * nqb) return;
+  const int pair = item / nqb, qb = item % nqb;
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int q = qb * 32 + l32;
 
-  float q[DKM], g[DVM], dq[DKM];
-  float D = 0.f, lse = 0.f;
+  float qv[KH], gv[VH];
+  load_half<KH>(qv, a.q, a.ldq, tok0, q, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
+  load_half<VH>(gv, a.dout, a.lddo, tok0, q, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+  float D;
+  {
+    float ov[VH];
+    load_half<VH>(ov, a.o, a.ldo, tok0, q, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+    float d0 = 0.f, d1 = 0.f;
 #pragma unroll
-  for (int e = 0; e < DKM; ++e) q[e] = dq[e] = 0.f;
-#pragma unroll
-  for (int e = 0; e < DVM; ++e) g[e] = 0.f;
-  if (active) {
-    const long long tok = (long long)b * a.S + qi;
-    const float* qr = a.q + tok * a.ldq + (long long)h * a.dk;
-    const float* gr = a.dout + tok * a.lddo + (long long)h * a.dv;
-    const float* orow = a.o + tok * a.ldo + (long long)h * a.dv;
-#pragma unroll
-    for (int e = 0; e < DKM; ++e) q[e] = e < a.dk ? qr[e] * a.scale : 0.f;
-#pragma unroll
-    for (int e = 0; e < DVM; ++e) {
-      g[e] = e < a.dv ? gr[e] : 0.f;
-      D = fmaf(g[e], e < a.dv ? orow[e] : 0.f, D);
+    for (int i = 0; i < VH; i += 2) {
+      d0 = fmaf(gv[i], ov[i], d0);
+      d1 = fmaf(gv[i + 1], ov[i + 1], d1);
     }
-    lse = a.lse[(long long)pair * a.S + qi];
-    a.D[(long long)pair * a.S + qi] = D;
+    D = d0 + d1;
+    D += __shfl_xor(D, 32, 64);
   }
-  const int qmax = min(a.S, (int)(blockIdx.y + 1) * a.QB);
-  const int kend = a.causal ? qmax : a.S;
-  for (int k0 = 0; k0 < kend; k0 += a.KT) {
-    const int nk = min(a.KT, kend - k0);
-    __syncthreads();
-    stage_rows<DKM>(Ks, a.k, a.ldk, a.dk, a, pair0, k0, a.KT);
-    stage_rows<DVM>(Vs, a.v, a.ldv, a.dv, a, pair0, k0, a.KT);
-    __syncthreads();
-    if (!active) continue;
-    const int jn = a.causal ? min(nk, qi - k0 + 1) : nk;
-    const float* kt = Ks + pl * a.KT * DKM;
-    const float* vt = Vs + pl * a.KT * DVM;
-    for (int j = 0; j < jn; ++j) {
-      const float s = dot_row<DKM>(q, kt + j * DKM);
-      const float dp = dot_row<DVM>(g, vt + j * DVM);
-      const float p = expf(s - lse);
-      const float ds = p * (dp - D);
+  const bool qok = q < a.S;
+  const float lse = qok ? a.lse[(long long)pair * a.S + q] : 0.f;
+  if (h == 0 && qok) a.D[(long long)pair * a.S + q] = D;
+
+  floatx16 dq[QB];
 #pragma unroll
-      for (int e = 0; e < DKM; ++e) dq[e] = fmaf(ds, kt[j * DKM + e], dq[e]);
+  for (int i = 0; i < QB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
+  const int kb_last = a.causal ? qb : (a.S - 1) >> 5;
+  for (int kb = 0; kb <= kb_last; ++kb) {
+    floatx16 sacc, pacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
+    {
+      float kv[KH];
+      load_half<KH>(kv, a.k, a.ldk, tok0, kb * 32 + l32, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
+      sacc = mfma_rows<KH>(kv, qv, sacc);
     }
+    {
+      float vv[VH];
+      load_half<VH>(vv, a.v, a.ldv, tok0, kb * 32 + l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+      pacc = mfma_rows<VH>(vv, gv, pacc);
+    }
+    float dS[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = kb * 32 + acc_row(r, h);
+      const bool ok = qok && key < a.S && (!a.causal || key <= q);
+      const float p = ok ? expf(sacc[r] - lse) : 0.f;
+      dS[r] = p * (pacc[r] - D);
+    }
+    mfma_p_rows<QB>(dS, a.k, a.ldk, tok0, kb * 32, a.S, hd * a.dk, a.dk, l32, h, dq);
   }
-  if (!active) return;
 #pragma unroll
-  for (int e = 0; e < DKM; ++e) dq[e] *= a.scale;
-  rope_transpose_row<DKM>(dq, a, qi);
-  float* dqr = a.dq + ((long long)b * a.S + qi) * a.lddq + (long long)h * a.dk;
+  for (int i = 0; i < QB; ++i)
 #pragma unroll
-  for (int e = 0; e < DKM; ++e)
-    if (e < a.dk) dqr[e] = dq[e];
+    for (int r = 0; r < 16; ++r) {
+      const int qr = qb * 32 + acc_row(r, h);
+      const int e = i * 32 + l32;
+      const float g = rope_t(dq[i][r] * a.scale, e, qr, a, qr < a.S);
+      if (qr < a.S && e < a.dk) a.dq[(tok0 + qr) * a.lddq + hd * a.dk + e] = g;
+    }
 }
 
-// dK and/or dV with one lane per key; query-side rows (Q, dO, lse, D) staged in LDS.
-template <int DKM, int DVM, bool DO_DK, bool DO_DV>
+// ---------------------------------------------------------------------------
+// dK / dV: wave per (pair, key block), S layout (lane <-> key)
+// ---------------------------------------------------------------------------
+template <int DKM, int DVM>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a) {
-  extern __shared__ float smem[];
-  float* Qs = smem;
-  float* Gs = Qs + a.P * a.KT * DKM;
-  float* Ls = Gs + a.P * a.KT * DVM;
-  float* Ds = Ls + a.P * a.KT;
-  const int t = threadIdx.x;
-  const int pl = t / a.QB;
-  const int kj = blockIdx.y * a.QB + t % a.QB;
-  const int pair0 = blockIdx.x * a.P;
-  const int pair = pair0 + pl;
-  const bool active = pl < a.P && pair < a.B * a.H && kj < a.S;
-  const int b = pair / a.H, h = pair % a.H;
+  constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int nkb = (a.S + 31) >> 5;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= a.B * a.H * nkb) return;
+  const int pair = item / nkb, kb = item % nkb;
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int key = kb * 32 + l32;
 
-  float k[DKM], v[DVM], dk[DKM], dv[DVM];
+  float kv[KH], vv[VH];
+  load_half<KH>(kv, a.k, a.ldk, tok0, key, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
+  load_half<VH>(vv, a.v, a.ldv, tok0, key, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+  floatx16 dk[KB], dv[VB];
 #pragma unroll
-  for (int e = 0; e < DKM; ++e) k[e] = dk[e] = 0.f;
+  for (int i = 0; i < KB; ++i)
 #pragma unroll
-  for (int e = 0; e < DVM; ++e) v[e] = dv[e] = 0.f;
-  if (active) {
-    const long long tok = (long long)b * a.S + kj;
-    const float* kr = a.k + tok * a.ldk + (long long)h * a.dk;
-    const float* vr = a.v + tok * a.ldv + (long long)h * a.dv;
+    for (int r = 0; r < 16; ++r) dk[i][r] = 0.f;
 #pragma unroll
-    for (int e = 0; e < DKM; ++e) k[e] = e < a.dk ? kr[e] * a.scale : 0.f;
-    if (DO_DK) {
+  for (int i = 0; i < VB; ++i)
 #pragma unroll
-      for (int e = 0; e < DVM; ++e) v[e] = e < a.dv ? vr[e] : 0.f;
+    for (int r = 0; r < 16; ++r) dv[i][r] = 0.f;
+  const bool kok = key < a.S;
+  const int nqb = (a.S + 31) >> 5;
+  for (int qb = a.causal ? kb : 0; qb < nqb; ++qb) {
+    floatx16 sacc, pacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
+    {
+      float qv[KH];
+      load_half<KH>(qv, a.q, a.ldq, tok0, qb * 32 + l32, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
+      sacc = mfma_rows<KH>(qv, kv, sacc);  // S[q, key]
     }
-  }
-  // queries i >= the smallest key of this block contribute when causal
-  const int qstart = a.causal ? (int)blockIdx.y * a.QB : 0;
-  for (int i0 = qstart - (qstart % a.KT); i0 < a.S; i0 += a.KT) {
-    const int ni = min(a.KT, a.S - i0);
-    __syncthreads();
-    stage_rows<DKM>(Qs, a.q, a.ldq, a.dk, a, pair0, i0, a.KT);
-    stage_rows<DVM>(Gs, a.dout, a.lddo, a.dv, a, pair0, i0, a.KT);
-    for (int idx = threadIdx.x; idx < a.P * a.KT; idx += blockDim.x) {
-      const int pp = idx / a.KT, r = idx % a.KT;
-      const int pr = pair0 + pp, row = i0 + r;
-      const bool ok = pr < a.B * a.H && row < a.S;
-      Ls[idx] = ok ? a.lse[(long long)pr * a.S + row] : 0.f;
-      Ds[idx] = ok ? a.D[(long long)pr * a.S + row] : 0.f;
+    {
+      float gq[VH];
+      load_half<VH>(gq, a.dout, a.lddo, tok0, qb * 32 + l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+      pacc = mfma_rows<VH>(gq, vv, pacc);  // dP[q, key]
     }
-    __syncthreads();
-    if (!active) continue;
-    const int ibeg = a.causal ? max(0, kj - i0) : 0;
-    const float* qt = Qs + pl * a.KT * DKM;
-    const float* gt = Gs + pl * a.KT * DVM;
-    const float* lt = Ls + pl * a.KT;
-    const float* dt = Ds + pl * a.KT;
-    for (int i = ibeg; i < ni; ++i) {
-      const float s = dot_row<DKM>(k, qt + i * DKM);
-      const float p = expf(s - lt[i]);
-      if (DO_DV) {
+    float P[16], dS[16];
 #pragma unroll
-        for (int e = 0; e < DVM; ++e) dv[e] = fmaf(p, gt[i * DVM + e], dv[e]);
-      }
-      if (DO_DK) {
-        const float dp = dot_row<DVM>(v, gt + i * DVM);
-        const float ds = p * (dp - dt[i]);
-#pragma unroll
-        for (int e = 0; e < DKM; ++e) dk[e] = fmaf(ds, qt[i * DKM + e], dk[e]);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int qr = qb * 32 + acc_row(r, h);
+      const bool ok = kok && qr < a.S && (!a.causal || key <= qr);
+      const long long li = (long long)pair * a.S + (qr < a.S ? qr : 0);
+      const float p = ok ? expf(sacc[r] - a.lse[li]) : 0.f;
+      P[r] = p;
+      dS[r] = p * (pacc[r] - (ok ? a.D[li] : 0.f));
     }
+    mfma_p_rows<VB>(P, a.dout, a.lddo, tok0, qb * 32, a.S, hd * a.dv, a.dv, l32, h, dv);
+    mfma_p_rows<KB>(dS, a.q, a.ldq, tok0, qb * 32, a.S, hd * a.dk, a.dk, l32, h, dk);
   }
-  if (!active) return;
-  const long long tok = (long long)b * a.S + kj;
-  if (DO_DK) {
+  // dK / dV in accumulator layout: register r <-> key kb*32 + acc_row(r, h), lane <-> column
 #pragma unroll
-    for (int e = 0; e < DKM; ++e) dk[e] *= a.scale;
-    rope_transpose_row<DKM>(dk, a, kj);
-    float* dkr = a.dk_out + tok * a.lddk + (long long)h * a.dk;
+  for (int i = 0; i < KB; ++i)
 #pragma unroll
-    for (int e = 0; e < DKM; ++e)
-      if (e < a.dk) dkr[e] = dk[e];
-  }
-  if (DO_DV) {
-    float* dvr = a.dv_out + tok * a.lddv + (long long)h * a.dv;
+    for (int r = 0; r < 16; ++r) {
+      const int kr = kb * 32 + acc_row(r, h);
+      const int e = i * 32 + l32;
+      const float g = rope_t(dk[i][r] * a.scale, e, kr, a, kr < a.S);
+      if (kr < a.S && e < a.dk) a.dk_out[(tok0 + kr) * a.lddk + hd * a.dk + e] = g;
+    }
 #pragma unroll
-    for (int e = 0; e < DVM; ++e)
-      if (e < a.dv) dvr[e] = dv[e];
-  }
+  for (int i = 0; i < VB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = kb * 32 + acc_row(r, h);
+      const int e = i * 32 + l32;
+      if (kr < a.S && e < a.dv) a.dv_out[(tok0 + kr) * a.lddv + hd * a.dv + e] = dv[i][r];
+    }
 }
 
-// Workgroup geometry: P pairs x QB queries (QB = min(S, 256)), tile of KT rows such that the
-// staged tiles stay within 48 KB of LDS.
-static void geometry(AttnArgs& a, int dkm, int dvm, int extra_per_row) {
-  a.QB = a.S < 256 ? a.S : 256;
-  a.P = a.S < 256 ? 256 / a.S : 1;
-  const int budget = 48 * 1024 / 4;
-  int kt = budget / (a.P * (dkm + dvm + extra_per_row));
-  kt = kt >= 64 ? 64 : (kt >= 32 ? 32 : (kt >= 16 ? 16 : 8));
-  a.KT = kt;
-}
-
+// ---------------------------------------------------------------------------
+// Launch
+// ---------------------------------------------------------------------------
 static bool pick_dims(int dk, int dv, int* dkm, int* dvm) {
   if (dk <= 32 && dv <= 32) { *dkm = 32; *dvm = 32; return true; }
   if (dk <= 64 && dv <= 64) { *dkm = 64; *dvm = 64; return true; }
@@ -329,19 +369,43 @@ static bool pick_dims(int dk, int dv, int* dkm, int* dvm) {
   return false;
 }
 
-// Algorithmic work of one pass over all (batch, head) pairs: `per_pair_flops` flops per
-// (query, key) pair that the mask keeps, `bytes` of HBM traffic.
+static AttnArgs make_args(const AttnDesc& d, int dkm, int dvm) {
+  AttnArgs a{};
+  a.B = d.batch; a.S = d.seq; a.H = d.heads; a.dk = d.dk; a.dv = d.dv; a.scale = d.scale; a.causal = d.causal;
+  a.q = d.q; a.ldq = d.ldq; a.k = d.k; a.ldk = d.ldk; a.v = d.v; a.ldv = d.ldv;
+  a.o = d.o; a.ldo = d.ldo; a.lse = d.lse;
+  a.dout = d.dout; a.lddo = d.lddo;
+  a.dq = d.dq; a.lddq = d.lddq; a.dk_out = d.dk_out; a.lddk = d.lddk; a.dv_out = d.dv_out; a.lddv = d.lddv;
+  a.rcos = d.rope_cos; a.rsin = d.rope_sin; a.rope_off = d.rope_off; a.rope_dim = d.rope_dim;
+  // row halves start at (token * ld + head * dim + half * dim/2): 16-byte aligned when all of
+  // ld, dim and dim/2 are multiples of 4 and the bases are aligned
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  bool vec = d.dk == dkm && d.dv == dvm && (dkm / 2) % 4 == 0 && (dvm / 2) % 4 == 0;
+  for (long long ld : {d.ldq, d.ldk, d.ldv, d.ldo}) vec = vec && ld % 4 == 0;
+  vec = vec && al(d.q) && al(d.k) && al(d.v) && al(d.o);
+  if (d.dout) vec = vec && d.lddo % 4 == 0 && al(d.dout);
+  a.vec = vec ? 1 : 0;
+  return a;
+}
+
+// Algorithmic work: flops per kept (query, key) pair, bytes of HBM traffic.
 static double kept_pairs(const AttnArgs& a) {
   const double S = a.S;
   return (double)a.B * a.H * (a.causal ? S * (S + 1) / 2 : S * S);
 }
 
-#define ATTN_DISPATCH(DK, DV, KERNEL, ...)                                                          \
-  if (dkm == DK && dvm == DV) {                                                                     \
-    ProfScope ps(s, #KERNEL "<" #DK ", " #DV ">", flops, bytes);                                    \
-    hipLaunchKernelGGL((KERNEL<DK, DV, ##__VA_ARGS__>), grid, dim3(256), lds, s, a);               \
-    return launch_status(#KERNEL);                                                                  \
+#define ATTN_DISPATCH(DK, DV, KERNEL)                                                     \
+  if (dkm == DK && dvm == DV) {                                                           \
+    ProfScope ps(s, #KERNEL "<" #DK ", " #DV ">", flops, bytes);                          \
+    hipLaunchKernelGGL((KERNEL<DK, DV>), grid, dim3(256), 0, s, a);                       \
+    return launch_status(#KERNEL);                                                        \
   }
+#define ATTN_ALL(KERNEL)           \
+  ATTN_DISPATCH(32, 32, KERNEL)    \
+  ATTN_DISPATCH(64, 64, KERNEL)    \
+  ATTN_DISPATCH(96, 64, KERNEL)    \
+  ATTN_DISPATCH(128, 128, KERNEL)  \
+  return TALOS_ERR_UNSUPPORTED;
 
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
   int dkm, dvm;
@@ -349,27 +413,39 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
     set_error("attention: head dims (%d, %d) exceed the supported (128, 128)", d.dk, d.dv);
     return TALOS_ERR_UNSUPPORTED;
   }
-  AttnArgs a{};
-  a.B = d.batch; a.S = d.seq; a.H = d.heads; a.dk = d.dk; a.dv = d.dv; a.scale = d.scale; a.causal = d.causal;
-  a.q = d.q; a.ldq = d.ldq; a.k = d.k; a.ldk = d.ldk; a.v = d.v; a.ldv = d.ldv;
-  a.o = d.o; a.ldo = d.ldo; a.lse = d.lse;
+  AttnArgs a = make_args(d, dkm, dvm);
   if ((long long)a.B * a.H * a.S == 0) return TALOS_OK;
-  geometry(a, dkm, dvm, 0);
-  const size_t lds = (size_t)a.P * a.KT * (dkm + dvm) * sizeof(float);
-  dim3 grid(ceil_div((size_t)a.B * a.H, a.P), ceil_div(a.S, a.QB));
+  const long long items = (long long)a.B * a.H * ((a.S + 31) / 32);
+  dim3 grid(ceil_div((size_t)items, 4));
   const double rows = (double)a.B * a.S * a.H;  // (token, head) rows
   // QK^T and PV over the kept pairs; q, k, v read, o and lse written
   const double flops = kept_pairs(a) * (2.0 * a.dk + 2.0 * a.dv);
   const double bytes = 4.0 * rows * (2.0 * a.dk + a.dv) + 4.0 * rows * (a.dv + 1.0);
-  ATTN_DISPATCH(32, 32, attn_fwd_kernel)
-  ATTN_DISPATCH(64, 64, attn_fwd_kernel)
-  ATTN_DISPATCH(96, 64, attn_fwd_kernel)
-  ATTN_DISPATCH(128, 128, attn_fwd_kernel)
-  return TALOS_ERR_UNSUPPORTED;
+  ATTN_ALL(attn_fwd_kernel)
 }
 
 size_t attn_bwd_workspace_bytes(const AttnDesc& d) {
   return (size_t)d.batch * d.heads * d.seq * sizeof(float);
+}
+
+static int attn_bwd_dq(const AttnArgs& a, int dkm, int dvm, hipStream_t s) {
+  const long long items = (long long)a.B * a.H * ((a.S + 31) / 32);
+  dim3 grid(ceil_div((size_t)items, 4));
+  const double rows = (double)a.B * a.S * a.H;
+  // s = q.k, dp = dO.v, dq += ds k; reads q k v o dO lse, writes dq and D
+  const double flops = kept_pairs(a) * (4.0 * a.dk + 2.0 * a.dv);
+  const double bytes = 4.0 * rows * (3.0 * a.dk + 3.0 * a.dv + 2.0);
+  ATTN_ALL(attn_bwd_dq_kernel)
+}
+
+static int attn_bwd_dkv(const AttnArgs& a, int dkm, int dvm, hipStream_t s) {
+  const long long items = (long long)a.B * a.H * ((a.S + 31) / 32);
+  dim3 grid(ceil_div((size_t)items, 4));
+  const double rows = (double)a.B * a.S * a.H;
+  // s = q.k, dp = dO.v, dv += p dO, dk += ds q; reads q dO lse D k v, writes dk dv
+  const double flops = kept_pairs(a) * (4.0 * a.dk + 4.0 * a.dv);
+  const double bytes = 4.0 * rows * (3.0 * a.dk + 3.0 * a.dv + 2.0);
+  ATTN_ALL(attn_bwd_dkv_kernel)
 }
 
 int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
@@ -378,57 +454,12 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
     set_error("attention: head dims (%d, %d) exceed the supported (128, 128)", d.dk, d.dv);
     return TALOS_ERR_UNSUPPORTED;
   }
-  AttnArgs a{};
-  a.B = d.batch; a.S = d.seq; a.H = d.heads; a.dk = d.dk; a.dv = d.dv; a.scale = d.scale; a.causal = d.causal;
-  a.q = d.q; a.ldq = d.ldq; a.k = d.k; a.ldk = d.ldk; a.v = d.v; a.ldv = d.ldv;
-  a.o = d.o; a.ldo = d.ldo; a.lse = d.lse;
-  a.dout = d.dout; a.lddo = d.lddo;
-  a.dq = d.dq; a.lddq = d.lddq; a.dk_out = d.dk_out; a.lddk = d.lddk; a.dv_out = d.dv_out; a.lddv = d.lddv;
+  AttnArgs a = make_args(d, dkm, dvm);
   a.D = ws;
-  a.rcos = d.rope_cos; a.rsin = d.rope_sin; a.rope_off = d.rope_off; a.rope_dim = d.rope_dim;
   if ((long long)a.B * a.H * a.S == 0) return TALOS_OK;
-  const double rows = (double)a.B * a.S * a.H;
-  int rc;
-  {
-    geometry(a, dkm, dvm, 0);
-    const size_t lds = (size_t)a.P * a.KT * (dkm + dvm) * sizeof(float);
-    dim3 grid(ceil_div((size_t)a.B * a.H, a.P), ceil_div(a.S, a.QB));
-    // s = q.k, dp = dO.v, dq += ds k; reads q k v o dO lse, writes dq and D
-    const double flops = kept_pairs(a) * (4.0 * a.dk + 2.0 * a.dv);
-    const double bytes = 4.0 * rows * (3.0 * a.dk + 3.0 * a.dv + 2.0);
-    rc = [&]() -> int {
-      ATTN_DISPATCH(32, 32, attn_bwd_dq_kernel)
-      ATTN_DISPATCH(64, 64, attn_bwd_dq_kernel)
-      ATTN_DISPATCH(96, 64, attn_bwd_dq_kernel)
-      ATTN_DISPATCH(128, 128, attn_bwd_dq_kernel)
-      return TALOS_ERR_UNSUPPORTED;
-    }();
-    if (rc) return rc;
-  }
-  geometry(a, dkm, dvm, 2);
-  const size_t lds = (size_t)a.P * a.KT * (dkm + dvm + 2) * sizeof(float);
-  dim3 grid(ceil_div((size_t)a.B * a.H, a.P), ceil_div(a.S, a.QB));
-  if (dkm + dvm <= 64) {
-    // small heads: one pass computes both dK and dV; reads q dO lse D k v, writes dk dv
-    const double flops = kept_pairs(a) * (4.0 * a.dk + 4.0 * a.dv);
-    const double bytes = 4.0 * rows * (3.0 * a.dk + 3.0 * a.dv + 2.0);
-    ATTN_DISPATCH(32, 32, attn_bwd_dkv_kernel, true, true)
-  }
-  rc = [&]() -> int {
-    const double flops = kept_pairs(a) * (4.0 * a.dk + 2.0 * a.dv);
-    const double bytes = 4.0 * rows * (3.0 * a.dk + 2.0 * a.dv + 2.0);
-    ATTN_DISPATCH(64, 64, attn_bwd_dkv_kernel, true, false)
-    ATTN_DISPATCH(96, 64, attn_bwd_dkv_kernel, true, false)
-    ATTN_DISPATCH(128, 128, attn_bwd_dkv_kernel, true, false)
-    return TALOS_ERR_UNSUPPORTED;
-  }();
+  int rc = attn_bwd_dq(a, dkm, dvm, s);
   if (rc) return rc;
-  const double flops = kept_pairs(a) * (2.0 * a.dk + 2.0 * a.dv);
-  const double bytes = 4.0 * rows * (2.0 * a.dk + 2.0 * a.dv + 1.0);
-  ATTN_DISPATCH(64, 64, attn_bwd_dkv_kernel, false, true)
-  ATTN_DISPATCH(96, 64, attn_bwd_dkv_kernel, false, true)
-  ATTN_DISPATCH(128, 128, attn_bwd_dkv_kernel, false, true)
-  return TALOS_ERR_UNSUPPORTED;
+  return attn_bwd_dkv(a, dkm, dvm, s);
 }
 
 static int check_attn(const char* fn, int batch, int seq, int heads, int qk_dim, int v_dim, int causal, int ld_q,

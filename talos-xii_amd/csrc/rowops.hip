@@ -181,9 +181,10 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_generic(int rows, int dim, fl
 // Backward: a bounded grid (at most kMaxParts workgroups) strides over the rows, one row per wave
 // at a time; each lane keeps its columns' dgain sums in registers, so a workgroup writes a single
 // f64 partial row that reduce_parts_kernel combines.
+constexpr int kRmsMaxBlocks = 2048;  // 8 waves per CU in flight; 2048 x dim f64 partials
 static int rms_bwd_blocks(int rows) {
   int b = (rows + 3) / 4;
-  return b < 1 ? 1 : (b > kMaxParts ? kMaxParts : b);
+  return b < 1 ? 1 : (b > kRmsMaxBlocks ? kRmsMaxBlocks : b);
 }
 
 template <int V>
