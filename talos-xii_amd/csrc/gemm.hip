@@ -25,6 +25,15 @@ constexpr int BM = 128, BN = 128, BK = 32;
 constexpr int LDS_S = 160;  // panel row stride (floats): the two half-waves read rows k, k+1
                             // whose offset 160 = 32 mod 64 keeps them on disjoint LDS banks
 constexpr int NT = 256;
+// Tuning knobs (compile-time): TALOS_GEMM_DBUF = 1 double-buffers the LDS panels (one barrier per
+// K chunk); TALOS_GEMM_WAVES = minimum waves per SIMD the register allocation must allow.
+#ifndef TALOS_GEMM_DBUF
+#define TALOS_GEMM_DBUF 0
+#endif
+#ifndef TALOS_GEMM_WAVES
+#define TALOS_GEMM_WAVES 2
+#endif
+constexpr int NBUF = TALOS_GEMM_DBUF ? 2 : 1;
 
 // Epilogue flags (template parameter E).
 enum : int {
@@ -195,10 +204,94 @@ __device__ __forceinline__ float epi_value(const GemmArgs& p, float acc, int row
   return v;
 }
 
+// Epilogue of four consecutive columns [col, col + 4) of one row, read from / written to global
+// memory as float4 (interior) or per element (edges). RoPE pairs (2i, 2i+1) sit in (x, y) and
+// (z, w) because col is a multiple of 4.
+template <int E>
+__device__ __forceinline__ void epi_store4(const GemmArgs& p, float4 v, int row, int col, float* C,
+                                           const float* __restrict__ resid, bool full) {
+  float o[4] = {v.x * p.alpha, v.y * p.alpha, v.z * p.alpha, v.w * p.alpha};
+  if constexpr ((E & E_ROPE) != 0) {
+    if (col < p.rope_cols) {
+      const int half = p.rope_dim >> 1;
+      const int pos = row % p.rope_seq;
+      const int pi = (col % p.rope_dim) >> 1;
+      const float* cs = p.rcos + pos * half + pi;
+      const float* sn = p.rsin + pos * half + pi;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float c = cs[j], s = sn[j];
+        const float x0 = o[2 * j], x1 = o[2 * j + 1];
+        o[2 * j] = fmaf(x0, c, -x1 * s);
+        o[2 * j + 1] = fmaf(x0, s, x1 * c);
+      }
+    }
+  }
+  const long long crow = (long long)row * p.ldc;
+  if (full) {
+    if constexpr ((E & E_BETA) != 0) {
+      const float4 c = *reinterpret_cast<const float4*>(C + crow + col);
+      o[0] += p.beta * c.x; o[1] += p.beta * c.y; o[2] += p.beta * c.z; o[3] += p.beta * c.w;
+    }
+    if constexpr ((E & E_BIAS) != 0) {
+      const float4 bv = *reinterpret_cast<const float4*>(p.bias + col);
+      o[0] += bv.x; o[1] += bv.y; o[2] += bv.z; o[3] += bv.w;
+    }
+    if constexpr ((E & E_RESID) != 0) {
+      const float4 r = *reinterpret_cast<const float4*>(resid + (long long)row * p.ldr + col);
+      o[0] += r.x; o[1] += r.y; o[2] += r.z; o[3] += r.w;
+    }
+    if constexpr ((E & (E_DGELU | E_DRELU)) != 0) {
+      const float4 u = *reinterpret_cast<const float4*>(p.aux + (long long)row * p.ldaux + col);
+      const float uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr ((E & E_DGELU) != 0) o[j] *= gelu_d(uu[j]);
+        else o[j] = uu[j] > 0.f ? o[j] : 0.f;
+      }
+    }
+    if constexpr ((E & (E_GELU | E_RELU)) != 0) {
+      if (p.aux) *reinterpret_cast<float4*>(p.aux + (long long)row * p.ldaux + col) = make_float4(o[0], o[1], o[2], o[3]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr ((E & E_GELU) != 0) o[j] = gelu_f(o[j]);
+        else o[j] = fmaxf(o[j], 0.f);
+      }
+    }
+    *reinterpret_cast<float4*>(C + crow + col) = make_float4(o[0], o[1], o[2], o[3]);
+    return;
+  }
+  if (row >= p.M) return;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int cj = col + j;
+    if (cj >= p.N) break;
+    float x = o[j];
+    if constexpr ((E & E_BETA) != 0) x += p.beta * C[crow + cj];
+    if constexpr ((E & E_BIAS) != 0) x += p.bias[cj];
+    if constexpr ((E & E_RESID) != 0) x += resid[(long long)row * p.ldr + cj];
+    if constexpr ((E & E_DGELU) != 0) x *= gelu_d(p.aux[(long long)row * p.ldaux + cj]);
+    if constexpr ((E & E_DRELU) != 0) x = p.aux[(long long)row * p.ldaux + cj] > 0.f ? x : 0.f;
+    if constexpr ((E & (E_GELU | E_RELU)) != 0) {
+      if (p.aux) p.aux[(long long)row * p.ldaux + cj] = x;
+      if constexpr ((E & E_GELU) != 0) x = gelu_f(x);
+      else x = fmaxf(x, 0.f);
+    }
+    C[crow + cj] = x;
+  }
+}
+
+constexpr int T_S = 136;  // pitch of the staged output tile: rows h*4 apart land 32 banks apart
+constexpr int T_ROWS = BM / 2;  // the tile is staged in two halves of 64 rows
+constexpr int SMEM_FLOATS = (2 * NBUF * BK * LDS_S > T_ROWS * T_S) ? 2 * NBUF * BK * LDS_S : T_ROWS * T_S;
+
 template <bool TA, bool TB, int E>
-__global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
-  __shared__ float As[BK * LDS_S];
-  __shared__ float Bs[BK * LDS_S];
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_WAVES))) void gemm_f32_kernel(
+    GemmArgs p) {
+  __shared__ __align__(16) float smem[SMEM_FLOATS];
+  // panels: As buffer i at smem + i*BK*LDS_S, Bs buffer i after the NBUF A buffers
+  float* const Abase = smem;
+  float* const Bbase = smem + NBUF * BK * LDS_S;
 
   const int tiles_n = (p.N + BN - 1) / BN;
   const int m0 = (blockIdx.x / tiles_n) * BM;
@@ -226,15 +319,16 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
   float4 ra[4], rb[4];
   if (kbeg < kend) {
     load_chunk<TA, TB>(p, A, B, m0, n0, kbeg, kend, interior, ra, rb);
-    store_a<TA>(As, ra);
-    store_b<TB>(Bs, rb);
+    store_a<TA>(Abase, ra);
+    store_b<TB>(Bbase, rb);
   }
   __syncthreads();
+  int buf = 0;
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
     const bool more = k0 + BK < kend;
     if (more) load_chunk<TA, TB>(p, A, B, m0, n0, k0 + BK, kend, interior, ra, rb);
-    const float* ap = As + h * LDS_S + wm * 64 + l32;
-    const float* bp = Bs + h * LDS_S + wn * 64 + l32;
+    const float* ap = Abase + buf * (BK * LDS_S) + h * LDS_S + wm * 64 + l32;
+    const float* bp = Bbase + buf * (BK * LDS_S) + h * LDS_S + wn * 64 + l32;
 #pragma unroll
     for (int s = 0; s < BK / 2; ++s) {
       const float a0 = ap[2 * s * LDS_S], a1 = ap[2 * s * LDS_S + 32];
@@ -244,53 +338,80 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
       acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
       acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
     }
-    __syncthreads();
-    if (more) {
-      store_a<TA>(As, ra);
-      store_b<TB>(Bs, rb);
+    if (NBUF == 2) {
+      // the other buffer was last read in the previous chunk, before the barrier that ended it
+      if (more) {
+        store_a<TA>(Abase + (buf ^ 1) * (BK * LDS_S), ra);
+        store_b<TB>(Bbase + (buf ^ 1) * (BK * LDS_S), rb);
+      }
       __syncthreads();
+      buf ^= 1;
+    } else {
+      __syncthreads();
+      if (more) {
+        store_a<TA>(Abase, ra);
+        store_b<TB>(Bbase, rb);
+        __syncthreads();
+      }
     }
   }
+  if (NBUF == 2 || kbeg >= kend) __syncthreads();
 
-  // Accumulator layout of v_mfma_f32_32x32x2_f32: lane l, register r holds
-  // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 block.
-  if constexpr ((E & E_SPLIT) != 0) {
-    float* P = p.part + ((long long)b * p.ksplit + split) * (long long)p.M * p.N;
+  // Stage the 128x128 tile through LDS, one 64-row half (the two waves with wm == half) at a time
+  // (accumulator layout of v_mfma_f32_32x32x2_f32: lane l, register r holds row
+  // 8*(r/4) + 4*(l/32) + r%4, column l%32 of its 32x32 block), then run the epilogue on
+  // row-contiguous float4s: thread t handles column group t%32 of rows t/32 + 8i of the half.
+  float* T = smem;
+  const int cg = 4 * (threadIdx.x & 31);
+  const int col = n0 + cg;
+  float* C = p.C + (long long)b * p.sC;
+  const float* resid = ((E & E_RESID) != 0) ? p.resid + (long long)b * p.sC : nullptr;
+  // float4 path needs every row start 16-byte aligned in each operand the epilogue touches
+  const bool full_cols = interior || (col + 3 < p.N);
+  const bool aligned = ((p.ldc & 3) == 0) && (((E & E_RESID) == 0) || (p.ldr & 3) == 0) &&
+                       (((E & (E_GELU | E_RELU | E_DGELU | E_DRELU)) == 0) || (p.ldaux & 3) == 0) &&
+                       ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+  for (int half = 0; half < 2; ++half) {
+    if (half) __syncthreads();  // the first half has been read out
+    if (wm == half) {
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          const int col = n0 + wn * 64 + nt * 32 + l32;
-          if (interior || (row < p.M && col < p.N)) P[(long long)row * p.N + col] = acc[mt][nt][r];
-        }
-  } else {
-    float* C = p.C + (long long)b * p.sC;
-    const float* resid = ((E & E_RESID) != 0) ? p.resid + (long long)b * p.sC : nullptr;
+        for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          const int col = n0 + wn * 64 + nt * 32 + l32;
-          float v = acc[mt][nt][r];
-          if constexpr ((E & E_ROPE) != 0) {
-            // interleaved pair (2i, 2i+1) of a head: the partner column is the neighbouring lane
-            const float partner = __shfl_xor(v, 1, 64);
-            if (col < p.rope_cols) {
-              const int half = p.rope_dim >> 1;
-              const int pi = (col % p.rope_dim) >> 1;
-              const int pos = row % p.rope_seq;
-              const float c = p.rcos[pos * half + pi], s = p.rsin[pos * half + pi];
-              v = (col & 1) ? fmaf(partner, s, v * c) : fmaf(v, c, -partner * s);
-            }
+          for (int r = 0; r < 16; ++r) {
+            const int row = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const int c = wn * 64 + nt * 32 + l32;
+            T[row * T_S + c] = acc[mt][nt][r];
           }
-          if (interior || (row < p.M && col < p.N)) C[(long long)row * p.ldc + col] = epi_value<E>(p, v, row, col, C, resid);
+    }
+    __syncthreads();
+    if constexpr ((E & E_SPLIT) != 0) {
+      float* P = p.part + ((long long)b * p.ksplit + split) * (long long)p.M * p.N;
+      const bool vec_out = (p.N & 3) == 0;
+#pragma unroll 4
+      for (int i = 0; i < T_ROWS / 8; ++i) {
+        const int lr = (threadIdx.x >> 5) + 8 * i;
+        const int row = m0 + half * T_ROWS + lr;
+        const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
+        if (row >= p.M) continue;
+        if (vec_out && col + 3 < p.N) {
+          *reinterpret_cast<float4*>(P + (long long)row * p.N + col) = v;
+        } else {
+          const float vv[4] = {v.x, v.y, v.z, v.w};
+          for (int j = 0; j < 4 && col + j < p.N; ++j) P[(long long)row * p.N + col + j] = vv[j];
         }
+      }
+    } else {
+#pragma unroll 4
+      for (int i = 0; i < T_ROWS / 8; ++i) {
+        const int lr = (threadIdx.x >> 5) + 8 * i;
+        const int row = m0 + half * T_ROWS + lr;
+        const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
+        epi_store4<E>(p, v, row, col, C, resid, aligned && full_cols && row < p.M);
+      }
+    }
   }
 }
 
