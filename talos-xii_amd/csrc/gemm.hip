@@ -33,6 +33,13 @@ constexpr int NT = 256;
 #ifndef TALOS_GEMM_WAVES
 #define TALOS_GEMM_WAVES 2
 #endif
+// Split-K sizing: target workgroups per CU and the minimum K per split.
+#ifndef TALOS_SPLITK_WG_PER_CU
+#define TALOS_SPLITK_WG_PER_CU 2
+#endif
+#ifndef TALOS_SPLITK_MIN_K
+#define TALOS_SPLITK_MIN_K 256
+#endif
 constexpr int NBUF = TALOS_GEMM_DBUF ? 2 : 1;
 
 // Epilogue flags (template parameter E).
@@ -45,7 +52,8 @@ enum : int {
   E_DGELU = 32,  // v *= gelu'(aux)
   E_DRELU = 64,  // v = aux > 0 ? v : 0
   E_ROPE = 128,  // rotate interleaved pairs of columns [0, rope_cols)
-  E_SPLIT = 256  // write the fp32 partial tile of this K split (no epilogue)
+  E_SPLIT = 256,  // write the fp32 partial tile of this K split (no epilogue)
+  E_DBIAS = 512   // also sum the columns of op(B) (bias gradient; transA = 1, transB = 0)
 };
 
 struct GemmArgs {
@@ -66,7 +74,9 @@ struct GemmArgs {
   const float* rsin;
   int rope_cols, rope_dim, rope_seq;
   int ksplit, kper;
-  float* part;
+  float* part;  // [batch][ksplit][M + (dbias ? 1 : 0)][N]
+  float* dbias;
+  float beta_dbias;
   int vecA, vecB;
 };
 
@@ -316,6 +326,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_W
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  float csum = 0.f;  // E_DBIAS: this thread's column sum over its half of each panel
   float4 ra[4], rb[4];
   if (kbeg < kend) {
     load_chunk<TA, TB>(p, A, B, m0, n0, kbeg, kend, interior, ra, rb);
@@ -338,6 +349,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_W
       acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
       acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
     }
+    if constexpr ((E & E_DBIAS) != 0) {
+      // column sums of the B panel Bs[k][n] (k-major): thread t sums column t%128 over half the rows
+      if (m0 == 0) {
+        const float* bc = Bbase + buf * (BK * LDS_S) + (threadIdx.x >> 7) * (BK / 2) * LDS_S + (threadIdx.x & 127);
+#pragma unroll
+        for (int kk = 0; kk < BK / 2; ++kk) csum += bc[kk * LDS_S];
+      }
+    }
     if (NBUF == 2) {
       // the other buffer was last read in the previous chunk, before the barrier that ended it
       if (more) {
@@ -356,6 +375,24 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_W
     }
   }
   if (NBUF == 2 || kbeg >= kend) __syncthreads();
+  if constexpr ((E & E_DBIAS) != 0) {
+    // combine the two row halves; the M-tile-0 workgroups write the bias-gradient row
+    if (m0 == 0) {
+      smem[threadIdx.x] = csum;
+      __syncthreads();
+      const int n = n0 + (int)threadIdx.x;
+      if (threadIdx.x < 128 && n < p.N) {
+        const float cs = smem[threadIdx.x] + smem[threadIdx.x + 128];
+        if constexpr ((E & E_SPLIT) != 0) {
+          p.part[(((long long)b * p.ksplit + split) * (p.M + 1) + p.M) * p.N + n] = cs;
+        } else {
+          float* db = p.dbias + (long long)b * p.N;
+          db[n] = p.beta_dbias != 0.f ? db[n] + cs : cs;
+        }
+      }
+      __syncthreads();
+    }
+  }
 
   // Stage the 128x128 tile through LDS, one 64-row half (the two waves with wm == half) at a time
   // (accumulator layout of v_mfma_f32_32x32x2_f32: lane l, register r holds row
@@ -388,7 +425,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_W
     }
     __syncthreads();
     if constexpr ((E & E_SPLIT) != 0) {
-      float* P = p.part + ((long long)b * p.ksplit + split) * (long long)p.M * p.N;
+      float* P = p.part + ((long long)b * p.ksplit + split) * (long long)(p.M + ((E & E_DBIAS) ? 1 : 0)) * p.N;
       const bool vec_out = (p.N & 3) == 0;
 #pragma unroll 4
       for (int i = 0; i < T_ROWS / 8; ++i) {
@@ -415,24 +452,44 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_W
   }
 }
 
-// Sums the split-K partials in f64 and applies the epilogue (beta and bias only).
+// Sums the split-K partials in f64 and applies the epilogue (beta and bias only). Workgroup of
+// 1024 threads = 16 waves: lane <-> one of 64 consecutive elements, wave w <-> splits w, w+16, ...
+// Row M of the partials (when present) holds the bias-gradient column sums.
 template <int E>
-__global__ void gemm_splitk_reduce(GemmArgs p) {
-  const long long MN = (long long)p.M * p.N;
+__global__ __launch_bounds__(1024) void gemm_splitk_reduce(GemmArgs p) {
+  __shared__ double red[16][64];
+  const int rows = p.M + (p.dbias ? 1 : 0);
+  const long long RN = (long long)rows * p.N;
   const int b = blockIdx.y;
-  const float* P = p.part + (long long)b * p.ksplit * MN;
-  float* C = p.C + (long long)b * p.sC;
-  for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < MN; e += (long long)gridDim.x * blockDim.x) {
-    double s0 = 0.0, s1 = 0.0;
-    int k = 0;
-    for (; k + 1 < p.ksplit; k += 2) {
-      s0 += (double)P[k * MN + e];
-      s1 += (double)P[(k + 1) * MN + e];
+  const float* P = p.part + (long long)b * p.ksplit * RN;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const long long e = (long long)blockIdx.x * 64 + lane;
+  double s0 = 0.0, s1 = 0.0;
+  if (e < RN) {
+    int k = w;
+    for (; k + 16 < p.ksplit; k += 32) {
+      s0 += (double)P[k * RN + e];
+      s1 += (double)P[(k + 16) * RN + e];
     }
-    if (k < p.ksplit) s0 += (double)P[k * MN + e];
-    const int row = (int)(e / p.N), col = (int)(e % p.N);
-    C[(long long)row * p.ldc + col] = epi_value<E>(p, (float)(s0 + s1), row, col, C, nullptr);
+    if (k < p.ksplit) s0 += (double)P[k * RN + e];
   }
+  red[w][lane] = s0 + s1;
+  __syncthreads();
+  if (w != 0 || e >= RN) return;
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s += red[i][lane];
+  const int row = (int)(e / p.N), col = (int)(e % p.N);
+  if (row == p.M) {
+    float* db = p.dbias + (long long)b * p.N;
+    db[col] = (float)(p.beta_dbias != 0.f ? (double)db[col] + s : s);
+    return;
+  }
+  float* C = p.C + (long long)b * p.sC;
+  float v = p.alpha * (float)s;
+  if constexpr ((E & E_BETA) != 0) v += p.beta * C[(long long)row * p.ldc + col];
+  if constexpr ((E & E_BIAS) != 0) v += p.bias[col];
+  C[(long long)row * p.ldc + col] = v;
 }
 
 static GemmArgs to_args(const GemmDesc& d) {
@@ -464,6 +521,8 @@ static GemmArgs to_args(const GemmDesc& d) {
   a.ksplit = d.ksplit < 1 ? 1 : d.ksplit;
   a.kper = d.K;
   a.part = d.workspace;
+  a.dbias = d.dbias;
+  a.beta_dbias = d.beta_dbias;
   auto aligned = [](const void* ptr, long long ld) {
     return ((reinterpret_cast<uintptr_t>(ptr) & 15) == 0) && (ld % 4 == 0);
   };
@@ -488,6 +547,7 @@ static int epi_flags(const GemmDesc& d) {
   if (d.dact == GEMM_DACT_GELU) e |= E_DGELU;
   if (d.dact == GEMM_DACT_RELU) e |= E_DRELU;
   if (d.rope_cols > 0) e |= E_ROPE;
+  if (d.dbias) e |= E_DBIAS;
   return e;
 }
 
@@ -496,15 +556,18 @@ size_t gemm_plan_split(GemmDesc& d, int num_cu) {
   if (d.ksplit == 0) {
     const long long tiles = (long long)((d.M + BM - 1) / BM) * ((d.N + BN - 1) / BN) * d.batch;
     int ks = 1;
-    // Split until the grid fills the CUs once, keeping >= 512 of K per split: fewer, longer
-    // splits keep the partial traffic (ksplit * M * N floats) small next to A and B.
-    while (tiles * ks * 2 <= (long long)num_cu && (long long)d.K / (ks * 2) >= 512) ks *= 2;
+    // Split until the grid holds TALOS_SPLITK_WG_PER_CU workgroups per CU, keeping at least
+    // TALOS_SPLITK_MIN_K of K per split: the partial traffic (ksplit * M * N floats) stays small
+    // next to A and B.
+    while (tiles * ks * 2 <= (long long)TALOS_SPLITK_WG_PER_CU * num_cu &&
+           (long long)d.K / (ks * 2) >= TALOS_SPLITK_MIN_K)
+      ks *= 2;
     d.ksplit = ks;
   }
-  if ((e & ~(E_BETA | E_BIAS)) != 0) d.ksplit = 1;  // only beta / bias survive a split
+  if ((e & ~(E_BETA | E_BIAS | E_DBIAS)) != 0) d.ksplit = 1;  // only beta / bias survive a split
   if (d.ksplit <= 1) return 0;
   GemmArgs a = to_args(d);
-  return (size_t)a.ksplit * d.M * d.N * d.batch * sizeof(float);
+  return (size_t)a.ksplit * (d.M + (d.dbias ? 1 : 0)) * d.N * d.batch * sizeof(float);
 }
 
 typedef void (*GemmKernel)(GemmArgs);
@@ -530,6 +593,9 @@ static GemmKernel pick_kernel(bool tA, bool tB, int e) {
   GEMM_CASE(true, false, 0)
   GEMM_CASE(true, false, E_BETA)
   GEMM_CASE(true, false, E_SPLIT)
+  GEMM_CASE(true, false, E_DBIAS)
+  GEMM_CASE(true, false, E_SPLIT | E_DBIAS)
+  GEMM_CASE(true, false, E_BETA | E_DBIAS)
   GEMM_CASE(true, true, 0)
   GEMM_CASE(true, true, E_BETA)
   GEMM_CASE(true, true, E_SPLIT)
@@ -550,7 +616,7 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
   }
   const int e = epi_flags(d);
   const bool split = a.ksplit > 1;
-  GemmKernel kern = pick_kernel(d.transA != 0, d.transB != 0, split ? E_SPLIT : e);
+  GemmKernel kern = pick_kernel(d.transA != 0, d.transB != 0, split ? (E_SPLIT | (e & E_DBIAS)) : e);
   if (kern == nullptr) {
     set_error("gemm: epilogue combination 0x%x is not instantiated for transA=%d transB=%d", e, d.transA, d.transB);
     return TALOS_ERR_UNSUPPORTED;
@@ -573,13 +639,14 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
     TALOS_LAUNCHED("gemm_f32_kernel");
   }
   if (split) {
-    const long long MN = (long long)d.M * d.N;
-    dim3 rg((unsigned)std::min<long long>((MN + 255) / 256, 4096), d.batch);
-    ProfScope ps(stream, "gemm_splitk_reduce", 0.0, 4.0 * (double)MN * d.batch * (a.ksplit + 1 + (d.beta != 0.f)));
-    if (e == 0) hipLaunchKernelGGL(gemm_splitk_reduce<0>, rg, dim3(256), 0, stream, a);
-    else if (e == E_BETA) hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA>, rg, dim3(256), 0, stream, a);
-    else if (e == E_BIAS) hipLaunchKernelGGL(gemm_splitk_reduce<E_BIAS>, rg, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA | E_BIAS>, rg, dim3(256), 0, stream, a);
+    const long long RN = (long long)(d.M + (d.dbias ? 1 : 0)) * d.N;
+    dim3 rg((unsigned)((RN + 63) / 64), d.batch);
+    ProfScope ps(stream, "gemm_splitk_reduce", 0.0, 4.0 * (double)RN * d.batch * (a.ksplit + 1 + (d.beta != 0.f)));
+    const int re = e & (E_BETA | E_BIAS);
+    if (re == 0) hipLaunchKernelGGL(gemm_splitk_reduce<0>, rg, dim3(1024), 0, stream, a);
+    else if (re == E_BETA) hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA>, rg, dim3(1024), 0, stream, a);
+    else if (re == E_BIAS) hipLaunchKernelGGL(gemm_splitk_reduce<E_BIAS>, rg, dim3(1024), 0, stream, a);
+    else hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA | E_BIAS>, rg, dim3(1024), 0, stream, a);
     TALOS_LAUNCHED("gemm_splitk_reduce");
   }
   return TALOS_OK;

@@ -40,7 +40,11 @@ struct GemmDesc {
   // Split-K: the K range is cut into ksplit parts of kper (multiple of 32) whose fp32 partial
   // tiles are summed in f64 by a second kernel. ksplit = 0 lets the library choose.
   int ksplit = 1;
-  float* workspace = nullptr;  // >= gemm_workspace_bytes(desc) when ksplit > 1
+  float* workspace = nullptr;  // >= gemm_plan_split(desc) bytes when ksplit > 1
+  // Fused bias gradient (transA = 1, transB = 0 only): dbias[n] = beta_dbias * dbias[n] +
+  // sum_k B[k][n], the column sums of op(B) accumulated from the panels already in LDS.
+  float* dbias = nullptr;
+  float beta_dbias = 0.f;
 };
 
 // Fills in ksplit (when 0) and returns the workspace bytes the descriptor needs.

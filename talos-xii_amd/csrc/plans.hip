@@ -180,6 +180,8 @@ static size_t wgrad_ws(talos_plan_s* p, int M_tok, int rows, int cols) {
   g.N = cols;
   g.K = M_tok;
   g.ksplit = 0;
+  float dummy = 0.f;
+  g.dbias = &dummy;  // sized with the fused bias-gradient row
   return gemm_plan_split(g, p->num_cu);
 }
 
@@ -247,7 +249,7 @@ static int alloc_workspaces(talos_plan_s* p) {
 // GEMM helpers ---------------------------------------------------------------
 static int mm(talos_plan_s* p, hipStream_t s, int tA, int tB, int M, int N, int K, const float* A, long long lda,
               const float* B, long long ldb, float* C, long long ldc, float beta = 0.f, const float* bias = nullptr,
-              const float* resid = nullptr, long long ldr = 0) {
+              const float* resid = nullptr, long long ldr = 0, float* dbias = nullptr) {
   GemmDesc g;
   g.transA = tA;
   g.transB = tB;
@@ -264,12 +266,12 @@ static int mm(talos_plan_s* p, hipStream_t s, int tA, int tB, int M, int N, int 
   g.bias = bias;
   g.resid = resid;
   g.ldr = ldr;
+  g.dbias = dbias;
   g.ksplit = 0;
   const size_t ws = gemm_plan_split(g, p->num_cu);
-  if (ws > p->gemm_ws_bytes) {
-    set_error("internal: split-K workspace %zu > planned %zu", ws, p->gemm_ws_bytes);
-    return TALOS_ERR_UNSUPPORTED;
-  }
+  // the plan sizes its split-K workspace for the weight-gradient products; any other product
+  // whose split would not fit runs unsplit
+  if (ws > p->gemm_ws_bytes) g.ksplit = 1;
   g.workspace = p->gemm_ws;
   return gemm_launch(g, s);
 }
@@ -350,9 +352,7 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
   const int M = c.batch * c.seq, d = c.d_model, F = c.ffn_dim;
   int rc;
   // out = h2 + a.W2 + b2
-  rc = mm(p, s, 1, 0, F, d, M, L.a, F, gout, d, G + o.w2, d);
-  if (rc) return rc;
-  rc = colsum_launch(M, d, gout, d, 0.f, G + o.b2, p->red_ws, s);
+  rc = mm(p, s, 1, 0, F, d, M, L.a, F, gout, d, G + o.w2, d, 0.f, nullptr, nullptr, 0, G + o.b2);
   if (rc) return rc;
   {
     GemmDesc g;
@@ -374,9 +374,7 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
     if (rc) return rc;
   }
   // u = xn2.W1 + b1
-  rc = mm(p, s, 1, 0, d, F, M, L.xn2, d, p->g_u, F, G + o.w1, F);
-  if (rc) return rc;
-  rc = colsum_launch(M, F, p->g_u, F, 0.f, G + o.b1, p->red_ws, s);
+  rc = mm(p, s, 1, 0, d, F, M, L.xn2, d, p->g_u, F, G + o.w1, F, 0.f, nullptr, nullptr, 0, G + o.b1);
   if (rc) return rc;
   rc = mm(p, s, 0, 1, M, d, F, p->g_u, F, P + o.w1, F, p->g_xn, d);
   if (rc) return rc;
@@ -703,22 +701,16 @@ int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* sta
   }
   float* G = dparams;
   // heads
-  rc = mm(p, s, 1, 0, d, A, B, p->pout, d, p->g_logits, A, G + po.wa, A);
+  rc = mm(p, s, 1, 0, d, A, B, p->pout, d, p->g_logits, A, G + po.wa, A, 0.f, nullptr, nullptr, 0, G + po.ba);
   if (rc) return rc;
-  rc = colsum_launch(B, A, p->g_logits, A, 0.f, G + po.ba, p->red_ws, s);
-  if (rc) return rc;
-  rc = mm(p, s, 1, 0, d, 1, B, p->pout, d, p->g_values, 1, G + po.wc, 1);
-  if (rc) return rc;
-  rc = colsum_launch(B, 1, p->g_values, 1, 0.f, G + po.bc, p->red_ws, s);
+  rc = mm(p, s, 1, 0, d, 1, B, p->pout, d, p->g_values, 1, G + po.wc, 1, 0.f, nullptr, nullptr, 0, G + po.bc);
   if (rc) return rc;
   rc = mm(p, s, 0, 1, B, d, A, p->g_logits, A, params + po.wa, A, p->g_pout, d);
   if (rc) return rc;
   rc = mm(p, s, 0, 1, B, d, 1, p->g_values, 1, params + po.wc, 1, p->g_pout, d, 1.f);
   if (rc) return rc;
   // out_proj
-  rc = mm(p, s, 1, 0, d, d, B, p->lastn, d, p->g_pout, d, G + po.wout, d);
-  if (rc) return rc;
-  rc = colsum_launch(B, d, p->g_pout, d, 0.f, G + po.bout, p->red_ws, s);
+  rc = mm(p, s, 1, 0, d, d, B, p->lastn, d, p->g_pout, d, G + po.wout, d, 0.f, nullptr, nullptr, 0, G + po.bout);
   if (rc) return rc;
   rc = mm(p, s, 0, 1, B, d, d, p->g_pout, d, params + po.wout, d, p->g_lastn, d);
   if (rc) return rc;
@@ -747,9 +739,7 @@ int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* sta
     std::swap(gcur, gnext);
   }
   // embed
-  rc = mm(p, s, 1, 0, c.in_dim, d, M, states, c.in_dim, gcur, d, G + po.we, d);
-  if (rc) return rc;
-  return colsum_launch(M, d, gcur, d, 0.f, G + po.be, p->red_ws, s);
+  return mm(p, s, 1, 0, c.in_dim, d, M, states, c.in_dim, gcur, d, G + po.we, d, 0.f, nullptr, nullptr, 0, G + po.be);
 }
 
 int talos_plan_profiler(talos_plan plan, talos_profiler* prof) {
