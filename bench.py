@@ -78,9 +78,10 @@ def traffic_of(kernel):
     if not os.path.exists(path):
         return None
     try:
-        return json.load(open(path)).get(kernel)
+        t = json.load(open(path)).get(kernel)
     except (OSError, ValueError):
         return None
+    return round(t["bytes"]) if t else None
 
 
 def cpu_baseline(cfg_t, seconds_budget=20.0):
@@ -130,6 +131,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--profile-table", action="store_true", help="print the per-kernel table to stderr")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="after the run, copy a buffer of this many MiB device-to-device 5 times: the known-size "
+                         "copy that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -224,6 +228,13 @@ def main():
     elif rank == 0:
         out["cpu_baseline"] = None
     plan.destroy()
+    if args.copy_calibration_mb > 0:
+        nbytes = args.copy_calibration_mb << 20
+        src, dst = th.DeviceArray.zeros(nbytes // 4), th.DeviceArray.zeros(nbytes // 4)
+        for _ in range(5):
+            th.call("talos_memcpy_d2d", dst.ptr, src.ptr, nbytes, None)
+        th.sync()
+        out["copy_calibration_bytes"] = nbytes
     if rank == 0:
         print(json.dumps(out))
 

@@ -78,6 +78,7 @@ struct GemmArgs {
   float* dbias;
   float beta_dbias;
   int vecA, vecB;
+  int nblocks;  // tiles * batch * ksplit (the grid is padded to a multiple of 8)
 };
 
 // Loads the op(A) panel [BM x BK] of chunk k0 into registers. CHECK = false: the whole panel
@@ -303,10 +304,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_W
   float* const Abase = smem;
   float* const Bbase = smem + NBUF * BK * LDS_S;
 
+  // XCD-aware order: the dispatcher sends workgroup i to XCD i % 8, so logical tiles are dealt
+  // out in contiguous runs per XCD; the N tiles of one M panel (and the tiles of one K split)
+  // then share that XCD's L2 instead of fetching the same operand panel once per XCD. The grid
+  // is padded to a multiple of 8; padding workgroups exit before any barrier.
   const int tiles_n = (p.N + BN - 1) / BN;
-  const int m0 = (blockIdx.x / tiles_n) * BM;
-  const int n0 = (blockIdx.x % tiles_n) * BN;
-  const int bz = blockIdx.y;
+  const int tiles = tiles_n * ((p.M + BM - 1) / BM);
+  const int per_xcd = (int)(gridDim.x >> 3);
+  const int logical = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  if (logical >= p.nblocks) return;
+  const int tile = logical % tiles;
+  const int m0 = (tile / tiles_n) * BM;
+  const int n0 = (tile % tiles_n) * BN;
+  const int bz = logical / tiles;
   const int b = bz / p.ksplit, split = bz % p.ksplit;
   const float* A = p.A + (long long)b * p.sA;
   const float* B = p.B + (long long)b * p.sB;
@@ -607,13 +617,13 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
   GemmArgs a = to_args(d);
   if (d.M == 0 || d.N == 0 || d.batch == 0) return TALOS_OK;
   const unsigned tiles = ceil_div(d.M, BM) * ceil_div(d.N, BN);
-  dim3 grid(tiles, d.batch * a.ksplit);
   if (d.K == 0) {
     // C = beta*C (+ epilogue): run the kernel with an empty K loop.
     a.ksplit = 1;
     a.kper = 0;
-    grid.y = d.batch;
   }
+  a.nblocks = (int)(tiles * (unsigned)d.batch * (unsigned)a.ksplit);
+  dim3 grid((unsigned)((a.nblocks + 7) / 8 * 8));
   const int e = epi_flags(d);
   const bool split = a.ksplit > 1;
   GemmKernel kern = pick_kernel(d.transA != 0, d.transB != 0, split ? (E_SPLIT | (e & E_DBIAS)) : e);
@@ -621,9 +631,10 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
     set_error("gemm: epilogue combination 0x%x is not instantiated for transA=%d transB=%d", e, d.transA, d.transB);
     return TALOS_ERR_UNSUPPORTED;
   }
-  static const char* names[4] = {"gemm_f32_kernel<false, false", "gemm_f32_kernel<false, true",
-                                 "gemm_f32_kernel<true, false", "gemm_f32_kernel<true, true"};
-  const int key = (d.transA ? 2 : 0) | (d.transB ? 1 : 0);
+  // profiler name = the kernel symbol's template arguments as rocprofv3 prints them
+  char name[64];
+  snprintf(name, sizeof(name), "gemm_f32_kernel<%s, %s, %d>", d.transA ? "true" : "false",
+           d.transB ? "true" : "false", split ? (E_SPLIT | (e & E_DBIAS)) : e);
   {
     // algorithmic work: 2MNK flops; A, B read once, C written once (+ C / residual / aux reads)
     const double MN = (double)d.M * d.N;
@@ -634,15 +645,17 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
       if (d.aux) bytes += 4.0 * MN;
       if (d.bias) bytes += 4.0 * d.N;
     }
-    ProfScope ps(stream, names[key], 2.0 * MN * d.K * d.batch, bytes * d.batch);
+    ProfScope ps(stream, name, 2.0 * MN * d.K * d.batch, bytes * d.batch);
     hipLaunchKernelGGL(kern, grid, dim3(NT), 0, stream, a);
     TALOS_LAUNCHED("gemm_f32_kernel");
   }
   if (split) {
     const long long RN = (long long)(d.M + (d.dbias ? 1 : 0)) * d.N;
     dim3 rg((unsigned)((RN + 63) / 64), d.batch);
-    ProfScope ps(stream, "gemm_splitk_reduce", 0.0, 4.0 * (double)RN * d.batch * (a.ksplit + 1 + (d.beta != 0.f)));
     const int re = e & (E_BETA | E_BIAS);
+    char rname[48];
+    snprintf(rname, sizeof(rname), "gemm_splitk_reduce<%d>", re);
+    ProfScope ps(stream, rname, 0.0, 4.0 * (double)RN * d.batch * (a.ksplit + 1 + (d.beta != 0.f)));
     if (re == 0) hipLaunchKernelGGL(gemm_splitk_reduce<0>, rg, dim3(1024), 0, stream, a);
     else if (re == E_BETA) hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA>, rg, dim3(1024), 0, stream, a);
     else if (re == E_BIAS) hipLaunchKernelGGL(gemm_splitk_reduce<E_BIAS>, rg, dim3(1024), 0, stream, a);
