@@ -235,6 +235,31 @@ typedef struct talos_ppo_cfg {
 
 size_t talos_ppo_param_count(const talos_ppo_cfg* cfg);
 
+/* MLA block (MultiHeadLatentAttention, transformer.rs:374-398, 428-560) with a pre-norm residual:
+ *   out = x + W_o . attn([q_c | rope(q_r)], [k_c | rope(k_r)], v),  xn = rmsnorm(x; g),
+ *   c_kv = xn . W_dkv, k_c = c_kv . W_uk, v = c_kv . W_uv, q_c = xn . W_q, q_r = xn . W_qr,
+ *   k_r = xn . W_kr, per-head concatenation of content and RoPE dims, scale 1/sqrt(head_dim +
+ *   rope_dim) (transformer.rs:542), RoPE position = sequence index. No biases (transformer.rs:441-460).
+ * Parameter layout: g[d] | W_dkv[d,L] | W_uk[L,H*hd] | W_uv[L,H*vd] | W_q[d,H*hd] | W_kr[d,H*r] |
+ *   W_qr[d,H*r] | W_o[H*vd,d]. */
+enum talos_precision { TALOS_PREC_FP32 = 0, TALOS_PREC_BF16 = 1 /* bf16-in / fp32-accumulate GEMMs */ };
+typedef struct talos_mla_cfg {
+  int batch;
+  int seq;
+  int d_model;
+  int n_heads;
+  int kv_latent;
+  int rope_dim;
+  int head_dim;  /* content dims of q / k per head */
+  int v_dim;
+  int causal;
+  int precision; /* talos_precision */
+  float eps;
+  float rope_base;
+} talos_mla_cfg;
+
+size_t talos_mla_param_count(const talos_mla_cfg* cfg);
+
 /* Opaque plans own device workspace sized for one configuration. */
 typedef struct talos_plan_s* talos_plan;
 
@@ -255,6 +280,12 @@ int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* sta
 /* Forward only: logits[batch, A] and values[batch] of the policy (for old log-probs). */
 int talos_ppo_forward_f32(talos_plan plan, const float* params, const float* states, float* logits,
                           float* values, talos_stream_t stream);
+
+/* MLA block forward + backward for loss = sum(out * gout): writes out[batch*seq, d], dparams
+ * (overwritten, same layout as params) and dx. */
+int talos_mla_plan_create(const talos_mla_cfg* cfg, talos_plan* plan);
+int talos_mla_fwd_bwd_f32(talos_plan plan, const float* params, const float* x, const float* gout, float* out,
+                          float* dparams, float* dx, talos_stream_t stream);
 
 int talos_plan_destroy(talos_plan plan);
 

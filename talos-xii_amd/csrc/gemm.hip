@@ -616,6 +616,10 @@ static GemmKernel pick_kernel(bool tA, bool tB, int e) {
 int gemm_launch(const GemmDesc& d, hipStream_t stream) {
   GemmArgs a = to_args(d);
   if (d.M == 0 || d.N == 0 || d.batch == 0) return TALOS_OK;
+  if (d.bf16) {
+    set_error("gemm: the bf16-in / fp32-accumulate variant is not built yet");
+    return TALOS_ERR_UNSUPPORTED;
+  }
   const unsigned tiles = ceil_div(d.M, BM) * ceil_div(d.N, BN);
   if (d.K == 0) {
     // C = beta*C (+ epilogue): run the kernel with an empty K loop.

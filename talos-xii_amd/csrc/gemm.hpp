@@ -45,6 +45,9 @@ struct GemmDesc {
   // sum_k B[k][n], the column sums of op(B) accumulated from the panels already in LDS.
   float* dbias = nullptr;
   float beta_dbias = 0.f;
+  // bf16-in / fp32-accumulate: operands are rounded to bf16 (nearest even) as they are staged
+  // into LDS and multiplied with v_mfma_f32_32x32x16_bf16; HBM layout and outputs stay fp32.
+  bool bf16 = false;
 };
 
 // Fills in ksplit (when 0) and returns the workspace bytes the descriptor needs.

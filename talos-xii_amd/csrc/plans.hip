@@ -54,7 +54,14 @@ struct talos_plan_s {
         *g_last = nullptr;
   double* loss_ws = nullptr;
   int num_cu = 256;
+  bool bf16 = false;  // bf16-in / fp32-accumulate GEMMs (MLA plans with TALOS_PREC_BF16)
   talos::Profiler* prof = nullptr;
+  // mla
+  talos_mla_cfg mla{};
+  struct MlaBufs {
+    float *xn, *rstd, *ckv, *kc, *v, *qc, *qr, *kr, *q, *k, *o, *lse;
+    float *g_o, *dq, *dk, *dv, *dqc, *dqr, *dkc, *dkr, *dckv, *dxn;
+  } mb{};
 };
 
 namespace talos {
@@ -267,6 +274,7 @@ static int mm(talos_plan_s* p, hipStream_t s, int tA, int tB, int M, int N, int 
   g.resid = resid;
   g.ldr = ldr;
   g.dbias = dbias;
+  g.bf16 = p->bf16;
   g.ksplit = 0;
   const size_t ws = gemm_plan_split(g, p->num_cu);
   // the plan sizes its split-K workspace for the weight-gradient products; any other product
@@ -555,6 +563,148 @@ static int ppo_forward(talos_plan_s* p, const float* P, const float* states, hip
   return mm(p, s, 0, 0, c.batch, 1, d, p->pout, d, P + po.wc, 1, p->values, 1, 0.f, P + po.bc);
 }
 
+
+// ---------------------------------------------------------------------------
+// MLA block (talos_mla_cfg): out = x + MLA(rmsnorm(x; g)), the graph of
+// MultiHeadLatentAttention::forward (src/transformer.rs:478-557) with the position of RoPE the
+// sequence index. Parameters: g[d] | W_dkv[d,L] | W_uk[L,H*hd] | W_uv[L,H*vd] | W_q[d,H*hd] |
+// W_kr[d,H*r] | W_qr[d,H*r] | W_o[H*vd,d].
+// ---------------------------------------------------------------------------
+struct MlaOff {
+  size_t g, wdkv, wuk, wuv, wq, wkr, wqr, wo, end;
+};
+static MlaOff mla_offsets(const talos_mla_cfg& c) {
+  const size_t d = c.d_model, H = c.n_heads, L = c.kv_latent, r = c.rope_dim, hd = c.head_dim, vd = c.v_dim;
+  MlaOff o;
+  o.g = 0;
+  o.wdkv = o.g + d;
+  o.wuk = o.wdkv + d * L;
+  o.wuv = o.wuk + L * H * hd;
+  o.wq = o.wuv + L * H * vd;
+  o.wkr = o.wq + d * H * hd;
+  o.wqr = o.wkr + d * H * r;
+  o.wo = o.wqr + d * H * r;
+  o.end = o.wo + H * vd * d;
+  return o;
+}
+
+static int check_mla_cfg(const talos_mla_cfg& c) {
+  TALOS_REQUIRE(c.batch > 0 && c.seq > 0 && c.d_model > 0 && c.n_heads > 0 && c.kv_latent > 0 && c.rope_dim > 0 &&
+                    c.head_dim > 0 && c.v_dim > 0,
+                TALOS_ERR_SHAPE, "mla cfg: sizes must be positive");
+  TALOS_REQUIRE(c.rope_dim % 2 == 0, TALOS_ERR_SHAPE, "mla cfg: rope_dim must be even");
+  TALOS_REQUIRE(c.head_dim + c.rope_dim <= 128 && c.v_dim <= 128, TALOS_ERR_UNSUPPORTED,
+                "mla cfg: head_dim + rope_dim and v_dim must be <= 128");
+  TALOS_REQUIRE(c.d_model % 4 == 0 && c.kv_latent % 4 == 0 && c.head_dim % 4 == 0 && c.rope_dim % 4 == 0 &&
+                    c.v_dim % 4 == 0,
+                TALOS_ERR_UNSUPPORTED, "mla cfg: all widths must be multiples of 4");
+  TALOS_REQUIRE(c.causal == 0 || c.causal == 1, TALOS_ERR_DTYPE, "mla cfg: causal must be 0 or 1");
+  TALOS_REQUIRE(c.precision == TALOS_PREC_FP32 || c.precision == TALOS_PREC_BF16, TALOS_ERR_DTYPE,
+                "mla cfg: unknown precision %d", c.precision);
+  TALOS_REQUIRE(c.eps >= 0.f && c.rope_base > 0.f, TALOS_ERR_SHAPE, "mla cfg: eps >= 0 and rope_base > 0 required");
+  TALOS_REQUIRE((long long)c.batch * c.seq * c.n_heads * (c.head_dim + c.rope_dim) < (1LL << 31),
+                TALOS_ERR_UNSUPPORTED, "mla cfg: too many elements for 32-bit indexing");
+  return TALOS_OK;
+}
+
+// Forward + backward of the MLA block for loss = sum(out * gout).
+static int mla_fwd_bwd(talos_plan_s* p, const float* P, const float* x, const float* gout, float* out, float* G,
+                       float* dx, hipStream_t s) {
+  const talos_mla_cfg& c = p->mla;
+  const MlaOff o = mla_offsets(c);
+  auto& b = p->mb;
+  const int M = c.batch * c.seq, d = c.d_model, H = c.n_heads, L = c.kv_latent, r = c.rope_dim, hd = c.head_dim,
+            vd = c.v_dim, td = hd + r;
+  const size_t MH = (size_t)M * H;
+  int rc;
+  auto rope_gemm = [&](const float* A, const float* W, float* C) {
+    GemmDesc g;
+    g.M = M;
+    g.N = H * r;
+    g.K = d;
+    g.A = A;
+    g.lda = d;
+    g.B = W;
+    g.ldb = H * r;
+    g.C = C;
+    g.ldc = H * r;
+    g.rope_cos = p->rcos;
+    g.rope_sin = p->rsin;
+    g.rope_cols = H * r;
+    g.rope_dim = r;
+    g.rope_seq = c.seq;
+    g.ksplit = 1;
+    g.bf16 = c.precision == TALOS_PREC_BF16;
+    return gemm_launch(g, s);
+  };
+  // ---- forward
+  rc = rmsnorm_fwd_launch(M, d, c.eps, x, P + o.g, b.xn, b.rstd, s);
+  if (rc) return rc;
+  if ((rc = mm(p, s, 0, 0, M, L, d, b.xn, d, P + o.wdkv, L, b.ckv, L))) return rc;
+  if ((rc = mm(p, s, 0, 0, M, H * hd, L, b.ckv, L, P + o.wuk, H * hd, b.kc, H * hd))) return rc;
+  if ((rc = mm(p, s, 0, 0, M, H * vd, L, b.ckv, L, P + o.wuv, H * vd, b.v, H * vd))) return rc;
+  if ((rc = mm(p, s, 0, 0, M, H * hd, d, b.xn, d, P + o.wq, H * hd, b.qc, H * hd))) return rc;
+  if ((rc = rope_gemm(b.xn, P + o.wqr, b.qr))) return rc;
+  if ((rc = rope_gemm(b.xn, P + o.wkr, b.kr))) return rc;
+  if ((rc = concat_launch(MH, hd, r, b.qc, b.qr, b.q, s))) return rc;
+  if ((rc = concat_launch(MH, hd, r, b.kc, b.kr, b.k, s))) return rc;
+  AttnDesc a;
+  a.batch = c.batch;
+  a.seq = c.seq;
+  a.heads = H;
+  a.dk = td;
+  a.dv = vd;
+  a.scale = (float)(1.0 / std::sqrt((double)td));  // src/transformer.rs:542
+  a.causal = c.causal;
+  a.q = b.q;
+  a.ldq = (long long)H * td;
+  a.k = b.k;
+  a.ldk = (long long)H * td;
+  a.v = b.v;
+  a.ldv = (long long)H * vd;
+  a.o = b.o;
+  a.ldo = (long long)H * vd;
+  a.lse = b.lse;
+  if ((rc = attn_fwd_launch(a, s))) return rc;
+  if ((rc = mm(p, s, 0, 0, M, d, H * vd, b.o, H * vd, P + o.wo, d, out, d, 0.f, nullptr, x, d))) return rc;
+  // ---- backward
+  if ((rc = mm(p, s, 1, 0, H * vd, d, M, b.o, H * vd, gout, d, G + o.wo, d))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, H * vd, d, gout, d, P + o.wo, d, b.g_o, H * vd))) return rc;
+  a.dout = b.g_o;
+  a.lddo = (long long)H * vd;
+  a.dq = b.dq;
+  a.lddq = (long long)H * td;
+  a.dk_out = b.dk;
+  a.lddk = (long long)H * td;
+  a.dv_out = b.dv;
+  a.lddv = (long long)H * vd;
+  a.rope_cos = p->rcos;
+  a.rope_sin = p->rsin;
+  a.rope_off = hd;  // the decoupled RoPE dims follow the content dims in each head
+  a.rope_dim = r;
+  if ((rc = attn_bwd_launch(a, p->attn_ws, s))) return rc;
+  if ((rc = split_launch(MH, hd, r, b.dq, b.dqc, b.dqr, false, s))) return rc;
+  if ((rc = split_launch(MH, hd, r, b.dk, b.dkc, b.dkr, false, s))) return rc;
+  // q / rope-k projections of xn
+  if ((rc = mm(p, s, 1, 0, d, H * hd, M, b.xn, d, b.dqc, H * hd, G + o.wq, H * hd))) return rc;
+  if ((rc = mm(p, s, 1, 0, d, H * r, M, b.xn, d, b.dqr, H * r, G + o.wqr, H * r))) return rc;
+  if ((rc = mm(p, s, 1, 0, d, H * r, M, b.xn, d, b.dkr, H * r, G + o.wkr, H * r))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, d, H * hd, b.dqc, H * hd, P + o.wq, H * hd, b.dxn, d))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, d, H * r, b.dqr, H * r, P + o.wqr, H * r, b.dxn, d, 1.f))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, d, H * r, b.dkr, H * r, P + o.wkr, H * r, b.dxn, d, 1.f))) return rc;
+  // up projections of the latent
+  if ((rc = mm(p, s, 1, 0, L, H * hd, M, b.ckv, L, b.dkc, H * hd, G + o.wuk, H * hd))) return rc;
+  if ((rc = mm(p, s, 1, 0, L, H * vd, M, b.ckv, L, b.dv, H * vd, G + o.wuv, H * vd))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, L, H * hd, b.dkc, H * hd, P + o.wuk, H * hd, b.dckv, L))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, L, H * vd, b.dv, H * vd, P + o.wuv, H * vd, b.dckv, L, 1.f))) return rc;
+  // down projection
+  if ((rc = mm(p, s, 1, 0, d, L, M, b.xn, d, b.dckv, L, G + o.wdkv, L))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, d, L, b.dckv, L, P + o.wdkv, L, b.dxn, d, 1.f))) return rc;
+  // residual + rmsnorm
+  TALOS_HIP(hipMemcpyAsync(dx, gout, (size_t)M * d * 4, hipMemcpyDeviceToDevice, s));
+  return rmsnorm_bwd_launch(M, d, x, P + o.g, b.rstd, b.dxn, 1.f, dx, 0.f, G + o.g, p->red_ws, s);
+}
+
 }  // namespace talos
 
 using namespace talos;
@@ -740,6 +890,90 @@ int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* sta
   }
   // embed
   return mm(p, s, 1, 0, c.in_dim, d, M, states, c.in_dim, gcur, d, G + po.we, d, 0.f, nullptr, nullptr, 0, G + po.be);
+}
+
+size_t talos_mla_param_count(const talos_mla_cfg* cfg) { return cfg ? mla_offsets(*cfg).end : 0; }
+
+int talos_mla_plan_create(const talos_mla_cfg* cfg, talos_plan* plan) {
+  TALOS_NONNULL(cfg);
+  TALOS_NONNULL(plan);
+  *plan = nullptr;
+  int rc = check_mla_cfg(*cfg);
+  if (rc) return rc;
+  TALOS_DEVICE();
+  auto* p = new talos_plan_s();
+  p->kind = 3;
+  p->prof = profiler_new();
+  p->mla = *cfg;
+  p->bf16 = cfg->precision == TALOS_PREC_BF16;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, 0) == hipSuccess) p->num_cu = prop.multiProcessorCount;
+  const talos_mla_cfg& c = *cfg;
+  const size_t M = (size_t)c.batch * c.seq, d = c.d_model, H = c.n_heads, L = c.kv_latent, r = c.rope_dim,
+               hd = c.head_dim, vd = c.v_dim, td = hd + r;
+  auto& b = p->mb;
+  rc = 0;
+  rc |= plan_alloc(p, &b.xn, M * d);
+  rc |= plan_alloc(p, &b.rstd, M);
+  rc |= plan_alloc(p, &b.ckv, M * L);
+  rc |= plan_alloc(p, &b.kc, M * H * hd);
+  rc |= plan_alloc(p, &b.v, M * H * vd);
+  rc |= plan_alloc(p, &b.qc, M * H * hd);
+  rc |= plan_alloc(p, &b.qr, M * H * r);
+  rc |= plan_alloc(p, &b.kr, M * H * r);
+  rc |= plan_alloc(p, &b.q, M * H * td);
+  rc |= plan_alloc(p, &b.k, M * H * td);
+  rc |= plan_alloc(p, &b.o, M * H * vd);
+  rc |= plan_alloc(p, &b.lse, M * H);
+  rc |= plan_alloc(p, &b.g_o, M * H * vd);
+  rc |= plan_alloc(p, &b.dq, M * H * td);
+  rc |= plan_alloc(p, &b.dk, M * H * td);
+  rc |= plan_alloc(p, &b.dv, M * H * vd);
+  rc |= plan_alloc(p, &b.dqc, M * H * hd);
+  rc |= plan_alloc(p, &b.dqr, M * H * r);
+  rc |= plan_alloc(p, &b.dkc, M * H * hd);
+  rc |= plan_alloc(p, &b.dkr, M * H * r);
+  rc |= plan_alloc(p, &b.dckv, M * L);
+  rc |= plan_alloc(p, &b.dxn, M * d);
+  rc |= plan_alloc(p, &p->attn_ws, M * H);
+  std::vector<float> cs, sn;
+  rope_table_host(c.seq, c.rope_dim, (double)c.rope_base, cs, sn);
+  rc |= plan_alloc(p, &p->rcos, cs.size());
+  rc |= plan_alloc(p, &p->rsin, sn.size());
+  if (rc == TALOS_OK) {
+    rc = hip_status(hipMemcpy(p->rcos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    if (rc == TALOS_OK) rc = hip_status(hipMemcpy(p->rsin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
+  }
+  if (rc == TALOS_OK) {
+    const int Mi = (int)M;
+    for (auto rc2 : {std::make_pair((int)d, (int)(H * hd)), std::make_pair((int)d, (int)(H * r)),
+                     std::make_pair((int)L, (int)(H * hd)), std::make_pair((int)L, (int)(H * vd)),
+                     std::make_pair((int)d, (int)L), std::make_pair((int)(H * vd), (int)d)})
+      p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, wgrad_ws(p, Mi, rc2.first, rc2.second));
+    p->red_ws_bytes = std::max(p->red_ws_bytes, rmsnorm_bwd_workspace_bytes(Mi, (int)d));
+    rc = alloc_workspaces(p);
+  }
+  if (rc) {
+    plan_free(p);
+    delete p;
+    return rc;
+  }
+  *plan = p;
+  return TALOS_OK;
+}
+
+int talos_mla_fwd_bwd_f32(talos_plan plan, const float* params, const float* x, const float* gout, float* out,
+                          float* dparams, float* dx, talos_stream_t stream) {
+  TALOS_REQUIRE(plan != nullptr && plan->kind == 3, TALOS_ERR_HANDLE, "%s: not an mla plan", __func__);
+  TALOS_NONNULL(params);
+  TALOS_NONNULL(x);
+  TALOS_NONNULL(gout);
+  TALOS_NONNULL(out);
+  TALOS_NONNULL(dparams);
+  TALOS_NONNULL(dx);
+  TALOS_DEVICE();
+  PlanCall pc(plan);
+  return mla_fwd_bwd(plan, params, x, gout, out, dparams, dx, as_stream(stream));
 }
 
 int talos_plan_profiler(talos_plan plan, talos_profiler* prof) {

@@ -614,15 +614,32 @@ __global__ void concat_kernel(size_t rows, int ca, int cb, const float* __restri
   }
 }
 __global__ void concat_bwd_kernel(size_t rows, int ca, int cb, const float* __restrict__ g, float* __restrict__ da,
-                                  float* __restrict__ db) {
+                                  float* __restrict__ db, int accumulate) {
   const int w = ca + cb;
   const size_t n = rows * w;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
     const size_t r = i / w;
     const int c = (int)(i % w);
-    if (c < ca) da[r * ca + c] += g[i];
-    else db[r * cb + (c - ca)] += g[i];
+    float* dst = c < ca ? &da[r * ca + c] : &db[r * cb + (c - ca)];
+    *dst = accumulate ? *dst + g[i] : g[i];
   }
+}
+
+int concat_launch(size_t rows, int ca, int cb, const float* a, const float* b, float* out, hipStream_t s) {
+  if (rows == 0 || ca + cb == 0) return TALOS_OK;
+  ProfScope ps(s, "concat_kernel", 0.0, 8.0 * rows * (ca + cb));
+  hipLaunchKernelGGL(concat_kernel, dim3(grid_for(rows * (ca + cb))), dim3(256), 0, s, rows, ca, cb, a, b, out);
+  TALOS_LAUNCHED("concat_kernel");
+  return TALOS_OK;
+}
+
+int split_launch(size_t rows, int ca, int cb, const float* g, float* da, float* db, bool accumulate, hipStream_t s) {
+  if (rows == 0 || ca + cb == 0) return TALOS_OK;
+  ProfScope ps(s, "concat_bwd_kernel", 0.0, (accumulate ? 12.0 : 8.0) * rows * (ca + cb));
+  hipLaunchKernelGGL(concat_bwd_kernel, dim3(grid_for(rows * (ca + cb))), dim3(256), 0, s, rows, ca, cb, g, da, db,
+                     accumulate ? 1 : 0);
+  TALOS_LAUNCHED("concat_bwd_kernel");
+  return TALOS_OK;
 }
 __global__ void broadcast_rows_kernel(size_t rows, int cols, const float* __restrict__ v, float* __restrict__ out) {
   const size_t n = rows * cols;
@@ -901,11 +918,8 @@ int talos_concat_last_bwd_f32(size_t rows, int ca, int cb, const float* dout, fl
   TALOS_NONNULL(db);
   TALOS_REQUIRE(ca >= 0 && cb >= 0, TALOS_ERR_SHAPE, "%s: negative width", __func__);
   TALOS_DEVICE();
-  if (rows == 0 || ca + cb == 0) return TALOS_OK;
-  hipLaunchKernelGGL(concat_bwd_kernel, dim3(grid_for(rows * (ca + cb))), dim3(256), 0, as_stream(stream), rows, ca, cb,
-                     dout, da, db);
-  TALOS_LAUNCHED("concat_bwd_kernel");
-  return TALOS_OK;
+  // the reference's closure accumulates into both parents (src/transformer.rs:1162-1179)
+  return split_launch(rows, ca, cb, dout, da, db, true, as_stream(stream));
 }
 
 int talos_broadcast_rows_f32(size_t rows, int cols, const float* v, float* out, talos_stream_t stream) {

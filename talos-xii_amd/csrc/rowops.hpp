@@ -20,6 +20,10 @@ int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float
 int rmsnorm_bwd_launch(int rows, int dim, const float* x, const float* w, const float* rstd, const float* dy,
                        float beta_dx, float* dx, float beta_dw, float* dw, double* ws, hipStream_t s);
 
+// out[r] = [a[r] | b[r]]; split: da[r] (+)= g[r][:ca], db[r] (+)= g[r][ca:]
+int concat_launch(size_t rows, int ca, int cb, const float* a, const float* b, float* out, hipStream_t s);
+int split_launch(size_t rows, int ca, int cb, const float* g, float* da, float* db, bool accumulate, hipStream_t s);
+
 void rope_table_host(int max_len, int dim, double base, std::vector<float>& c, std::vector<float>& s);
 int rope_table_device(int need_len, int dim, float base, const float** cosv, const float** sinv);
 int rope_launch(int n_seq, int seq, int heads, int dim, int start_pos, const float* cosv, const float* sinv,

@@ -44,6 +44,13 @@ class PpoCfg(ctypes.Structure):
                 ("eps", _f), ("rope_base", _f), ("clip_eps", _f), ("value_coef", _f), ("entropy_coef", _f)]
 
 
+class MlaCfg(ctypes.Structure):
+    _fields_ = [("batch", _i), ("seq", _i), ("d_model", _i), ("n_heads", _i), ("kv_latent", _i), ("rope_dim", _i),
+                ("head_dim", _i), ("v_dim", _i), ("causal", _i), ("precision", _i), ("eps", _f), ("rope_base", _f)]
+
+
+PREC_FP32, PREC_BF16 = 0, 1
+
 # name -> argtypes (restype int unless listed in _RESTYPE)
 _SIGS = {
     "talos_last_error": [],
@@ -96,6 +103,9 @@ _SIGS = {
     "talos_ppo_plan_create": [ctypes.POINTER(PpoCfg), ctypes.POINTER(_vp)],
     "talos_ppo_fwd_bwd_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "talos_ppo_forward_f32": [_vp, _vp, _vp, _vp, _vp, _vp],
+    "talos_mla_param_count": [ctypes.POINTER(MlaCfg)],
+    "talos_mla_plan_create": [ctypes.POINTER(MlaCfg), ctypes.POINTER(_vp)],
+    "talos_mla_fwd_bwd_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "talos_plan_destroy": [_vp],
     "talos_plan_profiler": [_vp, ctypes.POINTER(_vp)],
     "talos_profiler_enable": [_vp, _i, ctypes.c_char_p],
@@ -107,7 +117,7 @@ class ProfRecord(ctypes.Structure):
     _fields_ = [("kernel", ctypes.c_char * 64), ("flops", ctypes.c_double), ("bytes", ctypes.c_double),
                 ("ms", ctypes.c_float)]
 _RESTYPE = {"talos_last_error": ctypes.c_char_p, "talos_version": ctypes.c_char_p,
-            "talos_block_param_count": _sz, "talos_ppo_param_count": _sz}
+            "talos_block_param_count": _sz, "talos_ppo_param_count": _sz, "talos_mla_param_count": _sz}
 
 _lib = None
 
@@ -220,6 +230,9 @@ class Plan:
         if kind == "block":
             call("talos_block_plan_create", ctypes.byref(cfg), ctypes.byref(h))
             self.n_params = lib().talos_block_param_count(ctypes.byref(cfg))
+        elif kind == "mla":
+            call("talos_mla_plan_create", ctypes.byref(cfg), ctypes.byref(h))
+            self.n_params = lib().talos_mla_param_count(ctypes.byref(cfg))
         else:
             call("talos_ppo_plan_create", ctypes.byref(cfg), ctypes.byref(h))
             self.n_params = lib().talos_ppo_param_count(ctypes.byref(cfg))

@@ -120,3 +120,46 @@ def test_ppo_bad_action_is_nan_not_a_fault(oracle):
     z = np.zeros(4, np.float32)
     loss, dp, _, _ = run_ppo(cfg, p, states, actions, z, z, z)
     assert np.isnan(loss)
+
+
+MLA_NAMES = ["g", "W_dkv", "W_uk", "W_uv", "W_q", "W_kr", "W_qr", "W_o"]
+
+
+def mla_slices(ci):
+    B, S, d, H, L, r, hd, vd = ci[:8]
+    sizes = [d, d * L, L * H * hd, L * H * vd, d * H * hd, d * H * r, d * H * r, H * vd * d]
+    out, o = {}, 0
+    for n, s in zip(MLA_NAMES, sizes):
+        out[n] = slice(o, o + s)
+        o += s
+    return out
+
+
+def run_mla(ci, prec, p, x, G, eps=1e-5, base=10000.0):
+    B, S, d, H, L, r, hd, vd, causal = ci[:9]
+    cfg = th.MlaCfg(B, S, d, H, L, r, hd, vd, causal, prec, eps, base)
+    plan = th.Plan("mla", cfg)
+    assert plan.n_params == p.size
+    P, X, Gd = DA.from_numpy(p), DA.from_numpy(x), DA.from_numpy(G)
+    out, dp, dx = DA.zeros(x.shape), DA.zeros(p.size), DA.zeros(x.shape)
+    th.call("talos_mla_fwd_bwd_f32", plan.h, P.ptr, X.ptr, Gd.ptr, out.ptr, dp.ptr, dx.ptr, None)
+    res = out.numpy(), dp.numpy(), dx.numpy()
+    plan.destroy()
+    return res
+
+
+@pytest.mark.parametrize("ci", [[2, 5, 16, 2, 8, 4, 8, 8, 0, 0], [2, 37, 64, 2, 32, 8, 16, 16, 1, 0],
+                                [2, 64, 512, 8, 128, 32, 64, 64, 0, 0]])
+def test_mla_fwd_bwd_vs_oracle(oracle, ci):
+    # the last case is C5's block (d512, 8 heads, latent 128, rope 32, head 64, v 64) at batch 2
+    from common import mla_params
+    rng = np.random.default_rng(3000 + ci[1] + ci[2])
+    B, S, d = ci[:3]
+    p = f32(mla_params(rng, ci))
+    x, G = f32(rng.normal(size=(B, S, d))), f32(rng.normal(size=(B, S, d)))
+    out_r, dp_r, dx_r = oracle.mla_fwd_bwd(ci, 1e-5, 10000.0, p, x, G)
+    out, dp, dx = run_mla(ci, th.PREC_FP32, p, x, G)
+    check_close(out, out_r, name="out")
+    check_close(dx, dx_r, name="dx")
+    for n, sl in mla_slices(ci).items():
+        check_close(dp[sl], dp_r[sl], name=f"d{n}", scale_floor=GRAD_SCALE_FLOOR)
