@@ -88,6 +88,13 @@ int talos_device_info(char* name, size_t name_len, int* cu_count, int* clock_khz
 int talos_gemm_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
                    const float* B, int ldb, float beta, float* C, int ldc, talos_stream_t stream);
 
+/* Same contract, bf16-in / fp32-accumulate: A and B stay fp32 in memory and are rounded to bf16
+ * (nearest even) as they are staged into LDS; products use v_mfma_f32_32x32x16_bf16 with fp32
+ * accumulation and an fp32 C. No reference counterpart (the reference is f64 only,
+ * autograd.rs:16-17): this is the optional bf16 variant of talos_gemm_f32. */
+int talos_gemm_bf16acc_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
+                           const float* B, int ldb, float beta, float* C, int ldc, talos_stream_t stream);
+
 /* Batched C_b = alpha * A_b . op(B_b) + beta * C_b for b in [0,batch) with element strides
  * sA, sB, sC between consecutive matrices (same trans conventions as talos_gemm_f32).
  * Replaces batched_matmul_qt_k (transformer.rs:877-958: S = Q.K^T is transB = 1) and

@@ -296,7 +296,96 @@ constexpr int T_S = 136;  // pitch of the staged output tile: rows h*4 apart lan
 constexpr int T_ROWS = BM / 2;  // the tile is staged in two halves of 64 rows
 constexpr int SMEM_FLOATS = (2 * NBUF * BK * LDS_S > T_ROWS * T_S) ? 2 * NBUF * BK * LDS_S : T_ROWS * T_S;
 
-template <bool TA, bool TB, int E>
+// ---------------------------------------------------------------------------
+// bf16-in / fp32-accumulate operand staging: panels of BKB = 64 k values are rounded to bf16 and
+// stored k-contiguous (rows of PB bf16, 144 bytes: the 16-byte fragments of 8 consecutive rows
+// fall on distinct banks), so one ds_read_b128 gives a lane the 8 k values of an MFMA step.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+constexpr int BKB = 64;
+constexpr int PB = BKB + 8;
+
+// round-to-nearest-even fp32 -> bf16 of two values, packed low | high
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  auto r = [](float f) -> uint32_t {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // NaN stays a quiet NaN
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  };
+  return r(lo) | (r(hi) << 16);
+}
+
+// Loads the [rows r0.., k0..k0+64) panel of an operand X and packs it to bf16 pairs.
+// KC = true: X[r][k] with k contiguous; thread t takes k = 4*(t%16) of rows t/16 + 16i.
+// KC = false: X[k][r] with r contiguous; thread t takes r = 4*(t%32), k pairs 2*(t/32) + 16i.
+template <bool KC>
+__device__ __forceinline__ void load_bf(const float* __restrict__ X, long long ld, int r0, int rlim, int k0, int kend,
+                                        bool fast, bool vec, uint32_t (&o)[16]) {
+  const int t = threadIdx.x;
+  if (KC) {
+    const int k = k0 + 4 * (t & 15);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = r0 + (t >> 4) + 16 * i;
+      const float* src = X + (long long)r * ld + k;
+      float v[4];
+      if (fast || (vec && r < rlim && k + 3 < kend)) {
+        const float4 f = *reinterpret_cast<const float4*>(src);
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (r < rlim && k + j < kend) ? src[j] : 0.f;
+      }
+      o[2 * i] = pack_bf16(v[0], v[1]);
+      o[2 * i + 1] = pack_bf16(v[2], v[3]);
+    }
+  } else {
+    const int r = r0 + 4 * (t & 31);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = k0 + 2 * (t >> 5) + 16 * i;
+      float v0[4], v1[4];
+      const float* s0 = X + (long long)k * ld + r;
+      const float* s1 = s0 + ld;
+      if (fast || (vec && k + 1 < kend && r + 3 < rlim)) {
+        const float4 f0 = *reinterpret_cast<const float4*>(s0);
+        const float4 f1 = *reinterpret_cast<const float4*>(s1);
+        v0[0] = f0.x; v0[1] = f0.y; v0[2] = f0.z; v0[3] = f0.w;
+        v1[0] = f1.x; v1[1] = f1.y; v1[2] = f1.z; v1[3] = f1.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v0[j] = (k < kend && r + j < rlim) ? s0[j] : 0.f;
+          v1[j] = (k + 1 < kend && r + j < rlim) ? s1[j] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[4 * i + j] = pack_bf16(v0[j], v1[j]);
+    }
+  }
+}
+
+template <bool KC>
+__device__ __forceinline__ void store_bf(uint16_t* S, const uint32_t (&o)[16]) {
+  const int t = threadIdx.x;
+  if (KC) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = (t >> 4) + 16 * i;
+      *reinterpret_cast<uint2*>(S + r * PB + 4 * (t & 15)) = make_uint2(o[2 * i], o[2 * i + 1]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * (t & 31) + j, k = 2 * (t >> 5) + 16 * i;
+        *reinterpret_cast<uint32_t*>(S + r * PB + k) = o[4 * i + j];
+      }
+  }
+}
+
+template <bool TA, bool TB, int E, bool BF>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_WAVES))) void gemm_f32_kernel(
     GemmArgs p) {
   __shared__ __align__(16) float smem[SMEM_FLOATS];
@@ -337,6 +426,47 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_W
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   float csum = 0.f;  // E_DBIAS: this thread's column sum over its half of each panel
+  if constexpr (BF) {
+    static_assert((E & E_DBIAS) == 0, "the bf16 path has no fused bias gradient");
+    uint16_t* As16 = reinterpret_cast<uint16_t*>(smem);
+    uint16_t* Bs16 = As16 + BM * PB;
+    uint32_t pa[16], pb[16];
+    auto load = [&](int k0) {
+      const bool fast = interior && k0 + BKB <= kend;
+      load_bf<!TA>(A, p.lda, m0, p.M, k0, kend, fast, p.vecA, pa);
+      load_bf<TB>(B, p.ldb, n0, p.N, k0, kend, fast, p.vecB, pb);
+    };
+    if (kbeg < kend) {
+      load(kbeg);
+      store_bf<!TA>(As16, pa);
+      store_bf<TB>(Bs16, pb);
+    }
+    __syncthreads();
+    for (int k0 = kbeg; k0 < kend; k0 += BKB) {
+      const bool more = k0 + BKB < kend;
+      if (more) load(k0 + BKB);
+      const uint16_t* ap = As16 + (wm * 64 + l32) * PB + 8 * h;
+      const uint16_t* bp = Bs16 + (wn * 64 + l32) * PB + 8 * h;
+#pragma unroll
+      for (int s = 0; s < BKB / 16; ++s) {
+        const bf16x8 a0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(ap + 16 * s));
+        const bf16x8 a1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(ap + 32 * PB + 16 * s));
+        const bf16x8 b0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(bp + 16 * s));
+        const bf16x8 b1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(bp + 32 * PB + 16 * s));
+        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[1][1], 0, 0, 0);
+      }
+      __syncthreads();
+      if (more) {
+        store_bf<!TA>(As16, pa);
+        store_bf<TB>(Bs16, pb);
+        __syncthreads();
+      }
+    }
+    if (kbeg >= kend) __syncthreads();
+  } else {
   float4 ra[4], rb[4];
   if (kbeg < kend) {
     load_chunk<TA, TB>(p, A, B, m0, n0, kbeg, kend, interior, ra, rb);
@@ -385,6 +515,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_W
     }
   }
   if (NBUF == 2 || kbeg >= kend) __syncthreads();
+  }  // fp32 main loop
   if constexpr ((E & E_DBIAS) != 0) {
     // combine the two row halves; the M-tile-0 workgroups write the bias-gradient row
     if (m0 == 0) {
@@ -539,8 +670,9 @@ static GemmArgs to_args(const GemmDesc& d) {
   a.vecA = aligned(d.A, d.lda) && (d.batch == 1 || d.sA % 4 == 0);
   a.vecB = aligned(d.B, d.ldb) && (d.batch == 1 || d.sB % 4 == 0);
   if (a.ksplit > 1) {
+    const int chunk = d.bf16 ? BKB : BK;
     int kper = (d.K + a.ksplit - 1) / a.ksplit;
-    kper = (kper + BK - 1) / BK * BK;
+    kper = (kper + chunk - 1) / chunk * chunk;
     a.kper = kper;
     a.ksplit = (d.K + kper - 1) / kper;
   }
@@ -582,10 +714,14 @@ size_t gemm_plan_split(GemmDesc& d, int num_cu) {
 
 typedef void (*GemmKernel)(GemmArgs);
 
-// Instantiated (transA, transB, epilogue) combinations.
-#define GEMM_CASE(TA, TB, E)                                           \
-  if (tA == TA && tB == TB && e == (E)) return &gemm_f32_kernel<TA, TB, (E)>;
-static GemmKernel pick_kernel(bool tA, bool tB, int e) {
+// Instantiated (transA, transB, epilogue) combinations; bf16 covers the same set minus the fused
+// bias gradient.
+#define GEMM_CASE(TA, TB, E)                                                                     \
+  if (tA == TA && tB == TB && e == (E)) return bf ? &gemm_f32_kernel<TA, TB, (E), true>          \
+                                                  : &gemm_f32_kernel<TA, TB, (E), false>;
+#define GEMM_CASE_F32(TA, TB, E) \
+  if (!bf && tA == TA && tB == TB && e == (E)) return &gemm_f32_kernel<TA, TB, (E), false>;
+static GemmKernel pick_kernel(bool tA, bool tB, int e, bool bf) {
   GEMM_CASE(false, false, 0)
   GEMM_CASE(false, false, E_BETA)
   GEMM_CASE(false, false, E_BIAS)
@@ -603,23 +739,20 @@ static GemmKernel pick_kernel(bool tA, bool tB, int e) {
   GEMM_CASE(true, false, 0)
   GEMM_CASE(true, false, E_BETA)
   GEMM_CASE(true, false, E_SPLIT)
-  GEMM_CASE(true, false, E_DBIAS)
-  GEMM_CASE(true, false, E_SPLIT | E_DBIAS)
-  GEMM_CASE(true, false, E_BETA | E_DBIAS)
+  GEMM_CASE_F32(true, false, E_DBIAS)
+  GEMM_CASE_F32(true, false, E_SPLIT | E_DBIAS)
+  GEMM_CASE_F32(true, false, E_BETA | E_DBIAS)
   GEMM_CASE(true, true, 0)
   GEMM_CASE(true, true, E_BETA)
   GEMM_CASE(true, true, E_SPLIT)
   return nullptr;
 }
 #undef GEMM_CASE
+#undef GEMM_CASE_F32
 
 int gemm_launch(const GemmDesc& d, hipStream_t stream) {
   GemmArgs a = to_args(d);
   if (d.M == 0 || d.N == 0 || d.batch == 0) return TALOS_OK;
-  if (d.bf16) {
-    set_error("gemm: the bf16-in / fp32-accumulate variant is not built yet");
-    return TALOS_ERR_UNSUPPORTED;
-  }
   const unsigned tiles = ceil_div(d.M, BM) * ceil_div(d.N, BN);
   if (d.K == 0) {
     // C = beta*C (+ epilogue): run the kernel with an empty K loop.
@@ -630,15 +763,16 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
   dim3 grid((unsigned)((a.nblocks + 7) / 8 * 8));
   const int e = epi_flags(d);
   const bool split = a.ksplit > 1;
-  GemmKernel kern = pick_kernel(d.transA != 0, d.transB != 0, split ? (E_SPLIT | (e & E_DBIAS)) : e);
+  GemmKernel kern = pick_kernel(d.transA != 0, d.transB != 0, split ? (E_SPLIT | (e & E_DBIAS)) : e, d.bf16);
   if (kern == nullptr) {
-    set_error("gemm: epilogue combination 0x%x is not instantiated for transA=%d transB=%d", e, d.transA, d.transB);
+    set_error("gemm: epilogue combination 0x%x is not instantiated for transA=%d transB=%d%s", e, d.transA, d.transB,
+              d.bf16 ? " (bf16)" : "");
     return TALOS_ERR_UNSUPPORTED;
   }
   // profiler name = the kernel symbol's template arguments as rocprofv3 prints them
   char name[64];
-  snprintf(name, sizeof(name), "gemm_f32_kernel<%s, %s, %d>", d.transA ? "true" : "false",
-           d.transB ? "true" : "false", split ? (E_SPLIT | (e & E_DBIAS)) : e);
+  snprintf(name, sizeof(name), "gemm_f32_kernel<%s, %s, %d, %s>", d.transA ? "true" : "false",
+           d.transB ? "true" : "false", split ? (E_SPLIT | (e & E_DBIAS)) : e, d.bf16 ? "true" : "false");
   {
     // algorithmic work: 2MNK flops; A, B read once, C written once (+ C / residual / aux reads)
     const double MN = (double)d.M * d.N;
@@ -733,6 +867,30 @@ int talos_gemm_f32(int transA, int transB, int M, int N, int K, float alpha, con
   d.ldc = ldc;
   d.alpha = alpha;
   d.beta = beta;
+  d.ksplit = 0;
+  return run_gemm(d, as_stream(stream));
+}
+
+int talos_gemm_bf16acc_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
+                           const float* B, int ldb, float beta, float* C, int ldc, talos_stream_t stream) {
+  int rc = check_gemm(__func__, transA, transB, M, N, K, A, lda, B, ldb, beta, C, ldc, 1);
+  if (rc) return rc;
+  TALOS_DEVICE();
+  GemmDesc d;
+  d.transA = transA;
+  d.transB = transB;
+  d.M = M;
+  d.N = N;
+  d.K = K;
+  d.A = A;
+  d.lda = lda;
+  d.B = B;
+  d.ldb = ldb;
+  d.C = C;
+  d.ldc = ldc;
+  d.alpha = alpha;
+  d.beta = beta;
+  d.bf16 = true;
   d.ksplit = 0;
   return run_gemm(d, as_stream(stream));
 }

@@ -74,7 +74,8 @@ _SIGS = {
     "talos_event_elapsed_ms": [_vp, _vp, ctypes.POINTER(_f)],
     "talos_device_info": [ctypes.c_char_p, _sz, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_sz)],
     "talos_gemm_f32": [_i, _i, _i, _i, _i, _f, _vp, _i, _vp, _i, _f, _vp, _i, _vp],
-    "talos_gemm_batched_f32": [_i, _i, _i, _i, _i, _f, _vp, _i, _ll, _vp, _i, _ll, _f, _vp, _i, _ll, _i, _vp],
+    "talos_gemm_bf16acc_f32": [_i, _i, _i, _i, _i, _f, _vp, _i, _vp, _i, _f, _vp, _i, _vp],
+    "talos_gemm_batched_f32":[_i, _i, _i, _i, _i, _f, _vp, _i, _ll, _vp, _i, _ll, _f, _vp, _i, _ll, _i, _vp],
     "talos_bias_grad_f32": [_i, _i, _vp, _f, _vp, _vp],
     "talos_rmsnorm_fwd_f32": [_i, _i, _f, _vp, _vp, _vp, _vp, _vp],
     "talos_rmsnorm_bwd_f32": [_i, _i, _vp, _vp, _vp, _vp, _f, _vp, _f, _vp, _vp],

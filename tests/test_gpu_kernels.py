@@ -342,3 +342,41 @@ def test_empty_inputs_are_noops():
     assert np.array_equal(C.numpy(), np.full((2, 4), 3.0, np.float32))
     th.call("talos_gemm_f32", 0, 0, 2, 4, 0, 1.0, p.ptr, 1, p.ptr, 4, 0.0, C.ptr, 4, None)
     assert np.array_equal(C.numpy(), np.zeros((2, 4), np.float32))
+
+
+def bf16_round(a):
+    """Round-to-nearest-even fp32 -> bf16 (kept in fp32), the rounding the bf16 GEMM applies."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("tA,tB", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (37, 5, 3), (130, 257, 67), (256, 128, 128), (300, 129, 515)])
+def test_gemm_bf16acc_layouts(tA, tB, M, N, K):
+    # bf16 x bf16 products are exact in fp32, so against an f64 product of the bf16-rounded inputs
+    # only the fp32 accumulation error remains
+    rng = np.random.default_rng(7 * M + N + K)
+    A = rng.normal(size=(K, M) if tA else (M, K)).astype(np.float32)
+    B = rng.normal(size=(N, K) if tB else (K, N)).astype(np.float32)
+    dA, dB, dC = DA.from_numpy(A), DA.from_numpy(B), DA.zeros((M, N))
+    th.call("talos_gemm_bf16acc_f32", tA, tB, M, N, K, 1.0, dA.ptr, A.shape[1], dB.ptr, B.shape[1], 0.0, dC.ptr, N,
+            None)
+    got = dC.numpy()
+    Ab, Bb = bf16_round(A).astype(np.float64), bf16_round(B).astype(np.float64)
+    a, b = (Ab.T if tA else Ab), (Bb.T if tB else Bb)
+    ref = a @ b
+    bound = 1e-5 * (np.abs(a) @ np.abs(b)) + 1e-30
+    assert np.all(np.abs(got - ref) <= bound), np.max(np.abs(got - ref) / bound)
+
+
+def test_gemm_bf16acc_split_k():
+    rng = np.random.default_rng(8)
+    X = rng.normal(size=(40000, 128)).astype(np.float32)
+    G = rng.normal(size=(40000, 64)).astype(np.float32)
+    dX, dG, dC = DA.from_numpy(X), DA.from_numpy(G), DA.zeros((128, 64))
+    th.call("talos_gemm_bf16acc_f32", 1, 0, 128, 64, 40000, 1.0, dX.ptr, 128, dG.ptr, 64, 0.0, dC.ptr, 64, None)
+    Xb, Gb = bf16_round(X).astype(np.float64), bf16_round(G).astype(np.float64)
+    ref = Xb.T @ Gb
+    scale = np.abs(Xb).T @ np.abs(Gb)
+    assert np.all(np.abs(dC.numpy() - ref) <= 1e-6 * scale + 1e-6)

@@ -163,3 +163,28 @@ def test_mla_fwd_bwd_vs_oracle(oracle, ci):
     check_close(dx, dx_r, name="dx")
     for n, sl in mla_slices(ci).items():
         check_close(dp[sl], dp_r[sl], name=f"d{n}", scale_floor=GRAD_SCALE_FLOOR)
+
+
+@pytest.mark.parametrize("ci", [[2, 37, 64, 2, 32, 8, 16, 16, 1, 0], [2, 64, 512, 8, 128, 32, 64, 64, 0, 0]])
+def test_mla_bf16_vs_oracle(oracle, ci):
+    # bf16-in / fp32-accumulate GEMMs against the f64 oracle: every tensor within 2e-2 relative in the
+    # max norm, max|got - ref| <= 2e-2 * max|ref| (bf16 keeps 8 significand bits, so element-wise
+    # relative error on elements that cancel toward zero is unbounded)
+    from common import BF16_RTOL, mla_params
+    rng = np.random.default_rng(4000 + ci[1] + ci[2])
+    B, S, d = ci[:3]
+    p = f32(mla_params(rng, ci))
+    x, G = f32(rng.normal(size=(B, S, d))), f32(rng.normal(size=(B, S, d)))
+    out_r, dp_r, dx_r = oracle.mla_fwd_bwd(ci, 1e-5, 10000.0, p, x, G)
+    out, dp, dx = run_mla(ci, th.PREC_BF16, p, x, G)
+
+    def chk(got, ref, name):
+        assert np.all(np.isfinite(got)), name
+        rel = float(np.abs(got - ref).max() / np.abs(ref).max())
+        print(f"{name}: max|err| / max|ref| = {rel:.3e}")
+        assert rel <= BF16_RTOL, f"{name}: normwise relative error {rel:.3e} > {BF16_RTOL}"
+
+    chk(out, out_r, "out")
+    chk(dx, dx_r, "dx")
+    for n, sl in mla_slices(ci).items():
+        chk(dp[sl], dp_r[sl], f"d{n}")
