@@ -53,7 +53,24 @@ def build(verbose=False, jobs=None):
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_tape()
     return LIB
+
+
+TAPE_SRC = os.path.join(HERE, "host", "tape.cpp")
+TAPE_LIB = os.path.join(HERE, "libtalos_tape.so")
+
+
+def build_tape():
+    """Builds libtalos_tape.so, the host-side C++ tape (host/tape.cpp) over the C ABI."""
+    tmp = TAPE_LIB + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", TAPE_SRC, "-o", tmp, f"-L{HERE}", "-ltalos_hip",
+           "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed for {TAPE_SRC}:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, TAPE_LIB)
+    return TAPE_LIB
 
 
 if __name__ == "__main__":

@@ -1,0 +1,136 @@
+// tape.hpp -- host-side autograd tape over the C ABI of libtalos_hip.so.
+//
+// Mirrors the reference's Rust Tensor API (src/autograd.rs:14-20, 51-54, 94-196 and the ops of
+// :200-792, 1599-1862) and the Linear / RMSNorm modules (src/nn.rs:11-304), with tensors held in
+// device memory as fp32 and every op and backward closure executed by the library's kernels:
+//
+//   reference (Rust)                         here (C++)
+//   Tensor::new(data, shape)                 Tensor::from_vec(data, shape)
+//   Tensor::zeros / rand / detach / item     Tensor::zeros / rand / detach / item
+//   t.backward() / zero_grad / clear_graph   t.backward() / zero_grad / clear_graph
+//   t.data.read() / t.grad.read()            t.data() / t.grad()  (f64 host copies)
+//   matmul relu log exp sum mean broadcast   same names
+//   broadcast_to_batch sin cos sqrt transpose clip reshape mse_loss
+//   a + b, a - b, a * b, a / b, -a           same operators
+//
+// Semantics kept: grads accumulate (+=) and only zero_grad clears them; backward() seeds every
+// element of the root's grad with 1.0 and runs the closures in reverse DFS topological order,
+// visiting each tensor (identified by its grad storage) once; x * x with the same tensor on both
+// sides accumulates 2x.g once. Shape errors throw talos::tape::Panic where the reference panics
+// (assert!), and a failing kernel call throws with the library's message.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <functional>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace talos {
+namespace tape {
+
+struct Panic : std::runtime_error {
+  explicit Panic(const std::string& m) : std::runtime_error(m) {}
+};
+
+using Shape = std::vector<size_t>;
+
+// A device buffer of n fp32 values (freed with the last reference).
+struct Storage {
+  float* ptr = nullptr;
+  size_t n = 0;
+  explicit Storage(size_t n);
+  ~Storage();
+  Storage(const Storage&) = delete;
+  Storage& operator=(const Storage&) = delete;
+};
+
+class Tensor;
+struct Context {
+  std::vector<Tensor> parents;
+  // receives the output tensor (its grad is grad_out) and the parents
+  std::function<void(const Tensor& out, std::vector<Tensor>& parents)> backward_op;
+};
+
+class Tensor {
+ public:
+  std::shared_ptr<Storage> data_;
+  std::shared_ptr<Storage> grad_;
+  Shape shape;
+  std::shared_ptr<Context> _ctx;
+
+  static Tensor from_vec(const std::vector<double>& data, Shape shape);  // Tensor::new
+  static Tensor zeros(Shape shape);
+  // Tensor::rand: the reference's LCG x = x * 6364136223846793005 + 1, r = (x >> 33) / u32::MAX
+  // (src/autograd.rs:114-124), evaluated in f64 and stored as fp32
+  static Tensor rand(Shape shape, double min, double max, uint64_t seed);
+
+  size_t numel() const { return data_ ? data_->n : 0; }
+  std::vector<double> data() const;  // Tensor.data.read()
+  std::vector<double> grad() const;  // Tensor.grad.read()
+  void set_data(const std::vector<double>& v) const;  // Tensor.data.write() = v
+  double item() const;
+  Tensor detach() const;  // shares data and grad, drops the graph
+  void clear_graph() { _ctx.reset(); }
+  void zero_grad() const;
+  void backward() const;
+
+  Tensor matmul(const Tensor& other) const;
+  Tensor relu() const;
+  Tensor log() const;
+  Tensor exp() const;
+  Tensor sum() const;
+  Tensor mean() const;
+  Tensor broadcast(Shape new_shape) const;
+  Tensor broadcast_to_batch(size_t batch_size) const;
+  Tensor sin() const;
+  Tensor cos() const;
+  Tensor sqrt() const;
+  Tensor transpose(size_t dim0, size_t dim1) const;
+  Tensor clip(double min, double max) const;
+  Tensor reshape(Shape new_shape) const;
+  Tensor mse_loss(const Tensor& target) const;
+  // extensions used by the configurations (no reference counterpart): GELU and a scale
+  Tensor gelu() const;
+  Tensor scale(double s) const;
+};
+
+Tensor operator+(const Tensor& a, const Tensor& b);
+Tensor operator-(const Tensor& a, const Tensor& b);
+Tensor operator*(const Tensor& a, const Tensor& b);
+Tensor operator/(const Tensor& a, const Tensor& b);
+Tensor operator-(const Tensor& a);
+
+// Module (src/nn.rs:6-9)
+struct Module {
+  virtual ~Module() = default;
+  virtual Tensor forward(const Tensor& input) const = 0;
+  virtual std::vector<Tensor> parameters() const = 0;
+};
+
+// Linear (src/nn.rs:11-142): y = x . W + b with W stored [in, out]; N-D inputs are flattened to
+// [rows, in] and the result reshaped back; the bias is broadcast over the rows.
+struct Linear : Module {
+  Tensor weight, bias;
+  bool has_bias = true;
+  size_t in_features = 0, out_features = 0;
+  // Xavier-uniform limit sqrt(6/(in+out)) drawn with Tensor::rand, as Linear::new does (src/nn.rs:20-35)
+  Linear(size_t in, size_t out, bool bias, uint64_t seed);
+  Linear(Tensor weight, Tensor bias, bool has_bias);
+  Tensor forward(const Tensor& input) const override;
+  std::vector<Tensor> parameters() const override;
+};
+
+// RMSNorm (src/nn.rs:144-304): y = x / sqrt(mean(x^2) + eps) * w over the last dimension.
+struct RMSNorm : Module {
+  Tensor weight;
+  double eps = 1e-5;
+  explicit RMSNorm(size_t dim, double eps = 1e-5);
+  Tensor forward(const Tensor& x) const override;
+  std::vector<Tensor> parameters() const override;
+};
+
+}  // namespace tape
+}  // namespace talos
