@@ -187,6 +187,30 @@ int talos_concat_last_bwd_f32(size_t rows, int ca, int cb, const float* dout, fl
 int talos_broadcast_rows_f32(size_t rows, int cols, const float* v, float* out, talos_stream_t stream);
 
 /* ------------------------------------------------------------------------- */
+/* Optimizer step                                                             */
+/* ------------------------------------------------------------------------- */
+
+/* sumsq[0] = (accumulate ? sumsq[0] : 0) + sum_i grads[i]^2, summed in f64: the global-norm
+ * loop of the DQN optimizer (dqn.rs:207-214). sumsq is ONE device double; several parameter
+ * tensors share one norm by calling this once per tensor with accumulate = 1 after the first.
+ * Deterministic (fixed partition of the partial sums). */
+int talos_grad_sumsq_f32(size_t n, const float* grads, int accumulate, double* sumsq, talos_stream_t stream);
+
+/* One Adam step over n parameters, Adam::step (ppo.rs:519-533):
+ *   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2;
+ *   params -= lr * (m / (1 - b1^t)) / (sqrt(v / (1 - b2^t)) + eps)
+ * t is the step count AFTER the reference's increment (1 on the first call; t < 1 is
+ * TALOS_ERR_SHAPE). m and v are fp32 state, zero before the first step; the arithmetic runs in
+ * f64 and rounds once on the store. The reference uses b1 = 0.9, b2 = 0.999, eps = 1e-8.
+ * When sumsq != NULL (a device double from talos_grad_sumsq_f32) the gradient is first scaled by
+ * the DQN global-norm clip (dqn.rs:215-226): c = max_norm / sqrt(*sumsq) if sqrt(*sumsq) >
+ * max_norm, else 1 (the reference's max_norm is 1.0; max_norm <= 0 is TALOS_ERR_SHAPE).
+ * params, grads, m and v must not overlap. */
+int talos_adam_step_f32(size_t n, float* params, const float* grads, float* m, float* v, int t, double lr,
+                        double beta1, double beta2, double eps, const double* sumsq, double max_norm,
+                        talos_stream_t stream);
+
+/* ------------------------------------------------------------------------- */
 /* Fused model-level entry points                                             */
 /* ------------------------------------------------------------------------- */
 

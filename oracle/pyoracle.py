@@ -92,6 +92,9 @@ def lib():
         L.orc_ppo_param_count.argtypes = [ctypes.POINTER(PpoCfg)]
         L.orc_mla_param_count.restype = ctypes.c_size_t
         L.orc_mla_param_count.argtypes = [_i32p]
+        L.orc_adam_step.restype = None
+        L.orc_adam_step.argtypes = [ctypes.c_int64, _f64p, _f64p, _f64p, _f64p, ctypes.c_int, ctypes.c_double,
+                                    ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double]
         L.orc_threads.restype = ctypes.c_int
         L.orc_set_threads.argtypes = [ctypes.c_int]
         _lib = L
@@ -418,3 +421,14 @@ def mla_fwd_bwd(ci, eps, base, params, x, gout):
     _check(lib().orc_mla_fwd_bwd(ci.ctypes.data_as(_i32p), ctypes.c_double(eps), ctypes.c_double(base), _p(params),
                                  _p(x), _p(gout), _p(out), _p(dparams), _p(dx)))
     return out, dparams, dx
+
+
+def adam_step(p, g, m, v, t, lr, beta1=0.9, beta2=0.999, eps=1e-8, max_norm=0.0):
+    """One Adam step in f64 (src/ppo.rs:519-533); max_norm > 0 adds the DQN global-norm clip
+    (src/dqn.rs:207-226). Updates p, m, v (float64 arrays) in place."""
+    for a in (p, m, v):
+        assert a.dtype == np.float64 and a.flags.c_contiguous
+    g = _f64(g)
+    assert p.size == g.size == m.size == v.size
+    lib().orc_adam_step(p.size, _p(p), _p(g), _p(m), _p(v), int(t), float(lr), float(beta1), float(beta2),
+                        float(eps), float(max_norm))

@@ -19,7 +19,9 @@
  *     batched_matmul_probs_v / concat_last_dim (src/transformer.rs:877-1183), the MLA forward
  *     (src/transformer.rs:478-560) and the pre-norm block wiring (src/transformer.rs:71-90);
  *   - the PPO per-sample loss graph (src/ppo.rs:691-756) and the actor-critic heads
- *     (src/ppo.rs:246-300).
+ *     (src/ppo.rs:246-300);
+ *   - the optimizer step: Adam (src/ppo.rs:519-533) and the DQN optimizer's global-norm
+ *     gradient clip (src/dqn.rs:207-226).
  * Extensions the configurations need (each documented where defined): causal softmax mask,
  * GELU, explicit sequence positions for RoPE, a differentiable last-token gather, a standard
  * multi-head attention block, and a batched PPO loss with a closed-form backward.
@@ -1664,6 +1666,29 @@ int orc_mla_fwd_bwd(const int32_t* ci, double eps, double base, const double* pa
     P.grads(dparams);
     std::copy(X.grad->begin(), X.grad->end(), dx);
   })
+}
+
+// Adam::step (src/ppo.rs:519-533) over one flat parameter vector with f64 state; t is the step
+// count after the increment (src/ppo.rs:520). When max_norm > 0 the gradient is first clipped by
+// its global L2 norm as the DQN optimizer does (src/dqn.rs:207-226): the norm is summed in index
+// order, and g is multiplied by max_norm / norm when norm > max_norm (max_norm = 1.0 there).
+void orc_adam_step(int64_t n, double* p, const double* g, double* m, double* v, int t, double lr, double b1,
+                   double b2, double eps, double max_norm) {
+  double clip_coef = 1.0;
+  if (max_norm > 0.0) {
+    double total = 0.0;
+    for (int64_t j = 0; j < n; ++j) total += g[j] * g[j];
+    total = std::sqrt(total);
+    if (total > max_norm) clip_coef = max_norm / total;
+  }
+  const double bc1 = 1.0 - std::pow(b1, t), bc2 = 1.0 - std::pow(b2, t);
+  for (int64_t j = 0; j < n; ++j) {
+    const double gj = g[j] * clip_coef;
+    m[j] = b1 * m[j] + (1.0 - b1) * gj;
+    v[j] = b2 * v[j] + (1.0 - b2) * gj * gj;
+    const double m_hat = m[j] / bc1, v_hat = v[j] / bc2;
+    p[j] -= lr * m_hat / (std::sqrt(v_hat) + eps);
+  }
 }
 
 }  // extern "C"

@@ -355,5 +355,45 @@ Tensor RMSNorm::forward(const Tensor& x) const {
 
 std::vector<Tensor> RMSNorm::parameters() const { return {weight}; }
 
+// ---------------------------------------------------------------------------
+// Adam (src/ppo.rs:482-539; src/dqn.rs:173-246)
+// ---------------------------------------------------------------------------
+Adam::Adam(std::vector<Tensor> params, double lr, double max_grad_norm)
+    : params_(std::move(params)), lr_(lr), max_norm_(max_grad_norm) {
+  for (const Tensor& p : params_) {  // zero state, as Adam::new's vec![0.0; len]
+    m_.push_back(std::make_unique<Storage>(p.numel()));
+    v_.push_back(std::make_unique<Storage>(p.numel()));
+    ok(talos_fill_zero(m_.back()->ptr, p.numel() * sizeof(float), nullptr), "fill_zero");
+    ok(talos_fill_zero(v_.back()->ptr, p.numel() * sizeof(float), nullptr), "fill_zero");
+  }
+  if (max_norm_ > 0.0) {
+    void* p = nullptr;
+    ok(talos_malloc(&p, sizeof(double)), "talos_malloc");
+    sumsq_ = static_cast<double*>(p);
+  }
+}
+
+Adam::~Adam() {
+  if (sumsq_) talos_free(sumsq_);
+}
+
+void Adam::step() {
+  ++t_;
+  if (sumsq_) {  // src/dqn.rs:207-214: one norm over every parameter's gradient
+    for (size_t i = 0; i < params_.size(); ++i)
+      ok(talos_grad_sumsq_f32(params_[i].numel(), params_[i].grad_->ptr, i > 0, sumsq_, nullptr), "grad_sumsq");
+  }
+  for (size_t i = 0; i < params_.size(); ++i) {
+    const Tensor& p = params_[i];
+    ok(talos_adam_step_f32(p.numel(), p.data_->ptr, p.grad_->ptr, m_[i]->ptr, v_[i]->ptr, (int)t_, lr_, beta1, beta2,
+                           eps, sumsq_, max_norm_, nullptr),
+       "adam_step");
+  }
+}
+
+void Adam::zero_grad() const {
+  for (const Tensor& p : params_) p.zero_grad();
+}
+
 }  // namespace tape
 }  // namespace talos

@@ -12,6 +12,7 @@
 //   matmul relu log exp sum mean broadcast   same names
 //   broadcast_to_batch sin cos sqrt transpose clip reshape mse_loss
 //   a + b, a - b, a * b, a / b, -a           same operators
+//   Adam::new(params, lr) / step / zero_grad  Adam(params, lr[, max_grad_norm]) / step / zero_grad
 //
 // Semantics kept: grads accumulate (+=) and only zero_grad clears them; backward() seeds every
 // element of the root's grad with 1.0 and runs the closures in reverse DFS topological order,
@@ -130,6 +131,32 @@ struct RMSNorm : Module {
   explicit RMSNorm(size_t dim, double eps = 1e-5);
   Tensor forward(const Tensor& x) const override;
   std::vector<Tensor> parameters() const override;
+};
+
+// Adam (src/ppo.rs:482-539): Adam::new(params, lr), step(), zero_grad(), set_lr(); b1 = 0.9,
+// b2 = 0.999, eps = 1e-8. m and v are fp32 device buffers beside each parameter; step()
+// increments t and runs the library's fused Adam kernel once per parameter tensor. With
+// max_grad_norm > 0 it is the DQN optimizer (src/dqn.rs:173-246, max_grad_norm = 1.0): one f64
+// squared-norm pass over every parameter's grad first, then each kernel scales its gradient by
+// max_grad_norm / ||g|| when ||g|| > max_grad_norm.
+class Adam {
+ public:
+  Adam(std::vector<Tensor> params, double lr, double max_grad_norm = 0.0);
+  ~Adam();
+  Adam(const Adam&) = delete;
+  Adam& operator=(const Adam&) = delete;
+  void step();
+  void zero_grad() const;
+  void set_lr(double lr) { lr_ = lr; }
+  size_t t() const { return t_; }
+  double beta1 = 0.9, beta2 = 0.999, eps = 1e-8;
+
+ private:
+  std::vector<Tensor> params_;
+  std::vector<std::unique_ptr<Storage>> m_, v_;
+  double* sumsq_ = nullptr;  // one device double (clipping only)
+  size_t t_ = 0;
+  double lr_, max_norm_;
 };
 
 }  // namespace tape

@@ -97,6 +97,9 @@ _SIGS = {
     "talos_concat_last_f32": [_sz, _i, _i, _vp, _vp, _vp, _vp],
     "talos_concat_last_bwd_f32": [_sz, _i, _i, _vp, _vp, _vp, _vp],
     "talos_broadcast_rows_f32": [_sz, _i, _vp, _vp, _vp],
+    "talos_grad_sumsq_f32": [_sz, _vp, _i, _vp, _vp],
+    "talos_adam_step_f32": [_sz, _vp, _vp, _vp, _vp, _i, ctypes.c_double, ctypes.c_double, ctypes.c_double,
+                            ctypes.c_double, _vp, ctypes.c_double, _vp],
     "talos_block_param_count": [ctypes.POINTER(BlockCfg)],
     "talos_ppo_param_count": [ctypes.POINTER(PpoCfg)],
     "talos_block_plan_create": [ctypes.POINTER(BlockCfg), ctypes.POINTER(_vp)],

@@ -45,6 +45,8 @@ int64_t orc_mse_loss(int64_t a, int64_t b);
 int orc_backward(int64_t h);
 int orc_linear_mse(int64_t rows, int64_t in_f, int64_t out_f, const double* x, const double* w, const double* b,
                    const double* y, double* loss, double* dx, double* dw, double* db);
+void orc_adam_step(int64_t n, double* p, const double* g, double* m, double* v, int t, double lr, double b1,
+                   double b2, double eps, double max_norm);
 int orc_rmsnorm_fwd_bwd(int64_t rows, int64_t dim, double eps, const double* x, const double* w, const double* dy,
                         double* y, double* dx, double* dw);
 }
@@ -269,6 +271,52 @@ static void test_composite_graph() {
   close(T.grad(), ograd(oT, 24), "composite: dT");
 }
 
+// Adam over a Linear's parameters (src/ppo.rs:482-539), and the DQN variant with the global
+// gradient-norm clip (src/dqn.rs:207-226): three training steps through the tape against the
+// oracle's f64 Adam fed the same gradients. The target scale makes ||g|| > 1 in the clipped run.
+static void run_adam(double max_norm, double target_scale, const std::string& tag) {
+  uint64_t s = 23;
+  const auto xv = rng_normal(32 * 16, s);
+  auto yv = rng_normal(32 * 8, s);
+  for (double& y : yv) y *= target_scale;
+  Linear lin(16, 8, true, 7);
+  Tensor x = Tensor::from_vec(xv, {32, 16}), y = Tensor::from_vec(yv, {32, 8});
+  talos::tape::Adam opt(lin.parameters(), 1e-2, max_norm);
+  auto flat = [&](bool grads) {
+    std::vector<double> out;
+    for (const Tensor& p : lin.parameters()) {
+      const auto d = grads ? p.grad() : p.data();
+      out.insert(out.end(), d.begin(), d.end());
+    }
+    return out;
+  };
+  const std::vector<double> p0 = flat(false);
+  std::vector<double> pr = p0, m(p0.size(), 0.0), v(p0.size(), 0.0);
+  bool clipped = false;
+  for (int t = 1; t <= 3; ++t) {
+    opt.zero_grad();
+    lin.forward(x).mse_loss(y).backward();
+    const std::vector<double> g = flat(true);
+    double ss = 0.0;
+    for (double gi : g) ss += gi * gi;
+    clipped = clipped || std::sqrt(ss) > 1.0;
+    opt.step();
+    orc_adam_step((int64_t)pr.size(), pr.data(), g.data(), m.data(), v.data(), t, 1e-2, 0.9, 0.999, 1e-8, max_norm);
+    const std::vector<double> got = flat(false);
+    std::vector<double> dgot(got.size()), dref(got.size());
+    for (size_t i = 0; i < got.size(); ++i) {
+      dgot[i] = got[i] - p0[i];
+      dref[i] = pr[i] - p0[i];
+    }
+    close(dgot, dref, tag + ": parameter delta after step " + std::to_string(t));
+  }
+  check(opt.t() == 3, tag + ": step count");
+  if (max_norm > 0.0) check(clipped, tag + ": the clip engaged");
+}
+
+static void test_adam_ppo() { run_adam(0.0, 1.0, "adam"); }
+static void test_adam_dqn_clip() { run_adam(1.0, 30.0, "adam+clip"); }
+
 // Shape errors panic as the reference's assert! does (src/autograd.rs:209, 1611)
 static void test_shape_errors_panic() {
   bool threw = false;
@@ -309,6 +357,8 @@ int main() {
                {"rmsnorm_backward", test_rmsnorm_backward},
                {"linear_mse_c1", test_linear_mse_c1},
                {"composite_graph", test_composite_graph},
+               {"adam_ppo", test_adam_ppo},
+               {"adam_dqn_clip", test_adam_dqn_clip},
                {"shape_errors_panic", test_shape_errors_panic}};
   for (auto& t : tests) {
     std::printf("test %s\n", t.name);

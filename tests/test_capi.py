@@ -108,3 +108,15 @@ def test_no_device_is_a_clean_error(L):
     assert L.talos_malloc(ctypes.byref(p), 64) == th.ERR_NO_DEVICE
     assert L.talos_init() == th.ERR_NO_DEVICE
     assert b"GPU" in L.talos_last_error()
+
+
+def test_optimizer_argument_errors(L):
+    p = ctypes.c_void_p(16)
+    args = (0.9, 0.999, 1e-8)
+    assert L.talos_adam_step_f32(4, p, p, p, p, 0, 1e-3, *args, None, 0.0, None) == th.ERR_SHAPE  # t < 1
+    assert L.talos_adam_step_f32(4, p, p, p, p, 1, 1e-3, 1.0, 0.999, 1e-8, None, 0.0, None) == th.ERR_SHAPE
+    assert L.talos_adam_step_f32(4, p, p, p, p, 1, 1e-3, *args, p, 0.0, None) == th.ERR_SHAPE  # max_norm
+    assert L.talos_adam_step_f32(4, None, p, p, p, 1, 1e-3, *args, None, 0.0, None) == th.ERR_NULL
+    assert L.talos_adam_step_f32(0, None, None, None, None, 1, 1e-3, *args, None, 0.0, None) == th.OK
+    assert L.talos_grad_sumsq_f32(4, p, 0, None, None) == th.ERR_NULL
+    assert L.talos_grad_sumsq_f32(4, None, 0, p, None) == th.ERR_NULL

@@ -407,3 +407,64 @@ def test_linear_mse_closed_form(oracle):
     assert abs(loss - (r * r).mean()) < 1e-12
     assert np.allclose(dx, dY @ W.T, atol=1e-15) and np.allclose(dw, X.T @ dY, atol=1e-14)
     assert np.allclose(db, dY.sum(0), atol=1e-15)
+
+
+# ---------------------------------------------------------------------------
+# Optimizer step: Adam (src/ppo.rs:519-533) and the DQN global-norm clip (src/dqn.rs:207-226)
+# ---------------------------------------------------------------------------
+def test_adam_vs_torch_adam_f64(oracle):
+    """Five steps of the oracle's Adam equal torch.optim.Adam in float64 (same update written as
+    p -= (lr / (1 - b1^t)) * m / (sqrt(v) / sqrt(1 - b2^t) + eps))."""
+    rng = np.random.default_rng(7)
+    n = 1000
+    p0 = rng.normal(size=n)
+    p, m, v = p0.copy(), np.zeros(n), np.zeros(n)
+    tp = torch.tensor(p0, dtype=torch.float64, requires_grad=True)
+    opt = torch.optim.Adam([tp], lr=3e-3, betas=(0.9, 0.999), eps=1e-8)
+    for t in range(1, 6):
+        g = rng.normal(size=n) * (0.1 * t)
+        oracle.adam_step(p, g, m, v, t, 3e-3)
+        tp.grad = torch.tensor(g, dtype=torch.float64)
+        opt.step()
+        np.testing.assert_allclose(p - p0, tp.detach().numpy() - p0, rtol=1e-10, atol=1e-15)
+        st = opt.state[tp]
+        # torch forms m with lerp (m + (1 - b1)(g - m)): the same value up to f64 rounding
+        np.testing.assert_allclose(m, st["exp_avg"].numpy(), rtol=1e-10, atol=1e-16)
+        np.testing.assert_allclose(v, st["exp_avg_sq"].numpy(), rtol=1e-10, atol=1e-18)
+
+
+def test_adam_first_step_closed_form(oracle):
+    """At t = 1 from zero state the bias corrections cancel: m_hat = g, v_hat = g^2, so the update
+    is lr * g / (|g| + eps) (exactly 0 where g = 0)."""
+    rng = np.random.default_rng(8)
+    g = rng.normal(size=257)
+    g[::17] = 0.0
+    p0 = rng.normal(size=257)
+    p, m, v = p0.copy(), np.zeros(257), np.zeros(257)
+    oracle.adam_step(p, g, m, v, 1, 1e-2)
+    np.testing.assert_allclose(p0 - p, 1e-2 * g / (np.abs(g) + 1e-8), rtol=1e-12, atol=1e-18)
+    np.testing.assert_allclose(m, 0.1 * g, rtol=1e-15)
+    np.testing.assert_allclose(v, 0.001 * g * g, rtol=1e-12)
+
+
+@pytest.mark.parametrize("scale", [5.0, 0.01])
+def test_adam_global_norm_clip(oracle, scale):
+    """The DQN step equals the plain step on g / ||g|| when ||g|| > 1 and on g itself otherwise."""
+    rng = np.random.default_rng(9)
+    n = 300
+    g = rng.normal(size=n) * scale / math.sqrt(n)
+    norm = float(np.linalg.norm(g))
+    g_eff = g / norm if norm > 1.0 else g
+    p0 = rng.normal(size=n)
+    pa, ma, va = p0.copy(), np.zeros(n), np.zeros(n)
+    pb, mb, vb = p0.copy(), np.zeros(n), np.zeros(n)
+    for t in (1, 2):
+        oracle.adam_step(pa, g, ma, va, t, 1e-2, max_norm=1.0)
+        oracle.adam_step(pb, g_eff, mb, vb, t, 1e-2)
+    np.testing.assert_allclose(ma, mb, rtol=1e-13, atol=0)
+    np.testing.assert_allclose(va, vb, rtol=1e-12, atol=0)
+    np.testing.assert_allclose(pa - p0, pb - p0, rtol=1e-11, atol=1e-16)
+    if norm > 1.0:  # the clipped first moment has norm (1 - b1) * 1 after one step
+        m1 = np.zeros(n)
+        oracle.adam_step(p0.copy(), g, m1, np.zeros(n), 1, 1e-2, max_norm=1.0)
+        assert abs(np.linalg.norm(m1) - 0.1) < 1e-12
