@@ -387,8 +387,7 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
   rc = mm(p, s, 0, 1, M, d, F, p->g_u, F, P + o.w1, F, p->g_xn, d);
   if (rc) return rc;
   // h2 -> (residual) + rmsnorm2
-  TALOS_HIP(hipMemcpyAsync(p->g_h2, gout, (size_t)M * d * 4, hipMemcpyDeviceToDevice, s));
-  rc = rmsnorm_bwd_launch(M, d, L.h2, P + o.g2, L.rstd2, p->g_xn, 1.f, p->g_h2, 0.f, G + o.g2, p->red_ws, s);
+  rc = rmsnorm_bwd_launch(M, d, L.h2, P + o.g2, L.rstd2, p->g_xn, 1.f, p->g_h2, 0.f, G + o.g2, p->red_ws, s, gout);
   if (rc) return rc;
   // h2 = x + o.Wo
   rc = mm(p, s, 1, 0, d, d, M, L.o, d, p->g_h2, d, G + o.wo, d);
@@ -428,8 +427,7 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
   if (rc) return rc;
   rc = mm(p, s, 0, 1, M, d, 3 * d, p->g_qkv, 3 * d, P + o.wqkv, 3 * d, p->g_xn, d);
   if (rc) return rc;
-  if (dx != p->g_h2) TALOS_HIP(hipMemcpyAsync(dx, p->g_h2, (size_t)M * d * 4, hipMemcpyDeviceToDevice, s));
-  return rmsnorm_bwd_launch(M, d, L.x, P + o.g1, L.rstd1, p->g_xn, 1.f, dx, 0.f, G + o.g1, p->red_ws, s);
+  return rmsnorm_bwd_launch(M, d, L.x, P + o.g1, L.rstd1, p->g_xn, 1.f, dx, 0.f, G + o.g1, p->red_ws, s, p->g_h2);
 }
 
 // Last-token gather / scatter -----------------------------------------------
@@ -701,8 +699,7 @@ static int mla_fwd_bwd(talos_plan_s* p, const float* P, const float* x, const fl
   if ((rc = mm(p, s, 1, 0, d, L, M, b.xn, d, b.dckv, L, G + o.wdkv, L))) return rc;
   if ((rc = mm(p, s, 0, 1, M, d, L, b.dckv, L, P + o.wdkv, L, b.dxn, d, 1.f))) return rc;
   // residual + rmsnorm
-  TALOS_HIP(hipMemcpyAsync(dx, gout, (size_t)M * d * 4, hipMemcpyDeviceToDevice, s));
-  return rmsnorm_bwd_launch(M, d, x, P + o.g, b.rstd, b.dxn, 1.f, dx, 0.f, G + o.g, p->red_ws, s);
+  return rmsnorm_bwd_launch(M, d, x, P + o.g, b.rstd, b.dxn, 1.f, dx, 0.f, G + o.g, p->red_ws, s, gout);
 }
 
 }  // namespace talos

@@ -191,8 +191,8 @@ template <int V>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(int rows, int dim, const float* __restrict__ x,
                                                           const float* __restrict__ w,
                                                           const float* __restrict__ rstd,
-                                                          const float* __restrict__ dy, float beta_dx,
-                                                          float* __restrict__ dx, double* __restrict__ dw_part) {
+                                                          const float* __restrict__ dy, const float* add,
+                                                          float* dx, double* __restrict__ dw_part) {
   __shared__ float red[4][V * 256];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   float4 gw[V], dwacc[V];
@@ -234,8 +234,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(int rows, int dim, con
       if (c < dim) {
         float4 o = make_float4(r * (gg[j].x * gw[j].x - xh[j].x * md), r * (gg[j].y * gw[j].y - xh[j].y * md),
                                r * (gg[j].z * gw[j].z - xh[j].z * md), r * (gg[j].w * gw[j].w - xh[j].w * md));
-        if (beta_dx != 0.f) {
-          const float4 old = *reinterpret_cast<const float4*>(dxr + c);
+        if (add) {
+          const float4 old = *reinterpret_cast<const float4*>(add + (long long)row * dim + c);
           o.x += old.x;
           o.y += old.y;
           o.z += old.z;
@@ -258,8 +258,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(int rows, int dim, con
 __global__ __launch_bounds__(256) void rmsnorm_bwd_generic(int rows, int dim, const float* __restrict__ x,
                                                            const float* __restrict__ w,
                                                            const float* __restrict__ rstd,
-                                                           const float* __restrict__ dy, float beta_dx,
-                                                           float* __restrict__ dx, double* __restrict__ dw_part) {
+                                                           const float* __restrict__ dy, const float* add,
+                                                           float* dx, double* __restrict__ dw_part) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   for (int row = blockIdx.x * 4 + wv; row < rows; row += gridDim.x * 4) {
     const float r = rstd[row];
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_generic(int rows, int dim, co
     const float md = wave_sum(dot) / (float)dim;
     for (int c = lane; c < dim; c += 64) {
       float o = r * (gr[c] * w[c] - xr[c] * r * md);
-      if (beta_dx != 0.f) o += dx[(long long)row * dim + c];
+      if (add) o += add[(long long)row * dim + c];
       dx[(long long)row * dim + c] = o;
     }
   }
@@ -308,24 +308,28 @@ int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float
 }
 
 int rmsnorm_bwd_launch(int rows, int dim, const float* x, const float* w, const float* rstd, const float* dy,
-                       float beta_dx, float* dx, float beta_dw, float* dw, double* ws, hipStream_t s) {
+                       float beta_dx, float* dx, float beta_dw, float* dw, double* ws, hipStream_t s,
+                       const float* dres) {
   const int nblk = rows > 0 ? rms_bwd_blocks(rows) : 0;
   if (nblk > 0) {
     dim3 g(nblk), b(256);
     double* part = dw ? ws : nullptr;
+    // the addend: the residual branch's gradient, or dx itself when accumulating
+    const float* add = dres ? dres : (beta_dx != 0.f ? dx : nullptr);
     const bool vec = dim % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy) |
-                                       reinterpret_cast<uintptr_t>(dx) | reinterpret_cast<uintptr_t>(w)) & 15) == 0;
-    // x, dy read, dx written (read too when accumulating), gain + rstd read, dgain partials written
+                                       reinterpret_cast<uintptr_t>(dx) | reinterpret_cast<uintptr_t>(w) |
+                                       reinterpret_cast<uintptr_t>(add)) & 15) == 0;
+    // x, dy read, dx written (the addend read too), gain + rstd read, dgain partials written
     ProfScope ps(s, vec && dim <= 256 ? "rmsnorm_bwd_kernel<1>" : vec && dim <= 512 ? "rmsnorm_bwd_kernel<2>"
                     : "rmsnorm_bwd_generic",
-                 8.0 * rows * dim, 4.0 * ((3.0 + (beta_dx != 0.f)) * rows * dim + dim + rows) +
+                 8.0 * rows * dim, 4.0 * ((3.0 + (add != nullptr)) * rows * dim + dim + rows) +
                                        (part ? 8.0 * nblk * dim : 0.0));
     if (vec && dim <= 256)
-      hipLaunchKernelGGL(rmsnorm_bwd_kernel<1>, g, b, 0, s, rows, dim, x, w, rstd, dy, beta_dx, dx, part);
+      hipLaunchKernelGGL(rmsnorm_bwd_kernel<1>, g, b, 0, s, rows, dim, x, w, rstd, dy, add, dx, part);
     else if (vec && dim <= 512)
-      hipLaunchKernelGGL(rmsnorm_bwd_kernel<2>, g, b, 0, s, rows, dim, x, w, rstd, dy, beta_dx, dx, part);
+      hipLaunchKernelGGL(rmsnorm_bwd_kernel<2>, g, b, 0, s, rows, dim, x, w, rstd, dy, add, dx, part);
     else
-      hipLaunchKernelGGL(rmsnorm_bwd_generic, g, b, 0, s, rows, dim, x, w, rstd, dy, beta_dx, dx, part);
+      hipLaunchKernelGGL(rmsnorm_bwd_generic, g, b, 0, s, rows, dim, x, w, rstd, dy, add, dx, part);
     TALOS_LAUNCHED("rmsnorm_bwd");
   }
   if (dw) return reduce_parts_launch(dim, nblk, ws, beta_dw, dw, s);

@@ -17,8 +17,11 @@ int colsum_launch(int rows, int cols, const float* dy, long long ld, float beta,
 size_t rmsnorm_bwd_workspace_bytes(int rows, int dim);
 int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
                        hipStream_t s);
+// dx = (dres ? dres : beta_dx * dx) + d rmsnorm / dx . dy; dres (the residual branch's gradient)
+// may equal dx.
 int rmsnorm_bwd_launch(int rows, int dim, const float* x, const float* w, const float* rstd, const float* dy,
-                       float beta_dx, float* dx, float beta_dw, float* dw, double* ws, hipStream_t s);
+                       float beta_dx, float* dx, float beta_dw, float* dw, double* ws, hipStream_t s,
+                       const float* dres = nullptr);
 
 // out[r] = [a[r] | b[r]]; split: da[r] (+)= g[r][:ca], db[r] (+)= g[r][ca:]
 int concat_launch(size_t rows, int ca, int cb, const float* a, const float* b, float* out, hipStream_t s);
