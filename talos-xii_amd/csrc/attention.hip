@@ -57,22 +57,49 @@ struct AttnArgs {
 
 constexpr float kNegInf = -INFINITY;
 
+// Load style per kernel (SEL of load_half) and minimum waves per SIMD the register allocation
+// must allow (compile-time tuning knobs).
+#ifndef TALOS_ATTN_FWD_SEL
+#define TALOS_ATTN_FWD_SEL 0
+#endif
+#ifndef TALOS_ATTN_BWD_SEL
+#define TALOS_ATTN_BWD_SEL 0
+#endif
+#ifndef TALOS_ATTN_FUSED_SEL
+#define TALOS_ATTN_FUSED_SEL 1
+#endif
+constexpr bool kFwdSel = TALOS_ATTN_FWD_SEL, kBwdSel = TALOS_ATTN_BWD_SEL, kFusedSel = TALOS_ATTN_FUSED_SEL;
+#ifndef TALOS_ATTN_FWD_WAVES
+#define TALOS_ATTN_FWD_WAVES 1
+#endif
+#ifndef TALOS_ATTN_BWD_WAVES
+#define TALOS_ATTN_BWD_WAVES 1
+#endif
+
+// Zeros that out-of-range rows and columns read instead of memory: selecting the address (not the
+// loaded value) keeps every load unconditional, so a lane's loads issue back to back with no
+// branch around them, and the values are exactly 0.
+__device__ __align__(16) const float kAttnZeros[128] = {};
+
 // Loads half of row `row` (elements [HALF*h, HALF*h + HALF) of the head's `dim` values starting
-// at column col0) times `scale`; rows >= S and elements >= dim read as 0.
-template <int HALF>
+// at column col0) times `scale`; rows >= S and elements >= dim read as 0. SEL = true selects the
+// address (kAttnZeros for the out-of-range rows / columns), so the loads are unconditional and
+// issue back to back at the cost of registers; SEL = false branches around them (fewer registers,
+// more waves per SIMD).
+template <int HALF, bool SEL>
 __device__ __forceinline__ void load_half(float (&r)[HALF], const float* __restrict__ base, long long ld,
                                           long long tok0, int row, int S, int col0, int dim, int h, float scale,
                                           bool vec) {
-  if (row >= S) {
+  if (!SEL && row >= S) {
 #pragma unroll
     for (int i = 0; i < HALF; ++i) r[i] = 0.f;
     return;
   }
-  const float* src = base + (tok0 + row) * ld + col0 + HALF * h;
+  const float* src = (!SEL || row < S) ? base + (tok0 + row) * ld + col0 : kAttnZeros;
   if (vec) {
 #pragma unroll
     for (int i = 0; i < HALF; i += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(src + i);
+      const float4 v = *reinterpret_cast<const float4*>(src + HALF * h + i);
       r[i] = v.x * scale;
       r[i + 1] = v.y * scale;
       r[i + 2] = v.z * scale;
@@ -80,7 +107,13 @@ __device__ __forceinline__ void load_half(float (&r)[HALF], const float* __restr
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < HALF; ++i) r[i] = (HALF * h + i < dim) ? src[i] * scale : 0.f;
+    for (int i = 0; i < HALF; ++i) {
+      const int e = HALF * h + i;
+      if (SEL)
+        r[i] = *(e < dim ? src + e : kAttnZeros + e) * scale;
+      else
+        r[i] = e < dim ? src[e] * scale : 0.f;
+    }
   }
 }
 
@@ -99,17 +132,23 @@ __device__ __forceinline__ floatx16 mfma_rows(const float (&x)[HALF], const floa
 // acc[eb] += P_block . M[rows of the block, eb*32 + lane%32] for each 32-column block eb of the
 // head: P is given in accumulator layout (register s <-> block row acc_row(s, h)), M is read
 // from global memory row by row (rows >= S and columns >= dim read as 0).
-template <int NB>
+template <int NB, bool SEL>
 __device__ __forceinline__ void mfma_p_rows(const float (&P)[16], const float* __restrict__ base, long long ld,
                                             long long tok0, int row0, int S, int col0, int dim, int l32, int h,
                                             floatx16 (&acc)[NB]) {
+  // out-of-range rows / columns read as 0 (SEL: see load_half)
 #pragma unroll
   for (int s = 0; s < 16; ++s) {
     const int row = row0 + acc_row(s, h);
-    const float* src = base + (tok0 + row) * ld + col0 + l32;
+    const float* src = base + (tok0 + row) * ld + col0;
 #pragma unroll
     for (int eb = 0; eb < NB; ++eb) {
-      const float m = (row < S && eb * 32 + l32 < dim) ? src[eb * 32] : 0.f;
+      const int e = eb * 32 + l32;
+      float m;
+      if (SEL)
+        m = *((row < S && e < dim) ? src + e : kAttnZeros + e);
+      else
+        m = (row < S && e < dim) ? src[e] : 0.f;
       acc[eb] = __builtin_amdgcn_mfma_f32_32x32x2f32(P[s], m, acc[eb], 0, 0, 0);
     }
   }
@@ -117,21 +156,26 @@ __device__ __forceinline__ void mfma_p_rows(const float (&P)[16], const float* _
 
 // Applies R^T (rotation by -theta at position pos) to an output element of column e whose
 // pair partner (column e ^ 1) sits in the neighbouring lane. All lanes must call it.
+// Branch-free: the table (kAttnZeros when there is none) is read at a clamped index and the
+// result selected, so the loads of consecutive elements issue back to back.
 __device__ __forceinline__ float rope_t(float g, int e, int pos, const AttnArgs& a, bool active) {
   const float partner = __shfl_xor(g, 1, 64);
-  if (a.rcos == nullptr || !active || e < a.rope_off || e >= a.rope_off + a.rope_dim) return g;
+  const bool table = a.rcos != nullptr;
   const int half = a.rope_dim >> 1;
-  const int pi = (e - a.rope_off) >> 1;
-  const float c = a.rcos[pos * half + pi], s = a.rsin[pos * half + pi];
+  const bool in = table && active && e >= a.rope_off && e < a.rope_off + a.rope_dim;
+  const int idx = in ? pos * half + ((e - a.rope_off) >> 1) : 0;
+  const float c = (table ? a.rcos : kAttnZeros)[idx], s = (table ? a.rsin : kAttnZeros)[idx];
   // (g0, g1) -> (g0 c + g1 s, -g0 s + g1 c)
-  return (e & 1) ? fmaf(-partner, s, g * c) : fmaf(g, c, partner * s);
+  const float rot = (e & 1) ? fmaf(-partner, s, g * c) : fmaf(g, c, partner * s);
+  return in ? rot : g;
 }
 
 // ---------------------------------------------------------------------------
 // Forward: wave per (pair, query block)
 // ---------------------------------------------------------------------------
 template <int DKM, int DVM>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_FWD_WAVES))) void attn_fwd_kernel(
+    AttnArgs a) {
   constexpr int KH = DKM / 2, OB = DVM / 32;
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
   const int nqb = (a.S + 31) >> 5;
@@ -143,13 +187,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const int q = qb * 32 + l32;  // this lane's query (score columns)
 
   float qv[KH];
-  load_half<KH>(qv, a.q, a.ldq, tok0, q, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
+  load_half<KH, kFwdSel>(qv, a.q, a.ldq, tok0, q, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
   const int kb_last = a.causal ? qb : (a.S - 1) >> 5;
 
   // scores of key block kb in S^T layout, masked
   auto scores = [&](int kb, float (&sv)[16]) {
     float kv[KH];
-    load_half<KH>(kv, a.k, a.ldk, tok0, kb * 32 + l32, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
+    load_half<KH, kFwdSel>(kv, a.k, a.ldk, tok0, kb * 32 + l32, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
     floatx16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
@@ -192,7 +236,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     float P[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) P[r] = (m == kNegInf) ? 0.f : expf(sv[r] - m) * inv_l;
-    mfma_p_rows<OB>(P, a.v, a.ldv, tok0, kb * 32, a.S, hd * a.dv, a.dv, l32, h, oacc);
+    mfma_p_rows<OB, kFwdSel>(P, a.v, a.ldv, tok0, kb * 32, a.S, hd * a.dv, a.dv, l32, h, oacc);
   }
   // O in accumulator layout: register r <-> query qb*32 + acc_row(r, h), lane <-> column
 #pragma unroll
@@ -222,12 +266,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   const int q = qb * 32 + l32;
 
   float qv[KH], gv[VH];
-  load_half<KH>(qv, a.q, a.ldq, tok0, q, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
-  load_half<VH>(gv, a.dout, a.lddo, tok0, q, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+  load_half<KH, kBwdSel>(qv, a.q, a.ldq, tok0, q, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
+  load_half<VH, kBwdSel>(gv, a.dout, a.lddo, tok0, q, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
   float D;
   {
     float ov[VH];
-    load_half<VH>(ov, a.o, a.ldo, tok0, q, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+    load_half<VH, kBwdSel>(ov, a.o, a.ldo, tok0, q, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
     float d0 = 0.f, d1 = 0.f;
 #pragma unroll
     for (int i = 0; i < VH; i += 2) {
@@ -238,7 +282,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     D += __shfl_xor(D, 32, 64);
   }
   const bool qok = q < a.S;
-  const float lse = qok ? a.lse[(long long)pair * a.S + q] : 0.f;
+  const float lse = a.lse[(long long)pair * a.S + (qok ? q : 0)];
   if (h == 0 && qok) a.D[(long long)pair * a.S + q] = D;
 
   floatx16 dq[QB];
@@ -253,12 +297,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
     {
       float kv[KH];
-      load_half<KH>(kv, a.k, a.ldk, tok0, kb * 32 + l32, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
+      load_half<KH, kBwdSel>(kv, a.k, a.ldk, tok0, kb * 32 + l32, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
       sacc = mfma_rows<KH>(kv, qv, sacc);
     }
     {
       float vv[VH];
-      load_half<VH>(vv, a.v, a.ldv, tok0, kb * 32 + l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+      load_half<VH, kBwdSel>(vv, a.v, a.ldv, tok0, kb * 32 + l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
       pacc = mfma_rows<VH>(vv, gv, pacc);
     }
     float dS[16];
@@ -266,10 +310,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int key = kb * 32 + acc_row(r, h);
       const bool ok = qok && key < a.S && (!a.causal || key <= q);
-      const float p = ok ? expf(sacc[r] - lse) : 0.f;
+      const float p = expf(ok ? sacc[r] - lse : kNegInf);
       dS[r] = p * (pacc[r] - D);
     }
-    mfma_p_rows<QB>(dS, a.k, a.ldk, tok0, kb * 32, a.S, hd * a.dk, a.dk, l32, h, dq);
+    mfma_p_rows<QB, kBwdSel>(dS, a.k, a.ldk, tok0, kb * 32, a.S, hd * a.dk, a.dk, l32, h, dq);
   }
 #pragma unroll
   for (int i = 0; i < QB; ++i)
@@ -298,8 +342,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a) {
   const int key = kb * 32 + l32;
 
   float kv[KH], vv[VH];
-  load_half<KH>(kv, a.k, a.ldk, tok0, key, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
-  load_half<VH>(vv, a.v, a.ldv, tok0, key, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+  load_half<KH, kBwdSel>(kv, a.k, a.ldk, tok0, key, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
+  load_half<VH, kBwdSel>(vv, a.v, a.ldv, tok0, key, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
   floatx16 dk[KB], dv[VB];
 #pragma unroll
   for (int i = 0; i < KB; ++i)
@@ -317,12 +361,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
     {
       float qv[KH];
-      load_half<KH>(qv, a.q, a.ldq, tok0, qb * 32 + l32, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
+      load_half<KH, kBwdSel>(qv, a.q, a.ldq, tok0, qb * 32 + l32, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
       sacc = mfma_rows<KH>(qv, kv, sacc);  // S[q, key]
     }
     {
       float gq[VH];
-      load_half<VH>(gq, a.dout, a.lddo, tok0, qb * 32 + l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+      load_half<VH, kBwdSel>(gq, a.dout, a.lddo, tok0, qb * 32 + l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
       pacc = mfma_rows<VH>(gq, vv, pacc);  // dP[q, key]
     }
     float P[16], dS[16];
@@ -331,12 +375,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a) {
       const int qr = qb * 32 + acc_row(r, h);
       const bool ok = kok && qr < a.S && (!a.causal || key <= qr);
       const long long li = (long long)pair * a.S + (qr < a.S ? qr : 0);
-      const float p = ok ? expf(sacc[r] - a.lse[li]) : 0.f;
+      const float lse_r = a.lse[li], d_r = a.D[li];  // unconditional loads (clamped index)
+      const float p = expf(ok ? sacc[r] - lse_r : kNegInf);
       P[r] = p;
-      dS[r] = p * (pacc[r] - (ok ? a.D[li] : 0.f));
+      dS[r] = p * (pacc[r] - d_r);
     }
-    mfma_p_rows<VB>(P, a.dout, a.lddo, tok0, qb * 32, a.S, hd * a.dv, a.dv, l32, h, dv);
-    mfma_p_rows<KB>(dS, a.q, a.ldq, tok0, qb * 32, a.S, hd * a.dk, a.dk, l32, h, dk);
+    mfma_p_rows<VB, kBwdSel>(P, a.dout, a.lddo, tok0, qb * 32, a.S, hd * a.dv, a.dv, l32, h, dv);
+    mfma_p_rows<KB, kBwdSel>(dS, a.q, a.ldq, tok0, qb * 32, a.S, hd * a.dk, a.dk, l32, h, dk);
   }
   // dK / dV in accumulator layout: register r <-> key kb*32 + acc_row(r, h), lane <-> column
 #pragma unroll
@@ -355,6 +400,133 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a) {
       const int kr = kb * 32 + acc_row(r, h);
       const int e = i * 32 + l32;
       if (kr < a.S && e < a.dv) a.dv_out[(tok0 + kr) * a.lddv + hd * a.dv + e] = dv[i][r];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Single-block backward (seq <= 32): one wave per (batch, head) pair computes dQ, dK and dV from
+// one read of q, k, v, o and dO (D = dO . O is formed in the wave). S layout (lane <-> key,
+// register r <-> query acc_row(r, h)); dS is transposed through the wave's LDS slice for dQ.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+constexpr int kTS = 33;  // pitch of the transposed dS tile: a column read touches 32 banks
+
+template <int DKM, int DVM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BWD_WAVES))) void
+attn_bwd_fused_kernel(AttnArgs a) {
+  constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32;
+  __shared__ __align__(16) float lds[4][32 * kTS + 64];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int pair = blockIdx.x * 4 + wv;
+  if (pair >= a.B * a.H) return;  // uniform per wave; the kernel has no workgroup barrier
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  float* T = lds[wv];           // dS^T staging [query][key]
+  float* Dl = T + 32 * kTS;     // D[query]
+  float* Ll = Dl + 32;          // lse[query]
+  const bool rok = l32 < a.S;   // this lane's row (query l32 of q / dO / O, key l32 of k / v)
+
+  float gv[VH];
+  load_half<VH, kFusedSel>(gv, a.dout, a.lddo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+  {
+    float ov[VH];
+    load_half<VH, kFusedSel>(ov, a.o, a.ldo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < VH; i += 2) {
+      d0 = fmaf(gv[i], ov[i], d0);
+      d1 = fmaf(gv[i + 1], ov[i + 1], d1);
+    }
+    float D = d0 + d1;
+    D += __shfl_xor(D, 32, 64);
+    const float lse = a.lse[(long long)pair * a.S + (rok ? l32 : 0)];
+    if (h == 0) {
+      Dl[l32] = rok ? D : 0.f;
+      Ll[l32] = rok ? lse : 0.f;
+    }
+  }
+  floatx16 sacc, pacc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
+  {
+    float qv[KH], kv[KH];
+    load_half<KH, kFusedSel>(qv, a.q, a.ldq, tok0, l32, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
+    load_half<KH, kFusedSel>(kv, a.k, a.ldk, tok0, l32, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
+    sacc = mfma_rows<KH>(qv, kv, sacc);  // S[q, key]
+  }
+  {
+    float vv[VH];
+    load_half<VH, kFusedSel>(vv, a.v, a.ldv, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+    pacc = mfma_rows<VH>(gv, vv, pacc);  // dP[q, key]
+  }
+  wave_lds_sync();
+  // lse / D of the queries acc_row(4j .. 4j+3, h) = 8j + 4h + 0..3: one 16-byte read each
+  float lq[16], dq_[16];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float4 l4 = *reinterpret_cast<const float4*>(Ll + 8 * j + 4 * h);
+    const float4 d4 = *reinterpret_cast<const float4*>(Dl + 8 * j + 4 * h);
+    lq[4 * j] = l4.x; lq[4 * j + 1] = l4.y; lq[4 * j + 2] = l4.z; lq[4 * j + 3] = l4.w;
+    dq_[4 * j] = d4.x; dq_[4 * j + 1] = d4.y; dq_[4 * j + 2] = d4.z; dq_[4 * j + 3] = d4.w;
+  }
+  float P[16], dS[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int qr = acc_row(r, h);
+    const bool ok = rok && qr < a.S && (!a.causal || l32 <= qr);
+    const float p = expf(ok ? sacc[r] - lq[r] : kNegInf);  // exp(-inf) = 0: no branch
+    P[r] = p;
+    dS[r] = p * (pacc[r] - dq_[r]);
+    T[qr * kTS + l32] = dS[r];
+  }
+  floatx16 dk[KB], dv[VB];
+#pragma unroll
+  for (int i = 0; i < KB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dk[i][r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < VB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dv[i][r] = 0.f;
+  mfma_p_rows<VB, kFusedSel>(P, a.dout, a.lddo, tok0, 0, a.S, hd * a.dv, a.dv, l32, h, dv);  // dV = P^T . dO
+  mfma_p_rows<KB, kFusedSel>(dS, a.q, a.ldq, tok0, 0, a.S, hd * a.dk, a.dk, l32, h, dk);     // dK = dS^T . Q
+  wave_lds_sync();
+  float dST[16];  // lane <-> query l32, register r <-> key acc_row(r, h)
+#pragma unroll
+  for (int r = 0; r < 16; ++r) dST[r] = T[l32 * kTS + acc_row(r, h)];
+  floatx16 dq[KB];
+#pragma unroll
+  for (int i = 0; i < KB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
+  mfma_p_rows<KB, kFusedSel>(dST, a.k, a.ldk, tok0, 0, a.S, hd * a.dk, a.dk, l32, h, dq);  // dQ = dS . K
+  // row acc_row(r, h) of each result: a query for dQ, a key for dK / dV; lane <-> column
+#pragma unroll
+  for (int i = 0; i < KB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = acc_row(r, h);
+      const int e = i * 32 + l32;
+      const bool ok = row < a.S;
+      const float gq = rope_t(dq[i][r] * a.scale, e, row, a, ok);
+      const float gk = rope_t(dk[i][r] * a.scale, e, row, a, ok);
+      if (ok && e < a.dk) {
+        a.dq[(tok0 + row) * a.lddq + hd * a.dk + e] = gq;
+        a.dk_out[(tok0 + row) * a.lddk + hd * a.dk + e] = gk;
+      }
+    }
+#pragma unroll
+  for (int i = 0; i < VB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = acc_row(r, h);
+      const int e = i * 32 + l32;
+      if (row < a.S && e < a.dv) a.dv_out[(tok0 + row) * a.lddv + hd * a.dv + e] = dv[i][r];
     }
 }
 
@@ -448,6 +620,15 @@ static int attn_bwd_dkv(const AttnArgs& a, int dkm, int dvm, hipStream_t s) {
   ATTN_ALL(attn_bwd_dkv_kernel)
 }
 
+static int attn_bwd_fused(const AttnArgs& a, int dkm, int dvm, hipStream_t s) {
+  dim3 grid(ceil_div((size_t)a.B * a.H, 4));
+  const double rows = (double)a.B * a.S * a.H;
+  // s = q.k, dp = dO.v, dv = p^T dO, dk = ds^T q, dq = ds k; reads q k v o dO lse, writes dq dk dv
+  const double flops = kept_pairs(a) * (6.0 * a.dk + 4.0 * a.dv);
+  const double bytes = 4.0 * rows * (4.0 * a.dk + 4.0 * a.dv + 1.0);
+  ATTN_ALL(attn_bwd_fused_kernel)
+}
+
 int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
   int dkm, dvm;
   if (!pick_dims(d.dk, d.dv, &dkm, &dvm)) {
@@ -457,6 +638,7 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
   AttnArgs a = make_args(d, dkm, dvm);
   a.D = ws;
   if ((long long)a.B * a.H * a.S == 0) return TALOS_OK;
+  if (a.S <= 32) return attn_bwd_fused(a, dkm, dvm, s);
   int rc = attn_bwd_dq(a, dkm, dvm, s);
   if (rc) return rc;
   return attn_bwd_dkv(a, dkm, dvm, s);

@@ -215,7 +215,10 @@ def test_rope_start_pos_and_accumulate(oracle):
 # --- attention ----------------------------------------------------------------------------
 @pytest.mark.parametrize("causal", [0, 1])
 @pytest.mark.parametrize("B,S,H,dk,dv", [(2, 7, 3, 5, 4), (3, 32, 4, 32, 32), (2, 64, 4, 32, 32),
-                                         (1, 200, 2, 96, 64), (2, 300, 1, 16, 16)])
+                                         (1, 200, 2, 96, 64), (2, 300, 1, 16, 16),
+                                         # seq <= 32: the single-block backward at every head-dim class
+                                         (2, 20, 3, 64, 64), (2, 32, 2, 96, 64), (1, 17, 2, 128, 128),
+                                         (2, 31, 3, 40, 24), (5, 1, 2, 32, 32)])
 def test_attention_fwd_bwd_vs_oracle(oracle, causal, B, S, H, dk, dv):
     rng = np.random.default_rng(500 + S + dk + causal)
     q, k = f32(rng.normal(size=(B, S, H, dk))), f32(rng.normal(size=(B, S, H, dk)))
