@@ -105,14 +105,50 @@ __global__ __launch_bounds__(1024) void reduce_parts_kernel(int cols, int nparts
   }
 }
 
-int reduce_parts_launch(int cols, int nparts, const double* part, float beta, float* out, hipStream_t s) {
+// First level for many partials: workgroup (x = 64-column group, y = group of kGroupParts
+// partials) sums its group in a fixed order into part2[y][c], so the final pass reads at most
+// nparts / kGroupParts rows instead of one workgroup per 64 columns reading all of them.
+constexpr int kGroupParts = 32;
+__global__ __launch_bounds__(256) void group_parts_kernel(int cols, int nparts, const double* __restrict__ part,
+                                                          double* __restrict__ part2) {
+  __shared__ double red[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  const int p0 = blockIdx.y * kGroupParts, p1 = min(nparts, p0 + kGroupParts);
+  double acc = 0.0;
+  if (c < cols)
+    for (int p = p0 + w; p < p1; p += 4) acc += part[(long long)p * cols + c];
+  red[w][lane] = acc;
+  __syncthreads();
+  if (w == 0 && c < cols)
+    part2[(long long)blockIdx.y * cols + c] = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+}
+
+static int grouped_parts(int nparts) { return nparts > 2 * kGroupParts ? (nparts + kGroupParts - 1) / kGroupParts : 0; }
+
+// Workspace rows (of cols doubles) a reduction over nparts partials needs: the partials and the
+// first level's group sums after them.
+static size_t parts_rows(int nparts) { return (size_t)nparts + grouped_parts(nparts); }
+
+int reduce_parts_launch(int cols, int nparts, double* part, float beta, float* out, hipStream_t s) {
+  const int groups = grouped_parts(nparts);
+  if (groups > 0) {
+    // part is the start of a workspace of parts_rows(nparts) rows (every caller sizes it so)
+    double* part2 = part + (size_t)nparts * cols;
+    ProfScope ps(s, "group_parts_kernel", (double)nparts * cols, 8.0 * (nparts + groups) * cols);
+    hipLaunchKernelGGL(group_parts_kernel, dim3(ceil_div(cols, 64), groups), dim3(256), 0, s, cols, nparts, part,
+                       part2);
+    TALOS_LAUNCHED("group_parts_kernel");
+    part = part2;
+    nparts = groups;
+  }
   ProfScope ps(s, "reduce_parts_kernel", (double)nparts * cols, 8.0 * nparts * cols + 4.0 * cols);
   hipLaunchKernelGGL(reduce_parts_kernel, dim3(ceil_div(cols, 64)), dim3(1024), 0, s, cols, nparts, part, beta, out);
   TALOS_LAUNCHED("reduce_parts_kernel");
   return TALOS_OK;
 }
 
-size_t colsum_workspace_bytes(int rows, int cols) { return (size_t)colsum_parts(rows) * cols * sizeof(double); }
+size_t colsum_workspace_bytes(int rows, int cols) { return parts_rows(colsum_parts(rows)) * cols * sizeof(double); }
 
 int colsum_launch(int rows, int cols, const float* dy, long long ld, float beta, float* out, double* ws,
                   hipStream_t s) {
@@ -286,7 +322,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_generic(int rows, int dim, co
 }
 
 size_t rmsnorm_bwd_workspace_bytes(int rows, int dim) {
-  return (size_t)rms_bwd_blocks(rows) * dim * sizeof(double);
+  return parts_rows(rms_bwd_blocks(rows)) * dim * sizeof(double);
 }
 
 int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
