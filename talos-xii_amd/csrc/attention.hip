@@ -416,23 +416,62 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 constexpr int kTS = 33;  // pitch of the transposed dS tile: a column read touches 32 banks
 
+// Stores this lane's half row (the load_half layout) into row l32 of an LDS tile of pitch TP.
+template <int HALF, int TP>
+__device__ __forceinline__ void stage_half(float* tile, const float (&r)[HALF], int l32, int h) {
+#pragma unroll
+  for (int i = 0; i < HALF; i += 4)
+    *reinterpret_cast<float4*>(tile + l32 * TP + HALF * h + i) = make_float4(r[i], r[i + 1], r[i + 2], r[i + 3]);
+}
+
+// mfma_p_rows with the operand rows read from an LDS tile of pitch TP (rows >= S hold zeros).
+template <int NB, int TP>
+__device__ __forceinline__ void mfma_p_lds(const float (&P)[16], const float* tile, int l32, int h,
+                                           floatx16 (&acc)[NB]) {
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const float* src = tile + acc_row(s, h) * TP + l32;
+#pragma unroll
+    for (int eb = 0; eb < NB; ++eb)
+      acc[eb] = __builtin_amdgcn_mfma_f32_32x32x2f32(P[s], src[eb * 32], acc[eb], 0, 0, 0);
+  }
+}
+
+#ifndef TALOS_ATTN_STAGE
+#define TALOS_ATTN_STAGE 1
+#endif
+
 template <int DKM, int DVM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BWD_WAVES))) void
 attn_bwd_fused_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32;
-  __shared__ __align__(16) float lds[4][32 * kTS + 64];
+  // STAGE (head dims 32): the dO, Q and K rows the wave loads are also written to its LDS slice,
+  // and the three P-products read them there instead of re-reading global memory. The dS^T tile
+  // then reuses the dO tile.
+  constexpr bool STAGE = TALOS_ATTN_STAGE && DKM == 32 && DVM == 32;
+  // staged tile pitch: 16-byte rows; the dS^T tile (pitch kTS) spills from the dO tile into the
+  // Q tile, which is dead by then; 12.5 KB per wave keeps three workgroups on a CU
+  constexpr int TP = 32;
+  constexpr int WSZ = STAGE ? 3 * 32 * TP + 64 : 32 * kTS + 64;
+  __shared__ __align__(16) float lds[4][WSZ];
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
   const int pair = blockIdx.x * 4 + wv;
   if (pair >= a.B * a.H) return;  // uniform per wave; the kernel has no workgroup barrier
   const int b = pair / a.H, hd = pair % a.H;
   const long long tok0 = (long long)b * a.S;
-  float* T = lds[wv];           // dS^T staging [query][key]
-  float* Dl = T + 32 * kTS;     // D[query]
-  float* Ll = Dl + 32;          // lse[query]
-  const bool rok = l32 < a.S;   // this lane's row (query l32 of q / dO / O, key l32 of k / v)
+  float* const W = lds[wv];
+  float* const Gs = W;             // staged dO [query][e]
+  float* const Qs = W + 32 * TP;   // staged scale * Q [query][e]
+  float* const Ks = W + 64 * TP;   // staged K [key][e]
+  float* const T = W;              // dS^T [query][key] (pitch kTS)
+  static_assert(!STAGE || 32 * kTS <= 64 * TP, "the dS^T tile must end before the K tile");
+  float* const Dl = W + (STAGE ? 96 * TP : 32 * kTS);  // D[query]
+  float* const Ll = Dl + 32;                            // lse[query]
+  const bool rok = l32 < a.S;  // this lane's row (query l32 of q / dO / O, key l32 of k / v)
 
   float gv[VH];
   load_half<VH, kFusedSel>(gv, a.dout, a.lddo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+  if constexpr (STAGE) stage_half<VH, TP>(Gs, gv, l32, h);
   {
     float ov[VH];
     load_half<VH, kFusedSel>(ov, a.o, a.ldo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
@@ -457,6 +496,10 @@ attn_bwd_fused_kernel(AttnArgs a) {
     float qv[KH], kv[KH];
     load_half<KH, kFusedSel>(qv, a.q, a.ldq, tok0, l32, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
     load_half<KH, kFusedSel>(kv, a.k, a.ldk, tok0, l32, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
+    if constexpr (STAGE) {
+      stage_half<KH, TP>(Qs, qv, l32, h);
+      stage_half<KH, TP>(Ks, kv, l32, h);
+    }
     sacc = mfma_rows<KH>(qv, kv, sacc);  // S[q, key]
   }
   {
@@ -482,7 +525,7 @@ attn_bwd_fused_kernel(AttnArgs a) {
     const float p = expf(ok ? sacc[r] - lq[r] : kNegInf);  // exp(-inf) = 0: no branch
     P[r] = p;
     dS[r] = p * (pacc[r] - dq_[r]);
-    T[qr * kTS + l32] = dS[r];
+    if constexpr (!STAGE) T[qr * kTS + l32] = dS[r];
   }
   floatx16 dk[KB], dv[VB];
 #pragma unroll
@@ -493,8 +536,16 @@ attn_bwd_fused_kernel(AttnArgs a) {
   for (int i = 0; i < VB; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) dv[i][r] = 0.f;
-  mfma_p_rows<VB, kFusedSel>(P, a.dout, a.lddo, tok0, 0, a.S, hd * a.dv, a.dv, l32, h, dv);  // dV = P^T . dO
-  mfma_p_rows<KB, kFusedSel>(dS, a.q, a.ldq, tok0, 0, a.S, hd * a.dk, a.dk, l32, h, dk);     // dK = dS^T . Q
+  if constexpr (STAGE) {
+    mfma_p_lds<VB, TP>(P, Gs, l32, h, dv);   // dV = P^T . dO
+    mfma_p_lds<KB, TP>(dS, Qs, l32, h, dk);  // dK = dS^T . (scale Q)
+    wave_lds_sync();                         // the dO tile is free: dS^T goes there
+#pragma unroll
+    for (int r = 0; r < 16; ++r) T[acc_row(r, h) * kTS + l32] = dS[r];
+  } else {
+    mfma_p_rows<VB, kFusedSel>(P, a.dout, a.lddo, tok0, 0, a.S, hd * a.dv, a.dv, l32, h, dv);  // dV = P^T . dO
+    mfma_p_rows<KB, kFusedSel>(dS, a.q, a.ldq, tok0, 0, a.S, hd * a.dk, a.dk, l32, h, dk);     // dK = dS^T . Q
+  }
   wave_lds_sync();
   float dST[16];  // lane <-> query l32, register r <-> key acc_row(r, h)
 #pragma unroll
@@ -504,7 +555,11 @@ attn_bwd_fused_kernel(AttnArgs a) {
   for (int i = 0; i < KB; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
-  mfma_p_rows<KB, kFusedSel>(dST, a.k, a.ldk, tok0, 0, a.S, hd * a.dk, a.dk, l32, h, dq);  // dQ = dS . K
+  if constexpr (STAGE)
+    mfma_p_lds<KB, TP>(dST, Ks, l32, h, dq);  // dQ = dS . K
+  else
+    mfma_p_rows<KB, kFusedSel>(dST, a.k, a.ldk, tok0, 0, a.S, hd * a.dk, a.dk, l32, h, dq);  // dQ = dS . K
+  const float dk_scale = STAGE ? 1.f : a.scale;  // the staged Q already carries the scale
   // row acc_row(r, h) of each result: a query for dQ, a key for dK / dV; lane <-> column
 #pragma unroll
   for (int i = 0; i < KB; ++i)
@@ -514,7 +569,7 @@ attn_bwd_fused_kernel(AttnArgs a) {
       const int e = i * 32 + l32;
       const bool ok = row < a.S;
       const float gq = rope_t(dq[i][r] * a.scale, e, row, a, ok);
-      const float gk = rope_t(dk[i][r] * a.scale, e, row, a, ok);
+      const float gk = rope_t(dk[i][r] * dk_scale, e, row, a, ok);
       if (ok && e < a.dk) {
         a.dq[(tok0 + row) * a.lddq + hd * a.dk + e] = gq;
         a.dk_out[(tok0 + row) * a.lddk + hd * a.dk + e] = gk;
