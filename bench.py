@@ -121,6 +121,40 @@ def cpu_baseline(cfg_t, seconds_budget=20.0):
             "batched_sample": f"{n_b} samples as one batched f64 graph"}
 
 
+def optimizer_line(P, dP, steps):
+    """The optimizer step on the minibatch's gradients, timed apart from fwd+bwd: Adam over every
+    parameter (src/ppo.rs:519-533; 28 B of HBM traffic per parameter) and the DQN variant with
+    its global-norm clip (src/dqn.rs:207-239; + one 4 B gradient read for the norm)."""
+    n = P.size
+    m, v = th.DeviceArray.zeros(n), th.DeviceArray.zeros(n)
+    sumsq = th.DeviceArray.zeros(1, np.float64)
+    ws = th.DeviceArray.zeros(th.lib().talos_grad_sumsq_workspace_bytes() // 8, np.float64)
+    # a copy of the parameters: the timed steps must not move the ones the fwd+bwd line used
+    Pc = th.DeviceArray.zeros(n)
+    th.call("talos_memcpy_d2d", Pc.ptr, P.ptr, 4 * n, None)
+    timer = th.Timer(None)
+    res = {"params": n}
+    for name, clip in (("adam", False), ("adam_global_norm_clip", True)):
+        def one(t):
+            if clip:
+                th.call("talos_grad_sumsq_f32", n, dP.ptr, 0, sumsq.ptr, ws.ptr, None)
+            th.call("talos_adam_step_f32", n, Pc.ptr, dP.ptr, m.ptr, v.ptr, t, 3e-4, 0.9, 0.999, 1e-8,
+                    sumsq.ptr if clip else None, 1.0, None)
+        for t in range(1, 4):
+            one(t)
+        th.sync()
+        timer.start()
+        for t in range(4, 4 + steps):
+            one(t)
+        us = timer.stop_ms() / steps * 1e3
+        nbytes = 28.0 * n + (4.0 * n if clip else 0.0)
+        res[name] = {"us_per_step": round(us, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+    for a in (m, v, sumsq, ws, Pc):
+        a.free()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -219,6 +253,7 @@ def main():
                     for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3])},
         "device": info["name"],
     }
+    out["optimizer"] = optimizer_line(P, dP, args.steps)
     if args.profile_table:
         for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3]):
             print(f"{k:40s} n={v[0]:3d} {v[3]:8.3f} ms  {v[1] / max(v[3], 1e-9) / 1e9:8.2f} TFLOP/s "

@@ -193,8 +193,12 @@ int talos_broadcast_rows_f32(size_t rows, int cols, const float* v, float* out, 
 /* sumsq[0] = (accumulate ? sumsq[0] : 0) + sum_i grads[i]^2, summed in f64: the global-norm
  * loop of the DQN optimizer (dqn.rs:207-214). sumsq is ONE device double; several parameter
  * tensors share one norm by calling this once per tensor with accumulate = 1 after the first.
+ * workspace: NULL (the call allocates and frees its partial sums on the stream) or a device
+ * buffer of talos_grad_sumsq_workspace_bytes() bytes, reused across calls on one stream.
  * Deterministic (fixed partition of the partial sums). */
-int talos_grad_sumsq_f32(size_t n, const float* grads, int accumulate, double* sumsq, talos_stream_t stream);
+size_t talos_grad_sumsq_workspace_bytes(void);
+int talos_grad_sumsq_f32(size_t n, const float* grads, int accumulate, double* sumsq, double* workspace,
+                         talos_stream_t stream);
 
 /* One Adam step over n parameters, Adam::step (ppo.rs:519-533):
  *   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2;

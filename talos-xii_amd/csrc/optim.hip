@@ -164,11 +164,15 @@ using namespace talos;
 
 extern "C" {
 
-int talos_grad_sumsq_f32(size_t n, const float* grads, int accumulate, double* sumsq, talos_stream_t stream) {
+size_t talos_grad_sumsq_workspace_bytes(void) { return grad_sumsq_workspace_bytes(); }
+
+int talos_grad_sumsq_f32(size_t n, const float* grads, int accumulate, double* sumsq, double* workspace,
+                         talos_stream_t stream) {
   TALOS_NONNULL(sumsq);
   TALOS_REQUIRE(n == 0 || grads != nullptr, TALOS_ERR_NULL, "%s: null pointer argument 'grads'", __func__);
   TALOS_DEVICE();
   hipStream_t s = as_stream(stream);
+  if (workspace) return grad_sumsq_launch(n, grads, accumulate, sumsq, workspace, s);
   double* ws = nullptr;
   TALOS_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), grad_sumsq_workspace_bytes(), s));
   const int rc = grad_sumsq_launch(n, grads, accumulate, sumsq, ws, s);

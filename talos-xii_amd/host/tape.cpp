@@ -366,9 +366,9 @@ Adam::Adam(std::vector<Tensor> params, double lr, double max_grad_norm)
     ok(talos_fill_zero(m_.back()->ptr, p.numel() * sizeof(float), nullptr), "fill_zero");
     ok(talos_fill_zero(v_.back()->ptr, p.numel() * sizeof(float), nullptr), "fill_zero");
   }
-  if (max_norm_ > 0.0) {
+  if (max_norm_ > 0.0) {  // the norm and the partial sums behind it, allocated once
     void* p = nullptr;
-    ok(talos_malloc(&p, sizeof(double)), "talos_malloc");
+    ok(talos_malloc(&p, sizeof(double) + talos_grad_sumsq_workspace_bytes()), "talos_malloc");
     sumsq_ = static_cast<double*>(p);
   }
 }
@@ -381,7 +381,8 @@ void Adam::step() {
   ++t_;
   if (sumsq_) {  // src/dqn.rs:207-214: one norm over every parameter's gradient
     for (size_t i = 0; i < params_.size(); ++i)
-      ok(talos_grad_sumsq_f32(params_[i].numel(), params_[i].grad_->ptr, i > 0, sumsq_, nullptr), "grad_sumsq");
+      ok(talos_grad_sumsq_f32(params_[i].numel(), params_[i].grad_->ptr, i > 0, sumsq_, sumsq_ + 1, nullptr),
+         "grad_sumsq");
   }
   for (size_t i = 0; i < params_.size(); ++i) {
     const Tensor& p = params_[i];

@@ -154,7 +154,7 @@ class Adam {
  private:
   std::vector<Tensor> params_;
   std::vector<std::unique_ptr<Storage>> m_, v_;
-  double* sumsq_ = nullptr;  // one device double (clipping only)
+  double* sumsq_ = nullptr;  // clipping only: the norm, then the partial-sum workspace
   size_t t_ = 0;
   double lr_, max_norm_;
 };

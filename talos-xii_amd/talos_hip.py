@@ -97,7 +97,8 @@ _SIGS = {
     "talos_concat_last_f32": [_sz, _i, _i, _vp, _vp, _vp, _vp],
     "talos_concat_last_bwd_f32": [_sz, _i, _i, _vp, _vp, _vp, _vp],
     "talos_broadcast_rows_f32": [_sz, _i, _vp, _vp, _vp],
-    "talos_grad_sumsq_f32": [_sz, _vp, _i, _vp, _vp],
+    "talos_grad_sumsq_workspace_bytes": [],
+    "talos_grad_sumsq_f32": [_sz, _vp, _i, _vp, _vp, _vp],
     "talos_adam_step_f32": [_sz, _vp, _vp, _vp, _vp, _i, ctypes.c_double, ctypes.c_double, ctypes.c_double,
                             ctypes.c_double, _vp, ctypes.c_double, _vp],
     "talos_block_param_count": [ctypes.POINTER(BlockCfg)],
@@ -121,7 +122,7 @@ class ProfRecord(ctypes.Structure):
     _fields_ = [("kernel", ctypes.c_char * 64), ("flops", ctypes.c_double), ("bytes", ctypes.c_double),
                 ("ms", ctypes.c_float)]
 _RESTYPE = {"talos_last_error": ctypes.c_char_p, "talos_version": ctypes.c_char_p,
-            "talos_block_param_count": _sz, "talos_ppo_param_count": _sz, "talos_mla_param_count": _sz}
+            "talos_grad_sumsq_workspace_bytes": _sz, "talos_block_param_count": _sz, "talos_ppo_param_count": _sz, "talos_mla_param_count": _sz}
 
 _lib = None
 

@@ -118,5 +118,6 @@ def test_optimizer_argument_errors(L):
     assert L.talos_adam_step_f32(4, p, p, p, p, 1, 1e-3, *args, p, 0.0, None) == th.ERR_SHAPE  # max_norm
     assert L.talos_adam_step_f32(4, None, p, p, p, 1, 1e-3, *args, None, 0.0, None) == th.ERR_NULL
     assert L.talos_adam_step_f32(0, None, None, None, None, 1, 1e-3, *args, None, 0.0, None) == th.OK
-    assert L.talos_grad_sumsq_f32(4, p, 0, None, None) == th.ERR_NULL
-    assert L.talos_grad_sumsq_f32(4, None, 0, p, None) == th.ERR_NULL
+    assert L.talos_grad_sumsq_f32(4, p, 0, None, None, None) == th.ERR_NULL
+    assert L.talos_grad_sumsq_f32(4, None, 0, p, None, None) == th.ERR_NULL
+    assert L.talos_grad_sumsq_workspace_bytes() >= 8

@@ -80,12 +80,13 @@ def test_adam_global_norm_clip_multi_tensor(oracle, scale):
     dms = [DA.zeros(s) for s in sizes]
     dvs = [DA.zeros(s) for s in sizes]
     sumsq = DA.zeros(1, np.float64)
+    ws = DA.zeros(th.lib().talos_grad_sumsq_workspace_bytes() // 8, np.float64)  # caller workspace from t = 2
     lr = 1e-2
     for t in range(1, 4):
         g = f32(rng.normal(size=n) * scale / np.sqrt(n))
         dgs = [DA.from_numpy(x) for x in np.split(g, np.cumsum(sizes)[:-1])]
         for i, dg in enumerate(dgs):
-            th.call("talos_grad_sumsq_f32", sizes[i], dg.ptr, int(i > 0), sumsq.ptr, None)
+            th.call("talos_grad_sumsq_f32", sizes[i], dg.ptr, int(i > 0), sumsq.ptr, ws.ptr if t > 1 else None, None)
         ref_ss = float(np.sum(g.astype(np.float64) ** 2))
         got_ss = float(sumsq.numpy()[0])
         assert abs(got_ss - ref_ss) <= 1e-12 * ref_ss, (got_ss, ref_ss)
@@ -105,15 +106,15 @@ def test_adam_global_norm_clip_multi_tensor(oracle, scale):
 def test_grad_sumsq_edges_and_determinism():
     rng = np.random.default_rng(3)
     sumsq = DA.from_numpy(np.array([2.5]), np.float64)
-    th.call("talos_grad_sumsq_f32", 0, None, 1, sumsq.ptr, None)  # empty, accumulate: unchanged
+    th.call("talos_grad_sumsq_f32", 0, None, 1, sumsq.ptr, None, None)  # empty, accumulate: unchanged
     assert sumsq.numpy()[0] == 2.5
-    th.call("talos_grad_sumsq_f32", 0, None, 0, sumsq.ptr, None)  # empty, overwrite: zero
+    th.call("talos_grad_sumsq_f32", 0, None, 0, sumsq.ptr, None, None)  # empty, overwrite: zero
     assert sumsq.numpy()[0] == 0.0
     g = f32(rng.normal(size=3_000_001))
     dg = DA.from_numpy(g)
     results = []
     for off in (0, 0, 1):
-        th.call("talos_grad_sumsq_f32", g.size - off, dg.offset(off), 0, sumsq.ptr, None)
+        th.call("talos_grad_sumsq_f32", g.size - off, dg.offset(off), 0, sumsq.ptr, None, None)
         results.append(float(sumsq.numpy()[0]))
     assert results[0] == results[1]  # fixed partition: bit-identical repeats
     ref = float(np.sum(g.astype(np.float64) ** 2))
