@@ -316,6 +316,82 @@ int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* sta
 int talos_ppo_forward_f32(talos_plan plan, const float* params, const float* states, float* logits,
                           float* values, talos_stream_t stream);
 
+/* Sums over a minibatch's samples that talos_ppo_minibatch_f32 can write (device doubles):
+ * approx_kl = (ratio - 1) - log_ratio (ppo.rs:726-729), the chosen surrogate, (V - ret)^2, the
+ * entropy, and the sample count. */
+enum talos_ppo_stat {
+  TALOS_PPO_STAT_KL = 0,
+  TALOS_PPO_STAT_POLICY = 1,
+  TALOS_PPO_STAT_VALUE = 2,
+  TALOS_PPO_STAT_ENTROPY = 3,
+  TALOS_PPO_STAT_COUNT = 4,
+  TALOS_PPO_NSTATS = 5
+};
+
+/* The minibatch entry of the update loop: n samples (1 <= n <= cfg.batch; the loss is the mean
+ * over n, as ppo.rs:754-755 divides by chunk.len()). lengths (device int32[n], or NULL for all
+ * seq) gives each sample's token count, Q5 of the reference's varying state lengths: the last
+ * token of sample b is row lengths[b] - 1 and keys at or past lengths[b] are masked, so a
+ * right-padded sample gives exactly its unpadded result (padding rows must hold finite values).
+ * stats (device double[TALOS_PPO_NSTATS], or NULL) receives the sums above, added to its
+ * contents when stats_accumulate != 0. loss (device float[1]) may be NULL. */
+int talos_ppo_minibatch_f32(talos_plan plan, int n, const float* params, const float* states,
+                            const int32_t* lengths, const int32_t* actions, const float* adv, const float* ret,
+                            const float* old_logp, float* loss, float* dparams, double* stats,
+                            int stats_accumulate, talos_stream_t stream);
+/* Forward only for n samples with optional lengths (the rollout's log-probs and values). */
+int talos_ppo_forward_n_f32(talos_plan plan, int n, const float* params, const float* states,
+                            const int32_t* lengths, float* logits, float* values, talos_stream_t stream);
+
+/* Advantages and returns of one rollout, the f64 prologue of PPO::update (ppo.rs:650-676):
+ *   r_t   = clamp((rewards_t - r_mean) / (sqrt(r_var) + 1e-8), -r_clip, r_clip)
+ *           (RunningMeanStd::normalize, ppo.rs:477-479; r_clip = 10 at ppo.rs:655)
+ *   d_t   = r_t + gamma * V_{t+1} * (1 - done_t) - V_t,   V_len = 0
+ *   A_t   = d_t + gamma * lambda * (1 - done_t) * A_{t+1}, A_len = 0
+ *   ret_t = A_t + V_t;  adv_t = (A_t - mean(A)) / (std(A) + 1e-8)  (population std)
+ * The reference uses gamma 0.99, lambda 0.95 (ppo.rs:18-19). rewards, values: device double[len];
+ * terminals: device uint8[len] (0 / non-zero); adv, ret: device float[len] (the loss inputs);
+ * adv_raw: device double[len] or NULL. The recursion runs as a parallel linear-recurrence scan in
+ * f64 in one workgroup. */
+int talos_ppo_gae_f64(int len, const double* rewards, const double* values, const uint8_t* terminals,
+                      double r_mean, double r_var, double r_clip, double gamma, double lambda, float* adv,
+                      float* ret, double* adv_raw, talos_stream_t stream);
+
+/* PPO::update on the device (ppo.rs:625-770): GAE and advantage normalisation, then k_epochs
+ * passes over the rollout in order (no shuffling, as the reference's indices.chunks), each a
+ * minibatch forward + backward (talos_ppo_minibatch_f32, minibatch = the plan's batch, the last
+ * chunk shorter) followed by one Adam step (talos_adam_step_f32, b = (0.9, 0.999), eps 1e-8). An
+ * epoch whose mean approx_kl exceeds 1.5 * target_kl (0.015 at ppo.rs:678) ends the update
+ * (ppo.rs:761-768). The host synchronises once per epoch, for the KL check. */
+typedef struct talos_ppo_update_args {
+  int n;                     /* samples in the rollout */
+  const float* states;       /* device [n, seq, in_dim], right-padded when lengths != NULL */
+  const int32_t* lengths;    /* device [n] or NULL */
+  const int32_t* actions;    /* device [n] */
+  const float* old_logp;     /* device [n]: the rollout policy's log-probs */
+  const double* rewards;     /* device [n] */
+  const double* values;      /* device [n]: the rollout's critic values */
+  const uint8_t* terminals;  /* device [n] */
+  double reward_mean, reward_var, reward_clip;  /* the reward normaliser's state; clip 10 */
+  double gamma, lambda, target_kl;              /* 0.99, 0.95, 0.015 in the reference */
+  int k_epochs;
+  double lr;                 /* Adam::set_lr(current_lr), ppo.rs:630 */
+  float* params;             /* device, updated in place */
+  float* adam_m;             /* device, same size as params (zero before the first update) */
+  float* adam_v;
+  int adam_t;                /* Adam steps taken before this update; advanced by the update */
+  void* work;                /* device, talos_ppo_update_work_bytes(plan, n) bytes */
+} talos_ppo_update_args;
+typedef struct talos_ppo_update_result {
+  int epochs_run;            /* epochs completed, early stop included */
+  int stopped_early;         /* 1 when the KL check ended the update */
+  double approx_kl;          /* mean approx_kl of the last epoch run */
+  double mean_loss;          /* mean over the last epoch's samples of the per-sample loss */
+} talos_ppo_update_result;
+size_t talos_ppo_update_work_bytes(talos_plan plan, int n);
+int talos_ppo_update_f32(talos_plan plan, talos_ppo_update_args* args, talos_ppo_update_result* result,
+                         talos_stream_t stream);
+
 /* MLA block forward + backward for loss = sum(out * gout): writes out[batch*seq, d], dparams
  * (overwritten, same layout as params) and dx. */
 int talos_mla_plan_create(const talos_mla_cfg* cfg, talos_plan* plan);

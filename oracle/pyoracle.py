@@ -95,6 +95,10 @@ def lib():
         L.orc_adam_step.restype = None
         L.orc_adam_step.argtypes = [ctypes.c_int64, _f64p, _f64p, _f64p, _f64p, ctypes.c_int, ctypes.c_double,
                                     ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double]
+        L.orc_ppo_gae.restype = None
+        L.orc_ppo_gae.argtypes = [ctypes.c_int64, _f64p, _f64p, ctypes.POINTER(ctypes.c_uint8), ctypes.c_double,
+                                  ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double, _f64p, _f64p,
+                                  _f64p]
         L.orc_threads.restype = ctypes.c_int
         L.orc_set_threads.argtypes = [ctypes.c_int]
         _lib = L
@@ -432,3 +436,16 @@ def adam_step(p, g, m, v, t, lr, beta1=0.9, beta2=0.999, eps=1e-8, max_norm=0.0)
     assert p.size == g.size == m.size == v.size
     lib().orc_adam_step(p.size, _p(p), _p(g), _p(m), _p(v), int(t), float(lr), float(beta1), float(beta2),
                         float(eps), float(max_norm))
+
+
+def ppo_gae(rewards, values, terminals, r_mean=0.0, r_var=1.0, r_clip=10.0, gamma=0.99, lam=0.95):
+    """PPO::update's advantage prologue in f64 (src/ppo.rs:650-676). Returns (adv_raw, returns,
+    adv_norm)."""
+    r, v = _f64(rewards), _f64(values)
+    d = np.ascontiguousarray(np.asarray(terminals, dtype=np.uint8))
+    n = r.size
+    assert v.size == n and d.size == n and n > 0
+    a, ret, an = np.empty(n), np.empty(n), np.empty(n)
+    lib().orc_ppo_gae(n, _p(r), _p(v), d.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), float(r_mean), float(r_var),
+                      float(r_clip), float(gamma), float(lam), _p(a), _p(ret), _p(an))
+    return a, ret, an

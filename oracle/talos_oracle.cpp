@@ -21,7 +21,9 @@
  *   - the PPO per-sample loss graph (src/ppo.rs:691-756) and the actor-critic heads
  *     (src/ppo.rs:246-300);
  *   - the optimizer step: Adam (src/ppo.rs:519-533) and the DQN optimizer's global-norm
- *     gradient clip (src/dqn.rs:207-226).
+ *     gradient clip (src/dqn.rs:207-226);
+ *   - PPO::update's prologue: reward normalisation, GAE and advantage normalisation
+ *     (src/ppo.rs:650-676).
  * Extensions the configurations need (each documented where defined): causal softmax mask,
  * GELU, explicit sequence positions for RoPE, a differentiable last-token gather, a standard
  * multi-head attention block, and a batched PPO loss with a closed-form backward.
@@ -1689,6 +1691,34 @@ void orc_adam_step(int64_t n, double* p, const double* g, double* m, double* v, 
     const double m_hat = m[j] / bc1, v_hat = v[j] / bc2;
     p[j] -= lr * m_hat / (std::sqrt(v_hat) + eps);
   }
+}
+
+// PPO::update's advantage prologue (src/ppo.rs:650-676), sequential as the reference: rewards
+// normalised by the reward normaliser (RunningMeanStd::normalize, src/ppo.rs:477-479) and clipped
+// to [-r_clip, r_clip]; delta_t = r_t + gamma * V_{t+1} * nonterm_t - V_t with V_len = 0;
+// A_t = delta_t + gamma * lambda * nonterm_t * A_{t+1}; ret = A + V; the advantages are then
+// normalised by their mean and population std + 1e-8.
+void orc_ppo_gae(int64_t len, const double* rewards, const double* values, const uint8_t* terminals, double r_mean,
+                 double r_var, double r_clip, double gamma, double lambda, double* adv_raw, double* returns,
+                 double* adv_norm) {
+  double last = 0.0;
+  for (int64_t t = len - 1; t >= 0; --t) {
+    const double nr = std::min(std::max((rewards[t] - r_mean) / (std::sqrt(r_var) + 1e-8), -r_clip), r_clip);
+    const double non_terminal = terminals[t] ? 0.0 : 1.0;
+    const double val_next = t < len - 1 ? values[t + 1] : 0.0;
+    const double delta = nr + gamma * val_next * non_terminal - values[t];
+    const double gae = delta + gamma * lambda * non_terminal * last;
+    adv_raw[t] = gae;
+    returns[t] = gae + values[t];
+    last = gae;
+  }
+  double sum = 0.0;
+  for (int64_t t = 0; t < len; ++t) sum += adv_raw[t];
+  const double mean = sum / (double)len;
+  double ss = 0.0;
+  for (int64_t t = 0; t < len; ++t) ss += (adv_raw[t] - mean) * (adv_raw[t] - mean);
+  const double stdv = std::sqrt(ss / (double)len) + 1e-8;
+  for (int64_t t = 0; t < len; ++t) adv_norm[t] = (adv_raw[t] - mean) / stdv;
 }
 
 }  // extern "C"

@@ -53,7 +53,15 @@ struct AttnArgs {
   const float* rsin;
   int rope_off, rope_dim;
   int vec;  // every row half is 16-byte aligned and the head dims equal the template dims
+  const int32_t* lens;  // per-batch key count (nullptr: all S keys)
 };
+
+// Keys of batch entry b that take part: lens[b] clamped to [0, S] (rows past it are padding).
+__device__ __forceinline__ int key_len(const AttnArgs& a, int b) {
+  if (a.lens == nullptr) return a.S;
+  const int L = a.lens[b];
+  return L < 0 ? 0 : (L > a.S ? a.S : L);
+}
 
 constexpr float kNegInf = -INFINITY;
 
@@ -185,10 +193,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_
   const int b = pair / a.H, hd = pair % a.H;
   const long long tok0 = (long long)b * a.S;
   const int q = qb * 32 + l32;  // this lane's query (score columns)
+  const int Sk = key_len(a, b);
 
   float qv[KH];
   load_half<KH, kFwdSel>(qv, a.q, a.ldq, tok0, q, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
-  const int kb_last = a.causal ? qb : (a.S - 1) >> 5;
+  const int kb_last = a.causal ? min(qb, (Sk - 1) >> 5) : (Sk - 1) >> 5;
 
   // scores of key block kb in S^T layout, masked
   auto scores = [&](int kb, float (&sv)[16]) {
@@ -201,7 +210,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = kb * 32 + acc_row(r, h);
-      const bool ok = key < a.S && (!a.causal || key <= q);
+      const bool ok = key < Sk && (!a.causal || key <= q);
       sv[r] = ok ? acc[r] : kNegInf;
     }
   };
@@ -290,7 +299,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   for (int i = 0; i < QB; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
-  const int kb_last = a.causal ? qb : (a.S - 1) >> 5;
+  const int Sk = key_len(a, b);
+  const int kb_last = a.causal ? min(qb, (Sk - 1) >> 5) : (Sk - 1) >> 5;
   for (int kb = 0; kb <= kb_last; ++kb) {
     floatx16 sacc, pacc;
 #pragma unroll
@@ -309,7 +319,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = kb * 32 + acc_row(r, h);
-      const bool ok = qok && key < a.S && (!a.causal || key <= q);
+      const bool ok = qok && key < Sk && (!a.causal || key <= q);
       const float p = expf(ok ? sacc[r] - lse : kNegInf);
       dS[r] = p * (pacc[r] - D);
     }
@@ -353,7 +363,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a) {
   for (int i = 0; i < VB; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) dv[i][r] = 0.f;
-  const bool kok = key < a.S;
+  const bool kok = key < key_len(a, b);
   const int nqb = (a.S + 31) >> 5;
   for (int qb = a.causal ? kb : 0; qb < nqb; ++qb) {
     floatx16 sacc, pacc;
@@ -467,7 +477,8 @@ attn_bwd_fused_kernel(AttnArgs a) {
   static_assert(!STAGE || 32 * kTS <= 64 * TP, "the dS^T tile must end before the K tile");
   float* const Dl = W + (STAGE ? 96 * TP : 32 * kTS);  // D[query]
   float* const Ll = Dl + 32;                            // lse[query]
-  const bool rok = l32 < a.S;  // this lane's row (query l32 of q / dO / O, key l32 of k / v)
+  const bool rok = l32 < a.S;             // this lane's row (query l32 of q / dO / O)
+  const bool kok = l32 < key_len(a, b);   // ... and its key l32 of k / v takes part
 
   float gv[VH];
   load_half<VH, kFusedSel>(gv, a.dout, a.lddo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
@@ -521,7 +532,7 @@ attn_bwd_fused_kernel(AttnArgs a) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int qr = acc_row(r, h);
-    const bool ok = rok && qr < a.S && (!a.causal || l32 <= qr);
+    const bool ok = kok && qr < a.S && (!a.causal || l32 <= qr);
     const float p = expf(ok ? sacc[r] - lq[r] : kNegInf);  // exp(-inf) = 0: no branch
     P[r] = p;
     dS[r] = p * (pacc[r] - dq_[r]);
@@ -604,6 +615,7 @@ static AttnArgs make_args(const AttnDesc& d, int dkm, int dvm) {
   a.dout = d.dout; a.lddo = d.lddo;
   a.dq = d.dq; a.lddq = d.lddq; a.dk_out = d.dk_out; a.lddk = d.lddk; a.dv_out = d.dv_out; a.lddv = d.lddv;
   a.rcos = d.rope_cos; a.rsin = d.rope_sin; a.rope_off = d.rope_off; a.rope_dim = d.rope_dim;
+  a.lens = d.lens;
   // row halves start at (token * ld + head * dim + half * dim/2): 16-byte aligned when all of
   // ld, dim and dim/2 are multiples of 4 and the bases are aligned
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };

@@ -33,6 +33,9 @@ struct AttnDesc {
   const float* rope_cos = nullptr;
   const float* rope_sin = nullptr;
   int rope_off = 0, rope_dim = 0;
+  // optional per-batch key counts: keys >= lens[b] (clamped to [0, seq]) are masked for every
+  // query of batch entry b, so right-padded sequences attend only to their own tokens
+  const int32_t* lens = nullptr;
 };
 
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s);

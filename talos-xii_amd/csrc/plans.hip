@@ -25,6 +25,7 @@
 
 #include "attention.hpp"
 #include "gemm.hpp"
+#include "plans.hpp"
 #include "rowops.hpp"
 
 struct talos_plan_s {
@@ -53,6 +54,7 @@ struct talos_plan_s {
         *values = nullptr, *g_logits = nullptr, *g_values = nullptr, *g_pout = nullptr, *g_lastn = nullptr,
         *g_last = nullptr;
   double* loss_ws = nullptr;
+  const int32_t* lens = nullptr;  // per-sample lengths of the PPO call in progress (nullptr: all seq)
   int num_cu = 256;
   bool bf16 = false;  // bf16-in / fp32-accumulate GEMMs (MLA plans with TALOS_PREC_BF16)
   talos::Profiler* prof = nullptr;
@@ -325,6 +327,7 @@ static int block_forward(talos_plan_s* p, const talos_block_cfg& c, const float*
     a.o = L.o;
     a.ldo = d;
     a.lse = L.lse;
+    a.lens = p->lens;
     rc = attn_fwd_launch(a, s);
     if (rc) return rc;
   }
@@ -419,6 +422,7 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
     a.rope_sin = p->rsin;
     a.rope_off = 0;
     a.rope_dim = c.head_dim;
+    a.lens = p->lens;
     rc = attn_bwd_launch(a, p->attn_ws, s);
     if (rc) return rc;
   }
@@ -431,22 +435,31 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
 }
 
 // Last-token gather / scatter -----------------------------------------------
-__global__ void gather_last_kernel(int B, int S, int d, const float* __restrict__ h, float* __restrict__ out) {
+// The last token of sample b is row lens[b] - 1 (lens clamped to [1, S]; no lens: row S - 1), as
+// last_token reads row seq_len - 1 of each sample (src/transformer.rs:92-109).
+__device__ __forceinline__ int last_row(const int32_t* lens, int b, int S) {
+  if (lens == nullptr) return S - 1;
+  const int L = lens[b];
+  return (L < 1 ? 1 : (L > S ? S : L)) - 1;
+}
+__global__ void gather_last_kernel(int B, int S, int d, const int32_t* __restrict__ lens,
+                                   const float* __restrict__ h, float* __restrict__ out) {
   const long long n = (long long)B * d;
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
     const long long b = i / d;
     const int e = (int)(i % d);
-    out[i] = h[(b * S + (S - 1)) * d + e];
+    out[i] = h[(b * S + last_row(lens, (int)b, S)) * d + e];
   }
 }
-// g[M, d] = 0 except rows b*S + S-1 which receive gl[b]
-__global__ void scatter_last_kernel(int B, int S, int d, const float* __restrict__ gl, float* __restrict__ g) {
+// g[M, d] = 0 except the last-token rows, which receive gl[b]
+__global__ void scatter_last_kernel(int B, int S, int d, const int32_t* __restrict__ lens,
+                                    const float* __restrict__ gl, float* __restrict__ g) {
   const long long n = (long long)B * S * d;
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
     const long long row = i / d;
     const int e = (int)(i % d);
-    const int t = (int)(row % S);
-    g[i] = t == S - 1 ? gl[(row / S) * d + e] : 0.f;
+    const int b = (int)(row / S), t = (int)(row % S);
+    g[i] = t == last_row(lens, b, S) ? gl[(long long)b * d + e] : 0.f;
   }
 }
 
@@ -455,7 +468,9 @@ __global__ void scatter_last_kernel(int B, int S, int d, const float* __restrict
 // Per sample: lp = z - lse(z); ratio = exp(lp[a] - old); surr1 = ratio*adv;
 // surr2 = clip(ratio, 1-eps, 1+eps)*adv; the smaller by value is kept (ties take surr2, whose
 // gradient passes only inside the clip range); v = (value - ret)^2; ent = -sum p*lp;
-// loss = -pol + cv*v - ce*ent.
+// loss = -pol + cv*v - ce*ent. stats (optional) receives the sums over the samples of
+// approx_kl = (ratio - 1) - log_ratio (src/ppo.rs:726-729), pol, v, ent and the sample count,
+// added to its previous contents when stats_acc != 0.
 __global__ __launch_bounds__(256) void ppo_loss_kernel(int B, int A, float clip_eps, float cv, float ce,
                                                        const float* __restrict__ logits,
                                                        const float* __restrict__ values,
@@ -463,9 +478,9 @@ __global__ __launch_bounds__(256) void ppo_loss_kernel(int B, int A, float clip_
                                                        const float* __restrict__ adv, const float* __restrict__ ret,
                                                        const float* __restrict__ old_logp, float* __restrict__ loss,
                                                        float* __restrict__ dlogits, float* __restrict__ dvalues,
-                                                       int with_grad) {
+                                                       int with_grad, double* __restrict__ stats, int stats_acc) {
   __shared__ double red[4];
-  double total = 0.0;
+  double total = 0.0, s_kl = 0.0, s_pol = 0.0, s_v = 0.0, s_ent = 0.0;
   const double invB = 1.0 / (double)B;
   for (int b = threadIdx.x; b < B; b += blockDim.x) {
     const float* z = logits + (long long)b * A;
@@ -490,7 +505,8 @@ __global__ __launch_bounds__(256) void ppo_loss_kernel(int B, int A, float clip_
       }
       continue;
     }
-    const double ratio = exp(((double)z[a] - lse) - (double)old_logp[b]);
+    const double log_ratio = ((double)z[a] - lse) - (double)old_logp[b];
+    const double ratio = exp(log_ratio);
     const double ad = adv[b];
     const double lo = 1.0 - (double)clip_eps, hi = 1.0 + (double)clip_eps;
     const double s1 = ratio * ad;
@@ -506,6 +522,10 @@ __global__ __launch_bounds__(256) void ppo_loss_kernel(int B, int A, float clip_
     }
     const double vd = (double)values[b] - (double)ret[b];
     total += -pol + (double)cv * vd * vd - (double)ce * ent;
+    s_kl += (ratio - 1.0) - log_ratio;
+    s_pol += pol;
+    s_v += vd * vd;
+    s_ent += ent;
     if (with_grad) {
       for (int k = 0; k < A; ++k) {
         const double lp = (double)z[k] - lse;
@@ -518,6 +538,13 @@ __global__ __launch_bounds__(256) void ppo_loss_kernel(int B, int A, float clip_
   }
   total = block_sum(total, red);
   if (threadIdx.x == 0 && loss) loss[0] = (float)(total * invB);
+  if (stats) {
+    const double sums[4] = {block_sum(s_kl, red), block_sum(s_pol, red), block_sum(s_v, red), block_sum(s_ent, red)};
+    if (threadIdx.x == 0) {
+      for (int i = 0; i < 4; ++i) stats[i] = (stats_acc ? stats[i] : 0.0) + sums[i];
+      stats[4] = (stats_acc ? stats[4] : 0.0) + (double)B;
+    }
+  }
 }
 
 static int check_ppo_cfg(const talos_ppo_cfg& c) {
@@ -528,9 +555,10 @@ static int check_ppo_cfg(const talos_ppo_cfg& c) {
   return check_block_cfg(block_cfg_of(c));
 }
 
-// Policy forward up to logits / values.
-static int ppo_forward(talos_plan_s* p, const float* P, const float* states, hipStream_t s) {
-  const talos_ppo_cfg& c = p->ppo;
+// Policy forward up to logits / values for c.batch samples (at most the plan's batch); the
+// per-sample lengths of the call are p->lens.
+static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, const float* states,
+                       hipStream_t s) {
   const talos_block_cfg bc = block_cfg_of(c);
   const PpoOff po = ppo_offsets(c);
   const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions;
@@ -549,7 +577,7 @@ static int ppo_forward(talos_plan_s* p, const float* P, const float* states, hip
   {
     ProfScope ps_g(s, "gather_last_kernel", 0.0, 8.0 * c.batch * d);
     hipLaunchKernelGGL(gather_last_kernel, dim3(ceil_div((size_t)c.batch * d, 256)), dim3(256), 0, s, c.batch, c.seq,
-                       d, h, p->last);
+                       d, p->lens, h, p->last);
     TALOS_LAUNCHED("gather_last_kernel");
   }
   rc = rmsnorm_fwd_launch(c.batch, d, c.eps, p->last, P + po.gf, p->lastn, p->rstdf, s);
@@ -702,6 +730,10 @@ static int mla_fwd_bwd(talos_plan_s* p, const float* P, const float* x, const fl
   return rmsnorm_bwd_launch(M, d, x, P + o.g, b.rstd, b.dxn, 1.f, dx, 0.f, G + o.g, p->red_ws, s, gout);
 }
 
+const talos_ppo_cfg* ppo_plan_cfg(talos_plan plan) {
+  return (plan != nullptr && plan->kind == 2) ? &plan->ppo : nullptr;
+}
+
 }  // namespace talos
 
 using namespace talos;
@@ -802,48 +834,61 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
   return TALOS_OK;
 }
 
-int talos_ppo_forward_f32(talos_plan plan, const float* params, const float* states, float* logits, float* values,
-                          talos_stream_t stream) {
-  TALOS_REQUIRE(plan != nullptr && plan->kind == 2, TALOS_ERR_HANDLE, "%s: not a ppo plan", __func__);
-  TALOS_NONNULL(params);
-  TALOS_NONNULL(states);
-  TALOS_DEVICE();
-  hipStream_t s = as_stream(stream);
-  PlanCall pc(plan);
-  int rc = ppo_forward(plan, params, states, s);
-  if (rc) return rc;
-  const talos_ppo_cfg& c = plan->ppo;
-  if (logits)
-    TALOS_HIP(hipMemcpyAsync(logits, plan->logits, (size_t)c.batch * c.n_actions * 4, hipMemcpyDeviceToDevice, s));
-  if (values) TALOS_HIP(hipMemcpyAsync(values, plan->values, (size_t)c.batch * 4, hipMemcpyDeviceToDevice, s));
+// Lengths of the PPO call in progress, visible to the block kernels through the plan.
+struct LensScope {
+  talos_plan_s* p;
+  LensScope(talos_plan_s* p_, const int32_t* lens) : p(p_) { p->lens = lens; }
+  ~LensScope() { p->lens = nullptr; }
+};
+
+static int ppo_check_n(const talos_plan_s* p, int n, const char* fn) {
+  TALOS_REQUIRE(n >= 1 && n <= p->ppo.batch, TALOS_ERR_SHAPE, "%s: n=%d outside [1, %d] (the plan's batch)", fn, n,
+                p->ppo.batch);
   return TALOS_OK;
 }
 
-int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* states, const int32_t* actions,
-                          const float* adv, const float* ret, const float* old_logp, float* loss_out, float* dparams,
-                          talos_stream_t stream) {
+int talos_ppo_forward_n_f32(talos_plan plan, int n, const float* params, const float* states, const int32_t* lengths,
+                            float* logits, float* values, talos_stream_t stream) {
   TALOS_REQUIRE(plan != nullptr && plan->kind == 2, TALOS_ERR_HANDLE, "%s: not a ppo plan", __func__);
   TALOS_NONNULL(params);
   TALOS_NONNULL(states);
-  TALOS_NONNULL(actions);
-  TALOS_NONNULL(adv);
-  TALOS_NONNULL(ret);
-  TALOS_NONNULL(old_logp);
-  TALOS_NONNULL(dparams);
+  if (int rc = ppo_check_n(plan, n, __func__)) return rc;
   TALOS_DEVICE();
   hipStream_t s = as_stream(stream);
-  talos_plan_s* p = plan;
-  PlanCall pc(p);
-  const talos_ppo_cfg& c = p->ppo;
+  PlanCall pc(plan);
+  LensScope ls(plan, lengths);
+  talos_ppo_cfg c = plan->ppo;
+  c.batch = n;
+  int rc = ppo_forward(plan, c, params, states, s);
+  if (rc) return rc;
+  if (logits)
+    TALOS_HIP(hipMemcpyAsync(logits, plan->logits, (size_t)n * c.n_actions * 4, hipMemcpyDeviceToDevice, s));
+  if (values) TALOS_HIP(hipMemcpyAsync(values, plan->values, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
+  return TALOS_OK;
+}
+
+int talos_ppo_forward_f32(talos_plan plan, const float* params, const float* states, float* logits, float* values,
+                          talos_stream_t stream) {
+  TALOS_REQUIRE(plan != nullptr && plan->kind == 2, TALOS_ERR_HANDLE, "%s: not a ppo plan", __func__);
+  return talos_ppo_forward_n_f32(plan, plan->ppo.batch, params, states, nullptr, logits, values, stream);
+}
+
+// One minibatch of n samples: forward, loss (and its statistics), backward into dparams.
+static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const float* states, const int32_t* actions,
+                         const float* adv, const float* ret, const float* old_logp, float* loss_out, float* dparams,
+                         double* stats, int stats_acc, hipStream_t s) {
+  talos_ppo_cfg c = p->ppo;
+  c.batch = n;
   const talos_block_cfg bc = block_cfg_of(c);
   const PpoOff po = ppo_offsets(c);
   const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions, B = c.batch;
-  int rc = ppo_forward(p, params, states, s);
+  int rc = ppo_forward(p, c, params, states, s);
   if (rc) return rc;
   {
   ProfScope ps_l(s, "ppo_loss_kernel", 0.0, 4.0 * B * (2.0 * A + 5.0));
   hipLaunchKernelGGL(ppo_loss_kernel, dim3(1), dim3(256), 0, s, B, A, c.clip_eps, c.value_coef, c.entropy_coef,
-                     p->logits, p->values, actions, adv, ret, old_logp, loss_out, p->g_logits, p->g_values, 1);
+                     p->logits, p->values, actions, adv, ret, old_logp, loss_out, p->g_logits, p->g_values, 1, stats,
+                     stats_acc);
   TALOS_LAUNCHED("ppo_loss_kernel");
   }
   float* G = dparams;
@@ -868,7 +913,7 @@ int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* sta
   {
   ProfScope ps_s(s, "scatter_last_kernel", 0.0, 4.0 * ((double)M * d + (double)B * d));
   hipLaunchKernelGGL(scatter_last_kernel, dim3(ceil_div((size_t)M * d, 256) > 65536 ? 65536 : ceil_div((size_t)M * d, 256)),
-                     dim3(256), 0, s, B, c.seq, d, p->g_last, p->g_out);
+                     dim3(256), 0, s, B, c.seq, d, p->lens, p->g_last, p->g_out);
   TALOS_LAUNCHED("scatter_last_kernel");
   }
   // blocks, last to first; the gradient ping-pongs between g_out and g_x
@@ -887,6 +932,33 @@ int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* sta
   }
   // embed
   return mm(p, s, 1, 0, c.in_dim, d, M, states, c.in_dim, gcur, d, G + po.we, d, 0.f, nullptr, nullptr, 0, G + po.be);
+}
+
+int talos_ppo_minibatch_f32(talos_plan plan, int n, const float* params, const float* states, const int32_t* lengths,
+                            const int32_t* actions, const float* adv, const float* ret, const float* old_logp,
+                            float* loss, float* dparams, double* stats, int stats_accumulate, talos_stream_t stream) {
+  TALOS_REQUIRE(plan != nullptr && plan->kind == 2, TALOS_ERR_HANDLE, "%s: not a ppo plan", __func__);
+  TALOS_NONNULL(params);
+  TALOS_NONNULL(states);
+  TALOS_NONNULL(actions);
+  TALOS_NONNULL(adv);
+  TALOS_NONNULL(ret);
+  TALOS_NONNULL(old_logp);
+  TALOS_NONNULL(dparams);
+  if (int rc = ppo_check_n(plan, n, __func__)) return rc;
+  TALOS_DEVICE();
+  PlanCall pc(plan);
+  LensScope ls(plan, lengths);
+  return ppo_minibatch(plan, n, params, states, actions, adv, ret, old_logp, loss, dparams, stats, stats_accumulate,
+                       as_stream(stream));
+}
+
+int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* states, const int32_t* actions,
+                          const float* adv, const float* ret, const float* old_logp, float* loss_out, float* dparams,
+                          talos_stream_t stream) {
+  TALOS_REQUIRE(plan != nullptr && plan->kind == 2, TALOS_ERR_HANDLE, "%s: not a ppo plan", __func__);
+  return talos_ppo_minibatch_f32(plan, plan->ppo.batch, params, states, nullptr, actions, adv, ret, old_logp,
+                                 loss_out, dparams, nullptr, 0, stream);
 }
 
 size_t talos_mla_param_count(const talos_mla_cfg* cfg) { return cfg ? mla_offsets(*cfg).end : 0; }

@@ -24,6 +24,7 @@ _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _f = ctypes.c_float
 _sz = ctypes.c_size_t
+_d = ctypes.c_double
 _ll = ctypes.c_longlong
 
 
@@ -42,6 +43,22 @@ class PpoCfg(ctypes.Structure):
     _fields_ = [("batch", _i), ("seq", _i), ("in_dim", _i), ("d_model", _i), ("n_layers", _i), ("n_heads", _i),
                 ("head_dim", _i), ("ffn_dim", _i), ("n_actions", _i), ("causal", _i), ("activation", _i),
                 ("eps", _f), ("rope_base", _f), ("clip_eps", _f), ("value_coef", _f), ("entropy_coef", _f)]
+
+
+class PpoUpdateArgs(ctypes.Structure):
+    """talos_ppo_update_args (device pointers as integers)."""
+    _fields_ = [("n", _i), ("states", _vp), ("lengths", _vp), ("actions", _vp), ("old_logp", _vp),
+                ("rewards", _vp), ("values", _vp), ("terminals", _vp), ("reward_mean", _d), ("reward_var", _d),
+                ("reward_clip", _d), ("gamma", _d), ("lambda_", _d), ("target_kl", _d), ("k_epochs", _i),
+                ("lr", _d), ("params", _vp), ("adam_m", _vp), ("adam_v", _vp), ("adam_t", _i), ("work", _vp)]
+
+
+class PpoUpdateResult(ctypes.Structure):
+    _fields_ = [("epochs_run", _i), ("stopped_early", _i), ("approx_kl", _d), ("mean_loss", _d)]
+
+
+PPO_NSTATS = 5
+STAT_KL, STAT_POLICY, STAT_VALUE, STAT_ENTROPY, STAT_COUNT = range(5)
 
 
 class MlaCfg(ctypes.Structure):
@@ -108,6 +125,11 @@ _SIGS = {
     "talos_ppo_plan_create": [ctypes.POINTER(PpoCfg), ctypes.POINTER(_vp)],
     "talos_ppo_fwd_bwd_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "talos_ppo_forward_f32": [_vp, _vp, _vp, _vp, _vp, _vp],
+    "talos_ppo_forward_n_f32": [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp],
+    "talos_ppo_minibatch_f32": [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp],
+    "talos_ppo_gae_f64": [_i, _vp, _vp, _vp, _d, _d, _d, _d, _d, _vp, _vp, _vp, _vp],
+    "talos_ppo_update_work_bytes": [_vp, _i],
+    "talos_ppo_update_f32": [_vp, ctypes.c_void_p, ctypes.c_void_p, _vp],
     "talos_mla_param_count": [ctypes.POINTER(MlaCfg)],
     "talos_mla_plan_create": [ctypes.POINTER(MlaCfg), ctypes.POINTER(_vp)],
     "talos_mla_fwd_bwd_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
@@ -122,7 +144,7 @@ class ProfRecord(ctypes.Structure):
     _fields_ = [("kernel", ctypes.c_char * 64), ("flops", ctypes.c_double), ("bytes", ctypes.c_double),
                 ("ms", ctypes.c_float)]
 _RESTYPE = {"talos_last_error": ctypes.c_char_p, "talos_version": ctypes.c_char_p,
-            "talos_grad_sumsq_workspace_bytes": _sz, "talos_block_param_count": _sz, "talos_ppo_param_count": _sz, "talos_mla_param_count": _sz}
+            "talos_grad_sumsq_workspace_bytes": _sz, "talos_ppo_update_work_bytes": _sz, "talos_block_param_count": _sz, "talos_ppo_param_count": _sz, "talos_mla_param_count": _sz}
 
 _lib = None
 

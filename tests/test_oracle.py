@@ -468,3 +468,57 @@ def test_adam_global_norm_clip(oracle, scale):
         m1 = np.zeros(n)
         oracle.adam_step(p0.copy(), g, m1, np.zeros(n), 1, 1e-2, max_norm=1.0)
         assert abs(np.linalg.norm(m1) - 0.1) < 1e-12
+
+
+# ---------------------------------------------------------------------------
+# PPO::update prologue: reward normalisation, GAE, advantage normalisation (src/ppo.rs:650-676)
+# ---------------------------------------------------------------------------
+def _gae_by_sum(r, v, done, gamma, lam):
+    """A_t = sum_l (gamma lambda)^l (prod_{j<l} (1 - done_{t+j})) delta_{t+l}: the definition as a
+    sum, independent of the backward recursion."""
+    n = r.size
+    nonterm = 1.0 - done.astype(np.float64)
+    v_next = np.append(v[1:], 0.0)
+    delta = r + gamma * v_next * nonterm - v
+    a = np.zeros(n)
+    for t in range(n):
+        w = 1.0
+        for k in range(t, n):
+            a[t] += w * delta[k]
+            w *= gamma * lam * nonterm[k]
+            if w == 0.0:
+                break
+    return a
+
+
+@pytest.mark.parametrize("n,p_done", [(1, 0.0), (17, 0.2), (300, 0.05), (300, 1.0)])
+def test_gae_vs_sum_definition(oracle, n, p_done):
+    rng = np.random.default_rng(n)
+    rew, val = rng.normal(size=n) * 3.0, rng.normal(size=n)
+    done = rng.random(n) < p_done
+    mu, var = 0.4, 2.5
+    a, ret, an = oracle.ppo_gae(rew, val, done, mu, var, 10.0, 0.99, 0.95)
+    r = np.clip((rew - mu) / (np.sqrt(var) + 1e-8), -10.0, 10.0)
+    ref = _gae_by_sum(r, val, done, 0.99, 0.95)
+    np.testing.assert_allclose(a, ref, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(ret, ref + val, rtol=1e-12, atol=1e-12)
+    if n > 1:
+        np.testing.assert_allclose(an.mean(), 0.0, atol=1e-12)
+        np.testing.assert_allclose(an, (a - a.mean()) / (a.std() + 1e-8), rtol=1e-12, atol=1e-12)
+
+
+def test_gae_special_cases(oracle):
+    rng = np.random.default_rng(5)
+    rew, val = rng.normal(size=50), rng.normal(size=50)
+    done = rng.random(50) < 0.3
+    v_next = np.append(val[1:], 0.0)
+    r = rew / (1.0 + 1e-8)  # normalised with mean 0, var 1: (r - 0) / (sqrt(1) + 1e-8)
+    # lambda = 0: A is the one-step TD error
+    a, _, _ = oracle.ppo_gae(rew, val, done, 0.0, 1.0, 10.0, 0.9, 0.0)
+    np.testing.assert_allclose(a, r + 0.9 * v_next * (1 - done) - val, rtol=1e-12, atol=1e-13)
+    # gamma = 0: A = r - V
+    a, _, _ = oracle.ppo_gae(rew, val, done, 0.0, 1.0, 10.0, 0.0, 0.95)
+    np.testing.assert_allclose(a, r - val, rtol=1e-12, atol=1e-13)
+    # the reward clip: |r_norm| <= clip
+    a, _, _ = oracle.ppo_gae(rew * 1e6, val * 0, np.ones(50, bool), 0.0, 1.0, 10.0, 0.99, 0.95)
+    np.testing.assert_allclose(a, np.clip(rew * 1e6 / (1.0 + 1e-8), -10, 10), rtol=1e-15, atol=0)
