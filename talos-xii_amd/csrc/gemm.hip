@@ -15,6 +15,8 @@
 // Long-K products with a small C (the weight gradients, K = tokens) are split over K; the fp32
 // partial tiles are combined in f64 by a second kernel, which keeps the gradient sums over
 // 10^5 tokens within the accuracy of an fp32 dot product of length K/ksplit.
+#include <algorithm>
+
 #include "gemm.hpp"
 
 namespace talos {
@@ -697,14 +699,13 @@ size_t gemm_plan_split(GemmDesc& d, int num_cu) {
   const int e = epi_flags(d);
   if (d.ksplit == 0) {
     const long long tiles = (long long)((d.M + BM - 1) / BM) * ((d.N + BN - 1) / BN) * d.batch;
-    int ks = 1;
-    // Split until the grid holds TALOS_SPLITK_WG_PER_CU workgroups per CU, keeping at least
+    // Split so that the grid holds TALOS_SPLITK_WG_PER_CU workgroups per CU (any split count,
+    // not only powers of two: 3 tiles get 170 splits, not 128), keeping at least
     // TALOS_SPLITK_MIN_K of K per split: the partial traffic (ksplit * M * N floats) stays small
     // next to A and B.
-    while (tiles * ks * 2 <= (long long)TALOS_SPLITK_WG_PER_CU * num_cu &&
-           (long long)d.K / (ks * 2) >= TALOS_SPLITK_MIN_K)
-      ks *= 2;
-    d.ksplit = ks;
+    long long ks = (long long)TALOS_SPLITK_WG_PER_CU * num_cu / std::max(1LL, tiles);
+    ks = std::min(ks, (long long)d.K / TALOS_SPLITK_MIN_K);
+    d.ksplit = (int)std::max(1LL, ks);
   }
   if ((e & ~(E_BETA | E_BIAS | E_DBIAS)) != 0) d.ksplit = 1;  // only beta / bias survive a split
   if (d.ksplit <= 1) return 0;
