@@ -6,10 +6,13 @@
 //
 // Tiling: a 256-thread workgroup owns a 128x128 tile of C; each of its four waves owns a
 // 64x64 quarter as 2x2 MFMA 32x32 accumulators (64 accumulator registers per lane). K advances
-// in chunks of 32 staged through LDS as k-major panels As[k][m], Bs[k][n]; the next chunk is
-// fetched into registers while the matrix cores work on the current one. Both transposed and
-// plain operand layouts are read with 16-byte loads along their contiguous dimension; interior
-// tiles take an unchecked load / store path and only edge tiles test bounds per element.
+// in chunks of 32 staged through LDS; the next chunk is fetched into registers while the matrix
+// cores work on the current one. Each operand panel keeps the layout the operand has in memory:
+// k-contiguous operands (A plain, B transposed) as rows of 32 k values (pitch 36), read by the
+// MFMA lanes as 16-byte fragments of 4 consecutive k; the others k-major (pitch 136), read one
+// value per lane. Global loads and LDS stores are 16 bytes wide in both cases, and the k order
+// of the MFMA chain (step s, half h <-> k = 8(s/4) + 4h + s%4) is shared by the two operands.
+// Interior tiles take an unchecked load / store path; only edge tiles test bounds per element.
 // The epilogue (bias, residual, activation or its derivative, RoPE) is a compile-time set of
 // flags, so each instantiation carries only the code it uses.
 // Long-K products with a small C (the weight gradients, K = tokens) are split over K; the fp32
@@ -24,8 +27,13 @@ namespace talos {
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, BK = 32;
-constexpr int LDS_S = 160;  // panel row stride (floats): the two half-waves read rows k, k+1
-                            // whose offset 160 = 32 mod 64 keeps them on disjoint LDS banks
+// k-major panel X[k][r]: the two half-waves read rows k and k + 4, whose offset 4 * 136 = 32
+// mod 64 banks keeps them on disjoint banks.
+constexpr int LDS_S = 136;
+// k-contiguous panel X[r][k]: 16-byte fragments of 16 consecutive rows fall on 16 distinct
+// groups of 4 banks (row * 9 mod 16).
+constexpr int KP = 36;
+constexpr int PANEL = (BK * LDS_S > 128 * KP) ? BK * LDS_S : 128 * KP;  // floats per panel
 constexpr int NT = 256;
 // Tuning knobs (compile-time): TALOS_GEMM_DBUF = 1 double-buffers the LDS panels (one barrier per
 // K chunk); TALOS_GEMM_WAVES = minimum waves per SIMD the register allocation must allow.
@@ -33,7 +41,7 @@ constexpr int NT = 256;
 #define TALOS_GEMM_DBUF 0
 #endif
 #ifndef TALOS_GEMM_WAVES
-#define TALOS_GEMM_WAVES 2
+#define TALOS_GEMM_WAVES 4
 #endif
 // Split-K sizing: target workgroups per CU and the minimum K per split.
 #ifndef TALOS_SPLITK_WG_PER_CU
@@ -125,15 +133,11 @@ __device__ __forceinline__ void load_a(const GemmArgs& p, const float* __restric
 template <bool TA>
 __device__ __forceinline__ void store_a(float* As, const float4 (&r)[4]) {
   const int t = threadIdx.x;
-  if (!TA) {
+  if (!TA) {  // k-contiguous panel As[m][k]
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int kk = 4 * ((t >> 7) + 2 * i);
-      float* d = As + kk * LDS_S + (t & 127);
-      d[0] = r[i].x;
-      d[LDS_S] = r[i].y;
-      d[2 * LDS_S] = r[i].z;
-      d[3 * LDS_S] = r[i].w;
+      *reinterpret_cast<float4*>(As + (t & 127) * KP + kk) = r[i];
     }
   } else {
 #pragma unroll
@@ -185,6 +189,25 @@ __device__ __forceinline__ void load_b(const GemmArgs& p, const float* __restric
 template <bool TB>
 __device__ __forceinline__ void store_b(float* Bs, const float4 (&r)[4]) {
   store_a<!TB>(Bs, r);
+}
+
+// MFMA operand values of rows r and r + 32 of a panel at k = k0 .. k0 + 3 (k0 = 8j + 4h):
+// KC = true, a k-contiguous panel X[r][k] (two 16-byte reads); KC = false, a k-major panel
+// X[k][r] (one value per k).
+template <bool KC>
+__device__ __forceinline__ void frag4(const float* X, int r, int k0, float (&f0)[4], float (&f1)[4]) {
+  if (KC) {
+    const float4 v0 = *reinterpret_cast<const float4*>(X + r * KP + k0);
+    const float4 v1 = *reinterpret_cast<const float4*>(X + (r + 32) * KP + k0);
+    f0[0] = v0.x; f0[1] = v0.y; f0[2] = v0.z; f0[3] = v0.w;
+    f1[0] = v1.x; f1[1] = v1.y; f1[2] = v1.z; f1[3] = v1.w;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f0[q] = X[(k0 + q) * LDS_S + r];
+      f1[q] = X[(k0 + q) * LDS_S + r + 32];
+    }
+  }
 }
 
 template <bool TA, bool TB>
@@ -296,7 +319,7 @@ __device__ __forceinline__ void epi_store4(const GemmArgs& p, float4 v, int row,
 
 constexpr int T_S = 136;  // pitch of the staged output tile: rows h*4 apart land 32 banks apart
 constexpr int T_ROWS = BM / 2;  // the tile is staged in two halves of 64 rows
-constexpr int SMEM_FLOATS = (2 * NBUF * BK * LDS_S > T_ROWS * T_S) ? 2 * NBUF * BK * LDS_S : T_ROWS * T_S;
+constexpr int SMEM_FLOATS = (2 * NBUF * PANEL > T_ROWS * T_S) ? 2 * NBUF * PANEL : T_ROWS * T_S;
 
 // ---------------------------------------------------------------------------
 // bf16-in / fp32-accumulate operand staging: panels of BKB = 64 k values are rounded to bf16 and
@@ -388,12 +411,12 @@ __device__ __forceinline__ void store_bf(uint16_t* S, const uint32_t (&o)[16]) {
 }
 
 template <bool TA, bool TB, int E, bool BF>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_WAVES))) void gemm_f32_kernel(
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TALOS_GEMM_WAVES))) void gemm_f32_kernel(
     GemmArgs p) {
   __shared__ __align__(16) float smem[SMEM_FLOATS];
-  // panels: As buffer i at smem + i*BK*LDS_S, Bs buffer i after the NBUF A buffers
+  // panels: As buffer i at smem + i*PANEL, Bs buffer i after the NBUF A buffers
   float* const Abase = smem;
-  float* const Bbase = smem + NBUF * BK * LDS_S;
+  float* const Bbase = smem + NBUF * PANEL;
 
   // XCD-aware order: the dispatcher sends workgroup i to XCD i % 8, so logical tiles are dealt
   // out in contiguous runs per XCD; the N tiles of one M panel (and the tiles of one K split)
@@ -480,21 +503,26 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_W
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
     const bool more = k0 + BK < kend;
     if (more) load_chunk<TA, TB>(p, A, B, m0, n0, k0 + BK, kend, interior, ra, rb);
-    const float* ap = Abase + buf * (BK * LDS_S) + h * LDS_S + wm * 64 + l32;
-    const float* bp = Bbase + buf * (BK * LDS_S) + h * LDS_S + wn * 64 + l32;
+    const float* Ap = Abase + buf * PANEL;
+    const float* Bp = Bbase + buf * PANEL;
 #pragma unroll
-    for (int s = 0; s < BK / 2; ++s) {
-      const float a0 = ap[2 * s * LDS_S], a1 = ap[2 * s * LDS_S + 32];
-      const float b0 = bp[2 * s * LDS_S], b1 = bp[2 * s * LDS_S + 32];
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+    for (int j = 0; j < BK / 8; ++j) {
+      // fragments of steps 4j .. 4j+3: k = 8j + 4h + q for q = 0..3
+      float fa0[4], fa1[4], fb0[4], fb1[4];
+      frag4<!TA>(Ap, wm * 64 + l32, 8 * j + 4 * h, fa0, fa1);
+      frag4<TB>(Bp, wn * 64 + l32, 8 * j + 4 * h, fb0, fb1);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb0[q], acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb1[q], acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb0[q], acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb1[q], acc[1][1], 0, 0, 0);
+      }
     }
     if constexpr ((E & E_DBIAS) != 0) {
       // column sums of the B panel Bs[k][n] (k-major): thread t sums column t%128 over half the rows
       if (m0 == 0) {
-        const float* bc = Bbase + buf * (BK * LDS_S) + (threadIdx.x >> 7) * (BK / 2) * LDS_S + (threadIdx.x & 127);
+        const float* bc = Bbase + buf * PANEL + (threadIdx.x >> 7) * (BK / 2) * LDS_S + (threadIdx.x & 127);
 #pragma unroll
         for (int kk = 0; kk < BK / 2; ++kk) csum += bc[kk * LDS_S];
       }
@@ -502,8 +530,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_W
     if (NBUF == 2) {
       // the other buffer was last read in the previous chunk, before the barrier that ended it
       if (more) {
-        store_a<TA>(Abase + (buf ^ 1) * (BK * LDS_S), ra);
-        store_b<TB>(Bbase + (buf ^ 1) * (BK * LDS_S), rb);
+        store_a<TA>(Abase + (buf ^ 1) * PANEL, ra);
+        store_b<TB>(Bbase + (buf ^ 1) * PANEL, rb);
       }
       __syncthreads();
       buf ^= 1;
