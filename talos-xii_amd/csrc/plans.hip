@@ -468,21 +468,22 @@ __global__ void scatter_last_kernel(int B, int S, int d, const int32_t* __restri
 // Per sample: lp = z - lse(z); ratio = exp(lp[a] - old); surr1 = ratio*adv;
 // surr2 = clip(ratio, 1-eps, 1+eps)*adv; the smaller by value is kept (ties take surr2, whose
 // gradient passes only inside the clip range); v = (value - ret)^2; ent = -sum p*lp;
-// loss = -pol + cv*v - ce*ent. stats (optional) receives the sums over the samples of
-// approx_kl = (ratio - 1) - log_ratio (src/ppo.rs:726-729), pol, v, ent and the sample count,
-// added to its previous contents when stats_acc != 0.
+// loss = -pol + cv*v - ce*ent. One thread per sample; each workgroup writes its sums of the loss,
+// approx_kl = (ratio - 1) - log_ratio (src/ppo.rs:726-729), pol, v and ent to one partial row,
+// which ppo_loss_final_kernel adds up in a fixed order.
+constexpr int kLossParts = 5;
 __global__ __launch_bounds__(256) void ppo_loss_kernel(int B, int A, float clip_eps, float cv, float ce,
                                                        const float* __restrict__ logits,
                                                        const float* __restrict__ values,
                                                        const int32_t* __restrict__ actions,
                                                        const float* __restrict__ adv, const float* __restrict__ ret,
-                                                       const float* __restrict__ old_logp, float* __restrict__ loss,
+                                                       const float* __restrict__ old_logp,
                                                        float* __restrict__ dlogits, float* __restrict__ dvalues,
-                                                       int with_grad, double* __restrict__ stats, int stats_acc) {
+                                                       int with_grad, double* __restrict__ part) {
   __shared__ double red[4];
   double total = 0.0, s_kl = 0.0, s_pol = 0.0, s_v = 0.0, s_ent = 0.0;
   const double invB = 1.0 / (double)B;
-  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+  for (int b = blockIdx.x * blockDim.x + threadIdx.x; b < B; b += gridDim.x * blockDim.x) {
     const float* z = logits + (long long)b * A;
     double mx = -INFINITY;
     for (int j = 0; j < A; ++j) mx = fmax(mx, (double)z[j]);
@@ -536,14 +537,24 @@ __global__ __launch_bounds__(256) void ppo_loss_kernel(int B, int A, float clip_
       dvalues[b] = (float)(2.0 * (double)cv * vd * invB);
     }
   }
-  total = block_sum(total, red);
-  if (threadIdx.x == 0 && loss) loss[0] = (float)(total * invB);
+  const double sums[kLossParts] = {block_sum(total, red), block_sum(s_kl, red), block_sum(s_pol, red),
+                                   block_sum(s_v, red), block_sum(s_ent, red)};
+  if (threadIdx.x == 0)
+    for (int i = 0; i < kLossParts; ++i) part[(long long)blockIdx.x * kLossParts + i] = sums[i];
+}
+
+// loss[0] = mean loss; stats (optional) = (or +=) the sums of kl, pol, v, ent and the count.
+__global__ __launch_bounds__(64) void ppo_loss_final_kernel(int nblk, int B, const double* __restrict__ part,
+                                                            float* __restrict__ loss, double* __restrict__ stats,
+                                                            int stats_acc) {
+  if (threadIdx.x != 0) return;
+  double sums[kLossParts] = {0.0, 0.0, 0.0, 0.0, 0.0};
+  for (int k = 0; k < nblk; ++k)
+    for (int i = 0; i < kLossParts; ++i) sums[i] += part[(long long)k * kLossParts + i];
+  if (loss) loss[0] = (float)(sums[0] / (double)B);
   if (stats) {
-    const double sums[4] = {block_sum(s_kl, red), block_sum(s_pol, red), block_sum(s_v, red), block_sum(s_ent, red)};
-    if (threadIdx.x == 0) {
-      for (int i = 0; i < 4; ++i) stats[i] = (stats_acc ? stats[i] : 0.0) + sums[i];
-      stats[4] = (stats_acc ? stats[4] : 0.0) + (double)B;
-    }
+    for (int i = 0; i < 4; ++i) stats[i] = (stats_acc ? stats[i] : 0.0) + sums[i + 1];
+    stats[4] = (stats_acc ? stats[4] : 0.0) + (double)B;
   }
 }
 
@@ -818,6 +829,11 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
   rc |= plan_alloc(p, &p->g_pout, B * d);
   rc |= plan_alloc(p, &p->g_lastn, B * d);
   rc |= plan_alloc(p, &p->g_last, B * d);
+  {  // per-workgroup loss partials (doubles)
+    float* lw = nullptr;
+    rc |= plan_alloc(p, &lw, 2 * kLossParts * ceil_div(B, 256));
+    p->loss_ws = reinterpret_cast<double*>(lw);
+  }
   if (rc == TALOS_OK) {
     p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, wgrad_ws(p, (int)M, cfg->in_dim, (int)d));
     p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, wgrad_ws(p, (int)B, (int)d, (int)d));
@@ -885,11 +901,18 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
   int rc = ppo_forward(p, c, params, states, s);
   if (rc) return rc;
   {
-  ProfScope ps_l(s, "ppo_loss_kernel", 0.0, 4.0 * B * (2.0 * A + 5.0));
-  hipLaunchKernelGGL(ppo_loss_kernel, dim3(1), dim3(256), 0, s, B, A, c.clip_eps, c.value_coef, c.entropy_coef,
-                     p->logits, p->values, actions, adv, ret, old_logp, loss_out, p->g_logits, p->g_values, 1, stats,
+  const int nblk = (int)ceil_div((size_t)B, 256);
+  {
+    ProfScope ps_l(s, "ppo_loss_kernel", 0.0, 4.0 * B * (2.0 * A + 5.0));
+    hipLaunchKernelGGL(ppo_loss_kernel, dim3(nblk), dim3(256), 0, s, B, A, c.clip_eps, c.value_coef,
+                       c.entropy_coef, p->logits, p->values, actions, adv, ret, old_logp, p->g_logits, p->g_values, 1,
+                       p->loss_ws);
+    TALOS_LAUNCHED("ppo_loss_kernel");
+  }
+  ProfScope ps_f(s, "ppo_loss_final_kernel", 0.0, 8.0 * nblk * kLossParts);
+  hipLaunchKernelGGL(ppo_loss_final_kernel, dim3(1), dim3(64), 0, s, nblk, B, p->loss_ws, loss_out, stats,
                      stats_acc);
-  TALOS_LAUNCHED("ppo_loss_kernel");
+  TALOS_LAUNCHED("ppo_loss_final_kernel");
   }
   float* G = dparams;
   // heads
