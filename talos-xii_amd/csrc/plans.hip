@@ -286,10 +286,11 @@ static int mm(talos_plan_s* p, hipStream_t s, int tA, int tB, int M, int N, int 
   return gemm_launch(g, s);
 }
 
-// Forward of one block; L.x must be set. Writes L.out.
-static int block_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
-                         talos_plan_s::Layer& L, hipStream_t s) {
-  const int M = c.batch * c.seq, d = c.d_model, F = c.ffn_dim;
+// Attention half of a block's forward: xn1 = rmsnorm(x), qkv = xn1.Wqkv (RoPE in the epilogue),
+// o = attention(q, k, v) with lse saved. L.x must be set.
+static int block_attn_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
+                              talos_plan_s::Layer& L, hipStream_t s) {
+  const int M = c.batch * c.seq, d = c.d_model;
   int rc = rmsnorm_fwd_launch(M, d, c.eps, L.x, P + o.g1, L.xn1, L.rstd1, s);
   if (rc) return rc;
   {
@@ -312,91 +313,114 @@ static int block_forward(talos_plan_s* p, const talos_block_cfg& c, const float*
     rc = gemm_launch(g, s);
     if (rc) return rc;
   }
-  {
-    AttnDesc a;
-    a.batch = c.batch;
-    a.seq = c.seq;
-    a.heads = c.n_heads;
-    a.dk = a.dv = c.head_dim;
-    a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
-    a.causal = c.causal;
-    a.q = L.qkv;
-    a.k = L.qkv + d;
-    a.v = L.qkv + 2 * d;
-    a.ldq = a.ldk = a.ldv = 3 * d;
-    a.o = L.o;
-    a.ldo = d;
-    a.lse = L.lse;
-    a.lens = p->lens;
-    rc = attn_fwd_launch(a, s);
-    if (rc) return rc;
-  }
-  rc = mm(p, s, 0, 0, M, d, d, L.o, d, P + o.wo, d, L.h2, d, 0.f, nullptr, L.x, d);
+  AttnDesc a;
+  a.batch = c.batch;
+  a.seq = c.seq;
+  a.heads = c.n_heads;
+  a.dk = a.dv = c.head_dim;
+  a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+  a.causal = c.causal;
+  a.q = L.qkv;
+  a.k = L.qkv + d;
+  a.v = L.qkv + 2 * d;
+  a.ldq = a.ldk = a.ldv = 3 * d;
+  a.o = L.o;
+  a.ldo = d;
+  a.lse = L.lse;
+  a.lens = p->lens;
+  return attn_fwd_launch(a, s);
+}
+
+// Second half over R rows (all tokens, or only the last token of each sample): h2 = x + o.Wo,
+// xn2 = rmsnorm(h2), u = xn2.W1 + b1, a = act(u), out = h2 + a.W2 + b2.
+static int block_mlp_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o, int R,
+                             const float* x, const float* ob, float* h2, float* xn2, float* rstd2, float* u, float* a,
+                             float* out, hipStream_t s) {
+  const int d = c.d_model, F = c.ffn_dim;
+  int rc = mm(p, s, 0, 0, R, d, d, ob, d, P + o.wo, d, h2, d, 0.f, nullptr, x, d);
   if (rc) return rc;
-  rc = rmsnorm_fwd_launch(M, d, c.eps, L.h2, P + o.g2, L.xn2, L.rstd2, s);
+  rc = rmsnorm_fwd_launch(R, d, c.eps, h2, P + o.g2, xn2, rstd2, s);
   if (rc) return rc;
   {
     GemmDesc g;
-    g.M = M;
+    g.M = R;
     g.N = F;
     g.K = d;
-    g.A = L.xn2;
+    g.A = xn2;
     g.lda = d;
     g.B = P + o.w1;
     g.ldb = F;
-    g.C = L.a;
+    g.C = a;
     g.ldc = F;
     g.bias = P + o.b1;
     g.act = c.activation == TALOS_ACT_GELU ? GEMM_ACT_GELU : GEMM_ACT_RELU;
-    g.aux = L.u;
+    g.aux = u;
     g.ldaux = F;
     g.ksplit = 1;
     rc = gemm_launch(g, s);
     if (rc) return rc;
   }
-  return mm(p, s, 0, 0, M, d, F, L.a, F, P + o.w2, d, L.out, d, 0.f, P + o.b2, L.h2, d);
+  return mm(p, s, 0, 0, R, d, F, a, F, P + o.w2, d, out, d, 0.f, P + o.b2, h2, d);
 }
 
-// Backward of one block: gout = dL/dout (read), writes dparams slots and dx.
-static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
-                          talos_plan_s::Layer& L, const float* gout, float* dx, hipStream_t s) {
-  const int M = c.batch * c.seq, d = c.d_model, F = c.ffn_dim;
-  int rc;
+// Forward of one block; L.x must be set. Writes L.out.
+static int block_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
+                         talos_plan_s::Layer& L, hipStream_t s) {
+  int rc = block_attn_forward(p, c, P, o, L, s);
+  if (rc) return rc;
+  return block_mlp_forward(p, c, P, o, c.batch * c.seq, L.x, L.o, L.h2, L.xn2, L.rstd2, L.u, L.a, L.out, s);
+}
+
+// MLP half backward over R rows: gout = dL/dout; writes the W2 / W1 / gain2 gradients, the
+// gradient of h2 (g_h2, residual included) and of o (g_o), and uses g_u, g_xn as scratch.
+static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
+                              int R, const float* ob, const float* h2, const float* xn2, const float* rstd2,
+                              const float* u, const float* a, const float* gout, float* g_u, float* g_xn, float* g_h2,
+                              float* g_o, hipStream_t s) {
+  const int d = c.d_model, F = c.ffn_dim;
   // out = h2 + a.W2 + b2
-  rc = mm(p, s, 1, 0, F, d, M, L.a, F, gout, d, G + o.w2, d, 0.f, nullptr, nullptr, 0, G + o.b2);
+  int rc = mm(p, s, 1, 0, F, d, R, a, F, gout, d, G + o.w2, d, 0.f, nullptr, nullptr, 0, G + o.b2);
   if (rc) return rc;
   {
     GemmDesc g;
     g.transB = 1;
-    g.M = M;
+    g.M = R;
     g.N = F;
     g.K = d;
     g.A = gout;
     g.lda = d;
     g.B = P + o.w2;
     g.ldb = d;
-    g.C = p->g_u;
+    g.C = g_u;
     g.ldc = F;
     g.dact = c.activation == TALOS_ACT_GELU ? GEMM_DACT_GELU : GEMM_DACT_RELU;
-    g.aux = L.u;
+    g.aux = const_cast<float*>(u);  // read only: the derivative epilogue
     g.ldaux = F;
     g.ksplit = 1;
     rc = gemm_launch(g, s);
     if (rc) return rc;
   }
   // u = xn2.W1 + b1
-  rc = mm(p, s, 1, 0, d, F, M, L.xn2, d, p->g_u, F, G + o.w1, F, 0.f, nullptr, nullptr, 0, G + o.b1);
+  rc = mm(p, s, 1, 0, d, F, R, xn2, d, g_u, F, G + o.w1, F, 0.f, nullptr, nullptr, 0, G + o.b1);
   if (rc) return rc;
-  rc = mm(p, s, 0, 1, M, d, F, p->g_u, F, P + o.w1, F, p->g_xn, d);
+  rc = mm(p, s, 0, 1, R, d, F, g_u, F, P + o.w1, F, g_xn, d);
   if (rc) return rc;
   // h2 -> (residual) + rmsnorm2
-  rc = rmsnorm_bwd_launch(M, d, L.h2, P + o.g2, L.rstd2, p->g_xn, 1.f, p->g_h2, 0.f, G + o.g2, p->red_ws, s, gout);
+  rc = rmsnorm_bwd_launch(R, d, h2, P + o.g2, rstd2, g_xn, 1.f, g_h2, 0.f, G + o.g2, p->red_ws, s, gout);
   if (rc) return rc;
   // h2 = x + o.Wo
-  rc = mm(p, s, 1, 0, d, d, M, L.o, d, p->g_h2, d, G + o.wo, d);
+  rc = mm(p, s, 1, 0, d, d, R, ob, d, g_h2, d, G + o.wo, d);
   if (rc) return rc;
-  rc = mm(p, s, 0, 1, M, d, d, p->g_h2, d, P + o.wo, d, p->g_o, d);
-  if (rc) return rc;
+  return mm(p, s, 0, 1, R, d, d, g_h2, d, P + o.wo, d, g_o, d);
+}
+
+// Attention half backward over all rows: g_o = dL/do, g_h2 = the residual gradient reaching x
+// through h2; writes the Wqkv / gain1 gradients and dx.
+static int block_attn_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
+                               talos_plan_s::Layer& L, const float* g_o, const float* g_h2, float* dx,
+                               hipStream_t s) {
+  const int M = c.batch * c.seq, d = c.d_model;
+  int rc;
   {
     AttnDesc a;
     a.batch = c.batch;
@@ -412,7 +436,7 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
     a.o = L.o;
     a.ldo = d;
     a.lse = L.lse;
-    a.dout = p->g_o;
+    a.dout = g_o;
     a.lddo = d;
     a.dq = p->g_qkv;
     a.dk_out = p->g_qkv + d;
@@ -431,7 +455,17 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
   if (rc) return rc;
   rc = mm(p, s, 0, 1, M, d, 3 * d, p->g_qkv, 3 * d, P + o.wqkv, 3 * d, p->g_xn, d);
   if (rc) return rc;
-  return rmsnorm_bwd_launch(M, d, L.x, P + o.g1, L.rstd1, p->g_xn, 1.f, dx, 0.f, G + o.g1, p->red_ws, s, p->g_h2);
+  return rmsnorm_bwd_launch(M, d, L.x, P + o.g1, L.rstd1, p->g_xn, 1.f, dx, 0.f, G + o.g1, p->red_ws, s, g_h2);
+}
+
+// Backward of one block: gout = dL/dout (read), writes dparams slots and dx.
+static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
+                          talos_plan_s::Layer& L, const float* gout, float* dx, hipStream_t s) {
+  const int M = c.batch * c.seq;
+  int rc = block_mlp_backward(p, c, P, G, o, M, L.o, L.h2, L.xn2, L.rstd2, L.u, L.a, gout, p->g_u, p->g_xn, p->g_h2,
+                              p->g_o, s);
+  if (rc) return rc;
+  return block_attn_backward(p, c, P, G, o, L, p->g_o, p->g_h2, dx, s);
 }
 
 // Last-token gather / scatter -----------------------------------------------
