@@ -233,8 +233,11 @@ def main():
     roof["traffic"] = traffic_of(dominant)
     roof["algorithmic_per_launch"] = {"flops": fl / n, "bytes": by / n}
 
-    step_flops = wl.ppo_step_flops(B, cfg.seq, cfg.in_dim, cfg.d_model, cfg.n_layers, cfg.n_heads, cfg.ffn_dim,
-                                   cfg.n_actions)
+    # live work (what the loss depends on; the plan skips the last layer's dead rows) and the
+    # reference's whole graph
+    shape = (B, cfg.seq, cfg.in_dim, cfg.d_model, cfg.n_layers, cfg.n_heads, cfg.ffn_dim, cfg.n_actions)
+    step_flops = wl.ppo_step_flops(*shape)
+    graph_flops = wl.ppo_step_flops(*shape, live=False)
     info = th.device_info()
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
@@ -246,6 +249,7 @@ def main():
                    "n_heads": cfg.n_heads, "ffn_dim": cfg.ffn_dim, "n_actions": cfg.n_actions},
         "roofline": roof,
         "step": {"algorithmic_gflop": round(step_flops / 1e9, 2),
+                 "reference_graph_gflop": round(graph_flops / 1e9, 2),
                  "tflops": round(step_flops / (ms_step * 1e-3) / 1e12, 2),
                  "frac_fp32_mfma_peak": round(step_flops / (ms_step * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
                  "wall_ms_per_step": round(wall * 1e3 / args.steps, 4)},

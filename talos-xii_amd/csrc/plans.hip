@@ -54,6 +54,11 @@ struct talos_plan_s {
         *values = nullptr, *g_logits = nullptr, *g_values = nullptr, *g_pout = nullptr, *g_lastn = nullptr,
         *g_last = nullptr;
   double* loss_ws = nullptr;
+  // the last layer's MLP half on the last-token rows only: its inputs gathered from x and o,
+  // its activations and the backward scratch, [batch, d] / [batch, F]
+  struct LastRows {
+    float *x, *o, *h2, *xn2, *rstd2, *u, *a, *g_u, *g_xn, *g_h2, *g_o;
+  } lr{};
   const int32_t* lens = nullptr;  // per-sample lengths of the PPO call in progress (nullptr: all seq)
   int num_cu = 256;
   bool bf16 = false;  // bf16-in / fp32-accumulate GEMMs (MLA plans with TALOS_PREC_BF16)
@@ -611,19 +616,35 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
   if (rc) return rc;
   const float* h = p->h0;
   size_t base = po.blocks;
-  for (int l = 0; l < c.n_layers; ++l) {
-    BlockOff bo = block_offsets(bc, base);
-    p->layers[l].x = const_cast<float*>(h);
-    rc = block_forward(p, bc, P, bo, p->layers[l], s);
-    if (rc) return rc;
-    h = p->layers[l].out;
-    base = bo.end;
-  }
-  {
+  auto gather = [&](const float* src, float* dst) {
     ProfScope ps_g(s, "gather_last_kernel", 0.0, 8.0 * c.batch * d);
     hipLaunchKernelGGL(gather_last_kernel, dim3(ceil_div((size_t)c.batch * d, 256)), dim3(256), 0, s, c.batch, c.seq,
-                       d, p->lens, h, p->last);
-    TALOS_LAUNCHED("gather_last_kernel");
+                       d, p->lens, src, dst);
+    return launch_status("gather_last_kernel");
+  };
+  for (int l = 0; l < c.n_layers; ++l) {
+    BlockOff bo = block_offsets(bc, base);
+    auto& L = p->layers[l];
+    L.x = const_cast<float*>(h);
+    if (l + 1 < c.n_layers) {
+      rc = block_forward(p, bc, P, bo, L, s);
+      if (rc) return rc;
+      h = L.out;
+    } else {
+      // Only the last token of each sample reaches the heads, and everything after attention is
+      // per row: the last layer runs its MLP half on those B rows and writes p->last directly.
+      rc = block_attn_forward(p, bc, P, bo, L, s);
+      if (rc) return rc;
+      if ((rc = gather(L.x, p->lr.x)) || (rc = gather(L.o, p->lr.o))) return rc;
+      rc = block_mlp_forward(p, bc, P, bo, c.batch, p->lr.x, p->lr.o, p->lr.h2, p->lr.xn2, p->lr.rstd2, p->lr.u,
+                             p->lr.a, p->last, s);
+      if (rc) return rc;
+    }
+    base = bo.end;
+  }
+  if (c.n_layers == 0) {
+    rc = gather(h, p->last);
+    if (rc) return rc;
   }
   rc = rmsnorm_fwd_launch(c.batch, d, c.eps, p->last, P + po.gf, p->lastn, p->rstdf, s);
   if (rc) return rc;
@@ -863,6 +884,13 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
   rc |= plan_alloc(p, &p->g_pout, B * d);
   rc |= plan_alloc(p, &p->g_lastn, B * d);
   rc |= plan_alloc(p, &p->g_last, B * d);
+  {  // the last layer's last-token rows
+    const size_t F = cfg->ffn_dim;
+    auto& R = p->lr;
+    for (float** b : {&R.x, &R.o, &R.h2, &R.xn2, &R.g_xn, &R.g_h2, &R.g_o}) rc |= plan_alloc(p, b, B * d);
+    for (float** b : {&R.u, &R.a, &R.g_u}) rc |= plan_alloc(p, b, B * F);
+    rc |= plan_alloc(p, &R.rstd2, B);
+  }
   {  // per-workgroup loss partials (doubles)
     float* lw = nullptr;
     rc |= plan_alloc(p, &lw, 2 * kLossParts * ceil_div(B, 256));
@@ -967,22 +995,39 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
   rc = rmsnorm_bwd_launch(B, d, p->last, params + po.gf, p->rstdf, p->g_lastn, 0.f, p->g_last, 0.f, G + po.gf,
                           p->red_ws, s);
   if (rc) return rc;
-  {
-  ProfScope ps_s(s, "scatter_last_kernel", 0.0, 4.0 * ((double)M * d + (double)B * d));
-  hipLaunchKernelGGL(scatter_last_kernel, dim3(ceil_div((size_t)M * d, 256) > 65536 ? 65536 : ceil_div((size_t)M * d, 256)),
-                     dim3(256), 0, s, B, c.seq, d, p->lens, p->g_last, p->g_out);
-  TALOS_LAUNCHED("scatter_last_kernel");
-  }
-  // blocks, last to first; the gradient ping-pongs between g_out and g_x
-  float* gcur = p->g_out;
-  float* gnext = p->g_x;
+  // rows of a [B, d] last-token gradient into a full [M, d] one, zero elsewhere
+  auto scatter = [&](const float* src, float* dst) {
+    ProfScope ps_s(s, "scatter_last_kernel", 0.0, 4.0 * ((double)M * d + (double)B * d));
+    hipLaunchKernelGGL(scatter_last_kernel,
+                       dim3(ceil_div((size_t)M * d, 256) > 65536 ? 65536 : ceil_div((size_t)M * d, 256)), dim3(256), 0,
+                       s, B, c.seq, d, p->lens, src, dst);
+    return launch_status("scatter_last_kernel");
+  };
   std::vector<BlockOff> offs;
   size_t base = po.blocks;
   for (int l = 0; l < c.n_layers; ++l) {
     offs.push_back(block_offsets(bc, base));
     base = offs.back().end;
   }
-  for (int l = c.n_layers - 1; l >= 0; --l) {
+  // blocks, last to first; the gradient ping-pongs between g_out and g_x
+  float* gcur = p->g_out;
+  float* gnext = p->g_x;
+  if (c.n_layers == 0) {
+    rc = scatter(p->g_last, p->g_out);
+    if (rc) return rc;
+  } else {
+    // the last layer: MLP half on the last-token rows (the forward's p->lr), then its row
+    // gradients spread over the full token grid for the attention half
+    const int l = c.n_layers - 1;
+    auto& R = p->lr;
+    rc = block_mlp_backward(p, bc, params, G, offs[l], B, R.o, R.h2, R.xn2, R.rstd2, R.u, R.a, p->g_last, R.g_u,
+                            R.g_xn, R.g_h2, R.g_o, s);
+    if (rc) return rc;
+    if ((rc = scatter(R.g_o, p->g_o)) || (rc = scatter(R.g_h2, p->g_h2))) return rc;
+    rc = block_attn_backward(p, bc, params, G, offs[l], p->layers[l], p->g_o, p->g_h2, p->g_out, s);
+    if (rc) return rc;
+  }
+  for (int l = c.n_layers - 2; l >= 0; --l) {
     rc = block_backward(p, bc, params, G, offs[l], p->layers[l], gcur, gnext, s);
     if (rc) return rc;
     std::swap(gcur, gnext);

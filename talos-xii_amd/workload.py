@@ -66,16 +66,30 @@ def log_softmax(z):
     return z - mx - np.log(np.exp(z - mx).sum(-1, keepdims=True))
 
 
-def ppo_step_flops(B, S, in_dim, d, L, H, F, A, causal=True):
-    """Algorithmic flops of one minibatch forward + backward (multiply-add = 2 flops):
-    per layer the QKV / O projections (4 * 2 M d^2), the MLP (2 * 2 M d F) and attention
-    (QK^T and PV over the kept (query, key) pairs, 2 * 2 * B * H * hd * pairs); the embedding
-    (2 M in d), and on the B last-token rows out_proj (2 B d^2) and the heads (2 B d (A+1)).
-    The backward is twice the forward minus the embedding's input gradient, which is not formed."""
+def ppo_step_flops(B, S, in_dim, d, L, H, F, A, causal=True, live=True):
+    """Algorithmic flops of one minibatch forward + backward (multiply-add = 2 flops): per layer
+    the QKV / O projections (4 * 2 M d^2), the MLP (2 * 2 M d F) and attention (QK^T and PV over
+    the kept (query, key) pairs, 2 * 2 * B * H * hd * pairs); the embedding (2 M in d), and on the
+    B last-token rows out_proj (2 B d^2) and the heads (2 B d (A+1)). The backward is twice the
+    forward (dX and dW of every product) minus the embedding's input gradient, which is not formed.
+
+    live=False counts the whole graph the reference builds. live=True counts the work the loss
+    depends on: the heads read only the last token of each sample and everything after attention
+    acts per row, so in the last layer the query projection, attention, output projection and MLP
+    matter on those B rows only, while keys and values (and their gradients) still cover all M
+    rows. The live attention backward of one (sample, head) is 5 products of 2 * S * hd (the last
+    query's scores and dP recomputed, dq, dk, dv)."""
     M = B * S
     hd = d // H
     pairs = S * (S + 1) / 2 if causal else S * S
     layer = 4 * 2 * M * d * d + 2 * 2 * M * d * F + 2 * 2 * B * H * hd * pairs
     embed = 2 * M * in_dim * d
-    fwd = L * layer + embed + 2 * B * d * d + 2 * B * d * (A + 1)
-    return 3 * fwd - embed
+    heads = 2 * B * d * d + 2 * B * d * (A + 1)
+    if not live or L == 0:
+        return 3 * (L * layer + embed + heads) - embed
+    proj_kv, proj_q, proj_o = 2 * 2 * M * d * d, 2 * B * d * d, 2 * B * d * d
+    mlp = 2 * 2 * B * d * F
+    last_fwd = proj_kv + proj_q + 2 * 2 * B * H * hd * S + proj_o + mlp
+    last_bwd = 2 * (proj_kv + proj_q + proj_o + mlp) + 5 * 2 * B * H * hd * S
+    rest = (L - 1) * layer + embed + heads
+    return 3 * rest - embed + last_fwd + last_bwd
