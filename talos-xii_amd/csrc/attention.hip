@@ -711,6 +711,179 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
   return attn_bwd_dkv(a, dkm, dvm, s);
 }
 
+// ---------------------------------------------------------------------------
+// Last query only: attention for the one query row per sample a caller reads (the last token,
+// row key_len - 1), over all of that sample's keys. Row-parallel layout: a wave covers 64 / C
+// key rows per pass with C = D / 4 lanes per row, each lane holding 4 consecutive elements
+// (16-byte loads and stores, a row's C lanes read or write its D floats contiguously). Dot
+// products reduce over a row's C lanes, per-element sums over the wave's rows.
+// ---------------------------------------------------------------------------
+template <int C>
+__device__ __forceinline__ float row_sum(float v) {  // over the C lanes of a row
+#pragma unroll
+  for (int o = 1; o < C; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+template <int C>
+__device__ __forceinline__ float col_sum(float v) {  // over the rows of a pass (lanes c, c + C, ...)
+#pragma unroll
+  for (int o = C; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+template <int C>
+__device__ __forceinline__ float col_max(float v) {
+#pragma unroll
+  for (int o = C; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
+// R^T at position pos on the two interleaved pairs of elements e0 .. e0 + 3 (e0 even)
+__device__ __forceinline__ float4 rope_t4(float4 g, int e0, int pos, const AttnArgs& a) {
+  if (a.rcos == nullptr) return g;
+  const int half = a.rope_dim >> 1;
+  float r[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+  for (int i = 0; i < 4; i += 2) {
+    const int e = e0 + i;
+    if (e >= a.rope_off && e < a.rope_off + a.rope_dim) {
+      const int idx = pos * half + ((e - a.rope_off) >> 1);
+      const float c = a.rcos[idx], sn = a.rsin[idx];
+      const float g0 = r[i], g1 = r[i + 1];
+      r[i] = fmaf(g0, c, g1 * sn);
+      r[i + 1] = fmaf(-g0, sn, g1 * c);
+    }
+  }
+  return make_float4(r[0], r[1], r[2], r[3]);
+}
+
+// o_last[b, h] = softmax(scale q_t . K^T) V over keys j < L (t = L - 1); lse_last[b*H + h].
+template <int D>
+__global__ __launch_bounds__(256) void attn_fwd_lastq_kernel(AttnArgs a, float* __restrict__ o_last, long long ldol,
+                                                             float* __restrict__ lse_last) {
+  constexpr int C = D / 4, RPP = 64 / C;  // lanes per row, rows per pass
+  const int lane = threadIdx.x & 63, c = lane % C, r = lane / C;
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pair >= a.B * a.H) return;  // uniform per wave
+  const int b = pair / a.H, hh = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int Sk = key_len(a, b), t = Sk - 1;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float m = kNegInf, l = 0.f;
+  if (Sk > 0) {
+    float4 q = ld4(a.q + (tok0 + t) * a.ldq + hh * D + 4 * c);
+    q = make_float4(q.x * a.scale, q.y * a.scale, q.z * a.scale, q.w * a.scale);
+    for (int j0 = 0; j0 < Sk; j0 += RPP) {
+      const int j = j0 + r;
+      const bool ok = j < Sk;
+      const int jj = ok ? j : t;  // in-range row for the (discarded) loads of padding lanes
+      const float4 k = ld4(a.k + (tok0 + jj) * a.ldk + hh * D + 4 * c);
+      const float4 v = ld4(a.v + (tok0 + jj) * a.ldv + hh * D + 4 * c);
+      const float sc = row_sum<C>(dot4(q, k));
+      const float s = ok ? sc : kNegInf;
+      const float mn = fmaxf(m, col_max<C>(s));
+      const float p = ok ? expf(s - mn) : 0.f;
+      const float corr = m == kNegInf ? 0.f : expf(m - mn);
+      l = l * corr + col_sum<C>(p);  // p is the same on a row's C lanes: the sum over the pass's rows
+      acc = make_float4(acc.x * corr + p * v.x, acc.y * corr + p * v.y, acc.z * corr + p * v.z,
+                        acc.w * corr + p * v.w);
+      m = mn;
+    }
+  }
+  acc = make_float4(col_sum<C>(acc.x), col_sum<C>(acc.y), col_sum<C>(acc.z), col_sum<C>(acc.w));
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (r == 0) st4(o_last + (long long)b * ldol + hh * D + 4 * c, make_float4(acc.x * inv, acc.y * inv, acc.z * inv,
+                                                                          acc.w * inv));
+  if (lane == 0) lse_last[pair] = l > 0.f ? m + logf(l) : kNegInf;
+}
+
+// Backward with dO non-zero on the last query only: dv_j = p_j dO, dk_j = R^T(dS_j scale q_t),
+// dq_t = R^T(scale sum_j dS_j k_j), every other dq row 0; rows j >= L get dk = dv = 0.
+template <int D>
+__global__ __launch_bounds__(256) void attn_bwd_lastq_kernel(AttnArgs a, const float* __restrict__ o_last,
+                                                             long long ldol, const float* __restrict__ lse_last,
+                                                             const float* __restrict__ do_last, long long lddol) {
+  constexpr int C = D / 4, RPP = 64 / C;
+  const int lane = threadIdx.x & 63, c = lane % C, r = lane / C;
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pair >= a.B * a.H) return;
+  const int b = pair / a.H, hh = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int Sk = key_len(a, b), t = Sk > 0 ? Sk - 1 : 0;
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 qs = z4, g = z4;
+  float Dd = 0.f, lse = 0.f;
+  if (Sk > 0) {
+    const float4 q = ld4(a.q + (tok0 + t) * a.ldq + hh * D + 4 * c);
+    qs = make_float4(q.x * a.scale, q.y * a.scale, q.z * a.scale, q.w * a.scale);
+    g = ld4(do_last + (long long)b * lddol + hh * D + 4 * c);
+    Dd = row_sum<C>(dot4(g, ld4(o_last + (long long)b * ldol + hh * D + 4 * c)));
+    lse = lse_last[pair];
+  }
+  float4 dq = z4;
+  for (int j0 = 0; j0 < a.S; j0 += RPP) {
+    const int j = j0 + r;
+    const bool in = j < a.S, ok = j < Sk;
+    const int jj = ok ? j : 0;
+    const float4 k = ld4(a.k + (tok0 + jj) * a.ldk + hh * D + 4 * c);
+    const float4 v = ld4(a.v + (tok0 + jj) * a.ldv + hh * D + 4 * c);
+    const float s = row_sum<C>(dot4(qs, k));
+    const float p = ok ? expf(s - lse) : 0.f;
+    const float dp = row_sum<C>(dot4(g, v));
+    const float dS = p * (dp - Dd);
+    dq = make_float4(dq.x + dS * k.x, dq.y + dS * k.y, dq.z + dS * k.z, dq.w + dS * k.w);
+    if (in) {
+      const long long row = tok0 + j;
+      st4(a.dv_out + row * a.lddv + hh * D + 4 * c, make_float4(p * g.x, p * g.y, p * g.z, p * g.w));
+      st4(a.dk_out + row * a.lddk + hh * D + 4 * c,
+          rope_t4(make_float4(dS * qs.x, dS * qs.y, dS * qs.z, dS * qs.w), 4 * c, j, a));
+      if (j != t || Sk == 0) st4(a.dq + row * a.lddq + hh * D + 4 * c, z4);
+    }
+  }
+  dq = make_float4(col_sum<C>(dq.x) * a.scale, col_sum<C>(dq.y) * a.scale, col_sum<C>(dq.z) * a.scale,
+                   col_sum<C>(dq.w) * a.scale);
+  if (r == 0 && Sk > 0) st4(a.dq + (tok0 + t) * a.lddq + hh * D + 4 * c, rope_t4(dq, 4 * c, t, a));
+}
+
+int attn_lastq_supported(const AttnDesc& d) {
+  auto al = [](const void* p, long long ld) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && ld % 4 == 0; };
+  return (d.dk == d.dv && (d.dk == 32 || d.dk == 64) && al(d.q, d.ldq) && al(d.k, d.ldk) && al(d.v, d.ldv))
+             ? 1
+             : 0;
+}
+
+int attn_fwd_lastq_launch(const AttnDesc& d, float* o_last, long long ldol, float* lse_last, hipStream_t s) {
+  AttnArgs a = make_args(d, d.dk, d.dv);
+  if ((long long)a.B * a.H == 0) return TALOS_OK;
+  dim3 grid(ceil_div((size_t)a.B * a.H, 4));
+  // q row, k and v over the sample's keys read; o row and lse written
+  const double rows = (double)a.B * a.H;
+  ProfScope ps(s, d.dk == 32 ? "attn_fwd_lastq_kernel<32>" : "attn_fwd_lastq_kernel<64>",
+               rows * a.S * 4.0 * d.dk, 4.0 * rows * ((2.0 * a.S + 2.0) * d.dk + 1.0));
+  if (d.dk == 32)
+    hipLaunchKernelGGL(attn_fwd_lastq_kernel<32>, grid, dim3(256), 0, s, a, o_last, ldol, lse_last);
+  else
+    hipLaunchKernelGGL(attn_fwd_lastq_kernel<64>, grid, dim3(256), 0, s, a, o_last, ldol, lse_last);
+  return launch_status("attn_fwd_lastq_kernel");
+}
+
+int attn_bwd_lastq_launch(const AttnDesc& d, const float* o_last, long long ldol, const float* lse_last,
+                          const float* do_last, long long lddol, hipStream_t s) {
+  AttnArgs a = make_args(d, d.dk, d.dv);
+  if ((long long)a.B * a.H * a.S == 0) return TALOS_OK;
+  dim3 grid(ceil_div((size_t)a.B * a.H, 4));
+  // k, v read and dq, dk, dv written over every row; q, o, dO of the last row read
+  const double rows = (double)a.B * a.H;
+  ProfScope ps(s, d.dk == 32 ? "attn_bwd_lastq_kernel<32>" : "attn_bwd_lastq_kernel<64>",
+               rows * a.S * 10.0 * d.dk, 4.0 * rows * ((5.0 * a.S + 3.0) * d.dk + 1.0));
+  if (d.dk == 32)
+    hipLaunchKernelGGL(attn_bwd_lastq_kernel<32>, grid, dim3(256), 0, s, a, o_last, ldol, lse_last, do_last, lddol);
+  else
+    hipLaunchKernelGGL(attn_bwd_lastq_kernel<64>, grid, dim3(256), 0, s, a, o_last, ldol, lse_last, do_last, lddol);
+  return launch_status("attn_bwd_lastq_kernel");
+}
+
 static int check_attn(const char* fn, int batch, int seq, int heads, int qk_dim, int v_dim, int causal, int ld_q,
                       int ld_k, int ld_v, int ld_o) {
   TALOS_REQUIRE(batch >= 0 && seq >= 0 && heads >= 0 && qk_dim > 0 && v_dim > 0, TALOS_ERR_SHAPE,

@@ -39,6 +39,16 @@ struct AttnDesc {
 };
 
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s);
+
+// Attention of the last query row of each batch entry only (row lens[b] - 1, or seq - 1), over all
+// of that entry's keys: o_last / do_last are [batch, heads * dv] with row strides ldol / lddol,
+// lse_last is [batch * heads]. The backward takes dO on that row only and writes every row of
+// dq (zero except the last), dk and dv. Head dims 32 or 64 with dk == dv and 16-byte aligned
+// q / k / v rows (attn_lastq_supported).
+int attn_lastq_supported(const AttnDesc& d);
+int attn_fwd_lastq_launch(const AttnDesc& d, float* o_last, long long ldol, float* lse_last, hipStream_t s);
+int attn_bwd_lastq_launch(const AttnDesc& d, const float* o_last, long long ldol, const float* lse_last,
+                          const float* do_last, long long lddol, hipStream_t s);
 size_t attn_bwd_workspace_bytes(const AttnDesc& d);
 int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s);
 

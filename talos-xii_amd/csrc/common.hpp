@@ -124,4 +124,12 @@ __device__ __forceinline__ float gelu_d(float x) {
 
 inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
+// The last token of sample b of a [batch, S] token grid: row lens[b] - 1 with lens clamped to
+// [1, S], or S - 1 without lens (last_token, src/transformer.rs:92-109).
+__device__ __forceinline__ int last_row(const int32_t* lens, int b, int S) {
+  if (lens == nullptr) return S - 1;
+  const int L = lens[b];
+  return (L < 1 ? 1 : (L > S ? S : L)) - 1;
+}
+
 }  // namespace talos

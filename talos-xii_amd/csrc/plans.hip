@@ -57,7 +57,7 @@ struct talos_plan_s {
   // the last layer's MLP half on the last-token rows only: its inputs gathered from x and o,
   // its activations and the backward scratch, [batch, d] / [batch, F]
   struct LastRows {
-    float *x, *o, *h2, *xn2, *rstd2, *u, *a, *g_u, *g_xn, *g_h2, *g_o;
+    float *x, *o, *lse, *h2, *xn2, *rstd2, *u, *a, *g_u, *g_xn, *g_h2, *g_o;
   } lr{};
   const int32_t* lens = nullptr;  // per-sample lengths of the PPO call in progress (nullptr: all seq)
   int num_cu = 256;
@@ -291,10 +291,38 @@ static int mm(talos_plan_s* p, hipStream_t s, int tA, int tB, int M, int N, int 
   return gemm_launch(g, s);
 }
 
-// Attention half of a block's forward: xn1 = rmsnorm(x), qkv = xn1.Wqkv (RoPE in the epilogue),
-// o = attention(q, k, v) with lse saved. L.x must be set.
-static int block_attn_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
-                              talos_plan_s::Layer& L, hipStream_t s) {
+// The block's attention over its qkv buffer (q, k, v column blocks of one [tokens, 3d] buffer).
+static AttnDesc block_attn_desc(talos_plan_s* p, const talos_block_cfg& c, talos_plan_s::Layer& L) {
+  const int d = c.d_model;
+  AttnDesc a;
+  a.batch = c.batch;
+  a.seq = c.seq;
+  a.heads = c.n_heads;
+  a.dk = a.dv = c.head_dim;
+  a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+  a.causal = c.causal;
+  a.q = L.qkv;
+  a.k = L.qkv + d;
+  a.v = L.qkv + 2 * d;
+  a.ldq = a.ldk = a.ldv = 3 * d;
+  a.o = L.o;
+  a.ldo = d;
+  a.lse = L.lse;
+  a.dq = p->g_qkv;
+  a.dk_out = p->g_qkv + d;
+  a.dv_out = p->g_qkv + 2 * d;
+  a.lddq = a.lddk = a.lddv = 3 * d;
+  a.rope_cos = p->rcos;
+  a.rope_sin = p->rsin;
+  a.rope_off = 0;
+  a.rope_dim = c.head_dim;
+  a.lens = p->lens;
+  return a;
+}
+
+// xn1 = rmsnorm(x), qkv = xn1.Wqkv (RoPE in the epilogue). L.x must be set.
+static int block_qkv_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
+                             talos_plan_s::Layer& L, hipStream_t s) {
   const int M = c.batch * c.seq, d = c.d_model;
   int rc = rmsnorm_fwd_launch(M, d, c.eps, L.x, P + o.g1, L.xn1, L.rstd1, s);
   if (rc) return rc;
@@ -315,25 +343,16 @@ static int block_attn_forward(talos_plan_s* p, const talos_block_cfg& c, const f
     g.rope_dim = c.head_dim;
     g.rope_seq = c.seq;
     g.ksplit = 1;
-    rc = gemm_launch(g, s);
-    if (rc) return rc;
+    return gemm_launch(g, s);
   }
-  AttnDesc a;
-  a.batch = c.batch;
-  a.seq = c.seq;
-  a.heads = c.n_heads;
-  a.dk = a.dv = c.head_dim;
-  a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
-  a.causal = c.causal;
-  a.q = L.qkv;
-  a.k = L.qkv + d;
-  a.v = L.qkv + 2 * d;
-  a.ldq = a.ldk = a.ldv = 3 * d;
-  a.o = L.o;
-  a.ldo = d;
-  a.lse = L.lse;
-  a.lens = p->lens;
-  return attn_fwd_launch(a, s);
+}
+
+// Attention half of a block's forward: qkv, then o = attention(q, k, v) with lse saved.
+static int block_attn_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
+                              talos_plan_s::Layer& L, hipStream_t s) {
+  int rc = block_qkv_forward(p, c, P, o, L, s);
+  if (rc) return rc;
+  return attn_fwd_launch(block_attn_desc(p, c, L), s);
 }
 
 // Second half over R rows (all tokens, or only the last token of each sample): h2 = x + o.Wo,
@@ -419,48 +438,34 @@ static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const f
   return mm(p, s, 0, 1, R, d, d, g_h2, d, P + o.wo, d, g_o, d);
 }
 
+// From the qkv gradient (p->g_qkv) back to x: the Wqkv / gain1 gradients and dx = rmsnorm1's
+// backward + the residual gradient reaching x through h2, given on every row (g_h2) or on the
+// last token of each sample only (g_h2_last, [batch, d]).
+static int block_qkv_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
+                              talos_plan_s::Layer& L, const float* g_h2, const float* g_h2_last, float* dx,
+                              hipStream_t s) {
+  const int M = c.batch * c.seq, d = c.d_model;
+  // qkv = xn1.Wqkv
+  int rc = mm(p, s, 1, 0, d, 3 * d, M, L.xn1, d, p->g_qkv, 3 * d, G + o.wqkv, 3 * d);
+  if (rc) return rc;
+  rc = mm(p, s, 0, 1, M, d, 3 * d, p->g_qkv, 3 * d, P + o.wqkv, 3 * d, p->g_xn, d);
+  if (rc) return rc;
+  // dx is overwritten: the residual arrives through g_h2 or g_h2_last, never through dx's old contents
+  return rmsnorm_bwd_launch(M, d, L.x, P + o.g1, L.rstd1, p->g_xn, 0.f, dx, 0.f, G + o.g1, p->red_ws, s, g_h2,
+                            g_h2_last, c.seq, p->lens);
+}
+
 // Attention half backward over all rows: g_o = dL/do, g_h2 = the residual gradient reaching x
 // through h2; writes the Wqkv / gain1 gradients and dx.
 static int block_attn_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
                                talos_plan_s::Layer& L, const float* g_o, const float* g_h2, float* dx,
                                hipStream_t s) {
-  const int M = c.batch * c.seq, d = c.d_model;
-  int rc;
-  {
-    AttnDesc a;
-    a.batch = c.batch;
-    a.seq = c.seq;
-    a.heads = c.n_heads;
-    a.dk = a.dv = c.head_dim;
-    a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
-    a.causal = c.causal;
-    a.q = L.qkv;
-    a.k = L.qkv + d;
-    a.v = L.qkv + 2 * d;
-    a.ldq = a.ldk = a.ldv = 3 * d;
-    a.o = L.o;
-    a.ldo = d;
-    a.lse = L.lse;
-    a.dout = g_o;
-    a.lddo = d;
-    a.dq = p->g_qkv;
-    a.dk_out = p->g_qkv + d;
-    a.dv_out = p->g_qkv + 2 * d;
-    a.lddq = a.lddk = a.lddv = 3 * d;
-    a.rope_cos = p->rcos;
-    a.rope_sin = p->rsin;
-    a.rope_off = 0;
-    a.rope_dim = c.head_dim;
-    a.lens = p->lens;
-    rc = attn_bwd_launch(a, p->attn_ws, s);
-    if (rc) return rc;
-  }
-  // qkv = xn1.Wqkv
-  rc = mm(p, s, 1, 0, d, 3 * d, M, L.xn1, d, p->g_qkv, 3 * d, G + o.wqkv, 3 * d);
+  AttnDesc a = block_attn_desc(p, c, L);
+  a.dout = g_o;
+  a.lddo = c.d_model;
+  int rc = attn_bwd_launch(a, p->attn_ws, s);
   if (rc) return rc;
-  rc = mm(p, s, 0, 1, M, d, 3 * d, p->g_qkv, 3 * d, P + o.wqkv, 3 * d, p->g_xn, d);
-  if (rc) return rc;
-  return rmsnorm_bwd_launch(M, d, L.x, P + o.g1, L.rstd1, p->g_xn, 1.f, dx, 0.f, G + o.g1, p->red_ws, s, g_h2);
+  return block_qkv_backward(p, c, P, G, o, L, g_h2, nullptr, dx, s);
 }
 
 // Backward of one block: gout = dL/dout (read), writes dparams slots and dx.
@@ -473,14 +478,7 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
   return block_attn_backward(p, c, P, G, o, L, p->g_o, p->g_h2, dx, s);
 }
 
-// Last-token gather / scatter -----------------------------------------------
-// The last token of sample b is row lens[b] - 1 (lens clamped to [1, S]; no lens: row S - 1), as
-// last_token reads row seq_len - 1 of each sample (src/transformer.rs:92-109).
-__device__ __forceinline__ int last_row(const int32_t* lens, int b, int S) {
-  if (lens == nullptr) return S - 1;
-  const int L = lens[b];
-  return (L < 1 ? 1 : (L > S ? S : L)) - 1;
-}
+// Last-token gather / scatter (last_row: common.hpp) -------------------------
 __global__ void gather_last_kernel(int B, int S, int d, const int32_t* __restrict__ lens,
                                    const float* __restrict__ h, float* __restrict__ out) {
   const long long n = (long long)B * d;
@@ -633,9 +631,16 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
     } else {
       // Only the last token of each sample reaches the heads, and everything after attention is
       // per row: the last layer runs its MLP half on those B rows and writes p->last directly.
-      rc = block_attn_forward(p, bc, P, bo, L, s);
+      rc = block_qkv_forward(p, bc, P, bo, L, s);
       if (rc) return rc;
-      if ((rc = gather(L.x, p->lr.x)) || (rc = gather(L.o, p->lr.o))) return rc;
+      const AttnDesc ad = block_attn_desc(p, bc, L);
+      if (attn_lastq_supported(ad)) {  // attention of the last query only
+        rc = attn_fwd_lastq_launch(ad, p->lr.o, d, p->lr.lse, s);
+      } else {
+        rc = attn_fwd_launch(ad, s);
+        if (rc == TALOS_OK) rc = gather(L.o, p->lr.o);
+      }
+      if (rc || (rc = gather(L.x, p->lr.x))) return rc;
       rc = block_mlp_forward(p, bc, P, bo, c.batch, p->lr.x, p->lr.o, p->lr.h2, p->lr.xn2, p->lr.rstd2, p->lr.u,
                              p->lr.a, p->last, s);
       if (rc) return rc;
@@ -890,6 +895,7 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
     for (float** b : {&R.x, &R.o, &R.h2, &R.xn2, &R.g_xn, &R.g_h2, &R.g_o}) rc |= plan_alloc(p, b, B * d);
     for (float** b : {&R.u, &R.a, &R.g_u}) rc |= plan_alloc(p, b, B * F);
     rc |= plan_alloc(p, &R.rstd2, B);
+    rc |= plan_alloc(p, &R.lse, B * cfg->n_heads);
   }
   {  // per-workgroup loss partials (doubles)
     float* lw = nullptr;
@@ -1023,8 +1029,17 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
     rc = block_mlp_backward(p, bc, params, G, offs[l], B, R.o, R.h2, R.xn2, R.rstd2, R.u, R.a, p->g_last, R.g_u,
                             R.g_xn, R.g_h2, R.g_o, s);
     if (rc) return rc;
-    if ((rc = scatter(R.g_o, p->g_o)) || (rc = scatter(R.g_h2, p->g_h2))) return rc;
-    rc = block_attn_backward(p, bc, params, G, offs[l], p->layers[l], p->g_o, p->g_h2, p->g_out, s);
+    AttnDesc ad = block_attn_desc(p, bc, p->layers[l]);
+    if (attn_lastq_supported(ad)) {
+      rc = attn_bwd_lastq_launch(ad, R.o, d, R.lse, R.g_o, d, s);
+    } else {
+      ad.dout = p->g_o;
+      ad.lddo = d;
+      rc = scatter(R.g_o, p->g_o);
+      if (rc == TALOS_OK) rc = attn_bwd_launch(ad, p->attn_ws, s);
+    }
+    if (rc) return rc;
+    rc = block_qkv_backward(p, bc, params, G, offs[l], p->layers[l], nullptr, R.g_h2, p->g_out, s);
     if (rc) return rc;
   }
   for (int l = c.n_layers - 2; l >= 0; --l) {

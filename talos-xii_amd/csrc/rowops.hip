@@ -228,7 +228,9 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(int rows, int dim, con
                                                           const float* __restrict__ w,
                                                           const float* __restrict__ rstd,
                                                           const float* __restrict__ dy, const float* add,
-                                                          float* dx, double* __restrict__ dw_part) {
+                                                          float* dx, double* __restrict__ dw_part,
+                                                          const float* __restrict__ add_last, int seq,
+                                                          const int32_t* __restrict__ lens) {
   __shared__ float red[4][V * 256];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   float4 gw[V], dwacc[V];
@@ -277,6 +279,13 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(int rows, int dim, con
           o.z += old.z;
           o.w += old.w;
         }
+        if (add_last && row % seq == last_row(lens, row / seq, seq)) {
+          const float4 ex = *reinterpret_cast<const float4*>(add_last + (long long)(row / seq) * dim + c);
+          o.x += ex.x;
+          o.y += ex.y;
+          o.z += ex.z;
+          o.w += ex.w;
+        }
         *reinterpret_cast<float4*>(dxr + c) = o;
       }
     }
@@ -295,7 +304,9 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_generic(int rows, int dim, co
                                                            const float* __restrict__ w,
                                                            const float* __restrict__ rstd,
                                                            const float* __restrict__ dy, const float* add,
-                                                           float* dx, double* __restrict__ dw_part) {
+                                                           float* dx, double* __restrict__ dw_part,
+                                                           const float* __restrict__ add_last, int seq,
+                                                           const int32_t* __restrict__ lens) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   for (int row = blockIdx.x * 4 + wv; row < rows; row += gridDim.x * 4) {
     const float r = rstd[row];
@@ -307,6 +318,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_generic(int rows, int dim, co
     for (int c = lane; c < dim; c += 64) {
       float o = r * (gr[c] * w[c] - xr[c] * r * md);
       if (add) o += add[(long long)row * dim + c];
+      if (add_last && row % seq == last_row(lens, row / seq, seq)) o += add_last[(long long)(row / seq) * dim + c];
       dx[(long long)row * dim + c] = o;
     }
   }
@@ -345,7 +357,7 @@ int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float
 
 int rmsnorm_bwd_launch(int rows, int dim, const float* x, const float* w, const float* rstd, const float* dy,
                        float beta_dx, float* dx, float beta_dw, float* dw, double* ws, hipStream_t s,
-                       const float* dres) {
+                       const float* dres, const float* dres_last, int seq, const int32_t* lens) {
   const int nblk = rows > 0 ? rms_bwd_blocks(rows) : 0;
   if (nblk > 0) {
     dim3 g(nblk), b(256);
@@ -354,18 +366,22 @@ int rmsnorm_bwd_launch(int rows, int dim, const float* x, const float* w, const 
     const float* add = dres ? dres : (beta_dx != 0.f ? dx : nullptr);
     const bool vec = dim % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy) |
                                        reinterpret_cast<uintptr_t>(dx) | reinterpret_cast<uintptr_t>(w) |
-                                       reinterpret_cast<uintptr_t>(add)) & 15) == 0;
+                                       reinterpret_cast<uintptr_t>(add) | reinterpret_cast<uintptr_t>(dres_last)) & 15) == 0;
     // x, dy read, dx written (the addend read too), gain + rstd read, dgain partials written
     ProfScope ps(s, vec && dim <= 256 ? "rmsnorm_bwd_kernel<1>" : vec && dim <= 512 ? "rmsnorm_bwd_kernel<2>"
                     : "rmsnorm_bwd_generic",
                  8.0 * rows * dim, 4.0 * ((3.0 + (add != nullptr)) * rows * dim + dim + rows) +
                                        (part ? 8.0 * nblk * dim : 0.0));
+    const int sq = seq > 0 ? seq : 1;
     if (vec && dim <= 256)
-      hipLaunchKernelGGL(rmsnorm_bwd_kernel<1>, g, b, 0, s, rows, dim, x, w, rstd, dy, add, dx, part);
+      hipLaunchKernelGGL(rmsnorm_bwd_kernel<1>, g, b, 0, s, rows, dim, x, w, rstd, dy, add, dx, part, dres_last, sq,
+                         lens);
     else if (vec && dim <= 512)
-      hipLaunchKernelGGL(rmsnorm_bwd_kernel<2>, g, b, 0, s, rows, dim, x, w, rstd, dy, add, dx, part);
+      hipLaunchKernelGGL(rmsnorm_bwd_kernel<2>, g, b, 0, s, rows, dim, x, w, rstd, dy, add, dx, part, dres_last, sq,
+                         lens);
     else
-      hipLaunchKernelGGL(rmsnorm_bwd_generic, g, b, 0, s, rows, dim, x, w, rstd, dy, add, dx, part);
+      hipLaunchKernelGGL(rmsnorm_bwd_generic, g, b, 0, s, rows, dim, x, w, rstd, dy, add, dx, part, dres_last, sq,
+                         lens);
     TALOS_LAUNCHED("rmsnorm_bwd");
   }
   if (dw) return reduce_parts_launch(dim, nblk, ws, beta_dw, dw, s);

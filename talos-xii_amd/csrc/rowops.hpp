@@ -18,10 +18,12 @@ size_t rmsnorm_bwd_workspace_bytes(int rows, int dim);
 int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
                        hipStream_t s);
 // dx = (dres ? dres : beta_dx * dx) + d rmsnorm / dx . dy; dres (the residual branch's gradient)
-// may equal dx.
+// may equal dx. dres_last ([rows / seq, dim]) adds a gradient that is non-zero on the last token
+// of each sample only: row b * seq + last_row(lens, b, seq) receives dres_last[b].
 int rmsnorm_bwd_launch(int rows, int dim, const float* x, const float* w, const float* rstd, const float* dy,
                        float beta_dx, float* dx, float beta_dw, float* dw, double* ws, hipStream_t s,
-                       const float* dres = nullptr);
+                       const float* dres = nullptr, const float* dres_last = nullptr, int seq = 1,
+                       const int32_t* lens = nullptr);
 
 // out[r] = [a[r] | b[r]]; split: da[r] (+)= g[r][:ca], db[r] (+)= g[r][ca:]
 int concat_launch(size_t rows, int ca, int cb, const float* a, const float* b, float* out, hipStream_t s);

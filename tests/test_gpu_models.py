@@ -76,6 +76,10 @@ def run_ppo(cfg, p, states, actions, adv, ret, old):
     Ad, Re, Ol = DA.from_numpy(adv), DA.from_numpy(ret), DA.from_numpy(old)
     loss, dp = DA.zeros(1), DA.zeros(p.size)
     th.call("talos_ppo_fwd_bwd_f32", plan.h, P.ptr, St.ptr, Ac.ptr, Ad.ptr, Re.ptr, Ol.ptr, loss.ptr, dp.ptr, None)
+    first = dp.numpy()
+    # a second call on the same plan must give the same result: no state leaks between calls
+    th.call("talos_ppo_fwd_bwd_f32", plan.h, P.ptr, St.ptr, Ac.ptr, Ad.ptr, Re.ptr, Ol.ptr, loss.ptr, dp.ptr, None)
+    assert np.array_equal(first, dp.numpy()), "a repeated call on the same plan changed the gradients"
     lg, vl = DA.zeros((cfg.batch, cfg.n_actions)), DA.zeros(cfg.batch)
     th.call("talos_ppo_forward_f32", plan.h, P.ptr, St.ptr, lg.ptr, vl.ptr, None)
     res = float(loss.numpy()[0]), dp.numpy(), lg.numpy(), vl.numpy()

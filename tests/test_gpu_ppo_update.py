@@ -76,10 +76,11 @@ def _oracle_varlen(oracle, args, p, states, lens, actions, adv, ret, old):
     return loss, dp, np.array(logits)
 
 
-@pytest.mark.parametrize("causal", [1, 0])
-def test_minibatch_varlen_vs_oracle(oracle, causal):
-    rng = np.random.default_rng(11 + causal)
-    args = cfg_args(8, 12, causal)
+@pytest.mark.parametrize("causal,H", [(1, 2), (0, 2), (1, 1)])
+def test_minibatch_varlen_vs_oracle(oracle, causal, H):
+    # head dim 32 (H = 2) and 64 (H = 1): both last-query attention kernels of the last layer
+    rng = np.random.default_rng(11 + causal + H)
+    args = cfg_args(8, 12, causal, H=H)
     cfg, ocfg = th.PpoCfg(*args), oracle.PpoCfg(*args)
     p = f32(ppo_params(rng, ocfg))
     lens = [12, 1, 7, 12, 3]
