@@ -222,3 +222,27 @@ def test_update_kl_early_stop(oracle):
     th.call("talos_ppo_update_f32", plan.h, ctypes.byref(empty), ctypes.byref(out), None)
     assert out.epochs_run == 0
     plan.destroy()
+
+
+def test_update_one_step_vs_oracle(oracle):
+    """One epoch over one minibatch: GAE, the minibatch gradient and the first Adam step, against
+    the oracle's GAE, per-sample graphs and f64 Adam. At t = 1 Adam moves each parameter by
+    lr * g / (|g| + eps), i.e. by about lr * sign(g), so the comparison keeps the parameters whose
+    oracle gradient is not tiny (|g| > 1e-3 max|g|): for the others fp32 rounding may flip the
+    sign."""
+    ro = _Rollout(oracle, 23, n=8)  # n = the plan's batch: a single minibatch
+    plan = th.Plan("ppo", ro.cfg)
+    d = ro.device()
+    a, res = _run_harness(plan, ro, d, 1, target_kl=1e9)
+    assert res.epochs_run == 1 and a.adam_t == 1
+    _, _, adv_n = oracle.ppo_gae(ro.rew, ro.val, ro.done, RM, RV, CLIP, GAMMA, LAM)
+    _, ret_r, _ = oracle.ppo_gae(ro.rew, ro.val, ro.done, RM, RV, CLIP, GAMMA, LAM)
+    _, g_r, _ = _oracle_varlen(oracle, ro.args, ro.p0, ro.states, list(ro.lens), ro.actions, f32(adv_n), f32(ret_r),
+                               ro.old)
+    p_r, m_r, v_r = ro.p0.astype(np.float64), np.zeros(ro.p0.size), np.zeros(ro.p0.size)
+    oracle.adam_step(p_r, g_r, m_r, v_r, 1, LR)
+    keep = np.abs(g_r) > 1e-3 * np.abs(g_r).max()
+    assert keep.sum() > 0.5 * keep.size
+    got = d["P"].numpy().astype(np.float64) - ro.p0
+    check_close(got[keep], (p_r - ro.p0)[keep], rtol=1e-3, atol=1e-7, name="first Adam step")
+    plan.destroy()
