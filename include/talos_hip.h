@@ -220,26 +220,41 @@ int talos_adam_step_f32(size_t n, float* params, const float* grads, float* m, f
 
 enum talos_activation { TALOS_ACT_GELU = 0, TALOS_ACT_RELU = 1 };
 
-/* Pre-norm transformer block with standard multi-head attention and RoPE:
- *   h2  = x + Wo . attn(rope(q), rope(k), v),  [q|k|v] = rmsnorm(x; g1) . Wqkv
+/* Attention of a block: standard multi-head attention with RoPE on all of q and k, or the
+ * reference's multi-head latent attention (MultiHeadLatentAttention, transformer.rs:428-560). */
+enum talos_attention { TALOS_ATTN_MHA = 0, TALOS_ATTN_MLA = 1 };
+
+/* Pre-norm transformer block (the wiring of LuckTransformer::forward, transformer.rs:71-90):
+ *   h2  = x + Wo . attn(rmsnorm(x; g1))
  *   out = h2 + W2 . act(rmsnorm(h2; g2) . W1 + b1) + b2
- * The reference block (transformer.rs:71-90) is the same pre-norm residual layout with MLA
- * attention and a 2x ReLU MLP; this is its standard-MHA / 4x GELU restatement.
- * Parameter layout (fp32, contiguous, in this order), d = d_model, F = ffn_dim:
- *   g1[d] | Wqkv[d,3d] (columns q | k | v, heads contiguous) | Wo[d,d] | g2[d] |
- *   W1[d,F] | b1[F] | W2[F,d] | b2[d]
- * Linear weights are stored [in, out] as in the reference (nn.rs:22). */
+ * attention = TALOS_ATTN_MHA: [q|k|v] = rmsnorm(x; g1) . Wqkv, RoPE on q and k, head_dim per
+ *   head, n_heads * head_dim == d_model. Parameter layout (fp32, contiguous, in this order),
+ *   d = d_model, F = ffn_dim:
+ *     g1[d] | Wqkv[d,3d] (columns q | k | v, heads contiguous) | Wo[d,d] | g2[d] |
+ *     W1[d,F] | b1[F] | W2[F,d] | b2[d]
+ * attention = TALOS_ATTN_MLA: the attention of talos_mla_cfg below (latent kv_latent, decoupled
+ *   RoPE of rope_dim per head, content head_dim, value v_dim); with ReLU and F = 2d this is the
+ *   reference block exactly. Parameter layout (the order of LuckTransformer::parameters,
+ *   transformer.rs:205-215), H = n_heads, L = kv_latent, r = rope_dim, hd = head_dim, vd = v_dim:
+ *     g1[d] | W_dkv[d,L] | W_uk[L,H*hd] | W_uv[L,H*vd] | W_q[d,H*hd] | W_kr[d,H*r] |
+ *     W_qr[d,H*r] | W_o[H*vd,d] | g2[d] | W1[d,F] | b1[F] | W2[F,d] | b2[d]
+ * Linear weights are stored [in, out] as in the reference (nn.rs:22). The MLA fields are ignored
+ * (and may be left zero) for TALOS_ATTN_MHA. */
 typedef struct talos_block_cfg {
   int batch;
   int seq;
   int d_model;
   int n_heads;
-  int head_dim;   /* n_heads * head_dim == d_model */
+  int head_dim;   /* MHA: n_heads * head_dim == d_model; MLA: content q/k dims per head */
   int ffn_dim;
   int causal;     /* 1: causal attention mask */
   int activation; /* talos_activation */
   float eps;      /* RMSNorm eps */
   float rope_base;
+  int attention;  /* talos_attention */
+  int kv_latent;  /* MLA only */
+  int rope_dim;   /* MLA only */
+  int v_dim;      /* MLA only */
 } talos_block_cfg;
 
 size_t talos_block_param_count(const talos_block_cfg* cfg);
@@ -248,7 +263,11 @@ size_t talos_block_param_count(const talos_block_cfg* cfg);
  * n_layers blocks -> RMSNorm -> out_proj Linear(d,d)+b -> last token -> actor Linear(d,A)+b
  * and critic Linear(d,1)+b. Parameter layout:
  *   We[in,d] | be[d] | block_0 ... block_{L-1} (talos_block_cfg layout) | gf[d] |
- *   Wout[d,d] | bout[d] | Wa[d,A] | ba[A] | Wc[d,1] | bc[1] */
+ *   Wout[d,d] | bout[d] | Wa[d,A] | ba[A] | Wc[d,1] | bc[1]
+ * The reference's ActorCritic (ActorCritic::new, ppo.rs:254-258 with LuckTransformer::new,
+ * transformer.rs:48-69) is in_dim 8, d 64, one TALOS_ATTN_MLA layer (4 heads, latent 32, rope 16,
+ * head_dim = v_dim = 16), ffn 128 ReLU, eps 1e-5, no causal mask, 5 actions; its parameter order
+ * (ActorCritic::parameters, ppo.rs:302-307) is this layout. */
 typedef struct talos_ppo_cfg {
   int batch;      /* samples per minibatch */
   int seq;        /* tokens per sample (all samples padded to seq) */
@@ -266,6 +285,10 @@ typedef struct talos_ppo_cfg {
   float clip_eps;     /* 0.2, ppo.rs:17 */
   float value_coef;   /* 0.5, ppo.rs:20 */
   float entropy_coef; /* 0.01, ppo.rs:21 */
+  int attention;      /* talos_attention of every block, with the MLA widths below */
+  int kv_latent;
+  int rope_dim;
+  int v_dim;
 } talos_ppo_cfg;
 
 size_t talos_ppo_param_count(const talos_ppo_cfg* cfg);

@@ -34,7 +34,8 @@ class BlockCfg(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int), ("seq", ctypes.c_int), ("d_model", ctypes.c_int),
                 ("n_heads", ctypes.c_int), ("head_dim", ctypes.c_int), ("ffn_dim", ctypes.c_int),
                 ("causal", ctypes.c_int), ("activation", ctypes.c_int), ("eps", ctypes.c_float),
-                ("rope_base", ctypes.c_float)]
+                ("rope_base", ctypes.c_float), ("attention", ctypes.c_int), ("kv_latent", ctypes.c_int),
+                ("rope_dim", ctypes.c_int), ("v_dim", ctypes.c_int)]
 
 
 class PpoCfg(ctypes.Structure):
@@ -43,7 +44,8 @@ class PpoCfg(ctypes.Structure):
                 ("head_dim", ctypes.c_int), ("ffn_dim", ctypes.c_int), ("n_actions", ctypes.c_int),
                 ("causal", ctypes.c_int), ("activation", ctypes.c_int), ("eps", ctypes.c_float),
                 ("rope_base", ctypes.c_float), ("clip_eps", ctypes.c_float), ("value_coef", ctypes.c_float),
-                ("entropy_coef", ctypes.c_float)]
+                ("entropy_coef", ctypes.c_float), ("attention", ctypes.c_int), ("kv_latent", ctypes.c_int),
+                ("rope_dim", ctypes.c_int), ("v_dim", ctypes.c_int)]
 
 
 _lib = None
@@ -90,6 +92,8 @@ def lib():
         L.orc_lcg_rand.argtypes = [ctypes.c_int64, ctypes.c_double, ctypes.c_double, ctypes.c_uint64, _f64p]
         L.orc_ppo_param_count.restype = ctypes.c_size_t
         L.orc_ppo_param_count.argtypes = [ctypes.POINTER(PpoCfg)]
+        L.orc_block_param_count.restype = ctypes.c_size_t
+        L.orc_block_param_count.argtypes = [ctypes.POINTER(BlockCfg)]
         L.orc_mla_param_count.restype = ctypes.c_size_t
         L.orc_mla_param_count.argtypes = [_i32p]
         L.orc_adam_step.restype = None
@@ -351,8 +355,7 @@ def attention_fwd_bwd(q, k, v, dout, scale, causal):
 
 
 def block_param_count(cfg):
-    d, F = cfg.d_model, cfg.ffn_dim
-    return d + 3 * d * d + d * d + d + d * F + F + F * d + d
+    return int(lib().orc_block_param_count(ctypes.byref(cfg)))
 
 
 def block_fwd_bwd(cfg, params, x, gout):

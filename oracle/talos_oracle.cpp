@@ -920,13 +920,94 @@ static Linear make_linear(Params& P, size_t in, size_t out, bool bias) {
   return L;
 }
 
-// Standard multi-head attention block (talos_block_cfg). The Wqkv[d,3d] parameter is split
-// into three Linear(d,d) (columns q|k|v) whose gradients are packed back afterwards.
+// ---------------------------------------------------------------------------
+// MLA block (src/transformer.rs:478-557) with a pre-norm residual around it.
+// ---------------------------------------------------------------------------
+struct MlaCfg {
+  int batch, seq, d_model, n_heads, kv_latent, rope_dim, head_dim, v_dim;
+  int causal;       // extension
+  int literal_rope; // 1: rotate q_r/k_r along shape[-2] of [B,S,H,R] (the head index) like the
+                    // reference's training path; 0: rotate by the sequence position
+  double eps, rope_base;
+};
+struct Mla {
+  Tensor g;
+  Linear w_dkv, w_uk, w_uv, w_q, w_kr, w_qr, w_o;
+};
+static Mla make_mla(Params& P, const MlaCfg& c) {
+  Mla m;
+  size_t d = c.d_model, H = c.n_heads;
+  m.g = P.take({d});
+  m.w_dkv = make_linear(P, d, c.kv_latent, false);
+  m.w_uk = make_linear(P, c.kv_latent, H * c.head_dim, false);
+  m.w_uv = make_linear(P, c.kv_latent, H * c.v_dim, false);
+  m.w_q = make_linear(P, d, H * c.head_dim, false);
+  m.w_kr = make_linear(P, d, H * c.rope_dim, false);
+  m.w_qr = make_linear(P, d, H * c.rope_dim, false);
+  m.w_o = make_linear(P, H * c.v_dim, d, false);
+  return m;
+}
+static Tensor mla_forward(const Mla& m, const MlaCfg& c, const Rope& R, const Tensor& xin) {
+  size_t B = c.batch, S = c.seq, H = c.n_heads, hd = c.head_dim, rd = c.rope_dim, vd = c.v_dim;
+  Tensor x = rmsnorm(xin, m.g, c.eps);
+  Tensor c_kv = linear_forward(m.w_dkv, x);
+  Tensor k_c = linear_forward(m.w_uk, c_kv);
+  Tensor v_c = linear_forward(m.w_uv, c_kv);
+  Tensor k_r_flat = linear_forward(m.w_kr, x);
+  Tensor q_c = linear_forward(m.w_q, x);
+  Tensor q_r_flat = linear_forward(m.w_qr, x);
+  Tensor k_r = reshape(k_r_flat, {B, S, H, rd});
+  Tensor q_r = reshape(q_r_flat, {B, S, H, rd});
+  Tensor k_rot, q_rot;
+  if (c.literal_rope) {
+    k_rot = rope_forward(R, k_r, 0);
+    q_rot = rope_forward(R, q_r, 0);
+  } else {
+    k_rot = transpose(rope_forward(R, transpose(k_r, 1, 2), 0), 1, 2);
+    q_rot = transpose(rope_forward(R, transpose(q_r, 1, 2), 0), 1, 2);
+  }
+  Tensor q = concat_last(reshape(q_c, {B, S, H, hd}), q_rot);
+  Tensor k = concat_last(reshape(k_c, {B, S, H, hd}), k_rot);
+  Tensor v = reshape(v_c, {B, S, H, vd});
+  size_t td = hd + rd;
+  Tensor qf = reshape(transpose(q, 1, 2), {B * H, S, td});
+  Tensor kf = reshape(transpose(k, 1, 2), {B * H, S, td});
+  Tensor vf = reshape(transpose(v, 1, 2), {B * H, S, vd});
+  Tensor sc = bmm_qt_k(qf, kf, B * H, S, td);
+  Tensor scs = scale_tensor(sc, 1.0 / std::sqrt((double)td));
+  Tensor pr = softmax(scs, S, c.causal != 0);
+  Tensor o = bmm_p_v(pr, vf, B * H, S, vd);
+  o = reshape(transpose(reshape(o, {B, H, S, vd}), 1, 2), {B, S, H * vd});
+  return add(xin, linear_forward(m.w_o, o));
+}
+
+// Pre-norm block (talos_block_cfg). Standard multi-head attention: the Wqkv[d,3d] parameter is
+// split into three Linear(d,d) (columns q|k|v) whose gradients are packed back afterwards. MLA
+// attention: the Mla module above (its gain g is the block's g1, its residual the block's first).
 struct Block {
+  bool mla_attn = false;
   Tensor g1, g2;
   Tensor wqkv;
   Linear wq, wk, wv, wo, w1, w2;
+  Mla mla;
 };
+static MlaCfg mla_cfg_of(const talos_block_cfg& c, size_t batch, size_t seq) {
+  return MlaCfg{(int)batch, (int)seq, c.d_model, c.n_heads, c.kv_latent, c.rope_dim, c.head_dim, c.v_dim,
+                c.causal, 0, (double)c.eps, (double)c.rope_base};
+}
+// Width of the RoPE table of a block: the head for standard attention, the decoupled RoPE dims for MLA.
+static size_t rope_dim_of(const talos_block_cfg& c) {
+  return (size_t)(c.attention == TALOS_ATTN_MLA ? c.rope_dim : c.head_dim);
+}
+static size_t block_param_count(const talos_block_cfg& c) {
+  size_t d = c.d_model, F = c.ffn_dim, H = c.n_heads;
+  size_t mlp = d + d * F + F + F * d + d;
+  if (c.attention == TALOS_ATTN_MLA) {
+    size_t L = c.kv_latent, r = c.rope_dim, hd = c.head_dim, vd = c.v_dim;
+    return d + d * L + L * H * hd + L * H * vd + d * H * hd + 2 * d * H * r + H * vd * d + mlp;
+  }
+  return d + 3 * d * d + d * d + mlp;
+}
 static Tensor split_cols(const Tensor& w, size_t c0, size_t nc) {
   size_t r = w.shape[0], C = w.shape[1];
   Vec d(r * nc);
@@ -937,6 +1018,15 @@ static Tensor split_cols(const Tensor& w, size_t c0, size_t nc) {
 static Block make_block(Params& P, const talos_block_cfg& c) {
   Block b;
   size_t d = c.d_model, F = c.ffn_dim;
+  if (c.attention == TALOS_ATTN_MLA) {
+    b.mla_attn = true;
+    b.mla = make_mla(P, mla_cfg_of(c, c.batch, c.seq));
+    b.g1 = b.mla.g;
+    b.g2 = P.take({d});
+    b.w1 = make_linear(P, d, F, true);
+    b.w2 = make_linear(P, F, d, true);
+    return b;
+  }
   b.g1 = P.take({d});
   b.wqkv = P.take({d, 3 * d});
   b.wq.weight = split_cols(b.wqkv, 0, d);
@@ -954,6 +1044,7 @@ static Block make_block(Params& P, const talos_block_cfg& c) {
 }
 // After backward: pack the three split weight grads into the Wqkv leaf's grad.
 static void block_pack_grads(Block& b) {
+  if (b.mla_attn) return;
   size_t d = b.wq.in_f;
   Vec& G = *b.wqkv.grad;
   const Linear* L[3] = {&b.wq, &b.wk, &b.wv};
@@ -962,6 +1053,7 @@ static void block_pack_grads(Block& b) {
       for (size_t j = 0; j < d; ++j) G[i * 3 * d + s * d + j] += (*L[s]->weight.grad)[i * d + j];
 }
 static void block_zero_split_grads(Block& b) {
+  if (b.mla_attn) return;
   zero_grad(b.wq.weight);
   zero_grad(b.wk.weight);
   zero_grad(b.wv.weight);
@@ -969,8 +1061,16 @@ static void block_zero_split_grads(Block& b) {
 
 // Pre-norm block forward (wiring of src/transformer.rs:71-90 with the attention of
 // src/transformer.rs:478-557, standard heads): x [B,S,d] -> out [B,S,d].
+static Tensor block_mlp(const Block& b, const talos_block_cfg& c, const Tensor& h2) {
+  Tensor xn2 = rmsnorm(h2, b.g2, c.eps);
+  Tensor f1 = linear_forward(b.w1, xn2);
+  f1 = c.activation == TALOS_ACT_RELU ? relu(f1) : gelu(f1);
+  Tensor f2 = linear_forward(b.w2, f1);
+  return add(h2, f2);
+}
 static Tensor block_forward(const Block& b, const talos_block_cfg& c, const Rope& R, const Tensor& x) {
   size_t B = x.shape[0], S = x.shape[1], d = c.d_model, H = c.n_heads, hd = c.head_dim;
+  if (b.mla_attn) return block_mlp(b, c, mla_forward(b.mla, mla_cfg_of(c, B, S), R, x));
   Tensor xn = rmsnorm(x, b.g1, c.eps);
   auto heads = [&](const Linear& L, bool rot) {
     Tensor t = linear_forward(L, xn);                 // [B,S,d]
@@ -987,12 +1087,7 @@ static Tensor block_forward(const Block& b, const talos_block_cfg& c, const Rope
   o = reshape(o, {B, H, S, hd});
   o = transpose(o, 1, 2);
   o = reshape(o, {B, S, d});
-  Tensor h2 = add(x, linear_forward(b.wo, o));
-  Tensor xn2 = rmsnorm(h2, b.g2, c.eps);
-  Tensor f1 = linear_forward(b.w1, xn2);
-  f1 = c.activation == TALOS_ACT_RELU ? relu(f1) : gelu(f1);
-  Tensor f2 = linear_forward(b.w2, f1);
-  return add(h2, f2);
+  return block_mlp(b, c, add(x, linear_forward(b.wo, o)));
 }
 
 // ---------------------------------------------------------------------------
@@ -1010,6 +1105,10 @@ static talos_block_cfg block_cfg_of(const talos_ppo_cfg& p) {
   c.activation = p.activation;
   c.eps = p.eps;
   c.rope_base = p.rope_base;
+  c.attention = p.attention;
+  c.kv_latent = p.kv_latent;
+  c.rope_dim = p.rope_dim;
+  c.v_dim = p.v_dim;
   return c;
 }
 struct Policy {
@@ -1128,67 +1227,6 @@ static Tensor ppo_batched_loss(const talos_ppo_cfg& c, const Tensor& logits, con
     for (size_t i = 0; i < gz.size(); ++i) gz[i] += g[0] * (*dz)[i];
     for (size_t i = 0; i < gv.size(); ++i) gv[i] += g[0] * (*dv)[i];
   });
-}
-
-// ---------------------------------------------------------------------------
-// MLA block (src/transformer.rs:478-557) with a pre-norm residual around it.
-// ---------------------------------------------------------------------------
-struct MlaCfg {
-  int batch, seq, d_model, n_heads, kv_latent, rope_dim, head_dim, v_dim;
-  int causal;       // extension
-  int literal_rope; // 1: rotate q_r/k_r along shape[-2] of [B,S,H,R] (the head index) like the
-                    // reference's training path; 0: rotate by the sequence position
-  double eps, rope_base;
-};
-struct Mla {
-  Tensor g;
-  Linear w_dkv, w_uk, w_uv, w_q, w_kr, w_qr, w_o;
-};
-static Mla make_mla(Params& P, const MlaCfg& c) {
-  Mla m;
-  size_t d = c.d_model, H = c.n_heads;
-  m.g = P.take({d});
-  m.w_dkv = make_linear(P, d, c.kv_latent, false);
-  m.w_uk = make_linear(P, c.kv_latent, H * c.head_dim, false);
-  m.w_uv = make_linear(P, c.kv_latent, H * c.v_dim, false);
-  m.w_q = make_linear(P, d, H * c.head_dim, false);
-  m.w_kr = make_linear(P, d, H * c.rope_dim, false);
-  m.w_qr = make_linear(P, d, H * c.rope_dim, false);
-  m.w_o = make_linear(P, H * c.v_dim, d, false);
-  return m;
-}
-static Tensor mla_forward(const Mla& m, const MlaCfg& c, const Rope& R, const Tensor& xin) {
-  size_t B = c.batch, S = c.seq, H = c.n_heads, hd = c.head_dim, rd = c.rope_dim, vd = c.v_dim;
-  Tensor x = rmsnorm(xin, m.g, c.eps);
-  Tensor c_kv = linear_forward(m.w_dkv, x);
-  Tensor k_c = linear_forward(m.w_uk, c_kv);
-  Tensor v_c = linear_forward(m.w_uv, c_kv);
-  Tensor k_r_flat = linear_forward(m.w_kr, x);
-  Tensor q_c = linear_forward(m.w_q, x);
-  Tensor q_r_flat = linear_forward(m.w_qr, x);
-  Tensor k_r = reshape(k_r_flat, {B, S, H, rd});
-  Tensor q_r = reshape(q_r_flat, {B, S, H, rd});
-  Tensor k_rot, q_rot;
-  if (c.literal_rope) {
-    k_rot = rope_forward(R, k_r, 0);
-    q_rot = rope_forward(R, q_r, 0);
-  } else {
-    k_rot = transpose(rope_forward(R, transpose(k_r, 1, 2), 0), 1, 2);
-    q_rot = transpose(rope_forward(R, transpose(q_r, 1, 2), 0), 1, 2);
-  }
-  Tensor q = concat_last(reshape(q_c, {B, S, H, hd}), q_rot);
-  Tensor k = concat_last(reshape(k_c, {B, S, H, hd}), k_rot);
-  Tensor v = reshape(v_c, {B, S, H, vd});
-  size_t td = hd + rd;
-  Tensor qf = reshape(transpose(q, 1, 2), {B * H, S, td});
-  Tensor kf = reshape(transpose(k, 1, 2), {B * H, S, td});
-  Tensor vf = reshape(transpose(v, 1, 2), {B * H, S, vd});
-  Tensor sc = bmm_qt_k(qf, kf, B * H, S, td);
-  Tensor scs = scale_tensor(sc, 1.0 / std::sqrt((double)td));
-  Tensor pr = softmax(scs, S, c.causal != 0);
-  Tensor o = bmm_p_v(pr, vf, B * H, S, vd);
-  o = reshape(transpose(reshape(o, {B, H, S, vd}), 1, 2), {B, S, H * vd});
-  return add(xin, linear_forward(m.w_o, o));
 }
 
 }  // namespace orc
@@ -1527,6 +1565,8 @@ int orc_attention_fwd_bwd(int64_t B, int64_t S, int64_t H, int64_t dk, int64_t d
   })
 }
 
+size_t orc_block_param_count(const talos_block_cfg* c) { return block_param_count(*c); }
+
 // C3: one block fwd+bwd with loss = sum(out * gout).
 int orc_block_fwd_bwd(const talos_block_cfg* c, const double* params, const double* x, const double* gout,
                       double* out, double* dparams, double* dx) {
@@ -1534,7 +1574,7 @@ int orc_block_fwd_bwd(const talos_block_cfg* c, const double* params, const doub
     Params P;
     P.src = params;
     Block b = make_block(P, *c);
-    Rope R = rope_new((size_t)c->head_dim, (size_t)c->seq, c->rope_base);
+    Rope R = rope_new(rope_dim_of(*c), (size_t)c->seq, c->rope_base);
     Shape s{(size_t)c->batch, (size_t)c->seq, (size_t)c->d_model};
     Tensor X = tnew(Vec(x, x + prod(s)), s);
     Tensor O = block_forward(b, *c, R, X);
@@ -1548,8 +1588,8 @@ int orc_block_fwd_bwd(const talos_block_cfg* c, const double* params, const doub
 }
 
 size_t orc_ppo_param_count(const talos_ppo_cfg* c) {
-  size_t d = c->d_model, F = c->ffn_dim;
-  size_t blk = d + 3 * d * d + d * d + d + d * F + F + F * d + d;
+  size_t d = c->d_model;
+  size_t blk = block_param_count(block_cfg_of(*c));
   return c->in_dim * d + d + c->n_layers * blk + d + d * d + d + d * c->n_actions + c->n_actions + d + 1;
 }
 
@@ -1562,7 +1602,7 @@ int orc_ppo_fwd_bwd(const talos_ppo_cfg* c, const double* params, const double* 
     Params P;
     P.src = params;
     Policy pol = make_policy(P, *c);
-    Rope R = rope_new((size_t)c->head_dim, (size_t)c->seq, c->rope_base);
+    Rope R = rope_new(rope_dim_of(block_cfg_of(*c)), (size_t)c->seq, c->rope_base);
     size_t B = c->batch, S = c->seq, I = c->in_dim;
     Tensor X = tnew(Vec(states, states + B * S * I), {B, S, I});
     Tensor last = policy_last_hidden(pol, *c, R, X, true);
@@ -1590,7 +1630,7 @@ int orc_ppo_fwd_bwd_per_sample(const talos_ppo_cfg* c, const double* params, con
     Params P;
     P.src = params;
     Policy pol = make_policy(P, *c);
-    Rope R = rope_new((size_t)c->head_dim, (size_t)c->seq, c->rope_base);
+    Rope R = rope_new(rope_dim_of(block_cfg_of(*c)), (size_t)c->seq, c->rope_base);
     size_t B = c->batch, S = c->seq, I = c->in_dim, A = c->n_actions;
     Tensor acc = tzeros({1});
     for (size_t i = 0; i < B; ++i) {

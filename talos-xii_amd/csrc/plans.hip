@@ -3,11 +3,16 @@
 // A plan owns every device buffer one configuration needs (saved activations, gradient
 // scratch, split-K partials, the RoPE table), so a training step allocates nothing.
 //
-// Block (talos_block_cfg; the wiring of LuckTransformer::forward, src/transformer.rs:71-90, with
-// standard multi-head attention in place of MLA):
+// Block (talos_block_cfg; the wiring of LuckTransformer::forward, src/transformer.rs:71-90):
 //   xn1 = rmsnorm(x; g1)                       rowops  (rstd saved)
-//   qkv = xn1 . Wqkv, RoPE on the q|k columns   GEMM, RoPE in the epilogue
-//   o   = attention(q, k, v)                    fused attention (lse saved)
+//   standard attention (TALOS_ATTN_MHA):
+//     qkv = xn1 . Wqkv, RoPE on the q|k columns GEMM, RoPE in the epilogue
+//     o   = attention(q, k, v)                  fused attention (lse saved)
+//   latent attention (TALOS_ATTN_MLA, MultiHeadLatentAttention::forward, src/transformer.rs:478-557):
+//     c_kv = xn1 . W_dkv, k_c = c_kv . W_uk, v = c_kv . W_uv, q_c = xn1 . W_q,
+//     q_r = xn1 . W_qr, k_r = xn1 . W_kr        GEMMs, RoPE in the q_r / k_r epilogues
+//     q = [q_c | q_r], k = [k_c | k_r] per head concatenation
+//     o   = attention(q, k, v), scale 1/sqrt(head_dim + rope_dim)
 //   h2  = x + o . Wo                            GEMM, residual in the epilogue
 //   xn2 = rmsnorm(h2; g2)
 //   a   = act(xn2 . W1 + b1)                    GEMM, bias + activation epilogue (u saved)
@@ -29,16 +34,21 @@
 #include "rowops.hpp"
 
 struct talos_plan_s {
-  int kind = 0;  // 1 block, 2 ppo
+  int kind = 0;  // 1 block, 2 ppo, 3 mla
   talos_block_cfg blk{};
   talos_ppo_cfg ppo{};
   std::vector<void*> allocs;
-  // rope table [seq, head_dim/2]
+  // rope table [seq, rope width / 2] (the head for standard attention, rope_dim for MLA)
   float* rcos = nullptr;
   float* rsin = nullptr;
-  // per layer saved activations
+  // per layer saved activations; a latent-attention layer keeps c_kv, v and the concatenated
+  // q / k in m instead of qkv
+  struct MlaAct {
+    float *ckv, *v, *q, *k;
+  };
   struct Layer {
     float *x, *xn1, *rstd1, *qkv, *o, *lse, *h2, *xn2, *rstd2, *u, *a, *out;
+    MlaAct m;
   };
   std::vector<Layer> layers;
   // backward scratch
@@ -63,39 +73,73 @@ struct talos_plan_s {
   int num_cu = 256;
   bool bf16 = false;  // bf16-in / fp32-accumulate GEMMs (MLA plans with TALOS_PREC_BF16)
   talos::Profiler* prof = nullptr;
-  // mla
+  // latent attention: the projections before concatenation and the attention gradients,
+  // shared by all layers
+  struct MlaScratch {
+    float *qc, *qr, *kc, *kr, *dq, *dk, *dv, *dqc, *dqr, *dkc, *dkr, *dckv;
+  } ms{};
   talos_mla_cfg mla{};
-  struct MlaBufs {
-    float *xn, *rstd, *ckv, *kc, *v, *qc, *qr, *kr, *q, *k, *o, *lse;
-    float *g_o, *dq, *dk, *dv, *dqc, *dqr, *dkc, *dkr, *dckv, *dxn;
-  } mb{};
 };
 
 namespace talos {
 
-static size_t block_params(const talos_block_cfg& c) {
-  const size_t d = c.d_model, F = c.ffn_dim;
-  return d + 3 * d * d + d * d + d + d * F + F + F * d + d;
+// Shape of one latent attention (a TALOS_ATTN_MLA block, or an MLA plan).
+struct MlaDims {
+  int batch, seq, d, H, L, r, hd, vd, causal;
+};
+static MlaDims mla_dims(const talos_block_cfg& c) {
+  return MlaDims{c.batch, c.seq, c.d_model, c.n_heads, c.kv_latent, c.rope_dim, c.head_dim, c.v_dim, c.causal};
+}
+static MlaDims mla_dims(const talos_mla_cfg& c) {
+  return MlaDims{c.batch, c.seq, c.d_model, c.n_heads, c.kv_latent, c.rope_dim, c.head_dim, c.v_dim, c.causal};
 }
 
-static size_t ppo_params(const talos_ppo_cfg& c) {
-  const size_t d = c.d_model, F = c.ffn_dim;
-  const size_t blk = d + 3 * d * d + d * d + d + d * F + F + F * d + d;
-  return (size_t)c.in_dim * d + d + (size_t)c.n_layers * blk + d + d * d + d + d * (size_t)c.n_actions +
-         (size_t)c.n_actions + d + 1;
+// Offsets of the latent-attention weights W_dkv | W_uk | W_uv | W_q | W_kr | W_qr | W_o (the
+// order of MultiHeadLatentAttention::parameters, src/transformer.rs:466-476) from base.
+struct MlaW {
+  size_t wdkv, wuk, wuv, wq, wkr, wqr, wo, end;
+};
+static MlaW mla_weights(const MlaDims& D, size_t base) {
+  const size_t d = D.d, H = D.H, L = D.L, r = D.r, hd = D.hd, vd = D.vd;
+  MlaW w;
+  w.wdkv = base;
+  w.wuk = w.wdkv + d * L;
+  w.wuv = w.wuk + L * H * hd;
+  w.wq = w.wuv + L * H * vd;
+  w.wkr = w.wq + d * H * hd;
+  w.wqr = w.wkr + d * H * r;
+  w.wo = w.wqr + d * H * r;
+  w.end = w.wo + H * vd * d;
+  return w;
+}
+
+// Width of a block's attention output (the rows of Wo).
+static int attn_width(const talos_block_cfg& c) {
+  return c.attention == TALOS_ATTN_MLA ? c.n_heads * c.v_dim : c.d_model;
+}
+// Width of a block's RoPE table.
+static int rope_width(const talos_block_cfg& c) {
+  return c.attention == TALOS_ATTN_MLA ? c.rope_dim : c.head_dim;
 }
 
 // Offsets of one block's parameters inside a flat buffer.
 struct BlockOff {
   size_t g1, wqkv, wo, g2, w1, b1, w2, b2, end;
+  MlaW mla;  // TALOS_ATTN_MLA: the attention weights (mla.wo == wo)
 };
 static BlockOff block_offsets(const talos_block_cfg& c, size_t base) {
   const size_t d = c.d_model, F = c.ffn_dim;
-  BlockOff o;
+  BlockOff o{};
   o.g1 = base;
-  o.wqkv = o.g1 + d;
-  o.wo = o.wqkv + 3 * d * d;
-  o.g2 = o.wo + d * d;
+  if (c.attention == TALOS_ATTN_MLA) {
+    o.mla = mla_weights(mla_dims(c), o.g1 + d);
+    o.wo = o.mla.wo;
+    o.g2 = o.mla.end;
+  } else {
+    o.wqkv = o.g1 + d;
+    o.wo = o.wqkv + 3 * d * d;
+    o.g2 = o.wo + d * d;
+  }
   o.w1 = o.g2 + d;
   o.b1 = o.w1 + d * F;
   o.w2 = o.b1 + F;
@@ -104,46 +148,7 @@ static BlockOff block_offsets(const talos_block_cfg& c, size_t base) {
   return o;
 }
 
-struct PpoOff {
-  size_t we, be, blocks, gf, wout, bout, wa, ba, wc, bc, end;
-};
-static PpoOff ppo_offsets(const talos_ppo_cfg& c) {
-  const size_t d = c.d_model;
-  PpoOff o;
-  o.we = 0;
-  o.be = (size_t)c.in_dim * d;
-  o.blocks = o.be + d;
-  talos_block_cfg bc{};
-  bc.d_model = c.d_model;
-  bc.ffn_dim = c.ffn_dim;
-  o.gf = o.blocks + (size_t)c.n_layers * block_params(bc);
-  o.wout = o.gf + d;
-  o.bout = o.wout + d * d;
-  o.wa = o.bout + d;
-  o.ba = o.wa + d * (size_t)c.n_actions;
-  o.wc = o.ba + c.n_actions;
-  o.bc = o.wc + d;
-  o.end = o.bc + 1;
-  return o;
-}
-
-static int check_block_cfg(const talos_block_cfg& c) {
-  TALOS_REQUIRE(c.batch > 0 && c.seq > 0 && c.d_model > 0 && c.n_heads > 0 && c.head_dim > 0 && c.ffn_dim > 0,
-                TALOS_ERR_SHAPE, "block cfg: sizes must be positive");
-  TALOS_REQUIRE(c.n_heads * c.head_dim == c.d_model, TALOS_ERR_SHAPE, "block cfg: n_heads * head_dim (%d * %d) != d_model %d",
-                c.n_heads, c.head_dim, c.d_model);
-  TALOS_REQUIRE(c.head_dim % 2 == 0, TALOS_ERR_SHAPE, "block cfg: head_dim must be even for RoPE pairs");
-  TALOS_REQUIRE(c.head_dim <= 128, TALOS_ERR_UNSUPPORTED, "block cfg: head_dim %d > 128", c.head_dim);
-  TALOS_REQUIRE(c.causal == 0 || c.causal == 1, TALOS_ERR_DTYPE, "block cfg: causal must be 0 or 1");
-  TALOS_REQUIRE(c.activation == TALOS_ACT_GELU || c.activation == TALOS_ACT_RELU, TALOS_ERR_DTYPE,
-                "block cfg: unknown activation %d", c.activation);
-  TALOS_REQUIRE(c.d_model % 4 == 0 && c.ffn_dim % 4 == 0, TALOS_ERR_UNSUPPORTED,
-                "block cfg: d_model and ffn_dim must be multiples of 4");
-  TALOS_REQUIRE(c.eps >= 0.f && c.rope_base > 0.f, TALOS_ERR_SHAPE, "block cfg: eps >= 0 and rope_base > 0 required");
-  TALOS_REQUIRE((long long)c.batch * c.seq * (3LL * c.d_model) < (1LL << 31), TALOS_ERR_UNSUPPORTED,
-                "block cfg: batch*seq*3*d_model must stay below 2^31 elements");
-  return TALOS_OK;
-}
+static size_t block_params(const talos_block_cfg& c) { return block_offsets(c, 0).end; }
 
 static talos_block_cfg block_cfg_of(const talos_ppo_cfg& p) {
   talos_block_cfg c{};
@@ -157,7 +162,65 @@ static talos_block_cfg block_cfg_of(const talos_ppo_cfg& p) {
   c.activation = p.activation;
   c.eps = p.eps;
   c.rope_base = p.rope_base;
+  c.attention = p.attention;
+  c.kv_latent = p.kv_latent;
+  c.rope_dim = p.rope_dim;
+  c.v_dim = p.v_dim;
   return c;
+}
+
+struct PpoOff {
+  size_t we, be, blocks, gf, wout, bout, wa, ba, wc, bc, end;
+};
+static PpoOff ppo_offsets(const talos_ppo_cfg& c) {
+  const size_t d = c.d_model;
+  PpoOff o;
+  o.we = 0;
+  o.be = (size_t)c.in_dim * d;
+  o.blocks = o.be + d;
+  o.gf = o.blocks + (size_t)c.n_layers * block_params(block_cfg_of(c));
+  o.wout = o.gf + d;
+  o.bout = o.wout + d * d;
+  o.wa = o.bout + d;
+  o.ba = o.wa + d * (size_t)c.n_actions;
+  o.wc = o.ba + c.n_actions;
+  o.bc = o.wc + d;
+  o.end = o.bc + 1;
+  return o;
+}
+
+static size_t ppo_params(const talos_ppo_cfg& c) { return ppo_offsets(c).end; }
+
+static int check_block_cfg(const talos_block_cfg& c) {
+  TALOS_REQUIRE(c.batch > 0 && c.seq > 0 && c.d_model > 0 && c.n_heads > 0 && c.head_dim > 0 && c.ffn_dim > 0,
+                TALOS_ERR_SHAPE, "block cfg: sizes must be positive");
+  TALOS_REQUIRE(c.attention == TALOS_ATTN_MHA || c.attention == TALOS_ATTN_MLA, TALOS_ERR_DTYPE,
+                "block cfg: unknown attention %d", c.attention);
+  if (c.attention == TALOS_ATTN_MHA) {
+    TALOS_REQUIRE(c.n_heads * c.head_dim == c.d_model, TALOS_ERR_SHAPE,
+                  "block cfg: n_heads * head_dim (%d * %d) != d_model %d", c.n_heads, c.head_dim, c.d_model);
+    TALOS_REQUIRE(c.head_dim % 2 == 0, TALOS_ERR_SHAPE, "block cfg: head_dim must be even for RoPE pairs");
+    TALOS_REQUIRE(c.head_dim <= 128, TALOS_ERR_UNSUPPORTED, "block cfg: head_dim %d > 128", c.head_dim);
+  } else {
+    TALOS_REQUIRE(c.kv_latent > 0 && c.rope_dim > 0 && c.v_dim > 0, TALOS_ERR_SHAPE,
+                  "block cfg: kv_latent, rope_dim and v_dim must be positive for MLA attention");
+    TALOS_REQUIRE(c.rope_dim % 2 == 0, TALOS_ERR_SHAPE, "block cfg: rope_dim must be even");
+    TALOS_REQUIRE(c.head_dim + c.rope_dim <= 128 && c.v_dim <= 128, TALOS_ERR_UNSUPPORTED,
+                  "block cfg: head_dim + rope_dim and v_dim must be <= 128");
+    TALOS_REQUIRE(c.kv_latent % 4 == 0 && c.head_dim % 4 == 0 && c.rope_dim % 4 == 0 && c.v_dim % 4 == 0,
+                  TALOS_ERR_UNSUPPORTED, "block cfg: MLA widths must be multiples of 4");
+    TALOS_REQUIRE((long long)c.batch * c.seq * c.n_heads * (c.head_dim + c.rope_dim) < (1LL << 31),
+                  TALOS_ERR_UNSUPPORTED, "block cfg: too many elements for 32-bit indexing");
+  }
+  TALOS_REQUIRE(c.causal == 0 || c.causal == 1, TALOS_ERR_DTYPE, "block cfg: causal must be 0 or 1");
+  TALOS_REQUIRE(c.activation == TALOS_ACT_GELU || c.activation == TALOS_ACT_RELU, TALOS_ERR_DTYPE,
+                "block cfg: unknown activation %d", c.activation);
+  TALOS_REQUIRE(c.d_model % 4 == 0 && c.ffn_dim % 4 == 0, TALOS_ERR_UNSUPPORTED,
+                "block cfg: d_model and ffn_dim must be multiples of 4");
+  TALOS_REQUIRE(c.eps >= 0.f && c.rope_base > 0.f, TALOS_ERR_SHAPE, "block cfg: eps >= 0 and rope_base > 0 required");
+  TALOS_REQUIRE((long long)c.batch * c.seq * (3LL * c.d_model) < (1LL << 31), TALOS_ERR_UNSUPPORTED,
+                "block cfg: batch*seq*3*d_model must stay below 2^31 elements");
+  return TALOS_OK;
 }
 
 static int plan_alloc(talos_plan_s* p, float** out, size_t n) {
@@ -199,21 +262,63 @@ static size_t wgrad_ws(talos_plan_s* p, int M_tok, int rows, int cols) {
   return gemm_plan_split(g, p->num_cu);
 }
 
-static int alloc_block_buffers(talos_plan_s* p, const talos_block_cfg& c, int n_layers, bool own_input) {
-  const size_t M = (size_t)c.batch * c.seq, d = c.d_model, F = c.ffn_dim;
+// The saved activations of one latent attention (c_kv, v, q, k, o, lse) and, when scratch, the
+// buffers every layer shares (projections before concatenation, attention gradients).
+static int alloc_mla_layer(talos_plan_s* p, const MlaDims& D, talos_plan_s::Layer& L) {
+  const size_t M = (size_t)D.batch * D.seq, H = D.H, td = (size_t)D.hd + D.r;
+  int rc = 0;
+  rc |= plan_alloc(p, &L.m.ckv, M * D.L);
+  rc |= plan_alloc(p, &L.m.v, M * H * D.vd);
+  rc |= plan_alloc(p, &L.m.q, M * H * td);
+  rc |= plan_alloc(p, &L.m.k, M * H * td);
+  rc |= plan_alloc(p, &L.o, M * H * D.vd);
+  rc |= plan_alloc(p, &L.lse, M * H);
+  return rc ? TALOS_ERR_ALLOC : TALOS_OK;
+}
+static int alloc_mla_scratch(talos_plan_s* p, const MlaDims& D) {
+  const size_t M = (size_t)D.batch * D.seq, H = D.H, td = (size_t)D.hd + D.r;
+  auto& m = p->ms;
+  int rc = 0;
+  for (float** b : {&m.qc, &m.kc, &m.dqc, &m.dkc}) rc |= plan_alloc(p, b, M * H * D.hd);
+  for (float** b : {&m.qr, &m.kr, &m.dqr, &m.dkr}) rc |= plan_alloc(p, b, M * H * D.r);
+  for (float** b : {&m.dq, &m.dk}) rc |= plan_alloc(p, b, M * H * td);
+  rc |= plan_alloc(p, &m.dv, M * H * D.vd);
+  rc |= plan_alloc(p, &m.dckv, M * D.L);
+  if (rc) return TALOS_ERR_ALLOC;
+  // split-K workspace of the weight-gradient products
+  for (auto rc2 : {std::make_pair(D.d, D.H * D.hd), std::make_pair(D.d, D.H * D.r), std::make_pair(D.L, D.H * D.hd),
+                   std::make_pair(D.L, D.H * D.vd), std::make_pair(D.d, D.L), std::make_pair(D.H * D.vd, D.d)})
+    p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, wgrad_ws(p, (int)M, rc2.first, rc2.second));
+  return TALOS_OK;
+}
+static int upload_rope_table(talos_plan_s* p, int seq, int width, float base) {
+  std::vector<float> cs, sn;
+  rope_table_host(seq, width, (double)base, cs, sn);
+  int rc = plan_alloc(p, &p->rcos, cs.size());
+  rc |= plan_alloc(p, &p->rsin, sn.size());
+  if (rc) return TALOS_ERR_ALLOC;
+  TALOS_HIP(hipMemcpy(p->rcos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  TALOS_HIP(hipMemcpy(p->rsin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  return TALOS_OK;
+}
+
+static int alloc_block_buffers(talos_plan_s* p, const talos_block_cfg& c, int n_layers) {
+  const size_t M = (size_t)c.batch * c.seq, d = c.d_model, F = c.ffn_dim, ow = attn_width(c);
+  const bool mla = c.attention == TALOS_ATTN_MLA;
   p->layers.resize(n_layers);
   for (int l = 0; l < n_layers; ++l) {
     auto& L = p->layers[l];
     int rc = 0;
-    L.x = nullptr;
-    if (own_input || l > 0) {
-      // x of layer l is the out of layer l-1 (set below) except for the first layer
-    }
+    L.x = nullptr;  // the block input, set per call (the previous layer's out, or the caller's x)
     rc |= plan_alloc(p, &L.xn1, M * d);
     rc |= plan_alloc(p, &L.rstd1, M);
-    rc |= plan_alloc(p, &L.qkv, M * 3 * d);
-    rc |= plan_alloc(p, &L.o, M * d);
-    rc |= plan_alloc(p, &L.lse, M * c.n_heads);
+    if (mla) {
+      rc |= alloc_mla_layer(p, mla_dims(c), L);
+    } else {
+      rc |= plan_alloc(p, &L.qkv, M * 3 * d);
+      rc |= plan_alloc(p, &L.o, M * d);
+      rc |= plan_alloc(p, &L.lse, M * c.n_heads);
+    }
     rc |= plan_alloc(p, &L.h2, M * d);
     rc |= plan_alloc(p, &L.xn2, M * d);
     rc |= plan_alloc(p, &L.rstd2, M);
@@ -227,28 +332,25 @@ static int alloc_block_buffers(talos_plan_s* p, const talos_block_cfg& c, int n_
   rc |= plan_alloc(p, &p->g_h2, M * d);
   rc |= plan_alloc(p, &p->g_u, M * F);
   rc |= plan_alloc(p, &p->g_xn, M * d);
-  rc |= plan_alloc(p, &p->g_o, M * d);
-  rc |= plan_alloc(p, &p->g_qkv, M * 3 * d);
+  rc |= plan_alloc(p, &p->g_o, M * ow);
   rc |= plan_alloc(p, &p->g_x, M * d);
   rc |= plan_alloc(p, &p->attn_ws, M * c.n_heads);
+  if (mla)
+    rc |= alloc_mla_scratch(p, mla_dims(c));
+  else
+    rc |= plan_alloc(p, &p->g_qkv, M * 3 * d);
   if (rc) return TALOS_ERR_ALLOC;
   size_t ws = 0;
-  ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, 3 * (int)d));
-  ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, (int)d));
+  if (!mla) {
+    ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, 3 * (int)d));
+    ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, (int)d));
+  }
   ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, (int)F));
   ws = std::max(ws, wgrad_ws(p, (int)M, (int)F, (int)d));
   p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, ws);
   size_t red = std::max(colsum_workspace_bytes((int)M, (int)F), rmsnorm_bwd_workspace_bytes((int)M, (int)d));
   p->red_ws_bytes = std::max(p->red_ws_bytes, red);
-  // rope table
-  std::vector<float> cs, sn;
-  rope_table_host(c.seq, c.head_dim, (double)c.rope_base, cs, sn);
-  rc |= plan_alloc(p, &p->rcos, cs.size());
-  rc |= plan_alloc(p, &p->rsin, sn.size());
-  if (rc) return TALOS_ERR_ALLOC;
-  TALOS_HIP(hipMemcpy(p->rcos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
-  TALOS_HIP(hipMemcpy(p->rsin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
-  return TALOS_OK;
+  return upload_rope_table(p, c.seq, rope_width(c), c.rope_base);
 }
 
 static int alloc_workspaces(talos_plan_s* p) {
@@ -289,6 +391,110 @@ static int mm(talos_plan_s* p, hipStream_t s, int tA, int tB, int M, int N, int 
   if (ws > p->gemm_ws_bytes) g.ksplit = 1;
   g.workspace = p->gemm_ws;
   return gemm_launch(g, s);
+}
+
+// Latent attention (MultiHeadLatentAttention::forward, src/transformer.rs:478-557) --------------
+static AttnDesc mla_attn_desc(talos_plan_s* p, const MlaDims& D, const talos_plan_s::Layer& L) {
+  const int td = D.hd + D.r;
+  AttnDesc a;
+  a.batch = D.batch;
+  a.seq = D.seq;
+  a.heads = D.H;
+  a.dk = td;
+  a.dv = D.vd;
+  a.scale = (float)(1.0 / std::sqrt((double)td));  // src/transformer.rs:542
+  a.causal = D.causal;
+  a.q = L.m.q;
+  a.ldq = (long long)D.H * td;
+  a.k = L.m.k;
+  a.ldk = (long long)D.H * td;
+  a.v = L.m.v;
+  a.ldv = (long long)D.H * D.vd;
+  a.o = L.o;
+  a.ldo = (long long)D.H * D.vd;
+  a.lse = L.lse;
+  a.dq = p->ms.dq;
+  a.lddq = (long long)D.H * td;
+  a.dk_out = p->ms.dk;
+  a.lddk = (long long)D.H * td;
+  a.dv_out = p->ms.dv;
+  a.lddv = (long long)D.H * D.vd;
+  a.rope_cos = p->rcos;
+  a.rope_sin = p->rsin;
+  a.rope_off = D.hd;  // the decoupled RoPE dims follow the content dims in each head
+  a.rope_dim = D.r;
+  a.lens = p->lens;
+  return a;
+}
+
+// xn -> L.o (and L.lse): the projections, RoPE on q_r / k_r, per-head concatenation, attention.
+static int mla_attn_forward(talos_plan_s* p, const MlaDims& D, const float* P, const MlaW& w, const float* xn,
+                            talos_plan_s::Layer& L, hipStream_t s) {
+  const int M = D.batch * D.seq, d = D.d, H = D.H, Lt = D.L, r = D.r, hd = D.hd, vd = D.vd;
+  const size_t MH = (size_t)M * H;
+  auto& m = p->ms;
+  auto rope_gemm = [&](const float* W, float* C) {
+    GemmDesc g;
+    g.M = M;
+    g.N = H * r;
+    g.K = d;
+    g.A = xn;
+    g.lda = d;
+    g.B = W;
+    g.ldb = H * r;
+    g.C = C;
+    g.ldc = H * r;
+    g.rope_cos = p->rcos;
+    g.rope_sin = p->rsin;
+    g.rope_cols = H * r;
+    g.rope_dim = r;
+    g.rope_seq = D.seq;
+    g.ksplit = 1;
+    g.bf16 = p->bf16;
+    return gemm_launch(g, s);
+  };
+  int rc;
+  if ((rc = mm(p, s, 0, 0, M, Lt, d, xn, d, P + w.wdkv, Lt, L.m.ckv, Lt))) return rc;
+  if ((rc = mm(p, s, 0, 0, M, H * hd, Lt, L.m.ckv, Lt, P + w.wuk, H * hd, m.kc, H * hd))) return rc;
+  if ((rc = mm(p, s, 0, 0, M, H * vd, Lt, L.m.ckv, Lt, P + w.wuv, H * vd, L.m.v, H * vd))) return rc;
+  if ((rc = mm(p, s, 0, 0, M, H * hd, d, xn, d, P + w.wq, H * hd, m.qc, H * hd))) return rc;
+  if ((rc = rope_gemm(P + w.wqr, m.qr))) return rc;
+  if ((rc = rope_gemm(P + w.wkr, m.kr))) return rc;
+  if ((rc = concat_launch(MH, hd, r, m.qc, m.qr, L.m.q, s))) return rc;
+  if ((rc = concat_launch(MH, hd, r, m.kc, m.kr, L.m.k, s))) return rc;
+  return attn_fwd_launch(mla_attn_desc(p, D, L), s);
+}
+
+// From g_o = dL/d(L.o) [tokens, H*vd]: the gradients of the six projection weights (written to
+// G) and dxn = dL/dxn (overwritten).
+static int mla_attn_backward(talos_plan_s* p, const MlaDims& D, const float* P, float* G, const MlaW& w,
+                             const float* xn, const talos_plan_s::Layer& L, const float* g_o, float* dxn,
+                             hipStream_t s) {
+  const int M = D.batch * D.seq, d = D.d, H = D.H, Lt = D.L, r = D.r, hd = D.hd, vd = D.vd;
+  const size_t MH = (size_t)M * H;
+  auto& m = p->ms;
+  AttnDesc a = mla_attn_desc(p, D, L);
+  a.dout = g_o;
+  a.lddo = (long long)H * vd;
+  int rc;
+  if ((rc = attn_bwd_launch(a, p->attn_ws, s))) return rc;
+  if ((rc = split_launch(MH, hd, r, m.dq, m.dqc, m.dqr, false, s))) return rc;
+  if ((rc = split_launch(MH, hd, r, m.dk, m.dkc, m.dkr, false, s))) return rc;
+  // q / rope-k projections of xn
+  if ((rc = mm(p, s, 1, 0, d, H * hd, M, xn, d, m.dqc, H * hd, G + w.wq, H * hd))) return rc;
+  if ((rc = mm(p, s, 1, 0, d, H * r, M, xn, d, m.dqr, H * r, G + w.wqr, H * r))) return rc;
+  if ((rc = mm(p, s, 1, 0, d, H * r, M, xn, d, m.dkr, H * r, G + w.wkr, H * r))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, d, H * hd, m.dqc, H * hd, P + w.wq, H * hd, dxn, d))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, d, H * r, m.dqr, H * r, P + w.wqr, H * r, dxn, d, 1.f))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, d, H * r, m.dkr, H * r, P + w.wkr, H * r, dxn, d, 1.f))) return rc;
+  // up projections of the latent
+  if ((rc = mm(p, s, 1, 0, Lt, H * hd, M, L.m.ckv, Lt, m.dkc, H * hd, G + w.wuk, H * hd))) return rc;
+  if ((rc = mm(p, s, 1, 0, Lt, H * vd, M, L.m.ckv, Lt, m.dv, H * vd, G + w.wuv, H * vd))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, Lt, H * hd, m.dkc, H * hd, P + w.wuk, H * hd, m.dckv, Lt))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, Lt, H * vd, m.dv, H * vd, P + w.wuv, H * vd, m.dckv, Lt, 1.f))) return rc;
+  // down projection
+  if ((rc = mm(p, s, 1, 0, d, Lt, M, xn, d, m.dckv, Lt, G + w.wdkv, Lt))) return rc;
+  return mm(p, s, 0, 1, M, d, Lt, m.dckv, Lt, P + w.wdkv, Lt, dxn, d, 1.f);
 }
 
 // The block's attention over its qkv buffer (q, k, v column blocks of one [tokens, 3d] buffer).
@@ -347,9 +553,14 @@ static int block_qkv_forward(talos_plan_s* p, const talos_block_cfg& c, const fl
   }
 }
 
-// Attention half of a block's forward: qkv, then o = attention(q, k, v) with lse saved.
+// Attention half of a block's forward: o = attention(rmsnorm(x)) with lse saved.
 static int block_attn_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
                               talos_plan_s::Layer& L, hipStream_t s) {
+  if (c.attention == TALOS_ATTN_MLA) {
+    int rc = rmsnorm_fwd_launch(c.batch * c.seq, c.d_model, c.eps, L.x, P + o.g1, L.xn1, L.rstd1, s);
+    if (rc) return rc;
+    return mla_attn_forward(p, mla_dims(c), P, o.mla, L.xn1, L, s);
+  }
   int rc = block_qkv_forward(p, c, P, o, L, s);
   if (rc) return rc;
   return attn_fwd_launch(block_attn_desc(p, c, L), s);
@@ -360,8 +571,8 @@ static int block_attn_forward(talos_plan_s* p, const talos_block_cfg& c, const f
 static int block_mlp_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o, int R,
                              const float* x, const float* ob, float* h2, float* xn2, float* rstd2, float* u, float* a,
                              float* out, hipStream_t s) {
-  const int d = c.d_model, F = c.ffn_dim;
-  int rc = mm(p, s, 0, 0, R, d, d, ob, d, P + o.wo, d, h2, d, 0.f, nullptr, x, d);
+  const int d = c.d_model, F = c.ffn_dim, ow = attn_width(c);
+  int rc = mm(p, s, 0, 0, R, d, ow, ob, ow, P + o.wo, d, h2, d, 0.f, nullptr, x, d);
   if (rc) return rc;
   rc = rmsnorm_fwd_launch(R, d, c.eps, h2, P + o.g2, xn2, rstd2, s);
   if (rc) return rc;
@@ -401,7 +612,7 @@ static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const f
                               int R, const float* ob, const float* h2, const float* xn2, const float* rstd2,
                               const float* u, const float* a, const float* gout, float* g_u, float* g_xn, float* g_h2,
                               float* g_o, hipStream_t s) {
-  const int d = c.d_model, F = c.ffn_dim;
+  const int d = c.d_model, F = c.ffn_dim, ow = attn_width(c);
   // out = h2 + a.W2 + b2
   int rc = mm(p, s, 1, 0, F, d, R, a, F, gout, d, G + o.w2, d, 0.f, nullptr, nullptr, 0, G + o.b2);
   if (rc) return rc;
@@ -433,14 +644,24 @@ static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const f
   rc = rmsnorm_bwd_launch(R, d, h2, P + o.g2, rstd2, g_xn, 1.f, g_h2, 0.f, G + o.g2, p->red_ws, s, gout);
   if (rc) return rc;
   // h2 = x + o.Wo
-  rc = mm(p, s, 1, 0, d, d, R, ob, d, g_h2, d, G + o.wo, d);
+  rc = mm(p, s, 1, 0, ow, d, R, ob, ow, g_h2, d, G + o.wo, d);
   if (rc) return rc;
-  return mm(p, s, 0, 1, R, d, d, g_h2, d, P + o.wo, d, g_o, d);
+  return mm(p, s, 0, 1, R, ow, d, g_h2, d, P + o.wo, d, g_o, ow);
 }
 
-// From the qkv gradient (p->g_qkv) back to x: the Wqkv / gain1 gradients and dx = rmsnorm1's
-// backward + the residual gradient reaching x through h2, given on every row (g_h2) or on the
-// last token of each sample only (g_h2_last, [batch, d]).
+// rmsnorm1's backward from p->g_xn = dL/dxn1: the gain1 gradient and dx, which also receives the
+// residual gradient reaching x through h2, given on every row (g_h2) or on the last token of each
+// sample only (g_h2_last, [batch, d]). dx is overwritten: the residual arrives through g_h2 or
+// g_h2_last, never through dx's old contents.
+static int block_norm1_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G,
+                                const BlockOff& o, const talos_plan_s::Layer& L, const float* g_h2,
+                                const float* g_h2_last, float* dx, hipStream_t s) {
+  return rmsnorm_bwd_launch(c.batch * c.seq, c.d_model, L.x, P + o.g1, L.rstd1, p->g_xn, 0.f, dx, 0.f, G + o.g1,
+                            p->red_ws, s, g_h2, g_h2_last, c.seq, p->lens);
+}
+
+// Standard attention, from the qkv gradient (p->g_qkv) back to x: the Wqkv gradient, dxn1 and
+// rmsnorm1's backward (block_norm1_backward).
 static int block_qkv_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
                               talos_plan_s::Layer& L, const float* g_h2, const float* g_h2_last, float* dx,
                               hipStream_t s) {
@@ -450,22 +671,26 @@ static int block_qkv_backward(talos_plan_s* p, const talos_block_cfg& c, const f
   if (rc) return rc;
   rc = mm(p, s, 0, 1, M, d, 3 * d, p->g_qkv, 3 * d, P + o.wqkv, 3 * d, p->g_xn, d);
   if (rc) return rc;
-  // dx is overwritten: the residual arrives through g_h2 or g_h2_last, never through dx's old contents
-  return rmsnorm_bwd_launch(M, d, L.x, P + o.g1, L.rstd1, p->g_xn, 0.f, dx, 0.f, G + o.g1, p->red_ws, s, g_h2,
-                            g_h2_last, c.seq, p->lens);
+  return block_norm1_backward(p, c, P, G, o, L, g_h2, g_h2_last, dx, s);
 }
 
-// Attention half backward over all rows: g_o = dL/do, g_h2 = the residual gradient reaching x
-// through h2; writes the Wqkv / gain1 gradients and dx.
+// Attention half backward over all rows: g_o = dL/do [tokens, attn_width], the residual gradient
+// reaching x through h2 (g_h2 on every row, or g_h2_last on the last-token rows); writes the
+// attention weights' and gain1's gradients and dx.
 static int block_attn_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
-                               talos_plan_s::Layer& L, const float* g_o, const float* g_h2, float* dx,
-                               hipStream_t s) {
+                               talos_plan_s::Layer& L, const float* g_o, const float* g_h2, const float* g_h2_last,
+                               float* dx, hipStream_t s) {
+  if (c.attention == TALOS_ATTN_MLA) {
+    int rc = mla_attn_backward(p, mla_dims(c), P, G, o.mla, L.xn1, L, g_o, p->g_xn, s);
+    if (rc) return rc;
+    return block_norm1_backward(p, c, P, G, o, L, g_h2, g_h2_last, dx, s);
+  }
   AttnDesc a = block_attn_desc(p, c, L);
   a.dout = g_o;
   a.lddo = c.d_model;
   int rc = attn_bwd_launch(a, p->attn_ws, s);
   if (rc) return rc;
-  return block_qkv_backward(p, c, P, G, o, L, g_h2, nullptr, dx, s);
+  return block_qkv_backward(p, c, P, G, o, L, g_h2, g_h2_last, dx, s);
 }
 
 // Backward of one block: gout = dL/dout (read), writes dparams slots and dx.
@@ -475,7 +700,14 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
   int rc = block_mlp_backward(p, c, P, G, o, M, L.o, L.h2, L.xn2, L.rstd2, L.u, L.a, gout, p->g_u, p->g_xn, p->g_h2,
                               p->g_o, s);
   if (rc) return rc;
-  return block_attn_backward(p, c, P, G, o, L, p->g_o, p->g_h2, dx, s);
+  return block_attn_backward(p, c, P, G, o, L, p->g_o, p->g_h2, nullptr, dx, s);
+}
+
+// Whether the PPO plan's last layer runs the attention of the last query only (standard
+// attention with the head shapes of the last-query kernels); otherwise it runs full attention
+// and gathers the last rows.
+static bool ppo_lastq(talos_plan_s* p, const talos_block_cfg& c, talos_plan_s::Layer& L) {
+  return c.attention == TALOS_ATTN_MHA && attn_lastq_supported(block_attn_desc(p, c, L));
 }
 
 // Last-token gather / scatter (last_row: common.hpp) -------------------------
@@ -609,15 +841,16 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
                        hipStream_t s) {
   const talos_block_cfg bc = block_cfg_of(c);
   const PpoOff po = ppo_offsets(c);
-  const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions;
+  const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions, ow = attn_width(bc);
   int rc = mm(p, s, 0, 0, M, d, c.in_dim, states, c.in_dim, P + po.we, d, p->h0, d, 0.f, P + po.be);
   if (rc) return rc;
   const float* h = p->h0;
   size_t base = po.blocks;
-  auto gather = [&](const float* src, float* dst) {
-    ProfScope ps_g(s, "gather_last_kernel", 0.0, 8.0 * c.batch * d);
-    hipLaunchKernelGGL(gather_last_kernel, dim3(ceil_div((size_t)c.batch * d, 256)), dim3(256), 0, s, c.batch, c.seq,
-                       d, p->lens, src, dst);
+  // the last-token rows of a [M, w] buffer into [batch, w]
+  auto gather = [&](const float* src, float* dst, int w) {
+    ProfScope ps_g(s, "gather_last_kernel", 0.0, 8.0 * c.batch * w);
+    hipLaunchKernelGGL(gather_last_kernel, dim3(ceil_div((size_t)c.batch * w, 256)), dim3(256), 0, s, c.batch, c.seq,
+                       w, p->lens, src, dst);
     return launch_status("gather_last_kernel");
   };
   for (int l = 0; l < c.n_layers; ++l) {
@@ -631,16 +864,14 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
     } else {
       // Only the last token of each sample reaches the heads, and everything after attention is
       // per row: the last layer runs its MLP half on those B rows and writes p->last directly.
-      rc = block_qkv_forward(p, bc, P, bo, L, s);
-      if (rc) return rc;
-      const AttnDesc ad = block_attn_desc(p, bc, L);
-      if (attn_lastq_supported(ad)) {  // attention of the last query only
-        rc = attn_fwd_lastq_launch(ad, p->lr.o, d, p->lr.lse, s);
+      if (ppo_lastq(p, bc, L)) {  // attention of the last query only
+        rc = block_qkv_forward(p, bc, P, bo, L, s);
+        if (rc == TALOS_OK) rc = attn_fwd_lastq_launch(block_attn_desc(p, bc, L), p->lr.o, d, p->lr.lse, s);
       } else {
-        rc = attn_fwd_launch(ad, s);
-        if (rc == TALOS_OK) rc = gather(L.o, p->lr.o);
+        rc = block_attn_forward(p, bc, P, bo, L, s);
+        if (rc == TALOS_OK) rc = gather(L.o, p->lr.o, ow);
       }
-      if (rc || (rc = gather(L.x, p->lr.x))) return rc;
+      if (rc || (rc = gather(L.x, p->lr.x, d))) return rc;
       rc = block_mlp_forward(p, bc, P, bo, c.batch, p->lr.x, p->lr.o, p->lr.h2, p->lr.xn2, p->lr.rstd2, p->lr.u,
                              p->lr.a, p->last, s);
       if (rc) return rc;
@@ -648,7 +879,7 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
     base = bo.end;
   }
   if (c.n_layers == 0) {
-    rc = gather(h, p->last);
+    rc = gather(h, p->last, d);
     if (rc) return rc;
   }
   rc = rmsnorm_fwd_launch(c.batch, d, c.eps, p->last, P + po.gf, p->lastn, p->rstdf, s);
@@ -668,20 +899,15 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
 // W_kr[d,H*r] | W_qr[d,H*r] | W_o[H*vd,d].
 // ---------------------------------------------------------------------------
 struct MlaOff {
-  size_t g, wdkv, wuk, wuv, wq, wkr, wqr, wo, end;
+  size_t g;
+  MlaW w;
+  size_t end;
 };
 static MlaOff mla_offsets(const talos_mla_cfg& c) {
-  const size_t d = c.d_model, H = c.n_heads, L = c.kv_latent, r = c.rope_dim, hd = c.head_dim, vd = c.v_dim;
   MlaOff o;
   o.g = 0;
-  o.wdkv = o.g + d;
-  o.wuk = o.wdkv + d * L;
-  o.wuv = o.wuk + L * H * hd;
-  o.wq = o.wuv + L * H * vd;
-  o.wkr = o.wq + d * H * hd;
-  o.wqr = o.wkr + d * H * r;
-  o.wo = o.wqr + d * H * r;
-  o.end = o.wo + H * vd * d;
+  o.w = mla_weights(mla_dims(c), o.g + (size_t)c.d_model);
+  o.end = o.w.end;
   return o;
 }
 
@@ -709,96 +935,20 @@ static int mla_fwd_bwd(talos_plan_s* p, const float* P, const float* x, const fl
                        float* dx, hipStream_t s) {
   const talos_mla_cfg& c = p->mla;
   const MlaOff o = mla_offsets(c);
-  auto& b = p->mb;
-  const int M = c.batch * c.seq, d = c.d_model, H = c.n_heads, L = c.kv_latent, r = c.rope_dim, hd = c.head_dim,
-            vd = c.v_dim, td = hd + r;
-  const size_t MH = (size_t)M * H;
+  const MlaDims D = mla_dims(c);
+  auto& L = p->layers[0];
+  const int M = c.batch * c.seq, d = c.d_model, ow = c.n_heads * c.v_dim;
   int rc;
-  auto rope_gemm = [&](const float* A, const float* W, float* C) {
-    GemmDesc g;
-    g.M = M;
-    g.N = H * r;
-    g.K = d;
-    g.A = A;
-    g.lda = d;
-    g.B = W;
-    g.ldb = H * r;
-    g.C = C;
-    g.ldc = H * r;
-    g.rope_cos = p->rcos;
-    g.rope_sin = p->rsin;
-    g.rope_cols = H * r;
-    g.rope_dim = r;
-    g.rope_seq = c.seq;
-    g.ksplit = 1;
-    g.bf16 = c.precision == TALOS_PREC_BF16;
-    return gemm_launch(g, s);
-  };
   // ---- forward
-  rc = rmsnorm_fwd_launch(M, d, c.eps, x, P + o.g, b.xn, b.rstd, s);
-  if (rc) return rc;
-  if ((rc = mm(p, s, 0, 0, M, L, d, b.xn, d, P + o.wdkv, L, b.ckv, L))) return rc;
-  if ((rc = mm(p, s, 0, 0, M, H * hd, L, b.ckv, L, P + o.wuk, H * hd, b.kc, H * hd))) return rc;
-  if ((rc = mm(p, s, 0, 0, M, H * vd, L, b.ckv, L, P + o.wuv, H * vd, b.v, H * vd))) return rc;
-  if ((rc = mm(p, s, 0, 0, M, H * hd, d, b.xn, d, P + o.wq, H * hd, b.qc, H * hd))) return rc;
-  if ((rc = rope_gemm(b.xn, P + o.wqr, b.qr))) return rc;
-  if ((rc = rope_gemm(b.xn, P + o.wkr, b.kr))) return rc;
-  if ((rc = concat_launch(MH, hd, r, b.qc, b.qr, b.q, s))) return rc;
-  if ((rc = concat_launch(MH, hd, r, b.kc, b.kr, b.k, s))) return rc;
-  AttnDesc a;
-  a.batch = c.batch;
-  a.seq = c.seq;
-  a.heads = H;
-  a.dk = td;
-  a.dv = vd;
-  a.scale = (float)(1.0 / std::sqrt((double)td));  // src/transformer.rs:542
-  a.causal = c.causal;
-  a.q = b.q;
-  a.ldq = (long long)H * td;
-  a.k = b.k;
-  a.ldk = (long long)H * td;
-  a.v = b.v;
-  a.ldv = (long long)H * vd;
-  a.o = b.o;
-  a.ldo = (long long)H * vd;
-  a.lse = b.lse;
-  if ((rc = attn_fwd_launch(a, s))) return rc;
-  if ((rc = mm(p, s, 0, 0, M, d, H * vd, b.o, H * vd, P + o.wo, d, out, d, 0.f, nullptr, x, d))) return rc;
+  if ((rc = rmsnorm_fwd_launch(M, d, c.eps, x, P + o.g, L.xn1, L.rstd1, s))) return rc;
+  if ((rc = mla_attn_forward(p, D, P, o.w, L.xn1, L, s))) return rc;
+  if ((rc = mm(p, s, 0, 0, M, d, ow, L.o, ow, P + o.w.wo, d, out, d, 0.f, nullptr, x, d))) return rc;
   // ---- backward
-  if ((rc = mm(p, s, 1, 0, H * vd, d, M, b.o, H * vd, gout, d, G + o.wo, d))) return rc;
-  if ((rc = mm(p, s, 0, 1, M, H * vd, d, gout, d, P + o.wo, d, b.g_o, H * vd))) return rc;
-  a.dout = b.g_o;
-  a.lddo = (long long)H * vd;
-  a.dq = b.dq;
-  a.lddq = (long long)H * td;
-  a.dk_out = b.dk;
-  a.lddk = (long long)H * td;
-  a.dv_out = b.dv;
-  a.lddv = (long long)H * vd;
-  a.rope_cos = p->rcos;
-  a.rope_sin = p->rsin;
-  a.rope_off = hd;  // the decoupled RoPE dims follow the content dims in each head
-  a.rope_dim = r;
-  if ((rc = attn_bwd_launch(a, p->attn_ws, s))) return rc;
-  if ((rc = split_launch(MH, hd, r, b.dq, b.dqc, b.dqr, false, s))) return rc;
-  if ((rc = split_launch(MH, hd, r, b.dk, b.dkc, b.dkr, false, s))) return rc;
-  // q / rope-k projections of xn
-  if ((rc = mm(p, s, 1, 0, d, H * hd, M, b.xn, d, b.dqc, H * hd, G + o.wq, H * hd))) return rc;
-  if ((rc = mm(p, s, 1, 0, d, H * r, M, b.xn, d, b.dqr, H * r, G + o.wqr, H * r))) return rc;
-  if ((rc = mm(p, s, 1, 0, d, H * r, M, b.xn, d, b.dkr, H * r, G + o.wkr, H * r))) return rc;
-  if ((rc = mm(p, s, 0, 1, M, d, H * hd, b.dqc, H * hd, P + o.wq, H * hd, b.dxn, d))) return rc;
-  if ((rc = mm(p, s, 0, 1, M, d, H * r, b.dqr, H * r, P + o.wqr, H * r, b.dxn, d, 1.f))) return rc;
-  if ((rc = mm(p, s, 0, 1, M, d, H * r, b.dkr, H * r, P + o.wkr, H * r, b.dxn, d, 1.f))) return rc;
-  // up projections of the latent
-  if ((rc = mm(p, s, 1, 0, L, H * hd, M, b.ckv, L, b.dkc, H * hd, G + o.wuk, H * hd))) return rc;
-  if ((rc = mm(p, s, 1, 0, L, H * vd, M, b.ckv, L, b.dv, H * vd, G + o.wuv, H * vd))) return rc;
-  if ((rc = mm(p, s, 0, 1, M, L, H * hd, b.dkc, H * hd, P + o.wuk, H * hd, b.dckv, L))) return rc;
-  if ((rc = mm(p, s, 0, 1, M, L, H * vd, b.dv, H * vd, P + o.wuv, H * vd, b.dckv, L, 1.f))) return rc;
-  // down projection
-  if ((rc = mm(p, s, 1, 0, d, L, M, b.xn, d, b.dckv, L, G + o.wdkv, L))) return rc;
-  if ((rc = mm(p, s, 0, 1, M, d, L, b.dckv, L, P + o.wdkv, L, b.dxn, d, 1.f))) return rc;
+  if ((rc = mm(p, s, 1, 0, ow, d, M, L.o, ow, gout, d, G + o.w.wo, d))) return rc;
+  if ((rc = mm(p, s, 0, 1, M, ow, d, gout, d, P + o.w.wo, d, p->g_o, ow))) return rc;
+  if ((rc = mla_attn_backward(p, D, P, G, o.w, L.xn1, L, p->g_o, p->g_xn, s))) return rc;
   // residual + rmsnorm
-  return rmsnorm_bwd_launch(M, d, x, P + o.g, b.rstd, b.dxn, 1.f, dx, 0.f, G + o.g, p->red_ws, s, gout);
+  return rmsnorm_bwd_launch(M, d, x, P + o.g, L.rstd1, p->g_xn, 1.f, dx, 0.f, G + o.g, p->red_ws, s, gout);
 }
 
 const talos_ppo_cfg* ppo_plan_cfg(talos_plan plan) {
@@ -828,7 +978,7 @@ int talos_block_plan_create(const talos_block_cfg* cfg, talos_plan* plan) {
   p->blk = *cfg;
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, 0) == hipSuccess) p->num_cu = prop.multiProcessorCount;
-  rc = alloc_block_buffers(p, *cfg, 1, true);
+  rc = alloc_block_buffers(p, *cfg, 1);
   if (rc == TALOS_OK) rc = alloc_workspaces(p);
   if (rc) {
     plan_free(p);
@@ -876,7 +1026,7 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
   if (hipGetDeviceProperties(&prop, 0) == hipSuccess) p->num_cu = prop.multiProcessorCount;
   const talos_block_cfg bc = block_cfg_of(*cfg);
   const size_t M = (size_t)cfg->batch * cfg->seq, d = cfg->d_model, B = cfg->batch, A = cfg->n_actions;
-  rc = alloc_block_buffers(p, bc, cfg->n_layers, false);
+  rc = alloc_block_buffers(p, bc, cfg->n_layers);
   rc |= plan_alloc(p, &p->h0, M * d);
   rc |= plan_alloc(p, &p->last, B * d);
   rc |= plan_alloc(p, &p->lastn, B * d);
@@ -890,9 +1040,10 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
   rc |= plan_alloc(p, &p->g_lastn, B * d);
   rc |= plan_alloc(p, &p->g_last, B * d);
   {  // the last layer's last-token rows
-    const size_t F = cfg->ffn_dim;
+    const size_t F = cfg->ffn_dim, ow = attn_width(bc);
     auto& R = p->lr;
-    for (float** b : {&R.x, &R.o, &R.h2, &R.xn2, &R.g_xn, &R.g_h2, &R.g_o}) rc |= plan_alloc(p, b, B * d);
+    for (float** b : {&R.x, &R.h2, &R.xn2, &R.g_xn, &R.g_h2}) rc |= plan_alloc(p, b, B * d);
+    for (float** b : {&R.o, &R.g_o}) rc |= plan_alloc(p, b, B * ow);
     for (float** b : {&R.u, &R.a, &R.g_u}) rc |= plan_alloc(p, b, B * F);
     rc |= plan_alloc(p, &R.rstd2, B);
     rc |= plan_alloc(p, &R.lse, B * cfg->n_heads);
@@ -1001,12 +1152,12 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
   rc = rmsnorm_bwd_launch(B, d, p->last, params + po.gf, p->rstdf, p->g_lastn, 0.f, p->g_last, 0.f, G + po.gf,
                           p->red_ws, s);
   if (rc) return rc;
-  // rows of a [B, d] last-token gradient into a full [M, d] one, zero elsewhere
-  auto scatter = [&](const float* src, float* dst) {
-    ProfScope ps_s(s, "scatter_last_kernel", 0.0, 4.0 * ((double)M * d + (double)B * d));
-    hipLaunchKernelGGL(scatter_last_kernel,
-                       dim3(ceil_div((size_t)M * d, 256) > 65536 ? 65536 : ceil_div((size_t)M * d, 256)), dim3(256), 0,
-                       s, B, c.seq, d, p->lens, src, dst);
+  // rows of a [B, w] last-token gradient into a full [M, w] one, zero elsewhere
+  auto scatter = [&](const float* src, float* dst, int w) {
+    ProfScope ps_s(s, "scatter_last_kernel", 0.0, 4.0 * ((double)M * w + (double)B * w));
+    const size_t blocks = ceil_div((size_t)M * w, 256);
+    hipLaunchKernelGGL(scatter_last_kernel, dim3(blocks > 65536 ? 65536 : blocks), dim3(256), 0, s, B, c.seq, w,
+                       p->lens, src, dst);
     return launch_status("scatter_last_kernel");
   };
   std::vector<BlockOff> offs;
@@ -1019,27 +1170,26 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
   float* gcur = p->g_out;
   float* gnext = p->g_x;
   if (c.n_layers == 0) {
-    rc = scatter(p->g_last, p->g_out);
+    rc = scatter(p->g_last, p->g_out, d);
     if (rc) return rc;
   } else {
-    // the last layer: MLP half on the last-token rows (the forward's p->lr), then its row
-    // gradients spread over the full token grid for the attention half
+    // the last layer: MLP half on the last-token rows (the forward's p->lr), then the attention
+    // half from the last rows' gradients
     const int l = c.n_layers - 1;
     auto& R = p->lr;
+    auto& L = p->layers[l];
     rc = block_mlp_backward(p, bc, params, G, offs[l], B, R.o, R.h2, R.xn2, R.rstd2, R.u, R.a, p->g_last, R.g_u,
                             R.g_xn, R.g_h2, R.g_o, s);
     if (rc) return rc;
-    AttnDesc ad = block_attn_desc(p, bc, p->layers[l]);
-    if (attn_lastq_supported(ad)) {
-      rc = attn_bwd_lastq_launch(ad, R.o, d, R.lse, R.g_o, d, s);
+    if (ppo_lastq(p, bc, L)) {
+      rc = attn_bwd_lastq_launch(block_attn_desc(p, bc, L), R.o, d, R.lse, R.g_o, d, s);
+      if (rc == TALOS_OK) rc = block_qkv_backward(p, bc, params, G, offs[l], L, nullptr, R.g_h2, p->g_out, s);
     } else {
-      ad.dout = p->g_o;
-      ad.lddo = d;
-      rc = scatter(R.g_o, p->g_o);
-      if (rc == TALOS_OK) rc = attn_bwd_launch(ad, p->attn_ws, s);
+      // the row gradients spread over the full token grid
+      const int ow = attn_width(bc);
+      rc = scatter(R.g_o, p->g_o, ow);
+      if (rc == TALOS_OK) rc = block_attn_backward(p, bc, params, G, offs[l], L, p->g_o, nullptr, R.g_h2, p->g_out, s);
     }
-    if (rc) return rc;
-    rc = block_qkv_backward(p, bc, params, G, offs[l], p->layers[l], nullptr, R.g_h2, p->g_out, s);
     if (rc) return rc;
   }
   for (int l = c.n_layers - 2; l >= 0; --l) {
@@ -1095,48 +1245,21 @@ int talos_mla_plan_create(const talos_mla_cfg* cfg, talos_plan* plan) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, 0) == hipSuccess) p->num_cu = prop.multiProcessorCount;
   const talos_mla_cfg& c = *cfg;
-  const size_t M = (size_t)c.batch * c.seq, d = c.d_model, H = c.n_heads, L = c.kv_latent, r = c.rope_dim,
-               hd = c.head_dim, vd = c.v_dim, td = hd + r;
-  auto& b = p->mb;
+  const MlaDims D = mla_dims(c);
+  const size_t M = (size_t)c.batch * c.seq, d = c.d_model, H = c.n_heads;
+  p->layers.resize(1);
+  auto& L = p->layers[0];
   rc = 0;
-  rc |= plan_alloc(p, &b.xn, M * d);
-  rc |= plan_alloc(p, &b.rstd, M);
-  rc |= plan_alloc(p, &b.ckv, M * L);
-  rc |= plan_alloc(p, &b.kc, M * H * hd);
-  rc |= plan_alloc(p, &b.v, M * H * vd);
-  rc |= plan_alloc(p, &b.qc, M * H * hd);
-  rc |= plan_alloc(p, &b.qr, M * H * r);
-  rc |= plan_alloc(p, &b.kr, M * H * r);
-  rc |= plan_alloc(p, &b.q, M * H * td);
-  rc |= plan_alloc(p, &b.k, M * H * td);
-  rc |= plan_alloc(p, &b.o, M * H * vd);
-  rc |= plan_alloc(p, &b.lse, M * H);
-  rc |= plan_alloc(p, &b.g_o, M * H * vd);
-  rc |= plan_alloc(p, &b.dq, M * H * td);
-  rc |= plan_alloc(p, &b.dk, M * H * td);
-  rc |= plan_alloc(p, &b.dv, M * H * vd);
-  rc |= plan_alloc(p, &b.dqc, M * H * hd);
-  rc |= plan_alloc(p, &b.dqr, M * H * r);
-  rc |= plan_alloc(p, &b.dkc, M * H * hd);
-  rc |= plan_alloc(p, &b.dkr, M * H * r);
-  rc |= plan_alloc(p, &b.dckv, M * L);
-  rc |= plan_alloc(p, &b.dxn, M * d);
+  rc |= plan_alloc(p, &L.xn1, M * d);
+  rc |= plan_alloc(p, &L.rstd1, M);
+  rc |= alloc_mla_layer(p, D, L);
+  rc |= plan_alloc(p, &p->g_o, M * H * c.v_dim);
+  rc |= plan_alloc(p, &p->g_xn, M * d);
   rc |= plan_alloc(p, &p->attn_ws, M * H);
-  std::vector<float> cs, sn;
-  rope_table_host(c.seq, c.rope_dim, (double)c.rope_base, cs, sn);
-  rc |= plan_alloc(p, &p->rcos, cs.size());
-  rc |= plan_alloc(p, &p->rsin, sn.size());
+  if (rc == TALOS_OK) rc = alloc_mla_scratch(p, D);
+  if (rc == TALOS_OK) rc = upload_rope_table(p, c.seq, c.rope_dim, c.rope_base);
   if (rc == TALOS_OK) {
-    rc = hip_status(hipMemcpy(p->rcos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
-    if (rc == TALOS_OK) rc = hip_status(hipMemcpy(p->rsin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
-  }
-  if (rc == TALOS_OK) {
-    const int Mi = (int)M;
-    for (auto rc2 : {std::make_pair((int)d, (int)(H * hd)), std::make_pair((int)d, (int)(H * r)),
-                     std::make_pair((int)L, (int)(H * hd)), std::make_pair((int)L, (int)(H * vd)),
-                     std::make_pair((int)d, (int)L), std::make_pair((int)(H * vd), (int)d)})
-      p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, wgrad_ws(p, Mi, rc2.first, rc2.second));
-    p->red_ws_bytes = std::max(p->red_ws_bytes, rmsnorm_bwd_workspace_bytes(Mi, (int)d));
+    p->red_ws_bytes = std::max(p->red_ws_bytes, rmsnorm_bwd_workspace_bytes((int)M, (int)d));
     rc = alloc_workspaces(p);
   }
   if (rc) {

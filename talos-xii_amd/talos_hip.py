@@ -36,13 +36,18 @@ class TalosError(RuntimeError):
 
 class BlockCfg(ctypes.Structure):
     _fields_ = [("batch", _i), ("seq", _i), ("d_model", _i), ("n_heads", _i), ("head_dim", _i), ("ffn_dim", _i),
-                ("causal", _i), ("activation", _i), ("eps", _f), ("rope_base", _f)]
+                ("causal", _i), ("activation", _i), ("eps", _f), ("rope_base", _f), ("attention", _i),
+                ("kv_latent", _i), ("rope_dim", _i), ("v_dim", _i)]
 
 
 class PpoCfg(ctypes.Structure):
     _fields_ = [("batch", _i), ("seq", _i), ("in_dim", _i), ("d_model", _i), ("n_layers", _i), ("n_heads", _i),
                 ("head_dim", _i), ("ffn_dim", _i), ("n_actions", _i), ("causal", _i), ("activation", _i),
-                ("eps", _f), ("rope_base", _f), ("clip_eps", _f), ("value_coef", _f), ("entropy_coef", _f)]
+                ("eps", _f), ("rope_base", _f), ("clip_eps", _f), ("value_coef", _f), ("entropy_coef", _f),
+                ("attention", _i), ("kv_latent", _i), ("rope_dim", _i), ("v_dim", _i)]
+
+
+ATTN_MHA, ATTN_MLA = 0, 1
 
 
 class PpoUpdateArgs(ctypes.Structure):

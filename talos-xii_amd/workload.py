@@ -9,6 +9,15 @@ import math
 import numpy as np
 
 
+ATTN_MHA, ATTN_MLA = 0, 1  # talos_attention
+
+# The reference's ActorCritic (ActorCritic::new, src/ppo.rs:254-258; LuckTransformer::new,
+# src/transformer.rs:48-69) as talos_ppo_cfg fields after batch and seq: in_dim, d_model,
+# n_layers, n_heads, head_dim, ffn_dim, n_actions, causal, activation (ReLU), eps, rope_base,
+# clip_eps, value_coef, entropy_coef, attention, kv_latent, rope_dim, v_dim.
+REFERENCE_ACTOR_CRITIC = (8, 64, 1, 4, 16, 128, 5, 0, 1, 1e-5, 10000.0, 0.2, 0.5, 0.01, ATTN_MLA, 32, 16, 16)
+
+
 def xavier(rng, fan_in, fan_out, shape=None):
     """Xavier-uniform U(-l, l), l = sqrt(6 / (fan_in + fan_out)) (the limit of Linear::new,
     src/nn.rs:20-23, drawn over the full range)."""
@@ -26,12 +35,29 @@ def block_params(rng, d, F, gain_jitter=False):
     return np.concatenate([p.ravel() for p in parts])
 
 
+def mla_block_params(rng, cfg, gain_jitter=False):
+    """Flat talos_block_cfg parameters of a TALOS_ATTN_MLA block (the order of
+    LuckTransformer::parameters, src/transformer.rs:205-215): g1 | W_dkv | W_uk | W_uv | W_q |
+    W_kr | W_qr | W_o | g2 | W1 | b1 | W2 | b2."""
+    d, F, H = cfg.d_model, cfg.ffn_dim, cfg.n_heads
+    L, r, hd, vd = cfg.kv_latent, cfg.rope_dim, cfg.head_dim, cfg.v_dim
+    gain = (lambda: rng.uniform(0.9, 1.1, d)) if gain_jitter else (lambda: np.ones(d))
+    parts = [gain()] + [xavier(rng, a, b) for a, b in ((d, L), (L, H * hd), (L, H * vd), (d, H * hd), (d, H * r),
+                                                          (d, H * r), (H * vd, d))]
+    parts += [gain(), xavier(rng, d, F), rng.normal(0, 0.02, F) if gain_jitter else np.zeros(F), xavier(rng, F, d),
+              rng.normal(0, 0.02, d) if gain_jitter else np.zeros(d)]
+    return np.concatenate([p.ravel() for p in parts])
+
+
 def ppo_params(rng, cfg, jitter=True):
     """Flat talos_ppo_cfg parameters (Xavier weights; gains / biases jittered when jitter)."""
     d, F, I, A = cfg.d_model, cfg.ffn_dim, cfg.in_dim, cfg.n_actions
     parts = [xavier(rng, I, d), rng.normal(0, 0.02, d) if jitter else np.zeros(d)]
     for _ in range(cfg.n_layers):
-        parts.append(block_params(rng, d, F, gain_jitter=jitter))
+        if getattr(cfg, "attention", 0) == ATTN_MLA:
+            parts.append(mla_block_params(rng, cfg, gain_jitter=jitter))
+        else:
+            parts.append(block_params(rng, d, F, gain_jitter=jitter))
     parts += [rng.uniform(0.9, 1.1, d) if jitter else np.ones(d), xavier(rng, d, d),
               rng.normal(0, 0.02, d) if jitter else np.zeros(d), xavier(rng, d, A),
               rng.normal(0, 0.02, A) if jitter else np.zeros(A), xavier(rng, d, 1),

@@ -88,6 +88,11 @@ def test_plan_config_errors(L):
     assert L.talos_block_fwd_bwd_f32(None, *([ctypes.c_void_p(16)] * 6), None) == th.ERR_HANDLE
     pc = th.PpoCfg(4, 8, 8, 32, 2, 4, 8, 64, 0, 1, 0, 1e-5, 1e4, 0.2, 0.5, 0.01)  # 0 actions
     assert L.talos_ppo_plan_create(ctypes.byref(pc), ctypes.byref(h)) == th.ERR_SHAPE
+    # latent attention: unknown kind, odd RoPE width, missing latent, too-wide heads
+    for bad, code in (((2, 0, 0, 0), th.ERR_DTYPE), ((1, 32, 5, 16), th.ERR_SHAPE), ((1, 0, 16, 16), th.ERR_SHAPE),
+                      ((1, 32, 116, 16), th.ERR_UNSUPPORTED)):
+        cfg = th.BlockCfg(2, 8, 64, 4, 16, 128, 0, 1, 1e-5, 1e4, *bad)
+        assert L.talos_block_plan_create(ctypes.byref(cfg), ctypes.byref(h)) == code, bad
 
 
 def test_param_counts_match_oracle(oracle):
@@ -99,6 +104,26 @@ def test_param_counts_match_oracle(oracle):
     n = th.lib().talos_ppo_param_count(ctypes.byref(pc))
     assert n == oracle.ppo_param_count(opc)
     assert n == common.ppo_params(np.random.default_rng(0), opc).size
+
+
+def test_reference_actor_critic_param_count(oracle):
+    """The reference ActorCritic's parameter count, summed from the shapes of ActorCritic::new
+    (src/ppo.rs:254-258) and LuckTransformer::new (src/transformer.rs:48-69): embed 8x64+64,
+    norm_1 64, MLA w_dkv 64x32, w_uk / w_uv 32x64, w_q 64x64, w_kr / w_qr 64x64, w_o 64x64, norm_2
+    64, ffn_1 64x128+128, ffn_2 128x64+64, norm_final 64, out_proj 64x64+64, actor 64x5+5, critic
+    64x1+1."""
+    import workload
+    want = (8 * 64 + 64) + 64 + (64 * 32 + 2 * 32 * 64 + 64 * 64 + 2 * 64 * 64 + 64 * 64) + 64 + (64 * 128 + 128) + \
+        (128 * 64 + 64) + 64 + (64 * 64 + 64) + (64 * 5 + 5) + (64 + 1)
+    pc = th.PpoCfg(16, 16, *workload.REFERENCE_ACTOR_CRITIC)
+    opc = oracle.PpoCfg(16, 16, *workload.REFERENCE_ACTOR_CRITIC)
+    assert th.lib().talos_ppo_param_count(ctypes.byref(pc)) == want
+    assert oracle.ppo_param_count(opc) == want
+    assert workload.ppo_params(np.random.default_rng(0), opc).size == want
+    bc = th.BlockCfg(16, 16, 64, 4, 16, 128, 0, 1, 1e-5, 1e4, th.ATTN_MLA, 32, 16, 16)
+    obc = oracle.BlockCfg(16, 16, 64, 4, 16, 128, 0, 1, 1e-5, 1e4, th.ATTN_MLA, 32, 16, 16)
+    nb = th.lib().talos_block_param_count(ctypes.byref(bc))
+    assert nb == oracle.block_param_count(obc) == workload.mla_block_params(np.random.default_rng(0), obc).size
 
 
 def test_no_device_is_a_clean_error(L):

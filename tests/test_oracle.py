@@ -16,6 +16,7 @@ import torch
 
 import torch_ref as tr
 from common import block_params, gacha_states, mla_params, ppo_params, xavier
+from workload import REFERENCE_ACTOR_CRITIC, mla_block_params
 
 # ---------------------------------------------------------------------------
 # 1. Reference known-answer tests
@@ -395,6 +396,51 @@ def test_mla_reference_config_shapes(oracle):
     d, L = 16, 8
     assert abs(dp[d:d + d * L].sum()) > 0.0
     assert out.shape == (1, 3, 16)
+
+
+def _mla_block_cfg(oracle, B, S, causal=0):
+    # the reference block's shape family (LuckTransformer::new, src/transformer.rs:48-69) at d 16
+    return oracle.BlockCfg(B, S, 16, 2, 4, 32, causal, 1, 1e-5, 10000.0, 1, 8, 4, 4)
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_mla_block_vs_torch(oracle, causal):
+    rng = np.random.default_rng(13)
+    cfg = _mla_block_cfg(oracle, 2, 5, causal)
+    p = mla_block_params(rng, cfg, gain_jitter=True)
+    assert p.size == oracle.block_param_count(cfg)
+    x, G = rng.normal(size=(2, 5, 16)), rng.normal(size=(2, 5, 16))
+    out, dp, dx = oracle.block_fwd_bwd(cfg, p, x, G)
+    pt, xt = tr.t64(p, True), tr.t64(x, True)
+    ot, n = tr.mla_ffn_block(xt, pt, cfg)
+    assert n == p.size
+    (ot * tr.t64(G)).sum().backward()
+    assert np.allclose(out, ot.detach().numpy(), atol=1e-12)
+    assert np.allclose(dp, pt.grad.numpy(), atol=1e-11)
+    assert np.allclose(dx, xt.grad.numpy(), atol=1e-11)
+
+
+def test_reference_actor_critic_vs_per_sample_and_torch(oracle):
+    # the reference's own ActorCritic shape (in 8, d 64, one MLA layer, 5 actions, no mask)
+    rng = np.random.default_rng(14)
+    B, S = 4, 6
+    cfg = oracle.PpoCfg(B, S, *REFERENCE_ACTOR_CRITIC)
+    p = ppo_params(rng, cfg)
+    assert p.size == oracle.ppo_param_count(cfg)
+    states, actions, adv, ret, old = _ppo_inputs(rng, cfg, p, oracle)
+    loss, logits, values, dp = oracle.ppo_fwd_bwd(cfg, p, states, actions, adv, ret, old)
+    loss2, dp2 = oracle.ppo_fwd_bwd_per_sample(cfg, p, states, actions, adv, ret, old, diff_last=True)
+    assert abs(loss - loss2) < 1e-12
+    assert np.allclose(dp, dp2, atol=1e-12)
+    pt = tr.t64(p, True)
+    lt_, vt_ = tr.policy(tr.t64(states), pt, cfg)
+    assert np.allclose(logits, lt_.detach().numpy(), atol=1e-12)
+    assert np.allclose(values, vt_.detach().numpy(), atol=1e-12)
+    lt = tr.ppo_loss(lt_, vt_, actions, tr.t64(old), tr.t64(adv), tr.t64(ret), cfg.clip_eps, cfg.value_coef,
+                     cfg.entropy_coef)
+    lt.backward()
+    assert abs(loss - lt.item()) < 1e-12
+    assert np.allclose(dp, pt.grad.numpy(), atol=1e-11)
 
 
 def test_linear_mse_closed_form(oracle):

@@ -96,6 +96,10 @@ def policy(states, p, cfg):
     We, be = take((I, d)), take((d,))
     h = states @ We + be
     for _ in range(cfg.n_layers):
+        if getattr(cfg, "attention", 0) == 1:
+            h, n = mla_ffn_block(h, p[o:], cfg)
+            o += n
+            continue
         P, n = split_block_params(p[o:], d, F)
         o += n
         h = block(h, P, cfg.n_heads, cfg.head_dim, cfg.eps, cfg.rope_base, bool(cfg.causal),
@@ -161,3 +165,28 @@ def _rope_heads(x, base):
     c, s = rope_angles(H, R, base)
     xc = torch.view_as_complex(x.reshape(B, S, H, R // 2, 2).contiguous())
     return torch.view_as_real(xc * torch.complex(c, s)[None, None]).reshape(x.shape)
+
+
+def mla_param_count(d, H, L, r, hd, vd):
+    return d + d * L + L * H * hd + L * H * vd + d * H * hd + 2 * d * H * r + H * vd * d
+
+
+def mla_ffn_block(x, p, cfg):
+    """A talos_block_cfg block with MLA attention: x + MLA(rmsnorm(x)) followed by the pre-norm
+    MLP, the wiring of LuckTransformer::forward (src/transformer.rs:71-90). Returns (out, number of
+    parameters consumed)."""
+    B, S, _ = x.shape
+    d, F, H = cfg.d_model, cfg.ffn_dim, cfg.n_heads
+    ci = [B, S, d, H, cfg.kv_latent, cfg.rope_dim, cfg.head_dim, cfg.v_dim, cfg.causal, 0]
+    o = mla_param_count(d, H, cfg.kv_latent, cfg.rope_dim, cfg.head_dim, cfg.v_dim)
+    h2 = mla_block(x, p[:o], ci, cfg.eps, cfg.rope_base)
+    sizes = [(d,), (d, F), (F,), (F, d), (d,)]
+    ws = []
+    for shp in sizes:
+        n = int(np.prod(shp))
+        ws.append(p[o:o + n].reshape(shp))
+        o += n
+    g2, w1, b1, w2, b2 = ws
+    u = rmsnorm(h2, g2, cfg.eps) @ w1 + b1
+    a = gelu(u) if cfg.activation == 0 else torch.relu(u)
+    return h2 + a @ w2 + b2, o
