@@ -35,7 +35,9 @@ enum talos_status {
   TALOS_ERR_HIP = 5,         /* HIP runtime error (message carries hipGetErrorString) */
   TALOS_ERR_ALLOC = 6,       /* device allocation failed */
   TALOS_ERR_HANDLE = 7,      /* invalid or freed handle */
-  TALOS_ERR_UNSUPPORTED = 8  /* configuration outside what the kernels cover (message says which limit) */
+  TALOS_ERR_UNSUPPORTED = 8, /* configuration outside what the kernels cover (message says which limit) */
+  TALOS_ERR_IO = 9,          /* a checkpoint file could not be opened, read or written */
+  TALOS_ERR_FORMAT = 10      /* malformed checkpoint contents (truncated, bad JSON, wrong value types) */
 };
 
 /* ------------------------------------------------------------------------- */
@@ -422,6 +424,35 @@ int talos_mla_fwd_bwd_f32(talos_plan plan, const float* params, const float* x, 
                           float* dparams, float* dx, talos_stream_t stream);
 
 int talos_plan_destroy(talos_plan plan);
+
+/* ------------------------------------------------------------------------- */
+/* Checkpoints of the reference's ActorCritic                                 */
+/* ------------------------------------------------------------------------- */
+/* The two files of save_ppo_model / load_ppo_model (main.rs:123-166): "<path>.bin" in bincode 1.3
+ * (its fixed-width little-endian encoding) and "<path>" in serde_json, both of ActorCritic
+ * {backbone: LuckTransformer, actor_head, critic_head} (ppo.rs:246-251; transformer.rs:35-45,
+ * 8-17, 374-398, 219-225; nn.rs:11-17, 144-149; Tensor as {data, shape}, autograd.rs:22-49).
+ * params are HOST fp32 arrays in the talos_ppo_cfg layout (talos_ppo_param_count floats): saving
+ * widens each value exactly to the file's f64, loading rounds each f64 to the nearest fp32. The
+ * configuration must be one the format holds: TALOS_ATTN_MLA, n_layers 1 and head_dim == v_dim (the
+ * reference's q/k content heads are v_head_dim wide, transformer.rs:410-425), else
+ * TALOS_ERR_UNSUPPORTED. Loading checks every shape, in/out width, RMSNorm eps and the RoPE base
+ * against cfg (TALOS_ERR_SHAPE on a mismatch) and leaves params unchanged on any failure. These
+ * functions run on the host only and need no GPU. */
+enum talos_checkpoint_format { TALOS_CKPT_BINCODE = 0, TALOS_CKPT_JSON = 1 };
+/* Serialises into buf (cap bytes) and sets *size to the checkpoint's length; buf == NULL only
+ * measures. max_seq_len is MLAConfig::max_seq_len, the length of the RoPE caches the file holds
+ * (0 selects 256, LuckTransformer::new's value, transformer.rs:48-56). Non-finite values are
+ * written as JSON null, as serde_json does (and its reader rejects them). */
+int talos_ppo_checkpoint_encode(const talos_ppo_cfg* cfg, const float* params, int max_seq_len, int format,
+                                uint8_t* buf, size_t cap, size_t* size);
+int talos_ppo_checkpoint_decode(const talos_ppo_cfg* cfg, const uint8_t* buf, size_t size, int format,
+                                float* params);
+/* save_ppo_model: writes "<path>.bin", then "<path>" (each through a temporary file and a rename).
+ * load_ppo_model: reads "<path>.bin", falling back to "<path>" when the binary is missing or does
+ * not decode; TALOS_ERR_IO when neither file opens. */
+int talos_ppo_checkpoint_save(const talos_ppo_cfg* cfg, const float* params, int max_seq_len, const char* path);
+int talos_ppo_checkpoint_load(const talos_ppo_cfg* cfg, const char* path, float* params);
 
 /* Per-launch profiling of a plan's entry points (the reference has only ad-hoc Instant timers
  * that print, src/dqn.rs:483-583 and src/autograd.rs:1877-1890). While enabled, every kernel the

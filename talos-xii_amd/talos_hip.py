@@ -14,7 +14,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtalos_hip.so")
 
 # status codes (enum talos_status)
-OK, ERR_SHAPE, ERR_NULL, ERR_DTYPE, ERR_NO_DEVICE, ERR_HIP, ERR_ALLOC, ERR_HANDLE, ERR_UNSUPPORTED = range(9)
+(OK, ERR_SHAPE, ERR_NULL, ERR_DTYPE, ERR_NO_DEVICE, ERR_HIP, ERR_ALLOC, ERR_HANDLE, ERR_UNSUPPORTED, ERR_IO,
+ ERR_FORMAT) = range(11)
+CKPT_BINCODE, CKPT_JSON = 0, 1  # enum talos_checkpoint_format
 # enum talos_unary_op / talos_binary_op / talos_activation
 RELU, LOG, EXP, SIN, COS, SQRT, NEG, SCALE, CLIP, GELU, COPY = range(11)
 ADD, SUB, MUL, DIV = range(4)
@@ -139,6 +141,10 @@ _SIGS = {
     "talos_mla_plan_create": [ctypes.POINTER(MlaCfg), ctypes.POINTER(_vp)],
     "talos_mla_fwd_bwd_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "talos_plan_destroy": [_vp],
+    "talos_ppo_checkpoint_encode": [ctypes.POINTER(PpoCfg), _vp, _i, _i, _vp, _sz, ctypes.POINTER(_sz)],
+    "talos_ppo_checkpoint_decode": [ctypes.POINTER(PpoCfg), _vp, _sz, _i, _vp],
+    "talos_ppo_checkpoint_save": [ctypes.POINTER(PpoCfg), _vp, _i, ctypes.c_char_p],
+    "talos_ppo_checkpoint_load": [ctypes.POINTER(PpoCfg), ctypes.c_char_p, _vp],
     "talos_plan_profiler": [_vp, ctypes.POINTER(_vp)],
     "talos_profiler_enable": [_vp, _i, ctypes.c_char_p],
     "talos_profiler_read": [_vp, _vp, _i, ctypes.POINTER(_i)],
@@ -191,6 +197,46 @@ def device_info():
     cu, clk, mem = _i(), _i(), _sz()
     call("talos_device_info", name, 256, ctypes.byref(cu), ctypes.byref(clk), ctypes.byref(mem))
     return {"name": name.value.decode(), "cu_count": cu.value, "clock_khz": clk.value, "total_mem": mem.value}
+
+
+def _host_params(cfg, params):
+    p = np.ascontiguousarray(params, dtype=np.float32)
+    n = lib().talos_ppo_param_count(ctypes.byref(cfg))
+    if p.size != n:
+        raise TalosError(ERR_SHAPE, f"{p.size} parameters, the configuration has {n}")
+    return p
+
+
+def checkpoint_encode(cfg, params, fmt=CKPT_BINCODE, max_seq_len=0):
+    """The reference's ActorCritic checkpoint bytes (bincode or JSON) of host fp32 params."""
+    p = _host_params(cfg, params)
+    size = _sz()
+    call("talos_ppo_checkpoint_encode", ctypes.byref(cfg), p.ctypes.data, max_seq_len, fmt, None, 0,
+         ctypes.byref(size))
+    buf = ctypes.create_string_buffer(size.value)
+    call("talos_ppo_checkpoint_encode", ctypes.byref(cfg), p.ctypes.data, max_seq_len, fmt, buf, size.value,
+         ctypes.byref(size))
+    return buf.raw[:size.value]
+
+
+def checkpoint_decode(cfg, data, fmt=CKPT_BINCODE):
+    """Host fp32 params from checkpoint bytes."""
+    out = np.zeros(lib().talos_ppo_param_count(ctypes.byref(cfg)), np.float32)
+    call("talos_ppo_checkpoint_decode", ctypes.byref(cfg), data, len(data), fmt, out.ctypes.data)
+    return out
+
+
+def save_ppo_model(cfg, params, path, max_seq_len=0):
+    """Writes "<path>.bin" and "<path>" as the reference's save_ppo_model does."""
+    p = _host_params(cfg, params)
+    call("talos_ppo_checkpoint_save", ctypes.byref(cfg), p.ctypes.data, max_seq_len, os.fsencode(path))
+
+
+def load_ppo_model(cfg, path):
+    """Host fp32 params from "<path>.bin", or from "<path>" as the reference's load_ppo_model does."""
+    out = np.zeros(lib().talos_ppo_param_count(ctypes.byref(cfg)), np.float32)
+    call("talos_ppo_checkpoint_load", ctypes.byref(cfg), os.fsencode(path), out.ctypes.data)
+    return out
 
 
 class DeviceArray:

@@ -178,3 +178,43 @@ def test_actor_critic_update_runs_and_moves_params(oracle):
     for name, sl in ac_slices(ocfg).items():
         assert np.any(p1[sl] != p0[sl]), name
     plan.destroy()
+
+
+def test_checkpoint_interop_with_the_device_path(oracle, tmp_path):
+    """A reference-format checkpoint of f64 weights (the JSON document a serde_json writer would
+    produce) loads into the plan, whose forward then matches the oracle run on the f64 weights;
+    parameters updated on the device save back exactly (the f64 in the file is the fp32 value)."""
+    import json
+    from test_checkpoint import _jsonable, _tree
+
+    rng = np.random.default_rng(700)
+    B, S = 6, 16
+    args = ac_args(B, S)
+    cfg, ocfg = th.PpoCfg(*args), oracle.PpoCfg(*args)
+    p64 = ppo_params(rng, ocfg)
+    path = str(tmp_path / "ppo.cache")
+    with open(path, "w") as f:
+        json.dump(_jsonable(_tree(cfg, p64)), f)
+    p = th.load_ppo_model(cfg, path)
+    assert np.array_equal(p, p64.astype(np.float32))
+    states, actions, adv, ret, old = ac_inputs(rng, ocfg, p64, oracle)
+    _, logits_r, values_r, _ = oracle.ppo_fwd_bwd(ocfg, p64, states, actions, adv, ret, old)
+    plan = th.Plan("ppo", cfg)
+    P, St = DA.from_numpy(p), DA.from_numpy(states)
+    lg, vl = DA.zeros((B, cfg.n_actions)), DA.zeros(B)
+    th.call("talos_ppo_forward_f32", plan.h, P.ptr, St.ptr, lg.ptr, vl.ptr, None)
+    check_close(lg.numpy(), logits_r, name="logits from a loaded checkpoint")
+    check_close(vl.numpy(), values_r, name="values from a loaded checkpoint")
+    # one Adam step on the device, then save: the file holds the device's fp32 values exactly
+    Ac = DA.from_numpy(actions, np.int32)
+    Ad, Re, Ol = DA.from_numpy(adv), DA.from_numpy(ret), DA.from_numpy(old)
+    g, m, v = DA.zeros(p.size), DA.zeros(p.size), DA.zeros(p.size)
+    th.call("talos_ppo_fwd_bwd_f32", plan.h, P.ptr, St.ptr, Ac.ptr, Ad.ptr, Re.ptr, Ol.ptr, None, g.ptr, None)
+    th.call("talos_adam_step_f32", p.size, P.ptr, g.ptr, m.ptr, v.ptr, 1, 3e-4, 0.9, 0.999, 1e-8, None, 0.0, None)
+    p1 = P.numpy()
+    assert not np.array_equal(p1, p)
+    th.save_ppo_model(cfg, p1, path)
+    doc = json.load(open(path))
+    assert doc["backbone"]["embed"]["weight"]["data"] == p1[:8 * 64].astype(np.float64).tolist()
+    assert th.load_ppo_model(cfg, path).tobytes() == p1.tobytes()
+    plan.destroy()
