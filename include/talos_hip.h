@@ -426,6 +426,39 @@ int talos_mla_fwd_bwd_f32(talos_plan plan, const float* params, const float* x, 
 int talos_plan_destroy(talos_plan plan);
 
 /* ------------------------------------------------------------------------- */
+/* Rollout inference with the KV cache                                        */
+/* ------------------------------------------------------------------------- */
+/* The policy's step on one new token per environment with a cache of earlier tokens
+ * (LuckTransformer::forward_inference_step, transformer.rs:157-196;
+ * MultiHeadLatentAttention::forward_inference_cached, transformer.rs:688-805), for n_envs
+ * environments at once, each with its own cache, followed by prune_kv_cache to context_len rows
+ * (transformer.rs:807-840; sim.rs:578 prunes after every step) and the action draw of
+ * ActorCritic::step_inference_cached (ppo.rs:391-433). A step attends over the rows cached plus
+ * the new token (at most context_len + 1), then keeps the newest context_len. RoPE rotates q / k at
+ * the environment's position; positions >= max_seq_len (the reference's RoPE cache length, 0 selects
+ * 256) are left unrotated as the reference's `continue` does (transformer.rs:718-721). The
+ * configuration is any talos_ppo_cfg architecture (batch and seq are ignored); the decoder owns
+ * the caches (n_envs * n_layers * n_heads * (context_len + 1) * (dk + dv) floats) and its
+ * activations, so a step allocates nothing. */
+typedef struct talos_decoder_s* talos_decoder;
+int talos_ppo_decoder_create(const talos_ppo_cfg* cfg, int n_envs, int context_len, int max_seq_len,
+                             talos_decoder* dec);
+/* One token for environments 0..n-1 (n <= n_envs), all device buffers: tokens [n, in_dim],
+ * positions [n] (start_pos of each token), reset [n] (optional: nonzero clears that environment's
+ * cache before the token, KVCache::clear for a new episode), uniforms [n] (the draws the reference
+ * takes from rand::random; required for actions / logp). Outputs, each optional: logits [n, A],
+ * values [n] (the critic on the same hidden state), actions [n] (int32), logp [n] (ln p of the
+ * action). The action is the first i with r < p_i after subtracting the earlier p_j, or 0 when none
+ * qualifies, as the reference's loop leaves it. */
+int talos_ppo_decoder_step_f32(talos_decoder dec, int n, const float* params, const float* tokens,
+                               const int32_t* positions, const uint8_t* reset, const float* uniforms, float* logits,
+                               float* values, int32_t* actions, float* logp, talos_stream_t stream);
+/* Host copy of one environment's cached rows of a layer, oldest first: k [len, n_heads, dk] and
+ * v [len, n_heads, dv] (either may be NULL); *len = rows held. Waits for the device. */
+int talos_ppo_decoder_read_cache(talos_decoder dec, int layer, int env, float* k, float* v, int* len);
+int talos_ppo_decoder_destroy(talos_decoder dec);
+
+/* ------------------------------------------------------------------------- */
 /* Checkpoints of the reference's ActorCritic                                 */
 /* ------------------------------------------------------------------------- */
 /* The two files of save_ppo_model / load_ppo_model (main.rs:123-166): "<path>.bin" in bincode 1.3

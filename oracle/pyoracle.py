@@ -103,6 +103,19 @@ def lib():
         L.orc_ppo_gae.argtypes = [ctypes.c_int64, _f64p, _f64p, ctypes.POINTER(ctypes.c_uint8), ctypes.c_double,
                                   ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double, _f64p, _f64p,
                                   _f64p]
+        L.orc_decoder_new.restype = ctypes.c_void_p
+        L.orc_decoder_new.argtypes = [ctypes.POINTER(PpoCfg), _f64p, ctypes.c_int64, ctypes.c_int64]
+        L.orc_decoder_free.restype = None
+        L.orc_decoder_free.argtypes = [ctypes.c_void_p]
+        L.orc_decoder_step.argtypes = [ctypes.c_void_p, ctypes.c_int64, _f64p, ctypes.c_int64, _f64p, _f64p, _f64p]
+        L.orc_decoder_prune.restype = None
+        L.orc_decoder_prune.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64]
+        L.orc_decoder_clear.restype = None
+        L.orc_decoder_clear.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+        L.orc_decoder_cache.restype = ctypes.c_int64
+        L.orc_decoder_cache.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, _f64p, _f64p]
+        L.orc_sample_action.restype = ctypes.c_int
+        L.orc_sample_action.argtypes = [_f64p, ctypes.c_int64, ctypes.c_double, _f64p]
         L.orc_threads.restype = ctypes.c_int
         L.orc_set_threads.argtypes = [ctypes.c_int]
         _lib = L
@@ -452,3 +465,51 @@ def ppo_gae(rewards, values, terminals, r_mean=0.0, r_var=1.0, r_clip=10.0, gamm
     lib().orc_ppo_gae(n, _p(r), _p(v), d.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), float(r_mean), float(r_var),
                       float(r_clip), float(gamma), float(lam), _p(a), _p(ret), _p(an))
     return a, ret, an
+
+
+class Decoder:
+    """Rollout inference with the KV cache in f64 (forward_inference_step and
+    forward_inference_cached, src/transformer.rs:157-196, 688-805; prune_kv_cache, :807-840),
+    one cache per environment and layer."""
+
+    def __init__(self, cfg, params, max_seq_len=256, n_envs=1):
+        self.cfg = cfg
+        self._p = _f64(params)
+        self.h = lib().orc_decoder_new(ctypes.byref(cfg), _p(self._p), int(max_seq_len), int(n_envs))
+
+    def step(self, env, token, start_pos):
+        """Returns (logits [A], value, hidden [d]) for one token of env at start_pos."""
+        token = _f64(token)
+        lg, v, hid = np.zeros(self.cfg.n_actions), ctypes.c_double(), np.zeros(self.cfg.d_model)
+        _check(lib().orc_decoder_step(self.h, int(env), _p(token), int(start_pos), _p(lg), ctypes.byref(v), _p(hid)))
+        return lg, v.value, hid
+
+    def prune(self, env, max_len):
+        lib().orc_decoder_prune(self.h, int(env), int(max_len))
+
+    def clear(self, env):
+        lib().orc_decoder_clear(self.h, int(env))
+
+    def cache(self, env, layer=0):
+        """(k [len, H, dk], v [len, H, dv]) of env's cache at layer, oldest row first."""
+        c = self.cfg
+        mla = c.attention == 1
+        dk, dv = c.head_dim + (c.rope_dim if mla else 0), (c.v_dim if mla else c.head_dim)
+        n = lib().orc_decoder_cache(self.h, int(env), int(layer), None, None)
+        k, v = np.zeros((n, c.n_heads, dk)), np.zeros((n, c.n_heads, dv))
+        lib().orc_decoder_cache(self.h, int(env), int(layer), _p(k), _p(v))
+        return k, v
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_decoder_free(self.h)
+            self.h = None
+
+
+def sample_action(logits, r):
+    """The action choice of ActorCritic::step_inference_cached (src/ppo.rs:401-432) for the
+    uniform draw r; returns (action, log-probability of the action)."""
+    logits = _f64(logits)
+    lp = ctypes.c_double()
+    a = lib().orc_sample_action(_p(logits), logits.size, float(r), ctypes.byref(lp))
+    return a, lp.value

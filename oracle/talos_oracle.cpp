@@ -1229,6 +1229,149 @@ static Tensor ppo_batched_loss(const talos_ppo_cfg& c, const Tensor& logits, con
   });
 }
 
+// ---------------------------------------------------------------------------
+// Rollout inference with the KV cache: LuckTransformer::forward_inference_step
+// (src/transformer.rs:157-196), MultiHeadLatentAttention::forward_inference_cached (:688-805),
+// prune_kv_cache (:807-840), KVCache (:400-426) and ActorCritic::step_inference_cached
+// (src/ppo.rs:391-433). Plain f64 vectors, no tape, one token per call, as the reference.
+// Extension: blocks with standard multi-head attention (q | k | v columns of Wqkv, RoPE over the
+// whole head) and several layers, one cache per layer, with the same rules.
+// ---------------------------------------------------------------------------
+// Linear::forward_inference (src/nn.rs:37-70): out = b, then out += x_i * W[i, :] for each
+// non-zero input in order.
+static Vec linear_inf(const double* x, size_t in, size_t out, const double* W, const double* b) {
+  Vec y(out, 0.0);
+  if (b) std::copy(b, b + out, y.begin());
+  for (size_t i = 0; i < in; ++i) {
+    if (x[i] == 0.0) continue;
+    add_scaled_row(y.data(), W + i * out, x[i], out);
+  }
+  return y;
+}
+// RMSNorm::forward_inference (src/nn.rs:159-180)
+static Vec rmsnorm_inf(const Vec& x, const double* w, double eps) {
+  double ss = 0.0;
+  for (double v : x) ss += v * v;
+  const double rms = std::sqrt(ss / (double)x.size() + eps);
+  Vec y(x.size());
+  for (size_t i = 0; i < x.size(); ++i) y[i] = (x[i] / rms) * w[i];
+  return y;
+}
+
+struct KvCache {
+  std::vector<Vec> k, v;  // per head: rows of dk / dv values appended in order
+};
+struct Decoder {
+  talos_ppo_cfg c{};
+  Vec p;
+  Rope rope;
+  std::vector<std::vector<KvCache>> cache;  // [env][layer]
+};
+
+// Rotation of the pairs (2i, 2i+1) of x[0 .. dim) at pos; positions whose table offset lies past
+// the cache are left unrotated, as the reference's `continue` does (src/transformer.rs:718-721).
+static void rope_inf(const Rope& R, double* x, size_t pos) {
+  const size_t half = R.dim / 2, off = pos * half;
+  if (off >= R.cosc.size()) return;
+  for (size_t i = 0; i < half; ++i) {
+    const double c = R.cosc[off + i], s = R.sinc[off + i];
+    const double a = x[2 * i], b = x[2 * i + 1];
+    x[2 * i] = a * c - b * s;
+    x[2 * i + 1] = a * s + b * c;
+  }
+}
+
+// One block on one token: h -> out, appending the token's keys / values to kv.
+static Vec block_step(const Decoder& D, const double* P, const Vec& h, KvCache& kv, size_t pos) {
+  const talos_ppo_cfg& c = D.c;
+  const size_t d = c.d_model, H = c.n_heads, F = c.ffn_dim;
+  const bool mla = c.attention == TALOS_ATTN_MLA;
+  const size_t hd = c.head_dim, r = mla ? c.rope_dim : 0, vd = mla ? c.v_dim : hd, td = hd + r;
+  size_t o = 0;
+  const double* g1 = P + o;
+  o += d;
+  Vec xn = rmsnorm_inf(h, g1, c.eps);
+  std::vector<Vec> q(H, Vec(td)), k(H, Vec(td)), v(H, Vec(vd));
+  const double* Wo;
+  if (mla) {
+    const size_t L = c.kv_latent;
+    const double *Wdkv = P + o, *Wuk = Wdkv + d * L, *Wuv = Wuk + L * H * hd, *Wq = Wuv + L * H * vd,
+                 *Wkr = Wq + d * H * hd, *Wqr = Wkr + d * H * r;
+    Wo = Wqr + d * H * r;
+    o = (size_t)(Wo - P) + H * vd * d;
+    Vec ckv = linear_inf(xn.data(), d, L, Wdkv, nullptr);
+    Vec kc = linear_inf(ckv.data(), L, H * hd, Wuk, nullptr);
+    Vec vc = linear_inf(ckv.data(), L, H * vd, Wuv, nullptr);
+    Vec krf = linear_inf(xn.data(), d, H * r, Wkr, nullptr);
+    Vec qc = linear_inf(xn.data(), d, H * hd, Wq, nullptr);
+    Vec qrf = linear_inf(xn.data(), d, H * r, Wqr, nullptr);
+    for (size_t hh = 0; hh < H; ++hh) {
+      rope_inf(D.rope, &krf[hh * r], pos);
+      rope_inf(D.rope, &qrf[hh * r], pos);
+      for (size_t i = 0; i < hd; ++i) {
+        q[hh][i] = qc[hh * hd + i];
+        k[hh][i] = kc[hh * hd + i];
+      }
+      for (size_t i = 0; i < r; ++i) {
+        q[hh][hd + i] = qrf[hh * r + i];
+        k[hh][hd + i] = krf[hh * r + i];
+      }
+      for (size_t i = 0; i < vd; ++i) v[hh][i] = vc[hh * vd + i];
+    }
+  } else {
+    const double* Wqkv = P + o;
+    Wo = Wqkv + 3 * d * d;
+    o += 3 * d * d + d * d;
+    Vec qkv = linear_inf(xn.data(), d, 3 * d, Wqkv, nullptr);
+    for (size_t hh = 0; hh < H; ++hh) {
+      for (size_t i = 0; i < hd; ++i) {
+        q[hh][i] = qkv[hh * hd + i];
+        k[hh][i] = qkv[d + hh * hd + i];
+        v[hh][i] = qkv[2 * d + hh * hd + i];
+      }
+      rope_inf(D.rope, q[hh].data(), pos);
+      rope_inf(D.rope, k[hh].data(), pos);
+    }
+  }
+  // append, then attend over every cached row (src/transformer.rs:764-805)
+  for (size_t hh = 0; hh < H; ++hh) {
+    kv.k[hh].insert(kv.k[hh].end(), k[hh].begin(), k[hh].end());
+    kv.v[hh].insert(kv.v[hh].end(), v[hh].begin(), v[hh].end());
+  }
+  const size_t n = kv.k[0].size() / td;
+  const double scale = 1.0 / std::sqrt((double)td);
+  Vec att(H * vd, 0.0);
+  for (size_t hh = 0; hh < H; ++hh) {
+    Vec sc(n);
+    for (size_t j = 0; j < n; ++j) sc[j] = dot_product(q[hh].data(), &kv.k[hh][j * td], td) * scale;
+    double mx = -INFINITY;
+    for (double x : sc) mx = std::max(mx, x);
+    double sum = 0.0;
+    for (double& x : sc) {
+      x = std::exp(x - mx);
+      sum += x;
+    }
+    for (double& x : sc) x *= 1.0 / sum;
+    for (size_t j = 0; j < n; ++j) {
+      if (std::fabs(sc[j]) < 1e-9) continue;
+      add_scaled_row(&att[hh * vd], &kv.v[hh][j * vd], sc[j], vd);
+    }
+  }
+  Vec ao = linear_inf(att.data(), H * vd, d, Wo, nullptr);
+  Vec h2(d);
+  for (size_t i = 0; i < d; ++i) h2[i] = h[i] + ao[i];
+  const double* g2 = P + o;
+  o += d;
+  Vec xn2 = rmsnorm_inf(h2, g2, c.eps);
+  const double *W1 = P + o, *b1 = W1 + d * F, *W2 = b1 + F, *b2 = W2 + F * d;
+  Vec f1 = linear_inf(xn2.data(), d, F, W1, b1);
+  for (double& x : f1) x = c.activation == TALOS_ACT_RELU ? (x < 0.0 ? 0.0 : x) : gelu_f(x);
+  Vec f2 = linear_inf(f1.data(), F, d, W2, b2);
+  Vec out(d);
+  for (size_t i = 0; i < d; ++i) out[i] = h2[i] + f2[i];
+  return out;
+}
+
 }  // namespace orc
 
 // ===========================================================================
@@ -1759,6 +1902,118 @@ void orc_ppo_gae(int64_t len, const double* rewards, const double* values, const
   for (int64_t t = 0; t < len; ++t) ss += (adv_raw[t] - mean) * (adv_raw[t] - mean);
   const double stdv = std::sqrt(ss / (double)len) + 1e-8;
   for (int64_t t = 0; t < len; ++t) adv_norm[t] = (adv_raw[t] - mean) / stdv;
+}
+
+// Rollout decoder (see the orc::Decoder comment): one cache per environment and layer.
+void* orc_decoder_new(const talos_ppo_cfg* c, const double* params, int64_t max_seq_len, int64_t n_envs) {
+  auto* D = new Decoder();
+  D->c = *c;
+  D->p.assign(params, params + orc_ppo_param_count(c));
+  const size_t rw = c->attention == TALOS_ATTN_MLA ? (size_t)c->rope_dim : (size_t)c->head_dim;
+  D->rope = rope_new(rw, (size_t)max_seq_len, c->rope_base);
+  D->cache.assign((size_t)n_envs, std::vector<KvCache>((size_t)c->n_layers));
+  for (auto& env : D->cache)
+    for (auto& kv : env) {
+      kv.k.assign((size_t)c->n_heads, Vec());
+      kv.v.assign((size_t)c->n_heads, Vec());
+    }
+  return D;
+}
+void orc_decoder_free(void* h) { delete static_cast<Decoder*>(h); }
+// One token of environment env at position start_pos: logits [A], value, hidden [d] (the
+// out_proj output the heads read).
+int orc_decoder_step(void* h, int64_t env, const double* token, int64_t start_pos, double* logits, double* value,
+                     double* hidden) {
+  GUARD({
+    auto* D = static_cast<Decoder*>(h);
+    const talos_ppo_cfg& c = D->c;
+    const size_t d = c.d_model, A = c.n_actions;
+    const double* P = D->p.data();
+    Vec x = linear_inf(token, (size_t)c.in_dim, d, P, P + c.in_dim * d);
+    size_t o = (size_t)c.in_dim * d + d;
+    talos_block_cfg bc = block_cfg_of(c);
+    const size_t blk = block_param_count(bc);
+    for (int l = 0; l < c.n_layers; ++l) {
+      x = block_step(*D, P + o, x, D->cache[(size_t)env][(size_t)l], (size_t)start_pos);
+      o += blk;
+    }
+    Vec hf = rmsnorm_inf(x, P + o, c.eps);
+    o += d;
+    Vec out = linear_inf(hf.data(), d, d, P + o, P + o + d * d);
+    o += d * d + d;
+    Vec lg = linear_inf(out.data(), d, A, P + o, P + o + d * A);
+    o += d * A + A;
+    Vec val = linear_inf(out.data(), d, 1, P + o, P + o + d);
+    if (logits) std::copy(lg.begin(), lg.end(), logits);
+    if (value) *value = val[0];
+    if (hidden) std::copy(out.begin(), out.end(), hidden);
+  })
+}
+// prune_kv_cache: keep the newest max_len rows of every layer (src/transformer.rs:807-840).
+void orc_decoder_prune(void* h, int64_t env, int64_t max_len) {
+  auto* D = static_cast<Decoder*>(h);
+  const bool mla = D->c.attention == TALOS_ATTN_MLA;
+  const size_t td = (size_t)D->c.head_dim + (mla ? (size_t)D->c.rope_dim : 0);
+  const size_t vd = mla ? (size_t)D->c.v_dim : (size_t)D->c.head_dim;
+  for (auto& kv : D->cache[(size_t)env]) {
+    const size_t cur = kv.k[0].size() / td;
+    if (cur <= (size_t)max_len) continue;
+    const size_t rm = cur - (size_t)max_len;
+    for (size_t hh = 0; hh < kv.k.size(); ++hh) {
+      kv.k[hh].erase(kv.k[hh].begin(), kv.k[hh].begin() + (std::ptrdiff_t)(rm * td));
+      kv.v[hh].erase(kv.v[hh].begin(), kv.v[hh].begin() + (std::ptrdiff_t)(rm * vd));
+    }
+  }
+}
+void orc_decoder_clear(void* h, int64_t env) {
+  for (auto& kv : static_cast<Decoder*>(h)->cache[(size_t)env])
+    for (size_t hh = 0; hh < kv.k.size(); ++hh) {
+      kv.k[hh].clear();
+      kv.v[hh].clear();
+    }
+}
+// Rows cached for (env, layer), oldest first: k [len, H, dk] and v [len, H, dv] when non-null.
+int64_t orc_decoder_cache(void* h, int64_t env, int64_t layer, double* k, double* v) {
+  auto* D = static_cast<Decoder*>(h);
+  const bool mla = D->c.attention == TALOS_ATTN_MLA;
+  const size_t H = (size_t)D->c.n_heads, td = (size_t)D->c.head_dim + (mla ? (size_t)D->c.rope_dim : 0);
+  const size_t vd = mla ? (size_t)D->c.v_dim : (size_t)D->c.head_dim;
+  const KvCache& kv = D->cache[(size_t)env][(size_t)layer];
+  const size_t n = kv.k[0].size() / td;
+  for (size_t j = 0; j < n; ++j)
+    for (size_t hh = 0; hh < H; ++hh) {
+      if (k) std::copy(&kv.k[hh][j * td], &kv.k[hh][j * td] + td, k + (j * H + hh) * td);
+      if (v) std::copy(&kv.v[hh][j * vd], &kv.v[hh][j * vd] + vd, v + (j * H + hh) * vd);
+    }
+  return (int64_t)n;
+}
+// The action choice of ActorCritic::step / step_inference_cached (src/ppo.rs:311-346, 401-432)
+// with the uniform draw r given: probabilities by max-subtracted exp (max starts at -1e9), then
+// the first i with r < p_i, subtracting p_i otherwise. When no i qualifies (r at or past the
+// rounded total) the index keeps its initial 0: the reference's `action_idx == ACTION_SPACE`
+// fallback can never fire. *logp = ln p[a].
+int orc_sample_action(const double* logits, int64_t A, double r, double* logp) {
+  double mx = -1e9;
+  for (int64_t i = 0; i < A; ++i)
+    if (logits[i] > mx) mx = logits[i];
+  Vec p((size_t)A);
+  double sum = 0.0;
+  for (int64_t i = 0; i < A; ++i) {
+    p[(size_t)i] = std::exp(logits[i] - mx);
+    sum += p[(size_t)i];
+  }
+  for (auto& x : p) x /= sum;
+  int64_t a = 0;
+  for (int64_t i = 0; i < A; ++i) {
+    if (r < p[(size_t)i]) {
+      a = i;
+      break;
+    }
+    r -= p[(size_t)i];
+  }
+  if (a == A) a = A - 1;  // unreachable, kept as the reference writes it
+  if (logp) *logp = std::log(p[(size_t)a]);
+  return (int)a;
 }
 
 }  // extern "C"

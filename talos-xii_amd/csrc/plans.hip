@@ -83,23 +83,14 @@ struct talos_plan_s {
 
 namespace talos {
 
-// Shape of one latent attention (a TALOS_ATTN_MLA block, or an MLA plan).
-struct MlaDims {
-  int batch, seq, d, H, L, r, hd, vd, causal;
-};
-static MlaDims mla_dims(const talos_block_cfg& c) {
+MlaDims mla_dims(const talos_block_cfg& c) {
   return MlaDims{c.batch, c.seq, c.d_model, c.n_heads, c.kv_latent, c.rope_dim, c.head_dim, c.v_dim, c.causal};
 }
-static MlaDims mla_dims(const talos_mla_cfg& c) {
+MlaDims mla_dims(const talos_mla_cfg& c) {
   return MlaDims{c.batch, c.seq, c.d_model, c.n_heads, c.kv_latent, c.rope_dim, c.head_dim, c.v_dim, c.causal};
 }
 
-// Offsets of the latent-attention weights W_dkv | W_uk | W_uv | W_q | W_kr | W_qr | W_o (the
-// order of MultiHeadLatentAttention::parameters, src/transformer.rs:466-476) from base.
-struct MlaW {
-  size_t wdkv, wuk, wuv, wq, wkr, wqr, wo, end;
-};
-static MlaW mla_weights(const MlaDims& D, size_t base) {
+MlaW mla_weights(const MlaDims& D, size_t base) {
   const size_t d = D.d, H = D.H, L = D.L, r = D.r, hd = D.hd, vd = D.vd;
   MlaW w;
   w.wdkv = base;
@@ -113,21 +104,14 @@ static MlaW mla_weights(const MlaDims& D, size_t base) {
   return w;
 }
 
-// Width of a block's attention output (the rows of Wo).
-static int attn_width(const talos_block_cfg& c) {
+int attn_width(const talos_block_cfg& c) {
   return c.attention == TALOS_ATTN_MLA ? c.n_heads * c.v_dim : c.d_model;
 }
-// Width of a block's RoPE table.
-static int rope_width(const talos_block_cfg& c) {
+int rope_width(const talos_block_cfg& c) {
   return c.attention == TALOS_ATTN_MLA ? c.rope_dim : c.head_dim;
 }
 
-// Offsets of one block's parameters inside a flat buffer.
-struct BlockOff {
-  size_t g1, wqkv, wo, g2, w1, b1, w2, b2, end;
-  MlaW mla;  // TALOS_ATTN_MLA: the attention weights (mla.wo == wo)
-};
-static BlockOff block_offsets(const talos_block_cfg& c, size_t base) {
+BlockOff block_offsets(const talos_block_cfg& c, size_t base) {
   const size_t d = c.d_model, F = c.ffn_dim;
   BlockOff o{};
   o.g1 = base;
@@ -148,9 +132,9 @@ static BlockOff block_offsets(const talos_block_cfg& c, size_t base) {
   return o;
 }
 
-static size_t block_params(const talos_block_cfg& c) { return block_offsets(c, 0).end; }
+size_t block_params(const talos_block_cfg& c) { return block_offsets(c, 0).end; }
 
-static talos_block_cfg block_cfg_of(const talos_ppo_cfg& p) {
+talos_block_cfg block_cfg_of(const talos_ppo_cfg& p) {
   talos_block_cfg c{};
   c.batch = p.batch;
   c.seq = p.seq;
@@ -169,10 +153,7 @@ static talos_block_cfg block_cfg_of(const talos_ppo_cfg& p) {
   return c;
 }
 
-struct PpoOff {
-  size_t we, be, blocks, gf, wout, bout, wa, ba, wc, bc, end;
-};
-static PpoOff ppo_offsets(const talos_ppo_cfg& c) {
+PpoOff ppo_offsets(const talos_ppo_cfg& c) {
   const size_t d = c.d_model;
   PpoOff o;
   o.we = 0;
@@ -191,7 +172,7 @@ static PpoOff ppo_offsets(const talos_ppo_cfg& c) {
 
 static size_t ppo_params(const talos_ppo_cfg& c) { return ppo_offsets(c).end; }
 
-static int check_block_cfg(const talos_block_cfg& c) {
+int check_block_cfg(const talos_block_cfg& c) {
   TALOS_REQUIRE(c.batch > 0 && c.seq > 0 && c.d_model > 0 && c.n_heads > 0 && c.head_dim > 0 && c.ffn_dim > 0,
                 TALOS_ERR_SHAPE, "block cfg: sizes must be positive");
   TALOS_REQUIRE(c.attention == TALOS_ATTN_MHA || c.attention == TALOS_ATTN_MLA, TALOS_ERR_DTYPE,
@@ -827,7 +808,7 @@ __global__ __launch_bounds__(64) void ppo_loss_final_kernel(int nblk, int B, con
   }
 }
 
-static int check_ppo_cfg(const talos_ppo_cfg& c) {
+int check_ppo_cfg(const talos_ppo_cfg& c) {
   TALOS_REQUIRE(c.in_dim > 0 && c.n_layers >= 0 && c.n_actions > 0, TALOS_ERR_SHAPE,
                 "ppo cfg: in_dim, n_actions must be positive and n_layers >= 0");
   TALOS_REQUIRE(c.n_actions <= 64, TALOS_ERR_UNSUPPORTED, "ppo cfg: n_actions %d > 64", c.n_actions);

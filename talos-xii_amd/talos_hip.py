@@ -141,6 +141,10 @@ _SIGS = {
     "talos_mla_plan_create": [ctypes.POINTER(MlaCfg), ctypes.POINTER(_vp)],
     "talos_mla_fwd_bwd_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "talos_plan_destroy": [_vp],
+    "talos_ppo_decoder_create": [ctypes.POINTER(PpoCfg), _i, _i, _i, ctypes.POINTER(_vp)],
+    "talos_ppo_decoder_step_f32": [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    "talos_ppo_decoder_read_cache": [_vp, _i, _i, _vp, _vp, ctypes.POINTER(_i)],
+    "talos_ppo_decoder_destroy": [_vp],
     "talos_ppo_checkpoint_encode": [ctypes.POINTER(PpoCfg), _vp, _i, _i, _vp, _sz, ctypes.POINTER(_sz)],
     "talos_ppo_checkpoint_decode": [ctypes.POINTER(PpoCfg), _vp, _sz, _i, _vp],
     "talos_ppo_checkpoint_save": [ctypes.POINTER(PpoCfg), _vp, _i, ctypes.c_char_p],
@@ -237,6 +241,39 @@ def load_ppo_model(cfg, path):
     out = np.zeros(lib().talos_ppo_param_count(ctypes.byref(cfg)), np.float32)
     call("talos_ppo_checkpoint_load", ctypes.byref(cfg), os.fsencode(path), out.ctypes.data)
     return out
+
+
+class Decoder:
+    """A rollout decoder (talos_ppo_decoder_*): KV caches for n_envs environments."""
+
+    def __init__(self, cfg, n_envs, context_len, max_seq_len=0):
+        self.cfg = cfg
+        self.h = _vp()
+        call("talos_ppo_decoder_create", ctypes.byref(cfg), n_envs, context_len, max_seq_len, ctypes.byref(self.h))
+
+    def step(self, n, params, tokens, positions, reset=None, uniforms=None, logits=None, values=None,
+             actions=None, logp=None, stream=None):
+        """All arguments are DeviceArray (or None)."""
+        ptr = lambda a: None if a is None else a.ptr  # noqa: E731
+        call("talos_ppo_decoder_step_f32", self.h, n, ptr(params), ptr(tokens), ptr(positions), ptr(reset),
+             ptr(uniforms), ptr(logits), ptr(values), ptr(actions), ptr(logp), stream)
+
+    def cache(self, layer, env):
+        """(k [len, H, dk], v [len, H, dv]) of env's cache at layer, oldest row first."""
+        c = self.cfg
+        mla = c.attention == ATTN_MLA
+        dk, dv = c.head_dim + (c.rope_dim if mla else 0), (c.v_dim if mla else c.head_dim)
+        n = _i()
+        call("talos_ppo_decoder_read_cache", self.h, layer, env, None, None, ctypes.byref(n))
+        k = np.zeros((n.value, c.n_heads, dk), np.float32)
+        v = np.zeros((n.value, c.n_heads, dv), np.float32)
+        call("talos_ppo_decoder_read_cache", self.h, layer, env, k.ctypes.data, v.ctypes.data, ctypes.byref(n))
+        return k, v
+
+    def destroy(self):
+        if self.h:
+            call("talos_ppo_decoder_destroy", self.h)
+            self.h = _vp()
 
 
 class DeviceArray:

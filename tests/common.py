@@ -43,3 +43,26 @@ def check_close(got, ref, rtol=FP32_RTOL, atol=FP32_ATOL, name="", scale_floor=0
 
 
 from workload import block_params, gacha_states, log_softmax, mla_params, ppo_params, xavier  # noqa: E402,F401
+
+
+def reference_init_actor_critic(oracle, seed=12345):
+    """The parameters ActorCritic::new(seed) builds (src/ppo.rs:254-258 with LuckTransformer::new,
+    src/transformer.rs:48-69, and MultiHeadLatentAttention::new, :400-460): every Linear weight is
+    Tensor::rand([in, out], -l, l, seed') with l = sqrt(6 / (in + out)) (src/nn.rs:20-35; the
+    generator is the oracle's bit-exact LCG, src/autograd.rs:114-124), biases zero, RMSNorm gains
+    one. Seeds: embed seed, MLA seed + 10 + {0..6}, ffn_1 seed + 20, ffn_2 seed + 30, out_proj
+    seed + 40, actor seed + 100, critic seed + 200. Layout: workload.REFERENCE_ACTOR_CRITIC."""
+    def lin(fin, fout, s, bias):
+        lim = math.sqrt(6.0 / (fin + fout))
+        w = oracle.lcg_rand(fin * fout, -lim, lim, s)
+        return [w] + ([np.zeros(fout)] if bias else [])
+
+    d, L, H, r, vd, F, A = 64, 32, 4, 16, 16, 128, 5
+    parts = lin(8, d, seed, True) + [np.ones(d)]
+    m = seed + 10
+    parts += lin(d, L, m, False) + lin(L, H * vd, m + 1, False) + lin(L, H * vd, m + 2, False)
+    parts += lin(d, H * vd, m + 3, False) + lin(d, H * r, m + 4, False) + lin(d, H * r, m + 5, False)
+    parts += lin(H * vd, d, m + 6, False)
+    parts += [np.ones(d)] + lin(d, F, seed + 20, True) + lin(F, d, seed + 30, True) + [np.ones(d)]
+    parts += lin(d, d, seed + 40, True) + lin(d, A, seed + 100, True) + lin(d, 1, seed + 200, True)
+    return np.concatenate(parts)

@@ -106,6 +106,20 @@ def test_param_counts_match_oracle(oracle):
     assert n == common.ppo_params(np.random.default_rng(0), opc).size
 
 
+def test_decoder_argument_errors_without_a_device(L):
+    import workload
+    cfg = th.PpoCfg(1, 16, *workload.REFERENCE_ACTOR_CRITIC)
+    h = ctypes.c_void_p()
+    for n_envs, ctx, code in ((0, 8, th.ERR_SHAPE), (4, 0, th.ERR_UNSUPPORTED), (4, 1024, th.ERR_UNSUPPORTED)):
+        assert L.talos_ppo_decoder_create(ctypes.byref(cfg), n_envs, ctx, 256, ctypes.byref(h)) == code
+    bad = th.PpoCfg(1, 16, *workload.REFERENCE_ACTOR_CRITIC)
+    bad.attention = 3
+    assert L.talos_ppo_decoder_create(ctypes.byref(bad), 4, 8, 256, ctypes.byref(h)) == th.ERR_DTYPE
+    p = ctypes.c_void_p(16)
+    assert L.talos_ppo_decoder_step_f32(None, 1, p, p, p, None, None, None, None, None, None, None) == th.ERR_HANDLE
+    assert L.talos_ppo_decoder_destroy(None) == th.OK
+
+
 def test_reference_actor_critic_param_count(oracle):
     """The reference ActorCritic's parameter count, summed from the shapes of ActorCritic::new
     (src/ppo.rs:254-258) and LuckTransformer::new (src/transformer.rs:48-69): embed 8x64+64,

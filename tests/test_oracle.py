@@ -8,6 +8,7 @@ transposed operand fails at least one of them:
   3. closed forms and invariants, and torch float64 autograd (an independent library)
      on the composite models.
 """
+import ctypes
 import math
 
 import numpy as np
@@ -15,7 +16,7 @@ import pytest
 import torch
 
 import torch_ref as tr
-from common import block_params, gacha_states, mla_params, ppo_params, xavier
+from common import block_params, gacha_states, mla_params, ppo_params, reference_init_actor_critic, xavier
 from workload import REFERENCE_ACTOR_CRITIC, mla_block_params
 
 # ---------------------------------------------------------------------------
@@ -441,6 +442,124 @@ def test_reference_actor_critic_vs_per_sample_and_torch(oracle):
     lt.backward()
     assert abs(loss - lt.item()) < 1e-12
     assert np.allclose(dp, pt.grad.numpy(), atol=1e-11)
+
+
+# ---------------------------------------------------------------------------
+# Rollout inference with the KV cache
+# ---------------------------------------------------------------------------
+def _ac_cfg(oracle, B, S, **over):
+    c = oracle.PpoCfg(B, S, *REFERENCE_ACTOR_CRITIC)
+    for k, v in over.items():
+        setattr(c, k, v)
+    return c
+
+
+def _full_last_logits(oracle, cfg, p, tokens):
+    """The full-graph forward of one sequence (positions 0..S-1): logits and value of its last token."""
+    S = tokens.shape[0]
+    c = type(cfg)()
+    ctypes.pointer(c)[0] = cfg
+    c.batch, c.seq = 1, S
+    _, lg, val, _ = oracle.ppo_fwd_bwd(c, p, tokens[None], np.zeros(1, np.int32), np.zeros(1), np.zeros(1),
+                                       np.zeros(1))
+    return lg[0], val[0]
+
+
+def test_decoder_reference_fast_slow_alignment(oracle):
+    """The reference's own check (src/sim.rs:1180-1216): ActorCritic::new(12345), six tokens
+    flat[t, i] = 0.01 t + 0.001 i; the full forward's probabilities and those of six cached steps
+    differ by less than 1e-6 in sum. With RoPE by sequence position (not the head index of the
+    training path) they agree to rounding."""
+    cfg = _ac_cfg(oracle, 1, 6)
+    p = reference_init_actor_critic(oracle, 12345)
+    assert p.size == oracle.ppo_param_count(cfg)
+    flat = np.array([[t * 0.01 + i * 0.001 for i in range(8)] for t in range(6)])
+    slow, _ = _full_last_logits(oracle, cfg, p, flat)
+    dec = oracle.Decoder(cfg, p, 256, 1)
+    for t in range(6):
+        fast, _, _ = dec.step(0, flat[t], t)
+
+    def sm(z):
+        e = np.exp(z - z.max())
+        return e / e.sum()
+
+    assert np.abs(sm(slow) - sm(fast)).sum() < 1e-6
+    assert np.allclose(fast, slow, rtol=1e-12, atol=1e-13)
+
+
+@pytest.mark.parametrize("attention,layers,causal", [(1, 1, 0), (0, 2, 1), (1, 2, 1)])
+def test_decoder_equals_full_forward_last_token(oracle, attention, layers, causal):
+    """Feeding a sequence one token at a time gives the full graph's last-token logits and value:
+    with one layer for any mask (the last query sees every key either way), with several layers
+    when the mask is causal (earlier tokens never see later ones)."""
+    rng = np.random.default_rng(15 + layers)
+    if attention == 1:
+        cfg = _ac_cfg(oracle, 1, 7, n_layers=layers, causal=causal)
+    else:
+        cfg = oracle.PpoCfg(1, 7, 8, 32, layers, 2, 16, 64, 3, causal, 0, 1e-5, 10000.0, 0.2, 0.5, 0.01)
+    p = ppo_params(rng, cfg)
+    toks = gacha_states(rng, 1, 7)[0]
+    lg_r, v_r = _full_last_logits(oracle, cfg, p, toks)
+    dec = oracle.Decoder(cfg, p, 64, 1)
+    for t in range(7):
+        lg, v, _ = dec.step(0, toks[t], t)
+    assert np.allclose(lg, lg_r, rtol=1e-11, atol=1e-12)
+    assert abs(v - v_r) < 1e-11 * (1 + abs(v_r))
+    k, vv = dec.cache(0, layers - 1)
+    assert k.shape == (7, cfg.n_heads, cfg.head_dim + (cfg.rope_dim if attention == 1 else 0))
+
+
+def test_decoder_prune_keeps_a_sliding_window(oracle):
+    """After prune_kv_cache to W rows, a step attends to the newest W + 1 tokens; RoPE scores
+    depend only on position differences, so the step equals the full forward of that window
+    re-based to positions 0..W."""
+    rng = np.random.default_rng(16)
+    cfg = _ac_cfg(oracle, 1, 16)
+    p = ppo_params(rng, cfg)
+    toks = gacha_states(rng, 1, 12)[0]
+    W, p0 = 4, 9
+    dec = oracle.Decoder(cfg, p, 256, 1)
+    for t in range(12):
+        lg, _, _ = dec.step(0, toks[t], p0 + t)
+        lo = max(0, t - W)
+        lg_r, _ = _full_last_logits(oracle, cfg, p, toks[lo:t + 1])
+        assert np.allclose(lg, lg_r, rtol=1e-9, atol=1e-11), t
+        dec.prune(0, W)
+        assert dec.cache(0)[0].shape[0] == min(t + 1, W)
+    dec.clear(0)
+    assert dec.cache(0)[0].shape[0] == 0
+
+
+def test_decoder_positions_past_the_rope_cache_are_not_rotated(oracle):
+    """forward_inference_cached skips the rotation when pos * rope_dim / 2 is past the cos cache
+    (src/transformer.rs:718-721): positions >= max_seq_len act as position 0 (the identity)."""
+    rng = np.random.default_rng(17)
+    cfg = _ac_cfg(oracle, 1, 8)
+    p = ppo_params(rng, cfg)
+    toks = gacha_states(rng, 1, 5)[0]
+    a, b, c = oracle.Decoder(cfg, p, 32, 1), oracle.Decoder(cfg, p, 32, 1), oracle.Decoder(cfg, p, 32, 1)
+    for t in range(5):
+        la, _, _ = a.step(0, toks[t], 32 + 7 * t)  # all past the 32-position cache
+        lb, _, _ = b.step(0, toks[t], 0)
+        lc, _, _ = c.step(0, toks[t], t)
+    assert np.array_equal(la, lb)
+    assert not np.allclose(la, lc)  # while in range the rotation matters
+
+
+def test_sample_action_rule(oracle):
+    z = np.array([0.3, -1.0, 2.0, 0.0, 0.5])
+    e = np.exp(z - z.max())
+    pr = e / e.sum()
+    edges = np.cumsum(pr)
+    for a in range(5):
+        lo = 0.0 if a == 0 else edges[a - 1]
+        for r in (lo + 1e-6, (lo + edges[a]) / 2, edges[a] - 1e-6):
+            got, lp = oracle.sample_action(z, r)
+            assert got == a, (a, r)
+            assert abs(lp - math.log(pr[a])) < 1e-14
+    # no bucket (a draw at or past the rounded total): the index keeps its initial 0, since the
+    # reference's `action_idx == ACTION_SPACE` fallback never fires (src/ppo.rs:336-346)
+    assert oracle.sample_action(z, 1.5)[0] == 0
 
 
 def test_linear_mse_closed_form(oracle):
