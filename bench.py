@@ -155,6 +155,97 @@ def optimizer_line(P, dP, steps):
     return res
 
 
+def reference_model_line(steps, batch=4096, seq=16):
+    """PPO minibatch fwd+bwd of the reference's own ActorCritic (one MLA layer, d 64, ReLU 2x,
+    5 actions, no mask) at the trainer's context length 16: the model the reference trains,
+    beside the C4 restatement the headline metric is quoted on."""
+    cfg_t = (batch, seq, *wl.REFERENCE_ACTOR_CRITIC)
+    cfg, p, states, actions, adv, ret = make_inputs(cfg_t, seed=3)
+    plan = th.Plan("ppo", cfg)
+    P, St = th.DeviceArray.from_numpy(p), th.DeviceArray.from_numpy(states)
+    Ac = th.DeviceArray.from_numpy(actions, np.int32)
+    Ad, Re = th.DeviceArray.from_numpy(adv), th.DeviceArray.from_numpy(ret)
+    Ol = th.DeviceArray.from_numpy(np.full(batch, -1.6, np.float32))
+    loss, dP = th.DeviceArray.zeros(1), th.DeviceArray.zeros(p.size)
+
+    def step():
+        th.call("talos_ppo_fwd_bwd_f32", plan.h, P.ptr, St.ptr, Ac.ptr, Ad.ptr, Re.ptr, Ol.ptr, loss.ptr, dP.ptr, None)
+
+    for _ in range(3):
+        step()
+    th.sync()
+    timer = th.Timer(None)
+    timer.start()
+    for _ in range(steps):
+        step()
+    ms = timer.stop_ms() / steps
+    plan.destroy()
+    for a in (P, St, Ac, Ad, Re, Ol, loss, dP):
+        a.free()
+    return {"workload": f"reference ActorCritic minibatch fwd+bwd, {batch} samples x seq {seq}",
+            "samples_per_s": round(batch / (ms * 1e-3), 1), "ms_per_step": round(ms, 4), "params": int(p.size)}
+
+
+def rollout_line(steps, n_envs=4096, context_len=16, cpu=True):
+    """Rollout inference with the KV cache on the reference's own ActorCritic (one MLA layer,
+    d 64; ActorCritic::new, src/ppo.rs:254-258): one token for each of n_envs environments per
+    step, the cache window of ppo_context_len 16 (data/config.json:53-54), actions drawn
+    (step_inference_cached, src/ppo.rs:391-433). The caches are filled to the window before the
+    timed steps. The CPU baseline is the oracle's f64 restatement of forward_inference_step on
+    one thread for a bounded number of environment-steps (the reference decodes each simulation
+    on its own thread)."""
+    cfg_t = (1, context_len, *wl.REFERENCE_ACTOR_CRITIC)
+    cfg = th.PpoCfg(*cfg_t)
+    rng = np.random.default_rng(5)
+    p = wl.ppo_params(rng, cfg).astype(np.float32)
+    dec = th.Decoder(cfg, n_envs, context_len, 256)
+    P = th.DeviceArray.from_numpy(p)
+    toks = th.DeviceArray.from_numpy(wl.gacha_states(rng, n_envs, 1)[:, 0].astype(np.float32))
+    u = th.DeviceArray.from_numpy(rng.random(n_envs).astype(np.float32))
+    lg = th.DeviceArray.zeros((n_envs, cfg.n_actions))
+    vl, lp = th.DeviceArray.zeros(n_envs), th.DeviceArray.zeros(n_envs)
+    act = th.DeviceArray.zeros(n_envs, np.int32)
+    pos = [th.DeviceArray.from_numpy(np.full(n_envs, t, np.int32), np.int32) for t in range(context_len + steps)]
+
+    def one(t):
+        dec.step(n_envs, P, toks, pos[t], None, u, lg, vl, act, lp)
+
+    for t in range(context_len):
+        one(t)
+    th.sync()
+    timer = th.Timer(None)
+    timer.start()
+    for t in range(context_len, context_len + steps):
+        one(t)
+    ms = timer.stop_ms() / steps
+    res = {"workload": f"reference ActorCritic (1 MLA layer, d 64), {n_envs} environments x 1 token per step, "
+                       f"cache window {context_len}, caches full; logits, value, action and log-prob per token",
+           "tokens_per_s": round(n_envs / (ms * 1e-3), 1), "us_per_step": round(ms * 1e3, 2)}
+    if cpu:
+        import pyoracle
+        if not os.path.exists(pyoracle.LIB_PATH):
+            pyoracle.build()
+        ocfg = pyoracle.PpoCfg(*cfg_t)
+        od = pyoracle.Decoder(ocfg, p.astype(np.float64), 256, 1)
+        x = wl.gacha_states(rng, 1, 1)[0, 0]
+        for t in range(context_len):
+            od.step(0, x, t)
+            od.prune(0, context_len)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 2.0:
+            od.step(0, x, context_len + n)
+            od.prune(0, context_len)
+            n += 1
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(n / dt, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+                               "sample": f"{n} environment-steps of the f64 restatement of forward_inference_step "
+                                         f"+ prune_kv_cache, window {context_len}, one thread"}
+    for a in [P, toks, u, lg, vl, lp, act] + pos:
+        a.free()
+    dec.destroy()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -258,6 +349,8 @@ def main():
         "device": info["name"],
     }
     out["optimizer"] = optimizer_line(P, dP, args.steps)
+    out["reference_model"] = reference_model_line(args.steps)
+    out["rollout"] = rollout_line(args.steps, cpu=rank == 0 and not args.no_cpu_baseline)
     if args.profile_table:
         for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3]):
             print(f"{k:40s} n={v[0]:3d} {v[3]:8.3f} ms  {v[1] / max(v[3], 1e-9) / 1e9:8.2f} TFLOP/s "
