@@ -54,6 +54,10 @@ struct AttnArgs {
   int rope_off, rope_dim;
   int vec;  // every row half is 16-byte aligned and the head dims equal the template dims
   const int32_t* lens;  // per-batch key count (nullptr: all S keys)
+  const float* q_last;  // last-query kernels: unrotated query rows [B, H*dk] (nullptr: q's rows)
+  long long ldq_last;
+  float* dq_last;       // last-query backward: the query gradient rows [B, H*dk] (nullptr: dq)
+  long long lddq_last;
 };
 
 // Keys of batch entry b that take part: lens[b] clamped to [0, S] (rows past it are padding).
@@ -616,6 +620,7 @@ static AttnArgs make_args(const AttnDesc& d, int dkm, int dvm) {
   a.dq = d.dq; a.lddq = d.lddq; a.dk_out = d.dk_out; a.lddk = d.lddk; a.dv_out = d.dv_out; a.lddv = d.lddv;
   a.rcos = d.rope_cos; a.rsin = d.rope_sin; a.rope_off = d.rope_off; a.rope_dim = d.rope_dim;
   a.lens = d.lens;
+  a.q_last = d.q_last; a.ldq_last = d.ldq_last; a.dq_last = d.dq_last; a.lddq_last = d.lddq_last;
   // row halves start at (token * ld + head * dim + half * dim/2): 16-byte aligned when all of
   // ld, dim and dim/2 are multiples of 4 and the bases are aligned
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -758,6 +763,31 @@ __device__ __forceinline__ float4 rope_t4(float4 g, int e0, int pos, const AttnA
   return make_float4(r[0], r[1], r[2], r[3]);
 }
 
+// R at position pos on the two interleaved pairs of elements e0 .. e0 + 3 (e0 even):
+// (x0, x1) -> (x0 c - x1 s, x0 s + x1 c), the rotation of src/transformer.rs:276-292
+__device__ __forceinline__ float4 rope4(float4 x, int e0, int pos, const AttnArgs& a) {
+  if (a.rcos == nullptr) return x;
+  const int half = a.rope_dim >> 1;
+  float r[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int i = 0; i < 4; i += 2) {
+    const int e = e0 + i;
+    if (e >= a.rope_off && e < a.rope_off + a.rope_dim) {
+      const int idx = pos * half + ((e - a.rope_off) >> 1);
+      const float c = a.rcos[idx], sn = a.rsin[idx];
+      const float x0 = r[i], x1 = r[i + 1];
+      r[i] = fmaf(x0, c, -x1 * sn);
+      r[i + 1] = fmaf(x0, sn, x1 * c);
+    }
+  }
+  return make_float4(r[0], r[1], r[2], r[3]);
+}
+// The last query of batch entry b (row t), rotated: from q's row, or from q_last's row b.
+__device__ __forceinline__ float4 last_query(const AttnArgs& a, int b, long long tok0, int t, int hh, int D, int c) {
+  if (a.q_last) return rope4(ld4(a.q_last + (long long)b * a.ldq_last + hh * D + 4 * c), 4 * c, t, a);
+  return ld4(a.q + (tok0 + t) * a.ldq + hh * D + 4 * c);
+}
+
 // o_last[b, h] = softmax(scale q_t . K^T) V over keys j < L (t = L - 1); lse_last[b*H + h].
 template <int D>
 __global__ __launch_bounds__(256) void attn_fwd_lastq_kernel(AttnArgs a, float* __restrict__ o_last, long long ldol,
@@ -772,7 +802,7 @@ __global__ __launch_bounds__(256) void attn_fwd_lastq_kernel(AttnArgs a, float* 
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   float m = kNegInf, l = 0.f;
   if (Sk > 0) {
-    float4 q = ld4(a.q + (tok0 + t) * a.ldq + hh * D + 4 * c);
+    float4 q = last_query(a, b, tok0, t, hh, D, c);
     q = make_float4(q.x * a.scale, q.y * a.scale, q.z * a.scale, q.w * a.scale);
     for (int j0 = 0; j0 < Sk; j0 += RPP) {
       const int j = j0 + r;
@@ -815,7 +845,7 @@ __global__ __launch_bounds__(256) void attn_bwd_lastq_kernel(AttnArgs a, const f
   float4 qs = z4, g = z4;
   float Dd = 0.f, lse = 0.f;
   if (Sk > 0) {
-    const float4 q = ld4(a.q + (tok0 + t) * a.ldq + hh * D + 4 * c);
+    const float4 q = last_query(a, b, tok0, t, hh, D, c);
     qs = make_float4(q.x * a.scale, q.y * a.scale, q.z * a.scale, q.w * a.scale);
     g = ld4(do_last + (long long)b * lddol + hh * D + 4 * c);
     Dd = row_sum<C>(dot4(g, ld4(o_last + (long long)b * ldol + hh * D + 4 * c)));
@@ -838,17 +868,22 @@ __global__ __launch_bounds__(256) void attn_bwd_lastq_kernel(AttnArgs a, const f
       st4(a.dv_out + row * a.lddv + hh * D + 4 * c, make_float4(p * g.x, p * g.y, p * g.z, p * g.w));
       st4(a.dk_out + row * a.lddk + hh * D + 4 * c,
           rope_t4(make_float4(dS * qs.x, dS * qs.y, dS * qs.z, dS * qs.w), 4 * c, j, a));
-      if (j != t || Sk == 0) st4(a.dq + row * a.lddq + hh * D + 4 * c, z4);
+      if (a.dq_last == nullptr && (j != t || Sk == 0)) st4(a.dq + row * a.lddq + hh * D + 4 * c, z4);
     }
   }
   dq = make_float4(col_sum<C>(dq.x) * a.scale, col_sum<C>(dq.y) * a.scale, col_sum<C>(dq.z) * a.scale,
                    col_sum<C>(dq.w) * a.scale);
-  if (r == 0 && Sk > 0) st4(a.dq + (tok0 + t) * a.lddq + hh * D + 4 * c, rope_t4(dq, 4 * c, t, a));
+  if (a.dq_last) {
+    if (r == 0) st4(a.dq_last + (long long)b * a.lddq_last + hh * D + 4 * c, Sk > 0 ? rope_t4(dq, 4 * c, t, a) : z4);
+  } else if (r == 0 && Sk > 0) {
+    st4(a.dq + (tok0 + t) * a.lddq + hh * D + 4 * c, rope_t4(dq, 4 * c, t, a));
+  }
 }
 
 int attn_lastq_supported(const AttnDesc& d) {
   auto al = [](const void* p, long long ld) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && ld % 4 == 0; };
-  return (d.dk == d.dv && (d.dk == 32 || d.dk == 64) && al(d.q, d.ldq) && al(d.k, d.ldk) && al(d.v, d.ldv))
+  return (d.dk == d.dv && (d.dk == 32 || d.dk == 64) && al(d.q, d.ldq) && al(d.k, d.ldk) && al(d.v, d.ldv) &&
+          (d.q_last == nullptr || al(d.q_last, d.ldq_last)) && (d.dq_last == nullptr || al(d.dq_last, d.lddq_last)))
              ? 1
              : 0;
 }

@@ -36,6 +36,13 @@ struct AttnDesc {
   // optional per-batch key counts: keys >= lens[b] (clamped to [0, seq]) are masked for every
   // query of batch entry b, so right-padded sequences attend only to their own tokens
   const int32_t* lens = nullptr;
+  // last-query kernels only: the query of batch entry b is row b of q_last ([batch, heads * dk],
+  // not yet rotated: the kernels apply RoPE at the last row's position), and the backward writes
+  // the query gradient to row b of dq_last instead of every row of dq
+  const float* q_last = nullptr;
+  long long ldq_last = 0;
+  float* dq_last = nullptr;
+  long long lddq_last = 0;
 };
 
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s);

@@ -623,6 +623,199 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
   }
 }
 
+// ---------------------------------------------------------------------------
+// Small problems: 64x64 tiles. A product with fewer 128x128 tiles than half the CUs (the
+// per-sample rows of the policy's last layer and heads, B = 4096 rows) would keep most of the
+// chip idle while each workgroup walks K alone; a 64x64 tile gives four times the workgroups and
+// a quarter of the serial MFMA chain each. Same 256 threads, one 32x32 accumulator per wave,
+// the same panel layouts (k-contiguous pitch 36, k-major pitch 72) and the same epilogue code.
+// ---------------------------------------------------------------------------
+constexpr int SBM = 64, SBN = 64;
+// k-major panel X[k][r] of 64 rows: rows k and k + 4 read by the two half-waves sit 4 * 72 = 32
+// mod 64 banks apart
+constexpr int S_LDS = 72;
+constexpr int S_PANEL = (BK * S_LDS > SBM * KP) ? BK * S_LDS : SBM * KP;
+constexpr int S_TS = 72;  // staged output tile pitch (the half-wave rows 4 apart: 32 banks apart)
+constexpr int S_SMEM = (2 * S_PANEL > SBM * S_TS) ? 2 * S_PANEL : SBM * S_TS;
+
+// op(X) panel [64 rows x 32 k] of chunk k0 into registers. KC: X[r][k] (k contiguous), thread t
+// takes row t%64, k = 4*(t/64 + 4i); otherwise X[k][r] (r contiguous), thread t takes
+// r = 4*(t%16), k = t/16 + 16i.
+template <bool KC, bool CHECK>
+__device__ __forceinline__ void s_load(const float* __restrict__ X, long long ld, int r0, int rlim, int k0, int kend,
+                                       bool vec, float4 (&o)[2]) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    int r, k;
+    if (KC) {
+      r = r0 + (t & 63);
+      k = k0 + 4 * ((t >> 6) + 4 * i);
+    } else {
+      r = r0 + 4 * (t & 15);
+      k = k0 + (t >> 4) + 16 * i;
+    }
+    const float* src = KC ? X + (long long)r * ld + k : X + (long long)k * ld + r;
+    const bool ok = KC ? (r < rlim && k + 3 < kend) : (k < kend && r + 3 < rlim);
+    if (!CHECK || (vec && ok)) {
+      o[i] = *reinterpret_cast<const float4*>(src);
+    } else {
+      float v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool in = KC ? (r < rlim && k + j < kend) : (k < kend && r + j < rlim);
+        v[j] = in ? src[j] : 0.f;
+      }
+      o[i] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  }
+}
+template <bool KC>
+__device__ __forceinline__ void s_store(float* X, const float4 (&o)[2]) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (KC)
+      *reinterpret_cast<float4*>(X + (t & 63) * KP + 4 * ((t >> 6) + 4 * i)) = o[i];
+    else
+      *reinterpret_cast<float4*>(X + ((t >> 4) + 16 * i) * S_LDS + 4 * (t & 15)) = o[i];
+  }
+}
+// MFMA operand values of row r at k = k0 .. k0 + 3.
+template <bool KC>
+__device__ __forceinline__ void s_frag(const float* X, int r, int k0, float (&f)[4]) {
+  if (KC) {
+    const float4 v = *reinterpret_cast<const float4*>(X + r * KP + k0);
+    f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) f[q] = X[(k0 + q) * S_LDS + r];
+  }
+}
+
+template <bool TA, bool TB, int E>
+__global__ __launch_bounds__(NT) void gemm_small_kernel(GemmArgs p) {
+  __shared__ __align__(16) float smem[S_SMEM];
+  float* const As = smem;
+  float* const Bs = smem + S_PANEL;
+  const int tiles_n = (p.N + SBN - 1) / SBN;
+  const int tiles = tiles_n * ((p.M + SBM - 1) / SBM);
+  // XCD-aware order, as in gemm_f32_kernel
+  const int per_xcd = (int)(gridDim.x >> 3);
+  const int logical = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  if (logical >= p.nblocks) return;
+  const int tile = logical % tiles;
+  const int m0 = (tile / tiles_n) * SBM;
+  const int n0 = (tile % tiles_n) * SBN;
+  const int bz = logical / tiles;
+  const int b = bz / p.ksplit, split = bz % p.ksplit;
+  const float* A = p.A + (long long)b * p.sA;
+  const float* B = p.B + (long long)b * p.sB;
+  const int kbeg = split * p.kper;
+  const int kend = min(p.K, kbeg + p.kper);
+  const bool interior = p.vecA && p.vecB && m0 + SBM <= p.M && n0 + SBN <= p.N;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  const int l32 = lane & 31, h = lane >> 5;
+  floatx16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  float csum = 0.f;  // E_DBIAS: column t%64 of op(B) over rows 8*(t/64) .. +8 of each panel
+  float4 ra[2], rb[2];
+  auto load = [&](int k0) {
+    if (interior && k0 + BK <= kend) {
+      s_load<!TA, false>(A, p.lda, m0, p.M, k0, kend, p.vecA, ra);
+      s_load<TB, false>(B, p.ldb, n0, p.N, k0, kend, p.vecB, rb);
+    } else {
+      s_load<!TA, true>(A, p.lda, m0, p.M, k0, kend, p.vecA, ra);
+      s_load<TB, true>(B, p.ldb, n0, p.N, k0, kend, p.vecB, rb);
+    }
+  };
+  if (kbeg < kend) {
+    load(kbeg);
+    s_store<!TA>(As, ra);
+    s_store<TB>(Bs, rb);
+  }
+  __syncthreads();
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+    const bool more = k0 + BK < kend;
+    if (more) load(k0 + BK);
+#pragma unroll
+    for (int j = 0; j < BK / 8; ++j) {
+      float fa[4], fb[4];
+      s_frag<!TA>(As, wm * 32 + l32, 8 * j + 4 * h, fa);
+      s_frag<TB>(Bs, wn * 32 + l32, 8 * j + 4 * h, fb);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q], fb[q], acc, 0, 0, 0);
+    }
+    if constexpr ((E & E_DBIAS) != 0) {
+      if (m0 == 0) {
+        const float* bc = Bs + (threadIdx.x >> 6) * 8 * S_LDS + (threadIdx.x & 63);
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) csum += bc[kk * S_LDS];
+      }
+    }
+    __syncthreads();
+    if (more) {
+      s_store<!TA>(As, ra);
+      s_store<TB>(Bs, rb);
+      __syncthreads();
+    }
+  }
+  if constexpr ((E & E_DBIAS) != 0) {
+    if (m0 == 0) {
+      smem[threadIdx.x] = csum;
+      __syncthreads();
+      const int n = n0 + (int)threadIdx.x;
+      if (threadIdx.x < 64 && n < p.N) {
+        const float cs = smem[threadIdx.x] + smem[threadIdx.x + 64] + smem[threadIdx.x + 128] + smem[threadIdx.x + 192];
+        if constexpr ((E & E_SPLIT) != 0) {
+          p.part[(((long long)b * p.ksplit + split) * (p.M + 1) + p.M) * p.N + n] = cs;
+        } else {
+          float* db = p.dbias + (long long)b * p.N;
+          db[n] = p.beta_dbias != 0.f ? db[n] + cs : cs;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // stage the 64x64 tile through LDS, then the epilogue on row-contiguous float4s: thread t
+  // handles column group t%16 of rows t/16 + 16i
+  float* T = smem;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+    T[row * S_TS + wn * 32 + l32] = acc[r];
+  }
+  __syncthreads();
+  const int cg = 4 * (threadIdx.x & 15);
+  const int col = n0 + cg;
+  float* C = p.C + (long long)b * p.sC;
+  const float* resid = ((E & E_RESID) != 0) ? p.resid + (long long)b * p.sC : nullptr;
+  const bool full_cols = interior || (col + 3 < p.N);
+  const bool aligned = ((p.ldc & 3) == 0) && (((E & E_RESID) == 0) || (p.ldr & 3) == 0) &&
+                       (((E & (E_GELU | E_RELU | E_DGELU | E_DRELU)) == 0) || (p.ldaux & 3) == 0) &&
+                       ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+#pragma unroll
+  for (int i = 0; i < SBM / 16; ++i) {
+    const int lr = (threadIdx.x >> 4) + 16 * i;
+    const int row = m0 + lr;
+    const float4 v = *reinterpret_cast<const float4*>(T + lr * S_TS + cg);
+    if constexpr ((E & E_SPLIT) != 0) {
+      if (row >= p.M) continue;
+      float* P = p.part + ((long long)b * p.ksplit + split) * (long long)(p.M + ((E & E_DBIAS) ? 1 : 0)) * p.N;
+      if ((p.N & 3) == 0 && col + 3 < p.N) {
+        *reinterpret_cast<float4*>(P + (long long)row * p.N + col) = v;
+      } else {
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        for (int j = 0; j < 4 && col + j < p.N; ++j) P[(long long)row * p.N + col + j] = vv[j];
+      }
+    } else {
+      epi_store4<E>(p, v, row, col, C, resid, aligned && full_cols && row < p.M);
+    }
+  }
+}
+
 // Sums the split-K partials in f64 and applies the epilogue (beta and bias only). Workgroup of
 // 1024 threads = 16 waves: lane <-> one of 64 consecutive elements, wave w <-> splits w, w+16, ...
 // Row M of the partials (when present) holds the bias-gradient column sums.
@@ -723,10 +916,21 @@ static int epi_flags(const GemmDesc& d) {
   return e;
 }
 
+// Whether a product runs on 64x64 tiles: fp32, fewer 128x128 tiles than CUs, and little work in
+// all (at most 2^30 multiply-adds): long-K weight gradients over all tokens keep the 128x128 tiles
+// and split K instead, which reads each operand half as often.
+static bool use_small(const GemmDesc& d, int num_cu) {
+  const long long tiles = (long long)((d.M + BM - 1) / BM) * ((d.N + BN - 1) / BN) * d.batch;
+  const double macs = (double)d.M * d.N * d.K * d.batch;
+  return !d.bf16 && tiles < num_cu && macs <= 1073741824.0;
+}
+
 size_t gemm_plan_split(GemmDesc& d, int num_cu) {
   const int e = epi_flags(d);
   if (d.ksplit == 0) {
-    const long long tiles = (long long)((d.M + BM - 1) / BM) * ((d.N + BN - 1) / BN) * d.batch;
+    const bool small = use_small(d, num_cu);
+    const int bm = small ? SBM : BM, bn = small ? SBN : BN;
+    const long long tiles = (long long)((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn) * d.batch;
     // Split so that the grid holds TALOS_SPLITK_WG_PER_CU workgroups per CU (any split count,
     // not only powers of two: 3 tiles get 170 splits, not 128), keeping at least
     // TALOS_SPLITK_MIN_K of K per split: the partial traffic (ksplit * M * N floats) stays small
@@ -779,10 +983,43 @@ static GemmKernel pick_kernel(bool tA, bool tB, int e, bool bf) {
 #undef GEMM_CASE
 #undef GEMM_CASE_F32
 
+#define SMALL_CASE(TA, TB, E) \
+  if (tA == TA && tB == TB && e == (E)) return &gemm_small_kernel<TA, TB, (E)>;
+static GemmKernel pick_small(bool tA, bool tB, int e) {
+  SMALL_CASE(false, false, 0)
+  SMALL_CASE(false, false, E_BETA)
+  SMALL_CASE(false, false, E_BIAS)
+  SMALL_CASE(false, false, E_ROPE)
+  SMALL_CASE(false, false, E_RESID)
+  SMALL_CASE(false, false, E_BIAS | E_RESID)
+  SMALL_CASE(false, false, E_BIAS | E_GELU)
+  SMALL_CASE(false, false, E_BIAS | E_RELU)
+  SMALL_CASE(false, false, E_SPLIT)
+  SMALL_CASE(false, true, 0)
+  SMALL_CASE(false, true, E_BETA)
+  SMALL_CASE(false, true, E_DGELU)
+  SMALL_CASE(false, true, E_DRELU)
+  SMALL_CASE(false, true, E_SPLIT)
+  SMALL_CASE(true, false, 0)
+  SMALL_CASE(true, false, E_BETA)
+  SMALL_CASE(true, false, E_SPLIT)
+  SMALL_CASE(true, false, E_DBIAS)
+  SMALL_CASE(true, false, E_SPLIT | E_DBIAS)
+  SMALL_CASE(true, false, E_BETA | E_DBIAS)
+  SMALL_CASE(true, true, 0)
+  SMALL_CASE(true, true, E_BETA)
+  SMALL_CASE(true, true, E_SPLIT)
+  return nullptr;
+}
+#undef SMALL_CASE
+
+static int num_cus();
+
 int gemm_launch(const GemmDesc& d, hipStream_t stream) {
   GemmArgs a = to_args(d);
   if (d.M == 0 || d.N == 0 || d.batch == 0) return TALOS_OK;
-  const unsigned tiles = ceil_div(d.M, BM) * ceil_div(d.N, BN);
+  const bool small = use_small(d, num_cus());
+  const unsigned tiles = small ? ceil_div(d.M, SBM) * ceil_div(d.N, SBN) : ceil_div(d.M, BM) * ceil_div(d.N, BN);
   if (d.K == 0) {
     // C = beta*C (+ epilogue): run the kernel with an empty K loop.
     a.ksplit = 1;
@@ -792,7 +1029,9 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
   dim3 grid((unsigned)((a.nblocks + 7) / 8 * 8));
   const int e = epi_flags(d);
   const bool split = a.ksplit > 1;
-  GemmKernel kern = pick_kernel(d.transA != 0, d.transB != 0, split ? (E_SPLIT | (e & E_DBIAS)) : e, d.bf16);
+  const int ke = split ? (E_SPLIT | (e & E_DBIAS)) : e;
+  GemmKernel kern = small ? pick_small(d.transA != 0, d.transB != 0, ke)
+                          : pick_kernel(d.transA != 0, d.transB != 0, ke, d.bf16);
   if (kern == nullptr) {
     set_error("gemm: epilogue combination 0x%x is not instantiated for transA=%d transB=%d%s", e, d.transA, d.transB,
               d.bf16 ? " (bf16)" : "");
@@ -800,8 +1039,12 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
   }
   // profiler name = the kernel symbol's template arguments as rocprofv3 prints them
   char name[64];
-  snprintf(name, sizeof(name), "gemm_f32_kernel<%s, %s, %d, %s>", d.transA ? "true" : "false",
-           d.transB ? "true" : "false", split ? (E_SPLIT | (e & E_DBIAS)) : e, d.bf16 ? "true" : "false");
+  if (small)
+    snprintf(name, sizeof(name), "gemm_small_kernel<%s, %s, %d>", d.transA ? "true" : "false",
+             d.transB ? "true" : "false", ke);
+  else
+    snprintf(name, sizeof(name), "gemm_f32_kernel<%s, %s, %d, %s>", d.transA ? "true" : "false",
+             d.transB ? "true" : "false", ke, d.bf16 ? "true" : "false");
   {
     // algorithmic work: 2MNK flops; A, B read once, C written once (+ C / residual / aux reads)
     const double MN = (double)d.M * d.N;
@@ -814,7 +1057,7 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
     }
     ProfScope ps(stream, name, 2.0 * MN * d.K * d.batch, bytes * d.batch);
     hipLaunchKernelGGL(kern, grid, dim3(NT), 0, stream, a);
-    TALOS_LAUNCHED("gemm_f32_kernel");
+    TALOS_LAUNCHED(small ? "gemm_small_kernel" : "gemm_f32_kernel");
   }
   if (split) {
     const long long RN = (long long)(d.M + (d.dbias ? 1 : 0)) * d.N;

@@ -68,6 +68,7 @@ struct talos_plan_s {
   // its activations and the backward scratch, [batch, d] / [batch, F]
   struct LastRows {
     float *x, *o, *lse, *h2, *xn2, *rstd2, *u, *a, *g_u, *g_xn, *g_h2, *g_o;
+    float *xn1, *q, *dq, *g_xnq;  // the last layer's query path on these rows (last-query attention)
   } lr{};
   const int32_t* lens = nullptr;  // per-sample lengths of the PPO call in progress (nullptr: all seq)
   int num_cu = 256;
@@ -713,6 +714,17 @@ __global__ void scatter_last_kernel(int B, int S, int d, const int32_t* __restri
   }
 }
 
+// g[b * S + last_row(b)] += gl[b] (the rest of g unchanged)
+__global__ void scatter_add_last_kernel(int B, int S, int d, const int32_t* __restrict__ lens,
+                                        const float* __restrict__ gl, float* __restrict__ g) {
+  const long long n = (long long)B * d;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+    const long long b = i / d;
+    const int e = (int)(i % d);
+    g[(b * S + last_row(lens, (int)b, S)) * d + e] += gl[i];
+  }
+}
+
 // Clipped PPO loss over the minibatch (closed form of the per-sample graph of
 // src/ppo.rs:702-749, mean over the batch as src/ppo.rs:754-755). One workgroup; f64 math.
 // Per sample: lp = z - lse(z); ratio = exp(lp[a] - old); surr1 = ratio*adv;
@@ -845,9 +857,37 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
     } else {
       // Only the last token of each sample reaches the heads, and everything after attention is
       // per row: the last layer runs its MLP half on those B rows and writes p->last directly.
-      if (ppo_lastq(p, bc, L)) {  // attention of the last query only
-        rc = block_qkv_forward(p, bc, P, bo, L, s);
-        if (rc == TALOS_OK) rc = attn_fwd_lastq_launch(block_attn_desc(p, bc, L), p->lr.o, d, p->lr.lse, s);
+      if (ppo_lastq(p, bc, L)) {
+        // attention of the last query only: keys and values on every row, the query on the
+        // last rows (rotated inside the attention kernel)
+        auto& R = p->lr;
+        rc = rmsnorm_fwd_launch(M, d, c.eps, L.x, P + bo.g1, L.xn1, L.rstd1, s);
+        if (rc) return rc;
+        {
+          GemmDesc g;
+          g.M = M;
+          g.N = 2 * d;
+          g.K = d;
+          g.A = L.xn1;
+          g.lda = d;
+          g.B = P + bo.wqkv + d;
+          g.ldb = 3 * d;
+          g.C = L.qkv + d;
+          g.ldc = 3 * d;
+          g.rope_cos = p->rcos;
+          g.rope_sin = p->rsin;
+          g.rope_cols = d;  // the k columns
+          g.rope_dim = bc.head_dim;
+          g.rope_seq = c.seq;
+          g.ksplit = 1;
+          if ((rc = gemm_launch(g, s))) return rc;
+        }
+        if ((rc = gather(L.xn1, R.xn1, d))) return rc;
+        if ((rc = mm(p, s, 0, 0, c.batch, d, d, R.xn1, d, P + bo.wqkv, 3 * d, R.q, d))) return rc;
+        AttnDesc ad = block_attn_desc(p, bc, L);
+        ad.q_last = R.q;
+        ad.ldq_last = d;
+        rc = attn_fwd_lastq_launch(ad, R.o, d, R.lse, s);
       } else {
         rc = block_attn_forward(p, bc, P, bo, L, s);
         if (rc == TALOS_OK) rc = gather(L.o, p->lr.o, ow);
@@ -1023,7 +1063,7 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
   {  // the last layer's last-token rows
     const size_t F = cfg->ffn_dim, ow = attn_width(bc);
     auto& R = p->lr;
-    for (float** b : {&R.x, &R.h2, &R.xn2, &R.g_xn, &R.g_h2}) rc |= plan_alloc(p, b, B * d);
+    for (float** b : {&R.x, &R.h2, &R.xn2, &R.g_xn, &R.g_h2, &R.xn1, &R.q, &R.dq, &R.g_xnq}) rc |= plan_alloc(p, b, B * d);
     for (float** b : {&R.o, &R.g_o}) rc |= plan_alloc(p, b, B * ow);
     for (float** b : {&R.u, &R.a, &R.g_u}) rc |= plan_alloc(p, b, B * F);
     rc |= plan_alloc(p, &R.rstd2, B);
@@ -1163,8 +1203,26 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
                             R.g_xn, R.g_h2, R.g_o, s);
     if (rc) return rc;
     if (ppo_lastq(p, bc, L)) {
-      rc = attn_bwd_lastq_launch(block_attn_desc(p, bc, L), R.o, d, R.lse, R.g_o, d, s);
-      if (rc == TALOS_OK) rc = block_qkv_backward(p, bc, params, G, offs[l], L, nullptr, R.g_h2, p->g_out, s);
+      // keys / values on every row, the query on the last rows (its gradient in R.dq)
+      const BlockOff& o = offs[l];
+      AttnDesc ad = block_attn_desc(p, bc, L);
+      ad.q_last = R.q;
+      ad.ldq_last = d;
+      ad.dq_last = R.dq;
+      ad.lddq_last = d;
+      if ((rc = attn_bwd_lastq_launch(ad, R.o, d, R.lse, R.g_o, d, s))) return rc;
+      float* g_kv = p->g_qkv + d;
+      if ((rc = mm(p, s, 1, 0, d, 2 * d, M, L.xn1, d, g_kv, 3 * d, G + o.wqkv + d, 3 * d))) return rc;
+      if ((rc = mm(p, s, 1, 0, d, d, B, R.xn1, d, R.dq, d, G + o.wqkv, 3 * d))) return rc;
+      if ((rc = mm(p, s, 0, 1, M, d, 2 * d, g_kv, 3 * d, params + o.wqkv + d, 3 * d, p->g_xn, d))) return rc;
+      if ((rc = mm(p, s, 0, 1, B, d, d, R.dq, d, params + o.wqkv, 3 * d, R.g_xnq, d))) return rc;
+      {
+        ProfScope ps_s(s, "scatter_add_last_kernel", 0.0, 12.0 * B * d);
+        hipLaunchKernelGGL(scatter_add_last_kernel, dim3(ceil_div((size_t)B * d, 256)), dim3(256), 0, s, B, c.seq, d,
+                           p->lens, R.g_xnq, p->g_xn);
+        TALOS_LAUNCHED("scatter_add_last_kernel");
+      }
+      rc = block_norm1_backward(p, bc, params, G, o, L, nullptr, R.g_h2, p->g_out, s);
     } else {
       // the row gradients spread over the full token grid
       const int ow = attn_width(bc);
