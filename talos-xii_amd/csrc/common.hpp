@@ -121,6 +121,12 @@ __device__ __forceinline__ float gelu_d(float x) {
   const float pdf = 0.39894228040143268f * expf(-0.5f * x * x);
   return cdf + x * pdf;
 }
+// gelu(x) = x * Phi(x), and *d = gelu'(x), sharing the erf
+__device__ __forceinline__ float gelu_fd(float x, float* d) {
+  const float cdf = 0.5f * (1.0f + erff(x * 0.70710678118654752f));
+  *d = cdf + x * (0.39894228040143268f * expf(-0.5f * x * x));
+  return x * cdf;
+}
 
 inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 

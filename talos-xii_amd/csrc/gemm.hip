@@ -21,6 +21,7 @@
 #include <algorithm>
 
 #include "gemm.hpp"
+#include "rowops.hpp"
 
 namespace talos {
 
@@ -57,13 +58,14 @@ enum : int {
   E_BETA = 1,    // + beta * C
   E_BIAS = 2,    // + bias[col]
   E_RESID = 4,   // + resid[row, col]
-  E_GELU = 8,    // aux = v; v = gelu(v)
+  E_GELU = 8,    // aux = gelu'(v); v = gelu(v)   (the backward then multiplies by aux)
   E_RELU = 16,   // aux = v; v = relu(v)
-  E_DGELU = 32,  // v *= gelu'(aux)
+  E_DGELU = 32,  // v *= aux (aux = gelu' saved by the forward's E_GELU)
   E_DRELU = 64,  // v = aux > 0 ? v : 0
   E_ROPE = 128,  // rotate interleaved pairs of columns [0, rope_cols)
   E_SPLIT = 256,  // write the fp32 partial tile of this K split (no epilogue)
-  E_DBIAS = 512   // also sum the columns of op(B) (bias gradient; transA = 1, transB = 0)
+  E_DBIAS = 512,  // also sum the columns of op(B) (bias gradient; transA = 1, transB = 0)
+  E_NORM = 1024   // also RMSNorm each output row (N = 128: the whole row is in the tile)
 };
 
 struct GemmArgs {
@@ -87,6 +89,11 @@ struct GemmArgs {
   float* part;  // [batch][ksplit][M + (dbias ? 1 : 0)][N]
   float* dbias;
   float beta_dbias;
+  const float* norm_gain;  // E_NORM: norm_out = C * rstd * gain, rstd = 1 / sqrt(mean(C^2) + eps)
+  float* norm_out;
+  long long ldn;
+  float* norm_rstd;
+  float norm_eps;
   int vecA, vecB;
   int nblocks;  // tiles * batch * ksplit (the grid is padded to a multiple of 8)
 };
@@ -230,12 +237,16 @@ __device__ __forceinline__ float epi_value(const GemmArgs& p, float acc, int row
   if constexpr ((E & E_BETA) != 0) v += p.beta * C[(long long)row * p.ldc + col];
   if constexpr ((E & E_BIAS) != 0) v += p.bias[col];
   if constexpr ((E & E_RESID) != 0) v += resid[(long long)row * p.ldr + col];
-  if constexpr ((E & E_DGELU) != 0) v *= gelu_d(p.aux[(long long)row * p.ldaux + col]);
+  if constexpr ((E & E_DGELU) != 0) v *= p.aux[(long long)row * p.ldaux + col];
   if constexpr ((E & E_DRELU) != 0) v = p.aux[(long long)row * p.ldaux + col] > 0.f ? v : 0.f;
-  if constexpr ((E & (E_GELU | E_RELU)) != 0) {
+  if constexpr ((E & E_GELU) != 0) {
+    float dv;
+    v = gelu_fd(v, &dv);
+    if (p.aux) p.aux[(long long)row * p.ldaux + col] = dv;
+  }
+  if constexpr ((E & E_RELU) != 0) {
     if (p.aux) p.aux[(long long)row * p.ldaux + col] = v;
-    if constexpr ((E & E_GELU) != 0) v = gelu_f(v);
-    else v = fmaxf(v, 0.f);
+    v = fmaxf(v, 0.f);
   }
   return v;
 }
@@ -244,8 +255,8 @@ __device__ __forceinline__ float epi_value(const GemmArgs& p, float acc, int row
 // memory as float4 (interior) or per element (edges). RoPE pairs (2i, 2i+1) sit in (x, y) and
 // (z, w) because col is a multiple of 4.
 template <int E>
-__device__ __forceinline__ void epi_store4(const GemmArgs& p, float4 v, int row, int col, float* C,
-                                           const float* __restrict__ resid, bool full) {
+__device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int row, int col, float* C,
+                                             const float* __restrict__ resid, bool full) {
   float o[4] = {v.x * p.alpha, v.y * p.alpha, v.z * p.alpha, v.w * p.alpha};
   if constexpr ((E & E_ROPE) != 0) {
     if (col < p.rope_cols) {
@@ -282,22 +293,25 @@ __device__ __forceinline__ void epi_store4(const GemmArgs& p, float4 v, int row,
       const float uu[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if constexpr ((E & E_DGELU) != 0) o[j] *= gelu_d(uu[j]);
+        if constexpr ((E & E_DGELU) != 0) o[j] *= uu[j];
         else o[j] = uu[j] > 0.f ? o[j] : 0.f;
       }
     }
-    if constexpr ((E & (E_GELU | E_RELU)) != 0) {
+    if constexpr ((E & E_GELU) != 0) {
+      float dv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = gelu_fd(o[j], &dv[j]);
+      if (p.aux) *reinterpret_cast<float4*>(p.aux + (long long)row * p.ldaux + col) = make_float4(dv[0], dv[1], dv[2], dv[3]);
+    }
+    if constexpr ((E & E_RELU) != 0) {
       if (p.aux) *reinterpret_cast<float4*>(p.aux + (long long)row * p.ldaux + col) = make_float4(o[0], o[1], o[2], o[3]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if constexpr ((E & E_GELU) != 0) o[j] = gelu_f(o[j]);
-        else o[j] = fmaxf(o[j], 0.f);
-      }
+      for (int j = 0; j < 4; ++j) o[j] = fmaxf(o[j], 0.f);
     }
     *reinterpret_cast<float4*>(C + crow + col) = make_float4(o[0], o[1], o[2], o[3]);
-    return;
+    return make_float4(o[0], o[1], o[2], o[3]);
   }
-  if (row >= p.M) return;
+  if (row >= p.M) return make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int cj = col + j;
@@ -306,14 +320,43 @@ __device__ __forceinline__ void epi_store4(const GemmArgs& p, float4 v, int row,
     if constexpr ((E & E_BETA) != 0) x += p.beta * C[crow + cj];
     if constexpr ((E & E_BIAS) != 0) x += p.bias[cj];
     if constexpr ((E & E_RESID) != 0) x += resid[(long long)row * p.ldr + cj];
-    if constexpr ((E & E_DGELU) != 0) x *= gelu_d(p.aux[(long long)row * p.ldaux + cj]);
+    if constexpr ((E & E_DGELU) != 0) x *= p.aux[(long long)row * p.ldaux + cj];
     if constexpr ((E & E_DRELU) != 0) x = p.aux[(long long)row * p.ldaux + cj] > 0.f ? x : 0.f;
-    if constexpr ((E & (E_GELU | E_RELU)) != 0) {
+    if constexpr ((E & E_GELU) != 0) {
+      float dx;
+      x = gelu_fd(x, &dx);
+      if (p.aux) p.aux[(long long)row * p.ldaux + cj] = dx;
+    }
+    if constexpr ((E & E_RELU) != 0) {
       if (p.aux) p.aux[(long long)row * p.ldaux + cj] = x;
-      if constexpr ((E & E_GELU) != 0) x = gelu_f(x);
-      else x = fmaxf(x, 0.f);
+      x = fmaxf(x, 0.f);
     }
     C[crow + cj] = x;
+    o[j] = x;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (col + j >= p.N) o[j] = 0.f;  // columns past N take no part in a row norm
+  return make_float4(o[0], o[1], o[2], o[3]);
+}
+
+// RMSNorm of the rows of a 128-wide tile from the epilogue's float4s: the 32 lanes of one
+// half-wave hold one row (column groups 4 * (lane % 32)), so the row sum of squares is a
+// shuffle reduction over that half-wave. Same arithmetic as rmsnorm_fwd_kernel.
+__device__ __forceinline__ void epi_norm4(const GemmArgs& p, float4 o, int row, int col) {
+  float ss = o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  const float r = 1.0f / sqrtf(ss / (float)p.N + p.norm_eps);
+  if (row >= p.M) return;
+  if ((threadIdx.x & 31) == 0 && p.norm_rstd) p.norm_rstd[row] = r;
+  float* y = p.norm_out + (long long)row * p.ldn + col;
+  if (col + 3 < p.N) {
+    const float4 g = *reinterpret_cast<const float4*>(p.norm_gain + col);
+    *reinterpret_cast<float4*>(y) = make_float4(o.x * r * g.x, o.y * r * g.y, o.z * r * g.z, o.w * r * g.w);
+  } else {
+    const float oo[4] = {o.x, o.y, o.z, o.w};
+    for (int j = 0; j < 4 && col + j < p.N; ++j) y[j] = oo[j] * r * p.norm_gain[col + j];
   }
 }
 
@@ -617,7 +660,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
         const int lr = (threadIdx.x >> 5) + 8 * i;
         const int row = m0 + half * T_ROWS + lr;
         const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
-        epi_store4<E>(p, v, row, col, C, resid, aligned && full_cols && row < p.M);
+        const float4 o = epi_store4<E>(p, v, row, col, C, resid, aligned && full_cols && row < p.M);
+        if constexpr ((E & E_NORM) != 0) epi_norm4(p, o, row, col);
       }
     }
   }
@@ -887,6 +931,11 @@ static GemmArgs to_args(const GemmDesc& d) {
   a.part = d.workspace;
   a.dbias = d.dbias;
   a.beta_dbias = d.beta_dbias;
+  a.norm_gain = d.norm_gain;
+  a.norm_out = d.norm_out;
+  a.ldn = d.ldn;
+  a.norm_rstd = d.norm_rstd;
+  a.norm_eps = d.norm_eps;
   auto aligned = [](const void* ptr, long long ld) {
     return ((reinterpret_cast<uintptr_t>(ptr) & 15) == 0) && (ld % 4 == 0);
   };
@@ -913,6 +962,7 @@ static int epi_flags(const GemmDesc& d) {
   if (d.dact == GEMM_DACT_RELU) e |= E_DRELU;
   if (d.rope_cols > 0) e |= E_ROPE;
   if (d.dbias) e |= E_DBIAS;
+  if (d.norm_out) e |= E_NORM;
   return e;
 }
 
@@ -964,6 +1014,9 @@ static GemmKernel pick_kernel(bool tA, bool tB, int e, bool bf) {
   GEMM_CASE(false, false, E_BIAS | E_GELU)
   GEMM_CASE(false, false, E_BIAS | E_RELU)
   GEMM_CASE(false, false, E_SPLIT)
+  GEMM_CASE_F32(false, false, E_BIAS | E_NORM)
+  GEMM_CASE_F32(false, false, E_RESID | E_NORM)
+  GEMM_CASE_F32(false, false, E_BIAS | E_RESID | E_NORM)
   GEMM_CASE(false, true, 0)
   GEMM_CASE(false, true, E_BETA)
   GEMM_CASE(false, true, E_DGELU)
@@ -1016,6 +1069,16 @@ static GemmKernel pick_small(bool tA, bool tB, int e) {
 static int num_cus();
 
 int gemm_launch(const GemmDesc& d, hipStream_t stream) {
+  if (d.norm_out && (d.N != BN || d.bf16 || d.batch != 1 || use_small(d, num_cus()))) {
+    // the fused row norm needs the whole 128-wide row in one 128x128 tile: otherwise the product,
+    // then the separate row-norm kernel
+    TALOS_REQUIRE(d.ldc == d.N && d.ldn == d.N, TALOS_ERR_UNSUPPORTED,
+                  "gemm: a row norm after the product needs ldc == ldn == N");
+    GemmDesc g = d;
+    g.norm_out = nullptr;
+    if (int rc = gemm_launch(g, stream)) return rc;
+    return rmsnorm_fwd_launch(d.M, d.N, d.norm_eps, d.C, d.norm_gain, d.norm_out, d.norm_rstd, stream);
+  }
   GemmArgs a = to_args(d);
   if (d.M == 0 || d.N == 0 || d.batch == 0) return TALOS_OK;
   const bool small = use_small(d, num_cus());
@@ -1053,6 +1116,7 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
       if (d.beta != 0.f) bytes += 4.0 * MN;
       if (d.resid) bytes += 4.0 * MN;
       if (d.aux) bytes += 4.0 * MN;
+      if (d.norm_out) bytes += 4.0 * (MN + d.M + d.N);
       if (d.bias) bytes += 4.0 * d.N;
     }
     ProfScope ps(stream, name, 2.0 * MN * d.K * d.batch, bytes * d.batch);

@@ -7,12 +7,14 @@
 namespace talos {
 
 enum GemmAct { GEMM_ACT_NONE = 0, GEMM_ACT_GELU = 1, GEMM_ACT_RELU = 2 };
-// Epilogue multiplier of the backward of an activation: C = acc * act'(aux).
+// Epilogue of the backward of an activation: C = acc * aux for GELU (aux holds gelu' saved by
+// the forward), C = acc where aux > 0 for ReLU (aux holds the pre-activation).
 enum GemmDAct { GEMM_DACT_NONE = 0, GEMM_DACT_GELU = 1, GEMM_DACT_RELU = 2 };
 
 // C[b][M,N] = alpha * op(A[b]) . op(B[b]) + beta * C[b]  (+ bias[N]) (+ resid[M,N]),
-// then optionally act(.) with the pre-activation stored to aux, or the activation derivative
-// act'(aux) multiplied in; RoPE on columns [0, rope_cols) with position row % rope_seq.
+// then optionally act(.) storing to aux what its backward needs (gelu'(v) for GELU, the
+// pre-activation v for ReLU), or that saved value applied (GEMM_DACT_*); RoPE on columns
+// [0, rope_cols) with position row % rope_seq.
 // Row-major storage; op(A) is [M,K]: A[m*lda + k] (transA = 0) or A[k*lda + m] (transA = 1);
 // op(B) is [K,N]: B[k*ldb + n] (transB = 0) or B[n*ldb + k] (transB = 1).
 struct GemmDesc {
@@ -31,7 +33,7 @@ struct GemmDesc {
   long long ldr = 0;
   int act = GEMM_ACT_NONE;
   int dact = GEMM_DACT_NONE;
-  float* aux = nullptr;  // act: pre-activation output; dact: pre-activation input
+  float* aux = nullptr;  // act: output of what the backward needs; dact: that input
   long long ldaux = 0;
   // RoPE epilogue (interleaved pairs (2i, 2i+1) inside each rot_dim-wide head)
   const float* rope_cos = nullptr;
@@ -45,6 +47,15 @@ struct GemmDesc {
   // sum_k B[k][n], the column sums of op(B) accumulated from the panels already in LDS.
   float* dbias = nullptr;
   float beta_dbias = 0.f;
+  // Row norm after the epilogue (RMSNorm, rmsnorm_fwd_launch's arithmetic): norm_out[row] =
+  // C[row] * rstd * norm_gain with rstd = 1 / sqrt(mean(C[row]^2) + norm_eps), stored to
+  // norm_rstd[row]. Fused into the epilogue when N = 128 (one tile holds the row); other shapes
+  // run the row-norm kernel after the product (ldc = ldn = N).
+  const float* norm_gain = nullptr;
+  float* norm_out = nullptr;
+  long long ldn = 0;
+  float* norm_rstd = nullptr;
+  float norm_eps = 0.f;
   // bf16-in / fp32-accumulate: operands are rounded to bf16 (nearest even) as they are staged
   // into LDS and multiplied with v_mfma_f32_32x32x16_bf16; HBM layout and outputs stay fp32.
   bool bf16 = false;

@@ -15,7 +15,9 @@
 //     o   = attention(q, k, v), scale 1/sqrt(head_dim + rope_dim)
 //   h2  = x + o . Wo                            GEMM, residual in the epilogue
 //   xn2 = rmsnorm(h2; g2)
-//   a   = act(xn2 . W1 + b1)                    GEMM, bias + activation epilogue (u saved)
+//   a   = act(xn2 . W1 + b1)                    GEMM, bias + activation epilogue; u saved: gelu' of
+//                                               the pre-activation for GELU (the backward then
+//                                               multiplies by it), the pre-activation for ReLU
 //   out = h2 + a . W2 + b2                      GEMM, bias + residual epilogue
 // and the backward in reverse, with weight gradients as split-K GEMMs (f64 partial sums) and
 // the activation derivative / RoPE^T folded into the producing kernels.
@@ -508,12 +510,28 @@ static AttnDesc block_attn_desc(talos_plan_s* p, const talos_block_cfg& c, talos
   return a;
 }
 
-// xn1 = rmsnorm(x), qkv = xn1.Wqkv (RoPE in the epilogue). L.x must be set.
+// A row norm to fuse into the epilogue of the product that makes its input (the next layer's
+// RMSNorm1 after the MLP's output product, or layer 0's after the embedding).
+struct RowNorm {
+  const float* gain = nullptr;
+  float* out = nullptr;
+  float* rstd = nullptr;
+};
+static void set_norm(GemmDesc& g, const RowNorm& n, float eps) {
+  g.norm_gain = n.gain;
+  g.norm_out = n.out;
+  g.ldn = g.N;
+  g.norm_rstd = n.rstd;
+  g.norm_eps = eps;
+}
+
+// xn1 = rmsnorm(x) (unless the product that made x already wrote L.xn1: normed), qkv = xn1.Wqkv
+// (RoPE in the epilogue). L.x must be set.
 static int block_qkv_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
-                             talos_plan_s::Layer& L, hipStream_t s) {
+                             talos_plan_s::Layer& L, hipStream_t s, bool normed) {
   const int M = c.batch * c.seq, d = c.d_model;
-  int rc = rmsnorm_fwd_launch(M, d, c.eps, L.x, P + o.g1, L.xn1, L.rstd1, s);
-  if (rc) return rc;
+  if (!normed)
+    if (int rc = rmsnorm_fwd_launch(M, d, c.eps, L.x, P + o.g1, L.xn1, L.rstd1, s)) return rc;
   {
     GemmDesc g;
     g.M = M;
@@ -537,27 +555,42 @@ static int block_qkv_forward(talos_plan_s* p, const talos_block_cfg& c, const fl
 
 // Attention half of a block's forward: o = attention(rmsnorm(x)) with lse saved.
 static int block_attn_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
-                              talos_plan_s::Layer& L, hipStream_t s) {
+                              talos_plan_s::Layer& L, hipStream_t s, bool normed) {
   if (c.attention == TALOS_ATTN_MLA) {
-    int rc = rmsnorm_fwd_launch(c.batch * c.seq, c.d_model, c.eps, L.x, P + o.g1, L.xn1, L.rstd1, s);
-    if (rc) return rc;
+    if (!normed)
+      if (int rc = rmsnorm_fwd_launch(c.batch * c.seq, c.d_model, c.eps, L.x, P + o.g1, L.xn1, L.rstd1, s)) return rc;
     return mla_attn_forward(p, mla_dims(c), P, o.mla, L.xn1, L, s);
   }
-  int rc = block_qkv_forward(p, c, P, o, L, s);
+  int rc = block_qkv_forward(p, c, P, o, L, s, normed);
   if (rc) return rc;
   return attn_fwd_launch(block_attn_desc(p, c, L), s);
 }
 
 // Second half over R rows (all tokens, or only the last token of each sample): h2 = x + o.Wo,
-// xn2 = rmsnorm(h2), u = xn2.W1 + b1, a = act(u), out = h2 + a.W2 + b2.
+// xn2 = rmsnorm(h2) (fused into the Wo product's epilogue), u = xn2.W1 + b1, a = act(u),
+// out = h2 + a.W2 + b2, followed by the next row norm when next is set.
 static int block_mlp_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o, int R,
                              const float* x, const float* ob, float* h2, float* xn2, float* rstd2, float* u, float* a,
-                             float* out, hipStream_t s) {
+                             float* out, hipStream_t s, const RowNorm& next = RowNorm{}) {
   const int d = c.d_model, F = c.ffn_dim, ow = attn_width(c);
-  int rc = mm(p, s, 0, 0, R, d, ow, ob, ow, P + o.wo, d, h2, d, 0.f, nullptr, x, d);
-  if (rc) return rc;
-  rc = rmsnorm_fwd_launch(R, d, c.eps, h2, P + o.g2, xn2, rstd2, s);
-  if (rc) return rc;
+  int rc;
+  {
+    GemmDesc g;
+    g.M = R;
+    g.N = d;
+    g.K = ow;
+    g.A = ob;
+    g.lda = ow;
+    g.B = P + o.wo;
+    g.ldb = d;
+    g.C = h2;
+    g.ldc = d;
+    g.resid = x;
+    g.ldr = d;
+    g.ksplit = 1;
+    set_norm(g, RowNorm{P + o.g2, xn2, rstd2}, c.eps);
+    if ((rc = gemm_launch(g, s))) return rc;
+  }
   {
     GemmDesc g;
     g.M = R;
@@ -577,15 +610,32 @@ static int block_mlp_forward(talos_plan_s* p, const talos_block_cfg& c, const fl
     rc = gemm_launch(g, s);
     if (rc) return rc;
   }
-  return mm(p, s, 0, 0, R, d, F, a, F, P + o.w2, d, out, d, 0.f, P + o.b2, h2, d);
+  GemmDesc g;
+  g.M = R;
+  g.N = d;
+  g.K = F;
+  g.A = a;
+  g.lda = F;
+  g.B = P + o.w2;
+  g.ldb = d;
+  g.C = out;
+  g.ldc = d;
+  g.bias = P + o.b2;
+  g.resid = h2;
+  g.ldr = d;
+  g.ksplit = 1;
+  if (next.out) set_norm(g, next, c.eps);
+  return gemm_launch(g, s);
 }
 
-// Forward of one block; L.x must be set. Writes L.out.
+// Forward of one block; L.x must be set (and L.xn1 / L.rstd1 when normed). Writes L.out, and the
+// next row norm of L.out when next is set.
 static int block_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
-                         talos_plan_s::Layer& L, hipStream_t s) {
-  int rc = block_attn_forward(p, c, P, o, L, s);
+                         talos_plan_s::Layer& L, hipStream_t s, bool normed = false,
+                         const RowNorm& next = RowNorm{}) {
+  int rc = block_attn_forward(p, c, P, o, L, s, normed);
   if (rc) return rc;
-  return block_mlp_forward(p, c, P, o, c.batch * c.seq, L.x, L.o, L.h2, L.xn2, L.rstd2, L.u, L.a, L.out, s);
+  return block_mlp_forward(p, c, P, o, c.batch * c.seq, L.x, L.o, L.h2, L.xn2, L.rstd2, L.u, L.a, L.out, s, next);
 }
 
 // MLP half backward over R rows: gout = dL/dout; writes the W2 / W1 / gain2 gradients, the
@@ -835,8 +885,28 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
   const talos_block_cfg bc = block_cfg_of(c);
   const PpoOff po = ppo_offsets(c);
   const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions, ow = attn_width(bc);
-  int rc = mm(p, s, 0, 0, M, d, c.in_dim, states, c.in_dim, P + po.we, d, p->h0, d, 0.f, P + po.be);
-  if (rc) return rc;
+  // each layer's RMSNorm1 runs in the epilogue of the product that makes its input
+  auto norm1_of = [&](int l) {
+    const BlockOff bo = block_offsets(bc, po.blocks + (size_t)l * block_params(bc));
+    return RowNorm{P + bo.g1, p->layers[l].xn1, p->layers[l].rstd1};
+  };
+  int rc;
+  {
+    GemmDesc g;
+    g.M = M;
+    g.N = d;
+    g.K = c.in_dim;
+    g.A = states;
+    g.lda = c.in_dim;
+    g.B = P + po.we;
+    g.ldb = d;
+    g.C = p->h0;
+    g.ldc = d;
+    g.bias = P + po.be;
+    g.ksplit = 1;
+    if (c.n_layers > 0) set_norm(g, norm1_of(0), c.eps);
+    if ((rc = gemm_launch(g, s))) return rc;
+  }
   const float* h = p->h0;
   size_t base = po.blocks;
   // the last-token rows of a [M, w] buffer into [batch, w]
@@ -851,7 +921,7 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
     auto& L = p->layers[l];
     L.x = const_cast<float*>(h);
     if (l + 1 < c.n_layers) {
-      rc = block_forward(p, bc, P, bo, L, s);
+      rc = block_forward(p, bc, P, bo, L, s, true, norm1_of(l + 1));
       if (rc) return rc;
       h = L.out;
     } else {
@@ -861,8 +931,6 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
         // attention of the last query only: keys and values on every row, the query on the
         // last rows (rotated inside the attention kernel)
         auto& R = p->lr;
-        rc = rmsnorm_fwd_launch(M, d, c.eps, L.x, P + bo.g1, L.xn1, L.rstd1, s);
-        if (rc) return rc;
         {
           GemmDesc g;
           g.M = M;
@@ -889,7 +957,7 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
         ad.ldq_last = d;
         rc = attn_fwd_lastq_launch(ad, R.o, d, R.lse, s);
       } else {
-        rc = block_attn_forward(p, bc, P, bo, L, s);
+        rc = block_attn_forward(p, bc, P, bo, L, s, true);
         if (rc == TALOS_OK) rc = gather(L.o, p->lr.o, ow);
       }
       if (rc || (rc = gather(L.x, p->lr.x, d))) return rc;
