@@ -855,6 +855,153 @@ __global__ __launch_bounds__(256) void ppo_loss_kernel(int B, int A, float clip_
     for (int i = 0; i < kLossParts; ++i) part[(long long)blockIdx.x * kLossParts + i] = sums[i];
 }
 
+// The actor / critic heads, the clipped PPO loss and their backward in one kernel, from the
+// out_proj rows pout [B, d] (the closed form above, per sample). One wave per sample at a time:
+// lane k < A holds logit k = pout . Wa[:, k] + ba[k] (fp32 dot products reduced over the wave),
+// the loss terms run in f64 on those lanes, and the wave then writes the out_proj row gradient
+// g_pout = dz . Wa^T + dvalue . Wc^T and adds pout^T dz, dz, pout dvalue, dvalue to its share of
+// the head gradients (LDS, fp32 over its samples). Each workgroup writes its partial sums (f64) of
+// the loss statistics and of the head gradients, laid out as the parameters Wa | ba | Wc | bc;
+// ppo_heads_final_kernel adds the workgroups up in a fixed order.
+constexpr int kHeadWaves = 4;
+constexpr int kHeadSamples = 16;  // samples per workgroup (4 per wave) of the fused heads kernel
+constexpr int kHeadMaxRow = 2176;  // d * (A + 1) + A + 1 of the fused path (per-wave sums in LDS)
+__global__ __launch_bounds__(256) void ppo_heads_kernel(int B, int d, int A, float clip_eps, float cv, float ce,
+                                                        const float* __restrict__ pout, const float* __restrict__ Wa,
+                                                        const float* __restrict__ ba, const float* __restrict__ Wc,
+                                                        const float* __restrict__ bc,
+                                                        const int32_t* __restrict__ actions,
+                                                        const float* __restrict__ adv, const float* __restrict__ ret,
+                                                        const float* __restrict__ old_logp, float* __restrict__ g_pout,
+                                                        double* __restrict__ part) {
+  extern __shared__ float sh[];  // per wave: dWa [d*A] | dba [A] | dWc [d] | dbc [1]
+  __shared__ double sl[kHeadWaves][kLossParts];
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int R = d * (A + 1) + A + 1;
+  float* acc = sh + wv * R;
+  for (int i = lane; i < R; i += 64) acc[i] = 0.f;
+  __syncthreads();  // zeroed by other lanes than the ones that add to each entry
+  double total = 0.0, s_kl = 0.0, s_pol = 0.0, s_v = 0.0, s_ent = 0.0;
+  const double invB = 1.0 / (double)B;
+  const bool own = lane < A;
+  const int b_end = min(B, (int)(blockIdx.x + 1) * kHeadSamples);
+  for (int b = blockIdx.x * kHeadSamples + wv; b < b_end; b += kHeadWaves) {
+    const float* pr = pout + (long long)b * d;
+    float zk = 0.f;
+    for (int k = 0; k < A; ++k) {
+      float t = 0.f;
+      for (int i = lane; i < d; i += 64) t += pr[i] * Wa[(long long)i * A + k];
+      t = wave_sum(t);
+      if (lane == k) zk = t + ba[k];
+    }
+    float tv = 0.f;
+    for (int i = lane; i < d; i += 64) tv += pr[i] * Wc[i];
+    const double value = (double)(wave_sum(tv) + bc[0]);
+    // log-softmax over the A lanes, f64
+    double mx = own ? (double)zk : -INFINITY;
+    for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 64));
+    const double se = wave_sum(own ? exp((double)zk - mx) : 0.0);
+    const double lse = log(se) + mx;
+    const double lpk = (double)zk - lse, pk = own ? exp(lpk) : 0.0;
+    const double ent = -wave_sum(own ? pk * lpk : 0.0);
+    const int a = actions[b];
+    double dzk = 0.0, dv = 0.0;
+    if (a < 0 || a >= A) {
+      // the reference panics on an out-of-range action (mask[action], src/ppo.rs:714-720); here
+      // the loss becomes NaN and the sample contributes no gradient
+      total = NAN;
+    } else {
+      const double za = __shfl(lpk, a, 64);
+      const double log_ratio = za - (double)old_logp[b];
+      const double ratio = exp(log_ratio);
+      const double ad = adv[b];
+      const double lo = 1.0 - (double)clip_eps, hi = 1.0 + (double)clip_eps;
+      const double s1 = ratio * ad;
+      const double s2 = fmin(fmax(ratio, lo), hi) * ad;
+      double pol, gr;
+      if (s1 < s2) {
+        pol = s1;
+        gr = ad;
+      } else {
+        pol = s2;
+        gr = (ratio >= lo && ratio <= hi) ? ad : 0.0;
+      }
+      const double vd = value - (double)ret[b];
+      total += -pol + (double)cv * vd * vd - (double)ce * ent;
+      s_kl += (ratio - 1.0) - log_ratio;
+      s_pol += pol;
+      s_v += vd * vd;
+      s_ent += ent;
+      if (own) dzk = (-gr * ratio * ((lane == a ? 1.0 : 0.0) - pk) + (double)ce * pk * (lpk + ent)) * invB;
+      dv = 2.0 * (double)cv * vd * invB;
+    }
+    const float dzf = (float)dzk, dvf = (float)dv;
+    // g_pout and this wave's share of the head gradients
+    for (int i = lane; i < d; i += 64) {
+      const float x = pr[i];
+      float g = dvf * Wc[i];
+      for (int k = 0; k < A; ++k) {
+        const float dz = __shfl(dzf, k, 64);
+        g += dz * Wa[(long long)i * A + k];
+        acc[i * A + k] += x * dz;
+      }
+      acc[d * A + A + i] += x * dvf;
+      g_pout[(long long)b * d + i] = g;
+    }
+    if (own) acc[d * A + lane] += dzf;
+    if (lane == 0) acc[R - 1] += dvf;
+  }
+  if (lane == 0) {
+    sl[wv][0] = total;
+    sl[wv][1] = s_kl;
+    sl[wv][2] = s_pol;
+    sl[wv][3] = s_v;
+    sl[wv][4] = s_ent;
+  }
+  __syncthreads();
+  double* P = part + (long long)blockIdx.x * (kLossParts + R);
+  if (threadIdx.x < kLossParts) {
+    double t = 0.0;
+    for (int w = 0; w < kHeadWaves; ++w) t += sl[w][threadIdx.x];
+    P[threadIdx.x] = t;
+  }
+  for (int i = threadIdx.x; i < R; i += blockDim.x) {
+    double t = 0.0;
+    for (int w = 0; w < kHeadWaves; ++w) t += (double)sh[w * R + i];
+    P[kLossParts + i] = t;
+  }
+}
+
+// loss[0] = mean loss, stats (optional) = (or +=) the sums of kl, pol, v, ent and the count, and
+// the head gradients G[0, R) = Wa | ba | Wc | bc: each the fixed-order sum of the workgroups'
+// partials. 1024 threads per workgroup: lane <-> one of 64 consecutive elements, wave w <->
+// partials w, w + 16, ..., combined in LDS in wave order.
+__global__ __launch_bounds__(1024) void ppo_heads_final_kernel(int nblk, int B, int R, const double* __restrict__ part,
+                                                               float* __restrict__ loss, double* __restrict__ stats,
+                                                               int stats_acc, float* __restrict__ G) {
+  __shared__ double red[16][64];
+  const int W = kLossParts + R;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int e = blockIdx.x * 64 + lane;
+  double t = 0.0;
+  if (e < W)
+    for (int k = w; k < nblk; k += 16) t += part[(long long)k * W + e];
+  red[w][lane] = t;
+  __syncthreads();
+  if (w != 0 || e >= W) return;
+  double sum = 0.0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) sum += red[i][lane];
+  if (e >= kLossParts) {
+    G[e - kLossParts] = (float)sum;
+  } else if (e == 0) {
+    if (loss) loss[0] = (float)(sum / (double)B);
+    if (stats) stats[4] = (stats_acc ? stats[4] : 0.0) + (double)B;
+  } else if (stats) {
+    stats[e - 1] = (stats_acc ? stats[e - 1] : 0.0) + sum;
+  }
+}
+
 // loss[0] = mean loss; stats (optional) = (or +=) the sums of kl, pol, v, ent and the count.
 __global__ __launch_bounds__(64) void ppo_loss_final_kernel(int nblk, int B, const double* __restrict__ part,
                                                             float* __restrict__ loss, double* __restrict__ stats,
@@ -881,7 +1028,7 @@ int check_ppo_cfg(const talos_ppo_cfg& c) {
 // Policy forward up to logits / values for c.batch samples (at most the plan's batch); the
 // per-sample lengths of the call are p->lens.
 static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, const float* states,
-                       hipStream_t s) {
+                       hipStream_t s, bool heads = true) {
   const talos_block_cfg bc = block_cfg_of(c);
   const PpoOff po = ppo_offsets(c);
   const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions, ow = attn_width(bc);
@@ -975,6 +1122,7 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
   if (rc) return rc;
   rc = mm(p, s, 0, 0, c.batch, d, d, p->lastn, d, P + po.wout, d, p->pout, d, 0.f, P + po.bout);
   if (rc) return rc;
+  if (!heads) return TALOS_OK;  // the minibatch runs the heads inside ppo_heads_kernel
   rc = mm(p, s, 0, 0, c.batch, A, d, p->pout, d, P + po.wa, A, p->logits, A, 0.f, P + po.ba);
   if (rc) return rc;
   return mm(p, s, 0, 0, c.batch, 1, d, p->pout, d, P + po.wc, 1, p->values, 1, 0.f, P + po.bc);
@@ -1139,7 +1287,9 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
   }
   {  // per-workgroup loss partials (doubles)
     float* lw = nullptr;
-    rc |= plan_alloc(p, &lw, 2 * kLossParts * ceil_div(B, 256));
+    const size_t R = (size_t)cfg->d_model * (A + 1) + A + 1;
+    const size_t heads = (size_t)ceil_div(B, kHeadSamples) * (kLossParts + R);
+    rc |= plan_alloc(p, &lw, 2 * std::max((size_t)kLossParts * ceil_div(B, 256), heads));
     p->loss_ws = reinterpret_cast<double*>(lw);
   }
   if (rc == TALOS_OK) {
@@ -1206,32 +1356,52 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
   const talos_block_cfg bc = block_cfg_of(c);
   const PpoOff po = ppo_offsets(c);
   const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions, B = c.batch;
-  int rc = ppo_forward(p, c, params, states, s);
+  // the heads, loss and their backward in one kernel when the per-wave head gradients fit in LDS
+  const int R = d * (A + 1) + A + 1;
+  const bool fused_heads = R <= kHeadMaxRow;
+  int rc = ppo_forward(p, c, params, states, s, !fused_heads);
   if (rc) return rc;
-  {
-  const int nblk = (int)ceil_div((size_t)B, 256);
-  {
-    ProfScope ps_l(s, "ppo_loss_kernel", 0.0, 4.0 * B * (2.0 * A + 5.0));
-    hipLaunchKernelGGL(ppo_loss_kernel, dim3(nblk), dim3(256), 0, s, B, A, c.clip_eps, c.value_coef,
-                       c.entropy_coef, p->logits, p->values, actions, adv, ret, old_logp, p->g_logits, p->g_values, 1,
-                       p->loss_ws);
-    TALOS_LAUNCHED("ppo_loss_kernel");
-  }
-  ProfScope ps_f(s, "ppo_loss_final_kernel", 0.0, 8.0 * nblk * kLossParts);
-  hipLaunchKernelGGL(ppo_loss_final_kernel, dim3(1), dim3(64), 0, s, nblk, B, p->loss_ws, loss_out, stats,
-                     stats_acc);
-  TALOS_LAUNCHED("ppo_loss_final_kernel");
-  }
   float* G = dparams;
-  // heads
-  rc = mm(p, s, 1, 0, d, A, B, p->pout, d, p->g_logits, A, G + po.wa, A, 0.f, nullptr, nullptr, 0, G + po.ba);
-  if (rc) return rc;
-  rc = mm(p, s, 1, 0, d, 1, B, p->pout, d, p->g_values, 1, G + po.wc, 1, 0.f, nullptr, nullptr, 0, G + po.bc);
-  if (rc) return rc;
-  rc = mm(p, s, 0, 1, B, d, A, p->g_logits, A, params + po.wa, A, p->g_pout, d);
-  if (rc) return rc;
-  rc = mm(p, s, 0, 1, B, d, 1, p->g_values, 1, params + po.wc, 1, p->g_pout, d, 1.f);
-  if (rc) return rc;
+  if (fused_heads) {
+    const int nblk = (int)ceil_div((size_t)B, kHeadSamples);
+    {
+      ProfScope ps_h(s, "ppo_heads_kernel", 4.0 * B * (double)d * (A + 1),
+                     4.0 * (2.0 * B * d + 5.0 * B) + 8.0 * nblk * (kLossParts + R));
+      hipLaunchKernelGGL(ppo_heads_kernel, dim3(nblk), dim3(64 * kHeadWaves), (size_t)kHeadWaves * R * sizeof(float),
+                         s, B, d, A, c.clip_eps, c.value_coef, c.entropy_coef, p->pout, params + po.wa,
+                         params + po.ba, params + po.wc, params + po.bc, actions, adv, ret, old_logp, p->g_pout,
+                         p->loss_ws);
+      TALOS_LAUNCHED("ppo_heads_kernel");
+    }
+    ProfScope ps_f(s, "ppo_heads_final_kernel", 0.0, 8.0 * nblk * (kLossParts + R) + 4.0 * R);
+    hipLaunchKernelGGL(ppo_heads_final_kernel, dim3(ceil_div((size_t)kLossParts + R, 64)), dim3(1024), 0, s, nblk, B,
+                       R, p->loss_ws, loss_out, stats, stats_acc, G + po.wa);
+    TALOS_LAUNCHED("ppo_heads_final_kernel");
+  } else {
+    const int nblk = (int)ceil_div((size_t)B, 256);
+    {
+      ProfScope ps_l(s, "ppo_loss_kernel", 0.0, 4.0 * B * (2.0 * A + 5.0));
+      hipLaunchKernelGGL(ppo_loss_kernel, dim3(nblk), dim3(256), 0, s, B, A, c.clip_eps, c.value_coef,
+                         c.entropy_coef, p->logits, p->values, actions, adv, ret, old_logp, p->g_logits, p->g_values,
+                         1, p->loss_ws);
+      TALOS_LAUNCHED("ppo_loss_kernel");
+    }
+    {
+      ProfScope ps_f(s, "ppo_loss_final_kernel", 0.0, 8.0 * nblk * kLossParts);
+      hipLaunchKernelGGL(ppo_loss_final_kernel, dim3(1), dim3(64), 0, s, nblk, B, p->loss_ws, loss_out, stats,
+                         stats_acc);
+      TALOS_LAUNCHED("ppo_loss_final_kernel");
+    }
+    // heads
+    rc = mm(p, s, 1, 0, d, A, B, p->pout, d, p->g_logits, A, G + po.wa, A, 0.f, nullptr, nullptr, 0, G + po.ba);
+    if (rc) return rc;
+    rc = mm(p, s, 1, 0, d, 1, B, p->pout, d, p->g_values, 1, G + po.wc, 1, 0.f, nullptr, nullptr, 0, G + po.bc);
+    if (rc) return rc;
+    rc = mm(p, s, 0, 1, B, d, A, p->g_logits, A, params + po.wa, A, p->g_pout, d);
+    if (rc) return rc;
+    rc = mm(p, s, 0, 1, B, d, 1, p->g_values, 1, params + po.wc, 1, p->g_pout, d, 1.f);
+    if (rc) return rc;
+  }
   // out_proj
   rc = mm(p, s, 1, 0, d, d, B, p->lastn, d, p->g_pout, d, G + po.wout, d, 0.f, nullptr, nullptr, 0, G + po.bout);
   if (rc) return rc;
