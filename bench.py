@@ -256,6 +256,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--profile-table", action="store_true", help="print the per-kernel table to stderr")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="only the C4 line (no optimizer, reference-model or rollout lines): the command to run "
+                         "under rocprofv3, so that its per-kernel averages cover the headline step alone")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB device-to-device 5 times: the known-size "
                          "copy that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -348,9 +351,10 @@ def main():
                     for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3])},
         "device": info["name"],
     }
-    out["optimizer"] = optimizer_line(P, dP, args.steps)
-    out["reference_model"] = reference_model_line(args.steps)
-    out["rollout"] = rollout_line(args.steps, cpu=rank == 0 and not args.no_cpu_baseline)
+    if not args.headline_only:
+        out["optimizer"] = optimizer_line(P, dP, args.steps)
+        out["reference_model"] = reference_model_line(args.steps)
+        out["rollout"] = rollout_line(args.steps, cpu=rank == 0 and not args.no_cpu_baseline)
     if args.profile_table:
         for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3]):
             print(f"{k:40s} n={v[0]:3d} {v[3]:8.3f} ms  {v[1] / max(v[3], 1e-9) / 1e9:8.2f} TFLOP/s "
