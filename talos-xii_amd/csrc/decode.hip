@@ -8,16 +8,22 @@
 // Each environment's cache is a ring of cap = window + 1 rows per layer and head: a step attends
 // over the rows held plus the new token (at most window + 1), then the oldest row is dropped when
 // more than window remain, as the reference appends first and prunes afterwards. Layout per
-// layer: K [env][head][cap][dk], V [env][head][cap][dv], so a head's rows are contiguous; one
-// length and ring start per environment serve every layer.
-//
-// The projections run as GEMMs over the n environments' rows (M = n); the cached attention is
-// one wave per (environment, head): it rotates the new q / k at the environment's position,
-// stores k / v into the ring and attends over the ring. Positions whose RoPE table entry lies
-// past max_seq_len are not rotated, as the reference's inference path skips them
+// layer: V [env][head][cap][dv] and K [env][head][cap][dk] (layered step) or
+// [env][head][dk / 4][cap][4] (one-launch step), so a head's rows are contiguous; one length and
+// ring start per environment serve every layer. Positions whose RoPE table entry lies past
+// max_seq_len are not rotated, as the reference's inference path skips them
 // (src/transformer.rs:718-721).
+//
+// Two implementations of the step, chosen when the decoder is created:
+//  * the one-launch step (decode_fused_kernel) for the shapes it is instantiated for: every
+//    phase of the step in one kernel, 16 environments per workgroup;
+//  * the layered step (decode_step) for any configuration: the projections as GEMMs over the n
+//    environments' rows (M = n) and the cached attention as one wave per (environment, head),
+//    which rotates the new q / k, stores k / v into the ring and attends over the ring.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <type_traits>
 #include <vector>
 
 #include "gemm.hpp"
@@ -37,6 +43,8 @@ struct talos_decoder_s {
   float *x = nullptr, *y = nullptr, *xn = nullptr, *rstd = nullptr, *qkv = nullptr, *ckv = nullptr, *kcn = nullptr,
         *vn = nullptr, *qc = nullptr, *qr = nullptr, *kr = nullptr, *o = nullptr, *h2 = nullptr, *a = nullptr,
         *pout = nullptr, *logits = nullptr, *values = nullptr;
+  // the one-launch step (small policies): chosen at creation, with its LDS layout in floats
+  bool fused = false;  // the one-launch step applies (chosen at creation); its K cache is slot-minor
 };
 
 namespace talos {
@@ -204,16 +212,12 @@ __global__ void decode_advance_kernel(int n, int window, int cap, int32_t* __res
 // Probabilities in f64 with the reference's max start of -1e9, the first action whose
 // probability exceeds the remaining draw (0 when none does: the reference's index starts at 0 and
 // its ACTION_SPACE fallback never fires), ln p of the action (src/ppo.rs:401-432).
-__global__ void decode_sample_kernel(int n, int A, const float* __restrict__ logits, const float* __restrict__ u,
-                                     int32_t* __restrict__ actions, float* __restrict__ logp) {
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= n) return;
-  const float* z = logits + (long long)e * A;
+__device__ void sample_action(const float* z, int A, float u, int32_t* action, float* logp) {
   double mx = -1e9;
   for (int i = 0; i < A; ++i) mx = fmax(mx, (double)z[i]);
   double sum = 0.0;
   for (int i = 0; i < A; ++i) sum += exp((double)z[i] - mx);
-  double r = (double)u[e];
+  double r = (double)u;
   int act = 0;
   for (int i = 0; i < A; ++i) {
     const double p = exp((double)z[i] - mx) / sum;
@@ -223,8 +227,14 @@ __global__ void decode_sample_kernel(int n, int A, const float* __restrict__ log
     }
     r -= p;
   }
-  if (actions) actions[e] = act;
-  if (logp) logp[e] = (float)log(exp((double)z[act] - mx) / sum);
+  if (action) *action = act;
+  if (logp) *logp = (float)log(exp((double)z[act] - mx) / sum);
+}
+__global__ void decode_sample_kernel(int n, int A, const float* __restrict__ logits, const float* __restrict__ u,
+                                     int32_t* __restrict__ actions, float* __restrict__ logp) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  sample_action(logits + (long long)e * A, A, u[e], actions ? actions + e : nullptr, logp ? logp + e : nullptr);
 }
 
 int dmm(hipStream_t s, int M, int N, int K, const float* A, long long lda, const float* B, long long ldb, float* C,
@@ -246,6 +256,549 @@ int dmm(hipStream_t s, int M, int N, int K, const float* A, long long lda, const
   g.act = act;
   g.ksplit = 1;
   return gemm_launch(g, s);
+}
+
+// ---- The one-launch step --------------------------------------------------------------------
+// For the shapes it is instantiated for (the reference ActorCritic's, FusedShape below) and
+// windows up to kFusedMaxWindow, the whole step is one kernel: a workgroup of four waves owns 16
+// environments, keeps their activations in LDS through every layer and reads each weight once per
+// workgroup from L2. The products run on the fp32 matrix cores with the 16 environments as the
+// rows of one 16x16 tile; every dimension is a compile-time constant, so a lane issues all of its
+// weight loads before the first product. The phases are those of the layered path (decode_step
+// below), in the same order, separated by workgroup barriers instead of launches.
+constexpr int kFusedMaxWindow = 32;
+constexpr int kFusedEnvs = 16;  // the rows of a v_mfma_f32_16x16x4f32 tile
+constexpr int kFusedThreads = 256;
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int IN_, int D_, int H_, int HD_, int R_, int VD_, int LT_, int F_, int A_, bool MLA_>
+struct FusedShape {
+  static constexpr int IN = IN_, D = D_, H = H_, HD = HD_, R = R_, VD = VD_, LT = LT_, F = F_, A = A_;
+  static constexpr bool MLA = MLA_;
+  static constexpr int DK = MLA ? HD + R : HD, DV = MLA ? VD : HD;
+  static constexpr int ROPE_OFF = MLA ? HD : 0, ROPE = MLA ? R : HD;
+};
+// ActorCritic::new (src/ppo.rs:254-258): in_dim 8, d 64, MLA with 4 heads (content 16, rope 16,
+// value 16, latent 32), ffn 128, 5 actions
+using RefActorCritic = FusedShape<8, 64, 4, 16, 16, 16, 32, 128, 5, true>;
+
+template <class SH>
+bool fused_shape_matches(const talos_ppo_cfg& c) {
+  const bool mla = c.attention == TALOS_ATTN_MLA;
+  return mla == SH::MLA && c.in_dim == SH::IN && c.d_model == SH::D && c.n_heads == SH::H &&
+         c.head_dim == SH::HD && c.ffn_dim == SH::F && c.n_actions == SH::A &&
+         (!mla || (c.rope_dim == SH::R && c.v_dim == SH::VD && c.kv_latent == SH::LT));
+}
+
+struct FusedArgs {
+  int n, layers, cap, window, max_pos, relu;
+  float eps, scale;
+  const float* P;
+  const float *tokens, *u;
+  const int32_t* pos;
+  const uint8_t* reset;
+  float *logits, *values, *logp;
+  int32_t* actions;
+  int32_t *len, *head;
+  float *kc, *vc;                // layer-major caches
+  long long kc_layer, vc_layer;  // floats per layer
+  const float *rcos, *rsin;
+  // parameter offsets: embedding and heads; layer 0's block and the stride between layers
+  long long we, be, gf, wout, bout, wa, ba, wc, bc, lstride;
+  long long g1, g2, w1, b1, w2, b2, wo, wqkv, wdkv, wuk, wuv, wq, wkr, wqr;
+};
+
+// out(e, n, sum_k X[e][k] W[k][n] (+ bias[n])) for the workgroup's 16 environments on the matrix
+// cores. The 16-column tiles of Y go round the waves (tile t to wave (t + WOFF) % 4); for the 16 k
+// of group g a lane (row i = lane % 16, quad kq = lane / 16) reads X[i][16g + 4kq .. +3] as one
+// float4 from LDS and feeds the four v_mfma_f32_16x16x4f32 of the group (product u takes
+// k = 16g + 4kq + u) with B = W[16g + 4kq + u][n]. The result tile holds D[4kq + r][lane % 16] in
+// register r. K % 4 == 0; k past K (K % 16 != 0) and columns past N contribute zeros.
+//
+// The lane's weights (K / 4 a tile) and bias are loaded by FmmW::load, a phase or more before
+// fmm_run uses them, so the loads of the next product are in flight while the current phase runs.
+template <int K, int N, int LDW, int WOFF = 0>
+struct FmmW {
+  static constexpr int TILES = (N + 15) / 16, WAVES = kFusedThreads / 64, TPW = (TILES + WAVES - 1) / WAVES;
+  static constexpr int KG = (K + 15) / 16;
+  float w[TPW][4 * KG];
+  float b[TPW];
+  bool has_bias;
+  __device__ __forceinline__ static int tile_of(int tp) {
+    return ((int)(threadIdx.x >> 6) + WAVES - WOFF % WAVES) % WAVES + tp * WAVES;
+  }
+  __device__ __forceinline__ void load(const float* __restrict__ W, const float* __restrict__ bias) {
+    const int row = threadIdx.x & 15, kq = (threadIdx.x >> 4) & 3;
+    has_bias = bias != nullptr;
+#pragma unroll
+    for (int tp = 0; tp < TPW; ++tp) {
+      const int t = tile_of(tp), n = t * 16 + row;
+      const bool nv = t < TILES && n < N;
+#pragma unroll
+      for (int g = 0; g < KG; ++g)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int k = 16 * g + 4 * kq + u;
+          w[tp][4 * g + u] = nv && k < K ? W[k * LDW + n] : 0.f;
+        }
+      b[tp] = nv && bias ? bias[n] : 0.f;
+    }
+  }
+};
+template <int K, int N, int LDX, int LDW, int WOFF, class Out>
+__device__ __forceinline__ void fmm_run(const float* X, const FmmW<K, N, LDW, WOFF>& wt, Out out) {
+  static_assert(K % 4 == 0 && LDX % 4 == 0, "float4 rows");
+  using FW = FmmW<K, N, LDW, WOFF>;
+  const int row = threadIdx.x & 15, kq = (threadIdx.x >> 4) & 3;
+#pragma unroll
+  for (int tp = 0; tp < FW::TPW; ++tp) {
+    const int t = FW::tile_of(tp), n = t * 16 + row;
+    if (t >= FW::TILES) continue;  // wave-uniform
+    floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < FW::KG; ++g) {
+      const int k = 16 * g + 4 * kq;
+      const float4 xa = k < K ? *reinterpret_cast<const float4*>(X + row * LDX + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      floatx4& acc = (g & 1) ? acc1 : acc0;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, wt.w[tp][4 * g], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.y, wt.w[tp][4 * g + 1], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.z, wt.w[tp][4 * g + 2], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, wt.w[tp][4 * g + 3], acc, 0, 0, 0);
+    }
+    if (n < N) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float sum = acc0[r] + acc1[r];
+        out(4 * kq + r, n, wt.has_bias ? sum + wt.b[tp] : sum);
+      }
+    }
+  }
+}
+
+// Sum over aligned groups of W adjacent lanes (W a power of two <= 16) with DPP lane moves, every
+// lane of a group getting its sum; all lanes of the wave must be active.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(W >= 1 && W <= 16 && (W & (W - 1)) == 0, "group width");
+  auto dpp = [](float x, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xF, 0xF, false));
+  };
+  if constexpr (W >= 2) v += dpp(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+  if constexpr (W >= 4) v += dpp(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+  if constexpr (W >= 8) v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  if constexpr (W >= 16) v += dpp(v, std::integral_constant<int, 0x140>{});  // row_mirror
+  return v;
+}
+
+// y = x / sqrt(mean(x^2) + eps) * g over the workgroup's rows, 16 lanes per row; the lane's gains
+// are loaded by NormG::load ahead of the phase.
+template <int D>
+struct NormG {
+  static constexpr int LPR = kFusedThreads / kFusedEnvs, PER = (D + LPR - 1) / LPR;
+  float g[PER];
+  __device__ __forceinline__ void load(const float* __restrict__ gain) {
+    const int l = threadIdx.x % LPR;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) g[j] = l + j * LPR < D ? gain[l + j * LPR] : 0.f;
+  }
+};
+template <int D, int LD>
+__device__ __forceinline__ void fnorm(const float* x, float* y, float eps, const NormG<D>& gn) {
+  constexpr int LPR = NormG<D>::LPR, PER = NormG<D>::PER;
+  const int row = threadIdx.x / LPR, l = threadIdx.x % LPR;
+  float xv[PER];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = l + j * LPR;
+    xv[j] = c < D ? x[row * LD + c] : 0.f;
+    ss = fmaf(xv[j], xv[j], ss);
+  }
+  ss = group_sum<LPR>(ss);
+  const float r = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = l + j * LPR;
+    if (c < D) y[row * LD + c] = xv[j] * r * gn.g[j];
+  }
+}
+
+template <class SH>
+__global__ __launch_bounds__(kFusedThreads) void decode_fused_kernel(FusedArgs a) {
+  constexpr int T = kFusedThreads, E = kFusedEnvs;
+  constexpr int D = SH::D, H = SH::H, DK = SH::DK, DV = SH::DV, F = SH::F, A = SH::A, IN = SH::IN;
+  constexpr int LDD = D + 4, LDQ = H * DK + 4, LDV = H * DV + 4, LDF = F + 4, LDI = IN + 4, LDC = SH::LT + 4;
+  constexpr int CAPM = kFusedMaxWindow + 1, NF4 = DK / 4, NV4 = DV / 4;
+  static_assert(LDQ >= LDD && DK % 4 == 0 && DV % 4 == 0 && (NF4 & (NF4 - 1)) == 0 && NF4 <= 64, "layout");
+  __shared__ __align__(16) float x[E * LDD], xn[E * LDD], qh[E * (LDQ > LDF ? LDQ : LDF)], k[E * LDQ];
+  __shared__ __align__(16) float v[E * LDV], o[E * LDV], ckv[E * LDC], tok[E * LDI], lg[E * A];
+  __shared__ float pr[E * H * CAPM], inv[E * H];
+  __shared__ int slen[E], shead[E], spos[E];
+  float* q = qh;
+  float* hid = qh;  // the FFN rows reuse q's (dead after the attention) with stride LDF
+  float* pout = k;  // the out_proj rows reuse k's with stride LDD
+  const int env0 = blockIdx.x * E, tid = threadIdx.x, cap = a.cap;
+  const float* P = a.P;
+  if (tid < E) {
+    const int e = env0 + tid;
+    const bool on = e < a.n;
+    int l = on ? a.len[e] : -1, h = on ? a.head[e] : 0;
+    if (on && a.reset && a.reset[e]) {
+      l = 0;
+      h = 0;
+    }
+    slen[tid] = l;  // -1 marks an environment past n
+    shead[tid] = h;
+    spos[tid] = on ? a.pos[e] : -1;
+  }
+  for (int idx = tid; idx < E * IN; idx += T) {
+    const int e = idx / IN, c = idx % IN;
+    tok[e * LDI + c] = env0 + e < a.n ? a.tokens[(long long)(env0 + e) * IN + c] : 0.f;
+  }
+  // the first phases' weights and gains, in flight during the set-up
+  FmmW<IN, D, D> w_emb;
+  w_emb.load(P + a.we, P + a.be);
+  NormG<D> gn;
+  gn.load(P + a.g1);
+  __syncthreads();
+  // this thread's RoPE items (environment, head, pair) and their factors, reused by every layer;
+  // positions outside the table are not rotated (src/transformer.rs:718-721)
+  constexpr int HALF = SH::ROPE / 2, NROT = E * H * HALF, ROT_PER = (NROT + T - 1) / T;
+  float rc[ROT_PER], rs[ROT_PER];
+  bool rot[ROT_PER];
+#pragma unroll
+  for (int t = 0; t < ROT_PER; ++t) {
+    const int idx = tid + t * T, e = idx / (H * HALF), m = idx % HALF;
+    const int p = idx < NROT ? spos[e] : -1;
+    rot[t] = p >= 0 && p < a.max_pos;
+    rc[t] = rot[t] ? a.rcos[p * HALF + m] : 1.f;
+    rs[t] = rot[t] ? a.rsin[p * HALF + m] : 0.f;
+  }
+  constexpr int HD = SH::HD, R = SH::MLA ? SH::R : 1, LT = SH::MLA ? SH::LT : 4;
+  // the attention's input products: MLA's down-projection and the q / k_rope projections, or W_qkv
+  // as three column blocks of [d][3d]
+  FmmW<D, LT, LT, 2> w_dkv;
+  FmmW<D, H * HD, (SH::MLA ? H * HD : 3 * D)> w_q;
+  FmmW<D, H * R, H * R> w_qr, w_kr;
+  FmmW<D, D, 3 * D> w_k, w_v;
+  auto load_in = [&](const float* B) {
+    if constexpr (SH::MLA) {
+      w_dkv.load(B + a.wdkv, nullptr);
+      w_q.load(B + a.wq, nullptr);
+      w_qr.load(B + a.wqr, nullptr);
+      w_kr.load(B + a.wkr, nullptr);
+    } else {
+      w_q.load(B + a.wqkv, nullptr);
+      w_k.load(B + a.wqkv + D, nullptr);
+      w_v.load(B + a.wqkv + 2 * D, nullptr);
+    }
+  };
+  load_in(P + a.lstride * 0);
+  fmm_run<IN, D, LDI>(tok, w_emb, [&](int e, int n, float s) { x[e * LDD + n] = s; });
+  __syncthreads();
+  for (int l = 0; l < a.layers; ++l) {
+    const float* B = P + l * a.lstride;
+    fnorm<D, LDD>(x, xn, a.eps, gn);
+    __syncthreads();
+    FmmW<LT, H * HD, H * HD> w_uk;
+    FmmW<LT, H * DV, H * DV, 2> w_uv;
+    if constexpr (SH::MLA) {
+      w_uk.load(B + a.wuk, nullptr);
+      w_uv.load(B + a.wuv, nullptr);
+      fmm_run<D, LT, LDD>(xn, w_dkv, [&](int e, int n, float s) { ckv[e * LDC + n] = s; });
+      fmm_run<D, H * HD, LDD>(xn, w_q, [&](int e, int n, float s) { q[e * LDQ + (n / HD) * DK + n % HD] = s; });
+      fmm_run<D, H * R, LDD>(xn, w_qr, [&](int e, int n, float s) { q[e * LDQ + (n / R) * DK + HD + n % R] = s; });
+      fmm_run<D, H * R, LDD>(xn, w_kr, [&](int e, int n, float s) { k[e * LDQ + (n / R) * DK + HD + n % R] = s; });
+      __syncthreads();
+      fmm_run<LT, H * HD, LDC>(ckv, w_uk, [&](int e, int n, float s) { k[e * LDQ + (n / HD) * DK + n % HD] = s; });
+      fmm_run<LT, H * DV, LDC>(ckv, w_uv, [&](int e, int n, float s) { v[e * LDV + n] = s; });
+    } else {
+      fmm_run<D, D, LDD>(xn, w_q, [&](int e, int n, float s) { q[e * LDQ + n] = s; });
+      fmm_run<D, D, LDD>(xn, w_k, [&](int e, int n, float s) { k[e * LDQ + n] = s; });
+      fmm_run<D, D, LDD>(xn, w_v, [&](int e, int n, float s) { v[e * LDV + n] = s; });
+    }
+    __syncthreads();
+    // RoPE on the new q / k rows: (x0, x1) -> (x0 c - x1 s, x0 s + x1 c), src/transformer.rs:724-733
+#pragma unroll
+    for (int t = 0; t < ROT_PER; ++t) {
+      const int idx = tid + t * T;
+      if (idx < NROT && rot[t]) {
+        const int e = idx / (H * HALF), h = (idx / HALF) % H, m = idx % HALF;
+        const int at = e * LDQ + h * DK + SH::ROPE_OFF + 2 * m;
+        const float q0 = q[at], q1 = q[at + 1], k0 = k[at], k1 = k[at + 1];
+        q[at] = fmaf(q0, rc[t], -q1 * rs[t]);
+        q[at + 1] = fmaf(q0, rs[t], q1 * rc[t]);
+        k[at] = fmaf(k0, rc[t], -k1 * rs[t]);
+        k[at + 1] = fmaf(k0, rs[t], k1 * rc[t]);
+      }
+    }
+    __syncthreads();
+    float* kc = a.kc + l * a.kc_layer;
+    float* vc = a.vc + l * a.vc_layer;
+    // the new k / v rows into the ring slot after the held rows
+    for (int idx = tid; idx < E * H * (NF4 + NV4); idx += T) {
+      const int e = idx / (H * (NF4 + NV4)), hc = idx % (H * (NF4 + NV4));
+      if (slen[e] < 0) continue;
+      const int slot = (shead[e] + slen[e]) % cap;
+      if (hc < H * NF4) {  // K is slot-minor: [env][head][DK / 4][slot] of float4
+        const int h = hc / NF4, c4 = hc % NF4;
+        *reinterpret_cast<float4*>(kc + ((((long long)(env0 + e) * H + h) * NF4 + c4) * cap + slot) * 4) =
+            *reinterpret_cast<const float4*>(k + e * LDQ + h * DK + 4 * c4);
+      } else {
+        const int h = (hc - H * NF4) / NV4, c4 = (hc - H * NF4) % NV4;
+        *reinterpret_cast<float4*>(vc + (((long long)(env0 + e) * H + h) * cap + slot) * DV + 4 * c4) =
+            *reinterpret_cast<const float4*>(v + e * LDV + h * DV + 4 * c4);
+      }
+    }
+    // scores of the held rows: a lane per (environment, head, slot) of the workgroup's region,
+    // IB of them at once with all their K loads issued before the first product. K is slot-minor,
+    // so for each quarter-row c4 the lanes of consecutive slots read consecutive float4s
+    // (coalesced) and a lane sums its own row, with the q quarter-rows read from LDS. A slot
+    // outside the held rows (empty, or the new row's) is dropped. Item i is
+    // (e * H + h, slot) = (i / cap, i % cap), the quotient taken in fp32 from (i + 0.5) / cap
+    // (i < 2^16, cap <= 33: the rounding error is far below the 0.5 / cap margin).
+    {
+      constexpr int IB = (E * H * CAPM + T - 1) / T < 5 ? (E * H * CAPM + T - 1) / T : 5;
+      const int n_on = min(E, a.n - env0), items = n_on * H * cap;
+      const float4* kreg = reinterpret_cast<const float4*>(kc + (long long)env0 * H * NF4 * cap * 4);
+      const float rcap = 1.0f / (float)cap;
+      for (int i0 = tid; i0 < items; i0 += IB * T) {
+        float4 kb[IB][NF4];
+        int eh[IB], slot[IB];
+#pragma unroll
+        for (int b = 0; b < IB; ++b) {
+          const int i = i0 + b * T;
+          const bool on = i < items;
+          eh[b] = on ? (int)(((float)i + 0.5f) * rcap) : 0;
+          slot[b] = i - eh[b] * cap;
+          const float4* kr = kreg + (long long)eh[b] * NF4 * cap + slot[b];
+#pragma unroll
+          for (int c4 = 0; c4 < NF4; ++c4) kb[b][c4] = on ? kr[c4 * cap] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int b = 0; b < IB; ++b) {
+          if (i0 + b * T >= items) continue;
+          const int e = eh[b] / H, hd0 = shead[e], j = slot[b] - hd0 + (slot[b] < hd0 ? cap : 0);
+          if (j >= slen[e]) continue;
+          const float* qr = q + e * LDQ + (eh[b] - e * H) * DK;
+          float sc = 0.f;
+#pragma unroll
+          for (int c4 = 0; c4 < NF4; ++c4) {
+            const float4 q4 = *reinterpret_cast<const float4*>(qr + 4 * c4);
+            sc = fmaf(q4.x, kb[b][c4].x, sc);
+            sc = fmaf(q4.y, kb[b][c4].y, sc);
+            sc = fmaf(q4.z, kb[b][c4].z, sc);
+            sc = fmaf(q4.w, kb[b][c4].w, sc);
+          }
+          pr[eh[b] * CAPM + j] = sc * a.scale;
+        }
+      }
+    }
+    // the new row's score, from LDS
+    for (int idx = tid; idx < E * H; idx += T) {
+      const int e = idx / H, h = idx % H;
+      if (slen[e] < 0) continue;
+      float sc = 0.f;
+#pragma unroll
+      for (int i = 0; i < DK; ++i) sc = fmaf(q[e * LDQ + h * DK + i], k[e * LDQ + h * DK + i], sc);
+      pr[idx * CAPM + slen[e]] = sc * a.scale;
+    }
+    __syncthreads();
+    FmmW<H * DV, D, D> w_o;
+    w_o.load(B + a.wo, nullptr);
+    for (int idx = tid; idx < E * H; idx += T) {
+      const int rows = slen[idx / H] + 1;
+      float* p = pr + idx * CAPM;
+      float sv[CAPM];
+      float mx = -INFINITY, sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < CAPM; ++j) {
+        sv[j] = j < rows ? p[j] : -INFINITY;
+        mx = fmaxf(mx, sv[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < CAPM; ++j) {
+        if (j < rows) {
+          const float ex = __expf(sv[j] - mx);
+          p[j] = ex;
+          sum += ex;
+        }
+      }
+      inv[idx] = rows > 0 ? 1.f / sum : 0.f;
+    }
+    __syncthreads();
+    // P.V: a thread per (environment, head, 4 columns) loads all of its held rows before the
+    // first product (window <= kFusedMaxWindow)
+    for (int idx = tid; idx < E * H * NV4; idx += T) {
+      const int e = idx / (H * NV4), h = (idx / NV4) % H, c4 = idx % NV4;
+      const int rows = slen[e] + 1, hd0 = shead[e];
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (rows > 0) {
+        const float* p = pr + (e * H + h) * CAPM;
+        const float4* vb = reinterpret_cast<const float4*>(vc + ((long long)(env0 + e) * H + h) * cap * DV) + c4;
+        float4 vr[kFusedMaxWindow];
+#pragma unroll
+        for (int j = 0; j < kFusedMaxWindow; ++j) {
+          const int slot = hd0 + j - (hd0 + j >= cap ? cap : 0);
+          vr[j] = j < rows - 1 ? vb[slot * NV4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < kFusedMaxWindow; ++j) {
+          if (j < rows - 1) {
+            const float pj = p[j];
+            acc.x = fmaf(pj, vr[j].x, acc.x);
+            acc.y = fmaf(pj, vr[j].y, acc.y);
+            acc.z = fmaf(pj, vr[j].z, acc.z);
+            acc.w = fmaf(pj, vr[j].w, acc.w);
+          }
+        }
+        const float pl = p[rows - 1], iv = inv[e * H + h];
+        const float4 vn = *reinterpret_cast<const float4*>(v + e * LDV + h * DV + 4 * c4);
+        acc.x = fmaf(pl, vn.x, acc.x) * iv;
+        acc.y = fmaf(pl, vn.y, acc.y) * iv;
+        acc.z = fmaf(pl, vn.z, acc.z) * iv;
+        acc.w = fmaf(pl, vn.w, acc.w) * iv;
+      }
+      *reinterpret_cast<float4*>(o + e * LDV + h * DV + 4 * c4) = acc;
+    }
+    __syncthreads();
+    // h2 = x + o.Wo
+    gn.load(B + a.g2);
+    fmm_run<H * DV, D, LDV>(o, w_o, [&](int e, int n, float s) { x[e * LDD + n] = s + x[e * LDD + n]; });
+    __syncthreads();
+    FmmW<D, F, F> w_1;
+    w_1.load(B + a.w1, B + a.b1);
+    fnorm<D, LDD>(x, xn, a.eps, gn);
+    __syncthreads();
+    FmmW<F, D, D> w_2;
+    w_2.load(B + a.w2, B + a.b2);
+    const bool relu = a.relu;
+    fmm_run<D, F, LDD>(xn, w_1, [&](int e, int n, float s) { hid[e * LDF + n] = relu ? fmaxf(s, 0.f) : gelu_f(s); });
+    __syncthreads();
+    // x = h2 + act(.).W2 + b2; the next layer's (or the final) gains and input products in flight
+    const bool more = l + 1 < a.layers;
+    gn.load(more ? B + a.lstride + a.g1 : P + a.gf);
+    if (more) load_in(B + a.lstride);
+    fmm_run<F, D, LDF>(hid, w_2, [&](int e, int n, float s) { x[e * LDD + n] = s + x[e * LDD + n]; });
+    __syncthreads();
+  }
+  FmmW<D, D, D> w_out;
+  w_out.load(P + a.wout, P + a.bout);
+  fnorm<D, LDD>(x, xn, a.eps, gn);
+  __syncthreads();
+  FmmW<D, A, A> w_a;
+  FmmW<D, 1, 1, 1> w_c;
+  w_a.load(P + a.wa, P + a.ba);
+  if (a.values) w_c.load(P + a.wc, P + a.bc);
+  fmm_run<D, D, LDD>(xn, w_out, [&](int e, int n, float s) { pout[e * LDD + n] = s; });
+  __syncthreads();
+  {
+    float* logits = a.logits;
+    float* values = a.values;
+    const int n_env = a.n;
+    fmm_run<D, A, LDD>(pout, w_a, [&](int e, int n, float s) {
+      lg[e * A + n] = s;
+      if (logits && env0 + e < n_env) logits[(long long)(env0 + e) * A + n] = s;
+    });
+    if (values)
+      fmm_run<D, 1, LDD>(pout, w_c, [&](int e, int n, float s) {
+        if (env0 + e < n_env) values[env0 + e] = s;
+      });
+  }
+  __syncthreads();
+  if (tid < E && env0 + tid < a.n) {
+    const int e = env0 + tid;
+    if (a.actions || a.logp)
+      sample_action(lg + tid * A, A, a.u[e], a.actions ? a.actions + e : nullptr, a.logp ? a.logp + e : nullptr);
+    // the new row is held, then the oldest dropped past the window
+    const int l = slen[tid] + 1;
+    if (l > a.window) {
+      a.head[e] = (shead[tid] + 1) % cap;
+      a.len[e] = a.window;
+    } else {
+      a.head[e] = shead[tid];
+      a.len[e] = l;
+    }
+  }
+}
+
+// The one-launch step applies: an instantiated shape and a window within kFusedMaxWindow.
+bool fused_applies(const talos_ppo_cfg& c, int window) {
+  return window <= kFusedMaxWindow && fused_shape_matches<RefActorCritic>(c);
+}
+
+int decode_step_fused(talos_decoder_s* D, int n, const float* P, const float* tokens, const int32_t* pos,
+                      const uint8_t* reset, const float* uniforms, float* logits, float* values, int32_t* actions,
+                      float* logp, hipStream_t s) {
+  using SH = RefActorCritic;
+  const talos_ppo_cfg& c = D->cfg;
+  talos_block_cfg bc = D->bc;
+  bc.batch = n;
+  bc.seq = 1;
+  const PpoOff po = ppo_offsets(c);
+  const BlockOff b0 = block_offsets(bc, po.blocks);
+  FusedArgs a{};
+  a.n = n;
+  a.layers = c.n_layers;
+  a.cap = D->cap;
+  a.window = D->window;
+  a.max_pos = D->max_seq_len;
+  a.relu = c.activation == TALOS_ACT_RELU;
+  a.eps = c.eps;
+  a.scale = (float)(1.0 / std::sqrt((double)D->dk));
+  a.P = P;
+  a.tokens = tokens;
+  a.u = uniforms;
+  a.pos = pos;
+  a.reset = reset;
+  a.logits = logits;
+  a.values = values;
+  a.logp = logp;
+  a.actions = actions;
+  a.len = D->len;
+  a.head = D->head;
+  a.kc = D->kc[0];
+  a.vc = D->vc[0];
+  a.kc_layer = (long long)D->n_envs * c.n_heads * a.cap * D->dk;
+  a.vc_layer = (long long)D->n_envs * c.n_heads * a.cap * D->dv;
+  a.rcos = D->rcos;
+  a.rsin = D->rsin;
+  a.we = po.we;
+  a.be = po.be;
+  a.gf = po.gf;
+  a.wout = po.wout;
+  a.bout = po.bout;
+  a.wa = po.wa;
+  a.ba = po.ba;
+  a.wc = po.wc;
+  a.bc = po.bc;
+  a.lstride = (long long)(b0.end - po.blocks);
+  a.g1 = b0.g1;
+  a.g2 = b0.g2;
+  a.w1 = b0.w1;
+  a.b1 = b0.b1;
+  a.w2 = b0.w2;
+  a.b2 = b0.b2;
+  a.wo = b0.wo;
+  a.wqkv = b0.wqkv;
+  a.wdkv = b0.mla.wdkv;
+  a.wuk = b0.mla.wuk;
+  a.wuv = b0.mla.wuv;
+  a.wq = b0.mla.wq;
+  a.wkr = b0.mla.wkr;
+  a.wqr = b0.mla.wqr;
+  const double d = SH::D, F = SH::F, H = SH::H, A = SH::A;
+  const double attn_macs = SH::MLA ? d * SH::LT + SH::LT * H * (SH::HD + SH::DV) + d * H * (SH::HD + 2.0 * SH::R)
+                                   : 3.0 * d * d;
+  const double macs = SH::IN * d + c.n_layers * (attn_macs + H * SH::DV * d + 2.0 * d * F) + d * d + d * (A + 1);
+  // algorithmic bytes: the held cache rows read and the new rows written (every layer), the
+  // weights once, tokens and positions in, logits / value / action / log-prob out
+  const double cache = 4.0 * n * H * c.n_layers * (double)a.cap * (SH::DK + SH::DV);
+  ProfScope ps(s, "decode_fused_kernel", 2.0 * n * macs, cache + 4.0 * po.end + 4.0 * n * (SH::IN + A + 5));
+  hipLaunchKernelGGL((decode_fused_kernel<SH>), dim3(ceil_div((size_t)n, kFusedEnvs)), dim3(kFusedThreads), 0, s,
+                     a);
+  TALOS_LAUNCHED("decode_fused_kernel");
+  return TALOS_OK;
 }
 
 int decode_step(talos_decoder_s* D, int n, const float* P, const float* tokens, const int32_t* pos,
@@ -400,14 +953,19 @@ int talos_ppo_decoder_create(const talos_ppo_cfg* cfg, int n_envs, int context_l
   D->dk = dk;
   D->dv = dv;
   D->ow = attn_width(bc);
+  // the one-launch step where its limits allow; TALOS_DECODER_LAYERED=1 keeps the layered path
+  const char* layered = std::getenv("TALOS_DECODER_LAYERED");
+  D->fused = fused_applies(c, context_len) && !(layered && layered[0] == '1');
   const size_t n = (size_t)n_envs, d = c.d_model, F = c.ffn_dim, H = c.n_heads;
   int rc = 0;
-  for (int l = 0; l < c.n_layers; ++l) {
+  {  // one layer-major block each for K and V
     float *k = nullptr, *v = nullptr;
-    rc |= dec_alloc_n(D, &k, n * H * cap * dk);
-    rc |= dec_alloc_n(D, &v, n * H * cap * dv);
-    D->kc.push_back(k);
-    D->vc.push_back(v);
+    rc |= dec_alloc_n(D, &k, (size_t)c.n_layers * n * H * cap * dk);
+    rc |= dec_alloc_n(D, &v, (size_t)c.n_layers * n * H * cap * dv);
+    for (int l = 0; rc == TALOS_OK && l < c.n_layers; ++l) {
+      D->kc.push_back(k + (size_t)l * n * H * cap * dk);
+      D->vc.push_back(v + (size_t)l * n * H * cap * dv);
+    }
   }
   rc |= dec_alloc_n(D, &D->len, n);
   rc |= dec_alloc_n(D, &D->head, n);
@@ -460,6 +1018,9 @@ int talos_ppo_decoder_step_f32(talos_decoder dec, int n, const float* params, co
   TALOS_REQUIRE(uniforms != nullptr || (actions == nullptr && logp == nullptr), TALOS_ERR_NULL,
                 "%s: actions / logp need the uniform draws", __func__);
   TALOS_DEVICE();
+  if (dec->fused)
+    return decode_step_fused(dec, n, params, tokens, positions, reset, uniforms, logits, values, actions, logp,
+                             as_stream(stream));
   return decode_step(dec, n, params, tokens, positions, reset, uniforms, logits, values, actions, logp,
                      as_stream(stream));
 }
@@ -482,7 +1043,14 @@ int talos_ppo_decoder_read_cache(talos_decoder dec, int layer, int env, float* k
   for (int j = 0; j < L; ++j) {
     const int slot = (hd + j) % cap;
     for (int h = 0; h < H; ++h) {
-      if (k) std::copy_n(&kr[((size_t)h * cap + slot) * dk], dk, k + ((size_t)j * H + h) * dk);
+      if (k) {
+        float* kj = k + ((size_t)j * H + h) * dk;
+        if (dec->fused)  // [head][dk / 4][slot][4]
+          for (int c4 = 0; c4 < dk / 4; ++c4)
+            std::copy_n(&kr[(((size_t)h * (dk / 4) + c4) * cap + slot) * 4], 4, kj + 4 * c4);
+        else  // [head][slot][dk]
+          std::copy_n(&kr[((size_t)h * cap + slot) * dk], dk, kj);
+      }
       if (v) std::copy_n(&vr[((size_t)h * cap + slot) * dv], dv, v + ((size_t)j * H + h) * dv);
     }
   }

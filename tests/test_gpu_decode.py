@@ -7,6 +7,10 @@ Each test drives several environments with their own positions, resets and unifo
 after step, and compares every step's logits and values, the final caches and the actions.
 Tolerance: the fp32 rule of the other parity tests. An action is compared where the draw is not
 within 1e-4 of a bucket edge of the oracle's probabilities (an fp32 rounding may move it across).
+
+Every test runs on both device paths: the one-launch step (chosen for small policies with a
+window of at most 64) and the layered step (TALOS_DECODER_LAYERED=1 at decoder creation, and any
+configuration past the one-launch limits).
 """
 import numpy as np
 import pytest
@@ -17,6 +21,15 @@ from common import check_close, f32, gacha_states, ppo_params
 
 pytestmark = pytest.mark.gpu
 DA = th.DeviceArray
+
+
+@pytest.fixture(autouse=True, params=["fused", "layered"])
+def decoder_path(request, monkeypatch):
+    if request.param == "layered":
+        monkeypatch.setenv("TALOS_DECODER_LAYERED", "1")
+    else:
+        monkeypatch.delenv("TALOS_DECODER_LAYERED", raising=False)
+    return request.param
 
 
 def _probs(z):
@@ -99,6 +112,15 @@ def test_multi_layer_rollout(oracle, attention, layers):
         dec, odec, cfg = _run(oracle, args, p, T=7, n=3, W=W, max_seq_len=64, pos0=[0, 5, 60], seed=811 + W)
         _check_caches(dec, odec, cfg, range(3))
         dec.destroy()
+
+
+def test_window_past_the_one_launch_limit(oracle):
+    """A window of 70 (> 64: the layered step on both parametrisations) with pruning reached."""
+    args = (1, 16, *workload.REFERENCE_ACTOR_CRITIC)
+    p = f32(ppo_params(np.random.default_rng(830), oracle.PpoCfg(*args)))
+    dec, odec, cfg = _run(oracle, args, p, T=73, n=2, W=70, max_seq_len=256, pos0=[0, 180], seed=831)
+    _check_caches(dec, odec, cfg, range(2))
+    dec.destroy()
 
 
 def test_many_environments_and_a_partial_step(oracle):
