@@ -439,7 +439,12 @@ int talos_plan_destroy(talos_plan plan);
  * 256) are left unrotated as the reference's `continue` does (transformer.rs:718-721). The
  * configuration is any talos_ppo_cfg architecture (batch and seq are ignored); the decoder owns
  * the caches (n_envs * n_layers * n_heads * (context_len + 1) * (dk + dv) floats) and its
- * activations, so a step allocates nothing. */
+ * activations, so a step allocates nothing. For the reference ActorCritic's shape (in_dim 8, d 64,
+ * MLA with 4 heads, latent 32, rope 16, head and value dims 16, ffn 128, 5 actions) and
+ * context_len <= 16 the step is one kernel launch whose cache holds each token's latent row and
+ * rotated k_rope rows instead (n_envs * n_layers * (context_len + 1) * (kv_latent + n_heads *
+ * rope_dim) floats); the environment variable TALOS_DECODER_LAYERED=1 at creation selects the
+ * general path instead. */
 typedef struct talos_decoder_s* talos_decoder;
 int talos_ppo_decoder_create(const talos_ppo_cfg* cfg, int n_envs, int context_len, int max_seq_len,
                              talos_decoder* dec);
@@ -454,7 +459,9 @@ int talos_ppo_decoder_step_f32(talos_decoder dec, int n, const float* params, co
                                const int32_t* positions, const uint8_t* reset, const float* uniforms, float* logits,
                                float* values, int32_t* actions, float* logp, talos_stream_t stream);
 /* Host copy of one environment's cached rows of a layer, oldest first: k [len, n_heads, dk] and
- * v [len, n_heads, dv] (either may be NULL); *len = rows held. Waits for the device. */
+ * v [len, n_heads, dv] (either may be NULL); *len = rows held. Waits for the device. A latent cache
+ * is expanded to the reference's rows with the last step's parameters (k_h = [c.W_uk_h |
+ * k_rope_h], v_h = c.W_uv_h, in f64 on the host), which must still be valid device memory. */
 int talos_ppo_decoder_read_cache(talos_decoder dec, int layer, int env, float* k, float* v, int* len);
 int talos_ppo_decoder_destroy(talos_decoder dec);
 

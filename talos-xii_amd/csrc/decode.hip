@@ -44,7 +44,10 @@ struct talos_decoder_s {
         *vn = nullptr, *qc = nullptr, *qr = nullptr, *kr = nullptr, *o = nullptr, *h2 = nullptr, *a = nullptr,
         *pout = nullptr, *logits = nullptr, *values = nullptr;
   // the one-launch step (small policies): chosen at creation, with its LDS layout in floats
-  bool fused = false;  // the one-launch step applies (chosen at creation); its K cache is slot-minor
+  // the one-launch step applies (chosen at creation); its caches hold latent and k_rope rows
+  bool fused = false;
+  size_t k_layer = 0, v_layer = 0;  // floats per layer of kc / vc
+  const float* params = nullptr;     // the last step's parameters (read_cache expands latent rows)
 };
 
 namespace talos {
@@ -266,10 +269,16 @@ int dmm(hipStream_t s, int M, int N, int K, const float* A, long long lda, const
 // rows of one 16x16 tile; every dimension is a compile-time constant, so a lane issues all of its
 // weight loads before the first product. The phases are those of the layered path (decode_step
 // below), in the same order, separated by workgroup barriers instead of launches.
-constexpr int kFusedMaxWindow = 32;
+constexpr int kFusedMaxWindow = 16;  // the staged rows of 16 environments fit in LDS
 constexpr int kFusedEnvs = 16;  // the rows of a v_mfma_f32_16x16x4f32 tile
-constexpr int kFusedThreads = 256;
+#ifndef TALOS_FUSED_WAVES
+#define TALOS_FUSED_WAVES 8
+#endif
+constexpr int kFusedThreads = 64 * TALOS_FUSED_WAVES;  // two waves a SIMD hide each other's latency
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) void* gptr_t;  // global, for direct-to-LDS loads
+typedef __attribute__((address_space(3))) void* lptr_t;  // LDS
+constexpr int kVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0), expcnt / lgkmcnt not waited
 
 template <int IN_, int D_, int H_, int HD_, int R_, int VD_, int LT_, int F_, int A_, bool MLA_>
 struct FusedShape {
@@ -308,27 +317,31 @@ struct FusedArgs {
   long long g1, g2, w1, b1, w2, b2, wo, wqkv, wdkv, wuk, wuv, wq, wkr, wqr;
 };
 
-// out(e, n, sum_k X[e][k] W[k][n] (+ bias[n])) for the workgroup's 16 environments on the matrix
-// cores. The 16-column tiles of Y go round the waves (tile t to wave (t + WOFF) % 4); for the 16 k
-// of group g a lane (row i = lane % 16, quad kq = lane / 16) reads X[i][16g + 4kq .. +3] as one
-// float4 from LDS and feeds the four v_mfma_f32_16x16x4f32 of the group (product u takes
-// k = 16g + 4kq + u) with B = W[16g + 4kq + u][n]. The result tile holds D[4kq + r][lane % 16] in
-// register r. K % 4 == 0; k past K (K % 16 != 0) and columns past N contribute zeros.
+// out(e, n, sum_k X[e][k] W(k, n) (+ bias[n])) for the workgroup's 16 environments on the matrix
+// cores, W(k, n) = W[k * LDW + n] (or W[n * LDW + k] when TRANS). The 16-column tiles of Y go
+// round the waves (tile t to wave (t + woff) % waves); for the 16 k of group g a lane (row i =
+// lane % 16, quad kq = lane / 16) reads X[i][16g + 4kq .. +3] as one float4 from LDS and feeds the
+// four v_mfma_f32_16x16x4f32 of the group (product u takes k = 16g + 4kq + u) with
+// B = W(16g + 4kq + u, n). The result tile holds D[4kq + r][lane % 16] in register r. K % 4 == 0;
+// k past K (K % 16 != 0) and columns past N contribute zeros.
 //
 // The lane's weights (K / 4 a tile) and bias are loaded by FmmW::load, a phase or more before
 // fmm_run uses them, so the loads of the next product are in flight while the current phase runs.
-template <int K, int N, int LDW, int WOFF = 0>
+template <int K, int N, int LDW, bool TRANS = false>
 struct FmmW {
   static constexpr int TILES = (N + 15) / 16, WAVES = kFusedThreads / 64, TPW = (TILES + WAVES - 1) / WAVES;
   static constexpr int KG = (K + 15) / 16;
   float w[TPW][4 * KG];
   float b[TPW];
+  int woff;
   bool has_bias;
-  __device__ __forceinline__ static int tile_of(int tp) {
-    return ((int)(threadIdx.x >> 6) + WAVES - WOFF % WAVES) % WAVES + tp * WAVES;
+  __device__ __forceinline__ int tile_of(int tp) const {
+    return ((int)(threadIdx.x >> 6) + WAVES - woff % WAVES) % WAVES + tp * WAVES;
   }
-  __device__ __forceinline__ void load(const float* __restrict__ W, const float* __restrict__ bias) {
+  // (no __restrict__: loads the compiler cannot prove invariant are not re-issued at the use)
+  __device__ __forceinline__ void load(const float* W, const float* bias, int wo = 0) {
     const int row = threadIdx.x & 15, kq = (threadIdx.x >> 4) & 3;
+    woff = wo;
     has_bias = bias != nullptr;
 #pragma unroll
     for (int tp = 0; tp < TPW; ++tp) {
@@ -339,20 +352,20 @@ struct FmmW {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int k = 16 * g + 4 * kq + u;
-          w[tp][4 * g + u] = nv && k < K ? W[k * LDW + n] : 0.f;
+          w[tp][4 * g + u] = nv && k < K ? W[TRANS ? n * LDW + k : k * LDW + n] : 0.f;
         }
       b[tp] = nv && bias ? bias[n] : 0.f;
     }
   }
 };
-template <int K, int N, int LDX, int LDW, int WOFF, class Out>
-__device__ __forceinline__ void fmm_run(const float* X, const FmmW<K, N, LDW, WOFF>& wt, Out out) {
+template <int K, int N, int LDX, int LDW, bool TRANS, class Out>
+__device__ __forceinline__ void fmm_run(const float* X, const FmmW<K, N, LDW, TRANS>& wt, Out out) {
   static_assert(K % 4 == 0 && LDX % 4 == 0, "float4 rows");
-  using FW = FmmW<K, N, LDW, WOFF>;
+  using FW = FmmW<K, N, LDW, TRANS>;
   const int row = threadIdx.x & 15, kq = (threadIdx.x >> 4) & 3;
 #pragma unroll
   for (int tp = 0; tp < FW::TPW; ++tp) {
-    const int t = FW::tile_of(tp), n = t * 16 + row;
+    const int t = wt.tile_of(tp), n = t * 16 + row;
     if (t >= FW::TILES) continue;  // wave-uniform
     floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -375,6 +388,16 @@ __device__ __forceinline__ void fmm_run(const float* X, const FmmW<K, N, LDW, WO
   }
 }
 
+// A workgroup barrier that orders LDS only. The step's threads share data through LDS alone (the
+// cache rows they write to global memory are read by later launches, the staged rows are waited
+// for explicitly), so outstanding global loads and stores (prefetched weights, cache writes) need
+// not drain at every barrier, as they would behind __syncthreads().
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Sum over aligned groups of W adjacent lanes (W a power of two <= 16) with DPP lane moves, every
 // lane of a group getting its sum; all lanes of the wave must be active.
 template <int W>
@@ -394,9 +417,9 @@ __device__ __forceinline__ float group_sum(float v) {
 // are loaded by NormG::load ahead of the phase.
 template <int D>
 struct NormG {
-  static constexpr int LPR = kFusedThreads / kFusedEnvs, PER = (D + LPR - 1) / LPR;
+  static constexpr int LPR = 16, PER = (D + LPR - 1) / LPR;  // the first 16 x 16 threads
   float g[PER];
-  __device__ __forceinline__ void load(const float* __restrict__ gain) {
+  __device__ __forceinline__ void load(const float* gain) {
     const int l = threadIdx.x % LPR;
 #pragma unroll
     for (int j = 0; j < PER; ++j) g[j] = l + j * LPR < D ? gain[l + j * LPR] : 0.f;
@@ -405,6 +428,7 @@ struct NormG {
 template <int D, int LD>
 __device__ __forceinline__ void fnorm(const float* x, float* y, float eps, const NormG<D>& gn) {
   constexpr int LPR = NormG<D>::LPR, PER = NormG<D>::PER;
+  if (threadIdx.x >= kFusedEnvs * LPR) return;  // whole waves
   const int row = threadIdx.x / LPR, l = threadIdx.x % LPR;
   float xv[PER];
   float ss = 0.f;
@@ -423,22 +447,53 @@ __device__ __forceinline__ void fnorm(const float* x, float* y, float eps, const
   }
 }
 
+// The step of one workgroup. MLA attention runs in its absorbed form: the cache holds, per layer,
+// environment and slot, the latent row c = x.W_dkv ([LT]) and the rotated k_rope rows of every
+// head ([H][R]) instead of the per-head K and V of the reference (k_h = [c.W_uk_h | k_rope_h],
+// v_h = c.W_uv_h, src/transformer.rs:706-781), which halves the bytes a step reads:
+//   score_h(j) = (W_uk_h q_c_h) . c_j + q_rope_h . k_rope_h(j),
+//   o_h = (sum_j p_h(j) c_j) . W_uv_h.
+// Both are slot-minor, [env][LT / 4][cap] and [env][H][R / 4][cap] of float4, so a workgroup's
+// rows are one contiguous block of each, copied into LDS with direct-to-LDS loads
+// (global_load_lds_dwordx4) issued a phase or more before the attention: at the start for layer
+// 0, after the previous layer's attention for the others.
 template <class SH>
 __global__ __launch_bounds__(kFusedThreads) void decode_fused_kernel(FusedArgs a) {
+  static_assert(SH::MLA, "the one-launch step is instantiated for latent attention");
   constexpr int T = kFusedThreads, E = kFusedEnvs;
   constexpr int D = SH::D, H = SH::H, DK = SH::DK, DV = SH::DV, F = SH::F, A = SH::A, IN = SH::IN;
-  constexpr int LDD = D + 4, LDQ = H * DK + 4, LDV = H * DV + 4, LDF = F + 4, LDI = IN + 4, LDC = SH::LT + 4;
-  constexpr int CAPM = kFusedMaxWindow + 1, NF4 = DK / 4, NV4 = DV / 4;
-  static_assert(LDQ >= LDD && DK % 4 == 0 && DV % 4 == 0 && (NF4 & (NF4 - 1)) == 0 && NF4 <= 64, "layout");
-  __shared__ __align__(16) float x[E * LDD], xn[E * LDD], qh[E * (LDQ > LDF ? LDQ : LDF)], k[E * LDQ];
-  __shared__ __align__(16) float v[E * LDV], o[E * LDV], ckv[E * LDC], tok[E * LDI], lg[E * A];
+  constexpr int HD = SH::HD, R = SH::R, LT = SH::LT;
+  constexpr int LDD = D + 4, LDQ = H * DK + 4, LDV = H * DV + 4, LDF = F + 4, LDI = IN + 4, LDC = LT + 4;
+  constexpr int LDR = H * R + 4, LDA = H * LT + 4;
+  constexpr int CAPM = kFusedMaxWindow + 1, NC4 = LT / 4, NR4 = R / 4;
+  constexpr int CF4 = E * NC4 * CAPM, KF4 = E * H * NR4 * CAPM;  // float4s of the staged rows
+  static_assert(CF4 % 64 == 0 && KF4 % 64 == 0, "whole wave copies");
+  static_assert(LT % 16 == 0 && R % 4 == 0 && HD % 4 == 0 && LDA >= LDD, "layout");
+  __shared__ __align__(16) float x[E * LDD], xn[E * LDD], qh[E * (LDQ > LDF ? LDQ : LDF)], qa[E * LDA];
+  __shared__ __align__(16) float kr[E * LDR], ckv[E * LDC], o[E * LDV], tok[E * LDI], lg[E * A];
   __shared__ float pr[E * H * CAPM], inv[E * H];
+  __shared__ __align__(16) float sc_c[CF4 * 4], sc_k[KF4 * 4];  // the held latent / k_rope rows
   __shared__ int slen[E], shead[E], spos[E];
-  float* q = qh;
-  float* hid = qh;  // the FFN rows reuse q's (dead after the attention) with stride LDF
-  float* pout = k;  // the out_proj rows reuse k's with stride LDD
-  const int env0 = blockIdx.x * E, tid = threadIdx.x, cap = a.cap;
+  float* q = qh;     // [q_c | q_rope] per head
+  float* hid = qh;   // the FFN rows reuse q's (dead after the attention) with stride LDF
+  float* ctx = qa;   // sum_j p_h(j) c_j reuses W_uk_h q_c_h's rows (dead after the scores)
+  float* pout = qa;  // the out_proj rows, with stride LDD
+  const int env0 = blockIdx.x * E, tid = threadIdx.x, cap = a.cap, n_on = min(E, a.n - env0);
   const float* P = a.P;
+  // copy the workgroup's held rows of layer l into sc_c / sc_k: the blocks are contiguous
+  // (n_on * NC4 * cap and n_on * H * NR4 * cap float4s); a wave instruction fills 64 consecutive
+  // float4s of LDS, a lane past the block re-reads the block's last float4 (in bounds)
+  auto stage = [&](int l) {
+    const int wave = tid >> 6, lane = tid & 63;
+    const float4* gc = reinterpret_cast<const float4*>(a.kc + l * a.kc_layer) + (long long)env0 * NC4 * cap;
+    const float4* gk = reinterpret_cast<const float4*>(a.vc + l * a.vc_layer) + (long long)env0 * H * NR4 * cap;
+    const int nc = n_on * NC4 * cap, nk = n_on * H * NR4 * cap;
+    for (int i = wave; i * 64 < nc; i += T / 64)
+      __builtin_amdgcn_global_load_lds((gptr_t)(gc + min(i * 64 + lane, nc - 1)), (lptr_t)(sc_c + i * 256), 16, 0, 0);
+    for (int i = wave; i * 64 < nk; i += T / 64)
+      __builtin_amdgcn_global_load_lds((gptr_t)(gk + min(i * 64 + lane, nk - 1)), (lptr_t)(sc_k + i * 256), 16, 0, 0);
+  };
+  stage(0);
   if (tid < E) {
     const int e = env0 + tid;
     const bool on = e < a.n;
@@ -460,10 +515,10 @@ __global__ __launch_bounds__(kFusedThreads) void decode_fused_kernel(FusedArgs a
   w_emb.load(P + a.we, P + a.be);
   NormG<D> gn;
   gn.load(P + a.g1);
-  __syncthreads();
+  lds_barrier();
   // this thread's RoPE items (environment, head, pair) and their factors, reused by every layer;
   // positions outside the table are not rotated (src/transformer.rs:718-721)
-  constexpr int HALF = SH::ROPE / 2, NROT = E * H * HALF, ROT_PER = (NROT + T - 1) / T;
+  constexpr int HALF = R / 2, NROT = E * H * HALF, ROT_PER = (NROT + T - 1) / T;
   float rc[ROT_PER], rs[ROT_PER];
   bool rot[ROT_PER];
 #pragma unroll
@@ -474,125 +529,107 @@ __global__ __launch_bounds__(kFusedThreads) void decode_fused_kernel(FusedArgs a
     rc[t] = rot[t] ? a.rcos[p * HALF + m] : 1.f;
     rs[t] = rot[t] ? a.rsin[p * HALF + m] : 0.f;
   }
-  constexpr int HD = SH::HD, R = SH::MLA ? SH::R : 1, LT = SH::MLA ? SH::LT : 4;
-  // the attention's input products: MLA's down-projection and the q / k_rope projections, or W_qkv
-  // as three column blocks of [d][3d]
-  FmmW<D, LT, LT, 2> w_dkv;
-  FmmW<D, H * HD, (SH::MLA ? H * HD : 3 * D)> w_q;
+  // the layer's products from x_norm: down-projection, q_c, q_rope, k_rope
+  FmmW<D, LT, LT> w_dkv;
+  FmmW<D, H * HD, H * HD> w_q;
   FmmW<D, H * R, H * R> w_qr, w_kr;
-  FmmW<D, D, 3 * D> w_k, w_v;
   auto load_in = [&](const float* B) {
-    if constexpr (SH::MLA) {
-      w_dkv.load(B + a.wdkv, nullptr);
-      w_q.load(B + a.wq, nullptr);
-      w_qr.load(B + a.wqr, nullptr);
-      w_kr.load(B + a.wkr, nullptr);
-    } else {
-      w_q.load(B + a.wqkv, nullptr);
-      w_k.load(B + a.wqkv + D, nullptr);
-      w_v.load(B + a.wqkv + 2 * D, nullptr);
-    }
+    // tiles spread over the waves: q 0-3, q_rope 6,7,0,1, k_rope 2-5, W_dkv 4,5 (of 8)
+    w_dkv.load(B + a.wdkv, nullptr, 4);
+    w_q.load(B + a.wq, nullptr);
+    w_qr.load(B + a.wqr, nullptr, 6);
+    w_kr.load(B + a.wkr, nullptr, 2);
   };
-  load_in(P + a.lstride * 0);
+  load_in(P);
   fmm_run<IN, D, LDI>(tok, w_emb, [&](int e, int n, float s) { x[e * LDD + n] = s; });
-  __syncthreads();
+  lds_barrier();
   for (int l = 0; l < a.layers; ++l) {
     const float* B = P + l * a.lstride;
+    // W_uk_h^T per head (q_c_h -> the latent space) and W_uv_h per head
+    FmmW<HD, LT, H * HD, true> w_uk[H];
+    FmmW<LT, DV, H * DV> w_uv[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) w_uk[h].load(B + a.wuk + h * HD, nullptr, 2 * h);
     fnorm<D, LDD>(x, xn, a.eps, gn);
-    __syncthreads();
-    FmmW<LT, H * HD, H * HD> w_uk;
-    FmmW<LT, H * DV, H * DV, 2> w_uv;
-    if constexpr (SH::MLA) {
-      w_uk.load(B + a.wuk, nullptr);
-      w_uv.load(B + a.wuv, nullptr);
-      fmm_run<D, LT, LDD>(xn, w_dkv, [&](int e, int n, float s) { ckv[e * LDC + n] = s; });
-      fmm_run<D, H * HD, LDD>(xn, w_q, [&](int e, int n, float s) { q[e * LDQ + (n / HD) * DK + n % HD] = s; });
-      fmm_run<D, H * R, LDD>(xn, w_qr, [&](int e, int n, float s) { q[e * LDQ + (n / R) * DK + HD + n % R] = s; });
-      fmm_run<D, H * R, LDD>(xn, w_kr, [&](int e, int n, float s) { k[e * LDQ + (n / R) * DK + HD + n % R] = s; });
-      __syncthreads();
-      fmm_run<LT, H * HD, LDC>(ckv, w_uk, [&](int e, int n, float s) { k[e * LDQ + (n / HD) * DK + n % HD] = s; });
-      fmm_run<LT, H * DV, LDC>(ckv, w_uv, [&](int e, int n, float s) { v[e * LDV + n] = s; });
-    } else {
-      fmm_run<D, D, LDD>(xn, w_q, [&](int e, int n, float s) { q[e * LDQ + n] = s; });
-      fmm_run<D, D, LDD>(xn, w_k, [&](int e, int n, float s) { k[e * LDQ + n] = s; });
-      fmm_run<D, D, LDD>(xn, w_v, [&](int e, int n, float s) { v[e * LDV + n] = s; });
-    }
-    __syncthreads();
-    // RoPE on the new q / k rows: (x0, x1) -> (x0 c - x1 s, x0 s + x1 c), src/transformer.rs:724-733
+    lds_barrier();
+    fmm_run<D, LT, LDD>(xn, w_dkv, [&](int e, int n, float s) { ckv[e * LDC + n] = s; });
+    fmm_run<D, H * HD, LDD>(xn, w_q, [&](int e, int n, float s) { q[e * LDQ + (n / HD) * DK + n % HD] = s; });
+    fmm_run<D, H * R, LDD>(xn, w_qr, [&](int e, int n, float s) { q[e * LDQ + (n / R) * DK + HD + n % R] = s; });
+    fmm_run<D, H * R, LDD>(xn, w_kr, [&](int e, int n, float s) { kr[e * LDR + n] = s; });
+    lds_barrier();
+#pragma unroll
+    for (int h = 0; h < H; ++h) w_uv[h].load(B + a.wuv + h * DV, nullptr, 2 * h);
+    // RoPE on the new q_rope / k_rope rows: (x0, x1) -> (x0 c - x1 s, x0 s + x1 c),
+    // src/transformer.rs:724-733
 #pragma unroll
     for (int t = 0; t < ROT_PER; ++t) {
       const int idx = tid + t * T;
       if (idx < NROT && rot[t]) {
         const int e = idx / (H * HALF), h = (idx / HALF) % H, m = idx % HALF;
-        const int at = e * LDQ + h * DK + SH::ROPE_OFF + 2 * m;
-        const float q0 = q[at], q1 = q[at + 1], k0 = k[at], k1 = k[at + 1];
-        q[at] = fmaf(q0, rc[t], -q1 * rs[t]);
-        q[at + 1] = fmaf(q0, rs[t], q1 * rc[t]);
-        k[at] = fmaf(k0, rc[t], -k1 * rs[t]);
-        k[at + 1] = fmaf(k0, rs[t], k1 * rc[t]);
+        const int aq = e * LDQ + h * DK + HD + 2 * m, ak = e * LDR + h * R + 2 * m;
+        const float q0 = q[aq], q1 = q[aq + 1], k0 = kr[ak], k1 = kr[ak + 1];
+        q[aq] = fmaf(q0, rc[t], -q1 * rs[t]);
+        q[aq + 1] = fmaf(q0, rs[t], q1 * rc[t]);
+        kr[ak] = fmaf(k0, rc[t], -k1 * rs[t]);
+        kr[ak + 1] = fmaf(k0, rs[t], k1 * rc[t]);
       }
     }
-    __syncthreads();
-    float* kc = a.kc + l * a.kc_layer;
-    float* vc = a.vc + l * a.vc_layer;
-    // the new k / v rows into the ring slot after the held rows
-    for (int idx = tid; idx < E * H * (NF4 + NV4); idx += T) {
-      const int e = idx / (H * (NF4 + NV4)), hc = idx % (H * (NF4 + NV4));
+    // q_c_h -> W_uk_h q_c_h in the latent space (two tiles a head)
+#pragma unroll
+    for (int h = 0; h < H; ++h)
+      fmm_run<HD, LT, LDQ>(q + h * DK, w_uk[h], [&](int e, int n, float s) { qa[e * LDA + h * LT + n] = s; });
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);  // this wave's row copies have landed in LDS
+    lds_barrier();
+    float* cc = a.kc + l * a.kc_layer;  // [env][LT / 4][cap] of float4
+    float* kk = a.vc + l * a.vc_layer;  // [env][H][R / 4][cap] of float4
+    // the new latent and k_rope rows into the ring slot after the held rows
+    for (int idx = tid; idx < E * (NC4 + H * NR4); idx += T) {
+      const int e = idx / (NC4 + H * NR4), c = idx % (NC4 + H * NR4);
       if (slen[e] < 0) continue;
       const int slot = (shead[e] + slen[e]) % cap;
-      if (hc < H * NF4) {  // K is slot-minor: [env][head][DK / 4][slot] of float4
-        const int h = hc / NF4, c4 = hc % NF4;
-        *reinterpret_cast<float4*>(kc + ((((long long)(env0 + e) * H + h) * NF4 + c4) * cap + slot) * 4) =
-            *reinterpret_cast<const float4*>(k + e * LDQ + h * DK + 4 * c4);
-      } else {
-        const int h = (hc - H * NF4) / NV4, c4 = (hc - H * NF4) % NV4;
-        *reinterpret_cast<float4*>(vc + (((long long)(env0 + e) * H + h) * cap + slot) * DV + 4 * c4) =
-            *reinterpret_cast<const float4*>(v + e * LDV + h * DV + 4 * c4);
-      }
+      if (c < NC4)
+        *reinterpret_cast<float4*>(cc + (((long long)(env0 + e) * NC4 + c) * cap + slot) * 4) =
+            *reinterpret_cast<const float4*>(ckv + e * LDC + 4 * c);
+      else
+        *reinterpret_cast<float4*>(kk + (((long long)(env0 + e) * H * NR4 + (c - NC4)) * cap + slot) * 4) =
+            *reinterpret_cast<const float4*>(kr + e * LDR + 4 * (c - NC4));
     }
-    // scores of the held rows: a lane per (environment, head, slot) of the workgroup's region,
-    // IB of them at once with all their K loads issued before the first product. K is slot-minor,
-    // so for each quarter-row c4 the lanes of consecutive slots read consecutive float4s
-    // (coalesced) and a lane sums its own row, with the q quarter-rows read from LDS. A slot
-    // outside the held rows (empty, or the new row's) is dropped. Item i is
-    // (e * H + h, slot) = (i / cap, i % cap), the quotient taken in fp32 from (i + 0.5) / cap
-    // (i < 2^16, cap <= 33: the rounding error is far below the 0.5 / cap margin).
-    {
-      constexpr int IB = (E * H * CAPM + T - 1) / T < 5 ? (E * H * CAPM + T - 1) / T : 5;
-      const int n_on = min(E, a.n - env0), items = n_on * H * cap;
-      const float4* kreg = reinterpret_cast<const float4*>(kc + (long long)env0 * H * NF4 * cap * 4);
-      const float rcap = 1.0f / (float)cap;
-      for (int i0 = tid; i0 < items; i0 += IB * T) {
-        float4 kb[IB][NF4];
-        int eh[IB], slot[IB];
+    // scores of the held rows from LDS: a lane per (environment, head, slot), slot fastest, so a
+    // wave's lanes read consecutive float4s of each quarter-row plane. A slot outside the held
+    // rows (empty, or the new row's) is dropped.
+    // (unrolled over the lane's items so their LDS reads are in flight together; the quotient
+    // i / cap is taken in fp32 from (i + 0.5) / cap: i < 2^16 and cap <= 17 leave the rounding
+    // error far below the 0.5 / cap margin)
+    const float rcap = 1.0f / (float)cap;
 #pragma unroll
-        for (int b = 0; b < IB; ++b) {
-          const int i = i0 + b * T;
-          const bool on = i < items;
-          eh[b] = on ? (int)(((float)i + 0.5f) * rcap) : 0;
-          slot[b] = i - eh[b] * cap;
-          const float4* kr = kreg + (long long)eh[b] * NF4 * cap + slot[b];
+    for (int it = 0; it < (E * H * CAPM + T - 1) / T; ++it) {
+      const int i = tid + it * T;
+      if (i >= n_on * H * cap) continue;
+      const int eh = (int)(((float)i + 0.5f) * rcap), slot = i - eh * cap, e = eh / H, h = eh - e * H;
+      const int hd0 = shead[e], j = slot - hd0 + (slot < hd0 ? cap : 0);
+      if (j >= slen[e]) continue;
+      const float4* cr = reinterpret_cast<const float4*>(sc_c) + e * NC4 * cap + slot;
+      const float4* kq = reinterpret_cast<const float4*>(sc_k) + eh * NR4 * cap + slot;
+      const float* qar = qa + e * LDA + h * LT;
+      const float* qrr = q + e * LDQ + h * DK + HD;
+      float sc = 0.f;
 #pragma unroll
-          for (int c4 = 0; c4 < NF4; ++c4) kb[b][c4] = on ? kr[c4 * cap] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int b = 0; b < IB; ++b) {
-          if (i0 + b * T >= items) continue;
-          const int e = eh[b] / H, hd0 = shead[e], j = slot[b] - hd0 + (slot[b] < hd0 ? cap : 0);
-          if (j >= slen[e]) continue;
-          const float* qr = q + e * LDQ + (eh[b] - e * H) * DK;
-          float sc = 0.f;
-#pragma unroll
-          for (int c4 = 0; c4 < NF4; ++c4) {
-            const float4 q4 = *reinterpret_cast<const float4*>(qr + 4 * c4);
-            sc = fmaf(q4.x, kb[b][c4].x, sc);
-            sc = fmaf(q4.y, kb[b][c4].y, sc);
-            sc = fmaf(q4.z, kb[b][c4].z, sc);
-            sc = fmaf(q4.w, kb[b][c4].w, sc);
-          }
-          pr[eh[b] * CAPM + j] = sc * a.scale;
-        }
+      for (int c = 0; c < NC4; ++c) {
+        const float4 q4 = *reinterpret_cast<const float4*>(qar + 4 * c), c4 = cr[c * cap];
+        sc = fmaf(q4.x, c4.x, sc);
+        sc = fmaf(q4.y, c4.y, sc);
+        sc = fmaf(q4.z, c4.z, sc);
+        sc = fmaf(q4.w, c4.w, sc);
       }
+#pragma unroll
+      for (int c = 0; c < NR4; ++c) {
+        const float4 q4 = *reinterpret_cast<const float4*>(qrr + 4 * c), k4 = kq[c * cap];
+        sc = fmaf(q4.x, k4.x, sc);
+        sc = fmaf(q4.y, k4.y, sc);
+        sc = fmaf(q4.z, k4.z, sc);
+        sc = fmaf(q4.w, k4.w, sc);
+      }
+      pr[eh * CAPM + j] = sc * a.scale;
     }
     // the new row's score, from LDS
     for (int idx = tid; idx < E * H; idx += T) {
@@ -600,10 +637,12 @@ __global__ __launch_bounds__(kFusedThreads) void decode_fused_kernel(FusedArgs a
       if (slen[e] < 0) continue;
       float sc = 0.f;
 #pragma unroll
-      for (int i = 0; i < DK; ++i) sc = fmaf(q[e * LDQ + h * DK + i], k[e * LDQ + h * DK + i], sc);
+      for (int i = 0; i < LT; ++i) sc = fmaf(qa[e * LDA + h * LT + i], ckv[e * LDC + i], sc);
+#pragma unroll
+      for (int i = 0; i < R; ++i) sc = fmaf(q[e * LDQ + h * DK + HD + i], kr[e * LDR + h * R + i], sc);
       pr[idx * CAPM + slen[e]] = sc * a.scale;
     }
-    __syncthreads();
+    lds_barrier();
     FmmW<H * DV, D, D> w_o;
     w_o.load(B + a.wo, nullptr);
     for (int idx = tid; idx < E * H; idx += T) {
@@ -626,72 +665,73 @@ __global__ __launch_bounds__(kFusedThreads) void decode_fused_kernel(FusedArgs a
       }
       inv[idx] = rows > 0 ? 1.f / sum : 0.f;
     }
-    __syncthreads();
-    // P.V: a thread per (environment, head, 4 columns) loads all of its held rows before the
-    // first product (window <= kFusedMaxWindow)
-    for (int idx = tid; idx < E * H * NV4; idx += T) {
-      const int e = idx / (H * NV4), h = (idx / NV4) % H, c4 = idx % NV4;
+    lds_barrier();
+    // ctx_h = sum_j p_h(j) c_j from LDS: a lane per (environment, head, 4 latent columns)
+    for (int idx = tid; idx < E * H * NC4; idx += T) {
+      const int e = idx / (H * NC4), h = (idx / NC4) % H, c = idx % NC4;
       const int rows = slen[e] + 1, hd0 = shead[e];
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
       if (rows > 0) {
         const float* p = pr + (e * H + h) * CAPM;
-        const float4* vb = reinterpret_cast<const float4*>(vc + ((long long)(env0 + e) * H + h) * cap * DV) + c4;
-        float4 vr[kFusedMaxWindow];
-#pragma unroll
-        for (int j = 0; j < kFusedMaxWindow; ++j) {
-          const int slot = hd0 + j - (hd0 + j >= cap ? cap : 0);
-          vr[j] = j < rows - 1 ? vb[slot * NV4] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        const float4* cb = reinterpret_cast<const float4*>(sc_c) + (e * NC4 + c) * cap;
 #pragma unroll
         for (int j = 0; j < kFusedMaxWindow; ++j) {
           if (j < rows - 1) {
+            const int s = hd0 + j, slot = s - (s >= cap ? cap : 0);
+            const float4 cv = cb[slot];
             const float pj = p[j];
-            acc.x = fmaf(pj, vr[j].x, acc.x);
-            acc.y = fmaf(pj, vr[j].y, acc.y);
-            acc.z = fmaf(pj, vr[j].z, acc.z);
-            acc.w = fmaf(pj, vr[j].w, acc.w);
+            acc.x = fmaf(pj, cv.x, acc.x);
+            acc.y = fmaf(pj, cv.y, acc.y);
+            acc.z = fmaf(pj, cv.z, acc.z);
+            acc.w = fmaf(pj, cv.w, acc.w);
           }
         }
         const float pl = p[rows - 1], iv = inv[e * H + h];
-        const float4 vn = *reinterpret_cast<const float4*>(v + e * LDV + h * DV + 4 * c4);
-        acc.x = fmaf(pl, vn.x, acc.x) * iv;
-        acc.y = fmaf(pl, vn.y, acc.y) * iv;
-        acc.z = fmaf(pl, vn.z, acc.z) * iv;
-        acc.w = fmaf(pl, vn.w, acc.w) * iv;
+        const float4 cn = *reinterpret_cast<const float4*>(ckv + e * LDC + 4 * c);
+        acc.x = fmaf(pl, cn.x, acc.x) * iv;
+        acc.y = fmaf(pl, cn.y, acc.y) * iv;
+        acc.z = fmaf(pl, cn.z, acc.z) * iv;
+        acc.w = fmaf(pl, cn.w, acc.w) * iv;
       }
-      *reinterpret_cast<float4*>(o + e * LDV + h * DV + 4 * c4) = acc;
+      *reinterpret_cast<float4*>(ctx + e * LDA + h * LT + 4 * c) = acc;
     }
-    __syncthreads();
+    lds_barrier();
+    if (l + 1 < a.layers) stage(l + 1);  // the staged rows are free: the next layer's copies fly
+    // o_h = ctx_h . W_uv_h, a head per wave
+#pragma unroll
+    for (int h = 0; h < H; ++h)
+      fmm_run<LT, DV, LDA>(ctx + h * LT, w_uv[h], [&](int e, int n, float s) { o[e * LDV + h * DV + n] = s; });
+    lds_barrier();
     // h2 = x + o.Wo
     gn.load(B + a.g2);
     fmm_run<H * DV, D, LDV>(o, w_o, [&](int e, int n, float s) { x[e * LDD + n] = s + x[e * LDD + n]; });
-    __syncthreads();
+    lds_barrier();
     FmmW<D, F, F> w_1;
     w_1.load(B + a.w1, B + a.b1);
     fnorm<D, LDD>(x, xn, a.eps, gn);
-    __syncthreads();
+    lds_barrier();
     FmmW<F, D, D> w_2;
     w_2.load(B + a.w2, B + a.b2);
     const bool relu = a.relu;
     fmm_run<D, F, LDD>(xn, w_1, [&](int e, int n, float s) { hid[e * LDF + n] = relu ? fmaxf(s, 0.f) : gelu_f(s); });
-    __syncthreads();
+    lds_barrier();
     // x = h2 + act(.).W2 + b2; the next layer's (or the final) gains and input products in flight
     const bool more = l + 1 < a.layers;
     gn.load(more ? B + a.lstride + a.g1 : P + a.gf);
     if (more) load_in(B + a.lstride);
     fmm_run<F, D, LDF>(hid, w_2, [&](int e, int n, float s) { x[e * LDD + n] = s + x[e * LDD + n]; });
-    __syncthreads();
+    lds_barrier();
   }
   FmmW<D, D, D> w_out;
   w_out.load(P + a.wout, P + a.bout);
   fnorm<D, LDD>(x, xn, a.eps, gn);
-  __syncthreads();
+  lds_barrier();
   FmmW<D, A, A> w_a;
-  FmmW<D, 1, 1, 1> w_c;
+  FmmW<D, 1, 1> w_c;
   w_a.load(P + a.wa, P + a.ba);
-  if (a.values) w_c.load(P + a.wc, P + a.bc);
+  if (a.values) w_c.load(P + a.wc, P + a.bc, 1);
   fmm_run<D, D, LDD>(xn, w_out, [&](int e, int n, float s) { pout[e * LDD + n] = s; });
-  __syncthreads();
+  lds_barrier();
   {
     float* logits = a.logits;
     float* values = a.values;
@@ -705,7 +745,7 @@ __global__ __launch_bounds__(kFusedThreads) void decode_fused_kernel(FusedArgs a
         if (env0 + e < n_env) values[env0 + e] = s;
       });
   }
-  __syncthreads();
+  lds_barrier();
   if (tid < E && env0 + tid < a.n) {
     const int e = env0 + tid;
     if (a.actions || a.logp)
@@ -759,8 +799,8 @@ int decode_step_fused(talos_decoder_s* D, int n, const float* P, const float* to
   a.head = D->head;
   a.kc = D->kc[0];
   a.vc = D->vc[0];
-  a.kc_layer = (long long)D->n_envs * c.n_heads * a.cap * D->dk;
-  a.vc_layer = (long long)D->n_envs * c.n_heads * a.cap * D->dv;
+  a.kc_layer = (long long)D->k_layer;
+  a.vc_layer = (long long)D->v_layer;
   a.rcos = D->rcos;
   a.rsin = D->rsin;
   a.we = po.we;
@@ -791,9 +831,9 @@ int decode_step_fused(talos_decoder_s* D, int n, const float* P, const float* to
   const double attn_macs = SH::MLA ? d * SH::LT + SH::LT * H * (SH::HD + SH::DV) + d * H * (SH::HD + 2.0 * SH::R)
                                    : 3.0 * d * d;
   const double macs = SH::IN * d + c.n_layers * (attn_macs + H * SH::DV * d + 2.0 * d * F) + d * d + d * (A + 1);
-  // algorithmic bytes: the held cache rows read and the new rows written (every layer), the
-  // weights once, tokens and positions in, logits / value / action / log-prob out
-  const double cache = 4.0 * n * H * c.n_layers * (double)a.cap * (SH::DK + SH::DV);
+  // algorithmic bytes: the held latent and k_rope rows read and the new rows written (every
+  // layer), the weights once, tokens and positions in, logits / value / action / log-prob out
+  const double cache = 4.0 * n * c.n_layers * (double)a.cap * (SH::LT + H * SH::R);
   ProfScope ps(s, "decode_fused_kernel", 2.0 * n * macs, cache + 4.0 * po.end + 4.0 * n * (SH::IN + A + 5));
   hipLaunchKernelGGL((decode_fused_kernel<SH>), dim3(ceil_div((size_t)n, kFusedEnvs)), dim3(kFusedThreads), 0, s,
                      a);
@@ -958,13 +998,15 @@ int talos_ppo_decoder_create(const talos_ppo_cfg* cfg, int n_envs, int context_l
   D->fused = fused_applies(c, context_len) && !(layered && layered[0] == '1');
   const size_t n = (size_t)n_envs, d = c.d_model, F = c.ffn_dim, H = c.n_heads;
   int rc = 0;
-  {  // one layer-major block each for K and V
+  {  // one layer-major block each for K and V (layered), or the latent and k_rope rows (one-launch)
+    D->k_layer = D->fused ? n * cap * c.kv_latent : n * H * cap * dk;
+    D->v_layer = D->fused ? n * cap * H * c.rope_dim : n * H * cap * dv;
     float *k = nullptr, *v = nullptr;
-    rc |= dec_alloc_n(D, &k, (size_t)c.n_layers * n * H * cap * dk);
-    rc |= dec_alloc_n(D, &v, (size_t)c.n_layers * n * H * cap * dv);
+    rc |= dec_alloc_n(D, &k, (size_t)c.n_layers * D->k_layer);
+    rc |= dec_alloc_n(D, &v, (size_t)c.n_layers * D->v_layer);
     for (int l = 0; rc == TALOS_OK && l < c.n_layers; ++l) {
-      D->kc.push_back(k + (size_t)l * n * H * cap * dk);
-      D->vc.push_back(v + (size_t)l * n * H * cap * dv);
+      D->kc.push_back(k + (size_t)l * D->k_layer);
+      D->vc.push_back(v + (size_t)l * D->v_layer);
     }
   }
   rc |= dec_alloc_n(D, &D->len, n);
@@ -1018,6 +1060,7 @@ int talos_ppo_decoder_step_f32(talos_decoder dec, int n, const float* params, co
   TALOS_REQUIRE(uniforms != nullptr || (actions == nullptr && logp == nullptr), TALOS_ERR_NULL,
                 "%s: actions / logp need the uniform draws", __func__);
   TALOS_DEVICE();
+  dec->params = params;
   if (dec->fused)
     return decode_step_fused(dec, n, params, tokens, positions, reset, uniforms, logits, values, actions, logp,
                              as_stream(stream));
@@ -1032,25 +1075,63 @@ int talos_ppo_decoder_read_cache(talos_decoder dec, int layer, int env, float* k
   TALOS_NONNULL(len);
   TALOS_DEVICE();
   TALOS_HIP(hipDeviceSynchronize());
-  int32_t L = 0, hd = 0;
+  int32_t L = 0, hd0 = 0;
   TALOS_HIP(hipMemcpy(&L, dec->len + env, 4, hipMemcpyDeviceToHost));
-  TALOS_HIP(hipMemcpy(&hd, dec->head + env, 4, hipMemcpyDeviceToHost));
+  TALOS_HIP(hipMemcpy(&hd0, dec->head + env, 4, hipMemcpyDeviceToHost));
   *len = L;
   const int H = dec->cfg.n_heads, cap = dec->cap, dk = dec->dk, dv = dec->dv;
+  if (dec->fused) {
+    // latent rows c [LT / 4][slot][4] and k_rope rows [H][R / 4][slot][4] (slot-minor):
+    // k_h = [c.W_uk_h | k_rope_h], v_h = c.W_uv_h with the last step's weights
+    const talos_ppo_cfg& c = dec->cfg;
+    const int Lt = c.kv_latent, R = c.rope_dim, hd = c.head_dim, vd = c.v_dim;
+    std::vector<float> cr((size_t)cap * Lt), kr((size_t)cap * H * R);
+    TALOS_HIP(hipMemcpy(cr.data(), dec->kc[layer] + (size_t)env * cap * Lt, cr.size() * 4, hipMemcpyDeviceToHost));
+    TALOS_HIP(hipMemcpy(kr.data(), dec->vc[layer] + (size_t)env * cap * H * R, kr.size() * 4, hipMemcpyDeviceToHost));
+    if (L == 0) return TALOS_OK;
+    TALOS_REQUIRE(dec->params != nullptr, TALOS_ERR_HANDLE, "%s: no step has run", __func__);
+    talos_block_cfg bc = dec->bc;
+    bc.batch = 1;
+    bc.seq = 1;
+    size_t base = ppo_offsets(c).blocks;
+    for (int l = 0; l < layer; ++l) base = block_offsets(bc, base).end;
+    const MlaW w = block_offsets(bc, base).mla;
+    std::vector<float> wuk((size_t)Lt * H * hd), wuv((size_t)Lt * H * vd);
+    TALOS_HIP(hipMemcpy(wuk.data(), dec->params + w.wuk, wuk.size() * 4, hipMemcpyDeviceToHost));
+    TALOS_HIP(hipMemcpy(wuv.data(), dec->params + w.wuv, wuv.size() * 4, hipMemcpyDeviceToHost));
+    std::vector<float> cj(Lt);
+    for (int j = 0; j < L; ++j) {
+      const int slot = (hd0 + j) % cap;
+      for (int t = 0; t < Lt; ++t) cj[t] = cr[((size_t)(t / 4) * cap + slot) * 4 + t % 4];
+      for (int h = 0; h < H; ++h) {
+        if (k) {
+          float* kj = k + ((size_t)j * H + h) * dk;
+          for (int i = 0; i < hd; ++i) {
+            double sum = 0.0;
+            for (int t = 0; t < Lt; ++t) sum += (double)cj[t] * wuk[(size_t)t * H * hd + h * hd + i];
+            kj[i] = (float)sum;
+          }
+          for (int i = 0; i < R; ++i) kj[hd + i] = kr[(((size_t)h * (R / 4) + i / 4) * cap + slot) * 4 + i % 4];
+        }
+        if (v) {
+          float* vj = v + ((size_t)j * H + h) * dv;
+          for (int i = 0; i < vd; ++i) {
+            double sum = 0.0;
+            for (int t = 0; t < Lt; ++t) sum += (double)cj[t] * wuv[(size_t)t * H * vd + h * vd + i];
+            vj[i] = (float)sum;
+          }
+        }
+      }
+    }
+    return TALOS_OK;
+  }
   std::vector<float> kr((size_t)H * cap * dk), vr((size_t)H * cap * dv);
   TALOS_HIP(hipMemcpy(kr.data(), dec->kc[layer] + (size_t)env * H * cap * dk, kr.size() * 4, hipMemcpyDeviceToHost));
   TALOS_HIP(hipMemcpy(vr.data(), dec->vc[layer] + (size_t)env * H * cap * dv, vr.size() * 4, hipMemcpyDeviceToHost));
   for (int j = 0; j < L; ++j) {
-    const int slot = (hd + j) % cap;
+    const int slot = (hd0 + j) % cap;
     for (int h = 0; h < H; ++h) {
-      if (k) {
-        float* kj = k + ((size_t)j * H + h) * dk;
-        if (dec->fused)  // [head][dk / 4][slot][4]
-          for (int c4 = 0; c4 < dk / 4; ++c4)
-            std::copy_n(&kr[(((size_t)h * (dk / 4) + c4) * cap + slot) * 4], 4, kj + 4 * c4);
-        else  // [head][slot][dk]
-          std::copy_n(&kr[((size_t)h * cap + slot) * dk], dk, kj);
-      }
+      if (k) std::copy_n(&kr[((size_t)h * cap + slot) * dk], dk, k + ((size_t)j * H + h) * dk);
       if (v) std::copy_n(&vr[((size_t)h * cap + slot) * dv], dv, v + ((size_t)j * H + h) * dv);
     }
   }

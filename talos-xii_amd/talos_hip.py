@@ -253,10 +253,12 @@ class Decoder:
 
     def step(self, n, params, tokens, positions, reset=None, uniforms=None, logits=None, values=None,
              actions=None, logp=None, stream=None):
-        """All arguments are DeviceArray (or None)."""
+        """All arguments are DeviceArray (or None). The parameters are kept alive: cache() of a
+        latent cache expands its rows with the last step's weights."""
         ptr = lambda a: None if a is None else a.ptr  # noqa: E731
         call("talos_ppo_decoder_step_f32", self.h, n, ptr(params), ptr(tokens), ptr(positions), ptr(reset),
              ptr(uniforms), ptr(logits), ptr(values), ptr(actions), ptr(logp), stream)
+        self._params = params
 
     def cache(self, layer, env):
         """(k [len, H, dk], v [len, H, dv]) of env's cache at layer, oldest row first."""
