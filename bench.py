@@ -259,6 +259,9 @@ def main():
     ap.add_argument("--headline-only", action="store_true",
                     help="only the C4 line (no optimizer, reference-model or rollout lines): the command to run "
                          "under rocprofv3, so that its per-kernel averages cover the headline step alone")
+    ap.add_argument("--rollout-only", action="store_true",
+                    help="only the rollout line (its JSON object alone): the command to run under rocprofv3 for "
+                         "the rollout kernel's averages")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB device-to-device 5 times: the known-size "
                          "copy that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -269,6 +272,9 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
+    if args.rollout_only:
+        print(json.dumps({"rollout": rollout_line(args.steps, cpu=False)}))
+        return
 
     cfg_t = ppo_cfg(args.batch, args.seq)
     cfg, p, states, actions, adv, ret = make_inputs(cfg_t)
