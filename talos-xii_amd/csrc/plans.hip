@@ -28,6 +28,7 @@
 // sequence reaches the heads, so they run on the B last-token rows (same result as running them
 // on all B*S tokens and gathering afterwards, as the reference does).
 #include <cmath>
+#include <cstdlib>
 #include <vector>
 
 #include "attention.hpp"
@@ -61,6 +62,18 @@ struct talos_plan_s {
   size_t gemm_ws_bytes = 0;
   double* red_ws = nullptr;
   size_t red_ws_bytes = 0;
+  // The backward's side stream: weight-gradient products run there as soon as the main stream has
+  // produced their operands, with their own split-K workspace, overlapping the main stream's
+  // memory-bound kernels. Before the main stream overwrites a buffer such a product reads, it waits
+  // for that product's event (readers); every entry point joins the side stream before returning.
+  hipStream_t side = nullptr;
+  float* gemm_ws2 = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+  struct Reader {
+    const void* buf;
+    hipEvent_t ev;
+  };
+  std::vector<Reader> readers;
   // ppo
   float *h0 = nullptr, *last = nullptr, *lastn = nullptr, *rstdf = nullptr, *pout = nullptr, *logits = nullptr,
         *values = nullptr, *g_logits = nullptr, *g_values = nullptr, *g_pout = nullptr, *g_lastn = nullptr,
@@ -221,6 +234,15 @@ static int plan_alloc(talos_plan_s* p, float** out, size_t n) {
 }
 
 static void plan_free(talos_plan_s* p) {
+  if (p->side) {
+    (void)hipStreamSynchronize(p->side);
+    (void)hipStreamDestroy(p->side);
+    p->side = nullptr;
+  }
+  for (hipEvent_t e : {p->ev_fork, p->ev_join})
+    if (e) (void)hipEventDestroy(e);
+  for (auto& r : p->readers) (void)hipEventDestroy(r.ev);
+  p->readers.clear();
   for (void* a : p->allocs) (void)hipFree(a);
   p->allocs.clear();
   profiler_delete(p->prof);
@@ -343,13 +365,22 @@ static int alloc_workspaces(talos_plan_s* p) {
   float* red = nullptr;
   rc |= plan_alloc(p, &red, (p->red_ws_bytes + 3) / 4 + 2);
   p->red_ws = reinterpret_cast<double*>(red);
-  return rc ? TALOS_ERR_ALLOC : TALOS_OK;
+  if (rc) return TALOS_ERR_ALLOC;
+  // the side stream of the backward (TALOS_SINGLE_STREAM=1 keeps every launch on the caller's)
+  const char* one = std::getenv("TALOS_SINGLE_STREAM");
+  if (one && one[0] == '1') return TALOS_OK;
+  if (plan_alloc(p, &p->gemm_ws2, (p->gemm_ws_bytes + 3) / 4)) return TALOS_ERR_ALLOC;
+  TALOS_HIP(hipStreamCreateWithFlags(&p->side, hipStreamNonBlocking));
+  TALOS_HIP(hipEventCreateWithFlags(&p->ev_fork, hipEventDisableTiming));
+  TALOS_HIP(hipEventCreateWithFlags(&p->ev_join, hipEventDisableTiming));
+  return TALOS_OK;
 }
 
 // GEMM helpers ---------------------------------------------------------------
-static int mm(talos_plan_s* p, hipStream_t s, int tA, int tB, int M, int N, int K, const float* A, long long lda,
-              const float* B, long long ldb, float* C, long long ldc, float beta = 0.f, const float* bias = nullptr,
-              const float* resid = nullptr, long long ldr = 0, float* dbias = nullptr) {
+static int mm_ws(talos_plan_s* p, hipStream_t s, float* wsp, int tA, int tB, int M, int N, int K, const float* A,
+                 long long lda, const float* B, long long ldb, float* C, long long ldc, float beta = 0.f,
+                 const float* bias = nullptr, const float* resid = nullptr, long long ldr = 0,
+                 float* dbias = nullptr) {
   GemmDesc g;
   g.transA = tA;
   g.transB = tB;
@@ -373,8 +404,58 @@ static int mm(talos_plan_s* p, hipStream_t s, int tA, int tB, int M, int N, int 
   // the plan sizes its split-K workspace for the weight-gradient products; any other product
   // whose split would not fit runs unsplit
   if (ws > p->gemm_ws_bytes) g.ksplit = 1;
-  g.workspace = p->gemm_ws;
+  g.workspace = wsp;
   return gemm_launch(g, s);
+}
+static int mm(talos_plan_s* p, hipStream_t s, int tA, int tB, int M, int N, int K, const float* A, long long lda,
+              const float* B, long long ldb, float* C, long long ldc, float beta = 0.f, const float* bias = nullptr,
+              const float* resid = nullptr, long long ldr = 0, float* dbias = nullptr) {
+  return mm_ws(p, s, p->gemm_ws, tA, tB, M, N, K, A, lda, B, ldb, C, ldc, beta, bias, resid, ldr, dbias);
+}
+
+// The event recorded after the side-stream products that read buf (created on first use).
+static int reader_event(talos_plan_s* p, const void* buf, hipEvent_t* ev) {
+  for (auto& r : p->readers)
+    if (r.buf == buf) {
+      *ev = r.ev;
+      return TALOS_OK;
+    }
+  hipEvent_t e = nullptr;
+  TALOS_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  p->readers.push_back({buf, e});
+  *ev = e;
+  return TALOS_OK;
+}
+
+// A weight-gradient product C = A^T B (+ the bias gradient) on the side stream, ordered after
+// everything issued so far on s; `reads` names the gradient buffer it reads (B, or the buffer B
+// points into), which the main stream must not overwrite before the product has run.
+static int wgrad(talos_plan_s* p, hipStream_t s, const void* reads, int M, int N, int K, const float* A, long long lda,
+                 const float* B, long long ldb, float* C, long long ldc, float* dbias = nullptr) {
+  if (!p->side) return mm(p, s, 1, 0, M, N, K, A, lda, B, ldb, C, ldc, 0.f, nullptr, nullptr, 0, dbias);
+  TALOS_HIP(hipEventRecord(p->ev_fork, s));
+  TALOS_HIP(hipStreamWaitEvent(p->side, p->ev_fork, 0));
+  int rc = mm_ws(p, p->side, p->gemm_ws2, 1, 0, M, N, K, A, lda, B, ldb, C, ldc, 0.f, nullptr, nullptr, 0, dbias);
+  if (rc) return rc;
+  hipEvent_t e = nullptr;
+  if ((rc = reader_event(p, reads, &e))) return rc;
+  TALOS_HIP(hipEventRecord(e, p->side));
+  return TALOS_OK;
+}
+
+// The main stream s waits for the side-stream products that read buf before it overwrites buf.
+static int before_write(talos_plan_s* p, hipStream_t s, const void* buf) {
+  for (auto& r : p->readers)
+    if (r.buf == buf) TALOS_HIP(hipStreamWaitEvent(s, r.ev, 0));
+  return TALOS_OK;
+}
+
+// Everything issued on the side stream completes before anything issued later on s.
+static int join_side(talos_plan_s* p, hipStream_t s) {
+  if (!p->side) return TALOS_OK;
+  TALOS_HIP(hipEventRecord(p->ev_join, p->side));
+  TALOS_HIP(hipStreamWaitEvent(s, p->ev_join, 0));
+  return TALOS_OK;
 }
 
 // Latent attention (MultiHeadLatentAttention::forward, src/transformer.rs:478-557) --------------
@@ -646,8 +727,9 @@ static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const f
                               float* g_o, hipStream_t s) {
   const int d = c.d_model, F = c.ffn_dim, ow = attn_width(c);
   // out = h2 + a.W2 + b2
-  int rc = mm(p, s, 1, 0, F, d, R, a, F, gout, d, G + o.w2, d, 0.f, nullptr, nullptr, 0, G + o.b2);
+  int rc = wgrad(p, s, gout, F, d, R, a, F, gout, d, G + o.w2, d, G + o.b2);
   if (rc) return rc;
+  if ((rc = before_write(p, s, g_u))) return rc;
   {
     GemmDesc g;
     g.transB = 1;
@@ -668,15 +750,16 @@ static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const f
     if (rc) return rc;
   }
   // u = xn2.W1 + b1
-  rc = mm(p, s, 1, 0, d, F, R, xn2, d, g_u, F, G + o.w1, F, 0.f, nullptr, nullptr, 0, G + o.b1);
+  rc = wgrad(p, s, g_u, d, F, R, xn2, d, g_u, F, G + o.w1, F, G + o.b1);
   if (rc) return rc;
   rc = mm(p, s, 0, 1, R, d, F, g_u, F, P + o.w1, F, g_xn, d);
   if (rc) return rc;
   // h2 -> (residual) + rmsnorm2
+  if ((rc = before_write(p, s, g_h2))) return rc;
   rc = rmsnorm_bwd_launch(R, d, h2, P + o.g2, rstd2, g_xn, 1.f, g_h2, 0.f, G + o.g2, p->red_ws, s, gout);
   if (rc) return rc;
   // h2 = x + o.Wo
-  rc = mm(p, s, 1, 0, ow, d, R, ob, ow, g_h2, d, G + o.wo, d);
+  rc = wgrad(p, s, g_h2, ow, d, R, ob, ow, g_h2, d, G + o.wo, d);
   if (rc) return rc;
   return mm(p, s, 0, 1, R, ow, d, g_h2, d, P + o.wo, d, g_o, ow);
 }
@@ -688,6 +771,7 @@ static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const f
 static int block_norm1_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G,
                                 const BlockOff& o, const talos_plan_s::Layer& L, const float* g_h2,
                                 const float* g_h2_last, float* dx, hipStream_t s) {
+  if (int rc = before_write(p, s, dx)) return rc;
   return rmsnorm_bwd_launch(c.batch * c.seq, c.d_model, L.x, P + o.g1, L.rstd1, p->g_xn, 0.f, dx, 0.f, G + o.g1,
                             p->red_ws, s, g_h2, g_h2_last, c.seq, p->lens);
 }
@@ -699,7 +783,7 @@ static int block_qkv_backward(talos_plan_s* p, const talos_block_cfg& c, const f
                               hipStream_t s) {
   const int M = c.batch * c.seq, d = c.d_model;
   // qkv = xn1.Wqkv
-  int rc = mm(p, s, 1, 0, d, 3 * d, M, L.xn1, d, p->g_qkv, 3 * d, G + o.wqkv, 3 * d);
+  int rc = wgrad(p, s, p->g_qkv, d, 3 * d, M, L.xn1, d, p->g_qkv, 3 * d, G + o.wqkv, 3 * d);
   if (rc) return rc;
   rc = mm(p, s, 0, 1, M, d, 3 * d, p->g_qkv, 3 * d, P + o.wqkv, 3 * d, p->g_xn, d);
   if (rc) return rc;
@@ -720,7 +804,8 @@ static int block_attn_backward(talos_plan_s* p, const talos_block_cfg& c, const 
   AttnDesc a = block_attn_desc(p, c, L);
   a.dout = g_o;
   a.lddo = c.d_model;
-  int rc = attn_bwd_launch(a, p->attn_ws, s);
+  int rc = before_write(p, s, p->g_qkv);
+  if (rc == TALOS_OK) rc = attn_bwd_launch(a, p->attn_ws, s);
   if (rc) return rc;
   return block_qkv_backward(p, c, P, G, o, L, g_h2, g_h2_last, dx, s);
 }
@@ -1245,7 +1330,9 @@ int talos_block_fwd_bwd_f32(talos_plan plan, const float* params, const float* x
   int rc = block_forward(plan, c, params, bo, L, s);
   if (rc) return rc;
   if (out) TALOS_HIP(hipMemcpyAsync(out, L.out, M * d * 4, hipMemcpyDeviceToDevice, s));
-  return block_backward(plan, c, params, dparams, bo, L, gout, dx, s);
+  rc = block_backward(plan, c, params, dparams, bo, L, gout, dx, s);
+  if (rc) return rc;
+  return join_side(plan, s);
 }
 
 int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
@@ -1403,7 +1490,7 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
     if (rc) return rc;
   }
   // out_proj
-  rc = mm(p, s, 1, 0, d, d, B, p->lastn, d, p->g_pout, d, G + po.wout, d, 0.f, nullptr, nullptr, 0, G + po.bout);
+  rc = wgrad(p, s, p->g_pout, d, d, B, p->lastn, d, p->g_pout, d, G + po.wout, d, G + po.bout);
   if (rc) return rc;
   rc = mm(p, s, 0, 1, B, d, d, p->g_pout, d, params + po.wout, d, p->g_lastn, d);
   if (rc) return rc;
@@ -1448,10 +1535,12 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
       ad.ldq_last = d;
       ad.dq_last = R.dq;
       ad.lddq_last = d;
+      if ((rc = before_write(p, s, p->g_qkv))) return rc;
+      if ((rc = before_write(p, s, R.dq))) return rc;
       if ((rc = attn_bwd_lastq_launch(ad, R.o, d, R.lse, R.g_o, d, s))) return rc;
       float* g_kv = p->g_qkv + d;
-      if ((rc = mm(p, s, 1, 0, d, 2 * d, M, L.xn1, d, g_kv, 3 * d, G + o.wqkv + d, 3 * d))) return rc;
-      if ((rc = mm(p, s, 1, 0, d, d, B, R.xn1, d, R.dq, d, G + o.wqkv, 3 * d))) return rc;
+      if ((rc = wgrad(p, s, p->g_qkv, d, 2 * d, M, L.xn1, d, g_kv, 3 * d, G + o.wqkv + d, 3 * d))) return rc;
+      if ((rc = wgrad(p, s, R.dq, d, d, B, R.xn1, d, R.dq, d, G + o.wqkv, 3 * d))) return rc;
       if ((rc = mm(p, s, 0, 1, M, d, 2 * d, g_kv, 3 * d, params + o.wqkv + d, 3 * d, p->g_xn, d))) return rc;
       if ((rc = mm(p, s, 0, 1, B, d, d, R.dq, d, params + o.wqkv, 3 * d, R.g_xnq, d))) return rc;
       {
@@ -1475,7 +1564,9 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
     std::swap(gcur, gnext);
   }
   // embed
-  return mm(p, s, 1, 0, c.in_dim, d, M, states, c.in_dim, gcur, d, G + po.we, d, 0.f, nullptr, nullptr, 0, G + po.be);
+  rc = wgrad(p, s, gcur, c.in_dim, d, M, states, c.in_dim, gcur, d, G + po.we, d, G + po.be);
+  if (rc) return rc;
+  return join_side(p, s);
 }
 
 int talos_ppo_minibatch_f32(talos_plan plan, int n, const float* params, const float* states, const int32_t* lengths,

@@ -328,7 +328,8 @@ def test_reduce_transpose_concat_broadcast():
     th.call("talos_fill_add_f32", 9, 0.25, g.ptr, dx.ptr, None)
     assert np.array_equal(dx.numpy(), np.full(9, 0.5, np.float32))
     db = DA.from_numpy(np.ones(6))
-    th.call("talos_bias_grad_f32", 1000, 6, DA.from_numpy(np.ones((1000, 6))).ptr, 1.0, db.ptr, None)
+    ones = DA.from_numpy(np.ones((1000, 6)))  # held: a temporary would be freed before the launch
+    th.call("talos_bias_grad_f32", 1000, 6, ones.ptr, 1.0, db.ptr, None)
     assert np.array_equal(db.numpy(), np.full(6, 1001.0, np.float32))
 
 
