@@ -65,7 +65,8 @@ enum : int {
   E_ROPE = 128,  // rotate interleaved pairs of columns [0, rope_cols)
   E_SPLIT = 256,  // write the fp32 partial tile of this K split (no epilogue)
   E_DBIAS = 512,  // also sum the columns of op(B) (bias gradient; transA = 1, transB = 0)
-  E_NORM = 1024   // also RMSNorm each output row (N = 128: the whole row is in the tile)
+  E_NORM = 1024,  // also RMSNorm each output row (N = 128: the whole row is in the tile)
+  E_NORMB = 2048  // the output rows are dL/d(RMSNorm output): write that norm's backward instead
 };
 
 struct GemmArgs {
@@ -94,6 +95,16 @@ struct GemmArgs {
   long long ldn;
   float* norm_rstd;
   float norm_eps;
+  const float* nb_x;  // E_NORMB (GemmDesc::normb_*); nb_part [row tiles][N] f64 dgain partials
+  const float* nb_rstd;
+  const float* nb_gain;
+  const float* nb_add;
+  const float* nb_add_last;
+  const float* nb_dy_last;
+  int nb_seq;
+  const int32_t* nb_lens;
+  float* nb_dx;
+  double* nb_part;
   int vecA, vecB;
   int nblocks;  // tiles * batch * ksplit (the grid is padded to a multiple of 8)
 };
@@ -360,6 +371,60 @@ __device__ __forceinline__ void epi_norm4(const GemmArgs& p, float4 o, int row, 
   }
 }
 
+// RMSNorm backward of one row of a 128-wide tile from the epilogue's float4 gg = dL/dy (y the
+// norm's output; the 32 lanes of a half-wave hold one row): dx = rstd * (gg * gain - x_hat * md)
+// + the addends, md = mean(gg * gain * x_hat), x_hat = x * rstd; the lane's dgain terms gg * x_hat
+// are added to dw (column group col). Same arithmetic as rmsnorm_bwd_kernel. Every lane of the
+// half-wave takes part in the shuffle; rows past M contribute zeros.
+__device__ __forceinline__ void epi_normb4(const GemmArgs& p, float4 gg, int row, int col, float4& dw) {
+  const bool on = row < p.M;
+  const bool last = (p.nb_add_last || p.nb_dy_last) && on &&
+                    row % p.nb_seq == last_row(p.nb_lens, row / p.nb_seq, p.nb_seq);
+  if (last && p.nb_dy_last) {
+    const float4 a = *reinterpret_cast<const float4*>(p.nb_dy_last + (long long)(row / p.nb_seq) * p.N + col);
+    gg.x += a.x;
+    gg.y += a.y;
+    gg.z += a.z;
+    gg.w += a.w;
+  }
+  const float4 g = *reinterpret_cast<const float4*>(p.nb_gain + col);
+  float r = 0.f;
+  float4 xh = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (on) {
+    r = p.nb_rstd[row];
+    const float4 xv = *reinterpret_cast<const float4*>(p.nb_x + (long long)row * p.N + col);
+    xh = make_float4(xv.x * r, xv.y * r, xv.z * r, xv.w * r);
+  } else {
+    gg = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float dot = gg.x * g.x * xh.x + gg.y * g.y * xh.y + gg.z * g.z * xh.z + gg.w * g.w * xh.w;
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
+  const float md = dot * (1.0f / (float)p.N);
+  dw.x += gg.x * xh.x;
+  dw.y += gg.y * xh.y;
+  dw.z += gg.z * xh.z;
+  dw.w += gg.w * xh.w;
+  if (!on) return;
+  float4 o = make_float4(r * (gg.x * g.x - xh.x * md), r * (gg.y * g.y - xh.y * md), r * (gg.z * g.z - xh.z * md),
+                         r * (gg.w * g.w - xh.w * md));
+  if (p.nb_add) {
+    const float4 a = *reinterpret_cast<const float4*>(p.nb_add + (long long)row * p.N + col);
+    o.x += a.x;
+    o.y += a.y;
+    o.z += a.z;
+    o.w += a.w;
+  }
+  if (last && p.nb_add_last) {
+    const float4 a = *reinterpret_cast<const float4*>(p.nb_add_last + (long long)(row / p.nb_seq) * p.N + col);
+    o.x += a.x;
+    o.y += a.y;
+    o.z += a.z;
+    o.w += a.w;
+  }
+  *reinterpret_cast<float4*>(p.nb_dx + (long long)row * p.N + col) = o;
+}
+
 constexpr int T_S = 136;  // pitch of the staged output tile: rows h*4 apart land 32 banks apart
 constexpr int T_ROWS = BM / 2;  // the tile is staged in two halves of 64 rows
 constexpr int SMEM_FLOATS = (2 * NBUF * PANEL > T_ROWS * T_S) ? 2 * NBUF * PANEL : T_ROWS * T_S;
@@ -615,6 +680,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
   float* T = smem;
   const int cg = 4 * (threadIdx.x & 31);
   const int col = n0 + cg;
+  float4 nbw = make_float4(0.f, 0.f, 0.f, 0.f);  // E_NORMB: this thread's dgain terms
   float* C = p.C + (long long)b * p.sC;
   const float* resid = ((E & E_RESID) != 0) ? p.resid + (long long)b * p.sC : nullptr;
   // float4 path needs every row start 16-byte aligned in each operand the epilogue touches
@@ -654,6 +720,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
           for (int j = 0; j < 4 && col + j < p.N; ++j) P[(long long)row * p.N + col + j] = vv[j];
         }
       }
+    } else if constexpr ((E & E_NORMB) != 0) {
+#pragma unroll 1
+      for (int i = 0; i < T_ROWS / 8; ++i) {
+        const int lr = (threadIdx.x >> 5) + 8 * i;
+        const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
+        epi_normb4(p, v, m0 + half * T_ROWS + lr, col, nbw);
+      }
     } else {
 #pragma unroll 4
       for (int i = 0; i < T_ROWS / 8; ++i) {
@@ -663,6 +736,18 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
         const float4 o = epi_store4<E>(p, v, row, col, C, resid, aligned && full_cols && row < p.M);
         if constexpr ((E & E_NORM) != 0) epi_norm4(p, o, row, col);
       }
+    }
+  }
+  if constexpr ((E & E_NORMB) != 0) {
+    // the tile's dgain partial: the 8 row groups' sums of each column added in f64, in order
+    __syncthreads();  // T has been read out
+    *reinterpret_cast<float4*>(T + (threadIdx.x >> 5) * BN + cg) = nbw;
+    __syncthreads();
+    if (threadIdx.x < BN) {
+      double sum = 0.0;
+#pragma unroll
+      for (int g = 0; g < NT / 32; ++g) sum += (double)T[g * BN + threadIdx.x];
+      p.nb_part[(long long)(m0 / BM) * BN + threadIdx.x] = sum;
     }
   }
 }
@@ -936,6 +1021,16 @@ static GemmArgs to_args(const GemmDesc& d) {
   a.ldn = d.ldn;
   a.norm_rstd = d.norm_rstd;
   a.norm_eps = d.norm_eps;
+  a.nb_x = d.normb_x;
+  a.nb_rstd = d.normb_rstd;
+  a.nb_gain = d.normb_gain;
+  a.nb_add = d.normb_add;
+  a.nb_add_last = d.normb_add_last;
+  a.nb_dy_last = d.normb_dy_last;
+  a.nb_seq = d.normb_seq > 0 ? d.normb_seq : 1;
+  a.nb_lens = d.normb_lens;
+  a.nb_dx = d.normb_dx;
+  a.nb_part = d.normb_ws;
   auto aligned = [](const void* ptr, long long ld) {
     return ((reinterpret_cast<uintptr_t>(ptr) & 15) == 0) && (ld % 4 == 0);
   };
@@ -963,6 +1058,7 @@ static int epi_flags(const GemmDesc& d) {
   if (d.rope_cols > 0) e |= E_ROPE;
   if (d.dbias) e |= E_DBIAS;
   if (d.norm_out) e |= E_NORM;
+  if (d.normb_dx) e |= E_NORMB;
   return e;
 }
 
@@ -1022,6 +1118,7 @@ static GemmKernel pick_kernel(bool tA, bool tB, int e, bool bf) {
   GEMM_CASE(false, true, E_DGELU)
   GEMM_CASE(false, true, E_DRELU)
   GEMM_CASE(false, true, E_SPLIT)
+  GEMM_CASE_F32(false, true, E_NORMB)
   GEMM_CASE(true, false, 0)
   GEMM_CASE(true, false, E_BETA)
   GEMM_CASE(true, false, E_SPLIT)
@@ -1068,7 +1165,59 @@ static GemmKernel pick_small(bool tA, bool tB, int e) {
 
 static int num_cus();
 
+static int gemm_launch_one(const GemmDesc& d, hipStream_t stream);
+
+// c[b * seq + last_row(b)][:] += add[b][:] for each sample b (rows of width n).
+__global__ void add_last_rows_kernel(int nb, int seq, int n, const int32_t* __restrict__ lens,
+                                     const float* __restrict__ add, float* __restrict__ c) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)nb * n) return;
+  const int b = (int)(i / n), col = (int)(i % n);
+  c[((long long)b * seq + last_row(lens, b, seq)) * n + col] += add[i];
+}
+
+// Whether the RMSNorm backward of a product can run in its epilogue: 128x128 tiles holding the
+// whole 128-wide row, fp32, one batch, float4 rows, and room for the per-tile partials.
+static bool normb_fused(const GemmDesc& d) {
+  auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const int tiles_m = (d.M + BM - 1) / BM;
+  return d.N == BN && !d.bf16 && d.batch == 1 && !d.transA && d.transB && !use_small(d, num_cus()) &&
+         d.beta == 0.f && !d.bias && !d.resid && d.act == GEMM_ACT_NONE && d.dact == GEMM_DACT_NONE &&
+         d.rope_cols == 0 && !d.norm_out && !d.dbias && a16(d.normb_x) && a16(d.normb_dx) && a16(d.normb_gain) &&
+         a16(d.normb_add) && a16(d.normb_add_last) && a16(d.normb_dy_last) && d.normb_ws &&
+         d.normb_ws_bytes >= reduce_parts_workspace_bytes(tiles_m, d.N);
+}
+
 int gemm_launch(const GemmDesc& d, hipStream_t stream) {
+  if (d.normb_dx) {
+    if (!normb_fused(d)) {
+      // the product into C, then the row-norm backward kernel
+      TALOS_REQUIRE(d.C != nullptr && d.ldc == d.N, TALOS_ERR_UNSUPPORTED,
+                    "gemm: a row-norm backward after the product needs C with ldc == N");
+      GemmDesc g = d;
+      g.normb_dx = nullptr;
+      if (int rc = gemm_launch(g, stream)) return rc;
+      if (d.normb_dy_last) {
+        const int nb = d.M / (d.normb_seq > 0 ? d.normb_seq : 1);
+        ProfScope ps(stream, "add_last_rows_kernel", (double)nb * d.N, 12.0 * nb * d.N);
+        hipLaunchKernelGGL(add_last_rows_kernel, dim3(ceil_div((size_t)nb * d.N, 256)), dim3(256), 0, stream, nb,
+                           d.normb_seq > 0 ? d.normb_seq : 1, d.N, d.normb_lens, d.normb_dy_last, d.C);
+        TALOS_LAUNCHED("add_last_rows_kernel");
+      }
+      return rmsnorm_bwd_launch(d.M, d.N, d.normb_x, d.normb_gain, d.normb_rstd, d.C, 0.f, d.normb_dx,
+                                d.normb_beta_dw, d.normb_dw, d.normb_ws, stream, d.normb_add, d.normb_add_last,
+                                d.normb_seq, d.normb_lens);
+    }
+    GemmDesc g = d;
+    g.ksplit = 1;
+    if (int rc = gemm_launch_one(g, stream)) return rc;
+    if (!d.normb_dw) return TALOS_OK;
+    return reduce_parts_launch(d.N, (d.M + BM - 1) / BM, d.normb_ws, d.normb_beta_dw, d.normb_dw, stream);
+  }
+  return gemm_launch_one(d, stream);
+}
+
+static int gemm_launch_one(const GemmDesc& d, hipStream_t stream) {
   if (d.norm_out && (d.N != BN || d.bf16 || d.batch != 1 || use_small(d, num_cus()))) {
     // the fused row norm needs the whole 128-wide row in one 128x128 tile: otherwise the product,
     // then the separate row-norm kernel
@@ -1117,6 +1266,8 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
       if (d.resid) bytes += 4.0 * MN;
       if (d.aux) bytes += 4.0 * MN;
       if (d.norm_out) bytes += 4.0 * (MN + d.M + d.N);
+      // E_NORMB: x (and the addend) read, dx written instead of C, rstd and gain read
+      if (d.normb_dx) bytes += 4.0 * (MN * (1 + (d.normb_add != nullptr)) + d.M + d.N) + 8.0 * (d.M / BM + 1) * d.N;
       if (d.bias) bytes += 4.0 * d.N;
     }
     ProfScope ps(stream, name, 2.0 * MN * d.K * d.batch, bytes * d.batch);

@@ -56,6 +56,26 @@ struct GemmDesc {
   long long ldn = 0;
   float* norm_rstd = nullptr;
   float norm_eps = 0.f;
+  // RMSNorm backward after the product, C = dL/d(the norm's output) (rmsnorm_bwd_launch's
+  // arithmetic): normb_dx = rstd * (C * gain - x_hat * mean(C * gain * x_hat)) + normb_add (+
+  // normb_add_last[b] on the last row of each sample b, rows of normb_seq; normb_dy_last[b] is
+  // added to C on those rows before anything else), x_hat = x * rstd, and
+  // normb_dw = normb_beta_dw * normb_dw + the column sums of C * x_hat, through f64 partials in
+  // normb_ws. Fused into the epilogue when N = 128 (one tile holds the row; C is not written);
+  // other shapes write C (ldc = N) and run the row-norm backward kernel after the product.
+  const float* normb_x = nullptr;
+  const float* normb_rstd = nullptr;
+  const float* normb_gain = nullptr;
+  const float* normb_add = nullptr;
+  const float* normb_add_last = nullptr;
+  const float* normb_dy_last = nullptr;  // added to C on the last row of each sample first
+  int normb_seq = 1;
+  const int32_t* normb_lens = nullptr;
+  float* normb_dx = nullptr;
+  float* normb_dw = nullptr;
+  float normb_beta_dw = 0.f;
+  double* normb_ws = nullptr;
+  size_t normb_ws_bytes = 0;
   // bf16-in / fp32-accumulate: operands are rounded to bf16 (nearest even) as they are staged
   // into LDS and multiplied with v_mfma_f32_32x32x16_bf16; HBM layout and outputs stay fp32.
   bool bf16 = false;

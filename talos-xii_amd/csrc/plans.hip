@@ -450,6 +450,42 @@ static int before_write(talos_plan_s* p, hipStream_t s, const void* buf) {
   return TALOS_OK;
 }
 
+// dx = RMSNorm backward of dy = g.W^T ([M, K] x [d, K]^T, d = 128 fits one tile row) with the
+// norm's input x, gain and rstd; the product's epilogue computes it (C = dy is then not written,
+// else C is the scratch the separate kernels use). add: the residual gradient on every row;
+// add_last / dy_last: [batch, d] added to dx / dy on the last row of each sample; the gain's
+// gradient goes to dw.
+static int norm_bwd_mm(talos_plan_s* p, hipStream_t s, int M, int d, int K, const float* g, long long ldg,
+                       const float* W, long long ldw, float* C, const float* x, const float* gain, const float* rstd,
+                       const float* add, const float* add_last, const float* dy_last, int seq, float* dx,
+                       float* dw) {
+  GemmDesc gd;
+  gd.transB = 1;
+  gd.M = M;
+  gd.N = d;
+  gd.K = K;
+  gd.A = g;
+  gd.lda = ldg;
+  gd.B = W;
+  gd.ldb = ldw;
+  gd.C = C;
+  gd.ldc = d;
+  gd.ksplit = 1;
+  gd.normb_x = x;
+  gd.normb_gain = gain;
+  gd.normb_rstd = rstd;
+  gd.normb_add = add;
+  gd.normb_add_last = add_last;
+  gd.normb_dy_last = dy_last;
+  gd.normb_seq = seq;
+  gd.normb_lens = p->lens;
+  gd.normb_dx = dx;
+  gd.normb_dw = dw;
+  gd.normb_ws = p->red_ws;
+  gd.normb_ws_bytes = p->red_ws_bytes;
+  return gemm_launch(gd, s);
+}
+
 // Everything issued on the side stream completes before anything issued later on s.
 static int join_side(talos_plan_s* p, hipStream_t s) {
   if (!p->side) return TALOS_OK;
@@ -752,11 +788,10 @@ static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const f
   // u = xn2.W1 + b1
   rc = wgrad(p, s, g_u, d, F, R, xn2, d, g_u, F, G + o.w1, F, G + o.b1);
   if (rc) return rc;
-  rc = mm(p, s, 0, 1, R, d, F, g_u, F, P + o.w1, F, g_xn, d);
-  if (rc) return rc;
-  // h2 -> (residual) + rmsnorm2
+  // xn2 = rmsnorm2(h2): g_h2 = its backward of g_u.W1^T, plus the residual gradient gout
   if ((rc = before_write(p, s, g_h2))) return rc;
-  rc = rmsnorm_bwd_launch(R, d, h2, P + o.g2, rstd2, g_xn, 1.f, g_h2, 0.f, G + o.g2, p->red_ws, s, gout);
+  rc = norm_bwd_mm(p, s, R, d, F, g_u, F, P + o.w1, F, g_xn, h2, P + o.g2, rstd2, gout, nullptr, nullptr, 1, g_h2,
+                   G + o.g2);
   if (rc) return rc;
   // h2 = x + o.Wo
   rc = wgrad(p, s, g_h2, ow, d, R, ob, ow, g_h2, d, G + o.wo, d);
@@ -785,9 +820,10 @@ static int block_qkv_backward(talos_plan_s* p, const talos_block_cfg& c, const f
   // qkv = xn1.Wqkv
   int rc = wgrad(p, s, p->g_qkv, d, 3 * d, M, L.xn1, d, p->g_qkv, 3 * d, G + o.wqkv, 3 * d);
   if (rc) return rc;
-  rc = mm(p, s, 0, 1, M, d, 3 * d, p->g_qkv, 3 * d, P + o.wqkv, 3 * d, p->g_xn, d);
-  if (rc) return rc;
-  return block_norm1_backward(p, c, P, G, o, L, g_h2, g_h2_last, dx, s);
+  // xn1 = rmsnorm1(x): dx = its backward of g_qkv.Wqkv^T, plus the residual gradient through h2
+  if ((rc = before_write(p, s, dx))) return rc;
+  return norm_bwd_mm(p, s, M, d, 3 * d, p->g_qkv, 3 * d, P + o.wqkv, 3 * d, p->g_xn, L.x, P + o.g1, L.rstd1, g_h2,
+                     g_h2_last, nullptr, c.seq, dx, G + o.g1);
 }
 
 // Attention half backward over all rows: g_o = dL/do [tokens, attn_width], the residual gradient
@@ -846,17 +882,6 @@ __global__ void scatter_last_kernel(int B, int S, int d, const int32_t* __restri
     const int e = (int)(i % d);
     const int b = (int)(row / S), t = (int)(row % S);
     g[i] = t == last_row(lens, b, S) ? gl[(long long)b * d + e] : 0.f;
-  }
-}
-
-// g[b * S + last_row(b)] += gl[b] (the rest of g unchanged)
-__global__ void scatter_add_last_kernel(int B, int S, int d, const int32_t* __restrict__ lens,
-                                        const float* __restrict__ gl, float* __restrict__ g) {
-  const long long n = (long long)B * d;
-  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
-    const long long b = i / d;
-    const int e = (int)(i % d);
-    g[(b * S + last_row(lens, (int)b, S)) * d + e] += gl[i];
   }
 }
 
@@ -1541,15 +1566,12 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
       float* g_kv = p->g_qkv + d;
       if ((rc = wgrad(p, s, p->g_qkv, d, 2 * d, M, L.xn1, d, g_kv, 3 * d, G + o.wqkv + d, 3 * d))) return rc;
       if ((rc = wgrad(p, s, R.dq, d, d, B, R.xn1, d, R.dq, d, G + o.wqkv, 3 * d))) return rc;
-      if ((rc = mm(p, s, 0, 1, M, d, 2 * d, g_kv, 3 * d, params + o.wqkv + d, 3 * d, p->g_xn, d))) return rc;
+      // dxn1 = g_kv.Wkv^T on every row, plus dq.Wq^T on the last rows; then rmsnorm1's backward
+      // with the residual gradient R.g_h2 on the last rows
       if ((rc = mm(p, s, 0, 1, B, d, d, R.dq, d, params + o.wqkv, 3 * d, R.g_xnq, d))) return rc;
-      {
-        ProfScope ps_s(s, "scatter_add_last_kernel", 0.0, 12.0 * B * d);
-        hipLaunchKernelGGL(scatter_add_last_kernel, dim3(ceil_div((size_t)B * d, 256)), dim3(256), 0, s, B, c.seq, d,
-                           p->lens, R.g_xnq, p->g_xn);
-        TALOS_LAUNCHED("scatter_add_last_kernel");
-      }
-      rc = block_norm1_backward(p, bc, params, G, o, L, nullptr, R.g_h2, p->g_out, s);
+      if ((rc = before_write(p, s, p->g_out))) return rc;
+      rc = norm_bwd_mm(p, s, M, d, 2 * d, g_kv, 3 * d, params + o.wqkv + d, 3 * d, p->g_xn, L.x, params + o.g1,
+                       L.rstd1, nullptr, R.g_h2, R.g_xnq, c.seq, p->g_out, G + o.g1);
     } else {
       // the row gradients spread over the full token grid
       const int ow = attn_width(bc);

@@ -148,6 +148,8 @@ int reduce_parts_launch(int cols, int nparts, double* part, float beta, float* o
   return TALOS_OK;
 }
 
+size_t reduce_parts_workspace_bytes(int nparts, int cols) { return parts_rows(nparts) * cols * sizeof(double); }
+
 size_t colsum_workspace_bytes(int rows, int cols) { return parts_rows(colsum_parts(rows)) * cols * sizeof(double); }
 
 int colsum_launch(int rows, int cols, const float* dy, long long ld, float beta, float* out, double* ws,
