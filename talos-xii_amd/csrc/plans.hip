@@ -376,6 +376,10 @@ static int alloc_workspaces(talos_plan_s* p) {
   return TALOS_OK;
 }
 
+// The embedding gradient kernel's workgroups and input width (embed_wgrad_kernel).
+constexpr int kEmbedBlocks = 256;
+constexpr int kEmbedIn = 8;
+
 // GEMM helpers ---------------------------------------------------------------
 static int mm_ws(talos_plan_s* p, hipStream_t s, float* wsp, int tA, int tB, int M, int N, int K, const float* A,
                  long long lda, const float* B, long long ldb, float* C, long long ldc, float beta = 0.f,
@@ -1409,6 +1413,7 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
     p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, wgrad_ws(p, (int)B, (int)d, (int)d));
     p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, wgrad_ws(p, (int)B, (int)d, (int)A));
     p->red_ws_bytes = std::max(p->red_ws_bytes, colsum_workspace_bytes((int)M, (int)d));
+    p->red_ws_bytes = std::max(p->red_ws_bytes, reduce_parts_workspace_bytes(kEmbedBlocks, (kEmbedIn + 1) * (int)d));
     rc = alloc_workspaces(p);
   }
   if (rc) {
@@ -1460,6 +1465,57 @@ int talos_ppo_forward_f32(talos_plan plan, const float* params, const float* sta
 }
 
 // One minibatch of n samples: forward, loss (and its statistics), backward into dparams.
+// The embedding's weight and bias gradients, [I + 1][128] (W_e rows, then b_e): dW[i][c] =
+// sum_r states[r][i] g[r][c] and db[c] = sum_r g[r][c], for I = in_dim = 8 and d = 128. A
+// product of 8 rows would leave most of a 64x64 MFMA tile empty and write kEmbedBlocks-fold
+// split-K partials; here each workgroup sums a contiguous chunk of rows (32 float4 column groups
+// x 8 row lanes, f32 over the lane's rows, f64 across lanes) into one partial row, and
+// reduce_parts_launch adds the partials in a fixed order.
+__global__ __launch_bounds__(256) void embed_wgrad_kernel(int rows, const float* __restrict__ states,
+                                                          const float* __restrict__ g, double* __restrict__ part) {
+  constexpr int I = kEmbedIn, N = 128;
+  __shared__ float red[8][(I + 1) * N];
+  const int cg = threadIdx.x & 31, rl = threadIdx.x >> 5;
+  const int chunk = (rows + gridDim.x - 1) / gridDim.x, r0 = blockIdx.x * chunk, r1 = min(rows, r0 + chunk);
+  float4 acc[I + 1];
+#pragma unroll
+  for (int i = 0; i <= I; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+  for (int r = r0 + rl; r < r1; r += 8) {
+    const float4 gv = *reinterpret_cast<const float4*>(g + (long long)r * N + 4 * cg);
+    const float4 a0 = *reinterpret_cast<const float4*>(states + (long long)r * I);
+    const float4 a1 = *reinterpret_cast<const float4*>(states + (long long)r * I + 4);
+    const float av[I] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+      acc[i].x = fmaf(av[i], gv.x, acc[i].x);
+      acc[i].y = fmaf(av[i], gv.y, acc[i].y);
+      acc[i].z = fmaf(av[i], gv.z, acc[i].z);
+      acc[i].w = fmaf(av[i], gv.w, acc[i].w);
+    }
+    acc[I].x += gv.x;
+    acc[I].y += gv.y;
+    acc[I].z += gv.z;
+    acc[I].w += gv.w;
+  }
+#pragma unroll
+  for (int i = 0; i <= I; ++i) *reinterpret_cast<float4*>(&red[rl][i * N + 4 * cg]) = acc[i];
+  __syncthreads();
+  for (int c = threadIdx.x; c < (I + 1) * N; c += 256) {
+    double sum = 0.0;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) sum += (double)red[l][c];
+    part[(long long)blockIdx.x * (I + 1) * N + c] = sum;
+  }
+}
+
+// Whether the embedding gradient takes embed_wgrad_kernel: in_dim 8, d 128, b_e right after W_e,
+// 16-byte rows.
+static bool embed_wgrad_applies(const talos_ppo_cfg& c, const PpoOff& po, const float* states, const float* g) {
+  return c.in_dim == kEmbedIn && c.d_model == 128 && po.be == po.we + (size_t)kEmbedIn * 128 &&
+         ((reinterpret_cast<uintptr_t>(states) | reinterpret_cast<uintptr_t>(g)) & 15) == 0;
+}
+
 static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const float* states, const int32_t* actions,
                          const float* adv, const float* ret, const float* old_logp, float* loss_out, float* dparams,
                          double* stats, int stats_acc, hipStream_t s) {
@@ -1586,7 +1642,17 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
     std::swap(gcur, gnext);
   }
   // embed
-  rc = wgrad(p, s, gcur, c.in_dim, d, M, states, c.in_dim, gcur, d, G + po.we, d, G + po.be);
+  if (embed_wgrad_applies(c, po, states, gcur)) {
+    {
+      ProfScope ps_e(s, "embed_wgrad_kernel", 2.0 * M * (kEmbedIn + 1) * d,
+                     4.0 * M * (kEmbedIn + d) + 8.0 * kEmbedBlocks * (kEmbedIn + 1) * d);
+      hipLaunchKernelGGL(embed_wgrad_kernel, dim3(kEmbedBlocks), dim3(256), 0, s, M, states, gcur, p->red_ws);
+      TALOS_LAUNCHED("embed_wgrad_kernel");
+    }
+    rc = reduce_parts_launch((kEmbedIn + 1) * d, kEmbedBlocks, p->red_ws, 0.f, G + po.we, s);
+  } else {
+    rc = wgrad(p, s, gcur, c.in_dim, d, M, states, c.in_dim, gcur, d, G + po.we, d, G + po.be);
+  }
   if (rc) return rc;
   return join_side(p, s);
 }
