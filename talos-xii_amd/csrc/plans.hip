@@ -377,7 +377,7 @@ static int alloc_workspaces(talos_plan_s* p) {
 }
 
 // The embedding gradient kernel's workgroups and input width (embed_wgrad_kernel).
-constexpr int kEmbedBlocks = 256;
+constexpr int kEmbedBlocks = 1024;
 constexpr int kEmbedIn = 8;
 
 // GEMM helpers ---------------------------------------------------------------
@@ -1480,7 +1480,7 @@ __global__ __launch_bounds__(256) void embed_wgrad_kernel(int rows, const float*
   float4 acc[I + 1];
 #pragma unroll
   for (int i = 0; i <= I; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
+#pragma unroll 8
   for (int r = r0 + rl; r < r1; r += 8) {
     const float4 gv = *reinterpret_cast<const float4*>(g + (long long)r * N + 4 * cg);
     const float4 a0 = *reinterpret_cast<const float4*>(states + (long long)r * I);
