@@ -946,32 +946,36 @@ __global__ __launch_bounds__(NT) void gemm_small_kernel(GemmArgs p) {
 }
 
 // Sums the split-K partials in f64 and applies the epilogue (beta and bias only). Workgroup of
-// 1024 threads = 16 waves: lane <-> one of 64 consecutive elements, wave w <-> splits w, w+16, ...
+// 256 threads = 4 waves: lane <-> one of 64 consecutive elements, wave w <-> splits w, w+4, ...
+// (small workgroups, so the reduction finds room beside a product running on another stream).
 // Row M of the partials (when present) holds the bias-gradient column sums.
 template <int E>
-__global__ __launch_bounds__(1024) void gemm_splitk_reduce(GemmArgs p) {
-  __shared__ double red[16][64];
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmArgs p) {
+  constexpr int W = 4;
+  __shared__ double red[W][64];
   const int rows = p.M + (p.dbias ? 1 : 0);
   const long long RN = (long long)rows * p.N;
   const int b = blockIdx.y;
   const float* P = p.part + (long long)b * p.ksplit * RN;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const long long e = (long long)blockIdx.x * 64 + lane;
-  double s0 = 0.0, s1 = 0.0;
+  double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
   if (e < RN) {
     int k = w;
-    for (; k + 16 < p.ksplit; k += 32) {
+    for (; k + 3 * W < p.ksplit; k += 4 * W) {
       s0 += (double)P[k * RN + e];
-      s1 += (double)P[(k + 16) * RN + e];
+      s1 += (double)P[(k + W) * RN + e];
+      s2 += (double)P[(k + 2 * W) * RN + e];
+      s3 += (double)P[(k + 3 * W) * RN + e];
     }
-    if (k < p.ksplit) s0 += (double)P[k * RN + e];
+    for (; k < p.ksplit; k += W) s0 += (double)P[k * RN + e];
   }
-  red[w][lane] = s0 + s1;
+  red[w][lane] = (s0 + s1) + (s2 + s3);
   __syncthreads();
   if (w != 0 || e >= RN) return;
   double s = 0.0;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) s += red[i][lane];
+  for (int i = 0; i < W; ++i) s += red[i][lane];
   const int row = (int)(e / p.N), col = (int)(e % p.N);
   if (row == p.M) {
     float* db = p.dbias + (long long)b * p.N;
@@ -1281,10 +1285,10 @@ static int gemm_launch_one(const GemmDesc& d, hipStream_t stream) {
     char rname[48];
     snprintf(rname, sizeof(rname), "gemm_splitk_reduce<%d>", re);
     ProfScope ps(stream, rname, 0.0, 4.0 * (double)RN * d.batch * (a.ksplit + 1 + (d.beta != 0.f)));
-    if (re == 0) hipLaunchKernelGGL(gemm_splitk_reduce<0>, rg, dim3(1024), 0, stream, a);
-    else if (re == E_BETA) hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA>, rg, dim3(1024), 0, stream, a);
-    else if (re == E_BIAS) hipLaunchKernelGGL(gemm_splitk_reduce<E_BIAS>, rg, dim3(1024), 0, stream, a);
-    else hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA | E_BIAS>, rg, dim3(1024), 0, stream, a);
+    if (re == 0) hipLaunchKernelGGL(gemm_splitk_reduce<0>, rg, dim3(256), 0, stream, a);
+    else if (re == E_BETA) hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA>, rg, dim3(256), 0, stream, a);
+    else if (re == E_BIAS) hipLaunchKernelGGL(gemm_splitk_reduce<E_BIAS>, rg, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA | E_BIAS>, rg, dim3(256), 0, stream, a);
     TALOS_LAUNCHED("gemm_splitk_reduce");
   }
   return TALOS_OK;

@@ -81,18 +81,20 @@ __global__ __launch_bounds__(256) void colsum_partial_kernel(int rows, int cols,
   if (w == 0 && c < cols) part[(long long)blockIdx.y * cols + c] = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
 }
 
-// out[c] = beta*out[c] + sum_p part[p][c]: 16 waves per 64 columns, LDS combine in f64.
-__global__ __launch_bounds__(1024) void reduce_parts_kernel(int cols, int nparts, const double* __restrict__ part,
-                                                            float beta, float* __restrict__ out) {
-  __shared__ double red[16][64];
+// out[c] = beta*out[c] + sum_p part[p][c]: 4 waves per 64 columns, LDS combine in f64 (small
+// workgroups, so the reduction finds room beside a product running on another stream).
+__global__ __launch_bounds__(256) void reduce_parts_kernel(int cols, int nparts, const double* __restrict__ part,
+                                                           float beta, float* __restrict__ out) {
+  constexpr int W = 4;
+  __shared__ double red[W][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
   double s0 = 0.0, s1 = 0.0;
   if (c < cols) {
     int p = w;
-    for (; p + 16 < nparts; p += 32) {
+    for (; p + W < nparts; p += 2 * W) {
       s0 += part[(long long)p * cols + c];
-      s1 += part[(long long)(p + 16) * cols + c];
+      s1 += part[(long long)(p + W) * cols + c];
     }
     if (p < nparts) s0 += part[(long long)p * cols + c];
   }
@@ -100,7 +102,7 @@ __global__ __launch_bounds__(1024) void reduce_parts_kernel(int cols, int nparts
   __syncthreads();
   if (w == 0 && c < cols) {
     double s = 0.0;
-    for (int i = 0; i < 16; ++i) s += red[i][lane];
+    for (int i = 0; i < W; ++i) s += red[i][lane];
     out[c] = (float)(s + (beta != 0.f ? (double)out[c] : 0.0));
   }
 }
@@ -143,7 +145,7 @@ int reduce_parts_launch(int cols, int nparts, double* part, float beta, float* o
     nparts = groups;
   }
   ProfScope ps(s, "reduce_parts_kernel", (double)nparts * cols, 8.0 * nparts * cols + 4.0 * cols);
-  hipLaunchKernelGGL(reduce_parts_kernel, dim3(ceil_div(cols, 64)), dim3(1024), 0, s, cols, nparts, part, beta, out);
+  hipLaunchKernelGGL(reduce_parts_kernel, dim3(ceil_div(cols, 64)), dim3(256), 0, s, cols, nparts, part, beta, out);
   TALOS_LAUNCHED("reduce_parts_kernel");
   return TALOS_OK;
 }
