@@ -91,7 +91,7 @@ constexpr bool kFwdSel = TALOS_ATTN_FWD_SEL, kBwdSel = TALOS_ATTN_BWD_SEL, kFuse
 // Zeros that out-of-range rows and columns read instead of memory: selecting the address (not the
 // loaded value) keeps every load unconditional, so a lane's loads issue back to back with no
 // branch around them, and the values are exactly 0.
-__device__ __align__(16) const float kAttnZeros[128] = {};
+__device__ __align__(16) float kAttnZeros[128] = {};  // global (not constant) memory: selecting between it and a row keeps global loads
 
 // Loads half of row `row` (elements [HALF*h, HALF*h + HALF) of the head's `dim` values starting
 // at column col0) times `scale`; rows >= S and elements >= dim read as 0. SEL = true selects the
@@ -455,7 +455,9 @@ __device__ __forceinline__ void mfma_p_lds(const float (&P)[16], const float* ti
 #define TALOS_ATTN_STAGE 1
 #endif
 
-template <int DKM, int DVM>
+// VEC: every row is known 16-byte aligned (a.vec), so the row loads take no branch and the five
+// operands' loads are all in flight before the first use.
+template <int DKM, int DVM, bool VEC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BWD_WAVES))) void
 attn_bwd_fused_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32;
@@ -484,12 +486,17 @@ attn_bwd_fused_kernel(AttnArgs a) {
   const bool rok = l32 < a.S;             // this lane's row (query l32 of q / dO / O)
   const bool kok = l32 < key_len(a, b);   // ... and its key l32 of k / v takes part
 
-  float gv[VH];
-  load_half<VH, kFusedSel>(gv, a.dout, a.lddo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+  // every row this wave reads, issued before the first use: one memory latency, not five
+  float gv[VH], ov[VH], qv[KH], kv[KH], vv[VH];
+  const bool vec = VEC || a.vec;
+  load_half<VH, kFusedSel>(gv, a.dout, a.lddo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, vec);
+  load_half<VH, kFusedSel>(ov, a.o, a.ldo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, vec);
+  load_half<KH, kFusedSel>(qv, a.q, a.ldq, tok0, l32, a.S, hd * a.dk, a.dk, h, a.scale, vec);
+  load_half<KH, kFusedSel>(kv, a.k, a.ldk, tok0, l32, a.S, hd * a.dk, a.dk, h, 1.f, vec);
+  load_half<VH, kFusedSel>(vv, a.v, a.ldv, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, vec);
+  const float lse = a.lse[(long long)pair * a.S + (rok ? l32 : 0)];
   if constexpr (STAGE) stage_half<VH, TP>(Gs, gv, l32, h);
   {
-    float ov[VH];
-    load_half<VH, kFusedSel>(ov, a.o, a.ldo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
     float d0 = 0.f, d1 = 0.f;
 #pragma unroll
     for (int i = 0; i < VH; i += 2) {
@@ -498,7 +505,6 @@ attn_bwd_fused_kernel(AttnArgs a) {
     }
     float D = d0 + d1;
     D += __shfl_xor(D, 32, 64);
-    const float lse = a.lse[(long long)pair * a.S + (rok ? l32 : 0)];
     if (h == 0) {
       Dl[l32] = rok ? D : 0.f;
       Ll[l32] = rok ? lse : 0.f;
@@ -507,21 +513,12 @@ attn_bwd_fused_kernel(AttnArgs a) {
   floatx16 sacc, pacc;
 #pragma unroll
   for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
-  {
-    float qv[KH], kv[KH];
-    load_half<KH, kFusedSel>(qv, a.q, a.ldq, tok0, l32, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
-    load_half<KH, kFusedSel>(kv, a.k, a.ldk, tok0, l32, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
-    if constexpr (STAGE) {
-      stage_half<KH, TP>(Qs, qv, l32, h);
-      stage_half<KH, TP>(Ks, kv, l32, h);
-    }
-    sacc = mfma_rows<KH>(qv, kv, sacc);  // S[q, key]
+  if constexpr (STAGE) {
+    stage_half<KH, TP>(Qs, qv, l32, h);
+    stage_half<KH, TP>(Ks, kv, l32, h);
   }
-  {
-    float vv[VH];
-    load_half<VH, kFusedSel>(vv, a.v, a.ldv, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
-    pacc = mfma_rows<VH>(gv, vv, pacc);  // dP[q, key]
-  }
+  sacc = mfma_rows<KH>(qv, kv, sacc);  // S[q, key]
+  pacc = mfma_rows<VH>(gv, vv, pacc);  // dP[q, key]
   wave_lds_sync();
   // lse / D of the queries acc_row(4j .. 4j+3, h) = 8j + 4h + 0..3: one 16-byte read each
   float lq[16], dq_[16];
@@ -698,6 +695,11 @@ static int attn_bwd_fused(const AttnArgs& a, int dkm, int dvm, hipStream_t s) {
   // s = q.k, dp = dO.v, dv = p^T dO, dk = ds^T q, dq = ds k; reads q k v o dO lse, writes dq dk dv
   const double flops = kept_pairs(a) * (6.0 * a.dk + 4.0 * a.dv);
   const double bytes = 4.0 * rows * (4.0 * a.dk + 4.0 * a.dv + 1.0);
+  if (dkm == 32 && dvm == 32 && a.vec) {
+    ProfScope ps(s, "attn_bwd_fused_kernel<32, 32, true>", flops, bytes);
+    hipLaunchKernelGGL((attn_bwd_fused_kernel<32, 32, true>), grid, dim3(256), 0, s, a);
+    return launch_status("attn_bwd_fused_kernel");
+  }
   ATTN_ALL(attn_bwd_fused_kernel)
 }
 
