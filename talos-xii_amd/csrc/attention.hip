@@ -263,6 +263,64 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_
   if (h == 0 && q < a.S) a.lse[(long long)pair * a.S + q] = (l > 0.f) ? m + logf(l) : kNegInf;
 }
 
+// Forward for S <= 32 at head dims 32 / 32 with 16-byte rows: one key block, so a wave's q, k and
+// v rows are all in flight before the first product and the softmax needs no running rescale.
+// Same arithmetic as attn_fwd_kernel's single-block pass.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_FWD_WAVES))) void
+attn_fwd_s32_kernel(AttnArgs a) {
+  constexpr int KH = 16;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pair >= a.B * a.H) return;  // uniform per wave
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int q = l32;
+  const int Sk = key_len(a, b);
+  float qv[KH], kv[KH], vm[16];
+  load_half<KH, true>(qv, a.q, a.ldq, tok0, q, a.S, hd * a.dk, 32, h, a.scale, true);
+  load_half<KH, true>(kv, a.k, a.ldk, tok0, l32, a.S, hd * a.dk, 32, h, 1.f, true);
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const int row = acc_row(s, h);
+    vm[s] = *(row < a.S ? a.v + (tok0 + row) * a.ldv + hd * a.dv + l32 : kAttnZeros + l32);
+  }
+  floatx16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  acc = mfma_rows<KH>(kv, qv, acc);  // S^T: register r <-> key acc_row(r, h), lane <-> query
+  float sv[16], m = kNegInf;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int key = acc_row(r, h);
+    const bool ok = key < Sk && (!a.causal || key <= q);
+    sv[r] = ok ? acc[r] : kNegInf;
+    m = fmaxf(m, sv[r]);
+  }
+  m = fmaxf(m, __shfl_xor(m, 32, 64));
+  float l = 0.f;
+  if (m != kNegInf) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) l += expf(sv[r] - m);
+  }
+  l += __shfl_xor(l, 32, 64);
+  const float inv_l = l > 0.f ? 1.f / l : 0.f;
+  floatx16 oacc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) oacc[r] = 0.f;
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const float p = (m == kNegInf) ? 0.f : expf(sv[s] - m) * inv_l;
+    oacc = __builtin_amdgcn_mfma_f32_32x32x2f32(p, vm[s], oacc, 0, 0, 0);
+  }
+  // O in accumulator layout: register r <-> query acc_row(r, h), lane <-> column
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int qr = acc_row(r, h);
+    if (qr < a.S) a.o[(tok0 + qr) * a.ldo + hd * a.dv + l32] = oacc[r];
+  }
+  if (h == 0 && q < a.S) a.lse[(long long)pair * a.S + q] = (l > 0.f) ? m + logf(l) : kNegInf;
+}
+
 // ---------------------------------------------------------------------------
 // dQ (and D = dO . O): wave per (pair, query block), S^T layout
 // ---------------------------------------------------------------------------
@@ -662,6 +720,11 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
   // QK^T and PV over the kept pairs; q, k, v read, o and lse written
   const double flops = kept_pairs(a) * (2.0 * a.dk + 2.0 * a.dv);
   const double bytes = 4.0 * rows * (2.0 * a.dk + a.dv) + 4.0 * rows * (a.dv + 1.0);
+  if (d.dk == 32 && d.dv == 32 && a.S <= 32 && a.vec) {
+    ProfScope ps(s, "attn_fwd_s32_kernel", flops, bytes);
+    hipLaunchKernelGGL(attn_fwd_s32_kernel, dim3(ceil_div((size_t)a.B * a.H, 4)), dim3(256), 0, s, a);
+    return launch_status("attn_fwd_s32_kernel");
+  }
   ATTN_ALL(attn_fwd_kernel)
 }
 
