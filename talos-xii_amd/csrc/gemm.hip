@@ -375,9 +375,26 @@ __device__ __forceinline__ void epi_norm4(const GemmArgs& p, float4 o, int row, 
 // norm's output; the 32 lanes of a half-wave hold one row): dx = rstd * (gg * gain - x_hat * md)
 // + the addends, md = mean(gg * gain * x_hat), x_hat = x * rstd; the lane's dgain terms gg * x_hat
 // are added to dw (column group col). Same arithmetic as rmsnorm_bwd_kernel. Every lane of the
-// half-wave takes part in the shuffle; rows past M contribute zeros.
-__device__ __forceinline__ void epi_normb4(const GemmArgs& p, float4 gg, int row, int col, float4& dw) {
+// half-wave takes part in the shuffle; rows past M contribute zeros. The row's x and rstd are
+// loaded by normb_load one row ahead (normb_apply uses them), so the epilogue's loads overlap the
+// previous row's work instead of each row waiting on memory.
+struct NbIn {
+  float4 x;
+  float r;
+};
+__device__ __forceinline__ NbIn normb_load(const GemmArgs& p, int row, int col) {
+  NbIn in;
   const bool on = row < p.M;
+  in.r = on ? p.nb_rstd[row] : 0.f;
+  in.x = on ? *reinterpret_cast<const float4*>(p.nb_x + (long long)row * p.N + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+  return in;
+}
+__device__ __forceinline__ void normb_apply(const GemmArgs& p, float4 gg, int row, int col, const NbIn& in,
+                                            const float4& g, float4& dw) {
+  const bool on = row < p.M;
+  // the addend row, issued first: its latency runs under the row reduction below
+  const float4 add = on && p.nb_add ? *reinterpret_cast<const float4*>(p.nb_add + (long long)row * p.N + col)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
   const bool last = (p.nb_add_last || p.nb_dy_last) && on &&
                     row % p.nb_seq == last_row(p.nb_lens, row / p.nb_seq, p.nb_seq);
   if (last && p.nb_dy_last) {
@@ -387,16 +404,9 @@ __device__ __forceinline__ void epi_normb4(const GemmArgs& p, float4 gg, int row
     gg.z += a.z;
     gg.w += a.w;
   }
-  const float4 g = *reinterpret_cast<const float4*>(p.nb_gain + col);
-  float r = 0.f;
-  float4 xh = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (on) {
-    r = p.nb_rstd[row];
-    const float4 xv = *reinterpret_cast<const float4*>(p.nb_x + (long long)row * p.N + col);
-    xh = make_float4(xv.x * r, xv.y * r, xv.z * r, xv.w * r);
-  } else {
-    gg = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  if (!on) gg = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float r = in.r;
+  const float4 xh = make_float4(in.x.x * r, in.x.y * r, in.x.z * r, in.x.w * r);
   float dot = gg.x * g.x * xh.x + gg.y * g.y * xh.y + gg.z * g.z * xh.z + gg.w * g.w * xh.w;
 #pragma unroll
   for (int off = 16; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
@@ -408,13 +418,10 @@ __device__ __forceinline__ void epi_normb4(const GemmArgs& p, float4 gg, int row
   if (!on) return;
   float4 o = make_float4(r * (gg.x * g.x - xh.x * md), r * (gg.y * g.y - xh.y * md), r * (gg.z * g.z - xh.z * md),
                          r * (gg.w * g.w - xh.w * md));
-  if (p.nb_add) {
-    const float4 a = *reinterpret_cast<const float4*>(p.nb_add + (long long)row * p.N + col);
-    o.x += a.x;
-    o.y += a.y;
-    o.z += a.z;
-    o.w += a.w;
-  }
+  o.x += add.x;
+  o.y += add.y;
+  o.z += add.z;
+  o.w += add.w;
   if (last && p.nb_add_last) {
     const float4 a = *reinterpret_cast<const float4*>(p.nb_add_last + (long long)(row / p.nb_seq) * p.N + col);
     o.x += a.x;
@@ -721,11 +728,17 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
         }
       }
     } else if constexpr ((E & E_NORMB) != 0) {
+      const float4 g = *reinterpret_cast<const float4*>(p.nb_gain + col);
+      const int rbase = m0 + half * T_ROWS + (threadIdx.x >> 5);
+      NbIn cur = normb_load(p, rbase, col);
 #pragma unroll 1
       for (int i = 0; i < T_ROWS / 8; ++i) {
         const int lr = (threadIdx.x >> 5) + 8 * i;
+        NbIn nxt = cur;
+        if (i + 1 < T_ROWS / 8) nxt = normb_load(p, rbase + 8 * (i + 1), col);
         const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
-        epi_normb4(p, v, m0 + half * T_ROWS + lr, col, nbw);
+        normb_apply(p, v, rbase + 8 * i, col, cur, g, nbw);
+        cur = nxt;
       }
     } else {
 #pragma unroll 4
