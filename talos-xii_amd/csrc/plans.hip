@@ -366,9 +366,12 @@ static int alloc_workspaces(talos_plan_s* p) {
   rc |= plan_alloc(p, &red, (p->red_ws_bytes + 3) / 4 + 2);
   p->red_ws = reinterpret_cast<double*>(red);
   if (rc) return TALOS_ERR_ALLOC;
-  // the side stream of the backward (TALOS_SINGLE_STREAM=1 keeps every launch on the caller's)
-  const char* one = std::getenv("TALOS_SINGLE_STREAM");
-  if (one && one[0] == '1') return TALOS_OK;
+  // The backward's side stream, when TALOS_BWD_SIDE_STREAM=1 at plan creation. Off by default:
+  // overlapping the two streams gains about 1 % of the C4 step, but then the duration of a
+  // kernel (events, rocprofv3) includes the time it shares the GPU with the other stream, and
+  // per-kernel rooflines stop meaning anything.
+  const char* two = std::getenv("TALOS_BWD_SIDE_STREAM");
+  if (!(two && two[0] == '1')) return TALOS_OK;
   if (plan_alloc(p, &p->gemm_ws2, (p->gemm_ws_bytes + 3) / 4)) return TALOS_ERR_ALLOC;
   TALOS_HIP(hipStreamCreateWithFlags(&p->side, hipStreamNonBlocking));
   TALOS_HIP(hipEventCreateWithFlags(&p->ev_fork, hipEventDisableTiming));

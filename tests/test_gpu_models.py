@@ -115,6 +115,24 @@ def test_ppo_minibatch_vs_oracle(oracle, B, S, L):
         check_close(dp[sl], dp_r[sl], name=f"d{n}", scale_floor=GRAD_SCALE_FLOOR)
 
 
+@pytest.mark.parametrize("B,L", [(256, 3), (1024, 2)])
+def test_ppo_side_stream_backward_matches(oracle, monkeypatch, B, L):
+    """The weight-gradient products on the backward's side stream (TALOS_BWD_SIDE_STREAM=1) give
+    the same bits as the one-stream backward: the same products with the same splits, only
+    overlapped. Three layers exercise the guards on buffers a lower layer overwrites; B = 1024
+    runs the fused norm-backward epilogues and the full-width products."""
+    rng = np.random.default_rng(2100 + B)
+    cfg, ocfg = ppo_cfgs(oracle, B, S=32, L=L)
+    p = f32(ppo_params(rng, ocfg))
+    states, actions, adv, ret, old = ppo_inputs(rng, ocfg, p, oracle)
+    monkeypatch.delenv("TALOS_BWD_SIDE_STREAM", raising=False)
+    one = run_ppo(cfg, p, states, actions, adv, ret, old)
+    monkeypatch.setenv("TALOS_BWD_SIDE_STREAM", "1")
+    two = run_ppo(cfg, p, states, actions, adv, ret, old)
+    assert one[0] == two[0]
+    assert np.array_equal(one[1], two[1])
+
+
 def test_ppo_bad_action_is_nan_not_a_fault(oracle):
     rng = np.random.default_rng(7)
     cfg, ocfg = ppo_cfgs(oracle, 4, S=4, L=1)
