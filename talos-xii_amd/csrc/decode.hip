@@ -29,6 +29,7 @@
 #include "gemm.hpp"
 #include "plans.hpp"
 #include "rowops.hpp"
+#include "rowtile.hpp"
 
 struct talos_decoder_s {
   talos_ppo_cfg cfg{};
@@ -270,15 +271,13 @@ int dmm(hipStream_t s, int M, int N, int K, const float* A, long long lda, const
 // weight loads before the first product. The phases are those of the layered path (decode_step
 // below), in the same order, separated by workgroup barriers instead of launches.
 constexpr int kFusedMaxWindow = 16;  // the staged rows of 16 environments fit in LDS
-constexpr int kFusedEnvs = 16;  // the rows of a v_mfma_f32_16x16x4f32 tile
+constexpr int kFusedEnvs = kRowTileRows;  // the rows of a v_mfma_f32_16x16x4f32 tile
 #ifndef TALOS_FUSED_WAVES
 #define TALOS_FUSED_WAVES 8
 #endif
 constexpr int kFusedThreads = 64 * TALOS_FUSED_WAVES;  // two waves a SIMD hide each other's latency
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(1))) void* gptr_t;  // global, for direct-to-LDS loads
-typedef __attribute__((address_space(3))) void* lptr_t;  // LDS
-constexpr int kVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0), expcnt / lgkmcnt not waited
+typedef rt_gptr gptr_t;
+typedef rt_lptr lptr_t;
 
 template <int IN_, int D_, int H_, int HD_, int R_, int VD_, int LT_, int F_, int A_, bool MLA_>
 struct FusedShape {
@@ -317,134 +316,18 @@ struct FusedArgs {
   long long g1, g2, w1, b1, w2, b2, wo, wqkv, wdkv, wuk, wuv, wq, wkr, wqr;
 };
 
-// out(e, n, sum_k X[e][k] W(k, n) (+ bias[n])) for the workgroup's 16 environments on the matrix
-// cores, W(k, n) = W[k * LDW + n] (or W[n * LDW + k] when TRANS). The 16-column tiles of Y go
-// round the waves (tile t to wave (t + woff) % waves); for the 16 k of group g a lane (row i =
-// lane % 16, quad kq = lane / 16) reads X[i][16g + 4kq .. +3] as one float4 from LDS and feeds the
-// four v_mfma_f32_16x16x4f32 of the group (product u takes k = 16g + 4kq + u) with
-// B = W(16g + 4kq + u, n). The result tile holds D[4kq + r][lane % 16] in register r. K % 4 == 0;
-// k past K (K % 16 != 0) and columns past N contribute zeros.
-//
-// The lane's weights (K / 4 a tile) and bias are loaded by FmmW::load, a phase or more before
-// fmm_run uses them, so the loads of the next product are in flight while the current phase runs.
+// The row-tile products and norms of rowtile.hpp with this kernel's wave count.
 template <int K, int N, int LDW, bool TRANS = false>
-struct FmmW {
-  static constexpr int TILES = (N + 15) / 16, WAVES = kFusedThreads / 64, TPW = (TILES + WAVES - 1) / WAVES;
-  static constexpr int KG = (K + 15) / 16;
-  float w[TPW][4 * KG];
-  float b[TPW];
-  int woff;
-  bool has_bias;
-  __device__ __forceinline__ int tile_of(int tp) const {
-    return ((int)(threadIdx.x >> 6) + WAVES - woff % WAVES) % WAVES + tp * WAVES;
-  }
-  // (no __restrict__: loads the compiler cannot prove invariant are not re-issued at the use)
-  __device__ __forceinline__ void load(const float* W, const float* bias, int wo = 0) {
-    const int row = threadIdx.x & 15, kq = (threadIdx.x >> 4) & 3;
-    woff = wo;
-    has_bias = bias != nullptr;
-#pragma unroll
-    for (int tp = 0; tp < TPW; ++tp) {
-      const int t = tile_of(tp), n = t * 16 + row;
-      const bool nv = t < TILES && n < N;
-#pragma unroll
-      for (int g = 0; g < KG; ++g)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int k = 16 * g + 4 * kq + u;
-          w[tp][4 * g + u] = nv && k < K ? W[TRANS ? n * LDW + k : k * LDW + n] : 0.f;
-        }
-      b[tp] = nv && bias ? bias[n] : 0.f;
-    }
-  }
-};
+using FmmW = RowTileW<K, N, LDW, TRANS, kFusedThreads / 64>;
 template <int K, int N, int LDX, int LDW, bool TRANS, class Out>
 __device__ __forceinline__ void fmm_run(const float* X, const FmmW<K, N, LDW, TRANS>& wt, Out out) {
-  static_assert(K % 4 == 0 && LDX % 4 == 0, "float4 rows");
-  using FW = FmmW<K, N, LDW, TRANS>;
-  const int row = threadIdx.x & 15, kq = (threadIdx.x >> 4) & 3;
-#pragma unroll
-  for (int tp = 0; tp < FW::TPW; ++tp) {
-    const int t = wt.tile_of(tp), n = t * 16 + row;
-    if (t >= FW::TILES) continue;  // wave-uniform
-    floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int g = 0; g < FW::KG; ++g) {
-      const int k = 16 * g + 4 * kq;
-      const float4 xa = k < K ? *reinterpret_cast<const float4*>(X + row * LDX + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-      floatx4& acc = (g & 1) ? acc1 : acc0;
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, wt.w[tp][4 * g], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.y, wt.w[tp][4 * g + 1], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.z, wt.w[tp][4 * g + 2], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, wt.w[tp][4 * g + 3], acc, 0, 0, 0);
-    }
-    if (n < N) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float sum = acc0[r] + acc1[r];
-        out(4 * kq + r, n, wt.has_bias ? sum + wt.b[tp] : sum);
-      }
-    }
-  }
+  rowtile_mm<K, N, LDX>(X, wt, out);
 }
-
-// A workgroup barrier that orders LDS only. The step's threads share data through LDS alone (the
-// cache rows they write to global memory are read by later launches, the staged rows are waited
-// for explicitly), so outstanding global loads and stores (prefetched weights, cache writes) need
-// not drain at every barrier, as they would behind __syncthreads().
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// Sum over aligned groups of W adjacent lanes (W a power of two <= 16) with DPP lane moves, every
-// lane of a group getting its sum; all lanes of the wave must be active.
-template <int W>
-__device__ __forceinline__ float group_sum(float v) {
-  static_assert(W >= 1 && W <= 16 && (W & (W - 1)) == 0, "group width");
-  auto dpp = [](float x, auto ctrl) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xF, 0xF, false));
-  };
-  if constexpr (W >= 2) v += dpp(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
-  if constexpr (W >= 4) v += dpp(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
-  if constexpr (W >= 8) v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
-  if constexpr (W >= 16) v += dpp(v, std::integral_constant<int, 0x140>{});  // row_mirror
-  return v;
-}
-
-// y = x / sqrt(mean(x^2) + eps) * g over the workgroup's rows, 16 lanes per row; the lane's gains
-// are loaded by NormG::load ahead of the phase.
 template <int D>
-struct NormG {
-  static constexpr int LPR = 16, PER = (D + LPR - 1) / LPR;  // the first 16 x 16 threads
-  float g[PER];
-  __device__ __forceinline__ void load(const float* gain) {
-    const int l = threadIdx.x % LPR;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) g[j] = l + j * LPR < D ? gain[l + j * LPR] : 0.f;
-  }
-};
+using NormG = RowGain<D>;
 template <int D, int LD>
 __device__ __forceinline__ void fnorm(const float* x, float* y, float eps, const NormG<D>& gn) {
-  constexpr int LPR = NormG<D>::LPR, PER = NormG<D>::PER;
-  if (threadIdx.x >= kFusedEnvs * LPR) return;  // whole waves
-  const int row = threadIdx.x / LPR, l = threadIdx.x % LPR;
-  float xv[PER];
-  float ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int c = l + j * LPR;
-    xv[j] = c < D ? x[row * LD + c] : 0.f;
-    ss = fmaf(xv[j], xv[j], ss);
-  }
-  ss = group_sum<LPR>(ss);
-  const float r = 1.0f / sqrtf(ss / (float)D + eps);
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int c = l + j * LPR;
-    if (c < D) y[row * LD + c] = xv[j] * r * gn.g[j];
-  }
+  row_norm<D, LD>(x, y, eps, gn);
 }
 
 // The step of one workgroup. MLA attention runs in its absorbed form: the cache holds, per layer,

@@ -35,6 +35,7 @@
 #include "gemm.hpp"
 #include "plans.hpp"
 #include "rowops.hpp"
+#include "rowtile.hpp"
 
 struct talos_plan_s {
   int kind = 0;  // 1 block, 2 ppo, 3 mla
@@ -1144,11 +1145,331 @@ int check_ppo_cfg(const talos_ppo_cfg& c) {
 
 // Policy forward up to logits / values for c.batch samples (at most the plan's batch); the
 // per-sample lengths of the call are p->lens.
+// ---- The last layer's MLP half and the heads' inputs on the last-token rows -------------------
+// With B last-token rows (one per sample) the tail of the forward (h2 = x + o.Wo, RMSNorm2,
+// act(.W1 + b1), .W2 + b2 + h2, the final RMSNorm, out_proj) and the matching chain of the
+// backward (out_proj's dX, the final norm's backward, dGELU / dReLU, W1's dX, RMSNorm2's backward,
+// Wo's dX) are row-local: one kernel each keeps 16 rows in LDS and runs every product on the
+// matrix cores (rowtile.hpp) with the weights streamed from L2, instead of a dozen launches of
+// 4096-row GEMMs and row kernels that are each a few microseconds of latency. The saved
+// activations and the row gradients the weight-gradient products read are written as before.
+constexpr int kTailWaves = 8;
+constexpr int kTailThreads = 64 * kTailWaves;
+
+struct TailFwdArgs {
+  int B, relu, seq;
+  float eps;
+  const int32_t* lens;
+  const float* x;  // [B * seq][D]: the last layer's input, whose last-token rows are the residual
+  const float* o;  // [B][D]: the attention output on the last-token rows (attention width D)
+  const float *wo, *g2, *w1, *b1, *w2, *b2, *gf, *wout, *bout;
+  float *h2, *xn2, *rstd2, *u, *a, *last, *lastn, *rstdf, *pout;
+};
+
+// rows of [16][LD] LDS from global [rows][D] (zeros past n rows); with seq > 0, row b is the
+// last-token row b * seq + last_row(lens, b, seq) of a [B * seq][D] buffer
+template <int D, int LD>
+__device__ __forceinline__ void tail_rows_in(float* dst, const float* __restrict__ src, int r0, int n,
+                                             const int32_t* lens = nullptr, int seq = 0) {
+  for (int i = threadIdx.x; i < kRowTileRows * (D / 4); i += kTailThreads) {
+    const int e = i / (D / 4), c = 4 * (i % (D / 4));
+    long long row = r0 + e;
+    if (seq > 0 && e < n) row = row * seq + last_row(lens, r0 + e, seq);
+    const float4 v = e < n ? *reinterpret_cast<const float4*>(src + row * D + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    *reinterpret_cast<float4*>(dst + e * LD + c) = v;
+  }
+}
+// the first n rows of [16][LD] LDS to global [rows][D]
+template <int D, int LD>
+__device__ __forceinline__ void tail_rows_out(float* __restrict__ dst, const float* src, int r0, int n) {
+  for (int i = threadIdx.x; i < kRowTileRows * (D / 4); i += kTailThreads) {
+    const int e = i / (D / 4), c = 4 * (i % (D / 4));
+    if (e < n)
+      *reinterpret_cast<float4*>(dst + (long long)(r0 + e) * D + c) = *reinterpret_cast<const float4*>(src + e * LD + c);
+  }
+}
+
+template <int D, int F>
+__global__ __launch_bounds__(kTailThreads) void ppo_tail_fwd_kernel(TailFwdArgs a) {
+  constexpr int E = kRowTileRows, W = kTailWaves, LDD = D + 4, LDF = F + 4;
+  __shared__ __align__(16) float sx[E * LDD], sh[E * LDD], sn[E * LDD], sa[E * LDF];
+  __shared__ float srs[E];
+  const int r0 = blockIdx.x * E, nr = min(E, a.B - r0);
+  tail_rows_in<D, LDD>(sx, a.x, r0, nr, a.lens, a.seq);
+  tail_rows_in<D, LDD>(sn, a.o, r0, nr);
+  RowGain<D> gn;
+  gn.load(a.g2);
+  lds_barrier();
+  // h2 = x + o.Wo
+  rowtile_mm_stream<D, D, LDD, D, W, D, false>(sn, a.wo, nullptr, [&](int e, int n, float v) {
+    sh[e * LDD + n] = v + sx[e * LDD + n];
+  });
+  lds_barrier();
+  tail_rows_out<D, LDD>(a.h2, sh, r0, nr);
+  row_norm<D, LDD>(sh, sn, a.eps, gn, srs);  // xn2
+  RowGain<D> gf;
+  gf.load(a.gf);
+  lds_barrier();
+  tail_rows_out<D, LDD>(a.xn2, sn, r0, nr);
+  if (threadIdx.x < nr) a.rstd2[r0 + threadIdx.x] = srs[threadIdx.x];
+  // a = act(xn2.W1 + b1); u = gelu'(.) for GELU, the pre-activation for ReLU
+  const bool relu = a.relu;
+  float* ga = a.a;
+  float* gu = a.u;
+  rowtile_mm_stream<D, F, LDD, F, W, D, false>(sn, a.w1, a.b1, [&](int e, int n, float v) {
+    float act, aux;
+    if (relu) {
+      aux = v;
+      act = fmaxf(v, 0.f);
+    } else {
+      act = gelu_fd(v, &aux);
+    }
+    sa[e * LDF + n] = act;
+    if (e < nr) {
+      ga[(long long)(r0 + e) * F + n] = act;
+      gu[(long long)(r0 + e) * F + n] = aux;
+    }
+  });
+  lds_barrier();
+  // last = h2 + a.W2 + b2
+  rowtile_mm_stream<F, D, LDF, D, W, 128, false>(sa, a.w2, a.b2, [&](int e, int n, float v) {
+    sx[e * LDD + n] = v + sh[e * LDD + n];
+  });
+  lds_barrier();
+  tail_rows_out<D, LDD>(a.last, sx, r0, nr);
+  row_norm<D, LDD>(sx, sn, a.eps, gf, srs);  // the final norm
+  lds_barrier();
+  tail_rows_out<D, LDD>(a.lastn, sn, r0, nr);
+  if (threadIdx.x < nr) a.rstdf[r0 + threadIdx.x] = srs[threadIdx.x];
+  // pout = lastn.Wout + bout
+  float* po = a.pout;
+  rowtile_mm_stream<D, D, LDD, D, W, D, false>(sn, a.wout, a.bout, [&](int e, int n, float v) {
+    if (e < nr) po[(long long)(r0 + e) * D + n] = v;
+  });
+}
+
+struct TailBwdArgs {
+  int B, relu;
+  const float *g_pout;                 // [B][D] dL/dpout
+  const float *wout, *gf, *last, *rstdf;
+  const float *w2, *u, *w1, *g2, *h2, *rstd2, *wo;
+  float *g_last, *g_u, *g_h2, *g_o;  // row gradients
+  double *part_f, *part_2;           // [blocks][D] f64 partial dgains of the final norm and norm2
+};
+
+// RMSNorm backward of the 16 rows in LDS (16 lanes per row, threads 0..255): dx = rstd * (dy *
+// gain - x_hat * mean(dy * gain * x_hat)) (+ add), x_hat = x * rstd; the lane's dgain terms
+// dy * x_hat are summed over rows into part[c] (f64, in a fixed order) by the caller through dwl.
+template <int D, int LD>
+__device__ __forceinline__ void tail_norm_bwd(const float* x, const float* rstd, const RowGain<D>& gn,
+                                              const float* dy, const float* add, float* dx, float* dwl, int nr) {
+  constexpr int LPR = 16, PER = RowGain<D>::PER;
+  if (threadIdx.x >= kRowTileRows * LPR) return;  // whole waves
+  const int row = threadIdx.x / LPR, l = threadIdx.x % LPR;
+  const bool on = row < nr;
+  const float r = on ? rstd[row] : 0.f;
+  float xh[PER], gg[PER];
+  float dot = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = l + j * LPR;
+    xh[j] = on ? x[row * LD + c] * r : 0.f;
+    gg[j] = on ? dy[row * LD + c] : 0.f;
+    dot += gg[j] * gn.g[j] * xh[j];
+  }
+  dot = group_sum<LPR>(dot);
+  const float md = dot * (1.0f / (float)D);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = l + j * LPR;
+    float v = r * (gg[j] * gn.g[j] - xh[j] * md);
+    if (add) v += add[row * LD + c];
+    dx[row * LD + c] = v;
+    dwl[row * LD + c] = gg[j] * xh[j];
+  }
+}
+// part[c] = sum over the 16 rows of dwl[row][c], in row order, in f64
+template <int D, int LD>
+__device__ __forceinline__ void tail_dgain_part(const float* dwl, double* part) {
+  for (int c = threadIdx.x; c < D; c += kTailThreads) {
+    double s = 0.0;
+#pragma unroll
+    for (int e = 0; e < kRowTileRows; ++e) s += (double)dwl[e * LD + c];
+    part[(long long)blockIdx.x * D + c] = s;
+  }
+}
+
+template <int D, int F>
+__global__ __launch_bounds__(kTailThreads) void ppo_tail_bwd_kernel(TailBwdArgs a) {
+  constexpr int E = kRowTileRows, W = kTailWaves, LDD = D + 4, LDF = F + 4;
+  __shared__ __align__(16) float sg[E * LDD], sx[E * LDD], sy[E * LDD], sw[E * LDD], su[E * LDF];
+  __shared__ float srs[E];
+  const int r0 = blockIdx.x * E, nr = min(E, a.B - r0);
+  tail_rows_in<D, LDD>(sg, a.g_pout, r0, nr);
+  tail_rows_in<D, LDD>(sx, a.last, r0, nr);
+  if (threadIdx.x < E) srs[threadIdx.x] = threadIdx.x < nr ? a.rstdf[r0 + threadIdx.x] : 0.f;
+  RowGain<D> gf;
+  gf.load(a.gf);
+  lds_barrier();
+  // dL/dlastn = g_pout.Wout^T
+  rowtile_mm_stream<D, D, LDD, D, W, D, true>(sg, a.wout, nullptr, [&](int e, int n, float v) { sy[e * LDD + n] = v; });
+  lds_barrier();
+  // the final norm's backward: g_last
+  tail_norm_bwd<D, LDD>(sx, srs, gf, sy, nullptr, sg, sw, nr);
+  lds_barrier();
+  tail_dgain_part<D, LDD>(sw, a.part_f);
+  tail_rows_out<D, LDD>(a.g_last, sg, r0, nr);
+  tail_rows_in<D, LDD>(sx, a.h2, r0, nr);
+  if (threadIdx.x < E) srs[threadIdx.x] = threadIdx.x < nr ? a.rstd2[r0 + threadIdx.x] : 0.f;
+  // g_u = (g_last.W2^T) * gelu'(u), or masked by u > 0 for ReLU
+  const bool relu = a.relu;
+  const float* gu_in = a.u;
+  float* gu = a.g_u;
+  rowtile_mm_stream<D, F, LDD, D, W, D, true>(sg, a.w2, nullptr, [&](int e, int n, float v) {
+    float g = 0.f;
+    if (e < nr) {
+      const float uu = gu_in[(long long)(r0 + e) * F + n];
+      g = relu ? (uu > 0.f ? v : 0.f) : v * uu;
+      gu[(long long)(r0 + e) * F + n] = g;
+    }
+    su[e * LDF + n] = g;
+  });
+  RowGain<D> g2;
+  g2.load(a.g2);
+  lds_barrier();
+  // dL/dxn2 = g_u.W1^T
+  rowtile_mm_stream<F, D, LDF, F, W, 128, true>(su, a.w1, nullptr, [&](int e, int n, float v) { sy[e * LDD + n] = v; });
+  lds_barrier();
+  // RMSNorm2's backward with the residual gradient g_last: g_h2
+  tail_norm_bwd<D, LDD>(sx, srs, g2, sy, sg, sx, sw, nr);
+  lds_barrier();
+  tail_dgain_part<D, LDD>(sw, a.part_2);
+  tail_rows_out<D, LDD>(a.g_h2, sx, r0, nr);
+  // g_o = g_h2.Wo^T
+  float* go = a.g_o;
+  rowtile_mm_stream<D, D, LDD, D, W, D, true>(sx, a.wo, nullptr, [&](int e, int n, float v) {
+    if (e < nr) go[(long long)(r0 + e) * D + n] = v;
+  });
+}
+
+// Whether the last-row tail runs as the two kernels above: a standard or latent block whose
+// attention width is d, and an instantiated (d, ffn) shape.
+static bool tail_fused(const talos_ppo_cfg& c) {
+  if (c.n_layers < 1 || c.batch < 1) return false;
+  const talos_block_cfg bc = block_cfg_of(c);
+  if (attn_width(bc) != c.d_model) return false;
+  return (c.d_model == 128 && c.ffn_dim == 512) || (c.d_model == 64 && c.ffn_dim == 128);
+}
+
+// The forward tail on the c.batch last-token rows: x the last layer's input on every row, p->lr.o
+// the attention output on the last rows. Writes p->lr (h2, xn2, rstd2, u, a), p->last,
+// p->lastn, p->rstdf and p->pout.
+static int tail_fwd_launch(talos_plan_s* p, const talos_ppo_cfg& c, const talos_block_cfg& bc, const float* P,
+                           const BlockOff& bo, const PpoOff& po, const float* x, hipStream_t s) {
+  auto& R = p->lr;
+  const int B = c.batch, D = c.d_model, F = c.ffn_dim;
+  TailFwdArgs a{};
+  a.B = B;
+  a.relu = bc.activation != TALOS_ACT_GELU;
+  a.seq = c.seq;
+  a.eps = c.eps;
+  a.lens = p->lens;
+  a.x = x;
+  a.o = R.o;
+  a.wo = P + bo.wo;
+  a.g2 = P + bo.g2;
+  a.w1 = P + bo.w1;
+  a.b1 = P + bo.b1;
+  a.w2 = P + bo.w2;
+  a.b2 = P + bo.b2;
+  a.gf = P + po.gf;
+  a.wout = P + po.wout;
+  a.bout = P + po.bout;
+  a.h2 = R.h2;
+  a.xn2 = R.xn2;
+  a.rstd2 = R.rstd2;
+  a.u = R.u;
+  a.a = R.a;
+  a.last = p->last;
+  a.lastn = p->lastn;
+  a.rstdf = p->rstdf;
+  a.pout = p->pout;
+  const double flops = 2.0 * B * (2.0 * D * D + 2.0 * D * F);
+  const double bytes = 4.0 * (2.0 * D * D + 2.0 * D * F + F + 5.0 * D) + 4.0 * B * (2.0 * D + 5.0 * D + 2.0 * F + 2.0);
+  ProfScope ps(s, "ppo_tail_fwd_kernel", flops, bytes);
+  const dim3 grid((unsigned)ceil_div((size_t)B, kRowTileRows));
+  if (D == 128)
+    hipLaunchKernelGGL((ppo_tail_fwd_kernel<128, 512>), grid, dim3(kTailThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((ppo_tail_fwd_kernel<64, 128>), grid, dim3(kTailThreads), 0, s, a);
+  return launch_status("ppo_tail_fwd_kernel");
+}
+
+// Workspace of the backward tail: two partial-dgain arrays of reduce_parts_launch's size.
+static size_t tail_bwd_ws_bytes(int B, int D) {
+  return 2 * reduce_parts_workspace_bytes((int)ceil_div((size_t)B, kRowTileRows), D);
+}
+
+// The backward tail on the B last-token rows from p->g_pout: the row gradients p->g_last,
+// p->lr.g_u, p->lr.g_h2 and p->lr.g_o, the final gain's and gain2's gradients, and the weight
+// gradients of out_proj, W2, W1 and Wo.
+static int tail_bwd_launch(talos_plan_s* p, const talos_ppo_cfg& c, const talos_block_cfg& bc, const float* P,
+                           float* G, const BlockOff& bo, const PpoOff& po, hipStream_t s) {
+  auto& R = p->lr;
+  const int B = c.batch, D = c.d_model, F = c.ffn_dim;
+  const int nblk = (int)ceil_div((size_t)B, kRowTileRows);
+  TALOS_REQUIRE(tail_bwd_ws_bytes(B, D) <= p->red_ws_bytes, TALOS_ERR_SHAPE, "tail backward: workspace too small");
+  int rc;
+  for (float* b : {p->g_last, R.g_u, R.g_h2, R.g_o})
+    if ((rc = before_write(p, s, b))) return rc;
+  TailBwdArgs a{};
+  a.B = B;
+  a.relu = bc.activation != TALOS_ACT_GELU;
+  a.g_pout = p->g_pout;
+  a.wout = P + po.wout;
+  a.gf = P + po.gf;
+  a.last = p->last;
+  a.rstdf = p->rstdf;
+  a.w2 = P + bo.w2;
+  a.u = R.u;
+  a.w1 = P + bo.w1;
+  a.g2 = P + bo.g2;
+  a.h2 = R.h2;
+  a.rstd2 = R.rstd2;
+  a.wo = P + bo.wo;
+  a.g_last = p->g_last;
+  a.g_u = R.g_u;
+  a.g_h2 = R.g_h2;
+  a.g_o = R.g_o;
+  a.part_f = p->red_ws;
+  a.part_2 = p->red_ws + reduce_parts_workspace_bytes(nblk, D) / sizeof(double);
+  {
+    const double flops = 2.0 * B * (2.0 * D * D + 2.0 * D * F);
+    const double bytes = 4.0 * (2.0 * D * D + 2.0 * D * F + 2.0 * D) + 4.0 * B * (3.0 * D + 2.0 + F + 3.0 * D + F) +
+                         16.0 * nblk * D;
+    ProfScope ps(s, "ppo_tail_bwd_kernel", flops, bytes);
+    const dim3 grid((unsigned)nblk);
+    if (D == 128)
+      hipLaunchKernelGGL((ppo_tail_bwd_kernel<128, 512>), grid, dim3(kTailThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((ppo_tail_bwd_kernel<64, 128>), grid, dim3(kTailThreads), 0, s, a);
+    if ((rc = launch_status("ppo_tail_bwd_kernel"))) return rc;
+  }
+  if ((rc = reduce_parts_launch(D, nblk, a.part_f, 0.f, G + po.gf, s))) return rc;
+  if ((rc = reduce_parts_launch(D, nblk, a.part_2, 0.f, G + bo.g2, s))) return rc;
+  // out_proj, W2, W1 and Wo from the row gradients
+  if ((rc = wgrad(p, s, p->g_pout, D, D, B, p->lastn, D, p->g_pout, D, G + po.wout, D, G + po.bout))) return rc;
+  if ((rc = wgrad(p, s, p->g_last, F, D, B, R.a, F, p->g_last, D, G + bo.w2, D, G + bo.b2))) return rc;
+  if ((rc = wgrad(p, s, R.g_u, D, F, B, R.xn2, D, R.g_u, F, G + bo.w1, F, G + bo.b1))) return rc;
+  return wgrad(p, s, R.g_h2, D, D, B, R.o, D, R.g_h2, D, G + bo.wo, D);
+}
+
 static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, const float* states,
                        hipStream_t s, bool heads = true) {
   const talos_block_cfg bc = block_cfg_of(c);
   const PpoOff po = ppo_offsets(c);
   const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions, ow = attn_width(bc);
+  const bool tail = tail_fused(c);
   // each layer's RMSNorm1 runs in the epilogue of the product that makes its input
   auto norm1_of = [&](int l) {
     const BlockOff bo = block_offsets(bc, po.blocks + (size_t)l * block_params(bc));
@@ -1224,10 +1545,15 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
         rc = block_attn_forward(p, bc, P, bo, L, s, true);
         if (rc == TALOS_OK) rc = gather(L.o, p->lr.o, ow);
       }
-      if (rc || (rc = gather(L.x, p->lr.x, d))) return rc;
-      rc = block_mlp_forward(p, bc, P, bo, c.batch, p->lr.x, p->lr.o, p->lr.h2, p->lr.xn2, p->lr.rstd2, p->lr.u,
-                             p->lr.a, p->last, s);
       if (rc) return rc;
+      if (tail) {  // through out_proj in one kernel
+        if ((rc = tail_fwd_launch(p, c, bc, P, bo, po, L.x, s))) return rc;
+      } else {
+        if ((rc = gather(L.x, p->lr.x, d))) return rc;
+        rc = block_mlp_forward(p, bc, P, bo, c.batch, p->lr.x, p->lr.o, p->lr.h2, p->lr.xn2, p->lr.rstd2, p->lr.u,
+                               p->lr.a, p->last, s);
+        if (rc) return rc;
+      }
     }
     base = bo.end;
   }
@@ -1235,10 +1561,12 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
     rc = gather(h, p->last, d);
     if (rc) return rc;
   }
-  rc = rmsnorm_fwd_launch(c.batch, d, c.eps, p->last, P + po.gf, p->lastn, p->rstdf, s);
-  if (rc) return rc;
-  rc = mm(p, s, 0, 0, c.batch, d, d, p->lastn, d, P + po.wout, d, p->pout, d, 0.f, P + po.bout);
-  if (rc) return rc;
+  if (!tail) {
+    rc = rmsnorm_fwd_launch(c.batch, d, c.eps, p->last, P + po.gf, p->lastn, p->rstdf, s);
+    if (rc) return rc;
+    rc = mm(p, s, 0, 0, c.batch, d, d, p->lastn, d, P + po.wout, d, p->pout, d, 0.f, P + po.bout);
+    if (rc) return rc;
+  }
   if (!heads) return TALOS_OK;  // the minibatch runs the heads inside ppo_heads_kernel
   rc = mm(p, s, 0, 0, c.batch, A, d, p->pout, d, P + po.wa, A, p->logits, A, 0.f, P + po.ba);
   if (rc) return rc;
@@ -1417,6 +1745,7 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
     p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, wgrad_ws(p, (int)B, (int)d, (int)A));
     p->red_ws_bytes = std::max(p->red_ws_bytes, colsum_workspace_bytes((int)M, (int)d));
     p->red_ws_bytes = std::max(p->red_ws_bytes, reduce_parts_workspace_bytes(kEmbedBlocks, (kEmbedIn + 1) * (int)d));
+    p->red_ws_bytes = std::max(p->red_ws_bytes, tail_bwd_ws_bytes((int)B, (int)d));
     rc = alloc_workspaces(p);
   }
   if (rc) {
@@ -1573,15 +1902,26 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
     rc = mm(p, s, 0, 1, B, d, 1, p->g_values, 1, params + po.wc, 1, p->g_pout, d, 1.f);
     if (rc) return rc;
   }
-  // out_proj
-  rc = wgrad(p, s, p->g_pout, d, d, B, p->lastn, d, p->g_pout, d, G + po.wout, d, G + po.bout);
-  if (rc) return rc;
-  rc = mm(p, s, 0, 1, B, d, d, p->g_pout, d, params + po.wout, d, p->g_lastn, d);
-  if (rc) return rc;
-  // final rmsnorm on the last-token rows
-  rc = rmsnorm_bwd_launch(B, d, p->last, params + po.gf, p->rstdf, p->g_lastn, 0.f, p->g_last, 0.f, G + po.gf,
-                          p->red_ws, s);
-  if (rc) return rc;
+  std::vector<BlockOff> offs;
+  size_t base = po.blocks;
+  for (int l = 0; l < c.n_layers; ++l) {
+    offs.push_back(block_offsets(bc, base));
+    base = offs.back().end;
+  }
+  const bool tail = tail_fused(c);
+  if (tail) {  // out_proj through the last layer's MLP half: the row gradients in one kernel
+    if ((rc = tail_bwd_launch(p, c, bc, params, G, offs.back(), po, s))) return rc;
+  } else {
+    // out_proj
+    rc = wgrad(p, s, p->g_pout, d, d, B, p->lastn, d, p->g_pout, d, G + po.wout, d, G + po.bout);
+    if (rc) return rc;
+    rc = mm(p, s, 0, 1, B, d, d, p->g_pout, d, params + po.wout, d, p->g_lastn, d);
+    if (rc) return rc;
+    // final rmsnorm on the last-token rows
+    rc = rmsnorm_bwd_launch(B, d, p->last, params + po.gf, p->rstdf, p->g_lastn, 0.f, p->g_last, 0.f, G + po.gf,
+                            p->red_ws, s);
+    if (rc) return rc;
+  }
   // rows of a [B, w] last-token gradient into a full [M, w] one, zero elsewhere
   auto scatter = [&](const float* src, float* dst, int w) {
     ProfScope ps_s(s, "scatter_last_kernel", 0.0, 4.0 * ((double)M * w + (double)B * w));
@@ -1590,12 +1930,6 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
                        p->lens, src, dst);
     return launch_status("scatter_last_kernel");
   };
-  std::vector<BlockOff> offs;
-  size_t base = po.blocks;
-  for (int l = 0; l < c.n_layers; ++l) {
-    offs.push_back(block_offsets(bc, base));
-    base = offs.back().end;
-  }
   // blocks, last to first; the gradient ping-pongs between g_out and g_x
   float* gcur = p->g_out;
   float* gnext = p->g_x;
@@ -1608,9 +1942,11 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
     const int l = c.n_layers - 1;
     auto& R = p->lr;
     auto& L = p->layers[l];
-    rc = block_mlp_backward(p, bc, params, G, offs[l], B, R.o, R.h2, R.xn2, R.rstd2, R.u, R.a, p->g_last, R.g_u,
-                            R.g_xn, R.g_h2, R.g_o, s);
-    if (rc) return rc;
+    if (!tail) {
+      rc = block_mlp_backward(p, bc, params, G, offs[l], B, R.o, R.h2, R.xn2, R.rstd2, R.u, R.a, p->g_last, R.g_u,
+                              R.g_xn, R.g_h2, R.g_o, s);
+      if (rc) return rc;
+    }
     if (ppo_lastq(p, bc, L)) {
       // keys / values on every row, the query on the last rows (its gradient in R.dq)
       const BlockOff& o = offs[l];
