@@ -1254,7 +1254,7 @@ struct TailBwdArgs {
   const float *wout, *gf, *last, *rstdf;
   const float *w2, *u, *w1, *g2, *h2, *rstd2, *wo;
   float *g_last, *g_u, *g_h2, *g_o;  // row gradients
-  double *part_f, *part_2;           // [blocks][D] f64 partial dgains of the final norm and norm2
+  double* part;                      // [blocks][2D] f64 partial dgains: the final norm's, then norm2's
 };
 
 // RMSNorm backward of the 16 rows in LDS (16 lanes per row, threads 0..255): dx = rstd * (dy *
@@ -1295,7 +1295,7 @@ __device__ __forceinline__ void tail_dgain_part(const float* dwl, double* part) 
     double s = 0.0;
 #pragma unroll
     for (int e = 0; e < kRowTileRows; ++e) s += (double)dwl[e * LD + c];
-    part[(long long)blockIdx.x * D + c] = s;
+    part[c] = s;
   }
 }
 
@@ -1317,7 +1317,7 @@ __global__ __launch_bounds__(kTailThreads) void ppo_tail_bwd_kernel(TailBwdArgs 
   // the final norm's backward: g_last
   tail_norm_bwd<D, LDD>(sx, srs, gf, sy, nullptr, sg, sw, nr);
   lds_barrier();
-  tail_dgain_part<D, LDD>(sw, a.part_f);
+  tail_dgain_part<D, LDD>(sw, a.part + (long long)blockIdx.x * 2 * D);
   tail_rows_out<D, LDD>(a.g_last, sg, r0, nr);
   tail_rows_in<D, LDD>(sx, a.h2, r0, nr);
   if (threadIdx.x < E) srs[threadIdx.x] = threadIdx.x < nr ? a.rstd2[r0 + threadIdx.x] : 0.f;
@@ -1343,7 +1343,7 @@ __global__ __launch_bounds__(kTailThreads) void ppo_tail_bwd_kernel(TailBwdArgs 
   // RMSNorm2's backward with the residual gradient g_last: g_h2
   tail_norm_bwd<D, LDD>(sx, srs, g2, sy, sg, sx, sw, nr);
   lds_barrier();
-  tail_dgain_part<D, LDD>(sw, a.part_2);
+  tail_dgain_part<D, LDD>(sw, a.part + (long long)blockIdx.x * 2 * D + D);
   tail_rows_out<D, LDD>(a.g_h2, sx, r0, nr);
   // g_o = g_h2.Wo^T
   float* go = a.g_o;
@@ -1405,9 +1405,9 @@ static int tail_fwd_launch(talos_plan_s* p, const talos_ppo_cfg& c, const talos_
   return launch_status("ppo_tail_fwd_kernel");
 }
 
-// Workspace of the backward tail: two partial-dgain arrays of reduce_parts_launch's size.
+// Workspace of the backward tail: the partial dgains of both norms, reduced in one launch.
 static size_t tail_bwd_ws_bytes(int B, int D) {
-  return 2 * reduce_parts_workspace_bytes((int)ceil_div((size_t)B, kRowTileRows), D);
+  return reduce_parts_workspace_bytes((int)ceil_div((size_t)B, kRowTileRows), 2 * D);
 }
 
 // The backward tail on the B last-token rows from p->g_pout: the row gradients p->g_last,
@@ -1441,8 +1441,7 @@ static int tail_bwd_launch(talos_plan_s* p, const talos_ppo_cfg& c, const talos_
   a.g_u = R.g_u;
   a.g_h2 = R.g_h2;
   a.g_o = R.g_o;
-  a.part_f = p->red_ws;
-  a.part_2 = p->red_ws + reduce_parts_workspace_bytes(nblk, D) / sizeof(double);
+  a.part = p->red_ws;
   {
     const double flops = 2.0 * B * (2.0 * D * D + 2.0 * D * F);
     const double bytes = 4.0 * (2.0 * D * D + 2.0 * D * F + 2.0 * D) + 4.0 * B * (3.0 * D + 2.0 + F + 3.0 * D + F) +
@@ -1455,8 +1454,7 @@ static int tail_bwd_launch(talos_plan_s* p, const talos_ppo_cfg& c, const talos_
       hipLaunchKernelGGL((ppo_tail_bwd_kernel<64, 128>), grid, dim3(kTailThreads), 0, s, a);
     if ((rc = launch_status("ppo_tail_bwd_kernel"))) return rc;
   }
-  if ((rc = reduce_parts_launch(D, nblk, a.part_f, 0.f, G + po.gf, s))) return rc;
-  if ((rc = reduce_parts_launch(D, nblk, a.part_2, 0.f, G + bo.g2, s))) return rc;
+  if ((rc = reduce_parts_launch(2 * D, nblk, a.part, 0.f, G + po.gf, s, D, G + bo.g2))) return rc;
   // out_proj, W2, W1 and Wo from the row gradients
   if ((rc = wgrad(p, s, p->g_pout, D, D, B, p->lastn, D, p->g_pout, D, G + po.wout, D, G + po.bout))) return rc;
   if ((rc = wgrad(p, s, p->g_last, F, D, B, R.a, F, p->g_last, D, G + bo.w2, D, G + bo.b2))) return rc;

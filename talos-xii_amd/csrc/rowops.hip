@@ -81,29 +81,40 @@ __global__ __launch_bounds__(256) void colsum_partial_kernel(int rows, int cols,
   if (w == 0 && c < cols) part[(long long)blockIdx.y * cols + c] = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
 }
 
-// out[c] = beta*out[c] + sum_p part[p][c]: 4 waves per 64 columns, LDS combine in f64 (small
-// workgroups, so the reduction finds room beside a product running on another stream).
-__global__ __launch_bounds__(256) void reduce_parts_kernel(int cols, int nparts, const double* __restrict__ part,
-                                                           float beta, float* __restrict__ out) {
-  constexpr int W = 4;
-  __shared__ double red[W][64];
+// out[c] = beta*out[c] + sum_p part[p][c] in one pass: a workgroup takes 16 columns with 16
+// waves; lane (column lane % 16, q = lane / 16) of wave w adds partials p = 4w + q + 64i in order
+// into four f64 accumulators (i % 4, four independent loads in flight), so a wave reads four
+// 128-byte row pieces per load; the 64 sums of a column are then added in a fixed order.
+constexpr int kOnePassParts = 4096;
+// Columns from split on go to out2[c - split] (two gradients reduced in one launch).
+__global__ __launch_bounds__(1024) void reduce_parts_kernel(int cols, int nparts, const double* __restrict__ part,
+                                                            float beta, float* __restrict__ out, int split,
+                                                            float* __restrict__ out2) {
+  __shared__ double red[64][16];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int c = blockIdx.x * 64 + lane;
-  double s0 = 0.0, s1 = 0.0;
+  const int cl = lane & 15, q = lane >> 4;
+  const int c = blockIdx.x * 16 + cl;
+  double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
   if (c < cols) {
-    int p = w;
-    for (; p + W < nparts; p += 2 * W) {
-      s0 += part[(long long)p * cols + c];
-      s1 += part[(long long)(p + W) * cols + c];
+    const long long step = 64LL * cols;
+    int p = 4 * w + q;
+    for (; p + 192 < nparts; p += 256) {
+      const double* r = part + (long long)p * cols + c;
+      const double a0 = r[0], a1 = r[step], a2 = r[2 * step], a3 = r[3 * step];
+      s0 += a0;
+      s1 += a1;
+      s2 += a2;
+      s3 += a3;
     }
-    if (p < nparts) s0 += part[(long long)p * cols + c];
+    for (; p < nparts; p += 64) s0 += part[(long long)p * cols + c];
   }
-  red[w][lane] = s0 + s1;
+  red[4 * w + q][cl] = (s0 + s1) + (s2 + s3);
   __syncthreads();
-  if (w == 0 && c < cols) {
-    double s = 0.0;
-    for (int i = 0; i < W; ++i) s += red[i][lane];
-    out[c] = (float)(s + (beta != 0.f ? (double)out[c] : 0.0));
+  if (threadIdx.x < 16 && c < cols) {
+    double t = 0.0;
+    for (int j = 0; j < 64; ++j) t += red[j][cl];
+    float* o = c < split ? out + c : out2 + (c - split);
+    *o = (float)(t + (beta != 0.f ? (double)*o : 0.0));
   }
 }
 
@@ -126,13 +137,15 @@ __global__ __launch_bounds__(256) void group_parts_kernel(int cols, int nparts, 
     part2[(long long)blockIdx.y * cols + c] = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
 }
 
-static int grouped_parts(int nparts) { return nparts > 2 * kGroupParts ? (nparts + kGroupParts - 1) / kGroupParts : 0; }
+static int grouped_parts(int nparts) { return nparts > kOnePassParts ? (nparts + kGroupParts - 1) / kGroupParts : 0; }
 
 // Workspace rows (of cols doubles) a reduction over nparts partials needs: the partials and the
 // first level's group sums after them.
 static size_t parts_rows(int nparts) { return (size_t)nparts + grouped_parts(nparts); }
 
-int reduce_parts_launch(int cols, int nparts, double* part, float beta, float* out, hipStream_t s) {
+int reduce_parts_launch(int cols, int nparts, double* part, float beta, float* out, hipStream_t s, int split,
+                        float* out2) {
+  if (split < 0 || split > cols || out2 == nullptr) split = cols;
   const int groups = grouped_parts(nparts);
   if (groups > 0) {
     // part is the start of a workspace of parts_rows(nparts) rows (every caller sizes it so)
@@ -145,7 +158,8 @@ int reduce_parts_launch(int cols, int nparts, double* part, float beta, float* o
     nparts = groups;
   }
   ProfScope ps(s, "reduce_parts_kernel", (double)nparts * cols, 8.0 * nparts * cols + 4.0 * cols);
-  hipLaunchKernelGGL(reduce_parts_kernel, dim3(ceil_div(cols, 64)), dim3(256), 0, s, cols, nparts, part, beta, out);
+  hipLaunchKernelGGL(reduce_parts_kernel, dim3(ceil_div(cols, 16)), dim3(1024), 0, s, cols, nparts, part, beta, out,
+                     split, out2);
   TALOS_LAUNCHED("reduce_parts_kernel");
   return TALOS_OK;
 }

@@ -16,9 +16,11 @@ int colsum_launch(int rows, int cols, const float* dy, long long ld, float beta,
 
 size_t rmsnorm_bwd_workspace_bytes(int rows, int dim);
 // Bytes of the workspace reduce_parts_launch needs for nparts partial rows of cols doubles, and
-// the launch: out = beta * out + the fixed-order f64 sum of the partial rows.
+// the launch: out = beta * out + the fixed-order f64 sum of the partial rows (columns from split
+// on into out2 instead, when out2 is given).
 size_t reduce_parts_workspace_bytes(int nparts, int cols);
-int reduce_parts_launch(int cols, int nparts, double* part, float beta, float* out, hipStream_t s);
+int reduce_parts_launch(int cols, int nparts, double* part, float beta, float* out, hipStream_t s, int split = -1,
+                        float* out2 = nullptr);
 int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
                        hipStream_t s);
 // dx = (dres ? dres : beta_dx * dx) + d rmsnorm / dx . dy; dres (the residual branch's gradient)
