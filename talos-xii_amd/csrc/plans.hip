@@ -1361,6 +1361,183 @@ static bool tail_fused(const talos_ppo_cfg& c) {
   return (c.d_model == 128 && c.ffn_dim == 512) || (c.d_model == 64 && c.ffn_dim == 128);
 }
 
+// ---- Weight gradients over the last-token rows: dW = X^T G for several products in one launch ----
+// The products of the last layer's tail (out_proj, W2, W1, Wo) and its query projection reduce
+// over only B rows, too few for the big GEMM tiles: as split-K GEMMs each was a launch and a
+// reduction of mostly latency. Here every 64x64 output tile of every product, times row chunks
+// of kRowsChunk, is one 256-thread workgroup (wave = one 32x32 quadrant as 2x2
+// v_mfma_f32_16x16x4_f32 tiles, lane l feeding X[row + l / 16][m + l % 16] and
+// G[row + l / 16][n + l % 16]); the f32 chunk partials (and the bias column sums) are then added
+// in chunk order in f64 by one reduction launch.
+constexpr int kRowsWgradMax = 4;
+constexpr int kRowsChunk = 256;
+struct RowsWgradProblem {
+  const float* X;  // [rows][kx]
+  const float* G;  // [rows][ng]
+  float* dW;       // [kx][ng]
+  float* dbias;    // [ng] = sum of G over the rows, or null
+  long long ldx, ldg, ldw;
+  int kx, ng, tiles_n, tile0, bias0;
+};
+struct RowsWgradArgs {
+  int rows, nprob, chunks, ntiles, nbias;
+  float* part;  // [chunks][ntiles][64 * 64], then [chunks][nbias]
+  RowsWgradProblem pr[kRowsWgradMax];
+};
+
+__global__ __launch_bounds__(256) void rows_wgrad_kernel(RowsWgradArgs a) {
+  const int t = blockIdx.x % a.ntiles, chunk = blockIdx.x / a.ntiles;
+  int pi = 0;
+  while (pi + 1 < a.nprob && t >= a.pr[pi + 1].tile0) ++pi;
+  const RowsWgradProblem& P = a.pr[pi];
+  const int lt = t - P.tile0;
+  const int m0 = (lt / P.tiles_n) * 64, n0 = (lt % P.tiles_n) * 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1, i = lane & 15, kq = lane >> 4;
+  const int ma = m0 + 32 * wm + i, na = n0 + 32 * wn + i;
+  const bool am0 = ma < P.kx, am1 = ma + 16 < P.kx, bn0 = na < P.ng, bn1 = na + 16 < P.ng;
+  const int r0 = chunk * kRowsChunk, r1 = min(a.rows, r0 + kRowsChunk);
+  rt_floatx4 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = rt_floatx4{0.f, 0.f, 0.f, 0.f};
+  float bs0 = 0.f, bs1 = 0.f;  // bias column sums over this lane's rows
+  for (int r = r0; r < r1; r += 16) {
+    float xa[4][2], gb[4][2];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int row = r + 4 * s + kq;
+      const bool rv = row < r1;
+      const float* xr = P.X + (long long)row * P.ldx;
+      const float* gr = P.G + (long long)row * P.ldg;
+      xa[s][0] = rv && am0 ? xr[ma] : 0.f;
+      xa[s][1] = rv && am1 ? xr[ma + 16] : 0.f;
+      gb[s][0] = rv && bn0 ? gr[na] : 0.f;
+      gb[s][1] = rv && bn1 ? gr[na + 16] : 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s][x], gb[s][y], acc[x][y], 0, 0, 0);
+      bs0 += gb[s][0];
+      bs1 += gb[s][1];
+    }
+  }
+  float* tp = a.part + ((long long)chunk * a.ntiles + t) * 4096;
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = 32 * wm + 16 * x + 4 * kq + q, n = 32 * wn + 16 * y + i;
+        tp[m * 64 + n] = acc[x][y][q];
+      }
+  if (P.dbias && m0 == 0 && wm == 0) {
+    // the four row groups (kq) of a column, added in kq order
+    bs0 += __shfl_xor(bs0, 16);
+    bs1 += __shfl_xor(bs1, 16);
+    bs0 += __shfl_xor(bs0, 32);
+    bs1 += __shfl_xor(bs1, 32);
+    if (kq == 0) {
+      float* bp = a.part + (long long)a.chunks * a.ntiles * 4096 + (long long)chunk * a.nbias + P.bias0;
+      if (bn0) bp[na] = bs0;
+      if (bn1) bp[na + 16] = bs1;
+    }
+  }
+}
+
+// dW[k][n] (and dbias[n]) = the chunk partials added in chunk order in f64; thread per output.
+__global__ __launch_bounds__(256) void rows_wgrad_reduce_kernel(RowsWgradArgs a, long long nw) {
+  const long long o = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (o >= nw + a.nbias) return;
+  if (o < nw) {
+    long long off = o;
+    int pi = 0;
+    while (off >= (long long)a.pr[pi].kx * a.pr[pi].ng) {
+      off -= (long long)a.pr[pi].kx * a.pr[pi].ng;
+      ++pi;
+    }
+    const RowsWgradProblem& P = a.pr[pi];
+    const int k = (int)(off / P.ng), n = (int)(off % P.ng);
+    const long long e = (long long)(P.tile0 + (k / 64) * P.tiles_n + n / 64) * 4096 + (k % 64) * 64 + n % 64;
+    double s = 0.0;
+    for (int c = 0; c < a.chunks; ++c) s += (double)a.part[(long long)c * a.ntiles * 4096 + e];
+    P.dW[(long long)k * P.ldw + n] = (float)s;
+  } else {
+    const int b = (int)(o - nw);
+    int pi = a.nprob - 1;
+    while (pi > 0 && (a.pr[pi].dbias == nullptr || b < a.pr[pi].bias0)) --pi;
+    const RowsWgradProblem& P = a.pr[pi];
+    const float* bp = a.part + (long long)a.chunks * a.ntiles * 4096 + b;
+    double s = 0.0;
+    for (int c = 0; c < a.chunks; ++c) s += (double)bp[(long long)c * a.nbias];
+    P.dbias[b - P.bias0] = (float)s;
+  }
+}
+
+// Host side: collect up to kRowsWgradMax products over the same rows, then launch both kernels.
+struct RowsWgrad {
+  RowsWgradArgs a{};
+  void add(const float* X, long long ldx, int kx, const float* G, long long ldg, int ng, float* dW, long long ldw,
+           float* dbias = nullptr) {
+    RowsWgradProblem& P = a.pr[a.nprob++];
+    P.X = X;
+    P.ldx = ldx;
+    P.kx = kx;
+    P.G = G;
+    P.ldg = ldg;
+    P.ng = ng;
+    P.dW = dW;
+    P.ldw = ldw;
+    P.dbias = dbias;
+    P.tiles_n = (int)ceil_div((size_t)ng, 64);
+    P.tile0 = a.ntiles;
+    a.ntiles += (int)ceil_div((size_t)kx, 64) * P.tiles_n;
+    P.bias0 = a.nbias;
+    if (dbias) a.nbias += ng;
+  }
+  static size_t ws_floats(int rows, int ntiles, int nbias) {
+    const size_t chunks = std::max<size_t>(1, ceil_div((size_t)rows, kRowsChunk));
+    return chunks * ((size_t)ntiles * 4096 + nbias);
+  }
+  int launch(int rows, float* ws, size_t ws_floats_avail, hipStream_t s) {
+    a.rows = rows;
+    a.chunks = std::max(1, (int)ceil_div((size_t)rows, kRowsChunk));
+    a.part = ws;
+    TALOS_REQUIRE(ws_floats(rows, a.ntiles, a.nbias) <= ws_floats_avail, TALOS_ERR_SHAPE,
+                  "row weight gradients: workspace too small");
+    long long nw = 0;
+    double flops = 0.0, bytes = 0.0;
+    for (int i = 0; i < a.nprob; ++i) {
+      nw += (long long)a.pr[i].kx * a.pr[i].ng;
+      flops += 2.0 * rows * a.pr[i].kx * a.pr[i].ng;
+      bytes += 4.0 * ((double)rows * (a.pr[i].kx + a.pr[i].ng) + (double)a.pr[i].kx * a.pr[i].ng);
+    }
+    {
+      ProfScope ps(s, "rows_wgrad_kernel", flops, bytes + 4.0 * a.chunks * ((double)a.ntiles * 4096 + a.nbias));
+      hipLaunchKernelGGL(rows_wgrad_kernel, dim3((unsigned)(a.ntiles * a.chunks)), dim3(256), 0, s, a);
+      TALOS_LAUNCHED("rows_wgrad_kernel");
+    }
+    ProfScope ps(s, "rows_wgrad_reduce_kernel", 0.0, 4.0 * (a.chunks + 1.0) * ((double)a.ntiles * 4096 + a.nbias));
+    hipLaunchKernelGGL(rows_wgrad_reduce_kernel, dim3((unsigned)ceil_div((size_t)(nw + a.nbias), 256)), dim3(256), 0, s,
+                       a, nw);
+    TALOS_LAUNCHED("rows_wgrad_reduce_kernel");
+    return TALOS_OK;
+  }
+};
+
+// Workspace floats of the tail's row weight gradients (out_proj, W2, W1 with biases; Wo) and of
+// the last-query layer's dW_q, over B rows.
+static size_t rows_wgrad_ws_floats(int B, int d, int F) {
+  auto tl = [](int k, int n) { return (int)(ceil_div((size_t)k, 64) * ceil_div((size_t)n, 64)); };
+  return std::max(RowsWgrad::ws_floats(B, 2 * tl(d, d) + tl(F, d) + tl(d, F), 2 * d + F),
+                  RowsWgrad::ws_floats(B, tl(d, d), 0));
+}
+
 // The forward tail on the c.batch last-token rows: x the last layer's input on every row, p->lr.o
 // the attention output on the last rows. Writes p->lr (h2, xn2, rstd2, u, a), p->last,
 // p->lastn, p->rstdf and p->pout.
@@ -1456,10 +1633,12 @@ static int tail_bwd_launch(talos_plan_s* p, const talos_ppo_cfg& c, const talos_
   }
   if ((rc = reduce_parts_launch(2 * D, nblk, a.part, 0.f, G + po.gf, s, D, G + bo.g2))) return rc;
   // out_proj, W2, W1 and Wo from the row gradients
-  if ((rc = wgrad(p, s, p->g_pout, D, D, B, p->lastn, D, p->g_pout, D, G + po.wout, D, G + po.bout))) return rc;
-  if ((rc = wgrad(p, s, p->g_last, F, D, B, R.a, F, p->g_last, D, G + bo.w2, D, G + bo.b2))) return rc;
-  if ((rc = wgrad(p, s, R.g_u, D, F, B, R.xn2, D, R.g_u, F, G + bo.w1, F, G + bo.b1))) return rc;
-  return wgrad(p, s, R.g_h2, D, D, B, R.o, D, R.g_h2, D, G + bo.wo, D);
+  RowsWgrad rw;
+  rw.add(p->lastn, D, D, p->g_pout, D, D, G + po.wout, D, G + po.bout);
+  rw.add(R.a, F, F, p->g_last, D, D, G + bo.w2, D, G + bo.b2);
+  rw.add(R.xn2, D, D, R.g_u, F, F, G + bo.w1, F, G + bo.b1);
+  rw.add(R.o, D, D, R.g_h2, D, D, G + bo.wo, D);
+  return rw.launch(B, p->gemm_ws, p->gemm_ws_bytes / sizeof(float), s);
 }
 
 static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, const float* states,
@@ -1744,6 +1923,7 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
     p->red_ws_bytes = std::max(p->red_ws_bytes, colsum_workspace_bytes((int)M, (int)d));
     p->red_ws_bytes = std::max(p->red_ws_bytes, reduce_parts_workspace_bytes(kEmbedBlocks, (kEmbedIn + 1) * (int)d));
     p->red_ws_bytes = std::max(p->red_ws_bytes, tail_bwd_ws_bytes((int)B, (int)d));
+    p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, sizeof(float) * rows_wgrad_ws_floats((int)B, (int)d, cfg->ffn_dim));
     rc = alloc_workspaces(p);
   }
   if (rc) {
@@ -1958,7 +2138,11 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
       if ((rc = attn_bwd_lastq_launch(ad, R.o, d, R.lse, R.g_o, d, s))) return rc;
       float* g_kv = p->g_qkv + d;
       if ((rc = wgrad(p, s, p->g_qkv, d, 2 * d, M, L.xn1, d, g_kv, 3 * d, G + o.wqkv + d, 3 * d))) return rc;
-      if ((rc = wgrad(p, s, R.dq, d, d, B, R.xn1, d, R.dq, d, G + o.wqkv, 3 * d))) return rc;
+      {
+        RowsWgrad rw;  // dW_q over the last rows
+        rw.add(R.xn1, d, d, R.dq, d, d, G + o.wqkv, 3 * d);
+        if ((rc = rw.launch(B, p->gemm_ws, p->gemm_ws_bytes / sizeof(float), s))) return rc;
+      }
       // dxn1 = g_kv.Wkv^T on every row, plus dq.Wq^T on the last rows; then rmsnorm1's backward
       // with the residual gradient R.g_h2 on the last rows
       if ((rc = mm(p, s, 0, 1, B, d, d, R.dq, d, params + o.wqkv, 3 * d, R.g_xnq, d))) return rc;
