@@ -1367,8 +1367,8 @@ static bool tail_fused(const talos_ppo_cfg& c) {
 // reduction of mostly latency. Here every 64x64 output tile of every product, times row chunks
 // of kRowsChunk, is one 256-thread workgroup (wave = one 32x32 quadrant as 2x2
 // v_mfma_f32_16x16x4_f32 tiles, lane l feeding X[row + l / 16][m + l % 16] and
-// G[row + l / 16][n + l % 16]); the f32 chunk partials (and the bias column sums) are then added
-// in chunk order in f64 by one reduction launch.
+// G[row + l / 16][n + l % 16] from LDS); the f32 chunk partials (and the bias column sums) are
+// then added in a fixed order in f64 by one reduction launch.
 constexpr int kRowsWgradMax = 4;
 constexpr int kRowsChunk = 256;
 struct RowsWgradProblem {
@@ -1394,8 +1394,8 @@ __global__ __launch_bounds__(256) void rows_wgrad_kernel(RowsWgradArgs a) {
   const int m0 = (lt / P.tiles_n) * 64, n0 = (lt % P.tiles_n) * 64;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1, i = lane & 15, kq = lane >> 4;
-  const int ma = m0 + 32 * wm + i, na = n0 + 32 * wn + i;
-  const bool am0 = ma < P.kx, am1 = ma + 16 < P.kx, bn0 = na < P.ng, bn1 = na + 16 < P.ng;
+  const int na = n0 + 32 * wn + i;
+  const bool bn0 = na < P.ng, bn1 = na + 16 < P.ng;
   const int r0 = chunk * kRowsChunk, r1 = min(a.rows, r0 + kRowsChunk);
   rt_floatx4 acc[2][2];
 #pragma unroll
@@ -1403,27 +1403,60 @@ __global__ __launch_bounds__(256) void rows_wgrad_kernel(RowsWgradArgs a) {
 #pragma unroll
     for (int y = 0; y < 2; ++y) acc[x][y] = rt_floatx4{0.f, 0.f, 0.f, 0.f};
   float bs0 = 0.f, bs1 = 0.f;  // bias column sums over this lane's rows
-  for (int r = r0; r < r1; r += 16) {
-    float xa[4][2], gb[4][2];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int row = r + 4 * s + kq;
-      const bool rv = row < r1;
-      const float* xr = P.X + (long long)row * P.ldx;
-      const float* gr = P.G + (long long)row * P.ldg;
-      xa[s][0] = rv && am0 ? xr[ma] : 0.f;
-      xa[s][1] = rv && am1 ? xr[ma + 16] : 0.f;
-      gb[s][0] = rv && bn0 ? gr[na] : 0.f;
-      gb[s][1] = rv && bn1 ? gr[na + 16] : 0.f;
+  // Steps of 32 rows: the X and G pieces [32][64] are read as float4 (2 + 2 per thread) into
+  // registers one step ahead, then stored to one of two LDS buffers, from which each lane reads
+  // its operand columns.
+  constexpr int SR = 32, LDT = 80;  // row pitch: the four row groups of a read fall in distinct banks
+  __shared__ __align__(16) float sX[2][SR * LDT], sG[2][SR * LDT];
+  const int lr = threadIdx.x >> 4, lc = 4 * (threadIdx.x & 15);  // rows lr and lr + 16, columns lc..lc+3
+  const bool vx = P.kx % 4 == 0 && P.ldx % 4 == 0 && ((uintptr_t)P.X & 15) == 0;
+  const bool vg = P.ng % 4 == 0 && P.ldg % 4 == 0 && ((uintptr_t)P.G & 15) == 0;
+  auto ld4 = [&](const float* base, long long ld, int row, int col, int lim, bool vec) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row < r1) {
+      const float* q = base + (long long)row * ld + col;
+      if (vec) {
+        if (col < lim) v = *reinterpret_cast<const float4*>(q);
+      } else {
+        if (col < lim) v.x = q[0];
+        if (col + 1 < lim) v.y = q[1];
+        if (col + 2 < lim) v.z = q[2];
+        if (col + 3 < lim) v.w = q[3];
+      }
     }
+    return v;
+  };
+  float4 px[2], pg[2];
+  auto fetch = [&](int r) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int h = 0; h < 2; ++h) {
+      px[h] = ld4(P.X, P.ldx, r + lr + 16 * h, m0 + lc, P.kx, vx);
+      pg[h] = ld4(P.G, P.ldg, r + lr + 16 * h, n0 + lc, P.ng, vg);
+    }
+  };
+  fetch(r0);
+  int buf = 0;
+  for (int r = r0; r < r1; r += SR, buf ^= 1) {
 #pragma unroll
-      for (int x = 0; x < 2; ++x)
+    for (int h = 0; h < 2; ++h) {
+      *reinterpret_cast<float4*>(&sX[buf][(lr + 16 * h) * LDT + lc]) = px[h];
+      *reinterpret_cast<float4*>(&sG[buf][(lr + 16 * h) * LDT + lc]) = pg[h];
+    }
+    __syncthreads();
+    if (r + SR < r1) fetch(r + SR);
+    const float* xs = sX[buf];
+    const float* gs = sG[buf];
 #pragma unroll
-        for (int y = 0; y < 2; ++y) acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s][x], gb[s][y], acc[x][y], 0, 0, 0);
-      bs0 += gb[s][0];
-      bs1 += gb[s][1];
+    for (int s = 0; s < SR / 4; ++s) {
+      const int row = 4 * s + kq;
+      const float x0 = xs[row * LDT + 32 * wm + i], x1 = xs[row * LDT + 32 * wm + 16 + i];
+      const float g0 = gs[row * LDT + 32 * wn + i], g1 = gs[row * LDT + 32 * wn + 16 + i];
+      acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x0, g0, acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x0, g1, acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x1, g0, acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x1, g1, acc[1][1], 0, 0, 0);
+      bs0 += g0;
+      bs1 += g1;
     }
   }
   float* tp = a.part + ((long long)chunk * a.ntiles + t) * 4096;
@@ -1450,7 +1483,8 @@ __global__ __launch_bounds__(256) void rows_wgrad_kernel(RowsWgradArgs a) {
   }
 }
 
-// dW[k][n] (and dbias[n]) = the chunk partials added in chunk order in f64; thread per output.
+// dW[k][n] (and dbias[n]) = the chunk partials added in a fixed order in f64 (chunk c into
+// accumulator c % 4); thread per output.
 __global__ __launch_bounds__(256) void rows_wgrad_reduce_kernel(RowsWgradArgs a, long long nw) {
   const long long o = (long long)blockIdx.x * 256 + threadIdx.x;
   if (o >= nw + a.nbias) return;
@@ -1464,9 +1498,19 @@ __global__ __launch_bounds__(256) void rows_wgrad_reduce_kernel(RowsWgradArgs a,
     const RowsWgradProblem& P = a.pr[pi];
     const int k = (int)(off / P.ng), n = (int)(off % P.ng);
     const long long e = (long long)(P.tile0 + (k / 64) * P.tiles_n + n / 64) * 4096 + (k % 64) * 64 + n % 64;
-    double s = 0.0;
-    for (int c = 0; c < a.chunks; ++c) s += (double)a.part[(long long)c * a.ntiles * 4096 + e];
-    P.dW[(long long)k * P.ldw + n] = (float)s;
+    const long long step = (long long)a.ntiles * 4096;
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+    int c = 0;
+    for (; c + 3 < a.chunks; c += 4) {
+      const float* q = a.part + c * step + e;
+      const float v0 = q[0], v1 = q[step], v2 = q[2 * step], v3 = q[3 * step];
+      s0 += v0;
+      s1 += v1;
+      s2 += v2;
+      s3 += v3;
+    }
+    for (; c < a.chunks; ++c) s0 += (double)a.part[c * step + e];
+    P.dW[(long long)k * P.ldw + n] = (float)((s0 + s1) + (s2 + s3));
   } else {
     const int b = (int)(o - nw);
     int pi = a.nprob - 1;
