@@ -1685,6 +1685,55 @@ static int tail_bwd_launch(talos_plan_s* p, const talos_ppo_cfg& c, const talos_
   return rw.launch(B, p->gemm_ws, p->gemm_ws_bytes / sizeof(float), s);
 }
 
+// ---- Embedding with the first RMSNorm: h0 = states . We + be, xn1 = rmsnorm(h0; g1) ----------
+// K = 8 leaves the product nothing to do on the matrix cores; the launch is the 2 x 64 MB of row
+// writes. Half a wave per row: lane q of the 32 holds columns 4q..4q+3 of We (8 x 4 floats), be
+// and g1 in registers, reads the row's 8 states (one 32-byte piece shared by the 32 lanes), and
+// writes h0, xn1 as float4; the sum of squares is a 32-lane DPP / swizzle reduction.
+constexpr int kEmbedNormThreads = 256;
+__global__ __launch_bounds__(kEmbedNormThreads) void embed_norm_kernel(int rows, float eps,
+                                                                      const float* __restrict__ states,
+                                                                      const float* __restrict__ we,
+                                                                      const float* __restrict__ be,
+                                                                      const float* __restrict__ gain, float* __restrict__ h,
+                                                                      float* __restrict__ xn, float* __restrict__ rstd) {
+  constexpr int D = 128, IN = kEmbedIn;
+  const int q = threadIdx.x & 31, c = 4 * q;
+  float4 w[IN];
+#pragma unroll
+  for (int k = 0; k < IN; ++k) w[k] = *reinterpret_cast<const float4*>(we + k * D + c);
+  const float4 b = *reinterpret_cast<const float4*>(be + c), g = *reinterpret_cast<const float4*>(gain + c);
+  const int half = (blockIdx.x * kEmbedNormThreads + threadIdx.x) >> 5, halves = gridDim.x * kEmbedNormThreads / 32;
+  for (int r = half; r < rows; r += halves) {
+    const float4 s0 = *reinterpret_cast<const float4*>(states + (long long)r * IN);
+    const float4 s1 = *reinterpret_cast<const float4*>(states + (long long)r * IN + 4);
+    const float sv[IN] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    float4 o = b;
+#pragma unroll
+    for (int k = 0; k < IN; ++k) {
+      o.x = fmaf(sv[k], w[k].x, o.x);
+      o.y = fmaf(sv[k], w[k].y, o.y);
+      o.z = fmaf(sv[k], w[k].z, o.z);
+      o.w = fmaf(sv[k], w[k].w, o.w);
+    }
+    float ss = o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+    ss = group_sum<16>(ss);
+    ss += __shfl_xor(ss, 16);  // the two 16-lane halves of the row
+    const float rs = 1.0f / sqrtf(ss / (float)D + eps);
+    const long long base = (long long)r * D + c;
+    *reinterpret_cast<float4*>(h + base) = o;
+    *reinterpret_cast<float4*>(xn + base) = make_float4(o.x * rs * g.x, o.y * rs * g.y, o.z * rs * g.z, o.w * rs * g.w);
+    if (q == 0) rstd[r] = rs;
+  }
+}
+static bool embed_norm_applies(const talos_ppo_cfg& c, const PpoOff& po, const float* P, const float* states,
+                               const float* h, const RowNorm& n) {
+  const uintptr_t al = reinterpret_cast<uintptr_t>(states) | reinterpret_cast<uintptr_t>(P + po.we) |
+                       reinterpret_cast<uintptr_t>(P + po.be) | reinterpret_cast<uintptr_t>(n.gain) |
+                       reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(n.out);
+  return c.in_dim == kEmbedIn && c.d_model == 128 && n.out != nullptr && (al & 15) == 0;
+}
+
 static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, const float* states,
                        hipStream_t s, bool heads = true) {
   const talos_block_cfg bc = block_cfg_of(c);
@@ -1710,8 +1759,17 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
     g.ldc = d;
     g.bias = P + po.be;
     g.ksplit = 1;
-    if (c.n_layers > 0) set_norm(g, norm1_of(0), c.eps);
-    if ((rc = gemm_launch(g, s))) return rc;
+    const RowNorm n1 = c.n_layers > 0 ? norm1_of(0) : RowNorm{};
+    if (embed_norm_applies(c, po, P, states, p->h0, n1)) {
+      ProfScope ps_e(s, "embed_norm_kernel", 2.0 * M * kEmbedIn * d, 4.0 * M * (kEmbedIn + 2.0 * d + 1.0));
+      const unsigned blocks = std::min<unsigned>(ceil_div((size_t)M, kEmbedNormThreads / 32), 8192);
+      hipLaunchKernelGGL(embed_norm_kernel, dim3(blocks), dim3(kEmbedNormThreads), 0, s, M, c.eps, states, P + po.we,
+                         P + po.be, n1.gain, p->h0, n1.out, n1.rstd);
+      if ((rc = launch_status("embed_norm_kernel"))) return rc;
+    } else {
+      if (c.n_layers > 0) set_norm(g, n1, c.eps);
+      if ((rc = gemm_launch(g, s))) return rc;
+    }
   }
   const float* h = p->h0;
   size_t base = po.blocks;
