@@ -1685,6 +1685,56 @@ static int tail_bwd_launch(talos_plan_s* p, const talos_ppo_cfg& c, const talos_
   return rw.launch(B, p->gemm_ws, p->gemm_ws_bytes / sizeof(float), s);
 }
 
+// ---- Products over the last-token rows: Y = X W (or X W^T), 16 rows per workgroup ------------
+// The last layer's query projection (with the gather of its input rows, which the dW_q product
+// also reads) and its transpose in the backward: one row-tile launch each, instead of a gather
+// and a 64x64-tile GEMM.
+constexpr int kRowsMmWaves = 4;
+template <int D, int LDW, bool TRANS>
+__global__ __launch_bounds__(64 * kRowsMmWaves) void rows_mm_kernel(int B, int seq, const int32_t* lens,
+                                                                    const float* __restrict__ X, long long ldx,
+                                                                    float* __restrict__ xcopy, const float* W,
+                                                                    float* __restrict__ Y) {
+  constexpr int E = kRowTileRows, LD = D + 4;
+  __shared__ __align__(16) float sx[E * LD];
+  const int r0 = blockIdx.x * E, nr = min(E, B - r0);
+  for (int i = threadIdx.x; i < E * (D / 4); i += 64 * kRowsMmWaves) {
+    const int e = i / (D / 4), c = 4 * (i % (D / 4));
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (e < nr) {
+      long long row = r0 + e;
+      if (seq > 0) row = row * seq + last_row(lens, r0 + e, seq);
+      v = *reinterpret_cast<const float4*>(X + row * ldx + c);
+      if (xcopy) *reinterpret_cast<float4*>(xcopy + (long long)(r0 + e) * D + c) = v;
+    }
+    *reinterpret_cast<float4*>(sx + e * LD + c) = v;
+  }
+  __syncthreads();
+  rowtile_mm_stream<D, D, LD, LDW, kRowsMmWaves, D, TRANS>(sx, W, nullptr, [&](int e, int n, float v) {
+    if (e < nr) Y[(long long)(r0 + e) * D + n] = v;
+  });
+}
+// Y[B][d] = rows of X (the last-token rows of a [B * seq][ldx] buffer when seq > 0; copied to
+// xcopy when given) times the d x d block of W (row pitch ldw = 3d: the query columns of Wqkv;
+// W^T when trans). d = 128, 16-byte aligned rows.
+static bool rows_mm_applies(int d, const float* X, long long ldx, long long ldw, const float* Y, const float* xcopy) {
+  const uintptr_t al = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y) | reinterpret_cast<uintptr_t>(xcopy);
+  return d == 128 && ldw == 3 * d && ldx % 4 == 0 && (al & 15) == 0;
+}
+static int rows_mm_launch(int B, int seq, const int32_t* lens, const float* X, long long ldx, float* xcopy,
+                          const float* W, bool trans, float* Y, hipStream_t s) {
+  constexpr int D = 128;
+  ProfScope ps(s, "rows_mm_kernel", 2.0 * B * D * D, 4.0 * (D * D + (2.0 + (xcopy != nullptr)) * B * D));
+  const dim3 grid((unsigned)ceil_div((size_t)B, kRowTileRows));
+  if (trans)
+    hipLaunchKernelGGL((rows_mm_kernel<D, 3 * D, true>), grid, dim3(64 * kRowsMmWaves), 0, s, B, seq, lens, X, ldx,
+                       xcopy, W, Y);
+  else
+    hipLaunchKernelGGL((rows_mm_kernel<D, 3 * D, false>), grid, dim3(64 * kRowsMmWaves), 0, s, B, seq, lens, X, ldx,
+                       xcopy, W, Y);
+  return launch_status("rows_mm_kernel");
+}
+
 // ---- Embedding with the first RMSNorm: h0 = states . We + be, xn1 = rmsnorm(h0; g1) ----------
 // K = 8 leaves the product nothing to do on the matrix cores; the launch is the 2 x 64 MB of row
 // writes. Half a wave per row: lane q of the 32 holds columns 4q..4q+3 of We (8 x 4 floats), be
@@ -1814,8 +1864,12 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
           g.ksplit = 1;
           if ((rc = gemm_launch(g, s))) return rc;
         }
-        if ((rc = gather(L.xn1, R.xn1, d))) return rc;
-        if ((rc = mm(p, s, 0, 0, c.batch, d, d, R.xn1, d, P + bo.wqkv, 3 * d, R.q, d))) return rc;
+        if (rows_mm_applies(d, L.xn1, d, 3 * d, R.q, R.xn1)) {
+          if ((rc = rows_mm_launch(c.batch, c.seq, p->lens, L.xn1, d, R.xn1, P + bo.wqkv, false, R.q, s))) return rc;
+        } else {
+          if ((rc = gather(L.xn1, R.xn1, d))) return rc;
+          if ((rc = mm(p, s, 0, 0, c.batch, d, d, R.xn1, d, P + bo.wqkv, 3 * d, R.q, d))) return rc;
+        }
         AttnDesc ad = block_attn_desc(p, bc, L);
         ad.q_last = R.q;
         ad.ldq_last = d;
@@ -2247,7 +2301,11 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
       }
       // dxn1 = g_kv.Wkv^T on every row, plus dq.Wq^T on the last rows; then rmsnorm1's backward
       // with the residual gradient R.g_h2 on the last rows
-      if ((rc = mm(p, s, 0, 1, B, d, d, R.dq, d, params + o.wqkv, 3 * d, R.g_xnq, d))) return rc;
+      if (rows_mm_applies(d, R.dq, d, 3 * d, R.g_xnq, nullptr))
+        rc = rows_mm_launch(B, 0, nullptr, R.dq, d, nullptr, params + o.wqkv, true, R.g_xnq, s);
+      else
+        rc = mm(p, s, 0, 1, B, d, d, R.dq, d, params + o.wqkv, 3 * d, R.g_xnq, d);
+      if (rc) return rc;
       if ((rc = before_write(p, s, p->g_out))) return rc;
       rc = norm_bwd_mm(p, s, M, d, 2 * d, g_kv, 3 * d, params + o.wqkv + d, 3 * d, p->g_xn, L.x, params + o.g1,
                        L.rstd1, nullptr, R.g_h2, R.g_xnq, c.seq, p->g_out, G + o.g1);
