@@ -1097,19 +1097,32 @@ __global__ __launch_bounds__(256) void ppo_heads_kernel(int B, int d, int A, flo
 __global__ __launch_bounds__(1024) void ppo_heads_final_kernel(int nblk, int B, int R, const double* __restrict__ part,
                                                                float* __restrict__ loss, double* __restrict__ stats,
                                                                int stats_acc, float* __restrict__ G) {
-  __shared__ double red[16][64];
+  // 16 columns per workgroup: lane (column lane % 16, q = lane / 16) of wave w adds the partial
+  // rows k = 4w + q + 64i into four accumulators (i % 4), then 16 threads add a column's 64 sums
+  // in a fixed order
+  __shared__ double red[64][16];
   const int W = kLossParts + R;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int e = blockIdx.x * 64 + lane;
-  double t = 0.0;
-  if (e < W)
-    for (int k = w; k < nblk; k += 16) t += part[(long long)k * W + e];
-  red[w][lane] = t;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, cl = lane & 15;
+  const int e = blockIdx.x * 16 + cl;
+  double t0 = 0.0, t1 = 0.0, t2 = 0.0, t3 = 0.0;
+  if (e < W) {
+    const long long step = 64LL * W;
+    int k = 4 * w + (lane >> 4);
+    for (; k + 192 < nblk; k += 256) {
+      const double* q = part + (long long)k * W + e;
+      const double a0 = q[0], a1 = q[step], a2 = q[2 * step], a3 = q[3 * step];
+      t0 += a0;
+      t1 += a1;
+      t2 += a2;
+      t3 += a3;
+    }
+    for (; k < nblk; k += 64) t0 += part[(long long)k * W + e];
+  }
+  red[4 * w + (lane >> 4)][cl] = (t0 + t1) + (t2 + t3);
   __syncthreads();
-  if (w != 0 || e >= W) return;
+  if (threadIdx.x >= 16 || e >= W) return;
   double sum = 0.0;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) sum += red[i][lane];
+  for (int i = 0; i < 64; ++i) sum += red[i][cl];
   if (e >= kLossParts) {
     G[e - kLossParts] = (float)sum;
   } else if (e == 0) {
@@ -2208,7 +2221,7 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
       TALOS_LAUNCHED("ppo_heads_kernel");
     }
     ProfScope ps_f(s, "ppo_heads_final_kernel", 0.0, 8.0 * nblk * (kLossParts + R) + 4.0 * R);
-    hipLaunchKernelGGL(ppo_heads_final_kernel, dim3(ceil_div((size_t)kLossParts + R, 64)), dim3(1024), 0, s, nblk, B,
+    hipLaunchKernelGGL(ppo_heads_final_kernel, dim3(ceil_div((size_t)kLossParts + R, 16)), dim3(1024), 0, s, nblk, B,
                        R, p->loss_ws, loss_out, stats, stats_acc, G + po.wa);
     TALOS_LAUNCHED("ppo_heads_final_kernel");
   } else {
