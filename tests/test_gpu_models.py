@@ -52,8 +52,8 @@ def test_block_fwd_bwd_vs_oracle(oracle, B, S, d, H, F, causal, act):
         check_close(dp[sl], dp_r[sl], name=f"d{n}", scale_floor=GRAD_SCALE_FLOOR)
 
 
-def ppo_cfgs(oracle, B, S=32, d=128, L=2, H=4, F=512, A=3):
-    args = (B, S, 8, d, L, H, d // H, F, A, 1, 0, 1e-5, 10000.0, 0.2, 0.5, 0.01)
+def ppo_cfgs(oracle, B, S=32, d=128, L=2, H=4, F=512, A=3, act=0):
+    args = (B, S, 8, d, L, H, d // H, F, A, 1, act, 1e-5, 10000.0, 0.2, 0.5, 0.01)
     return th.PpoCfg(*args), oracle.PpoCfg(*args)
 
 
@@ -100,10 +100,12 @@ def ppo_slices(cfg):
     return out
 
 
-@pytest.mark.parametrize("B,S,L", [(6, 5, 2), (64, 32, 2), (16, 32, 1)])
-def test_ppo_minibatch_vs_oracle(oracle, B, S, L):
+# (B, S, layers, activation): B = 6 and 40 leave a partial 16-row tile in the last-row kernels;
+# act 1 (ReLU) takes their ReLU branch at the C4 width (d 128, F 512).
+@pytest.mark.parametrize("B,S,L,act", [(6, 5, 2, 0), (64, 32, 2, 0), (16, 32, 1, 0), (40, 16, 2, 1)])
+def test_ppo_minibatch_vs_oracle(oracle, B, S, L, act):
     rng = np.random.default_rng(2000 + B + S)
-    cfg, ocfg = ppo_cfgs(oracle, B, S=S, L=L)
+    cfg, ocfg = ppo_cfgs(oracle, B, S=S, L=L, act=act)
     p = f32(ppo_params(rng, ocfg))
     states, actions, adv, ret, old = ppo_inputs(rng, ocfg, p, oracle)
     loss_r, logits_r, values_r, dp_r = oracle.ppo_fwd_bwd(ocfg, p, states, actions, adv, ret, old)
