@@ -112,19 +112,35 @@ __device__ __forceinline__ T block_sum(T v, T* red) {
   return t;
 }
 
+// Phi(x), the standard normal CDF, and e = exp(-x^2 / 2). erf(z) for z >= 0 by Abramowitz &
+// Stegun 7.1.26 (Hastings): erf(z) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2),
+// t = 1 / (1 + p z), |error| <= 1.5e-7; with z = |x| / sqrt(2), exp(-z^2) is the same
+// exp(-x^2 / 2) the density needs, so GELU and its derivative take one exponential. The lower
+// tail 0.5 erfc(z) is formed directly (no cancellation for x < 0).
+__device__ __forceinline__ float normal_cdf(float x, float* e) {
+  const float z = fabsf(x) * 0.70710678118654752f;
+  *e = __expf(-0.5f * x * x);  // hardware exp2 of the scaled argument: relative error ~|x^2| 2^-24
+  const float t = __frcp_rn(fmaf(0.3275911f, z, 1.0f));
+  const float poly =
+      t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, 1.061405429f, -1.453152027f), 1.421413741f), -0.284496736f), 0.254829592f);
+  const float tail = 0.5f * poly * *e;  // P(X > |x|)
+  return x >= 0.f ? 1.0f - tail : tail;
+}
 __device__ __forceinline__ float gelu_f(float x) {
-  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+  float e;
+  return x * normal_cdf(x, &e);
 }
 // d/dx of x * Phi(x) = Phi(x) + x * phi(x)
 __device__ __forceinline__ float gelu_d(float x) {
-  const float cdf = 0.5f * (1.0f + erff(x * 0.70710678118654752f));
-  const float pdf = 0.39894228040143268f * expf(-0.5f * x * x);
-  return cdf + x * pdf;
+  float e;
+  const float cdf = normal_cdf(x, &e);
+  return cdf + x * (0.39894228040143268f * e);
 }
-// gelu(x) = x * Phi(x), and *d = gelu'(x), sharing the erf
+// gelu(x) = x * Phi(x), and *d = gelu'(x), sharing the exponential
 __device__ __forceinline__ float gelu_fd(float x, float* d) {
-  const float cdf = 0.5f * (1.0f + erff(x * 0.70710678118654752f));
-  *d = cdf + x * (0.39894228040143268f * expf(-0.5f * x * x));
+  float e;
+  const float cdf = normal_cdf(x, &e);
+  *d = cdf + x * (0.39894228040143268f * e);
   return x * cdf;
 }
 
