@@ -265,9 +265,12 @@ __device__ __forceinline__ float epi_value(const GemmArgs& p, float acc, int row
 // Epilogue of four consecutive columns [col, col + 4) of one row, read from / written to global
 // memory as float4 (interior) or per element (edges). RoPE pairs (2i, 2i+1) sit in (x, y) and
 // (z, w) because col is a multiple of 4.
-template <int E>
+// PRE: the aux row piece the backward's multiply reads (E_DGELU / E_DRELU) was loaded by the
+// caller, ahead of this row's stores (pre), so the loads of several rows are in flight together.
+template <int E, bool PRE = false>
 __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int row, int col, float* C,
-                                             const float* __restrict__ resid, bool full) {
+                                             const float* __restrict__ resid, bool full,
+                                             float4 pre = make_float4(0.f, 0.f, 0.f, 0.f)) {
   float o[4] = {v.x * p.alpha, v.y * p.alpha, v.z * p.alpha, v.w * p.alpha};
   if constexpr ((E & E_ROPE) != 0) {
     if (col < p.rope_cols) {
@@ -300,7 +303,7 @@ __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int ro
       o[0] += r.x; o[1] += r.y; o[2] += r.z; o[3] += r.w;
     }
     if constexpr ((E & (E_DGELU | E_DRELU)) != 0) {
-      const float4 u = *reinterpret_cast<const float4*>(p.aux + (long long)row * p.ldaux + col);
+      const float4 u = PRE ? pre : *reinterpret_cast<const float4*>(p.aux + (long long)row * p.ldaux + col);
       const float uu[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -739,6 +742,25 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
         const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
         normb_apply(p, v, rbase + 8 * i, col, cur, g, nbw);
         cur = nxt;
+      }
+    } else if constexpr ((E & (E_DGELU | E_DRELU)) != 0) {
+      // the aux pieces of all of this thread's rows are loaded before the first store (C and aux
+      // may alias as far as the compiler knows, so a load after a store would wait for it)
+      const bool fast = aligned && full_cols;
+      float4 ax[T_ROWS / 8];
+#pragma unroll
+      for (int i = 0; i < T_ROWS / 8; ++i) {
+        const int row = m0 + half * T_ROWS + (threadIdx.x >> 5) + 8 * i;
+        ax[i] = fast && row < p.M ? *reinterpret_cast<const float4*>(p.aux + (long long)row * p.ldaux + col)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int i = 0; i < T_ROWS / 8; ++i) {
+        const int lr = (threadIdx.x >> 5) + 8 * i;
+        const int row = m0 + half * T_ROWS + lr;
+        const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
+        const float4 o = epi_store4<E, true>(p, v, row, col, C, resid, fast && row < p.M, ax[i]);
+        if constexpr ((E & E_NORM) != 0) epi_norm4(p, o, row, col);
       }
     } else {
 #pragma unroll 4
