@@ -265,12 +265,33 @@ __device__ __forceinline__ float epi_value(const GemmArgs& p, float acc, int row
 // Epilogue of four consecutive columns [col, col + 4) of one row, read from / written to global
 // memory as float4 (interior) or per element (edges). RoPE pairs (2i, 2i+1) sit in (x, y) and
 // (z, w) because col is a multiple of 4.
-// PRE: the aux row piece the backward's multiply reads (E_DGELU / E_DRELU) was loaded by the
-// caller, ahead of this row's stores (pre), so the loads of several rows are in flight together.
+// Operands of one row's epilogue loaded by the caller ahead of the stores of earlier rows (C
+// may alias them as far as the compiler knows, so a load after a store would wait for it): the
+// aux piece the backward's multiply reads (E_DGELU / E_DRELU), the RoPE cos / sin pairs, the bias.
+struct EpiPre {
+  float4 aux, rope, bias;
+};
+template <int E>
+__device__ __forceinline__ EpiPre epi_preload(const GemmArgs& p, int row, int col, bool full, float4 bias) {
+  EpiPre q;
+  q.bias = bias;
+  q.aux = make_float4(0.f, 0.f, 0.f, 0.f);
+  q.rope = make_float4(1.f, 1.f, 0.f, 0.f);
+  if constexpr ((E & (E_DGELU | E_DRELU)) != 0)
+    if (full) q.aux = *reinterpret_cast<const float4*>(p.aux + (long long)row * p.ldaux + col);
+  if constexpr ((E & E_ROPE) != 0) {
+    if (row < p.M && col < p.rope_cols) {
+      const int half = p.rope_dim >> 1, pos = row % p.rope_seq, pi = (col % p.rope_dim) >> 1;
+      const float* cs = p.rcos + pos * half + pi;
+      const float* sn = p.rsin + pos * half + pi;
+      q.rope = make_float4(cs[0], cs[1], sn[0], sn[1]);
+    }
+  }
+  return q;
+}
 template <int E, bool PRE = false>
 __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int row, int col, float* C,
-                                             const float* __restrict__ resid, bool full,
-                                             float4 pre = make_float4(0.f, 0.f, 0.f, 0.f)) {
+                                             const float* __restrict__ resid, bool full, const EpiPre& pre = EpiPre{}) {
   float o[4] = {v.x * p.alpha, v.y * p.alpha, v.z * p.alpha, v.w * p.alpha};
   if constexpr ((E & E_ROPE) != 0) {
     if (col < p.rope_cols) {
@@ -281,7 +302,7 @@ __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int ro
       const float* sn = p.rsin + pos * half + pi;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const float c = cs[j], s = sn[j];
+        const float c = PRE ? (j ? pre.rope.y : pre.rope.x) : cs[j], s = PRE ? (j ? pre.rope.w : pre.rope.z) : sn[j];
         const float x0 = o[2 * j], x1 = o[2 * j + 1];
         o[2 * j] = fmaf(x0, c, -x1 * s);
         o[2 * j + 1] = fmaf(x0, s, x1 * c);
@@ -295,7 +316,7 @@ __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int ro
       o[0] += p.beta * c.x; o[1] += p.beta * c.y; o[2] += p.beta * c.z; o[3] += p.beta * c.w;
     }
     if constexpr ((E & E_BIAS) != 0) {
-      const float4 bv = *reinterpret_cast<const float4*>(p.bias + col);
+      const float4 bv = PRE ? pre.bias : *reinterpret_cast<const float4*>(p.bias + col);
       o[0] += bv.x; o[1] += bv.y; o[2] += bv.z; o[3] += bv.w;
     }
     if constexpr ((E & E_RESID) != 0) {
@@ -303,7 +324,7 @@ __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int ro
       o[0] += r.x; o[1] += r.y; o[2] += r.z; o[3] += r.w;
     }
     if constexpr ((E & (E_DGELU | E_DRELU)) != 0) {
-      const float4 u = PRE ? pre : *reinterpret_cast<const float4*>(p.aux + (long long)row * p.ldaux + col);
+      const float4 u = PRE ? pre.aux : *reinterpret_cast<const float4*>(p.aux + (long long)row * p.ldaux + col);
       const float uu[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -743,33 +764,29 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
         normb_apply(p, v, rbase + 8 * i, col, cur, g, nbw);
         cur = nxt;
       }
-    } else if constexpr ((E & (E_DGELU | E_DRELU)) != 0) {
-      // the aux pieces of all of this thread's rows are loaded before the first store (C and aux
-      // may alias as far as the compiler knows, so a load after a store would wait for it)
-      const bool fast = aligned && full_cols;
-      float4 ax[T_ROWS / 8];
-#pragma unroll
-      for (int i = 0; i < T_ROWS / 8; ++i) {
-        const int row = m0 + half * T_ROWS + (threadIdx.x >> 5) + 8 * i;
-        ax[i] = fast && row < p.M ? *reinterpret_cast<const float4*>(p.aux + (long long)row * p.ldaux + col)
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int i = 0; i < T_ROWS / 8; ++i) {
-        const int lr = (threadIdx.x >> 5) + 8 * i;
-        const int row = m0 + half * T_ROWS + lr;
-        const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
-        const float4 o = epi_store4<E, true>(p, v, row, col, C, resid, fast && row < p.M, ax[i]);
-        if constexpr ((E & E_NORM) != 0) epi_norm4(p, o, row, col);
-      }
     } else {
-#pragma unroll 4
-      for (int i = 0; i < T_ROWS / 8; ++i) {
-        const int lr = (threadIdx.x >> 5) + 8 * i;
-        const int row = m0 + half * T_ROWS + lr;
-        const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
-        const float4 o = epi_store4<E>(p, v, row, col, C, resid, aligned && full_cols && row < p.M);
-        if constexpr ((E & E_NORM) != 0) epi_norm4(p, o, row, col);
+      // the row-dependent operands of four rows at a time (and the bias once) are loaded before
+      // those rows' stores
+      const bool fast = aligned && full_cols;
+      float4 bias = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr ((E & E_BIAS) != 0)
+        if (fast) bias = *reinterpret_cast<const float4*>(p.bias + col);
+#pragma unroll 1
+      for (int i0 = 0; i0 < T_ROWS / 8; i0 += 4) {
+        EpiPre pre[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int row = m0 + half * T_ROWS + (threadIdx.x >> 5) + 8 * (i0 + j);
+          pre[j] = epi_preload<E>(p, row, col, fast && row < p.M, bias);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int lr = (threadIdx.x >> 5) + 8 * (i0 + j);
+          const int row = m0 + half * T_ROWS + lr;
+          const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
+          const float4 o = epi_store4<E, true>(p, v, row, col, C, resid, fast && row < p.M, pre[j]);
+          if constexpr ((E & E_NORM) != 0) epi_norm4(p, o, row, col);
+        }
       }
     }
   }
