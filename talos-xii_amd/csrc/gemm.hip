@@ -378,7 +378,9 @@ __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int ro
 // RMSNorm of the rows of a 128-wide tile from the epilogue's float4s: the 32 lanes of one
 // half-wave hold one row (column groups 4 * (lane % 32)), so the row sum of squares is a
 // shuffle reduction over that half-wave. Same arithmetic as rmsnorm_fwd_kernel.
-__device__ __forceinline__ void epi_norm4(const GemmArgs& p, float4 o, int row, int col) {
+// g: the gain piece of columns col..col+3 when they are all inside N, loaded by the caller once
+// (a load here would follow the previous rows' stores and wait for them)
+__device__ __forceinline__ void epi_norm4(const GemmArgs& p, float4 o, int row, int col, float4 g) {
   float ss = o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
 #pragma unroll
   for (int off = 16; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
@@ -387,7 +389,6 @@ __device__ __forceinline__ void epi_norm4(const GemmArgs& p, float4 o, int row, 
   if ((threadIdx.x & 31) == 0 && p.norm_rstd) p.norm_rstd[row] = r;
   float* y = p.norm_out + (long long)row * p.ldn + col;
   if (col + 3 < p.N) {
-    const float4 g = *reinterpret_cast<const float4*>(p.norm_gain + col);
     *reinterpret_cast<float4*>(y) = make_float4(o.x * r * g.x, o.y * r * g.y, o.z * r * g.z, o.w * r * g.w);
   } else {
     const float oo[4] = {o.x, o.y, o.z, o.w};
@@ -768,9 +769,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
       // the row-dependent operands of four rows at a time (and the bias once) are loaded before
       // those rows' stores
       const bool fast = aligned && full_cols;
-      float4 bias = make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 bias = make_float4(0.f, 0.f, 0.f, 0.f), ngain = make_float4(0.f, 0.f, 0.f, 0.f);
       if constexpr ((E & E_BIAS) != 0)
         if (fast) bias = *reinterpret_cast<const float4*>(p.bias + col);
+      if constexpr ((E & E_NORM) != 0)
+        if (col + 3 < p.N) ngain = *reinterpret_cast<const float4*>(p.norm_gain + col);
 #pragma unroll 1
       for (int i0 = 0; i0 < T_ROWS / 8; i0 += 4) {
         EpiPre pre[4];
@@ -785,7 +788,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
           const int row = m0 + half * T_ROWS + lr;
           const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
           const float4 o = epi_store4<E, true>(p, v, row, col, C, resid, fast && row < p.M, pre[j]);
-          if constexpr ((E & E_NORM) != 0) epi_norm4(p, o, row, col);
+          if constexpr ((E & E_NORM) != 0) epi_norm4(p, o, row, col, ngain);
         }
       }
     }
