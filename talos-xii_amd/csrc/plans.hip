@@ -1320,6 +1320,9 @@ __global__ __launch_bounds__(kTailThreads) void ppo_tail_bwd_kernel(TailBwdArgs 
   const int r0 = blockIdx.x * E, nr = min(E, a.B - r0);
   tail_rows_in<D, LDD>(sg, a.g_pout, r0, nr);
   tail_rows_in<D, LDD>(sx, a.last, r0, nr);
+  // u (gelu' or the pre-activation) staged in LDS now: read in the dGELU / dReLU phase from LDS
+  // instead of by loads that would each wait behind the previous element's store of g_u
+  tail_rows_in<F, LDF>(su, a.u, r0, nr);
   if (threadIdx.x < E) srs[threadIdx.x] = threadIdx.x < nr ? a.rstdf[r0 + threadIdx.x] : 0.f;
   RowGain<D> gf;
   gf.load(a.gf);
@@ -1336,15 +1339,11 @@ __global__ __launch_bounds__(kTailThreads) void ppo_tail_bwd_kernel(TailBwdArgs 
   if (threadIdx.x < E) srs[threadIdx.x] = threadIdx.x < nr ? a.rstd2[r0 + threadIdx.x] : 0.f;
   // g_u = (g_last.W2^T) * gelu'(u), or masked by u > 0 for ReLU
   const bool relu = a.relu;
-  const float* gu_in = a.u;
   float* gu = a.g_u;
   rowtile_mm_stream<D, F, LDD, D, W, D, true>(sg, a.w2, nullptr, [&](int e, int n, float v) {
-    float g = 0.f;
-    if (e < nr) {
-      const float uu = gu_in[(long long)(r0 + e) * F + n];
-      g = relu ? (uu > 0.f ? v : 0.f) : v * uu;
-      gu[(long long)(r0 + e) * F + n] = g;
-    }
+    const float uu = su[e * LDF + n];  // zero on rows past nr
+    const float g = relu ? (uu > 0.f ? v : 0.f) : v * uu;
+    if (e < nr) gu[(long long)(r0 + e) * F + n] = g;
     su[e * LDF + n] = g;
   });
   RowGain<D> g2;
