@@ -981,9 +981,10 @@ __global__ __launch_bounds__(256) void ppo_loss_kernel(int B, int A, float clip_
 // the head gradients (LDS, fp32 over its samples). Each workgroup writes its partial sums (f64) of
 // the loss statistics and of the head gradients, laid out as the parameters Wa | ba | Wc | bc;
 // ppo_heads_final_kernel adds the workgroups up in a fixed order.
-constexpr int kHeadWaves = 8;
-constexpr int kHeadSamples = 16;  // samples per workgroup (2 per wave) of the fused heads kernel
-constexpr int kHeadMaxRow = 2176;  // d * (A + 1) + A + 1 of the fused path (per-wave sums in LDS)
+constexpr int kHeadWaves = 16;
+constexpr int kHeadSamples = 16;  // samples per workgroup (1 per wave) of the fused heads kernel
+// d * (A + 1) + A + 1 of the fused path: the per-wave sums of 16 waves stay within 64 KB of LDS
+constexpr int kHeadMaxRow = 1008;
 __global__ __launch_bounds__(64 * kHeadWaves) void ppo_heads_kernel(int B, int d, int A, float clip_eps, float cv, float ce,
                                                         const float* __restrict__ pout, const float* __restrict__ Wa,
                                                         const float* __restrict__ ba, const float* __restrict__ Wc,
