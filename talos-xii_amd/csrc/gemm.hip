@@ -262,6 +262,15 @@ __device__ __forceinline__ float epi_value(const GemmArgs& p, float acc, int row
   return v;
 }
 
+// Index into the [rope_seq, rope_dim / 2] cos / sin table of the interleaved pair that starts at
+// column c (even) of row `row`: position row % rope_seq, pair (c % rope_dim) / 2 of its head. Each
+// pair is indexed on its own, so a head whose width is not a multiple of 4 (its pairs straddle the
+// float4 groups) takes its own pairs, never the next head's. -1 for columns past rope_cols.
+__device__ __forceinline__ int rope_index(const GemmArgs& p, int row, int c) {
+  if (c >= p.rope_cols) return -1;
+  return (row % p.rope_seq) * (p.rope_dim >> 1) + ((c % p.rope_dim) >> 1);
+}
+
 // Epilogue of four consecutive columns [col, col + 4) of one row, read from / written to global
 // memory as float4 (interior) or per element (edges). RoPE pairs (2i, 2i+1) sit in (x, y) and
 // (z, w) because col is a multiple of 4.
@@ -281,10 +290,8 @@ __device__ __forceinline__ EpiPre epi_preload(const GemmArgs& p, int row, int co
     if (full) q.aux = *reinterpret_cast<const float4*>(p.aux + (long long)row * p.ldaux + col);
   if constexpr ((E & E_ROPE) != 0) {
     if (row < p.M && col < p.rope_cols) {
-      const int half = p.rope_dim >> 1, pos = row % p.rope_seq, pi = (col % p.rope_dim) >> 1;
-      const float* cs = p.rcos + pos * half + pi;
-      const float* sn = p.rsin + pos * half + pi;
-      q.rope = make_float4(cs[0], cs[1], sn[0], sn[1]);
+      const int i0 = rope_index(p, row, col), i1 = rope_index(p, row, col + 2);
+      q.rope = make_float4(p.rcos[i0], i1 >= 0 ? p.rcos[i1] : 1.f, p.rsin[i0], i1 >= 0 ? p.rsin[i1] : 0.f);
     }
   }
   return q;
@@ -294,15 +301,13 @@ __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int ro
                                              const float* __restrict__ resid, bool full, const EpiPre& pre = EpiPre{}) {
   float o[4] = {v.x * p.alpha, v.y * p.alpha, v.z * p.alpha, v.w * p.alpha};
   if constexpr ((E & E_ROPE) != 0) {
-    if (col < p.rope_cols) {
-      const int half = p.rope_dim >> 1;
-      const int pos = row % p.rope_seq;
-      const int pi = (col % p.rope_dim) >> 1;
-      const float* cs = p.rcos + pos * half + pi;
-      const float* sn = p.rsin + pos * half + pi;
+    if (col < p.rope_cols && row < p.M) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const float c = PRE ? (j ? pre.rope.y : pre.rope.x) : cs[j], s = PRE ? (j ? pre.rope.w : pre.rope.z) : sn[j];
+        // the table entry of pair (col + 2j, col + 2j + 1); -1 (identity) past the rotated columns
+        const int ij = PRE ? 0 : rope_index(p, row, col + 2 * j);
+        const float c = PRE ? (j ? pre.rope.y : pre.rope.x) : (ij >= 0 ? p.rcos[ij] : 1.f);
+        const float s = PRE ? (j ? pre.rope.w : pre.rope.z) : (ij >= 0 ? p.rsin[ij] : 0.f);
         const float x0 = o[2 * j], x1 = o[2 * j + 1];
         o[2 * j] = fmaf(x0, c, -x1 * s);
         o[2 * j + 1] = fmaf(x0, s, x1 * c);
@@ -1240,7 +1245,7 @@ __global__ void add_last_rows_kernel(int nb, int seq, int n, const int32_t* __re
 static bool normb_fused(const GemmDesc& d) {
   auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
   const int tiles_m = (d.M + BM - 1) / BM;
-  return d.N == BN && !d.bf16 && d.batch == 1 && !d.transA && d.transB && !use_small(d, num_cus()) &&
+  return d.fuse_norm && d.N == BN && !d.bf16 && d.batch == 1 && !d.transA && d.transB && !use_small(d, num_cus()) &&
          d.beta == 0.f && !d.bias && !d.resid && d.act == GEMM_ACT_NONE && d.dact == GEMM_DACT_NONE &&
          d.rope_cols == 0 && !d.norm_out && !d.dbias && a16(d.normb_x) && a16(d.normb_dx) && a16(d.normb_gain) &&
          a16(d.normb_add) && a16(d.normb_add_last) && a16(d.normb_dy_last) && d.normb_ws &&
@@ -1277,7 +1282,7 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
 }
 
 static int gemm_launch_one(const GemmDesc& d, hipStream_t stream) {
-  if (d.norm_out && (d.N != BN || d.bf16 || d.batch != 1 || use_small(d, num_cus()))) {
+  if (d.norm_out && (!d.fuse_norm || d.N != BN || d.bf16 || d.batch != 1 || use_small(d, num_cus()))) {
     // the fused row norm needs the whole 128-wide row in one 128x128 tile: otherwise the product,
     // then the separate row-norm kernel
     TALOS_REQUIRE(d.ldc == d.N && d.ldn == d.N, TALOS_ERR_UNSUPPORTED,

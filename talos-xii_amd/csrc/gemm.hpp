@@ -79,6 +79,9 @@ struct GemmDesc {
   // bf16-in / fp32-accumulate: operands are rounded to bf16 (nearest even) as they are staged
   // into LDS and multiplied with v_mfma_f32_32x32x16_bf16; HBM layout and outputs stay fp32.
   bool bf16 = false;
+  // false: the row norm (norm_out) and the row-norm backward (normb_dx) always run as the separate
+  // row kernels after the product, never in its epilogue (the cross-check of the fused epilogues)
+  bool fuse_norm = true;
 };
 
 // Fills in ksplit (when 0) and returns the workspace bytes the descriptor needs.

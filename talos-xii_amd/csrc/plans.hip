@@ -88,6 +88,10 @@ struct talos_plan_s {
   } lr{};
   const int32_t* lens = nullptr;  // per-sample lengths of the PPO call in progress (nullptr: all seq)
   int num_cu = 256;
+  // TALOS_PLAN_UNFUSED=1 at creation: every fused alternative (row norms in GEMM epilogues, the
+  // embedding + norm kernel, the fused heads, the last-row tail kernels) takes its separate-kernel
+  // path instead; the same results, as the tests check at full size
+  bool unfused = false;
   bool bf16 = false;  // bf16-in / fp32-accumulate GEMMs (MLA plans with TALOS_PREC_BF16)
   talos::Profiler* prof = nullptr;
   // latent attention: the projections before concatenation and the attention gradients,
@@ -219,6 +223,12 @@ int check_block_cfg(const talos_block_cfg& c) {
   TALOS_REQUIRE((long long)c.batch * c.seq * (3LL * c.d_model) < (1LL << 31), TALOS_ERR_UNSUPPORTED,
                 "block cfg: batch*seq*3*d_model must stay below 2^31 elements");
   return TALOS_OK;
+}
+
+// Whether the environment variable is set to 1 (read when a plan is created).
+static bool env_flag(const char* name) {
+  const char* v = std::getenv(name);
+  return v && v[0] == '1' && v[1] == 0;
 }
 
 static int plan_alloc(talos_plan_s* p, float** out, size_t n) {
@@ -491,6 +501,7 @@ static int norm_bwd_mm(talos_plan_s* p, hipStream_t s, int M, int d, int K, cons
   gd.normb_dw = dw;
   gd.normb_ws = p->red_ws;
   gd.normb_ws_bytes = p->red_ws_bytes;
+  gd.fuse_norm = !p->unfused;
   return gemm_launch(gd, s);
 }
 
@@ -642,7 +653,8 @@ struct RowNorm {
   float* out = nullptr;
   float* rstd = nullptr;
 };
-static void set_norm(GemmDesc& g, const RowNorm& n, float eps) {
+static void set_norm(const talos_plan_s* p, GemmDesc& g, const RowNorm& n, float eps) {
+  g.fuse_norm = !p->unfused;
   g.norm_gain = n.gain;
   g.norm_out = n.out;
   g.ldn = g.N;
@@ -713,7 +725,7 @@ static int block_mlp_forward(talos_plan_s* p, const talos_block_cfg& c, const fl
     g.resid = x;
     g.ldr = d;
     g.ksplit = 1;
-    set_norm(g, RowNorm{P + o.g2, xn2, rstd2}, c.eps);
+    set_norm(p, g, RowNorm{P + o.g2, xn2, rstd2}, c.eps);
     if ((rc = gemm_launch(g, s))) return rc;
   }
   {
@@ -749,7 +761,7 @@ static int block_mlp_forward(talos_plan_s* p, const talos_block_cfg& c, const fl
   g.resid = h2;
   g.ldr = d;
   g.ksplit = 1;
-  if (next.out) set_norm(g, next, c.eps);
+  if (next.out) set_norm(p, g, next, c.eps);
   return gemm_launch(g, s);
 }
 
@@ -1367,8 +1379,8 @@ __global__ __launch_bounds__(kTailThreads) void ppo_tail_bwd_kernel(TailBwdArgs 
 
 // Whether the last-row tail runs as the two kernels above: a standard or latent block whose
 // attention width is d, and an instantiated (d, ffn) shape.
-static bool tail_fused(const talos_ppo_cfg& c) {
-  if (c.n_layers < 1 || c.batch < 1) return false;
+static bool tail_fused(const talos_plan_s* p, const talos_ppo_cfg& c) {
+  if (p->unfused || c.n_layers < 1 || c.batch < 1) return false;
   const talos_block_cfg bc = block_cfg_of(c);
   if (attn_width(bc) != c.d_model) return false;
   return (c.d_model == 128 && c.ffn_dim == 512) || (c.d_model == 64 && c.ffn_dim == 128);
@@ -1802,7 +1814,7 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
   const talos_block_cfg bc = block_cfg_of(c);
   const PpoOff po = ppo_offsets(c);
   const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions, ow = attn_width(bc);
-  const bool tail = tail_fused(c);
+  const bool tail = tail_fused(p, c);
   // each layer's RMSNorm1 runs in the epilogue of the product that makes its input
   auto norm1_of = [&](int l) {
     const BlockOff bo = block_offsets(bc, po.blocks + (size_t)l * block_params(bc));
@@ -1823,14 +1835,14 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
     g.bias = P + po.be;
     g.ksplit = 1;
     const RowNorm n1 = c.n_layers > 0 ? norm1_of(0) : RowNorm{};
-    if (embed_norm_applies(c, po, P, states, p->h0, n1)) {
+    if (!p->unfused && embed_norm_applies(c, po, P, states, p->h0, n1)) {
       ProfScope ps_e(s, "embed_norm_kernel", 2.0 * M * kEmbedIn * d, 4.0 * M * (kEmbedIn + 2.0 * d + 1.0));
       const unsigned blocks = std::min<unsigned>(ceil_div((size_t)M, kEmbedNormThreads / 32), 8192);
       hipLaunchKernelGGL(embed_norm_kernel, dim3(blocks), dim3(kEmbedNormThreads), 0, s, M, c.eps, states, P + po.we,
                          P + po.be, n1.gain, p->h0, n1.out, n1.rstd);
       if ((rc = launch_status("embed_norm_kernel"))) return rc;
     } else {
-      if (c.n_layers > 0) set_norm(g, n1, c.eps);
+      if (c.n_layers > 0) set_norm(p, g, n1, c.eps);
       if ((rc = gemm_launch(g, s))) return rc;
     }
   }
@@ -2003,6 +2015,7 @@ int talos_block_plan_create(const talos_block_cfg* cfg, talos_plan* plan) {
   auto* p = new talos_plan_s();
   p->kind = 1;
   p->prof = profiler_new();
+  p->unfused = env_flag("TALOS_PLAN_UNFUSED");
   p->blk = *cfg;
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, 0) == hipSuccess) p->num_cu = prop.multiProcessorCount;
@@ -2051,6 +2064,7 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
   auto* p = new talos_plan_s();
   p->kind = 2;
   p->prof = profiler_new();
+  p->unfused = env_flag("TALOS_PLAN_UNFUSED");
   p->ppo = *cfg;
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, 0) == hipSuccess) p->num_cu = prop.multiProcessorCount;
@@ -2205,7 +2219,7 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
   const int M = c.batch * c.seq, d = c.d_model, A = c.n_actions, B = c.batch;
   // the heads, loss and their backward in one kernel when the per-wave head gradients fit in LDS
   const int R = d * (A + 1) + A + 1;
-  const bool fused_heads = R <= kHeadMaxRow;
+  const bool fused_heads = R <= kHeadMaxRow && !p->unfused;
   int rc = ppo_forward(p, c, params, states, s, !fused_heads);
   if (rc) return rc;
   float* G = dparams;
@@ -2255,7 +2269,7 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
     offs.push_back(block_offsets(bc, base));
     base = offs.back().end;
   }
-  const bool tail = tail_fused(c);
+  const bool tail = tail_fused(p, c);
   if (tail) {  // out_proj through the last layer's MLP half: the row gradients in one kernel
     if ((rc = tail_bwd_launch(p, c, bc, params, G, offs.back(), po, s))) return rc;
   } else {
@@ -2390,6 +2404,7 @@ int talos_mla_plan_create(const talos_mla_cfg* cfg, talos_plan* plan) {
   auto* p = new talos_plan_s();
   p->kind = 3;
   p->prof = profiler_new();
+  p->unfused = env_flag("TALOS_PLAN_UNFUSED");
   p->mla = *cfg;
   p->bf16 = cfg->precision == TALOS_PREC_BF16;
   hipDeviceProp_t prop;

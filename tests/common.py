@@ -1,5 +1,6 @@
 """Shared input generators and the comparison rule of the parity tests."""
 import math
+import os
 
 import numpy as np
 
@@ -23,16 +24,29 @@ def f32(a):
 GRAD_SCALE_FLOOR = 1e-6
 
 
+# One record per check_close call that was given a scale floor: which tensor, the absolute floor
+# it got, and how many of its elements pass only because of that floor (they would fail the plain
+# rtol * |ref| + atol rule). conftest.py prints the records with a non-zero count at the end of
+# the session and writes all of them to $TALOS_TOLERANCE_AUDIT (a JSON file) when that is set.
+FLOOR_AUDIT = []
+
+
 def check_close(got, ref, rtol=FP32_RTOL, atol=FP32_ATOL, name="", scale_floor=0.0):
     """Element-wise |got - ref| <= rtol * |ref| + max(atol, scale_floor * max|ref|); reports the
-    worst element."""
+    worst element. With a scale floor, the elements that need it are counted in FLOOR_AUDIT."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     assert got.shape == ref.shape, f"{name}: shape {got.shape} vs {ref.shape}"
     assert np.all(np.isfinite(got)), f"{name}: non-finite values"
     err = np.abs(got - ref)
     if scale_floor and ref.size:
-        atol = max(atol, scale_floor * float(np.abs(ref).max()))
+        plain = err > rtol * np.abs(ref) + atol
+        floor = max(atol, scale_floor * float(np.abs(ref).max()))
+        FLOOR_AUDIT.append({"test": os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0], "tensor": name,
+                            "size": int(ref.size), "floor": floor, "plain_atol": atol,
+                            "max_abs_ref": float(np.abs(ref).max()), "needs_floor": int(plain.sum()),
+                            "worst_err_over_plain": float(np.max(err / (rtol * np.abs(ref) + atol)))})
+        atol = floor
     bound = rtol * np.abs(ref) + atol
     bad = err > bound
     if bad.any():

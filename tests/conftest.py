@@ -1,3 +1,4 @@
+import json
 import os
 import sys
 
@@ -17,4 +18,30 @@ def pytest_configure(config):
 def oracle():
     import pyoracle
     pyoracle.build()
+    # the CPU share of a GPU box is 16 cores whatever the machine reports
+    pyoracle.set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
     return pyoracle
+
+
+def pytest_terminal_summary(terminalreporter):
+    """The parameter-gradient tolerance audit: every tensor that needed the raised absolute floor
+    (common.GRAD_SCALE_FLOOR) to pass, with the floor and the number of elements that needed it."""
+    try:
+        import common
+    except ImportError:
+        return
+    recs = common.FLOOR_AUDIT
+    if not recs:
+        return
+    out = os.environ.get("TALOS_TOLERANCE_AUDIT")
+    if out:
+        with open(out, "w") as f:
+            json.dump(recs, f, indent=1)
+    need = [r for r in recs if r["needs_floor"]]
+    tr = terminalreporter
+    tr.section("parameter-gradient tolerance audit")
+    tr.write_line(f"{len(recs)} tensors checked with the scale floor; {len(need)} have elements that need it")
+    for r in sorted(need, key=lambda r: -r["needs_floor"]):
+        tr.write_line(f"  {r['test']} {r['tensor']}: {r['needs_floor']}/{r['size']} elements, floor "
+                      f"{r['floor']:.3e} (max|ref| {r['max_abs_ref']:.3e}), worst err / plain bound "
+                      f"{r['worst_err_over_plain']:.2f}")

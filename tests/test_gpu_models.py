@@ -36,8 +36,11 @@ def run_block(cfg, p, x, G):
     return res
 
 
+# head dims 6 and 10 (not multiples of 4): the RoPE epilogue's interleaved pairs straddle the
+# float4 column groups and the heads, so each pair must take its own head's table entry
 @pytest.mark.parametrize("B,S,d,H,F,causal,act", [(2, 6, 16, 4, 64, 1, 0), (3, 64, 128, 4, 512, 1, 0),
-                                                  (2, 33, 64, 2, 128, 0, 1)])
+                                                  (2, 33, 64, 2, 128, 0, 1), (2, 5, 24, 4, 48, 1, 0),
+                                                  (3, 9, 40, 4, 80, 0, 1)])
 def test_block_fwd_bwd_vs_oracle(oracle, B, S, d, H, F, causal, act):
     rng = np.random.default_rng(1000 + S + d)
     cfg = th.BlockCfg(B, S, d, H, d // H, F, causal, act, 1e-6, 10000.0)
@@ -100,12 +103,15 @@ def ppo_slices(cfg):
     return out
 
 
-# (B, S, layers, activation): B = 6 and 40 leave a partial 16-row tile in the last-row kernels;
-# act 1 (ReLU) takes their ReLU branch at the C4 width (d 128, F 512).
-@pytest.mark.parametrize("B,S,L,act", [(6, 5, 2, 0), (64, 32, 2, 0), (16, 32, 1, 0), (40, 16, 2, 1)])
-def test_ppo_minibatch_vs_oracle(oracle, B, S, L, act):
-    rng = np.random.default_rng(2000 + B + S)
-    cfg, ocfg = ppo_cfgs(oracle, B, S=S, L=L, act=act)
+# (B, S, layers, activation, actions): B = 6 and 40 leave a partial 16-row tile in the last-row
+# kernels; act 1 (ReLU) takes their ReLU branch at the C4 width (d 128, F 512); 8 actions make the
+# heads' per-wave gradient rows (d (A + 1) + A + 1 = 1161 floats) too wide for the fused heads
+# kernel, so the loss kernel and the head products run instead.
+@pytest.mark.parametrize("B,S,L,act,A", [(6, 5, 2, 0, 3), (64, 32, 2, 0, 3), (16, 32, 1, 0, 3), (40, 16, 2, 1, 3),
+                                         (40, 16, 2, 0, 8)])
+def test_ppo_minibatch_vs_oracle(oracle, B, S, L, act, A):
+    rng = np.random.default_rng(2000 + B + S + A)
+    cfg, ocfg = ppo_cfgs(oracle, B, S=S, L=L, act=act, A=A)
     p = f32(ppo_params(rng, ocfg))
     states, actions, adv, ret, old = ppo_inputs(rng, ocfg, p, oracle)
     loss_r, logits_r, values_r, dp_r = oracle.ppo_fwd_bwd(ocfg, p, states, actions, adv, ret, old)
