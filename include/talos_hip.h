@@ -155,6 +155,18 @@ int talos_attn_bwd_f32(int batch, int seq, int heads, int qk_dim, int v_dim, flo
                        const float* o, int ld_o, const float* lse, const float* dout, int ld_do,
                        float* dq, int ld_dq, float* dk, int ld_dk, float* dv, int ld_dv, talos_stream_t stream);
 
+/* Same contract and results as talos_attn_bwd_f32, allocating nothing. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). For seq > 32 the backward keeps
+ * D = rowsum(dO * O) of each (batch, head, query) row in a static device array of 2^20 rows (4 MiB,
+ * which each GPU the library runs on holds until the process ends); batch * heads * seq above 2^20
+ * is TALOS_ERR_UNSUPPORTED. Every call on one GPU shares that array: calls that overlap on one GPU
+ * (on other streams or threads) race. */
+int talos_attn_bwd_noalloc_f32(int batch, int seq, int heads, int qk_dim, int v_dim, float scale, int causal,
+                               const float* q, int ld_q, const float* k, int ld_k, const float* v, int ld_v,
+                               const float* o, int ld_o, const float* lse, const float* dout, int ld_do, float* dq,
+                               int ld_dq, float* dk, int ld_dk, float* dv, int ld_dv, talos_stream_t stream);
+
 /* Element-wise ops of the tape (autograd.rs:356-792, 1606-1862). */
 enum talos_unary_op {
   TALOS_RELU = 0, TALOS_LOG = 1, TALOS_EXP = 2, TALOS_SIN = 3, TALOS_COS = 4, TALOS_SQRT = 5,

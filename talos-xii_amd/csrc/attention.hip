@@ -21,6 +21,8 @@
 // normalised P . V) and saves lse = max + log(sum); the backward recomputes P = exp(s - lse)
 // and uses D_q = dO_q . O_q. Causal masking (key <= query) and the sequence end are applied to
 // the scores, so masked probabilities are exactly 0; key blocks past the diagonal are skipped.
+#include <mutex>
+
 #include "attention.hpp"
 
 namespace talos {
@@ -766,6 +768,10 @@ static int attn_bwd_fused(const AttnArgs& a, int dkm, int dvm, hipStream_t s) {
   ATTN_ALL(attn_bwd_fused_kernel)
 }
 
+bool attn_bwd_uses_workspace(const AttnDesc& d) {
+  return (long long)d.batch * d.heads * d.seq > 0 && d.seq > 32;
+}
+
 int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
   int dkm, dvm;
   if (!pick_dims(d.dk, d.dv, &dkm, &dvm)) {
@@ -996,6 +1002,59 @@ static int check_attn(const char* fn, int batch, int seq, int heads, int qk_dim,
   return TALOS_OK;
 }
 
+// Validates the arguments of the attention backward entry points and fills the descriptor.
+static int attn_bwd_desc(const char* fn, int batch, int seq, int heads, int qk_dim, int v_dim, float scale, int causal,
+                         const float* q, int ld_q, const float* k, int ld_k, const float* v, int ld_v, const float* o,
+                         int ld_o, const float* lse, const float* dout, int ld_do, float* dq, int ld_dq, float* dk,
+                         int ld_dk, float* dv, int ld_dv, AttnDesc* out) {
+  TALOS_NONNULL(q);
+  TALOS_NONNULL(k);
+  TALOS_NONNULL(v);
+  TALOS_NONNULL(o);
+  TALOS_NONNULL(lse);
+  TALOS_NONNULL(dout);
+  TALOS_NONNULL(dq);
+  TALOS_NONNULL(dk);
+  TALOS_NONNULL(dv);
+  int rc = check_attn(fn, batch, seq, heads, qk_dim, v_dim, causal, ld_q, ld_k, ld_v, ld_o);
+  if (rc) return rc;
+  TALOS_REQUIRE(ld_do >= heads * v_dim && ld_dq >= heads * qk_dim && ld_dk >= heads * qk_dim && ld_dv >= heads * v_dim,
+                TALOS_ERR_SHAPE, "%s: a gradient row stride is smaller than heads * dim", fn);
+  AttnDesc& d = *out;
+  d.batch = batch; d.seq = seq; d.heads = heads; d.dk = qk_dim; d.dv = v_dim; d.scale = scale; d.causal = causal;
+  d.q = q; d.ldq = ld_q; d.k = k; d.ldk = ld_k; d.v = v; d.ldv = ld_v;
+  d.o = const_cast<float*>(o); d.ldo = ld_o; d.lse = const_cast<float*>(lse);
+  d.dout = dout; d.lddo = ld_do; d.dq = dq; d.lddq = ld_dq; d.dk_out = dk; d.lddk = ld_dk; d.dv_out = dv; d.lddv = ld_dv;
+  return TALOS_OK;
+}
+
+// The static scratch of talos_attn_bwd_noalloc_f32: D = rowsum(dO * O) of every (batch, head,
+// query) row, written by attn_bwd_dq_kernel and read by attn_bwd_dkv_kernel of the same call (so
+// nothing in it needs clearing). Each GPU holds its own copy for the life of the process; its
+// device address is looked up once per device (hipGetSymbolAddress) and kept, and only that
+// address is ever handed to a kernel. Calls that overlap on one GPU share the array and race.
+constexpr size_t kAttnScratchRows = size_t(1) << 20;  // 4 MiB
+static __device__ __align__(256) float scratch[kAttnScratchRows];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_ptr[kMaxDevices] = {};
+
+static int attn_scratch(float** out) {
+  int dev = 0;
+  TALOS_HIP(hipGetDevice(&dev));
+  TALOS_REQUIRE(dev >= 0 && dev < kMaxDevices, TALOS_ERR_UNSUPPORTED, "attention scratch: device %d >= %d", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    TALOS_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    TALOS_REQUIRE(ptr != nullptr, TALOS_ERR_HIP, "attention scratch: hipGetSymbolAddress gave no address");
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return TALOS_OK;
+}
+
 }  // namespace talos
 
 using namespace talos;
@@ -1023,32 +1082,37 @@ int talos_attn_bwd_f32(int batch, int seq, int heads, int qk_dim, int v_dim, flo
                        int ld_q, const float* k, int ld_k, const float* v, int ld_v, const float* o, int ld_o,
                        const float* lse, const float* dout, int ld_do, float* dq, int ld_dq, float* dk, int ld_dk,
                        float* dv, int ld_dv, talos_stream_t stream) {
-  TALOS_NONNULL(q);
-  TALOS_NONNULL(k);
-  TALOS_NONNULL(v);
-  TALOS_NONNULL(o);
-  TALOS_NONNULL(lse);
-  TALOS_NONNULL(dout);
-  TALOS_NONNULL(dq);
-  TALOS_NONNULL(dk);
-  TALOS_NONNULL(dv);
-  int rc = check_attn(__func__, batch, seq, heads, qk_dim, v_dim, causal, ld_q, ld_k, ld_v, ld_o);
-  if (rc) return rc;
-  TALOS_REQUIRE(ld_do >= heads * v_dim && ld_dq >= heads * qk_dim && ld_dk >= heads * qk_dim && ld_dv >= heads * v_dim,
-                TALOS_ERR_SHAPE, "%s: a gradient row stride is smaller than heads * dim", __func__);
-  TALOS_DEVICE();
   AttnDesc d;
-  d.batch = batch; d.seq = seq; d.heads = heads; d.dk = qk_dim; d.dv = v_dim; d.scale = scale; d.causal = causal;
-  d.q = q; d.ldq = ld_q; d.k = k; d.ldk = ld_k; d.v = v; d.ldv = ld_v;
-  d.o = const_cast<float*>(o); d.ldo = ld_o; d.lse = const_cast<float*>(lse);
-  d.dout = dout; d.lddo = ld_do; d.dq = dq; d.lddq = ld_dq; d.dk_out = dk; d.lddk = ld_dk; d.dv_out = dv; d.lddv = ld_dv;
+  int rc = attn_bwd_desc(__func__, batch, seq, heads, qk_dim, v_dim, scale, causal, q, ld_q, k, ld_k, v, ld_v, o, ld_o,
+                         lse, dout, ld_do, dq, ld_dq, dk, ld_dk, dv, ld_dv, &d);
+  if (rc) return rc;
+  TALOS_DEVICE();
   hipStream_t s = as_stream(stream);
   float* ws = nullptr;
-  const size_t bytes = attn_bwd_workspace_bytes(d);
+  const size_t bytes = attn_bwd_uses_workspace(d) ? attn_bwd_workspace_bytes(d) : 0;
   if (bytes) TALOS_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, s));
   rc = attn_bwd_launch(d, ws, s);
   if (ws) TALOS_HIP(hipFreeAsync(ws, s));
   return rc;
+}
+
+int talos_attn_bwd_noalloc_f32(int batch, int seq, int heads, int qk_dim, int v_dim, float scale, int causal,
+                               const float* q, int ld_q, const float* k, int ld_k, const float* v, int ld_v,
+                               const float* o, int ld_o, const float* lse, const float* dout, int ld_do, float* dq,
+                               int ld_dq, float* dk, int ld_dk, float* dv, int ld_dv, talos_stream_t stream) {
+  AttnDesc d;
+  int rc = attn_bwd_desc(__func__, batch, seq, heads, qk_dim, v_dim, scale, causal, q, ld_q, k, ld_k, v, ld_v, o, ld_o,
+                         lse, dout, ld_do, dq, ld_dq, dk, ld_dk, dv, ld_dv, &d);
+  if (rc) return rc;
+  const size_t rows = (size_t)batch * heads * seq;
+  TALOS_REQUIRE(rows <= kAttnScratchRows, TALOS_ERR_UNSUPPORTED,
+                "%s: batch * heads * seq = %zu exceeds the %zu (batch, head, query) rows of the static scratch", __func__,
+                rows, kAttnScratchRows);
+  TALOS_DEVICE();
+  float* ws = nullptr;
+  if (attn_bwd_uses_workspace(d))
+    if ((rc = attn_scratch(&ws))) return rc;
+  return attn_bwd_launch(d, ws, as_stream(stream));
 }
 
 }  // extern "C"

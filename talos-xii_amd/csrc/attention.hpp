@@ -57,6 +57,9 @@ int attn_fwd_lastq_launch(const AttnDesc& d, float* o_last, long long ldol, floa
 int attn_bwd_lastq_launch(const AttnDesc& d, const float* o_last, long long ldol, const float* lse_last,
                           const float* do_last, long long lddol, hipStream_t s);
 size_t attn_bwd_workspace_bytes(const AttnDesc& d);
+// Whether attn_bwd_launch reads its workspace: the split dQ / dK-dV kernels of seq > 32 keep
+// D = rowsum(dO * O) there; the single-block kernel of seq <= 32 forms D in registers.
+bool attn_bwd_uses_workspace(const AttnDesc& d);
 int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s);
 
 }  // namespace talos

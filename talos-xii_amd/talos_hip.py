@@ -111,6 +111,8 @@ _SIGS = {
     "talos_attn_fwd_f32": [_i, _i, _i, _i, _i, _f, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _vp],
     "talos_attn_bwd_f32": [_i, _i, _i, _i, _i, _f, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _vp, _i, _vp, _i,
                            _vp, _i, _vp, _i, _vp],
+    "talos_attn_bwd_noalloc_f32": [_i, _i, _i, _i, _i, _f, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _vp, _i, _vp,
+                                   _i, _vp, _i, _vp, _i, _vp],
     "talos_unary_fwd_f32": [_i, _sz, _f, _f, _vp, _vp, _vp],
     "talos_unary_bwd_f32": [_i, _sz, _f, _f, _vp, _vp, _vp, _vp],
     "talos_binary_fwd_f32": [_i, _sz, _vp, _vp, _vp, _vp],
