@@ -30,6 +30,7 @@ import workload as wl  # noqa: E402
 METRIC = "PPO policy fwd+bwd samples/sec (d128 block, 1 GPU); % MFMA/HBM roofline"
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_MFMA_TFLOPS = 2516.6
 
 
 def ppo_cfg(B, S):
@@ -61,15 +62,24 @@ def aggregate(records):
     return agg
 
 
-def roofline_of(name, n, flops, bytes_, ms):
+def roofline_of(name, n, flops, bytes_, ms, peak_tflops=None):
+    """The roofline of a kernel symbol from its launches: matrix-core bound when its arithmetic
+    intensity (algorithmic flops per algorithmic HBM byte) is above the ridge point of the MFMA
+    peak it runs on (fp32 157.3 TFLOP/s, or bf16 2.5 PFLOP/s for the bf16-in GEMMs), HBM-bound
+    below it. achieved = algorithmic work per launch / average launch time."""
     avg_ms = ms / n
-    if name.startswith("gemm_f32_kernel"):
+    if peak_tflops is None:
+        peak_tflops = PEAK_BF16_MFMA_TFLOPS if name.endswith("true>") and name.startswith("gemm_f32_kernel") \
+            else PEAK_FP32_MFMA_TFLOPS
+    ridge = peak_tflops * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if flops > 0 and (bytes_ <= 0 or flops / bytes_ >= ridge):
         achieved = flops / n / (avg_ms * 1e-3) / 1e12
-        return {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4)}
+        return {"bound": "mfma", "achieved": round(achieved, 3), "peak": peak_tflops, "unit": "TFLOP/s",
+                "frac": round(achieved / peak_tflops, 4), "intensity_flop_per_byte": round(flops / max(bytes_, 1), 2)}
     achieved = bytes_ / n / (avg_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4)}
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "intensity_flop_per_byte": round(flops / max(bytes_, 1), 2)}
 
 
 def traffic_of(kernel):
@@ -91,7 +101,7 @@ def cpu_baseline(cfg_t, seconds_budget=20.0):
     import pyoracle
     if not os.path.exists(pyoracle.LIB_PATH):
         pyoracle.build()
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
     pyoracle.set_threads(threads)
 
     def run(n, per_sample):
@@ -118,7 +128,39 @@ def cpu_baseline(cfg_t, seconds_budget=20.0):
                       f"sample with the backbone run for actor and critic as src/ppo.rs:691-757 does; C++ "
                       f"restatement of the Rust autograd on {threads} threads",
             "batched_value": round(n_b / t_b, 2),
-            "batched_sample": f"{n_b} samples as one batched f64 graph"}
+            "batched_sample": f"{n_b} samples as one batched f64 graph", "host": host_info()}
+
+
+def host_info():
+    """The host the CPU baseline ran on: CPU model, logical CPUs the OS reports, and the CPUs this
+    process may run on."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+
+
+def device_line():
+    """Device 0 as the runtime reports it, with the product name rocm-smi gives when it is there."""
+    info = th.device_info()
+    out = {"name": info["name"], "cu_count": info["cu_count"], "clock_mhz": info["clock_khz"] // 1000,
+           "memory_gib": round(info["total_mem"] / 2 ** 30, 1)}
+    try:
+        import subprocess
+        r = subprocess.run(["rocm-smi", "--showproductname"], capture_output=True, text=True, timeout=20)
+        for line in r.stdout.splitlines():
+            if "Card Series" in line or "Card series" in line:
+                out["product"] = line.split(":")[-1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return out
 
 
 def optimizer_line(P, dP, steps):
@@ -246,6 +288,194 @@ def rollout_line(steps, n_envs=4096, context_len=16, cpu=True):
     return res
 
 
+def dominant_roofline(plan, step, steps):
+    """One profiled step for the per-kernel table, then `steps` steps with the launches of the
+    kernel symbol that took the most time bracketed by HIP events on their stream: its roofline."""
+    plan.profile(True)
+    step()
+    th.sync()
+    agg = aggregate(plan.profile_records())
+    plan.profile(False)
+    dominant = max(agg, key=lambda k: agg[k][3])
+    plan.profile(True, dominant)
+    for _ in range(steps):
+        step()
+    th.sync()
+    n, fl, by, ms = aggregate(plan.profile_records())[dominant]
+    plan.profile(False)
+    roof = roofline_of(dominant, n, fl, by, ms)
+    roof.update({"kernel": dominant, "launches_per_step": n // steps, "avg_launch_us": round(ms / n * 1e3, 2),
+                 "traffic": traffic_of(dominant), "algorithmic_per_launch": {"flops": fl / n, "bytes": by / n}})
+    total = sum(a[3] for a in agg.values())
+    kernels = {k: {"launches": v[0], "ms": round(v[3], 4), "pct": round(100 * v[3] / total, 1)}
+               for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3])}
+    return roof, kernels
+
+
+def timed(step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    th.sync()
+    timer = th.Timer(None)
+    timer.start()
+    for _ in range(steps):
+        step()
+    return timer.stop_ms() / steps
+
+
+def c3_line(steps, warmup):
+    """C3: one pre-norm block forward + backward at batch 512, seq 64, d_model 128, 4 heads x 32,
+    RoPE, causal attention, 4x GELU MLP, loss = sum(out * G): talos_block_fwd_bwd_f32 on
+    device-resident inputs. Work: the forward's four d x d products and two MLP products over the
+    32768 tokens plus causal attention, the backward twice that (3 x 13.43 = 40.3 GFLOP)."""
+    B, S, d, H, F = 512, 64, 128, 4, 512
+    cfg = th.BlockCfg(B, S, d, H, d // H, F, 1, th.ACT_GELU, 1e-6, 10000.0)
+    rng = np.random.default_rng(3)
+    p = wl.block_params(rng, d, F, gain_jitter=True).astype(np.float32)
+    plan = th.Plan("block", cfg)
+    P = th.DeviceArray.from_numpy(p)
+    X = th.DeviceArray.from_numpy(rng.normal(size=(B, S, d)).astype(np.float32))
+    G = th.DeviceArray.from_numpy(rng.normal(size=(B, S, d)).astype(np.float32))
+    out, dP, dX = th.DeviceArray.zeros((B, S, d)), th.DeviceArray.zeros(p.size), th.DeviceArray.zeros((B, S, d))
+
+    def step():
+        th.call("talos_block_fwd_bwd_f32", plan.h, P.ptr, X.ptr, G.ptr, out.ptr, dP.ptr, dX.ptr, None)
+
+    ms = timed(step, steps, warmup)
+    roof, kernels = dominant_roofline(plan, step, steps)
+    M, hd = B * S, d // H
+    flops = 3.0 * (4 * 2 * M * d * d + 2 * 2 * M * d * F + 2 * 2 * B * H * hd * S * (S + 1) / 2)
+    plan.destroy()
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"metric": "C3 pre-norm block fwd+bwd ms/step (B512 S64 d128, 1 GPU); % fp32 MFMA roofline",
+            "value": round(ms, 4), "unit": "ms", "higher_is_better": False, "steps": steps, "warmup": warmup,
+            "dtype": "fp32", "data": "synthetic",
+            "config": {"workload": "C3: one pre-norm transformer block fwd+bwd, batch 512 x seq 64, d_model 128, "
+                                   "4 heads x 32, RoPE, causal attention, 4x GELU MLP, loss sum(out * G)"},
+            "step": {"algorithmic_gflop": round(flops / 1e9, 2), "tflops": round(tf, 2),
+                     "frac_fp32_mfma_peak": round(tf / PEAK_FP32_MFMA_TFLOPS, 4), "target_ms": 0.51},
+            "roofline": roof, "kernels": kernels, "device": device_line()}
+
+
+def c5_line(steps, warmup, precision):
+    """C5: the MLA block forward + backward at batch 64, seq 256, d_model 512, 8 heads, KV latent
+    128, decoupled RoPE 32, head and value dims 64 (talos_mla_fwd_bwd_f32), fp32 or with the
+    bf16-in / fp32-accumulate GEMMs. Work: the seven projections over 16384 tokens (32.21 GFLOP)
+    and full attention over 256 x 256 pairs per head with q/k width 96 and v width 64 (10.74
+    GFLOP), the backward twice that."""
+    ci = [64, 256, 512, 8, 128, 32, 64, 64, 0]
+    B, S, d, H, L, r, hd, vd, causal = ci
+    cfg = th.MlaCfg(B, S, d, H, L, r, hd, vd, causal, precision, 1e-5, 10000.0)
+    rng = np.random.default_rng(5)
+    p = wl.mla_params(rng, ci).astype(np.float32)
+    plan = th.Plan("mla", cfg)
+    P = th.DeviceArray.from_numpy(p)
+    X = th.DeviceArray.from_numpy(rng.normal(size=(B, S, d)).astype(np.float32))
+    G = th.DeviceArray.from_numpy(rng.normal(size=(B, S, d)).astype(np.float32))
+    out, dP, dX = th.DeviceArray.zeros((B, S, d)), th.DeviceArray.zeros(p.size), th.DeviceArray.zeros((B, S, d))
+
+    def step():
+        th.call("talos_mla_fwd_bwd_f32", plan.h, P.ptr, X.ptr, G.ptr, out.ptr, dP.ptr, dX.ptr, None)
+
+    ms = timed(step, steps, warmup)
+    roof, kernels = dominant_roofline(plan, step, steps)
+    M = B * S
+    gemm = 2.0 * M * (d * L + L * H * hd + L * H * vd + d * H * hd + 2 * d * H * r + H * vd * d)
+    attn = 2.0 * B * H * S * S * ((hd + r) + vd)
+    flops = 3.0 * (gemm + attn)
+    plan.destroy()
+    tf = flops / (ms * 1e-3) / 1e12
+    bf = precision == th.PREC_BF16
+    peak = PEAK_BF16_MFMA_TFLOPS if bf else PEAK_FP32_MFMA_TFLOPS
+    return {"metric": f"C5 MLA block fwd+bwd ms/step (B64 S256 d512, {'bf16-in/fp32-acc' if bf else 'fp32'}, 1 GPU)",
+            "value": round(ms, 4), "unit": "ms", "higher_is_better": False, "steps": steps, "warmup": warmup,
+            "dtype": "bf16-in/fp32-acc" if bf else "fp32", "data": "synthetic",
+            "config": {"workload": "C5: MLA attention block fwd+bwd, batch 64 x seq 256, d_model 512, 8 heads, "
+                                   "KV latent 128, decoupled RoPE 32, head / value dims 64, RMSNorm, no mask"},
+            "step": {"algorithmic_gflop": round(flops / 1e9, 2), "tflops": round(tf, 2),
+                     "frac_mfma_peak": round(tf / peak, 4), "mfma_peak_tflops": peak},
+            "roofline": roof, "kernels": kernels, "device": device_line()}
+
+
+def c2_line(steps):
+    """C2: the standalone row-op backward kernels on [4096, 256] fp32 rows: RMSNorm backward (eps
+    1e-6, gain U(0.9,1.1), with the gain gradient), causal softmax backward (row r is query r mod
+    256), and RoPE backward on [64 sequences x 64 positions, 4 heads, 64] (base 1e4). Each runs on
+    rotating buffer sets of more than 300 MB in all, so the 256 MB Infinity Cache cannot hold the
+    operands between launches; the time per launch is the HIP-event time of `steps` back-to-back
+    launches over the sets, divided by `steps`. A caller-owned workspace is bound, so no launch
+    allocates. Algorithmic bytes per launch: RMSNorm x, dy read and dx written (3 x 4 MiB) plus
+    rstd and the gain read and its gradient written; softmax y and dy read on the kept (unmasked)
+    entries only and dx written densely; RoPE dy read and dx written plus the cos / sin table."""
+    R, C = 4096, 256
+    rng = np.random.default_rng(2)
+    ws = th.DeviceArray.zeros(1 << 20)
+    th.call("talos_workspace_bind", ws.ptr, 4 << 20)
+    res = {}
+    timer = th.Timer(None)
+
+    def measure(name, nbytes, sets, launch):
+        for i in range(len(sets)):
+            launch(sets[i])
+        th.sync()
+        timer.start()
+        for i in range(steps):
+            launch(sets[i % len(sets)])
+        us = timer.stop_ms() / steps * 1e3
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"us_per_launch": round(us, 3), "algorithmic_bytes": int(nbytes), "GB/s": round(gbs, 1),
+                     "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4), "buffer_sets": len(sets),
+                     "rotated_mb": round(len(sets) * sum(a.nbytes for a in sets[0]) / 1e6, 1)}
+
+    try:
+        # RMSNorm backward
+        x = rng.normal(size=(R, C)).astype(np.float32)
+        w = rng.uniform(0.9, 1.1, C).astype(np.float32)
+        rstd = (1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(1) + 1e-6)).astype(np.float32)
+        sets = []
+        for _ in range(25):
+            sets.append([th.DeviceArray.from_numpy(x), th.DeviceArray.from_numpy(rng.normal(size=(R, C))),
+                         th.DeviceArray.zeros((R, C)), th.DeviceArray.from_numpy(rstd), th.DeviceArray.from_numpy(w),
+                         th.DeviceArray.zeros(C)])
+        measure("rmsnorm_bwd", 3 * R * C * 4 + R * 4 + 2 * C * 4, sets,
+                lambda b: th.call("talos_rmsnorm_bwd_f32", R, C, b[0].ptr, b[4].ptr, b[3].ptr, b[1].ptr, 0.0, b[2].ptr,
+                                  0.0, b[5].ptr, None))
+        for b in sets:
+            for a in b:
+                a.free()
+        # causal softmax backward
+        sm = np.exp(rng.normal(size=(R, C)))
+        q = np.arange(R) % C
+        sm[np.arange(C)[None, :] > q[:, None]] = 0.0
+        sm = (sm / sm.sum(1, keepdims=True)).astype(np.float32)
+        sets = [[th.DeviceArray.from_numpy(sm), th.DeviceArray.from_numpy(rng.normal(size=(R, C))),
+                 th.DeviceArray.zeros((R, C))] for _ in range(25)]
+        kept = int(np.sum(q + 1))
+        measure("softmax_causal_bwd", 2 * kept * 4 + R * C * 4, sets,
+                lambda b: th.call("talos_softmax_bwd_f32", R, C, 1, b[0].ptr, b[1].ptr, 0.0, b[2].ptr, None))
+        for b in sets:
+            for a in b:
+                a.free()
+        # RoPE backward on [64, 64, 4, 64]
+        sets = [[th.DeviceArray.from_numpy(rng.normal(size=(64, 64, 4, 64))), th.DeviceArray.zeros((64, 64, 4, 64))]
+                for _ in range(37)]
+        measure("rope_bwd", 2 * R * C * 4 + 2 * 64 * 32 * 4, sets,
+                lambda b: th.call("talos_rope_bwd_f32", 64, 64, 4, 64, 0, 10000.0, b[0].ptr, 0.0, b[1].ptr, None))
+        for b in sets:
+            for a in b:
+                a.free()
+    finally:
+        th.call("talos_workspace_bind", None, 0)
+        ws.free()
+    return {"metric": "C2 row-op backward HBM GB/s ([4096,256] RMSNorm / causal softmax, RoPE [4096,4,64]; 1 GPU)",
+            "value": res, "unit": "GB/s", "higher_is_better": True, "steps": steps, "dtype": "fp32",
+            "data": "synthetic",
+            "config": {"workload": "C2: standalone RMSNorm backward (eps 1e-6, gain U(0.9,1.1)) and causal softmax "
+                                   "backward on [4096,256], RoPE backward on [4096 = 64 x 64 positions, 4, 64]"},
+            "target_us": {"rmsnorm_bwd": 2.62, "softmax_causal_bwd": 1.75, "rope_bwd": 1.75},
+            "device": device_line()}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -262,6 +492,9 @@ def main():
     ap.add_argument("--rollout-only", action="store_true",
                     help="only the rollout line (its JSON object alone): the command to run under rocprofv3 for "
                          "the rollout kernel's averages")
+    ap.add_argument("--config", default="C4", choices=["C4", "C2", "C3", "C5", "all"],
+                    help="C4 (default): the headline PPO minibatch line; C2 / C3 / C5: the line of that "
+                         "configuration instead (C5 prints fp32 and bf16 lines); all: every line, C4 first")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB device-to-device 5 times: the known-size "
                          "copy that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -275,7 +508,20 @@ def main():
     if args.rollout_only:
         print(json.dumps({"rollout": rollout_line(args.steps, cpu=False)}))
         return
+    if args.config in ("C4", "all"):
+        main_c4(args, rank)
+    if args.config in ("C2", "all"):
+        print(json.dumps(c2_line(max(args.steps, 200))), flush=True)
+    if args.config in ("C3", "all"):
+        print(json.dumps(c3_line(args.steps, args.warmup)), flush=True)
+    if args.config in ("C5", "all"):
+        for prec in (th.PREC_FP32, th.PREC_BF16):
+            print(json.dumps(c5_line(args.steps, args.warmup, prec)), flush=True)
 
+
+def main_c4(args, rank):
+    """The headline line: the C4 PPO minibatch (and, unless --headline-only, the optimizer,
+    reference-model and rollout side lines)."""
     cfg_t = ppo_cfg(args.batch, args.seq)
     cfg, p, states, actions, adv, ret = make_inputs(cfg_t)
     B = cfg.batch
@@ -338,7 +584,6 @@ def main():
     shape = (B, cfg.seq, cfg.in_dim, cfg.d_model, cfg.n_layers, cfg.n_heads, cfg.ffn_dim, cfg.n_actions)
     step_flops = wl.ppo_step_flops(*shape)
     graph_flops = wl.ppo_step_flops(*shape, live=False)
-    info = th.device_info()
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
@@ -355,7 +600,7 @@ def main():
                  "wall_ms_per_step": round(wall * 1e3 / args.steps, 4)},
         "kernels": {k: {"launches": v[0], "ms": round(v[3], 4), "pct": round(100 * v[3] / sum(a[3] for a in agg.values()), 1)}
                     for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3])},
-        "device": info["name"],
+        "device": device_line(),
     }
     if not args.headline_only:
         out["optimizer"] = optimizer_line(P, dP, args.steps)

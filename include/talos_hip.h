@@ -73,6 +73,19 @@ int talos_event_create(void** ev);
 int talos_event_destroy(void* ev);
 int talos_event_record(void* ev, talos_stream_t stream);
 int talos_event_elapsed_ms(void* start, void* stop, float* ms);
+/* Caller-owned scratch for the kernel-level entry points called from this thread: the split-K
+ * partials of the GEMMs, the D rows of talos_attn_bwd_f32 and the f64 partial sums of the
+ * reductions (talos_bias_grad_f32, talos_rmsnorm_bwd_f32, talos_reduce_sum_f32,
+ * talos_grad_sumsq_f32 with a NULL workspace). A call whose scratch fits the bound buffer uses it
+ * and allocates nothing; a GEMM whose split-K partials would not fit splits K fewer times (down to
+ * no split) instead; any other call that needs more allocates and frees on its stream
+ * (hipMallocAsync / hipFreeAsync), as every call does when nothing is bound. ptr must be device
+ * memory, 256-byte aligned; NULL, 0 unbinds. The library never frees it, and calls that share one
+ * binding must not overlap on the device (issue them on one stream). The reference has no
+ * counterpart (its ops allocate host vectors per call, src/autograd.rs:262-264). */
+int talos_workspace_bind(void* ptr, size_t bytes);
+/* The largest scratch (bytes) a call on this thread asked for since the last bind. */
+size_t talos_workspace_high_water(void);
 /* Name (with gfx arch), compute-unit count, peak clock (kHz) and memory of device 0. */
 int talos_device_info(char* name, size_t name_len, int* cu_count, int* clock_khz, size_t* total_mem);
 

@@ -1088,12 +1088,11 @@ int talos_attn_bwd_f32(int batch, int seq, int heads, int qk_dim, int v_dim, flo
   if (rc) return rc;
   TALOS_DEVICE();
   hipStream_t s = as_stream(stream);
-  float* ws = nullptr;
-  const size_t bytes = attn_bwd_uses_workspace(d) ? attn_bwd_workspace_bytes(d) : 0;
-  if (bytes) TALOS_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, s));
-  rc = attn_bwd_launch(d, ws, s);
-  if (ws) TALOS_HIP(hipFreeAsync(ws, s));
-  return rc;
+  EntryScratch ws;
+  if ((rc = ws.acquire(attn_bwd_uses_workspace(d) ? attn_bwd_workspace_bytes(d) : 0, s))) return rc;
+  rc = attn_bwd_launch(d, static_cast<float*>(ws.ptr), s);
+  const int rel = ws.release();
+  return rc ? rc : rel;
 }
 
 int talos_attn_bwd_noalloc_f32(int batch, int seq, int heads, int qk_dim, int v_dim, float scale, int causal,

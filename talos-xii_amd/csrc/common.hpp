@@ -38,6 +38,22 @@ void profiler_set_current(Profiler* p);  // thread-local; nullptr switches profi
 int prof_begin(hipStream_t s, const char* kernel, double flops, double bytes);
 void prof_end(hipStream_t s, int idx);
 
+// Scratch of a kernel-level entry point: the workspace the caller bound on this thread
+// (talos_workspace_bind) when it holds `bytes`, else a stream-ordered allocation that release()
+// frees on the same stream. acquire(0) takes nothing.
+struct EntryScratch {
+  void* ptr = nullptr;
+  bool owned = false;
+  hipStream_t s = nullptr;
+  int acquire(size_t bytes, hipStream_t stream);
+  int release();
+  ~EntryScratch() { (void)release(); }
+};
+// The bytes of the workspace bound on this thread (0 when none), and a note of a call's need
+// for talos_workspace_high_water.
+size_t bound_workspace_bytes();
+void note_workspace_need(size_t bytes);
+
 struct ProfScope {
   hipStream_t s;
   int idx;

@@ -1380,17 +1380,28 @@ static int check_gemm(const char* fn, int transA, int transB, int M, int N, int 
   return TALOS_OK;
 }
 
+// Split-K partials of a kernel-level product: with a workspace bound on this thread the split
+// count shrinks until the partials fit it (down to no split), so the call allocates nothing;
+// without one the partials are allocated on the stream for the call.
 static int run_gemm(GemmDesc& d, hipStream_t stream) {
-  const size_t ws = gemm_plan_split(d, num_cus());
-  if (ws) {
-    TALOS_HIP(hipMallocAsync(reinterpret_cast<void**>(&d.workspace), ws, stream));
+  size_t ws = gemm_plan_split(d, num_cus());
+  const size_t bound = bound_workspace_bytes();
+  if (ws && bound && ws > bound) {
+    note_workspace_need(ws);
+    const size_t per_split = (size_t)(d.M + (d.dbias ? 1 : 0)) * d.N * d.batch * sizeof(float);
+    d.ksplit = (int)std::max<size_t>(1, bound / per_split);
+    ws = d.ksplit > 1 ? gemm_plan_split(d, num_cus()) : 0;
+    if (ws > bound) {  // the rounding of K to whole chunks can add a split
+      d.ksplit = 1;
+      ws = 0;
+    }
   }
-  int rc = gemm_launch(d, stream);
-  if (ws) {
-    hipError_t e = hipFreeAsync(d.workspace, stream);
-    if (rc == TALOS_OK) rc = hip_status(e, "hipFreeAsync");
-  }
-  return rc;
+  EntryScratch scratch;
+  if (int rc = scratch.acquire(ws, stream)) return rc;
+  d.workspace = static_cast<float*>(scratch.ptr);
+  const int rc = gemm_launch(d, stream);
+  const int rel = scratch.release();
+  return rc ? rc : rel;
 }
 
 }  // namespace talos

@@ -173,11 +173,11 @@ int talos_grad_sumsq_f32(size_t n, const float* grads, int accumulate, double* s
   TALOS_DEVICE();
   hipStream_t s = as_stream(stream);
   if (workspace) return grad_sumsq_launch(n, grads, accumulate, sumsq, workspace, s);
-  double* ws = nullptr;
-  TALOS_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), grad_sumsq_workspace_bytes(), s));
-  const int rc = grad_sumsq_launch(n, grads, accumulate, sumsq, ws, s);
-  TALOS_HIP(hipFreeAsync(ws, s));
-  return rc;
+  EntryScratch ws;
+  if (int rc = ws.acquire(grad_sumsq_workspace_bytes(), s)) return rc;
+  const int rc = grad_sumsq_launch(n, grads, accumulate, sumsq, static_cast<double*>(ws.ptr), s);
+  const int rel = ws.release();
+  return rc ? rc : rel;
 }
 
 int talos_adam_step_f32(size_t n, float* params, const float* grads, float* m, float* v, int t, double lr,

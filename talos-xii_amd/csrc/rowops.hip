@@ -743,12 +743,12 @@ int talos_bias_grad_f32(int rows, int cols, const float* dy, float beta, float* 
   TALOS_REQUIRE(beta == 0.f || beta == 1.f, TALOS_ERR_UNSUPPORTED, "%s: beta must be 0 or 1", __func__);
   TALOS_DEVICE();
   hipStream_t s = as_stream(stream);
-  double* ws = nullptr;
-  const size_t bytes = colsum_workspace_bytes(rows, cols);
-  if (bytes) TALOS_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, s));
-  int rc = colsum_launch(rows, cols, dy, cols, beta, db, ws, s);
-  if (ws) TALOS_HIP(hipFreeAsync(ws, s));
-  return rc;
+  EntryScratch ws;
+  int rc = ws.acquire(colsum_workspace_bytes(rows, cols), s);
+  if (rc) return rc;
+  rc = colsum_launch(rows, cols, dy, cols, beta, db, static_cast<double*>(ws.ptr), s);
+  const int rel = ws.release();
+  return rc ? rc : rel;
 }
 
 int talos_rmsnorm_fwd_f32(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
@@ -774,12 +774,12 @@ int talos_rmsnorm_bwd_f32(int rows, int dim, const float* x, const float* w, con
                 "%s: beta_dx / beta_dw must be 0 or 1", __func__);
   TALOS_DEVICE();
   hipStream_t s = as_stream(stream);
-  double* ws = nullptr;
-  const size_t bytes = dw ? rmsnorm_bwd_workspace_bytes(rows, dim) : 0;
-  if (bytes) TALOS_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, s));
-  int rc = rmsnorm_bwd_launch(rows, dim, x, w, rstd, dy, beta_dx, dx, beta_dw, dw, ws, s);
-  if (ws) TALOS_HIP(hipFreeAsync(ws, s));
-  return rc;
+  EntryScratch ws;
+  int rc = ws.acquire(dw ? rmsnorm_bwd_workspace_bytes(rows, dim) : 0, s);
+  if (rc) return rc;
+  rc = rmsnorm_bwd_launch(rows, dim, x, w, rstd, dy, beta_dx, dx, beta_dw, dw, static_cast<double*>(ws.ptr), s);
+  const int rel = ws.release();
+  return rc ? rc : rel;
 }
 
 int talos_softmax_fwd_f32(int rows, int cols, int causal, const float* x, float* y, talos_stream_t stream) {
@@ -918,16 +918,18 @@ int talos_reduce_sum_f32(size_t n, float scale, const float* x, float* out, talo
   TALOS_DEVICE();
   hipStream_t s = as_stream(stream);
   const int nparts = (int)std::min<size_t>(1024, std::max<size_t>(1, (n + 1023) / 1024));
-  double* ws = nullptr;
-  TALOS_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), nparts * sizeof(double), s));
+  EntryScratch scratch;
+  int rc = scratch.acquire(nparts * sizeof(double), s);
+  if (rc) return rc;
+  double* ws = static_cast<double*>(scratch.ptr);
   hipLaunchKernelGGL(reduce_partial_kernel, dim3(nparts), dim3(256), 0, s, n, x, ws);
-  int rc = launch_status("reduce_partial_kernel");
+  rc = launch_status("reduce_partial_kernel");
   if (rc == TALOS_OK) {
     hipLaunchKernelGGL(reduce_final_kernel, dim3(1), dim3(256), 0, s, nparts, scale, ws, out);
     rc = launch_status("reduce_final_kernel");
   }
-  TALOS_HIP(hipFreeAsync(ws, s));
-  return rc;
+  const int rel = scratch.release();
+  return rc ? rc : rel;
 }
 
 int talos_fill_add_f32(size_t n, float scale, const float* g, float* dx, talos_stream_t stream) {

@@ -38,6 +38,38 @@ int launch_status(const char* kernel) {
   return TALOS_ERR_HIP;
 }
 
+// The caller-owned workspace of the kernel-level entry points on this thread.
+static thread_local void* t_ws = nullptr;
+static thread_local size_t t_ws_bytes = 0;
+static thread_local size_t t_ws_high = 0;
+
+size_t bound_workspace_bytes() { return t_ws ? t_ws_bytes : 0; }
+void note_workspace_need(size_t bytes) {
+  if (bytes > t_ws_high) t_ws_high = bytes;
+}
+
+int EntryScratch::acquire(size_t bytes, hipStream_t stream) {
+  s = stream;
+  if (bytes == 0) return TALOS_OK;
+  note_workspace_need(bytes);
+  if (t_ws && bytes <= t_ws_bytes) {
+    ptr = t_ws;
+    owned = false;
+    return TALOS_OK;
+  }
+  TALOS_HIP(hipMallocAsync(&ptr, bytes, stream));
+  owned = true;
+  return TALOS_OK;
+}
+
+int EntryScratch::release() {
+  if (!owned || !ptr) return TALOS_OK;
+  const hipError_t e = hipFreeAsync(ptr, s);
+  ptr = nullptr;
+  owned = false;
+  return hip_status(e, "hipFreeAsync");
+}
+
 static std::once_flag g_init_once;
 static int g_init_status = TALOS_OK;
 static std::string g_init_error;
@@ -299,11 +331,29 @@ int talos_event_elapsed_ms(void* start, void* stop, float* ms) {
   return TALOS_OK;
 }
 
+int talos_workspace_bind(void* ptr, size_t bytes) {
+  TALOS_REQUIRE(ptr != nullptr || bytes == 0, TALOS_ERR_NULL, "%s: null buffer of %zu bytes", __func__, bytes);
+  TALOS_REQUIRE((reinterpret_cast<uintptr_t>(ptr) & 255) == 0, TALOS_ERR_SHAPE,
+                "%s: the workspace must be 256-byte aligned", __func__);
+  t_ws = bytes ? ptr : nullptr;
+  t_ws_bytes = bytes;
+  t_ws_high = 0;
+  return TALOS_OK;
+}
+
+size_t talos_workspace_high_water(void) { return t_ws_high; }
+
 int talos_device_info(char* name, size_t name_len, int* cu_count, int* clock_khz, size_t* total_mem) {
   TALOS_DEVICE();
   hipDeviceProp_t prop;
   TALOS_HIP(hipGetDeviceProperties(&prop, 0));
-  if (name && name_len) snprintf(name, name_len, "%s (%s)", prop.name, prop.gcnArchName);
+  // some drivers report no marketing name: fall back to the architecture and CU count
+  if (name && name_len) {
+    if (prop.name[0])
+      snprintf(name, name_len, "%s (%s)", prop.name, prop.gcnArchName);
+    else
+      snprintf(name, name_len, "AMD GPU with %d CUs (%s)", prop.multiProcessorCount, prop.gcnArchName);
+  }
   if (cu_count) *cu_count = prop.multiProcessorCount;
   if (clock_khz) *clock_khz = prop.clockRate;
   if (total_mem) *total_mem = prop.totalGlobalMem;

@@ -1,7 +1,8 @@
 """Summarises rocprofv3 output of bench.py runs into the text files kept under profiles/.
 
   python talos-xii_amd/prof_summary.py --stats <kernel_stats.csv> [--fetch <fetch counter_collection.csv>
-      --write <write counter_collection.csv>] --bench-json <bench line> --command "<command>" --out <file.md>
+      --write <write counter_collection.csv>] [--mfma <mfma counter_collection.csv>] --bench-json <bench lines>
+      [--metric <metric prefix>] --title <title> --command "<command>" --out <file.md>
       [--traffic-json profiles/traffic.json]
 
 Kernel-trace stats give each kernel's launch count and average duration. The FETCH_SIZE and
@@ -32,11 +33,13 @@ def short(name):
     return "".join(out)
 
 
-def counters(path, counter):
+def counters(path, counter, scale=1024.0):
+    """Per kernel symbol, the counter's value of each dispatch (FETCH_SIZE / WRITE_SIZE are KiB:
+    scale 1024 gives bytes)."""
     per = collections.defaultdict(list)
     for r in csv.DictReader(open(path)):
         if r["Counter_Name"] == counter:
-            per[short(r["Kernel_Name"])].append(float(r["Counter_Value"]) * 1024.0)  # KiB -> bytes
+            per[short(r["Kernel_Name"])].append(float(r["Counter_Value"]) * scale)
     return per
 
 
@@ -48,31 +51,89 @@ def calibration(per, copy_bytes):
     return copy_bytes / (sum(big) / len(big)), len(big), sum(big) / len(big)
 
 
+def pick_line(path, metric_prefix):
+    """The bench JSON line whose metric starts with metric_prefix (the last line when empty)."""
+    lines = [json.loads(l) for l in open(path).read().strip().splitlines() if l.startswith("{")]
+    for d in lines:
+        if metric_prefix and d.get("metric", "").startswith(metric_prefix):
+            return d
+    return lines[-1]
+
+
+def bench_sentence(bench):
+    if isinstance(bench.get("value"), dict):  # per-kernel lines (C2)
+        parts = [f"`{k}` {v['us_per_launch']} us per launch ({v['GB/s']} GB/s)" for k, v in bench["value"].items()]
+        return "bench line under the profiler: " + "; ".join(parts) + "."
+    s = f"bench line under the profiler: {bench['value']} {bench['unit']}"
+    if "ms_per_step" in bench:
+        s += f", {bench['ms_per_step']} ms/step"
+    roof = bench.get("roofline")
+    if roof:
+        s += (f"; dominant kernel `{roof['kernel']}` bench-measured average {roof['avg_launch_us']} us per launch "
+              f"({roof['achieved']} {roof['unit']}, {100 * roof['frac']:.1f}% of the {roof['bound']} peak)")
+    return s + "."
+
+
+def mfma_table(path, stats, simds):
+    """Per kernel: MFMA busy (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs) and the fp32
+    MFMA flops counted (SQ_INSTS_VALU_MFMA_MOPS_F32 x 512) per launch. GRBM_GUI_ACTIVE is reported
+    summed over the XCDs; the per-XCD cycle count is that sum divided by the XCD count, found as the
+    ratio of the sum to the cycles the kernel's duration holds at the measured clock."""
+    busy, gui, mops = (counters(path, c, scale=1.0) for c in
+                       ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_F32"))
+    dur = {short(r["Name"]): float(r["AverageNs"]) for r in stats}
+    rows = []
+    for k in sorted(busy, key=lambda k: -sum(busy[k])):
+        if k.startswith("__amd") or not gui.get(k):
+            continue
+        g = sum(gui[k]) / len(gui[k])
+        xcds = max(1, round(g / (dur.get(k, 0) * 2.1))) if dur.get(k) else 1  # ~2.1 GHz under load
+        util = sum(busy[k]) / len(busy[k]) / (g / xcds * simds)
+        fl = 512.0 * sum(mops.get(k, [0.0])) / max(1, len(mops.get(k, [])))
+        clock = g / xcds / dur[k] if dur.get(k) else 0.0
+        rows.append((k, len(busy[k]), util, fl, clock))
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--stats", required=True)
     ap.add_argument("--fetch")
     ap.add_argument("--write")
+    ap.add_argument("--mfma", help="counter CSV of a --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F32 "
+                                   "GRBM_GUI_ACTIVE pass")
+    ap.add_argument("--simds", type=int, default=1024)
     ap.add_argument("--bench-json", required=True)
+    ap.add_argument("--metric", default="", help="prefix of the bench line's metric to quote")
+    ap.add_argument("--title", default="C4 PPO minibatch fwd+bwd")
     ap.add_argument("--command", required=True)
     ap.add_argument("--pmc-command", default="")
+    ap.add_argument("--mfma-command", default="")
     ap.add_argument("--out", required=True)
     ap.add_argument("--traffic-json")
     ap.add_argument("--top", type=int, default=16)
     a = ap.parse_args()
 
-    bench = json.loads(open(a.bench_json).read().strip().splitlines()[-1])
+    bench = pick_line(a.bench_json, a.metric)
     stats = list(csv.DictReader(open(a.stats)))
     total_ns = sum(float(r["TotalDurationNs"]) for r in stats)
-    lines = [f"# rocprofv3 kernel summary: {bench['config']['workload'].split(':')[0]} PPO minibatch fwd+bwd", "",
+    lines = [f"# rocprofv3 kernel summary: {a.title}", "",
              "Command (kernel trace + stats):", "", "```", a.command, "```", ""]
-    lines += [f"bench line under the profiler: {bench['value']} samples/s, {bench['ms_per_step']} ms/step; "
-              f"dominant kernel `{bench['roofline']['kernel']}` bench-measured average "
-              f"{bench['roofline']['avg_launch_us']} us per launch.", ""]
+    lines += [bench_sentence(bench), ""]
     lines += ["| kernel | calls | avg us | total % |", "|---|---:|---:|---:|"]
     for r in stats[:a.top]:
         lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
                      f"{100 * float(r['TotalDurationNs']) / total_ns:.2f} |")
+    if a.mfma:
+        rows = mfma_table(a.mfma, stats, a.simds)
+        lines += ["", "Matrix-core counters (rocprofv3 --pmc, one pass):", "", "```", a.mfma_command, "```", "",
+                  f"MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x {a.simds} SIMDs); fp32 MFMA "
+                  "flops = SQ_INSTS_VALU_MFMA_MOPS_F32 x 512 per launch; clock = GRBM_GUI_ACTIVE per XCD / the "
+                  "kernel's average duration from the trace above.", "",
+                  "| kernel | launches | MFMA busy % | fp32 MFMA GFLOP/launch | clock GHz |",
+                  "|---|---:|---:|---:|---:|"]
+        for k, n, util, fl, clock in rows[:a.top]:
+            lines.append(f"| `{k}` | {n} | {100 * util:.1f} | {fl / 1e9:.3f} | {clock:.2f} |")
     traffic = {}
     if a.fetch and a.write:
         copy_bytes = bench.get("copy_calibration_bytes") or (1024 << 20)
@@ -94,7 +155,13 @@ def main():
             t = traffic[k]
             lines.append(f"| `{k}` | {len(f[k])} | {t['fetch_bytes'] / 1e6:.1f} | {t['write_bytes'] / 1e6:.1f} |")
         if a.traffic_json:
-            json.dump(traffic, open(a.traffic_json, "w"), indent=1, sort_keys=True)
+            old = {}
+            try:
+                old = json.load(open(a.traffic_json))
+            except (OSError, ValueError):
+                pass
+            old.update(traffic)
+            json.dump(old, open(a.traffic_json, "w"), indent=1, sort_keys=True)
     open(a.out, "w").write("\n".join(lines) + "\n")
 
 

@@ -45,7 +45,7 @@ def check_close(got, ref, rtol=FP32_RTOL, atol=FP32_ATOL, name="", scale_floor=0
         FLOOR_AUDIT.append({"test": os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0], "tensor": name,
                             "size": int(ref.size), "floor": floor, "plain_atol": atol,
                             "max_abs_ref": float(np.abs(ref).max()), "needs_floor": int(plain.sum()),
-                            "worst_err_over_plain": float(np.max(err / (rtol * np.abs(ref) + atol)))})
+                            "worst_err_over_plain": float(np.max(err / np.maximum(rtol * np.abs(ref) + atol, 1e-300)))})
         atol = floor
     bound = rtol * np.abs(ref) + atol
     bad = err > bound

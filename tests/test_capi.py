@@ -160,3 +160,13 @@ def test_optimizer_argument_errors(L):
     assert L.talos_grad_sumsq_f32(4, p, 0, None, None, None) == th.ERR_NULL
     assert L.talos_grad_sumsq_f32(4, None, 0, p, None, None) == th.ERR_NULL
     assert L.talos_grad_sumsq_workspace_bytes() >= 8
+
+
+def test_workspace_bind_validation():
+    L = th.lib()
+    assert L.talos_workspace_bind(None, 0) == th.OK
+    assert L.talos_workspace_bind(None, 4096) == th.ERR_NULL
+    assert L.talos_workspace_bind(ctypes.c_void_p(4096 + 16), 4096) == th.ERR_SHAPE
+    assert L.talos_workspace_bind(ctypes.c_void_p(4096), 4096) == th.OK
+    assert L.talos_workspace_high_water() == 0
+    assert L.talos_workspace_bind(None, 0) == th.OK

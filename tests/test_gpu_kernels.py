@@ -74,6 +74,44 @@ def test_gemm_split_k_long_reduction():
     assert np.all(err <= 1e-6 * scale + 1e-6), float(np.max(err / scale))
 
 
+def test_bound_workspace_replaces_per_call_allocation():
+    # A caller-owned workspace bound on this thread serves the scratch of the kernel-level entry
+    # points: results equal the unbound calls' (the split-K product within its bound, since a
+    # workspace too small for the library's split count makes it split K fewer times).
+    rng = np.random.default_rng(6)
+    ws_bytes = 1 << 20
+    ws = DA.zeros(ws_bytes // 4)
+    X = rng.normal(size=(65536, 64)).astype(np.float32)
+    G = rng.normal(size=(65536, 64)).astype(np.float32)
+    free = gemm(1, 0, X, G)
+    x, dy = rng.normal(size=(5000, 96)), rng.normal(size=(5000, 96))
+    w, rstd = rng.uniform(0.9, 1.1, 96), 1.0 / np.sqrt((x * x).mean(1) + 1e-6)
+    Xd, Wd, Rd, DYd = (DA.from_numpy(a) for a in (x, w, rstd, dy))
+
+    def norm_bwd():
+        dx, dw = DA.zeros((5000, 96)), DA.zeros(96)
+        th.call("talos_rmsnorm_bwd_f32", 5000, 96, Xd.ptr, Wd.ptr, Rd.ptr, DYd.ptr, 0.0, dx.ptr, 0.0, dw.ptr, None)
+        s = DA.zeros(1)
+        th.call("talos_reduce_sum_f32", 5000 * 96, 1.0, DYd.ptr, s.ptr, None)
+        db = DA.zeros(96)
+        th.call("talos_bias_grad_f32", 5000, 96, DYd.ptr, 0.0, db.ptr, None)
+        return dx.numpy(), dw.numpy(), s.numpy(), db.numpy()
+
+    ref = norm_bwd()
+    th.call("talos_workspace_bind", ws.ptr, ws_bytes)
+    try:
+        bound = gemm(1, 0, X, G)
+        got = norm_bwd()
+        high = th.lib().talos_workspace_high_water()
+    finally:
+        th.call("talos_workspace_bind", None, 0)
+    scale = np.abs(f32(X)).T @ np.abs(f32(G))
+    assert np.all(np.abs(bound - free) <= 2e-6 * scale), "split-K product with the bound workspace"
+    for a, b in zip(got, ref):
+        assert np.array_equal(a, b)
+    assert high > ws_bytes, "the split-K product asked for more than the bound workspace"
+
+
 def test_gemm_batched_qk_pv():
     rng = np.random.default_rng(5)
     Bt, S, D = 6, 33, 20
