@@ -6,6 +6,7 @@
 // stream, so results are observed in program order as with the reference's synchronous ops.
 #include "tape.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <sstream>
 #include <unordered_set>
@@ -39,8 +40,23 @@ void require(bool c, const std::string& msg) {
   if (!c) throw Panic(msg);
 }
 
+// The scratch of the library calls made by this thread's ops (split-K partials, reduction
+// partials, attention rows): one device buffer bound on the thread's first op and kept for the
+// life of the process, so an op never allocates scratch per call (a split-K product splits fewer
+// times rather than outgrow it). Every op runs on the null stream, so calls sharing it never overlap.
+constexpr size_t kTapeWorkspaceBytes = size_t(16) << 20;
+void bind_workspace_once() {
+  thread_local bool bound = false;
+  if (bound) return;
+  void* p = nullptr;
+  ok(talos_malloc(&p, kTapeWorkspaceBytes), "talos_malloc (tape workspace)");
+  ok(talos_workspace_bind(p, kTapeWorkspaceBytes), "talos_workspace_bind");
+  bound = true;
+}
+
 // A new tensor with zeroed grad; data left for the op to fill.
 Tensor fresh(Shape shape) {
+  bind_workspace_once();
   Tensor t;
   const size_t n = prod(shape);
   t.data_ = std::make_shared<Storage>(n);
@@ -181,7 +197,8 @@ Tensor Tensor::matmul(const Tensor& other) const {
   const int k = shape.size() == 1 ? (int)shape[0] : (int)shape[1];
   const int k2 = (int)other.shape[0], n = (int)other.shape[1];
   require(k == k2, "MatMul dimension mismatch");  // src/autograd.rs:209
-  Tensor out = fresh({(size_t)m, (size_t)n});
+  // a rank-1 left operand gives a rank-1 result [n] (src/autograd.rs:254-258)
+  Tensor out = fresh(shape.size() == 1 ? Shape{(size_t)n} : Shape{(size_t)m, (size_t)n});
   ok(talos_gemm_f32(0, 0, m, n, k, 1.f, data_->ptr, k, other.data_->ptr, n, 0.f, out.data_->ptr, n, nullptr),
      "matmul");
   return with_ctx(out, {*this, other}, [m, n, k](const Tensor& o, std::vector<Tensor>& p) {
@@ -354,6 +371,207 @@ Tensor RMSNorm::forward(const Tensor& x) const {
 }
 
 std::vector<Tensor> RMSNorm::parameters() const { return {weight}; }
+
+// ---------------------------------------------------------------------------
+// Attention ops (src/transformer.rs:877-1183)
+// ---------------------------------------------------------------------------
+// S[b] = Q[b] . K[b]^T on [b, seq, dim] buffers (batched_matmul_qt_k, :877-958): the batched GEMM
+// with transB; backward dQ += G . K, dK += G^T . Q (beta 1: grads accumulate, :940-955).
+Tensor batched_matmul_qt_k(const Tensor& q, const Tensor& k, size_t b, size_t seq, size_t dim) {
+  require(q.numel() == b * seq * dim && k.numel() == b * seq * dim, "batched_matmul_qt_k: q / k size mismatch");
+  Tensor out = fresh({b, seq, seq});
+  const int S = (int)seq, D = (int)dim, B = (int)b;
+  const long long sq = (long long)seq * dim, ss = (long long)seq * seq;
+  ok(talos_gemm_batched_f32(0, 1, S, S, D, 1.f, q.data_->ptr, D, sq, k.data_->ptr, D, sq, 0.f, out.data_->ptr, S, ss, B,
+                            nullptr),
+     "batched_matmul_qt_k");
+  return with_ctx(out, {q, k}, [S, D, B, sq, ss](const Tensor& o, std::vector<Tensor>& p) {
+    ok(talos_gemm_batched_f32(0, 0, S, D, S, 1.f, o.grad_->ptr, S, ss, p[1].data_->ptr, D, sq, 1.f, p[0].grad_->ptr, D,
+                              sq, B, nullptr),
+       "batched_matmul_qt_k dQ");
+    ok(talos_gemm_batched_f32(1, 0, S, D, S, 1.f, o.grad_->ptr, S, ss, p[0].data_->ptr, D, sq, 1.f, p[1].grad_->ptr, D,
+                              sq, B, nullptr),
+       "batched_matmul_qt_k dK");
+  });
+}
+
+// O[b] = P[b] . V[b] (batched_matmul_probs_v, :961-1050); backward dP += G . V^T, dV += P^T . G.
+Tensor batched_matmul_probs_v(const Tensor& probs, const Tensor& v, size_t b, size_t seq, size_t dim_v) {
+  require(probs.numel() == b * seq * seq && v.numel() == b * seq * dim_v,
+          "batched_matmul_probs_v: probs / v size mismatch");
+  Tensor out = fresh({b, seq, dim_v});
+  const int S = (int)seq, D = (int)dim_v, B = (int)b;
+  const long long sv = (long long)seq * dim_v, ss = (long long)seq * seq;
+  ok(talos_gemm_batched_f32(0, 0, S, D, S, 1.f, probs.data_->ptr, S, ss, v.data_->ptr, D, sv, 0.f, out.data_->ptr, D,
+                            sv, B, nullptr),
+     "batched_matmul_probs_v");
+  return with_ctx(out, {probs, v}, [S, D, B, sv, ss](const Tensor& o, std::vector<Tensor>& p) {
+    ok(talos_gemm_batched_f32(0, 1, S, S, D, 1.f, o.grad_->ptr, D, sv, p[1].data_->ptr, D, sv, 1.f, p[0].grad_->ptr, S,
+                              ss, B, nullptr),
+       "batched_matmul_probs_v dP");
+    ok(talos_gemm_batched_f32(1, 0, S, D, S, 1.f, p[0].data_->ptr, S, ss, o.grad_->ptr, D, sv, 1.f, p[1].grad_->ptr, D,
+                              sv, B, nullptr),
+       "batched_matmul_probs_v dV");
+  });
+}
+
+Tensor scale_tensor(const Tensor& t, double scale) { return t.scale(scale); }  // :1052-1072
+
+// Row softmax (:1074-1121): the closure reads the forward's output (kept alive with the graph).
+Tensor softmax(const Tensor& t, size_t seq_len, bool causal) {
+  require(seq_len > 0 && t.numel() % seq_len == 0, "softmax: length is not a multiple of seq_len");
+  Tensor out = fresh(t.shape);
+  const int rows = (int)(t.numel() / seq_len), cols = (int)seq_len, c = causal ? 1 : 0;
+  ok(talos_softmax_fwd_f32(rows, cols, c, t.data_->ptr, out.data_->ptr, nullptr), "softmax");
+  std::shared_ptr<Storage> y = out.data_;
+  return with_ctx(out, {t}, [rows, cols, c, y](const Tensor& o, std::vector<Tensor>& p) {
+    ok(talos_softmax_bwd_f32(rows, cols, c, y->ptr, o.grad_->ptr, 1.f, p[0].grad_->ptr, nullptr), "softmax bwd");
+  });
+}
+
+// concat_last_dim (:1123-1183); the backward adds each half of the gradient to its parent.
+Tensor concat_last_dim(const Tensor& a, const Tensor& b) {
+  require(!a.shape.empty() && a.shape.size() == b.shape.size() &&
+              std::equal(a.shape.begin(), a.shape.end() - 1, b.shape.begin()),
+          "concat_last_dim: leading dims differ");
+  const size_t ca = a.shape.back(), cb = b.shape.back(), rows = ca ? a.numel() / ca : b.numel() / cb;
+  Shape ns(a.shape.begin(), a.shape.end() - 1);
+  ns.push_back(ca + cb);
+  Tensor out = fresh(ns);
+  ok(talos_concat_last_f32(rows, (int)ca, (int)cb, a.data_->ptr, b.data_->ptr, out.data_->ptr, nullptr), "concat");
+  return with_ctx(out, {a, b}, [rows, ca, cb](const Tensor& o, std::vector<Tensor>& p) {
+    ok(talos_concat_last_bwd_f32(rows, (int)ca, (int)cb, o.grad_->ptr, p[0].grad_->ptr, p[1].grad_->ptr, nullptr),
+       "concat bwd");
+  });
+}
+
+RoPE::RoPE(size_t d, size_t len) : dim(d), max_len(len) { require(d % 2 == 0, "RoPE dim must be even"); }
+
+// RoPE::forward (:253-337): rows of shape[-1] = dim, the position of a row is start_pos + its index
+// along shape[-2]; the backward rotates by -theta and adds.
+Tensor RoPE::forward(const Tensor& x, size_t start_pos) const {
+  require(x.shape.size() >= 2 && x.shape.back() == dim, "RoPE: the last dimension must equal the RoPE dim");
+  const size_t T = x.shape[x.shape.size() - 2];
+  require(start_pos + T <= max_len, "RoPE: position past the cached table (index out of bounds)");
+  const int n_seq = (int)(T ? x.numel() / (T * dim) : 0), seq = (int)T, D = (int)dim, sp = (int)start_pos;
+  const float b = (float)base;
+  Tensor out = fresh(x.shape);
+  ok(talos_rope_fwd_f32(n_seq, seq, 1, D, sp, b, x.data_->ptr, out.data_->ptr, nullptr), "rope");
+  return with_ctx(out, {x}, [n_seq, seq, D, sp, b](const Tensor& o, std::vector<Tensor>& p) {
+    ok(talos_rope_bwd_f32(n_seq, seq, 1, D, sp, b, o.grad_->ptr, 1.f, p[0].grad_->ptr, nullptr), "rope bwd");
+  });
+}
+
+MLAConfig MLAConfig::deepseek_v2_lite() {  // src/transformer.rs:21-31
+  MLAConfig c;
+  c.dim = 512;
+  c.num_heads = 8;
+  c.q_lora_rank = 0;
+  c.kv_lora_rank = 128;
+  c.qk_rope_dim = 32;
+  c.v_head_dim = 64;
+  c.max_seq_len = 2048;
+  return c;
+}
+
+// MultiHeadLatentAttention::new (:428-464): projections seeded seed .. seed + 6, no biases
+MultiHeadLatentAttention::MultiHeadLatentAttention(const MLAConfig& c, uint64_t seed)
+    : config(c),
+      w_dkv(c.dim, c.kv_lora_rank, false, seed),
+      w_uk(c.kv_lora_rank, c.num_heads * c.v_head_dim, false, seed + 1),
+      w_uv(c.kv_lora_rank, c.num_heads * c.v_head_dim, false, seed + 2),
+      w_q(c.dim, c.num_heads * c.v_head_dim, false, seed + 3),
+      w_kr(c.dim, c.num_heads * c.qk_rope_dim, false, seed + 4),
+      w_qr(c.dim, c.num_heads * c.qk_rope_dim, false, seed + 5),
+      w_o(c.num_heads * c.v_head_dim, c.dim, false, seed + 6),
+      rope(c.qk_rope_dim, c.max_seq_len) {}
+
+std::vector<Tensor> MultiHeadLatentAttention::parameters() const {  // :466-476
+  return {w_dkv.weight, w_uk.weight, w_uv.weight, w_q.weight, w_kr.weight, w_qr.weight, w_o.weight};
+}
+
+// MultiHeadLatentAttention::forward (:478-560), op for op.
+Tensor MultiHeadLatentAttention::forward(const Tensor& x) const {
+  require(x.shape.size() == 3, "MultiHeadLatentAttention expects [batch, seq, dim]");
+  const size_t B = x.shape[0], S = x.shape[1], H = config.num_heads, hd = config.v_head_dim,
+               R = config.qk_rope_dim;
+  const Tensor c_kv = w_dkv.forward(x);
+  const Tensor k_c = w_uk.forward(c_kv), v_c = w_uv.forward(c_kv);
+  const Tensor k_r_flat = w_kr.forward(x);
+  const Tensor q_c = w_q.forward(x), q_r_flat = w_qr.forward(x);
+  // RoPE on [B, S, H, R]: rows are indexed along H, the reference's shape[-2]
+  const Tensor k_r_rot = rope.forward(k_r_flat.reshape({B, S, H, R}), 0);
+  const Tensor q_r_rot = rope.forward(q_r_flat.reshape({B, S, H, R}), 0);
+  const Tensor q = concat_last_dim(q_c.reshape({B, S, H, hd}), q_r_rot);
+  const Tensor k = concat_last_dim(k_c.reshape({B, S, H, hd}), k_r_rot);
+  const Tensor v = v_c.reshape({B, S, H, hd});
+  const size_t bh = B * H, total = hd + R;
+  const Tensor q_flat = q.transpose(1, 2).reshape({bh, S, total});
+  const Tensor k_flat = k.transpose(1, 2).reshape({bh, S, total});
+  const Tensor v_flat = v.transpose(1, 2).reshape({bh, S, hd});
+  const Tensor scores = batched_matmul_qt_k(q_flat, k_flat, bh, S, total);
+  const Tensor probs = softmax(scale_tensor(scores, 1.0 / std::sqrt((double)total)), S);
+  const Tensor att = batched_matmul_probs_v(probs, v_flat, bh, S, hd);
+  const Tensor merged = att.reshape({B, H, S, hd}).transpose(1, 2).reshape({B, S, H * hd});
+  return w_o.forward(merged);
+}
+
+// LuckTransformer::new (:48-69): the MLA's config is fixed by hidden_dim
+static MLAConfig luck_mla_config(size_t hidden) {
+  MLAConfig c;
+  c.dim = hidden;
+  c.num_heads = 4;
+  c.q_lora_rank = 0;
+  c.kv_lora_rank = 32;
+  c.qk_rope_dim = 16;
+  c.v_head_dim = hidden / 4;
+  c.max_seq_len = 256;
+  return c;
+}
+
+LuckTransformer::LuckTransformer(size_t in_dim, size_t hidden, bool, uint64_t seed)
+    : embed(in_dim, hidden, true, seed),
+      norm_1(hidden, 1e-5),
+      mla_layer(luck_mla_config(hidden), seed + 10),
+      norm_2(hidden, 1e-5),
+      ffn_1(hidden, hidden * 2, true, seed + 20),
+      ffn_2(hidden * 2, hidden, true, seed + 30),
+      norm_final(hidden, 1e-5),
+      out_proj(hidden, hidden, true, seed + 40) {}
+
+Tensor LuckTransformer::forward(const Tensor& x) const {  // :71-90
+  const Tensor h = embed.forward(x);
+  const Tensor h2 = h + mla_layer.forward(norm_1.forward(h));
+  const Tensor f2 = ffn_2.forward(ffn_1.forward(norm_2.forward(h2)).relu());
+  const Tensor h3 = h2 + f2;
+  return out_proj.forward(norm_final.forward(h3));
+}
+
+Tensor LuckTransformer::last_token(const Tensor& x, bool differentiable) const {  // :92-109
+  require(x.shape.size() == 3 && x.shape[1] > 0, "last_token expects [batch, seq, dim]");
+  const size_t B = x.shape[0], S = x.shape[1], d = x.shape[2];
+  Tensor out = fresh({B, d});
+  for (size_t b = 0; b < B; ++b)
+    ok(talos_memcpy_d2d(out.data_->ptr + b * d, x.data_->ptr + (b * S + S - 1) * d, d * sizeof(float), nullptr),
+       "last_token");
+  if (!differentiable) return out;
+  return with_ctx(out, {x}, [B, S, d](const Tensor& o, std::vector<Tensor>& p) {
+    for (size_t b = 0; b < B; ++b) {
+      float* row = p[0].grad_->ptr + (b * S + S - 1) * d;
+      ok(talos_binary_fwd_f32(TALOS_ADD, d, row, o.grad_->ptr + b * d, row, nullptr), "last_token bwd");
+    }
+  });
+}
+
+std::vector<Tensor> LuckTransformer::parameters() const {  // :205-215
+  std::vector<Tensor> p;
+  for (const Module* m : std::initializer_list<const Module*>{&embed, &norm_1, &mla_layer, &norm_2, &ffn_1, &ffn_2,
+                                                              &norm_final, &out_proj}) {
+    const auto q = m->parameters();
+    p.insert(p.end(), q.begin(), q.end());
+  }
+  return p;
+}
 
 // ---------------------------------------------------------------------------
 // Adam (src/ppo.rs:482-539; src/dqn.rs:173-246)

@@ -12,6 +12,9 @@
 //   matmul relu log exp sum mean broadcast   same names
 //   broadcast_to_batch sin cos sqrt transpose clip reshape mse_loss
 //   a + b, a - b, a * b, a / b, -a           same operators
+//   MLA's batched_matmul_qt_k / _probs_v,    free functions of the same names
+//   scale_tensor, softmax, concat_last_dim
+//   RoPE, MLAConfig, MultiHeadLatentAttention, LuckTransformer  same names (src/transformer.rs)
 //   Adam::new(params, lr) / step / zero_grad  Adam(params, lr[, max_grad_norm]) / step / zero_grad
 //
 // Semantics kept: grads accumulate (+=) and only zero_grad clears them; backward() seeds every
@@ -130,6 +133,77 @@ struct RMSNorm : Module {
   double eps = 1e-5;
   explicit RMSNorm(size_t dim, double eps = 1e-5);
   Tensor forward(const Tensor& x) const override;
+  std::vector<Tensor> parameters() const override;
+};
+
+// ---------------------------------------------------------------------------------------------
+// Attention ops: the helpers of MultiHeadLatentAttention (src/transformer.rs:877-1183), free
+// functions here since they use no module state
+// ---------------------------------------------------------------------------------------------
+// q, k [b, seq, dim] -> scores [b, seq, seq], s[b,i,j] = q[b,i,:] . k[b,j,:]
+// (batched_matmul_qt_k, :877-958); backward dq += g . k, dk += g^T . q
+Tensor batched_matmul_qt_k(const Tensor& q, const Tensor& k, size_t b, size_t seq, size_t dim);
+// probs [b, seq, seq], v [b, seq, dim_v] -> [b, seq, dim_v] (batched_matmul_probs_v, :961-1050);
+// backward dp += g . v^T, dv += p^T . g. The reference skips |p| < 1e-9 in the forward product;
+// every probability is multiplied here (the difference is below 1e-9 per term)
+Tensor batched_matmul_probs_v(const Tensor& probs, const Tensor& v, size_t b, size_t seq, size_t dim_v);
+// t * scale (scale_tensor, :1052-1072)
+Tensor scale_tensor(const Tensor& t, double scale);
+// softmax over consecutive rows of seq_len with max subtraction (softmax, :1074-1121); the
+// backward reads the saved output. causal = true (extension, no reference counterpart): row r is
+// query r mod seq_len and keys past it get probability 0
+Tensor softmax(const Tensor& t, size_t seq_len, bool causal = false);
+// [.., ca] ++ [.., cb] -> [.., ca + cb] (concat_last_dim, :1123-1183)
+Tensor concat_last_dim(const Tensor& a, const Tensor& b);
+
+// RoPE (src/transformer.rs:219-337): interleaved pairs (2i, 2i+1) of the last dimension rotated by
+// pos * base^(-2i/dim), pos = start_pos + the index along shape[-2]; the cos / sin table is
+// evaluated in f64 for max_len positions (the library rounds it to fp32), and a position at or past
+// max_len panics as the reference's table index does
+struct RoPE {
+  size_t dim = 0, max_len = 0;
+  double base = 10000.0;
+  RoPE(size_t dim, size_t max_len);
+  Tensor forward(const Tensor& x, size_t start_pos) const;
+};
+
+// MLAConfig (src/transformer.rs:9-33)
+struct MLAConfig {
+  size_t dim = 0, num_heads = 0, q_lora_rank = 0, kv_lora_rank = 0, qk_rope_dim = 0, v_head_dim = 0,
+         max_seq_len = 0;
+  static MLAConfig deepseek_v2_lite();  // dim 512, 8 heads, kv latent 128, rope 32, v 64, 2048
+};
+
+// MultiHeadLatentAttention (src/transformer.rs:374-560): the latent down / up projections, the
+// decoupled RoPE parts (rotated by RoPE::forward on [B, S, H, R], so position = head index as in
+// the reference), per-head concatenation, the [B*H, S, hd + R] attention through the ops above with
+// scale 1/sqrt(hd + R), and W_o. No biases. Parameters in the reference's order.
+struct MultiHeadLatentAttention : Module {
+  MLAConfig config;
+  Linear w_dkv, w_uk, w_uv, w_q, w_kr, w_qr, w_o;
+  RoPE rope;
+  MultiHeadLatentAttention(const MLAConfig& config, uint64_t seed);  // seeds seed .. seed + 6
+  Tensor forward(const Tensor& x) const override;  // x [B, S, dim]
+  std::vector<Tensor> parameters() const override;
+};
+
+// LuckTransformer (src/transformer.rs:35-109, 200-216): embed -> RMSNorm -> MLA -> + residual ->
+// RMSNorm -> Linear(d, 2d) + ReLU -> Linear(2d, d) -> + residual -> RMSNorm -> out_proj, with the
+// MLA of LuckTransformer::new (4 heads, kv latent 32, rope 16, v_head_dim = d / 4, 256 positions)
+struct LuckTransformer : Module {
+  Linear embed;
+  RMSNorm norm_1;
+  MultiHeadLatentAttention mla_layer;
+  RMSNorm norm_2;
+  Linear ffn_1, ffn_2;
+  RMSNorm norm_final;
+  Linear out_proj;
+  LuckTransformer(size_t in_dim, size_t hidden_dim, bool bias, uint64_t seed);
+  Tensor forward(const Tensor& x) const override;  // x [B, S, in_dim] -> [B, S, hidden_dim]
+  // [B, S, d] -> [B, d], row S - 1 of each sequence, built as a new tensor without a graph as the
+  // reference does (no gradient reaches x); differentiable = true (extension) records a gather
+  // whose backward adds the rows' gradient into row S - 1
+  Tensor last_token(const Tensor& x, bool differentiable = false) const;
   std::vector<Tensor> parameters() const override;
 };
 
