@@ -98,9 +98,7 @@ def cpu_baseline(cfg_t, seconds_budget=20.0):
     """The f64 oracle on this host: reference-faithful per-sample batch-1 graphs (the backbone run
     for the actor and again for the critic, src/ppo.rs:691-757) on a bounded sample, plus the
     batched restatement. Threads: this host's cores, at most 16 (a GPU box's CPU share)."""
-    import pyoracle
-    if not os.path.exists(pyoracle.LIB_PATH):
-        pyoracle.build()
+    import pyoracle  # prebuilt by __graft_entry__.build(); never compiled from a GPU process
     threads = max(1, min(16, len(os.sched_getaffinity(0))))
     pyoracle.set_threads(threads)
 
@@ -147,20 +145,11 @@ def host_info():
 
 
 def device_line():
-    """Device 0 as the runtime reports it, with the product name rocm-smi gives when it is there."""
+    """Device 0 as the runtime reports it. (No subprocess: this process has initialised the GPU,
+    and a child it forks must not exec another program.)"""
     info = th.device_info()
-    out = {"name": info["name"], "cu_count": info["cu_count"], "clock_mhz": info["clock_khz"] // 1000,
-           "memory_gib": round(info["total_mem"] / 2 ** 30, 1)}
-    try:
-        import subprocess
-        r = subprocess.run(["rocm-smi", "--showproductname"], capture_output=True, text=True, timeout=20)
-        for line in r.stdout.splitlines():
-            if "Card Series" in line or "Card series" in line:
-                out["product"] = line.split(":")[-1].strip()
-                break
-    except (OSError, subprocess.SubprocessError):
-        pass
-    return out
+    return {"name": info["name"], "cu_count": info["cu_count"], "clock_mhz": info["clock_khz"] // 1000,
+            "memory_gib": round(info["total_mem"] / 2 ** 30, 1)}
 
 
 def optimizer_line(P, dP, steps):
@@ -265,8 +254,6 @@ def rollout_line(steps, n_envs=4096, context_len=16, cpu=True):
            "tokens_per_s": round(n_envs / (ms * 1e-3), 1), "us_per_step": round(ms * 1e3, 2)}
     if cpu:
         import pyoracle
-        if not os.path.exists(pyoracle.LIB_PATH):
-            pyoracle.build()
         ocfg = pyoracle.PpoCfg(*cfg_t)
         od = pyoracle.Decoder(ocfg, p.astype(np.float64), 256, 1)
         x = wl.gacha_states(rng, 1, 1)[0, 0]

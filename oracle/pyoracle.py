@@ -52,10 +52,12 @@ _lib = None
 
 
 def lib():
+    """Loads the prebuilt liboracle.so (__graft_entry__.build() compiles it). It is never compiled
+    here: a process that has initialised the GPU must not start the compiler."""
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
-            build()
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() (or pyoracle.build()) first")
         L = ctypes.CDLL(LIB_PATH)
         L.orc_last_error.restype = ctypes.c_char_p
         for name in ["orc_tensor_new", "orc_tensor_new_len", "orc_tensor_rand", "orc_relu", "orc_log", "orc_exp",

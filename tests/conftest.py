@@ -17,7 +17,9 @@ def pytest_configure(config):
 @pytest.fixture(scope="session")
 def oracle():
     import pyoracle
-    pyoracle.build()
+    # the prebuilt checker (__graft_entry__.build() compiles it before any test runs; building it
+    # here could start the compiler from a process that has already initialised the GPU)
+    pyoracle.lib()
     # the CPU share of a GPU box is 16 cores whatever the machine reports
     pyoracle.set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
     return pyoracle
