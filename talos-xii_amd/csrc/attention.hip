@@ -21,6 +21,7 @@
 // normalised P . V) and saves lse = max + log(sum); the backward recomputes P = exp(s - lse)
 // and uses D_q = dO_q . O_q. Causal masking (key <= query) and the sequence end are applied to
 // the scores, so masked probabilities are exactly 0; key blocks past the diagonal are skipped.
+#include <cstdlib>
 #include <mutex>
 
 #include "attention.hpp"
@@ -324,6 +325,167 @@ attn_fwd_s32_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Forward for seq > 32: a workgroup per (pair, tile of 128 queries), one wave per 32-query block.
+// K and V stream through LDS in blocks of 32 keys, one copy serving the four waves, the next
+// block fetched into registers while the current one is in use. One pass with the running
+// softmax: a block's scores raise the row maximum, and the O accumulators and the row sum are
+// rescaled by exp(m_old - m_new) before the block's P.V is added. S^T layout as
+// attn_fwd_kernel (register r <-> key acc_row(r, h), lane <-> query), so the probabilities are
+// the A operand of P.V straight from registers; the per-query factors reach O's layout
+// (register r <-> query acc_row(r, h)) through a 32-float LDS slice per wave.
+// ---------------------------------------------------------------------------
+constexpr int kQTile = 128;  // queries per workgroup (4 waves x 32)
+
+// Element group g (4 consecutive floats) of a [32 rows, DM] block starting at row0: row 4g / DM,
+// column 4g % DM; rows >= nrows and columns >= dim read as 0.
+template <int DM>
+__device__ __forceinline__ float4 block_ld4(const float* __restrict__ base, long long ld, long long tok0, int row0,
+                                            int nrows, int col0, int dim, int g, bool vec) {
+  const int idx = 4 * g, row = idx / DM, col = idx % DM;
+  const int r = row0 + row;
+  if (r >= nrows) return make_float4(0.f, 0.f, 0.f, 0.f);
+  const float* src = base + (tok0 + r) * ld + col0 + col;
+  if (vec) return *reinterpret_cast<const float4*>(src);
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = col + j < dim ? src[j] : 0.f;
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+// ... and its place in an LDS block of pitch P
+template <int DM, int P>
+__device__ __forceinline__ void block_st4(float* tile, int g, float4 v) {
+  const int idx = 4 * g;
+  *reinterpret_cast<float4*>(tile + (idx / DM) * P + idx % DM) = v;
+}
+
+// Per-query factors of this wave (lane l32 holds query l32's; h == 0 writes) into O's layout:
+// f[r] is the factor of query acc_row(r, h).
+__device__ __forceinline__ void bcast_rows(float* slice, float v, int l32, int h, float (&f)[16]);
+
+#ifndef TALOS_ATTN_TILED_WAVES
+#define TALOS_ATTN_TILED_WAVES 3
+#endif
+template <int DKM, int DVM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DKM > 96 ? 2 : TALOS_ATTN_TILED_WAVES))) void
+attn_fwd_tiled_kernel(AttnArgs a) {
+  constexpr int KH = DKM / 2, OB = DVM / 32;
+  constexpr int PK = DKM + 4, PV = DVM + 4;  // 16-byte rows; eight consecutive rows on distinct bank groups
+  constexpr int KL = DKM / 32, VL = DVM / 32;  // float4 groups per thread per block
+  __shared__ __align__(16) float Ks[32 * PK];
+  __shared__ __align__(16) float Vs[32 * PV];
+  __shared__ __align__(16) float Wr[4][32];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int ntile = (a.S + kQTile - 1) / kQTile;
+  const int pair = blockIdx.x / ntile, tile = blockIdx.x % ntile;
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int Sk = key_len(a, b);
+  const int qb = tile * 4 + wv;
+  const int q = qb * 32 + l32;
+  const bool wave_on = qb * 32 < a.S;
+  const int q_hi = min(a.S, (tile + 1) * kQTile) - 1;
+  const int kb_end = Sk == 0 ? -1 : (a.causal ? min(q_hi, Sk - 1) : Sk - 1) >> 5;  // uniform per workgroup
+  const int wave_kb_end = a.causal ? min(kb_end, qb) : kb_end;
+
+  float qv[KH];
+  load_half<KH, kFwdSel>(qv, a.q, a.ldq, tok0, q, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
+  float4 rk[KL], rv[VL];
+  auto fetch = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < KL; ++i)
+      rk[i] = block_ld4<DKM>(a.k, a.ldk, tok0, kb * 32, a.S, hd * a.dk, a.dk, i * 256 + (int)threadIdx.x, a.vec);
+#pragma unroll
+    for (int i = 0; i < VL; ++i)
+      rv[i] = block_ld4<DVM>(a.v, a.ldv, tok0, kb * 32, a.S, hd * a.dv, a.dv, i * 256 + (int)threadIdx.x, a.vec);
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < KL; ++i) block_st4<DKM, PK>(Ks, i * 256 + (int)threadIdx.x, rk[i]);
+#pragma unroll
+    for (int i = 0; i < VL; ++i) block_st4<DVM, PV>(Vs, i * 256 + (int)threadIdx.x, rv[i]);
+  };
+
+  float m = kNegInf, l = 0.f;
+  floatx16 oacc[OB];
+#pragma unroll
+  for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[ob][r] = 0.f;
+  if (kb_end >= 0) {
+    fetch(0);
+    stash();
+  }
+  __syncthreads();
+  for (int kb = 0; kb <= kb_end; ++kb) {
+    const bool more = kb < kb_end;
+    if (more) fetch(kb + 1);
+    if (wave_on && kb <= wave_kb_end) {
+      floatx16 acc;  // S^T, this lane's half of key row l32 read from LDS four values at a time
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+      for (int i = 0; i < KH; i += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(Ks + l32 * PK + KH * h + i);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.x, qv[i], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.y, qv[i + 1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.z, qv[i + 2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.w, qv[i + 3], acc, 0, 0, 0);
+      }
+      float sv[16], bm = kNegInf;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb * 32 + acc_row(r, h);
+        const bool ok = key < Sk && (!a.causal || key <= q);
+        sv[r] = ok ? acc[r] : kNegInf;
+        bm = fmaxf(bm, sv[r]);
+      }
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      const float mn = fmaxf(m, bm);
+      const float alpha = (m == kNegInf) ? 0.f : expf(m - mn);
+      float P[16], bs = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        P[r] = (mn == kNegInf) ? 0.f : expf(sv[r] - mn);  // exp(-inf) = 0 for the masked keys
+        bs += P[r];
+      }
+      bs += __shfl_xor(bs, 32, 64);
+      l = l * alpha + bs;
+      m = mn;
+      float al[16];
+      bcast_rows(Wr[wv], alpha, l32, h, al);
+#pragma unroll
+      for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[ob][r] *= al[r];
+#pragma unroll
+      for (int s2 = 0; s2 < 16; ++s2) {
+        const float* vrow = Vs + acc_row(s2, h) * PV + l32;
+#pragma unroll
+        for (int ob = 0; ob < OB; ++ob)
+          oacc[ob] = __builtin_amdgcn_mfma_f32_32x32x2f32(P[s2], vrow[ob * 32], oacc[ob], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+    if (more) {
+      stash();
+      __syncthreads();
+    }
+  }
+  if (!wave_on) return;
+  float il[16];
+  bcast_rows(Wr[wv], l > 0.f ? 1.f / l : 0.f, l32, h, il);
+#pragma unroll
+  for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qr = qb * 32 + acc_row(r, h);
+      const int e = ob * 32 + l32;
+      if (qr < a.S && e < a.dv) a.o[(tok0 + qr) * a.ldo + hd * a.dv + e] = oacc[ob][r] * il[r];
+    }
+  if (h == 0 && q < a.S) a.lse[(long long)pair * a.S + q] = (l > 0.f) ? m + logf(l) : kNegInf;
+}
+
+// ---------------------------------------------------------------------------
 // dQ (and D = dO . O): wave per (pair, query block), S^T layout
 // ---------------------------------------------------------------------------
 template <int DKM, int DVM>
@@ -478,6 +640,292 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Backward for seq > 32, LDS-tiled like attn_fwd_tiled_kernel (FlashAttention-2's split):
+//  * dQ (and D = dO . O): a workgroup per (pair, 128-query tile), one wave per 32-query block,
+//    K and V streaming through LDS in 32-key blocks. S^T = K.Q^T and dP^T = V.dO^T in the S^T
+//    layout, P = exp(S - lse), dS = P (dP - D); dQ += dS . K with dS the A operand in registers
+//    and K's columns read from the staged block.
+//  * dK / dV: a workgroup per (pair, 128-key tile), one wave per 32-key block, Q, dO, lse and D
+//    streaming through LDS in 32-query blocks. S = Q.K^T and dP = dO.V^T in the S layout
+//    (register r <-> query acc_row(r, h), lane <-> key); dV += P^T . dO and dK += dS^T . Q.
+// ---------------------------------------------------------------------------
+template <int DKM, int DVM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DKM > 64 ? 2 : TALOS_ATTN_TILED_WAVES))) void
+attn_bwd_dq_tiled_kernel(AttnArgs a) {
+  constexpr int KH = DKM / 2, VH = DVM / 2, QB = DKM / 32;
+  constexpr int PK = DKM + 4, PV = DVM + 4;
+  constexpr int KL = DKM / 32, VL = DVM / 32;
+  __shared__ __align__(16) float Ks[32 * PK];
+  __shared__ __align__(16) float Vs[32 * PV];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int ntile = (a.S + kQTile - 1) / kQTile;
+  const int pair = blockIdx.x / ntile, tile = blockIdx.x % ntile;
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int Sk = key_len(a, b);
+  const int qb = tile * 4 + wv;
+  const int q = qb * 32 + l32;
+  const bool wave_on = qb * 32 < a.S;
+  const bool qok = q < a.S;
+  const int q_hi = min(a.S, (tile + 1) * kQTile) - 1;
+  const int kb_end = Sk == 0 ? -1 : (a.causal ? min(q_hi, Sk - 1) : Sk - 1) >> 5;
+  const int wave_kb_end = a.causal ? min(kb_end, qb) : kb_end;
+
+  float qv[KH], gv[VH];
+  load_half<KH, kBwdSel>(qv, a.q, a.ldq, tok0, q, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
+  load_half<VH, kBwdSel>(gv, a.dout, a.lddo, tok0, q, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+  float D;
+  {
+    float ov[VH];
+    load_half<VH, kBwdSel>(ov, a.o, a.ldo, tok0, q, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < VH; i += 2) {
+      d0 = fmaf(gv[i], ov[i], d0);
+      d1 = fmaf(gv[i + 1], ov[i + 1], d1);
+    }
+    D = d0 + d1;
+    D += __shfl_xor(D, 32, 64);
+  }
+  const float lse = a.lse[(long long)pair * a.S + (qok ? q : 0)];
+  if (h == 0 && qok) a.D[(long long)pair * a.S + q] = D;
+
+  // PF: the next block is fetched into registers during the current one; at head dims past 96
+  // those registers would spill, so the block is loaded after the barrier instead and the other
+  // workgroup on the CU covers the latency
+  constexpr bool PF = DKM + DVM <= 160;
+  float4 rk[KL], rv[VL];
+  auto fetch = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < KL; ++i)
+      rk[i] = block_ld4<DKM>(a.k, a.ldk, tok0, kb * 32, a.S, hd * a.dk, a.dk, i * 256 + (int)threadIdx.x, a.vec);
+#pragma unroll
+    for (int i = 0; i < VL; ++i)
+      rv[i] = block_ld4<DVM>(a.v, a.ldv, tok0, kb * 32, a.S, hd * a.dv, a.dv, i * 256 + (int)threadIdx.x, a.vec);
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < KL; ++i) block_st4<DKM, PK>(Ks, i * 256 + (int)threadIdx.x, rk[i]);
+#pragma unroll
+    for (int i = 0; i < VL; ++i) block_st4<DVM, PV>(Vs, i * 256 + (int)threadIdx.x, rv[i]);
+  };
+  floatx16 dq[QB];
+#pragma unroll
+  for (int i = 0; i < QB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
+  if (kb_end >= 0) {
+    fetch(0);
+    stash();
+  }
+  __syncthreads();
+  for (int kb = 0; kb <= kb_end; ++kb) {
+    const bool more = kb < kb_end;
+    if (PF && more) fetch(kb + 1);
+    if (wave_on && kb <= wave_kb_end) {
+      floatx16 sacc, pacc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
+#pragma unroll
+      for (int i = 0; i < KH; i += 4) {  // S^T = K . (scale Q)^T
+        const float4 v = *reinterpret_cast<const float4*>(Ks + l32 * PK + KH * h + i);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.x, qv[i], sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.y, qv[i + 1], sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.z, qv[i + 2], sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.w, qv[i + 3], sacc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < VH; i += 4) {  // dP^T = V . dO^T
+        const float4 v = *reinterpret_cast<const float4*>(Vs + l32 * PV + VH * h + i);
+        pacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.x, gv[i], pacc, 0, 0, 0);
+        pacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.y, gv[i + 1], pacc, 0, 0, 0);
+        pacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.z, gv[i + 2], pacc, 0, 0, 0);
+        pacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.w, gv[i + 3], pacc, 0, 0, 0);
+      }
+      float dS[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb * 32 + acc_row(r, h);
+        const bool ok = qok && key < Sk && (!a.causal || key <= q);
+        const float p = expf(ok ? sacc[r] - lse : kNegInf);
+        dS[r] = p * (pacc[r] - D);
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < 16; ++s2) {  // dQ += dS . K
+        const float* krow = Ks + acc_row(s2, h) * PK + l32;
+#pragma unroll
+        for (int i = 0; i < QB; ++i) dq[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(dS[s2], krow[i * 32], dq[i], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+    if (more) {
+      if (!PF) fetch(kb + 1);
+      stash();
+      __syncthreads();
+    }
+  }
+  if (!wave_on) return;
+#pragma unroll
+  for (int i = 0; i < QB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qr = qb * 32 + acc_row(r, h);
+      const int e = i * 32 + l32;
+      const float g = rope_t(dq[i][r] * a.scale, e, qr, a, qr < a.S);
+      if (qr < a.S && e < a.dk) a.dq[(tok0 + qr) * a.lddq + hd * a.dk + e] = g;
+    }
+}
+
+template <int DKM, int DVM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DKM > 32 ? 2 : TALOS_ATTN_TILED_WAVES))) void
+attn_bwd_dkv_tiled_kernel(AttnArgs a) {
+  constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32;
+  constexpr int PK = DKM + 4, PV = DVM + 4;
+  constexpr int KL = DKM / 32, VL = DVM / 32;
+  __shared__ __align__(16) float Qs[32 * PK];
+  __shared__ __align__(16) float Gs[32 * PV];
+  __shared__ __align__(16) float LD[2][32];  // lse, D of the staged query block
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int t = threadIdx.x;
+  const int ntile = (a.S + kQTile - 1) / kQTile;
+  const int pair = blockIdx.x / ntile, tile = blockIdx.x % ntile;
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int kb = tile * 4 + wv;  // this wave's key block
+  const int key = kb * 32 + l32;
+  const bool wave_on = kb * 32 < a.S;
+  const bool kok = key < key_len(a, b);
+  const int nqb = (a.S + 31) >> 5;
+  const int qb_beg = a.causal ? tile * 4 : 0;  // the tile's first key block can see no earlier query
+  if (key_len(a, b) <= tile * kQTile) {
+    // no key of this tile takes part: dK = dV = 0
+    if (!wave_on) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = kb * 32 + acc_row(r, h);
+      if (kr >= a.S) continue;
+      for (int e = l32; e < a.dk; e += 32) a.dk_out[(tok0 + kr) * a.lddk + hd * a.dk + e] = 0.f;
+      for (int e = l32; e < a.dv; e += 32) a.dv_out[(tok0 + kr) * a.lddv + hd * a.dv + e] = 0.f;
+    }
+    return;
+  }
+
+  float kv[KH], vv[VH];
+  load_half<KH, kBwdSel>(kv, a.k, a.ldk, tok0, key, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
+  load_half<VH, kBwdSel>(vv, a.v, a.ldv, tok0, key, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+  floatx16 dk[KB], dv[VB];
+#pragma unroll
+  for (int i = 0; i < KB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dk[i][r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < VB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dv[i][r] = 0.f;
+
+  constexpr bool PF = DKM + DVM <= 128;  // as in attn_bwd_dq_tiled_kernel (K, V rows, dK, dV live)
+  float4 rq[KL], rg[VL];
+  float rl = 0.f;
+  auto fetch = [&](int qb) {
+#pragma unroll
+    for (int i = 0; i < KL; ++i)
+      rq[i] = block_ld4<DKM>(a.q, a.ldq, tok0, qb * 32, a.S, hd * a.dk, a.dk, i * 256 + t, a.vec);
+#pragma unroll
+    for (int i = 0; i < VL; ++i)
+      rg[i] = block_ld4<DVM>(a.dout, a.lddo, tok0, qb * 32, a.S, hd * a.dv, a.dv, i * 256 + t, a.vec);
+    if (t < 64) {  // lse (t < 32) and D (32 <= t < 64) of the block's queries
+      const int qr = qb * 32 + (t & 31);
+      const long long li = (long long)pair * a.S + (qr < a.S ? qr : 0);
+      rl = (t < 32 ? a.lse : a.D)[li];
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < KL; ++i) block_st4<DKM, PK>(Qs, i * 256 + t, rq[i]);
+#pragma unroll
+    for (int i = 0; i < VL; ++i) block_st4<DVM, PV>(Gs, i * 256 + t, rg[i]);
+    if (t < 64) LD[t >> 5][t & 31] = rl;
+  };
+  fetch(qb_beg);
+  stash();
+  __syncthreads();
+  for (int qb = qb_beg; qb < nqb; ++qb) {
+    const bool more = qb + 1 < nqb;
+    if (PF && more) fetch(qb + 1);
+    if (wave_on && (!a.causal || qb >= kb)) {
+      floatx16 sacc, pacc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
+#pragma unroll
+      for (int i = 0; i < KH; i += 4) {  // S = Q . (scale K)^T
+        const float4 v = *reinterpret_cast<const float4*>(Qs + l32 * PK + KH * h + i);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.x, kv[i], sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.y, kv[i + 1], sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.z, kv[i + 2], sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.w, kv[i + 3], sacc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < VH; i += 4) {  // dP = dO . V^T
+        const float4 v = *reinterpret_cast<const float4*>(Gs + l32 * PV + VH * h + i);
+        pacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.x, vv[i], pacc, 0, 0, 0);
+        pacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.y, vv[i + 1], pacc, 0, 0, 0);
+        pacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.z, vv[i + 2], pacc, 0, 0, 0);
+        pacc = __builtin_amdgcn_mfma_f32_32x32x2f32(v.w, vv[i + 3], pacc, 0, 0, 0);
+      }
+      float P[16], dS[16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {  // queries 8j + 4h + 0..3 of the block
+        const float4 l4 = *reinterpret_cast<const float4*>(&LD[0][8 * j + 4 * h]);
+        const float4 d4 = *reinterpret_cast<const float4*>(&LD[1][8 * j + 4 * h]);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int r = 4 * j + u;
+          const int qr = qb * 32 + acc_row(r, h);
+          const bool ok = kok && qr < a.S && (!a.causal || key <= qr);
+          const float p = expf(ok ? sacc[r] - lv[u] : kNegInf);
+          P[r] = p;
+          dS[r] = p * (pacc[r] - dv4[u]);
+        }
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < 16; ++s2) {  // dV += P^T . dO, dK += dS^T . Q
+        const float* grow = Gs + acc_row(s2, h) * PV + l32;
+        const float* qrow = Qs + acc_row(s2, h) * PK + l32;
+#pragma unroll
+        for (int i = 0; i < VB; ++i) dv[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(P[s2], grow[i * 32], dv[i], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < KB; ++i) dk[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(dS[s2], qrow[i * 32], dk[i], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+    if (more) {
+      if (!PF) fetch(qb + 1);
+      stash();
+      __syncthreads();
+    }
+  }
+  if (!wave_on) return;
+#pragma unroll
+  for (int i = 0; i < KB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = kb * 32 + acc_row(r, h);
+      const int e = i * 32 + l32;
+      const float g = rope_t(dk[i][r] * a.scale, e, kr, a, kr < a.S);
+      if (kr < a.S && e < a.dk) a.dk_out[(tok0 + kr) * a.lddk + hd * a.dk + e] = g;
+    }
+#pragma unroll
+  for (int i = 0; i < VB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = kb * 32 + acc_row(r, h);
+      const int e = i * 32 + l32;
+      if (kr < a.S && e < a.dv) a.dv_out[(tok0 + kr) * a.lddv + hd * a.dv + e] = dv[i][r];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Single-block backward (seq <= 32): one wave per (batch, head) pair computes dQ, dK and dV from
 // one read of q, k, v, o and dO (D = dO . O is formed in the wave). S layout (lane <-> key,
 // register r <-> query acc_row(r, h)); dS is transposed through the wave's LDS slice for dQ.
@@ -486,6 +934,17 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ void bcast_rows(float* slice, float v, int l32, int h, float (&f)[16]) {
+  if (h == 0) slice[l32] = v;
+  wave_lds_sync();
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {  // queries 8j + 4h + 0..3: one 16-byte read each
+    const float4 x = *reinterpret_cast<const float4*>(slice + 8 * j + 4 * h);
+    f[4 * j] = x.x; f[4 * j + 1] = x.y; f[4 * j + 2] = x.z; f[4 * j + 3] = x.w;
+  }
+  wave_lds_sync();  // every lane has read before the slice is written again
 }
 
 constexpr int kTS = 33;  // pitch of the transposed dS tile: a column read touches 32 banks
@@ -660,6 +1119,16 @@ attn_bwd_fused_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Launch
 // ---------------------------------------------------------------------------
+// TALOS_ATTN_LEGACY=1 (read once): the per-wave kernels for seq > 32 instead of the LDS-tiled
+// ones (the same results; kept as the cross-check of the tiled kernels).
+static bool attn_legacy() {
+  static const bool v = [] {
+    const char* e = std::getenv("TALOS_ATTN_LEGACY");
+    return e && e[0] == '1';
+  }();
+  return v;
+}
+
 static bool pick_dims(int dk, int dv, int* dkm, int* dvm) {
   if (dk <= 32 && dv <= 32) { *dkm = 32; *dvm = 32; return true; }
   if (dk <= 64 && dv <= 64) { *dkm = 64; *dvm = 64; return true; }
@@ -727,6 +1196,24 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
     hipLaunchKernelGGL(attn_fwd_s32_kernel, dim3(ceil_div((size_t)a.B * a.H, 4)), dim3(256), 0, s, a);
     return launch_status("attn_fwd_s32_kernel");
   }
+  if (a.S > 32 && !attn_legacy()) {
+    // K / V rows are read once per 128-query tile (the queries' rows and the outputs once)
+    const double tiles = (a.S + kQTile - 1) / kQTile;
+    const double tbytes = 4.0 * rows * (a.dk + 2.0 * a.dv + 1.0) + 4.0 * a.B * a.H * tiles * a.S * (a.dk + a.dv);
+    grid = dim3((unsigned)((long long)a.B * a.H * (long long)tiles));
+#define TILED(DK, DV)                                                                       \
+    if (dkm == DK && dvm == DV) {                                                           \
+      ProfScope ps(s, "attn_fwd_tiled_kernel<" #DK ", " #DV ">", flops, tbytes);            \
+      hipLaunchKernelGGL((attn_fwd_tiled_kernel<DK, DV>), grid, dim3(256), 0, s, a);        \
+      return launch_status("attn_fwd_tiled_kernel");                                        \
+    }
+    TILED(32, 32)
+    TILED(64, 64)
+    TILED(96, 64)
+    TILED(128, 128)
+#undef TILED
+    return TALOS_ERR_UNSUPPORTED;
+  }
   ATTN_ALL(attn_fwd_kernel)
 }
 
@@ -741,6 +1228,24 @@ static int attn_bwd_dq(const AttnArgs& a, int dkm, int dvm, hipStream_t s) {
   // s = q.k, dp = dO.v, dq += ds k; reads q k v o dO lse, writes dq and D
   const double flops = kept_pairs(a) * (4.0 * a.dk + 2.0 * a.dv);
   const double bytes = 4.0 * rows * (3.0 * a.dk + 3.0 * a.dv + 2.0);
+  // up to 64 queries a 128-query tile leaves half its waves idle: the per-wave kernel is faster
+  if (!attn_legacy() && a.S > 64) {
+    // q, dO, O rows read and dq, D written once; K / V rows once per 128-query tile
+    const double tiles = (a.S + kQTile - 1) / kQTile;
+    const double tbytes = 4.0 * rows * (2.0 * a.dk + 2.0 * a.dv + 2.0) + 4.0 * a.B * a.H * tiles * a.S * (a.dk + a.dv);
+    grid = dim3((unsigned)((long long)a.B * a.H * (long long)tiles));
+#define TILED(DK, DV)                                                                        \
+    if (dkm == DK && dvm == DV) {                                                            \
+      ProfScope ps(s, "attn_bwd_dq_tiled_kernel<" #DK ", " #DV ">", flops, tbytes);          \
+      hipLaunchKernelGGL((attn_bwd_dq_tiled_kernel<DK, DV>), grid, dim3(256), 0, s, a);      \
+      return launch_status("attn_bwd_dq_tiled_kernel");                                      \
+    }
+    TILED(32, 32)
+    TILED(64, 64)
+    TILED(96, 64)
+#undef TILED
+    // head dims 128: the tiled kernel's operands and accumulators exceed the register file
+  }
   ATTN_ALL(attn_bwd_dq_kernel)
 }
 
@@ -751,6 +1256,23 @@ static int attn_bwd_dkv(const AttnArgs& a, int dkm, int dvm, hipStream_t s) {
   // s = q.k, dp = dO.v, dv += p dO, dk += ds q; reads q dO lse D k v, writes dk dv
   const double flops = kept_pairs(a) * (4.0 * a.dk + 4.0 * a.dv);
   const double bytes = 4.0 * rows * (3.0 * a.dk + 3.0 * a.dv + 2.0);
+  if (!attn_legacy()) {
+    // k, v rows read and dk, dv written once; Q / dO rows and lse / D once per 128-key tile
+    const double tiles = (a.S + kQTile - 1) / kQTile;
+    const double tbytes = 4.0 * rows * (2.0 * a.dk + 2.0 * a.dv) + 4.0 * a.B * a.H * tiles * a.S * (a.dk + a.dv + 2.0);
+    grid = dim3((unsigned)((long long)a.B * a.H * (long long)tiles));
+#define TILED(DK, DV)                                                                        \
+    if (dkm == DK && dvm == DV) {                                                            \
+      ProfScope ps(s, "attn_bwd_dkv_tiled_kernel<" #DK ", " #DV ">", flops, tbytes);         \
+      hipLaunchKernelGGL((attn_bwd_dkv_tiled_kernel<DK, DV>), grid, dim3(256), 0, s, a);     \
+      return launch_status("attn_bwd_dkv_tiled_kernel");                                     \
+    }
+    TILED(32, 32)
+    TILED(64, 64)
+    TILED(96, 64)
+#undef TILED
+    // head dims 128: as in attn_bwd_dq
+  }
   ATTN_ALL(attn_bwd_dkv_kernel)
 }
 
