@@ -4,10 +4,13 @@
  *
  * Every entry point takes plain pointers and sizes. Device pointers are fp32 buffers
  * allocated with talos_malloc or any HIP allocator. Streams are hipStream_t passed as void*;
- * NULL is the null (default) stream. Kernel entry points enqueue their work on the stream and
- * return without waiting (talos_stream_sync waits), as GPU libraries do; the host <-> device
- * copies are synchronous. The reference's Tensor ops are synchronous (src/autograd.rs:200-354
- * return finished host vectors); a caller that mirrors them syncs before reading results.
+ * NULL is the null (default) stream. Calls are synchronous by default, as the reference's
+ * Tensor ops are (src/autograd.rs:200-354 return finished host vectors): a kernel entry point
+ * enqueues its work on the stream, waits for the stream and returns the stream's error, if any.
+ * talos_set_async(1) turns the calling thread's kernel entries into their asynchronous forms,
+ * which return as soon as the work is enqueued (talos_stream_sync or a synchronous copy waits),
+ * as GPU libraries do; code that captures a HIP graph must use that mode. The host <-> device
+ * copies are synchronous in both modes.
  * Status codes: 0 on success, a talos_status otherwise; talos_last_error() returns a
  * thread-local message for the last failure. Arguments are validated on the host before any
  * launch, so every error path below can be exercised on a machine without a GPU.
@@ -65,6 +68,11 @@ int talos_memcpy_d2h_f64(double* dst, const float* src, size_t n, talos_stream_t
 /* Zero-fills with a kernel (no hipMemsetAsync, so it is safe inside a captured graph). */
 int talos_fill_zero(void* dst, size_t bytes, talos_stream_t stream);
 int talos_stream_sync(talos_stream_t stream);
+/* Completion mode of the calling thread's kernel entry points: 0 (the default) synchronous,
+ * 1 asynchronous (the *_async behaviour of a GPU library). No reference counterpart: the
+ * reference's ops are always synchronous. talos_get_async returns the thread's mode. */
+int talos_set_async(int on);
+int talos_get_async(void);
 /* Non-blocking stream at the default priority. */
 int talos_stream_create(talos_stream_t* stream);
 int talos_stream_destroy(talos_stream_t stream);
@@ -192,6 +200,13 @@ int talos_unary_fwd_f32(int op, size_t n, float p0, float p1, const float* x, fl
  * clip where min <= x <= max, sqrt only where x > 0). */
 int talos_unary_bwd_f32(int op, size_t n, float p0, float p1, const float* x, const float* dy, float* dx,
                         talos_stream_t stream);
+/* GELU (an extension: the reference has relu only, autograd.rs:356-386; the configurations'
+ * MLPs use GELU): y = 0.5 x (1 + erf(x / sqrt(2))). The same function as op TALOS_GELU, with a
+ * float4 kernel. */
+int talos_gelu_fwd_f32(size_t n, const float* x, float* y, talos_stream_t stream);
+/* dx = beta * dx + dy * (Phi(x) + x phi(x)), beta 0 (overwrite) or 1 (accumulate, as the tape's
+ * grads do). */
+int talos_gelu_bwd_f32(size_t n, const float* x, const float* dy, float beta, float* dx, talos_stream_t stream);
 int talos_binary_fwd_f32(int op, size_t n, const float* a, const float* b, float* y, talos_stream_t stream);
 /* da += d/da, db += d/db. When da == db (the same tensor on both sides, autograd.rs:1729, 1792)
  * the combined derivative is accumulated once. */
@@ -389,6 +404,26 @@ int talos_ppo_minibatch_f32(talos_plan plan, int n, const float* params, const f
                             const int32_t* lengths, const int32_t* actions, const float* adv, const float* ret,
                             const float* old_logp, float* loss, float* dparams, double* stats,
                             int stats_accumulate, talos_stream_t stream);
+/* The clipped PPO loss of a minibatch from the actor logits [n, n_actions] and critic values [n]
+ * (replaces the per-sample loss graph of ppo.rs:702-749 and its mean, ppo.rs:754-755). Per sample,
+ * in f64: logp = log_softmax(logits), ratio = exp(logp[action] - old_logp), surrogates ratio * adv
+ * and clip(ratio, 1 - clip_eps, 1 + clip_eps) * adv, the smaller kept (ties take the clipped one);
+ * loss = mean(-surrogate + value_coef (value - ret)^2 - entropy_coef H). loss (device float[1])
+ * and stats (device double[TALOS_PPO_NSTATS], added into when stats_accumulate != 0) may each be
+ * NULL, not both. An action outside [0, n_actions) makes the loss NaN (the reference panics).
+ * n_actions may be any positive count here (the plans take at most 64). */
+int talos_ppo_head_loss_fwd_f32(int n, int n_actions, float clip_eps, float value_coef, float entropy_coef,
+                                const float* logits, const float* values, const int32_t* actions, const float* adv,
+                                const float* ret, const float* old_logp, float* loss, double* stats,
+                                int stats_accumulate, talos_stream_t stream);
+/* Its gradient with respect to the logits and values (the closures of the same graph,
+ * ppo.rs:702-755, in closed form): dlogits [n, n_actions] and dvalues [n] are overwritten; loss
+ * (device float[1]) is written too when not NULL. A sample with an out-of-range action gets a
+ * zero gradient. */
+int talos_ppo_head_loss_bwd_f32(int n, int n_actions, float clip_eps, float value_coef, float entropy_coef,
+                                const float* logits, const float* values, const int32_t* actions, const float* adv,
+                                const float* ret, const float* old_logp, float* dlogits, float* dvalues, float* loss,
+                                talos_stream_t stream);
 /* Forward only for n samples with optional lengths (the rollout's log-probs and values). */
 int talos_ppo_forward_n_f32(talos_plan plan, int n, const float* params, const float* states,
                             const int32_t* lengths, float* logits, float* values, talos_stream_t stream);

@@ -1597,7 +1597,7 @@ int talos_attn_fwd_f32(int batch, int seq, int heads, int qk_dim, int v_dim, flo
   AttnDesc d;
   d.batch = batch; d.seq = seq; d.heads = heads; d.dk = qk_dim; d.dv = v_dim; d.scale = scale; d.causal = causal;
   d.q = q; d.ldq = ld_q; d.k = k; d.ldk = ld_k; d.v = v; d.ldv = ld_v; d.o = o; d.ldo = ld_o; d.lse = lse;
-  return attn_fwd_launch(d, as_stream(stream));
+  return entry_done(attn_fwd_launch(d, as_stream(stream)), as_stream(stream));
 }
 
 int talos_attn_bwd_f32(int batch, int seq, int heads, int qk_dim, int v_dim, float scale, int causal, const float* q,
@@ -1614,7 +1614,7 @@ int talos_attn_bwd_f32(int batch, int seq, int heads, int qk_dim, int v_dim, flo
   if ((rc = ws.acquire(attn_bwd_uses_workspace(d) ? attn_bwd_workspace_bytes(d) : 0, s))) return rc;
   rc = attn_bwd_launch(d, static_cast<float*>(ws.ptr), s);
   const int rel = ws.release();
-  return rc ? rc : rel;
+  return entry_done(rc ? rc : rel, as_stream(stream));
 }
 
 int talos_attn_bwd_noalloc_f32(int batch, int seq, int heads, int qk_dim, int v_dim, float scale, int causal,
@@ -1633,7 +1633,7 @@ int talos_attn_bwd_noalloc_f32(int batch, int seq, int heads, int qk_dim, int v_
   float* ws = nullptr;
   if (attn_bwd_uses_workspace(d))
     if ((rc = attn_scratch(&ws))) return rc;
-  return attn_bwd_launch(d, ws, as_stream(stream));
+  return entry_done(attn_bwd_launch(d, ws, as_stream(stream)), as_stream(stream));
 }
 
 }  // extern "C"

@@ -25,6 +25,12 @@ inline hipStream_t as_stream(talos_stream_t s) { return reinterpret_cast<hipStre
 // Returns TALOS_ERR_HIP with the runtime's message when e != hipSuccess.
 int hip_status(hipError_t e, const char* what);
 
+// The last step of every kernel entry point. In the calling thread's default mode the entry is
+// synchronous, as the reference's Tensor ops return finished results: it waits for its stream and
+// returns the stream's error, if any. After talos_set_async(1) on the thread it returns rc as soon
+// as the work is enqueued. A non-zero rc is returned at once in both modes.
+int entry_done(int rc, hipStream_t s);
+
 // Checks the launch that was just enqueued.
 int launch_status(const char* kernel);
 

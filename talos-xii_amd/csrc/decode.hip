@@ -944,11 +944,11 @@ int talos_ppo_decoder_step_f32(talos_decoder dec, int n, const float* params, co
                 "%s: actions / logp need the uniform draws", __func__);
   TALOS_DEVICE();
   dec->params = params;
-  if (dec->fused)
-    return decode_step_fused(dec, n, params, tokens, positions, reset, uniforms, logits, values, actions, logp,
-                             as_stream(stream));
-  return decode_step(dec, n, params, tokens, positions, reset, uniforms, logits, values, actions, logp,
-                     as_stream(stream));
+  const hipStream_t s = as_stream(stream);
+  const int rc = dec->fused
+                     ? decode_step_fused(dec, n, params, tokens, positions, reset, uniforms, logits, values, actions, logp, s)
+                     : decode_step(dec, n, params, tokens, positions, reset, uniforms, logits, values, actions, logp, s);
+  return entry_done(rc, s);
 }
 
 int talos_ppo_decoder_read_cache(talos_decoder dec, int layer, int env, float* k, float* v, int* len) {

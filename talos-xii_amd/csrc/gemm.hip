@@ -1430,7 +1430,7 @@ int talos_gemm_f32(int transA, int transB, int M, int N, int K, float alpha, con
   d.alpha = alpha;
   d.beta = beta;
   d.ksplit = 0;
-  return run_gemm(d, as_stream(stream));
+  return entry_done(run_gemm(d, as_stream(stream)), as_stream(stream));
 }
 
 int talos_gemm_bf16acc_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
@@ -1454,7 +1454,7 @@ int talos_gemm_bf16acc_f32(int transA, int transB, int M, int N, int K, float al
   d.beta = beta;
   d.bf16 = true;
   d.ksplit = 0;
-  return run_gemm(d, as_stream(stream));
+  return entry_done(run_gemm(d, as_stream(stream)), as_stream(stream));
 }
 
 int talos_gemm_batched_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
@@ -1483,7 +1483,7 @@ int talos_gemm_batched_f32(int transA, int transB, int M, int N, int K, float al
   d.alpha = alpha;
   d.beta = beta;
   d.ksplit = 0;
-  return run_gemm(d, as_stream(stream));
+  return entry_done(run_gemm(d, as_stream(stream)), as_stream(stream));
 }
 
 }  // extern "C"

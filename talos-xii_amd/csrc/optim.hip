@@ -177,7 +177,7 @@ int talos_grad_sumsq_f32(size_t n, const float* grads, int accumulate, double* s
   if (int rc = ws.acquire(grad_sumsq_workspace_bytes(), s)) return rc;
   const int rc = grad_sumsq_launch(n, grads, accumulate, sumsq, static_cast<double*>(ws.ptr), s);
   const int rel = ws.release();
-  return rc ? rc : rel;
+  return entry_done(rc ? rc : rel, as_stream(stream));
 }
 
 int talos_adam_step_f32(size_t n, float* params, const float* grads, float* m, float* v, int t, double lr,
@@ -194,7 +194,8 @@ int talos_adam_step_f32(size_t n, float* params, const float* grads, float* m, f
   TALOS_NONNULL(m);
   TALOS_NONNULL(v);
   TALOS_DEVICE();
-  return adam_launch(n, params, grads, m, v, t, lr, beta1, beta2, eps, sumsq, max_norm, as_stream(stream));
+  const int rc = adam_launch(n, params, grads, m, v, t, lr, beta1, beta2, eps, sumsq, max_norm, as_stream(stream));
+  return entry_done(rc, as_stream(stream));
 }
 
 }  // extern "C"

@@ -2051,7 +2051,7 @@ int talos_block_fwd_bwd_f32(talos_plan plan, const float* params, const float* x
   if (out) TALOS_HIP(hipMemcpyAsync(out, L.out, M * d * 4, hipMemcpyDeviceToDevice, s));
   rc = block_backward(plan, c, params, dparams, bo, L, gout, dx, s);
   if (rc) return rc;
-  return join_side(plan, s);
+  return entry_done(join_side(plan, s), as_stream(stream));
 }
 
 int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
@@ -2148,7 +2148,7 @@ int talos_ppo_forward_n_f32(talos_plan plan, int n, const float* params, const f
   if (logits)
     TALOS_HIP(hipMemcpyAsync(logits, plan->logits, (size_t)n * c.n_actions * 4, hipMemcpyDeviceToDevice, s));
   if (values) TALOS_HIP(hipMemcpyAsync(values, plan->values, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
 }
 
 int talos_ppo_forward_f32(talos_plan plan, const float* params, const float* states, float* logits, float* values,
@@ -2380,8 +2380,9 @@ int talos_ppo_minibatch_f32(talos_plan plan, int n, const float* params, const f
   TALOS_DEVICE();
   PlanCall pc(plan);
   LensScope ls(plan, lengths);
-  return ppo_minibatch(plan, n, params, states, actions, adv, ret, old_logp, loss, dparams, stats, stats_accumulate,
-                       as_stream(stream));
+  const int rc = ppo_minibatch(plan, n, params, states, actions, adv, ret, old_logp, loss, dparams, stats,
+                               stats_accumulate, as_stream(stream));
+  return entry_done(rc, as_stream(stream));
 }
 
 int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* states, const int32_t* actions,
@@ -2390,6 +2391,54 @@ int talos_ppo_fwd_bwd_f32(talos_plan plan, const float* params, const float* sta
   TALOS_REQUIRE(plan != nullptr && plan->kind == 2, TALOS_ERR_HANDLE, "%s: not a ppo plan", __func__);
   return talos_ppo_minibatch_f32(plan, plan->ppo.batch, params, states, nullptr, actions, adv, ret, old_logp,
                                  loss_out, dparams, nullptr, 0, stream);
+}
+
+static int ppo_head_loss(const char* fn, int n, int A, float clip_eps, float cv, float ce, const float* logits,
+                         const float* values, const int32_t* actions, const float* adv, const float* ret,
+                         const float* old_logp, float* loss, double* stats, int stats_acc, float* dlogits,
+                         float* dvalues, talos_stream_t stream) {
+  TALOS_REQUIRE(n >= 0 && A > 0, TALOS_ERR_SHAPE, "%s: bad shape n=%d n_actions=%d", fn, n, A);
+  TALOS_REQUIRE(clip_eps >= 0.f, TALOS_ERR_SHAPE, "%s: clip_eps must be >= 0", fn);
+  TALOS_REQUIRE(stats_acc == 0 || stats_acc == 1, TALOS_ERR_SHAPE, "%s: stats_accumulate must be 0 or 1", fn);
+  TALOS_REQUIRE(n == 0 || (logits && values && actions && adv && ret && old_logp), TALOS_ERR_NULL,
+                "%s: null input", fn);
+  TALOS_DEVICE();
+  const hipStream_t s = as_stream(stream);
+  // an empty minibatch: the mean over no samples (NaN, as 0.0 / 0 in the reference's f64), no gradient
+  const int nblk = (int)std::max<size_t>(1, ceil_div((size_t)n, 256));
+  EntryScratch ws;
+  int rc = ws.acquire((size_t)nblk * kLossParts * sizeof(double), s);
+  if (rc) return rc;
+  double* part = static_cast<double*>(ws.ptr);
+  const int with_grad = dlogits != nullptr;
+  hipLaunchKernelGGL(ppo_loss_kernel, dim3(nblk), dim3(256), 0, s, n, A, clip_eps, cv, ce, logits, values, actions,
+                     adv, ret, old_logp, dlogits, dvalues, with_grad, part);
+  rc = launch_status("ppo_loss_kernel");
+  if (!rc && (loss || stats)) {
+    hipLaunchKernelGGL(ppo_loss_final_kernel, dim3(1), dim3(64), 0, s, nblk, n, part, loss, stats, stats_acc);
+    rc = launch_status("ppo_loss_final_kernel");
+  }
+  const int rel = ws.release();
+  return entry_done(rc ? rc : rel, s);
+}
+
+int talos_ppo_head_loss_fwd_f32(int n, int n_actions, float clip_eps, float value_coef, float entropy_coef,
+                                const float* logits, const float* values, const int32_t* actions, const float* adv,
+                                const float* ret, const float* old_logp, float* loss, double* stats,
+                                int stats_accumulate, talos_stream_t stream) {
+  TALOS_REQUIRE(loss || stats, TALOS_ERR_NULL, "%s: loss and stats are both null", __func__);
+  return ppo_head_loss(__func__, n, n_actions, clip_eps, value_coef, entropy_coef, logits, values, actions, adv, ret,
+                       old_logp, loss, stats, stats_accumulate, nullptr, nullptr, stream);
+}
+
+int talos_ppo_head_loss_bwd_f32(int n, int n_actions, float clip_eps, float value_coef, float entropy_coef,
+                                const float* logits, const float* values, const int32_t* actions, const float* adv,
+                                const float* ret, const float* old_logp, float* dlogits, float* dvalues, float* loss,
+                                talos_stream_t stream) {
+  TALOS_NONNULL(dlogits);
+  TALOS_NONNULL(dvalues);
+  return ppo_head_loss(__func__, n, n_actions, clip_eps, value_coef, entropy_coef, logits, values, actions, adv, ret,
+                       old_logp, loss, nullptr, 0, dlogits, dvalues, stream);
 }
 
 size_t talos_mla_param_count(const talos_mla_cfg* cfg) { return cfg ? mla_offsets(*cfg).end : 0; }
@@ -2447,7 +2496,7 @@ int talos_mla_fwd_bwd_f32(talos_plan plan, const float* params, const float* x, 
   TALOS_NONNULL(dx);
   TALOS_DEVICE();
   PlanCall pc(plan);
-  return mla_fwd_bwd(plan, params, x, gout, out, dparams, dx, as_stream(stream));
+  return entry_done(mla_fwd_bwd(plan, params, x, gout, out, dparams, dx, as_stream(stream)), as_stream(stream));
 }
 
 int talos_plan_profiler(talos_plan plan, talos_profiler* prof) {

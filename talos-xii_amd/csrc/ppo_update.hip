@@ -174,8 +174,9 @@ int talos_ppo_gae_f64(int len, const double* rewards, const double* values, cons
   TALOS_NONNULL(adv);
   TALOS_NONNULL(ret);
   TALOS_DEVICE();
-  return gae_launch(len, rewards, values, terminals, r_mean, r_var, r_clip, gamma, lambda, adv, ret, adv_raw,
-                    as_stream(stream));
+  const int rc = gae_launch(len, rewards, values, terminals, r_mean, r_var, r_clip, gamma, lambda, adv, ret, adv_raw,
+                            as_stream(stream));
+  return entry_done(rc, as_stream(stream));
 }
 
 size_t talos_ppo_update_work_bytes(talos_plan plan, int n) {
@@ -243,7 +244,7 @@ int talos_ppo_update_f32(talos_plan plan, talos_ppo_update_args* a, talos_ppo_up
   }
   a->adam_t = t;
   if (result) *result = res;
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
 }
 
 }  // extern "C"

@@ -610,6 +610,42 @@ __global__ void unary_bwd_kernel(int op, size_t n, float p0, float p1, const flo
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
     dx[i] += unary_d(op, x[i], p0, p1) * dy[i];
 }
+// GELU (y = x Phi(x)) and its backward (dx = beta dx + dy (Phi(x) + x phi(x))), HBM-bound: 8 bytes
+// per element forward, 12 (beta 0) or 16 (beta 1) backward. vec: n % 4 == 0 and every pointer
+// 16-byte aligned, so each thread moves float4s; otherwise one element per thread.
+template <bool BWD>
+__global__ __launch_bounds__(256) void gelu_kernel(size_t n, float beta, const float* __restrict__ x,
+                                                   const float* __restrict__ dy, float* __restrict__ out, int vec) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (vec) {
+    for (; i < n / 4; i += stride) {
+      const float4 v = reinterpret_cast<const float4*>(x)[i];
+      float4 r;
+      if (BWD) {
+        const float4 g = reinterpret_cast<const float4*>(dy)[i];
+        r = make_float4(gelu_d(v.x) * g.x, gelu_d(v.y) * g.y, gelu_d(v.z) * g.z, gelu_d(v.w) * g.w);
+        if (beta != 0.f) {
+          const float4 o = reinterpret_cast<const float4*>(out)[i];
+          r = make_float4(o.x + r.x, o.y + r.y, o.z + r.z, o.w + r.w);
+        }
+      } else {
+        r = make_float4(gelu_f(v.x), gelu_f(v.y), gelu_f(v.z), gelu_f(v.w));
+      }
+      reinterpret_cast<float4*>(out)[i] = r;
+    }
+    return;
+  }
+  for (; i < n; i += stride) {
+    if (BWD) {
+      const float r = gelu_d(x[i]) * dy[i];
+      out[i] = beta != 0.f ? out[i] + r : r;
+    } else {
+      out[i] = gelu_f(x[i]);
+    }
+  }
+}
+
 __global__ void binary_fwd_kernel(int op, size_t n, const float* __restrict__ a, const float* __restrict__ b,
                                   float* __restrict__ y) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
@@ -733,7 +769,7 @@ extern "C" {
 int talos_fill_zero(void* dst, size_t bytes, talos_stream_t stream) {
   TALOS_NONNULL(dst);
   TALOS_DEVICE();
-  return fill_zero(dst, bytes, as_stream(stream));
+  return entry_done(fill_zero(dst, bytes, as_stream(stream)), as_stream(stream));
 }
 
 int talos_bias_grad_f32(int rows, int cols, const float* dy, float beta, float* db, talos_stream_t stream) {
@@ -748,7 +784,7 @@ int talos_bias_grad_f32(int rows, int cols, const float* dy, float beta, float* 
   if (rc) return rc;
   rc = colsum_launch(rows, cols, dy, cols, beta, db, static_cast<double*>(ws.ptr), s);
   const int rel = ws.release();
-  return rc ? rc : rel;
+  return entry_done(rc ? rc : rel, as_stream(stream));
 }
 
 int talos_rmsnorm_fwd_f32(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
@@ -759,7 +795,7 @@ int talos_rmsnorm_fwd_f32(int rows, int dim, float eps, const float* x, const fl
   TALOS_REQUIRE(rows >= 0 && dim > 0, TALOS_ERR_SHAPE, "%s: bad shape rows=%d dim=%d", __func__, rows, dim);
   TALOS_REQUIRE(eps >= 0.f, TALOS_ERR_SHAPE, "%s: eps must be >= 0", __func__);
   TALOS_DEVICE();
-  return rmsnorm_fwd_launch(rows, dim, eps, x, w, y, rstd, as_stream(stream));
+  return entry_done(rmsnorm_fwd_launch(rows, dim, eps, x, w, y, rstd, as_stream(stream)), as_stream(stream));
 }
 
 int talos_rmsnorm_bwd_f32(int rows, int dim, const float* x, const float* w, const float* rstd, const float* dy,
@@ -779,7 +815,7 @@ int talos_rmsnorm_bwd_f32(int rows, int dim, const float* x, const float* w, con
   if (rc) return rc;
   rc = rmsnorm_bwd_launch(rows, dim, x, w, rstd, dy, beta_dx, dx, beta_dw, dw, static_cast<double*>(ws.ptr), s);
   const int rel = ws.release();
-  return rc ? rc : rel;
+  return entry_done(rc ? rc : rel, as_stream(stream));
 }
 
 int talos_softmax_fwd_f32(int rows, int cols, int causal, const float* x, float* y, talos_stream_t stream) {
@@ -792,7 +828,7 @@ int talos_softmax_fwd_f32(int rows, int cols, int causal, const float* x, float*
   hipLaunchKernelGGL(softmax_fwd_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, as_stream(stream), rows, cols, causal,
                      x, y);
   TALOS_LAUNCHED("softmax_fwd_kernel");
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
 }
 
 int talos_softmax_bwd_f32(int rows, int cols, int causal, const float* y, const float* dy, float beta, float* dx,
@@ -810,7 +846,7 @@ int talos_softmax_bwd_f32(int rows, int cols, int causal, const float* y, const 
   hipLaunchKernelGGL(softmax_bwd_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, as_stream(stream), rows, cols, causal,
                      y, dy, beta, dx, vec);
   TALOS_LAUNCHED("softmax_bwd_kernel");
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
 }
 
 static int check_rope(const char* fn, int n_seq, int seq_len, int heads, int dim, int start_pos, float base) {
@@ -831,7 +867,7 @@ int talos_rope_fwd_f32(int n_seq, int seq_len, int heads, int dim, int start_pos
   const float *c, *s;
   rc = rope_table_device(start_pos + seq_len, dim, base, &c, &s);
   if (rc) return rc;
-  return rope_launch(n_seq, seq_len, heads, dim, start_pos, c, s, x, 0.f, y, false, as_stream(stream));
+  return entry_done(rope_launch(n_seq, seq_len, heads, dim, start_pos, c, s, x, 0.f, y, false, as_stream(stream)), as_stream(stream));
 }
 
 int talos_rope_bwd_f32(int n_seq, int seq_len, int heads, int dim, int start_pos, float base, const float* dy,
@@ -845,7 +881,7 @@ int talos_rope_bwd_f32(int n_seq, int seq_len, int heads, int dim, int start_pos
   const float *c, *s;
   rc = rope_table_device(start_pos + seq_len, dim, base, &c, &s);
   if (rc) return rc;
-  return rope_launch(n_seq, seq_len, heads, dim, start_pos, c, s, dy, beta, dx, true, as_stream(stream));
+  return entry_done(rope_launch(n_seq, seq_len, heads, dim, start_pos, c, s, dy, beta, dx, true, as_stream(stream)), as_stream(stream));
 }
 
 int talos_rope_table_f32(int max_len, int dim, float base, float* cos_out, float* sin_out, talos_stream_t stream) {
@@ -859,7 +895,7 @@ int talos_rope_table_f32(int max_len, int dim, float base, float* cos_out, float
   TALOS_HIP(hipMemcpyAsync(cos_out, c.data(), c.size() * 4, hipMemcpyHostToDevice, as_stream(stream)));
   TALOS_HIP(hipMemcpyAsync(sin_out, s.data(), s.size() * 4, hipMemcpyHostToDevice, as_stream(stream)));
   TALOS_HIP(hipStreamSynchronize(as_stream(stream)));
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
 }
 
 int talos_unary_fwd_f32(int op, size_t n, float p0, float p1, const float* x, float* y, talos_stream_t stream) {
@@ -870,7 +906,7 @@ int talos_unary_fwd_f32(int op, size_t n, float p0, float p1, const float* x, fl
   if (n == 0) return TALOS_OK;
   hipLaunchKernelGGL(unary_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), op, n, p0, p1, x, y);
   TALOS_LAUNCHED("unary_fwd_kernel");
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
 }
 
 int talos_unary_bwd_f32(int op, size_t n, float p0, float p1, const float* x, const float* dy, float* dx,
@@ -883,7 +919,37 @@ int talos_unary_bwd_f32(int op, size_t n, float p0, float p1, const float* x, co
   if (n == 0) return TALOS_OK;
   hipLaunchKernelGGL(unary_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), op, n, p0, p1, x, dy, dx);
   TALOS_LAUNCHED("unary_bwd_kernel");
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
+}
+
+static int gelu_launch(bool bwd, size_t n, float beta, const float* x, const float* dy, float* out,
+                       hipStream_t s) {
+  const int vec = n % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy) |
+                                  reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  const unsigned grid = grid_for(vec ? n / 4 : n);
+  if (bwd)
+    hipLaunchKernelGGL(gelu_kernel<true>, dim3(grid), dim3(256), 0, s, n, beta, x, dy, out, vec);
+  else
+    hipLaunchKernelGGL(gelu_kernel<false>, dim3(grid), dim3(256), 0, s, n, beta, x, dy, out, vec);
+  return launch_status(bwd ? "gelu_kernel<true>" : "gelu_kernel<false>");
+}
+
+int talos_gelu_fwd_f32(size_t n, const float* x, float* y, talos_stream_t stream) {
+  TALOS_NONNULL(x);
+  TALOS_NONNULL(y);
+  TALOS_DEVICE();
+  if (n == 0) return TALOS_OK;
+  return entry_done(gelu_launch(false, n, 0.f, x, nullptr, y, as_stream(stream)), as_stream(stream));
+}
+
+int talos_gelu_bwd_f32(size_t n, const float* x, const float* dy, float beta, float* dx, talos_stream_t stream) {
+  TALOS_NONNULL(x);
+  TALOS_NONNULL(dy);
+  TALOS_NONNULL(dx);
+  TALOS_REQUIRE(beta == 0.f || beta == 1.f, TALOS_ERR_UNSUPPORTED, "%s: beta must be 0 or 1", __func__);
+  TALOS_DEVICE();
+  if (n == 0) return TALOS_OK;
+  return entry_done(gelu_launch(true, n, beta, x, dy, dx, as_stream(stream)), as_stream(stream));
 }
 
 int talos_binary_fwd_f32(int op, size_t n, const float* a, const float* b, float* y, talos_stream_t stream) {
@@ -895,7 +961,7 @@ int talos_binary_fwd_f32(int op, size_t n, const float* a, const float* b, float
   if (n == 0) return TALOS_OK;
   hipLaunchKernelGGL(binary_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), op, n, a, b, y);
   TALOS_LAUNCHED("binary_fwd_kernel");
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
 }
 
 int talos_binary_bwd_f32(int op, size_t n, const float* a, const float* b, const float* dy, float* da, float* db,
@@ -909,7 +975,7 @@ int talos_binary_bwd_f32(int op, size_t n, const float* a, const float* b, const
   if (n == 0) return TALOS_OK;
   hipLaunchKernelGGL(binary_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), op, n, a, b, dy, da, db);
   TALOS_LAUNCHED("binary_bwd_kernel");
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
 }
 
 int talos_reduce_sum_f32(size_t n, float scale, const float* x, float* out, talos_stream_t stream) {
@@ -929,7 +995,7 @@ int talos_reduce_sum_f32(size_t n, float scale, const float* x, float* out, talo
     rc = launch_status("reduce_final_kernel");
   }
   const int rel = scratch.release();
-  return rc ? rc : rel;
+  return entry_done(rc ? rc : rel, as_stream(stream));
 }
 
 int talos_fill_add_f32(size_t n, float scale, const float* g, float* dx, talos_stream_t stream) {
@@ -939,7 +1005,7 @@ int talos_fill_add_f32(size_t n, float scale, const float* g, float* dx, talos_s
   if (n == 0) return TALOS_OK;
   hipLaunchKernelGGL(fill_add_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), n, scale, g, dx);
   TALOS_LAUNCHED("fill_add_kernel");
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
 }
 
 int talos_transpose_f32(int rank, const long long* shape, int dim0, int dim1, const float* x, float* y, int accumulate,
@@ -970,7 +1036,7 @@ int talos_transpose_f32(int rank, const long long* shape, int dim0, int dim1, co
   std::swap(ts.stride_in[dim0], ts.stride_in[dim1]);
   hipLaunchKernelGGL(transpose_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), n, ts, x, y, accumulate);
   TALOS_LAUNCHED("transpose_kernel");
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
 }
 
 int talos_concat_last_f32(size_t rows, int ca, int cb, const float* a, const float* b, float* out,
@@ -984,7 +1050,7 @@ int talos_concat_last_f32(size_t rows, int ca, int cb, const float* a, const flo
   hipLaunchKernelGGL(concat_kernel, dim3(grid_for(rows * (ca + cb))), dim3(256), 0, as_stream(stream), rows, ca, cb, a,
                      b, out);
   TALOS_LAUNCHED("concat_kernel");
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
 }
 
 int talos_concat_last_bwd_f32(size_t rows, int ca, int cb, const float* dout, float* da, float* db,
@@ -995,7 +1061,7 @@ int talos_concat_last_bwd_f32(size_t rows, int ca, int cb, const float* dout, fl
   TALOS_REQUIRE(ca >= 0 && cb >= 0, TALOS_ERR_SHAPE, "%s: negative width", __func__);
   TALOS_DEVICE();
   // the reference's closure accumulates into both parents (src/transformer.rs:1162-1179)
-  return split_launch(rows, ca, cb, dout, da, db, true, as_stream(stream));
+  return entry_done(split_launch(rows, ca, cb, dout, da, db, true, as_stream(stream)), as_stream(stream));
 }
 
 int talos_broadcast_rows_f32(size_t rows, int cols, const float* v, float* out, talos_stream_t stream) {
@@ -1007,7 +1073,7 @@ int talos_broadcast_rows_f32(size_t rows, int cols, const float* v, float* out, 
   hipLaunchKernelGGL(broadcast_rows_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, as_stream(stream), rows, cols, v,
                      out);
   TALOS_LAUNCHED("broadcast_rows_kernel");
-  return TALOS_OK;
+  return entry_done(TALOS_OK, as_stream(stream));
 }
 
 }  // extern "C"

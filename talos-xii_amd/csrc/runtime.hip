@@ -31,6 +31,14 @@ int hip_status(hipError_t e, const char* what) {
   return TALOS_ERR_HIP;
 }
 
+// Per-thread completion mode of the kernel entry points (false: synchronous, the default).
+static thread_local bool t_async = false;
+
+int entry_done(int rc, hipStream_t s) {
+  if (rc != TALOS_OK || t_async) return rc;
+  return hip_status(hipStreamSynchronize(s), "kernel entry (synchronous mode): hipStreamSynchronize");
+}
+
 int launch_status(const char* kernel) {
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) return TALOS_OK;
@@ -273,6 +281,14 @@ int talos_memcpy_d2h_f64(double* dst, const float* src, size_t n, talos_stream_t
   for (size_t i = 0; i < n; ++i) dst[i] = (double)tmp[i];
   return TALOS_OK;
 }
+
+int talos_set_async(int on) {
+  TALOS_REQUIRE(on == 0 || on == 1, TALOS_ERR_SHAPE, "%s: on must be 0 or 1", __func__);
+  t_async = on != 0;
+  return TALOS_OK;
+}
+
+int talos_get_async(void) { return t_async ? 1 : 0; }
 
 int talos_stream_sync(talos_stream_t stream) {
   TALOS_DEVICE();

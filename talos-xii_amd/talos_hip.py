@@ -92,6 +92,8 @@ _SIGS = {
     "talos_memcpy_d2h_f64": [_vp, _vp, _sz, _vp],
     "talos_fill_zero": [_vp, _sz, _vp],
     "talos_stream_sync": [_vp],
+    "talos_set_async": [_i],
+    "talos_get_async": [],
     "talos_stream_create": [ctypes.POINTER(_vp)],
     "talos_stream_destroy": [_vp],
     "talos_event_create": [ctypes.POINTER(_vp)],
@@ -117,6 +119,8 @@ _SIGS = {
                                    _i, _vp, _i, _vp, _i, _vp],
     "talos_unary_fwd_f32": [_i, _sz, _f, _f, _vp, _vp, _vp],
     "talos_unary_bwd_f32": [_i, _sz, _f, _f, _vp, _vp, _vp, _vp],
+    "talos_gelu_fwd_f32": [_sz, _vp, _vp, _vp],
+    "talos_gelu_bwd_f32": [_sz, _vp, _vp, _f, _vp, _vp],
     "talos_binary_fwd_f32": [_i, _sz, _vp, _vp, _vp, _vp],
     "talos_binary_bwd_f32": [_i, _sz, _vp, _vp, _vp, _vp, _vp, _vp],
     "talos_reduce_sum_f32": [_sz, _f, _vp, _vp, _vp],
@@ -138,6 +142,8 @@ _SIGS = {
     "talos_ppo_forward_f32": [_vp, _vp, _vp, _vp, _vp, _vp],
     "talos_ppo_forward_n_f32": [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp],
     "talos_ppo_minibatch_f32": [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp],
+    "talos_ppo_head_loss_fwd_f32": [_i, _i, _f, _f, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp],
+    "talos_ppo_head_loss_bwd_f32": [_i, _i, _f, _f, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "talos_ppo_gae_f64": [_i, _vp, _vp, _vp, _d, _d, _d, _d, _d, _vp, _vp, _vp, _vp],
     "talos_ppo_update_work_bytes": [_vp, _i],
     "talos_ppo_update_f32": [_vp, ctypes.c_void_p, ctypes.c_void_p, _vp],
@@ -339,6 +345,21 @@ class DeviceArray:
 
 def sync():
     call("talos_stream_sync", None)
+
+
+class async_mode:
+    """Context manager: the calling thread's kernel entries return once their work is enqueued
+    (talos_set_async(1)) inside the block; the previous mode is restored on exit. The default
+    mode is synchronous."""
+
+    def __enter__(self):
+        self.prev = lib().talos_get_async()
+        call("talos_set_async", 1)
+        return self
+
+    def __exit__(self, *exc):
+        call("talos_set_async", self.prev)
+        return False
 
 
 class Plan:

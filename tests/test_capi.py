@@ -170,3 +170,35 @@ def test_workspace_bind_validation():
     assert L.talos_workspace_bind(ctypes.c_void_p(4096), 4096) == th.OK
     assert L.talos_workspace_high_water() == 0
     assert L.talos_workspace_bind(None, 0) == th.OK
+
+
+def test_completion_mode_switch():
+    # synchronous by default (the reference's ops return finished results); per thread
+    L = th.lib()
+    assert L.talos_get_async() == 0
+    assert L.talos_set_async(2) == th.ERR_SHAPE
+    with th.async_mode():
+        assert L.talos_get_async() == 1
+        seen = []
+        import threading
+        t = threading.Thread(target=lambda: seen.append(L.talos_get_async()))
+        t.start()
+        t.join()
+        assert seen == [0]  # another thread keeps its own (default) mode
+    assert L.talos_get_async() == 0
+
+
+def test_gelu_and_head_loss_argument_errors(L):
+    p = ctypes.c_void_p(16)
+    assert L.talos_gelu_fwd_f32(4, None, p, None) == th.ERR_NULL
+    assert L.talos_gelu_bwd_f32(4, p, p, 0.5, p, None) == th.ERR_UNSUPPORTED
+    assert L.talos_gelu_bwd_f32(4, p, None, 0.0, p, None) == th.ERR_NULL
+    args = (0.2, 0.5, 0.01, p, p, p, p, p, p)
+    assert L.talos_ppo_head_loss_fwd_f32(4, 3, *args, None, None, 0, None) == th.ERR_NULL  # no output
+    assert L.talos_ppo_head_loss_fwd_f32(-1, 3, *args, p, None, 0, None) == th.ERR_SHAPE
+    assert L.talos_ppo_head_loss_fwd_f32(4, 0, *args, p, None, 0, None) == th.ERR_SHAPE
+    assert L.talos_ppo_head_loss_fwd_f32(4, 3, -0.1, 0.5, 0.01, p, p, p, p, p, p, p, None, 0, None) == th.ERR_SHAPE
+    assert L.talos_ppo_head_loss_fwd_f32(4, 3, *args, p, None, 2, None) == th.ERR_SHAPE
+    assert L.talos_ppo_head_loss_fwd_f32(4, 3, 0.2, 0.5, 0.01, p, None, p, p, p, p, p, None, 0, None) == th.ERR_NULL
+    assert L.talos_ppo_head_loss_bwd_f32(4, 3, *args, None, p, None, None) == th.ERR_NULL
+    assert L.talos_ppo_head_loss_bwd_f32(4, 3, *args, p, None, None, None) == th.ERR_NULL

@@ -422,3 +422,134 @@ def test_gemm_bf16acc_split_k():
     ref = Xb.T @ Gb
     scale = np.abs(Xb).T @ np.abs(Gb)
     assert np.all(np.abs(dC.numpy() - ref) <= 1e-6 * scale + 1e-6)
+
+
+@pytest.mark.parametrize("n,off", [(1 << 16, 0), (4097, 0), (4096, 1)])
+def test_gelu_entries(oracle, n, off):
+    """talos_gelu_{fwd,bwd}_f32 against the oracle's gelu and its gradient, on the float4 path
+    (n % 4 == 0, aligned) and the one-element path (ragged n, or pointers offset by one element),
+    and bit-exact against the TALOS_GELU op of the unary entries (the same device function)."""
+    rng = np.random.default_rng(31 + n + off)
+    x, g, d0 = (f32(rng.normal(size=n) * s) for s in (3.0, 1.0, 1.0))
+    t = oracle.T.new(x, [n])
+    y = t.gelu()
+    y.sum().backward()
+    dref = np.asarray(t.grad)  # gelu'(x) in f64
+    bufs = [DA.zeros(n + off) for _ in range(5)]
+    X, G, Y, DX, DU = (b.offset(off) for b in bufs)
+    for buf, a in ((bufs[0], x), (bufs[1], g), (bufs[3], d0)):
+        buf.upload(np.concatenate([np.zeros(off, np.float32), a]))
+    th.call("talos_gelu_fwd_f32", n, X, Y, None)
+    check_close(bufs[2].numpy()[off:], y.data, name="gelu")
+    th.call("talos_gelu_bwd_f32", n, X, G, 1.0, DX, None)  # accumulate into d0
+    check_close(bufs[3].numpy()[off:], d0.astype(np.float64) + dref * g, name="gelu' (beta 1)")
+    th.call("talos_gelu_bwd_f32", n, X, G, 0.0, DX, None)  # overwrite
+    got = bufs[3].numpy()[off:]
+    check_close(got, dref * g, name="gelu' (beta 0)")
+    th.call("talos_unary_fwd_f32", th.GELU, n, 0.0, 0.0, X, DU, None)
+    assert np.array_equal(bufs[4].numpy()[off:], bufs[2].numpy()[off:])
+    bufs[4].upload(np.zeros(n + off, np.float32))
+    th.call("talos_unary_bwd_f32", th.GELU, n, 0.0, 0.0, X, G, DU, None)
+    assert np.array_equal(bufs[4].numpy()[off:], got)
+
+
+def test_gelu_entries_c3_size():
+    """At the MLP activation size of C3 ([32768, 512]) the float4 entries equal the unary op bit
+    for bit (the oracle-checked function); every output is finite."""
+    n = 32768 * 512
+    rng = np.random.default_rng(5)
+    x = f32(rng.normal(size=n) * 2)
+    X, Y, U = DA.from_numpy(x), DA.zeros(n), DA.zeros(n)
+    th.call("talos_gelu_fwd_f32", n, X.ptr, Y.ptr, None)
+    th.call("talos_unary_fwd_f32", th.GELU, n, 0.0, 0.0, X.ptr, U.ptr, None)
+    y, u = Y.numpy(), U.numpy()
+    assert np.isfinite(y).all() and np.array_equal(y, u)
+
+
+def _log_softmax(z):
+    z = z.astype(np.float64)
+    m = z.max(axis=1, keepdims=True)
+    return z - m - np.log(np.exp(z - m).sum(axis=1, keepdims=True))
+
+
+@pytest.mark.parametrize("n,A", [(1000, 3), (257, 7), (64, 40), (1, 1)])
+def test_ppo_head_loss_entries(oracle, n, A):
+    """talos_ppo_head_loss_{fwd,bwd}_f32 against the oracle's batched PPO loss graph (pinned
+    against the per-sample graph of ppo.rs:702-749): loss, dlogits and dvalues; old log-probs
+    spread so that samples fall inside and outside the clip range; stats sums add up to the loss
+    and accumulate on a second call."""
+    rng = np.random.default_rng(7 * n + A)
+    logits = f32(rng.normal(size=(n, A)) * 1.5)
+    values, ret, adv = (f32(rng.normal(size=n)) for _ in range(3))
+    actions = rng.integers(0, A, n).astype(np.int32)
+    lp = _log_softmax(logits)[np.arange(n), actions]
+    old = f32(lp + rng.normal(scale=0.3, size=n))
+    clip, cv, ce = 0.2, 0.5, 0.01
+    cfg = oracle.PpoCfg(n, 1, 1, 1, 0, 1, 1, 1, A, 0, 0, 1e-5, 1e4, clip, cv, ce)
+    ref_loss, ref_dl, ref_dv = oracle.ppo_batched_loss(cfg, logits, values, actions, old, adv, ret)
+    Z, V, Ad, R, O = (DA.from_numpy(a) for a in (logits, values, adv, ret, old))
+    Ac = DA.from_numpy(actions, np.int32)
+    loss, stats = DA.zeros(1), DA.zeros(5, np.float64)
+    th.call("talos_ppo_head_loss_fwd_f32", n, A, clip, cv, ce, Z.ptr, V.ptr, Ac.ptr, Ad.ptr, R.ptr, O.ptr,
+            loss.ptr, stats.ptr, 0, None)
+    check_close(loss.numpy(), [ref_loss], name="loss")
+    st = stats.numpy()
+    assert st[4] == n
+    assert abs((-st[1] + cv * st[2] - ce * st[3]) / n - ref_loss) <= 1e-9 * max(1.0, abs(ref_loss))
+    th.call("talos_ppo_head_loss_fwd_f32", n, A, clip, cv, ce, Z.ptr, V.ptr, Ac.ptr, Ad.ptr, R.ptr, O.ptr,
+            None, stats.ptr, 1, None)
+    assert np.allclose(stats.numpy(), 2 * st, rtol=1e-12, atol=0)
+    DZ, DV, loss2 = DA.from_numpy(np.full((n, A), 7.0)), DA.from_numpy(np.full(n, 7.0)), DA.zeros(1)
+    th.call("talos_ppo_head_loss_bwd_f32", n, A, clip, cv, ce, Z.ptr, V.ptr, Ac.ptr, Ad.ptr, R.ptr, O.ptr,
+            DZ.ptr, DV.ptr, loss2.ptr, None)
+    check_close(DZ.numpy(), ref_dl, name="dlogits")
+    check_close(DV.numpy(), ref_dv, name="dvalues")
+    assert loss2.numpy()[0] == loss.numpy()[0]
+
+
+def test_ppo_head_loss_ratio_one_closed_form():
+    """With old_logp equal to the current log-probability the ratio is exactly 1, both surrogates
+    equal adv, and the loss reduces to mean(-adv + cv (v - ret)^2 - ce H)."""
+    n, A = 48, 3
+    rng = np.random.default_rng(2)
+    logits = f32(rng.normal(size=(n, A)))
+    values, ret, adv = (f32(rng.normal(size=n)) for _ in range(3))
+    actions = (np.arange(n) % A).astype(np.int32)
+    old = f32(_log_softmax(logits)[np.arange(n), actions])  # ratio 1 for every sample
+    Z, V, Ad, R, O = (DA.from_numpy(a) for a in (logits, values, adv, ret, old))
+    Ac = DA.from_numpy(actions, np.int32)
+    loss = DA.zeros(1)
+    th.call("talos_ppo_head_loss_fwd_f32", n, A, 0.2, 0.5, 0.01, Z.ptr, V.ptr, Ac.ptr, Ad.ptr, R.ptr, O.ptr,
+            loss.ptr, None, 0, None)
+    # ratio == 1: the surrogate is adv (both branches), so the loss has a closed form
+    z = _log_softmax(logits)
+    ent = -(np.exp(z) * z).sum(axis=1)
+    closed = np.mean(-adv.astype(np.float64) + 0.5 * (values.astype(np.float64) - ret) ** 2 - 0.01 * ent)
+    check_close(loss.numpy(), [closed], name="loss at ratio 1")
+
+
+def test_async_mode_gives_the_same_results():
+    """The asynchronous completion mode (talos_set_async(1)) enqueues the same work: a GEMM chain
+    run in it and read after talos_stream_sync equals the default synchronous run bit for bit."""
+    rng = np.random.default_rng(12)
+    a, b = f32(rng.normal(size=(300, 200))), f32(rng.normal(size=(200, 130)))
+    A, B = DA.from_numpy(a), DA.from_numpy(b)
+    outs = []
+    for mode in (0, 1):
+        C, D = DA.zeros((300, 130)), DA.zeros((300, 130))
+        th.call("talos_set_async", mode)
+        try:
+            th.call("talos_gemm_f32", 0, 0, 300, 130, 200, 1.0, A.ptr, 200, B.ptr, 130, 0.0, C.ptr, 130, None)
+            th.call("talos_gelu_fwd_f32", 300 * 130, C.ptr, D.ptr, None)
+            th.call("talos_stream_sync", None)
+        finally:
+            th.call("talos_set_async", 0)
+        outs.append(D.numpy())
+    assert np.array_equal(outs[0], outs[1])
+    check_close(outs[0], np.asarray(oracle_free_gelu(ref_gemm(0, 0, a, b))), rtol=1e-4, atol=1e-4, name="gelu(AB)")
+
+
+def oracle_free_gelu(v):
+    from scipy.special import erf
+    v = np.asarray(v, np.float64)
+    return 0.5 * v * (1.0 + erf(v / np.sqrt(2.0)))
