@@ -232,24 +232,28 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_generic(int rows, int dim, fl
   for (int c = lane; c < dim; c += 64) y[(long long)row * dim + c] = xr[c] * r * w[c];
 }
 
-// Backward: a bounded grid (at most kMaxParts workgroups) strides over the rows, one row per wave
-// at a time; each lane keeps its columns' dgain sums in registers, so a workgroup writes a single
-// f64 partial row that reduce_parts_kernel combines.
-constexpr int kRmsMaxBlocks = 2048;  // 8 waves per CU in flight; 2048 x dim f64 partials
+// Backward: a bounded grid of 16-wave workgroups strides over the rows, one row per wave up to
+// 16 * kRmsMaxBlocks rows, and beyond that kRmsRowsPerWave rows of a wave's stride class per pass
+// (their loads in flight together). Each lane keeps its columns' dgain sums in registers; a
+// workgroup adds its 16 waves' sums in LDS in a fixed order and writes one f64 partial row, which
+// reduce_parts_kernel combines. (The generic kernel runs 4-wave workgroups on the same grid.)
+constexpr int kRmsWaves = 16, kRmsThreads = 64 * kRmsWaves;
+constexpr int kRmsRowsPerWave = 2;
+constexpr int kRmsMaxBlocks = 1024;  // 4 workgroups per CU; 1024 x dim f64 partials at most
 static int rms_bwd_blocks(int rows) {
-  int b = (rows + 3) / 4;
+  int b = (rows + kRmsWaves - 1) / kRmsWaves;
   return b < 1 ? 1 : (b > kRmsMaxBlocks ? kRmsMaxBlocks : b);
 }
 
 template <int V>
-__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(int rows, int dim, const float* __restrict__ x,
+__global__ __launch_bounds__(kRmsThreads) void rmsnorm_bwd_kernel(int rows, int dim, const float* __restrict__ x,
                                                           const float* __restrict__ w,
                                                           const float* __restrict__ rstd,
                                                           const float* __restrict__ dy, const float* add,
                                                           float* dx, double* __restrict__ dw_part,
                                                           const float* __restrict__ add_last, int seq,
                                                           const int32_t* __restrict__ lens) {
-  __shared__ float red[4][V * 256];
+  __shared__ float red[kRmsWaves][V * 256];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   float4 gw[V], dwacc[V];
 #pragma unroll
@@ -259,52 +263,70 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(int rows, int dim, con
     dwacc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   const float inv_dim = 1.0f / (float)dim;
-  for (int row = blockIdx.x * 4 + wv; row < rows; row += gridDim.x * 4) {
-    const float r = rstd[row];
-    const float* xr = x + (long long)row * dim;
-    const float* gr = dy + (long long)row * dim;
-    float4 xh[V], gg[V];
-    float dot = 0.f;
+  const int stride = gridDim.x * kRmsWaves;
+  // kRmsRowsPerWave rows per pass, all of their loads issued before the first row is reduced
+  for (int row0 = blockIdx.x * kRmsWaves + wv; row0 < rows; row0 += kRmsRowsPerWave * stride) {
+    float4 xh[kRmsRowsPerWave][V], gg[kRmsRowsPerWave][V];
+    float r[kRmsRowsPerWave];
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-      const int c = 4 * lane + 256 * j;
-      if (c < dim) {
-        const float4 xv = *reinterpret_cast<const float4*>(xr + c);
-        gg[j] = *reinterpret_cast<const float4*>(gr + c);
-        xh[j] = make_float4(xv.x * r, xv.y * r, xv.z * r, xv.w * r);
-      } else {
-        gg[j] = xh[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < kRmsRowsPerWave; ++k) {
+      const int row = row0 + k * stride;
+      const bool live = row < rows;
+      r[k] = live ? rstd[row] : 0.f;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int c = 4 * lane + 256 * j;
+        if (live && c < dim) {
+          xh[k][j] = *reinterpret_cast<const float4*>(x + (long long)row * dim + c);
+          gg[k][j] = *reinterpret_cast<const float4*>(dy + (long long)row * dim + c);
+        } else {
+          xh[k][j] = gg[k][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
       }
-      dot += gg[j].x * gw[j].x * xh[j].x + gg[j].y * gw[j].y * xh[j].y + gg[j].z * gw[j].z * xh[j].z +
-             gg[j].w * gw[j].w * xh[j].w;
-      dwacc[j].x += gg[j].x * xh[j].x;
-      dwacc[j].y += gg[j].y * xh[j].y;
-      dwacc[j].z += gg[j].z * xh[j].z;
-      dwacc[j].w += gg[j].w * xh[j].w;
     }
-    const float md = wave_sum(dot) * inv_dim;
-    float* dxr = dx + (long long)row * dim;
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-      const int c = 4 * lane + 256 * j;
-      if (c < dim) {
-        float4 o = make_float4(r * (gg[j].x * gw[j].x - xh[j].x * md), r * (gg[j].y * gw[j].y - xh[j].y * md),
-                               r * (gg[j].z * gw[j].z - xh[j].z * md), r * (gg[j].w * gw[j].w - xh[j].w * md));
-        if (add) {
-          const float4 old = *reinterpret_cast<const float4*>(add + (long long)row * dim + c);
-          o.x += old.x;
-          o.y += old.y;
-          o.z += old.z;
-          o.w += old.w;
+    for (int k = 0; k < kRmsRowsPerWave; ++k) {
+      const int row = row0 + k * stride;
+      if (row >= rows) break;
+      const float rk = r[k];
+      float dot = 0.f;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        float4& h = xh[k][j];
+        const float4 g = gg[k][j];
+        h = make_float4(h.x * rk, h.y * rk, h.z * rk, h.w * rk);
+        dot += g.x * gw[j].x * h.x + g.y * gw[j].y * h.y + g.z * gw[j].z * h.z + g.w * gw[j].w * h.w;
+        dwacc[j].x += g.x * h.x;
+        dwacc[j].y += g.y * h.y;
+        dwacc[j].z += g.z * h.z;
+        dwacc[j].w += g.w * h.w;
+      }
+      const float md = wave_sum(dot) * inv_dim;
+      float* dxr = dx + (long long)row * dim;
+      const bool last = add_last && row % seq == last_row(lens, row / seq, seq);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int c = 4 * lane + 256 * j;
+        if (c < dim) {
+          const float4 h = xh[k][j], g = gg[k][j];
+          float4 o = make_float4(rk * (g.x * gw[j].x - h.x * md), rk * (g.y * gw[j].y - h.y * md),
+                                 rk * (g.z * gw[j].z - h.z * md), rk * (g.w * gw[j].w - h.w * md));
+          if (add) {
+            const float4 old = *reinterpret_cast<const float4*>(add + (long long)row * dim + c);
+            o.x += old.x;
+            o.y += old.y;
+            o.z += old.z;
+            o.w += old.w;
+          }
+          if (last) {
+            const float4 ex = *reinterpret_cast<const float4*>(add_last + (long long)(row / seq) * dim + c);
+            o.x += ex.x;
+            o.y += ex.y;
+            o.z += ex.z;
+            o.w += ex.w;
+          }
+          *reinterpret_cast<float4*>(dxr + c) = o;
         }
-        if (add_last && row % seq == last_row(lens, row / seq, seq)) {
-          const float4 ex = *reinterpret_cast<const float4*>(add_last + (long long)(row / seq) * dim + c);
-          o.x += ex.x;
-          o.y += ex.y;
-          o.z += ex.z;
-          o.w += ex.w;
-        }
-        *reinterpret_cast<float4*>(dxr + c) = o;
       }
     }
   }
@@ -312,8 +334,10 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(int rows, int dim, con
 #pragma unroll
   for (int j = 0; j < V; ++j) *reinterpret_cast<float4*>(&red[wv][4 * lane + 256 * j]) = dwacc[j];
   __syncthreads();
-  for (int c = threadIdx.x; c < dim; c += 256) {
-    const double s = (double)red[0][c] + (double)red[1][c] + (double)red[2][c] + (double)red[3][c];
+  for (int c = threadIdx.x; c < dim; c += kRmsThreads) {
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < kRmsWaves; ++i) s += (double)red[i][c];
     dw_part[(long long)blockIdx.x * dim + c] = s;
   }
 }
@@ -391,11 +415,12 @@ int rmsnorm_bwd_launch(int rows, int dim, const float* x, const float* w, const 
                  8.0 * rows * dim, 4.0 * ((3.0 + (add != nullptr)) * rows * dim + dim + rows) +
                                        (part ? 8.0 * nblk * dim : 0.0));
     const int sq = seq > 0 ? seq : 1;
+    const dim3 bv(kRmsThreads);
     if (vec && dim <= 256)
-      hipLaunchKernelGGL(rmsnorm_bwd_kernel<1>, g, b, 0, s, rows, dim, x, w, rstd, dy, add, dx, part, dres_last, sq,
+      hipLaunchKernelGGL(rmsnorm_bwd_kernel<1>, g, bv, 0, s, rows, dim, x, w, rstd, dy, add, dx, part, dres_last, sq,
                          lens);
     else if (vec && dim <= 512)
-      hipLaunchKernelGGL(rmsnorm_bwd_kernel<2>, g, b, 0, s, rows, dim, x, w, rstd, dy, add, dx, part, dres_last, sq,
+      hipLaunchKernelGGL(rmsnorm_bwd_kernel<2>, g, bv, 0, s, rows, dim, x, w, rstd, dy, add, dx, part, dres_last, sq,
                          lens);
     else
       hipLaunchKernelGGL(rmsnorm_bwd_generic, g, b, 0, s, rows, dim, x, w, rstd, dy, add, dx, part, dres_last, sq,
@@ -430,6 +455,48 @@ __global__ __launch_bounds__(256) void softmax_fwd_kernel(int rows, int cols, in
 
 // dx = beta*dx + y * (g - sum(g*y)); masked entries (y = 0) get exactly 0 and are not read.
 // Vector path: each lane owns float4 groups; a group entirely past the causal limit is skipped.
+// Single-pass backward for rows of at most 256 * V columns on the float4 path: a lane keeps its
+// columns' y and dy in registers, so each is read from memory once; keys past the causal limit
+// are neither read nor summed (dx there is 0 plus the accumulated old value).
+template <int V>
+__global__ __launch_bounds__(256) void softmax_bwd_rows_kernel(int rows, int cols, int causal,
+                                                               const float* __restrict__ y,
+                                                               const float* __restrict__ dy, float beta,
+                                                               float* __restrict__ dx) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lim = causal ? (row % cols) + 1 : cols;
+  const long long base = (long long)row * cols;
+  float4 yv[V], gv[V], old[V];
+  float dot = 0.f;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int c = 4 * lane + 256 * j;
+    yv[j] = gv[j] = old[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c < lim) {
+      yv[j] = *reinterpret_cast<const float4*>(y + base + c);
+      gv[j] = *reinterpret_cast<const float4*>(dy + base + c);
+      // entries at or past lim are masked: drop them from the dot product and the output
+      if (c + 1 >= lim) yv[j].y = gv[j].y = 0.f;
+      if (c + 2 >= lim) yv[j].z = gv[j].z = 0.f;
+      if (c + 3 >= lim) yv[j].w = gv[j].w = 0.f;
+    }
+    if (beta != 0.f && c < cols) old[j] = *reinterpret_cast<const float4*>(dx + base + c);
+    dot += yv[j].x * gv[j].x + yv[j].y * gv[j].y + yv[j].z * gv[j].z + yv[j].w * gv[j].w;
+  }
+  dot = wave_sum(dot);
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int c = 4 * lane + 256 * j;
+    if (c < cols) {
+      const float4 o = make_float4(yv[j].x * (gv[j].x - dot) + old[j].x, yv[j].y * (gv[j].y - dot) + old[j].y,
+                                   yv[j].z * (gv[j].z - dot) + old[j].z, yv[j].w * (gv[j].w - dot) + old[j].w);
+      *reinterpret_cast<float4*>(dx + base + c) = o;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void softmax_bwd_kernel(int rows, int cols, int causal, const float* __restrict__ y,
                                                           const float* __restrict__ dy, float beta,
                                                           float* __restrict__ dx, int vec) {
@@ -555,10 +622,47 @@ int rope_table_device(int need_len, int dim, float base, const float** cosv, con
   return TALOS_OK;
 }
 
+// Two interleaved pairs (four consecutive elements) per thread for dim % 4 == 0 with 16-byte
+// aligned rows: one float4 of x, one float2 each of the cos / sin table (pairs i, i + 1 of the
+// same position), 32-bit index arithmetic (the launcher checks the element count fits).
+__global__ __launch_bounds__(256) void rope4_kernel(unsigned n4, int seq, int heads, int dim, int start_pos,
+                                                    float sign, const float* __restrict__ cosv,
+                                                    const float* __restrict__ sinv, const float* __restrict__ x,
+                                                    float beta, float* __restrict__ y) {
+  const unsigned q = blockIdx.x * 256u + threadIdx.x;
+  if (q >= n4) return;
+  const unsigned per_row = (unsigned)dim >> 2;  // float4s per (token, head) row
+  const unsigned row = q / per_row;
+  const int i = 2 * (int)(q - row * per_row);  // first pair of the four elements
+  const int t = (int)((row / (unsigned)heads) % (unsigned)seq);
+  const int ci = (start_pos + t) * (dim >> 1) + i;
+  const float2 c = *reinterpret_cast<const float2*>(cosv + ci);
+  const float2 sn = *reinterpret_cast<const float2*>(sinv + ci);
+  const float s0 = sign * sn.x, s1 = sign * sn.y;
+  const float4 v = reinterpret_cast<const float4*>(x)[q];
+  float4 o = make_float4(v.x * c.x - v.y * s0, v.x * s0 + v.y * c.x, v.z * c.y - v.w * s1, v.z * s1 + v.w * c.y);
+  if (beta != 0.f) {
+    const float4 old = reinterpret_cast<const float4*>(y)[q];
+    o.x += old.x;
+    o.y += old.y;
+    o.z += old.z;
+    o.w += old.w;
+  }
+  reinterpret_cast<float4*>(y)[q] = o;
+}
+
 int rope_launch(int n_seq, int seq, int heads, int dim, int start_pos, const float* cosv, const float* sinv,
                 const float* x, float beta, float* y, bool backward, hipStream_t s) {
   const long long npairs = (long long)n_seq * seq * heads * (dim / 2);
   if (npairs == 0) return TALOS_OK;
+  const long long n4 = npairs / 2;
+  if (dim % 4 == 0 && n4 < (1LL << 31) &&
+      ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0) {
+    hipLaunchKernelGGL(rope4_kernel, dim3((unsigned)ceil_div((size_t)n4, 256)), dim3(256), 0, s, (unsigned)n4, seq,
+                       heads, dim, start_pos, backward ? -1.f : 1.f, cosv, sinv, x, beta, y);
+    TALOS_LAUNCHED("rope4_kernel");
+    return TALOS_OK;
+  }
   hipLaunchKernelGGL(rope_kernel, dim3(grid_for((size_t)npairs)), dim3(256), 0, s, npairs, seq, heads, dim,
                      start_pos, backward ? -1.f : 1.f, cosv, sinv, x, beta, y);
   TALOS_LAUNCHED("rope_kernel");
@@ -843,10 +947,18 @@ int talos_softmax_bwd_f32(int rows, int cols, int causal, const float* y, const 
   if (rows == 0) return TALOS_OK;
   const int vec = cols % 4 == 0 && ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(dy) |
                                      reinterpret_cast<uintptr_t>(dx)) & 15) == 0;
-  hipLaunchKernelGGL(softmax_bwd_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, as_stream(stream), rows, cols, causal,
-                     y, dy, beta, dx, vec);
-  TALOS_LAUNCHED("softmax_bwd_kernel");
-  return entry_done(TALOS_OK, as_stream(stream));
+  const hipStream_t s = as_stream(stream);
+  const dim3 g(ceil_div(rows, 4)), b(256);
+  if (vec && cols <= 256)
+    hipLaunchKernelGGL(softmax_bwd_rows_kernel<1>, g, b, 0, s, rows, cols, causal, y, dy, beta, dx);
+  else if (vec && cols <= 512)
+    hipLaunchKernelGGL(softmax_bwd_rows_kernel<2>, g, b, 0, s, rows, cols, causal, y, dy, beta, dx);
+  else if (vec && cols <= 1024)
+    hipLaunchKernelGGL(softmax_bwd_rows_kernel<4>, g, b, 0, s, rows, cols, causal, y, dy, beta, dx);
+  else
+    hipLaunchKernelGGL(softmax_bwd_kernel, g, b, 0, s, rows, cols, causal, y, dy, beta, dx, vec);
+  TALOS_LAUNCHED("softmax_bwd");
+  return entry_done(TALOS_OK, s);
 }
 
 static int check_rope(const char* fn, int n_seq, int seq_len, int heads, int dim, int start_pos, float base) {

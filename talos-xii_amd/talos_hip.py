@@ -409,6 +409,80 @@ class Plan:
             pass
 
 
+_hip = None
+
+
+def hip_runtime():
+    """The HIP runtime library the extension is linked against (for graph capture)."""
+    global _hip
+    if _hip is None:
+        lib()  # loads libamdhip64 as a dependency of the extension
+        H = ctypes.CDLL("libamdhip64.so", mode=ctypes.RTLD_GLOBAL)
+        for name, args in {"hipStreamBeginCapture": [_vp, _i], "hipStreamEndCapture": [_vp, ctypes.POINTER(_vp)],
+                           "hipGraphInstantiate": [ctypes.POINTER(_vp), _vp, _vp, _vp, _sz],
+                           "hipGraphLaunch": [_vp, _vp], "hipGraphExecDestroy": [_vp], "hipGraphDestroy": [_vp],
+                           "hipMemcpyAsync": [_vp, _vp, _sz, _i, _vp]}.items():
+            fn = getattr(H, name)
+            fn.argtypes = args
+            fn.restype = _i
+        _hip = H
+    return _hip
+
+
+def _hip_check(rc, what):
+    if rc != 0:
+        raise TalosError(ERR_HIP, f"{what} failed with hipError_t {rc}")
+
+
+def stream_create():
+    """A non-blocking stream at the default priority (talos_stream_create); free it with
+    stream_destroy."""
+    h = _vp()
+    call("talos_stream_create", ctypes.byref(h))
+    return h.value
+
+
+def stream_destroy(h):
+    call("talos_stream_destroy", h)
+
+
+class Graph:
+    """A HIP graph captured from the work fn() enqueues on `stream` (a talos_stream_create
+    stream). The library's entries are captured in their asynchronous mode (synchronous entries
+    would wait on a capturing stream); fn must not allocate, so a caller-owned workspace should
+    be bound (talos_workspace_bind) for entries that need scratch memory."""
+
+    def __init__(self, stream, fn):
+        H = hip_runtime()
+        self.stream = stream
+        self.exec = None
+        with async_mode():
+            _hip_check(H.hipStreamBeginCapture(stream, 1), "hipStreamBeginCapture")  # thread-local mode
+            try:
+                fn()
+            finally:
+                g = _vp()
+                rc = H.hipStreamEndCapture(stream, ctypes.byref(g))
+            _hip_check(rc, "hipStreamEndCapture")
+        self.graph = g.value
+        e = _vp()
+        _hip_check(H.hipGraphInstantiate(ctypes.byref(e), self.graph, None, None, 0), "hipGraphInstantiate")
+        self.exec = e.value
+
+    def launch(self):
+        _hip_check(hip_runtime().hipGraphLaunch(self.exec, self.stream), "hipGraphLaunch")
+
+    def __del__(self):
+        try:
+            if _hip is not None:
+                if self.exec:
+                    _hip.hipGraphExecDestroy(self.exec)
+                if getattr(self, "graph", None):
+                    _hip.hipGraphDestroy(self.graph)
+        except Exception:
+            pass
+
+
 class Timer:
     """HIP events on a stream (the stream the measured kernels are launched on)."""
 

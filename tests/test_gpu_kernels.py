@@ -553,3 +553,49 @@ def oracle_free_gelu(v):
     from scipy.special import erf
     v = np.asarray(v, np.float64)
     return 0.5 * v * (1.0 + erf(v / np.sqrt(2.0)))
+
+
+def test_graph_capture_of_entries_replays_exactly():
+    """The kernel entries captured into a HIP graph in the asynchronous mode (with a bound
+    workspace, so nothing allocates) replay to the eager results bit for bit, three times, with
+    eager work that scribbles over the outputs between the replays; the captured entries record
+    fill kernels, not memset nodes."""
+    rng = np.random.default_rng(21)
+    R, C = 2048, 256
+    x, dy = f32(rng.normal(size=(R, C))), f32(rng.normal(size=(R, C)))
+    w = f32(rng.uniform(0.9, 1.1, C))
+    rstd = f32(1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(1) + 1e-6))
+    sm = np.exp(rng.normal(size=(R, C)))
+    sm = f32(sm / sm.sum(1, keepdims=True))
+    a, b = f32(rng.normal(size=(4096, 96))), f32(rng.normal(size=(4096, 80)))
+    X, DY, W, RS, SM, A, B = (DA.from_numpy(v) for v in (x, dy, w, rstd, sm, a, b))
+    DX, DW, DS, G, WG = DA.zeros((R, C)), DA.zeros(C), DA.zeros((R, C)), DA.zeros((R, C)), DA.zeros((96, 80))
+    outs = (DX, DW, DS, G, WG)
+    ws = DA.zeros(1 << 20)
+    stream = th.stream_create()
+
+    def work():
+        th.call("talos_rmsnorm_bwd_f32", R, C, X.ptr, W.ptr, RS.ptr, DY.ptr, 0.0, DX.ptr, 0.0, DW.ptr, stream)
+        th.call("talos_softmax_bwd_f32", R, C, 1, SM.ptr, DY.ptr, 0.0, DS.ptr, stream)
+        th.call("talos_gelu_fwd_f32", R * C, DX.ptr, G.ptr, stream)
+        # a weight-gradient product over 4096 rows (split over K, partials in the workspace)
+        th.call("talos_gemm_f32", 1, 0, 96, 80, 4096, 1.0, A.ptr, 96, B.ptr, 80, 0.0, WG.ptr, 80, stream)
+
+    th.call("talos_workspace_bind", ws.ptr, 4 << 20)
+    try:
+        work()
+        th.call("talos_stream_sync", stream)
+        eager = [o.numpy() for o in outs]
+        graph = th.Graph(stream, work)
+        for rep in range(3):
+            for o in outs:  # eager work between the replays
+                o.upload(np.full(o.shape, np.nan, np.float32))
+            graph.launch()
+            th.call("talos_stream_sync", stream)
+            for o, e in zip(outs, eager):
+                assert np.array_equal(o.numpy(), e), f"replay {rep}"
+        del graph
+    finally:
+        th.call("talos_workspace_bind", None, 0)
+        th.stream_destroy(stream)
+    check_close(eager[4], ref_gemm(1, 0, a, b), rtol=1e-4, atol=1e-3, name="captured wgrad")
