@@ -268,13 +268,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_
 
 // Forward for S <= 32 at head dims 32 / 32 with 16-byte rows: one key block, so a wave's q, k and
 // v rows are all in flight before the first product and the softmax needs no running rescale.
-// Same arithmetic as attn_fwd_kernel's single-block pass.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_FWD_WAVES))) void
-attn_fwd_s32_kernel(AttnArgs a) {
+// Same arithmetic as attn_fwd_kernel's single-block pass. s32_pair is one wave's (batch, head)
+// pair: it stores O and the row logsumexp and returns O in accumulator layout (register r <->
+// query acc_row(r, h), lane <-> column l32).
+__device__ __forceinline__ floatx16 s32_pair(const AttnArgs& a, int pair, int l32, int h) {
   constexpr int KH = 16;
-  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
-  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (pair >= a.B * a.H) return;  // uniform per wave
   const int b = pair / a.H, hd = pair % a.H;
   const long long tok0 = (long long)b * a.S;
   const int q = l32;
@@ -315,13 +313,91 @@ attn_fwd_s32_kernel(AttnArgs a) {
     const float p = (m == kNegInf) ? 0.f : expf(sv[s] - m) * inv_l;
     oacc = __builtin_amdgcn_mfma_f32_32x32x2f32(p, vm[s], oacc, 0, 0, 0);
   }
-  // O in accumulator layout: register r <-> query acc_row(r, h), lane <-> column
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int qr = acc_row(r, h);
     if (qr < a.S) a.o[(tok0 + qr) * a.ldo + hd * a.dv + l32] = oacc[r];
   }
   if (h == 0 && q < a.S) a.lse[(long long)pair * a.S + q] = (l > 0.f) ? m + logf(l) : kNegInf;
+  return oacc;
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_FWD_WAVES))) void
+attn_fwd_s32_kernel(AttnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pair >= a.B * a.H) return;  // uniform per wave
+  (void)s32_pair(a, pair, lane & 31, lane >> 5);
+}
+
+// The attention output projection, its residual and the next RMSNorm fused behind the S <= 32
+// attention of four 32-wide heads (d = 128): h2 = x + O.Wo, xn = rmsnorm(h2) * gain, rstd (the
+// first product of the block's MLP half and its norm epilogue, in the order the GEMM epilogue
+// adds them). A workgroup is one batch entry: its four waves are the entry's four heads, whose O
+// blocks meet in LDS as the entry's [32, 128] attention output; wave w then forms the columns
+// [32 w, 32 w + 32) of O.Wo with v_mfma_f32_32x32x2f32 (A = O rows from LDS, B = Wo rows from
+// memory, both walking k in the same order 8j + 4h + q), and after a second pass through LDS each
+// wave takes eight whole token rows for the residual, the row norm and the coalesced stores.
+constexpr int kWoD = 128, kWoP = kWoD + 4;
+struct WoArgs {
+  const float* wo;     // [128, 128], row k = input feature
+  const float* resid;  // x, rows of 128
+  float* h2;
+  const float* gain;
+  float* xn;
+  float* rstd;
+  float eps;
+};
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_FWD_WAVES))) void
+attn_fwd_s32_wo_kernel(AttnArgs a, WoArgs w) {
+  __shared__ __align__(16) float T[32 * kWoP];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int b = blockIdx.x;
+  const long long tok0 = (long long)b * a.S;
+  const floatx16 oacc = s32_pair(a, b * 4 + wv, l32, h);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) T[acc_row(r, h) * kWoP + wv * 32 + l32] = oacc[r];
+  __syncthreads();
+  const int n = wv * 32 + l32;
+  floatx16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll 4
+  for (int j = 0; j < kWoD / 8; ++j) {
+    const float4 o4 = *reinterpret_cast<const float4*>(T + l32 * kWoP + 8 * j + 4 * h);
+    const float* wr = w.wo + (long long)(8 * j + 4 * h) * kWoD + n;
+    const float w0 = wr[0], w1 = wr[kWoD], w2 = wr[2 * kWoD], w3 = wr[3 * kWoD];
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(o4.x, w0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(o4.y, w1, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(o4.z, w2, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(o4.w, w3, acc, 0, 0, 0);
+  }
+  __syncthreads();  // every wave has read the O rows
+#pragma unroll
+  for (int r = 0; r < 16; ++r) T[acc_row(r, h) * kWoP + n] = acc[r];
+  __syncthreads();
+  // rows: wave wv takes tokens 8 wv .. 8 wv + 7, lane the columns 2 lane, 2 lane + 1
+  float2 res[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int t = wv * 8 + i;
+    res[i] = t < a.S ? *reinterpret_cast<const float2*>(w.resid + (tok0 + t) * kWoD + 2 * lane)
+                     : make_float2(0.f, 0.f);
+  }
+  const float2 g = *reinterpret_cast<const float2*>(w.gain + 2 * lane);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int t = wv * 8 + i;
+    if (t >= a.S) break;  // uniform per wave
+    const float2 pv = *reinterpret_cast<const float2*>(T + t * kWoP + 2 * lane);
+    const float2 v = make_float2(pv.x + res[i].x, pv.y + res[i].y);
+    const long long row = tok0 + t;
+    *reinterpret_cast<float2*>(w.h2 + row * kWoD + 2 * lane) = v;
+    const float ss = wave_sum(v.x * v.x + v.y * v.y);
+    const float r = 1.0f / sqrtf(ss / (float)kWoD + w.eps);
+    *reinterpret_cast<float2*>(w.xn + row * kWoD + 2 * lane) = make_float2(v.x * r * g.x, v.y * r * g.y);
+    if (lane == 0 && w.rstd) w.rstd[row] = r;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1215,6 +1291,30 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
     return TALOS_ERR_UNSUPPORTED;
   }
   ATTN_ALL(attn_fwd_kernel)
+}
+
+int attn_fwd_wo_supported(const AttnDesc& d, const AttnWoDesc& w) {
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  return d.dk == 32 && d.dv == 32 && d.heads == 4 && d.seq >= 1 && d.seq <= 32 && d.ldo == kWoD &&
+         w.wo != nullptr && w.resid != nullptr && w.h2 != nullptr && w.gain != nullptr && w.xn != nullptr &&
+         al(w.wo) && al(w.resid) && al(w.h2) && al(w.gain) && al(w.xn) && make_args(d, 32, 32).vec;
+}
+
+int attn_fwd_wo_launch(const AttnDesc& d, const AttnWoDesc& wd, hipStream_t s) {
+  if (!attn_fwd_wo_supported(d, wd)) {
+    set_error("attention + Wo: the fused kernel takes S <= 32, four 32-wide heads, d = 128 and aligned rows");
+    return TALOS_ERR_UNSUPPORTED;
+  }
+  AttnArgs a = make_args(d, 32, 32);
+  if (a.B == 0) return TALOS_OK;
+  WoArgs w{wd.wo, wd.resid, wd.h2, wd.gain, wd.xn, wd.rstd, wd.eps};
+  const double rows = (double)a.B * a.S * a.H, tok = (double)a.B * a.S;
+  const double flops = kept_pairs(a) * (2.0 * a.dk + 2.0 * a.dv) + 2.0 * tok * kWoD * kWoD;
+  // q, k, v, x read; o, lse, h2, xn, rstd written (Wo from cache)
+  const double bytes = 4.0 * rows * (2.0 * a.dk + a.dv) + 4.0 * rows * (a.dv + 1.0) + 4.0 * tok * (3.0 * kWoD + 1.0);
+  ProfScope ps(s, "attn_fwd_s32_wo_kernel", flops, bytes);
+  hipLaunchKernelGGL(attn_fwd_s32_wo_kernel, dim3(a.B), dim3(256), 0, s, a, w);
+  return launch_status("attn_fwd_s32_wo_kernel");
 }
 
 size_t attn_bwd_workspace_bytes(const AttnDesc& d) {

@@ -47,6 +47,21 @@ struct AttnDesc {
 
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s);
 
+// The attention forward fused with the output projection, its residual and the following
+// RMSNorm (S <= 32, four 32-wide heads, d = 128, o rows of 128): besides o and lse it writes
+// h2 = resid + o.Wo, xn = rmsnorm(h2) * gain and rstd (optional), all rows of 128 floats.
+struct AttnWoDesc {
+  const float* wo = nullptr;  // [128, 128], row = input feature
+  const float* resid = nullptr;
+  float* h2 = nullptr;
+  const float* gain = nullptr;
+  float* xn = nullptr;
+  float* rstd = nullptr;
+  float eps = 1e-5f;
+};
+int attn_fwd_wo_supported(const AttnDesc& d, const AttnWoDesc& w);
+int attn_fwd_wo_launch(const AttnDesc& d, const AttnWoDesc& w, hipStream_t s);
+
 // Attention of the last query row of each batch entry only (row lens[b] - 1, or seq - 1), over all
 // of that entry's keys: o_last / do_last are [batch, heads * dv] with row strides ldol / lddol,
 // lse_last is [batch * heads]. The backward takes dO on that row only and writes every row of

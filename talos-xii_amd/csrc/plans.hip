@@ -708,10 +708,10 @@ static int block_attn_forward(talos_plan_s* p, const talos_block_cfg& c, const f
 // out = h2 + a.W2 + b2, followed by the next row norm when next is set.
 static int block_mlp_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o, int R,
                              const float* x, const float* ob, float* h2, float* xn2, float* rstd2, float* u, float* a,
-                             float* out, hipStream_t s, const RowNorm& next = RowNorm{}) {
+                             float* out, hipStream_t s, const RowNorm& next = RowNorm{}, bool wo_done = false) {
   const int d = c.d_model, F = c.ffn_dim, ow = attn_width(c);
   int rc;
-  {
+  if (!wo_done) {  // (wo_done: the attention kernel already wrote h2, xn2 and rstd2)
     GemmDesc g;
     g.M = R;
     g.N = d;
@@ -767,12 +767,27 @@ static int block_mlp_forward(talos_plan_s* p, const talos_block_cfg& c, const fl
 
 // Forward of one block; L.x must be set (and L.xn1 / L.rstd1 when normed). Writes L.out, and the
 // next row norm of L.out when next is set.
+constexpr int kWoFuseD = 128;  // the model width attn_fwd_wo_launch takes
+
+// At S <= 32 with four 32-wide heads and d = 128 (C4's blocks) the attention kernel also forms
+// h2 = x + o.Wo and its RMSNorm (attn_fwd_wo_launch), and the MLP half starts at W1.
 static int block_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
                          talos_plan_s::Layer& L, hipStream_t s, bool normed = false,
                          const RowNorm& next = RowNorm{}) {
-  int rc = block_attn_forward(p, c, P, o, L, s, normed);
-  if (rc) return rc;
-  return block_mlp_forward(p, c, P, o, c.batch * c.seq, L.x, L.o, L.h2, L.xn2, L.rstd2, L.u, L.a, L.out, s, next);
+  bool wo_done = false;
+  int rc;
+  if (c.attention == TALOS_ATTN_MHA && !p->unfused && !p->bf16 && c.d_model == kWoFuseD && attn_width(c) == kWoFuseD) {
+    const AttnWoDesc wd{P + o.wo, L.x, L.h2, P + o.g2, L.xn2, L.rstd2, c.eps};
+    const AttnDesc ad = block_attn_desc(p, c, L);
+    if (attn_fwd_wo_supported(ad, wd)) {
+      if ((rc = block_qkv_forward(p, c, P, o, L, s, normed))) return rc;
+      if ((rc = attn_fwd_wo_launch(ad, wd, s))) return rc;
+      wo_done = true;
+    }
+  }
+  if (!wo_done && (rc = block_attn_forward(p, c, P, o, L, s, normed))) return rc;
+  return block_mlp_forward(p, c, P, o, c.batch * c.seq, L.x, L.o, L.h2, L.xn2, L.rstd2, L.u, L.a, L.out, s, next,
+                           wo_done);
 }
 
 // MLP half backward over R rows: gout = dL/dout; writes the W2 / W1 / gain2 gradients, the

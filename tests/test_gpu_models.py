@@ -37,10 +37,13 @@ def run_block(cfg, p, x, G):
 
 
 # head dims 6 and 10 (not multiples of 4): the RoPE epilogue's interleaved pairs straddle the
-# float4 column groups and the heads, so each pair must take its own head's table entry
+# float4 column groups and the heads, so each pair must take its own head's table entry.
+# S <= 32 with four 32-wide heads at d 128 (causal and not) runs the attention kernel that also
+# forms o.Wo, the residual and RMSNorm2.
 @pytest.mark.parametrize("B,S,d,H,F,causal,act", [(2, 6, 16, 4, 64, 1, 0), (3, 64, 128, 4, 512, 1, 0),
                                                   (2, 33, 64, 2, 128, 0, 1), (2, 5, 24, 4, 48, 1, 0),
-                                                  (3, 9, 40, 4, 80, 0, 1)])
+                                                  (3, 9, 40, 4, 80, 0, 1), (3, 23, 128, 4, 256, 0, 0),
+                                                  (2, 32, 128, 4, 512, 1, 1)])
 def test_block_fwd_bwd_vs_oracle(oracle, B, S, d, H, F, causal, act):
     rng = np.random.default_rng(1000 + S + d)
     cfg = th.BlockCfg(B, S, d, H, d // H, F, causal, act, 1e-6, 10000.0)
