@@ -1050,47 +1050,41 @@ __device__ __forceinline__ void mfma_p_lds(const float (&P)[16], const float* ti
 #define TALOS_ATTN_STAGE 1
 #endif
 
-// VEC: every row is known 16-byte aligned (a.vec), so the row loads take no branch and the five
-// operands' loads are all in flight before the first use.
-template <int DKM, int DVM, bool VEC = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BWD_WAVES))) void
-attn_bwd_fused_kernel(AttnArgs a) {
+// The per-wave LDS slice of the fused backward. STAGE (head dims 32): the dO, Q and K rows the
+// wave loads are also written to its slice, and the three P-products read them there instead of
+// re-reading global memory; the dS^T tile then reuses the dO tile. Staged tile pitch: 16-byte
+// rows; the dS^T tile (pitch kTS) spills from the dO tile into the Q tile, which is dead by then;
+// 12.5 KB per wave keeps three workgroups on a CU.
+template <int DKM, int DVM>
+struct BwdSlice {
+  static constexpr bool STAGE = TALOS_ATTN_STAGE && DKM == 32 && DVM == 32;
+  static constexpr int TP = 32;
+  static constexpr int WSZ = STAGE ? 3 * 32 * TP + 64 : 32 * kTS + 64;
+  static_assert(!STAGE || 32 * kTS <= 64 * TP, "the dS^T tile must end before the K tile");
+};
+
+// The fused backward of one (batch, head) pair once its rows are in registers (load_half layout:
+// gv = dO, ov = O, qv = scale * Q, kv = K, vv = V) with the query row's lse; W is the wave's LDS
+// slice. GS_STAGED: the dO tile already holds gv (the kernel that forms dO itself put it there).
+template <int DKM, int DVM, bool GS_STAGED>
+__device__ __forceinline__ void bwd_fused_core(const AttnArgs& a, float* W, int pair, int l32, int h,
+                                               const float (&gv)[DVM / 2], const float (&ov)[DVM / 2],
+                                               const float (&qv)[DKM / 2], const float (&kv)[DKM / 2],
+                                               const float (&vv)[DVM / 2], float lse) {
   constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32;
-  // STAGE (head dims 32): the dO, Q and K rows the wave loads are also written to its LDS slice,
-  // and the three P-products read them there instead of re-reading global memory. The dS^T tile
-  // then reuses the dO tile.
-  constexpr bool STAGE = TALOS_ATTN_STAGE && DKM == 32 && DVM == 32;
-  // staged tile pitch: 16-byte rows; the dS^T tile (pitch kTS) spills from the dO tile into the
-  // Q tile, which is dead by then; 12.5 KB per wave keeps three workgroups on a CU
-  constexpr int TP = 32;
-  constexpr int WSZ = STAGE ? 3 * 32 * TP + 64 : 32 * kTS + 64;
-  __shared__ __align__(16) float lds[4][WSZ];
-  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
-  const int pair = blockIdx.x * 4 + wv;
-  if (pair >= a.B * a.H) return;  // uniform per wave; the kernel has no workgroup barrier
+  constexpr bool STAGE = BwdSlice<DKM, DVM>::STAGE;
+  constexpr int TP = BwdSlice<DKM, DVM>::TP;
   const int b = pair / a.H, hd = pair % a.H;
   const long long tok0 = (long long)b * a.S;
-  float* const W = lds[wv];
   float* const Gs = W;             // staged dO [query][e]
   float* const Qs = W + 32 * TP;   // staged scale * Q [query][e]
   float* const Ks = W + 64 * TP;   // staged K [key][e]
   float* const T = W;              // dS^T [query][key] (pitch kTS)
-  static_assert(!STAGE || 32 * kTS <= 64 * TP, "the dS^T tile must end before the K tile");
   float* const Dl = W + (STAGE ? 96 * TP : 32 * kTS);  // D[query]
   float* const Ll = Dl + 32;                            // lse[query]
   const bool rok = l32 < a.S;             // this lane's row (query l32 of q / dO / O)
   const bool kok = l32 < key_len(a, b);   // ... and its key l32 of k / v takes part
-
-  // every row this wave reads, issued before the first use: one memory latency, not five
-  float gv[VH], ov[VH], qv[KH], kv[KH], vv[VH];
-  const bool vec = VEC || a.vec;
-  load_half<VH, kFusedSel>(gv, a.dout, a.lddo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, vec);
-  load_half<VH, kFusedSel>(ov, a.o, a.ldo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, vec);
-  load_half<KH, kFusedSel>(qv, a.q, a.ldq, tok0, l32, a.S, hd * a.dk, a.dk, h, a.scale, vec);
-  load_half<KH, kFusedSel>(kv, a.k, a.ldk, tok0, l32, a.S, hd * a.dk, a.dk, h, 1.f, vec);
-  load_half<VH, kFusedSel>(vv, a.v, a.ldv, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, vec);
-  const float lse = a.lse[(long long)pair * a.S + (rok ? l32 : 0)];
-  if constexpr (STAGE) stage_half<VH, TP>(Gs, gv, l32, h);
+  if constexpr (STAGE && !GS_STAGED) stage_half<VH, TP>(Gs, gv, l32, h);
   {
     float d0 = 0.f, d1 = 0.f;
 #pragma unroll
@@ -1190,6 +1184,91 @@ attn_bwd_fused_kernel(AttnArgs a) {
       const int e = i * 32 + l32;
       if (row < a.S && e < a.dv) a.dv_out[(tok0 + row) * a.lddv + hd * a.dv + e] = dv[i][r];
     }
+}
+
+
+// VEC: every row is known 16-byte aligned (a.vec), so the row loads take no branch and the five
+// operands' loads are all in flight before the first use.
+template <int DKM, int DVM, bool VEC = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BWD_WAVES))) void
+attn_bwd_fused_kernel(AttnArgs a) {
+  constexpr int KH = DKM / 2, VH = DVM / 2;
+  __shared__ __align__(16) float lds[4][BwdSlice<DKM, DVM>::WSZ];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int pair = blockIdx.x * 4 + wv;
+  if (pair >= a.B * a.H) return;  // uniform per wave; the kernel has no workgroup barrier
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const bool rok = l32 < a.S;
+  // every row this wave reads, issued before the first use: one memory latency, not five
+  float gv[VH], ov[VH], qv[KH], kv[KH], vv[VH];
+  const bool vec = VEC || a.vec;
+  load_half<VH, kFusedSel>(gv, a.dout, a.lddo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, vec);
+  load_half<VH, kFusedSel>(ov, a.o, a.ldo, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, vec);
+  load_half<KH, kFusedSel>(qv, a.q, a.ldq, tok0, l32, a.S, hd * a.dk, a.dk, h, a.scale, vec);
+  load_half<KH, kFusedSel>(kv, a.k, a.ldk, tok0, l32, a.S, hd * a.dk, a.dk, h, 1.f, vec);
+  load_half<VH, kFusedSel>(vv, a.v, a.ldv, tok0, l32, a.S, hd * a.dv, a.dv, h, 1.f, vec);
+  const float lse = a.lse[(long long)pair * a.S + (rok ? l32 : 0)];
+  bwd_fused_core<DKM, DVM, false>(a, lds[wv], pair, l32, h, gv, ov, qv, kv, vv, lse);
+}
+
+// The S <= 32 backward of four 32-wide heads (d = 128) with the output projection's input
+// gradient folded in: dO = dh2 . Wo^T is formed here instead of read (h2 = x + O.Wo, Wo [128,
+// 128] with row j = O's column j). A workgroup is one batch entry, its waves the entry's heads:
+// the waves load the entry's dh2 rows [32, 128] into the dO tiles of their four LDS slices
+// (wave w: columns [32 w, 32 w + 32)); after a barrier wave w forms its head's dO[t][e] =
+// sum_n dh2[t][n] Wo[32 w + e][n] with v_mfma_f32_32x32x2f32 (A = dh2 rows from the slices, B =
+// Wo rows read as float4s along n, both walking n in the order 8j + 4h + q), and after a second
+// barrier writes dO into its own dO tile and reads it back in load_half layout; from there the
+// pair's backward is attn_bwd_fused_kernel's.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BWD_WAVES))) void
+attn_bwd_s32_wo_kernel(AttnArgs a, const float* __restrict__ wo, const float* __restrict__ gh2) {
+  constexpr int TP = BwdSlice<32, 32>::TP;
+  static_assert(BwdSlice<32, 32>::STAGE, "the folded dO lives in the staged dO tile");
+  __shared__ __align__(16) float lds[4][BwdSlice<32, 32>::WSZ];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int b = blockIdx.x, pair = b * 4 + wv;
+  const long long tok0 = (long long)b * a.S;
+  const bool rok = l32 < a.S;
+  float gv[16], ov[16], qv[16], kv[16], vv[16];
+  // this wave's quarter of the dh2 rows (token l32, columns 32 wv + 16 h ..), zero past S
+  load_half<16, true>(gv, gh2, kWoD, tok0, l32, a.S, wv * 32, 32, h, 1.f, true);
+  load_half<16, true>(ov, a.o, a.ldo, tok0, l32, a.S, wv * a.dv, a.dv, h, 1.f, true);
+  load_half<16, true>(qv, a.q, a.ldq, tok0, l32, a.S, wv * a.dk, a.dk, h, a.scale, true);
+  load_half<16, true>(kv, a.k, a.ldk, tok0, l32, a.S, wv * a.dk, a.dk, h, 1.f, true);
+  load_half<16, true>(vv, a.v, a.ldv, tok0, l32, a.S, wv * a.dv, a.dv, h, 1.f, true);
+  const float lse = a.lse[(long long)pair * a.S + (rok ? l32 : 0)];
+  stage_half<16, TP>(lds[wv], gv, l32, h);
+  __syncthreads();
+  floatx16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  const float* wrow = wo + (long long)(wv * 32 + l32) * kWoD;
+#pragma unroll 4
+  for (int j = 0; j < kWoD / 8; ++j) {
+    const int n0 = 8 * j + 4 * h;  // columns n0 .. n0 + 3 of dh2 and of Wo's row
+    const float4 g4 = *reinterpret_cast<const float4*>(lds[n0 >> 5] + l32 * TP + (n0 & 31));
+    const float4 w4 = *reinterpret_cast<const float4*>(wrow + n0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(g4.x, w4.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(g4.y, w4.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(g4.z, w4.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(g4.w, w4.w, acc, 0, 0, 0);
+  }
+  __syncthreads();  // every wave has read the dh2 quarters
+  // dO in accumulator layout (register r <-> token acc_row(r, h), lane <-> e) into the dO tile
+  float* const Gs = lds[wv];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) Gs[acc_row(r, h) * TP + l32] = acc[r];
+  wave_lds_sync();
+#pragma unroll
+  for (int i = 0; i < 16; i += 4) {
+    const float4 g4 = *reinterpret_cast<const float4*>(Gs + l32 * TP + 16 * h + i);
+    gv[i] = g4.x;
+    gv[i + 1] = g4.y;
+    gv[i + 2] = g4.z;
+    gv[i + 3] = g4.w;
+  }
+  bwd_fused_core<32, 32, true>(a, lds[wv], pair, l32, h, gv, ov, qv, kv, vv, lse);
 }
 
 // ---------------------------------------------------------------------------
@@ -1315,6 +1394,30 @@ int attn_fwd_wo_launch(const AttnDesc& d, const AttnWoDesc& wd, hipStream_t s) {
   ProfScope ps(s, "attn_fwd_s32_wo_kernel", flops, bytes);
   hipLaunchKernelGGL(attn_fwd_s32_wo_kernel, dim3(a.B), dim3(256), 0, s, a, w);
   return launch_status("attn_fwd_s32_wo_kernel");
+}
+
+int attn_bwd_wo_supported(const AttnDesc& d, const float* wo, const float* gh2) {
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  return d.dk == 32 && d.dv == 32 && d.heads == 4 && d.seq >= 1 && d.seq <= 32 && d.ldo == kWoD && wo && gh2 &&
+         al(wo) && al(gh2) && d.dq && d.dk_out && d.dv_out && make_args(d, 32, 32).vec;
+}
+
+int attn_bwd_wo_launch(const AttnDesc& d, const float* wo, const float* gh2, hipStream_t s) {
+  if (!attn_bwd_wo_supported(d, wo, gh2)) {
+    set_error("attention backward + Wo: the fused kernel takes S <= 32, four 32-wide heads, d = 128 and aligned "
+              "rows");
+    return TALOS_ERR_UNSUPPORTED;
+  }
+  AttnArgs a = make_args(d, 32, 32);
+  if (a.B == 0) return TALOS_OK;
+  const double rows = (double)a.B * a.S * a.H, tok = (double)a.B * a.S;
+  // S = QK^T, dP = dO V^T, dV = P^T dO, dK = dS^T Q, dQ = dS K over the kept pairs, plus dO = dh2 Wo^T;
+  // dh2, O, Q, K, V, lse read, dQ, dK, dV written (Wo from cache)
+  const double flops = kept_pairs(a) * (4.0 * a.dk + 6.0 * a.dv) + 2.0 * tok * kWoD * kWoD;
+  const double bytes = 4.0 * tok * kWoD + 4.0 * rows * (2.0 * a.dk + 2.0 * a.dv + 1.0) + 4.0 * rows * (2.0 * a.dk + a.dv);
+  ProfScope ps(s, "attn_bwd_s32_wo_kernel", flops, bytes);
+  hipLaunchKernelGGL(attn_bwd_s32_wo_kernel, dim3(a.B), dim3(256), 0, s, a, wo, gh2);
+  return launch_status("attn_bwd_s32_wo_kernel");
 }
 
 size_t attn_bwd_workspace_bytes(const AttnDesc& d) {

@@ -76,5 +76,10 @@ size_t attn_bwd_workspace_bytes(const AttnDesc& d);
 // D = rowsum(dO * O) there; the single-block kernel of seq <= 32 forms D in registers.
 bool attn_bwd_uses_workspace(const AttnDesc& d);
 int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s);
+// The S <= 32 backward with the output projection's input gradient folded in (four 32-wide
+// heads, d = 128): dO = gh2 . Wo^T is formed in the kernel from gh2 = dL/dh2 (rows of 128) and
+// Wo ([128, 128]); d.dout is not read. Writes dq, dk, dv as attn_bwd_launch does.
+int attn_bwd_wo_supported(const AttnDesc& d, const float* wo, const float* gh2);
+int attn_bwd_wo_launch(const AttnDesc& d, const float* wo, const float* gh2, hipStream_t s);
 
 }  // namespace talos

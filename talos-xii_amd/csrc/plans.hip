@@ -795,7 +795,7 @@ static int block_forward(talos_plan_s* p, const talos_block_cfg& c, const float*
 static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
                               int R, const float* ob, const float* h2, const float* xn2, const float* rstd2,
                               const float* u, const float* a, const float* gout, float* g_u, float* g_xn, float* g_h2,
-                              float* g_o, hipStream_t s) {
+                              float* g_o, hipStream_t s, bool skip_go = false) {
   const int d = c.d_model, F = c.ffn_dim, ow = attn_width(c);
   // out = h2 + a.W2 + b2
   int rc = wgrad(p, s, gout, F, d, R, a, F, gout, d, G + o.w2, d, G + o.b2);
@@ -831,6 +831,7 @@ static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const f
   // h2 = x + o.Wo
   rc = wgrad(p, s, g_h2, ow, d, R, ob, ow, g_h2, d, G + o.wo, d);
   if (rc) return rc;
+  if (skip_go) return TALOS_OK;  // the attention backward forms g_o = g_h2.Wo^T itself
   return mm(p, s, 0, 1, R, ow, d, g_h2, d, P + o.wo, d, g_o, ow);
 }
 
@@ -881,14 +882,23 @@ static int block_attn_backward(talos_plan_s* p, const talos_block_cfg& c, const 
   return block_qkv_backward(p, c, P, G, o, L, g_h2, g_h2_last, dx, s);
 }
 
-// Backward of one block: gout = dL/dout (read), writes dparams slots and dx.
+// Backward of one block: gout = dL/dout (read), writes dparams slots and dx. Where the forward
+// fused o.Wo into the attention (S <= 32, four 32-wide heads, d = 128), the backward folds the
+// input gradient of that product, g_o = g_h2.Wo^T, into the attention backward
+// (attn_bwd_wo_launch) instead of storing g_o and reading it back.
 static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
                           talos_plan_s::Layer& L, const float* gout, float* dx, hipStream_t s) {
   const int M = c.batch * c.seq;
+  AttnDesc ad = block_attn_desc(p, c, L);
+  const bool fold = c.attention == TALOS_ATTN_MHA && !p->unfused && !p->bf16 && c.d_model == kWoFuseD &&
+                    attn_width(c) == kWoFuseD && attn_bwd_wo_supported(ad, P + o.wo, p->g_h2);
   int rc = block_mlp_backward(p, c, P, G, o, M, L.o, L.h2, L.xn2, L.rstd2, L.u, L.a, gout, p->g_u, p->g_xn, p->g_h2,
-                              p->g_o, s);
+                              p->g_o, s, fold);
   if (rc) return rc;
-  return block_attn_backward(p, c, P, G, o, L, p->g_o, p->g_h2, nullptr, dx, s);
+  if (!fold) return block_attn_backward(p, c, P, G, o, L, p->g_o, p->g_h2, nullptr, dx, s);
+  if ((rc = before_write(p, s, p->g_qkv))) return rc;
+  if ((rc = attn_bwd_wo_launch(ad, P + o.wo, p->g_h2, s))) return rc;
+  return block_qkv_backward(p, c, P, G, o, L, p->g_h2, nullptr, dx, s);
 }
 
 // Whether the PPO plan's last layer runs the attention of the last query only (standard
