@@ -82,9 +82,9 @@ __global__ __launch_bounds__(256) void colsum_partial_kernel(int rows, int cols,
 }
 
 // out[c] = beta*out[c] + sum_p part[p][c] in one pass: a workgroup takes 16 columns with 16
-// waves; lane (column lane % 16, q = lane / 16) of wave w adds partials p = 4w + q + 64i in order
-// into four f64 accumulators (i % 4, four independent loads in flight), so a wave reads four
-// 128-byte row pieces per load; the 64 sums of a column are then added in a fixed order.
+// waves; lane (column lane % 16, q = lane / 16) of wave w adds partials p = 4w + q + 64i in i
+// order with eight loads in flight, so a wave reads four 128-byte row pieces per load; the 64
+// sums of a column are then added in a fixed order.
 constexpr int kOnePassParts = 4096;
 // Columns from split on go to out2[c - split] (two gradients reduced in one launch).
 __global__ __launch_bounds__(1024) void reduce_parts_kernel(int cols, int nparts, const double* __restrict__ part,
@@ -94,25 +94,34 @@ __global__ __launch_bounds__(1024) void reduce_parts_kernel(int cols, int nparts
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int cl = lane & 15, q = lane >> 4;
   const int c = blockIdx.x * 16 + cl;
-  double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+  double acc = 0.0;
   if (c < cols) {
     const long long step = 64LL * cols;
     int p = 4 * w + q;
-    for (; p + 192 < nparts; p += 256) {
+    for (; p + 7 * 64 < nparts; p += 8 * 64) {
       const double* r = part + (long long)p * cols + c;
-      const double a0 = r[0], a1 = r[step], a2 = r[2 * step], a3 = r[3 * step];
-      s0 += a0;
-      s1 += a1;
-      s2 += a2;
-      s3 += a3;
+      double a[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) a[u] = r[u * step];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += a[u];
     }
-    for (; p < nparts; p += 64) s0 += part[(long long)p * cols + c];
+    for (; p < nparts; p += 64) acc += part[(long long)p * cols + c];
   }
-  red[4 * w + q][cl] = (s0 + s1) + (s2 + s3);
+  red[4 * w + q][cl] = acc;
+  __syncthreads();
+  // 64 threads add 16 of a column's 64 sums each, then 16 threads the four, in a fixed order
+  __shared__ double red4[4][16];
+  if (threadIdx.x < 64) {
+    const int col = threadIdx.x & 15, quarter = threadIdx.x >> 4;
+    double t = 0.0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) t += red[16 * quarter + j][col];
+    red4[quarter][col] = t;
+  }
   __syncthreads();
   if (threadIdx.x < 16 && c < cols) {
-    double t = 0.0;
-    for (int j = 0; j < 64; ++j) t += red[j][cl];
+    const double t = (red4[0][cl] + red4[1][cl]) + (red4[2][cl] + red4[3][cl]);
     float* o = c < split ? out + c : out2 + (c - split);
     *o = (float)(t + (beta != 0.f ? (double)*o : 0.0));
   }
