@@ -277,7 +277,9 @@ def rollout_line(steps, n_envs=4096, context_len=16, cpu=True):
 
 def dominant_roofline(plan, step, steps):
     """One profiled step for the per-kernel table, then `steps` steps with the launches of the
-    kernel symbol that took the most time bracketed by HIP events on their stream: its roofline."""
+    kernel symbol that took the most time bracketed by HIP events on their stream: its roofline.
+    The counter-measured traffic (profiles/traffic.json) is of the C4 step's launches, so the
+    C3 / C5 lines, whose launches of the same symbols have other shapes, report none."""
     plan.profile(True)
     step()
     th.sync()
@@ -292,7 +294,7 @@ def dominant_roofline(plan, step, steps):
     plan.profile(False)
     roof = roofline_of(dominant, n, fl, by, ms)
     roof.update({"kernel": dominant, "launches_per_step": n // steps, "avg_launch_us": round(ms / n * 1e3, 2),
-                 "traffic": traffic_of(dominant), "algorithmic_per_launch": {"flops": fl / n, "bytes": by / n}})
+                 "traffic": None, "algorithmic_per_launch": {"flops": fl / n, "bytes": by / n}})
     total = sum(a[3] for a in agg.values())
     kernels = {k: {"launches": v[0], "ms": round(v[3], 4), "pct": round(100 * v[3] / total, 1)}
                for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3])}
