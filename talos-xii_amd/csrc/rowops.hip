@@ -848,18 +848,66 @@ __global__ void concat_bwd_kernel(size_t rows, int ca, int cb, const float* __re
   }
 }
 
+// The same copies four floats per thread when both widths are multiples of 4 and every buffer is
+// 16-byte aligned (each float4 then lies inside one of a / b), with 32-bit index arithmetic.
+__global__ __launch_bounds__(256) void concat4_kernel(unsigned n4, int ca4, int cb4, const float4* __restrict__ a,
+                                                      const float4* __restrict__ b, float4* __restrict__ out) {
+  const unsigned i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= n4) return;
+  const unsigned w4 = (unsigned)(ca4 + cb4), r = i / w4;
+  const int c = (int)(i - r * w4);
+  out[i] = c < ca4 ? a[r * (unsigned)ca4 + c] : b[r * (unsigned)cb4 + (c - ca4)];
+}
+__global__ __launch_bounds__(256) void split4_kernel(unsigned n4, int ca4, int cb4, const float4* __restrict__ g,
+                                                     float4* __restrict__ da, float4* __restrict__ db,
+                                                     int accumulate) {
+  const unsigned i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= n4) return;
+  const unsigned w4 = (unsigned)(ca4 + cb4), r = i / w4;
+  const int c = (int)(i - r * w4);
+  float4* dst = c < ca4 ? &da[r * (unsigned)ca4 + c] : &db[r * (unsigned)cb4 + (c - ca4)];
+  float4 v = g[i];
+  if (accumulate) {
+    const float4 o = *dst;
+    v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+  }
+  *dst = v;
+}
+static bool concat_vec(size_t rows, int ca, int cb, const void* p0, const void* p1, const void* p2) {
+  return ca % 4 == 0 && cb % 4 == 0 && rows * (size_t)(ca + cb) / 4 < (1ull << 31) &&
+         ((reinterpret_cast<uintptr_t>(p0) | reinterpret_cast<uintptr_t>(p1) | reinterpret_cast<uintptr_t>(p2)) & 15) == 0;
+}
+
 int concat_launch(size_t rows, int ca, int cb, const float* a, const float* b, float* out, hipStream_t s) {
   if (rows == 0 || ca + cb == 0) return TALOS_OK;
-  ProfScope ps(s, "concat_kernel", 0.0, 8.0 * rows * (ca + cb));
-  hipLaunchKernelGGL(concat_kernel, dim3(grid_for(rows * (ca + cb))), dim3(256), 0, s, rows, ca, cb, a, b, out);
+  const size_t n = rows * (size_t)(ca + cb);
+  if (concat_vec(rows, ca, cb, a, b, out)) {
+    ProfScope ps(s, "concat4_kernel", 0.0, 8.0 * n);
+    hipLaunchKernelGGL(concat4_kernel, dim3(ceil_div(n / 4, 256)), dim3(256), 0, s, (unsigned)(n / 4), ca / 4, cb / 4,
+                       reinterpret_cast<const float4*>(a), reinterpret_cast<const float4*>(b),
+                       reinterpret_cast<float4*>(out));
+    TALOS_LAUNCHED("concat4_kernel");
+    return TALOS_OK;
+  }
+  ProfScope ps(s, "concat_kernel", 0.0, 8.0 * n);
+  hipLaunchKernelGGL(concat_kernel, dim3(grid_for(n)), dim3(256), 0, s, rows, ca, cb, a, b, out);
   TALOS_LAUNCHED("concat_kernel");
   return TALOS_OK;
 }
 
 int split_launch(size_t rows, int ca, int cb, const float* g, float* da, float* db, bool accumulate, hipStream_t s) {
   if (rows == 0 || ca + cb == 0) return TALOS_OK;
-  ProfScope ps(s, "concat_bwd_kernel", 0.0, (accumulate ? 12.0 : 8.0) * rows * (ca + cb));
-  hipLaunchKernelGGL(concat_bwd_kernel, dim3(grid_for(rows * (ca + cb))), dim3(256), 0, s, rows, ca, cb, g, da, db,
+  const size_t n = rows * (size_t)(ca + cb);
+  if (concat_vec(rows, ca, cb, g, da, db)) {
+    ProfScope ps(s, "split4_kernel", 0.0, (accumulate ? 12.0 : 8.0) * n);
+    hipLaunchKernelGGL(split4_kernel, dim3(ceil_div(n / 4, 256)), dim3(256), 0, s, (unsigned)(n / 4), ca / 4, cb / 4,
+                       reinterpret_cast<const float4*>(g), reinterpret_cast<float4*>(da), reinterpret_cast<float4*>(db),
+                       accumulate ? 1 : 0);
+    TALOS_LAUNCHED("split4_kernel");
+    return TALOS_OK;
+  }
+  ProfScope ps(s, "concat_bwd_kernel", 0.0, (accumulate ? 12.0 : 8.0) * n);
+  hipLaunchKernelGGL(concat_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, s, rows, ca, cb, g, da, db,
                      accumulate ? 1 : 0);
   TALOS_LAUNCHED("concat_bwd_kernel");
   return TALOS_OK;
@@ -1168,10 +1216,7 @@ int talos_concat_last_f32(size_t rows, int ca, int cb, const float* a, const flo
   TALOS_REQUIRE(ca >= 0 && cb >= 0, TALOS_ERR_SHAPE, "%s: negative width", __func__);
   TALOS_DEVICE();
   if (rows == 0 || ca + cb == 0) return TALOS_OK;
-  hipLaunchKernelGGL(concat_kernel, dim3(grid_for(rows * (ca + cb))), dim3(256), 0, as_stream(stream), rows, ca, cb, a,
-                     b, out);
-  TALOS_LAUNCHED("concat_kernel");
-  return entry_done(TALOS_OK, as_stream(stream));
+  return entry_done(concat_launch(rows, ca, cb, a, b, out, as_stream(stream)), as_stream(stream));
 }
 
 int talos_concat_last_bwd_f32(size_t rows, int ca, int cb, const float* dout, float* da, float* db,

@@ -599,3 +599,25 @@ def test_graph_capture_of_entries_replays_exactly():
         th.call("talos_workspace_bind", None, 0)
         th.stream_destroy(stream)
     check_close(eager[4], ref_gemm(1, 0, a, b), rtol=1e-4, atol=1e-3, name="captured wgrad")
+
+
+@pytest.mark.parametrize("rows,ca,cb", [(1000, 64, 32), (7, 4, 8), (33, 12, 0)])
+def test_concat_split_float4_path(rows, ca, cb):
+    """concat_last / its backward on widths that are multiples of 4 (the float4 kernels MLA's q / k
+    concatenation uses) equal numpy bit for bit; the backward accumulates into da / db."""
+    rng = np.random.default_rng(rows + ca)
+    a, b = f32(rng.normal(size=(rows, ca))), f32(rng.normal(size=(rows, cb)))
+    Ad, Bd, C = DA.from_numpy(a if ca else np.zeros((rows, 1))), DA.from_numpy(b if cb else np.zeros((rows, 1))), \
+        DA.zeros((rows, ca + cb))
+    th.call("talos_concat_last_f32", rows, ca, cb, Ad.ptr, Bd.ptr, C.ptr, None)
+    cat = np.concatenate([a, b], 1)
+    assert np.array_equal(C.numpy(), cat)
+    ga0, gb0 = f32(rng.normal(size=(rows, ca))), f32(rng.normal(size=(rows, cb)))
+    ga = DA.from_numpy(ga0 if ca else np.zeros((rows, 1)))
+    gb = DA.from_numpy(gb0 if cb else np.zeros((rows, 1)))
+    th.call("talos_concat_last_bwd_f32", rows, ca, cb, C.ptr, ga.ptr, gb.ptr, None)
+    # the kernels add in fp32
+    if ca:
+        assert np.array_equal(ga.numpy(), ga0.astype(np.float32) + a.astype(np.float32))
+    if cb:
+        assert np.array_equal(gb.numpy(), gb0.astype(np.float32) + b.astype(np.float32))
