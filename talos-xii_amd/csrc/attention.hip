@@ -1066,13 +1066,18 @@ struct BwdSlice {
 // The fused backward of one (batch, head) pair once its rows are in registers (load_half layout:
 // gv = dO, ov = O, qv = scale * Q, kv = K, vv = V) with the query row's lse; W is the wave's LDS
 // slice. GS_STAGED: the dO tile already holds gv (the kernel that forms dO itself put it there).
-template <int DKM, int DVM, bool GS_STAGED>
+// BLOCK (head dims 32): the wave's rows are the 32 queries from q0 and the 32 keys from k0 of a
+// longer sequence, and the block's dQ (unscaled), dK and dV accumulators are returned in out[0..2]
+// instead of stored, for the caller to add to the other blocks' before the store.
+template <int DKM, int DVM, bool GS_STAGED, bool BLOCK = false>
 __device__ __forceinline__ void bwd_fused_core(const AttnArgs& a, float* W, int pair, int l32, int h,
                                                const float (&gv)[DVM / 2], const float (&ov)[DVM / 2],
                                                const float (&qv)[DKM / 2], const float (&kv)[DKM / 2],
-                                               const float (&vv)[DVM / 2], float lse) {
+                                               const float (&vv)[DVM / 2], float lse, int q0 = 0, int k0 = 0,
+                                               floatx16* out = nullptr) {
   constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32;
   constexpr bool STAGE = BwdSlice<DKM, DVM>::STAGE;
+  static_assert(!BLOCK || (STAGE && KB == 1 && VB == 1), "the block form is for staged head dims 32");
   constexpr int TP = BwdSlice<DKM, DVM>::TP;
   const int b = pair / a.H, hd = pair % a.H;
   const long long tok0 = (long long)b * a.S;
@@ -1082,8 +1087,8 @@ __device__ __forceinline__ void bwd_fused_core(const AttnArgs& a, float* W, int 
   float* const T = W;              // dS^T [query][key] (pitch kTS)
   float* const Dl = W + (STAGE ? 96 * TP : 32 * kTS);  // D[query]
   float* const Ll = Dl + 32;                            // lse[query]
-  const bool rok = l32 < a.S;             // this lane's row (query l32 of q / dO / O)
-  const bool kok = l32 < key_len(a, b);   // ... and its key l32 of k / v takes part
+  const bool rok = q0 + l32 < a.S;             // this lane's row (query q0 + l32 of q / dO / O)
+  const bool kok = k0 + l32 < key_len(a, b);   // ... and its key k0 + l32 of k / v takes part
   if constexpr (STAGE && !GS_STAGED) stage_half<VH, TP>(Gs, gv, l32, h);
   {
     float d0 = 0.f, d1 = 0.f;
@@ -1122,7 +1127,7 @@ __device__ __forceinline__ void bwd_fused_core(const AttnArgs& a, float* W, int 
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int qr = acc_row(r, h);
-    const bool ok = kok && qr < a.S && (!a.causal || l32 <= qr);
+    const bool ok = kok && q0 + qr < a.S && (!a.causal || k0 + l32 <= q0 + qr);
     const float p = expf(ok ? sacc[r] - lq[r] : kNegInf);  // exp(-inf) = 0: no branch
     P[r] = p;
     dS[r] = p * (pacc[r] - dq_[r]);
@@ -1160,6 +1165,12 @@ __device__ __forceinline__ void bwd_fused_core(const AttnArgs& a, float* W, int 
     mfma_p_lds<KB, TP>(dST, Ks, l32, h, dq);  // dQ = dS . K
   else
     mfma_p_rows<KB, kFusedSel>(dST, a.k, a.ldk, tok0, 0, a.S, hd * a.dk, a.dk, l32, h, dq);  // dQ = dS . K
+  if constexpr (BLOCK) {
+    out[0] = dq[0];
+    out[1] = dk[0];
+    out[2] = dv[0];
+    return;
+  }
   const float dk_scale = STAGE ? 1.f : a.scale;  // the staged Q already carries the scale
   // row acc_row(r, h) of each result: a query for dQ, a key for dK / dV; lane <-> column
 #pragma unroll
@@ -1269,6 +1280,72 @@ attn_bwd_s32_wo_kernel(AttnArgs a, const float* __restrict__ wo, const float* __
     gv[i + 3] = g4.w;
   }
   bwd_fused_core<32, 32, true>(a, lds[wv], pair, l32, h, gv, ov, qv, kv, vv, lse);
+}
+
+// The backward for 32 < S <= 64 at head dims 32: a workgroup per (batch, head) pair, wave w the
+// 32 x 32 block of queries [32 qb, 32 qb + 32) and keys [32 kb, 32 kb + 32), qb = w / 2, kb =
+// w % 2. Each wave runs the fused single-block backward on its block (its q / dO / O rows and
+// its k / v rows loaded before the first product, dO, Q and K staged in its LDS slice) and keeps
+// the block's dQ, dK and dV accumulators; then the blocks meet in LDS: dQ of queries qb = block
+// (qb, 0) + block (qb, 1), dK and dV of keys kb = block (0, kb) + block (1, kb), added in that
+// order and stored by the first of the two waves. Replaces the split dQ / dK-dV kernels (and
+// their D workspace) at these lengths, where one workgroup per pair keeps all four waves busy.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BWD_WAVES))) void
+attn_bwd_s64_kernel(AttnArgs a) {
+  constexpr int TP = BwdSlice<32, 32>::TP, WSZ = BwdSlice<32, 32>::WSZ;
+  static_assert(3 * 2 * 16 * 64 <= 4 * WSZ, "the six partial blocks fit the four slices");
+  __shared__ __align__(16) float lds[4][WSZ];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int qb = wv >> 1, kb = wv & 1, q0 = 32 * qb, k0 = 32 * kb;
+  const int pair = blockIdx.x, b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  float gv[16], ov[16], qv[16], kv[16], vv[16];
+  load_half<16, true>(gv, a.dout, a.lddo, tok0, q0 + l32, a.S, hd * a.dv, 32, h, 1.f, true);
+  load_half<16, true>(ov, a.o, a.ldo, tok0, q0 + l32, a.S, hd * a.dv, 32, h, 1.f, true);
+  load_half<16, true>(qv, a.q, a.ldq, tok0, q0 + l32, a.S, hd * a.dk, 32, h, a.scale, true);
+  load_half<16, true>(kv, a.k, a.ldk, tok0, k0 + l32, a.S, hd * a.dk, 32, h, 1.f, true);
+  load_half<16, true>(vv, a.v, a.ldv, tok0, k0 + l32, a.S, hd * a.dv, 32, h, 1.f, true);
+  const float lse = a.lse[(long long)pair * a.S + min(q0 + l32, a.S - 1)];
+  floatx16 res[3];  // dQ (unscaled), dK, dV of this block
+  bwd_fused_core<32, 32, false, true>(a, lds[wv], pair, l32, h, gv, ov, qv, kv, vv, lse, q0, k0, res);
+  __syncthreads();  // every wave is done with its slice
+  // partial blocks in accumulator layout (register r of lane l at [r][l]): dQ of qb at X[qb],
+  // dK / dV of kb at X[2 + 2 kb] / X[3 + 2 kb]
+  float* const X = &lds[0][0];
+  if (kb == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) X[(qb * 16 + r) * 64 + lane] = res[0][r];
+  }
+  if (qb == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      X[((2 + 2 * kb) * 16 + r) * 64 + lane] = res[1][r];
+      X[((3 + 2 * kb) * 16 + r) * 64 + lane] = res[2][r];
+    }
+  }
+  __syncthreads();
+  if (kb == 0) {  // dQ rows q0 + acc_row(r, h)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = q0 + acc_row(r, h);
+      const bool ok = row < a.S;
+      const float g = rope_t((res[0][r] + X[(qb * 16 + r) * 64 + lane]) * a.scale, l32, row, a, ok);
+      if (ok) a.dq[(tok0 + row) * a.lddq + hd * a.dk + l32] = g;
+    }
+  }
+  if (qb == 0) {  // dK, dV rows k0 + acc_row(r, h); the staged Q carried the scale
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = k0 + acc_row(r, h);
+      const bool ok = row < a.S;
+      const float gk = rope_t(res[1][r] + X[((2 + 2 * kb) * 16 + r) * 64 + lane], l32, row, a, ok);
+      const float gvv = res[2][r] + X[((3 + 2 * kb) * 16 + r) * 64 + lane];
+      if (ok) {
+        a.dk_out[(tok0 + row) * a.lddk + hd * a.dk + l32] = gk;
+        a.dv_out[(tok0 + row) * a.lddv + hd * a.dv + l32] = gvv;
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1507,6 +1584,13 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
   a.D = ws;
   if ((long long)a.B * a.H * a.S == 0) return TALOS_OK;
   if (a.S <= 32) return attn_bwd_fused(a, dkm, dvm, s);
+  if (a.S <= 64 && d.dk == 32 && d.dv == 32 && a.vec && !attn_legacy()) {
+    const double rows = (double)a.B * a.S * a.H;
+    ProfScope ps(s, "attn_bwd_s64_kernel", kept_pairs(a) * (6.0 * a.dk + 4.0 * a.dv),
+                 4.0 * rows * (4.0 * a.dk + 4.0 * a.dv + 1.0));
+    hipLaunchKernelGGL(attn_bwd_s64_kernel, dim3((unsigned)((long long)a.B * a.H)), dim3(256), 0, s, a);
+    return launch_status("attn_bwd_s64_kernel");
+  }
   int rc = attn_bwd_dq(a, dkm, dvm, s);
   if (rc) return rc;
   return attn_bwd_dkv(a, dkm, dvm, s);

@@ -252,7 +252,9 @@ def test_rope_start_pos_and_accumulate(oracle):
 
 # --- attention ----------------------------------------------------------------------------
 @pytest.mark.parametrize("causal", [0, 1])
+# 32 < seq <= 64 at head dims 32: the four-block backward (33 and 47 leave a partial second block)
 @pytest.mark.parametrize("B,S,H,dk,dv", [(2, 7, 3, 5, 4), (3, 32, 4, 32, 32), (2, 64, 4, 32, 32),
+                                         (3, 33, 2, 32, 32), (2, 47, 3, 32, 32),
                                          (1, 200, 2, 96, 64), (2, 300, 1, 16, 16),
                                          # seq <= 32: the single-block backward at every head-dim class
                                          (2, 20, 3, 64, 64), (2, 32, 2, 96, 64), (1, 17, 2, 128, 128),

@@ -76,14 +76,17 @@ def _oracle_varlen(oracle, args, p, states, lens, actions, adv, ret, old):
     return loss, dp, np.array(logits)
 
 
-@pytest.mark.parametrize("causal,H", [(1, 2), (0, 2), (1, 1)])
-def test_minibatch_varlen_vs_oracle(oracle, causal, H):
-    # head dim 32 (H = 2) and 64 (H = 1): both last-query attention kernels of the last layer
-    rng = np.random.default_rng(11 + causal + H)
-    args = cfg_args(8, 12, causal, H=H)
+@pytest.mark.parametrize("causal,H,S,lens", [(1, 2, 12, [12, 1, 7, 12, 3]), (0, 2, 12, [12, 1, 7, 12, 3]),
+                                             (1, 1, 12, [12, 1, 7, 12, 3]), (1, 2, 40, [40, 1, 33, 17, 40]),
+                                             (0, 2, 40, [40, 1, 33, 17, 40])])
+def test_minibatch_varlen_vs_oracle(oracle, causal, H, S, lens):
+    # head dim 32 (H = 2) and 64 (H = 1): both last-query attention kernels of the last layer;
+    # seq 40 at head dim 32: the first layer's backward on the four-block kernel, keys masked past
+    # each sample's length
+    rng = np.random.default_rng(11 + causal + H + S)
+    args = cfg_args(8, S, causal, H=H)
     cfg, ocfg = th.PpoCfg(*args), oracle.PpoCfg(*args)
     p = f32(ppo_params(rng, ocfg))
-    lens = [12, 1, 7, 12, 3]
     n = len(lens)
     states, actions, adv, ret, old = _varlen_inputs(rng, ocfg, n, lens)
     loss_r, dp_r, logits_r = _oracle_varlen(oracle, args, p, states, lens, actions, adv, ret, old)
