@@ -12,6 +12,7 @@ on the stream the kernels run on); and the CPU baseline: the f64 oracle (a C++ r
 the reference's Rust autograd) timed on this host's cores on a bounded sample.
 """
 import argparse
+import glob
 import json
 import os
 import sys
@@ -144,12 +145,31 @@ def host_info():
     return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
 
 
+def product_names():
+    """The marketing names the kernel driver exposes in sysfs for the visible cards (empty where
+    there is no such file). Read as files: this process has initialised the GPU, and a child it
+    forks must not exec another program, so no rocm-smi."""
+    names = []
+    for path in sorted(glob.glob("/sys/class/drm/card*/device/product_name")):
+        try:
+            n = open(path).read().strip()
+        except OSError:
+            continue
+        if n and n not in names:
+            names.append(n)
+    return names
+
+
 def device_line():
-    """Device 0 as the runtime reports it. (No subprocess: this process has initialised the GPU,
-    and a child it forks must not exec another program.)"""
+    """Device 0 as the runtime reports it, with the driver's product name when the runtime gives
+    none."""
     info = th.device_info()
-    return {"name": info["name"], "cu_count": info["cu_count"], "clock_mhz": info["clock_khz"] // 1000,
-            "memory_gib": round(info["total_mem"] / 2 ** 30, 1)}
+    name = info["name"]
+    products = product_names()
+    if products and name.startswith("AMD GPU with"):
+        name = f"{products[0]} {name[name.find('('):]}" if "(" in name else products[0]
+    return {"name": name, "cu_count": info["cu_count"], "clock_mhz": info["clock_khz"] // 1000,
+            "memory_gib": round(info["total_mem"] / 2 ** 30, 1), "product_names": products}
 
 
 def optimizer_line(P, dP, steps):
