@@ -348,23 +348,23 @@ struct WoArgs {
   float* rstd;
   float eps;
 };
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_FWD_WAVES))) void
-attn_fwd_s32_wo_kernel(AttnArgs a, WoArgs w) {
-  __shared__ __align__(16) float T[32 * kWoP];
-  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
-  const int b = blockIdx.x;
-  const long long tok0 = (long long)b * a.S;
-  const floatx16 oacc = s32_pair(a, b * 4 + wv, l32, h);
-#pragma unroll
-  for (int r = 0; r < 16; ++r) T[acc_row(r, h) * kWoP + wv * 32 + l32] = oacc[r];
-  __syncthreads();
-  const int n = wv * 32 + l32;
+// The tail both fused kernels share, once the entry's attention output rows [0, 32 RB) are in T
+// (pitch kWoP): wave wv (of 4 RB) forms the 32 x 32 block (rows 32 (wv / 4).., columns
+// 32 (wv % 4)..) of O.Wo with v_mfma_f32_32x32x2f32 (A = O rows from T, B = Wo rows from memory,
+// both walking k in the order 8j + 4h + q), the blocks pass through T again, and wave wv takes
+// the eight token rows 8 wv .. 8 wv + 7 for the residual, the row norm and the stores (lane <->
+// columns 2 lane, 2 lane + 1). Rows >= nrows are neither read nor written.
+template <int RB>
+__device__ __forceinline__ void wo_resid_norm(const WoArgs& w, float* T, long long tok0, int nrows, int lane,
+                                              int wv) {
+  const int l32 = lane & 31, h = lane >> 5;
+  const int r0 = 32 * (wv >> 2), n = 32 * (wv & 3) + l32;
   floatx16 acc;
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 #pragma unroll 4
   for (int j = 0; j < kWoD / 8; ++j) {
-    const float4 o4 = *reinterpret_cast<const float4*>(T + l32 * kWoP + 8 * j + 4 * h);
+    const float4 o4 = *reinterpret_cast<const float4*>(T + (r0 + l32) * kWoP + 8 * j + 4 * h);
     const float* wr = w.wo + (long long)(8 * j + 4 * h) * kWoD + n;
     const float w0 = wr[0], w1 = wr[kWoD], w2 = wr[2 * kWoD], w3 = wr[3 * kWoD];
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(o4.x, w0, acc, 0, 0, 0);
@@ -374,21 +374,20 @@ attn_fwd_s32_wo_kernel(AttnArgs a, WoArgs w) {
   }
   __syncthreads();  // every wave has read the O rows
 #pragma unroll
-  for (int r = 0; r < 16; ++r) T[acc_row(r, h) * kWoP + n] = acc[r];
+  for (int r = 0; r < 16; ++r) T[(r0 + acc_row(r, h)) * kWoP + n] = acc[r];
   __syncthreads();
-  // rows: wave wv takes tokens 8 wv .. 8 wv + 7, lane the columns 2 lane, 2 lane + 1
   float2 res[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int t = wv * 8 + i;
-    res[i] = t < a.S ? *reinterpret_cast<const float2*>(w.resid + (tok0 + t) * kWoD + 2 * lane)
-                     : make_float2(0.f, 0.f);
+    res[i] = t < nrows ? *reinterpret_cast<const float2*>(w.resid + (tok0 + t) * kWoD + 2 * lane)
+                       : make_float2(0.f, 0.f);
   }
   const float2 g = *reinterpret_cast<const float2*>(w.gain + 2 * lane);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int t = wv * 8 + i;
-    if (t >= a.S) break;  // uniform per wave
+    if (t >= nrows) break;  // uniform per wave
     const float2 pv = *reinterpret_cast<const float2*>(T + t * kWoP + 2 * lane);
     const float2 v = make_float2(pv.x + res[i].x, pv.y + res[i].y);
     const long long row = tok0 + t;
@@ -398,6 +397,103 @@ attn_fwd_s32_wo_kernel(AttnArgs a, WoArgs w) {
     *reinterpret_cast<float2*>(w.xn + row * kWoD + 2 * lane) = make_float2(v.x * r * g.x, v.y * r * g.y);
     if (lane == 0 && w.rstd) w.rstd[row] = r;
   }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_FWD_WAVES))) void
+attn_fwd_s32_wo_kernel(AttnArgs a, WoArgs w) {
+  __shared__ __align__(16) float T[32 * kWoP];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int b = blockIdx.x;
+  const floatx16 oacc = s32_pair(a, b * 4 + wv, l32, h);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) T[acc_row(r, h) * kWoP + wv * 32 + l32] = oacc[r];
+  __syncthreads();
+  wo_resid_norm<1>(w, T, (long long)b * a.S, a.S, lane, wv);
+}
+
+// The same for 32 < S <= 64: a workgroup of eight waves per batch entry. The entry's V rows [64,
+// 128] are staged in LDS first (coalesced float4 loads; the P.V products read their B operand
+// there, which keeps the kernel within 128 VGPRs, two workgroups per CU). Wave wv takes the
+// query block qb = wv / 4 of head wv % 4 (so each SIMD holds one wave of each query block, and
+// the causal first block, which has one key block, pairs with the second, which has two): the
+// scores of its one or two key blocks in S^T layout, one softmax over both, O = P.V as in
+// s32_pair, O and lse stored, and O's block into T. Then O.Wo and the rows as above, over the
+// entry's 64 token rows.
+constexpr int kVP = kWoD + 8;  // V tile pitch: rows 4 apart start 32 banks apart
+__global__ __launch_bounds__(512) void attn_fwd_s64_wo_kernel(AttnArgs a, WoArgs w) {
+  constexpr int KH = 16;
+  __shared__ __align__(16) float T[64 * kWoP];
+  __shared__ __align__(16) float Vs[64 * kVP];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int b = blockIdx.x, hd = wv & 3, qb = wv >> 2, pair = b * 4 + hd;
+  const long long tok0 = (long long)b * a.S;
+  const int q = 32 * qb + l32;
+  const int Sk = key_len(a, b);
+  const bool two = (!a.causal || qb == 1) && Sk > 32;  // the second key block takes part (uniform)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // V rows: 64 x 32 float4s, rows >= S as zeros
+    const int idx = threadIdx.x + 512 * i, row = idx >> 5, c = 4 * (idx & 31);
+    const float* src = row < a.S ? a.v + (tok0 + row) * a.ldv + c : kAttnZeros + c;
+    *reinterpret_cast<float4*>(Vs + row * kVP + c) = *reinterpret_cast<const float4*>(src);
+  }
+  float qv[KH], kv[2][KH];
+  load_half<KH, true>(qv, a.q, a.ldq, tok0, q, a.S, hd * a.dk, 32, h, a.scale, true);
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    if (kb == 1 && !two) break;
+    load_half<KH, true>(kv[kb], a.k, a.ldk, tok0, 32 * kb + l32, a.S, hd * a.dk, 32, h, 1.f, true);
+  }
+  float sv[2][16], m = kNegInf;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    if (kb == 1 && !two) break;
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    acc = mfma_rows<KH>(kv[kb], qv, acc);  // S^T: register r <-> key 32 kb + acc_row(r, h), lane <-> query
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = 32 * kb + acc_row(r, h);
+      const bool ok = key < Sk && (!a.causal || key <= q);
+      sv[kb][r] = ok ? acc[r] : kNegInf;
+      m = fmaxf(m, sv[kb][r]);
+    }
+  }
+  m = fmaxf(m, __shfl_xor(m, 32, 64));
+  float l = 0.f;
+  if (m != kNegInf) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      if (kb == 1 && !two) break;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) l += expf(sv[kb][r] - m);
+    }
+  }
+  l += __shfl_xor(l, 32, 64);
+  const float inv_l = l > 0.f ? 1.f / l : 0.f;
+  __syncthreads();  // the V tile is staged
+  floatx16 oacc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) oacc[r] = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    if (kb == 1 && !two) break;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const float p = (m == kNegInf) ? 0.f : expf(sv[kb][s] - m) * inv_l;
+      const float vm = Vs[(32 * kb + acc_row(s, h)) * kVP + hd * 32 + l32];
+      oacc = __builtin_amdgcn_mfma_f32_32x32x2f32(p, vm, oacc, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int qr = 32 * qb + acc_row(r, h);
+    if (qr < a.S) a.o[(tok0 + qr) * a.ldo + hd * a.dv + l32] = oacc[r];
+    T[qr * kWoP + hd * 32 + l32] = oacc[r];
+  }
+  if (h == 0 && q < a.S) a.lse[(long long)pair * a.S + q] = (l > 0.f) ? m + logf(l) : kNegInf;
+  __syncthreads();
+  wo_resid_norm<2>(w, T, tok0, a.S, lane, wv);
 }
 
 // ---------------------------------------------------------------------------
@@ -1282,21 +1378,28 @@ attn_bwd_s32_wo_kernel(AttnArgs a, const float* __restrict__ wo, const float* __
   bwd_fused_core<32, 32, true>(a, lds[wv], pair, l32, h, gv, ov, qv, kv, vv, lse);
 }
 
-// The backward for 32 < S <= 64 at head dims 32: a workgroup per (batch, head) pair, wave w the
-// 32 x 32 block of queries [32 qb, 32 qb + 32) and keys [32 kb, 32 kb + 32), qb = w / 2, kb =
-// w % 2. Each wave runs the fused single-block backward on its block (its q / dO / O rows and
-// its k / v rows loaded before the first product, dO, Q and K staged in its LDS slice) and keeps
-// the block's dQ, dK and dV accumulators; then the blocks meet in LDS: dQ of queries qb = block
-// (qb, 0) + block (qb, 1), dK and dV of keys kb = block (0, kb) + block (1, kb), added in that
-// order and stored by the first of the two waves. Replaces the split dQ / dK-dV kernels (and
-// their D workspace) at these lengths, where one workgroup per pair keeps all four waves busy.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BWD_WAVES))) void
+// The backward for 32 < S <= 64 at head dims 32: a workgroup per (batch, head) pair, each wave a
+// 32 x 32 block of queries [32 qb, 32 qb + 32) and keys [32 kb, 32 kb + 32). NW = 4: all four
+// blocks, wave w = (qb, kb) = (w / 2, w % 2); NW = 3 (causal): the three blocks on or below the
+// diagonal, w = 0, 1, 2 -> (0, 0), (1, 0), (1, 1), since block (0, 1) has every key masked (three
+// LDS slices also fit four workgroups on a CU where four fit three). Each wave runs the fused
+// single-block backward on its block (its q / dO / O rows and its k / v rows loaded before the
+// first product, dO, Q and K staged in its LDS slice) and keeps the block's dQ, dK and dV
+// accumulators; then the blocks meet in LDS: dQ of queries qb = block (qb, 0) + block (qb, 1),
+// dK and dV of keys kb = block (0, kb) + block (1, kb), added in that order and stored by the
+// first of the two waves (a block with no partner stores its own). A block whose keys are all
+// past the entry's length adds zeros. Replaces the split dQ / dK-dV kernels (and their D
+// workspace) at these lengths.
+template <int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BWD_WAVES))) void
 attn_bwd_s64_kernel(AttnArgs a) {
-  constexpr int TP = BwdSlice<32, 32>::TP, WSZ = BwdSlice<32, 32>::WSZ;
-  static_assert(3 * 2 * 16 * 64 <= 4 * WSZ, "the six partial blocks fit the four slices");
-  __shared__ __align__(16) float lds[4][WSZ];
+  static_assert(NW == 3 || NW == 4, "three (causal) or four blocks");
+  constexpr bool TRI = NW == 3;
+  constexpr int WSZ = BwdSlice<32, 32>::WSZ;
+  static_assert(4 * 16 * 64 <= NW * WSZ, "the partial blocks fit the slices");
+  __shared__ __align__(16) float lds[NW][WSZ];
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
-  const int qb = wv >> 1, kb = wv & 1, q0 = 32 * qb, k0 = 32 * kb;
+  const int qb = TRI ? (wv + 1) >> 1 : wv >> 1, kb = TRI ? wv >> 1 : wv & 1, q0 = 32 * qb, k0 = 32 * kb;
   const int pair = blockIdx.x, b = pair / a.H, hd = pair % a.H;
   const long long tok0 = (long long)b * a.S;
   float gv[16], ov[16], qv[16], kv[16], vv[16];
@@ -1307,16 +1410,26 @@ attn_bwd_s64_kernel(AttnArgs a) {
   load_half<16, true>(vv, a.v, a.ldv, tok0, k0 + l32, a.S, hd * a.dv, 32, h, 1.f, true);
   const float lse = a.lse[(long long)pair * a.S + min(q0 + l32, a.S - 1)];
   floatx16 res[3];  // dQ (unscaled), dK, dV of this block
-  bwd_fused_core<32, 32, false, true>(a, lds[wv], pair, l32, h, gv, ov, qv, kv, vv, lse, q0, k0, res);
+  if ((a.causal && k0 > q0 + 31) || k0 >= key_len(a, b)) {  // every key masked (uniform per wave)
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) res[i][r] = 0.f;
+  } else {
+    bwd_fused_core<32, 32, false, true>(a, lds[wv], pair, l32, h, gv, ov, qv, kv, vv, lse, q0, k0, res);
+  }
   __syncthreads();  // every wave is done with its slice
+  // which sums this wave takes part in: dQ of qb pairs (qb, 0) with (qb, 1), dK / dV of kb pairs
+  // (0, kb) with (1, kb); under TRI, block (0, 0) stores dQ alone and block (1, 1) dK / dV alone
+  const bool dq_pair = !(TRI && qb == 0), dkv_pair = !(TRI && kb == 1);
   // partial blocks in accumulator layout (register r of lane l at [r][l]): dQ of qb at X[qb],
   // dK / dV of kb at X[2 + 2 kb] / X[3 + 2 kb]
   float* const X = &lds[0][0];
-  if (kb == 1) {
+  if (kb == 1 && dq_pair) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) X[(qb * 16 + r) * 64 + lane] = res[0][r];
   }
-  if (qb == 1) {
+  if (qb == 1 && dkv_pair) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       X[((2 + 2 * kb) * 16 + r) * 64 + lane] = res[1][r];
@@ -1329,20 +1442,22 @@ attn_bwd_s64_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int row = q0 + acc_row(r, h);
       const bool ok = row < a.S;
-      const float g = rope_t((res[0][r] + X[(qb * 16 + r) * 64 + lane]) * a.scale, l32, row, a, ok);
+      const float sum = dq_pair ? res[0][r] + X[(qb * 16 + r) * 64 + lane] : res[0][r];
+      const float g = rope_t(sum * a.scale, l32, row, a, ok);
       if (ok) a.dq[(tok0 + row) * a.lddq + hd * a.dk + l32] = g;
     }
   }
-  if (qb == 0) {  // dK, dV rows k0 + acc_row(r, h); the staged Q carried the scale
+  if (qb == 0 || !dkv_pair) {  // dK, dV rows k0 + acc_row(r, h); the staged Q carried the scale
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = k0 + acc_row(r, h);
       const bool ok = row < a.S;
-      const float gk = rope_t(res[1][r] + X[((2 + 2 * kb) * 16 + r) * 64 + lane], l32, row, a, ok);
-      const float gvv = res[2][r] + X[((3 + 2 * kb) * 16 + r) * 64 + lane];
+      const float sk = dkv_pair ? res[1][r] + X[((2 + 2 * kb) * 16 + r) * 64 + lane] : res[1][r];
+      const float sv = dkv_pair ? res[2][r] + X[((3 + 2 * kb) * 16 + r) * 64 + lane] : res[2][r];
+      const float gk = rope_t(sk, l32, row, a, ok);
       if (ok) {
         a.dk_out[(tok0 + row) * a.lddk + hd * a.dk + l32] = gk;
-        a.dv_out[(tok0 + row) * a.lddv + hd * a.dv + l32] = gvv;
+        a.dv_out[(tok0 + row) * a.lddv + hd * a.dv + l32] = sv;
       }
     }
   }
@@ -1451,14 +1566,14 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
 
 int attn_fwd_wo_supported(const AttnDesc& d, const AttnWoDesc& w) {
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  return d.dk == 32 && d.dv == 32 && d.heads == 4 && d.seq >= 1 && d.seq <= 32 && d.ldo == kWoD &&
+  return d.dk == 32 && d.dv == 32 && d.heads == 4 && d.seq >= 1 && d.seq <= 64 && d.ldo == kWoD &&
          w.wo != nullptr && w.resid != nullptr && w.h2 != nullptr && w.gain != nullptr && w.xn != nullptr &&
          al(w.wo) && al(w.resid) && al(w.h2) && al(w.gain) && al(w.xn) && make_args(d, 32, 32).vec;
 }
 
 int attn_fwd_wo_launch(const AttnDesc& d, const AttnWoDesc& wd, hipStream_t s) {
   if (!attn_fwd_wo_supported(d, wd)) {
-    set_error("attention + Wo: the fused kernel takes S <= 32, four 32-wide heads, d = 128 and aligned rows");
+    set_error("attention + Wo: the fused kernels take S <= 64, four 32-wide heads, d = 128 and aligned rows");
     return TALOS_ERR_UNSUPPORTED;
   }
   AttnArgs a = make_args(d, 32, 32);
@@ -1468,6 +1583,11 @@ int attn_fwd_wo_launch(const AttnDesc& d, const AttnWoDesc& wd, hipStream_t s) {
   const double flops = kept_pairs(a) * (2.0 * a.dk + 2.0 * a.dv) + 2.0 * tok * kWoD * kWoD;
   // q, k, v, x read; o, lse, h2, xn, rstd written (Wo from cache)
   const double bytes = 4.0 * rows * (2.0 * a.dk + a.dv) + 4.0 * rows * (a.dv + 1.0) + 4.0 * tok * (3.0 * kWoD + 1.0);
+  if (a.S > 32) {
+    ProfScope ps(s, "attn_fwd_s64_wo_kernel", flops, bytes);
+    hipLaunchKernelGGL(attn_fwd_s64_wo_kernel, dim3(a.B), dim3(512), 0, s, a, w);
+    return launch_status("attn_fwd_s64_wo_kernel");
+  }
   ProfScope ps(s, "attn_fwd_s32_wo_kernel", flops, bytes);
   hipLaunchKernelGGL(attn_fwd_s32_wo_kernel, dim3(a.B), dim3(256), 0, s, a, w);
   return launch_status("attn_fwd_s32_wo_kernel");
@@ -1586,9 +1706,12 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
   if (a.S <= 32) return attn_bwd_fused(a, dkm, dvm, s);
   if (a.S <= 64 && d.dk == 32 && d.dv == 32 && a.vec && !attn_legacy()) {
     const double rows = (double)a.B * a.S * a.H;
-    ProfScope ps(s, "attn_bwd_s64_kernel", kept_pairs(a) * (6.0 * a.dk + 4.0 * a.dv),
+    ProfScope ps(s, a.causal ? "attn_bwd_s64_kernel<3>" : "attn_bwd_s64_kernel<4>", kept_pairs(a) * (6.0 * a.dk + 4.0 * a.dv),
                  4.0 * rows * (4.0 * a.dk + 4.0 * a.dv + 1.0));
-    hipLaunchKernelGGL(attn_bwd_s64_kernel, dim3((unsigned)((long long)a.B * a.H)), dim3(256), 0, s, a);
+    if (a.causal)
+      hipLaunchKernelGGL(attn_bwd_s64_kernel<3>, dim3((unsigned)((long long)a.B * a.H)), dim3(192), 0, s, a);
+    else
+      hipLaunchKernelGGL(attn_bwd_s64_kernel<4>, dim3((unsigned)((long long)a.B * a.H)), dim3(256), 0, s, a);
     return launch_status("attn_bwd_s64_kernel");
   }
   int rc = attn_bwd_dq(a, dkm, dvm, s);

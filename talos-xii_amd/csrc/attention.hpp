@@ -48,7 +48,7 @@ struct AttnDesc {
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s);
 
 // The attention forward fused with the output projection, its residual and the following
-// RMSNorm (S <= 32, four 32-wide heads, d = 128, o rows of 128): besides o and lse it writes
+// RMSNorm (S <= 64, four 32-wide heads, d = 128, o rows of 128): besides o and lse it writes
 // h2 = resid + o.Wo, xn = rmsnorm(h2) * gain and rstd (optional), all rows of 128 floats.
 struct AttnWoDesc {
   const float* wo = nullptr;  // [128, 128], row = input feature

@@ -769,7 +769,7 @@ static int block_mlp_forward(talos_plan_s* p, const talos_block_cfg& c, const fl
 // next row norm of L.out when next is set.
 constexpr int kWoFuseD = 128;  // the model width attn_fwd_wo_launch takes
 
-// At S <= 32 with four 32-wide heads and d = 128 (C4's blocks) the attention kernel also forms
+// At S <= 64 with four 32-wide heads and d = 128 (the C3 / C4 blocks) the attention kernel also forms
 // h2 = x + o.Wo and its RMSNorm (attn_fwd_wo_launch), and the MLP half starts at W1.
 static int block_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
                          talos_plan_s::Layer& L, hipStream_t s, bool normed = false,
@@ -882,10 +882,9 @@ static int block_attn_backward(talos_plan_s* p, const talos_block_cfg& c, const 
   return block_qkv_backward(p, c, P, G, o, L, g_h2, g_h2_last, dx, s);
 }
 
-// Backward of one block: gout = dL/dout (read), writes dparams slots and dx. Where the forward
-// fused o.Wo into the attention (S <= 32, four 32-wide heads, d = 128), the backward folds the
-// input gradient of that product, g_o = g_h2.Wo^T, into the attention backward
-// (attn_bwd_wo_launch) instead of storing g_o and reading it back.
+// Backward of one block: gout = dL/dout (read), writes dparams slots and dx. At S <= 32 with
+// four 32-wide heads and d = 128 the backward folds the input gradient of o.Wo, g_o = g_h2.Wo^T,
+// into the attention backward (attn_bwd_wo_launch) instead of storing g_o and reading it back.
 static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
                           talos_plan_s::Layer& L, const float* gout, float* dx, hipStream_t s) {
   const int M = c.batch * c.seq;

@@ -43,7 +43,7 @@ def run_block(cfg, p, x, G):
 @pytest.mark.parametrize("B,S,d,H,F,causal,act", [(2, 6, 16, 4, 64, 1, 0), (3, 64, 128, 4, 512, 1, 0),
                                                   (2, 33, 64, 2, 128, 0, 1), (2, 5, 24, 4, 48, 1, 0),
                                                   (3, 9, 40, 4, 80, 0, 1), (3, 23, 128, 4, 256, 0, 0),
-                                                  (2, 32, 128, 4, 512, 1, 1)])
+                                                  (2, 32, 128, 4, 512, 1, 1), (2, 47, 128, 4, 256, 0, 1)])
 def test_block_fwd_bwd_vs_oracle(oracle, B, S, d, H, F, causal, act):
     rng = np.random.default_rng(1000 + S + d)
     cfg = th.BlockCfg(B, S, d, H, d // H, F, causal, act, 1e-6, 10000.0)

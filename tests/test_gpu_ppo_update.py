@@ -76,15 +76,18 @@ def _oracle_varlen(oracle, args, p, states, lens, actions, adv, ret, old):
     return loss, dp, np.array(logits)
 
 
-@pytest.mark.parametrize("causal,H,S,lens", [(1, 2, 12, [12, 1, 7, 12, 3]), (0, 2, 12, [12, 1, 7, 12, 3]),
-                                             (1, 1, 12, [12, 1, 7, 12, 3]), (1, 2, 40, [40, 1, 33, 17, 40]),
-                                             (0, 2, 40, [40, 1, 33, 17, 40])])
-def test_minibatch_varlen_vs_oracle(oracle, causal, H, S, lens):
+@pytest.mark.parametrize("causal,H,S,lens,d", [(1, 2, 12, [12, 1, 7, 12, 3], 64), (0, 2, 12, [12, 1, 7, 12, 3], 64),
+                                               (1, 1, 12, [12, 1, 7, 12, 3], 64), (1, 2, 40, [40, 1, 33, 17, 40], 64),
+                                               (0, 2, 40, [40, 1, 33, 17, 40], 64),
+                                               (1, 4, 47, [47, 1, 33, 20, 32], 128),
+                                               (0, 4, 64, [64, 2, 40, 31, 64], 128)])
+def test_minibatch_varlen_vs_oracle(oracle, causal, H, S, lens, d):
     # head dim 32 (H = 2) and 64 (H = 1): both last-query attention kernels of the last layer;
     # seq 40 at head dim 32: the first layer's backward on the four-block kernel, keys masked past
-    # each sample's length
+    # each sample's length; d = 128 with four heads of 32 at seq 47 / 64: the first layer's
+    # forward on the eight-wave attention kernel with o.Wo, the residual and RMSNorm2 fused
     rng = np.random.default_rng(11 + causal + H + S)
-    args = cfg_args(8, S, causal, H=H)
+    args = cfg_args(8, S, causal, d=d, H=H)
     cfg, ocfg = th.PpoCfg(*args), oracle.PpoCfg(*args)
     p = f32(ppo_params(rng, ocfg))
     n = len(lens)
