@@ -109,17 +109,19 @@ struct GemmArgs {
   int nblocks;  // tiles * batch * ksplit (the grid is padded to a multiple of 8)
 };
 
-// Loads the op(A) panel [BM x BK] of chunk k0 into registers. CHECK = false: the whole panel
-// is in bounds and 16-byte aligned.
-template <bool TA, bool CHECK>
+// Loads the op(A) panel [ROWS x BK] of chunk k0 into registers (ROWS / 32 float4s a thread).
+// CHECK = false: the whole panel is in bounds and 16-byte aligned.
+template <bool TA, bool CHECK, int ROWS = BM>
 __device__ __forceinline__ void load_a(const GemmArgs& p, const float* __restrict__ A, int m0, int k0, int kend,
-                                       float4 (&r)[4]) {
+                                       float4 (&r)[ROWS / 32]) {
+  static_assert(ROWS == 128 || ROWS == 64, "128- or 64-row panels");
+  constexpr int RS = ROWS == 128 ? 7 : 6;  // log2(ROWS)
   const int t = threadIdx.x;
   if (!TA) {
-    const int m = m0 + (t & 127);
+    const int m = m0 + (t & (ROWS - 1));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int k = k0 + 4 * ((t >> 7) + 2 * i);
+    for (int i = 0; i < ROWS / 32; ++i) {
+      const int k = k0 + 4 * ((t >> RS) + (NT / ROWS) * i);
       const float* src = A + (long long)m * p.lda + k;
       if (!CHECK || (p.vecA && m < p.M && k + 3 < kend)) {
         r[i] = *reinterpret_cast<const float4*>(src);
@@ -131,10 +133,10 @@ __device__ __forceinline__ void load_a(const GemmArgs& p, const float* __restric
       }
     }
   } else {
-    const int m = m0 + 4 * (t & 31);
+    const int m = m0 + 4 * (t & (ROWS / 4 - 1));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int k = k0 + (t >> 5) + 8 * i;
+    for (int i = 0; i < ROWS / 32; ++i) {
+      const int k = k0 + (t >> (RS - 2)) + (NT / (ROWS / 4)) * i;
       const float* src = A + (long long)k * p.lda + m;
       if (!CHECK || (p.vecA && k < kend && m + 3 < p.M)) {
         r[i] = *reinterpret_cast<const float4*>(src);
@@ -148,20 +150,21 @@ __device__ __forceinline__ void load_a(const GemmArgs& p, const float* __restric
   }
 }
 
-template <bool TA>
-__device__ __forceinline__ void store_a(float* As, const float4 (&r)[4]) {
+template <bool TA, int ROWS = BM>
+__device__ __forceinline__ void store_a(float* As, const float4 (&r)[ROWS / 32]) {
+  constexpr int RS = ROWS == 128 ? 7 : 6;  // log2(ROWS)
   const int t = threadIdx.x;
   if (!TA) {  // k-contiguous panel As[m][k]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kk = 4 * ((t >> 7) + 2 * i);
-      *reinterpret_cast<float4*>(As + (t & 127) * KP + kk) = r[i];
+    for (int i = 0; i < ROWS / 32; ++i) {
+      const int kk = 4 * ((t >> RS) + (NT / ROWS) * i);
+      *reinterpret_cast<float4*>(As + (t & (ROWS - 1)) * KP + kk) = r[i];
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kk = (t >> 5) + 8 * i;
-      *reinterpret_cast<float4*>(As + kk * LDS_S + 4 * (t & 31)) = r[i];
+    for (int i = 0; i < ROWS / 32; ++i) {
+      const int kk = (t >> (RS - 2)) + (NT / (ROWS / 4)) * i;
+      *reinterpret_cast<float4*>(As + kk * LDS_S + 4 * (t & (ROWS / 4 - 1))) = r[i];
     }
   }
 }
@@ -206,7 +209,7 @@ __device__ __forceinline__ void load_b(const GemmArgs& p, const float* __restric
 
 template <bool TB>
 __device__ __forceinline__ void store_b(float* Bs, const float4 (&r)[4]) {
-  store_a<!TB>(Bs, r);
+  store_a<!TB, BN>(Bs, r);
 }
 
 // MFMA operand values of rows r and r + 32 of a panel at k = k0 .. k0 + 3 (k0 = 8j + 4h):
@@ -228,14 +231,26 @@ __device__ __forceinline__ void frag4(const float* X, int r, int k0, float (&f0)
   }
 }
 
-template <bool TA, bool TB>
+// frag4's first row block only (row r at k = k0 .. k0 + 3)
+template <bool KC>
+__device__ __forceinline__ void frag1(const float* X, int r, int k0, float (&f0)[4]) {
+  if (KC) {
+    const float4 v0 = *reinterpret_cast<const float4*>(X + r * KP + k0);
+    f0[0] = v0.x; f0[1] = v0.y; f0[2] = v0.z; f0[3] = v0.w;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) f0[q] = X[(k0 + q) * LDS_S + r];
+  }
+}
+
+template <bool TA, bool TB, int ROWS = BM>
 __device__ __forceinline__ void load_chunk(const GemmArgs& p, const float* A, const float* B, int m0, int n0, int k0,
-                                           int kend, bool interior, float4 (&ra)[4], float4 (&rb)[4]) {
+                                           int kend, bool interior, float4 (&ra)[ROWS / 32], float4 (&rb)[4]) {
   if (interior && k0 + BK <= kend) {
-    load_a<TA, false>(p, A, m0, k0, kend, ra);
+    load_a<TA, false, ROWS>(p, A, m0, k0, kend, ra);
     load_b<TB, false>(p, B, n0, k0, kend, rb);
   } else {
-    load_a<TA, true>(p, A, m0, k0, kend, ra);
+    load_a<TA, true, ROWS>(p, A, m0, k0, kend, ra);
     load_b<TB, true>(p, B, n0, k0, kend, rb);
   }
 }
@@ -463,7 +478,7 @@ __device__ __forceinline__ void normb_apply(const GemmArgs& p, float4 gg, int ro
 }
 
 constexpr int T_S = 136;  // pitch of the staged output tile: rows h*4 apart land 32 banks apart
-constexpr int T_ROWS = BM / 2;  // the tile is staged in two halves of 64 rows
+constexpr int T_ROWS = 64;  // the tile is staged 64 rows at a time
 constexpr int SMEM_FLOATS = (2 * NBUF * PANEL > T_ROWS * T_S) ? 2 * NBUF * PANEL : T_ROWS * T_S;
 
 // ---------------------------------------------------------------------------
@@ -555,10 +570,14 @@ __device__ __forceinline__ void store_bf(uint16_t* S, const uint32_t (&o)[16]) {
   }
 }
 
-template <bool TA, bool TB, int E, bool BF>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TALOS_GEMM_WAVES))) void gemm_f32_kernel(
-    GemmArgs p) {
+// One output tile of BMT (128 or 64) x 128 rows / columns: four waves, wave (wm, wn) the
+// [BMT / 2, 64] block at rows wm BMT / 2, columns 64 wn, as 2 x 2 (BMT = 128) or 1 x 2 (BMT = 64)
+// 32 x 32 accumulators.
+template <bool TA, bool TB, int E, bool BF, int BMT>
+__device__ __forceinline__ void gemm_tile(GemmArgs p) {
   __shared__ __align__(16) float smem[SMEM_FLOATS];
+  static_assert(BMT == 128 || (BMT == 64 && !BF), "64-row tiles are fp32 only");
+  constexpr int MT = BMT / 64;  // 32-row accumulator blocks per wave
   // panels: As buffer i at smem + i*PANEL, Bs buffer i after the NBUF A buffers
   float* const Abase = smem;
   float* const Bbase = smem + NBUF * PANEL;
@@ -568,12 +587,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
   // then share that XCD's L2 instead of fetching the same operand panel once per XCD. The grid
   // is padded to a multiple of 8; padding workgroups exit before any barrier.
   const int tiles_n = (p.N + BN - 1) / BN;
-  const int tiles = tiles_n * ((p.M + BM - 1) / BM);
+  const int tiles = tiles_n * ((p.M + BMT - 1) / BMT);
   const int per_xcd = (int)(gridDim.x >> 3);
   const int logical = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
   if (logical >= p.nblocks) return;
   const int tile = logical % tiles;
-  const int m0 = (tile / tiles_n) * BM;
+  const int m0 = (tile / tiles_n) * BMT;
   const int n0 = (tile % tiles_n) * BN;
   const int bz = logical / tiles;
   const int b = bz / p.ksplit, split = bz % p.ksplit;
@@ -581,22 +600,22 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
   const float* B = p.B + (long long)b * p.sB;
   const int kbeg = split * p.kper;
   const int kend = min(p.K, kbeg + p.kper);
-  const bool interior = p.vecA && p.vecB && m0 + BM <= p.M && n0 + BN <= p.N;
+  const bool interior = p.vecA && p.vecB && m0 + BMT <= p.M && n0 + BN <= p.N;
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
   const int l32 = lane & 31, h = lane >> 5;
 
-  floatx16 acc[2][2];
+  floatx16 acc[MT][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   float csum = 0.f;  // E_DBIAS: this thread's column sum over its half of each panel
-  if constexpr (BF) {
+  if constexpr (BF && BMT == 128) {
     static_assert((E & E_DBIAS) == 0, "the bf16 path has no fused bias gradient");
     uint16_t* As16 = reinterpret_cast<uint16_t*>(smem);
     uint16_t* Bs16 = As16 + BM * PB;
@@ -637,31 +656,36 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
     }
     if (kbeg >= kend) __syncthreads();
   } else {
-  float4 ra[4], rb[4];
+  float4 ra[BMT / 32], rb[4];
   if (kbeg < kend) {
-    load_chunk<TA, TB>(p, A, B, m0, n0, kbeg, kend, interior, ra, rb);
-    store_a<TA>(Abase, ra);
+    load_chunk<TA, TB, BMT>(p, A, B, m0, n0, kbeg, kend, interior, ra, rb);
+    store_a<TA, BMT>(Abase, ra);
     store_b<TB>(Bbase, rb);
   }
   __syncthreads();
   int buf = 0;
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
     const bool more = k0 + BK < kend;
-    if (more) load_chunk<TA, TB>(p, A, B, m0, n0, k0 + BK, kend, interior, ra, rb);
+    if (more) load_chunk<TA, TB, BMT>(p, A, B, m0, n0, k0 + BK, kend, interior, ra, rb);
     const float* Ap = Abase + buf * PANEL;
     const float* Bp = Bbase + buf * PANEL;
 #pragma unroll
     for (int j = 0; j < BK / 8; ++j) {
       // fragments of steps 4j .. 4j+3: k = 8j + 4h + q for q = 0..3
       float fa0[4], fa1[4], fb0[4], fb1[4];
-      frag4<!TA>(Ap, wm * 64 + l32, 8 * j + 4 * h, fa0, fa1);
+      if constexpr (MT == 2)
+        frag4<!TA>(Ap, wm * 64 + l32, 8 * j + 4 * h, fa0, fa1);
+      else
+        frag1<!TA>(Ap, wm * 32 + l32, 8 * j + 4 * h, fa0);
       frag4<TB>(Bp, wn * 64 + l32, 8 * j + 4 * h, fb0, fb1);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb0[q], acc[0][0], 0, 0, 0);
         acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb1[q], acc[0][1], 0, 0, 0);
-        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb0[q], acc[1][0], 0, 0, 0);
-        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb1[q], acc[1][1], 0, 0, 0);
+        if constexpr (MT == 2) {
+          acc[MT - 1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb0[q], acc[MT - 1][0], 0, 0, 0);
+          acc[MT - 1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb1[q], acc[MT - 1][1], 0, 0, 0);
+        }
       }
     }
     if constexpr ((E & E_DBIAS) != 0) {
@@ -675,7 +699,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
     if (NBUF == 2) {
       // the other buffer was last read in the previous chunk, before the barrier that ended it
       if (more) {
-        store_a<TA>(Abase + (buf ^ 1) * PANEL, ra);
+        store_a<TA, BMT>(Abase + (buf ^ 1) * PANEL, ra);
         store_b<TB>(Bbase + (buf ^ 1) * PANEL, rb);
       }
       __syncthreads();
@@ -683,7 +707,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
     } else {
       __syncthreads();
       if (more) {
-        store_a<TA>(Abase, ra);
+        store_a<TA, BMT>(Abase, ra);
         store_b<TB>(Bbase, rb);
         __syncthreads();
       }
@@ -710,10 +734,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
     }
   }
 
-  // Stage the 128x128 tile through LDS, one 64-row half (the two waves with wm == half) at a time
-  // (accumulator layout of v_mfma_f32_32x32x2_f32: lane l, register r holds row
-  // 8*(r/4) + 4*(l/32) + r%4, column l%32 of its 32x32 block), then run the epilogue on
-  // row-contiguous float4s: thread t handles column group t%32 of rows t/32 + 8i of the half.
+  // Stage the tile through LDS 64 rows at a time (BMT = 128: one half, the two waves with
+  // wm == half; BMT = 64: all four waves) (accumulator layout of v_mfma_f32_32x32x2_f32: lane l,
+  // register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32 of its 32x32 block), then run the
+  // epilogue on row-contiguous float4s: thread t handles column group t%32 of rows t/32 + 8i.
   float* T = smem;
   const int cg = 4 * (threadIdx.x & 31);
   const int col = n0 + cg;
@@ -726,16 +750,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
                        (((E & (E_GELU | E_RELU | E_DGELU | E_DRELU)) == 0) || (p.ldaux & 3) == 0) &&
                        ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
+  for (int half = 0; half < BMT / T_ROWS; ++half) {
     if (half) __syncthreads();  // the first half has been read out
-    if (wm == half) {
+    if (MT == 1 || wm == half) {
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int row = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const int row = (MT == 1 ? wm * 32 : mt * 32) + 8 * (r >> 2) + 4 * h + (r & 3);
             const int c = wn * 64 + nt * 32 + l32;
             T[row * T_S + c] = acc[mt][nt][r];
           }
@@ -807,9 +831,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
       double sum = 0.0;
 #pragma unroll
       for (int g = 0; g < NT / 32; ++g) sum += (double)T[g * BN + threadIdx.x];
-      p.nb_part[(long long)(m0 / BM) * BN + threadIdx.x] = sum;
+      p.nb_part[(long long)(m0 / BMT) * BN + threadIdx.x] = sum;
     }
   }
+}
+
+template <bool TA, bool TB, int E, bool BF>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TALOS_GEMM_WAVES))) void gemm_f32_kernel(
+    GemmArgs p) {
+  gemm_tile<TA, TB, E, BF, BM>(p);
+}
+
+// 64 x 128 tiles for the products whose 128 x 128 tiles would leave each CU fewer than two
+// workgroups (d = 128 outputs over 32K rows): twice the workgroups, half the serial chain each.
+template <bool TA, bool TB, int E>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_WAVES))) void gemm_f32_m64_kernel(
+    GemmArgs p) {
+  gemm_tile<TA, TB, E, false, 64>(p);
 }
 
 // ---------------------------------------------------------------------------
@@ -1227,7 +1265,29 @@ static GemmKernel pick_small(bool tA, bool tB, int e) {
 }
 #undef SMALL_CASE
 
+// The 64 x 128 tile kernel: the d = 128-wide products of a block (norm backward, the MLP output
+// with its residual, the attention output projection with the next norm).
+static GemmKernel pick_m64(bool tA, bool tB, int e) {
+  if (tA) return nullptr;
+  if (tB) return e == E_NORMB ? &gemm_f32_m64_kernel<false, true, E_NORMB> : nullptr;
+  if (e == (E_BIAS | E_RESID)) return &gemm_f32_m64_kernel<false, false, E_BIAS | E_RESID>;
+  if (e == (E_RESID | E_NORM)) return &gemm_f32_m64_kernel<false, false, E_RESID | E_NORM>;
+  if (e == (E_BIAS | E_RESID | E_NORM)) return &gemm_f32_m64_kernel<false, false, E_BIAS | E_RESID | E_NORM>;
+  return nullptr;
+}
+
 static int num_cus();
+
+// Rows per tile of an fp32 product on the 128-wide tiles with final epilogue e (after the
+// split-K decision): 64 when the output is one tile wide, the 128-row tiles would give fewer
+// than two workgroups per CU, K is not split and the 64-row kernel is instantiated for e
+// (measured at 32768 rows: the norm-backward products 61 -> 56 us at K = 512 and 41 -> 36 us at
+// K = 256; with 1024 or more tiles the 128-row tiles are 3-12% faster).
+static int tile_rows(const GemmDesc& d, int e, int ksplit) {
+  const long long tiles = (long long)((d.M + BM - 1) / BM) * ((d.N + BN - 1) / BN) * d.batch;
+  if (d.bf16 || d.batch != 1 || d.N > BN || ksplit > 1 || tiles >= 2LL * num_cus()) return BM;
+  return pick_m64(d.transA != 0, d.transB != 0, e) ? 64 : BM;
+}
 
 static int gemm_launch_one(const GemmDesc& d, hipStream_t stream);
 
@@ -1244,7 +1304,8 @@ __global__ void add_last_rows_kernel(int nb, int seq, int n, const int32_t* __re
 // whole 128-wide row, fp32, one batch, float4 rows, and room for the per-tile partials.
 static bool normb_fused(const GemmDesc& d) {
   auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-  const int tiles_m = (d.M + BM - 1) / BM;
+  const int bm = tile_rows(d, E_NORMB, 1);
+  const int tiles_m = (d.M + bm - 1) / bm;
   return d.fuse_norm && d.N == BN && !d.bf16 && d.batch == 1 && !d.transA && d.transB && !use_small(d, num_cus()) &&
          d.beta == 0.f && !d.bias && !d.resid && d.act == GEMM_ACT_NONE && d.dact == GEMM_DACT_NONE &&
          d.rope_cols == 0 && !d.norm_out && !d.dbias && a16(d.normb_x) && a16(d.normb_dx) && a16(d.normb_gain) &&
@@ -1276,7 +1337,8 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
     g.ksplit = 1;
     if (int rc = gemm_launch_one(g, stream)) return rc;
     if (!d.normb_dw) return TALOS_OK;
-    return reduce_parts_launch(d.N, (d.M + BM - 1) / BM, d.normb_ws, d.normb_beta_dw, d.normb_dw, stream);
+    const int bm = tile_rows(d, E_NORMB, 1);
+    return reduce_parts_launch(d.N, (d.M + bm - 1) / bm, d.normb_ws, d.normb_beta_dw, d.normb_dw, stream);
   }
   return gemm_launch_one(d, stream);
 }
@@ -1295,19 +1357,21 @@ static int gemm_launch_one(const GemmDesc& d, hipStream_t stream) {
   GemmArgs a = to_args(d);
   if (d.M == 0 || d.N == 0 || d.batch == 0) return TALOS_OK;
   const bool small = use_small(d, num_cus());
-  const unsigned tiles = small ? ceil_div(d.M, SBM) * ceil_div(d.N, SBN) : ceil_div(d.M, BM) * ceil_div(d.N, BN);
   if (d.K == 0) {
     // C = beta*C (+ epilogue): run the kernel with an empty K loop.
     a.ksplit = 1;
     a.kper = 0;
   }
-  a.nblocks = (int)(tiles * (unsigned)d.batch * (unsigned)a.ksplit);
-  dim3 grid((unsigned)((a.nblocks + 7) / 8 * 8));
   const int e = epi_flags(d);
   const bool split = a.ksplit > 1;
   const int ke = split ? (E_SPLIT | (e & E_DBIAS)) : e;
-  GemmKernel kern = small ? pick_small(d.transA != 0, d.transB != 0, ke)
-                          : pick_kernel(d.transA != 0, d.transB != 0, ke, d.bf16);
+  const int bm = small ? SBM : tile_rows(d, ke, a.ksplit);
+  const unsigned tiles = small ? ceil_div(d.M, SBM) * ceil_div(d.N, SBN) : ceil_div(d.M, bm) * ceil_div(d.N, BN);
+  a.nblocks = (int)(tiles * (unsigned)d.batch * (unsigned)a.ksplit);
+  dim3 grid((unsigned)((a.nblocks + 7) / 8 * 8));
+  GemmKernel kern = small      ? pick_small(d.transA != 0, d.transB != 0, ke)
+                    : bm == 64 ? pick_m64(d.transA != 0, d.transB != 0, ke)
+                               : pick_kernel(d.transA != 0, d.transB != 0, ke, d.bf16);
   if (kern == nullptr) {
     set_error("gemm: epilogue combination 0x%x is not instantiated for transA=%d transB=%d%s", e, d.transA, d.transB,
               d.bf16 ? " (bf16)" : "");
@@ -1317,6 +1381,9 @@ static int gemm_launch_one(const GemmDesc& d, hipStream_t stream) {
   char name[64];
   if (small)
     snprintf(name, sizeof(name), "gemm_small_kernel<%s, %s, %d>", d.transA ? "true" : "false",
+             d.transB ? "true" : "false", ke);
+  else if (bm == 64)
+    snprintf(name, sizeof(name), "gemm_f32_m64_kernel<%s, %s, %d>", d.transA ? "true" : "false",
              d.transB ? "true" : "false", ke);
   else
     snprintf(name, sizeof(name), "gemm_f32_kernel<%s, %s, %d, %s>", d.transA ? "true" : "false",
@@ -1331,12 +1398,12 @@ static int gemm_launch_one(const GemmDesc& d, hipStream_t stream) {
       if (d.aux) bytes += 4.0 * MN;
       if (d.norm_out) bytes += 4.0 * (MN + d.M + d.N);
       // E_NORMB: x (and the addend) read, dx written instead of C, rstd and gain read
-      if (d.normb_dx) bytes += 4.0 * (MN * (1 + (d.normb_add != nullptr)) + d.M + d.N) + 8.0 * (d.M / BM + 1) * d.N;
+      if (d.normb_dx) bytes += 4.0 * (MN * (1 + (d.normb_add != nullptr)) + d.M + d.N) + 8.0 * (d.M / bm + 1) * d.N;
       if (d.bias) bytes += 4.0 * d.N;
     }
     ProfScope ps(stream, name, 2.0 * MN * d.K * d.batch, bytes * d.batch);
     hipLaunchKernelGGL(kern, grid, dim3(NT), 0, stream, a);
-    TALOS_LAUNCHED(small ? "gemm_small_kernel" : "gemm_f32_kernel");
+    TALOS_LAUNCHED(small ? "gemm_small_kernel" : bm == 64 ? "gemm_f32_m64_kernel" : "gemm_f32_kernel");
   }
   if (split) {
     const long long RN = (long long)(d.M + (d.dbias ? 1 : 0)) * d.N;

@@ -160,12 +160,15 @@ def _block_run(unfused, cfg, p, x, G):
     return res
 
 
-def test_c3_block_full_size(oracle):
-    B, S, d, H, F = 512, 64, 128, 4, 512
-    rng = np.random.default_rng(33)
+@pytest.mark.parametrize("B,S,causal", [(512, 64, 1), (289, 61, 0)])
+def test_c3_block_full_size(oracle, B, S, causal):
+    # (289, 61): 17629 rows, not a multiple of 64, so the 64-row tiles of the d = 128 products
+    # (norm backward at K = 512, the MLP output with its residual) end in a partial tile
+    d, H, F = 128, 4, 512
+    rng = np.random.default_rng(33 + S)
     p = f32(block_params(rng, d, F, gain_jitter=True))
     x, G = f32(rng.normal(size=(B, S, d))), f32(rng.normal(size=(B, S, d)))
-    args = (B, S, d, H, d // H, F, 1, 0, 1e-6, 1e4)
+    args = (B, S, d, H, d // H, F, causal, 0, 1e-6, 1e4)
     out_r, dp_r, dx_r = oracle.block_fwd_bwd(oracle.BlockCfg(*args), p, x, G)
     for unfused in (False, True):
         tag = "unfused" if unfused else "fused"
