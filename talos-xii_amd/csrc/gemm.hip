@@ -570,11 +570,20 @@ __device__ __forceinline__ void store_bf(uint16_t* S, const uint32_t (&o)[16]) {
   }
 }
 
-// One output tile of BMT (128 or 64) x 128 rows / columns: four waves, wave (wm, wn) the
-// [BMT / 2, 64] block at rows wm BMT / 2, columns 64 wn, as 2 x 2 (BMT = 128) or 1 x 2 (BMT = 64)
-// 32 x 32 accumulators.
+// The XCD-aware order: the dispatcher sends workgroup i to XCD i % 8, so logical tiles are dealt
+// out in contiguous runs per XCD; the N tiles of one M panel (and the tiles of one K split)
+// then share that XCD's L2 instead of fetching the same operand panel once per XCD. The grid is
+// padded to a multiple of 8; padding workgroups exit before any barrier.
+__device__ __forceinline__ int xcd_logical() {
+  const int per_xcd = (int)(gridDim.x >> 3);
+  return (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+}
+
+// One output tile of BMT (128 or 64) x 128 rows / columns for logical workgroup `logical` (in
+// [0, p.nblocks)): four waves, wave (wm, wn) the [BMT / 2, 64] block at rows wm BMT / 2,
+// columns 64 wn, as 2 x 2 (BMT = 128) or 1 x 2 (BMT = 64) 32 x 32 accumulators.
 template <bool TA, bool TB, int E, bool BF, int BMT>
-__device__ __forceinline__ void gemm_tile(GemmArgs p) {
+__device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
   __shared__ __align__(16) float smem[SMEM_FLOATS];
   static_assert(BMT == 128 || (BMT == 64 && !BF), "64-row tiles are fp32 only");
   constexpr int MT = BMT / 64;  // 32-row accumulator blocks per wave
@@ -582,15 +591,8 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p) {
   float* const Abase = smem;
   float* const Bbase = smem + NBUF * PANEL;
 
-  // XCD-aware order: the dispatcher sends workgroup i to XCD i % 8, so logical tiles are dealt
-  // out in contiguous runs per XCD; the N tiles of one M panel (and the tiles of one K split)
-  // then share that XCD's L2 instead of fetching the same operand panel once per XCD. The grid
-  // is padded to a multiple of 8; padding workgroups exit before any barrier.
   const int tiles_n = (p.N + BN - 1) / BN;
   const int tiles = tiles_n * ((p.M + BMT - 1) / BMT);
-  const int per_xcd = (int)(gridDim.x >> 3);
-  const int logical = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
-  if (logical >= p.nblocks) return;
   const int tile = logical % tiles;
   const int m0 = (tile / tiles_n) * BMT;
   const int n0 = (tile % tiles_n) * BN;
@@ -839,7 +841,9 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p) {
 template <bool TA, bool TB, int E, bool BF>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TALOS_GEMM_WAVES))) void gemm_f32_kernel(
     GemmArgs p) {
-  gemm_tile<TA, TB, E, BF, BM>(p);
+  const int logical = xcd_logical();
+  if (logical >= p.nblocks) return;
+  gemm_tile<TA, TB, E, BF, BM>(p, logical);
 }
 
 // 64 x 128 tiles for the products whose 128 x 128 tiles would leave each CU fewer than two
@@ -847,7 +851,22 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BF ? 2 : TAL
 template <bool TA, bool TB, int E>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_WAVES))) void gemm_f32_m64_kernel(
     GemmArgs p) {
-  gemm_tile<TA, TB, E, false, 64>(p);
+  const int logical = xcd_logical();
+  if (logical >= p.nblocks) return;
+  gemm_tile<TA, TB, E, false, 64>(p, logical);
+}
+
+// Two split-K products of one shape class in one grid (the weight gradients of a block's MLP):
+// the first p0.nblocks logical workgroups run p0, the next p1.nblocks p1. Four workgroups per CU
+// where each product alone would give two.
+template <bool TA, bool TB, int E>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_WAVES))) void gemm_f32_pair_kernel(
+    GemmArgs p0, GemmArgs p1) {
+  const int logical = xcd_logical();
+  if (logical < p0.nblocks)
+    gemm_tile<TA, TB, E, false, BM>(p0, logical);
+  else if (logical < p0.nblocks + p1.nblocks)
+    gemm_tile<TA, TB, E, false, BM>(p1, logical - p0.nblocks);
 }
 
 // ---------------------------------------------------------------------------
@@ -1343,6 +1362,22 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
   return gemm_launch_one(d, stream);
 }
 
+// The fixed-order f64 combination of a split-K product's partials (and the bias epilogue).
+static int split_reduce(const GemmDesc& d, const GemmArgs& a, int e, hipStream_t stream) {
+  const long long RN = (long long)(d.M + (d.dbias ? 1 : 0)) * d.N;
+  dim3 rg((unsigned)((RN + 63) / 64), d.batch);
+  const int re = e & (E_BETA | E_BIAS);
+  char rname[48];
+  snprintf(rname, sizeof(rname), "gemm_splitk_reduce<%d>", re);
+  ProfScope ps(stream, rname, 0.0, 4.0 * (double)RN * d.batch * (a.ksplit + 1 + (d.beta != 0.f)));
+  if (re == 0) hipLaunchKernelGGL(gemm_splitk_reduce<0>, rg, dim3(256), 0, stream, a);
+  else if (re == E_BETA) hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA>, rg, dim3(256), 0, stream, a);
+  else if (re == E_BIAS) hipLaunchKernelGGL(gemm_splitk_reduce<E_BIAS>, rg, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA | E_BIAS>, rg, dim3(256), 0, stream, a);
+  TALOS_LAUNCHED("gemm_splitk_reduce");
+  return TALOS_OK;
+}
+
 static int gemm_launch_one(const GemmDesc& d, hipStream_t stream) {
   if (d.norm_out && (!d.fuse_norm || d.N != BN || d.bf16 || d.batch != 1 || use_small(d, num_cus()))) {
     // the fused row norm needs the whole 128-wide row in one 128x128 tile: otherwise the product,
@@ -1405,20 +1440,44 @@ static int gemm_launch_one(const GemmDesc& d, hipStream_t stream) {
     hipLaunchKernelGGL(kern, grid, dim3(NT), 0, stream, a);
     TALOS_LAUNCHED(small ? "gemm_small_kernel" : bm == 64 ? "gemm_f32_m64_kernel" : "gemm_f32_kernel");
   }
-  if (split) {
-    const long long RN = (long long)(d.M + (d.dbias ? 1 : 0)) * d.N;
-    dim3 rg((unsigned)((RN + 63) / 64), d.batch);
-    const int re = e & (E_BETA | E_BIAS);
-    char rname[48];
-    snprintf(rname, sizeof(rname), "gemm_splitk_reduce<%d>", re);
-    ProfScope ps(stream, rname, 0.0, 4.0 * (double)RN * d.batch * (a.ksplit + 1 + (d.beta != 0.f)));
-    if (re == 0) hipLaunchKernelGGL(gemm_splitk_reduce<0>, rg, dim3(256), 0, stream, a);
-    else if (re == E_BETA) hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA>, rg, dim3(256), 0, stream, a);
-    else if (re == E_BIAS) hipLaunchKernelGGL(gemm_splitk_reduce<E_BIAS>, rg, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL(gemm_splitk_reduce<E_BETA | E_BIAS>, rg, dim3(256), 0, stream, a);
-    TALOS_LAUNCHED("gemm_splitk_reduce");
-  }
+  if (split) return split_reduce(d, a, e, stream);
   return TALOS_OK;
+}
+
+// Two products launched as one grid (gemm_f32_pair_kernel) when both are fp32 split-K weight
+// gradients (transA, op(B) plain, one batch) on 128-row tiles with the same epilogue (with or
+// without the fused bias gradient), each with its own workspace; otherwise one after the other.
+// Each product's partials are then combined by its own reduction, as gemm_launch does.
+int gemm_launch_pair(const GemmDesc& d0, const GemmDesc& d1, hipStream_t stream) {
+  const int ncu = num_cus();
+  GemmArgs a0 = to_args(d0), a1 = to_args(d1);
+  const int e0 = epi_flags(d0), e1 = epi_flags(d1);
+  auto pairable = [&](const GemmDesc& d, const GemmArgs& a, int e) {
+    return d.transA && !d.transB && !d.bf16 && d.batch == 1 && d.M > 0 && d.N > 0 && d.K > 0 && a.ksplit > 1 &&
+           !use_small(d, ncu) && (e & ~E_DBIAS) == 0 && d.workspace != nullptr;
+  };
+  if (!pairable(d0, a0, e0) || !pairable(d1, a1, e1) || e0 != e1 || d0.workspace == d1.workspace) {
+    if (int rc = gemm_launch(d0, stream)) return rc;
+    return gemm_launch(d1, stream);
+  }
+  const int ke = E_SPLIT | (e0 & E_DBIAS);
+  a0.nblocks = (int)(ceil_div(d0.M, BM) * ceil_div(d0.N, BN) * (unsigned)a0.ksplit);
+  a1.nblocks = (int)(ceil_div(d1.M, BM) * ceil_div(d1.N, BN) * (unsigned)a1.ksplit);
+  dim3 grid((unsigned)((a0.nblocks + a1.nblocks + 7) / 8 * 8));
+  {
+    const double f = 2.0 * ((double)d0.M * d0.N * d0.K + (double)d1.M * d1.N * d1.K);
+    const double bytes = 4.0 * ((double)d0.M * d0.K + (double)d0.K * d0.N + (double)d0.M * d0.N +
+                                (double)d1.M * d1.K + (double)d1.K * d1.N + (double)d1.M * d1.N);
+    char name[64];
+    snprintf(name, sizeof(name), "gemm_f32_pair_kernel<true, false, %d>", ke);
+    ProfScope ps(stream, name, f, bytes);
+    void (*kern)(GemmArgs, GemmArgs) = ke == E_SPLIT ? &gemm_f32_pair_kernel<true, false, E_SPLIT>
+                                                     : &gemm_f32_pair_kernel<true, false, E_SPLIT | E_DBIAS>;
+    hipLaunchKernelGGL(kern, grid, dim3(NT), 0, stream, a0, a1);
+    TALOS_LAUNCHED("gemm_f32_pair_kernel");
+  }
+  if (int rc = split_reduce(d0, a0, e0, stream)) return rc;
+  return split_reduce(d1, a1, e1, stream);
 }
 
 static int num_cus() {

@@ -88,5 +88,8 @@ struct GemmDesc {
 size_t gemm_plan_split(GemmDesc& d, int num_cu);
 // Enqueues the GEMM. Validation of shapes and pointers is the caller's job.
 int gemm_launch(const GemmDesc& d, hipStream_t stream);
+// Two products in one launch where both are split-K weight gradients of one shape class (each
+// with its own workspace); otherwise gemm_launch on each.
+int gemm_launch_pair(const GemmDesc& d0, const GemmDesc& d1, hipStream_t stream);
 
 }  // namespace talos

@@ -267,6 +267,7 @@ struct PlanCall {
 };
 
 // Largest split-K workspace among the weight-gradient GEMMs of a configuration.
+static size_t align_ws(size_t bytes) { return (bytes + 255) / 256 * 256; }
 static size_t wgrad_ws(talos_plan_s* p, int M_tok, int rows, int cols) {
   GemmDesc g;
   g.transA = 1;
@@ -362,8 +363,8 @@ static int alloc_block_buffers(talos_plan_s* p, const talos_block_cfg& c, int n_
     ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, 3 * (int)d));
     ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, (int)d));
   }
-  ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, (int)F));
-  ws = std::max(ws, wgrad_ws(p, (int)M, (int)F, (int)d));
+  // the MLP's two weight gradients run as one launch, each in its own part of the workspace
+  ws = std::max(ws, align_ws(wgrad_ws(p, (int)M, (int)F, (int)d)) + wgrad_ws(p, (int)M, (int)d, (int)F));
   p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, ws);
   size_t red = std::max(colsum_workspace_bytes((int)M, (int)F), rmsnorm_bwd_workspace_bytes((int)M, (int)d));
   p->red_ws_bytes = std::max(p->red_ws_bytes, red);
@@ -458,6 +459,74 @@ static int wgrad(talos_plan_s* p, hipStream_t s, const void* reads, int M, int N
   hipEvent_t e = nullptr;
   if ((rc = reader_event(p, reads, &e))) return rc;
   TALOS_HIP(hipEventRecord(e, p->side));
+  return TALOS_OK;
+}
+
+// One weight-gradient product C = A^T B (+ the bias gradient into dbias); `reads` names the
+// gradient buffer it reads (B, or the buffer B points into).
+struct WgradOp {
+  const void* reads;
+  int M, N, K;
+  const float* A;
+  long long lda;
+  const float* B;
+  long long ldb;
+  float* C;
+  long long ldc;
+  float* dbias;
+};
+
+// Its GemmDesc with the split-K count planned for a workspace of ws_bytes at wsp (unsplit when
+// the split would not fit); *used = the workspace bytes the split takes.
+static GemmDesc wgrad_desc(const talos_plan_s* p, const WgradOp& w, float* wsp, size_t ws_bytes, size_t* used) {
+  GemmDesc g;
+  g.transA = 1;
+  g.M = w.M;
+  g.N = w.N;
+  g.K = w.K;
+  g.A = w.A;
+  g.lda = w.lda;
+  g.B = w.B;
+  g.ldb = w.ldb;
+  g.C = w.C;
+  g.ldc = w.ldc;
+  g.dbias = w.dbias;
+  g.bf16 = p->bf16;
+  g.ksplit = 0;
+  size_t ws = gemm_plan_split(g, p->num_cu);
+  if (ws > ws_bytes) {
+    g.ksplit = 1;
+    ws = 0;
+  }
+  g.workspace = wsp;
+  *used = ws;
+  return g;
+}
+
+// The two weight-gradient products of a block's MLP (W2 and W1, both over all tokens) as one
+// launch (gemm_launch_pair: four workgroups per CU where each alone gives two), on the side stream
+// when there is one; the first takes the front of the workspace, the second what follows.
+static int wgrad_pair(talos_plan_s* p, hipStream_t s, const WgradOp& w0, const WgradOp& w1) {
+  hipStream_t ls = s;
+  float* base = p->gemm_ws;
+  if (p->side) {
+    TALOS_HIP(hipEventRecord(p->ev_fork, s));
+    TALOS_HIP(hipStreamWaitEvent(p->side, p->ev_fork, 0));
+    ls = p->side;
+    base = p->gemm_ws2;
+  }
+  size_t u0 = 0, u1 = 0;
+  const GemmDesc g0 = wgrad_desc(p, w0, base, p->gemm_ws_bytes, &u0);
+  const size_t off = align_ws(u0);
+  const GemmDesc g1 =
+      wgrad_desc(p, w1, base + off / sizeof(float), off < p->gemm_ws_bytes ? p->gemm_ws_bytes - off : 0, &u1);
+  int rc = gemm_launch_pair(g0, g1, ls);
+  if (rc || !p->side) return rc;
+  for (const void* buf : {w0.reads, w1.reads}) {
+    hipEvent_t e = nullptr;
+    if ((rc = reader_event(p, buf, &e))) return rc;
+    TALOS_HIP(hipEventRecord(e, p->side));
+  }
   return TALOS_OK;
 }
 
@@ -797,10 +866,8 @@ static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const f
                               const float* u, const float* a, const float* gout, float* g_u, float* g_xn, float* g_h2,
                               float* g_o, hipStream_t s, bool skip_go = false) {
   const int d = c.d_model, F = c.ffn_dim, ow = attn_width(c);
-  // out = h2 + a.W2 + b2
-  int rc = wgrad(p, s, gout, F, d, R, a, F, gout, d, G + o.w2, d, G + o.b2);
+  int rc = before_write(p, s, g_u);
   if (rc) return rc;
-  if ((rc = before_write(p, s, g_u))) return rc;
   {
     GemmDesc g;
     g.transB = 1;
@@ -820,8 +887,9 @@ static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const f
     rc = gemm_launch(g, s);
     if (rc) return rc;
   }
-  // u = xn2.W1 + b1
-  rc = wgrad(p, s, g_u, d, F, R, xn2, d, g_u, F, G + o.w1, F, G + o.b1);
+  // the weight gradients of out = h2 + a.W2 + b2 and of u = xn2.W1 + b1, in one launch
+  rc = wgrad_pair(p, s, WgradOp{gout, F, d, R, a, F, gout, d, G + o.w2, d, G + o.b2},
+                  WgradOp{g_u, d, F, R, xn2, d, g_u, F, G + o.w1, F, G + o.b1});
   if (rc) return rc;
   // xn2 = rmsnorm2(h2): g_h2 = its backward of g_u.W1^T, plus the residual gradient gout
   if ((rc = before_write(p, s, g_h2))) return rc;
