@@ -857,16 +857,25 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_W
 }
 
 // Two split-K products of one shape class in one grid (the weight gradients of a block's MLP):
-// the first p0.nblocks logical workgroups run p0, the next p1.nblocks p1. Four workgroups per CU
-// where each product alone would give two.
+// the logical workgroups alternate between the products (even: p0, odd: p1) while both have
+// some left, then the larger one takes the rest, so every XCD runs both products in contiguous
+// runs of each. Four workgroups per CU where each product alone would give two.
 template <bool TA, bool TB, int E>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(TALOS_GEMM_WAVES))) void gemm_f32_pair_kernel(
     GemmArgs p0, GemmArgs p1) {
   const int logical = xcd_logical();
-  if (logical < p0.nblocks)
-    gemm_tile<TA, TB, E, false, BM>(p0, logical);
-  else if (logical < p0.nblocks + p1.nblocks)
-    gemm_tile<TA, TB, E, false, BM>(p1, logical - p0.nblocks);
+  const int m = min(p0.nblocks, p1.nblocks);
+  if (logical < 2 * m) {
+    if (logical & 1)
+      gemm_tile<TA, TB, E, false, BM>(p1, logical >> 1);
+    else
+      gemm_tile<TA, TB, E, false, BM>(p0, logical >> 1);
+  } else if (logical < p0.nblocks + p1.nblocks) {
+    if (p0.nblocks > m)
+      gemm_tile<TA, TB, E, false, BM>(p0, logical - m);
+    else
+      gemm_tile<TA, TB, E, false, BM>(p1, logical - m);
+  }
 }
 
 // ---------------------------------------------------------------------------
