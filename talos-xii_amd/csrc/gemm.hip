@@ -66,7 +66,8 @@ enum : int {
   E_SPLIT = 256,  // write the fp32 partial tile of this K split (no epilogue)
   E_DBIAS = 512,  // also sum the columns of op(B) (bias gradient; transA = 1, transB = 0)
   E_NORM = 1024,  // also RMSNorm each output row (N = 128: the whole row is in the tile)
-  E_NORMB = 2048  // the output rows are dL/d(RMSNorm output): write that norm's backward instead
+  E_NORMB = 2048,  // the output rows are dL/d(RMSNorm output): write that norm's backward instead
+  E_NORMIN = 4096  // RMSNorm A's rows first (GemmDesc::nin_*): B rows scaled by the gain, rows by rstd
 };
 
 struct GemmArgs {
@@ -95,6 +96,10 @@ struct GemmArgs {
   long long ldn;
   float* norm_rstd;
   float norm_eps;
+  const float* nin_gain;  // E_NORMIN
+  float* nin_out;
+  float* nin_rstd;
+  float nin_eps;
   const float* nb_x;  // E_NORMB (GemmDesc::normb_*); nb_part [row tiles][N] f64 dgain partials
   const float* nb_rstd;
   const float* nb_gain;
@@ -659,8 +664,25 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
     if (kbeg >= kend) __syncthreads();
   } else {
   float4 ra[BMT / 32], rb[4];
+  // E_NORMIN: this thread's sum of squares over the A values it loads (thread t and t + 128 load
+  // the halves of tile row t % 128), and the gain applied to the B rows as they are loaded
+  float ssq = 0.f;
+  auto normin = [&](int k0) {
+    if constexpr ((E & E_NORMIN) != 0) {
+      static_assert(!TA && !TB && BMT == 128, "input norm: A and B plain, 128-row tiles");
+#pragma unroll
+      for (int i = 0; i < BMT / 32; ++i) ssq += ra[i].x * ra[i].x + ra[i].y * ra[i].y + ra[i].z * ra[i].z + ra[i].w * ra[i].w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int k = k0 + (threadIdx.x >> 5) + 8 * i;
+        const float g = k < kend ? p.nin_gain[k] : 0.f;
+        rb[i] = make_float4(rb[i].x * g, rb[i].y * g, rb[i].z * g, rb[i].w * g);
+      }
+    }
+  };
   if (kbeg < kend) {
     load_chunk<TA, TB, BMT>(p, A, B, m0, n0, kbeg, kend, interior, ra, rb);
+    normin(kbeg);
     store_a<TA, BMT>(Abase, ra);
     store_b<TB>(Bbase, rb);
   }
@@ -668,7 +690,10 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
   int buf = 0;
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
     const bool more = k0 + BK < kend;
-    if (more) load_chunk<TA, TB, BMT>(p, A, B, m0, n0, k0 + BK, kend, interior, ra, rb);
+    if (more) {
+      load_chunk<TA, TB, BMT>(p, A, B, m0, n0, k0 + BK, kend, interior, ra, rb);
+      normin(k0 + BK);
+    }
     const float* Ap = Abase + buf * PANEL;
     const float* Bp = Bbase + buf * PANEL;
 #pragma unroll
@@ -716,6 +741,39 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
     }
   }
   if (NBUF == 2 || kbeg >= kend) __syncthreads();
+  if constexpr ((E & E_NORMIN) != 0) {
+    // rstd of each tile row, the accumulators scaled by their row's, and (first column tile) the
+    // normalised rows and rstd written out
+    __shared__ float nin_rs[BMT];
+    smem[threadIdx.x] = ssq;
+    __syncthreads();
+    if (threadIdx.x < BMT)
+      nin_rs[threadIdx.x] = 1.0f / sqrtf((smem[threadIdx.x] + smem[threadIdx.x + BMT]) / (float)p.K + p.nin_eps);
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[mt][nt][r] *= nin_rs[wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3)];
+    {
+      // the tile rows lr = tn, tn + tiles_n, ... are this column tile's to write (the work is shared
+      // by the row's column tiles)
+      const int tn = n0 / BN, k4 = p.K >> 2, mine = (BMT - tn + tiles_n - 1) / tiles_n;
+      for (int i = threadIdx.x; i < mine * k4; i += NT) {
+        const int lr = tn + tiles_n * (i / k4), c = 4 * (i % k4), row = m0 + lr;
+        if (row >= p.M) continue;
+        const float rs = nin_rs[lr];
+        const float4 x = *reinterpret_cast<const float4*>(A + (long long)row * p.lda + c);
+        const float4 g = *reinterpret_cast<const float4*>(p.nin_gain + c);
+        *reinterpret_cast<float4*>(p.nin_out + (long long)row * p.K + c) =
+            make_float4(x.x * rs * g.x, x.y * rs * g.y, x.z * rs * g.z, x.w * rs * g.w);
+      }
+      const int lr = tn + tiles_n * (int)threadIdx.x;
+      if (lr < BMT && m0 + lr < p.M && p.nin_rstd) p.nin_rstd[m0 + lr] = nin_rs[lr];
+    }
+    __syncthreads();  // smem is the staging tile next
+  }
   }  // fp32 main loop
   if constexpr ((E & E_DBIAS) != 0) {
     // combine the two row halves; the M-tile-0 workgroups write the bias-gradient row
@@ -1151,6 +1209,10 @@ static GemmArgs to_args(const GemmDesc& d) {
   a.ldn = d.ldn;
   a.norm_rstd = d.norm_rstd;
   a.norm_eps = d.norm_eps;
+  a.nin_gain = d.nin_gain;
+  a.nin_out = d.nin_out;
+  a.nin_rstd = d.nin_rstd;
+  a.nin_eps = d.nin_eps;
   a.nb_x = d.normb_x;
   a.nb_rstd = d.normb_rstd;
   a.nb_gain = d.normb_gain;
@@ -1189,6 +1251,7 @@ static int epi_flags(const GemmDesc& d) {
   if (d.dbias) e |= E_DBIAS;
   if (d.norm_out) e |= E_NORM;
   if (d.normb_dx) e |= E_NORMB;
+  if (d.nin_gain) e |= E_NORMIN;
   return e;
 }
 
@@ -1243,6 +1306,8 @@ static GemmKernel pick_kernel(bool tA, bool tB, int e, bool bf) {
   GEMM_CASE_F32(false, false, E_BIAS | E_NORM)
   GEMM_CASE_F32(false, false, E_RESID | E_NORM)
   GEMM_CASE_F32(false, false, E_BIAS | E_RESID | E_NORM)
+  GEMM_CASE_F32(false, false, E_NORMIN)
+  GEMM_CASE_F32(false, false, E_ROPE | E_NORMIN)
   GEMM_CASE(false, true, 0)
   GEMM_CASE(false, true, E_BETA)
   GEMM_CASE(false, true, E_DGELU)
@@ -1326,6 +1391,14 @@ __global__ void add_last_rows_kernel(int nb, int seq, int n, const int32_t* __re
   if (i >= (long long)nb * n) return;
   const int b = (int)(i / n), col = (int)(i % n);
   c[((long long)b * seq + last_row(lens, b, seq)) * n + col] += add[i];
+}
+
+bool gemm_normin_supported(const GemmDesc& d) {
+  auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const int e = epi_flags(d) | E_NORMIN;
+  return !d.bf16 && !d.transA && !d.transB && d.batch == 1 && d.ksplit <= 1 && d.K > 0 && d.K <= 512 && d.K % 4 == 0 &&
+         (d.lda & 3) == 0 && a16(d.A) && a16(d.nin_gain) && a16(d.nin_out) && !use_small(d, num_cus()) &&
+         tile_rows(d, e, 1) == BM && pick_kernel(false, false, e, false) != nullptr;
 }
 
 // Whether the RMSNorm backward of a product can run in its epilogue: 128x128 tiles holding the

@@ -56,6 +56,14 @@ struct GemmDesc {
   long long ldn = 0;
   float* norm_rstd = nullptr;
   float norm_eps = 0.f;
+  // RMSNorm of A's rows before the product (A plain, K = the norm's width): the product is
+  // rmsnorm(A) * nin_gain times op(B), formed as rstd[row] * (A . (nin_gain (x) B)) with rstd =
+  // 1 / sqrt(mean(A[row]^2) + nin_eps) from the A rows the tile loads anyway; the normalised rows
+  // go to nin_out (row stride K) and rstd to nin_rstd. Only where gemm_normin_supported holds.
+  const float* nin_gain = nullptr;
+  float* nin_out = nullptr;
+  float* nin_rstd = nullptr;
+  float nin_eps = 0.f;
   // RMSNorm backward after the product, C = dL/d(the norm's output) (rmsnorm_bwd_launch's
   // arithmetic): normb_dx = rstd * (C * gain - x_hat * mean(C * gain * x_hat)) + normb_add (+
   // normb_add_last[b] on the last row of each sample b, rows of normb_seq; normb_dy_last[b] is
@@ -83,6 +91,10 @@ struct GemmDesc {
   // row kernels after the product, never in its epilogue (the cross-check of the fused epilogues)
   bool fuse_norm = true;
 };
+
+// Whether a product can normalise its A rows itself (nin_*): fp32, A plain with K <= 512 and a
+// multiple of 4 and 16-byte rows, 128-row tiles, one batch, no split, an instantiated epilogue.
+bool gemm_normin_supported(const GemmDesc& d);
 
 // Fills in ksplit (when 0) and returns the workspace bytes the descriptor needs.
 size_t gemm_plan_split(GemmDesc& d, int num_cu);

@@ -736,27 +736,34 @@ static void set_norm(const talos_plan_s* p, GemmDesc& g, const RowNorm& n, float
 static int block_qkv_forward(talos_plan_s* p, const talos_block_cfg& c, const float* P, const BlockOff& o,
                              talos_plan_s::Layer& L, hipStream_t s, bool normed) {
   const int M = c.batch * c.seq, d = c.d_model;
-  if (!normed)
+  GemmDesc g;
+  g.M = M;
+  g.N = 3 * d;
+  g.K = d;
+  g.A = L.xn1;
+  g.lda = d;
+  g.B = P + o.wqkv;
+  g.ldb = 3 * d;
+  g.C = L.qkv;
+  g.ldc = 3 * d;
+  g.rope_cos = p->rcos;
+  g.rope_sin = p->rsin;
+  g.rope_cols = 2 * d;
+  g.rope_dim = c.head_dim;
+  g.rope_seq = c.seq;
+  g.ksplit = 1;
+  if (!normed) {
+    // the product normalises x's rows itself (and writes xn1 and rstd1) where it can
+    GemmDesc gn = g;
+    gn.A = L.x;
+    gn.nin_gain = P + o.g1;
+    gn.nin_out = L.xn1;
+    gn.nin_rstd = L.rstd1;
+    gn.nin_eps = c.eps;
+    if (!p->unfused && !p->bf16 && gemm_normin_supported(gn)) return gemm_launch(gn, s);
     if (int rc = rmsnorm_fwd_launch(M, d, c.eps, L.x, P + o.g1, L.xn1, L.rstd1, s)) return rc;
-  {
-    GemmDesc g;
-    g.M = M;
-    g.N = 3 * d;
-    g.K = d;
-    g.A = L.xn1;
-    g.lda = d;
-    g.B = P + o.wqkv;
-    g.ldb = 3 * d;
-    g.C = L.qkv;
-    g.ldc = 3 * d;
-    g.rope_cos = p->rcos;
-    g.rope_sin = p->rsin;
-    g.rope_cols = 2 * d;
-    g.rope_dim = c.head_dim;
-    g.rope_seq = c.seq;
-    g.ksplit = 1;
-    return gemm_launch(g, s);
   }
+  return gemm_launch(g, s);
 }
 
 // Attention half of a block's forward: o = attention(rmsnorm(x)) with lse saved.
@@ -2138,9 +2145,14 @@ int talos_block_fwd_bwd_f32(talos_plan plan, const float* params, const float* x
   BlockOff bo = block_offsets(c, 0);
   auto& L = plan->layers[0];
   L.x = const_cast<float*>(x);
+  // the forward's last product writes the caller's out itself (the backward does not read it)
+  float* const own_out = L.out;
+  const bool direct = out && out != x;
+  if (direct) L.out = out;
   int rc = block_forward(plan, c, params, bo, L, s);
+  L.out = own_out;
   if (rc) return rc;
-  if (out) TALOS_HIP(hipMemcpyAsync(out, L.out, M * d * 4, hipMemcpyDeviceToDevice, s));
+  if (out && !direct) TALOS_HIP(hipMemcpyAsync(out, L.out, M * d * 4, hipMemcpyDeviceToDevice, s));
   rc = block_backward(plan, c, params, dparams, bo, L, gout, dx, s);
   if (rc) return rc;
   return entry_done(join_side(plan, s), as_stream(stream));
