@@ -1530,18 +1530,27 @@ static int gemm_launch_one(const GemmDesc& d, hipStream_t stream) {
 // gradients (transA, op(B) plain, one batch) on 128-row tiles with the same epilogue (with or
 // without the fused bias gradient), each with its own workspace; otherwise one after the other.
 // Each product's partials are then combined by its own reduction, as gemm_launch does.
-int gemm_launch_pair(const GemmDesc& d0, const GemmDesc& d1, hipStream_t stream) {
-  const int ncu = num_cus();
-  GemmArgs a0 = to_args(d0), a1 = to_args(d1);
+bool gemm_pairable(const GemmDesc& d0, const GemmDesc& d1) {
+  const GemmArgs a0 = to_args(d0), a1 = to_args(d1);
   const int e0 = epi_flags(d0), e1 = epi_flags(d1);
+  // (a product planned for 64x64 tiles runs on the 128x128 body here: the split-K partial layout
+  // does not depend on the tile; the two products' splits must be of similar length, or the
+  // longer one's workgroups run on alone)
   auto pairable = [&](const GemmDesc& d, const GemmArgs& a, int e) {
     return d.transA && !d.transB && !d.bf16 && d.batch == 1 && d.M > 0 && d.N > 0 && d.K > 0 && a.ksplit > 1 &&
-           !use_small(d, ncu) && (e & ~E_DBIAS) == 0 && d.workspace != nullptr;
+           (e & ~E_DBIAS) == 0 && d.workspace != nullptr;
   };
-  if (!pairable(d0, a0, e0) || !pairable(d1, a1, e1) || e0 != e1 || d0.workspace == d1.workspace) {
+  const int klo = std::min(a0.kper, a1.kper), khi = std::max(a0.kper, a1.kper);
+  return pairable(d0, a0, e0) && pairable(d1, a1, e1) && e0 == e1 && d0.workspace != d1.workspace && 2 * khi <= 3 * klo;
+}
+
+int gemm_launch_pair(const GemmDesc& d0, const GemmDesc& d1, hipStream_t stream) {
+  if (!gemm_pairable(d0, d1)) {
     if (int rc = gemm_launch(d0, stream)) return rc;
     return gemm_launch(d1, stream);
   }
+  GemmArgs a0 = to_args(d0), a1 = to_args(d1);
+  const int e0 = epi_flags(d0), e1 = epi_flags(d1);
   const int ke = E_SPLIT | (e0 & E_DBIAS);
   a0.nblocks = (int)(ceil_div(d0.M, BM) * ceil_div(d0.N, BN) * (unsigned)a0.ksplit);
   a1.nblocks = (int)(ceil_div(d1.M, BM) * ceil_div(d1.N, BN) * (unsigned)a1.ksplit);

@@ -103,5 +103,8 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream);
 // Two products in one launch where both are split-K weight gradients of one shape class (each
 // with its own workspace); otherwise gemm_launch on each.
 int gemm_launch_pair(const GemmDesc& d0, const GemmDesc& d1, hipStream_t stream);
+// Whether gemm_launch_pair runs the two as one grid (split-K weight gradients of one epilogue
+// with splits within 1.5x of each other in length).
+bool gemm_pairable(const GemmDesc& d0, const GemmDesc& d1);
 
 }  // namespace talos

@@ -359,10 +359,8 @@ static int alloc_block_buffers(talos_plan_s* p, const talos_block_cfg& c, int n_
     rc |= plan_alloc(p, &p->g_qkv, M * 3 * d);
   if (rc) return TALOS_ERR_ALLOC;
   size_t ws = 0;
-  if (!mla) {
-    ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, 3 * (int)d));
-    ws = std::max(ws, wgrad_ws(p, (int)M, (int)d, (int)d));
-  }
+  if (!mla)  // the Wqkv and Wo weight gradients run as one launch
+    ws = std::max(ws, align_ws(wgrad_ws(p, (int)M, (int)d, 3 * (int)d)) + wgrad_ws(p, (int)M, (int)d, (int)d));
   // the MLP's two weight gradients run as one launch, each in its own part of the workspace
   ws = std::max(ws, align_ws(wgrad_ws(p, (int)M, (int)F, (int)d)) + wgrad_ws(p, (int)M, (int)d, (int)F));
   p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, ws);
@@ -506,6 +504,22 @@ static GemmDesc wgrad_desc(const talos_plan_s* p, const WgradOp& w, float* wsp, 
 // The two weight-gradient products of a block's MLP (W2 and W1, both over all tokens) as one
 // launch (gemm_launch_pair: four workgroups per CU where each alone gives two), on the side stream
 // when there is one; the first takes the front of the workspace, the second what follows.
+// The pair's descriptors: the first at the front of the workspace base, the second after it.
+static void pair_descs(const talos_plan_s* p, float* base, const WgradOp& w0, const WgradOp& w1, GemmDesc* g0,
+                       GemmDesc* g1) {
+  size_t u0 = 0, u1 = 0;
+  *g0 = wgrad_desc(p, w0, base, p->gemm_ws_bytes, &u0);
+  const size_t off = align_ws(u0);
+  *g1 = wgrad_desc(p, w1, base + off / sizeof(float), off < p->gemm_ws_bytes ? p->gemm_ws_bytes - off : 0, &u1);
+}
+
+// Whether wgrad_pair would run w0 and w1 as one grid.
+static bool wgrad_pairable(const talos_plan_s* p, const WgradOp& w0, const WgradOp& w1) {
+  GemmDesc g0, g1;
+  pair_descs(p, p->gemm_ws, w0, w1, &g0, &g1);
+  return gemm_pairable(g0, g1);
+}
+
 static int wgrad_pair(talos_plan_s* p, hipStream_t s, const WgradOp& w0, const WgradOp& w1) {
   hipStream_t ls = s;
   float* base = p->gemm_ws;
@@ -515,11 +529,8 @@ static int wgrad_pair(talos_plan_s* p, hipStream_t s, const WgradOp& w0, const W
     ls = p->side;
     base = p->gemm_ws2;
   }
-  size_t u0 = 0, u1 = 0;
-  const GemmDesc g0 = wgrad_desc(p, w0, base, p->gemm_ws_bytes, &u0);
-  const size_t off = align_ws(u0);
-  const GemmDesc g1 =
-      wgrad_desc(p, w1, base + off / sizeof(float), off < p->gemm_ws_bytes ? p->gemm_ws_bytes - off : 0, &u1);
+  GemmDesc g0, g1;
+  pair_descs(p, base, w0, w1, &g0, &g1);
   int rc = gemm_launch_pair(g0, g1, ls);
   if (rc || !p->side) return rc;
   for (const void* buf : {w0.reads, w1.reads}) {
@@ -871,7 +882,7 @@ static int block_forward(talos_plan_s* p, const talos_block_cfg& c, const float*
 static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
                               int R, const float* ob, const float* h2, const float* xn2, const float* rstd2,
                               const float* u, const float* a, const float* gout, float* g_u, float* g_xn, float* g_h2,
-                              float* g_o, hipStream_t s, bool skip_go = false) {
+                              float* g_o, hipStream_t s, bool skip_go = false, bool defer_wo = false) {
   const int d = c.d_model, F = c.ffn_dim, ow = attn_width(c);
   int rc = before_write(p, s, g_u);
   if (rc) return rc;
@@ -903,9 +914,8 @@ static int block_mlp_backward(talos_plan_s* p, const talos_block_cfg& c, const f
   rc = norm_bwd_mm(p, s, R, d, F, g_u, F, P + o.w1, F, g_xn, h2, P + o.g2, rstd2, gout, nullptr, nullptr, 1, g_h2,
                    G + o.g2);
   if (rc) return rc;
-  // h2 = x + o.Wo
-  rc = wgrad(p, s, g_h2, ow, d, R, ob, ow, g_h2, d, G + o.wo, d);
-  if (rc) return rc;
+  // h2 = x + o.Wo (defer_wo: the caller launches this weight gradient together with Wqkv's)
+  if (!defer_wo && (rc = wgrad(p, s, g_h2, ow, d, R, ob, ow, g_h2, d, G + o.wo, d))) return rc;
   if (skip_go) return TALOS_OK;  // the attention backward forms g_o = g_h2.Wo^T itself
   return mm(p, s, 0, 1, R, ow, d, g_h2, d, P + o.wo, d, g_o, ow);
 }
@@ -926,10 +936,13 @@ static int block_norm1_backward(talos_plan_s* p, const talos_block_cfg& c, const
 // rmsnorm1's backward (block_norm1_backward).
 static int block_qkv_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
                               talos_plan_s::Layer& L, const float* g_h2, const float* g_h2_last, float* dx,
-                              hipStream_t s) {
+                              hipStream_t s, const WgradOp* with = nullptr) {
   const int M = c.batch * c.seq, d = c.d_model;
-  // qkv = xn1.Wqkv
-  int rc = wgrad(p, s, p->g_qkv, d, 3 * d, M, L.xn1, d, p->g_qkv, 3 * d, G + o.wqkv, 3 * d);
+  // qkv = xn1.Wqkv (with: another weight gradient over the same tokens, launched together where
+  // their splits are alike, else one after the other)
+  const WgradOp wqkv{p->g_qkv, d, 3 * d, M, L.xn1, d, p->g_qkv, 3 * d, G + o.wqkv, 3 * d, nullptr};
+  int rc = with ? wgrad_pair(p, s, wqkv, *with)
+                : wgrad(p, s, wqkv.reads, wqkv.M, wqkv.N, wqkv.K, wqkv.A, wqkv.lda, wqkv.B, wqkv.ldb, wqkv.C, wqkv.ldc);
   if (rc) return rc;
   // xn1 = rmsnorm1(x): dx = its backward of g_qkv.Wqkv^T, plus the residual gradient through h2
   if ((rc = before_write(p, s, dx))) return rc;
@@ -942,7 +955,7 @@ static int block_qkv_backward(talos_plan_s* p, const talos_block_cfg& c, const f
 // attention weights' and gain1's gradients and dx.
 static int block_attn_backward(talos_plan_s* p, const talos_block_cfg& c, const float* P, float* G, const BlockOff& o,
                                talos_plan_s::Layer& L, const float* g_o, const float* g_h2, const float* g_h2_last,
-                               float* dx, hipStream_t s) {
+                               float* dx, hipStream_t s, const WgradOp* with = nullptr) {
   if (c.attention == TALOS_ATTN_MLA) {
     int rc = mla_attn_backward(p, mla_dims(c), P, G, o.mla, L.xn1, L, g_o, p->g_xn, s);
     if (rc) return rc;
@@ -954,7 +967,7 @@ static int block_attn_backward(talos_plan_s* p, const talos_block_cfg& c, const 
   int rc = before_write(p, s, p->g_qkv);
   if (rc == TALOS_OK) rc = attn_bwd_launch(a, p->attn_ws, s);
   if (rc) return rc;
-  return block_qkv_backward(p, c, P, G, o, L, g_h2, g_h2_last, dx, s);
+  return block_qkv_backward(p, c, P, G, o, L, g_h2, g_h2_last, dx, s, with);
 }
 
 // Backward of one block: gout = dL/dout (read), writes dparams slots and dx. At S <= 32 with
@@ -964,15 +977,23 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
                           talos_plan_s::Layer& L, const float* gout, float* dx, hipStream_t s) {
   const int M = c.batch * c.seq;
   AttnDesc ad = block_attn_desc(p, c, L);
-  const bool fold = c.attention == TALOS_ATTN_MHA && !p->unfused && !p->bf16 && c.d_model == kWoFuseD &&
-                    attn_width(c) == kWoFuseD && attn_bwd_wo_supported(ad, P + o.wo, p->g_h2);
+  const bool mha = c.attention == TALOS_ATTN_MHA;
+  const bool fold = mha && !p->unfused && !p->bf16 && c.d_model == kWoFuseD && attn_width(c) == kWoFuseD &&
+                    attn_bwd_wo_supported(ad, P + o.wo, p->g_h2);
+  // standard attention: where their splits are alike (C3's 32K tokens), the Wo weight gradient
+  // waits for Wqkv's and launches with it; otherwise (C4's, 771 against 256 tokens a split) it
+  // runs as soon as g_h2 is ready
+  const int d = c.d_model, ow = attn_width(c);
+  const WgradOp wo{p->g_h2, ow, d, M, L.o, ow, p->g_h2, d, G + o.wo, d, nullptr};
+  const WgradOp wqkv{p->g_qkv, d, 3 * d, M, L.xn1, d, p->g_qkv, 3 * d, G + o.wqkv, 3 * d, nullptr};
+  const bool pair = mha && wgrad_pairable(p, wqkv, wo);
   int rc = block_mlp_backward(p, c, P, G, o, M, L.o, L.h2, L.xn2, L.rstd2, L.u, L.a, gout, p->g_u, p->g_xn, p->g_h2,
-                              p->g_o, s, fold);
+                              p->g_o, s, fold, pair);
   if (rc) return rc;
-  if (!fold) return block_attn_backward(p, c, P, G, o, L, p->g_o, p->g_h2, nullptr, dx, s);
+  if (!fold) return block_attn_backward(p, c, P, G, o, L, p->g_o, p->g_h2, nullptr, dx, s, pair ? &wo : nullptr);
   if ((rc = before_write(p, s, p->g_qkv))) return rc;
   if ((rc = attn_bwd_wo_launch(ad, P + o.wo, p->g_h2, s))) return rc;
-  return block_qkv_backward(p, c, P, G, o, L, p->g_h2, nullptr, dx, s);
+  return block_qkv_backward(p, c, P, G, o, L, p->g_h2, nullptr, dx, s, pair ? &wo : nullptr);
 }
 
 // Whether the PPO plan's last layer runs the attention of the last query only (standard
