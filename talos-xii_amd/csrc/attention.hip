@@ -1883,6 +1883,191 @@ __global__ __launch_bounds__(256) void attn_bwd_lastq_kernel(AttnArgs a, const f
   }
 }
 
+// ---------------------------------------------------------------------------
+// Last query with the value projection absorbed (the policy's last layer): v_j = xn_j . Wv per
+// head, and V carries no rotation, so o_h = sum_j p_j v_j = (sum_j p_j xn_j) . Wv_h. The forward
+// forms z_h = sum_j p_j xn_j over the sample's normalised input rows xn (width W = 128) instead
+// of reading value rows, and the caller multiplies z_h by Wv_h (a small batched product); the
+// backward takes u_h = Wv_h dO_h from the caller, forms dP_j = xn_j . u_h, and writes, besides dK
+// and the last query's dq, the value path's share of dL/dxn_j, sum_h p_j^h u_h, for the product
+// that forms the rest of dL/dxn. No value rows are ever formed.
+// ---------------------------------------------------------------------------
+constexpr int kVabsW = 128, kVabsH = 4, kVabsMaxS = 256;
+
+// z[b, h] = sum_j p_j xn_j / l (lanes hold columns 2 lane, 2 lane + 1); lse_last[b*H + h]. The
+// scores, the running maximum and the rescale are attn_fwd_lastq_kernel's.
+template <int D>
+__global__ __launch_bounds__(256) void attn_fwd_lastq_z_kernel(AttnArgs a, const float* __restrict__ xn, long long ldx,
+                                                               float* __restrict__ z, float* __restrict__ lse_last) {
+  constexpr int C = D / 4, RPP = 64 / C;
+  const int lane = threadIdx.x & 63, c = lane % C, r = lane / C;
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pair >= a.B * a.H) return;  // uniform per wave
+  const int b = pair / a.H, hh = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int Sk = key_len(a, b), t = Sk - 1;
+  float2 acc = make_float2(0.f, 0.f);
+  float m = kNegInf, l = 0.f;
+  if (Sk > 0) {
+    float4 q = last_query(a, b, tok0, t, hh, D, c);
+    q = make_float4(q.x * a.scale, q.y * a.scale, q.z * a.scale, q.w * a.scale);
+    for (int j0 = 0; j0 < Sk; j0 += RPP) {
+      const int j = j0 + r;
+      const bool ok = j < Sk;
+      const int jj = ok ? j : t;
+      const float4 k = ld4(a.k + (tok0 + jj) * a.ldk + hh * D + 4 * c);
+      const float sc = row_sum<C>(dot4(q, k));
+      const float s = ok ? sc : kNegInf;
+      const float mn = fmaxf(m, col_max<C>(s));
+      const float pj = ok ? expf(s - mn) : 0.f;
+      const float corr = m == kNegInf ? 0.f : expf(m - mn);
+      l = l * corr + col_sum<C>(pj);
+      acc = make_float2(acc.x * corr, acc.y * corr);
+      // the pass's rows, one at a time: p of row i from its lanes, the row's xn in column layout
+#pragma unroll
+      for (int i = 0; i < RPP; ++i) {
+        const float p_i = __shfl(pj, i * C, 64);
+        const int ji = min(j0 + i, Sk - 1);
+        const float2 x = *reinterpret_cast<const float2*>(xn + (tok0 + ji) * ldx + 2 * lane);
+        acc = make_float2(fmaf(p_i, x.x, acc.x), fmaf(p_i, x.y, acc.y));
+      }
+      m = mn;
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  *reinterpret_cast<float2*>(z + (long long)pair * kVabsW + 2 * lane) = make_float2(acc.x * inv, acc.y * inv);
+  if (lane == 0) lse_last[pair] = l > 0.f ? m + logf(l) : kNegInf;
+}
+
+// A workgroup per sample, wave h its head h (kVabsH heads of D). dk rows j < S (zero past the
+// sample's keys), dq_last, and wpre[b*S + j] = sum_h p_j^h u_h (zero past the keys), u = [B][H][W].
+template <int D>
+__global__ __launch_bounds__(64 * kVabsH) void attn_bwd_lastq_z_kernel(AttnArgs a, const float* __restrict__ xn,
+                                                                       long long ldx, const float* __restrict__ u,
+                                                                       const float* __restrict__ o_last, long long ldol,
+                                                                       const float* __restrict__ lse_last,
+                                                                       const float* __restrict__ do_last,
+                                                                       long long lddol, float* __restrict__ wpre) {
+  constexpr int C = D / 4, RPP = 64 / C;
+  __shared__ float ps[kVabsH][kVabsMaxS], dss[kVabsH][kVabsMaxS];
+  __shared__ __align__(16) float us[kVabsH][kVabsW];
+  const int lane = threadIdx.x & 63, c = lane % C, r = lane / C, hh = threadIdx.x >> 6;
+  const int b = blockIdx.x, pair = b * a.H + hh;
+  const long long tok0 = (long long)b * a.S;
+  const int Sk = key_len(a, b), t = Sk > 0 ? Sk - 1 : 0;
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 qs = z4;
+  float Dd = 0.f, lse = 0.f;
+  if (Sk > 0) {
+    const float4 q = last_query(a, b, tok0, t, hh, D, c);
+    qs = make_float4(q.x * a.scale, q.y * a.scale, q.z * a.scale, q.w * a.scale);
+    const float4 g = ld4(do_last + (long long)b * lddol + hh * D + 4 * c);
+    Dd = row_sum<C>(dot4(g, ld4(o_last + (long long)b * ldol + hh * D + 4 * c)));
+    lse = lse_last[pair];
+  }
+  const float2 uh = *reinterpret_cast<const float2*>(u + (long long)pair * kVabsW + 2 * lane);
+  *reinterpret_cast<float2*>(&us[hh][2 * lane]) = uh;
+  // u_h again in the two-rows-a-pass layout of the dP pass: lane (row half rh, c2) holds columns
+  // 4 c2 .. 4 c2 + 3
+  constexpr int C2 = kVabsW / 4;  // 32 lanes per xn row
+  const int c2 = lane % C2, rh = lane / C2;
+  const float4 u4 = ld4(u + (long long)pair * kVabsW + 4 * c2);
+  // p_j for every key (row layout)
+  for (int j0 = 0; j0 < a.S; j0 += RPP) {
+    const int j = j0 + r;
+    const bool ok = j < Sk;
+    const float4 k = ld4(a.k + (tok0 + (ok ? j : 0)) * a.ldk + hh * D + 4 * c);
+    const float s = row_sum<C>(dot4(qs, k));
+    if (c == 0 && j < a.S) ps[hh][j] = ok ? expf(s - lse) : 0.f;
+  }
+  __syncthreads();
+  // dS_j = p_j (xn_j . u_h - D): two rows a pass (32 lanes a row, float4 each), four passes'
+  // loads in flight together
+#pragma unroll 4
+  for (int j0 = 0; j0 < Sk; j0 += 2) {
+    const int j = j0 + rh;
+    const bool ok = j < Sk;
+    const float4 x = ld4(xn + (tok0 + (ok ? j : j0)) * ldx + 4 * c2);
+    const float dp = row_sum<C2>(dot4(x, u4));
+    if (ok && c2 == 0) dss[hh][j] = ps[hh][j] * (dp - Dd);
+  }
+  __syncthreads();
+  // dk_j = R^T(dS_j scale q), dq = R^T(scale sum_j dS_j k_j) (row layout)
+  float4 dq = z4;
+  for (int j0 = 0; j0 < a.S; j0 += RPP) {
+    const int j = j0 + r;
+    const bool ok = j < Sk;
+    const float dS = ok ? dss[hh][j] : 0.f;
+    if (ok) {
+      const float4 k = ld4(a.k + (tok0 + j) * a.ldk + hh * D + 4 * c);
+      dq = make_float4(dq.x + dS * k.x, dq.y + dS * k.y, dq.z + dS * k.z, dq.w + dS * k.w);
+    }
+    if (j < a.S)
+      st4(a.dk_out + (tok0 + j) * a.lddk + hh * D + 4 * c,
+          rope_t4(make_float4(dS * qs.x, dS * qs.y, dS * qs.z, dS * qs.w), 4 * c, j, a));
+  }
+  dq = make_float4(col_sum<C>(dq.x) * a.scale, col_sum<C>(dq.y) * a.scale, col_sum<C>(dq.z) * a.scale,
+                   col_sum<C>(dq.w) * a.scale);
+  if (r == 0) st4(a.dq_last + (long long)b * a.lddq_last + hh * D + 4 * c, Sk > 0 ? rope_t4(dq, 4 * c, t, a) : z4);
+  // the value path's dL/dxn rows: wave h takes rows j = h, h + H, ..., heads added in order
+  for (int j = hh; j < a.S; j += kVabsH) {
+    float2 w = make_float2(0.f, 0.f);
+    if (j < Sk) {
+#pragma unroll
+      for (int i = 0; i < kVabsH; ++i) {
+        const float pj = ps[i][j];
+        const float2 ui = *reinterpret_cast<const float2*>(&us[i][2 * lane]);
+        w = make_float2(fmaf(pj, ui.x, w.x), fmaf(pj, ui.y, w.y));
+      }
+    }
+    *reinterpret_cast<float2*>(wpre + (tok0 + j) * kVabsW + 2 * lane) = w;
+  }
+}
+
+int attn_lastq_vabs_supported(const AttnDesc& d, const float* xn, long long ldx) {
+  auto al = [](const void* p, long long ld) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && ld % 4 == 0; };
+  return d.dk == 32 && d.dv == 32 && d.heads == kVabsH && d.seq >= 1 && d.seq <= kVabsMaxS && xn != nullptr &&
+         al(xn, ldx) && al(d.k, d.ldk) && d.q_last != nullptr && al(d.q_last, d.ldq_last) && d.dq_last != nullptr &&
+         al(d.dq_last, d.lddq_last) && (d.dk_out == nullptr || al(d.dk_out, d.lddk));
+}
+
+int attn_fwd_lastq_z_launch(const AttnDesc& d, const float* xn, long long ldx, float* z, float* lse_last,
+                            hipStream_t s) {
+  if (!attn_lastq_vabs_supported(d, xn, ldx)) {
+    set_error("attention (last query, absorbed values): needs head dims 32, %d heads, seq <= %d, aligned rows",
+              kVabsH, kVabsMaxS);
+    return TALOS_ERR_UNSUPPORTED;
+  }
+  AttnArgs a = make_args(d, 32, 32);
+  if ((long long)a.B * a.H == 0) return TALOS_OK;
+  const double rows = (double)a.B * a.H;
+  // q row, k rows and xn rows of the sample read; z and lse written
+  ProfScope ps(s, "attn_fwd_lastq_z_kernel<32>", rows * a.S * 2.0 * (d.dk + kVabsW),
+               4.0 * (rows * (a.S * d.dk + d.dk + kVabsW + 1.0) + (double)a.B * a.S * kVabsW));
+  hipLaunchKernelGGL(attn_fwd_lastq_z_kernel<32>, dim3(ceil_div((size_t)a.B * a.H, 4)), dim3(256), 0, s, a, xn, ldx, z,
+                     lse_last);
+  return launch_status("attn_fwd_lastq_z_kernel");
+}
+
+int attn_bwd_lastq_z_launch(const AttnDesc& d, const float* xn, long long ldx, const float* u, const float* o_last,
+                            long long ldol, const float* lse_last, const float* do_last, long long lddol, float* wpre,
+                            hipStream_t s) {
+  if (!attn_lastq_vabs_supported(d, xn, ldx) || d.dk_out == nullptr || wpre == nullptr) {
+    set_error("attention backward (last query, absorbed values): needs head dims 32, %d heads, seq <= %d, dk and "
+              "the value-path rows", kVabsH, kVabsMaxS);
+    return TALOS_ERR_UNSUPPORTED;
+  }
+  AttnArgs a = make_args(d, 32, 32);
+  if ((long long)a.B * a.S == 0) return TALOS_OK;
+  const double rows = (double)a.B * a.H;
+  // k and xn rows read, dk and the value-path rows written; q, o, dO, u of the last row read
+  ProfScope ps(s, "attn_bwd_lastq_z_kernel<32>", rows * a.S * (6.0 * d.dk + 2.0 * kVabsW),
+               4.0 * (rows * a.S * 2.0 * d.dk + 2.0 * (double)a.B * a.S * kVabsW + rows * (4.0 * d.dk + kVabsW)));
+  hipLaunchKernelGGL(attn_bwd_lastq_z_kernel<32>, dim3((unsigned)a.B), dim3(64 * kVabsH), 0, s, a, xn, ldx, u, o_last,
+                     ldol, lse_last, do_last, lddol, wpre);
+  return launch_status("attn_bwd_lastq_z_kernel");
+}
+
 int attn_lastq_supported(const AttnDesc& d) {
   auto al = [](const void* p, long long ld) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && ld % 4 == 0; };
   return (d.dk == d.dv && (d.dk == 32 || d.dk == 64) && al(d.q, d.ldq) && al(d.k, d.ldk) && al(d.v, d.ldv) &&

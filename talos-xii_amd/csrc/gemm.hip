@@ -67,7 +67,8 @@ enum : int {
   E_DBIAS = 512,  // also sum the columns of op(B) (bias gradient; transA = 1, transB = 0)
   E_NORM = 1024,  // also RMSNorm each output row (N = 128: the whole row is in the tile)
   E_NORMB = 2048,  // the output rows are dL/d(RMSNorm output): write that norm's backward instead
-  E_NORMIN = 4096  // RMSNorm A's rows first (GemmDesc::nin_*): B rows scaled by the gain, rows by rstd
+  E_NORMIN = 4096,  // RMSNorm A's rows first (GemmDesc::nin_*): B rows scaled by the gain, rows by rstd
+  E_NBPRE = 8192    // with E_NORMB: a full [M][N] addend to the product before the norm backward
 };
 
 struct GemmArgs {
@@ -106,6 +107,7 @@ struct GemmArgs {
   const float* nb_add;
   const float* nb_add_last;
   const float* nb_dy_last;
+  const float* nb_pre;  // E_NBPRE
   int nb_seq;
   const int32_t* nb_lens;
   float* nb_dx;
@@ -439,9 +441,18 @@ __device__ __forceinline__ NbIn normb_load(const GemmArgs& p, int row, int col) 
   in.x = on ? *reinterpret_cast<const float4*>(p.nb_x + (long long)row * p.N + col) : make_float4(0.f, 0.f, 0.f, 0.f);
   return in;
 }
+template <bool PRE>
 __device__ __forceinline__ void normb_apply(const GemmArgs& p, float4 gg, int row, int col, const NbIn& in,
                                             const float4& g, float4& dw) {
   const bool on = row < p.M;
+  if constexpr (PRE) {  // the product's full-size addend (E_NBPRE), before anything else
+    const float4 a = on ? *reinterpret_cast<const float4*>(p.nb_pre + (long long)row * p.N + col)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+    gg.x += a.x;
+    gg.y += a.y;
+    gg.z += a.z;
+    gg.w += a.w;
+  }
   // the addend row, issued first: its latency runs under the row reduction below
   const float4 add = on && p.nb_add ? *reinterpret_cast<const float4*>(p.nb_add + (long long)row * p.N + col)
                                     : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -844,14 +855,18 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
     } else if constexpr ((E & E_NORMB) != 0) {
       const float4 g = *reinterpret_cast<const float4*>(p.nb_gain + col);
       const int rbase = m0 + half * T_ROWS + (threadIdx.x >> 5);
+      // the next row's x and rstd load under this row's work (with the E_NBPRE addend, loaded in
+      // the row's own step, there are no registers for that)
+      constexpr bool PRE = (E & E_NBPRE) != 0;
       NbIn cur = normb_load(p, rbase, col);
 #pragma unroll 1
       for (int i = 0; i < T_ROWS / 8; ++i) {
         const int lr = (threadIdx.x >> 5) + 8 * i;
         NbIn nxt = cur;
-        if (i + 1 < T_ROWS / 8) nxt = normb_load(p, rbase + 8 * (i + 1), col);
+        if (!PRE && i + 1 < T_ROWS / 8) nxt = normb_load(p, rbase + 8 * (i + 1), col);
         const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
-        normb_apply(p, v, rbase + 8 * i, col, cur, g, nbw);
+        normb_apply<PRE>(p, v, rbase + 8 * i, col, cur, g, nbw);
+        if (PRE && i + 1 < T_ROWS / 8) nxt = normb_load(p, rbase + 8 * (i + 1), col);
         cur = nxt;
       }
     } else {
@@ -1219,6 +1234,7 @@ static GemmArgs to_args(const GemmDesc& d) {
   a.nb_add = d.normb_add;
   a.nb_add_last = d.normb_add_last;
   a.nb_dy_last = d.normb_dy_last;
+  a.nb_pre = d.normb_pre;
   a.nb_seq = d.normb_seq > 0 ? d.normb_seq : 1;
   a.nb_lens = d.normb_lens;
   a.nb_dx = d.normb_dx;
@@ -1251,6 +1267,7 @@ static int epi_flags(const GemmDesc& d) {
   if (d.dbias) e |= E_DBIAS;
   if (d.norm_out) e |= E_NORM;
   if (d.normb_dx) e |= E_NORMB;
+  if (d.normb_dx && d.normb_pre) e |= E_NBPRE;
   if (d.nin_gain) e |= E_NORMIN;
   return e;
 }
@@ -1314,6 +1331,7 @@ static GemmKernel pick_kernel(bool tA, bool tB, int e, bool bf) {
   GEMM_CASE(false, true, E_DRELU)
   GEMM_CASE(false, true, E_SPLIT)
   GEMM_CASE_F32(false, true, E_NORMB)
+  GEMM_CASE_F32(false, true, E_NORMB | E_NBPRE)
   GEMM_CASE(true, false, 0)
   GEMM_CASE(true, false, E_BETA)
   GEMM_CASE(true, false, E_SPLIT)
@@ -1384,6 +1402,12 @@ static int tile_rows(const GemmDesc& d, int e, int ksplit) {
 
 static int gemm_launch_one(const GemmDesc& d, hipStream_t stream);
 
+// c[i] += add[i]
+__global__ void add_inplace_kernel(long long n, const float* __restrict__ add, float* __restrict__ c) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) c[i] += add[i];
+}
+
 // c[b * seq + last_row(b)][:] += add[b][:] for each sample b (rows of width n).
 __global__ void add_last_rows_kernel(int nb, int seq, int n, const int32_t* __restrict__ lens,
                                      const float* __restrict__ add, float* __restrict__ c) {
@@ -1405,12 +1429,12 @@ bool gemm_normin_supported(const GemmDesc& d) {
 // whole 128-wide row, fp32, one batch, float4 rows, and room for the per-tile partials.
 static bool normb_fused(const GemmDesc& d) {
   auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-  const int bm = tile_rows(d, E_NORMB, 1);
+  const int bm = tile_rows(d, epi_flags(d), 1);
   const int tiles_m = (d.M + bm - 1) / bm;
   return d.fuse_norm && d.N == BN && !d.bf16 && d.batch == 1 && !d.transA && d.transB && !use_small(d, num_cus()) &&
          d.beta == 0.f && !d.bias && !d.resid && d.act == GEMM_ACT_NONE && d.dact == GEMM_DACT_NONE &&
          d.rope_cols == 0 && !d.norm_out && !d.dbias && a16(d.normb_x) && a16(d.normb_dx) && a16(d.normb_gain) &&
-         a16(d.normb_add) && a16(d.normb_add_last) && a16(d.normb_dy_last) && d.normb_ws &&
+         a16(d.normb_add) && a16(d.normb_add_last) && a16(d.normb_dy_last) && a16(d.normb_pre) && d.normb_ws &&
          d.normb_ws_bytes >= reduce_parts_workspace_bytes(tiles_m, d.N);
 }
 
@@ -1422,7 +1446,15 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
                     "gemm: a row-norm backward after the product needs C with ldc == N");
       GemmDesc g = d;
       g.normb_dx = nullptr;
+      g.normb_pre = nullptr;
       if (int rc = gemm_launch(g, stream)) return rc;
+      if (d.normb_pre) {
+        const size_t n = (size_t)d.M * d.N;
+        ProfScope ps(stream, "add_inplace_kernel", (double)n, 12.0 * n);
+        hipLaunchKernelGGL(add_inplace_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, stream, (long long)n, d.normb_pre,
+                           d.C);
+        TALOS_LAUNCHED("add_inplace_kernel");
+      }
       if (d.normb_dy_last) {
         const int nb = d.M / (d.normb_seq > 0 ? d.normb_seq : 1);
         ProfScope ps(stream, "add_last_rows_kernel", (double)nb * d.N, 12.0 * nb * d.N);
@@ -1438,7 +1470,7 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
     g.ksplit = 1;
     if (int rc = gemm_launch_one(g, stream)) return rc;
     if (!d.normb_dw) return TALOS_OK;
-    const int bm = tile_rows(d, E_NORMB, 1);
+    const int bm = tile_rows(d, epi_flags(d), 1);
     return reduce_parts_launch(d.N, (d.M + bm - 1) / bm, d.normb_ws, d.normb_beta_dw, d.normb_dw, stream);
   }
   return gemm_launch_one(d, stream);

@@ -77,6 +77,7 @@ struct GemmDesc {
   const float* normb_add = nullptr;
   const float* normb_add_last = nullptr;
   const float* normb_dy_last = nullptr;  // added to C on the last row of each sample first
+  const float* normb_pre = nullptr;      // [M][N], added to C on every row first
   int normb_seq = 1;
   const int32_t* normb_lens = nullptr;
   float* normb_dx = nullptr;

@@ -85,7 +85,9 @@ struct talos_plan_s {
   struct LastRows {
     float *x, *o, *lse, *h2, *xn2, *rstd2, *u, *a, *g_u, *g_xn, *g_h2, *g_o;
     float *xn1, *q, *dq, *g_xnq;  // the last layer's query path on these rows (last-query attention)
+    float *z, *uv;  // absorbed values: sum_j p_j xn1_j and Wv_h dO_h per (sample, head), [batch][H][d]
   } lr{};
+  float* wpre = nullptr;  // absorbed values: the value path's dL/dxn1 on every row of the last layer
   const int32_t* lens = nullptr;  // per-sample lengths of the PPO call in progress (nullptr: all seq)
   int num_cu = 256;
   // TALOS_PLAN_UNFUSED=1 at creation: every fused alternative (row norms in GEMM epilogues, the
@@ -556,7 +558,7 @@ static int before_write(talos_plan_s* p, hipStream_t s, const void* buf) {
 static int norm_bwd_mm(talos_plan_s* p, hipStream_t s, int M, int d, int K, const float* g, long long ldg,
                        const float* W, long long ldw, float* C, const float* x, const float* gain, const float* rstd,
                        const float* add, const float* add_last, const float* dy_last, int seq, float* dx,
-                       float* dw) {
+                       float* dw, const float* pre = nullptr) {
   GemmDesc gd;
   gd.transB = 1;
   gd.M = M;
@@ -575,6 +577,7 @@ static int norm_bwd_mm(talos_plan_s* p, hipStream_t s, int M, int d, int K, cons
   gd.normb_add = add;
   gd.normb_add_last = add_last;
   gd.normb_dy_last = dy_last;
+  gd.normb_pre = pre;
   gd.normb_seq = seq;
   gd.normb_lens = p->lens;
   gd.normb_dx = dx;
@@ -1001,6 +1004,63 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
 // and gathers the last rows.
 static bool ppo_lastq(talos_plan_s* p, const talos_block_cfg& c, talos_plan_s::Layer& L) {
   return c.attention == TALOS_ATTN_MHA && attn_lastq_supported(block_attn_desc(p, c, L));
+}
+
+// Whether the last layer's last-query attention absorbs its value projection (v_j = xn1_j . Wv,
+// which carries no rotation): o_h = (sum_j p_j xn1_j) . Wv_h, so the values are never formed on
+// every row, their weight gradient is a product over the samples (sum_b z_bh^T dO_bh) and their
+// share of dL/dxn1 rows (sum_h p_j^h Wv_h dO_h) joins the keys' in the dX product's epilogue.
+// Four 32-wide heads, d = 128 (the kernels' shapes); the plan's buffers exist (p->wpre).
+static bool ppo_vabs(talos_plan_s* p, const talos_block_cfg& c, talos_plan_s::Layer& L) {
+  if (!p->wpre || !ppo_lastq(p, c, L)) return false;
+  AttnDesc ad = block_attn_desc(p, c, L);
+  ad.q_last = p->lr.q;
+  ad.ldq_last = c.d_model;
+  ad.dq_last = p->lr.dq;
+  ad.lddq_last = c.d_model;
+  return attn_lastq_vabs_supported(ad, L.xn1, c.d_model) != 0;
+}
+
+// o[:, h] = z[:, h] . Wv_h for the H heads of hd (one batched product; Wv_h the columns
+// 2d + h hd of Wqkv) and its transpose u[:, h] = dO[:, h] . Wv_h^T.
+static int vabs_out(talos_plan_s* p, int B, int d, int H, int hd, const float* z, const float* wv, long long ldw,
+                    float* o, hipStream_t s) {
+  GemmDesc g;
+  g.M = B;
+  g.N = hd;
+  g.K = d;
+  g.A = z;
+  g.lda = (long long)H * d;
+  g.sA = d;
+  g.B = wv;
+  g.ldb = ldw;
+  g.sB = hd;
+  g.C = o;
+  g.ldc = (long long)H * hd;
+  g.sC = hd;
+  g.batch = H;
+  g.ksplit = 1;
+  return gemm_launch(g, s);
+}
+static int vabs_u(talos_plan_s* p, int B, int d, int H, int hd, const float* g_o, const float* wv, long long ldw,
+                  float* u, hipStream_t s) {
+  GemmDesc g;
+  g.transB = 1;
+  g.M = B;
+  g.N = d;
+  g.K = hd;
+  g.A = g_o;
+  g.lda = (long long)H * hd;
+  g.sA = hd;
+  g.B = wv;
+  g.ldb = ldw;
+  g.sB = hd;
+  g.C = u;
+  g.ldc = (long long)H * d;
+  g.sC = d;
+  g.batch = H;
+  g.ksplit = 1;
+  return gemm_launch(g, s);
 }
 
 // Last-token gather / scatter (last_row: common.hpp) -------------------------
@@ -1514,7 +1574,7 @@ static bool tail_fused(const talos_plan_s* p, const talos_ppo_cfg& c) {
 // v_mfma_f32_16x16x4_f32 tiles, lane l feeding X[row + l / 16][m + l % 16] and
 // G[row + l / 16][n + l % 16] from LDS); the f32 chunk partials (and the bias column sums) are
 // then added in a fixed order in f64 by one reduction launch.
-constexpr int kRowsWgradMax = 4;
+constexpr int kRowsWgradMax = 6;
 constexpr int kRowsChunk = 256;
 struct RowsWgradProblem {
   const float* X;  // [rows][kx]
@@ -1986,14 +2046,15 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
     } else {
       // Only the last token of each sample reaches the heads, and everything after attention is
       // per row: the last layer runs its MLP half on those B rows and writes p->last directly.
+      const bool vabs = ppo_vabs(p, bc, L);
       if (ppo_lastq(p, bc, L)) {
-        // attention of the last query only: keys and values on every row, the query on the
-        // last rows (rotated inside the attention kernel)
+        // attention of the last query only: keys (and values, unless absorbed) on every row, the
+        // query on the last rows (rotated inside the attention kernel)
         auto& R = p->lr;
         {
           GemmDesc g;
           g.M = M;
-          g.N = 2 * d;
+          g.N = vabs ? d : 2 * d;
           g.K = d;
           g.A = L.xn1;
           g.lda = d;
@@ -2018,7 +2079,14 @@ static int ppo_forward(talos_plan_s* p, const talos_ppo_cfg& c, const float* P, 
         AttnDesc ad = block_attn_desc(p, bc, L);
         ad.q_last = R.q;
         ad.ldq_last = d;
-        rc = attn_fwd_lastq_launch(ad, R.o, d, R.lse, s);
+        if (vabs) {
+          ad.dq_last = R.dq;  // (only checked for alignment here)
+          ad.lddq_last = d;
+          rc = attn_fwd_lastq_z_launch(ad, L.xn1, d, R.z, R.lse, s);
+          if (rc == TALOS_OK) rc = vabs_out(p, c.batch, d, bc.n_heads, bc.head_dim, R.z, P + bo.wqkv + 2 * d, 3 * d, R.o, s);
+        } else {
+          rc = attn_fwd_lastq_launch(ad, R.o, d, R.lse, s);
+        }
       } else {
         rc = block_attn_forward(p, bc, P, bo, L, s, true);
         if (rc == TALOS_OK) rc = gather(L.o, p->lr.o, ow);
@@ -2216,6 +2284,12 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
     for (float** b : {&R.u, &R.a, &R.g_u}) rc |= plan_alloc(p, b, B * F);
     rc |= plan_alloc(p, &R.rstd2, B);
     rc |= plan_alloc(p, &R.lse, B * cfg->n_heads);
+    // the absorbed-value path (four 32-wide heads, d = 128: the kernels' shapes)
+    if (!p->unfused && bc.attention == TALOS_ATTN_MHA && d == 128 && cfg->n_heads == 4 && bc.head_dim == 32 &&
+        cfg->seq <= 256 && cfg->n_layers > 0) {
+      for (float** b : {&R.z, &R.uv}) rc |= plan_alloc(p, b, B * cfg->n_heads * d);
+      rc |= plan_alloc(p, &p->wpre, M * d);
+    }
   }
   {  // per-workgroup loss partials (doubles)
     float* lw = nullptr;
@@ -2443,12 +2517,26 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
       ad.lddq_last = d;
       if ((rc = before_write(p, s, p->g_qkv))) return rc;
       if ((rc = before_write(p, s, R.dq))) return rc;
-      if ((rc = attn_bwd_lastq_launch(ad, R.o, d, R.lse, R.g_o, d, s))) return rc;
+      const bool vabs = ppo_vabs(p, bc, L);
+      const int H = bc.n_heads, hd = bc.head_dim;
+      if (vabs) {
+        if ((rc = vabs_u(p, B, d, H, hd, R.g_o, params + o.wqkv + 2 * d, 3 * d, R.uv, s))) return rc;
+        if ((rc = before_write(p, s, p->wpre))) return rc;
+        rc = attn_bwd_lastq_z_launch(ad, L.xn1, d, R.uv, R.o, d, R.lse, R.g_o, d, p->wpre, s);
+      } else {
+        rc = attn_bwd_lastq_launch(ad, R.o, d, R.lse, R.g_o, d, s);
+      }
+      if (rc) return rc;
       float* g_kv = p->g_qkv + d;
-      if ((rc = wgrad(p, s, p->g_qkv, d, 2 * d, M, L.xn1, d, g_kv, 3 * d, G + o.wqkv + d, 3 * d))) return rc;
+      // the key (and value) weight gradients over every row
+      if ((rc = wgrad(p, s, p->g_qkv, d, vabs ? d : 2 * d, M, L.xn1, d, g_kv, 3 * d, G + o.wqkv + d, 3 * d))) return rc;
       {
-        RowsWgrad rw;  // dW_q over the last rows
+        RowsWgrad rw;  // dW_q over the last rows; absorbed values: dWv_h = sum_b z_bh^T dO_bh
         rw.add(R.xn1, d, d, R.dq, d, d, G + o.wqkv, 3 * d);
+        if (vabs)
+          for (int h = 0; h < H; ++h)
+            rw.add(R.z + (size_t)h * d, (long long)H * d, d, R.g_o + (size_t)h * hd, d, hd, G + o.wqkv + 2 * d + h * hd,
+                   3 * d);
         if ((rc = rw.launch(B, p->gemm_ws, p->gemm_ws_bytes / sizeof(float), s))) return rc;
       }
       // dxn1 = g_kv.Wkv^T on every row, plus dq.Wq^T on the last rows; then rmsnorm1's backward
@@ -2459,8 +2547,9 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
         rc = mm(p, s, 0, 1, B, d, d, R.dq, d, params + o.wqkv, 3 * d, R.g_xnq, d);
       if (rc) return rc;
       if ((rc = before_write(p, s, p->g_out))) return rc;
-      rc = norm_bwd_mm(p, s, M, d, 2 * d, g_kv, 3 * d, params + o.wqkv + d, 3 * d, p->g_xn, L.x, params + o.g1,
-                       L.rstd1, nullptr, R.g_h2, R.g_xnq, c.seq, p->g_out, G + o.g1);
+      rc = norm_bwd_mm(p, s, M, d, vabs ? d : 2 * d, g_kv, 3 * d, params + o.wqkv + d, 3 * d, p->g_xn, L.x,
+                       params + o.g1, L.rstd1, nullptr, R.g_h2, R.g_xnq, c.seq, p->g_out, G + o.g1,
+                       vabs ? p->wpre : nullptr);
     } else {
       // the row gradients spread over the full token grid
       const int ow = attn_width(bc);
