@@ -1894,49 +1894,67 @@ __global__ __launch_bounds__(256) void attn_bwd_lastq_kernel(AttnArgs a, const f
 // ---------------------------------------------------------------------------
 constexpr int kVabsW = 128, kVabsH = 4, kVabsMaxS = 256;
 
-// z[b, h] = sum_j p_j xn_j / l (lanes hold columns 2 lane, 2 lane + 1); lse_last[b*H + h]. The
-// scores, the running maximum and the rescale are attn_fwd_lastq_kernel's.
+// A workgroup per sample, wave h its head h: z[b, h] = sum_j p_j xn_j ([B][H][W]) and
+// lse_last[b*H + h]. Each wave first scores its head over the sample's keys (row layout, the
+// scores kept in LDS, exact maximum and sum); then wave w takes the keys j = w, w + H, ..., loads
+// each such xn row once (two columns a lane) and accumulates p_j^h xn_j for all H heads; the H
+// waves' partial sums are added in wave order.
 template <int D>
-__global__ __launch_bounds__(256) void attn_fwd_lastq_z_kernel(AttnArgs a, const float* __restrict__ xn, long long ldx,
-                                                               float* __restrict__ z, float* __restrict__ lse_last) {
+__global__ __launch_bounds__(64 * kVabsH) void attn_fwd_lastq_z_kernel(AttnArgs a, const float* __restrict__ xn,
+                                                                       long long ldx, float* __restrict__ z,
+                                                                       float* __restrict__ lse_last) {
   constexpr int C = D / 4, RPP = 64 / C;
-  const int lane = threadIdx.x & 63, c = lane % C, r = lane / C;
-  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (pair >= a.B * a.H) return;  // uniform per wave
-  const int b = pair / a.H, hh = pair % a.H;
+  __shared__ float ps[kVabsH][kVabsMaxS];
+  __shared__ float mh[kVabsH], ilh[kVabsH];
+  __shared__ __align__(16) float zp[kVabsH][kVabsH][kVabsW];  // [wave][head][column]
+  const int lane = threadIdx.x & 63, c = lane % C, r = lane / C, hh = threadIdx.x >> 6;
+  const int b = blockIdx.x, pair = b * a.H + hh;
   const long long tok0 = (long long)b * a.S;
   const int Sk = key_len(a, b), t = Sk - 1;
-  float2 acc = make_float2(0.f, 0.f);
-  float m = kNegInf, l = 0.f;
+  float m = kNegInf;
   if (Sk > 0) {
     float4 q = last_query(a, b, tok0, t, hh, D, c);
     q = make_float4(q.x * a.scale, q.y * a.scale, q.z * a.scale, q.w * a.scale);
     for (int j0 = 0; j0 < Sk; j0 += RPP) {
       const int j = j0 + r;
       const bool ok = j < Sk;
-      const int jj = ok ? j : t;
-      const float4 k = ld4(a.k + (tok0 + jj) * a.ldk + hh * D + 4 * c);
-      const float sc = row_sum<C>(dot4(q, k));
-      const float s = ok ? sc : kNegInf;
-      const float mn = fmaxf(m, col_max<C>(s));
-      const float pj = ok ? expf(s - mn) : 0.f;
-      const float corr = m == kNegInf ? 0.f : expf(m - mn);
-      l = l * corr + col_sum<C>(pj);
-      acc = make_float2(acc.x * corr, acc.y * corr);
-      // the pass's rows, one at a time: p of row i from its lanes, the row's xn in column layout
-#pragma unroll
-      for (int i = 0; i < RPP; ++i) {
-        const float p_i = __shfl(pj, i * C, 64);
-        const int ji = min(j0 + i, Sk - 1);
-        const float2 x = *reinterpret_cast<const float2*>(xn + (tok0 + ji) * ldx + 2 * lane);
-        acc = make_float2(fmaf(p_i, x.x, acc.x), fmaf(p_i, x.y, acc.y));
-      }
-      m = mn;
+      const float4 k = ld4(a.k + (tok0 + (ok ? j : t)) * a.ldk + hh * D + 4 * c);
+      const float s = ok ? row_sum<C>(dot4(q, k)) : kNegInf;
+      if (ok && c == 0) ps[hh][j] = s;
+      m = fmaxf(m, col_max<C>(s));
     }
   }
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  *reinterpret_cast<float2*>(z + (long long)pair * kVabsW + 2 * lane) = make_float2(acc.x * inv, acc.y * inv);
-  if (lane == 0) lse_last[pair] = l > 0.f ? m + logf(l) : kNegInf;
+  wave_lds_sync();
+  float l = 0.f;
+  for (int j = lane; j < Sk; j += 64) l += expf(ps[hh][j] - m);
+  l = wave_sum(l);
+  if (lane == 0) {
+    mh[hh] = m;
+    ilh[hh] = l > 0.f ? 1.f / l : 0.f;
+    lse_last[pair] = l > 0.f ? m + logf(l) : kNegInf;
+  }
+  __syncthreads();
+  float2 acc[kVabsH];
+#pragma unroll
+  for (int i = 0; i < kVabsH; ++i) acc[i] = make_float2(0.f, 0.f);
+  for (int j = hh; j < Sk; j += kVabsH) {
+    const float2 x = *reinterpret_cast<const float2*>(xn + (tok0 + j) * ldx + 2 * lane);
+#pragma unroll
+    for (int i = 0; i < kVabsH; ++i) {
+      const float pj = expf(ps[i][j] - mh[i]) * ilh[i];
+      acc[i] = make_float2(fmaf(pj, x.x, acc[i].x), fmaf(pj, x.y, acc[i].y));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kVabsH; ++i) *reinterpret_cast<float2*>(&zp[hh][i][2 * lane]) = acc[i];
+  __syncthreads();
+  float2 zs = make_float2(0.f, 0.f);
+#pragma unroll
+  for (int w = 0; w < kVabsH; ++w) {
+    const float2 v = *reinterpret_cast<const float2*>(&zp[w][hh][2 * lane]);
+    zs = make_float2(zs.x + v.x, zs.y + v.y);
+  }
+  *reinterpret_cast<float2*>(z + (long long)pair * kVabsW + 2 * lane) = zs;
 }
 
 // A workgroup per sample, wave h its head h (kVabsH heads of D). dk rows j < S (zero past the
@@ -1967,11 +1985,8 @@ __global__ __launch_bounds__(64 * kVabsH) void attn_bwd_lastq_z_kernel(AttnArgs 
   }
   const float2 uh = *reinterpret_cast<const float2*>(u + (long long)pair * kVabsW + 2 * lane);
   *reinterpret_cast<float2*>(&us[hh][2 * lane]) = uh;
-  // u_h again in the two-rows-a-pass layout of the dP pass: lane (row half rh, c2) holds columns
-  // 4 c2 .. 4 c2 + 3
-  constexpr int C2 = kVabsW / 4;  // 32 lanes per xn row
-  const int c2 = lane % C2, rh = lane / C2;
-  const float4 u4 = ld4(u + (long long)pair * kVabsW + 4 * c2);
+  __shared__ float Dl[kVabsH];
+  if (lane == 0) Dl[hh] = Dd;
   // p_j for every key (row layout)
   for (int j0 = 0; j0 < a.S; j0 += RPP) {
     const int j = j0 + r;
@@ -1981,15 +1996,24 @@ __global__ __launch_bounds__(64 * kVabsH) void attn_bwd_lastq_z_kernel(AttnArgs 
     if (c == 0 && j < a.S) ps[hh][j] = ok ? expf(s - lse) : 0.f;
   }
   __syncthreads();
-  // dS_j = p_j (xn_j . u_h - D): two rows a pass (32 lanes a row, float4 each), four passes'
-  // loads in flight together
-#pragma unroll 4
-  for (int j0 = 0; j0 < Sk; j0 += 2) {
-    const int j = j0 + rh;
-    const bool ok = j < Sk;
-    const float4 x = ld4(xn + (tok0 + (ok ? j : j0)) * ldx + 4 * c2);
-    const float dp = row_sum<C2>(dot4(x, u4));
-    if (ok && c2 == 0) dss[hh][j] = ps[hh][j] * (dp - Dd);
+  // dS_j^h = p_j^h (xn_j . u_h - D_h) for every head: wave w takes the key pairs j0 = 2w, 2w + 2H,
+  // ... (32 lanes a row, float4 each, two rows a pass), each xn row read once for all H heads
+  {
+    constexpr int C2 = kVabsW / 4;  // 32 lanes per xn row
+    const int c2 = lane % C2, rh = lane / C2;
+    float4 u4[kVabsH];
+#pragma unroll
+    for (int i = 0; i < kVabsH; ++i) u4[i] = *reinterpret_cast<const float4*>(&us[i][4 * c2]);
+    for (int j0 = 2 * hh; j0 < Sk; j0 += 2 * kVabsH) {
+      const int j = j0 + rh;
+      const bool ok = j < Sk;
+      const float4 x = ld4(xn + (tok0 + (ok ? j : j0)) * ldx + 4 * c2);
+#pragma unroll
+      for (int i = 0; i < kVabsH; ++i) {
+        const float dp = row_sum<C2>(dot4(x, u4[i]));
+        if (ok && c2 == 0) dss[i][j] = ps[i][j] * (dp - Dl[i]);
+      }
+    }
   }
   __syncthreads();
   // dk_j = R^T(dS_j scale q), dq = R^T(scale sum_j dS_j k_j) (row layout)
@@ -2044,7 +2068,7 @@ int attn_fwd_lastq_z_launch(const AttnDesc& d, const float* xn, long long ldx, f
   // q row, k rows and xn rows of the sample read; z and lse written
   ProfScope ps(s, "attn_fwd_lastq_z_kernel<32>", rows * a.S * 2.0 * (d.dk + kVabsW),
                4.0 * (rows * (a.S * d.dk + d.dk + kVabsW + 1.0) + (double)a.B * a.S * kVabsW));
-  hipLaunchKernelGGL(attn_fwd_lastq_z_kernel<32>, dim3(ceil_div((size_t)a.B * a.H, 4)), dim3(256), 0, s, a, xn, ldx, z,
+  hipLaunchKernelGGL(attn_fwd_lastq_z_kernel<32>, dim3((unsigned)a.B), dim3(64 * kVabsH), 0, s, a, xn, ldx, z,
                      lse_last);
   return launch_status("attn_fwd_lastq_z_kernel");
 }
