@@ -80,7 +80,9 @@ def _oracle_varlen(oracle, args, p, states, lens, actions, adv, ret, old):
                                                (1, 1, 12, [12, 1, 7, 12, 3], 64), (1, 2, 40, [40, 1, 33, 17, 40], 64),
                                                (0, 2, 40, [40, 1, 33, 17, 40], 64),
                                                (1, 4, 47, [47, 1, 33, 20, 32], 128),
-                                               (0, 4, 64, [64, 2, 40, 31, 64], 128)])
+                                               (0, 4, 64, [64, 2, 40, 31, 64], 128),
+                                               (1, 4, 32, [32, 1, 17, 20, 31], 128),
+                                               (0, 4, 20, [20, 3, 20, 9, 1], 128)])
 def test_minibatch_varlen_vs_oracle(oracle, causal, H, S, lens, d):
     # head dim 32 (H = 2) and 64 (H = 1): both last-query attention kernels of the last layer;
     # seq 40 at head dim 32: the first layer's backward on the four-block kernel, keys masked past
