@@ -44,12 +44,14 @@ constexpr int NT = 256;
 #ifndef TALOS_GEMM_WAVES
 #define TALOS_GEMM_WAVES 4
 #endif
-// Split-K sizing: target workgroups per CU and the minimum K per split.
+// Split-K sizing: target workgroups per CU and the minimum K per split (512: at 32768 tokens the
+// weight gradients take 64 splits instead of 128, C3 0.614-0.620 -> 0.608-0.609 ms; 768 and 1024
+// starve the grid, 128 doubles the partials).
 #ifndef TALOS_SPLITK_WG_PER_CU
 #define TALOS_SPLITK_WG_PER_CU 2
 #endif
 #ifndef TALOS_SPLITK_MIN_K
-#define TALOS_SPLITK_MIN_K 256
+#define TALOS_SPLITK_MIN_K 512
 #endif
 constexpr int NBUF = TALOS_GEMM_DBUF ? 2 : 1;
 

@@ -984,7 +984,7 @@ static int block_backward(talos_plan_s* p, const talos_block_cfg& c, const float
   const bool fold = mha && !p->unfused && !p->bf16 && c.d_model == kWoFuseD && attn_width(c) == kWoFuseD &&
                     attn_bwd_wo_supported(ad, P + o.wo, p->g_h2);
   // standard attention: where their splits are alike (C3's 32K tokens), the Wo weight gradient
-  // waits for Wqkv's and launches with it; otherwise (C4's, 771 against 256 tokens a split) it
+  // waits for Wqkv's and launches with it; otherwise (C4's, 771 against 512 tokens a split) it
   // runs as soon as g_h2 is ready
   const int d = c.d_model, ow = attn_width(c);
   const WgradOp wo{p->g_h2, ow, d, M, L.o, ow, p->g_h2, d, G + o.wo, d, nullptr};
