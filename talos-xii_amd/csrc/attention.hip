@@ -1121,21 +1121,50 @@ __device__ __forceinline__ void bcast_rows(float* slice, float v, int l32, int h
 
 constexpr int kTS = 33;  // pitch of the transposed dS tile: a column read touches 32 banks
 
+// Offset of element (row, col) in a staged tile of pitch TP. At TP = 32 a row is 128 bytes, so
+// the 16-byte accesses of 16 lanes to 16 consecutive rows would share two groups of banks (eight
+// lanes on each); the row's 16-byte column groups are therefore permuted by (row / 2) % 8, which
+// puts those 16 accesses on 16 distinct groups of four banks. A float4 at a column that is a
+// multiple of 4 stays contiguous.
+template <int TP>
+__device__ __forceinline__ int stg(int row, int col) {
+  if constexpr (TP == 32) return row * 32 + ((((col >> 2) ^ (row >> 1)) & 7) << 2) + (col & 3);
+  return row * TP + col;
+}
+
+// The element (acc_row(s, h), l32) of a swizzled 32-pitch tile: row acc_row = 8 (s / 4) + 4 h +
+// s % 4 puts bits 1 and 3 of s into the permutation, so the lane needs four base offsets (one per
+// value of those bits, h and l32 folded in), and the rest, (8 (s / 4) + s % 4) * 32, is a constant
+// of the unrolled loop.
+struct AccRowBases {
+  int o[4];
+  __device__ __forceinline__ AccRowBases(int l32, int h) {
+    const int v = (l32 >> 2) ^ (h << 1);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = 128 * h + ((((k & 1) | ((k >> 1) << 2)) ^ v) << 2) + (l32 & 3);
+  }
+  __device__ __forceinline__ int at(int s) const {
+    return o[((s >> 1) & 1) | (((s >> 2) & 1) << 1)] + (8 * (s >> 2) + (s & 3)) * 32;
+  }
+};
+
 // Stores this lane's half row (the load_half layout) into row l32 of an LDS tile of pitch TP.
 template <int HALF, int TP>
 __device__ __forceinline__ void stage_half(float* tile, const float (&r)[HALF], int l32, int h) {
 #pragma unroll
   for (int i = 0; i < HALF; i += 4)
-    *reinterpret_cast<float4*>(tile + l32 * TP + HALF * h + i) = make_float4(r[i], r[i + 1], r[i + 2], r[i + 3]);
+    *reinterpret_cast<float4*>(tile + stg<TP>(l32, HALF * h + i)) = make_float4(r[i], r[i + 1], r[i + 2], r[i + 3]);
 }
 
 // mfma_p_rows with the operand rows read from an LDS tile of pitch TP (rows >= S hold zeros).
 template <int NB, int TP>
 __device__ __forceinline__ void mfma_p_lds(const float (&P)[16], const float* tile, int l32, int h,
                                            floatx16 (&acc)[NB]) {
+  static_assert(TP != 32 || NB == 1, "a swizzled tile is one 32-column block");
+  const AccRowBases ab(l32, h);
 #pragma unroll
   for (int s = 0; s < 16; ++s) {
-    const float* src = tile + acc_row(s, h) * TP + l32;
+    const float* src = tile + (TP == 32 ? ab.at(s) : acc_row(s, h) * TP + l32);
 #pragma unroll
     for (int eb = 0; eb < NB; ++eb)
       acc[eb] = __builtin_amdgcn_mfma_f32_32x32x2f32(P[s], src[eb * 32], acc[eb], 0, 0, 0);
@@ -1354,7 +1383,7 @@ attn_bwd_s32_wo_kernel(AttnArgs a, const float* __restrict__ wo, const float* __
 #pragma unroll 4
   for (int j = 0; j < kWoD / 8; ++j) {
     const int n0 = 8 * j + 4 * h;  // columns n0 .. n0 + 3 of dh2 and of Wo's row
-    const float4 g4 = *reinterpret_cast<const float4*>(lds[n0 >> 5] + l32 * TP + (n0 & 31));
+    const float4 g4 = *reinterpret_cast<const float4*>(lds[n0 >> 5] + stg<TP>(l32, n0 & 31));
     const float4 w4 = *reinterpret_cast<const float4*>(wrow + n0);
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(g4.x, w4.x, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(g4.y, w4.y, acc, 0, 0, 0);
@@ -1364,12 +1393,15 @@ attn_bwd_s32_wo_kernel(AttnArgs a, const float* __restrict__ wo, const float* __
   __syncthreads();  // every wave has read the dh2 quarters
   // dO in accumulator layout (register r <-> token acc_row(r, h), lane <-> e) into the dO tile
   float* const Gs = lds[wv];
+  {
+    const AccRowBases ab(l32, h);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) Gs[acc_row(r, h) * TP + l32] = acc[r];
+    for (int r = 0; r < 16; ++r) Gs[ab.at(r)] = acc[r];
+  }
   wave_lds_sync();
 #pragma unroll
   for (int i = 0; i < 16; i += 4) {
-    const float4 g4 = *reinterpret_cast<const float4*>(Gs + l32 * TP + 16 * h + i);
+    const float4 g4 = *reinterpret_cast<const float4*>(Gs + stg<TP>(l32, 16 * h + i));
     gv[i] = g4.x;
     gv[i + 1] = g4.y;
     gv[i + 2] = g4.z;
