@@ -1921,8 +1921,9 @@ __global__ __launch_bounds__(256) void attn_bwd_lastq_kernel(AttnArgs a, const f
 // forms z_h = sum_j p_j xn_j over the sample's normalised input rows xn (width W = 128) instead
 // of reading value rows, and the caller multiplies z_h by Wv_h (a small batched product); the
 // backward takes u_h = Wv_h dO_h from the caller, forms dP_j = xn_j . u_h, and writes, besides dK
-// and the last query's dq, the value path's share of dL/dxn_j, sum_h p_j^h u_h, for the product
-// that forms the rest of dL/dxn. No value rows are ever formed.
+// and the last query's dq, the weights p_j^h of every row, from which the product that forms the
+// rest of dL/dxn adds the value path's share, sum_h p_j^h u_h, in its epilogue. No value rows are
+// ever formed.
 // ---------------------------------------------------------------------------
 constexpr int kVabsW = 128, kVabsH = 4, kVabsMaxS = 256;
 
@@ -1990,14 +1991,14 @@ __global__ __launch_bounds__(64 * kVabsH) void attn_fwd_lastq_z_kernel(AttnArgs 
 }
 
 // A workgroup per sample, wave h its head h (kVabsH heads of D). dk rows j < S (zero past the
-// sample's keys), dq_last, and wpre[b*S + j] = sum_h p_j^h u_h (zero past the keys), u = [B][H][W].
+// sample's keys), dq_last, and prow[b*S + j][h] = p_j^h (zero past the keys); u = [B][H][W].
 template <int D>
 __global__ __launch_bounds__(64 * kVabsH) void attn_bwd_lastq_z_kernel(AttnArgs a, const float* __restrict__ xn,
                                                                        long long ldx, const float* __restrict__ u,
                                                                        const float* __restrict__ o_last, long long ldol,
                                                                        const float* __restrict__ lse_last,
                                                                        const float* __restrict__ do_last,
-                                                                       long long lddol, float* __restrict__ wpre) {
+                                                                       long long lddol, float* __restrict__ prow) {
   constexpr int C = D / 4, RPP = 64 / C;
   __shared__ float ps[kVabsH][kVabsMaxS], dss[kVabsH][kVabsMaxS];
   __shared__ __align__(16) float us[kVabsH][kVabsW];
@@ -2065,19 +2066,8 @@ __global__ __launch_bounds__(64 * kVabsH) void attn_bwd_lastq_z_kernel(AttnArgs 
   dq = make_float4(col_sum<C>(dq.x) * a.scale, col_sum<C>(dq.y) * a.scale, col_sum<C>(dq.z) * a.scale,
                    col_sum<C>(dq.w) * a.scale);
   if (r == 0) st4(a.dq_last + (long long)b * a.lddq_last + hh * D + 4 * c, Sk > 0 ? rope_t4(dq, 4 * c, t, a) : z4);
-  // the value path's dL/dxn rows: wave h takes rows j = h, h + H, ..., heads added in order
-  for (int j = hh; j < a.S; j += kVabsH) {
-    float2 w = make_float2(0.f, 0.f);
-    if (j < Sk) {
-#pragma unroll
-      for (int i = 0; i < kVabsH; ++i) {
-        const float pj = ps[i][j];
-        const float2 ui = *reinterpret_cast<const float2*>(&us[i][2 * lane]);
-        w = make_float2(fmaf(pj, ui.x, w.x), fmaf(pj, ui.y, w.y));
-      }
-    }
-    *reinterpret_cast<float2*>(wpre + (tok0 + j) * kVabsW + 2 * lane) = w;
-  }
+  // every row's weights p_j^h (the value path's share of dL/dxn is formed from them downstream)
+  for (int f = threadIdx.x; f < a.S * kVabsH; f += 64 * kVabsH) prow[tok0 * kVabsH + f] = ps[f % kVabsH][f / kVabsH];
 }
 
 int attn_lastq_vabs_supported(const AttnDesc& d, const float* xn, long long ldx) {
@@ -2106,9 +2096,9 @@ int attn_fwd_lastq_z_launch(const AttnDesc& d, const float* xn, long long ldx, f
 }
 
 int attn_bwd_lastq_z_launch(const AttnDesc& d, const float* xn, long long ldx, const float* u, const float* o_last,
-                            long long ldol, const float* lse_last, const float* do_last, long long lddol, float* wpre,
+                            long long ldol, const float* lse_last, const float* do_last, long long lddol, float* prow,
                             hipStream_t s) {
-  if (!attn_lastq_vabs_supported(d, xn, ldx) || d.dk_out == nullptr || wpre == nullptr) {
+  if (!attn_lastq_vabs_supported(d, xn, ldx) || d.dk_out == nullptr || prow == nullptr) {
     set_error("attention backward (last query, absorbed values): needs head dims 32, %d heads, seq <= %d, dk and "
               "the value-path rows", kVabsH, kVabsMaxS);
     return TALOS_ERR_UNSUPPORTED;
@@ -2116,11 +2106,11 @@ int attn_bwd_lastq_z_launch(const AttnDesc& d, const float* xn, long long ldx, c
   AttnArgs a = make_args(d, 32, 32);
   if ((long long)a.B * a.S == 0) return TALOS_OK;
   const double rows = (double)a.B * a.H;
-  // k and xn rows read, dk and the value-path rows written; q, o, dO, u of the last row read
+  // k and xn rows read, dk rows and the weights written; q, o, dO, u of the last row read
   ProfScope ps(s, "attn_bwd_lastq_z_kernel<32>", rows * a.S * (6.0 * d.dk + 2.0 * kVabsW),
-               4.0 * (rows * a.S * 2.0 * d.dk + 2.0 * (double)a.B * a.S * kVabsW + rows * (4.0 * d.dk + kVabsW)));
+               4.0 * (rows * a.S * (2.0 * d.dk + 1.0) + (double)a.B * a.S * kVabsW + rows * (4.0 * d.dk + kVabsW)));
   hipLaunchKernelGGL(attn_bwd_lastq_z_kernel<32>, dim3((unsigned)a.B), dim3(64 * kVabsH), 0, s, a, xn, ldx, u, o_last,
-                     ldol, lse_last, do_last, lddol, wpre);
+                     ldol, lse_last, do_last, lddol, prow);
   return launch_status("attn_bwd_lastq_z_kernel");
 }
 

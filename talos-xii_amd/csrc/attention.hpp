@@ -74,13 +74,13 @@ int attn_bwd_lastq_launch(const AttnDesc& d, const float* o_last, long long ldol
 // The last query with the value projection absorbed (v_j = xn_j . Wv carries no rotation): the
 // forward writes z[b][h] = sum_j p_j xn_j ([B][H][128], the caller forms o_h = z_h . Wv_h) and
 // lse; the backward takes u[b][h] = Wv_h . dO_h ([B][H][128]) and writes dk (d.dk_out), the last
-// query's dq (d.dq_last) and the value path's share of dL/dxn, wpre = sum_h p_j^h u_h ([B*S][128],
+// query's dq (d.dq_last) and every row's weights prow[b*S + j][h] = p_j^h ([B*S][4],
 // zero past each sample's keys). Head dims 32, four heads, xn rows of 128 (attn_lastq_vabs_supported).
 int attn_lastq_vabs_supported(const AttnDesc& d, const float* xn, long long ldx);
 int attn_fwd_lastq_z_launch(const AttnDesc& d, const float* xn, long long ldx, float* z, float* lse_last,
                             hipStream_t s);
 int attn_bwd_lastq_z_launch(const AttnDesc& d, const float* xn, long long ldx, const float* u, const float* o_last,
-                            long long ldol, const float* lse_last, const float* do_last, long long lddol, float* wpre,
+                            long long ldol, const float* lse_last, const float* do_last, long long lddol, float* prow,
                             hipStream_t s);
 size_t attn_bwd_workspace_bytes(const AttnDesc& d);
 // Whether attn_bwd_launch reads its workspace: the split dQ / dK-dV kernels of seq > 32 keep

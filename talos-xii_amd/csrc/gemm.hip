@@ -70,7 +70,7 @@ enum : int {
   E_NORM = 1024,  // also RMSNorm each output row (N = 128: the whole row is in the tile)
   E_NORMB = 2048,  // the output rows are dL/d(RMSNorm output): write that norm's backward instead
   E_NORMIN = 4096,  // RMSNorm A's rows first (GemmDesc::nin_*): B rows scaled by the gain, rows by rstd
-  E_NBPRE = 8192    // with E_NORMB: a full [M][N] addend to the product before the norm backward
+  E_NBPRE = 8192    // with E_NORMB: the addend sum_h P[row][h] U[sample][h] (four terms) before the norm backward
 };
 
 struct GemmArgs {
@@ -109,7 +109,8 @@ struct GemmArgs {
   const float* nb_add;
   const float* nb_add_last;
   const float* nb_dy_last;
-  const float* nb_pre;  // E_NBPRE
+  const float* nb_pre_p;  // E_NBPRE: [M][4]
+  const float* nb_pre_u;  // E_NBPRE: [M / nb_seq][4][N]
   int nb_seq;
   const int32_t* nb_lens;
   float* nb_dx;
@@ -447,13 +448,22 @@ template <bool PRE>
 __device__ __forceinline__ void normb_apply(const GemmArgs& p, float4 gg, int row, int col, const NbIn& in,
                                             const float4& g, float4& dw) {
   const bool on = row < p.M;
-  if constexpr (PRE) {  // the product's full-size addend (E_NBPRE), before anything else
-    const float4 a = on ? *reinterpret_cast<const float4*>(p.nb_pre + (long long)row * p.N + col)
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
-    gg.x += a.x;
-    gg.y += a.y;
-    gg.z += a.z;
-    gg.w += a.w;
+  if constexpr (PRE) {  // the addend sum_h P[row][h] U[sample][h] (E_NBPRE), before anything else
+    if (on) {
+      const float4 w = *reinterpret_cast<const float4*>(p.nb_pre_p + (long long)row * 4);
+      const float* u = p.nb_pre_u + (long long)(row / p.nb_seq) * 4 * p.N + col;
+      const float wh[4] = {w.x, w.y, w.z, w.w};
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float4 uh = *reinterpret_cast<const float4*>(u + t * p.N);
+        a = make_float4(fmaf(wh[t], uh.x, a.x), fmaf(wh[t], uh.y, a.y), fmaf(wh[t], uh.z, a.z), fmaf(wh[t], uh.w, a.w));
+      }
+      gg.x += a.x;
+      gg.y += a.y;
+      gg.z += a.z;
+      gg.w += a.w;
+    }
   }
   // the addend row, issued first: its latency runs under the row reduction below
   const float4 add = on && p.nb_add ? *reinterpret_cast<const float4*>(p.nb_add + (long long)row * p.N + col)
@@ -1236,7 +1246,8 @@ static GemmArgs to_args(const GemmDesc& d) {
   a.nb_add = d.normb_add;
   a.nb_add_last = d.normb_add_last;
   a.nb_dy_last = d.normb_dy_last;
-  a.nb_pre = d.normb_pre;
+  a.nb_pre_p = d.normb_pre_p;
+  a.nb_pre_u = d.normb_pre_u;
   a.nb_seq = d.normb_seq > 0 ? d.normb_seq : 1;
   a.nb_lens = d.normb_lens;
   a.nb_dx = d.normb_dx;
@@ -1269,7 +1280,7 @@ static int epi_flags(const GemmDesc& d) {
   if (d.dbias) e |= E_DBIAS;
   if (d.norm_out) e |= E_NORM;
   if (d.normb_dx) e |= E_NORMB;
-  if (d.normb_dx && d.normb_pre) e |= E_NBPRE;
+  if (d.normb_dx && d.normb_pre_p) e |= E_NBPRE;
   if (d.nin_gain) e |= E_NORMIN;
   return e;
 }
@@ -1404,10 +1415,17 @@ static int tile_rows(const GemmDesc& d, int e, int ksplit) {
 
 static int gemm_launch_one(const GemmDesc& d, hipStream_t stream);
 
-// c[i] += add[i]
-__global__ void add_inplace_kernel(long long n, const float* __restrict__ add, float* __restrict__ c) {
+// c[row][col] += sum_h p[row][h] u[row / seq][h][col] over four h, in the epilogue's order
+__global__ void add_pre_kernel(int M, int N, int seq, const float* __restrict__ p, const float* __restrict__ u,
+                               float* __restrict__ c) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) c[i] += add[i];
+  if (i >= (long long)M * N) return;
+  const long long row = i / N;
+  const int col = (int)(i % N);
+  float a = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) a = fmaf(p[row * 4 + t], u[((row / seq) * 4 + t) * N + col], a);
+  c[i] += a;
 }
 
 // c[b * seq + last_row(b)][:] += add[b][:] for each sample b (rows of width n).
@@ -1436,7 +1454,7 @@ static bool normb_fused(const GemmDesc& d) {
   return d.fuse_norm && d.N == BN && !d.bf16 && d.batch == 1 && !d.transA && d.transB && !use_small(d, num_cus()) &&
          d.beta == 0.f && !d.bias && !d.resid && d.act == GEMM_ACT_NONE && d.dact == GEMM_DACT_NONE &&
          d.rope_cols == 0 && !d.norm_out && !d.dbias && a16(d.normb_x) && a16(d.normb_dx) && a16(d.normb_gain) &&
-         a16(d.normb_add) && a16(d.normb_add_last) && a16(d.normb_dy_last) && a16(d.normb_pre) && d.normb_ws &&
+         a16(d.normb_add) && a16(d.normb_add_last) && a16(d.normb_dy_last) && a16(d.normb_pre_p) && a16(d.normb_pre_u) && d.normb_ws &&
          d.normb_ws_bytes >= reduce_parts_workspace_bytes(tiles_m, d.N);
 }
 
@@ -1448,14 +1466,14 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
                     "gemm: a row-norm backward after the product needs C with ldc == N");
       GemmDesc g = d;
       g.normb_dx = nullptr;
-      g.normb_pre = nullptr;
+      g.normb_pre_p = g.normb_pre_u = nullptr;
       if (int rc = gemm_launch(g, stream)) return rc;
-      if (d.normb_pre) {
+      if (d.normb_pre_p) {
         const size_t n = (size_t)d.M * d.N;
-        ProfScope ps(stream, "add_inplace_kernel", (double)n, 12.0 * n);
-        hipLaunchKernelGGL(add_inplace_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, stream, (long long)n, d.normb_pre,
-                           d.C);
-        TALOS_LAUNCHED("add_inplace_kernel");
+        ProfScope ps(stream, "add_pre_kernel", 8.0 * n, 8.0 * n);
+        hipLaunchKernelGGL(add_pre_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, stream, d.M, d.N,
+                           d.normb_seq > 0 ? d.normb_seq : 1, d.normb_pre_p, d.normb_pre_u, d.C);
+        TALOS_LAUNCHED("add_pre_kernel");
       }
       if (d.normb_dy_last) {
         const int nb = d.M / (d.normb_seq > 0 ? d.normb_seq : 1);

@@ -77,7 +77,10 @@ struct GemmDesc {
   const float* normb_add = nullptr;
   const float* normb_add_last = nullptr;
   const float* normb_dy_last = nullptr;  // added to C on the last row of each sample first
-  const float* normb_pre = nullptr;      // [M][N], added to C on every row first
+  // [M][4] and [M / normb_seq][4][N]: C[row] += sum_h normb_pre_p[row][h] normb_pre_u[sample][h]
+  // on every row first (h = 0..3, fmaf from zero in h order)
+  const float* normb_pre_p = nullptr;
+  const float* normb_pre_u = nullptr;
   int normb_seq = 1;
   const int32_t* normb_lens = nullptr;
   float* normb_dx = nullptr;

@@ -87,7 +87,7 @@ struct talos_plan_s {
     float *xn1, *q, *dq, *g_xnq;  // the last layer's query path on these rows (last-query attention)
     float *z, *uv;  // absorbed values: sum_j p_j xn1_j and Wv_h dO_h per (sample, head), [batch][H][d]
   } lr{};
-  float* wpre = nullptr;  // absorbed values: the value path's dL/dxn1 on every row of the last layer
+  float* wpre = nullptr;  // absorbed values: the four heads' p_j^h on every row of the last layer, [M][4]
   const int32_t* lens = nullptr;  // per-sample lengths of the PPO call in progress (nullptr: all seq)
   int num_cu = 256;
   // TALOS_PLAN_UNFUSED=1 at creation: every fused alternative (row norms in GEMM epilogues, the
@@ -553,12 +553,13 @@ static int before_write(talos_plan_s* p, hipStream_t s, const void* buf) {
 // dx = RMSNorm backward of dy = g.W^T ([M, K] x [d, K]^T, d = 128 fits one tile row) with the
 // norm's input x, gain and rstd; the product's epilogue computes it (C = dy is then not written,
 // else C is the scratch the separate kernels use). add: the residual gradient on every row;
-// add_last / dy_last: [batch, d] added to dx / dy on the last row of each sample; the gain's
-// gradient goes to dw.
+// add_last / dy_last: [batch, d] added to dx / dy on the last row of each sample; pre_p / pre_u:
+// dy += sum_h pre_p[row][h] pre_u[sample][h] on every row (four terms); the gain's gradient goes
+// to dw.
 static int norm_bwd_mm(talos_plan_s* p, hipStream_t s, int M, int d, int K, const float* g, long long ldg,
                        const float* W, long long ldw, float* C, const float* x, const float* gain, const float* rstd,
                        const float* add, const float* add_last, const float* dy_last, int seq, float* dx,
-                       float* dw, const float* pre = nullptr) {
+                       float* dw, const float* pre_p = nullptr, const float* pre_u = nullptr) {
   GemmDesc gd;
   gd.transB = 1;
   gd.M = M;
@@ -577,7 +578,8 @@ static int norm_bwd_mm(talos_plan_s* p, hipStream_t s, int M, int d, int K, cons
   gd.normb_add = add;
   gd.normb_add_last = add_last;
   gd.normb_dy_last = dy_last;
-  gd.normb_pre = pre;
+  gd.normb_pre_p = pre_p;
+  gd.normb_pre_u = pre_u;
   gd.normb_seq = seq;
   gd.normb_lens = p->lens;
   gd.normb_dx = dx;
@@ -1009,7 +1011,8 @@ static bool ppo_lastq(talos_plan_s* p, const talos_block_cfg& c, talos_plan_s::L
 // Whether the last layer's last-query attention absorbs its value projection (v_j = xn1_j . Wv,
 // which carries no rotation): o_h = (sum_j p_j xn1_j) . Wv_h, so the values are never formed on
 // every row, their weight gradient is a product over the samples (sum_b z_bh^T dO_bh) and their
-// share of dL/dxn1 rows (sum_h p_j^h Wv_h dO_h) joins the keys' in the dX product's epilogue.
+// share of dL/dxn1 rows (sum_h p_j^h Wv_h dO_h) is formed in the dX product's epilogue from the
+// rows' weights p_j^h and u_h = Wv_h dO_h, added to the keys' share there.
 // Four 32-wide heads, d = 128 (the kernels' shapes); the plan's buffers exist (p->wpre).
 static bool ppo_vabs(talos_plan_s* p, const talos_block_cfg& c, talos_plan_s::Layer& L) {
   if (!p->wpre || !ppo_lastq(p, c, L)) return false;
@@ -2288,7 +2291,7 @@ int talos_ppo_plan_create(const talos_ppo_cfg* cfg, talos_plan* plan) {
     if (!p->unfused && bc.attention == TALOS_ATTN_MHA && d == 128 && cfg->n_heads == 4 && bc.head_dim == 32 &&
         cfg->seq <= 256 && cfg->n_layers > 0) {
       for (float** b : {&R.z, &R.uv}) rc |= plan_alloc(p, b, B * cfg->n_heads * d);
-      rc |= plan_alloc(p, &p->wpre, M * d);
+      rc |= plan_alloc(p, &p->wpre, M * 4);
     }
   }
   {  // per-workgroup loss partials (doubles)
@@ -2549,7 +2552,7 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
       if ((rc = before_write(p, s, p->g_out))) return rc;
       rc = norm_bwd_mm(p, s, M, d, vabs ? d : 2 * d, g_kv, 3 * d, params + o.wqkv + d, 3 * d, p->g_xn, L.x,
                        params + o.g1, L.rstd1, nullptr, R.g_h2, R.g_xnq, c.seq, p->g_out, G + o.g1,
-                       vabs ? p->wpre : nullptr);
+                       vabs ? p->wpre : nullptr, vabs ? R.uv : nullptr);
     } else {
       // the row gradients spread over the full token grid
       const int ow = attn_width(bc);
