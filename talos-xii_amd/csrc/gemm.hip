@@ -54,6 +54,10 @@ constexpr int NT = 256;
 #define TALOS_SPLITK_MIN_K 512
 #endif
 constexpr int NBUF = TALOS_GEMM_DBUF ? 2 : 1;
+// Wave priority (s_setprio) of the main loop's products, 0..3 (1: C4 2.398 -> 2.388 ms).
+#ifndef TALOS_GEMM_PRIO
+#define TALOS_GEMM_PRIO 1
+#endif
 
 // Epilogue flags (template parameter E).
 enum : int {
@@ -719,6 +723,9 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
     }
     const float* Ap = Abase + buf * PANEL;
     const float* Bp = Bbase + buf * PANEL;
+    // the chunk's products at a raised wave priority: a wave with products ready issues ahead of
+    // the waves of the CU's other workgroups that are storing panels or waiting at the barrier
+    __builtin_amdgcn_s_setprio(TALOS_GEMM_PRIO);
 #pragma unroll
     for (int j = 0; j < BK / 8; ++j) {
       // fragments of steps 4j .. 4j+3: k = 8j + 4h + q for q = 0..3
@@ -738,6 +745,7 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     if constexpr ((E & E_DBIAS) != 0) {
       // column sums of the B panel Bs[k][n] (k-major): thread t sums column t%128 over half the rows
       if (m0 == 0) {
