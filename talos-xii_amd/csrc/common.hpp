@@ -138,11 +138,13 @@ __device__ __forceinline__ T block_sum(T v, T* red) {
 // Stegun 7.1.26 (Hastings): erf(z) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2),
 // t = 1 / (1 + p z), |error| <= 1.5e-7; with z = |x| / sqrt(2), exp(-z^2) is the same
 // exp(-x^2 / 2) the density needs, so GELU and its derivative take one exponential. The lower
-// tail 0.5 erfc(z) is formed directly (no cancellation for x < 0).
+// tail 0.5 erfc(z) is formed directly (no cancellation for x < 0). t is the hardware reciprocal
+// (v_rcp_f32, about 1 ulp on [1, inf)): a correctly rounded one is the ten-instruction division
+// sequence, a third of the epilogue's per-element work, for an error far below the formula's.
 __device__ __forceinline__ float normal_cdf(float x, float* e) {
   const float z = fabsf(x) * 0.70710678118654752f;
   *e = __expf(-0.5f * x * x);  // hardware exp2 of the scaled argument: relative error ~|x^2| 2^-24
-  const float t = __frcp_rn(fmaf(0.3275911f, z, 1.0f));
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
   const float poly =
       t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, 1.061405429f, -1.453152027f), 1.421413741f), -0.284496736f), 0.254829592f);
   const float tail = 0.5f * poly * *e;  // P(X > |x|)
