@@ -71,6 +71,9 @@ __device__ __forceinline__ int key_len(const AttnArgs& a, int b) {
 }
 
 constexpr float kNegInf = -INFINITY;
+// Every exponential here is of a softmax argument s - max or s - lse (<= 0, -inf for a masked
+// key): __expf, the hardware exp2 of the scaled argument (relative error about |x| 2^-24, and
+// exactly 0 at -inf), instead of expf's range-reduced sequence of a dozen instructions.
 
 // Load style per kernel (SEL of load_half) and minimum waves per SIMD the register allocation
 // must allow (compile-time tuning knobs).
@@ -234,10 +237,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_
     float bs = 0.f;
     if (mn != kNegInf) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) bs += expf(sv[r] - mn);
+      for (int r = 0; r < 16; ++r) bs += __expf(sv[r] - mn);
     }
     bs += __shfl_xor(bs, 32, 64);
-    l = (m == kNegInf ? 0.f : l * expf(m - mn)) + bs;
+    l = (m == kNegInf ? 0.f : l * __expf(m - mn)) + bs;
     m = mn;
   }
   const float inv_l = l > 0.f ? 1.f / l : 0.f;
@@ -251,7 +254,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_
     if (kb_last > 0) scores(kb, sv);  // one key block: the scores of pass 1 are still in sv
     float P[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) P[r] = (m == kNegInf) ? 0.f : expf(sv[r] - m) * inv_l;
+    for (int r = 0; r < 16; ++r) P[r] = (m == kNegInf) ? 0.f : __expf(sv[r] - m) * inv_l;
     mfma_p_rows<OB, kFwdSel>(P, a.v, a.ldv, tok0, kb * 32, a.S, hd * a.dv, a.dv, l32, h, oacc);
   }
   // O in accumulator layout: register r <-> query qb*32 + acc_row(r, h), lane <-> column
@@ -301,7 +304,7 @@ __device__ __forceinline__ floatx16 s32_pair(const AttnArgs& a, int pair, int l3
   float l = 0.f;
   if (m != kNegInf) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) l += expf(sv[r] - m);
+    for (int r = 0; r < 16; ++r) l += __expf(sv[r] - m);
   }
   l += __shfl_xor(l, 32, 64);
   const float inv_l = l > 0.f ? 1.f / l : 0.f;
@@ -310,7 +313,7 @@ __device__ __forceinline__ floatx16 s32_pair(const AttnArgs& a, int pair, int l3
   for (int r = 0; r < 16; ++r) oacc[r] = 0.f;
 #pragma unroll
   for (int s = 0; s < 16; ++s) {
-    const float p = (m == kNegInf) ? 0.f : expf(sv[s] - m) * inv_l;
+    const float p = (m == kNegInf) ? 0.f : __expf(sv[s] - m) * inv_l;
     oacc = __builtin_amdgcn_mfma_f32_32x32x2f32(p, vm[s], oacc, 0, 0, 0);
   }
 #pragma unroll
@@ -466,7 +469,7 @@ __global__ __launch_bounds__(512) void attn_fwd_s64_wo_kernel(AttnArgs a, WoArgs
     for (int kb = 0; kb < 2; ++kb) {
       if (kb == 1 && !two) break;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) l += expf(sv[kb][r] - m);
+      for (int r = 0; r < 16; ++r) l += __expf(sv[kb][r] - m);
     }
   }
   l += __shfl_xor(l, 32, 64);
@@ -480,7 +483,7 @@ __global__ __launch_bounds__(512) void attn_fwd_s64_wo_kernel(AttnArgs a, WoArgs
     if (kb == 1 && !two) break;
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
-      const float p = (m == kNegInf) ? 0.f : expf(sv[kb][s] - m) * inv_l;
+      const float p = (m == kNegInf) ? 0.f : __expf(sv[kb][s] - m) * inv_l;
       const float vm = Vs[(32 * kb + acc_row(s, h)) * kVP + hd * 32 + l32];
       oacc = __builtin_amdgcn_mfma_f32_32x32x2f32(p, vm, oacc, 0, 0, 0);
     }
@@ -613,11 +616,11 @@ attn_fwd_tiled_kernel(AttnArgs a) {
       }
       bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
       const float mn = fmaxf(m, bm);
-      const float alpha = (m == kNegInf) ? 0.f : expf(m - mn);
+      const float alpha = (m == kNegInf) ? 0.f : __expf(m - mn);
       float P[16], bs = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        P[r] = (mn == kNegInf) ? 0.f : expf(sv[r] - mn);  // exp(-inf) = 0 for the masked keys
+        P[r] = (mn == kNegInf) ? 0.f : __expf(sv[r] - mn);  // exp(-inf) = 0 for the masked keys
         bs += P[r];
       }
       bs += __shfl_xor(bs, 32, 64);
@@ -718,7 +721,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int key = kb * 32 + acc_row(r, h);
       const bool ok = qok && key < Sk && (!a.causal || key <= q);
-      const float p = expf(ok ? sacc[r] - lse : kNegInf);
+      const float p = __expf(ok ? sacc[r] - lse : kNegInf);
       dS[r] = p * (pacc[r] - D);
     }
     mfma_p_rows<QB, kBwdSel>(dS, a.k, a.ldk, tok0, kb * 32, a.S, hd * a.dk, a.dk, l32, h, dq);
@@ -784,7 +787,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a) {
       const bool ok = kok && qr < a.S && (!a.causal || key <= qr);
       const long long li = (long long)pair * a.S + (qr < a.S ? qr : 0);
       const float lse_r = a.lse[li], d_r = a.D[li];  // unconditional loads (clamped index)
-      const float p = expf(ok ? sacc[r] - lse_r : kNegInf);
+      const float p = __expf(ok ? sacc[r] - lse_r : kNegInf);
       P[r] = p;
       dS[r] = p * (pacc[r] - d_r);
     }
@@ -919,7 +922,7 @@ attn_bwd_dq_tiled_kernel(AttnArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int key = kb * 32 + acc_row(r, h);
         const bool ok = qok && key < Sk && (!a.causal || key <= q);
-        const float p = expf(ok ? sacc[r] - lse : kNegInf);
+        const float p = __expf(ok ? sacc[r] - lse : kNegInf);
         dS[r] = p * (pacc[r] - D);
       }
 #pragma unroll
@@ -1055,7 +1058,7 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
           const int r = 4 * j + u;
           const int qr = qb * 32 + acc_row(r, h);
           const bool ok = kok && qr < a.S && (!a.causal || key <= qr);
-          const float p = expf(ok ? sacc[r] - lv[u] : kNegInf);
+          const float p = __expf(ok ? sacc[r] - lv[u] : kNegInf);
           P[r] = p;
           dS[r] = p * (pacc[r] - dv4[u]);
         }
@@ -1253,7 +1256,7 @@ __device__ __forceinline__ void bwd_fused_core(const AttnArgs& a, float* W, int 
   for (int r = 0; r < 16; ++r) {
     const int qr = acc_row(r, h);
     const bool ok = kok && q0 + qr < a.S && (!a.causal || k0 + l32 <= q0 + qr);
-    const float p = expf(ok ? sacc[r] - lq[r] : kNegInf);  // exp(-inf) = 0: no branch
+    const float p = __expf(ok ? sacc[r] - lq[r] : kNegInf);  // exp(-inf) = 0: no branch
     P[r] = p;
     dS[r] = p * (pacc[r] - dq_[r]);
     if constexpr (!STAGE) T[qr * kTS + l32] = dS[r];
@@ -1848,8 +1851,8 @@ __global__ __launch_bounds__(256) void attn_fwd_lastq_kernel(AttnArgs a, float* 
       const float sc = row_sum<C>(dot4(q, k));
       const float s = ok ? sc : kNegInf;
       const float mn = fmaxf(m, col_max<C>(s));
-      const float p = ok ? expf(s - mn) : 0.f;
-      const float corr = m == kNegInf ? 0.f : expf(m - mn);
+      const float p = ok ? __expf(s - mn) : 0.f;
+      const float corr = m == kNegInf ? 0.f : __expf(m - mn);
       l = l * corr + col_sum<C>(p);  // p is the same on a row's C lanes: the sum over the pass's rows
       acc = make_float4(acc.x * corr + p * v.x, acc.y * corr + p * v.y, acc.z * corr + p * v.z,
                         acc.w * corr + p * v.w);
@@ -1894,7 +1897,7 @@ __global__ __launch_bounds__(256) void attn_bwd_lastq_kernel(AttnArgs a, const f
     const float4 k = ld4(a.k + (tok0 + jj) * a.ldk + hh * D + 4 * c);
     const float4 v = ld4(a.v + (tok0 + jj) * a.ldv + hh * D + 4 * c);
     const float s = row_sum<C>(dot4(qs, k));
-    const float p = ok ? expf(s - lse) : 0.f;
+    const float p = ok ? __expf(s - lse) : 0.f;
     const float dp = row_sum<C>(dot4(g, v));
     const float dS = p * (dp - Dd);
     dq = make_float4(dq.x + dS * k.x, dq.y + dS * k.y, dq.z + dS * k.z, dq.w + dS * k.w);
@@ -1959,7 +1962,7 @@ __global__ __launch_bounds__(64 * kVabsH) void attn_fwd_lastq_z_kernel(AttnArgs 
   }
   wave_lds_sync();
   float l = 0.f;
-  for (int j = lane; j < Sk; j += 64) l += expf(ps[hh][j] - m);
+  for (int j = lane; j < Sk; j += 64) l += __expf(ps[hh][j] - m);
   l = wave_sum(l);
   if (lane == 0) {
     mh[hh] = m;
@@ -1974,7 +1977,7 @@ __global__ __launch_bounds__(64 * kVabsH) void attn_fwd_lastq_z_kernel(AttnArgs 
     const float2 x = *reinterpret_cast<const float2*>(xn + (tok0 + j) * ldx + 2 * lane);
 #pragma unroll
     for (int i = 0; i < kVabsH; ++i) {
-      const float pj = expf(ps[i][j] - mh[i]) * ilh[i];
+      const float pj = __expf(ps[i][j] - mh[i]) * ilh[i];
       acc[i] = make_float2(fmaf(pj, x.x, acc[i].x), fmaf(pj, x.y, acc[i].y));
     }
   }
@@ -2026,7 +2029,7 @@ __global__ __launch_bounds__(64 * kVabsH) void attn_bwd_lastq_z_kernel(AttnArgs 
     const bool ok = j < Sk;
     const float4 k = ld4(a.k + (tok0 + (ok ? j : 0)) * a.ldk + hh * D + 4 * c);
     const float s = row_sum<C>(dot4(qs, k));
-    if (c == 0 && j < a.S) ps[hh][j] = ok ? expf(s - lse) : 0.f;
+    if (c == 0 && j < a.S) ps[hh][j] = ok ? __expf(s - lse) : 0.f;
   }
   __syncthreads();
   // dS_j^h = p_j^h (xn_j . u_h - D_h) for every head: wave w takes the key pairs j0 = 2w, 2w + 2H,
