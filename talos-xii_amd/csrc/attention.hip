@@ -34,6 +34,7 @@ struct AttnArgs {
   int B, S, H, dk, dv;
   float scale;
   int causal;
+  float* ds;  // the tiled backward's dS rows ([B*H][S][S]) when it forms dQ from them, else null
   const float* q;
   long long ldq;
   const float* k;
@@ -533,6 +534,13 @@ __device__ __forceinline__ void block_st4(float* tile, int g, float4 v) {
   *reinterpret_cast<float4*>(tile + (idx / DM) * P + idx % DM) = v;
 }
 
+// Orders the wave's own LDS writes before its later reads (no workgroup barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Per-query factors of this wave (lane l32 holds query l32's; h == 0 writes) into O's layout:
 // f[r] is the factor of query acc_row(r, h).
 __device__ __forceinline__ void bcast_rows(float* slice, float v, int l32, int h, float (&f)[16]);
@@ -951,7 +959,10 @@ attn_bwd_dq_tiled_kernel(AttnArgs a) {
     }
 }
 
-template <int DKM, int DVM>
+// DS: D = rowsum(dO * O) of each staged query block is formed here (O rows loaded beside the dO
+// rows) instead of read, and every dS value of the wave's key block is stored to a.ds (row of
+// query q, column of key: each store is 32 consecutive keys of a row) for attn_bwd_dq_ds_kernel.
+template <int DKM, int DVM, bool DS = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DKM > 32 ? 2 : TALOS_ATTN_TILED_WAVES))) void
 attn_bwd_dkv_tiled_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32;
@@ -960,6 +971,7 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
   __shared__ __align__(16) float Qs[32 * PK];
   __shared__ __align__(16) float Gs[32 * PV];
   __shared__ __align__(16) float LD[2][32];  // lse, D of the staged query block
+  __shared__ float Ts[DS ? 4 : 1][DS ? 32 * 33 : 1];  // DS: each wave's dS tile on its way out
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
   const int t = threadIdx.x;
   const int ntile = (a.S + kQTile - 1) / kQTile;
@@ -999,7 +1011,8 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) dv[i][r] = 0.f;
 
   constexpr bool PF = DKM + DVM <= 128;  // as in attn_bwd_dq_tiled_kernel (K, V rows, dK, dV live)
-  float4 rq[KL], rg[VL];
+  float4 rq[KL], rg[VL], ro[DS && PF ? VL : 1];
+  float dpart[DS ? VL : 1];  // DS: the thread's piece of its rows' D
   float rl = 0.f;
   auto fetch = [&](int qb) {
 #pragma unroll
@@ -1008,7 +1021,18 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < VL; ++i)
       rg[i] = block_ld4<DVM>(a.dout, a.lddo, tok0, qb * 32, a.S, hd * a.dv, a.dv, i * 256 + t, a.vec);
-    if (t < 64) {  // lse (t < 32) and D (32 <= t < 64) of the block's queries
+    if constexpr (DS) {
+#pragma unroll
+      for (int i = 0; i < VL; ++i) {
+        const float4 o4 = block_ld4<DVM>(a.o, a.ldo, tok0, qb * 32, a.S, hd * a.dv, a.dv, i * 256 + t, a.vec);
+        if constexpr (PF) {
+          ro[i] = o4;  // the dot waits for the stash: the loads stay in flight under the block's work
+        } else {
+          dpart[i] = rg[i].x * o4.x + rg[i].y * o4.y + rg[i].z * o4.z + rg[i].w * o4.w;
+        }
+      }
+    }
+    if (t < (DS ? 32 : 64)) {  // lse (t < 32) and D (32 <= t < 64) of the block's queries
       const int qr = qb * 32 + (t & 31);
       const long long li = (long long)pair * a.S + (qr < a.S ? qr : 0);
       rl = (t < 32 ? a.lse : a.D)[li];
@@ -1019,7 +1043,20 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
     for (int i = 0; i < KL; ++i) block_st4<DKM, PK>(Qs, i * 256 + t, rq[i]);
 #pragma unroll
     for (int i = 0; i < VL; ++i) block_st4<DVM, PV>(Gs, i * 256 + t, rg[i]);
-    if (t < 64) LD[t >> 5][t & 31] = rl;
+    if (t < (DS ? 32 : 64)) LD[t >> 5][t & 31] = rl;
+    if constexpr (DS) {
+      // the DVM / 4 consecutive threads holding row (i * 256 + t) / (DVM / 4) add their pieces
+      constexpr int LPR = DVM / 4;
+#pragma unroll
+      for (int i = 0; i < VL; ++i) {
+        float d = PF ? rg[i].x * ro[0 + (PF ? i : 0)].x + rg[i].y * ro[PF ? i : 0].y + rg[i].z * ro[PF ? i : 0].z +
+                           rg[i].w * ro[PF ? i : 0].w
+                     : dpart[i];
+#pragma unroll
+        for (int o = 1; o < LPR; o <<= 1) d += __shfl_xor(d, o, 64);
+        if ((t & (LPR - 1)) == 0) LD[1][(i * 256 + t) / LPR] = d;
+      }
+    }
   };
   fetch(qb_beg);
   stash();
@@ -1061,6 +1098,7 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
           const float p = __expf(ok ? sacc[r] - lv[u] : kNegInf);
           P[r] = p;
           dS[r] = p * (pacc[r] - dv4[u]);
+          if constexpr (DS) Ts[wv][acc_row(r, h) * 33 + l32] = dS[r];  // row: query, column: key
         }
       }
 #pragma unroll
@@ -1071,6 +1109,18 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
         for (int i = 0; i < VB; ++i) dv[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(P[s2], grow[i * 32], dv[i], 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < KB; ++i) dk[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(dS[s2], qrow[i * 32], dk[i], 0, 0, 0);
+      }
+      if constexpr (DS) {  // the block's dS tile [32 queries][32 keys] to a.ds, 16-byte row pieces
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int g = i * 64 + lane, row = g >> 3, c = 4 * (g & 7);
+          const int qr = qb * 32 + row, k0 = kb * 32 + c;
+          const float* tr = Ts[wv] + row * 33 + c;
+          if (qr < a.S && k0 < a.S)
+            *reinterpret_cast<float4*>(a.ds + ((long long)pair * a.S + qr) * a.S + k0) =
+                make_float4(tr[0], tr[1], tr[2], tr[3]);
+        }
       }
     }
     __syncthreads();
@@ -1100,16 +1150,101 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
     }
 }
 
+// dQ = dS . K from the dS rows attn_bwd_dkv_tiled_kernel<.., .., true> stored (a.ds), instead of
+// forming S, P and dP again: a workgroup is 128 queries of one (batch, head) pair as in
+// attn_bwd_dq_tiled_kernel (wave = 32 queries), and for each 32-key block the K rows and the
+// tile's [128 x 32] dS block are staged in LDS (loaded one block ahead into registers); the dS
+// block is read transposed there (pitch 33), one value a product step. seq % 4 == 0.
+template <int DKM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_TILED_WAVES))) void
+attn_bwd_dq_ds_kernel(AttnArgs a) {
+  constexpr int QB = DKM / 32, PK = DKM + 4, KL = DKM / 32, PD = 33;
+  __shared__ __align__(16) float Ks[32 * PK];
+  __shared__ float Ds[kQTile * PD];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int t = threadIdx.x;
+  const int ntile = (a.S + kQTile - 1) / kQTile;
+  const int pair = blockIdx.x / ntile, tile = blockIdx.x % ntile;
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int Sk = key_len(a, b);
+  const int qb = tile * 4 + wv;
+  const bool wave_on = qb * 32 < a.S;
+  const int q_hi = min(a.S, (tile + 1) * kQTile) - 1;
+  const int kb_end = Sk == 0 ? -1 : (a.causal ? min(q_hi, Sk - 1) : Sk - 1) >> 5;
+  const int wave_kb_end = a.causal ? min(kb_end, qb) : kb_end;
+  const float* dsp = a.ds + (long long)pair * a.S * a.S;
+  float4 rk[KL], rd[4];
+  auto fetch = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < KL; ++i)
+      rk[i] = block_ld4<DKM>(a.k, a.ldk, tok0, kb * 32, a.S, hd * a.dk, a.dk, i * 256 + t, a.vec);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // float4 i * 256 + t of the block: query row / 8, keys 4 (t % 8) ..
+      const int g = i * 256 + t, qr = tile * kQTile + (g >> 3), key = kb * 32 + 4 * (g & 7);
+      rd[i] = qr < a.S && key < a.S ? *reinterpret_cast<const float4*>(dsp + (long long)qr * a.S + key)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < KL; ++i) block_st4<DKM, PK>(Ks, i * 256 + t, rk[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int g = i * 256 + t;
+      float* d = Ds + (g >> 3) * PD + 4 * (g & 7);
+      d[0] = rd[i].x;
+      d[1] = rd[i].y;
+      d[2] = rd[i].z;
+      d[3] = rd[i].w;
+    }
+  };
+  floatx16 dq[QB];
+#pragma unroll
+  for (int i = 0; i < QB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
+  if (kb_end >= 0) {
+    fetch(0);
+    stash();
+  }
+  __syncthreads();
+  for (int kb = 0; kb <= kb_end; ++kb) {
+    const bool more = kb < kb_end;
+    if (more) fetch(kb + 1);
+    if (wave_on && kb <= wave_kb_end) {
+      const float* drow = Ds + (wv * 32 + l32) * PD;
+#pragma unroll
+      for (int s2 = 0; s2 < 16; ++s2) {  // dQ += dS . K
+        const float dsv = drow[acc_row(s2, h)];
+        const float* krow = Ks + acc_row(s2, h) * PK + l32;
+#pragma unroll
+        for (int i = 0; i < QB; ++i) dq[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(dsv, krow[i * 32], dq[i], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+    if (more) {
+      stash();
+      __syncthreads();
+    }
+  }
+  if (!wave_on) return;
+#pragma unroll
+  for (int i = 0; i < QB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qr = qb * 32 + acc_row(r, h);
+      const int e = i * 32 + l32;
+      const float g = rope_t(dq[i][r] * a.scale, e, qr, a, qr < a.S);
+      if (qr < a.S && e < a.dk) a.dq[(tok0 + qr) * a.lddq + hd * a.dk + e] = g;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Single-block backward (seq <= 32): one wave per (batch, head) pair computes dQ, dK and dV from
 // one read of q, k, v, o and dO (D = dO . O is formed in the wave). S layout (lane <-> key,
 // register r <-> query acc_row(r, h)); dS is transposed through the wave's LDS slice for dQ.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 __device__ __forceinline__ void bcast_rows(float* slice, float v, int l32, int h, float (&f)[16]) {
   if (h == 0) slice[l32] = v;
@@ -1725,6 +1860,55 @@ static int attn_bwd_fused(const AttnArgs& a, int dkm, int dvm, hipStream_t s) {
   ATTN_ALL(attn_bwd_fused_kernel)
 }
 
+// The tiled backward with dQ formed from stored dS rows (d.ds): seq > 64 on the tiled kernels'
+// head dims, rows of whole float4s.
+bool attn_bwd_ds_supported(const AttnDesc& d) {
+  int dkm, dvm;
+  if (attn_legacy() || d.seq <= 64 || d.seq % 4 != 0 || !pick_dims(d.dk, d.dv, &dkm, &dvm)) return false;
+  return (dkm == 32 && dvm == 32) || (dkm == 64 && dvm == 64) || (dkm == 96 && dvm == 64);
+}
+
+size_t attn_bwd_ds_bytes(const AttnDesc& d) {
+  return attn_bwd_ds_supported(d) ? sizeof(float) * (size_t)d.batch * d.heads * d.seq * d.seq : 0;
+}
+
+static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, hipStream_t s) {
+  a.ds = ds;
+  const double rows = (double)a.B * a.S * a.H, tiles = (a.S + kQTile - 1) / kQTile, pairs = kept_pairs(a);
+  // dK / dV: s = q.k, dp = dO.v, dv += p dO, dk += ds q; k, v rows once, q / dO / O rows and lse
+  // once per 128-key tile; dS written
+  {
+    const double bytes = 4.0 * rows * (2.0 * a.dk + 2.0 * a.dv) +
+                         4.0 * a.B * a.H * tiles * a.S * (a.dk + 2.0 * a.dv + 1.0) + 4.0 * pairs;
+    dim3 grid((unsigned)((long long)a.B * a.H * (long long)tiles));
+#define TILED(DK, DV)                                                                              \
+    if (dkm == DK && dvm == DV) {                                                                  \
+      ProfScope ps(s, "attn_bwd_dkv_tiled_kernel<" #DK ", " #DV ", true>", pairs * (4.0 * a.dk + 4.0 * a.dv), bytes); \
+      hipLaunchKernelGGL((attn_bwd_dkv_tiled_kernel<DK, DV, true>), grid, dim3(256), 0, s, a);    \
+      if (int rc = launch_status("attn_bwd_dkv_tiled_kernel")) return rc;                          \
+    }
+    TILED(32, 32)
+    TILED(64, 64)
+    TILED(96, 64)
+#undef TILED
+  }
+  // dQ = dS . K: dS read, K rows once per 128-query tile, dq written
+  const double bytes = 4.0 * pairs + 4.0 * a.B * a.H * tiles * a.S * a.dk + 4.0 * rows * a.dk;
+  dim3 grid((unsigned)((long long)a.B * a.H * (long long)tiles));
+#define TILED(DK)                                                                                  \
+  if (dkm == DK) {                                                                                 \
+    ProfScope ps(s, "attn_bwd_dq_ds_kernel<" #DK ">", pairs * 2.0 * a.dk, bytes);                 \
+    hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<DK>), grid, dim3(256), 0, s, a);                    \
+    return launch_status("attn_bwd_dq_ds_kernel");                                                 \
+  }
+  TILED(32)
+  TILED(64)
+  TILED(96)
+#undef TILED
+  set_error("attention backward: no dS kernel for head dims (%d, %d)", dkm, dvm);
+  return TALOS_ERR_UNSUPPORTED;
+}
+
 bool attn_bwd_uses_workspace(const AttnDesc& d) {
   return (long long)d.batch * d.heads * d.seq > 0 && d.seq > 32;
 }
@@ -1749,6 +1933,8 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
       hipLaunchKernelGGL(attn_bwd_s64_kernel<4>, dim3((unsigned)((long long)a.B * a.H)), dim3(256), 0, s, a);
     return launch_status("attn_bwd_s64_kernel");
   }
+  if (d.ds && attn_bwd_ds_supported(d) && (reinterpret_cast<uintptr_t>(d.ds) & 15) == 0)
+    return attn_bwd_with_ds(a, dkm, dvm, d.ds, s);
   int rc = attn_bwd_dq(a, dkm, dvm, s);
   if (rc) return rc;
   return attn_bwd_dkv(a, dkm, dvm, s);

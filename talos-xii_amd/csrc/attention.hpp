@@ -43,6 +43,10 @@ struct AttnDesc {
   long long ldq_last = 0;
   float* dq_last = nullptr;
   long long lddq_last = 0;
+  // optional scratch of attn_bwd_ds_bytes(d) bytes (16-byte aligned): where attn_bwd_ds_supported
+  // holds, the backward stores dS ([batch * heads][seq][seq]) from its dK / dV kernel and forms dQ =
+  // dS . K from it instead of forming S, P and dP a second time
+  float* ds = nullptr;
 };
 
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s);
@@ -83,6 +87,8 @@ int attn_bwd_lastq_z_launch(const AttnDesc& d, const float* xn, long long ldx, c
                             long long ldol, const float* lse_last, const float* do_last, long long lddol, float* prow,
                             hipStream_t s);
 size_t attn_bwd_workspace_bytes(const AttnDesc& d);
+bool attn_bwd_ds_supported(const AttnDesc& d);
+size_t attn_bwd_ds_bytes(const AttnDesc& d);
 // Whether attn_bwd_launch reads its workspace: the split dQ / dK-dV kernels of seq > 32 keep
 // D = rowsum(dO * O) there; the single-block kernel of seq <= 32 forms D in registers.
 bool attn_bwd_uses_workspace(const AttnDesc& d);

@@ -100,6 +100,7 @@ struct talos_plan_s {
   // shared by all layers
   struct MlaScratch {
     float *qc, *qr, *kc, *kr, *dq, *dk, *dv, *dqc, *dqr, *dkc, *dkr, *dckv;
+    float* ds = nullptr;  // the attention backward's dS rows (attn_bwd_ds_supported)
   } ms{};
   talos_mla_cfg mla{};
 };
@@ -304,6 +305,15 @@ static int alloc_mla_scratch(talos_plan_s* p, const MlaDims& D) {
   for (float** b : {&m.dq, &m.dk}) rc |= plan_alloc(p, b, M * H * td);
   rc |= plan_alloc(p, &m.dv, M * H * D.vd);
   rc |= plan_alloc(p, &m.dckv, M * D.L);
+  {
+    AttnDesc ad;
+    ad.batch = D.batch;
+    ad.seq = D.seq;
+    ad.heads = D.H;
+    ad.dk = (int)td;
+    ad.dv = D.vd;
+    if (!p->unfused && attn_bwd_ds_supported(ad)) rc |= plan_alloc(p, &m.ds, attn_bwd_ds_bytes(ad) / sizeof(float));
+  }
   if (rc) return TALOS_ERR_ALLOC;
   // split-K workspace of the weight-gradient products
   for (auto rc2 : {std::make_pair(D.d, D.H * D.hd), std::make_pair(D.d, D.H * D.r), std::make_pair(D.L, D.H * D.hd),
@@ -629,6 +639,7 @@ static AttnDesc mla_attn_desc(talos_plan_s* p, const MlaDims& D, const talos_pla
   a.rope_off = D.hd;  // the decoupled RoPE dims follow the content dims in each head
   a.rope_dim = D.r;
   a.lens = p->lens;
+  a.ds = p->ms.ds;
   return a;
 }
 

@@ -182,9 +182,12 @@ def run_mla(ci, prec, p, x, G, eps=1e-5, base=10000.0):
 
 
 @pytest.mark.parametrize("ci", [[2, 5, 16, 2, 8, 4, 8, 8, 0, 0], [2, 37, 64, 2, 32, 8, 16, 16, 1, 0],
-                                [2, 64, 512, 8, 128, 32, 64, 64, 0, 0]])
+                                [2, 64, 512, 8, 128, 32, 64, 64, 0, 0], [2, 100, 64, 2, 32, 8, 16, 16, 1, 0],
+                                [1, 132, 512, 8, 128, 32, 64, 64, 1, 0]])
 def test_mla_fwd_bwd_vs_oracle(oracle, ci):
-    # the last case is C5's block (d512, 8 heads, latent 128, rope 32, head 64, v 64) at batch 2
+    # the third case is C5's block (d512, 8 heads, latent 128, rope 32, head 64, v 64) at batch 2;
+    # the last two (seq 100, 132: a partial last key block, causal) take the backward that stores
+    # dS from its dK / dV kernel and forms dQ from it
     from common import mla_params
     rng = np.random.default_rng(3000 + ci[1] + ci[2])
     B, S, d = ci[:3]
