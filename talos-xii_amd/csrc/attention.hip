@@ -959,9 +959,9 @@ attn_bwd_dq_tiled_kernel(AttnArgs a) {
     }
 }
 
-// DS: D = rowsum(dO * O) of each staged query block is formed here (O rows loaded beside the dO
-// rows) instead of read, and every dS value of the wave's key block is stored to a.ds (row of
-// query q, column of key: each store is 32 consecutive keys of a row) for attn_bwd_dq_ds_kernel.
+// DS: every dS value of the wave's key blocks is also stored to a.ds (row of query q, column of
+// key), through a per-wave LDS tile so the global stores are 16-byte pieces of rows, for
+// attn_bwd_dq_ds_kernel; D comes from attn_rowdot_kernel.
 template <int DKM, int DVM, bool DS = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DKM > 32 ? 2 : TALOS_ATTN_TILED_WAVES))) void
 attn_bwd_dkv_tiled_kernel(AttnArgs a) {
@@ -1011,8 +1011,7 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) dv[i][r] = 0.f;
 
   constexpr bool PF = DKM + DVM <= 128;  // as in attn_bwd_dq_tiled_kernel (K, V rows, dK, dV live)
-  float4 rq[KL], rg[VL], ro[DS && PF ? VL : 1];
-  float dpart[DS ? VL : 1];  // DS: the thread's piece of its rows' D
+  float4 rq[KL], rg[VL];
   float rl = 0.f;
   auto fetch = [&](int qb) {
 #pragma unroll
@@ -1021,18 +1020,7 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < VL; ++i)
       rg[i] = block_ld4<DVM>(a.dout, a.lddo, tok0, qb * 32, a.S, hd * a.dv, a.dv, i * 256 + t, a.vec);
-    if constexpr (DS) {
-#pragma unroll
-      for (int i = 0; i < VL; ++i) {
-        const float4 o4 = block_ld4<DVM>(a.o, a.ldo, tok0, qb * 32, a.S, hd * a.dv, a.dv, i * 256 + t, a.vec);
-        if constexpr (PF) {
-          ro[i] = o4;  // the dot waits for the stash: the loads stay in flight under the block's work
-        } else {
-          dpart[i] = rg[i].x * o4.x + rg[i].y * o4.y + rg[i].z * o4.z + rg[i].w * o4.w;
-        }
-      }
-    }
-    if (t < (DS ? 32 : 64)) {  // lse (t < 32) and D (32 <= t < 64) of the block's queries
+    if (t < 64) {  // lse (t < 32) and D (32 <= t < 64) of the block's queries
       const int qr = qb * 32 + (t & 31);
       const long long li = (long long)pair * a.S + (qr < a.S ? qr : 0);
       rl = (t < 32 ? a.lse : a.D)[li];
@@ -1043,20 +1031,7 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
     for (int i = 0; i < KL; ++i) block_st4<DKM, PK>(Qs, i * 256 + t, rq[i]);
 #pragma unroll
     for (int i = 0; i < VL; ++i) block_st4<DVM, PV>(Gs, i * 256 + t, rg[i]);
-    if (t < (DS ? 32 : 64)) LD[t >> 5][t & 31] = rl;
-    if constexpr (DS) {
-      // the DVM / 4 consecutive threads holding row (i * 256 + t) / (DVM / 4) add their pieces
-      constexpr int LPR = DVM / 4;
-#pragma unroll
-      for (int i = 0; i < VL; ++i) {
-        float d = PF ? rg[i].x * ro[0 + (PF ? i : 0)].x + rg[i].y * ro[PF ? i : 0].y + rg[i].z * ro[PF ? i : 0].z +
-                           rg[i].w * ro[PF ? i : 0].w
-                     : dpart[i];
-#pragma unroll
-        for (int o = 1; o < LPR; o <<= 1) d += __shfl_xor(d, o, 64);
-        if ((t & (LPR - 1)) == 0) LD[1][(i * 256 + t) / LPR] = d;
-      }
-    }
+    if (t < 64) LD[t >> 5][t & 31] = rl;
   };
   fetch(qb_beg);
   stash();
@@ -1148,6 +1123,25 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
       const int e = i * 32 + l32;
       if (kr < a.S && e < a.dv) a.dv_out[(tok0 + kr) * a.lddv + hd * a.dv + e] = dv[i][r];
     }
+}
+
+// D[pair * S + q] = sum_e dO[q][e] O[q][e] over the head's dv columns: 16 lanes a row (elements
+// lane, lane + 16, ...), 16 rows a workgroup.
+__global__ __launch_bounds__(256) void attn_rowdot_kernel(AttnArgs a) {
+  const long long r = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int c = threadIdx.x & 15;
+  const long long rows = (long long)a.B * a.H * a.S;
+  float d = 0.f;
+  if (r < rows) {
+    const int pair = (int)(r / a.S), q = (int)(r % a.S), b = pair / a.H, hd = pair % a.H;
+    const long long row = (long long)b * a.S + q;
+    const float* g = a.dout + row * a.lddo + (long long)hd * a.dv;
+    const float* o = a.o + row * a.ldo + (long long)hd * a.dv;
+    for (int e = c; e < a.dv; e += 16) d = fmaf(g[e], o[e], d);
+  }
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) d += __shfl_xor(d, off, 64);
+  if (r < rows && c == 0) a.D[r] = d;
 }
 
 // dQ = dS . K from the dS rows attn_bwd_dkv_tiled_kernel<.., .., true> stored (a.ds), instead of
@@ -1875,11 +1869,16 @@ size_t attn_bwd_ds_bytes(const AttnDesc& d) {
 static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, hipStream_t s) {
   a.ds = ds;
   const double rows = (double)a.B * a.S * a.H, tiles = (a.S + kQTile - 1) / kQTile, pairs = kept_pairs(a);
+  {  // D = rowsum(dO * O)
+    ProfScope ps(s, "attn_rowdot_kernel", 2.0 * rows * a.dv, 4.0 * rows * (2.0 * a.dv + 1.0));
+    hipLaunchKernelGGL(attn_rowdot_kernel, dim3(ceil_div((size_t)rows, 16)), dim3(256), 0, s, a);
+    if (int rc = launch_status("attn_rowdot_kernel")) return rc;
+  }
   // dK / dV: s = q.k, dp = dO.v, dv += p dO, dk += ds q; k, v rows once, q / dO / O rows and lse
   // once per 128-key tile; dS written
   {
     const double bytes = 4.0 * rows * (2.0 * a.dk + 2.0 * a.dv) +
-                         4.0 * a.B * a.H * tiles * a.S * (a.dk + 2.0 * a.dv + 1.0) + 4.0 * pairs;
+                         4.0 * a.B * a.H * tiles * a.S * (a.dk + a.dv + 2.0) + 4.0 * pairs;
     dim3 grid((unsigned)((long long)a.B * a.H * (long long)tiles));
 #define TILED(DK, DV)                                                                              \
     if (dkm == DK && dvm == DV) {                                                                  \
@@ -1933,7 +1932,7 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
       hipLaunchKernelGGL(attn_bwd_s64_kernel<4>, dim3((unsigned)((long long)a.B * a.H)), dim3(256), 0, s, a);
     return launch_status("attn_bwd_s64_kernel");
   }
-  if (d.ds && attn_bwd_ds_supported(d) && (reinterpret_cast<uintptr_t>(d.ds) & 15) == 0)
+  if (d.ds && ws && attn_bwd_ds_supported(d) && (reinterpret_cast<uintptr_t>(d.ds) & 15) == 0)
     return attn_bwd_with_ds(a, dkm, dvm, d.ds, s);
   int rc = attn_bwd_dq(a, dkm, dvm, s);
   if (rc) return rc;

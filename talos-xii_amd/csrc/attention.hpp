@@ -44,8 +44,9 @@ struct AttnDesc {
   float* dq_last = nullptr;
   long long lddq_last = 0;
   // optional scratch of attn_bwd_ds_bytes(d) bytes (16-byte aligned): where attn_bwd_ds_supported
-  // holds, the backward stores dS ([batch * heads][seq][seq]) from its dK / dV kernel and forms dQ =
-  // dS . K from it instead of forming S, P and dP a second time
+  // holds and the workspace is given, the backward forms D = rowsum(dO * O) first, stores dS
+  // ([batch * heads][seq][seq]) from its dK / dV kernel and forms dQ = dS . K from it instead of
+  // forming S, P and dP a second time
   float* ds = nullptr;
 };
 
