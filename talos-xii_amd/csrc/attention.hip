@@ -35,6 +35,11 @@ struct AttnArgs {
   float scale;
   int causal;
   float* ds;  // the tiled backward's dS rows ([B*H][S][S]) when it forms dQ from them, else null
+  // with ds: dq / dk columns [dsplit, dk) of each head go to dq2 / dk2 (head width dk - dsplit) and
+  // columns [0, dsplit) to dq / dk_out at head width dsplit (null: one buffer, head width dk)
+  float *dq2, *dk2;
+  long long lddq2, lddk2;
+  int dsplit;
   const float* q;
   long long ldq;
   const float* k;
@@ -959,6 +964,15 @@ attn_bwd_dq_tiled_kernel(AttnArgs a) {
     }
 }
 
+// Column e of head hd of a dq / dk row: into dst (head width dk), or split at `split` between dst
+// (head width split) and dst2 (head width dk - split) when dst2 is given.
+__device__ __forceinline__ void store_head_col(float* dst, long long ld, float* dst2, long long ld2, int split,
+                                               long long row, int hd, int dk, int e, float g) {
+  if (dst2 == nullptr) dst[row * ld + (long long)hd * dk + e] = g;
+  else if (e < split) dst[row * ld + (long long)hd * split + e] = g;
+  else dst2[row * ld2 + (long long)hd * (dk - split) + (e - split)] = g;
+}
+
 // DS: every dS value of the wave's key blocks is also stored to a.ds (row of query q, column of
 // key), through a per-wave LDS tile so the global stores are 16-byte pieces of rows, for
 // attn_bwd_dq_ds_kernel; D comes from attn_rowdot_kernel.
@@ -991,7 +1005,12 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int kr = kb * 32 + acc_row(r, h);
       if (kr >= a.S) continue;
-      for (int e = l32; e < a.dk; e += 32) a.dk_out[(tok0 + kr) * a.lddk + hd * a.dk + e] = 0.f;
+      for (int e = l32; e < a.dk; e += 32) {
+        if constexpr (DS)
+          store_head_col(a.dk_out, a.lddk, a.dk2, a.lddk2, a.dsplit, tok0 + kr, hd, a.dk, e, 0.f);
+        else
+          a.dk_out[(tok0 + kr) * a.lddk + hd * a.dk + e] = 0.f;
+      }
       for (int e = l32; e < a.dv; e += 32) a.dv_out[(tok0 + kr) * a.lddv + hd * a.dv + e] = 0.f;
     }
     return;
@@ -1113,7 +1132,12 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
       const int kr = kb * 32 + acc_row(r, h);
       const int e = i * 32 + l32;
       const float g = rope_t(dk[i][r] * a.scale, e, kr, a, kr < a.S);
-      if (kr < a.S && e < a.dk) a.dk_out[(tok0 + kr) * a.lddk + hd * a.dk + e] = g;
+      if (kr < a.S && e < a.dk) {
+        if constexpr (DS)
+          store_head_col(a.dk_out, a.lddk, a.dk2, a.lddk2, a.dsplit, tok0 + kr, hd, a.dk, e, g);
+        else
+          a.dk_out[(tok0 + kr) * a.lddk + hd * a.dk + e] = g;
+      }
     }
 #pragma unroll
   for (int i = 0; i < VB; ++i)
@@ -1125,8 +1149,8 @@ attn_bwd_dkv_tiled_kernel(AttnArgs a) {
     }
 }
 
-// D[pair * S + q] = sum_e dO[q][e] O[q][e] over the head's dv columns: 16 lanes a row (elements
-// lane, lane + 16, ...), 16 rows a workgroup.
+// D[pair * S + q] = sum_e dO[q][e] O[q][e] over the head's dv columns: 16 lanes a row (float4s of
+// columns 4 lane + 64 j on 16-byte rows, else elements lane + 16 j), 16 rows a workgroup.
 __global__ __launch_bounds__(256) void attn_rowdot_kernel(AttnArgs a) {
   const long long r = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int c = threadIdx.x & 15;
@@ -1137,7 +1161,14 @@ __global__ __launch_bounds__(256) void attn_rowdot_kernel(AttnArgs a) {
     const long long row = (long long)b * a.S + q;
     const float* g = a.dout + row * a.lddo + (long long)hd * a.dv;
     const float* o = a.o + row * a.ldo + (long long)hd * a.dv;
-    for (int e = c; e < a.dv; e += 16) d = fmaf(g[e], o[e], d);
+    if (a.vec) {  // 16-byte rows: a float4 a lane, 64 columns a pass
+      for (int e = 4 * c; e < a.dv; e += 64) {
+        const float4 g4 = *reinterpret_cast<const float4*>(g + e), o4 = *reinterpret_cast<const float4*>(o + e);
+        d = fmaf(g4.x, o4.x, fmaf(g4.y, o4.y, fmaf(g4.z, o4.z, fmaf(g4.w, o4.w, d))));
+      }
+    } else {
+      for (int e = c; e < a.dv; e += 16) d = fmaf(g[e], o[e], d);
+    }
   }
 #pragma unroll
   for (int off = 1; off < 16; off <<= 1) d += __shfl_xor(d, off, 64);
@@ -1230,7 +1261,7 @@ attn_bwd_dq_ds_kernel(AttnArgs a) {
       const int qr = qb * 32 + acc_row(r, h);
       const int e = i * 32 + l32;
       const float g = rope_t(dq[i][r] * a.scale, e, qr, a, qr < a.S);
-      if (qr < a.S && e < a.dk) a.dq[(tok0 + qr) * a.lddq + hd * a.dk + e] = g;
+      if (qr < a.S && e < a.dk) store_head_col(a.dq, a.lddq, a.dq2, a.lddq2, a.dsplit, tok0 + qr, hd, a.dk, e, g);
     }
 }
 
@@ -1658,6 +1689,7 @@ static AttnArgs make_args(const AttnDesc& d, int dkm, int dvm) {
   a.rcos = d.rope_cos; a.rsin = d.rope_sin; a.rope_off = d.rope_off; a.rope_dim = d.rope_dim;
   a.lens = d.lens;
   a.q_last = d.q_last; a.ldq_last = d.ldq_last; a.dq_last = d.dq_last; a.lddq_last = d.lddq_last;
+  a.dq2 = d.dq2; a.lddq2 = d.lddq2; a.dk2 = d.dk2; a.lddk2 = d.lddk2; a.dsplit = d.dsplit;
   // row halves start at (token * ld + head * dim + half * dim/2): 16-byte aligned when all of
   // ld, dim and dim/2 are multiples of 4 and the bases are aligned
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -1862,6 +1894,10 @@ bool attn_bwd_ds_supported(const AttnDesc& d) {
   return (dkm == 32 && dvm == 32) || (dkm == 64 && dvm == 64) || (dkm == 96 && dvm == 64);
 }
 
+bool attn_bwd_takes_ds(const AttnDesc& d, const float* ws) {
+  return d.ds && ws && attn_bwd_ds_supported(d) && (reinterpret_cast<uintptr_t>(d.ds) & 15) == 0;
+}
+
 size_t attn_bwd_ds_bytes(const AttnDesc& d) {
   return attn_bwd_ds_supported(d) ? sizeof(float) * (size_t)d.batch * d.heads * d.seq * d.seq : 0;
 }
@@ -1932,8 +1968,11 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
       hipLaunchKernelGGL(attn_bwd_s64_kernel<4>, dim3((unsigned)((long long)a.B * a.H)), dim3(256), 0, s, a);
     return launch_status("attn_bwd_s64_kernel");
   }
-  if (d.ds && ws && attn_bwd_ds_supported(d) && (reinterpret_cast<uintptr_t>(d.ds) & 15) == 0)
-    return attn_bwd_with_ds(a, dkm, dvm, d.ds, s);
+  if (attn_bwd_takes_ds(d, ws)) return attn_bwd_with_ds(a, dkm, dvm, d.ds, s);
+  if (d.dq2 || d.dk2) {
+    set_error("attention backward: split dq / dk outputs need the dS path (attn_bwd_takes_ds)");
+    return TALOS_ERR_UNSUPPORTED;
+  }
   int rc = attn_bwd_dq(a, dkm, dvm, s);
   if (rc) return rc;
   return attn_bwd_dkv(a, dkm, dvm, s);

@@ -48,6 +48,14 @@ struct AttnDesc {
   // ([batch * heads][seq][seq]) from its dK / dV kernel and forms dQ = dS . K from it instead of
   // forming S, P and dP a second time
   float* ds = nullptr;
+  // on that path only (attn_bwd_takes_ds): columns [dsplit, dk) of each head's dq / dk go to dq2 /
+  // dk2 (head width dk - dsplit, row pitch lddq2 / lddk2) and columns [0, dsplit) to dq / dk_out
+  // at head width dsplit, instead of one [.., heads * dk] row each
+  float* dq2 = nullptr;
+  long long lddq2 = 0;
+  float* dk2 = nullptr;
+  long long lddk2 = 0;
+  int dsplit = 0;
 };
 
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s);
@@ -89,6 +97,7 @@ int attn_bwd_lastq_z_launch(const AttnDesc& d, const float* xn, long long ldx, c
                             hipStream_t s);
 size_t attn_bwd_workspace_bytes(const AttnDesc& d);
 bool attn_bwd_ds_supported(const AttnDesc& d);
+bool attn_bwd_takes_ds(const AttnDesc& d, const float* ws);
 size_t attn_bwd_ds_bytes(const AttnDesc& d);
 // Whether attn_bwd_launch reads its workspace: the split dQ / dK-dV kernels of seq > 32 keep
 // D = rowsum(dO * O) there; the single-block kernel of seq <= 32 forms D in registers.

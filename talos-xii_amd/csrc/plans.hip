@@ -693,9 +693,23 @@ static int mla_attn_backward(talos_plan_s* p, const MlaDims& D, const float* P, 
   a.dout = g_o;
   a.lddo = (long long)H * vd;
   int rc;
-  if ((rc = attn_bwd_launch(a, p->attn_ws, s))) return rc;
-  if ((rc = split_launch(MH, hd, r, m.dq, m.dqc, m.dqr, false, s))) return rc;
-  if ((rc = split_launch(MH, hd, r, m.dk, m.dkc, m.dkr, false, s))) return rc;
+  if (attn_bwd_takes_ds(a, p->attn_ws)) {
+    // the backward writes the content and rope parts of dq / dk to their own buffers
+    a.dq = m.dqc;
+    a.lddq = (long long)H * hd;
+    a.dq2 = m.dqr;
+    a.lddq2 = (long long)H * r;
+    a.dk_out = m.dkc;
+    a.lddk = (long long)H * hd;
+    a.dk2 = m.dkr;
+    a.lddk2 = (long long)H * r;
+    a.dsplit = hd;
+    if ((rc = attn_bwd_launch(a, p->attn_ws, s))) return rc;
+  } else {
+    if ((rc = attn_bwd_launch(a, p->attn_ws, s))) return rc;
+    if ((rc = split_launch(MH, hd, r, m.dq, m.dqc, m.dqr, false, s))) return rc;
+    if ((rc = split_launch(MH, hd, r, m.dk, m.dkc, m.dkr, false, s))) return rc;
+  }
   // q / rope-k projections of xn
   if ((rc = mm(p, s, 1, 0, d, H * hd, M, xn, d, m.dqc, H * hd, G + w.wq, H * hd))) return rc;
   if ((rc = mm(p, s, 1, 0, d, H * r, M, xn, d, m.dqr, H * r, G + w.wqr, H * r))) return rc;
