@@ -1296,9 +1296,16 @@ static int epi_flags(const GemmDesc& d) {
 // Whether a product runs on 64x64 tiles: fp32, fewer 128x128 tiles than CUs, and little work in
 // all (at most 2^30 multiply-adds): long-K weight gradients over all tokens keep the 128x128 tiles
 // and split K instead, which reads each operand half as often.
+static void (*pick_m64(bool tA, bool tB, int e))(GemmArgs);
+// The 64 x 64 tile kernel for products of fewer 128 x 128 tiles than CUs and at most 2^30 MACs;
+// not for one 128-wide column of tiles over at least 64 rows a CU where the 64 x 128 tiles are
+// instantiated (C5's M = 16384, N = 128 products: 1.669 -> 1.650 ms).
 static bool use_small(const GemmDesc& d, int num_cu) {
   const long long tiles = (long long)((d.M + BM - 1) / BM) * ((d.N + BN - 1) / BN) * d.batch;
   const double macs = (double)d.M * d.N * d.K * d.batch;
+  if (!d.bf16 && d.batch == 1 && d.N <= BN && d.M >= 64 * num_cu && !d.transA && d.ksplit <= 1 &&
+      pick_m64(false, d.transB != 0, epi_flags(d)) != nullptr)
+    return false;  // one 128-wide column of tiles over many rows: the 64-row tiles
   return !d.bf16 && tiles < num_cu && macs <= 1073741824.0;
 }
 
@@ -1401,7 +1408,13 @@ static GemmKernel pick_small(bool tA, bool tB, int e) {
 // with its residual, the attention output projection with the next norm).
 static GemmKernel pick_m64(bool tA, bool tB, int e) {
   if (tA) return nullptr;
-  if (tB) return e == E_NORMB ? &gemm_f32_m64_kernel<false, true, E_NORMB> : nullptr;
+  if (tB) {
+    if (e == E_NORMB) return &gemm_f32_m64_kernel<false, true, E_NORMB>;
+    if (e == 0) return &gemm_f32_m64_kernel<false, true, 0>;
+    if (e == E_BETA) return &gemm_f32_m64_kernel<false, true, E_BETA>;
+    return nullptr;
+  }
+  if (e == 0) return &gemm_f32_m64_kernel<false, false, 0>;
   if (e == (E_BIAS | E_RESID)) return &gemm_f32_m64_kernel<false, false, E_BIAS | E_RESID>;
   if (e == (E_RESID | E_NORM)) return &gemm_f32_m64_kernel<false, false, E_RESID | E_NORM>;
   if (e == (E_BIAS | E_RESID | E_NORM)) return &gemm_f32_m64_kernel<false, false, E_BIAS | E_RESID | E_NORM>;
