@@ -522,14 +522,14 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int BKB = 64;
 constexpr int PB = BKB + 8;
 
-// round-to-nearest-even fp32 -> bf16 of two values, packed low | high
+// round-to-nearest-even fp32 -> bf16 of two values, packed low | high: gfx950's
+// v_cvt_pk_bf16_f32, one instruction a pair (an integer rounding sequence of about six
+// instructions a pair made the staging, not the products, bound the bf16-in main loop)
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  auto r = [](float f) -> uint32_t {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // NaN stays a quiet NaN
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  };
-  return r(lo) | (r(hi) << 16);
+  const floatx2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 // Loads the [rows r0.., k0..k0+64) panel of an operand X and packs it to bf16 pairs.
