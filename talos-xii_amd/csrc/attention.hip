@@ -1266,6 +1266,438 @@ attn_bwd_dq_ds_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// bf16-in / fp32-accumulate variants of the tiled forward and the dS backward (plans whose
+// products take bf16 operands): the same workgroup layout, online softmax and dS round trip, with
+// every contraction on v_mfma_f32_32x32x16_bf16 (eight head or key values a lane per product
+// instead of one). Operands are rounded to bf16 (nearest even, v_cvt_pk_bf16_f32) as they are
+// staged; softmax, the scores, P, dS, lse, D and all accumulators stay fp32.
+//
+// Operand maps. A product's k-slots 8h + j (j < 8) of lane (l32, h) must name the same head
+// dimension or key in A and B:
+//  * row products (S^T = K Q^T, S = Q K^T, dP = dO V^T): slot 8h + j of product s is head column
+//    HALF*h + 8s + j, the lane's A fragment one 16-byte read of a row-major bf16 tile, its B
+//    fragment the lane's own row half converted once;
+//  * accumulator products (O += P V, dV += P^T dO, dK += dS^T Q): A is P / dS straight from the
+//    accumulator registers, so slot 8h + j of product t is block row acc_row(8t + j, h) =
+//    16t + 8(j / 4) + 4h + j % 4, and B reads those rows of one column from a transposed bf16 tile
+//    as two 8-byte pieces;
+//  * dQ += dS K: slot 8h + j of product t is key 16t + 8h + j, one 16-byte read each from the
+//    bf16 dS rows and the transposed K tile.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  const floatx2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+__device__ __forceinline__ bf16x8 frag8(const float* f) {
+  const uint4 u = {pk_bf16(f[0], f[1]), pk_bf16(f[2], f[3]), pk_bf16(f[4], f[5]), pk_bf16(f[6], f[7])};
+  return __builtin_bit_cast(bf16x8, u);
+}
+__device__ __forceinline__ bf16x8 lds_frag16(const uint16_t* p) {  // 16-byte aligned
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
+}
+// Rows 16t + 4h + 0..3 and 16t + 8 + 4h + 0..3 of column tile row `col` (pitch TP, 8-byte aligned).
+template <int TP>
+__device__ __forceinline__ bf16x8 lds_frag_acc(const uint16_t* tile, int col, int t, int h) {
+  const uint16_t* p = tile + col * TP + 16 * t + 4 * h;
+  const uint2 lo = *reinterpret_cast<const uint2*>(p), hi = *reinterpret_cast<const uint2*>(p + 8);
+  const uint4 u = {lo.x, lo.y, hi.x, hi.y};
+  return __builtin_bit_cast(bf16x8, u);
+}
+// Element group g of a [32, DM] block (as block_st4), times sc, into a row-major bf16 tile of
+// pitch RP ...
+template <int DM, int RP>
+__device__ __forceinline__ void block_st4_bf(uint16_t* tile, int g, float4 v, float sc = 1.f) {
+  const int idx = 4 * g;
+  *reinterpret_cast<uint2*>(tile + (idx / DM) * RP + idx % DM) =
+      make_uint2(pk_bf16(v.x * sc, v.y * sc), pk_bf16(v.z * sc, v.w * sc));
+}
+// ... and into a transposed one ([DM][TP]: element (row, col) at col * TP + row)
+template <int DM, int TP>
+__device__ __forceinline__ void block_st4_bft(uint16_t* tile, int g, float4 v) {
+  const int idx = 4 * g, row = idx / DM, col = idx % DM;
+  const uint32_t a = pk_bf16(v.x, v.y), b = pk_bf16(v.z, v.w);
+  tile[col * TP + row] = (uint16_t)a;
+  tile[(col + 1) * TP + row] = (uint16_t)(a >> 16);
+  tile[(col + 2) * TP + row] = (uint16_t)b;
+  tile[(col + 3) * TP + row] = (uint16_t)(b >> 16);
+}
+// Pitches (bf16 elements): row-major tiles DM + 8 (rows 16 bytes apart in bank offset, so the 16
+// lanes of a 16-byte read hit distinct banks); transposed tiles read 8 bytes a lane 36, read 16
+// bytes a lane 40.
+constexpr int kBfT8 = 36, kBfT16 = 40;
+
+template <int DKM, int DVM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_TILED_WAVES))) void
+attn_fwd_tiled_bf16_kernel(AttnArgs a) {
+  constexpr int KH = DKM / 2, OB = DVM / 32, KS = KH / 8;
+  constexpr int RK = DKM + 8;
+  constexpr int KL = DKM / 32, VL = DVM / 32;
+  __shared__ __align__(16) uint16_t Kb[32 * RK];
+  __shared__ __align__(16) uint16_t Vt[DVM * kBfT8];
+  __shared__ __align__(16) float Wr[4][32];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int t = threadIdx.x;
+  const int ntile = (a.S + kQTile - 1) / kQTile;
+  const int pair = blockIdx.x / ntile, tile = blockIdx.x % ntile;
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int Sk = key_len(a, b);
+  const int qb = tile * 4 + wv;
+  const int q = qb * 32 + l32;
+  const bool wave_on = qb * 32 < a.S;
+  const int q_hi = min(a.S, (tile + 1) * kQTile) - 1;
+  const int kb_end = Sk == 0 ? -1 : (a.causal ? min(q_hi, Sk - 1) : Sk - 1) >> 5;
+  const int wave_kb_end = a.causal ? min(kb_end, qb) : kb_end;
+
+  bf16x8 qf[KS];
+  {
+    float qv[KH];
+    load_half<KH, kFwdSel>(qv, a.q, a.ldq, tok0, q, a.S, hd * a.dk, a.dk, h, a.scale, a.vec);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = frag8(qv + 8 * s);
+  }
+  float4 rk[KL], rv[VL];
+  auto fetch = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < KL; ++i)
+      rk[i] = block_ld4<DKM>(a.k, a.ldk, tok0, kb * 32, a.S, hd * a.dk, a.dk, i * 256 + t, a.vec);
+#pragma unroll
+    for (int i = 0; i < VL; ++i)
+      rv[i] = block_ld4<DVM>(a.v, a.ldv, tok0, kb * 32, a.S, hd * a.dv, a.dv, i * 256 + t, a.vec);
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < KL; ++i) block_st4_bf<DKM, RK>(Kb, i * 256 + t, rk[i]);
+#pragma unroll
+    for (int i = 0; i < VL; ++i) block_st4_bft<DVM, kBfT8>(Vt, i * 256 + t, rv[i]);
+  };
+
+  float m = kNegInf, l = 0.f;
+  floatx16 oacc[OB];
+#pragma unroll
+  for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[ob][r] = 0.f;
+  if (kb_end >= 0) {
+    fetch(0);
+    stash();
+  }
+  __syncthreads();
+  for (int kb = 0; kb <= kb_end; ++kb) {
+    const bool more = kb < kb_end;
+    if (more) fetch(kb + 1);
+    if (wave_on && kb <= wave_kb_end) {
+      floatx16 acc;  // S^T: rows keys, columns queries
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_frag16(Kb + l32 * RK + KH * h + 8 * s), qf[s], acc, 0, 0, 0);
+      float sv[16], bm = kNegInf;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb * 32 + acc_row(r, h);
+        const bool ok = key < Sk && (!a.causal || key <= q);
+        sv[r] = ok ? acc[r] : kNegInf;
+        bm = fmaxf(bm, sv[r]);
+      }
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      const float mn = fmaxf(m, bm);
+      const float alpha = (m == kNegInf) ? 0.f : __expf(m - mn);
+      float P[16], bs = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        P[r] = (mn == kNegInf) ? 0.f : __expf(sv[r] - mn);
+        bs += P[r];
+      }
+      bs += __shfl_xor(bs, 32, 64);
+      l = l * alpha + bs;
+      m = mn;
+      float al[16];
+      bcast_rows(Wr[wv], alpha, l32, h, al);
+#pragma unroll
+      for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[ob][r] *= al[r];
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {  // O += P V over the block's keys, 16 a product
+        const bf16x8 pf = frag8(P + 8 * t2);
+#pragma unroll
+        for (int ob = 0; ob < OB; ++ob)
+          oacc[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, lds_frag_acc<kBfT8>(Vt, ob * 32 + l32, t2, h),
+                                                             oacc[ob], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+    if (more) {
+      stash();
+      __syncthreads();
+    }
+  }
+  if (!wave_on) return;
+  float il[16];
+  bcast_rows(Wr[wv], l > 0.f ? 1.f / l : 0.f, l32, h, il);
+#pragma unroll
+  for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qr = qb * 32 + acc_row(r, h);
+      const int e = ob * 32 + l32;
+      if (qr < a.S && e < a.dv) a.o[(tok0 + qr) * a.ldo + hd * a.dv + e] = oacc[ob][r] * il[r];
+    }
+  if (h == 0 && q < a.S) a.lse[(long long)pair * a.S + q] = (l > 0.f) ? m + logf(l) : kNegInf;
+}
+
+template <int DKM, int DVM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+attn_bwd_dkv_bf16_kernel(AttnArgs a) {
+  constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32, KS = KH / 8, VS = VH / 8;
+  constexpr int RK = DKM + 8, RV = DVM + 8;
+  constexpr int KL = DKM / 32, VL = DVM / 32;
+  __shared__ __align__(16) uint16_t Qb[32 * RK];
+  __shared__ __align__(16) uint16_t Qt[DKM * kBfT8];
+  __shared__ __align__(16) uint16_t Gb[32 * RV];
+  __shared__ __align__(16) uint16_t Gt[DVM * kBfT8];
+  __shared__ __align__(16) float LD[2][32];
+  __shared__ float Ts[4][32 * 33];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int t = threadIdx.x;
+  const int ntile = (a.S + kQTile - 1) / kQTile;
+  const int pair = blockIdx.x / ntile, tile = blockIdx.x % ntile;
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int kb = tile * 4 + wv;
+  const int key = kb * 32 + l32;
+  const bool wave_on = kb * 32 < a.S;
+  const bool kok = key < key_len(a, b);
+  const int nqb = (a.S + 31) >> 5;
+  const int qb_beg = a.causal ? tile * 4 : 0;
+  if (key_len(a, b) <= tile * kQTile) {
+    if (!wave_on) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = kb * 32 + acc_row(r, h);
+      if (kr >= a.S) continue;
+      for (int e = l32; e < a.dk; e += 32)
+        store_head_col(a.dk_out, a.lddk, a.dk2, a.lddk2, a.dsplit, tok0 + kr, hd, a.dk, e, 0.f);
+      for (int e = l32; e < a.dv; e += 32) a.dv_out[(tok0 + kr) * a.lddv + hd * a.dv + e] = 0.f;
+    }
+    return;
+  }
+
+  bf16x8 kf[KS], vf[VS];
+  {
+    float kv[KH], vv[VH];
+    // the scale goes on the staged Q rows (as the forward's on q), so S = bf16(scale q) bf16(k)^T
+    // is the forward's product and exp(S - lse) its P
+    load_half<KH, kBwdSel>(kv, a.k, a.ldk, tok0, key, a.S, hd * a.dk, a.dk, h, 1.f, a.vec);
+    load_half<VH, kBwdSel>(vv, a.v, a.ldv, tok0, key, a.S, hd * a.dv, a.dv, h, 1.f, a.vec);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) kf[s] = frag8(kv + 8 * s);
+#pragma unroll
+    for (int s = 0; s < VS; ++s) vf[s] = frag8(vv + 8 * s);
+  }
+  floatx16 dk[KB], dv[VB];
+#pragma unroll
+  for (int i = 0; i < KB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dk[i][r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < VB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dv[i][r] = 0.f;
+
+  float4 rq[KL], rg[VL];
+  float rl = 0.f;
+  auto fetch = [&](int qb) {
+#pragma unroll
+    for (int i = 0; i < KL; ++i)
+      rq[i] = block_ld4<DKM>(a.q, a.ldq, tok0, qb * 32, a.S, hd * a.dk, a.dk, i * 256 + t, a.vec);
+#pragma unroll
+    for (int i = 0; i < VL; ++i)
+      rg[i] = block_ld4<DVM>(a.dout, a.lddo, tok0, qb * 32, a.S, hd * a.dv, a.dv, i * 256 + t, a.vec);
+    if (t < 64) {
+      const int qr = qb * 32 + (t & 31);
+      const long long li = (long long)pair * a.S + (qr < a.S ? qr : 0);
+      rl = (t < 32 ? a.lse : a.D)[li];
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+      block_st4_bf<DKM, RK>(Qb, i * 256 + t, rq[i], a.scale);
+      block_st4_bft<DKM, kBfT8>(Qt, i * 256 + t, rq[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      block_st4_bf<DVM, RV>(Gb, i * 256 + t, rg[i]);
+      block_st4_bft<DVM, kBfT8>(Gt, i * 256 + t, rg[i]);
+    }
+    if (t < 64) LD[t >> 5][t & 31] = rl;
+  };
+  fetch(qb_beg);
+  stash();
+  __syncthreads();
+  for (int qb = qb_beg; qb < nqb; ++qb) {
+    const bool more = qb + 1 < nqb;
+    if (more) fetch(qb + 1);
+    if (wave_on && (!a.causal || qb >= kb)) {
+      floatx16 sacc, pacc;  // rows queries, columns keys
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_frag16(Qb + l32 * RK + KH * h + 8 * s), kf[s], sacc, 0, 0, 0);
+#pragma unroll
+      for (int s = 0; s < VS; ++s)
+        pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_frag16(Gb + l32 * RV + VH * h + 8 * s), vf[s], pacc, 0, 0, 0);
+      float P[16], dS[16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 l4 = *reinterpret_cast<const float4*>(&LD[0][8 * j + 4 * h]);
+        const float4 d4 = *reinterpret_cast<const float4*>(&LD[1][8 * j + 4 * h]);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int r = 4 * j + u;
+          const int qr = qb * 32 + acc_row(r, h);
+          const bool ok = kok && qr < a.S && (!a.causal || key <= qr);
+          const float p = __expf(ok ? sacc[r] - lv[u] : kNegInf);
+          P[r] = p;
+          dS[r] = p * (pacc[r] - dv4[u]);
+          Ts[wv][acc_row(r, h) * 33 + l32] = dS[r];
+        }
+      }
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {  // dV += P^T dO, dK += dS^T Q over the block's queries
+        const bf16x8 pf = frag8(P + 8 * t2), sf = frag8(dS + 8 * t2);
+#pragma unroll
+        for (int i = 0; i < VB; ++i)
+          dv[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, lds_frag_acc<kBfT8>(Gt, i * 32 + l32, t2, h), dv[i], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < KB; ++i)
+          dk[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sf, lds_frag_acc<kBfT8>(Qt, i * 32 + l32, t2, h), dk[i], 0, 0, 0);
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {  // the block's dS tile [32 queries][32 keys] to a.ds
+        const int g = i * 64 + lane, row = g >> 3, c = 4 * (g & 7);
+        const int qr = qb * 32 + row, k0 = kb * 32 + c;
+        const float* tr = Ts[wv] + row * 33 + c;
+        if (qr < a.S && k0 < a.S)
+          *reinterpret_cast<float4*>(a.ds + ((long long)pair * a.S + qr) * a.S + k0) =
+              make_float4(tr[0], tr[1], tr[2], tr[3]);
+      }
+    }
+    __syncthreads();
+    if (more) {
+      stash();
+      __syncthreads();
+    }
+  }
+  if (!wave_on) return;
+#pragma unroll
+  for (int i = 0; i < KB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = kb * 32 + acc_row(r, h);
+      const int e = i * 32 + l32;
+      const float g = rope_t(dk[i][r] * a.scale, e, kr, a, kr < a.S);
+      if (kr < a.S && e < a.dk) store_head_col(a.dk_out, a.lddk, a.dk2, a.lddk2, a.dsplit, tok0 + kr, hd, a.dk, e, g);
+    }
+#pragma unroll
+  for (int i = 0; i < VB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = kb * 32 + acc_row(r, h);
+      const int e = i * 32 + l32;
+      if (kr < a.S && e < a.dv) a.dv_out[(tok0 + kr) * a.lddv + hd * a.dv + e] = dv[i][r];
+    }
+}
+
+template <int DKM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_TILED_WAVES))) void
+attn_bwd_dq_ds_bf16_kernel(AttnArgs a) {
+  constexpr int QB = DKM / 32, KL = DKM / 32;
+  __shared__ __align__(16) uint16_t Kt[DKM * kBfT16];
+  __shared__ __align__(16) uint16_t Db[kQTile * kBfT16];  // dS rows of the tile's queries, bf16
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
+  const int t = threadIdx.x;
+  const int ntile = (a.S + kQTile - 1) / kQTile;
+  const int pair = blockIdx.x / ntile, tile = blockIdx.x % ntile;
+  const int b = pair / a.H, hd = pair % a.H;
+  const long long tok0 = (long long)b * a.S;
+  const int Sk = key_len(a, b);
+  const int qb = tile * 4 + wv;
+  const bool wave_on = qb * 32 < a.S;
+  const int q_hi = min(a.S, (tile + 1) * kQTile) - 1;
+  const int kb_end = Sk == 0 ? -1 : (a.causal ? min(q_hi, Sk - 1) : Sk - 1) >> 5;
+  const int wave_kb_end = a.causal ? min(kb_end, qb) : kb_end;
+  const float* dsp = a.ds + (long long)pair * a.S * a.S;
+  float4 rk[KL], rd[4];
+  auto fetch = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < KL; ++i)
+      rk[i] = block_ld4<DKM>(a.k, a.ldk, tok0, kb * 32, a.S, hd * a.dk, a.dk, i * 256 + t, a.vec);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int g = i * 256 + t, qr = tile * kQTile + (g >> 3), k = kb * 32 + 4 * (g & 7);
+      rd[i] = qr < a.S && k < a.S ? *reinterpret_cast<const float4*>(dsp + (long long)qr * a.S + k)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < KL; ++i) block_st4_bft<DKM, kBfT16>(Kt, i * 256 + t, rk[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) block_st4_bf<32, kBfT16>(Db, i * 256 + t, rd[i]);
+  };
+  floatx16 dq[QB];
+#pragma unroll
+  for (int i = 0; i < QB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
+  if (kb_end >= 0) {
+    fetch(0);
+    stash();
+  }
+  __syncthreads();
+  for (int kb = 0; kb <= kb_end; ++kb) {
+    const bool more = kb < kb_end;
+    if (more) fetch(kb + 1);
+    if (wave_on && kb <= wave_kb_end) {
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {  // dQ += dS K over keys 16 t2 + 8 h + 0..7
+        const bf16x8 df = lds_frag16(Db + (wv * 32 + l32) * kBfT16 + 16 * t2 + 8 * h);
+#pragma unroll
+        for (int i = 0; i < QB; ++i)
+          dq[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(df, lds_frag16(Kt + (i * 32 + l32) * kBfT16 + 16 * t2 + 8 * h),
+                                                          dq[i], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+    if (more) {
+      stash();
+      __syncthreads();
+    }
+  }
+  if (!wave_on) return;
+#pragma unroll
+  for (int i = 0; i < QB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qr = qb * 32 + acc_row(r, h);
+      const int e = i * 32 + l32;
+      const float g = rope_t(dq[i][r] * a.scale, e, qr, a, qr < a.S);
+      if (qr < a.S && e < a.dk) store_head_col(a.dq, a.lddq, a.dq2, a.lddq2, a.dsplit, tok0 + qr, hd, a.dk, e, g);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Single-block backward (seq <= 32): one wave per (batch, head) pair computes dQ, dK and dV from
 // one read of q, k, v, o and dO (D = dO . O is formed in the wave). S layout (lane <-> key,
 // register r <-> query acc_row(r, h)); dS is transposed through the wave's LDS slice for dQ.
@@ -1744,6 +2176,18 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
     const double tiles = (a.S + kQTile - 1) / kQTile;
     const double tbytes = 4.0 * rows * (a.dk + 2.0 * a.dv + 1.0) + 4.0 * a.B * a.H * tiles * a.S * (a.dk + a.dv);
     grid = dim3((unsigned)((long long)a.B * a.H * (long long)tiles));
+    // bf16 only where the backward is the bf16 dS path, so both form P from the same products
+    const bool bf16 = d.bf16 && d.ds && attn_bwd_ds_supported(d);
+#define TILED_BF(DK, DV)                                                                    \
+    if (dkm == DK && dvm == DV && bf16) {                                                   \
+      ProfScope ps(s, "attn_fwd_tiled_bf16_kernel<" #DK ", " #DV ">", flops, tbytes);       \
+      hipLaunchKernelGGL((attn_fwd_tiled_bf16_kernel<DK, DV>), grid, dim3(256), 0, s, a);   \
+      return launch_status("attn_fwd_tiled_bf16_kernel");                                   \
+    }
+    TILED_BF(32, 32)
+    TILED_BF(64, 64)
+    TILED_BF(96, 64)
+#undef TILED_BF
 #define TILED(DK, DV)                                                                       \
     if (dkm == DK && dvm == DV) {                                                           \
       ProfScope ps(s, "attn_fwd_tiled_kernel<" #DK ", " #DV ">", flops, tbytes);            \
@@ -1902,7 +2346,7 @@ size_t attn_bwd_ds_bytes(const AttnDesc& d) {
   return attn_bwd_ds_supported(d) ? sizeof(float) * (size_t)d.batch * d.heads * d.seq * d.seq : 0;
 }
 
-static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, hipStream_t s) {
+static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, bool bf16, hipStream_t s) {
   a.ds = ds;
   const double rows = (double)a.B * a.S * a.H, tiles = (a.S + kQTile - 1) / kQTile, pairs = kept_pairs(a);
   {  // D = rowsum(dO * O)
@@ -1917,7 +2361,11 @@ static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, hipStream_t
                          4.0 * a.B * a.H * tiles * a.S * (a.dk + a.dv + 2.0) + 4.0 * pairs;
     dim3 grid((unsigned)((long long)a.B * a.H * (long long)tiles));
 #define TILED(DK, DV)                                                                              \
-    if (dkm == DK && dvm == DV) {                                                                  \
+    if (dkm == DK && dvm == DV && bf16) {                                                          \
+      ProfScope ps(s, "attn_bwd_dkv_bf16_kernel<" #DK ", " #DV ">", pairs * (4.0 * a.dk + 4.0 * a.dv), bytes); \
+      hipLaunchKernelGGL((attn_bwd_dkv_bf16_kernel<DK, DV>), grid, dim3(256), 0, s, a);           \
+      if (int rc = launch_status("attn_bwd_dkv_bf16_kernel")) return rc;                           \
+    } else if (dkm == DK && dvm == DV) {                                                           \
       ProfScope ps(s, "attn_bwd_dkv_tiled_kernel<" #DK ", " #DV ", true>", pairs * (4.0 * a.dk + 4.0 * a.dv), bytes); \
       hipLaunchKernelGGL((attn_bwd_dkv_tiled_kernel<DK, DV, true>), grid, dim3(256), 0, s, a);    \
       if (int rc = launch_status("attn_bwd_dkv_tiled_kernel")) return rc;                          \
@@ -1931,6 +2379,11 @@ static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, hipStream_t
   const double bytes = 4.0 * pairs + 4.0 * a.B * a.H * tiles * a.S * a.dk + 4.0 * rows * a.dk;
   dim3 grid((unsigned)((long long)a.B * a.H * (long long)tiles));
 #define TILED(DK)                                                                                  \
+  if (dkm == DK && bf16) {                                                                         \
+    ProfScope ps(s, "attn_bwd_dq_ds_bf16_kernel<" #DK ">", pairs * 2.0 * a.dk, bytes);            \
+    hipLaunchKernelGGL((attn_bwd_dq_ds_bf16_kernel<DK>), grid, dim3(256), 0, s, a);               \
+    return launch_status("attn_bwd_dq_ds_bf16_kernel");                                            \
+  }                                                                                                \
   if (dkm == DK) {                                                                                 \
     ProfScope ps(s, "attn_bwd_dq_ds_kernel<" #DK ">", pairs * 2.0 * a.dk, bytes);                 \
     hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<DK>), grid, dim3(256), 0, s, a);                    \
@@ -1968,7 +2421,7 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
       hipLaunchKernelGGL(attn_bwd_s64_kernel<4>, dim3((unsigned)((long long)a.B * a.H)), dim3(256), 0, s, a);
     return launch_status("attn_bwd_s64_kernel");
   }
-  if (attn_bwd_takes_ds(d, ws)) return attn_bwd_with_ds(a, dkm, dvm, d.ds, s);
+  if (attn_bwd_takes_ds(d, ws)) return attn_bwd_with_ds(a, dkm, dvm, d.ds, d.bf16 != 0, s);
   if (d.dq2 || d.dk2) {
     set_error("attention backward: split dq / dk outputs need the dS path (attn_bwd_takes_ds)");
     return TALOS_ERR_UNSUPPORTED;

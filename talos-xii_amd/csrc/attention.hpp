@@ -56,6 +56,11 @@ struct AttnDesc {
   float* dk2 = nullptr;
   long long lddk2 = 0;
   int dsplit = 0;
+  // 1: where the backward takes the dS path (ds given, attn_bwd_ds_supported), the tiled forward
+  // and that backward take bf16 operands in their QK^T, PV and gradient contractions (rounded to
+  // nearest even as staged, fp32 accumulation; softmax, lse, D and dS in fp32), for plans whose
+  // products are bf16-in. Other shapes run in fp32, forward and backward alike.
+  int bf16 = 0;
 };
 
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s);

@@ -640,6 +640,7 @@ static AttnDesc mla_attn_desc(talos_plan_s* p, const MlaDims& D, const talos_pla
   a.rope_dim = D.r;
   a.lens = p->lens;
   a.ds = p->ms.ds;
+  a.bf16 = p->bf16 ? 1 : 0;
   return a;
 }
 
