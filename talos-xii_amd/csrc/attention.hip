@@ -1270,7 +1270,8 @@ attn_bwd_dq_ds_kernel(AttnArgs a) {
 // products take bf16 operands): the same workgroup layout, online softmax and dS round trip, with
 // every contraction on v_mfma_f32_32x32x16_bf16 (eight head or key values a lane per product
 // instead of one). Operands are rounded to bf16 (nearest even, v_cvt_pk_bf16_f32) as they are
-// staged; softmax, the scores, P, dS, lse, D and all accumulators stay fp32.
+// staged; softmax, the scores, P, lse, D and all accumulators stay fp32. The dS rows go out as
+// bf16 (the dQ product rounds them to bf16 as its operand either way), half the fp32 bytes.
 //
 // Operand maps. A product's k-slots 8h + j (j < 8) of lane (l32, h) must name the same head
 // dimension or key in A and B:
@@ -1584,13 +1585,13 @@ attn_bwd_dkv_bf16_kernel(AttnArgs a) {
       }
       wave_lds_sync();
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {  // the block's dS tile [32 queries][32 keys] to a.ds
+      for (int i = 0; i < 4; ++i) {  // the block's dS tile [32 queries][32 keys] to a.ds as bf16
         const int g = i * 64 + lane, row = g >> 3, c = 4 * (g & 7);
         const int qr = qb * 32 + row, k0 = kb * 32 + c;
         const float* tr = Ts[wv] + row * 33 + c;
         if (qr < a.S && k0 < a.S)
-          *reinterpret_cast<float4*>(a.ds + ((long long)pair * a.S + qr) * a.S + k0) =
-              make_float4(tr[0], tr[1], tr[2], tr[3]);
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.ds) + ((long long)pair * a.S + qr) * a.S + k0) =
+              make_uint2(pk_bf16(tr[0], tr[1]), pk_bf16(tr[2], tr[3]));
       }
     }
     __syncthreads();
@@ -1637,24 +1638,27 @@ attn_bwd_dq_ds_bf16_kernel(AttnArgs a) {
   const int q_hi = min(a.S, (tile + 1) * kQTile) - 1;
   const int kb_end = Sk == 0 ? -1 : (a.causal ? min(q_hi, Sk - 1) : Sk - 1) >> 5;
   const int wave_kb_end = a.causal ? min(kb_end, qb) : kb_end;
-  const float* dsp = a.ds + (long long)pair * a.S * a.S;
-  float4 rk[KL], rd[4];
+  const uint16_t* dsp = reinterpret_cast<const uint16_t*>(a.ds) + (long long)pair * a.S * a.S;  // bf16 rows
+  float4 rk[KL];
+  uint2 rd[4];
   auto fetch = [&](int kb) {
 #pragma unroll
     for (int i = 0; i < KL; ++i)
       rk[i] = block_ld4<DKM>(a.k, a.ldk, tok0, kb * 32, a.S, hd * a.dk, a.dk, i * 256 + t, a.vec);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i) {  // query row g / 8 of the tile, keys 4 (g % 8) .. + 3
       const int g = i * 256 + t, qr = tile * kQTile + (g >> 3), k = kb * 32 + 4 * (g & 7);
-      rd[i] = qr < a.S && k < a.S ? *reinterpret_cast<const float4*>(dsp + (long long)qr * a.S + k)
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+      rd[i] = qr < a.S && k < a.S ? *reinterpret_cast<const uint2*>(dsp + (long long)qr * a.S + k) : make_uint2(0u, 0u);
     }
   };
   auto stash = [&]() {
 #pragma unroll
     for (int i = 0; i < KL; ++i) block_st4_bft<DKM, kBfT16>(Kt, i * 256 + t, rk[i]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) block_st4_bf<32, kBfT16>(Db, i * 256 + t, rd[i]);
+    for (int i = 0; i < 4; ++i) {
+      const int g = i * 256 + t;
+      *reinterpret_cast<uint2*>(Db + (g >> 3) * kBfT16 + 4 * (g & 7)) = rd[i];
+    }
   };
   floatx16 dq[QB];
 #pragma unroll
@@ -2358,7 +2362,7 @@ static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, bool bf16, 
   // once per 128-key tile; dS written
   {
     const double bytes = 4.0 * rows * (2.0 * a.dk + 2.0 * a.dv) +
-                         4.0 * a.B * a.H * tiles * a.S * (a.dk + a.dv + 2.0) + 4.0 * pairs;
+                         4.0 * a.B * a.H * tiles * a.S * (a.dk + a.dv + 2.0) + (bf16 ? 2.0 : 4.0) * pairs;
     dim3 grid((unsigned)((long long)a.B * a.H * (long long)tiles));
 #define TILED(DK, DV)                                                                              \
     if (dkm == DK && dvm == DV && bf16) {                                                          \
@@ -2376,7 +2380,7 @@ static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, bool bf16, 
 #undef TILED
   }
   // dQ = dS . K: dS read, K rows once per 128-query tile, dq written
-  const double bytes = 4.0 * pairs + 4.0 * a.B * a.H * tiles * a.S * a.dk + 4.0 * rows * a.dk;
+  const double bytes = (bf16 ? 2.0 : 4.0) * pairs + 4.0 * a.B * a.H * tiles * a.S * a.dk + 4.0 * rows * a.dk;
   dim3 grid((unsigned)((long long)a.B * a.H * (long long)tiles));
 #define TILED(DK)                                                                                  \
   if (dkm == DK && bf16) {                                                                         \

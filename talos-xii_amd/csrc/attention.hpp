@@ -58,8 +58,9 @@ struct AttnDesc {
   int dsplit = 0;
   // 1: where the backward takes the dS path (ds given, attn_bwd_ds_supported), the tiled forward
   // and that backward take bf16 operands in their QK^T, PV and gradient contractions (rounded to
-  // nearest even as staged, fp32 accumulation; softmax, lse, D and dS in fp32), for plans whose
-  // products are bf16-in. Other shapes run in fp32, forward and backward alike.
+  // nearest even as staged, fp32 accumulation; softmax, lse and D in fp32, dS formed in fp32 and
+  // kept in ds as bf16 rows), for plans whose products are bf16-in. Other shapes run in fp32,
+  // forward and backward alike.
   int bf16 = 0;
 };
 
