@@ -534,7 +534,8 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 
 // Loads the [rows r0.., k0..k0+64) panel of an operand X and packs it to bf16 pairs.
 // KC = true: X[r][k] with k contiguous; thread t takes k = 4*(t%16) of rows t/16 + 16i.
-// KC = false: X[k][r] with r contiguous; thread t takes r = 4*(t%32), k pairs 2*(t/32) + 16i.
+// KC = false: X[k][r] with r contiguous; thread t takes r = 4*(t%32) .. + 3 and k = 8*(t/32) .. + 7
+// (eight float4 rows), packed to four rows of eight k values.
 template <bool KC>
 __device__ __forceinline__ void load_bf(const float* __restrict__ X, long long ld, int r0, int rlim, int k0, int kend,
                                         bool fast, bool vec, uint32_t (&o)[16]) {
@@ -557,28 +558,24 @@ __device__ __forceinline__ void load_bf(const float* __restrict__ X, long long l
       o[2 * i + 1] = pack_bf16(v[2], v[3]);
     }
   } else {
-    const int r = r0 + 4 * (t & 31);
+    const int r = r0 + 4 * (t & 31), kb = k0 + 8 * (t >> 5);
+    float v[8][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int k = k0 + 2 * (t >> 5) + 16 * i;
-      float v0[4], v1[4];
-      const float* s0 = X + (long long)k * ld + r;
-      const float* s1 = s0 + ld;
-      if (fast || (vec && k + 1 < kend && r + 3 < rlim)) {
-        const float4 f0 = *reinterpret_cast<const float4*>(s0);
-        const float4 f1 = *reinterpret_cast<const float4*>(s1);
-        v0[0] = f0.x; v0[1] = f0.y; v0[2] = f0.z; v0[3] = f0.w;
-        v1[0] = f1.x; v1[1] = f1.y; v1[2] = f1.z; v1[3] = f1.w;
+    for (int u = 0; u < 8; ++u) {
+      const int k = kb + u;
+      const float* src = X + (long long)k * ld + r;
+      if (fast || (vec && k < kend && r + 3 < rlim)) {
+        const float4 f = *reinterpret_cast<const float4*>(src);
+        v[u][0] = f.x; v[u][1] = f.y; v[u][2] = f.z; v[u][3] = f.w;
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v0[j] = (k < kend && r + j < rlim) ? s0[j] : 0.f;
-          v1[j] = (k + 1 < kend && r + j < rlim) ? s1[j] : 0.f;
-        }
+        for (int j = 0; j < 4; ++j) v[u][j] = (k < kend && r + j < rlim) ? src[j] : 0.f;
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) o[4 * i + j] = pack_bf16(v0[j], v1[j]);
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)  // row r + j: k pairs (kb + 2u, kb + 2u + 1)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) o[4 * j + u] = pack_bf16(v[2 * u][j], v[2 * u + 1][j]);
   }
 }
 
@@ -591,14 +588,12 @@ __device__ __forceinline__ void store_bf(uint16_t* S, const uint32_t (&o)[16]) {
       const int r = (t >> 4) + 16 * i;
       *reinterpret_cast<uint2*>(S + r * PB + 4 * (t & 15)) = make_uint2(o[2 * i], o[2 * i + 1]);
     }
-  } else {
+  } else {  // four 16-byte row pieces
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 4 * (t & 31) + j, k = 2 * (t >> 5) + 16 * i;
-        *reinterpret_cast<uint32_t*>(S + r * PB + k) = o[4 * i + j];
-      }
+    for (int j = 0; j < 4; ++j) {
+      const int r = 4 * (t & 31) + j, k = 8 * (t >> 5);
+      *reinterpret_cast<uint4*>(S + r * PB + k) = make_uint4(o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]);
+    }
   }
 }
 
