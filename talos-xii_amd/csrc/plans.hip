@@ -644,6 +644,24 @@ static AttnDesc mla_attn_desc(talos_plan_s* p, const MlaDims& D, const talos_pla
   return a;
 }
 
+// bf16 plans on the dS path: points a's q / k at the split content / rope halves of L.m.q / L.m.k
+// ([M][H*hd] then [M][H*r]) and returns true; else leaves a alone (whole heads of width hd + r).
+// The fp32 kernels' split twins spill at C5's head dims (27-48 VGPRs) and measured slower than the
+// two concatenation copies they replace, so fp32 plans keep the copies.
+static bool mla_split_qk(talos_plan_s* p, AttnDesc& a) {
+  if (!p->bf16 || !attn_bwd_takes_ds(a, p->attn_ws)) return false;
+  const int hd = a.rope_off, r = a.rope_dim;
+  const long long MH = (long long)a.batch * a.seq * a.heads;
+  a.ldq = (long long)a.heads * hd;
+  a.q2 = a.q + MH * hd;
+  a.ldq2 = (long long)a.heads * r;
+  a.ldk = (long long)a.heads * hd;
+  a.k2 = a.k + MH * hd;
+  a.ldk2 = (long long)a.heads * r;
+  a.dsplit = hd;
+  return true;
+}
+
 // xn -> L.o (and L.lse): the projections, RoPE on q_r / k_r, per-head concatenation, attention.
 static int mla_attn_forward(talos_plan_s* p, const MlaDims& D, const float* P, const MlaW& w, const float* xn,
                             talos_plan_s::Layer& L, hipStream_t s) {
@@ -671,15 +689,26 @@ static int mla_attn_forward(talos_plan_s* p, const MlaDims& D, const float* P, c
     return gemm_launch(g, s);
   };
   int rc;
+  AttnDesc a = mla_attn_desc(p, D, L);
+  // on the dS path the attention reads the content and rope parts of q / k where the projections
+  // write them, the two halves of the layer's L.m.q / L.m.k ([M][H*hd] then [M][H*r]); otherwise
+  // the parts are concatenated per head into L.m.q / L.m.k
+  const bool split = mla_split_qk(p, a);
+  float* qc = split ? L.m.q : m.qc;
+  float* qr = split ? L.m.q + MH * hd : m.qr;
+  float* kc = split ? L.m.k : m.kc;
+  float* kr = split ? L.m.k + MH * hd : m.kr;
   if ((rc = mm(p, s, 0, 0, M, Lt, d, xn, d, P + w.wdkv, Lt, L.m.ckv, Lt))) return rc;
-  if ((rc = mm(p, s, 0, 0, M, H * hd, Lt, L.m.ckv, Lt, P + w.wuk, H * hd, m.kc, H * hd))) return rc;
+  if ((rc = mm(p, s, 0, 0, M, H * hd, Lt, L.m.ckv, Lt, P + w.wuk, H * hd, kc, H * hd))) return rc;
   if ((rc = mm(p, s, 0, 0, M, H * vd, Lt, L.m.ckv, Lt, P + w.wuv, H * vd, L.m.v, H * vd))) return rc;
-  if ((rc = mm(p, s, 0, 0, M, H * hd, d, xn, d, P + w.wq, H * hd, m.qc, H * hd))) return rc;
-  if ((rc = rope_gemm(P + w.wqr, m.qr))) return rc;
-  if ((rc = rope_gemm(P + w.wkr, m.kr))) return rc;
-  if ((rc = concat_launch(MH, hd, r, m.qc, m.qr, L.m.q, s))) return rc;
-  if ((rc = concat_launch(MH, hd, r, m.kc, m.kr, L.m.k, s))) return rc;
-  return attn_fwd_launch(mla_attn_desc(p, D, L), s);
+  if ((rc = mm(p, s, 0, 0, M, H * hd, d, xn, d, P + w.wq, H * hd, qc, H * hd))) return rc;
+  if ((rc = rope_gemm(P + w.wqr, qr))) return rc;
+  if ((rc = rope_gemm(P + w.wkr, kr))) return rc;
+  if (!split) {
+    if ((rc = concat_launch(MH, hd, r, m.qc, m.qr, L.m.q, s))) return rc;
+    if ((rc = concat_launch(MH, hd, r, m.kc, m.kr, L.m.k, s))) return rc;
+  }
+  return attn_fwd_launch(a, s);
 }
 
 // From g_o = dL/d(L.o) [tokens, H*vd]: the gradients of the six projection weights (written to
@@ -695,7 +724,9 @@ static int mla_attn_backward(talos_plan_s* p, const MlaDims& D, const float* P, 
   a.lddo = (long long)H * vd;
   int rc;
   if (attn_bwd_takes_ds(a, p->attn_ws)) {
-    // the backward writes the content and rope parts of dq / dk to their own buffers
+    // the content and rope parts of dq / dk to their own buffers (and, for bf16 plans, the
+    // forward's split q / k halves in)
+    mla_split_qk(p, a);
     a.dq = m.dqc;
     a.lddq = (long long)H * hd;
     a.dq2 = m.dqr;
