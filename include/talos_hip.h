@@ -342,7 +342,10 @@ size_t talos_ppo_param_count(const talos_ppo_cfg* cfg);
  *   rope_dim) (transformer.rs:542), RoPE position = sequence index. No biases (transformer.rs:441-460).
  * Parameter layout: g[d] | W_dkv[d,L] | W_uk[L,H*hd] | W_uv[L,H*vd] | W_q[d,H*hd] | W_kr[d,H*r] |
  *   W_qr[d,H*r] | W_o[H*vd,d]. */
-enum talos_precision { TALOS_PREC_FP32 = 0, TALOS_PREC_BF16 = 1 /* bf16-in / fp32-accumulate GEMMs */ };
+/* TALOS_PREC_BF16: the projections' GEMMs, and the attention's QK^T, PV and gradient contractions
+ * where seq > 64, seq % 4 == 0 and the head dims fit (32, 32), (64, 64) or (96, 64) (fused plans), take bf16
+ * operands (nearest even) with fp32 accumulation; softmax, lse and the norm stay fp32. */
+enum talos_precision { TALOS_PREC_FP32 = 0, TALOS_PREC_BF16 = 1 /* bf16-in / fp32-accumulate */ };
 typedef struct talos_mla_cfg {
   int batch;
   int seq;
