@@ -1399,9 +1399,21 @@ __device__ __forceinline__ void block_st4_bft(uint16_t* tile, int g, float4 v) {
 // lanes of a 16-byte read hit distinct banks); transposed tiles read 8 bytes a lane 36, read 16
 // bytes a lane 40.
 constexpr int kBfT8 = 36, kBfT16 = 40;
+// waves per SIMD the bf16 kernels are compiled for (forward, dK / dV, dQ); C5: four waves for dQ
+// (8 VGPRs spill in its split twin) 0.883-0.892 -> 0.878-0.881 ms, two for the forward no better,
+// three for dK / dV or four for the forward spill 43-376 VGPRs
+#ifndef TALOS_ATTN_BF_FWD_WAVES
+#define TALOS_ATTN_BF_FWD_WAVES 3
+#endif
+#ifndef TALOS_ATTN_BF_DKV_WAVES
+#define TALOS_ATTN_BF_DKV_WAVES 2
+#endif
+#ifndef TALOS_ATTN_BF_DQ_WAVES
+#define TALOS_ATTN_BF_DQ_WAVES 4
+#endif
 
 template <int DKM, int DVM, bool SPLIT = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_TILED_WAVES))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BF_FWD_WAVES))) void
 attn_fwd_tiled_bf16_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, OB = DVM / 32, KS = KH / 8;
   constexpr int RK = DKM + 8;
@@ -1523,7 +1535,7 @@ attn_fwd_tiled_bf16_kernel(AttnArgs a) {
 }
 
 template <int DKM, int DVM, bool SPLIT = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BF_DKV_WAVES))) void
 attn_bwd_dkv_bf16_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32, KS = KH / 8, VS = VH / 8;
   constexpr int RK = DKM + 8, RV = DVM + 8;
@@ -1690,7 +1702,7 @@ attn_bwd_dkv_bf16_kernel(AttnArgs a) {
 }
 
 template <int DKM, bool SPLIT = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_TILED_WAVES))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BF_DQ_WAVES))) void
 attn_bwd_dq_ds_bf16_kernel(AttnArgs a) {
   constexpr int QB = DKM / 32, KL = DKM / 32;
   __shared__ __align__(16) uint16_t Kt[DKM * kBfT16];
