@@ -146,6 +146,11 @@ def threads():
     return lib().orc_threads()
 
 
+def track_mag(on):
+    """Leaves created while on carry gradient magnitude sums (T.mag)."""
+    lib().orc_set_track_mag(int(bool(on)))
+
+
 def set_threads(n):
     lib().orc_set_threads(int(n))
 
@@ -189,6 +194,13 @@ class T:
     def grad(self):
         out = np.zeros(lib().orc_tensor_numel(self.h))
         lib().orc_tensor_grad(self.h, _p(out))
+        return out.reshape(self.shape)
+
+    @property
+    def mag(self):
+        """Gradient magnitude sums of a leaf created under track_mag(True) (zeros otherwise)."""
+        out = np.zeros(lib().orc_tensor_numel(self.h))
+        lib().orc_tensor_mag(self.h, _p(out))
         return out.reshape(self.shape)
 
     @property
@@ -373,18 +385,31 @@ def block_param_count(cfg):
     return int(lib().orc_block_param_count(ctypes.byref(cfg)))
 
 
-def block_fwd_bwd(cfg, params, x, gout):
+def _mag_out(params, mag):
+    """The magnitude output of a model call: an array like params when asked for, else NULL."""
+    return np.zeros_like(params) if mag else None
+
+
+def _pm(a):
+    return _p(a) if a is not None else None
+
+
+def block_fwd_bwd(cfg, params, x, gout, mag=False):
+    """out, dparams, dx (and with mag=True the parameter-gradient magnitude sums, Tensor::mag)."""
     params, x, gout = map(_f64, (params, x, gout))
     out, dparams, dx = np.zeros_like(x), np.zeros_like(params), np.zeros_like(x)
-    _check(lib().orc_block_fwd_bwd(ctypes.byref(cfg), _p(params), _p(x), _p(gout), _p(out), _p(dparams), _p(dx)))
-    return out, dparams, dx
+    dmag = _mag_out(params, mag)
+    _check(lib().orc_block_fwd_bwd(ctypes.byref(cfg), _p(params), _p(x), _p(gout), _p(out), _p(dparams), _p(dx),
+                                   _pm(dmag)))
+    return (out, dparams, dx, dmag) if mag else (out, dparams, dx)
 
 
 def ppo_param_count(cfg):
     return int(lib().orc_ppo_param_count(ctypes.byref(cfg)))
 
 
-def ppo_fwd_bwd(cfg, params, states, actions, adv, ret, old_logp):
+def ppo_fwd_bwd(cfg, params, states, actions, adv, ret, old_logp, mag=False):
+    """loss, logits, values, dparams (and with mag=True the parameter-gradient magnitude sums)."""
     params, states, adv, ret, old_logp = map(_f64, (params, states, adv, ret, old_logp))
     actions = np.ascontiguousarray(actions, dtype=np.int32)
     B = cfg.batch
@@ -392,20 +417,23 @@ def ppo_fwd_bwd(cfg, params, states, actions, adv, ret, old_logp):
     logits = np.zeros((B, cfg.n_actions))
     values = np.zeros(B)
     dparams = np.zeros_like(params)
+    dmag = _mag_out(params, mag)
     _check(lib().orc_ppo_fwd_bwd(ctypes.byref(cfg), _p(params), _p(states), actions.ctypes.data_as(_i32p), _p(adv),
-                                 _p(ret), _p(old_logp), ctypes.byref(loss), _p(logits), _p(values), _p(dparams)))
-    return loss.value, logits, values, dparams
+                                 _p(ret), _p(old_logp), ctypes.byref(loss), _p(logits), _p(values), _p(dparams),
+                                 _pm(dmag)))
+    return (loss.value, logits, values, dparams, dmag) if mag else (loss.value, logits, values, dparams)
 
 
-def ppo_fwd_bwd_per_sample(cfg, params, states, actions, adv, ret, old_logp, diff_last=True):
+def ppo_fwd_bwd_per_sample(cfg, params, states, actions, adv, ret, old_logp, diff_last=True, mag=False):
     params, states, adv, ret, old_logp = map(_f64, (params, states, adv, ret, old_logp))
     actions = np.ascontiguousarray(actions, dtype=np.int32)
     loss = ctypes.c_double()
     dparams = np.zeros_like(params)
+    dmag = _mag_out(params, mag)
     _check(lib().orc_ppo_fwd_bwd_per_sample(ctypes.byref(cfg), _p(params), _p(states), actions.ctypes.data_as(_i32p),
                                             _p(adv), _p(ret), _p(old_logp), ctypes.c_int(int(diff_last)),
-                                            ctypes.byref(loss), _p(dparams)))
-    return loss.value, dparams
+                                            ctypes.byref(loss), _p(dparams), _pm(dmag)))
+    return (loss.value, dparams, dmag) if mag else (loss.value, dparams)
 
 
 def ppo_sample_loss(cfg, logits, value, action, old_logp, adv, ret):
@@ -435,14 +463,16 @@ def mla_param_count(ci):
     return int(lib().orc_mla_param_count(ci.ctypes.data_as(_i32p)))
 
 
-def mla_fwd_bwd(ci, eps, base, params, x, gout):
-    """ci = [batch, seq, d_model, n_heads, kv_latent, rope_dim, head_dim, v_dim, causal, literal_rope]."""
+def mla_fwd_bwd(ci, eps, base, params, x, gout, mag=False):
+    """ci = [batch, seq, d_model, n_heads, kv_latent, rope_dim, head_dim, v_dim, causal, literal_rope].
+    out, dparams, dx (and with mag=True the parameter-gradient magnitude sums)."""
     ci = np.ascontiguousarray(ci, dtype=np.int32)
     params, x, gout = map(_f64, (params, x, gout))
     out, dparams, dx = np.zeros_like(x), np.zeros_like(params), np.zeros_like(x)
+    dmag = _mag_out(params, mag)
     _check(lib().orc_mla_fwd_bwd(ci.ctypes.data_as(_i32p), ctypes.c_double(eps), ctypes.c_double(base), _p(params),
-                                 _p(x), _p(gout), _p(out), _p(dparams), _p(dx)))
-    return out, dparams, dx
+                                 _p(x), _p(gout), _p(out), _p(dparams), _p(dx), _pm(dmag)))
+    return (out, dparams, dx, dmag) if mag else (out, dparams, dx)
 
 
 def adam_step(p, g, m, v, t, lr, beta1=0.9, beta2=0.999, eps=1e-8, max_norm=0.0):

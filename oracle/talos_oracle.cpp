@@ -27,6 +27,9 @@
  * Extensions the configurations need (each documented where defined): causal softmax mask,
  * GELU, explicit sequence positions for RoPE, a differentiable last-token gather, a standard
  * multi-head attention block, and a batched PPO loss with a closed-form backward.
+ * Checker support, not in the reference: gradient magnitude sums (Tensor::mag, the sum of
+ * |term| over each gradient element's terms), from which the parity tests derive the rounding
+ * allowance of parameter gradients; pinned by their closed forms in tests/test_oracle.py.
  *
  * Parallelism mirrors the reference: row-parallel loops on one global pool sized to all host
  * cores (rayon's global pool), matmul's serial path below m*n*k < 32768 (src/autograd.rs:222).
@@ -187,10 +190,27 @@ using Shape = std::vector<size_t>;
 struct Ctx;
 struct Tensor {
   std::shared_ptr<Vec> data, grad;
+  // Leaves created while magnitude tracking is on (parity-bound support, not part of the
+  // reference): for each gradient element, the sum of |term| over every term the backward
+  // closures add into it -- (|X|^T |G|)_ij for dW = X^T G, sum_r |g x_hat| for an RMSNorm gain,
+  // sum_r |g| for a broadcast bias. An fp32 evaluation of the same sum errs by a small multiple
+  // of 2^-24 of it; a dropped or misplaced term errs by a whole term.
+  std::shared_ptr<Vec> mag;
   Shape shape;
   std::shared_ptr<Ctx> ctx;
   size_t numel() const { return data->size(); }
 };
+static bool g_track_mag = false;
+// The magnitude buffer of a tracked tensor (nullptr when untracked).
+static double* mag_of(const Tensor& t) { return t.mag ? t.mag->data() : nullptr; }
+// While a closure runs: the magnitudes of the gradient it receives (its output's), or nullptr.
+// Pass-through closures (reshape, transpose, the element-wise ops) forward them; reductions
+// (matmul, an RMSNorm gain, a broadcast bias) start from |g| itself. A closure that keeps no
+// magnitudes leaves its parents' at 0, so a magnitude is taken as at least |g|.
+static const double* g_out_mag = nullptr;
+static inline double mag_in(const Vec& g, size_t i) {
+  return g_out_mag ? std::max(g_out_mag[i], std::fabs(g[i])) : std::fabs(g[i]);
+}
 using BackFn = std::function<void(const Vec& gout, std::vector<Tensor>& parents)>;
 struct Ctx {
   std::vector<Tensor> parents;
@@ -216,9 +236,16 @@ static Tensor tnew(Vec data, Shape shape) {
   t.shape = std::move(shape);
   return t;
 }
+// A leaf whose gradient magnitudes are tracked when tracking is on.
+static Tensor tleaf(Vec data, Shape shape) {
+  Tensor t = tnew(std::move(data), std::move(shape));
+  if (g_track_mag) t.mag = std::make_shared<Vec>(t.numel(), 0.0);
+  return t;
+}
 // Output tensor recorded on the tape.
 static Tensor tout(Vec data, Shape shape, std::vector<Tensor> parents, BackFn fn) {
   Tensor t = tnew(std::move(data), std::move(shape));
+  if (g_track_mag) t.mag = std::make_shared<Vec>(t.numel(), 0.0);
   t.ctx = std::make_shared<Ctx>();
   t.ctx->parents = std::move(parents);
   t.ctx->backward_op = std::move(fn);
@@ -271,11 +298,16 @@ static void backward(const Tensor& root) {
   for (auto it = topo.rbegin(); it != topo.rend(); ++it) {
     if (it->ctx) {
       const Vec& g = *it->grad;
+      g_out_mag = it->mag ? it->mag->data() : nullptr;
       it->ctx->backward_op(g, it->ctx->parents);
+      g_out_mag = nullptr;
     }
   }
 }
-static void zero_grad(const Tensor& t) { std::fill(t.grad->begin(), t.grad->end(), 0.0); }
+static void zero_grad(const Tensor& t) {
+  std::fill(t.grad->begin(), t.grad->end(), 0.0);
+  if (t.mag) std::fill(t.mag->begin(), t.mag->end(), 0.0);
+}
 static Tensor detach(const Tensor& t) {
   Tensor d = t;
   d.ctx.reset();
@@ -363,6 +395,25 @@ static Tensor matmul(const Tensor& a, const Tensor& b) {
       } else {
         par_rows(k, i_fn);
       }
+    }
+    // magnitudes of tracked operands: |dC| |B|^T and |A|^T |dC|
+    if (double* ma = mag_of(p[0])) {
+      par_rows(m, [&](size_t r) {
+        for (size_t i = 0; i < k; ++i) {
+          double s = 0;
+          for (size_t j = 0; j < n; ++j) s += std::fabs(g[r * n + j]) * std::fabs(B[i * n + j]);
+          ma[r * k + i] += s;
+        }
+      });
+    }
+    if (double* mb = mag_of(p[1])) {
+      par_rows(k, [&](size_t i) {
+        for (size_t r = 0; r < m; ++r) {
+          double s = std::fabs(A[r * k + i]);
+          if (s == 0.0) continue;
+          for (size_t j = 0; j < n; ++j) mb[i * n + j] += s * std::fabs(g[r * n + j]);
+        }
+      });
     }
   });
 }
@@ -471,6 +522,9 @@ static Tensor broadcast_to_batch(const Tensor& x, size_t batch) {
     size_t cs = gx.size();
     for (size_t c = 0; c + cs <= g.size(); c += cs)
       for (size_t i = 0; i < cs; ++i) gx[i] += g[c + i];
+    if (double* mx = mag_of(p[0]))
+      for (size_t c = 0; c + cs <= g.size(); c += cs)
+        for (size_t i = 0; i < cs; ++i) mx[i] += std::fabs(g[c + i]);
   });
 }
 // transpose (:632-739): generic N-D swap of two dims, one coordinate vector per element
@@ -508,6 +562,7 @@ static Tensor transpose(const Tensor& x, size_t d0, size_t d1) {
     for (size_t i = rank - 1; i-- > 0;) st[i] = st[i + 1] * sh[i + 1];
     for (size_t i = rank - 1; i-- > 0;) nst[i] = nst[i + 1] * ns[i + 1];
     Vec& gx = *p[0].grad;
+    double* mx = mag_of(p[0]);
     for (size_t i = 0; i < g.size(); ++i) {
       size_t t = i;
       std::vector<size_t> c(rank, 0);
@@ -519,6 +574,7 @@ static Tensor transpose(const Tensor& x, size_t d0, size_t d1) {
       size_t o = 0;
       for (size_t k = 0; k < rank; ++k) o += c[k] * st[k];
       gx[o] += g[i];
+      if (mx) mx[o] += mag_in(g, i);
     }
   });
 }
@@ -528,6 +584,7 @@ static Tensor reshape(const Tensor& x, Shape ns) {
   return tout(*x.data, ns, {x}, [](const Vec& g, std::vector<Tensor>& p) {
     Vec& gx = *p[0].grad;
     par_for(gx.size(), [&](size_t i) { gx[i] += g[i]; });
+    if (double* mx = mag_of(p[0])) par_for(gx.size(), [&](size_t i) { mx[i] += mag_in(g, i); });
   });
 }
 
@@ -572,6 +629,22 @@ static Tensor binary(const Tensor& a, const Tensor& b, Bin op) {
         par_for(gb.size(), [&](size_t i) { gb[i] -= g[i] * A[i] / (B[i] * B[i]); });
       }
     }
+    // magnitudes of tracked operands: the output's, scaled by each operand's partial derivative
+    double* ma = mag_of(p[0]);
+    double* mb = alias ? nullptr : mag_of(p[1]);
+    if (ma || mb)
+      par_for(g.size(), [&](size_t i) {
+        const double m = mag_in(g, i);
+        double ta, tb;
+        switch (op) {
+          case ADD:
+          case SUB: ta = tb = m; break;
+          case MUL: ta = m * std::fabs(B[i]); tb = m * std::fabs(A[i]); break;
+          default: ta = m / std::fabs(B[i]); tb = m * std::fabs(A[i] / (B[i] * B[i])); break;
+        }
+        if (ma) ma[i] += alias ? ta + tb : ta;
+        if (mb) mb[i] += tb;
+      });
   });
 }
 static Tensor add(const Tensor& a, const Tensor& b) { return binary(a, b, ADD); }
@@ -681,6 +754,13 @@ static Tensor rmsnorm(const Tensor& x, const Tensor& w, double eps) {
       for (size_t r = 0; r < rows; ++r) s += g[r * dim + i] * xh[r * dim + i];
       gw[i] += s;
     });
+    if (double* mw = mag_of(p[1])) {
+      par_rows(dim, [&](size_t i) {
+        double s = 0;
+        for (size_t r = 0; r < rows; ++r) s += std::fabs(g[r * dim + i] * xh[r * dim + i]);
+        mw[i] += s;
+      });
+    }
   });
 }
 
@@ -863,6 +943,15 @@ static Tensor concat_last(const Tensor& a, const Tensor& b) {
       for (size_t k = 0; k < la; ++k) ga[r * la + k] += g[r * (la + lb) + k];
       for (size_t k = 0; k < lb; ++k) gb[r * lb + k] += g[r * (la + lb) + la + k];
     });
+    double* ma = mag_of(p[0]);
+    double* mb = mag_of(p[1]);
+    if (ma || mb)
+      par_rows(rows, [&](size_t r) {
+        if (ma)
+          for (size_t k = 0; k < la; ++k) ma[r * la + k] += mag_in(g, r * (la + lb) + k);
+        if (mb)
+          for (size_t k = 0; k < lb; ++k) mb[r * lb + k] += mag_in(g, r * (la + lb) + la + k);
+      });
   });
 }
 // last_token (src/transformer.rs:92-109) takes row S-1 of each sequence. The reference
@@ -880,8 +969,12 @@ static Tensor last_token(const Tensor& x, bool differentiable) {
   if (!differentiable) return tnew(std::move(out), {B, D});
   return tout(std::move(out), {B, D}, {x}, [B, S, D](const Vec& g, std::vector<Tensor>& p) {
     Vec& gx = *p[0].grad;
+    double* mx = mag_of(p[0]);
     for (size_t b = 0; b < B; ++b)
-      for (size_t i = 0; i < D; ++i) gx[b * S * D + (S - 1) * D + i] += g[b * D + i];
+      for (size_t i = 0; i < D; ++i) {
+        gx[b * S * D + (S - 1) * D + i] += g[b * D + i];
+        if (mx) mx[b * S * D + (S - 1) * D + i] += mag_in(g, b * D + i);
+      }
   });
 }
 
@@ -896,7 +989,7 @@ struct Params {
     size_t n = prod(s);
     Vec d(src + off, src + off + n);
     off += n;
-    Tensor t = tnew(std::move(d), s);
+    Tensor t = tleaf(std::move(d), s);
     leaves.push_back(t);
     return t;
   }
@@ -904,6 +997,17 @@ struct Params {
     size_t o = 0;
     for (auto& t : leaves) {
       std::copy(t.grad->begin(), t.grad->end(), dst + o);
+      o += t.numel();
+    }
+  }
+  // the gradient magnitudes of the leaves (zeros for an untracked leaf)
+  void mags(double* dst) const {
+    size_t o = 0;
+    for (auto& t : leaves) {
+      if (t.mag)
+        std::copy(t.mag->begin(), t.mag->end(), dst + o);
+      else
+        std::fill(dst + o, dst + o + t.numel(), 0.0);
       o += t.numel();
     }
   }
@@ -1013,7 +1117,7 @@ static Tensor split_cols(const Tensor& w, size_t c0, size_t nc) {
   Vec d(r * nc);
   for (size_t i = 0; i < r; ++i)
     for (size_t j = 0; j < nc; ++j) d[i * nc + j] = (*w.data)[i * C + c0 + j];
-  return tnew(std::move(d), {r, nc});
+  return tleaf(std::move(d), {r, nc});
 }
 static Block make_block(Params& P, const talos_block_cfg& c) {
   Block b;
@@ -1051,6 +1155,10 @@ static void block_pack_grads(Block& b) {
   for (int s = 0; s < 3; ++s)
     for (size_t i = 0; i < d; ++i)
       for (size_t j = 0; j < d; ++j) G[i * 3 * d + s * d + j] += (*L[s]->weight.grad)[i * d + j];
+  if (b.wqkv.mag)
+    for (int s = 0; s < 3; ++s)
+      for (size_t i = 0; i < d; ++i)
+        for (size_t j = 0; j < d; ++j) (*b.wqkv.mag)[i * 3 * d + s * d + j] += (*L[s]->weight.mag)[i * d + j];
 }
 static void block_zero_split_grads(Block& b) {
   if (b.mla_attn) return;
@@ -1380,6 +1488,13 @@ static Vec block_step(const Decoder& D, const double* P, const Vec& h, KvCache& 
 using namespace orc;
 
 static thread_local std::string g_err;
+// Magnitude tracking for the duration of one model call whose dmag output is non-null.
+struct TrackMag {
+  bool prev;
+  explicit TrackMag(bool on) : prev(g_track_mag) { g_track_mag = on; }
+  ~TrackMag() { g_track_mag = prev; }
+};
+
 #define GUARD(...)                  \
   try {                             \
     __VA_ARGS__;                    \
@@ -1415,7 +1530,7 @@ static Tensor get(int64_t h) {
 int64_t orc_tensor_new(const double* data, const int64_t* shape, int rank) {
   try {
     Shape s(shape, shape + rank);
-    return put(tnew(Vec(data, data + prod(s)), s));
+    return put(tleaf(Vec(data, data + prod(s)), s));
   } catch (const std::exception& e) {
     g_err = e.what();
     return 0;
@@ -1424,7 +1539,7 @@ int64_t orc_tensor_new(const double* data, const int64_t* shape, int rank) {
 int64_t orc_tensor_new_len(const double* data, int64_t len, const int64_t* shape, int rank) {
   try {
     Shape s(shape, shape + rank);
-    return put(tnew(Vec(data, data + len), s));
+    return put(tleaf(Vec(data, data + len), s));
   } catch (const std::exception& e) {
     g_err = e.what();
     return 0;
@@ -1455,6 +1570,16 @@ void orc_tensor_data(int64_t h, double* out) {
 void orc_tensor_grad(int64_t h, double* out) {
   Tensor t = get(h);
   std::copy(t.grad->begin(), t.grad->end(), out);
+}
+// Leaves created after orc_set_track_mag(1) carry gradient magnitudes (see Tensor::mag);
+// orc_tensor_mag copies them (zeros for an untracked tensor).
+void orc_set_track_mag(int on) { g_track_mag = on != 0; }
+void orc_tensor_mag(int64_t h, double* out) {
+  Tensor t = get(h);
+  if (t.mag)
+    std::copy(t.mag->begin(), t.mag->end(), out);
+  else
+    std::fill(out, out + t.numel(), 0.0);
 }
 int orc_tensor_has_ctx(int64_t h) { return get(h).ctx ? 1 : 0; }
 
@@ -1711,9 +1836,11 @@ int orc_attention_fwd_bwd(int64_t B, int64_t S, int64_t H, int64_t dk, int64_t d
 size_t orc_block_param_count(const talos_block_cfg* c) { return block_param_count(*c); }
 
 // C3: one block fwd+bwd with loss = sum(out * gout).
+// dmag (nullable): the magnitude sums of the parameter gradients (Tensor::mag), same layout.
 int orc_block_fwd_bwd(const talos_block_cfg* c, const double* params, const double* x, const double* gout,
-                      double* out, double* dparams, double* dx) {
+                      double* out, double* dparams, double* dx, double* dmag) {
   GUARD({
+    TrackMag tm(dmag != nullptr);
     Params P;
     P.src = params;
     Block b = make_block(P, *c);
@@ -1726,6 +1853,7 @@ int orc_block_fwd_bwd(const talos_block_cfg* c, const double* params, const doub
     block_pack_grads(b);
     std::copy(O.data->begin(), O.data->end(), out);
     P.grads(dparams);
+    if (dmag) P.mags(dmag);
     std::copy(X.grad->begin(), X.grad->end(), dx);
   })
 }
@@ -1740,8 +1868,9 @@ size_t orc_ppo_param_count(const talos_ppo_cfg* c) {
 // Writes loss, logits [B,A], values [B], dparams.
 int orc_ppo_fwd_bwd(const talos_ppo_cfg* c, const double* params, const double* states, const int32_t* actions,
                     const double* adv, const double* ret, const double* old_logp, double* loss, double* logits_out,
-                    double* values_out, double* dparams) {
+                    double* values_out, double* dparams, double* dmag) {
   GUARD({
+    TrackMag tm(dmag != nullptr);
     Params P;
     P.src = params;
     Policy pol = make_policy(P, *c);
@@ -1760,6 +1889,7 @@ int orc_ppo_fwd_bwd(const talos_ppo_cfg* c, const double* params, const double* 
     if (logits_out) std::copy(logits.data->begin(), logits.data->end(), logits_out);
     if (values_out) std::copy(values.data->begin(), values.data->end(), values_out);
     P.grads(dparams);
+    if (dmag) P.mags(dmag);
   })
 }
 
@@ -1768,8 +1898,10 @@ int orc_ppo_fwd_bwd(const talos_ppo_cfg* c, const double* params, const double* 
 // length. diff_last = 0 reproduces the reference's graph cut at last_token (src/transformer.rs:92-109).
 int orc_ppo_fwd_bwd_per_sample(const talos_ppo_cfg* c, const double* params, const double* states,
                                const int32_t* actions, const double* adv, const double* ret,
-                               const double* old_logp, int diff_last, double* loss, double* dparams) {
+                               const double* old_logp, int diff_last, double* loss, double* dparams,
+                               double* dmag) {
   GUARD({
+    TrackMag tm(dmag != nullptr);
     Params P;
     P.src = params;
     Policy pol = make_policy(P, *c);
@@ -1794,6 +1926,7 @@ int orc_ppo_fwd_bwd_per_sample(const talos_ppo_cfg* c, const double* params, con
     for (auto& b : pol.blocks) block_pack_grads(b);
     *loss = (*fl.data)[0];
     P.grads(dparams);
+    if (dmag) P.mags(dmag);
   })
 }
 
@@ -1834,8 +1967,9 @@ size_t orc_mla_param_count(const int32_t* ci) {
   return d + d * L + L * H * hd + L * H * vd + d * H * hd + d * H * r + d * H * r + H * vd * d;
 }
 int orc_mla_fwd_bwd(const int32_t* ci, double eps, double base, const double* params, const double* x,
-                    const double* gout, double* out, double* dparams, double* dx) {
+                    const double* gout, double* out, double* dparams, double* dx, double* dmag) {
   GUARD({
+    TrackMag tm(dmag != nullptr);
     MlaCfg c{ci[0], ci[1], ci[2], ci[3], ci[4], ci[5], ci[6], ci[7], ci[8], ci[9], eps, base};
     Params P;
     P.src = params;
@@ -1849,6 +1983,7 @@ int orc_mla_fwd_bwd(const int32_t* ci, double eps, double base, const double* pa
     backward(tsum(mul(O, G)));
     std::copy(O.data->begin(), O.data->end(), out);
     P.grads(dparams);
+    if (dmag) P.mags(dmag);
     std::copy(X.grad->begin(), X.grad->end(), dx);
   })
 }

@@ -26,24 +26,26 @@ def oracle():
 
 
 def pytest_terminal_summary(terminalreporter):
-    """The parameter-gradient tolerance audit: every tensor that needed the raised absolute floor
-    (common.GRAD_SCALE_FLOOR) to pass, with the floor and the number of elements that needed it."""
+    """The parameter-gradient tolerance audit: every tensor with elements that needed the
+    magnitude-derived allowance (common.check_grad) to pass, how many, and the kappa they needed."""
     try:
         import common
     except ImportError:
         return
-    recs = common.FLOOR_AUDIT
+    recs = common.GRAD_AUDIT
     if not recs:
         return
     out = os.environ.get("TALOS_TOLERANCE_AUDIT")
     if out:
         with open(out, "w") as f:
             json.dump(recs, f, indent=1)
-    need = [r for r in recs if r["needs_floor"]]
+    need = [r for r in recs if r["needs_mag"]]
     tr = terminalreporter
     tr.section("parameter-gradient tolerance audit")
-    tr.write_line(f"{len(recs)} tensors checked with the scale floor; {len(need)} have elements that need it")
-    for r in sorted(need, key=lambda r: -r["needs_floor"]):
-        tr.write_line(f"  {r['test']} {r['tensor']}: {r['needs_floor']}/{r['size']} elements, floor "
-                      f"{r['floor']:.3e} (max|ref| {r['max_abs_ref']:.3e}), worst err / plain bound "
-                      f"{r['worst_err_over_plain']:.2f}")
+    worst = max(r["kappa_needed"] for r in recs)
+    tr.write_line(f"{len(recs)} parameter-gradient tensors checked; {len(need)} have elements beyond the plain "
+                  f"1e-4 |ref| + 1e-5 rule; largest kappa needed {worst:.2f} (allowed {recs[0]['kappa']:.0f})")
+    for r in sorted(need, key=lambda r: -r["kappa_needed"]):
+        tr.write_line(f"  {r['test']} {r['tensor']}: {r['needs_mag']}/{r['size']} elements beyond the plain rule, "
+                      f"kappa needed {r['kappa_needed']:.2f}, worst err / plain bound {r['worst_err_over_plain']:.2f} "
+                      f"(max|ref| {r['max_abs_ref']:.3e})")

@@ -44,7 +44,9 @@ def _host(d, n, offset):
 def _check_state(n, off, dp, dm, dv, p0, rp, rm, rv, tag):
     check_close(_host(dp, n, off).astype(np.float64) - p0, rp - p0, name=f"{tag} delta p")
     check_close(_host(dm, n, off), rm, name=f"{tag} m")
-    check_close(_host(dv, n, off), rv, atol=0.0, scale_floor=1e-6, name=f"{tag} v")
+    # v is a positive combination of g^2 terms (no cancellation), each step's update formed in f64
+    # and rounded once to fp32: a relative error of a few 2^-24, so purely relative, no floor
+    check_close(_host(dv, n, off), rv, atol=0.0, name=f"{tag} v")
 
 
 @pytest.mark.parametrize("n", [1, 3, 4, 4099, 1000003])
@@ -98,7 +100,7 @@ def test_adam_global_norm_clip_multi_tensor(oracle, scale):
         got_p = np.concatenate([d.numpy() for d in dps]).astype(np.float64)
         check_close(got_p - p0, rp - p0, name=f"clip scale={scale} t={t} delta p")
         check_close(np.concatenate([d.numpy() for d in dms]), rm, name=f"clip t={t} m")
-        check_close(np.concatenate([d.numpy() for d in dvs]), rv, atol=0.0, scale_floor=1e-6, name=f"clip t={t} v")
+        check_close(np.concatenate([d.numpy() for d in dvs]), rv, atol=0.0, name=f"clip t={t} v")
         for dg in dgs:
             dg.free()
 

@@ -687,3 +687,109 @@ def test_gae_special_cases(oracle):
     # the reward clip: |r_norm| <= clip
     a, _, _ = oracle.ppo_gae(rew * 1e6, val * 0, np.ones(50, bool), 0.0, 1.0, 10.0, 0.99, 0.95)
     np.testing.assert_allclose(a, np.clip(rew * 1e6 / (1.0 + 1e-8), -10, 10), rtol=1e-15, atol=0)
+
+
+# ---------------------------------------------------------------------------
+# 4. Gradient magnitude sums (the allowance of the parameter-gradient bound, common.check_grad)
+# ---------------------------------------------------------------------------
+
+
+def test_magnitude_sums_closed_forms(oracle):
+    """Under track_mag the oracle's leaves carry, per gradient element, the sum of |term| over its
+    terms: (|X|^T |G|) for a weight, sum_r |g x_hat| for an RMSNorm gain, sum_r |g| for a bias,
+    |G| |W|^T for the input of a product."""
+    T = oracle.T
+    rng = np.random.default_rng(8)
+    rows, k, n = 37, 6, 5
+    X, W, b, G = rng.normal(size=(rows, k)), rng.normal(size=(k, n)), rng.normal(size=n), rng.normal(size=(rows, n))
+    oracle.track_mag(True)
+    try:
+        x, w, bb, g = T.new(X, X.shape), T.new(W, W.shape), T.new(b, b.shape), T.new(G, G.shape)
+        y = x.matmul(w) + bb.broadcast_to_batch(rows)
+        (y * g).sum().backward()
+        assert np.allclose(w.mag, np.abs(X).T @ np.abs(G), rtol=1e-13)
+        assert np.allclose(bb.mag, np.abs(G).sum(0), rtol=1e-13)
+        assert np.allclose(x.mag, np.abs(G) @ np.abs(W).T, rtol=1e-13)
+        assert np.allclose(w.grad, X.T @ G, rtol=1e-12)  # the gradients themselves are unchanged
+        # RMSNorm gain: sum_r |g x_hat|
+        gain = rng.uniform(0.9, 1.1, k)
+        x2, w2 = T.new(X, X.shape), T.new(gain, gain.shape)
+        G2 = rng.normal(size=(rows, k))
+        (x2.rmsnorm(w2, 1e-6) * T.new(G2, G2.shape)).sum().backward()
+        xh = X / np.sqrt((X * X).mean(1, keepdims=True) + 1e-6)
+        assert np.allclose(w2.mag, np.abs(G2 * xh).sum(0), rtol=1e-13)
+    finally:
+        oracle.track_mag(False)
+    # untracked leaves report zeros
+    z = T.new(W, W.shape)
+    assert not z.mag.any()
+
+
+def test_magnitude_sums_bound_the_model_gradients(oracle):
+    """On the composite models every parameter's magnitude sum is at least |grad| (the triangle
+    inequality; equality when no term cancels), and the returned gradients do not depend on
+    tracking."""
+    rng = np.random.default_rng(9)
+    B, S, d, H, F = 2, 7, 16, 2, 32
+    args = (B, S, d, H, d // H, F, 1, 0, 1e-6, 1e4)
+    p = block_params(rng, d, F, gain_jitter=True)
+    x, G = rng.normal(size=(B, S, d)), rng.normal(size=(B, S, d))
+    out0, dp0, dx0 = oracle.block_fwd_bwd(oracle.BlockCfg(*args), p, x, G)
+    out1, dp1, dx1, mag = oracle.block_fwd_bwd(oracle.BlockCfg(*args), p, x, G, mag=True)
+    assert np.array_equal(dp0, dp1) and np.array_equal(dx0, dx1) and np.array_equal(out0, out1)
+    assert np.all(mag >= np.abs(dp1) * (1 - 1e-12)) and mag.min() > 0
+    ci = [2, 9, 16, 2, 8, 4, 8, 8, 1, 0]
+    pm = mla_params(rng, ci)
+    xm, Gm = rng.normal(size=(2, 9, 16)), rng.normal(size=(2, 9, 16))
+    _, dpm, _, magm = oracle.mla_fwd_bwd(ci, 1e-5, 1e4, pm, xm, Gm, mag=True)
+    assert np.all(magm >= np.abs(dpm) * (1 - 1e-12)) and magm.min() > 0
+    cfg = oracle.PpoCfg(5, 6, 8, 16, 2, 2, 8, 32, 3, 1, 0, 1e-5, 1e4, 0.2, 0.5, 0.01)
+    pp = ppo_params(rng, cfg)
+    st = gacha_states(rng, 5, 6)
+    acts = rng.integers(0, 3, 5).astype(np.int32)
+    adv, ret, old = rng.normal(size=5), rng.normal(size=5), rng.normal(size=5) * 0.2 - 1.1
+    _, _, _, dpp, magp = oracle.ppo_fwd_bwd(cfg, pp, st, acts, adv, ret, old, mag=True)
+    assert np.all(magp >= np.abs(dpp) * (1 - 1e-12)) and magp.min() > 0
+    # per-sample graphs (biases reach the loss through reshape and element-wise adds)
+    _, dps, mags = oracle.ppo_fwd_bwd_per_sample(cfg, pp, st, acts, adv, ret, old, mag=True)
+    assert np.all(mags >= np.abs(dps) * (1 - 1e-12))
+    # a product of non-negative factors has no cancellation: magnitude == |grad|
+    T = oracle.T
+    oracle.track_mag(True)
+    try:
+        A, Gp = rng.uniform(0, 1, (50, 4)), rng.uniform(0, 1, (50, 3))
+        a, w = T.new(A, A.shape), T.new(np.ones((4, 3)), (4, 3))
+        (a.matmul(w) * T.new(Gp, Gp.shape)).sum().backward()
+        assert np.allclose(w.mag, w.grad, rtol=1e-13)
+    finally:
+        oracle.track_mag(False)
+
+
+def test_gradient_bound_accepts_fp32_rounding_and_rejects_planted_mistakes(oracle):
+    """The parameter-gradient bound of common.check_grad, 1e-4 |r| + max(1e-5, 32 u M), on a
+    weight gradient over 32768 rows with N(0,1) factors (sums of +-terms that cancel to ~0.6 % of
+    their magnitude): an fp32 evaluation (numpy float32 products, blocked accumulation) passes it,
+    and so does one in 512-row fp32 splits combined in f64 (the device's weight-gradient shape);
+    a dropped row, a doubled row, a transposed index and a sign error each fail it."""
+    from common import check_grad
+    rng = np.random.default_rng(10)
+    rows, k, n = 32768, 16, 16
+    X = rng.normal(size=(rows, k)).astype(np.float32).astype(np.float64)
+    G = rng.normal(size=(rows, n)).astype(np.float32).astype(np.float64)
+    ref = X.T @ G
+    mag = np.abs(X).T @ np.abs(G)
+    got32 = (X.astype(np.float32).T @ G.astype(np.float32)).astype(np.float64)
+    check_grad(got32, ref, mag, name="fp32 evaluation")
+    split = sum((X[s:s + 512].astype(np.float32).T @ G[s:s + 512].astype(np.float32)).astype(np.float64)
+                for s in range(0, rows, 512))
+    check_grad(split, ref, mag, name="fp32 splits")
+    r = int(np.argmax(np.abs(X).sum(1) * np.abs(G).sum(1) < 1e9))  # any row
+    mistakes = {
+        "dropped row": ref - np.outer(X[r], G[r]),
+        "doubled row": ref + np.outer(X[r], G[r]),
+        "transposed index": ref.T.copy(),
+        "sign error": -ref,
+    }
+    for what, bad in mistakes.items():
+        with pytest.raises(AssertionError):
+            check_grad(bad, ref, mag, name=what, audit=False)
