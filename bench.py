@@ -63,6 +63,12 @@ def aggregate(records):
     return agg
 
 
+def runs_on_bf16_mfma(name):
+    """Kernel symbols whose products run on the bf16 matrix cores: the bf16-in GEMMs
+    (gemm_f32_kernel<TA, TB, E, true>) and the attention kernels with bf16 in their name."""
+    return "bf16" in name or (name.startswith("gemm_f32_kernel") and name.endswith("true>"))
+
+
 def roofline_of(name, n, flops, bytes_, ms, peak_tflops=None):
     """The roofline of a kernel symbol from its launches: matrix-core bound when its arithmetic
     intensity (algorithmic flops per algorithmic HBM byte) is above the ridge point of the MFMA
@@ -70,8 +76,7 @@ def roofline_of(name, n, flops, bytes_, ms, peak_tflops=None):
     below it. achieved = algorithmic work per launch / average launch time."""
     avg_ms = ms / n
     if peak_tflops is None:
-        peak_tflops = PEAK_BF16_MFMA_TFLOPS if name.endswith("true>") and name.startswith("gemm_f32_kernel") \
-            else PEAK_FP32_MFMA_TFLOPS
+        peak_tflops = PEAK_BF16_MFMA_TFLOPS if runs_on_bf16_mfma(name) else PEAK_FP32_MFMA_TFLOPS
     ridge = peak_tflops * 1e12 / (PEAK_HBM_GBS * 1e9)
     if flops > 0 and (bytes_ <= 0 or flops / bytes_ >= ridge):
         achieved = flops / n / (avg_ms * 1e-3) / 1e12
@@ -83,9 +88,12 @@ def roofline_of(name, n, flops, bytes_, ms, peak_tflops=None):
             "intensity_flop_per_byte": round(flops / max(bytes_, 1), 2)}
 
 
-def traffic_of(kernel):
-    """HBM bytes per launch of the kernel from the committed rocprofv3 --pmc summary, if any."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
+def traffic_of(kernel, config="C4"):
+    """HBM bytes per launch of the kernel symbol in the given configuration, from the committed
+    rocprofv3 --pmc summary of that configuration's run (profiles/traffic.json for C4,
+    profiles/traffic_<config>.json for the others), if any."""
+    name = "traffic.json" if config == "C4" else f"traffic_{config.lower()}.json"
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     try:
@@ -93,6 +101,57 @@ def traffic_of(kernel):
     except (OSError, ValueError):
         return None
     return round(t["bytes"]) if t else None
+
+
+def _sized_run(run, n0, n_max, seconds):
+    """Calibrates run(n) at n0, then runs it at the n (<= n_max) that takes about `seconds`."""
+    t0 = run(n0)
+    n = int(max(n0, min(n_max, seconds / max(t0 / n0, 1e-6))))
+    return n, run(n)
+
+
+def cpu_baseline_c3(seconds=6.0):
+    """The f64 oracle's C3 block fwd+bwd (a C++ restatement of the reference's Rust autograd) on
+    this host's cores, on a bounded number of the 512 sequences, reported as the time of a whole
+    C3 step at that rate."""
+    import pyoracle
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    pyoracle.set_threads(threads)
+    d, H, F = 128, 4, 512
+    rng = np.random.default_rng(3)
+    p = wl.block_params(rng, d, F, gain_jitter=True)
+
+    def run(b):
+        x, G = rng.normal(size=(b, 64, d)), rng.normal(size=(b, 64, d))
+        t0 = time.perf_counter()
+        pyoracle.block_fwd_bwd(pyoracle.BlockCfg(b, 64, d, H, d // H, F, 1, 0, 1e-6, 1e4), p, x, G)
+        return time.perf_counter() - t0
+
+    b, t = _sized_run(run, 2, 512, seconds)
+    return {"value": round(t / b * 512 * 1e3, 1), "unit": "ms per C3 step", "cores": threads, "kind": "port",
+            "sample": f"{b} of the 512 sequences (seq 64, d128) as one batched f64 graph, the time scaled to 512; "
+                      f"C++ restatement of the Rust autograd on {threads} threads"}
+
+
+def cpu_baseline_c5(seconds=6.0):
+    """The f64 oracle's C5 MLA block fwd+bwd on this host's cores on a bounded number of the 64
+    sequences, reported as the time of a whole C5 step at that rate."""
+    import pyoracle
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    pyoracle.set_threads(threads)
+    rng = np.random.default_rng(5)
+    p = wl.mla_params(rng, [1, 256, 512, 8, 128, 32, 64, 64, 0])
+
+    def run(b):
+        x, G = rng.normal(size=(b, 256, 512)), rng.normal(size=(b, 256, 512))
+        t0 = time.perf_counter()
+        pyoracle.mla_fwd_bwd([b, 256, 512, 8, 128, 32, 64, 64, 0, 0], 1e-5, 1e4, p, x, G)
+        return time.perf_counter() - t0
+
+    b, t = _sized_run(run, 1, 64, seconds)
+    return {"value": round(t / b * 64 * 1e3, 1), "unit": "ms per C5 step", "cores": threads, "kind": "port",
+            "sample": f"{b} of the 64 sequences (seq 256, d512 MLA) as one batched f64 graph, the time scaled to 64; "
+                      f"C++ restatement of the Rust autograd on {threads} threads"}
 
 
 def cpu_baseline(cfg_t, seconds_budget=20.0):
@@ -295,11 +354,10 @@ def rollout_line(steps, n_envs=4096, context_len=16, cpu=True):
     return res
 
 
-def dominant_roofline(plan, step, steps):
+def dominant_roofline(plan, step, steps, config):
     """One profiled step for the per-kernel table, then `steps` steps with the launches of the
-    kernel symbol that took the most time bracketed by HIP events on their stream: its roofline.
-    The counter-measured traffic (profiles/traffic.json) is of the C4 step's launches, so the
-    C3 / C5 lines, whose launches of the same symbols have other shapes, report none."""
+    kernel symbol that took the most time bracketed by HIP events on their stream: its roofline,
+    with the counter-measured traffic of that symbol in this configuration's profile."""
     plan.profile(True)
     step()
     th.sync()
@@ -314,7 +372,8 @@ def dominant_roofline(plan, step, steps):
     plan.profile(False)
     roof = roofline_of(dominant, n, fl, by, ms)
     roof.update({"kernel": dominant, "launches_per_step": n // steps, "avg_launch_us": round(ms / n * 1e3, 2),
-                 "traffic": None, "algorithmic_per_launch": {"flops": fl / n, "bytes": by / n}})
+                 "traffic": traffic_of(dominant, config),
+                 "algorithmic_per_launch": {"flops": fl / n, "bytes": by / n}})
     total = sum(a[3] for a in agg.values())
     kernels = {k: {"launches": v[0], "ms": round(v[3], 4), "pct": round(100 * v[3] / total, 1)}
                for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3])}
@@ -351,7 +410,7 @@ def c3_line(steps, warmup):
         th.call("talos_block_fwd_bwd_f32", plan.h, P.ptr, X.ptr, G.ptr, out.ptr, dP.ptr, dX.ptr, None)
 
     ms = timed(step, steps, warmup)
-    roof, kernels = dominant_roofline(plan, step, steps)
+    roof, kernels = dominant_roofline(plan, step, steps, "C3")
     M, hd = B * S, d // H
     flops = 3.0 * (4 * 2 * M * d * d + 2 * 2 * M * d * F + 2 * 2 * B * H * hd * S * (S + 1) / 2)
     plan.destroy()
@@ -387,14 +446,14 @@ def c5_line(steps, warmup, precision):
         th.call("talos_mla_fwd_bwd_f32", plan.h, P.ptr, X.ptr, G.ptr, out.ptr, dP.ptr, dX.ptr, None)
 
     ms = timed(step, steps, warmup)
-    roof, kernels = dominant_roofline(plan, step, steps)
+    bf = precision == th.PREC_BF16
+    roof, kernels = dominant_roofline(plan, step, steps, "C5_bf16" if bf else "C5")
     M = B * S
     gemm = 2.0 * M * (d * L + L * H * hd + L * H * vd + d * H * hd + 2 * d * H * r + H * vd * d)
     attn = 2.0 * B * H * S * S * ((hd + r) + vd)
     flops = 3.0 * (gemm + attn)
     plan.destroy()
     tf = flops / (ms * 1e-3) / 1e12
-    bf = precision == th.PREC_BF16
     peak = PEAK_BF16_MFMA_TFLOPS if bf else PEAK_FP32_MFMA_TFLOPS
     return {"metric": f"C5 MLA block fwd+bwd ms/step (B64 S256 d512, {'bf16-in/fp32-acc' if bf else 'fp32'}, 1 GPU)",
             "value": round(ms, 4), "unit": "ms", "higher_is_better": False, "steps": steps, "warmup": warmup,
@@ -404,6 +463,11 @@ def c5_line(steps, warmup, precision):
             "step": {"algorithmic_gflop": round(flops / 1e9, 2), "tflops": round(tf, 2),
                      "frac_mfma_peak": round(tf / peak, 4), "mfma_peak_tflops": peak},
             "roofline": roof, "kernels": kernels, "device": device_line()}
+
+
+# the kernel symbols one call of each C2 op launches (their counter traffic is summed)
+C2_KERNELS = {"rmsnorm_bwd": ["rmsnorm_bwd_kernel<1>", "reduce_parts_kernel"],
+              "softmax_causal_bwd": ["softmax_bwd_rows_kernel<1>"], "rope_bwd": ["rope4_kernel"]}
 
 
 def c2_line(steps):
@@ -444,16 +508,20 @@ def c2_line(steps):
             t.append(timer.stop_ms() / steps * 1e3)
         return sorted(t)[1]
 
-    def measure(name, nbytes, sets, launch, copy_bytes):
+    def measure(name, nbytes, sets, launch, copy_bytes, kernels):
         us = per_launch_us(sets, launch)
         # the runtime's copy of copy_bytes from the first buffer of a set into its output buffer
         cus = per_launch_us(sets, lambda b: th._hip_check(
             H.hipMemcpyAsync(b[-1].ptr, b[0].ptr, copy_bytes, 3, stream), "hipMemcpyAsync"))
         gbs = nbytes / (us * 1e-6) / 1e9
+        traffic = [traffic_of(k, "C2") for k in kernels]
         res[name] = {"us_per_launch": round(us, 3), "algorithmic_bytes": int(nbytes), "GB/s": round(gbs, 1),
                      "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4), "buffer_sets": len(sets),
                      "rotated_mb": round(len(sets) * sum(a.nbytes for a in sets[0]) / 1e6, 1),
-                     "copy_floor_us": round(cus, 3), "copy_floor_bytes": int(2 * copy_bytes)}
+                     "copy_floor_us": round(cus, 3), "copy_floor_bytes": int(2 * copy_bytes),
+                     "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                  "frac": round(gbs / PEAK_HBM_GBS, 4), "kernels": kernels,
+                                  "traffic": sum(traffic) if None not in traffic else None}}
 
     try:
         # RMSNorm backward
@@ -467,7 +535,7 @@ def c2_line(steps):
                          th.DeviceArray.zeros((R, C))])
         measure("rmsnorm_bwd", 3 * R * C * 4 + R * 4 + 2 * C * 4, sets,
                 lambda b: th.call("talos_rmsnorm_bwd_f32", R, C, b[0].ptr, b[3].ptr, b[2].ptr, b[1].ptr, 0.0, b[5].ptr,
-                                  0.0, b[4].ptr, stream), R * C * 4)
+                                  0.0, b[4].ptr, stream), R * C * 4, C2_KERNELS["rmsnorm_bwd"])
         for b in sets:
             for a in b:
                 a.free()
@@ -481,7 +549,7 @@ def c2_line(steps):
         kept = int(np.sum(q + 1))
         measure("softmax_causal_bwd", 2 * kept * 4 + R * C * 4, sets,
                 lambda b: th.call("talos_softmax_bwd_f32", R, C, 1, b[0].ptr, b[1].ptr, 0.0, b[2].ptr, stream),
-                R * C * 4)
+                R * C * 4, C2_KERNELS["softmax_causal_bwd"])
         for b in sets:
             for a in b:
                 a.free()
@@ -490,7 +558,7 @@ def c2_line(steps):
                 for _ in range(37)]
         measure("rope_bwd", 2 * R * C * 4 + 2 * 64 * 32 * 4, sets,
                 lambda b: th.call("talos_rope_bwd_f32", 64, 64, 4, 64, 0, 10000.0, b[0].ptr, 0.0, b[1].ptr, stream),
-                R * C * 4)
+                R * C * 4, C2_KERNELS["rope_bwd"])
         for b in sets:
             for a in b:
                 a.free()
@@ -515,6 +583,8 @@ def main():
     ap.add_argument("--batch", type=int, default=4096)
     ap.add_argument("--seq", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="leave the C2 / C3 / C5 results out of the default line")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--profile-table", action="store_true", help="print the per-kernel table to stderr")
     ap.add_argument("--headline-only", action="store_true",
@@ -543,15 +613,51 @@ def main():
     if args.rollout_only:
         print(json.dumps({"rollout": rollout_line(args.steps, cpu=False)}))
         return
+    if args.config == "all":
+        args.no_configs = True  # each configuration prints its own line
     if args.config in ("C4", "all"):
         main_c4(args, rank)
+    elif args.copy_calibration_mb > 0:
+        print(json.dumps({"copy_calibration_bytes": copy_calibration(args.copy_calibration_mb)}), flush=True)
     if args.config in ("C2", "all"):
         print(json.dumps(c2_line(max(args.steps, 200))), flush=True)
+    cpu = rank == 0 and not args.no_cpu_baseline
     if args.config in ("C3", "all"):
-        print(json.dumps(c3_line(args.steps, args.warmup)), flush=True)
+        line = c3_line(args.steps, args.warmup)
+        if cpu:
+            line["cpu_baseline"] = cpu_baseline_c3()
+        print(json.dumps(line), flush=True)
     if args.config in ("C5", "all"):
         for prec in (th.PREC_FP32, th.PREC_BF16):
-            print(json.dumps(c5_line(args.steps, args.warmup, prec)), flush=True)
+            line = c5_line(args.steps, args.warmup, prec)
+            if cpu and prec == th.PREC_FP32:
+                line["cpu_baseline"] = cpu_baseline_c5()
+            print(json.dumps(line), flush=True)
+
+
+def other_configs(args, rank):
+    """The other configurations of BASELINE.json, measured in the default run beside the headline
+    line: C2's row-op backward kernels, the C3 block and the C5 MLA block in fp32 and bf16-in, each
+    with its roofline (the C2 ops per op; C3 and C5 of their dominant kernel) and, on rank 0, the
+    f64 oracle's time for the same work on this host (C3, C5)."""
+    cpu = rank == 0 and not args.no_cpu_baseline
+
+    def trim(line, top=6):
+        out = {k: v for k, v in line.items() if k not in ("kernels", "device", "steps", "warmup", "data")}
+        out["top_kernels"] = dict(list(line["kernels"].items())[:top])
+        return out
+
+    res = {}
+    c2 = c2_line(max(args.steps, 200))
+    res["C2"] = {k: c2[k] for k in ("metric", "value", "unit", "target_us")}
+    res["C3"] = trim(c3_line(args.steps, args.warmup))
+    if cpu:
+        res["C3"]["cpu_baseline"] = cpu_baseline_c3()
+    res["C5_fp32"] = trim(c5_line(args.steps, args.warmup, th.PREC_FP32))
+    res["C5_bf16"] = trim(c5_line(args.steps, args.warmup, th.PREC_BF16))
+    if cpu:
+        res["C5_fp32"]["cpu_baseline"] = cpu_baseline_c5()
+    return res
 
 
 def main_c4(args, rank):
@@ -619,6 +725,7 @@ def main_c4(args, rank):
     shape = (B, cfg.seq, cfg.in_dim, cfg.d_model, cfg.n_layers, cfg.n_heads, cfg.ffn_dim, cfg.n_actions)
     step_flops = wl.ppo_step_flops(*shape)
     graph_flops = wl.ppo_step_flops(*shape, live=False)
+    exec_flops = wl.ppo_step_executed_flops(*shape)
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
@@ -630,8 +737,12 @@ def main_c4(args, rank):
         "roofline": roof,
         "step": {"algorithmic_gflop": round(step_flops / 1e9, 2),
                  "reference_graph_gflop": round(graph_flops / 1e9, 2),
+                 "executed_gflop": round(exec_flops / 1e9, 2),
                  "tflops": round(step_flops / (ms_step * 1e-3) / 1e12, 2),
                  "frac_fp32_mfma_peak": round(step_flops / (ms_step * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+                 "executed_tflops": round(exec_flops / (ms_step * 1e-3) / 1e12, 2),
+                 "executed_frac_fp32_mfma_peak": round(exec_flops / (ms_step * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
+                                                       4),
                  "wall_ms_per_step": round(wall * 1e3 / args.steps, 4)},
         "kernels": {k: {"launches": v[0], "ms": round(v[3], 4), "pct": round(100 * v[3] / sum(a[3] for a in agg.values()), 1)}
                     for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3])},
@@ -641,6 +752,8 @@ def main_c4(args, rank):
         out["optimizer"] = optimizer_line(P, dP, args.steps)
         out["reference_model"] = reference_model_line(args.steps)
         out["rollout"] = rollout_line(args.steps, cpu=rank == 0 and not args.no_cpu_baseline)
+    if not args.headline_only and not args.no_configs:
+        out["configs"] = other_configs(args, rank)
     if args.profile_table:
         for k, v in sorted(agg.items(), key=lambda kv: -kv[1][3]):
             print(f"{k:40s} n={v[0]:3d} {v[3]:8.3f} ms  {v[1] / max(v[3], 1e-9) / 1e9:8.2f} TFLOP/s "
@@ -651,14 +764,22 @@ def main_c4(args, rank):
         out["cpu_baseline"] = None
     plan.destroy()
     if args.copy_calibration_mb > 0:
-        nbytes = args.copy_calibration_mb << 20
-        src, dst = th.DeviceArray.zeros(nbytes // 4), th.DeviceArray.zeros(nbytes // 4)
-        for _ in range(5):
-            th.call("talos_memcpy_d2d", dst.ptr, src.ptr, nbytes, None)
-        th.sync()
-        out["copy_calibration_bytes"] = nbytes
+        out["copy_calibration_bytes"] = copy_calibration(args.copy_calibration_mb)
     if rank == 0:
         print(json.dumps(out))
+
+
+def copy_calibration(mb):
+    """Five device-to-device copies of mb MiB: the known-size copy that scales rocprofv3
+    FETCH_SIZE / WRITE_SIZE counters to bytes (talos-xii_amd/prof_summary.py)."""
+    nbytes = mb << 20
+    src, dst = th.DeviceArray.zeros(nbytes // 4), th.DeviceArray.zeros(nbytes // 4)
+    for _ in range(5):
+        th.call("talos_memcpy_d2d", dst.ptr, src.ptr, nbytes, None)
+    th.sync()
+    src.free()
+    dst.free()
+    return nbytes
 
 
 if __name__ == "__main__":

@@ -94,6 +94,9 @@ int talos_event_elapsed_ms(void* start, void* stop, float* ms);
 int talos_workspace_bind(void* ptr, size_t bytes);
 /* The largest scratch (bytes) a call on this thread asked for since the last bind. */
 size_t talos_workspace_high_water(void);
+/* Bytes of the workspace bound on this thread (0 when none). No reference counterpart: it lets a
+ * layer above (the C++ tape) leave a caller's binding in place. */
+size_t talos_workspace_bytes(void);
 /* Name (with gfx arch), compute-unit count, peak clock (kHz) and memory of device 0. */
 int talos_device_info(char* name, size_t name_len, int* cu_count, int* clock_khz, size_t* total_mem);
 

@@ -2239,6 +2239,7 @@ static double kept_pairs(const AttnArgs& a) {
   ATTN_DISPATCH(64, 64, KERNEL)    \
   ATTN_DISPATCH(96, 64, KERNEL)    \
   ATTN_DISPATCH(128, 128, KERNEL)  \
+  set_error("attention: no kernel for head dims (%d, %d)", dkm, dvm); \
   return TALOS_ERR_UNSUPPORTED;
 
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
@@ -2247,8 +2248,8 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
     set_error("attention: head dims (%d, %d) exceed the supported (128, 128)", d.dk, d.dv);
     return TALOS_ERR_UNSUPPORTED;
   }
-  if ((d.q2 || d.k2) && !(d.q2 && d.k2 && attn_bwd_ds_supported(d))) {
-    set_error("attention forward: split q / k inputs (both) need the dS path's shapes (attn_bwd_ds_supported)");
+  if ((d.q2 || d.k2) && !(d.q2 && d.k2 && attn_ds_path(d))) {
+    set_error("attention forward: split q / k inputs (both) need the dS path (attn_ds_path)");
     return TALOS_ERR_UNSUPPORTED;
   }
   AttnArgs a = make_args(d, dkm, dvm);
@@ -2270,7 +2271,7 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
     const double tbytes = 4.0 * rows * (a.dk + 2.0 * a.dv + 1.0) + 4.0 * a.B * a.H * tiles * a.S * (a.dk + a.dv);
     grid = dim3((unsigned)((long long)a.B * a.H * (long long)tiles));
     // bf16 only where the backward is the bf16 dS path, so both form P from the same products
-    const bool bf16 = d.bf16 && d.ds && attn_bwd_ds_supported(d);
+    const bool bf16 = d.bf16 && attn_ds_path(d);
 #define TILED_BF(DK, DV)                                                                    \
     if (dkm == DK && dvm == DV && bf16) {                                                   \
       ProfScope ps(s, "attn_fwd_tiled_bf16_kernel<" #DK ", " #DV ">", flops, tbytes);       \
@@ -2299,6 +2300,7 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
       TILED_SPLIT(64, 64)
       TILED_SPLIT(96, 64)
 #undef TILED_SPLIT
+      set_error("attention forward: no split-input kernel for head dims (%d, %d)", dkm, dvm);
       return TALOS_ERR_UNSUPPORTED;
     }
     TILED(32, 32)
@@ -2306,6 +2308,7 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
     TILED(96, 64)
     TILED(128, 128)
 #undef TILED
+    set_error("attention forward: no tiled kernel for head dims (%d, %d)", dkm, dvm);
     return TALOS_ERR_UNSUPPORTED;
   }
   ATTN_ALL(attn_fwd_kernel)
@@ -2445,12 +2448,13 @@ bool attn_bwd_ds_supported(const AttnDesc& d) {
   return (dkm == 32 && dvm == 32) || (dkm == 64 && dvm == 64) || (dkm == 96 && dvm == 64);
 }
 
-bool attn_bwd_takes_ds(const AttnDesc& d, const float* ws) {
-  return d.ds && ws && attn_bwd_ds_supported(d) && (reinterpret_cast<uintptr_t>(d.ds) & 15) == 0;
+bool attn_ds_path(const AttnDesc& d) {
+  return d.ds && (reinterpret_cast<uintptr_t>(d.ds) & 15) == 0 && attn_bwd_ds_supported(d);
 }
 
 size_t attn_bwd_ds_bytes(const AttnDesc& d) {
-  return attn_bwd_ds_supported(d) ? sizeof(float) * (size_t)d.batch * d.heads * d.seq * d.seq : 0;
+  const size_t entry = d.bf16 ? 2 : 4;  // bf16 plans keep dS as bf16 rows
+  return attn_bwd_ds_supported(d) ? entry * (size_t)d.batch * d.heads * d.seq * d.seq : 0;
 }
 
 static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, bool bf16, hipStream_t s) {
@@ -2518,8 +2522,8 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
     set_error("attention: head dims (%d, %d) exceed the supported (128, 128)", d.dk, d.dv);
     return TALOS_ERR_UNSUPPORTED;
   }
-  if ((d.q2 || d.k2) && !(d.q2 && d.k2 && attn_bwd_takes_ds(d, ws))) {
-    set_error("attention backward: split q / k inputs (both) need the dS path (attn_bwd_takes_ds)");
+  if ((d.q2 || d.k2) && !(d.q2 && d.k2 && attn_ds_path(d))) {
+    set_error("attention backward: split q / k inputs (both) need the dS path (attn_ds_path)");
     return TALOS_ERR_UNSUPPORTED;
   }
   AttnArgs a = make_args(d, dkm, dvm);
@@ -2536,9 +2540,17 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
       hipLaunchKernelGGL(attn_bwd_s64_kernel<4>, dim3((unsigned)((long long)a.B * a.H)), dim3(256), 0, s, a);
     return launch_status("attn_bwd_s64_kernel");
   }
-  if (attn_bwd_takes_ds(d, ws)) return attn_bwd_with_ds(a, dkm, dvm, d.ds, d.bf16 != 0, s);
+  if (attn_ds_path(d)) {
+    // the forward decided on the same predicate (its bf16 kernel, split inputs): the backward
+    // must not fall back to another path here
+    if (!ws) {
+      set_error("attention backward: the dS path needs the workspace (attn_bwd_workspace_bytes)");
+      return TALOS_ERR_NULL;
+    }
+    return attn_bwd_with_ds(a, dkm, dvm, d.ds, d.bf16 != 0, s);
+  }
   if (d.dq2 || d.dk2) {
-    set_error("attention backward: split dq / dk outputs need the dS path (attn_bwd_takes_ds)");
+    set_error("attention backward: split dq / dk outputs need the dS path (attn_ds_path)");
     return TALOS_ERR_UNSUPPORTED;
   }
   int rc = attn_bwd_dq(a, dkm, dvm, s);

@@ -44,11 +44,11 @@ struct AttnDesc {
   float* dq_last = nullptr;
   long long lddq_last = 0;
   // optional scratch of attn_bwd_ds_bytes(d) bytes (16-byte aligned): where attn_bwd_ds_supported
-  // holds and the workspace is given, the backward forms D = rowsum(dO * O) first, stores dS
+  // holds (attn_ds_path), the backward forms D = rowsum(dO * O) first, stores dS
   // ([batch * heads][seq][seq]) from its dK / dV kernel and forms dQ = dS . K from it instead of
   // forming S, P and dP a second time
   float* ds = nullptr;
-  // on that path only (attn_bwd_takes_ds): columns [dsplit, dk) of each head's dq / dk go to dq2 /
+  // on that path only (attn_ds_path): columns [dsplit, dk) of each head's dq / dk go to dq2 /
   // dk2 (head width dk - dsplit, row pitch lddq2 / lddk2) and columns [0, dsplit) to dq / dk_out
   // at head width dsplit, instead of one [.., heads * dk] row each
   float* dq2 = nullptr;
@@ -59,7 +59,7 @@ struct AttnDesc {
   // with dsplit, the inputs may be split the same way: head columns [0, dsplit) of q / k in q / k
   // (head width dsplit, row pitch ldq / ldk) and [dsplit, dk) in q2 / k2 (head width dk - dsplit,
   // row pitch ldq2 / ldk2), so no concatenated copy is made; the tiled forward (seq > 32) and the
-  // dS backward (attn_bwd_takes_ds) only
+  // dS backward (attn_ds_path) only
   const float* q2 = nullptr;
   long long ldq2 = 0;
   const float* k2 = nullptr;
@@ -111,7 +111,11 @@ int attn_bwd_lastq_z_launch(const AttnDesc& d, const float* xn, long long ldx, c
                             hipStream_t s);
 size_t attn_bwd_workspace_bytes(const AttnDesc& d);
 bool attn_bwd_ds_supported(const AttnDesc& d);
-bool attn_bwd_takes_ds(const AttnDesc& d, const float* ws);
+// The one predicate of the dS path: ds given, 16-byte aligned, on attn_bwd_ds_supported's shapes.
+// The forward's bf16 kernel, the split q / k inputs and the backward all follow it, so a forward
+// and its backward always form P from the same products (the backward then needs the workspace).
+bool attn_ds_path(const AttnDesc& d);
+// bytes of the dS scratch: batch * heads * seq^2 entries of 4 bytes, 2 for bf16 (d.bf16)
 size_t attn_bwd_ds_bytes(const AttnDesc& d);
 // Whether attn_bwd_launch reads its workspace: the split dQ / dK-dV kernels of seq > 32 keep
 // D = rowsum(dO * O) there; the single-block kernel of seq <= 32 forms D in registers.

@@ -296,6 +296,13 @@ static int alloc_mla_layer(talos_plan_s* p, const MlaDims& D, talos_plan_s::Laye
   rc |= plan_alloc(p, &L.lse, M * H);
   return rc ? TALOS_ERR_ALLOC : TALOS_OK;
 }
+// The largest dS buffer an MLA plan allocates: 4 GiB (B * H * S^2 entries; C5 needs 134 MB in
+// fp32, seq 2048 at batch 64 and 8 heads 8.6 GB). TALOS_DS_BUDGET_MB at plan creation overrides
+// it (0 turns the dS path off).
+static size_t ds_budget_bytes() {
+  if (const char* e = std::getenv("TALOS_DS_BUDGET_MB")) return (size_t)std::strtoull(e, nullptr, 10) << 20;
+  return size_t(4) << 30;
+}
 static int alloc_mla_scratch(talos_plan_s* p, const MlaDims& D) {
   const size_t M = (size_t)D.batch * D.seq, H = D.H, td = (size_t)D.hd + D.r;
   auto& m = p->ms;
@@ -305,16 +312,29 @@ static int alloc_mla_scratch(talos_plan_s* p, const MlaDims& D) {
   for (float** b : {&m.dq, &m.dk}) rc |= plan_alloc(p, b, M * H * td);
   rc |= plan_alloc(p, &m.dv, M * H * D.vd);
   rc |= plan_alloc(p, &m.dckv, M * D.L);
+  if (rc) return TALOS_ERR_ALLOC;
   {
+    // the dS rows of the attention backward (B * H * S^2 entries, 2 bytes each in bf16 plans):
+    // taken within ds_budget_bytes() and when the allocation succeeds; otherwise m.ds stays null,
+    // and the forward and backward both take the tiled path, whose scratch is O(S)
     AttnDesc ad;
     ad.batch = D.batch;
     ad.seq = D.seq;
     ad.heads = D.H;
     ad.dk = (int)td;
     ad.dv = D.vd;
-    if (!p->unfused && attn_bwd_ds_supported(ad)) rc |= plan_alloc(p, &m.ds, attn_bwd_ds_bytes(ad) / sizeof(float));
+    ad.bf16 = p->bf16 ? 1 : 0;
+    const size_t bytes = attn_bwd_ds_bytes(ad);
+    if (!p->unfused && bytes && bytes <= ds_budget_bytes()) {
+      void* ptr = nullptr;
+      if (hipMalloc(&ptr, bytes) == hipSuccess) {
+        p->allocs.push_back(ptr);
+        m.ds = static_cast<float*>(ptr);
+      } else {
+        (void)hipGetLastError();  // clear the failed allocation; the plan runs without dS
+      }
+    }
   }
-  if (rc) return TALOS_ERR_ALLOC;
   // split-K workspace of the weight-gradient products
   for (auto rc2 : {std::make_pair(D.d, D.H * D.hd), std::make_pair(D.d, D.H * D.r), std::make_pair(D.L, D.H * D.hd),
                    std::make_pair(D.L, D.H * D.vd), std::make_pair(D.d, D.L), std::make_pair(D.H * D.vd, D.d)})
@@ -649,7 +669,7 @@ static AttnDesc mla_attn_desc(talos_plan_s* p, const MlaDims& D, const talos_pla
 // The fp32 kernels' split twins spill at C5's head dims (27-48 VGPRs) and measured slower than the
 // two concatenation copies they replace, so fp32 plans keep the copies.
 static bool mla_split_qk(talos_plan_s* p, AttnDesc& a) {
-  if (!p->bf16 || !attn_bwd_takes_ds(a, p->attn_ws)) return false;
+  if (!p->bf16 || !attn_ds_path(a)) return false;
   const int hd = a.rope_off, r = a.rope_dim;
   const long long MH = (long long)a.batch * a.seq * a.heads;
   a.ldq = (long long)a.heads * hd;
@@ -723,7 +743,7 @@ static int mla_attn_backward(talos_plan_s* p, const MlaDims& D, const float* P, 
   a.dout = g_o;
   a.lddo = (long long)H * vd;
   int rc;
-  if (attn_bwd_takes_ds(a, p->attn_ws)) {
+  if (attn_ds_path(a)) {
     // the content and rope parts of dq / dk to their own buffers (and, for bf16 plans, the
     // forward's split q / k halves in)
     mla_split_qk(p, a);

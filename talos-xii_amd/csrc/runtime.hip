@@ -359,6 +359,8 @@ int talos_workspace_bind(void* ptr, size_t bytes) {
 
 size_t talos_workspace_high_water(void) { return t_ws_high; }
 
+size_t talos_workspace_bytes(void) { return bound_workspace_bytes(); }
+
 int talos_device_info(char* name, size_t name_len, int* cu_count, int* clock_khz, size_t* total_mem) {
   TALOS_DEVICE();
   hipDeviceProp_t prop;

@@ -41,17 +41,30 @@ void require(bool c, const std::string& msg) {
 }
 
 // The scratch of the library calls made by this thread's ops (split-K partials, reduction
-// partials, attention rows): one device buffer bound on the thread's first op and kept for the
-// life of the process, so an op never allocates scratch per call (a split-K product splits fewer
-// times rather than outgrow it). Every op runs on the null stream, so calls sharing it never overlap.
+// partials, attention rows): one device buffer bound on the thread's first op and held until the
+// thread exits, so an op never allocates scratch per call (a split-K product splits fewer times
+// rather than outgrow it). Every op runs on the null stream, so calls sharing it never overlap.
+// A workspace the caller bound on this thread before its first op stays bound instead.
 constexpr size_t kTapeWorkspaceBytes = size_t(16) << 20;
+struct TapeWorkspace {
+  void* ptr = nullptr;
+  bool checked = false;
+  ~TapeWorkspace() {  // thread exit: unbind and free (a pool thread that ends leaks nothing)
+    if (ptr) {
+      talos_workspace_bind(nullptr, 0);
+      talos_free(ptr);
+    }
+  }
+};
 void bind_workspace_once() {
-  thread_local bool bound = false;
-  if (bound) return;
+  thread_local TapeWorkspace ws;
+  if (ws.checked) return;
+  ws.checked = true;
+  if (talos_workspace_bytes() > 0) return;
   void* p = nullptr;
   ok(talos_malloc(&p, kTapeWorkspaceBytes), "talos_malloc (tape workspace)");
+  ws.ptr = p;
   ok(talos_workspace_bind(p, kTapeWorkspaceBytes), "talos_workspace_bind");
-  bound = true;
 }
 
 // A new tensor with zeroed grad; data left for the op to fill.

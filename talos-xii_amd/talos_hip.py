@@ -80,6 +80,7 @@ _SIGS = {
     "talos_last_error": [],
     "talos_workspace_bind": [_vp, _sz],
     "talos_workspace_high_water": [],
+    "talos_workspace_bytes": [],
     "talos_version": [],
     "talos_init": [],
     "talos_device_count": [ctypes.POINTER(_i)],
@@ -169,7 +170,7 @@ class ProfRecord(ctypes.Structure):
     _fields_ = [("kernel", ctypes.c_char * 64), ("flops", ctypes.c_double), ("bytes", ctypes.c_double),
                 ("ms", ctypes.c_float)]
 _RESTYPE = {"talos_last_error": ctypes.c_char_p, "talos_version": ctypes.c_char_p, "talos_workspace_high_water": _sz,
-            "talos_grad_sumsq_workspace_bytes": _sz, "talos_ppo_update_work_bytes": _sz, "talos_block_param_count": _sz, "talos_ppo_param_count": _sz, "talos_mla_param_count": _sz}
+            "talos_workspace_bytes": _sz, "talos_grad_sumsq_workspace_bytes": _sz, "talos_ppo_update_work_bytes": _sz, "talos_block_param_count": _sz, "talos_ppo_param_count": _sz, "talos_mla_param_count": _sz}
 
 _lib = None
 

@@ -119,3 +119,18 @@ def ppo_step_flops(B, S, in_dim, d, L, H, F, A, causal=True, live=True):
     last_bwd = 2 * (proj_kv + proj_q + proj_o + mlp) + 5 * 2 * B * H * hd * S
     rest = (L - 1) * layer + embed + heads
     return 3 * rest - embed + last_fwd + last_bwd
+
+def ppo_step_executed_flops(B, S, in_dim, d, L, H, F, A, causal=True):
+    """The flops the PPO plan's kernels execute for the live work (ppo_step_flops(live=True)),
+    where the last layer's value projection is absorbed into its last-query attention (four heads
+    of 32 at d 128): the value rows v_j = xn1_j Wv over all M rows (forward, their input gradient
+    and Wv's gradient, 3 * 2 M d^2) are never formed. In their place the forward forms
+    z_h = sum_j p_j xn1_j per (sample, head) and o_h = z_h Wv_h; the backward u_h = Wv_h dO_h,
+    dP_j = xn1_j . u_h, the value path's share sum_h p_j^h u_h of each row's input gradient, and
+    dWv = sum_b z_bh^T dO_bh."""
+    live = ppo_step_flops(B, S, in_dim, d, L, H, F, A, causal)
+    if L == 0 or not (H == 4 and d == 128):
+        return live
+    M = B * S
+    absorbed = 3 * 2 * B * H * S * d + 3 * 2 * B * d * d
+    return live - 3 * 2 * M * d * d + absorbed

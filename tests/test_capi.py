@@ -169,7 +169,9 @@ def test_workspace_bind_validation():
     assert L.talos_workspace_bind(ctypes.c_void_p(4096 + 16), 4096) == th.ERR_SHAPE
     assert L.talos_workspace_bind(ctypes.c_void_p(4096), 4096) == th.OK
     assert L.talos_workspace_high_water() == 0
+    assert L.talos_workspace_bytes() == 4096
     assert L.talos_workspace_bind(None, 0) == th.OK
+    assert L.talos_workspace_bytes() == 0
 
 
 def test_completion_mode_switch():

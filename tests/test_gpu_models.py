@@ -201,6 +201,38 @@ def test_mla_fwd_bwd_vs_oracle(oracle, ci):
         check_grad(dp[sl], dp_r[sl], mag[sl], name=f"d{n}")
 
 
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_mla_without_ds_buffer_vs_oracle(oracle, monkeypatch, prec):
+    """With the dS budget at 0 (TALOS_DS_BUDGET_MB=0 at plan creation) the MLA plan keeps no dS
+    rows: its forward and backward both take the tiled path (fp32 attention, also in a bf16 plan)
+    and still match the oracle, at seq 132 (causal, C5's head dims) where the dS path would run."""
+    from common import BF16_RTOL, mla_params
+    monkeypatch.setenv("TALOS_DS_BUDGET_MB", "0")
+    ci = [1, 132, 512, 8, 128, 32, 64, 64, 1, 0]
+    rng = np.random.default_rng(4100)
+    p = f32(mla_params(rng, ci))
+    x, G = f32(rng.normal(size=(1, 132, 512))), f32(rng.normal(size=(1, 132, 512)))
+    out_r, dp_r, dx_r, mag = oracle.mla_fwd_bwd(ci, 1e-5, 10000.0, p, x, G, mag=True)
+    out, dp, dx = run_mla(ci, th.PREC_FP32 if prec == "fp32" else th.PREC_BF16, p, x, G)
+    if prec == "fp32":
+        check_close(out, out_r, name="out")
+        check_close(dx, dx_r, name="dx")
+        for n, sl in mla_slices(ci).items():
+            check_grad(dp[sl], dp_r[sl], mag[sl], name=f"d{n}")
+    else:
+        for name, got, ref in [("out", out, out_r), ("dx", dx, dx_r)] + [(f"d{n}", dp[sl], dp_r[sl])
+                                                                          for n, sl in mla_slices(ci).items()]:
+            assert float(np.abs(got - ref).max() / np.abs(ref).max()) <= BF16_RTOL, name
+
+
+def test_mla_plan_over_ds_budget_is_created():
+    """A plan whose dS rows would exceed the budget (seq 2048 at batch 64, 8 heads: 8.6 GB in
+    fp32, 4.3 GB in bf16, against 4 GiB) is still created, on the tiled path."""
+    for prec in (th.PREC_FP32, th.PREC_BF16):
+        plan = th.Plan("mla", th.MlaCfg(64, 2048, 512, 8, 128, 32, 64, 64, 0, prec, 1e-5, 10000.0))
+        plan.destroy()
+
+
 # seq 100 / 132 / 256 reach the bf16 tiled forward and dS backward (causal with ragged tiles,
 # C5's head dims non-causal); at 37 and 64 attention runs in fp32
 @pytest.mark.parametrize("ci", [[2, 37, 64, 2, 32, 8, 16, 16, 1, 0], [2, 64, 512, 8, 128, 32, 64, 64, 0, 0],
