@@ -176,6 +176,46 @@ def test_c2_rmsnorm_fwd_bwd_vs_oracle(oracle):
     check_close(dwo.numpy(), 2 * dw_r, name="dgain accumulate")
 
 
+# (rows, dim): 256 partial rows (C2), 34, 1024 (two rows a wave), 19, a single partial, and the
+# generic kernel (dim 1000)
+@pytest.mark.parametrize("rows,dim", [(4096, 256), (16 * 33 + 5, 128), (40000, 256), (300, 100), (7, 512),
+                                      (37, 1000)])
+def test_rmsnorm_bwd_workspace_deterministic(oracle, rows, dim):
+    """talos_rmsnorm_bwd_f32 from a bound workspace (the C2 bench's mode): it matches the oracle,
+    repeated calls give the same bits (the gain gradient's partial rows are added in a fixed
+    order), and the accumulate mode adds onto dx and dgain."""
+    from common import check_grad
+    rng = np.random.default_rng(rows + dim)
+    eps = 1e-6
+    x, g = f32(rng.normal(size=(rows, dim))), f32(rng.normal(size=(rows, dim)))
+    w = f32(rng.uniform(0.9, 1.1, dim))
+    y_r, dx_r, dw_r = oracle.rmsnorm_fwd_bwd(x, w, g, eps)
+    xh = x / np.sqrt((x * x).mean(1, keepdims=True) + eps)
+    mag = np.abs(g * xh).sum(0)  # the gain gradient's magnitude sums
+    ws = DA.zeros(1 << 20)
+    th.call("talos_workspace_bind", ws.ptr, 4 << 20)
+    try:
+        dx_, dw_, dg_ = DA.from_numpy(x), DA.from_numpy(w), DA.from_numpy(g)
+        y, rstd, dxo, dwo = DA.zeros((rows, dim)), DA.zeros(rows), DA.zeros((rows, dim)), DA.zeros(dim)
+        th.call("talos_rmsnorm_fwd_f32", rows, dim, eps, dx_.ptr, dw_.ptr, y.ptr, rstd.ptr, None)
+        th.call("talos_rmsnorm_bwd_f32", rows, dim, dx_.ptr, dw_.ptr, rstd.ptr, dg_.ptr, 0.0, dxo.ptr, 0.0, dwo.ptr,
+                None)
+        first_dx, first_dw = dxo.numpy(), dwo.numpy()
+        check_close(first_dx, dx_r, name="dx")
+        check_grad(first_dw, dw_r, mag, name="dgain")
+        for _ in range(3):
+            th.call("talos_rmsnorm_bwd_f32", rows, dim, dx_.ptr, dw_.ptr, rstd.ptr, dg_.ptr, 0.0, dxo.ptr, 0.0,
+                    dwo.ptr, None)
+            assert np.array_equal(dwo.numpy(), first_dw) and np.array_equal(dxo.numpy(), first_dx)
+        th.call("talos_rmsnorm_bwd_f32", rows, dim, dx_.ptr, dw_.ptr, rstd.ptr, dg_.ptr, 1.0, dxo.ptr, 1.0, dwo.ptr,
+                None)
+        check_close(dxo.numpy(), 2 * dx_r, name="dx accumulate")
+        check_grad(dwo.numpy(), 2 * dw_r, 2 * mag, name="dgain accumulate")
+    finally:
+        th.call("talos_workspace_bind", None, 0)
+        ws.free()
+
+
 @pytest.mark.parametrize("dim", [8, 100, 128, 512, 1000])
 def test_rmsnorm_dims(oracle, dim):
     rng = np.random.default_rng(dim)
