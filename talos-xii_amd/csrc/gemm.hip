@@ -54,6 +54,14 @@ constexpr int NT = 256;
 #define TALOS_SPLITK_MIN_K 512
 #endif
 constexpr int NBUF = TALOS_GEMM_DBUF ? 2 : 1;
+// Rows whose operands the 64-row norm-backward epilogue keeps in flight ahead of the row it
+// finishes (normb_rows), without and with the last-row addends.
+#ifndef TALOS_NB_AHEAD
+#define TALOS_NB_AHEAD 4
+#endif
+#ifndef TALOS_NB_AHEAD_LAST
+#define TALOS_NB_AHEAD_LAST 1
+#endif
 // Wave priority (s_setprio) of the main loop's products, 0..3 (1: C4 2.398 -> 2.388 ms).
 #ifndef TALOS_GEMM_PRIO
 #define TALOS_GEMM_PRIO 1
@@ -74,7 +82,8 @@ enum : int {
   E_NORM = 1024,  // also RMSNorm each output row (N = 128: the whole row is in the tile)
   E_NORMB = 2048,  // the output rows are dL/d(RMSNorm output): write that norm's backward instead
   E_NORMIN = 4096,  // RMSNorm A's rows first (GemmDesc::nin_*): B rows scaled by the gain, rows by rstd
-  E_NBPRE = 8192    // with E_NORMB: the addend sum_h P[row][h] U[sample][h] (four terms) before the norm backward
+  E_NBPRE = 8192,   // with E_NORMB: the addend sum_h P[row][h] U[sample][h] (four terms) before the norm backward
+  E_NBLAST = 32768  // with E_NORMB: the last-row addends (GemmDesc::normb_add_last / normb_dy_last) may be set
 };
 
 struct GemmArgs {
@@ -448,6 +457,75 @@ __device__ __forceinline__ NbIn normb_load(const GemmArgs& p, int row, int col) 
   in.x = on ? *reinterpret_cast<const float4*>(p.nb_x + (long long)row * p.N + col) : make_float4(0.f, 0.f, 0.f, 0.f);
   return in;
 }
+// Every operand of one row of the pipelined norm-backward epilogue (64-row tiles, E_NORMB without E_NBPRE),
+// loaded kNbAhead rows ahead of its use with no branch around a load: the last-row addends are
+// read for every row (a clamped, valid row) and kept only for the sample's last row, so the
+// compiler can wait for exactly the loads a row needs instead of all of them.
+struct NbRow {
+  float4 x, add, dyl, addl;
+  float r;
+  bool last;
+};
+// q, rem: the row's sample and its index in the sample (row = q * seq + rem); LAST: the product
+// may have last-row addends (E_NBLAST)
+template <bool LAST>
+__device__ __forceinline__ NbRow normb_row_load(const GemmArgs& p, int row, int q, int rem, int col) {
+  NbRow in;
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+  const bool on = row < p.M;
+  const int rr = on ? row : 0;
+  in.r = on ? p.nb_rstd[rr] : 0.f;
+  in.x = *reinterpret_cast<const float4*>(p.nb_x + (long long)rr * p.N + col);
+  in.add = p.nb_add ? *reinterpret_cast<const float4*>(p.nb_add + (long long)rr * p.N + col) : z;
+  if (!on) in.x = in.add = z;
+  in.dyl = in.addl = z;
+  in.last = false;
+  if (LAST && (p.nb_add_last || p.nb_dy_last)) {  // uniform
+    const int qq = on ? q : 0;
+    int lr = p.nb_seq - 1;
+    if (p.nb_lens) {
+      const int L = p.nb_lens[qq];
+      lr = (L < 1 ? 1 : (L > p.nb_seq ? p.nb_seq : L)) - 1;
+    }
+    in.last = on && rem == lr;
+    const float4 dyl = p.nb_dy_last ? *reinterpret_cast<const float4*>(p.nb_dy_last + (long long)qq * p.N + col) : z;
+    const float4 addl = p.nb_add_last ? *reinterpret_cast<const float4*>(p.nb_add_last + (long long)qq * p.N + col) : z;
+    if (in.last) {
+      in.dyl = dyl;
+      in.addl = addl;
+    }
+  }
+  return in;
+}
+// The row's norm backward from its preloaded operands (normb_apply's arithmetic).
+__device__ __forceinline__ void normb_row_apply(const GemmArgs& p, float4 gg, int row, int col, const NbRow& in,
+                                                const float4& g, float4& dw) {
+  const bool on = row < p.M;
+  gg.x += in.dyl.x;
+  gg.y += in.dyl.y;
+  gg.z += in.dyl.z;
+  gg.w += in.dyl.w;
+  if (!on) gg = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float r = in.r;
+  const float4 xh = make_float4(in.x.x * r, in.x.y * r, in.x.z * r, in.x.w * r);
+  float dot = gg.x * g.x * xh.x + gg.y * g.y * xh.y + gg.z * g.z * xh.z + gg.w * g.w * xh.w;
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
+  const float md = dot * (1.0f / (float)p.N);
+  dw.x += gg.x * xh.x;
+  dw.y += gg.y * xh.y;
+  dw.z += gg.z * xh.z;
+  dw.w += gg.w * xh.w;
+  if (!on) return;
+  float4 o = make_float4(r * (gg.x * g.x - xh.x * md), r * (gg.y * g.y - xh.y * md), r * (gg.z * g.z - xh.z * md),
+                         r * (gg.w * g.w - xh.w * md));
+  o.x += in.add.x + in.addl.x;
+  o.y += in.add.y + in.addl.y;
+  o.z += in.add.z + in.addl.z;
+  o.w += in.add.w + in.addl.w;
+  *reinterpret_cast<float4*>(p.nb_dx + (long long)row * p.N + col) = o;
+}
+
 template <bool PRE>
 __device__ __forceinline__ void normb_apply(const GemmArgs& p, float4 gg, int row, int col, const NbIn& in,
                                             const float4& g, float4& dw) {
@@ -609,6 +687,54 @@ __device__ __forceinline__ int xcd_logical() {
 // One output tile of BMT (128 or 64) x 128 rows / columns for logical workgroup `logical` (in
 // [0, p.nblocks)): four waves, wave (wm, wn) the [BMT / 2, 64] block at rows wm BMT / 2,
 // columns 64 wn, as 2 x 2 (BMT = 128) or 1 x 2 (BMT = 64) 32 x 32 accumulators.
+// The accumulators of the waves staging a 64-row half into the tile T (row pitch T_S): 128-row
+// tiles (MT = 2) pass the half's waves' two 32-row blocks, 64-row tiles (MT = 1) every wave's one
+// (accumulator layout of v_mfma_f32_32x32x2_f32: lane l, register r holds row
+// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32 of its 32 x 32 block).
+template <int MT>
+__device__ __forceinline__ void stage_acc(float* T, const floatx16 (&acc)[MT][2], int wm, int wn, int h, int l32,
+                                          int) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = (MT == 1 ? wm * 32 : mt * 32) + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int c = wn * 64 + nt * 32 + l32;
+        T[row * T_S + c] = acc[mt][nt][r];
+      }
+}
+
+// The norm backward of the 64 staged rows of T (row pitch T_S; tile rows r0 - (t / 32) + 0..63):
+// thread t takes column group cg of rows r0 + 8 i, i < 8, with the operands of AHEAD rows in
+// flight ahead of the row it finishes; the row's sample q and its index rem in the sample are kept
+// incrementally (no division per row).
+template <int AHEAD, bool LAST>
+__device__ __forceinline__ void normb_rows(const GemmArgs& p, const float* T, int cg, int col, int r0,
+                                           const float4& g, float4& nbw) {
+  constexpr int RT = T_ROWS / 8;
+  int lq = r0 / p.nb_seq, lrem = r0 - lq * p.nb_seq;  // of the next row to load
+  auto load_next = [&](int i) {
+    const NbRow in = normb_row_load<LAST>(p, r0 + 8 * i, lq, lrem, col);
+    lrem += 8;
+    while (lrem >= p.nb_seq) {
+      lrem -= p.nb_seq;
+      ++lq;
+    }
+    return in;
+  };
+  NbRow in[RT];
+#pragma unroll
+  for (int i = 0; i < AHEAD; ++i) in[i] = load_next(i);
+#pragma unroll
+  for (int i = 0; i < RT; ++i) {
+    if (i + AHEAD < RT) in[i + AHEAD] = load_next(i + AHEAD);
+    const float4 v = *reinterpret_cast<const float4*>(T + ((threadIdx.x >> 5) + 8 * i) * T_S + cg);
+    normb_row_apply(p, v, r0 + 8 * i, col, in[i], g, nbw);
+  }
+}
+
 template <bool TA, bool TB, int E, bool BF, int BMT>
 __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
   __shared__ __align__(16) float smem[SMEM_FLOATS];
@@ -835,8 +961,22 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
   const bool aligned = ((p.ldc & 3) == 0) && (((E & E_RESID) == 0) || (p.ldr & 3) == 0) &&
                        (((E & (E_GELU | E_RELU | E_DGELU | E_DRELU)) == 0) || (p.ldaux & 3) == 0) &&
                        ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+  // E_NORMB on 64-row tiles: the whole tile is staged at once, so no accumulator is live in the
+  // epilogue, and each thread keeps the x, rstd and addend rows of a few rows in flight ahead of
+  // the row it finishes (normb_rows). (On 128-row tiles the second half's accumulators are live
+  // through the first half's epilogue, which leaves registers for x one row ahead; there the
+  // epilogue phase of the lockstep grid runs at the bandwidth of its mixed reads and writes, and
+  // deeper prefetching of the second half measured the same.)
+  constexpr bool NB_PIPE = (E & E_NORMB) != 0 && (E & E_NBPRE) == 0 && MT == 1;
+  if constexpr (NB_PIPE) {
+    constexpr bool LAST = (E & E_NBLAST) != 0;
+    stage_acc<MT>(T, acc, wm, wn, h, l32, 0);
+    __syncthreads();
+    const float4 g = *reinterpret_cast<const float4*>(p.nb_gain + col);
+    normb_rows<LAST ? TALOS_NB_AHEAD_LAST : TALOS_NB_AHEAD, LAST>(p, T, cg, col, m0 + (threadIdx.x >> 5), g, nbw);
+  }
 #pragma unroll
-  for (int half = 0; half < BMT / T_ROWS; ++half) {
+  for (int half = 0; half < (NB_PIPE ? 0 : BMT / T_ROWS); ++half) {
     if (half) __syncthreads();  // the first half has been read out
     if (MT == 1 || wm == half) {
 #pragma unroll
@@ -1284,6 +1424,7 @@ static int epi_flags(const GemmDesc& d) {
   if (d.norm_out) e |= E_NORM;
   if (d.normb_dx) e |= E_NORMB;
   if (d.normb_dx && d.normb_pre_p) e |= E_NBPRE;
+  if (d.normb_dx && (d.normb_add_last || d.normb_dy_last)) e |= E_NBLAST;
   if (d.nin_gain) e |= E_NORMIN;
   return e;
 }
@@ -1354,7 +1495,9 @@ static GemmKernel pick_kernel(bool tA, bool tB, int e, bool bf) {
   GEMM_CASE(false, true, E_DRELU)
   GEMM_CASE(false, true, E_SPLIT)
   GEMM_CASE_F32(false, true, E_NORMB)
+  GEMM_CASE_F32(false, true, E_NORMB | E_NBLAST)
   GEMM_CASE_F32(false, true, E_NORMB | E_NBPRE)
+  GEMM_CASE_F32(false, true, E_NORMB | E_NBPRE | E_NBLAST)
   GEMM_CASE(true, false, 0)
   GEMM_CASE(true, false, E_BETA)
   GEMM_CASE(true, false, E_SPLIT)
@@ -1405,6 +1548,7 @@ static GemmKernel pick_m64(bool tA, bool tB, int e) {
   if (tA) return nullptr;
   if (tB) {
     if (e == E_NORMB) return &gemm_f32_m64_kernel<false, true, E_NORMB>;
+    if (e == (E_NORMB | E_NBLAST)) return &gemm_f32_m64_kernel<false, true, E_NORMB | E_NBLAST>;
     if (e == 0) return &gemm_f32_m64_kernel<false, true, 0>;
     if (e == E_BETA) return &gemm_f32_m64_kernel<false, true, E_BETA>;
     return nullptr;

@@ -397,6 +397,8 @@ static int alloc_block_buffers(talos_plan_s* p, const talos_block_cfg& c, int n_
   ws = std::max(ws, align_ws(wgrad_ws(p, (int)M, (int)F, (int)d)) + wgrad_ws(p, (int)M, (int)d, (int)F));
   p->gemm_ws_bytes = std::max(p->gemm_ws_bytes, ws);
   size_t red = std::max(colsum_workspace_bytes((int)M, (int)F), rmsnorm_bwd_workspace_bytes((int)M, (int)d));
+  // the dgain partials of a dX product with the norm backward in its epilogue, one per 64-row tile
+  red = std::max(red, reduce_parts_workspace_bytes(((int)M + 63) / 64, (int)d));
   p->red_ws_bytes = std::max(p->red_ws_bytes, red);
   return upload_rope_table(p, c.seq, rope_width(c), c.rope_base);
 }
