@@ -447,7 +447,7 @@ def c5_line(steps, warmup, precision):
 
     ms = timed(step, steps, warmup)
     bf = precision == th.PREC_BF16
-    roof, kernels = dominant_roofline(plan, step, steps, "C5_bf16" if bf else "C5")
+    roof, kernels = dominant_roofline(plan, step, steps, "C5")
     M = B * S
     gemm = 2.0 * M * (d * L + L * H * hd + L * H * vd + d * H * hd + 2 * d * H * r + H * vd * d)
     attn = 2.0 * B * H * S * S * ((hd + r) + vd)

@@ -75,12 +75,14 @@ def bench_sentence(bench):
 
 
 def mfma_table(path, stats, simds):
-    """Per kernel: MFMA busy (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs) and the fp32
-    MFMA flops counted (SQ_INSTS_VALU_MFMA_MOPS_F32 x 512) per launch. GRBM_GUI_ACTIVE is reported
-    summed over the XCDs; the per-XCD cycle count is that sum divided by the XCD count, found as the
-    ratio of the sum to the cycles the kernel's duration holds at the measured clock."""
-    busy, gui, mops = (counters(path, c, scale=1.0) for c in
-                       ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_F32"))
+    """Per kernel: MFMA busy (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs) and the MFMA
+    flops counted per launch (SQ_INSTS_VALU_MFMA_MOPS_F32, and _BF16 when the pass collected it,
+    x 512). GRBM_GUI_ACTIVE is reported summed over the XCDs; the per-XCD cycle count is that sum
+    divided by the XCD count, found as the ratio of the sum to the cycles the kernel's duration
+    holds at the measured clock."""
+    busy, gui, mops, mops16 = (counters(path, c, scale=1.0) for c in
+                               ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_F32",
+                                "SQ_INSTS_VALU_MFMA_MOPS_BF16"))
     dur = {short(r["Name"]): float(r["AverageNs"]) for r in stats}
     rows = []
     for k in sorted(busy, key=lambda k: -sum(busy[k])):
@@ -90,8 +92,9 @@ def mfma_table(path, stats, simds):
         xcds = max(1, round(g / (dur.get(k, 0) * 2.1))) if dur.get(k) else 1  # ~2.1 GHz under load
         util = sum(busy[k]) / len(busy[k]) / (g / xcds * simds)
         fl = 512.0 * sum(mops.get(k, [0.0])) / max(1, len(mops.get(k, [])))
+        fl16 = 512.0 * sum(mops16.get(k, [0.0])) / max(1, len(mops16.get(k, [])))
         clock = g / xcds / dur[k] if dur.get(k) else 0.0
-        rows.append((k, len(busy[k]), util, fl, clock))
+        rows.append((k, len(busy[k]), util, fl, fl16, clock))
     return rows
 
 
@@ -127,13 +130,14 @@ def main():
     if a.mfma:
         rows = mfma_table(a.mfma, stats, a.simds)
         lines += ["", "Matrix-core counters (rocprofv3 --pmc, one pass):", "", "```", a.mfma_command, "```", "",
-                  f"MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x {a.simds} SIMDs); fp32 MFMA "
-                  "flops = SQ_INSTS_VALU_MFMA_MOPS_F32 x 512 per launch; clock = GRBM_GUI_ACTIVE per XCD / the "
-                  "kernel's average duration from the trace above.", "",
-                  "| kernel | launches | MFMA busy % | fp32 MFMA GFLOP/launch | clock GHz |",
-                  "|---|---:|---:|---:|---:|"]
-        for k, n, util, fl, clock in rows[:a.top]:
-            lines.append(f"| `{k}` | {n} | {100 * util:.1f} | {fl / 1e9:.3f} | {clock:.2f} |")
+                  f"MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x {a.simds} SIMDs); fp32 and "
+                  "bf16 MFMA flops = SQ_INSTS_VALU_MFMA_MOPS_F32 / _BF16 x 512 per launch (bf16 blank when the pass "
+                  "did not collect it); clock = GRBM_GUI_ACTIVE per XCD / the kernel's average duration from the "
+                  "trace above.", "",
+                  "| kernel | launches | MFMA busy % | fp32 MFMA GFLOP/launch | bf16 MFMA GFLOP/launch | clock GHz |",
+                  "|---|---:|---:|---:|---:|---:|"]
+        for k, n, util, fl, fl16, clock in rows[:a.top]:
+            lines.append(f"| `{k}` | {n} | {100 * util:.1f} | {fl / 1e9:.3f} | {fl16 / 1e9:.3f} | {clock:.2f} |")
     traffic = {}
     if a.fetch and a.write:
         copy_bytes = bench.get("copy_calibration_bytes") or (1024 << 20)
@@ -144,16 +148,24 @@ def main():
                   f"Calibration: a {copy_bytes >> 20} MiB device-to-device copy (x{nf}) reads FETCH_SIZE = "
                   f"{cf / 2**20:.1f} MiB and WRITE_SIZE = {cw / 2**20:.1f} MiB, so the factors are "
                   f"fetch x{ff:.3f}, write x{fw:.3f}.", "",
-                  "| kernel | launches | HBM read MB/launch | HBM write MB/launch |", "|---|---:|---:|---:|"]
+                  "Achieved = (read + write) / the kernel's average traced duration above, against the 8 TB/s "
+                  "HBM peak (the tracer adds its own time to short launches).", "",
+                  "| kernel | launches | HBM read MB/launch | HBM write MB/launch | achieved GB/s | of HBM peak |",
+                  "|---|---:|---:|---:|---:|---:|"]
         for k in sorted(f, key=lambda k: -sum(f[k])):
-            if k.startswith("__amd"):
+            # the runtime's copies (the calibration) and the set-up fills of plan buffers, whose
+            # launches differ in size between the traced and the counted run
+            if k.startswith("__amd") or k.startswith("fill_zero"):
                 continue
             rd = ff * sum(f[k]) / len(f[k])
             wr = fw * sum(w.get(k, [0.0])) / max(1, len(w.get(k, [])))
             traffic[k] = {"fetch_bytes": rd, "write_bytes": wr, "bytes": rd + wr}
+        dur = {short(r["Name"]): float(r["AverageNs"]) for r in stats}
         for k in list(traffic)[:a.top]:
             t = traffic[k]
-            lines.append(f"| `{k}` | {len(f[k])} | {t['fetch_bytes'] / 1e6:.1f} | {t['write_bytes'] / 1e6:.1f} |")
+            gbs = t["bytes"] / dur[k] if dur.get(k) else 0.0  # bytes / ns = GB/s
+            lines.append(f"| `{k}` | {len(f[k])} | {t['fetch_bytes'] / 1e6:.1f} | {t['write_bytes'] / 1e6:.1f} | "
+                         f"{gbs:.0f} | {gbs / 8000.0:.2f} |")
         if a.traffic_json:
             old = {}
             try:
