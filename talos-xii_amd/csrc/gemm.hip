@@ -129,6 +129,10 @@ struct GemmArgs {
   float* nb_dx;
   double* nb_part;
   int vecA, vecB;
+  const uint16_t* A16;  // bf16 copies of A / B (bf16-in products; GemmDesc::A16 / B16)
+  const uint16_t* B16;
+  uint16_t* C16;        // bf16 copy of C written by the epilogue
+  int vecA16, vecB16, vecC16;  // 16-byte rows of A16 / B16, 8-byte rows of C16
   int nblocks;  // tiles * batch * ksplit (the grid is padded to a multiple of 8)
 };
 
@@ -599,6 +603,8 @@ constexpr int SMEM_FLOATS = (2 * NBUF * PANEL > T_ROWS * T_S) ? 2 * NBUF * PANEL
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int BKB = 64;
 constexpr int PB = BKB + 8;
+// the bf16 main loop's LDS: two stages of the A and B panels (BM + BN rows of PB bf16), 73.7 KB
+constexpr int SMEM_BF = 2 * (BM + BN) * PB / 2;
 
 // round-to-nearest-even fp32 -> bf16 of two values, packed low | high: gfx950's
 // v_cvt_pk_bf16_f32, one instruction a pair (an integer rounding sequence of about six
@@ -657,6 +663,95 @@ __device__ __forceinline__ void load_bf(const float* __restrict__ X, long long l
   }
 }
 
+// A panel read from a bf16 copy of the operand (already rounded), in 16-byte loads of 8 bf16 (a
+// panel is 4 loads a thread, half the load instructions of load_bf's float4 reads or of 8-byte
+// reads, which is what bounds the bf16 main loop: the per-instruction cost of the texture
+// address and data path, not bytes or latency). Layout of o[16] (store_bf16src):
+//  KC = true  (rows r k-contiguous): o[4i .. 4i + 3] = row (t >> 3) + 32 i, k 8 (t & 7) .. + 7.
+//  KC = false (k rows, r contiguous): thread (cg = t & 15, q = t >> 4) loads k rows 4q .. 4q + 3
+//    of columns 8 cg .. 8 cg + 7; o[2c], o[2c + 1] = column 8 cg + c, k 4q .. 4q + 3 (pairs).
+template <bool KC>
+__device__ __forceinline__ void load_bf16src(const uint16_t* __restrict__ X, long long ld, int r0, int rlim, int k0,
+                                             int kend, bool fast, bool vec, uint32_t (&o)[16]) {
+  const int t = threadIdx.x;
+  auto piece = [&](const uint16_t* src, bool full, int valid) {  // 8 values, zero past valid
+    if (full) return *reinterpret_cast<const uint4*>(src);
+    uint32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = j < valid ? src[j] : 0u;
+    return make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16));
+  };
+  if (KC) {
+    const int k = k0 + 8 * (t & 7);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = r0 + (t >> 3) + 32 * i;
+      const int valid = r < rlim ? min(8, kend - k) : 0;
+      const uint4 w = piece(X + (long long)r * ld + k, fast || (vec && valid == 8), valid);
+      o[4 * i] = w.x;
+      o[4 * i + 1] = w.y;
+      o[4 * i + 2] = w.z;
+      o[4 * i + 3] = w.w;
+    }
+  } else {
+    const int r = r0 + 8 * (t & 15), kq = k0 + 4 * (t >> 4);
+    uint4 w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = kq + j;
+      const int valid = k < kend ? min(8, rlim - r) : 0;
+      w[j] = piece(X + (long long)k * ld + r, fast || (vec && valid == 8), valid);
+    }
+    auto pack = [&](int u, uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3) {  // columns 2u, 2u + 1
+      o[4 * u] = (x0 & 0xffffu) | (x1 << 16);
+      o[4 * u + 1] = (x2 & 0xffffu) | (x3 << 16);
+      o[4 * u + 2] = (x0 >> 16) | (x1 & 0xffff0000u);
+      o[4 * u + 3] = (x2 >> 16) | (x3 & 0xffff0000u);
+    };
+    pack(0, w[0].x, w[1].x, w[2].x, w[3].x);
+    pack(1, w[0].y, w[1].y, w[2].y, w[3].y);
+    pack(2, w[0].z, w[1].z, w[2].z, w[3].z);
+    pack(3, w[0].w, w[1].w, w[2].w, w[3].w);
+  }
+}
+
+// Stores load_bf16src's o[16] into a k-contiguous panel (rows of PB bf16).
+template <bool KC>
+__device__ __forceinline__ void store_bf16src(uint16_t* S, const uint32_t (&o)[16]) {
+  const int t = threadIdx.x;
+  if (KC) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = (t >> 3) + 32 * i;
+      *reinterpret_cast<uint4*>(S + r * PB + 8 * (t & 7)) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    }
+  } else {
+    // eight 8-byte pieces, rows 8 cg + c. Rows 8 apart are 8 * 36 = 32 mod 64 banks apart, so in
+    // one store the 16 lanes of a row group would share two bank pairs; lane cg writes its columns
+    // in the rotated order c = (i + cg) & 7 instead (rotation by three conditional shifts), which
+    // leaves at most two lanes on a bank pair.
+    const int cg = t & 15, kq = 4 * (t >> 4);
+    uint2 g[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) g[c] = make_uint2(o[2 * c], o[2 * c + 1]);
+#pragma unroll
+    for (int sh = 1; sh < 8; sh *= 2) {
+      if (cg & sh) {
+        uint2 h[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) h[c] = g[(c + sh) & 7];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) g[c] = h[c];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 8 * cg + ((i + cg) & 7);
+      *reinterpret_cast<uint2*>(S + r * PB + kq) = g[i];
+    }
+  }
+}
+
 template <bool KC>
 __device__ __forceinline__ void store_bf(uint16_t* S, const uint32_t (&o)[16]) {
   const int t = threadIdx.x;
@@ -666,11 +761,34 @@ __device__ __forceinline__ void store_bf(uint16_t* S, const uint32_t (&o)[16]) {
       const int r = (t >> 4) + 16 * i;
       *reinterpret_cast<uint2*>(S + r * PB + 4 * (t & 15)) = make_uint2(o[2 * i], o[2 * i + 1]);
     }
-  } else {  // four 16-byte row pieces
+  } else {
+    // four 16-byte row pieces, rows 4 (t & 31) + j. Rows 4 apart are 4 * 36 = 16 mod 64 banks
+    // apart, so in one store lanes 4 apart would meet on the same banks (4-way conflict); lane
+    // group q = (t >> 2) & 3 writes its pieces in the rotated order j = (i + q) & 3 instead, which
+    // moves those lanes 36 banks further per step and spreads 16 lanes over 16 distinct bank
+    // groups. The rotation is two conditional swaps of whole pieces.
+    const int q = (t >> 2) & 3;
+    uint4 g[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = 4 * (t & 31) + j, k = 8 * (t >> 5);
-      *reinterpret_cast<uint4*>(S + r * PB + k) = make_uint4(o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]);
+    for (int j = 0; j < 4; ++j) g[j] = make_uint4(o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]);
+    if (q & 1) {
+      const uint4 g0 = g[0];
+      g[0] = g[1];
+      g[1] = g[2];
+      g[2] = g[3];
+      g[3] = g0;
+    }
+    if (q & 2) {
+      const uint4 g0 = g[0], g1 = g[1];
+      g[0] = g[2];
+      g[1] = g[3];
+      g[2] = g0;
+      g[3] = g1;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * (t & 31) + ((i + q) & 3), k = 8 * (t >> 5);
+      *reinterpret_cast<uint4*>(S + r * PB + k) = g[i];
     }
   }
 }
@@ -737,8 +855,9 @@ __device__ __forceinline__ void normb_rows(const GemmArgs& p, const float* T, in
 
 template <bool TA, bool TB, int E, bool BF, int BMT>
 __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
-  __shared__ __align__(16) float smem[SMEM_FLOATS];
+  __shared__ __align__(16) float smem[BF ? SMEM_BF : SMEM_FLOATS];
   static_assert(BMT == 128 || (BMT == 64 && !BF), "64-row tiles are fp32 only");
+  static_assert(SMEM_BF >= T_ROWS * T_S, "the staged output tile fits the bf16 panels");
   constexpr int MT = BMT / 64;  // 32-row accumulator blocks per wave
   // panels: As buffer i at smem + i*PANEL, Bs buffer i after the NBUF A buffers
   float* const Abase = smem;
@@ -772,25 +891,41 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
   float csum = 0.f;  // E_DBIAS: this thread's column sum over its half of each panel
   if constexpr (BF && BMT == 128) {
     static_assert((E & E_DBIAS) == 0, "the bf16 path has no fused bias gradient");
-    uint16_t* As16 = reinterpret_cast<uint16_t*>(smem);
-    uint16_t* Bs16 = As16 + BM * PB;
-    uint32_t pa[16], pb[16];
-    auto load = [&](int k0) {
-      const bool fast = interior && k0 + BKB <= kend;
-      load_bf<!TA>(A, p.lda, m0, p.M, k0, kend, fast, p.vecA, pa);
-      load_bf<TB>(B, p.ldb, n0, p.N, k0, kend, fast, p.vecB, pb);
+    // Two LDS stages of [A panel | B panel] and two register sets: chunk i's products read stage
+    // i & 1; then the registers holding chunk i + 1 (loaded two chunks earlier) go to the other
+    // stage and take the loads of chunk i + 3. So a chunk's loads have two chunks of products and
+    // barriers to land, and there is one barrier a chunk.
+    constexpr int STAGE = (BM + BN) * PB;
+    uint16_t* const S16 = reinterpret_cast<uint16_t*>(smem);
+    uint32_t pa0[16], pb0[16], pa1[16], pb1[16];
+    // from the operands' bf16 copies where given (uniform branches)
+    const uint16_t* A16 = p.A16 ? p.A16 + (long long)b * p.sA : nullptr;
+    const uint16_t* B16 = p.B16 ? p.B16 + (long long)b * p.sB : nullptr;
+    const bool tile_in = m0 + BMT <= p.M && n0 + BN <= p.N;
+    auto load = [&](int k0, uint32_t(&pa)[16], uint32_t(&pb)[16]) {
+      if (A16)
+        load_bf16src<!TA>(A16, p.lda, m0, p.M, k0, kend, tile_in && p.vecA16 && k0 + BKB <= kend, p.vecA16, pa);
+      else
+        load_bf<!TA>(A, p.lda, m0, p.M, k0, kend, interior && k0 + BKB <= kend, p.vecA, pa);
+      if (B16)
+        load_bf16src<TB>(B16, p.ldb, n0, p.N, k0, kend, tile_in && p.vecB16 && k0 + BKB <= kend, p.vecB16, pb);
+      else
+        load_bf<TB>(B, p.ldb, n0, p.N, k0, kend, interior && k0 + BKB <= kend, p.vecB, pb);
     };
-    if (kbeg < kend) {
-      load(kbeg);
-      store_bf<!TA>(As16, pa);
-      store_bf<TB>(Bs16, pb);
-    }
-    __syncthreads();
-    for (int k0 = kbeg; k0 < kend; k0 += BKB) {
-      const bool more = k0 + BKB < kend;
-      if (more) load(k0 + BKB);
-      const uint16_t* ap = As16 + (wm * 64 + l32) * PB + 8 * h;
-      const uint16_t* bp = Bs16 + (wn * 64 + l32) * PB + 8 * h;
+    auto store = [&](uint16_t* S, const uint32_t(&pa)[16], const uint32_t(&pb)[16]) {
+      if (A16)
+        store_bf16src<!TA>(S, pa);
+      else
+        store_bf<!TA>(S, pa);
+      if (B16)
+        store_bf16src<TB>(S + BM * PB, pb);
+      else
+        store_bf<TB>(S + BM * PB, pb);
+    };
+    // chunk k0 from stage st; (ra, rb) hold chunk k0 + BKB
+    auto step = [&](int k0, int st, uint32_t(&ra)[16], uint32_t(&rb)[16]) {
+      const uint16_t* ap = S16 + st * STAGE + (wm * 64 + l32) * PB + 8 * h;
+      const uint16_t* bp = S16 + st * STAGE + BM * PB + (wn * 64 + l32) * PB + 8 * h;
 #pragma unroll
       for (int s = 0; s < BKB / 16; ++s) {
         const bf16x8 a0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(ap + 16 * s));
@@ -802,14 +937,55 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
         acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
         acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[1][1], 0, 0, 0);
       }
+      if (k0 + BKB < kend) {
+        store(S16 + (st ^ 1) * STAGE, ra, rb);
+        if (k0 + 3 * BKB < kend) load(k0 + 3 * BKB, ra, rb);
+      }
       __syncthreads();
-      if (more) {
-        store_bf<!TA>(As16, pa);
-        store_bf<TB>(Bs16, pb);
+    };
+    if (A16 && B16) {
+      if (kbeg < kend) {
+        load(kbeg, pa0, pb0);
+        store(S16, pa0, pb0);
+        if (kbeg + BKB < kend) load(kbeg + BKB, pa1, pb1);
+        if (kbeg + 2 * BKB < kend) load(kbeg + 2 * BKB, pa0, pb0);
+      }
+      __syncthreads();
+      for (int k0 = kbeg; k0 < kend; k0 += 2 * BKB) {
+        step(k0, 0, pa1, pb1);
+        if (k0 + BKB < kend) step(k0 + BKB, 1, pa0, pb0);
+      }
+    } else {
+      // an fp32 operand is rounded as it is loaded, which makes the wave wait for its loads
+      // there: one register set and one stage, the next chunk's loads issued before the products
+      if (kbeg < kend) {
+        load(kbeg, pa0, pb0);
+        store(S16, pa0, pb0);
+      }
+      __syncthreads();
+      for (int k0 = kbeg; k0 < kend; k0 += BKB) {
+        const bool more = k0 + BKB < kend;
+        if (more) load(k0 + BKB, pa0, pb0);
+        const uint16_t* ap = S16 + (wm * 64 + l32) * PB + 8 * h;
+        const uint16_t* bp = S16 + BM * PB + (wn * 64 + l32) * PB + 8 * h;
+#pragma unroll
+        for (int s = 0; s < BKB / 16; ++s) {
+          const bf16x8 a0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(ap + 16 * s));
+          const bf16x8 a1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(ap + 32 * PB + 16 * s));
+          const bf16x8 b0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(bp + 16 * s));
+          const bf16x8 b1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(bp + 32 * PB + 16 * s));
+          acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
+          acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc[0][1], 0, 0, 0);
+          acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
+          acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[1][1], 0, 0, 0);
+        }
         __syncthreads();
+        if (more) {
+          store(S16, pa0, pb0);
+          __syncthreads();
+        }
       }
     }
-    if (kbeg >= kend) __syncthreads();
   } else {
   float4 ra[BMT / 32], rb[4];
   // E_NORMIN: this thread's sum of squares over the A values it loads (thread t and t + 128 load
@@ -1048,6 +1224,17 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
           const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
           const float4 o = epi_store4<E, true>(p, v, row, col, C, resid, fast && row < p.M, pre[j]);
           if constexpr ((E & E_NORM) != 0) epi_norm4(p, o, row, col, ngain);
+          if constexpr (BF) {
+            if (p.C16 && row < p.M) {  // the bf16 copy of the stored values
+              uint16_t* c16 = p.C16 + (long long)b * p.sC + (long long)row * p.ldc + col;
+              if (fast && p.vecC16) {
+                *reinterpret_cast<uint2*>(c16) = make_uint2(pack_bf16(o.x, o.y), pack_bf16(o.z, o.w));
+              } else {
+                const float oo[4] = {o.x, o.y, o.z, o.w};
+                for (int q = 0; q < 4 && col + q < p.N; ++q) c16[q] = (uint16_t)(pack_bf16(oo[q], 0.f) & 0xffffu);
+              }
+            }
+          }
         }
       }
     }
@@ -1400,6 +1587,18 @@ static GemmArgs to_args(const GemmDesc& d) {
   };
   a.vecA = aligned(d.A, d.lda) && (d.batch == 1 || d.sA % 4 == 0);
   a.vecB = aligned(d.B, d.ldb) && (d.batch == 1 || d.sB % 4 == 0);
+  auto aligned8 = [](const void* ptr, long long ld) {
+    return ((reinterpret_cast<uintptr_t>(ptr) & 7) == 0) && (ld % 4 == 0);
+  };
+  auto aligned16 = [](const void* ptr, long long ld) {
+    return ((reinterpret_cast<uintptr_t>(ptr) & 15) == 0) && (ld % 8 == 0);
+  };
+  a.A16 = d.bf16 ? d.A16 : nullptr;
+  a.B16 = d.bf16 ? d.B16 : nullptr;
+  a.C16 = d.bf16 ? d.C16 : nullptr;
+  a.vecA16 = a.A16 && aligned16(d.A16, d.lda) && (d.batch == 1 || d.sA % 8 == 0);
+  a.vecB16 = a.B16 && aligned16(d.B16, d.ldb) && (d.batch == 1 || d.sB % 8 == 0);
+  a.vecC16 = a.C16 && aligned8(d.C16, d.ldc) && (d.batch == 1 || d.sC % 4 == 0);
   if (a.ksplit > 1) {
     const int chunk = d.bf16 ? BKB : BK;
     int kper = (d.K + a.ksplit - 1) / a.ksplit;
@@ -1460,6 +1659,7 @@ size_t gemm_plan_split(GemmDesc& d, int num_cu) {
     d.ksplit = (int)std::max(1LL, ks);
   }
   if ((e & ~(E_BETA | E_BIAS | E_DBIAS)) != 0) d.ksplit = 1;  // only beta / bias survive a split
+  if (d.C16) d.ksplit = 1;  // the bf16 copy of C is written by the epilogue
   if (d.ksplit <= 1) return 0;
   GemmArgs a = to_args(d);
   return (size_t)a.ksplit * (d.M + (d.dbias ? 1 : 0)) * d.N * d.batch * sizeof(float);

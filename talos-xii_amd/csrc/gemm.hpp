@@ -27,6 +27,14 @@ struct GemmDesc {
   long long ldb = 0, sB = 0;
   float* C = nullptr;
   long long ldc = 0, sC = 0;
+  // bf16-in products (bf16 = true): optional bf16 copies of A / B (same layout, leading dimensions
+  // and batch strides, each value rounded to nearest even), which the staging reads instead of
+  // loading and rounding the fp32 operand; and C16, a bf16 copy of C (leading dimension ldc) that
+  // the epilogue also writes (not with a split K, the row norm or its backward, or an activation's
+  // saved input).
+  const uint16_t* A16 = nullptr;
+  const uint16_t* B16 = nullptr;
+  uint16_t* C16 = nullptr;
   float alpha = 1.f, beta = 0.f;
   const float* bias = nullptr;
   const float* resid = nullptr;

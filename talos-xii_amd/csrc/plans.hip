@@ -102,6 +102,18 @@ struct talos_plan_s {
     float *qc, *qr, *kc, *kr, *dq, *dk, *dv, *dqc, *dqr, *dkc, *dkr, *dckv;
     float* ds = nullptr;  // the attention backward's dS rows (attn_bwd_ds_supported)
   } ms{};
+  // bf16 MLA plans: bf16 copies of the fp32 tensors the bf16-in products read (an operand inside
+  // [base, base + n) is read from copy + offset), each written by the step that writes the tensor
+  // (the norm, a product's epilogue) or converted right after it (the attention's outputs and
+  // gradients; the caller's weights and output gradient at the start of a call, whose bases are
+  // set then)
+  struct Shadow {
+    const float* base;
+    size_t n;
+    uint16_t* copy;
+  };
+  std::vector<Shadow> shadows;
+  uint16_t *p16 = nullptr, *g16 = nullptr;  // the copies of the caller's weights and output gradient
   talos_mla_cfg mla{};
 };
 
@@ -283,6 +295,48 @@ static size_t wgrad_ws(talos_plan_s* p, int M_tok, int rows, int cols) {
   return gemm_plan_split(g, p->num_cu);
 }
 
+// A bf16 copy of n floats registered for base (nullptr: a caller's buffer, set per call).
+static uint16_t* add_shadow(talos_plan_s* p, const float* base, size_t n, int* rc) {
+  float* mem = nullptr;
+  *rc |= plan_alloc(p, &mem, (n + 1) / 2);
+  if (!mem) return nullptr;
+  p->shadows.push_back({base, n, reinterpret_cast<uint16_t*>(mem)});
+  return reinterpret_cast<uint16_t*>(mem);
+}
+static void set_shadow_base(talos_plan_s* p, const uint16_t* copy, const float* base) {
+  for (auto& sh : p->shadows)
+    if (sh.copy == copy) sh.base = base;
+}
+// The bf16 copy of the operand at ptr, or nullptr (fp32 plans keep none).
+static uint16_t* shadow_of(const talos_plan_s* p, const void* ptr) {
+  const float* f = static_cast<const float*>(ptr);
+  for (auto& sh : p->shadows)
+    if (sh.base && f >= sh.base && f < sh.base + sh.n) return sh.copy + (f - sh.base);
+  return nullptr;
+}
+static void bf16_operands(const talos_plan_s* p, GemmDesc& g) {
+  if (!p->bf16) return;
+  g.A16 = shadow_of(p, g.A);
+  g.B16 = shadow_of(p, g.B);
+  g.C16 = shadow_of(p, g.C);
+}
+// bf16 copies of the registered fp32 tensors starting at each of srcs (their producers just ran)
+static int refresh_shadows(talos_plan_s* p, std::initializer_list<const float*> srcs, hipStream_t s) {
+  const float* src[8];
+  uint16_t* dst[8];
+  long long n[8];
+  int k = 0;
+  for (const float* f : srcs)
+    for (auto& sh : p->shadows)
+      if (sh.base == f && k < 8) {
+        src[k] = f;
+        dst[k] = sh.copy;
+        n[k] = (long long)sh.n;
+        ++k;
+      }
+  return cvt_bf16_launch(k, src, dst, n, s);
+}
+
 // The saved activations of one latent attention (c_kv, v, q, k, o, lse) and, when scratch, the
 // buffers every layer shares (projections before concatenation, attention gradients).
 static int alloc_mla_layer(talos_plan_s* p, const MlaDims& D, talos_plan_s::Layer& L) {
@@ -450,6 +504,7 @@ static int mm_ws(talos_plan_s* p, hipStream_t s, float* wsp, int tA, int tB, int
   g.ldr = ldr;
   g.dbias = dbias;
   g.bf16 = p->bf16;
+  bf16_operands(p, g);
   g.ksplit = 0;
   const size_t ws = gemm_plan_split(g, p->num_cu);
   // the plan sizes its split-K workspace for the weight-gradient products; any other product
@@ -524,6 +579,7 @@ static GemmDesc wgrad_desc(const talos_plan_s* p, const WgradOp& w, float* wsp, 
   g.ldc = w.ldc;
   g.dbias = w.dbias;
   g.bf16 = p->bf16;
+  bf16_operands(p, g);
   g.ksplit = 0;
   size_t ws = gemm_plan_split(g, p->num_cu);
   if (ws > ws_bytes) {
@@ -708,6 +764,7 @@ static int mla_attn_forward(talos_plan_s* p, const MlaDims& D, const float* P, c
     g.rope_seq = D.seq;
     g.ksplit = 1;
     g.bf16 = p->bf16;
+    bf16_operands(p, g);
     return gemm_launch(g, s);
   };
   int rc;
@@ -764,6 +821,8 @@ static int mla_attn_backward(talos_plan_s* p, const MlaDims& D, const float* P, 
     if ((rc = split_launch(MH, hd, r, m.dq, m.dqc, m.dqr, false, s))) return rc;
     if ((rc = split_launch(MH, hd, r, m.dk, m.dkc, m.dkr, false, s))) return rc;
   }
+  // bf16 plans: the products below read the attention gradients in bf16
+  if ((rc = refresh_shadows(p, {m.dqc, m.dqr, m.dkc, m.dkr, m.dv}, s))) return rc;
   // q / rope-k projections of xn
   if ((rc = mm(p, s, 1, 0, d, H * hd, M, xn, d, m.dqc, H * hd, G + w.wq, H * hd))) return rc;
   if ((rc = mm(p, s, 1, 0, d, H * r, M, xn, d, m.dqr, H * r, G + w.wqr, H * r))) return rc;
@@ -2249,9 +2308,15 @@ static int mla_fwd_bwd(talos_plan_s* p, const float* P, const float* x, const fl
   auto& L = p->layers[0];
   const int M = c.batch * c.seq, d = c.d_model, ow = c.n_heads * c.v_dim;
   int rc;
+  // bf16 plans: this call's weights and output gradient have bf16 copies, made with the norm's
+  // output and with the attention's output (one conversion launch each)
+  set_shadow_base(p, p->p16, p->p16 ? P : nullptr);
+  set_shadow_base(p, p->g16, p->g16 ? gout : nullptr);
   // ---- forward
   if ((rc = rmsnorm_fwd_launch(M, d, c.eps, x, P + o.g, L.xn1, L.rstd1, s))) return rc;
+  if ((rc = refresh_shadows(p, {P, L.xn1}, s))) return rc;
   if ((rc = mla_attn_forward(p, D, P, o.w, L.xn1, L, s))) return rc;
+  if ((rc = refresh_shadows(p, {L.o, gout}, s))) return rc;
   if ((rc = mm(p, s, 0, 0, M, d, ow, L.o, ow, P + o.w.wo, d, out, d, 0.f, nullptr, x, d))) return rc;
   // ---- backward
   if ((rc = mm(p, s, 1, 0, ow, d, M, L.o, ow, gout, d, G + o.w.wo, d))) return rc;
@@ -2767,6 +2832,24 @@ int talos_mla_plan_create(const talos_mla_cfg* cfg, talos_plan* plan) {
   rc |= plan_alloc(p, &p->g_xn, M * d);
   rc |= plan_alloc(p, &p->attn_ws, M * H);
   if (rc == TALOS_OK) rc = alloc_mla_scratch(p, D);
+  if (rc == TALOS_OK && p->bf16 && !p->unfused) {
+    // the bf16 copies of every tensor a bf16-in product reads (the activations, the attention's
+    // output and gradients, the latent's gradient, the weights and the output gradient)
+    const size_t Hh = H * c.head_dim, Hr = H * c.rope_dim, Hv = H * c.v_dim, Lt = c.kv_latent;
+    auto& m = p->ms;
+    add_shadow(p, L.xn1, M * d, &rc);
+    add_shadow(p, L.m.ckv, M * Lt, &rc);
+    add_shadow(p, L.o, M * Hv, &rc);
+    add_shadow(p, m.dqc, M * Hh, &rc);
+    add_shadow(p, m.dqr, M * Hr, &rc);
+    add_shadow(p, m.dkc, M * Hh, &rc);
+    add_shadow(p, m.dkr, M * Hr, &rc);
+    add_shadow(p, m.dv, M * Hv, &rc);
+    add_shadow(p, m.dckv, M * Lt, &rc);
+    p->p16 = add_shadow(p, nullptr, mla_offsets(c).end, &rc);
+    p->g16 = add_shadow(p, nullptr, M * d, &rc);
+    rc = rc ? TALOS_ERR_ALLOC : TALOS_OK;
+  }
   if (rc == TALOS_OK) rc = upload_rope_table(p, c.seq, c.rope_dim, c.rope_base);
   if (rc == TALOS_OK) {
     p->red_ws_bytes = std::max(p->red_ws_bytes, rmsnorm_bwd_workspace_bytes((int)M, (int)d));

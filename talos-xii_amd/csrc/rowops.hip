@@ -191,6 +191,65 @@ int colsum_launch(int rows, int cols, const float* dy, long long ld, float beta,
 }
 
 // ---------------------------------------------------------------------------
+// fp32 -> bf16 copies (the bf16 operands of bf16-in products)
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float floatx2_t __attribute__((ext_vector_type(2)));
+// two values rounded to nearest even (v_cvt_pk_bf16_f32, the conversion the GEMM staging makes),
+// lo in the low half
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+  const floatx2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// Up to kCvtMax tensors in one launch: blockIdx.y picks the tensor, the x grid strides its
+// elements four at a time (float4 in, 8 bytes out; a scalar tail).
+constexpr int kCvtMax = 8;
+struct CvtList {
+  const float* src[kCvtMax];
+  uint16_t* dst[kCvtMax];
+  long long n[kCvtMax];
+};
+__global__ __launch_bounds__(256) void cvt_bf16_kernel(CvtList l) {
+  const int t = blockIdx.y;
+  const float* x = l.src[t];
+  uint16_t* y = l.dst[t];
+  const long long n = l.n[t];
+  // float4 reads and 8-byte writes where both ends allow, else element by element
+  const bool vec = ((reinterpret_cast<uintptr_t>(x) & 15) | (reinterpret_cast<uintptr_t>(y) & 7)) == 0;
+  const long long n4 = vec ? n / 4 : 0;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    const float4 v = reinterpret_cast<const float4*>(x)[i];
+    reinterpret_cast<uint2*>(y)[i] = make_uint2(bf16_pair(v.x, v.y), bf16_pair(v.z, v.w));
+  }
+  for (long long i = 4 * n4 + (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    y[i] = (uint16_t)(bf16_pair(x[i], 0.f) & 0xffffu);
+}
+
+int cvt_bf16_launch(int count, const float* const* src, uint16_t* const* dst, const long long* n, hipStream_t s) {
+  CvtList l{};
+  long long most = 0, bytes = 0;
+  TALOS_REQUIRE(count >= 0 && count <= kCvtMax, TALOS_ERR_SHAPE, "bf16 conversion: %d tensors (at most %d)", count,
+                kCvtMax);
+  for (int i = 0; i < count; ++i) {
+    TALOS_REQUIRE((reinterpret_cast<uintptr_t>(src[i]) & 3) == 0 && (reinterpret_cast<uintptr_t>(dst[i]) & 1) == 0,
+                  TALOS_ERR_SHAPE, "bf16 conversion: misaligned fp32 source or bf16 destination");
+    l.src[i] = src[i];
+    l.dst[i] = dst[i];
+    l.n[i] = n[i];
+    most = std::max(most, n[i]);
+    bytes += 6 * n[i];
+  }
+  if (count == 0 || most == 0) return TALOS_OK;
+  const unsigned gx = (unsigned)std::min<long long>(2048, (most / 4 + 255) / 256 + 1);
+  ProfScope ps(s, "cvt_bf16_kernel", 0.0, (double)bytes);
+  hipLaunchKernelGGL(cvt_bf16_kernel, dim3(gx, count), dim3(256), 0, s, l);
+  TALOS_LAUNCHED("cvt_bf16_kernel");
+  return TALOS_OK;
+}
+
+// ---------------------------------------------------------------------------
 // RMSNorm
 // ---------------------------------------------------------------------------
 // Each wave handles rows; lane l holds elements [4*l + 256*j, +4) for j < dim/256 (dim % 4 == 0,

@@ -23,6 +23,9 @@ int reduce_parts_launch(int cols, int nparts, double* part, float beta, float* o
                         float* out2 = nullptr);
 int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
                        hipStream_t s);
+// bf16 copies (rounded to nearest even, the GEMM staging's conversion) of count <= 8 fp32 tensors
+// of n[i] elements in one launch
+int cvt_bf16_launch(int count, const float* const* src, uint16_t* const* dst, const long long* n, hipStream_t s);
 // dx = (dres ? dres : beta_dx * dx) + d rmsnorm / dx . dy; dres (the residual branch's gradient)
 // may equal dx. dres_last ([rows / seq, dim]) adds a gradient that is non-zero on the last token
 // of each sample only: row b * seq + last_row(lens, b, seq) receives dres_last[b].
