@@ -55,12 +55,18 @@ constexpr int NT = 256;
 #endif
 constexpr int NBUF = TALOS_GEMM_DBUF ? 2 : 1;
 // Rows whose operands the 64-row norm-backward epilogue keeps in flight ahead of the row it
-// finishes (normb_rows), without and with the last-row addends.
+// finishes (normb_rows), without and with the last-row addends (8: a thread's eight rows all
+// issued before the first, C3 0.587-0.592 -> 0.584-0.587 ms against 4).
 #ifndef TALOS_NB_AHEAD
-#define TALOS_NB_AHEAD 4
+#define TALOS_NB_AHEAD 8
 #endif
 #ifndef TALOS_NB_AHEAD_LAST
 #define TALOS_NB_AHEAD_LAST 1
+#endif
+// Whether the products with the four-term addend (E_NBPRE) take 64-row tiles at every size (1) or
+// only where the 128-row tiles would leave fewer than two workgroups per CU (0).
+#ifndef TALOS_NBPRE_M64
+#define TALOS_NBPRE_M64 0
 #endif
 // Wave priority (s_setprio) of the main loop's products, 0..3 (1: C4 2.398 -> 2.388 ms).
 #ifndef TALOS_GEMM_PRIO
@@ -480,7 +486,10 @@ __device__ __forceinline__ NbRow normb_row_load(const GemmArgs& p, int row, int 
   const int rr = on ? row : 0;
   in.r = on ? p.nb_rstd[rr] : 0.f;
   in.x = *reinterpret_cast<const float4*>(p.nb_x + (long long)rr * p.N + col);
-  in.add = p.nb_add ? *reinterpret_cast<const float4*>(p.nb_add + (long long)rr * p.N + col) : z;
+  // the addend row is read from x's row when there is none and then zeroed: a load whose
+  // pointer may be null would be compiled as a flat load from a zeroed stack slot instead
+  const float4 add = *reinterpret_cast<const float4*>((p.nb_add ? p.nb_add : p.nb_x) + (long long)rr * p.N + col);
+  in.add = p.nb_add ? add : z;
   if (!on) in.x = in.add = z;
   in.dyl = in.addl = z;
   in.last = false;
@@ -492,8 +501,11 @@ __device__ __forceinline__ NbRow normb_row_load(const GemmArgs& p, int row, int 
       lr = (L < 1 ? 1 : (L > p.nb_seq ? p.nb_seq : L)) - 1;
     }
     in.last = on && rem == lr;
-    const float4 dyl = p.nb_dy_last ? *reinterpret_cast<const float4*>(p.nb_dy_last + (long long)qq * p.N + col) : z;
-    const float4 addl = p.nb_add_last ? *reinterpret_cast<const float4*>(p.nb_add_last + (long long)qq * p.N + col) : z;
+    // (absent rows read from x's first rows, [samples][N] fits inside x's [M][N], then zeroed)
+    const float4 dy4 = *reinterpret_cast<const float4*>((p.nb_dy_last ? p.nb_dy_last : p.nb_x) + (long long)qq * p.N + col);
+    const float4 ad4 = *reinterpret_cast<const float4*>((p.nb_add_last ? p.nb_add_last : p.nb_x) + (long long)qq * p.N + col);
+    const float4 dyl = p.nb_dy_last ? dy4 : z;
+    const float4 addl = p.nb_add_last ? ad4 : z;
     if (in.last) {
       in.dyl = dyl;
       in.addl = addl;
@@ -828,6 +840,39 @@ __device__ __forceinline__ void stage_acc(float* T, const floatx16 (&acc)[MT][2]
 // thread t takes column group cg of rows r0 + 8 i, i < 8, with the operands of AHEAD rows in
 // flight ahead of the row it finishes; the row's sample q and its index rem in the sample are kept
 // incrementally (no division per row).
+// E_NBPRE on 64-row tiles: the four-term addend sum_h P[row][h] U[row / seq][h] added to the
+// thread's own staged rows of T (the rows and columns normb_rows then reads), four rows' P and U
+// loads in flight at once; normb_apply adds it to the product in the same order.
+__device__ __forceinline__ void normb_pre_rows(const GemmArgs& p, float* T, int cg, int col, int r0) {
+  constexpr int RT = T_ROWS / 8;
+#pragma unroll
+  for (int i0 = 0; i0 < RT; i0 += 4) {
+    float4 w[4], u[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = r0 + 8 * (i0 + j);
+      const int rr = row < p.M ? row : 0;
+      w[j] = *reinterpret_cast<const float4*>(p.nb_pre_p + (long long)rr * 4);
+      const float* ur = p.nb_pre_u + (long long)(rr / p.nb_seq) * 4 * p.N + col;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) u[j][t] = *reinterpret_cast<const float4*>(ur + t * p.N);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (r0 + 8 * (i0 + j) >= p.M) continue;
+      const float wh[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        a = make_float4(fmaf(wh[t], u[j][t].x, a.x), fmaf(wh[t], u[j][t].y, a.y), fmaf(wh[t], u[j][t].z, a.z),
+                        fmaf(wh[t], u[j][t].w, a.w));
+      float4* tp = reinterpret_cast<float4*>(T + ((threadIdx.x >> 5) + 8 * (i0 + j)) * T_S + cg);
+      const float4 v = *tp;
+      *tp = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
+    }
+  }
+}
+
 template <int AHEAD, bool LAST>
 __device__ __forceinline__ void normb_rows(const GemmArgs& p, const float* T, int cg, int col, int r0,
                                            const float4& g, float4& nbw) {
@@ -1143,11 +1188,13 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
   // through the first half's epilogue, which leaves registers for x one row ahead; there the
   // epilogue phase of the lockstep grid runs at the bandwidth of its mixed reads and writes, and
   // deeper prefetching of the second half measured the same.)
-  constexpr bool NB_PIPE = (E & E_NORMB) != 0 && (E & E_NBPRE) == 0 && MT == 1;
+  constexpr bool NB_PIPE = (E & E_NORMB) != 0 && MT == 1;
   if constexpr (NB_PIPE) {
     constexpr bool LAST = (E & E_NBLAST) != 0;
     stage_acc<MT>(T, acc, wm, wn, h, l32, 0);
     __syncthreads();
+    // (each thread reads and writes only its own rows' columns of T from here on)
+    if constexpr ((E & E_NBPRE) != 0) normb_pre_rows(p, T, cg, col, m0 + (threadIdx.x >> 5));
     const float4 g = *reinterpret_cast<const float4*>(p.nb_gain + col);
     normb_rows<LAST ? TALOS_NB_AHEAD_LAST : TALOS_NB_AHEAD, LAST>(p, T, cg, col, m0 + (threadIdx.x >> 5), g, nbw);
   }
@@ -1749,6 +1796,8 @@ static GemmKernel pick_m64(bool tA, bool tB, int e) {
   if (tB) {
     if (e == E_NORMB) return &gemm_f32_m64_kernel<false, true, E_NORMB>;
     if (e == (E_NORMB | E_NBLAST)) return &gemm_f32_m64_kernel<false, true, E_NORMB | E_NBLAST>;
+    if (e == (E_NORMB | E_NBPRE)) return &gemm_f32_m64_kernel<false, true, E_NORMB | E_NBPRE>;
+    if (e == (E_NORMB | E_NBPRE | E_NBLAST)) return &gemm_f32_m64_kernel<false, true, E_NORMB | E_NBPRE | E_NBLAST>;
     if (e == 0) return &gemm_f32_m64_kernel<false, true, 0>;
     if (e == E_BETA) return &gemm_f32_m64_kernel<false, true, E_BETA>;
     return nullptr;
@@ -1769,7 +1818,8 @@ static int num_cus();
 // K = 256; with 1024 or more tiles the 128-row tiles are 3-12% faster).
 static int tile_rows(const GemmDesc& d, int e, int ksplit) {
   const long long tiles = (long long)((d.M + BM - 1) / BM) * ((d.N + BN - 1) / BN) * d.batch;
-  if (d.bf16 || d.batch != 1 || d.N > BN || ksplit > 1 || tiles >= 2LL * num_cus()) return BM;
+  if (d.bf16 || d.batch != 1 || d.N > BN || ksplit > 1) return BM;
+  if (tiles >= 2LL * num_cus() && !(TALOS_NBPRE_M64 && (e & E_NBPRE) != 0)) return BM;
   return pick_m64(d.transA != 0, d.transB != 0, e) ? 64 : BM;
 }
 

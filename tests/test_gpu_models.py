@@ -234,8 +234,11 @@ def test_mla_plan_over_ds_budget_is_created():
 
 
 # seq 100 / 132 / 256 reach the bf16 tiled forward and dS backward (causal with ragged tiles,
-# C5's head dims non-causal); at 37 and 64 attention runs in fp32
-@pytest.mark.parametrize("ci", [[2, 37, 64, 2, 32, 8, 16, 16, 1, 0], [2, 64, 512, 8, 128, 32, 64, 64, 0, 0],
+# C5's head dims non-causal); at 37 and 64 attention runs in fp32. The d = 20 case has row lengths
+# (20, 36, 12, 12) that are multiples of 4, as the plan requires, but not of 8, so the products
+# read their operands' bf16 copies element by element instead of in 16-byte pieces.
+@pytest.mark.parametrize("ci", [[2, 37, 20, 3, 12, 4, 12, 4, 1, 0],
+                                [2, 37, 64, 2, 32, 8, 16, 16, 1, 0], [2, 64, 512, 8, 128, 32, 64, 64, 0, 0],
                                 [2, 100, 64, 2, 32, 8, 16, 16, 1, 0], [1, 132, 512, 8, 128, 32, 64, 64, 1, 0],
                                 [1, 256, 512, 8, 128, 32, 64, 64, 0, 0]])
 def test_mla_bf16_vs_oracle(oracle, ci):
