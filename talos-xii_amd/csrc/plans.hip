@@ -2832,7 +2832,11 @@ int talos_mla_plan_create(const talos_mla_cfg* cfg, talos_plan* plan) {
   rc |= plan_alloc(p, &p->g_xn, M * d);
   rc |= plan_alloc(p, &p->attn_ws, M * H);
   if (rc == TALOS_OK) rc = alloc_mla_scratch(p, D);
-  if (rc == TALOS_OK && p->bf16 && !p->unfused) {
+  // TALOS_BF16_COPIES=0 at plan creation: no bf16 copies (every bf16-in product reads its fp32
+  // operands and rounds them at staging; the same roundings, so the same results)
+  const char* copies_env = std::getenv("TALOS_BF16_COPIES");
+  const bool copies = !(copies_env && copies_env[0] == '0');
+  if (rc == TALOS_OK && p->bf16 && !p->unfused && copies) {
     // the bf16 copies of every tensor a bf16-in product reads (the activations, the attention's
     // output and gradients, the latent's gradient, the weights and the output gradient)
     const size_t Hh = H * c.head_dim, Hr = H * c.rope_dim, Hv = H * c.v_dim, Lt = c.kv_latent;

@@ -39,13 +39,18 @@ def pytest_terminal_summary(terminalreporter):
     if out:
         with open(out, "w") as f:
             json.dump(recs, f, indent=1)
-    need = [r for r in recs if r["needs_mag"]]
     tr = terminalreporter
     tr.section("parameter-gradient tolerance audit")
-    worst = max(r["kappa_needed"] for r in recs)
-    tr.write_line(f"{len(recs)} parameter-gradient tensors checked; {len(need)} have elements beyond the plain "
-                  f"1e-4 |ref| + 1e-5 rule; largest kappa needed {worst:.2f} (allowed {recs[0]['kappa']:.0f})")
-    for r in sorted(need, key=lambda r: -r["kappa_needed"]):
-        tr.write_line(f"  {r['test']} {r['tensor']}: {r['needs_mag']}/{r['size']} elements beyond the plain rule, "
-                      f"kappa needed {r['kappa_needed']:.2f}, worst err / plain bound {r['worst_err_over_plain']:.2f} "
-                      f"(max|ref| {r['max_abs_ref']:.3e})")
+    for rule, plain, unit in (("fp32", "1e-4 |ref| + 1e-5", "2^-24"), ("bf16", "2e-2 |ref| + 1e-5", "2^-8")):
+        rs = [r for r in recs if r.get("rule", "fp32") == rule]
+        if not rs:
+            continue
+        need = [r for r in rs if r["needs_mag"]]
+        worst = max(r["kappa_needed"] for r in rs)
+        tr.write_line(f"{rule}: {len(rs)} parameter-gradient tensors checked; {len(need)} have elements beyond the "
+                      f"plain {plain} rule; largest kappa needed {worst:.2f} (allowed {rs[0]['kappa']:.0f}, "
+                      f"unit {unit})")
+        for r in sorted(need, key=lambda r: -r["kappa_needed"]):
+            tr.write_line(f"  {r['test']} {r['tensor']}: {r['needs_mag']}/{r['size']} elements beyond the plain "
+                          f"rule, kappa needed {r['kappa_needed']:.2f}, worst err / plain bound "
+                          f"{r['worst_err_over_plain']:.2f} (max|ref| {r['max_abs_ref']:.3e})")

@@ -24,7 +24,7 @@ import numpy as np
 import pytest
 
 import talos_hip as th
-from common import (BF16_RTOL, FP32_ATOL, FP32_RTOL, GRAD_KAPPA, block_params, check_close, check_grad, f32,
+from common import (BF16_RTOL, FP32_ATOL, FP32_RTOL, GRAD_KAPPA, block_params, check_close, check_grad, check_grad_bf16, f32,
                     gacha_states, mla_params, ppo_params)
 from test_gpu_models import block_slices, mla_slices, ppo_slices
 
@@ -220,3 +220,5 @@ def test_c5_mla_full_size(c5_case, prec):
         for name, got, ref in pairs:
             rel = float(np.abs(got - ref).max() / np.abs(ref).max())
             assert rel <= BF16_RTOL, f"{name}: normwise relative error {rel:.3e}"
+        for n, sl in mla_slices(C5).items():  # and element-wise, with the magnitude-derived allowance
+            check_grad_bf16(dp[sl], dp_r[sl], mag[sl], name=f"d{n}")

@@ -225,6 +225,26 @@ def test_mla_without_ds_buffer_vs_oracle(oracle, monkeypatch, prec):
             assert float(np.abs(got - ref).max() / np.abs(ref).max()) <= BF16_RTOL, name
 
 
+@pytest.mark.parametrize("ci", [[2, 64, 512, 8, 128, 32, 64, 64, 0, 0], [2, 100, 64, 2, 32, 8, 16, 16, 1, 0],
+                                [2, 37, 20, 3, 12, 4, 12, 4, 1, 0], [64, 256, 512, 8, 128, 32, 64, 64, 0, 0]])
+def test_mla_bf16_copies_bit_identical(monkeypatch, ci):
+    """The bf16 plan's copies (weights, output gradient, activations and attention results
+    converted to bf16 once, products reading them) give bit-identical results to the same plan
+    rounding the fp32 operands at staging (TALOS_BF16_COPIES=0): the roundings, the products'
+    accumulation order and the splits are the same, so any difference is a copy that is stale,
+    misplaced or read at the wrong offset."""
+    from common import mla_params
+    rng = np.random.default_rng(4200 + ci[1] + ci[2])
+    B, S, d = ci[:3]
+    p = f32(mla_params(rng, ci))
+    x, G = f32(rng.normal(size=(B, S, d))), f32(rng.normal(size=(B, S, d)))
+    with_copies = run_mla(ci, th.PREC_BF16, p, x, G)
+    monkeypatch.setenv("TALOS_BF16_COPIES", "0")
+    without = run_mla(ci, th.PREC_BF16, p, x, G)
+    for name, a, b in zip(("out", "dparams", "dx"), with_copies, without):
+        assert np.array_equal(a, b), f"{name}: {int((a != b).sum())} elements differ, max {np.abs(a - b).max():.3e}"
+
+
 def test_mla_plan_over_ds_budget_is_created():
     """A plan whose dS rows would exceed the budget (seq 2048 at batch 64, 8 heads: 8.6 GB in
     fp32, 4.3 GB in bf16, against 4 GiB) is still created, on the tiled path."""
@@ -242,15 +262,17 @@ def test_mla_plan_over_ds_budget_is_created():
                                 [2, 100, 64, 2, 32, 8, 16, 16, 1, 0], [1, 132, 512, 8, 128, 32, 64, 64, 1, 0],
                                 [1, 256, 512, 8, 128, 32, 64, 64, 0, 0]])
 def test_mla_bf16_vs_oracle(oracle, ci):
-    # bf16-in / fp32-accumulate GEMMs against the f64 oracle: every tensor within 2e-2 relative in the
-    # max norm, max|got - ref| <= 2e-2 * max|ref| (bf16 keeps 8 significand bits, so element-wise
-    # relative error on elements that cancel toward zero is unbounded)
-    from common import BF16_RTOL, mla_params
+    # bf16-in / fp32-accumulate GEMMs against the f64 oracle: out and dx within 2e-2 relative in the
+    # max norm, max|got - ref| <= 2e-2 * max|ref|; every parameter-gradient element within 2e-2 of
+    # its own value plus the magnitude-derived allowance (common.check_grad_bf16), the form of the
+    # fp32 rule with bf16's unit roundoff (bf16 keeps 8 significand bits, so an element that cancels
+    # toward zero has no element-wise relative bound of its own)
+    from common import BF16_RTOL, check_grad_bf16, mla_params
     rng = np.random.default_rng(4000 + ci[1] + ci[2])
     B, S, d = ci[:3]
     p = f32(mla_params(rng, ci))
     x, G = f32(rng.normal(size=(B, S, d))), f32(rng.normal(size=(B, S, d)))
-    out_r, dp_r, dx_r = oracle.mla_fwd_bwd(ci, 1e-5, 10000.0, p, x, G)
+    out_r, dp_r, dx_r, mag = oracle.mla_fwd_bwd(ci, 1e-5, 10000.0, p, x, G, mag=True)
     out, dp, dx = run_mla(ci, th.PREC_BF16, p, x, G)
 
     def chk(got, ref, name):
@@ -263,3 +285,4 @@ def test_mla_bf16_vs_oracle(oracle, ci):
     chk(dx, dx_r, "dx")
     for n, sl in mla_slices(ci).items():
         chk(dp[sl], dp_r[sl], f"d{n}")
+        check_grad_bf16(dp[sl], dp_r[sl], mag[sl], name=f"d{n}")
