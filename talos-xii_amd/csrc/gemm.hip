@@ -89,6 +89,7 @@ enum : int {
   E_NORMB = 2048,  // the output rows are dL/d(RMSNorm output): write that norm's backward instead
   E_NORMIN = 4096,  // RMSNorm A's rows first (GemmDesc::nin_*): B rows scaled by the gain, rows by rstd
   E_NBPRE = 8192,   // with E_NORMB: the addend sum_h P[row][h] U[sample][h] (four terms) before the norm backward
+  E_CMAP = 16384,   // C's columns through the output column map (GemmArgs::cmap_*)
   E_NBLAST = 32768  // with E_NORMB: the last-row addends (GemmDesc::normb_add_last / normb_dy_last) may be set
 };
 
@@ -109,6 +110,7 @@ struct GemmArgs {
   const float* rcos;
   const float* rsin;
   int rope_cols, rope_dim, rope_seq;
+  int cmap_w, cmap_pitch, cmap_off;  // output column map (GemmDesc::cmap_*; cmap_w 0: none)
   int ksplit, kper;
   float* part;  // [batch][ksplit][M + (dbias ? 1 : 0)][N]
   float* dbias;
@@ -344,6 +346,13 @@ __device__ __forceinline__ EpiPre epi_preload(const GemmArgs& p, int row, int co
   }
   return q;
 }
+// C's column of product column c (E_CMAP: GemmArgs::cmap_*)
+template <int E>
+__device__ __forceinline__ int out_col(const GemmArgs& p, int c) {
+  if constexpr ((E & E_CMAP) != 0) return (c / p.cmap_w) * p.cmap_pitch + p.cmap_off + c % p.cmap_w;
+  return c;
+}
+
 template <int E, bool PRE = false>
 __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int row, int col, float* C,
                                              const float* __restrict__ resid, bool full, const EpiPre& pre = EpiPre{}) {
@@ -363,9 +372,10 @@ __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int ro
     }
   }
   const long long crow = (long long)row * p.ldc;
+  const int ccol = out_col<E>(p, col);  // (a group of 4 never straddles a mapped block: cmap_w % 4 == 0)
   if (full) {
     if constexpr ((E & E_BETA) != 0) {
-      const float4 c = *reinterpret_cast<const float4*>(C + crow + col);
+      const float4 c = *reinterpret_cast<const float4*>(C + crow + ccol);
       o[0] += p.beta * c.x; o[1] += p.beta * c.y; o[2] += p.beta * c.z; o[3] += p.beta * c.w;
     }
     if constexpr ((E & E_BIAS) != 0) {
@@ -396,7 +406,7 @@ __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int ro
 #pragma unroll
       for (int j = 0; j < 4; ++j) o[j] = fmaxf(o[j], 0.f);
     }
-    *reinterpret_cast<float4*>(C + crow + col) = make_float4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<float4*>(C + crow + ccol) = make_float4(o[0], o[1], o[2], o[3]);
     return make_float4(o[0], o[1], o[2], o[3]);
   }
   if (row >= p.M) return make_float4(0.f, 0.f, 0.f, 0.f);
@@ -405,7 +415,8 @@ __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int ro
     const int cj = col + j;
     if (cj >= p.N) break;
     float x = o[j];
-    if constexpr ((E & E_BETA) != 0) x += p.beta * C[crow + cj];
+    const int oc = out_col<E>(p, cj);
+    if constexpr ((E & E_BETA) != 0) x += p.beta * C[crow + oc];
     if constexpr ((E & E_BIAS) != 0) x += p.bias[cj];
     if constexpr ((E & E_RESID) != 0) x += resid[(long long)row * p.ldr + cj];
     if constexpr ((E & E_DGELU) != 0) x *= p.aux[(long long)row * p.ldaux + cj];
@@ -419,7 +430,7 @@ __device__ __forceinline__ float4 epi_store4(const GemmArgs& p, float4 v, int ro
       if (p.aux) p.aux[(long long)row * p.ldaux + cj] = x;
       x = fmaxf(x, 0.f);
     }
-    C[crow + cj] = x;
+    C[crow + oc] = x;
     o[j] = x;
   }
 #pragma unroll
@@ -1273,7 +1284,7 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
           if constexpr ((E & E_NORM) != 0) epi_norm4(p, o, row, col, ngain);
           if constexpr (BF) {
             if (p.C16 && row < p.M) {  // the bf16 copy of the stored values
-              uint16_t* c16 = p.C16 + (long long)b * p.sC + (long long)row * p.ldc + col;
+              uint16_t* c16 = p.C16 + (long long)b * p.sC + (long long)row * p.ldc + out_col<E>(p, col);
               if (fast && p.vecC16) {
                 *reinterpret_cast<uint2*>(c16) = make_uint2(pack_bf16(o.x, o.y), pack_bf16(o.z, o.w));
               } else {
@@ -1603,6 +1614,9 @@ static GemmArgs to_args(const GemmDesc& d) {
   a.rope_cols = d.rope_cols;
   a.rope_dim = d.rope_dim > 0 ? d.rope_dim : 2;
   a.rope_seq = d.rope_seq > 0 ? d.rope_seq : 1;
+  a.cmap_w = d.cmap_w;
+  a.cmap_pitch = d.cmap_pitch;
+  a.cmap_off = d.cmap_off;
   a.ksplit = d.ksplit < 1 ? 1 : d.ksplit;
   a.kper = d.K;
   a.part = d.workspace;
@@ -1672,6 +1686,7 @@ static int epi_flags(const GemmDesc& d) {
   if (d.normb_dx && d.normb_pre_p) e |= E_NBPRE;
   if (d.normb_dx && (d.normb_add_last || d.normb_dy_last)) e |= E_NBLAST;
   if (d.nin_gain) e |= E_NORMIN;
+  if (d.cmap_w) e |= E_CMAP;
   return e;
 }
 
@@ -1688,7 +1703,7 @@ static bool use_small(const GemmDesc& d, int num_cu) {
   if (!d.bf16 && d.batch == 1 && d.N <= BN && d.M >= 64 * num_cu && !d.transA && d.ksplit <= 1 &&
       pick_m64(false, d.transB != 0, epi_flags(d)) != nullptr)
     return false;  // one 128-wide column of tiles over many rows: the 64-row tiles
-  return !d.bf16 && tiles < num_cu && macs <= 1073741824.0;
+  return !d.bf16 && d.cmap_w == 0 && tiles < num_cu && macs <= 1073741824.0;
 }
 
 size_t gemm_plan_split(GemmDesc& d, int num_cu) {
@@ -1707,6 +1722,7 @@ size_t gemm_plan_split(GemmDesc& d, int num_cu) {
   }
   if ((e & ~(E_BETA | E_BIAS | E_DBIAS)) != 0) d.ksplit = 1;  // only beta / bias survive a split
   if (d.C16) d.ksplit = 1;  // the bf16 copy of C is written by the epilogue
+  if (d.cmap_w) d.ksplit = 1;  // the column map is the epilogue's
   if (d.ksplit <= 1) return 0;
   GemmArgs a = to_args(d);
   return (size_t)a.ksplit * (d.M + (d.dbias ? 1 : 0)) * d.N * d.batch * sizeof(float);
@@ -1726,6 +1742,8 @@ static GemmKernel pick_kernel(bool tA, bool tB, int e, bool bf) {
   GEMM_CASE(false, false, E_BETA)
   GEMM_CASE(false, false, E_BIAS)
   GEMM_CASE(false, false, E_ROPE)
+  GEMM_CASE(false, false, E_CMAP)
+  GEMM_CASE(false, false, E_ROPE | E_CMAP)
   GEMM_CASE(false, false, E_RESID)
   GEMM_CASE(false, false, E_BIAS | E_RESID)
   GEMM_CASE(false, false, E_BIAS | E_GELU)
@@ -1869,6 +1887,15 @@ static bool normb_fused(const GemmDesc& d) {
 }
 
 int gemm_launch(const GemmDesc& d, hipStream_t stream) {
+  if (d.cmap_w) {
+    const int e = epi_flags(d);
+    TALOS_REQUIRE(d.cmap_w > 0 && d.cmap_w % 4 == 0 && d.cmap_pitch % 4 == 0 && d.cmap_off % 4 == 0 &&
+                      d.cmap_off + d.cmap_w <= d.cmap_pitch && d.batch == 1 && !d.normb_dx &&
+                      (e & ~(E_BETA | E_BIAS | E_ROPE | E_CMAP)) == 0,
+                  TALOS_ERR_UNSUPPORTED,
+                  "gemm: an output column map needs widths, pitch and offset in multiples of 4 and a plain, bias or "
+                  "RoPE epilogue");
+  }
   if (d.normb_dx) {
     if (!normb_fused(d)) {
       // the product into C, then the row-norm backward kernel

@@ -47,6 +47,11 @@ struct GemmDesc {
   const float* rope_cos = nullptr;
   const float* rope_sin = nullptr;
   int rope_cols = 0, rope_dim = 0, rope_seq = 1;
+  // Output column map (cmap_w > 0): product column c is stored at column
+  // (c / cmap_w) * cmap_pitch + cmap_off + c % cmap_w of C (ldc wide), e.g. a head's content or
+  // rope part into a head-interleaved row; the epilogue's own arithmetic (RoPE) sees c. cmap_w a
+  // multiple of 4; not with a split K (the library keeps it unsplit), the row norms or activations.
+  int cmap_w = 0, cmap_pitch = 0, cmap_off = 0;
   // Split-K: the K range is cut into ksplit parts of kper (multiple of 32) whose fp32 partial
   // tiles are summed in f64 by a second kernel. ksplit = 0 lets the library choose.
   int ksplit = 1;

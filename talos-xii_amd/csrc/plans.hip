@@ -99,7 +99,7 @@ struct talos_plan_s {
   // latent attention: the projections before concatenation and the attention gradients,
   // shared by all layers
   struct MlaScratch {
-    float *qc, *qr, *kc, *kr, *dq, *dk, *dv, *dqc, *dqr, *dkc, *dkr, *dckv;
+    float *dq, *dk, *dv, *dqc, *dqr, *dkc, *dkr, *dckv;
     float* ds = nullptr;  // the attention backward's dS rows (attn_bwd_ds_supported)
   } ms{};
   // bf16 MLA plans: bf16 copies of the fp32 tensors the bf16-in products read (an operand inside
@@ -361,8 +361,8 @@ static int alloc_mla_scratch(talos_plan_s* p, const MlaDims& D) {
   const size_t M = (size_t)D.batch * D.seq, H = D.H, td = (size_t)D.hd + D.r;
   auto& m = p->ms;
   int rc = 0;
-  for (float** b : {&m.qc, &m.kc, &m.dqc, &m.dkc}) rc |= plan_alloc(p, b, M * H * D.hd);
-  for (float** b : {&m.qr, &m.kr, &m.dqr, &m.dkr}) rc |= plan_alloc(p, b, M * H * D.r);
+  for (float** b : {&m.dqc, &m.dkc}) rc |= plan_alloc(p, b, M * H * D.hd);
+  for (float** b : {&m.dqr, &m.dkr}) rc |= plan_alloc(p, b, M * H * D.r);
   for (float** b : {&m.dq, &m.dk}) rc |= plan_alloc(p, b, M * H * td);
   rc |= plan_alloc(p, &m.dv, M * H * D.vd);
   rc |= plan_alloc(p, &m.dckv, M * D.L);
@@ -745,48 +745,49 @@ static int mla_attn_forward(talos_plan_s* p, const MlaDims& D, const float* P, c
                             talos_plan_s::Layer& L, hipStream_t s) {
   const int M = D.batch * D.seq, d = D.d, H = D.H, Lt = D.L, r = D.r, hd = D.hd, vd = D.vd;
   const size_t MH = (size_t)M * H;
-  auto& m = p->ms;
-  auto rope_gemm = [&](const float* W, float* C) {
+  int rc;
+  AttnDesc a = mla_attn_desc(p, D, L);
+  // on the dS path the attention reads the content and rope parts of q / k where the projections
+  // write them, the two halves of the layer's L.m.q / L.m.k ([M][H*hd] then [M][H*r]); otherwise
+  // the projections write each head's content and rope columns straight into the head-interleaved
+  // rows of L.m.q / L.m.k ([M][H*(hd+r)], an output column map in their epilogue)
+  const bool split = mla_split_qk(p, a);
+  const int td = hd + r;
+  // A[M][K] . B[K][N] into C, columns mapped when !split (width cw at offset co of each td block)
+  auto proj = [&](int N, int K, const float* A, const float* B, float* C, int cw, int co, bool rope) {
     GemmDesc g;
     g.M = M;
-    g.N = H * r;
-    g.K = d;
-    g.A = xn;
-    g.lda = d;
-    g.B = W;
-    g.ldb = H * r;
+    g.N = N;
+    g.K = K;
+    g.A = A;
+    g.lda = K;
+    g.B = B;
+    g.ldb = N;
     g.C = C;
-    g.ldc = H * r;
-    g.rope_cos = p->rcos;
-    g.rope_sin = p->rsin;
-    g.rope_cols = H * r;
-    g.rope_dim = r;
-    g.rope_seq = D.seq;
+    g.ldc = split ? N : (long long)H * td;
+    if (!split) {
+      g.cmap_w = cw;
+      g.cmap_pitch = td;
+      g.cmap_off = co;
+    }
+    if (rope) {
+      g.rope_cos = p->rcos;
+      g.rope_sin = p->rsin;
+      g.rope_cols = N;
+      g.rope_dim = r;
+      g.rope_seq = D.seq;
+    }
     g.ksplit = 1;
     g.bf16 = p->bf16;
     bf16_operands(p, g);
     return gemm_launch(g, s);
   };
-  int rc;
-  AttnDesc a = mla_attn_desc(p, D, L);
-  // on the dS path the attention reads the content and rope parts of q / k where the projections
-  // write them, the two halves of the layer's L.m.q / L.m.k ([M][H*hd] then [M][H*r]); otherwise
-  // the parts are concatenated per head into L.m.q / L.m.k
-  const bool split = mla_split_qk(p, a);
-  float* qc = split ? L.m.q : m.qc;
-  float* qr = split ? L.m.q + MH * hd : m.qr;
-  float* kc = split ? L.m.k : m.kc;
-  float* kr = split ? L.m.k + MH * hd : m.kr;
   if ((rc = mm(p, s, 0, 0, M, Lt, d, xn, d, P + w.wdkv, Lt, L.m.ckv, Lt))) return rc;
-  if ((rc = mm(p, s, 0, 0, M, H * hd, Lt, L.m.ckv, Lt, P + w.wuk, H * hd, kc, H * hd))) return rc;
+  if ((rc = proj(H * hd, Lt, L.m.ckv, P + w.wuk, L.m.k, hd, 0, false))) return rc;
   if ((rc = mm(p, s, 0, 0, M, H * vd, Lt, L.m.ckv, Lt, P + w.wuv, H * vd, L.m.v, H * vd))) return rc;
-  if ((rc = mm(p, s, 0, 0, M, H * hd, d, xn, d, P + w.wq, H * hd, qc, H * hd))) return rc;
-  if ((rc = rope_gemm(P + w.wqr, qr))) return rc;
-  if ((rc = rope_gemm(P + w.wkr, kr))) return rc;
-  if (!split) {
-    if ((rc = concat_launch(MH, hd, r, m.qc, m.qr, L.m.q, s))) return rc;
-    if ((rc = concat_launch(MH, hd, r, m.kc, m.kr, L.m.k, s))) return rc;
-  }
+  if ((rc = proj(H * hd, d, xn, P + w.wq, L.m.q, hd, 0, false))) return rc;
+  if ((rc = proj(H * r, d, xn, P + w.wqr, split ? L.m.q + MH * hd : L.m.q, r, hd, true))) return rc;
+  if ((rc = proj(H * r, d, xn, P + w.wkr, split ? L.m.k + MH * hd : L.m.k, r, hd, true))) return rc;
   return attn_fwd_launch(a, s);
 }
 
