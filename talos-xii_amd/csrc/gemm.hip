@@ -909,6 +909,43 @@ __device__ __forceinline__ void normb_rows(const GemmArgs& p, const float* T, in
   }
 }
 
+// ---------------------------------------------------------------------------
+// Direct-to-LDS panels (TALOS_GEMM_DLDS; NT products, whose two operands are both k-contiguous,
+// on 128-row tiles: C4 2.361-2.370 -> 2.339 ms; the NN products, whose B panel is k-major, lost
+// more than the NT ones gained, 235 -> 242 and 205 -> 219 us at C4): interior tiles stream their panels straight from global memory into LDS with
+// global_load_lds_dwordx4 (no register staging, no LDS store instructions), DK = 16 k a chunk in
+// two LDS stages. A wave's load writes 1 KB of consecutive LDS (16 bytes a lane), so the panels
+// X[r][k] (16 floats a row, 16 rows a 1 KB block) are unpadded and their 16-byte pieces permuted
+// instead, by choosing which global piece each lane fetches: piece p of row r sits in slot
+// p ^ ((r >> 2) & 3), so the 16 rows one fragment read spans fall on 16 distinct bank groups.
+// ---------------------------------------------------------------------------
+#ifndef TALOS_GEMM_DLDS
+#define TALOS_GEMM_DLDS 1
+#endif
+constexpr int DK = 16;
+// The ROWS-row panel of X (k-contiguous rows of pitch ld) at rows r0.., k0.. into S: block b
+// (rows 16 b .. 16 b + 15) by wave b % 4
+template <int ROWS>
+__device__ __forceinline__ void dl_panel(const float* __restrict__ X, long long ld, int r0, int k0, float* S) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int blk = w; blk < ROWS / 16; blk += 4) {
+    const int row = 16 * blk + (lane >> 2), piece = (lane & 3) ^ ((row >> 2) & 3);
+    __builtin_amdgcn_global_load_lds(X + (long long)(r0 + row) * ld + k0 + 4 * piece, S + 256 * blk, 16, 0, 0);
+  }
+}
+// row r's (and, TWO, row r + 32's) values at k = k0 .. k0 + 3 of a direct-load panel
+template <bool TWO>
+__device__ __forceinline__ void dl_frag(const float* X, int r, int k0, float (&f0)[4], float (&f1)[4]) {
+  const int o = 4 * ((k0 >> 2) ^ ((r >> 2) & 3));  // rows r and r + 32 share the permutation
+  const float4 v0 = *reinterpret_cast<const float4*>(X + r * DK + o);
+  f0[0] = v0.x; f0[1] = v0.y; f0[2] = v0.z; f0[3] = v0.w;
+  if (TWO) {
+    const float4 v1 = *reinterpret_cast<const float4*>(X + (r + 32) * DK + o);
+    f1[0] = v1.x; f1[1] = v1.y; f1[2] = v1.z; f1[3] = v1.w;
+  }
+}
+
 template <bool TA, bool TB, int E, bool BF, int BMT>
 __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
   __shared__ __align__(16) float smem[BF ? SMEM_BF : SMEM_FLOATS];
@@ -1043,10 +1080,53 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
       }
     }
   } else {
+  float ssq = 0.f;  // E_NORMIN: below
+  bool direct = false;
+  // (128-row tiles: on the 64-row tiles the direct loads measured 2-5% slower at C3)
+  if constexpr (TALOS_GEMM_DLDS && MT == 2 && !TA && TB && (E & (E_NORMIN | E_DBIAS)) == 0) {
+    direct = interior && kbeg < kend && (kend - kbeg) % DK == 0;
+    if (direct) {
+      // stage s: the A panel (BMT rows) at smem + s (BMT + BN) DK, the B panel (BN rows) after it
+      constexpr int STG = (BMT + BN) * DK;
+      static_assert(2 * STG <= SMEM_FLOATS, "two stages fit the panels' LDS");
+      auto issue = [&](int k0, int st) {
+        dl_panel<BMT>(A, p.lda, m0, k0, smem + st * STG);
+        dl_panel<BN>(B, p.ldb, n0, k0, smem + st * STG + BMT * DK);
+      };
+      issue(kbeg, 0);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      int st = 0;
+      for (int k0 = kbeg; k0 < kend; k0 += DK, st ^= 1) {
+        if (k0 + DK < kend) issue(k0 + DK, st ^ 1);  // the other stage was read before the last barrier
+        const float* Ap = smem + st * STG;
+        const float* Bp = Ap + BMT * DK;
+        __builtin_amdgcn_s_setprio(TALOS_GEMM_PRIO);
+#pragma unroll
+        for (int j = 0; j < DK / 8; ++j) {
+          float fa0[4], fa1[4], fb0[4], fb1[4];
+          dl_frag<MT == 2>(Ap, (MT == 2 ? wm * 64 : wm * 32) + l32, 8 * j + 4 * h, fa0, fa1);
+          dl_frag<true>(Bp, wn * 64 + l32, 8 * j + 4 * h, fb0, fb1);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb0[q], acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb1[q], acc[0][1], 0, 0, 0);
+            if constexpr (MT == 2) {
+              acc[MT - 1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb0[q], acc[MT - 1][0], 0, 0, 0);
+              acc[MT - 1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb1[q], acc[MT - 1][1], 0, 0, 0);
+            }
+          }
+        }
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next chunk have landed
+        __syncthreads();                // everyone's, and every wave is done with this stage
+      }
+    }
+  }
+  if (!direct) {
   float4 ra[BMT / 32], rb[4];
   // E_NORMIN: this thread's sum of squares over the A values it loads (thread t and t + 128 load
   // the halves of tile row t % 128), and the gain applied to the B rows as they are loaded
-  float ssq = 0.f;
   auto normin = [&](int k0) {
     if constexpr ((E & E_NORMIN) != 0) {
       static_assert(!TA && !TB && BMT == 128, "input norm: A and B plain, 128-row tiles");
@@ -1125,6 +1205,7 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
     }
   }
   if (NBUF == 2 || kbeg >= kend) __syncthreads();
+  }  // !direct
   if constexpr ((E & E_NORMIN) != 0) {
     // rstd of each tile row, the accumulators scaled by their row's, and (first column tile) the
     // normalised rows and rstd written out
