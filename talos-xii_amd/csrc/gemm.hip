@@ -946,6 +946,24 @@ __device__ __forceinline__ void dl_frag(const float* X, int r, int k0, float (&f
   }
 }
 
+// The bf16 copies' k-contiguous 128-row panels (rows of BKB = 64 bf16, 128 bytes: eight rows a
+// 1 KB block) straight into LDS; piece p (8 values) of row r sits in slot p ^ ((r >> 1) & 7), so
+// a fragment read's 16 rows (8 even rows on one half of the banks, 8 odd on the other) fall on
+// distinct 16-byte bank groups.
+__device__ __forceinline__ void dl_panel_bf16(const uint16_t* __restrict__ X, long long ld, int r0, int k0,
+                                              uint16_t* S) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int blk = w; blk < 16; blk += 4) {
+    const int row = 8 * blk + (lane >> 3), piece = (lane & 7) ^ ((row >> 1) & 7);
+    __builtin_amdgcn_global_load_lds(X + (long long)(r0 + row) * ld + k0 + 8 * piece, S + 512 * blk, 16, 0, 0);
+  }
+}
+// row r's 8 values of piece pc (k = 8 pc .. 8 pc + 7) of a dl_panel_bf16 panel
+__device__ __forceinline__ bf16x8 dl_frag_bf16(const uint16_t* S, int r, int pc) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(S + r * BKB + 8 * (pc ^ ((r >> 1) & 7))));
+}
+
 template <bool TA, bool TB, int E, bool BF, int BMT>
 __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
   __shared__ __align__(16) float smem[BF ? SMEM_BF : SMEM_FLOATS];
@@ -1036,7 +1054,39 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
       }
       __syncthreads();
     };
-    if (A16 && B16) {
+    if (TALOS_GEMM_DLDS && !TA && TB && A16 && B16 && tile_in && p.vecA16 && p.vecB16 && kbeg < kend &&
+        (kend - kbeg) % BKB == 0) {
+      // NT with both bf16 copies: the panels straight into LDS (dl_panel_bf16), two stages, one
+      // barrier a chunk
+      constexpr int STG = (BM + BN) * BKB;  // bf16 values a stage
+      static_assert(2 * STG <= 2 * SMEM_BF, "two stages fit the bf16 LDS");
+      auto issue = [&](int k0, int st) {
+        dl_panel_bf16(A16, p.lda, m0, k0, S16 + st * STG);
+        dl_panel_bf16(B16, p.ldb, n0, k0, S16 + st * STG + BM * BKB);
+      };
+      issue(kbeg, 0);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      int st = 0;
+      for (int k0 = kbeg; k0 < kend; k0 += BKB, st ^= 1) {
+        if (k0 + BKB < kend) issue(k0 + BKB, st ^ 1);
+        const uint16_t* As = S16 + st * STG;
+        const uint16_t* Bs = As + BM * BKB;
+#pragma unroll
+        for (int s = 0; s < BKB / 16; ++s) {
+          const bf16x8 a0 = dl_frag_bf16(As, wm * 64 + l32, 2 * s + h);
+          const bf16x8 a1 = dl_frag_bf16(As, wm * 64 + 32 + l32, 2 * s + h);
+          const bf16x8 b0 = dl_frag_bf16(Bs, wn * 64 + l32, 2 * s + h);
+          const bf16x8 b1 = dl_frag_bf16(Bs, wn * 64 + 32 + l32, 2 * s + h);
+          acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
+          acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc[0][1], 0, 0, 0);
+          acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
+          acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[1][1], 0, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+      }
+    } else if (A16 && B16) {
       if (kbeg < kend) {
         load(kbeg, pa0, pb0);
         store(S16, pa0, pb0);
