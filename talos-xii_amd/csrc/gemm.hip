@@ -1132,9 +1132,10 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
   } else {
   float ssq = 0.f;  // E_NORMIN: below
   bool direct = false;
-  // (128-row tiles: on the 64-row tiles the direct loads measured 2-5% slower at C3)
+  // (128-row tiles: on the 64-row tiles the direct loads measured 2-5% slower at C3; one column
+  // tile: with four column tiles per row panel, N = 512 at C5, they measured 4% slower)
   if constexpr (TALOS_GEMM_DLDS && MT == 2 && !TA && TB && (E & (E_NORMIN | E_DBIAS)) == 0) {
-    direct = interior && kbeg < kend && (kend - kbeg) % DK == 0;
+    direct = interior && p.N <= BN && kbeg < kend && (kend - kbeg) % DK == 0;
     if (direct) {
       // stage s: the A panel (BMT rows) at smem + s (BMT + BN) DK, the B panel (BN rows) after it
       constexpr int STG = (BMT + BN) * DK;
