@@ -722,38 +722,18 @@ static AttnDesc mla_attn_desc(talos_plan_s* p, const MlaDims& D, const talos_pla
   return a;
 }
 
-// bf16 plans on the dS path: points a's q / k at the split content / rope halves of L.m.q / L.m.k
-// ([M][H*hd] then [M][H*r]) and returns true; else leaves a alone (whole heads of width hd + r).
-// The fp32 kernels' split twins spill at C5's head dims (27-48 VGPRs) and measured slower than the
-// two concatenation copies they replace, so fp32 plans keep the copies.
-static bool mla_split_qk(talos_plan_s* p, AttnDesc& a) {
-  if (!p->bf16 || !attn_ds_path(a)) return false;
-  const int hd = a.rope_off, r = a.rope_dim;
-  const long long MH = (long long)a.batch * a.seq * a.heads;
-  a.ldq = (long long)a.heads * hd;
-  a.q2 = a.q + MH * hd;
-  a.ldq2 = (long long)a.heads * r;
-  a.ldk = (long long)a.heads * hd;
-  a.k2 = a.k + MH * hd;
-  a.ldk2 = (long long)a.heads * r;
-  a.dsplit = hd;
-  return true;
-}
-
 // xn -> L.o (and L.lse): the projections, RoPE on q_r / k_r, per-head concatenation, attention.
 static int mla_attn_forward(talos_plan_s* p, const MlaDims& D, const float* P, const MlaW& w, const float* xn,
                             talos_plan_s::Layer& L, hipStream_t s) {
   const int M = D.batch * D.seq, d = D.d, H = D.H, Lt = D.L, r = D.r, hd = D.hd, vd = D.vd;
-  const size_t MH = (size_t)M * H;
   int rc;
   AttnDesc a = mla_attn_desc(p, D, L);
-  // on the dS path the attention reads the content and rope parts of q / k where the projections
-  // write them, the two halves of the layer's L.m.q / L.m.k ([M][H*hd] then [M][H*r]); otherwise
   // the projections write each head's content and rope columns straight into the head-interleaved
-  // rows of L.m.q / L.m.k ([M][H*(hd+r)], an output column map in their epilogue)
-  const bool split = mla_split_qk(p, a);
+  // rows of L.m.q / L.m.k ([M][H*(hd+r)], an output column map in their epilogue). (Reading the
+  // content and rope parts from two buffers instead takes the attention kernels' split twins,
+  // which spill 8-48 VGPRs at C5's head dims: bf16 C5 0.825 against 0.832 ms.)
   const int td = hd + r;
-  // A[M][K] . B[K][N] into C, columns mapped when !split (width cw at offset co of each td block)
+  // A[M][K] . B[K][N] into C, columns mapped (width cw at offset co of each td block)
   auto proj = [&](int N, int K, const float* A, const float* B, float* C, int cw, int co, bool rope) {
     GemmDesc g;
     g.M = M;
@@ -764,12 +744,10 @@ static int mla_attn_forward(talos_plan_s* p, const MlaDims& D, const float* P, c
     g.B = B;
     g.ldb = N;
     g.C = C;
-    g.ldc = split ? N : (long long)H * td;
-    if (!split) {
-      g.cmap_w = cw;
-      g.cmap_pitch = td;
-      g.cmap_off = co;
-    }
+    g.ldc = (long long)H * td;
+    g.cmap_w = cw;
+    g.cmap_pitch = td;
+    g.cmap_off = co;
     if (rope) {
       g.rope_cos = p->rcos;
       g.rope_sin = p->rsin;
@@ -786,8 +764,8 @@ static int mla_attn_forward(talos_plan_s* p, const MlaDims& D, const float* P, c
   if ((rc = proj(H * hd, Lt, L.m.ckv, P + w.wuk, L.m.k, hd, 0, false))) return rc;
   if ((rc = mm(p, s, 0, 0, M, H * vd, Lt, L.m.ckv, Lt, P + w.wuv, H * vd, L.m.v, H * vd))) return rc;
   if ((rc = proj(H * hd, d, xn, P + w.wq, L.m.q, hd, 0, false))) return rc;
-  if ((rc = proj(H * r, d, xn, P + w.wqr, split ? L.m.q + MH * hd : L.m.q, r, hd, true))) return rc;
-  if ((rc = proj(H * r, d, xn, P + w.wkr, split ? L.m.k + MH * hd : L.m.k, r, hd, true))) return rc;
+  if ((rc = proj(H * r, d, xn, P + w.wqr, L.m.q, r, hd, true))) return rc;
+  if ((rc = proj(H * r, d, xn, P + w.wkr, L.m.k, r, hd, true))) return rc;
   return attn_fwd_launch(a, s);
 }
 
@@ -804,9 +782,7 @@ static int mla_attn_backward(talos_plan_s* p, const MlaDims& D, const float* P, 
   a.lddo = (long long)H * vd;
   int rc;
   if (attn_ds_path(a)) {
-    // the content and rope parts of dq / dk to their own buffers (and, for bf16 plans, the
-    // forward's split q / k halves in)
-    mla_split_qk(p, a);
+    // the content and rope parts of dq / dk to their own buffers
     a.dq = m.dqc;
     a.lddq = (long long)H * hd;
     a.dq2 = m.dqr;
