@@ -40,9 +40,6 @@ struct AttnArgs {
   float *dq2, *dk2;
   long long lddq2, lddk2;
   int dsplit;
-  // q / k inputs split at dsplit the same way (null: q / k hold whole heads of width dk)
-  const float *q2, *k2;
-  long long ldq2, ldk2;
   const float* q;
   long long ldq;
   const float* k;
@@ -542,71 +539,13 @@ __device__ __forceinline__ void block_st4(float* tile, int g, float4 v) {
   *reinterpret_cast<float4*>(tile + (idx / DM) * P + idx % DM) = v;
 }
 
-// As load_half / block_ld4 for a q / k operand split at `split` (see AttnArgs::q2): head column e
-// of row `row` is x[row * ld + hd * split + e] for e < split, else
-// x2[row * ld2 + hd * (dim - split) + e - split]. With vec, split and dim - split are multiples of 4.
-template <int HALF>
-__device__ __forceinline__ void load_half_split(float (&r)[HALF], const float* __restrict__ x, long long ld,
-                                                const float* __restrict__ x2, long long ld2, int split,
-                                                long long tok0, int row, int S, int hd, int dim, int h, float scale,
-                                                bool vec) {
-  if (row >= S) {
-#pragma unroll
-    for (int i = 0; i < HALF; ++i) r[i] = 0.f;
-    return;
-  }
-  const float* p1 = x + (tok0 + row) * ld + (long long)hd * split;
-  const float* p2 = x2 + (tok0 + row) * ld2 + (long long)hd * (dim - split);
-  if (vec) {
-#pragma unroll
-    for (int i = 0; i < HALF; i += 4) {
-      const int e = HALF * h + i;
-      const float4 v = *reinterpret_cast<const float4*>(e < split ? p1 + e : p2 + (e - split));
-      r[i] = v.x * scale;
-      r[i + 1] = v.y * scale;
-      r[i + 2] = v.z * scale;
-      r[i + 3] = v.w * scale;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < HALF; ++i) {
-      const int e = HALF * h + i;
-      r[i] = e < dim ? (e < split ? p1[e] : p2[e - split]) * scale : 0.f;
-    }
-  }
-}
-template <int DM>
-__device__ __forceinline__ float4 block_ld4_split(const float* __restrict__ x, long long ld, const float* __restrict__ x2,
-                                                  long long ld2, int split, long long tok0, int row0, int nrows, int hd,
-                                                  int dim, int g, bool vec) {
-  const int idx = 4 * g, row = idx / DM, col = idx % DM;
-  const int r = row0 + row;
-  if (r >= nrows) return make_float4(0.f, 0.f, 0.f, 0.f);
-  const float* p1 = x + (tok0 + r) * ld + (long long)hd * split;
-  const float* p2 = x2 + (tok0 + r) * ld2 + (long long)hd * (dim - split);
-  if (vec) return *reinterpret_cast<const float4*>(col < split ? p1 + col : p2 + (col - split));
-  float v[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int c = col + j;
-    v[j] = c < dim ? (c < split ? p1[c] : p2[c - split]) : 0.f;
-  }
-  return make_float4(v[0], v[1], v[2], v[3]);
-}
-// q / k rows of head hd through either layout (a kernel's AttnArgs a, tok0, hd and its compile-time
-// SPLIT in scope: true for the split twins the dS path launches when q2 / k2 are given)
-#define ATTN_LD_Q_HALF(HALF, SEL, r, row, h, scale)                                                                 \
-  (SPLIT ? load_half_split<HALF>(r, a.q, a.ldq, a.q2, a.ldq2, a.dsplit, tok0, row, a.S, hd, a.dk, h, scale, a.vec)   \
-        : load_half<HALF, SEL>(r, a.q, a.ldq, tok0, row, a.S, hd * a.dk, a.dk, h, scale, a.vec))
-#define ATTN_LD_K_HALF(HALF, SEL, r, row, h, scale)                                                                 \
-  (SPLIT ? load_half_split<HALF>(r, a.k, a.ldk, a.k2, a.ldk2, a.dsplit, tok0, row, a.S, hd, a.dk, h, scale, a.vec)   \
-        : load_half<HALF, SEL>(r, a.k, a.ldk, tok0, row, a.S, hd * a.dk, a.dk, h, scale, a.vec))
-#define ATTN_BLK_Q(DM, row0, g)                                                                                      \
-  (SPLIT ? block_ld4_split<DM>(a.q, a.ldq, a.q2, a.ldq2, a.dsplit, tok0, row0, a.S, hd, a.dk, g, a.vec)              \
-        : block_ld4<DM>(a.q, a.ldq, tok0, row0, a.S, hd * a.dk, a.dk, g, a.vec))
-#define ATTN_BLK_K(DM, row0, g)                                                                                      \
-  (SPLIT ? block_ld4_split<DM>(a.k, a.ldk, a.k2, a.ldk2, a.dsplit, tok0, row0, a.S, hd, a.dk, g, a.vec)              \
-        : block_ld4<DM>(a.k, a.ldk, tok0, row0, a.S, hd * a.dk, a.dk, g, a.vec))
+// q / k rows of head hd (a kernel's AttnArgs a and tok0 in scope)
+#define ATTN_LD_Q_HALF(HALF, SEL, r, row, h, scale) \
+  load_half<HALF, SEL>(r, a.q, a.ldq, tok0, row, a.S, hd * a.dk, a.dk, h, scale, a.vec)
+#define ATTN_LD_K_HALF(HALF, SEL, r, row, h, scale) \
+  load_half<HALF, SEL>(r, a.k, a.ldk, tok0, row, a.S, hd * a.dk, a.dk, h, scale, a.vec)
+#define ATTN_BLK_Q(DM, row0, g) block_ld4<DM>(a.q, a.ldq, tok0, row0, a.S, hd * a.dk, a.dk, g, a.vec)
+#define ATTN_BLK_K(DM, row0, g) block_ld4<DM>(a.k, a.ldk, tok0, row0, a.S, hd * a.dk, a.dk, g, a.vec)
 
 // Orders the wave's own LDS writes before its later reads (no workgroup barrier).
 __device__ __forceinline__ void wave_lds_sync() {
@@ -622,7 +561,7 @@ __device__ __forceinline__ void bcast_rows(float* slice, float v, int l32, int h
 #ifndef TALOS_ATTN_TILED_WAVES
 #define TALOS_ATTN_TILED_WAVES 3
 #endif
-template <int DKM, int DVM, bool SPLIT = false>
+template <int DKM, int DVM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DKM > 96 ? 2 : TALOS_ATTN_TILED_WAVES))) void
 attn_fwd_tiled_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, OB = DVM / 32;
@@ -1045,7 +984,7 @@ __device__ __forceinline__ void store_head_col(float* dst, long long ld, float* 
 // DS: every dS value of the wave's key blocks is also stored to a.ds (row of query q, column of
 // key), through a per-wave LDS tile so the global stores are 16-byte pieces of rows, for
 // attn_bwd_dq_ds_kernel; D comes from attn_rowdot_kernel.
-template <int DKM, int DVM, bool DS = false, bool SPLIT = false>
+template <int DKM, int DVM, bool DS = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DKM > 32 ? 2 : TALOS_ATTN_TILED_WAVES))) void
 attn_bwd_dkv_tiled_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32;
@@ -1249,7 +1188,7 @@ __global__ __launch_bounds__(256) void attn_rowdot_kernel(AttnArgs a) {
 // attn_bwd_dq_tiled_kernel (wave = 32 queries), and for each 32-key block the K rows and the
 // tile's [128 x 32] dS block are staged in LDS (loaded one block ahead into registers); the dS
 // block is read transposed there (pitch 33), one value a product step. seq % 4 == 0.
-template <int DKM, bool SPLIT = false>
+template <int DKM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_TILED_WAVES))) void
 attn_bwd_dq_ds_kernel(AttnArgs a) {
   constexpr int QB = DKM / 32, PK = DKM + 4, KL = DKM / 32, PD = 33;
@@ -1412,7 +1351,7 @@ constexpr int kBfT8 = 36, kBfT16 = 40;
 #define TALOS_ATTN_BF_DQ_WAVES 4
 #endif
 
-template <int DKM, int DVM, bool SPLIT = false>
+template <int DKM, int DVM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BF_FWD_WAVES))) void
 attn_fwd_tiled_bf16_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, OB = DVM / 32, KS = KH / 8;
@@ -1534,7 +1473,7 @@ attn_fwd_tiled_bf16_kernel(AttnArgs a) {
   if (h == 0 && q < a.S) a.lse[(long long)pair * a.S + q] = (l > 0.f) ? m + logf(l) : kNegInf;
 }
 
-template <int DKM, int DVM, bool SPLIT = false>
+template <int DKM, int DVM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BF_DKV_WAVES))) void
 attn_bwd_dkv_bf16_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32, KS = KH / 8, VS = VH / 8;
@@ -1701,7 +1640,7 @@ attn_bwd_dkv_bf16_kernel(AttnArgs a) {
     }
 }
 
-template <int DKM, bool SPLIT = false>
+template <int DKM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BF_DQ_WAVES))) void
 attn_bwd_dq_ds_bf16_kernel(AttnArgs a) {
   constexpr int QB = DKM / 32, KL = DKM / 32;
@@ -2207,7 +2146,6 @@ static AttnArgs make_args(const AttnDesc& d, int dkm, int dvm) {
   a.lens = d.lens;
   a.q_last = d.q_last; a.ldq_last = d.ldq_last; a.dq_last = d.dq_last; a.lddq_last = d.lddq_last;
   a.dq2 = d.dq2; a.lddq2 = d.lddq2; a.dk2 = d.dk2; a.lddk2 = d.lddk2; a.dsplit = d.dsplit;
-  a.q2 = d.q2; a.ldq2 = d.ldq2; a.k2 = d.k2; a.ldk2 = d.ldk2;
   // row halves start at (token * ld + head * dim + half * dim/2): 16-byte aligned when all of
   // ld, dim and dim/2 are multiples of 4 and the bases are aligned
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -2215,9 +2153,6 @@ static AttnArgs make_args(const AttnDesc& d, int dkm, int dvm) {
   for (long long ld : {d.ldq, d.ldk, d.ldv, d.ldo}) vec = vec && ld % 4 == 0;
   vec = vec && al(d.q) && al(d.k) && al(d.v) && al(d.o);
   if (d.dout) vec = vec && d.lddo % 4 == 0 && al(d.dout);
-  if (d.q2 || d.k2) vec = vec && d.dsplit % 4 == 0 && (d.dk - d.dsplit) % 4 == 0;  // no float4 straddles the split
-  if (d.q2) vec = vec && d.ldq2 % 4 == 0 && al(d.q2);
-  if (d.k2) vec = vec && d.ldk2 % 4 == 0 && al(d.k2);
   a.vec = vec ? 1 : 0;
   return a;
 }
@@ -2248,10 +2183,6 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
     set_error("attention: head dims (%d, %d) exceed the supported (128, 128)", d.dk, d.dv);
     return TALOS_ERR_UNSUPPORTED;
   }
-  if ((d.q2 || d.k2) && !(d.q2 && d.k2 && attn_ds_path(d))) {
-    set_error("attention forward: split q / k inputs (both) need the dS path (attn_ds_path)");
-    return TALOS_ERR_UNSUPPORTED;
-  }
   AttnArgs a = make_args(d, dkm, dvm);
   if ((long long)a.B * a.H * a.S == 0) return TALOS_OK;
   const long long items = (long long)a.B * a.H * ((a.S + 31) / 32);
@@ -2275,8 +2206,7 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
 #define TILED_BF(DK, DV)                                                                    \
     if (dkm == DK && dvm == DV && bf16) {                                                   \
       ProfScope ps(s, "attn_fwd_tiled_bf16_kernel<" #DK ", " #DV ">", flops, tbytes);       \
-      if (a.q2) hipLaunchKernelGGL((attn_fwd_tiled_bf16_kernel<DK, DV, true>), grid, dim3(256), 0, s, a); \
-      else hipLaunchKernelGGL((attn_fwd_tiled_bf16_kernel<DK, DV>), grid, dim3(256), 0, s, a); \
+      hipLaunchKernelGGL((attn_fwd_tiled_bf16_kernel<DK, DV>), grid, dim3(256), 0, s, a);   \
       return launch_status("attn_fwd_tiled_bf16_kernel");                                   \
     }
     TILED_BF(32, 32)
@@ -2288,20 +2218,6 @@ int attn_fwd_launch(const AttnDesc& d, hipStream_t s) {
       ProfScope ps(s, "attn_fwd_tiled_kernel<" #DK ", " #DV ">", flops, tbytes);            \
       hipLaunchKernelGGL((attn_fwd_tiled_kernel<DK, DV>), grid, dim3(256), 0, s, a);        \
       return launch_status("attn_fwd_tiled_kernel");                                        \
-    }
-    if (a.q2) {  // split q / k (dims checked above)
-#define TILED_SPLIT(DK, DV)                                                                 \
-      if (dkm == DK && dvm == DV) {                                                         \
-        ProfScope ps(s, "attn_fwd_tiled_kernel<" #DK ", " #DV ">", flops, tbytes);          \
-        hipLaunchKernelGGL((attn_fwd_tiled_kernel<DK, DV, true>), grid, dim3(256), 0, s, a); \
-        return launch_status("attn_fwd_tiled_kernel");                                      \
-      }
-      TILED_SPLIT(32, 32)
-      TILED_SPLIT(64, 64)
-      TILED_SPLIT(96, 64)
-#undef TILED_SPLIT
-      set_error("attention forward: no split-input kernel for head dims (%d, %d)", dkm, dvm);
-      return TALOS_ERR_UNSUPPORTED;
     }
     TILED(32, 32)
     TILED(64, 64)
@@ -2474,13 +2390,11 @@ static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, bool bf16, 
 #define TILED(DK, DV)                                                                              \
     if (dkm == DK && dvm == DV && bf16) {                                                          \
       ProfScope ps(s, "attn_bwd_dkv_bf16_kernel<" #DK ", " #DV ">", pairs * (4.0 * a.dk + 4.0 * a.dv), bytes); \
-      if (a.q2) hipLaunchKernelGGL((attn_bwd_dkv_bf16_kernel<DK, DV, true>), grid, dim3(256), 0, s, a); \
-      else hipLaunchKernelGGL((attn_bwd_dkv_bf16_kernel<DK, DV>), grid, dim3(256), 0, s, a);      \
+      hipLaunchKernelGGL((attn_bwd_dkv_bf16_kernel<DK, DV>), grid, dim3(256), 0, s, a);           \
       if (int rc = launch_status("attn_bwd_dkv_bf16_kernel")) return rc;                           \
     } else if (dkm == DK && dvm == DV) {                                                           \
       ProfScope ps(s, "attn_bwd_dkv_tiled_kernel<" #DK ", " #DV ", true>", pairs * (4.0 * a.dk + 4.0 * a.dv), bytes); \
-      if (a.q2) hipLaunchKernelGGL((attn_bwd_dkv_tiled_kernel<DK, DV, true, true>), grid, dim3(256), 0, s, a); \
-      else hipLaunchKernelGGL((attn_bwd_dkv_tiled_kernel<DK, DV, true>), grid, dim3(256), 0, s, a); \
+      hipLaunchKernelGGL((attn_bwd_dkv_tiled_kernel<DK, DV, true>), grid, dim3(256), 0, s, a);    \
       if (int rc = launch_status("attn_bwd_dkv_tiled_kernel")) return rc;                          \
     }
     TILED(32, 32)
@@ -2494,14 +2408,12 @@ static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, bool bf16, 
 #define TILED(DK)                                                                                  \
   if (dkm == DK && bf16) {                                                                         \
     ProfScope ps(s, "attn_bwd_dq_ds_bf16_kernel<" #DK ">", pairs * 2.0 * a.dk, bytes);            \
-    if (a.k2) hipLaunchKernelGGL((attn_bwd_dq_ds_bf16_kernel<DK, true>), grid, dim3(256), 0, s, a); \
-    else hipLaunchKernelGGL((attn_bwd_dq_ds_bf16_kernel<DK>), grid, dim3(256), 0, s, a);          \
+    hipLaunchKernelGGL((attn_bwd_dq_ds_bf16_kernel<DK>), grid, dim3(256), 0, s, a);               \
     return launch_status("attn_bwd_dq_ds_bf16_kernel");                                            \
   }                                                                                                \
   if (dkm == DK) {                                                                                 \
     ProfScope ps(s, "attn_bwd_dq_ds_kernel<" #DK ">", pairs * 2.0 * a.dk, bytes);                 \
-    if (a.k2) hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<DK, true>), grid, dim3(256), 0, s, a);     \
-    else hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<DK>), grid, dim3(256), 0, s, a);               \
+    hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<DK>), grid, dim3(256), 0, s, a);                    \
     return launch_status("attn_bwd_dq_ds_kernel");                                                 \
   }
   TILED(32)
@@ -2520,10 +2432,6 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
   int dkm, dvm;
   if (!pick_dims(d.dk, d.dv, &dkm, &dvm)) {
     set_error("attention: head dims (%d, %d) exceed the supported (128, 128)", d.dk, d.dv);
-    return TALOS_ERR_UNSUPPORTED;
-  }
-  if ((d.q2 || d.k2) && !(d.q2 && d.k2 && attn_ds_path(d))) {
-    set_error("attention backward: split q / k inputs (both) need the dS path (attn_ds_path)");
     return TALOS_ERR_UNSUPPORTED;
   }
   AttnArgs a = make_args(d, dkm, dvm);

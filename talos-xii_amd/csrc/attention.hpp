@@ -56,14 +56,6 @@ struct AttnDesc {
   float* dk2 = nullptr;
   long long lddk2 = 0;
   int dsplit = 0;
-  // with dsplit, the inputs may be split the same way: head columns [0, dsplit) of q / k in q / k
-  // (head width dsplit, row pitch ldq / ldk) and [dsplit, dk) in q2 / k2 (head width dk - dsplit,
-  // row pitch ldq2 / ldk2), so no concatenated copy is made; the tiled forward (seq > 32) and the
-  // dS backward (attn_ds_path) only
-  const float* q2 = nullptr;
-  long long ldq2 = 0;
-  const float* k2 = nullptr;
-  long long ldk2 = 0;
   // 1: where the backward takes the dS path (ds given, attn_bwd_ds_supported), the tiled forward
   // and that backward take bf16 operands in their QK^T, PV and gradient contractions (rounded to
   // nearest even as staged, fp32 accumulation; softmax, lse and D in fp32, dS formed in fp32 and
