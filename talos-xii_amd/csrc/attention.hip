@@ -1288,10 +1288,10 @@ attn_bwd_dq_ds_kernel(AttnArgs a) {
 //    fragment the lane's own row half converted once;
 //  * accumulator products (O += P V, dV += P^T dO, dK += dS^T Q): A is P / dS straight from the
 //    accumulator registers, so slot 8h + j of product t is block row acc_row(8t + j, h) =
-//    16t + 8(j / 4) + 4h + j % 4, and B reads those rows of one column from a transposed bf16 tile
-//    as two 8-byte pieces;
-//  * dQ += dS K: slot 8h + j of product t is key 16t + 8h + j, one 16-byte read each from the
-//    bf16 dS rows and the transposed K tile.
+//    16t + 8(j / 4) + 4h + j % 4, and B reads those rows of one column from the row-major bf16
+//    tile (V, dO, scale Q) by two transposing reads (lds_frag_tr);
+//  * dQ += dS K: slot 8h + j of product t is key 16t + 8h + j, one 16-byte read from the bf16 dS
+//    rows and two transposing reads of the row-major K tile.
 // ---------------------------------------------------------------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -1308,12 +1308,22 @@ __device__ __forceinline__ bf16x8 frag8(const float* f) {
 __device__ __forceinline__ bf16x8 lds_frag16(const uint16_t* p) {  // 16-byte aligned
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
 }
-// Rows 16t + 4h + 0..3 and 16t + 8 + 4h + 0..3 of column tile row `col` (pitch TP, 8-byte aligned).
-template <int TP>
-__device__ __forceinline__ bf16x8 lds_frag_acc(const uint16_t* tile, int col, int t, int h) {
-  const uint16_t* p = tile + col * TP + 16 * t + 4 * h;
-  const uint2 lo = *reinterpret_cast<const uint2*>(p), hi = *reinterpret_cast<const uint2*>(p + 8);
-  const uint4 u = {lo.x, lo.y, hi.x, hi.y};
+// A B fragment over rows of a row-major bf16 tile (pitch P, a multiple of 4): lane (l32, h) gets
+// column c0 + l32 of rows r0 + HS h + 0..3, then of rows r0 + HS h + D2 + 0..3, by two
+// ds_read_b64_tr_b16. That instruction works on groups of 16 lanes: lane 4a + j of a group gives
+// the address of four consecutive values (row a of a 4 x 16 block, columns 4j .. 4j + 3) and lane
+// l receives column l of the block's four rows. Group g = lane / 16 covers columns 16 (g % 2) ..
+// of its rows (h = g / 2), so each lane reads one 8-byte piece and no tile is stored transposed.
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+template <int HS, int D2>
+__device__ __forceinline__ bf16x8 lds_frag_tr(const uint16_t* tile, int P, int r0, int c0, int lane) {
+  typedef __attribute__((address_space(3))) shortx4* lds_x4;
+  const int g = lane >> 4, a = (lane >> 2) & 3, j = lane & 3;
+  const uint16_t* p = tile + (r0 + HS * (g >> 1) + a) * P + c0 + 16 * (g & 1) + 4 * j;
+  const shortx4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_x4)(p));
+  const shortx4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_x4)(p + D2 * P));
+  const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+  const uint4 u = {l2.x, l2.y, h2.x, h2.y};
   return __builtin_bit_cast(bf16x8, u);
 }
 // Element group g of a [32, DM] block (as block_st4), times sc, into a row-major bf16 tile of
@@ -1324,20 +1334,9 @@ __device__ __forceinline__ void block_st4_bf(uint16_t* tile, int g, float4 v, fl
   *reinterpret_cast<uint2*>(tile + (idx / DM) * RP + idx % DM) =
       make_uint2(pk_bf16(v.x * sc, v.y * sc), pk_bf16(v.z * sc, v.w * sc));
 }
-// ... and into a transposed one ([DM][TP]: element (row, col) at col * TP + row)
-template <int DM, int TP>
-__device__ __forceinline__ void block_st4_bft(uint16_t* tile, int g, float4 v) {
-  const int idx = 4 * g, row = idx / DM, col = idx % DM;
-  const uint32_t a = pk_bf16(v.x, v.y), b = pk_bf16(v.z, v.w);
-  tile[col * TP + row] = (uint16_t)a;
-  tile[(col + 1) * TP + row] = (uint16_t)(a >> 16);
-  tile[(col + 2) * TP + row] = (uint16_t)b;
-  tile[(col + 3) * TP + row] = (uint16_t)(b >> 16);
-}
 // Pitches (bf16 elements): row-major tiles DM + 8 (rows 16 bytes apart in bank offset, so the 16
-// lanes of a 16-byte read hit distinct banks); transposed tiles read 8 bytes a lane 36, read 16
-// bytes a lane 40.
-constexpr int kBfT8 = 36, kBfT16 = 40;
+// lanes of a 16-byte read hit distinct banks); the dQ kernel's dS rows 32 + 8.
+constexpr int kDsP = 40;
 // waves per SIMD the bf16 kernels are compiled for (forward, dK / dV, dQ); C5: four waves for dQ
 // (8 VGPRs spill in its split twin) 0.883-0.892 -> 0.878-0.881 ms, two for the forward no better,
 // three for dK / dV or four for the forward spill 43-376 VGPRs
@@ -1355,10 +1354,10 @@ template <int DKM, int DVM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BF_FWD_WAVES))) void
 attn_fwd_tiled_bf16_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, OB = DVM / 32, KS = KH / 8;
-  constexpr int RK = DKM + 8;
+  constexpr int RK = DKM + 8, RV = DVM + 8;
   constexpr int KL = DKM / 32, VL = DVM / 32;
   __shared__ __align__(16) uint16_t Kb[32 * RK];
-  __shared__ __align__(16) uint16_t Vt[DVM * kBfT8];
+  __shared__ __align__(16) uint16_t Vb[32 * RV];
   __shared__ __align__(16) float Wr[4][32];
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
   const int t = threadIdx.x;
@@ -1394,7 +1393,7 @@ attn_fwd_tiled_bf16_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < KL; ++i) block_st4_bf<DKM, RK>(Kb, i * 256 + t, rk[i]);
 #pragma unroll
-    for (int i = 0; i < VL; ++i) block_st4_bft<DVM, kBfT8>(Vt, i * 256 + t, rv[i]);
+    for (int i = 0; i < VL; ++i) block_st4_bf<DVM, RV>(Vb, i * 256 + t, rv[i]);
   };
 
   float m = kNegInf, l = 0.f;
@@ -1449,7 +1448,7 @@ attn_fwd_tiled_bf16_kernel(AttnArgs a) {
         const bf16x8 pf = frag8(P + 8 * t2);
 #pragma unroll
         for (int ob = 0; ob < OB; ++ob)
-          oacc[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, lds_frag_acc<kBfT8>(Vt, ob * 32 + l32, t2, h),
+          oacc[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, lds_frag_tr<4, 8>(Vb, RV, 16 * t2, ob * 32, lane),
                                                              oacc[ob], 0, 0, 0);
       }
     }
@@ -1479,10 +1478,8 @@ attn_bwd_dkv_bf16_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32, KS = KH / 8, VS = VH / 8;
   constexpr int RK = DKM + 8, RV = DVM + 8;
   constexpr int KL = DKM / 32, VL = DVM / 32;
-  __shared__ __align__(16) uint16_t Qb[32 * RK];
-  __shared__ __align__(16) uint16_t Qt[DKM * kBfT8];
-  __shared__ __align__(16) uint16_t Gb[32 * RV];
-  __shared__ __align__(16) uint16_t Gt[DVM * kBfT8];
+  __shared__ __align__(16) uint16_t Qb[32 * RK];  // bf16(scale q) rows: S and, transposed, dK
+  __shared__ __align__(16) uint16_t Gb[32 * RV];  // bf16(dO) rows: dP and, transposed, dV
   __shared__ __align__(16) float LD[2][32];
   __shared__ float Ts[4][32 * 33];
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
@@ -1549,15 +1546,9 @@ attn_bwd_dkv_bf16_kernel(AttnArgs a) {
   };
   auto stash = [&]() {
 #pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      block_st4_bf<DKM, RK>(Qb, i * 256 + t, rq[i], a.scale);
-      block_st4_bft<DKM, kBfT8>(Qt, i * 256 + t, rq[i]);
-    }
+    for (int i = 0; i < KL; ++i) block_st4_bf<DKM, RK>(Qb, i * 256 + t, rq[i], a.scale);
 #pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      block_st4_bf<DVM, RV>(Gb, i * 256 + t, rg[i]);
-      block_st4_bft<DVM, kBfT8>(Gt, i * 256 + t, rg[i]);
-    }
+    for (int i = 0; i < VL; ++i) block_st4_bf<DVM, RV>(Gb, i * 256 + t, rg[i]);
     if (t < 64) LD[t >> 5][t & 31] = rl;
   };
   fetch(qb_beg);
@@ -1598,10 +1589,12 @@ attn_bwd_dkv_bf16_kernel(AttnArgs a) {
         const bf16x8 pf = frag8(P + 8 * t2), sf = frag8(dS + 8 * t2);
 #pragma unroll
         for (int i = 0; i < VB; ++i)
-          dv[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, lds_frag_acc<kBfT8>(Gt, i * 32 + l32, t2, h), dv[i], 0, 0, 0);
+          dv[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, lds_frag_tr<4, 8>(Gb, RV, 16 * t2, i * 32, lane), dv[i],
+                                                          0, 0, 0);
 #pragma unroll
         for (int i = 0; i < KB; ++i)
-          dk[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sf, lds_frag_acc<kBfT8>(Qt, i * 32 + l32, t2, h), dk[i], 0, 0, 0);
+          dk[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sf, lds_frag_tr<4, 8>(Qb, RK, 16 * t2, i * 32, lane), dk[i],
+                                                          0, 0, 0);
       }
       wave_lds_sync();
 #pragma unroll
@@ -1627,7 +1620,7 @@ attn_bwd_dkv_bf16_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int kr = kb * 32 + acc_row(r, h);
       const int e = i * 32 + l32;
-      const float g = rope_t(dk[i][r] * a.scale, e, kr, a, kr < a.S);
+      const float g = rope_t(dk[i][r], e, kr, a, kr < a.S);  // the staged Q rows carry the scale
       if (kr < a.S && e < a.dk) store_head_col(a.dk_out, a.lddk, a.dk2, a.lddk2, a.dsplit, tok0 + kr, hd, a.dk, e, g);
     }
 #pragma unroll
@@ -1644,8 +1637,9 @@ template <int DKM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TALOS_ATTN_BF_DQ_WAVES))) void
 attn_bwd_dq_ds_bf16_kernel(AttnArgs a) {
   constexpr int QB = DKM / 32, KL = DKM / 32;
-  __shared__ __align__(16) uint16_t Kt[DKM * kBfT16];
-  __shared__ __align__(16) uint16_t Db[kQTile * kBfT16];  // dS rows of the tile's queries, bf16
+  constexpr int RK = DKM + 8;
+  __shared__ __align__(16) uint16_t Kb[32 * RK];         // bf16(k) rows, read transposed
+  __shared__ __align__(16) uint16_t Db[kQTile * kDsP];  // dS rows of the tile's queries, bf16
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5, wv = threadIdx.x >> 6;
   const int t = threadIdx.x;
   const int ntile = (a.S + kQTile - 1) / kQTile;
@@ -1673,11 +1667,11 @@ attn_bwd_dq_ds_bf16_kernel(AttnArgs a) {
   };
   auto stash = [&]() {
 #pragma unroll
-    for (int i = 0; i < KL; ++i) block_st4_bft<DKM, kBfT16>(Kt, i * 256 + t, rk[i]);
+    for (int i = 0; i < KL; ++i) block_st4_bf<DKM, RK>(Kb, i * 256 + t, rk[i]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int g = i * 256 + t;
-      *reinterpret_cast<uint2*>(Db + (g >> 3) * kBfT16 + 4 * (g & 7)) = rd[i];
+      *reinterpret_cast<uint2*>(Db + (g >> 3) * kDsP + 4 * (g & 7)) = rd[i];
     }
   };
   floatx16 dq[QB];
@@ -1696,10 +1690,10 @@ attn_bwd_dq_ds_bf16_kernel(AttnArgs a) {
     if (wave_on && kb <= wave_kb_end) {
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {  // dQ += dS K over keys 16 t2 + 8 h + 0..7
-        const bf16x8 df = lds_frag16(Db + (wv * 32 + l32) * kBfT16 + 16 * t2 + 8 * h);
+        const bf16x8 df = lds_frag16(Db + (wv * 32 + l32) * kDsP + 16 * t2 + 8 * h);
 #pragma unroll
         for (int i = 0; i < QB; ++i)
-          dq[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(df, lds_frag16(Kt + (i * 32 + l32) * kBfT16 + 16 * t2 + 8 * h),
+          dq[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(df, lds_frag_tr<8, 4>(Kb, RK, 16 * t2, i * 32, lane),
                                                           dq[i], 0, 0, 0);
       }
     }
