@@ -964,6 +964,38 @@ __device__ __forceinline__ bf16x8 dl_frag_bf16(const uint16_t* S, int r, int pc)
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(S + r * BKB + 8 * (pc ^ ((r >> 1) & 7))));
 }
 
+// The bf16 copies' k-major panels (X[k][c], c contiguous: BKB = 64 k rows of 128 columns, 256
+// bytes a row, four rows a 1 KB block) straight into LDS; piece p (columns 8 p ..) of k row r sits
+// in slot p ^ 4 (r mod 4), so the transposing fragment reads below (four consecutive k rows, four
+// consecutive pieces, per half-wave) fall on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ void dl_panel_kmaj(const uint16_t* __restrict__ X, long long ld, int k0, int c0,
+                                              uint16_t* S) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int blk = w; blk < 16; blk += 4) {
+    const int row = 4 * blk + (lane >> 4), piece = (lane & 15) ^ (4 * (lane >> 4));
+    __builtin_amdgcn_global_load_lds(X + (long long)(k0 + row) * ld + c0 + 8 * piece, S + 512 * blk, 16, 0, 0);
+  }
+}
+// The MFMA fragment of product s (k = 16 s + 8 h + 0..7, the slots of dl_frag_bf16's piece
+// 2 s + h) for column cb + l32 (cb a multiple of 32) of a dl_panel_kmaj panel, by two
+// ds_read_b64_tr_b16. That instruction works on groups of 16 lanes: lane 4a + j of a group gives
+// the address of four consecutive values (row a of a 4 x 16 block, columns 4j .. 4j + 3) and lane
+// l receives column l of the block's four rows. Group g = lane / 16 takes columns cb + 16 (g mod 2)
+// .. + 15 of k rows 16 s + 8 (g / 2) + 0..3, then + 4..7.
+__device__ __forceinline__ bf16x8 dl_frag_kmaj(const uint16_t* S, int s, int cb, int lane) {
+  typedef short shortx4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) shortx4* lds_x4;
+  const int g = lane >> 4, a = (lane >> 2) & 3, j = lane & 3;
+  const int k = 16 * s + 8 * (g >> 1) + a, pc = (cb >> 3) + 2 * (g & 1) + (j >> 1);
+  const uint16_t* q = S + k * 128 + 8 * (pc ^ (4 * a)) + 4 * (j & 1);  // k mod 4 = a
+  const shortx4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_x4)(q));
+  const shortx4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_x4)(q + 4 * 128));
+  const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+  const uint4 u = {l2.x, l2.y, h2.x, h2.y};
+  return __builtin_bit_cast(bf16x8, u);
+}
+
 template <bool TA, bool TB, int E, bool BF, int BMT>
 __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
   __shared__ __align__(16) float smem[BF ? SMEM_BF : SMEM_FLOATS];
@@ -1054,15 +1086,21 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
       }
       __syncthreads();
     };
-    if (TALOS_GEMM_DLDS && !TA && TB && A16 && B16 && tile_in && p.vecA16 && p.vecB16 && kbeg < kend &&
+    if (TALOS_GEMM_DLDS && A16 && B16 && tile_in && p.vecA16 && p.vecB16 && kbeg < kend &&
         (kend - kbeg) % BKB == 0) {
-      // NT with both bf16 copies: the panels straight into LDS (dl_panel_bf16), two stages, one
-      // barrier a chunk
+      // both bf16 copies: the panels straight into LDS (k-contiguous operands by dl_panel_bf16,
+      // k-major ones by dl_panel_kmaj, read back transposed), two stages, one barrier a chunk
       constexpr int STG = (BM + BN) * BKB;  // bf16 values a stage
       static_assert(2 * STG <= 2 * SMEM_BF, "two stages fit the bf16 LDS");
       auto issue = [&](int k0, int st) {
-        dl_panel_bf16(A16, p.lda, m0, k0, S16 + st * STG);
-        dl_panel_bf16(B16, p.ldb, n0, k0, S16 + st * STG + BM * BKB);
+        if (TA)
+          dl_panel_kmaj(A16, p.lda, k0, m0, S16 + st * STG);
+        else
+          dl_panel_bf16(A16, p.lda, m0, k0, S16 + st * STG);
+        if (TB)
+          dl_panel_bf16(B16, p.ldb, n0, k0, S16 + st * STG + BM * BKB);
+        else
+          dl_panel_kmaj(B16, p.ldb, k0, n0, S16 + st * STG + BM * BKB);
       };
       issue(kbeg, 0);
       __builtin_amdgcn_s_waitcnt(0);
@@ -1074,10 +1112,12 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
         const uint16_t* Bs = As + BM * BKB;
 #pragma unroll
         for (int s = 0; s < BKB / 16; ++s) {
-          const bf16x8 a0 = dl_frag_bf16(As, wm * 64 + l32, 2 * s + h);
-          const bf16x8 a1 = dl_frag_bf16(As, wm * 64 + 32 + l32, 2 * s + h);
-          const bf16x8 b0 = dl_frag_bf16(Bs, wn * 64 + l32, 2 * s + h);
-          const bf16x8 b1 = dl_frag_bf16(Bs, wn * 64 + 32 + l32, 2 * s + h);
+          const bf16x8 a0 = TA ? dl_frag_kmaj(As, s, wm * 64, lane) : dl_frag_bf16(As, wm * 64 + l32, 2 * s + h);
+          const bf16x8 a1 =
+              TA ? dl_frag_kmaj(As, s, wm * 64 + 32, lane) : dl_frag_bf16(As, wm * 64 + 32 + l32, 2 * s + h);
+          const bf16x8 b0 = TB ? dl_frag_bf16(Bs, wn * 64 + l32, 2 * s + h) : dl_frag_kmaj(Bs, s, wn * 64, lane);
+          const bf16x8 b1 =
+              TB ? dl_frag_bf16(Bs, wn * 64 + 32 + l32, 2 * s + h) : dl_frag_kmaj(Bs, s, wn * 64 + 32, lane);
           acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
           acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc[0][1], 0, 0, 0);
           acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
