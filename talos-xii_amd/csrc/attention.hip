@@ -40,6 +40,7 @@ struct AttnArgs {
   float *dq2, *dk2;
   long long lddq2, lddk2;
   int dsplit;
+  int out16;  // the bf16 dS kernels: dq / dq2 / dk_out / dk2 / dv_out are bf16 buffers (AttnDesc::out_bf16)
   const float* q;
   long long ldq;
   const float* k;
@@ -1334,6 +1335,20 @@ __device__ __forceinline__ void block_st4_bf(uint16_t* tile, int g, float4 v, fl
   *reinterpret_cast<uint2*>(tile + (idx / DM) * RP + idx % DM) =
       make_uint2(pk_bf16(v.x * sc, v.y * sc), pk_bf16(v.z * sc, v.w * sc));
 }
+// A gradient element g of a bf16 kernel's output: fp32, or with out16 its bf16 (nearest even, as
+// the plans' conversion launch rounds) in a uint16_t buffer; store_head_col's layouts.
+__device__ __forceinline__ void put_out(float* dst, long long idx, float g, bool out16) {
+  if (out16)
+    reinterpret_cast<uint16_t*>(dst)[idx] = (uint16_t)pk_bf16(g, 0.f);
+  else
+    dst[idx] = g;
+}
+__device__ __forceinline__ void store_head_col_o(float* dst, long long ld, float* dst2, long long ld2, int split,
+                                                 long long row, int hd, int dk, int e, float g, bool out16) {
+  if (dst2 == nullptr) put_out(dst, row * ld + (long long)hd * dk + e, g, out16);
+  else if (e < split) put_out(dst, row * ld + (long long)hd * split + e, g, out16);
+  else put_out(dst2, row * ld2 + (long long)hd * (dk - split) + (e - split), g, out16);
+}
 // Pitches (bf16 elements): row-major tiles DM + 8 (rows 16 bytes apart in bank offset, so the 16
 // lanes of a 16-byte read hit distinct banks); the dQ kernel's dS rows 32 + 8.
 constexpr int kDsP = 40;
@@ -1501,8 +1516,8 @@ attn_bwd_dkv_bf16_kernel(AttnArgs a) {
       const int kr = kb * 32 + acc_row(r, h);
       if (kr >= a.S) continue;
       for (int e = l32; e < a.dk; e += 32)
-        store_head_col(a.dk_out, a.lddk, a.dk2, a.lddk2, a.dsplit, tok0 + kr, hd, a.dk, e, 0.f);
-      for (int e = l32; e < a.dv; e += 32) a.dv_out[(tok0 + kr) * a.lddv + hd * a.dv + e] = 0.f;
+        store_head_col_o(a.dk_out, a.lddk, a.dk2, a.lddk2, a.dsplit, tok0 + kr, hd, a.dk, e, 0.f, a.out16);
+      for (int e = l32; e < a.dv; e += 32) put_out(a.dv_out, (tok0 + kr) * a.lddv + hd * a.dv + e, 0.f, a.out16);
     }
     return;
   }
@@ -1621,7 +1636,8 @@ attn_bwd_dkv_bf16_kernel(AttnArgs a) {
       const int kr = kb * 32 + acc_row(r, h);
       const int e = i * 32 + l32;
       const float g = rope_t(dk[i][r], e, kr, a, kr < a.S);  // the staged Q rows carry the scale
-      if (kr < a.S && e < a.dk) store_head_col(a.dk_out, a.lddk, a.dk2, a.lddk2, a.dsplit, tok0 + kr, hd, a.dk, e, g);
+      if (kr < a.S && e < a.dk)
+        store_head_col_o(a.dk_out, a.lddk, a.dk2, a.lddk2, a.dsplit, tok0 + kr, hd, a.dk, e, g, a.out16);
     }
 #pragma unroll
   for (int i = 0; i < VB; ++i)
@@ -1629,7 +1645,7 @@ attn_bwd_dkv_bf16_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int kr = kb * 32 + acc_row(r, h);
       const int e = i * 32 + l32;
-      if (kr < a.S && e < a.dv) a.dv_out[(tok0 + kr) * a.lddv + hd * a.dv + e] = dv[i][r];
+      if (kr < a.S && e < a.dv) put_out(a.dv_out, (tok0 + kr) * a.lddv + hd * a.dv + e, dv[i][r], a.out16);
     }
 }
 
@@ -1711,7 +1727,7 @@ attn_bwd_dq_ds_bf16_kernel(AttnArgs a) {
       const int qr = qb * 32 + acc_row(r, h);
       const int e = i * 32 + l32;
       const float g = rope_t(dq[i][r] * a.scale, e, qr, a, qr < a.S);
-      if (qr < a.S && e < a.dk) store_head_col(a.dq, a.lddq, a.dq2, a.lddq2, a.dsplit, tok0 + qr, hd, a.dk, e, g);
+      if (qr < a.S && e < a.dk) store_head_col_o(a.dq, a.lddq, a.dq2, a.lddq2, a.dsplit, tok0 + qr, hd, a.dk, e, g, a.out16);
     }
 }
 
@@ -2140,6 +2156,7 @@ static AttnArgs make_args(const AttnDesc& d, int dkm, int dvm) {
   a.lens = d.lens;
   a.q_last = d.q_last; a.ldq_last = d.ldq_last; a.dq_last = d.dq_last; a.lddq_last = d.lddq_last;
   a.dq2 = d.dq2; a.lddq2 = d.lddq2; a.dk2 = d.dk2; a.lddk2 = d.lddk2; a.dsplit = d.dsplit;
+  a.out16 = d.out_bf16;
   // row halves start at (token * ld + head * dim + half * dim/2): 16-byte aligned when all of
   // ld, dim and dim/2 are multiples of 4 and the bases are aligned
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -2441,6 +2458,10 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
     else
       hipLaunchKernelGGL(attn_bwd_s64_kernel<4>, dim3((unsigned)((long long)a.B * a.H)), dim3(256), 0, s, a);
     return launch_status("attn_bwd_s64_kernel");
+  }
+  if (d.out_bf16 && !(d.bf16 && attn_ds_path(d))) {
+    set_error("attention backward: bf16 gradient outputs need the bf16 dS path (bf16, attn_ds_path)");
+    return TALOS_ERR_UNSUPPORTED;
   }
   if (attn_ds_path(d)) {
     // the forward decided on the same predicate (its bf16 kernel, split inputs): the backward

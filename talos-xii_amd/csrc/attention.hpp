@@ -62,6 +62,10 @@ struct AttnDesc {
   // kept in ds as bf16 rows), for plans whose products are bf16-in. Other shapes run in fp32,
   // forward and backward alike.
   int bf16 = 0;
+  // 1 (with bf16, on the dS path only): the backward writes dq, dq2, dk_out, dk2 and dv_out as bf16
+  // (nearest even) into uint16_t buffers at those pointers, with the same leading dimensions in
+  // elements, instead of fp32, for plans whose later products read only bf16 copies of them.
+  int out_bf16 = 0;
 };
 
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s);

@@ -781,6 +781,7 @@ static int mla_attn_backward(talos_plan_s* p, const MlaDims& D, const float* P, 
   a.dout = g_o;
   a.lddo = (long long)H * vd;
   int rc;
+  bool out16 = false;
   if (attn_ds_path(a)) {
     // the content and rope parts of dq / dk to their own buffers
     a.dq = m.dqc;
@@ -792,6 +793,20 @@ static int mla_attn_backward(talos_plan_s* p, const MlaDims& D, const float* P, 
     a.dk2 = m.dkr;
     a.lddk2 = (long long)H * r;
     a.dsplit = hd;
+    // bf16 plans with copies: the products below read only the gradients' bf16 copies, so the
+    // bf16 kernels write those instead of the fp32 tensors (the same roundings the conversion
+    // launch would make)
+    uint16_t* c16[5] = {shadow_of(p, m.dqc), shadow_of(p, m.dqr), shadow_of(p, m.dkc), shadow_of(p, m.dkr),
+                        shadow_of(p, m.dv)};
+    out16 = a.bf16 && c16[0] && c16[1] && c16[2] && c16[3] && c16[4];
+    if (out16) {
+      a.dq = reinterpret_cast<float*>(c16[0]);
+      a.dq2 = reinterpret_cast<float*>(c16[1]);
+      a.dk_out = reinterpret_cast<float*>(c16[2]);
+      a.dk2 = reinterpret_cast<float*>(c16[3]);
+      a.dv_out = reinterpret_cast<float*>(c16[4]);
+      a.out_bf16 = 1;
+    }
     if ((rc = attn_bwd_launch(a, p->attn_ws, s))) return rc;
   } else {
     if ((rc = attn_bwd_launch(a, p->attn_ws, s))) return rc;
@@ -799,7 +814,7 @@ static int mla_attn_backward(talos_plan_s* p, const MlaDims& D, const float* P, 
     if ((rc = split_launch(MH, hd, r, m.dk, m.dkc, m.dkr, false, s))) return rc;
   }
   // bf16 plans: the products below read the attention gradients in bf16
-  if ((rc = refresh_shadows(p, {m.dqc, m.dqr, m.dkc, m.dkr, m.dv}, s))) return rc;
+  if (!out16 && (rc = refresh_shadows(p, {m.dqc, m.dqr, m.dkc, m.dkr, m.dv}, s))) return rc;
   // q / rope-k projections of xn
   if ((rc = mm(p, s, 1, 0, d, H * hd, M, xn, d, m.dqc, H * hd, G + w.wq, H * hd))) return rc;
   if ((rc = mm(p, s, 1, 0, d, H * r, M, xn, d, m.dqr, H * r, G + w.wqr, H * r))) return rc;
