@@ -2300,13 +2300,13 @@ static int mla_fwd_bwd(talos_plan_s* p, const float* P, const float* x, const fl
   auto& L = p->layers[0];
   const int M = c.batch * c.seq, d = c.d_model, ow = c.n_heads * c.v_dim;
   int rc;
-  // bf16 plans: this call's weights and output gradient have bf16 copies, made with the norm's
-  // output and with the attention's output (one conversion launch each)
+  // bf16 plans: this call's weights and output gradient have bf16 copies (one conversion launch
+  // each, the output gradient's with the attention's output); the norm writes its output's copy
   set_shadow_base(p, p->p16, p->p16 ? P : nullptr);
   set_shadow_base(p, p->g16, p->g16 ? gout : nullptr);
   // ---- forward
-  if ((rc = rmsnorm_fwd_launch(M, d, c.eps, x, P + o.g, L.xn1, L.rstd1, s))) return rc;
-  if ((rc = refresh_shadows(p, {P, L.xn1}, s))) return rc;
+  if ((rc = rmsnorm_fwd_launch(M, d, c.eps, x, P + o.g, L.xn1, L.rstd1, s, shadow_of(p, L.xn1)))) return rc;
+  if ((rc = refresh_shadows(p, {P}, s))) return rc;
   if ((rc = mla_attn_forward(p, D, P, o.w, L.xn1, L, s))) return rc;
   if ((rc = refresh_shadows(p, {L.o, gout}, s))) return rc;
   if ((rc = mm(p, s, 0, 0, M, d, ow, L.o, ow, P + o.w.wo, d, out, d, 0.f, nullptr, x, d))) return rc;

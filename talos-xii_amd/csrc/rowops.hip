@@ -254,10 +254,11 @@ int cvt_bf16_launch(int count, const float* const* src, uint16_t* const* dst, co
 // ---------------------------------------------------------------------------
 // Each wave handles rows; lane l holds elements [4*l + 256*j, +4) for j < dim/256 (dim % 4 == 0,
 // dim <= 1024 on the vector path). Generic dims fall back to a strided scalar loop.
-template <int V>  // float4 vectors per lane
+// Y16: each lane also writes its four values' bf16 copy (8 bytes) to y16.
+template <int V, bool Y16 = false>  // float4 vectors per lane
 __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(int rows, int dim, float eps, const float* __restrict__ x,
                                                           const float* __restrict__ w, float* __restrict__ y,
-                                                          float* __restrict__ rstd) {
+                                                          float* __restrict__ rstd, uint16_t* __restrict__ y16) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -279,8 +280,10 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(int rows, int dim, flo
     const int c = 4 * lane + 256 * j;
     if (c < dim) {
       const float4 g = *reinterpret_cast<const float4*>(w + c);
-      *reinterpret_cast<float4*>(yr + c) =
-          make_float4(v[j].x * r * g.x, v[j].y * r * g.y, v[j].z * r * g.z, v[j].w * r * g.w);
+      const float4 o = make_float4(v[j].x * r * g.x, v[j].y * r * g.y, v[j].z * r * g.z, v[j].w * r * g.w);
+      *reinterpret_cast<float4*>(yr + c) = o;
+      if (Y16)
+        *reinterpret_cast<uint2*>(y16 + (long long)row * dim + c) = make_uint2(bf16_pair(o.x, o.y), bf16_pair(o.z, o.w));
     }
   }
 }
@@ -448,18 +451,39 @@ size_t rmsnorm_bwd_workspace_bytes(int rows, int dim) {
 }
 
 int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
-                       hipStream_t s) {
+                       hipStream_t s, uint16_t* y16) {
   if (rows == 0) return TALOS_OK;
   dim3 g(ceil_div(rows, 4)), b(256);
   const bool vec = dim % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
                                      reinterpret_cast<uintptr_t>(w)) & 15) == 0;
+  if (y16) {
+    if (vec && dim <= 1024 && (reinterpret_cast<uintptr_t>(y16) & 7) == 0) {
+      // x read, y and its bf16 copy written, gain read, rstd written
+      ProfScope ps(s, dim <= 256 ? "rmsnorm_fwd_kernel<1, true>" : dim <= 512 ? "rmsnorm_fwd_kernel<2, true>"
+                                                                              : "rmsnorm_fwd_kernel<4, true>",
+                   4.0 * rows * dim, 4.0 * (2.0 * rows * dim + dim + (rstd ? rows : 0)) + 2.0 * rows * dim);
+      if (dim <= 256)
+        hipLaunchKernelGGL((rmsnorm_fwd_kernel<1, true>), g, b, 0, s, rows, dim, eps, x, w, y, rstd, y16);
+      else if (dim <= 512)
+        hipLaunchKernelGGL((rmsnorm_fwd_kernel<2, true>), g, b, 0, s, rows, dim, eps, x, w, y, rstd, y16);
+      else
+        hipLaunchKernelGGL((rmsnorm_fwd_kernel<4, true>), g, b, 0, s, rows, dim, eps, x, w, y, rstd, y16);
+      TALOS_LAUNCHED("rmsnorm_fwd");
+      return TALOS_OK;
+    }
+    if (int rc = rmsnorm_fwd_launch(rows, dim, eps, x, w, y, rstd, s)) return rc;
+    const float* src[1] = {y};
+    uint16_t* dst[1] = {y16};
+    const long long n[1] = {(long long)rows * dim};
+    return cvt_bf16_launch(1, src, dst, n, s);
+  }
   // x read, y written, gain read, rstd written
   ProfScope ps(s, vec && dim <= 256 ? "rmsnorm_fwd_kernel<1>" : vec && dim <= 512 ? "rmsnorm_fwd_kernel<2>"
                   : vec && dim <= 1024 ? "rmsnorm_fwd_kernel<4>" : "rmsnorm_fwd_generic",
                4.0 * rows * dim, 4.0 * (2.0 * rows * dim + dim + (rstd ? rows : 0)));
-  if (vec && dim <= 256) hipLaunchKernelGGL(rmsnorm_fwd_kernel<1>, g, b, 0, s, rows, dim, eps, x, w, y, rstd);
-  else if (vec && dim <= 512) hipLaunchKernelGGL(rmsnorm_fwd_kernel<2>, g, b, 0, s, rows, dim, eps, x, w, y, rstd);
-  else if (vec && dim <= 1024) hipLaunchKernelGGL(rmsnorm_fwd_kernel<4>, g, b, 0, s, rows, dim, eps, x, w, y, rstd);
+  if (vec && dim <= 256) hipLaunchKernelGGL(rmsnorm_fwd_kernel<1>, g, b, 0, s, rows, dim, eps, x, w, y, rstd, nullptr);
+  else if (vec && dim <= 512) hipLaunchKernelGGL(rmsnorm_fwd_kernel<2>, g, b, 0, s, rows, dim, eps, x, w, y, rstd, nullptr);
+  else if (vec && dim <= 1024) hipLaunchKernelGGL(rmsnorm_fwd_kernel<4>, g, b, 0, s, rows, dim, eps, x, w, y, rstd, nullptr);
   else hipLaunchKernelGGL(rmsnorm_fwd_generic, g, b, 0, s, rows, dim, eps, x, w, y, rstd);
   TALOS_LAUNCHED("rmsnorm_fwd");
   return TALOS_OK;

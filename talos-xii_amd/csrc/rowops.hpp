@@ -21,8 +21,9 @@ size_t rmsnorm_bwd_workspace_bytes(int rows, int dim);
 size_t reduce_parts_workspace_bytes(int nparts, int cols);
 int reduce_parts_launch(int cols, int nparts, double* part, float beta, float* out, hipStream_t s, int split = -1,
                         float* out2 = nullptr);
+// y16 (optional): also y's bf16 copy (nearest even, as cvt_bf16_launch rounds), same layout
 int rmsnorm_fwd_launch(int rows, int dim, float eps, const float* x, const float* w, float* y, float* rstd,
-                       hipStream_t s);
+                       hipStream_t s, uint16_t* y16 = nullptr);
 // bf16 copies (rounded to nearest even, the GEMM staging's conversion) of count <= 8 fp32 tensors
 // of n[i] elements in one launch
 int cvt_bf16_launch(int count, const float* const* src, uint16_t* const* dst, const long long* n, hipStream_t s);
