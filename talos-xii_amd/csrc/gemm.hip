@@ -977,6 +977,59 @@ __device__ __forceinline__ void dl_panel_kmaj(const uint16_t* __restrict__ X, lo
     __builtin_amdgcn_global_load_lds(X + (long long)(k0 + row) * ld + c0 + 8 * piece, S + 512 * blk, 16, 0, 0);
   }
 }
+// The four-stage form of the direct path takes 32-k chunks: k-contiguous panels with rows of
+// DKB = 32 bf16 (64 bytes, sixteen rows a 1 KB block), piece p of row r in slot p ^ ((r / 4) mod
+// 4), so a fragment read's 16 rows fall on distinct 16-byte bank groups; k-major panels as above
+// with 32 k rows.
+#ifndef TALOS_GEMM_BF_STAGES
+#define TALOS_GEMM_BF_STAGES 4
+#endif
+constexpr int DKB = 32;
+// One 16-byte piece a lane into LDS at lds + 16 lane (lds wave-uniform): global_load_lds_dwordx4
+// issued from inline assembly. The compiler then does not track these LDS writes, so it puts no
+// vmcnt(0) before later LDS reads (it does for the builtin, which drains every chunk in flight at
+// each chunk); the caller waits for them itself (TALOS_WAIT_VM) before the barrier that publishes
+// them. M0 holds the LDS address (the compiler sets M0 anew before each of its own uses).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_untracked(const void* src, const void* lds) {
+  const uint32_t off =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(off), "v"(src) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ void dl_panel_bf16_32(const uint16_t* __restrict__ X, long long ld, int r0, int k0,
+                                                 uint16_t* S) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int blk = w; blk < 8; blk += 4) {
+    const int row = 16 * blk + (lane >> 2), piece = (lane & 3) ^ ((row >> 2) & 3);
+    dma16_untracked(X + (long long)(r0 + row) * ld + k0 + 8 * piece, S + 512 * blk);
+  }
+}
+// dl_panel_kmaj for 32-k chunks, untracked as above
+__device__ __forceinline__ void dl_panel_kmaj_32(const uint16_t* __restrict__ X, long long ld, int k0, int c0,
+                                                 uint16_t* S) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int blk = w; blk < DKB / 4; blk += 4) {
+    const int row = 4 * blk + (lane >> 4), piece = (lane & 15) ^ (4 * (lane >> 4));
+    dma16_untracked(X + (long long)(k0 + row) * ld + c0 + 8 * piece, S + 512 * blk);
+  }
+}
+__device__ __forceinline__ bf16x8 dl_frag_bf16_32(const uint16_t* S, int r, int pc) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(S + r * DKB + 8 * (pc ^ ((r >> 2) & 3))));
+}
+// s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding: vmcnt bits 3:0,
+// expcnt 6:4, lgkmcnt 11:8)
+#define TALOS_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
+// A workgroup barrier that orders LDS accesses only: __syncthreads() also waits for every
+// outstanding global load (vmcnt 0), which would drain the later chunks' direct loads at each
+// barrier; their completion is waited for explicitly with TALOS_WAIT_VM instead.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // The MFMA fragment of product s (k = 16 s + 8 h + 0..7, the slots of dl_frag_bf16's piece
 // 2 s + h) for column cb + l32 (cb a multiple of 32) of a dl_panel_kmaj panel, by two
 // ds_read_b64_tr_b16. That instruction works on groups of 16 lanes: lane 4a + j of a group gives
@@ -1086,7 +1139,53 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
       }
       __syncthreads();
     };
-    if (TALOS_GEMM_DLDS && A16 && B16 && tile_in && p.vecA16 && p.vecB16 && kbeg < kend &&
+    if (TALOS_GEMM_DLDS && TALOS_GEMM_BF_STAGES == 4 && A16 && B16 && tile_in && p.vecA16 && p.vecB16 &&
+        kbeg < kend && (kend - kbeg) % DKB == 0) {
+      // both bf16 copies, four stages of 32-k chunks: three chunks' loads in flight while one is
+      // multiplied (four load instructions a wave a chunk), one barrier a chunk
+      constexpr int NS = 4, STG = (BM + BN) * DKB;  // bf16 values a stage
+      static_assert(NS * STG <= 2 * SMEM_BF, "four stages fit the bf16 LDS");
+      auto issue = [&](int k0, int st) {
+        if (TA)
+          dl_panel_kmaj_32(A16, p.lda, k0, m0, S16 + st * STG);
+        else
+          dl_panel_bf16_32(A16, p.lda, m0, k0, S16 + st * STG);
+        if (TB)
+          dl_panel_bf16_32(B16, p.ldb, n0, k0, S16 + st * STG + BM * DKB);
+        else
+          dl_panel_kmaj_32(B16, p.ldb, k0, n0, S16 + st * STG + BM * DKB);
+      };
+      const int nch = (kend - kbeg) / DKB;
+      for (int c = 0; c < NS - 1 && c < nch; ++c) issue(kbeg + c * DKB, c);
+      for (int c = 0; c < nch; ++c) {
+        // chunk c landed: only the chunks issued after it (at most two, four loads each) may be out
+        const int after = min(NS - 2, nch - 1 - c);
+        if (after >= 2)
+          TALOS_WAIT_VM(8);
+        else if (after == 1)
+          TALOS_WAIT_VM(4);
+        else
+          TALOS_WAIT_VM(0);
+        lds_barrier();  // every wave's pieces of chunk c are in; every wave is done with chunk c - 1
+        if (c + NS - 1 < nch) issue(kbeg + (c + NS - 1) * DKB, (c + NS - 1) % NS);  // into chunk c - 1's stage
+        const uint16_t* As = S16 + (c % NS) * STG;
+        const uint16_t* Bs = As + BM * DKB;
+#pragma unroll
+        for (int s = 0; s < DKB / 16; ++s) {
+          const bf16x8 a0 = TA ? dl_frag_kmaj(As, s, wm * 64, lane) : dl_frag_bf16_32(As, wm * 64 + l32, 2 * s + h);
+          const bf16x8 a1 =
+              TA ? dl_frag_kmaj(As, s, wm * 64 + 32, lane) : dl_frag_bf16_32(As, wm * 64 + 32 + l32, 2 * s + h);
+          const bf16x8 b0 = TB ? dl_frag_bf16_32(Bs, wn * 64 + l32, 2 * s + h) : dl_frag_kmaj(Bs, s, wn * 64, lane);
+          const bf16x8 b1 =
+              TB ? dl_frag_bf16_32(Bs, wn * 64 + 32 + l32, 2 * s + h) : dl_frag_kmaj(Bs, s, wn * 64 + 32, lane);
+          acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
+          acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc[0][1], 0, 0, 0);
+          acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
+          acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[1][1], 0, 0, 0);
+        }
+      }
+      __syncthreads();  // the epilogue reuses the LDS
+    } else if (TALOS_GEMM_DLDS && A16 && B16 && tile_in && p.vecA16 && p.vecB16 && kbeg < kend &&
         (kend - kbeg) % BKB == 0) {
       // both bf16 copies: the panels straight into LDS (k-contiguous operands by dl_panel_bf16,
       // k-major ones by dl_panel_kmaj, read back transposed), two stages, one barrier a chunk
