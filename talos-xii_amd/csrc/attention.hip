@@ -2384,10 +2384,10 @@ size_t attn_bwd_ds_bytes(const AttnDesc& d) {
   return attn_bwd_ds_supported(d) ? entry * (size_t)d.batch * d.heads * d.seq * d.seq : 0;
 }
 
-static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, bool bf16, hipStream_t s) {
+static int attn_bwd_with_ds(AttnArgs a, int dkm, int dvm, float* ds, bool bf16, bool d_ready, hipStream_t s) {
   a.ds = ds;
   const double rows = (double)a.B * a.S * a.H, tiles = (a.S + kQTile - 1) / kQTile, pairs = kept_pairs(a);
-  {  // D = rowsum(dO * O)
+  if (!d_ready) {  // D = rowsum(dO * O)
     ProfScope ps(s, "attn_rowdot_kernel", 2.0 * rows * a.dv, 4.0 * rows * (2.0 * a.dv + 1.0));
     hipLaunchKernelGGL(attn_rowdot_kernel, dim3(ceil_div((size_t)rows, 16)), dim3(256), 0, s, a);
     if (int rc = launch_status("attn_rowdot_kernel")) return rc;
@@ -2470,7 +2470,7 @@ int attn_bwd_launch(const AttnDesc& d, float* ws, hipStream_t s) {
       set_error("attention backward: the dS path needs the workspace (attn_bwd_workspace_bytes)");
       return TALOS_ERR_NULL;
     }
-    return attn_bwd_with_ds(a, dkm, dvm, d.ds, d.bf16 != 0, s);
+    return attn_bwd_with_ds(a, dkm, dvm, d.ds, d.bf16 != 0, d.d_ready != 0, s);
   }
   if (d.dq2 || d.dk2) {
     set_error("attention backward: split dq / dk outputs need the dS path (attn_ds_path)");

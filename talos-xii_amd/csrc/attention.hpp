@@ -66,6 +66,9 @@ struct AttnDesc {
   // (nearest even) into uint16_t buffers at those pointers, with the same leading dimensions in
   // elements, instead of fp32, for plans whose later products read only bf16 copies of them.
   int out_bf16 = 0;
+  // 1 (on the dS path): D = rowsum(dO . O) is already in the backward's workspace (ws[(b * heads +
+  // h) * seq + query], e.g. from the product that formed dO, GemmDesc::rd_*), so it is not formed.
+  int d_ready = 0;
 };
 
 int attn_fwd_launch(const AttnDesc& d, hipStream_t s);

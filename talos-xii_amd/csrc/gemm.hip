@@ -90,7 +90,8 @@ enum : int {
   E_NORMIN = 4096,  // RMSNorm A's rows first (GemmDesc::nin_*): B rows scaled by the gain, rows by rstd
   E_NBPRE = 8192,   // with E_NORMB: the addend sum_h P[row][h] U[sample][h] (four terms) before the norm backward
   E_CMAP = 16384,   // C's columns through the output column map (GemmArgs::cmap_*)
-  E_NBLAST = 32768  // with E_NORMB: the last-row addends (GemmDesc::normb_add_last / normb_dy_last) may be set
+  E_NBLAST = 32768,  // with E_NORMB: the last-row addends (GemmDesc::normb_add_last / normb_dy_last) may be set
+  E_ROWDOT = 65536   // also the row dots by head of C with rd_o (GemmDesc::rd_*)
 };
 
 struct GemmArgs {
@@ -111,6 +112,10 @@ struct GemmArgs {
   const float* rsin;
   int rope_cols, rope_dim, rope_seq;
   int cmap_w, cmap_pitch, cmap_off;  // output column map (GemmDesc::cmap_*; cmap_w 0: none)
+  const float* rd_o;  // E_ROWDOT (GemmDesc::rd_*)
+  long long rd_ldo;
+  float* rd_D;
+  int rd_w, rd_seq, rd_heads;
   int ksplit, kper;
   float* part;  // [batch][ksplit][M + (dbias ? 1 : 0)][N]
   float* dbias;
@@ -1553,6 +1558,23 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
           const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
           const float4 o = epi_store4<E, true>(p, v, row, col, C, resid, fast && row < p.M, pre[j]);
           if constexpr ((E & E_NORM) != 0) epi_norm4(p, o, row, col, ngain);
+          if constexpr ((E & E_ROWDOT) != 0) {
+            // the row's dot with rd_o over each head's columns: rd_w / 4 lanes a head (a 32-lane
+            // group holds one row), the products and the lane sums in the attention row-dot
+            // kernel's order (lane c holds columns 4c .. 4c + 3 of the head)
+            const bool ok = fast && row < p.M;
+            float dd = 0.f;
+            if (ok) {
+              const float4 x = *reinterpret_cast<const float4*>(p.rd_o + (long long)row * p.rd_ldo + col);
+              dd = fmaf(o.x, x.x, fmaf(o.y, x.y, fmaf(o.z, x.z, fmaf(o.w, x.w, 0.f))));
+            }
+            dd += __shfl_xor(dd, 1, 64);
+            dd += __shfl_xor(dd, 2, 64);
+            dd += __shfl_xor(dd, 4, 64);
+            if (p.rd_w == 64) dd += __shfl_xor(dd, 8, 64);
+            if (ok && col % p.rd_w == 0)
+              p.rd_D[((long long)(row / p.rd_seq) * p.rd_heads + col / p.rd_w) * p.rd_seq + row % p.rd_seq] = dd;
+          }
           if constexpr (BF) {
             if (p.C16 && row < p.M) {  // the bf16 copy of the stored values
               uint16_t* c16 = p.C16 + (long long)b * p.sC + (long long)row * p.ldc + out_col<E>(p, col);
@@ -1888,6 +1910,12 @@ static GemmArgs to_args(const GemmDesc& d) {
   a.cmap_w = d.cmap_w;
   a.cmap_pitch = d.cmap_pitch;
   a.cmap_off = d.cmap_off;
+  a.rd_o = d.rd_o;
+  a.rd_ldo = d.rd_ldo;
+  a.rd_D = d.rd_D;
+  a.rd_w = d.rd_w;
+  a.rd_seq = d.rd_seq > 0 ? d.rd_seq : 1;
+  a.rd_heads = d.rd_heads > 0 ? d.rd_heads : 1;
   a.ksplit = d.ksplit < 1 ? 1 : d.ksplit;
   a.kper = d.K;
   a.part = d.workspace;
@@ -1958,6 +1986,7 @@ static int epi_flags(const GemmDesc& d) {
   if (d.normb_dx && (d.normb_add_last || d.normb_dy_last)) e |= E_NBLAST;
   if (d.nin_gain) e |= E_NORMIN;
   if (d.cmap_w) e |= E_CMAP;
+  if (d.rd_D) e |= E_ROWDOT;
   return e;
 }
 
@@ -1974,7 +2003,7 @@ static bool use_small(const GemmDesc& d, int num_cu) {
   if (!d.bf16 && d.batch == 1 && d.N <= BN && d.M >= 64 * num_cu && !d.transA && d.ksplit <= 1 &&
       pick_m64(false, d.transB != 0, epi_flags(d)) != nullptr)
     return false;  // one 128-wide column of tiles over many rows: the 64-row tiles
-  return !d.bf16 && d.cmap_w == 0 && tiles < num_cu && macs <= 1073741824.0;
+  return !d.bf16 && d.cmap_w == 0 && !d.rd_D && tiles < num_cu && macs <= 1073741824.0;
 }
 
 size_t gemm_plan_split(GemmDesc& d, int num_cu) {
@@ -2030,6 +2059,7 @@ static GemmKernel pick_kernel(bool tA, bool tB, int e, bool bf) {
   GEMM_CASE(false, true, E_DGELU)
   GEMM_CASE(false, true, E_DRELU)
   GEMM_CASE(false, true, E_SPLIT)
+  GEMM_CASE(false, true, E_ROWDOT)
   GEMM_CASE_F32(false, true, E_NORMB)
   GEMM_CASE_F32(false, true, E_NORMB | E_NBLAST)
   GEMM_CASE_F32(false, true, E_NORMB | E_NBPRE)
@@ -2158,6 +2188,16 @@ static bool normb_fused(const GemmDesc& d) {
 }
 
 int gemm_launch(const GemmDesc& d, hipStream_t stream) {
+  if (d.rd_D) {
+    auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    TALOS_REQUIRE(!d.transA && d.transB && epi_flags(d) == E_ROWDOT && d.batch == 1 && d.N % BN == 0 &&
+                      (d.rd_w == 32 || d.rd_w == 64) && d.rd_seq > 0 && d.rd_heads > 0 &&
+                      d.N == d.rd_w * d.rd_heads && d.M % d.rd_seq == 0 && d.ldc % 4 == 0 && d.rd_ldo % 4 == 0 &&
+                      a16(d.C) && a16(d.rd_o),
+                  TALOS_ERR_UNSUPPORTED,
+                  "gemm: row dots need an NT product with a plain epilogue, N = rd_w * rd_heads a multiple of "
+                  "128 (rd_w 32 or 64), 16-byte rows");
+  }
   if (d.cmap_w) {
     const int e = epi_flags(d);
     TALOS_REQUIRE(d.cmap_w > 0 && d.cmap_w % 4 == 0 && d.cmap_pitch % 4 == 0 && d.cmap_off % 4 == 0 &&

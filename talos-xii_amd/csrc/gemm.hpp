@@ -52,6 +52,15 @@ struct GemmDesc {
   // rope part into a head-interleaved row; the epilogue's own arithmetic (RoPE) sees c. cmap_w a
   // multiple of 4; not with a split K (the library keeps it unsplit), the row norms or activations.
   int cmap_w = 0, cmap_pitch = 0, cmap_off = 0;
+  // Row dots by head (rd_D given; transA = 0, transB = 1, a plain epilogue, N % 128 == 0, rd_w
+  // 32 or 64): rd_D[((row / rd_seq) * rd_heads + c / rd_w) * rd_seq + row % rd_seq] = sum over
+  // the rd_w columns c of that head of C[row][c] * rd_o[row][c] (ldc and rd_ldo multiples of 4,
+  // 16-byte aligned), summed as the attention backward's D = rowsum(dO . O) would be when this
+  // product forms dO: that kernel's lanes and order, so the values are the same.
+  const float* rd_o = nullptr;
+  long long rd_ldo = 0;
+  float* rd_D = nullptr;
+  int rd_w = 0, rd_seq = 1, rd_heads = 1;
   // Split-K: the K range is cut into ksplit parts of kper (multiple of 32) whose fp32 partial
   // tiles are summed in f64 by a second kernel. ksplit = 0 lets the library choose.
   int ksplit = 1;

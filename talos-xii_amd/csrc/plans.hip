@@ -95,6 +95,7 @@ struct talos_plan_s {
   // path instead; the same results, as the tests check at full size
   bool unfused = false;
   bool bf16 = false;  // bf16-in / fp32-accumulate GEMMs (MLA plans with TALOS_PREC_BF16)
+  bool rowdot = true;  // MLA plans: the dO product forms the attention backward's D (TALOS_MLA_ROWDOT)
   talos::Profiler* prof = nullptr;
   // latent attention: the projections before concatenation and the attention gradients,
   // shared by all layers
@@ -773,7 +774,7 @@ static int mla_attn_forward(talos_plan_s* p, const MlaDims& D, const float* P, c
 // G) and dxn = dL/dxn (overwritten).
 static int mla_attn_backward(talos_plan_s* p, const MlaDims& D, const float* P, float* G, const MlaW& w,
                              const float* xn, const talos_plan_s::Layer& L, const float* g_o, float* dxn,
-                             hipStream_t s) {
+                             hipStream_t s, bool d_ready = false) {
   const int M = D.batch * D.seq, d = D.d, H = D.H, Lt = D.L, r = D.r, hd = D.hd, vd = D.vd;
   const size_t MH = (size_t)M * H;
   auto& m = p->ms;
@@ -783,6 +784,7 @@ static int mla_attn_backward(talos_plan_s* p, const MlaDims& D, const float* P, 
   int rc;
   bool out16 = false;
   if (attn_ds_path(a)) {
+    a.d_ready = d_ready ? 1 : 0;
     // the content and rope parts of dq / dk to their own buffers
     a.dq = m.dqc;
     a.lddq = (long long)H * hd;
@@ -2312,8 +2314,36 @@ static int mla_fwd_bwd(talos_plan_s* p, const float* P, const float* x, const fl
   if ((rc = mm(p, s, 0, 0, M, d, ow, L.o, ow, P + o.w.wo, d, out, d, 0.f, nullptr, x, d))) return rc;
   // ---- backward
   if ((rc = mm(p, s, 1, 0, ow, d, M, L.o, ow, gout, d, G + o.w.wo, d))) return rc;
-  if ((rc = mm(p, s, 0, 1, M, ow, d, gout, d, P + o.w.wo, d, p->g_o, ow))) return rc;
-  if ((rc = mla_attn_backward(p, D, P, G, o.w, L.xn1, L, p->g_o, p->g_xn, s))) return rc;
+  // dO = gout . Wo^T; where the attention backward takes the dS path, the product's epilogue also
+  // forms that backward's D = rowsum(dO . O) into its workspace (no row-dot launch)
+  const bool d_ready =
+      p->rowdot && attn_ds_path(mla_attn_desc(p, D, L)) && (c.v_dim == 32 || c.v_dim == 64) && ow % 128 == 0;
+  if (d_ready) {
+    GemmDesc g;
+    g.transB = 1;
+    g.M = M;
+    g.N = ow;
+    g.K = d;
+    g.A = gout;
+    g.lda = d;
+    g.B = P + o.w.wo;
+    g.ldb = d;
+    g.C = p->g_o;
+    g.ldc = ow;
+    g.rd_o = L.o;
+    g.rd_ldo = ow;
+    g.rd_D = p->attn_ws;
+    g.rd_w = c.v_dim;
+    g.rd_seq = c.seq;
+    g.rd_heads = c.n_heads;
+    g.ksplit = 1;
+    g.bf16 = p->bf16;
+    bf16_operands(p, g);
+    if ((rc = gemm_launch(g, s))) return rc;
+  } else if ((rc = mm(p, s, 0, 1, M, ow, d, gout, d, P + o.w.wo, d, p->g_o, ow))) {
+    return rc;
+  }
+  if ((rc = mla_attn_backward(p, D, P, G, o.w, L.xn1, L, p->g_o, p->g_xn, s, d_ready))) return rc;
   // residual + rmsnorm
   return rmsnorm_bwd_launch(M, d, x, P + o.g, L.rstd1, p->g_xn, 1.f, dx, 0.f, G + o.g, p->red_ws, s, gout);
 }
@@ -2824,6 +2854,9 @@ int talos_mla_plan_create(const talos_mla_cfg* cfg, talos_plan* plan) {
   rc |= plan_alloc(p, &p->g_xn, M * d);
   rc |= plan_alloc(p, &p->attn_ws, M * H);
   if (rc == TALOS_OK) rc = alloc_mla_scratch(p, D);
+  // TALOS_MLA_ROWDOT=0 at plan creation: the attention backward forms D itself (attn_rowdot_kernel)
+  const char* rowdot_env = std::getenv("TALOS_MLA_ROWDOT");
+  p->rowdot = !(rowdot_env && rowdot_env[0] == '0');
   // TALOS_BF16_COPIES=0 at plan creation: no bf16 copies (every bf16-in product reads its fp32
   // operands and rounds them at staging; the same roundings, so the same results)
   const char* copies_env = std::getenv("TALOS_BF16_COPIES");

@@ -245,6 +245,26 @@ def test_mla_bf16_copies_bit_identical(monkeypatch, ci):
         assert np.array_equal(a, b), f"{name}: {int((a != b).sum())} elements differ, max {np.abs(a - b).max():.3e}"
 
 
+@pytest.mark.parametrize("prec", [th.PREC_FP32, th.PREC_BF16])
+@pytest.mark.parametrize("ci", [[2, 100, 128, 4, 32, 8, 24, 32, 1, 0], [1, 132, 512, 8, 128, 32, 64, 64, 1, 0],
+                                [2, 256, 512, 8, 128, 32, 64, 64, 0, 0]])
+def test_mla_fused_rowdot_bit_identical(monkeypatch, ci, prec):
+    """The attention backward's D = rowsum(dO . O) formed in the epilogue of the product that
+    forms dO gives bit-identical results to the row-dot kernel (TALOS_MLA_ROWDOT=0): the epilogue
+    sums each head's products in that kernel's lanes and order, so a difference is a wrong row,
+    head or D index. Head widths 32 and 64, causal and not."""
+    from common import mla_params
+    rng = np.random.default_rng(4300 + ci[1] + ci[2])
+    B, S, d = ci[:3]
+    p = f32(mla_params(rng, ci))
+    x, G = f32(rng.normal(size=(B, S, d))), f32(rng.normal(size=(B, S, d)))
+    fused = run_mla(ci, prec, p, x, G)
+    monkeypatch.setenv("TALOS_MLA_ROWDOT", "0")
+    apart = run_mla(ci, prec, p, x, G)
+    for name, a, b in zip(("out", "dparams", "dx"), fused, apart):
+        assert np.array_equal(a, b), f"{name}: {int((a != b).sum())} elements differ, max {np.abs(a - b).max():.3e}"
+
+
 def test_mla_plan_over_ds_budget_is_created():
     """A plan whose dS rows would exceed the budget (seq 2048 at batch 64, 8 heads: 8.6 GB in
     fp32, 4.3 GB in bf16, against 4 GiB) is still created, on the tiled path."""
