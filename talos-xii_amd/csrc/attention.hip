@@ -533,6 +533,15 @@ __device__ __forceinline__ float4 block_ld4(const float* __restrict__ base, long
   for (int j = 0; j < 4; ++j) v[j] = col + j < dim ? src[j] : 0.f;
   return make_float4(v[0], v[1], v[2], v[3]);
 }
+// block_ld4's element group g as an offset from the block's first element (row0's, at col0): where
+// every row of a block is below nrows and dim == DM (16-byte rows), a tiled kernel's loop loads
+// it from the block's wave-uniform start plus this loop-invariant offset, one unconditional
+// float4 load each (rows * ld < 2^31: the plans' 32-bit indexing bound)
+template <int DM>
+__device__ __forceinline__ int block_off(long long ld, int g) {
+  const int idx = 4 * g;
+  return (int)((idx / DM) * ld) + idx % DM;
+}
 // ... and its place in an LDS block of pitch P
 template <int DM, int P>
 __device__ __forceinline__ void block_st4(float* tile, int g, float4 v) {
@@ -1671,10 +1680,21 @@ attn_bwd_dq_ds_bf16_kernel(AttnArgs a) {
   const uint16_t* dsp = reinterpret_cast<const uint16_t*>(a.ds) + (long long)pair * a.S * a.S;  // bf16 rows
   float4 rk[KL];
   uint2 rd[4];
-  auto fetch = [&](int kb) {
+  // whole 32-row blocks with 16-byte rows and no head padding: loop-invariant addresses
+  const bool fast = a.vec && a.dk == DKM;
+  int kbo[KL];
 #pragma unroll
-    for (int i = 0; i < KL; ++i)
-      rk[i] = ATTN_BLK_K(DKM, kb * 32, i * 256 + t);
+  for (int i = 0; i < KL; ++i) kbo[i] = block_off<DKM>(a.ldk, i * 256 + t);
+  auto fetch = [&](int kb) {
+    if (fast && (kb + 1) * 32 <= a.S) {
+      const float* kblk = a.k + (tok0 + kb * 32) * a.ldk + hd * a.dk;
+#pragma unroll
+      for (int i = 0; i < KL; ++i) rk[i] = *reinterpret_cast<const float4*>(kblk + kbo[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < KL; ++i)
+        rk[i] = ATTN_BLK_K(DKM, kb * 32, i * 256 + t);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {  // query row g / 8 of the tile, keys 4 (g % 8) .. + 3
       const int g = i * 256 + t, qr = tile * kQTile + (g >> 3), k = kb * 32 + 4 * (g & 7);
