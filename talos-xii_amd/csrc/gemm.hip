@@ -2208,6 +2208,7 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
                   "RoPE epilogue");
   }
   if (d.normb_dx) {
+    if (d.normb_defer) d.normb_defer->cols = 0;  // (filled below where held back)
     if (!normb_fused(d)) {
       // the product into C, then the row-norm backward kernel
       TALOS_REQUIRE(d.C != nullptr && d.ldc == d.N, TALOS_ERR_UNSUPPORTED,
@@ -2239,7 +2240,19 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
     if (int rc = gemm_launch_one(g, stream)) return rc;
     if (!d.normb_dw) return TALOS_OK;
     const int bm = tile_rows(d, epi_flags(d), 1);
-    return reduce_parts_launch(d.N, (d.M + bm - 1) / bm, d.normb_ws, d.normb_beta_dw, d.normb_dw, stream);
+    const int nparts = (d.M + bm - 1) / bm;
+    if (d.normb_defer && nparts <= kPartsOnePass) {
+      PartsJob& J = *d.normb_defer;
+      J.cols = d.N;
+      J.nparts = nparts;
+      J.part = d.normb_ws;
+      J.beta = d.normb_beta_dw;
+      J.out = d.normb_dw;
+      J.split = -1;
+      J.out2 = nullptr;
+      return TALOS_OK;
+    }
+    return reduce_parts_launch(d.N, nparts, d.normb_ws, d.normb_beta_dw, d.normb_dw, stream);
   }
   return gemm_launch_one(d, stream);
 }

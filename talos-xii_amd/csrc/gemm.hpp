@@ -3,6 +3,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "rowops.hpp"
 
 namespace talos {
 
@@ -110,6 +111,11 @@ struct GemmDesc {
   float normb_beta_dw = 0.f;
   double* normb_ws = nullptr;
   size_t normb_ws_bytes = 0;
+  // Where the gain gradient's combination would be one reduce_parts pass after the fused
+  // product: held back into *normb_defer instead of launched (for reduce_parts_batch_launch;
+  // normb_ws must then stay untouched until that runs). Otherwise normb_defer->cols is set to 0
+  // and it runs here.
+  PartsJob* normb_defer = nullptr;
   // bf16-in / fp32-accumulate: operands are rounded to bf16 (nearest even) as they are staged
   // into LDS and multiplied with v_mfma_f32_32x32x16_bf16; HBM layout and outputs stay fp32.
   bool bf16 = false;

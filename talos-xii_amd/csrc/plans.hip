@@ -63,6 +63,13 @@ struct talos_plan_s {
   size_t gemm_ws_bytes = 0;
   double* red_ws = nullptr;
   size_t red_ws_bytes = 0;
+  // PPO backward: the gain and embedding gradients' partial-sum combinations are held back and
+  // run as one launch at the end (reduce_parts_batch_launch), each job's partials in a slot of
+  // hold_ws (red_ws_bytes each) of its own until then
+  double* hold_ws = nullptr;
+  int hold_slots = 0, hold_next = 0;
+  bool holding = false;
+  std::vector<talos::PartsJob> held;
   // The backward's side stream: weight-gradient products run there as soon as the main stream has
   // produced their operands, with their own split-K workspace, overlapping the main stream's
   // memory-bound kernels. Before the main stream overwrites a buffer such a product reads, it waits
@@ -464,6 +471,13 @@ static int alloc_workspaces(talos_plan_s* p) {
   float* red = nullptr;
   rc |= plan_alloc(p, &red, (p->red_ws_bytes + 3) / 4 + 2);
   p->red_ws = reinterpret_cast<double*>(red);
+  if (p->kind == 2 && !p->unfused) {
+    // two norm gains a layer, the tail's pair and the embedding, one slot each (8-byte aligned)
+    p->hold_slots = 2 * p->ppo.n_layers + 2;
+    float* hold = nullptr;
+    rc |= plan_alloc(p, &hold, (size_t)p->hold_slots * ((p->red_ws_bytes + 7) / 8) * 2);
+    p->hold_ws = reinterpret_cast<double*>(hold);
+  }
   if (rc) return TALOS_ERR_ALLOC;
   // The backward's side stream, when TALOS_BWD_SIDE_STREAM=1 at plan creation. Off by default:
   // overlapping the two streams gains about 1 % of the C4 step, but then the duration of a
@@ -639,6 +653,21 @@ static int before_write(talos_plan_s* p, hipStream_t s, const void* buf) {
   return TALOS_OK;
 }
 
+// The next free slot of hold_ws while the PPO backward holds its reductions back, else nullptr.
+static double* hold_slot(talos_plan_s* p) {
+  if (!p->holding || !p->hold_ws || p->hold_next >= p->hold_slots) return nullptr;
+  return p->hold_ws + (size_t)(p->hold_next++) * ((p->red_ws_bytes + 7) / 8);
+}
+// The held-back reductions, in batches of kPartsJobsMax.
+static int hold_flush(talos_plan_s* p, hipStream_t s) {
+  int rc = TALOS_OK;
+  for (size_t i = 0; i < p->held.size() && rc == TALOS_OK; i += kPartsJobsMax)
+    rc = reduce_parts_batch_launch((int)std::min<size_t>(kPartsJobsMax, p->held.size() - i), p->held.data() + i, s);
+  p->held.clear();
+  p->hold_next = 0;
+  return rc;
+}
+
 // dx = RMSNorm backward of dy = g.W^T ([M, K] x [d, K]^T, d = 128 fits one tile row) with the
 // norm's input x, gain and rstd; the product's epilogue computes it (C = dy is then not written,
 // else C is the scratch the separate kernels use). add: the residual gradient on every row;
@@ -673,10 +702,16 @@ static int norm_bwd_mm(talos_plan_s* p, hipStream_t s, int M, int d, int K, cons
   gd.normb_lens = p->lens;
   gd.normb_dx = dx;
   gd.normb_dw = dw;
-  gd.normb_ws = p->red_ws;
+  // the gain gradient's combination held back where the PPO backward collects them
+  double* slot = dw ? hold_slot(p) : nullptr;
+  PartsJob job;
+  gd.normb_ws = slot ? slot : p->red_ws;
   gd.normb_ws_bytes = p->red_ws_bytes;
+  gd.normb_defer = slot ? &job : nullptr;
   gd.fuse_norm = !p->unfused;
-  return gemm_launch(gd, s);
+  const int rc = gemm_launch(gd, s);
+  if (rc == TALOS_OK && job.cols > 0) p->held.push_back(job);
+  return rc;
 }
 
 // Everything issued on the side stream completes before anything issued later on s.
@@ -2002,7 +2037,8 @@ static int tail_bwd_launch(talos_plan_s* p, const talos_ppo_cfg& c, const talos_
   a.g_u = R.g_u;
   a.g_h2 = R.g_h2;
   a.g_o = R.g_o;
-  a.part = p->red_ws;
+  double* slot = hold_slot(p);  // (held back where the PPO backward collects them)
+  a.part = slot ? slot : p->red_ws;
   {
     const double flops = 2.0 * B * (2.0 * D * D + 2.0 * D * F);
     const double bytes = 4.0 * (2.0 * D * D + 2.0 * D * F + 2.0 * D) + 4.0 * B * (3.0 * D + 2.0 + F + 3.0 * D + F) +
@@ -2015,7 +2051,18 @@ static int tail_bwd_launch(talos_plan_s* p, const talos_ppo_cfg& c, const talos_
       hipLaunchKernelGGL((ppo_tail_bwd_kernel<64, 128>), grid, dim3(kTailThreads), 0, s, a);
     if ((rc = launch_status("ppo_tail_bwd_kernel"))) return rc;
   }
-  if ((rc = reduce_parts_launch(2 * D, nblk, a.part, 0.f, G + po.gf, s, D, G + bo.g2))) return rc;
+  if (slot && nblk <= kPartsOnePass) {
+    PartsJob job;
+    job.cols = 2 * D;
+    job.nparts = nblk;
+    job.part = a.part;
+    job.out = G + po.gf;
+    job.split = D;
+    job.out2 = G + bo.g2;
+    p->held.push_back(job);
+  } else if ((rc = reduce_parts_launch(2 * D, nblk, a.part, 0.f, G + po.gf, s, D, G + bo.g2))) {
+    return rc;
+  }
   // out_proj, W2, W1 and Wo from the row gradients
   RowsWgrad rw;
   rw.add(p->lastn, D, D, p->g_pout, D, D, G + po.wout, D, G + po.bout);
@@ -2637,6 +2684,10 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
     offs.push_back(block_offsets(bc, base));
     base = offs.back().end;
   }
+  // from here the gain and embedding gradients' combinations are held back (hold_flush below)
+  p->held.clear();
+  p->hold_next = 0;
+  p->holding = p->hold_ws != nullptr;
   const bool tail = tail_fused(p, c);
   if (tail) {  // out_proj through the last layer's MLP half: the row gradients in one kernel
     if ((rc = tail_bwd_launch(p, c, bc, params, G, offs.back(), po, s))) return rc;
@@ -2734,17 +2785,31 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
   }
   // embed
   if (embed_wgrad_applies(c, po, states, gcur)) {
+    double* slot = kEmbedBlocks <= kPartsOnePass ? hold_slot(p) : nullptr;
+    double* part = slot ? slot : p->red_ws;
     {
       ProfScope ps_e(s, "embed_wgrad_kernel", 2.0 * M * (kEmbedIn + 1) * d,
                      4.0 * M * (kEmbedIn + d) + 8.0 * kEmbedBlocks * (kEmbedIn + 1) * d);
-      hipLaunchKernelGGL(embed_wgrad_kernel, dim3(kEmbedBlocks), dim3(256), 0, s, M, states, gcur, p->red_ws);
+      hipLaunchKernelGGL(embed_wgrad_kernel, dim3(kEmbedBlocks), dim3(256), 0, s, M, states, gcur, part);
       TALOS_LAUNCHED("embed_wgrad_kernel");
     }
-    rc = reduce_parts_launch((kEmbedIn + 1) * d, kEmbedBlocks, p->red_ws, 0.f, G + po.we, s);
+    if (slot) {
+      PartsJob job;
+      job.cols = (kEmbedIn + 1) * d;
+      job.nparts = kEmbedBlocks;
+      job.part = part;
+      job.out = G + po.we;
+      p->held.push_back(job);
+    } else {
+      rc = reduce_parts_launch((kEmbedIn + 1) * d, kEmbedBlocks, part, 0.f, G + po.we, s);
+    }
   } else {
     rc = wgrad(p, s, gcur, c.in_dim, d, M, states, c.in_dim, gcur, d, G + po.we, d, G + po.be);
   }
   if (rc) return rc;
+  // the held-back gain and embedding gradient combinations, in one launch
+  p->holding = false;
+  if ((rc = hold_flush(p, s))) return rc;
   return join_side(p, s);
 }
 

@@ -85,15 +85,16 @@ __global__ __launch_bounds__(256) void colsum_partial_kernel(int rows, int cols,
 // waves; lane (column lane % 16, q = lane / 16) of wave w adds partials p = 4w + q + 64i in i
 // order with eight loads in flight, so a wave reads four 128-byte row pieces per load; the 64
 // sums of a column are then added in a fixed order.
-constexpr int kOnePassParts = 4096;
-// Columns from split on go to out2[c - split] (two gradients reduced in one launch).
-__global__ __launch_bounds__(1024) void reduce_parts_kernel(int cols, int nparts, const double* __restrict__ part,
-                                                            float beta, float* __restrict__ out, int split,
-                                                            float* __restrict__ out2) {
+constexpr int kOnePassParts = kPartsOnePass;
+// Columns from split on go to out2[c - split] (two gradients reduced in one launch). blk: the
+// workgroup's 16-column group.
+__device__ __forceinline__ void reduce_parts_cols(int cols, int nparts, const double* __restrict__ part, float beta,
+                                                  float* __restrict__ out, int split, float* __restrict__ out2,
+                                                  int blk) {
   __shared__ double red[64][16];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int cl = lane & 15, q = lane >> 4;
-  const int c = blockIdx.x * 16 + cl;
+  const int c = blk * 16 + cl;
   double acc = 0.0;
   if (c < cols) {
     const long long step = 64LL * cols;
@@ -125,6 +126,23 @@ __global__ __launch_bounds__(1024) void reduce_parts_kernel(int cols, int nparts
     float* o = c < split ? out + c : out2 + (c - split);
     *o = (float)(t + (beta != 0.f ? (double)*o : 0.0));
   }
+}
+__global__ __launch_bounds__(1024) void reduce_parts_kernel(int cols, int nparts, const double* __restrict__ part,
+                                                            float beta, float* __restrict__ out, int split,
+                                                            float* __restrict__ out2) {
+  reduce_parts_cols(cols, nparts, part, beta, out, split, out2, blockIdx.x);
+}
+// Held-back reductions in one launch: job k takes workgroups [start[k], start[k + 1]).
+struct PartsBatch {
+  PartsJob j[kPartsJobsMax];
+  int start[kPartsJobsMax + 1];
+  int n;
+};
+__global__ __launch_bounds__(1024) void reduce_parts_batch_kernel(PartsBatch b) {
+  int k = 0;
+  while (k + 1 < b.n && (int)blockIdx.x >= b.start[k + 1]) ++k;  // uniform
+  const PartsJob& J = b.j[k];
+  reduce_parts_cols(J.cols, J.nparts, J.part, J.beta, J.out, J.split, J.out2, (int)blockIdx.x - b.start[k]);
 }
 
 // First level for many partials: workgroup (x = 64-column group, y = group of kGroupParts
@@ -174,6 +192,31 @@ int reduce_parts_launch(int cols, int nparts, double* part, float beta, float* o
 }
 
 size_t reduce_parts_workspace_bytes(int nparts, int cols) { return parts_rows(nparts) * cols * sizeof(double); }
+
+int reduce_parts_batch_launch(int count, const PartsJob* jobs, hipStream_t s) {
+  TALOS_REQUIRE(count >= 0 && count <= kPartsJobsMax, TALOS_ERR_SHAPE, "reduction batch: %d jobs (at most %d)", count,
+                kPartsJobsMax);
+  PartsBatch b{};
+  b.n = 0;
+  b.start[0] = 0;
+  double cells = 0.0;
+  for (int i = 0; i < count; ++i) {
+    PartsJob J = jobs[i];
+    if (J.cols <= 0) continue;
+    TALOS_REQUIRE(J.nparts >= 0 && J.nparts <= kOnePassParts && J.part && J.out, TALOS_ERR_SHAPE,
+                  "reduction batch: a job needs one pass (at most %d partials), partials and an output", kOnePassParts);
+    if (J.split < 0 || J.split > J.cols || J.out2 == nullptr) J.split = J.cols;
+    b.j[b.n] = J;
+    b.start[b.n + 1] = b.start[b.n] + (int)ceil_div(J.cols, 16);
+    cells += (double)J.nparts * J.cols;
+    ++b.n;
+  }
+  if (b.n == 0) return TALOS_OK;
+  ProfScope ps(s, "reduce_parts_batch_kernel", cells, 8.0 * cells);
+  hipLaunchKernelGGL(reduce_parts_batch_kernel, dim3(b.start[b.n]), dim3(1024), 0, s, b);
+  TALOS_LAUNCHED("reduce_parts_batch_kernel");
+  return TALOS_OK;
+}
 
 size_t colsum_workspace_bytes(int rows, int cols) { return parts_rows(colsum_parts(rows)) * cols * sizeof(double); }
 

@@ -19,6 +19,22 @@ size_t rmsnorm_bwd_workspace_bytes(int rows, int dim);
 // the launch: out = beta * out + the fixed-order f64 sum of the partial rows (columns from split
 // on into out2 instead, when out2 is given).
 size_t reduce_parts_workspace_bytes(int nparts, int cols);
+// A reduce_parts_launch held back to run in a batch (one pass: nparts <= 4096): the same
+// arguments. cols == 0: none.
+struct PartsJob {
+  int cols = 0, nparts = 0;
+  const double* part = nullptr;
+  float beta = 0.f;
+  float* out = nullptr;
+  int split = -1;
+  float* out2 = nullptr;
+};
+constexpr int kPartsJobsMax = 8;
+constexpr int kPartsOnePass = 4096;  // partial rows one reduce_parts pass takes
+// Up to kPartsJobsMax held-back reductions in one launch, each summed as reduce_parts_launch
+// would (the same workgroups' arithmetic and order: the same results); their outputs must be
+// distinct.
+int reduce_parts_batch_launch(int count, const PartsJob* jobs, hipStream_t s);
 int reduce_parts_launch(int cols, int nparts, double* part, float beta, float* out, hipStream_t s, int split = -1,
                         float* out2 = nullptr);
 // y16 (optional): also y's bf16 copy (nearest even, as cvt_bf16_launch rounds), same layout
