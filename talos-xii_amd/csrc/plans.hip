@@ -63,9 +63,9 @@ struct talos_plan_s {
   size_t gemm_ws_bytes = 0;
   double* red_ws = nullptr;
   size_t red_ws_bytes = 0;
-  // PPO backward: the gain and embedding gradients' partial-sum combinations are held back and
-  // run as one launch at the end (reduce_parts_batch_launch), each job's partials in a slot of
-  // hold_ws (red_ws_bytes each) of its own until then
+  // Block and PPO backward: the gain (and embedding) gradients' partial-sum combinations are held
+  // back and run as one launch at the end (reduce_parts_batch_launch), each job's partials in a
+  // slot of hold_ws (red_ws_bytes each) of its own until then
   double* hold_ws = nullptr;
   int hold_slots = 0, hold_next = 0;
   bool holding = false;
@@ -471,9 +471,9 @@ static int alloc_workspaces(talos_plan_s* p) {
   float* red = nullptr;
   rc |= plan_alloc(p, &red, (p->red_ws_bytes + 3) / 4 + 2);
   p->red_ws = reinterpret_cast<double*>(red);
-  if (p->kind == 2 && !p->unfused) {
-    // two norm gains a layer, the tail's pair and the embedding, one slot each (8-byte aligned)
-    p->hold_slots = 2 * p->ppo.n_layers + 2;
+  if ((p->kind == 1 || p->kind == 2) && !p->unfused) {
+    // two norm gains a layer (and the PPO plans' tail pair and embedding), one slot each
+    p->hold_slots = p->kind == 1 ? 2 : 2 * p->ppo.n_layers + 2;
     float* hold = nullptr;
     rc |= plan_alloc(p, &hold, (size_t)p->hold_slots * ((p->red_ws_bytes + 7) / 8) * 2);
     p->hold_ws = reinterpret_cast<double*>(hold);
@@ -658,6 +658,16 @@ static double* hold_slot(talos_plan_s* p) {
   if (!p->holding || !p->hold_ws || p->hold_next >= p->hold_slots) return nullptr;
   return p->hold_ws + (size_t)(p->hold_next++) * ((p->red_ws_bytes + 7) / 8);
 }
+// Ends the holding when the backward returns, also on an early error return.
+struct HoldScope {
+  talos_plan_s* p;
+  explicit HoldScope(talos_plan_s* q) : p(q) {
+    p->held.clear();
+    p->hold_next = 0;
+    p->holding = p->hold_ws != nullptr;
+  }
+  ~HoldScope() { p->holding = false; }
+};
 // The held-back reductions, in batches of kPartsJobsMax.
 static int hold_flush(talos_plan_s* p, hipStream_t s) {
   int rc = TALOS_OK;
@@ -2458,7 +2468,13 @@ int talos_block_fwd_bwd_f32(talos_plan plan, const float* params, const float* x
   L.out = own_out;
   if (rc) return rc;
   if (out && !direct) TALOS_HIP(hipMemcpyAsync(out, L.out, M * d * 4, hipMemcpyDeviceToDevice, s));
-  rc = block_backward(plan, c, params, dparams, bo, L, gout, dx, s);
+  {
+    // the two gain gradients' combinations held back and run as one launch after the backward
+    HoldScope hold(plan);
+    rc = block_backward(plan, c, params, dparams, bo, L, gout, dx, s);
+    plan->holding = false;
+    if (rc == TALOS_OK) rc = hold_flush(plan, s);
+  }
   if (rc) return rc;
   return entry_done(join_side(plan, s), as_stream(stream));
 }
@@ -2685,9 +2701,7 @@ static int ppo_minibatch(talos_plan_s* p, int n, const float* params, const floa
     base = offs.back().end;
   }
   // from here the gain and embedding gradients' combinations are held back (hold_flush below)
-  p->held.clear();
-  p->hold_next = 0;
-  p->holding = p->hold_ws != nullptr;
+  HoldScope hold(p);
   const bool tail = tail_fused(p, c);
   if (tail) {  // out_proj through the last layer's MLP half: the row gradients in one kernel
     if ((rc = tail_bwd_launch(p, c, bc, params, G, offs.back(), po, s))) return rc;
