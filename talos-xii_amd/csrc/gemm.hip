@@ -1842,15 +1842,14 @@ __global__ __launch_bounds__(NT) void gemm_small_kernel(GemmArgs p) {
 // (small workgroups, so the reduction finds room beside a product running on another stream).
 // Row M of the partials (when present) holds the bias-gradient column sums.
 template <int E>
-__global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmArgs p) {
+__device__ __forceinline__ void splitk_reduce_tile(const GemmArgs& p, int blk, int b) {
   constexpr int W = 4;
   __shared__ double red[W][64];
   const int rows = p.M + (p.dbias ? 1 : 0);
   const long long RN = (long long)rows * p.N;
-  const int b = blockIdx.y;
   const float* P = p.part + (long long)b * p.ksplit * RN;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const long long e = (long long)blockIdx.x * 64 + lane;
+  const long long e = (long long)blk * 64 + lane;
   double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
   if (e < RN) {
     int k = w;
@@ -1879,6 +1878,32 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmArgs p) {
   if constexpr ((E & E_BETA) != 0) v += p.beta * C[(long long)row * p.ldc + col];
   if constexpr ((E & E_BIAS) != 0) v += p.bias[col];
   C[(long long)row * p.ldc + col] = v;
+}
+template <int E>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmArgs p) {
+  splitk_reduce_tile<E>(p, blockIdx.x, blockIdx.y);
+}
+// Held-back plain combinations in one launch: job k takes workgroups [start[k], start[k + 1]).
+struct SplitBatch {
+  SplitJob j[kSplitJobsMax];
+  int start[kSplitJobsMax + 1];
+  int n;
+};
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_batch(SplitBatch sb) {
+  int k = 0;
+  while (k + 1 < sb.n && (int)blockIdx.x >= sb.start[k + 1]) ++k;  // uniform
+  const SplitJob& J = sb.j[k];
+  GemmArgs p{};
+  p.part = const_cast<float*>(J.part);
+  p.ksplit = J.ksplit;
+  p.M = J.M;
+  p.N = J.N;
+  p.C = J.C;
+  p.ldc = J.ldc;
+  p.alpha = J.alpha;
+  p.dbias = J.dbias;
+  p.beta_dbias = J.beta_dbias;
+  splitk_reduce_tile<0>(p, (int)blockIdx.x - sb.start[k], 0);
 }
 
 static GemmArgs to_args(const GemmDesc& d) {
@@ -2187,7 +2212,30 @@ static bool normb_fused(const GemmDesc& d) {
          d.normb_ws_bytes >= reduce_parts_workspace_bytes(tiles_m, d.N);
 }
 
+int gemm_splitk_batch_launch(int count, const SplitJob* jobs, hipStream_t stream) {
+  TALOS_REQUIRE(count >= 0 && count <= kSplitJobsMax, TALOS_ERR_SHAPE, "split-K batch: %d jobs (at most %d)", count,
+                kSplitJobsMax);
+  SplitBatch sb{};
+  sb.n = 0;
+  sb.start[0] = 0;
+  double moved = 0.0;
+  for (int i = 0; i < count; ++i) {
+    if (!jobs[i].part) continue;
+    const long long RN = (long long)(jobs[i].M + (jobs[i].dbias ? 1 : 0)) * jobs[i].N;
+    sb.j[sb.n] = jobs[i];
+    sb.start[sb.n + 1] = sb.start[sb.n] + (int)((RN + 63) / 64);
+    moved += 4.0 * (double)RN * (jobs[i].ksplit + 1);
+    ++sb.n;
+  }
+  if (sb.n == 0) return TALOS_OK;
+  ProfScope ps(stream, "gemm_splitk_reduce_batch", 0.0, moved);
+  hipLaunchKernelGGL(gemm_splitk_reduce_batch, dim3(sb.start[sb.n]), dim3(256), 0, stream, sb);
+  TALOS_LAUNCHED("gemm_splitk_reduce_batch");
+  return TALOS_OK;
+}
+
 int gemm_launch(const GemmDesc& d, hipStream_t stream) {
+  if (d.split_defer) d.split_defer->part = nullptr;  // (filled where the combination is held back)
   if (d.rd_D) {
     auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
     TALOS_REQUIRE(!d.transA && d.transB && epi_flags(d) == E_ROWDOT && d.batch == 1 && d.N % BN == 0 &&
@@ -2260,6 +2308,19 @@ int gemm_launch(const GemmDesc& d, hipStream_t stream) {
 // The fixed-order f64 combination of a split-K product's partials (and the bias epilogue).
 static int split_reduce(const GemmDesc& d, const GemmArgs& a, int e, hipStream_t stream) {
   const long long RN = (long long)(d.M + (d.dbias ? 1 : 0)) * d.N;
+  if (d.split_defer && (e & (E_BETA | E_BIAS)) == 0 && d.batch == 1) {
+    SplitJob& J = *d.split_defer;
+    J.part = a.part;
+    J.ksplit = a.ksplit;
+    J.M = d.M;
+    J.N = d.N;
+    J.C = d.C;
+    J.ldc = d.ldc;
+    J.alpha = a.alpha;
+    J.dbias = d.dbias;
+    J.beta_dbias = d.beta_dbias;
+    return TALOS_OK;
+  }
   dim3 rg((unsigned)((RN + 63) / 64), d.batch);
   const int re = e & (E_BETA | E_BIAS);
   char rname[48];

@@ -18,6 +18,18 @@ enum GemmDAct { GEMM_DACT_NONE = 0, GEMM_DACT_GELU = 1, GEMM_DACT_RELU = 2 };
 // [0, rope_cols) with position row % rope_seq.
 // Row-major storage; op(A) is [M,K]: A[m*lda + k] (transA = 0) or A[k*lda + m] (transA = 1);
 // op(B) is [K,N]: B[k*ldb + n] (transB = 0) or B[n*ldb + k] (transB = 1).
+// A split-K product's partials' combination held back (GemmDesc::split_defer). part null: none.
+struct SplitJob {
+  const float* part = nullptr;
+  int ksplit = 0, M = 0, N = 0;
+  float* C = nullptr;
+  long long ldc = 0;
+  float alpha = 1.f;
+  float* dbias = nullptr;
+  float beta_dbias = 0.f;
+};
+constexpr int kSplitJobsMax = 8;
+
 struct GemmDesc {
   int transA = 0, transB = 0;
   int M = 0, N = 0, K = 0;
@@ -116,6 +128,11 @@ struct GemmDesc {
   // normb_ws must then stay untouched until that runs). Otherwise normb_defer->cols is set to 0
   // and it runs here.
   PartsJob* normb_defer = nullptr;
+  // A split-K product whose partials' combination is plain (beta 0, no bias; the fused bias
+  // gradient allowed), one batch: that combination held back into *split_defer instead of
+  // launched, for gemm_splitk_batch_launch (the workspace must stay untouched until then).
+  // Otherwise split_defer->part is set to null and it runs here.
+  SplitJob* split_defer = nullptr;
   // bf16-in / fp32-accumulate: operands are rounded to bf16 (nearest even) as they are staged
   // into LDS and multiplied with v_mfma_f32_32x32x16_bf16; HBM layout and outputs stay fp32.
   bool bf16 = false;
@@ -132,6 +149,10 @@ bool gemm_normin_supported(const GemmDesc& d);
 size_t gemm_plan_split(GemmDesc& d, int num_cu);
 // Enqueues the GEMM. Validation of shapes and pointers is the caller's job.
 int gemm_launch(const GemmDesc& d, hipStream_t stream);
+// Up to kSplitJobsMax held-back split-K combinations in one launch, each summed as the
+// product's own combination would be (the same workgroups' arithmetic and order: the same
+// results); their outputs must be distinct.
+int gemm_splitk_batch_launch(int count, const SplitJob* jobs, hipStream_t stream);
 // Two products in one launch where both are split-K weight gradients of one shape class (each
 // with its own workspace); otherwise gemm_launch on each.
 int gemm_launch_pair(const GemmDesc& d0, const GemmDesc& d1, hipStream_t stream);

@@ -70,6 +70,12 @@ struct talos_plan_s {
   int hold_slots = 0, hold_next = 0;
   bool holding = false;
   std::vector<talos::PartsJob> held;
+  // Block and MLA backward (one stream): the split-K weight gradients' combinations too, each
+  // product's partials in a slot of hold_gws (gemm_ws_bytes each). Not the PPO plans': their
+  // partials (64 MB a product at C4) would leave the Infinity Cache before the end.
+  float* hold_gws = nullptr;
+  int hold_gslots = 0, hold_gnext = 0;
+  std::vector<talos::SplitJob> held_split;
   // The backward's side stream: weight-gradient products run there as soon as the main stream has
   // produced their operands, with their own split-K workspace, overlapping the main stream's
   // memory-bound kernels. Before the main stream overwrites a buffer such a product reads, it waits
@@ -478,6 +484,11 @@ static int alloc_workspaces(talos_plan_s* p) {
     rc |= plan_alloc(p, &hold, (size_t)p->hold_slots * ((p->red_ws_bytes + 7) / 8) * 2);
     p->hold_ws = reinterpret_cast<double*>(hold);
   }
+  if ((p->kind == 1 || p->kind == 3) && !p->unfused && p->gemm_ws_bytes > 0) {
+    // the block's four weight-gradient products (two launches when paired), the MLA block's seven
+    p->hold_gslots = p->kind == 1 ? 4 : 8;
+    rc |= plan_alloc(p, &p->hold_gws, (size_t)p->hold_gslots * (align_ws(p->gemm_ws_bytes) / sizeof(float)));
+  }
   if (rc) return TALOS_ERR_ALLOC;
   // The backward's side stream, when TALOS_BWD_SIDE_STREAM=1 at plan creation. Off by default:
   // overlapping the two streams gains about 1 % of the C4 step, but then the duration of a
@@ -495,6 +506,42 @@ static int alloc_workspaces(talos_plan_s* p) {
 // The embedding gradient kernel's workgroups and input width (embed_wgrad_kernel).
 constexpr int kEmbedBlocks = 1024;
 constexpr int kEmbedIn = 8;
+
+// The next free slot of hold_ws while the PPO backward holds its reductions back, else nullptr.
+static double* hold_slot(talos_plan_s* p) {
+  if (!p->holding || !p->hold_ws || p->hold_next >= p->hold_slots) return nullptr;
+  return p->hold_ws + (size_t)(p->hold_next++) * ((p->red_ws_bytes + 7) / 8);
+}
+// The next free split-K workspace slot while the backward holds combinations back (one stream
+// only: a side stream's products would not be ordered before the flush), else nullptr.
+static float* hold_gslot(talos_plan_s* p) {
+  if (!p->holding || !p->hold_gws || p->side || p->hold_gnext >= p->hold_gslots) return nullptr;
+  return p->hold_gws + (size_t)(p->hold_gnext++) * (align_ws(p->gemm_ws_bytes) / sizeof(float));
+}
+// Ends the holding when the backward returns, also on an early error return.
+struct HoldScope {
+  talos_plan_s* p;
+  explicit HoldScope(talos_plan_s* q) : p(q) {
+    p->held.clear();
+    p->held_split.clear();
+    p->hold_next = p->hold_gnext = 0;
+    p->holding = p->hold_ws != nullptr || p->hold_gws != nullptr;
+  }
+  ~HoldScope() { p->holding = false; }
+};
+// The held-back combinations, in batches of kPartsJobsMax / kSplitJobsMax.
+static int hold_flush(talos_plan_s* p, hipStream_t s) {
+  int rc = TALOS_OK;
+  for (size_t i = 0; i < p->held.size() && rc == TALOS_OK; i += kPartsJobsMax)
+    rc = reduce_parts_batch_launch((int)std::min<size_t>(kPartsJobsMax, p->held.size() - i), p->held.data() + i, s);
+  for (size_t i = 0; i < p->held_split.size() && rc == TALOS_OK; i += kSplitJobsMax)
+    rc = gemm_splitk_batch_launch((int)std::min<size_t>(kSplitJobsMax, p->held_split.size() - i),
+                                  p->held_split.data() + i, s);
+  p->held.clear();
+  p->held_split.clear();
+  p->hold_next = p->hold_gnext = 0;
+  return rc;
+}
 
 // GEMM helpers ---------------------------------------------------------------
 static int mm_ws(talos_plan_s* p, hipStream_t s, float* wsp, int tA, int tB, int M, int N, int K, const float* A,
@@ -526,7 +573,16 @@ static int mm_ws(talos_plan_s* p, hipStream_t s, float* wsp, int tA, int tB, int
   // whose split would not fit runs unsplit
   if (ws > p->gemm_ws_bytes) g.ksplit = 1;
   g.workspace = wsp;
-  return gemm_launch(g, s);
+  // a split product's combination held back where the backward collects them
+  float* slot = g.ksplit > 1 && wsp == p->gemm_ws ? hold_gslot(p) : nullptr;
+  SplitJob job;
+  if (slot) {
+    g.workspace = slot;
+    g.split_defer = &job;
+  }
+  const int rc = gemm_launch(g, s);
+  if (rc == TALOS_OK && job.part) p->held_split.push_back(job);
+  return rc;
 }
 static int mm(talos_plan_s* p, hipStream_t s, int tA, int tB, int M, int N, int K, const float* A, long long lda,
               const float* B, long long ldb, float* C, long long ldc, float beta = 0.f, const float* bias = nullptr,
@@ -634,9 +690,20 @@ static int wgrad_pair(talos_plan_s* p, hipStream_t s, const WgradOp& w0, const W
     ls = p->side;
     base = p->gemm_ws2;
   }
+  // (one stream: the pair's combinations held back where the backward collects them, its
+  // partials in a slot of their own)
+  float* slot = p->side ? nullptr : hold_gslot(p);
+  if (slot) base = slot;
   GemmDesc g0, g1;
   pair_descs(p, base, w0, w1, &g0, &g1);
+  SplitJob j0, j1;
+  if (slot) {
+    g0.split_defer = &j0;
+    g1.split_defer = &j1;
+  }
   int rc = gemm_launch_pair(g0, g1, ls);
+  if (rc == TALOS_OK && j0.part) p->held_split.push_back(j0);
+  if (rc == TALOS_OK && j1.part) p->held_split.push_back(j1);
   if (rc || !p->side) return rc;
   for (const void* buf : {w0.reads, w1.reads}) {
     hipEvent_t e = nullptr;
@@ -651,31 +718,6 @@ static int before_write(talos_plan_s* p, hipStream_t s, const void* buf) {
   for (auto& r : p->readers)
     if (r.buf == buf) TALOS_HIP(hipStreamWaitEvent(s, r.ev, 0));
   return TALOS_OK;
-}
-
-// The next free slot of hold_ws while the PPO backward holds its reductions back, else nullptr.
-static double* hold_slot(talos_plan_s* p) {
-  if (!p->holding || !p->hold_ws || p->hold_next >= p->hold_slots) return nullptr;
-  return p->hold_ws + (size_t)(p->hold_next++) * ((p->red_ws_bytes + 7) / 8);
-}
-// Ends the holding when the backward returns, also on an early error return.
-struct HoldScope {
-  talos_plan_s* p;
-  explicit HoldScope(talos_plan_s* q) : p(q) {
-    p->held.clear();
-    p->hold_next = 0;
-    p->holding = p->hold_ws != nullptr;
-  }
-  ~HoldScope() { p->holding = false; }
-};
-// The held-back reductions, in batches of kPartsJobsMax.
-static int hold_flush(talos_plan_s* p, hipStream_t s) {
-  int rc = TALOS_OK;
-  for (size_t i = 0; i < p->held.size() && rc == TALOS_OK; i += kPartsJobsMax)
-    rc = reduce_parts_batch_launch((int)std::min<size_t>(kPartsJobsMax, p->held.size() - i), p->held.data() + i, s);
-  p->held.clear();
-  p->hold_next = 0;
-  return rc;
 }
 
 // dx = RMSNorm backward of dy = g.W^T ([M, K] x [d, K]^T, d = 128 fits one tile row) with the
@@ -2369,7 +2411,8 @@ static int mla_fwd_bwd(talos_plan_s* p, const float* P, const float* x, const fl
   if ((rc = mla_attn_forward(p, D, P, o.w, L.xn1, L, s))) return rc;
   if ((rc = refresh_shadows(p, {L.o, gout}, s))) return rc;
   if ((rc = mm(p, s, 0, 0, M, d, ow, L.o, ow, P + o.w.wo, d, out, d, 0.f, nullptr, x, d))) return rc;
-  // ---- backward
+  // ---- backward (its split-K weight gradients' combinations held back to one launch at the end)
+  HoldScope hold(p);
   if ((rc = mm(p, s, 1, 0, ow, d, M, L.o, ow, gout, d, G + o.w.wo, d))) return rc;
   // dO = gout . Wo^T; where the attention backward takes the dS path, the product's epilogue also
   // forms that backward's D = rowsum(dO . O) into its workspace (no row-dot launch)
@@ -2402,7 +2445,10 @@ static int mla_fwd_bwd(talos_plan_s* p, const float* P, const float* x, const fl
   }
   if ((rc = mla_attn_backward(p, D, P, G, o.w, L.xn1, L, p->g_o, p->g_xn, s, d_ready))) return rc;
   // residual + rmsnorm
-  return rmsnorm_bwd_launch(M, d, x, P + o.g, L.rstd1, p->g_xn, 1.f, dx, 0.f, G + o.g, p->red_ws, s, gout);
+  if ((rc = rmsnorm_bwd_launch(M, d, x, P + o.g, L.rstd1, p->g_xn, 1.f, dx, 0.f, G + o.g, p->red_ws, s, gout)))
+    return rc;
+  p->holding = false;
+  return hold_flush(p, s);
 }
 
 const talos_ppo_cfg* ppo_plan_cfg(talos_plan plan) {

@@ -265,6 +265,35 @@ def test_mla_fused_rowdot_bit_identical(monkeypatch, ci, prec):
         assert np.array_equal(a, b), f"{name}: {int((a != b).sum())} elements differ, max {np.abs(a - b).max():.3e}"
 
 
+@pytest.mark.parametrize("kind", ["block", "mla_fp32", "mla_bf16"])
+def test_held_split_combinations_bit_identical(monkeypatch, kind):
+    """The block and MLA backward hold their split-K weight gradients' combinations back and run
+    them as one batched launch at the end (each product's partials in a workspace slot of its
+    own); the batch sums each as the product's own combination would, so the results equal the
+    backward that combines each product at once (TALOS_BWD_SIDE_STREAM=1, under which nothing is
+    held: a side stream's products would not be ordered before the batch)."""
+    from common import mla_params
+    rng = np.random.default_rng(4400 + len(kind))
+    if kind == "block":
+        B, S, d, F = 64, 64, 128, 512
+        cfg = th.BlockCfg(B, S, d, 4, d // 4, F, 1, 0, 1e-6, 10000.0)
+        p = f32(block_params(rng, d, F, gain_jitter=True))
+        x, G = f32(rng.normal(size=(B, S, d))), f32(rng.normal(size=(B, S, d)))
+        run = lambda: run_block(cfg, p, x, G)  # noqa: E731
+    else:
+        ci = [8, 256, 512, 8, 128, 32, 64, 64, 0, 0]
+        prec = th.PREC_BF16 if kind == "mla_bf16" else th.PREC_FP32
+        p = f32(mla_params(rng, ci))
+        x, G = f32(rng.normal(size=(ci[0], ci[1], ci[2]))), f32(rng.normal(size=(ci[0], ci[1], ci[2])))
+        run = lambda: run_mla(ci, prec, p, x, G)  # noqa: E731
+    monkeypatch.delenv("TALOS_BWD_SIDE_STREAM", raising=False)
+    held = run()
+    monkeypatch.setenv("TALOS_BWD_SIDE_STREAM", "1")
+    at_once = run()
+    for name, a, b in zip(("out", "dparams", "dx"), held, at_once):
+        assert np.array_equal(a, b), f"{name}: {int((a != b).sum())} elements differ, max {np.abs(a - b).max():.3e}"
+
+
 def test_mla_plan_over_ds_budget_is_created():
     """A plan whose dS rows would exceed the budget (seq 2048 at batch 64, 8 heads: 8.6 GB in
     fp32, 4.3 GB in bf16, against 4 GiB) is still created, on the tiled path."""
