@@ -572,7 +572,7 @@ __device__ __forceinline__ void bcast_rows(float* slice, float v, int l32, int h
 #define TALOS_ATTN_TILED_WAVES 3
 #endif
 template <int DKM, int DVM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DKM > 96 ? 2 : TALOS_ATTN_TILED_WAVES))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DKM > 64 ? 2 : TALOS_ATTN_TILED_WAVES))) void
 attn_fwd_tiled_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, OB = DVM / 32;
   constexpr int PK = DKM + 4, PV = DVM + 4;  // 16-byte rows; eight consecutive rows on distinct bank groups
@@ -856,7 +856,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a) {
 //    (register r <-> query acc_row(r, h), lane <-> key); dV += P^T . dO and dK += dS^T . Q.
 // ---------------------------------------------------------------------------
 template <int DKM, int DVM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DKM > 64 ? 2 : TALOS_ATTN_TILED_WAVES))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DKM > 32 ? 2 : TALOS_ATTN_TILED_WAVES))) void
 attn_bwd_dq_tiled_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, VH = DVM / 2, QB = DKM / 32;
   constexpr int PK = DKM + 4, PV = DVM + 4;
@@ -993,9 +993,10 @@ __device__ __forceinline__ void store_head_col(float* dst, long long ld, float* 
 
 // DS: every dS value of the wave's key blocks is also stored to a.ds (row of query q, column of
 // key), through a per-wave LDS tile so the global stores are 16-byte pieces of rows, for
-// attn_bwd_dq_ds_kernel; D comes from attn_rowdot_kernel.
+// attn_bwd_dq_ds_kernel; D comes from attn_rowdot_kernel. (Two waves a SIMD at every head dim: at
+// three, head dims 32 spilled 2 VGPRs, 28 with DS.)
 template <int DKM, int DVM, bool DS = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DKM > 32 ? 2 : TALOS_ATTN_TILED_WAVES))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
 attn_bwd_dkv_tiled_kernel(AttnArgs a) {
   constexpr int KH = DKM / 2, VH = DVM / 2, KB = DKM / 32, VB = DVM / 32;
   constexpr int PK = DKM + 4, PV = DVM + 4;
