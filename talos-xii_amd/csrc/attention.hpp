@@ -111,7 +111,7 @@ int attn_bwd_lastq_z_launch(const AttnDesc& d, const float* xn, long long ldx, c
 size_t attn_bwd_workspace_bytes(const AttnDesc& d);
 bool attn_bwd_ds_supported(const AttnDesc& d);
 // The one predicate of the dS path: ds given, 16-byte aligned, on attn_bwd_ds_supported's shapes.
-// The forward's bf16 kernel, the split q / k inputs and the backward all follow it, so a forward
+// The forward's bf16 kernel and the backward both follow it, so a forward
 // and its backward always form P from the same products (the backward then needs the workspace).
 bool attn_ds_path(const AttnDesc& d);
 // bytes of the dS scratch: batch * heads * seq^2 entries of 4 bytes, 2 for bf16 (d.bf16)
