@@ -353,7 +353,10 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_generic(int rows, int dim, fl
 // reduce_parts_kernel combines. (The generic kernel runs 4-wave workgroups on the same grid.)
 constexpr int kRmsWaves = 16, kRmsThreads = 64 * kRmsWaves;
 constexpr int kRmsRowsPerWave = 2;
-constexpr int kRmsMaxBlocks = 1024;  // 4 workgroups per CU; 1024 x dim f64 partials at most
+// one 16-wave workgroup per CU; 256 x dim f64 partials at most (at 16384 rows of 512 the
+// workgroups' waves take four rows each, two passes of two: 24.3 us against 28.3 with 1024
+// workgroups of one row a wave, which run in two rounds of two workgroups per CU)
+constexpr int kRmsMaxBlocks = 256;
 static int rms_bwd_blocks(int rows) {
   int b = (rows + kRmsWaves - 1) / kRmsWaves;
   return b < 1 ? 1 : (b > kRmsMaxBlocks ? kRmsMaxBlocks : b);
@@ -380,7 +383,7 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_bwd_kernel(int rows, int 
   const int stride = gridDim.x * kRmsWaves;
   // kRmsRowsPerWave rows per pass, all of their loads issued before the first row is reduced
   for (int row0 = blockIdx.x * kRmsWaves + wv; row0 < rows; row0 += kRmsRowsPerWave * stride) {
-    float4 xh[kRmsRowsPerWave][V], gg[kRmsRowsPerWave][V];
+    float4 xh[kRmsRowsPerWave][V], gg[kRmsRowsPerWave][V], ad[kRmsRowsPerWave][V];
     float r[kRmsRowsPerWave];
 #pragma unroll
     for (int k = 0; k < kRmsRowsPerWave; ++k) {
@@ -390,9 +393,12 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_bwd_kernel(int rows, int 
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         const int c = 4 * lane + 256 * j;
+        ad[k][j] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (live && c < dim) {
           xh[k][j] = *reinterpret_cast<const float4*>(x + (long long)row * dim + c);
           gg[k][j] = *reinterpret_cast<const float4*>(dy + (long long)row * dim + c);
+          // the addend row too, so a row waits on memory once (before its reduction)
+          if (add) ad[k][j] = *reinterpret_cast<const float4*>(add + (long long)row * dim + c);
         } else {
           xh[k][j] = gg[k][j] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
@@ -426,7 +432,7 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_bwd_kernel(int rows, int 
           float4 o = make_float4(rk * (g.x * gw[j].x - h.x * md), rk * (g.y * gw[j].y - h.y * md),
                                  rk * (g.z * gw[j].z - h.z * md), rk * (g.w * gw[j].w - h.w * md));
           if (add) {
-            const float4 old = *reinterpret_cast<const float4*>(add + (long long)row * dim + c);
+            const float4 old = ad[k][j];
             o.x += old.x;
             o.y += old.y;
             o.z += old.z;
