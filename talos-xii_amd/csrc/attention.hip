@@ -2154,7 +2154,7 @@ attn_bwd_s64_kernel(AttnArgs a) {
 // Launch
 // ---------------------------------------------------------------------------
 // TALOS_ATTN_LEGACY=1 (read once): the per-wave kernels for seq > 32 instead of the LDS-tiled
-// ones (the same results; kept as the cross-check of the tiled kernels).
+// ones (a debugging switch: the two differ by fp32 rounding).
 static bool attn_legacy() {
   static const bool v = [] {
     const char* e = std::getenv("TALOS_ATTN_LEGACY");
