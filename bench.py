@@ -602,7 +602,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
-              "The minibatch would shard over samples with one gradient all-reduce; see DESIGN.md.",
+              "The minibatch would shard over samples, each GPU running this step on its share, with one "
+              "all-reduce of the parameter gradients.",
               file=sys.stderr)
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
