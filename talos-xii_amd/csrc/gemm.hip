@@ -1454,6 +1454,38 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
     }
   }
 
+  // E_NBPRE on 128-row tiles whose samples are a multiple of 32 rows: each 32 x 32 accumulator
+  // block lies in one sample, so its addend sum_h P[row][h] U[sample][h][col] is a 32 x 4 by 4 x 32
+  // product, two more v_mfma_f32_32x32x2_f32 steps (lane half h supplies head 2 s + h at step s),
+  // and the epilogue runs without the addend's per-row loads.
+  bool pre_folded = false;
+  if constexpr ((E & E_NBPRE) != 0 && MT == 2) {
+    pre_folded = p.nb_seq % 32 == 0;
+    if (pre_folded) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int r0 = m0 + wm * 64 + mt * 32, row = r0 + l32;
+        // (a block that starts past M has zero P rows: any U row serves it)
+        const long long smp = (long long)(r0 < p.M ? r0 : 0) / p.nb_seq;
+        float pa[2], ub[2][2];  // P: [step]; U: [nt][step]
+#pragma unroll
+        for (int st = 0; st < 2; ++st) pa[st] = row < p.M ? p.nb_pre_p[(long long)row * 4 + 2 * st + h] : 0.f;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const int col = n0 + wn * 64 + nt * 32 + l32;
+#pragma unroll
+          for (int st = 0; st < 2; ++st)
+            ub[nt][st] = col < p.N ? p.nb_pre_u[(smp * 4 + 2 * st + h) * p.N + col] : 0.f;
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int st = 0; st < 2; ++st)
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[st], ub[nt][st], acc[mt][nt], 0, 0, 0);
+      }
+    }
+  }
+
   // Stage the tile through LDS 64 rows at a time (BMT = 128: one half, the two waves with
   // wm == half; BMT = 64: all four waves) (accumulator layout of v_mfma_f32_32x32x2_f32: lane l,
   // register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32 of its 32x32 block), then run the
@@ -1520,18 +1552,27 @@ __device__ __forceinline__ void gemm_tile(GemmArgs p, int logical) {
     } else if constexpr ((E & E_NORMB) != 0) {
       const float4 g = *reinterpret_cast<const float4*>(p.nb_gain + col);
       const int rbase = m0 + half * T_ROWS + (threadIdx.x >> 5);
-      // the next row's x and rstd load under this row's work (with the E_NBPRE addend, loaded in
-      // the row's own step, there are no registers for that)
-      constexpr bool PRE = (E & E_NBPRE) != 0;
+      // the next row's x and rstd load under this row's work; with E_NBPRE, after the row (its
+      // last-row terms leave no registers for them ahead: 16 bytes a lane spilled, 80.6 against
+      // 79.3 us at C4), and the addend's P and U loaded in the row's own step unless the products
+      // already added it (82.3 us when they did not)
+      const bool pre = (E & E_NBPRE) != 0 && !pre_folded;
       NbIn cur = normb_load(p, rbase, col);
 #pragma unroll 1
       for (int i = 0; i < T_ROWS / 8; ++i) {
         const int lr = (threadIdx.x >> 5) + 8 * i;
         NbIn nxt = cur;
-        if (!PRE && i + 1 < T_ROWS / 8) nxt = normb_load(p, rbase + 8 * (i + 1), col);
+        if ((E & E_NBPRE) == 0 && i + 1 < T_ROWS / 8) nxt = normb_load(p, rbase + 8 * (i + 1), col);
         const float4 v = *reinterpret_cast<const float4*>(T + lr * T_S + cg);
-        normb_apply<PRE>(p, v, rbase + 8 * i, col, cur, g, nbw);
-        if (PRE && i + 1 < T_ROWS / 8) nxt = normb_load(p, rbase + 8 * (i + 1), col);
+        if constexpr ((E & E_NBPRE) != 0) {
+          if (pre)
+            normb_apply<true>(p, v, rbase + 8 * i, col, cur, g, nbw);
+          else
+            normb_apply<false>(p, v, rbase + 8 * i, col, cur, g, nbw);
+        } else {
+          normb_apply<false>(p, v, rbase + 8 * i, col, cur, g, nbw);
+        }
+        if ((E & E_NBPRE) != 0 && i + 1 < T_ROWS / 8) nxt = normb_load(p, rbase + 8 * (i + 1), col);
         cur = nxt;
       }
     } else {
