@@ -54,11 +54,11 @@ def plan_mode(unfused):
 # ---------------------------------------------------------------------------------------------
 # C4: PPO minibatch
 # ---------------------------------------------------------------------------------------------
-def _ppo_inputs(seed, n, lens=None):
+def _ppo_inputs(seed, n, lens=None, seq=None):
     rng = np.random.default_rng(seed)
     ocfg_args = list(C4_ARGS)
     p = f32(ppo_params(rng, th.PpoCfg(*ocfg_args)))
-    S = C4_ARGS[1]
+    S = seq or C4_ARGS[1]
     states = f32(gacha_states(rng, n, S))
     if lens is not None:
         for b, L in enumerate(lens):  # padding rows hold finite garbage: they must not leak
@@ -94,8 +94,10 @@ def _ppo_oracle(oracle, p, states, lens, actions, adv, ret, old, chunk=512):
 
 def _ppo_gpu(unfused, p, states, lens, actions, adv, ret, old):
     n = states.shape[0]
+    args = list(C4_ARGS)
+    args[1] = states.shape[1]  # the plan's sequence length is the inputs'
     with plan_mode(unfused):
-        plan = th.Plan("ppo", th.PpoCfg(*C4_ARGS))
+        plan = th.Plan("ppo", th.PpoCfg(*args))
     P, St, Ac = DA.from_numpy(p), DA.from_numpy(states), DA.from_numpy(actions, np.int32)
     Ad, Re, Ol = DA.from_numpy(adv), DA.from_numpy(ret), DA.from_numpy(old)
     Ln = DA.from_numpy(np.asarray(lens), np.int32) if lens is not None else None
@@ -149,6 +151,16 @@ def test_c4_ppo_ragged_full_size(oracle):
     for unfused in (False, True):
         got = _ppo_gpu(unfused, p, states, lens, actions, adv, ret, old)
         _check_ppo("unfused" if unfused else "fused", got, ref)
+
+
+def test_c4_ppo_seq24_full_size(oracle):
+    # 4096 samples of 24 tokens: the last layer's key-gradient product still runs on 128-row
+    # tiles, whose 32-row accumulator blocks now straddle samples, so it adds the value-path addend
+    # row by row in its epilogue (at 32 tokens it adds it with two more matrix steps a block)
+    B = C4_ARGS[0]
+    p, states, actions, adv, ret, old = _ppo_inputs(47, B, seq=24)
+    ref = _ppo_oracle(oracle, p, states, None, actions, adv, ret, old)
+    _check_ppo("seq 24", _ppo_gpu(False, p, states, None, actions, adv, ret, old), ref)
 
 
 # ---------------------------------------------------------------------------------------------
